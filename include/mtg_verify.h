@@ -1,0 +1,255 @@
+/* mtg_verify.h - C ABI of the MI355X speculative draft->verify decode path.
+ *
+ * The library (libmtg.so) runs the Qwen3 target pass of moss-transcribe.cpp's
+ * speculative decoder on one gfx950 GPU: T verify rows (seed + drafts) go through
+ * all decoder layers as one batch over a persistent device KV cache, followed by
+ * the tied lm_head, a greedy first-max choice per row (optional repetition
+ * penalty) and longest-prefix acceptance on the device.
+ *
+ * Reference interfaces each entry point replaces (paths relative to the
+ * moss-transcribe.cpp source tree):
+ *   mtg_create/mtg_destroy    Qwen3Decoder::load, ~Qwen3Decoder     src/qwen3_decoder.cpp:16-85
+ *   mtg_prefill               Qwen3Decoder::prefill                 src/qwen3_decoder.cpp:162-166
+ *   mtg_append                CpuSpeculativeDecoder::append -> run  src/cpu_speculative.cpp:37-39, src/qwen3_decoder.cpp:91-160
+ *   mtg_logits                Qwen3Decoder::logits_from_hidden      src/qwen3_decoder.cpp:174-205
+ *   mtg_embed                 embed_rows_f32                        src/generate.cpp:68-111
+ *   mtg_verify                append + lazy logits + cpu_greedy_choice + accept loop
+ *                                                                    src/cpu_speculative.cpp:127-148
+ *   mtg_rewind/mtg_past_len   CpuSpeculativeDecoder::rewind, Qwen3Decoder::past_len
+ *                                                                    src/cpu_speculative.cpp:40-43, src/qwen3_decoder.hpp:262
+ *   mtg_remaining             CpuSpeculativeDecoder::remaining       src/cpu_speculative.cpp:43
+ *   mtg_generate              cpu_speculative_generate               src/cpu_speculative.cpp:86-165
+ *   mtg_ngram_draft           cpu_ngram_draft                        src/cpu_speculative.cpp:45-56
+ *   mtg_greedy_choice         cpu_greedy_choice                      src/cpu_speculative.cpp:57-68
+ *   mtg_q8_pack/mtg_q8_mul_mat  cpu_pack_q8 / cpu_decode_mul_mat     src/cpu_q8.hpp:131-145, src/cpu_q8.cpp:177-276
+ *   mtg_causal_context        cpu_causal_context                     src/cpu_context.hpp:69-73, src/cpu_context.cpp:13-56
+ *   mtg_last_error            moss_transcribe_capi_last_error        include/moss_transcribe_capi.h:50-53
+ *
+ * Conventions: every function returns an int status (MTG_OK == 0, negative on
+ * error) and never lets a C++ exception cross; the error text is owned by the
+ * context (mtg_last_error). Calls on one context are serialized by the caller
+ * (as the reference serializes graph execution). Host pointers are plain host
+ * memory; the *_dev entry points take device pointers.
+ */
+#ifndef MTG_VERIFY_H
+#define MTG_VERIFY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MTG_ABI_VERSION 1
+#define MTG_MAX_BATCH 16 /* verify rows per step (seed + up to 15 drafts) */
+
+/* Tensor element types, numbered as ggml numbers them (ggml.h GGML_TYPE_*). */
+enum {
+  MTG_TYPE_F32 = 0,
+  MTG_TYPE_F16 = 1,
+  MTG_TYPE_Q8_0 = 8,
+  MTG_TYPE_Q4_K = 12
+};
+
+enum {
+  MTG_OK = 0,
+  MTG_ERR_INVALID = -1,     /* bad argument (reference: returns false / throws) */
+  MTG_ERR_UNSUPPORTED = -2, /* shape or type not handled (reference: nullptr fallback) */
+  MTG_ERR_DEVICE = -3,      /* HIP runtime error */
+  MTG_ERR_CAPACITY = -4,    /* past + T > max_seq (reference: run() returns false) */
+  MTG_ERR_NOMEM = -5,
+  MTG_ERR_STATE = -6        /* invalid rewind / call order */
+};
+
+/* Decoder dimensions (reference: Qwen3Hparams, src/qwen3.hpp:7). */
+typedef struct mtg_hparams {
+  int32_t hidden;       /* 1024 */
+  int32_t n_heads;      /* 16 */
+  int32_t n_kv_heads;   /* 8 */
+  int32_t head_dim;     /* 128 */
+  int32_t intermediate; /* 3072 */
+  int32_t n_layers;     /* 28 */
+  int32_t vocab;        /* 151936 */
+  float rope_base;      /* 1e6 */
+  float rms_eps;        /* 1e-6 */
+} mtg_hparams;
+
+/* One decoder layer, tensor names of the reference GGUF (src/qwen3.cpp:44-54).
+ * Matrices are row-major "N rows of K" in ggml block layout of weight_type:
+ * ggml ne = [K, N]. Norm gains are f32. */
+typedef struct mtg_layer_tensors {
+  const float* attn_norm;   /* [hidden] */
+  const void* attn_q;       /* N = n_heads*head_dim, K = hidden */
+  const void* attn_k;       /* N = n_kv_heads*head_dim, K = hidden */
+  const void* attn_v;       /* N = n_kv_heads*head_dim, K = hidden */
+  const void* attn_o;       /* N = hidden, K = n_heads*head_dim */
+  const float* attn_q_norm; /* [head_dim] */
+  const float* attn_k_norm; /* [head_dim] */
+  const float* ffn_norm;    /* [hidden] */
+  const void* ffn_gate;     /* N = intermediate, K = hidden */
+  const void* ffn_up;       /* N = intermediate, K = hidden */
+  const void* ffn_down;     /* N = hidden, K = intermediate */
+} mtg_layer_tensors;
+
+typedef struct mtg_model_desc {
+  mtg_hparams hp;
+  int32_t weight_type;              /* MTG_TYPE_Q8_0, MTG_TYPE_F16 or MTG_TYPE_Q4_K */
+  const void* token_embd;           /* N = vocab, K = hidden; also the tied lm_head */
+  const float* output_norm;         /* [hidden] */
+  const mtg_layer_tensors* layers;  /* n_layers entries */
+} mtg_model_desc;
+
+typedef struct mtg_ctx mtg_ctx;
+
+int mtg_abi_version(void);
+
+/* Upload weights (re-tiled for the gfx950 kernels) and allocate a KV cache of
+ * max_seq positions of kv_type (MTG_TYPE_F32 or MTG_TYPE_F16). The host tensors
+ * may be freed after the call. */
+int mtg_create(const mtg_model_desc* desc, int32_t max_seq, int32_t kv_type, mtg_ctx** out);
+void mtg_destroy(mtg_ctx* ctx);
+const char* mtg_last_error(const mtg_ctx* ctx);
+
+int32_t mtg_past_len(const mtg_ctx* ctx);
+int32_t mtg_remaining(const mtg_ctx* ctx);
+/* Logical rewind; fails with MTG_ERR_STATE unless 0 <= position <= past_len. */
+int mtg_rewind(mtg_ctx* ctx, int32_t position);
+
+/* Dequantized embedding rows of ids (token-major, n x hidden floats). */
+int mtg_embed(mtg_ctx* ctx, const int32_t* ids, int32_t n, float* out);
+
+/* reset + run S rows; hidden_out (nullable) receives the final-normed hidden of
+ * every row (S x hidden). Rows are processed in verify batches of up to
+ * MTG_MAX_BATCH, each causal over everything before it. */
+int mtg_prefill(mtg_ctx* ctx, const float* embeds, int32_t S, float* hidden_out);
+
+/* Append T (1..MTG_MAX_BATCH) embedding rows at past_len; past_len += T.
+ * hidden_out (nullable) receives T x hidden final-normed rows. */
+int mtg_append(mtg_ctx* ctx, const float* embeds, int32_t T, float* hidden_out);
+
+/* Tied lm_head for T rows of final-normed hidden: logits_out T x vocab. */
+int mtg_logits(mtg_ctx* ctx, const float* hidden, int32_t T, float* logits_out);
+
+/* One verify step. tokens = {seed, draft_1 .. draft_{T-1}}. Appends all T rows
+ * at past_len (past_len += T), computes the greedy choice after every row with
+ * the repetition penalty applied over the last 100 ids of
+ * history ++ tokens[0..i] (penalty <= 1 disables it), and the number of leading
+ * drafts equal to the choice of the row before them:
+ *   n_match = max m such that tokens[i+1] == choice[i] for all i < m.
+ * Only T+1 ints come back from the device; hidden_out / logits_out (nullable)
+ * additionally return T x hidden / T x vocab floats for parity checks.
+ * Stop rules and the rewind to past + keep are the caller's (mtg_generate). */
+int mtg_verify(mtg_ctx* ctx, const int32_t* tokens, int32_t T,
+               const int32_t* history, int32_t n_history, float penalty,
+               int32_t* choice_out, int32_t* n_match_out,
+               float* hidden_out, float* logits_out);
+
+/* KV cache exchange, layout [layer][kv_head][position][head_dim] in kv_type.
+ * mtg_kv_write sets past_len = n_pos. */
+int mtg_kv_write(mtg_ctx* ctx, const void* k, const void* v, int32_t n_pos);
+int mtg_kv_read(mtg_ctx* ctx, void* k, void* v, int32_t n_pos);
+
+/* ---- speculative generation controller (host C++) ---- */
+
+/* Draft hook: write up to `budget` proposals for the committed ids into out and
+ * return the count (reference: CpuSpeculativeHooks::draft, src/cpu_speculative.hpp:11). */
+typedef int32_t (*mtg_draft_fn)(void* user, const int32_t* ids, int32_t n_ids, int32_t budget,
+                                int32_t* out);
+/* Commit hook, called after every step with the committed ids and whether a stop
+ * rule fired (reference: CpuSpeculativeHooks::committed, src/cpu_speculative.hpp:14). */
+typedef void (*mtg_commit_fn)(void* user, const int32_t* ids, int32_t n_ids, int32_t past_len,
+                              int32_t stopped);
+
+typedef struct mtg_gen_stats {
+  int64_t target_calls, drafted_calls, proposed, accepted, target_input_tokens, rewinds;
+  double prefill_seconds, verify_seconds, draft_seconds;
+  int32_t stop_reason; /* 0 none/error, 1 eos, 2 token_limit */
+  int32_t next_seed;   /* greedy choice of the last kept row (the next step's seed) */
+} mtg_gen_stats;
+
+/* cpu_speculative_generate on the device decoder: prefill `seq` fused rows, take
+ * the first greedy seed, then loop {draft <= max_draft, verify, accept, rewind}
+ * until eos or max_new tokens. draft == NULL uses mtg_ngram_draft. ids_out must
+ * hold max_new ids. */
+int mtg_generate(mtg_ctx* ctx, const float* fused, int32_t seq, int32_t max_new, int32_t eos,
+                 float penalty, int32_t max_draft, mtg_draft_fn draft, mtg_commit_fn commit,
+                 void* user, int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats);
+
+/* Same loop, continuing from the current KV state instead of a prefill.
+ * first_seed: the greedy choice of the last row already in the cache.
+ * prior_ids (nullable): ids committed before, visible to the drafter and the
+ * penalty window. max_steps <= 0: run until a stop rule fires. */
+int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids,
+                      int32_t n_prior, int32_t max_new, int32_t max_steps, int32_t eos,
+                      float penalty, int32_t max_draft, mtg_draft_fn draft, mtg_commit_fn commit,
+                      void* user, int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats);
+
+/* Draft hook for long-context workloads (pass mtg_stream_draft as `draft` and a
+ * mtg_stream_drafter as `user`): the reference n-gram proposal over
+ * prompt ++ ids, completed up to the budget from a periodic token stream
+ * aligned to the absolute position of the next token. */
+typedef struct mtg_stream_drafter {
+  const int32_t* prompt; /* text ids that precede generation */
+  int32_t n_prompt;
+  const int32_t* stream; /* one period of the token stream */
+  int32_t period;        /* 0: n-gram proposal only */
+} mtg_stream_drafter;
+int32_t mtg_stream_draft(void* user, const int32_t* ids, int32_t n_ids, int32_t budget,
+                         int32_t* out);
+
+/* 1 (default): replay each step from a captured HIP graph; 0: launch eagerly. */
+int mtg_set_graphs(mtg_ctx* ctx, int32_t enable);
+
+/* Host policy functions (reference: cpu_ngram_draft, cpu_greedy_choice). */
+int32_t mtg_ngram_draft(const int32_t* history, int32_t n, int32_t maximum, int32_t* out);
+int32_t mtg_greedy_choice(const float* raw, int32_t n, const int32_t* history, int32_t n_history,
+                          float penalty);
+
+/* ---- kernel-level entry points on device pointers ---- */
+
+typedef struct mtg_q8_packed mtg_q8_packed;
+/* Upload and re-tile one q8_0 matrix (N rows of K, K % 64 == 0, N % 16 == 0).
+ * Returns MTG_ERR_UNSUPPORTED for other shapes (the caller keeps its own path). */
+int mtg_q8_pack(const void* blocks, int32_t k, int32_t n, mtg_q8_packed** out);
+void mtg_q8_free(mtg_q8_packed* p);
+/* y_dev[t][n] = q8_0 dot of the packed rows with x_dev[t][:] (T x K floats,
+ * quantized to q8_0 per 32-block on the device), T in 1..MTG_MAX_BATCH. */
+int mtg_q8_mul_mat_dev(const mtg_q8_packed* w, const float* x_dev, int32_t T, float* y_dev);
+
+/* out_dev[h][q][f] = sum_{k <= past+q} v[h/groups][k][f] * p[h][q][k]
+ * v_dev: [kv_heads][kv_len][head_dim] f32, p_dev: [heads][queries][kv_len] f32,
+ * past = kv_len - queries; each query reads exactly its valid length. */
+int mtg_causal_context_dev(const float* v_dev, const float* p_dev, int32_t head_dim,
+                           int32_t kv_heads, int32_t heads, int32_t queries, int32_t kv_len,
+                           float* out_dev);
+
+/* ---- synthetic model (workload generator; stands in for the GGUF loader) ---- */
+
+typedef struct mtg_synth_model mtg_synth_model;
+/* Seeded N(0, std) weights quantized to weight_type, norm gains
+ * 1 + gain_jitter * N(0,1). */
+int mtg_synth_create(const mtg_hparams* hp, int32_t weight_type, uint64_t seed, float std,
+                     float gain_jitter, mtg_synth_model** out);
+void mtg_synth_free(mtg_synth_model* m);
+const mtg_model_desc* mtg_synth_desc(const mtg_synth_model* m);
+
+/* Standard normal stream shared by the workload generators:
+ * out[i] = N(0,1) sample number (first + i) of the stream named by seed. */
+void mtg_normal_fill(uint64_t seed, uint64_t first, float* out, size_t n);
+
+/* Weight quantizers of the synthetic model. q8_0: ggml's reference rule as the
+ * GGUF converter applies it (d = amax/127 stored f16, codes = roundf(x * 1/d));
+ * block = {f16 d, int8 qs[32]}. */
+void mtg_quantize_q8_0_weight(const float* x, int64_t k, void* blocks);
+void mtg_quantize_q4_k(const float* x, int64_t k, void* blocks);
+void mtg_dequantize(int32_t type, const void* blocks, int64_t k, float* out);
+size_t mtg_row_bytes(int32_t type, int64_t k);
+uint16_t mtg_f32_to_f16(float f);
+float mtg_f16_to_f32(uint16_t h);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTG_VERIFY_H */

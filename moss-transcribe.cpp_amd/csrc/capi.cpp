@@ -1,0 +1,392 @@
+// capi.cpp - the extern "C" boundary and the speculative generation controller.
+//
+// Every entry point catches all exceptions and reports through an int status and
+// the context's error text, as moss_transcribe_capi.cpp:80-94 does for the
+// product API.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <new>
+#include <set>
+#include <vector>
+
+#include "kernels.hpp"
+#include "runtime.hpp"
+
+using mtg::Ctx;
+
+namespace {
+thread_local std::string g_create_error;
+
+double seconds_since(std::chrono::steady_clock::time_point t0) {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+}
+}  // namespace
+
+extern "C" {
+
+int mtg_abi_version(void) { return MTG_ABI_VERSION; }
+
+int mtg_create(const mtg_model_desc* desc, int32_t max_seq, int32_t kv_type, mtg_ctx** out) {
+  if (!out) return MTG_ERR_INVALID;
+  *out = nullptr;
+  if (!desc || !desc->layers || !desc->token_embd || !desc->output_norm) return MTG_ERR_INVALID;
+  try {
+    auto* c = new (std::nothrow) mtg_ctx();
+    if (!c) return MTG_ERR_NOMEM;
+    const int rc = c->impl.init(desc, max_seq, kv_type);
+    if (rc) {
+      g_create_error = c->impl.error;
+      delete c;
+      return rc;
+    }
+    *out = c;
+    return MTG_OK;
+  } catch (...) {
+    return MTG_ERR_NOMEM;
+  }
+}
+
+void mtg_destroy(mtg_ctx* ctx) { delete ctx; }
+
+const char* mtg_last_error(const mtg_ctx* ctx) {
+  return ctx ? ctx->impl.error.c_str() : g_create_error.c_str();
+}
+
+int mtg_set_graphs(mtg_ctx* ctx, int32_t enable) {
+  if (!ctx) return MTG_ERR_INVALID;
+  ctx->impl.use_graphs = enable != 0;
+  return MTG_OK;
+}
+
+int32_t mtg_past_len(const mtg_ctx* ctx) { return ctx ? ctx->impl.past : 0; }
+int32_t mtg_remaining(const mtg_ctx* ctx) { return ctx ? ctx->impl.max_seq - ctx->impl.past : 0; }
+
+// CpuSpeculativeDecoder::rewind (src/cpu_speculative.cpp:40-42): logical only;
+// positions >= past_len are never read again before being rewritten.
+int mtg_rewind(mtg_ctx* ctx, int32_t position) {
+  if (!ctx) return MTG_ERR_INVALID;
+  if (position < 0 || position > ctx->impl.past)
+    return ctx->impl.fail(MTG_ERR_STATE, "invalid rewind to %d (past_len %d)", position, ctx->impl.past);
+  ctx->impl.past = position;
+  return MTG_OK;
+}
+
+int mtg_embed(mtg_ctx* ctx, const int32_t* ids, int32_t n, float* out) {
+  if (!ctx) return MTG_ERR_INVALID;
+  try {
+    return ctx->impl.embed(ids, n, out);
+  } catch (...) {
+    return ctx->impl.fail(MTG_ERR_DEVICE, "embed: exception");
+  }
+}
+
+int mtg_append(mtg_ctx* ctx, const float* embeds, int32_t T, float* hidden_out) {
+  if (!ctx) return MTG_ERR_INVALID;
+  try {
+    return ctx->impl.append(embeds, T, hidden_out);
+  } catch (...) {
+    return ctx->impl.fail(MTG_ERR_DEVICE, "append: exception");
+  }
+}
+
+int mtg_prefill(mtg_ctx* ctx, const float* embeds, int32_t S, float* hidden_out) {
+  if (!ctx) return MTG_ERR_INVALID;
+  if (!embeds || S <= 0) return ctx->impl.fail(MTG_ERR_INVALID, "prefill: bad arguments");
+  if (S > ctx->impl.max_seq) return ctx->impl.fail(MTG_ERR_CAPACITY, "prefill exceeds max_seq");
+  try {
+    ctx->impl.past = 0;
+    const int H = ctx->impl.hp.hidden;
+    for (int s0 = 0; s0 < S; s0 += MTG_MAX_BATCH) {
+      const int n = std::min(MTG_MAX_BATCH, S - s0);
+      const int rc = ctx->impl.append(embeds + (size_t)s0 * H, n,
+                                      hidden_out ? hidden_out + (size_t)s0 * H : nullptr);
+      if (rc) return rc;
+    }
+    return MTG_OK;
+  } catch (...) {
+    return ctx->impl.fail(MTG_ERR_DEVICE, "prefill: exception");
+  }
+}
+
+int mtg_logits(mtg_ctx* ctx, const float* hidden, int32_t T, float* logits_out) {
+  if (!ctx) return MTG_ERR_INVALID;
+  try {
+    return ctx->impl.logits_of(hidden, T, logits_out);
+  } catch (...) {
+    return ctx->impl.fail(MTG_ERR_DEVICE, "logits: exception");
+  }
+}
+
+int mtg_verify(mtg_ctx* ctx, const int32_t* tokens, int32_t T, const int32_t* history,
+               int32_t n_history, float penalty, int32_t* choice_out, int32_t* n_match_out,
+               float* hidden_out, float* logits_out) {
+  if (!ctx) return MTG_ERR_INVALID;
+  try {
+    return ctx->impl.verify(tokens, T, history, n_history, penalty, choice_out, n_match_out,
+                            hidden_out, logits_out);
+  } catch (...) {
+    return ctx->impl.fail(MTG_ERR_DEVICE, "verify: exception");
+  }
+}
+
+int mtg_kv_write(mtg_ctx* ctx, const void* k, const void* v, int32_t n_pos) {
+  if (!ctx) return MTG_ERR_INVALID;
+  return ctx->impl.kv_io(const_cast<void*>(k), const_cast<void*>(v), n_pos, true);
+}
+
+int mtg_kv_read(mtg_ctx* ctx, void* k, void* v, int32_t n_pos) {
+  if (!ctx) return MTG_ERR_INVALID;
+  return ctx->impl.kv_io(k, v, n_pos, false);
+}
+
+// cpu_ngram_draft (src/cpu_speculative.cpp:45-56).
+int32_t mtg_ngram_draft(const int32_t* h, int32_t size, int32_t maximum, int32_t* out) {
+  if (!h || !out || maximum <= 0 || size < 3) return 0;
+  for (int n = std::min<int>(16, size - 1); n >= 2; --n)
+    for (int start = size - n - 1; start >= 0; --start)
+      if (std::equal(h + size - n, h + size, h + start)) {
+        const int begin = start + n, count = std::min<int>(maximum, size - begin);
+        std::copy(h + begin, h + begin + count, out);
+        return count;
+      }
+  return 0;
+}
+
+// cpu_greedy_choice (src/cpu_speculative.cpp:57-68).
+int32_t mtg_greedy_choice(const float* raw, int32_t n, const int32_t* history, int32_t nh,
+                          float penalty) {
+  if (!raw || n <= 0) return -1;
+  auto value = [&](int i) { return raw[i]; };
+  if (!(penalty > 1.0f)) {
+    int best = 0;
+    for (int i = 1; i < n; ++i)
+      if (value(i) > value(best)) best = i;
+    return best;
+  }
+  std::vector<float> adj(raw, raw + n);
+  std::set<int32_t> recent;
+  for (int i = std::max(0, nh - 100); i < nh; ++i) recent.insert(history[i]);
+  for (int32_t id : recent)
+    if (id >= 0 && id < n) adj[id] = adj[id] > 0 ? adj[id] / penalty : adj[id] * penalty;
+  int best = 0;
+  for (int i = 1; i < n; ++i)
+    if (adj[i] > adj[best]) best = i;
+  return best;
+}
+
+// The loop of cpu_speculative_generate (src/cpu_speculative.cpp:118-155) on the
+// device decoder. Differences: the draft width is a parameter (the reference
+// fixes 4), and all T logits rows come from one lm_head pass with on-device
+// choices instead of one lazily computed row at a time; the accepted tokens, the
+// kept KV rows and the rewinds are the same.
+int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
+                      int32_t max_new, int32_t max_steps, int32_t eos, float penalty,
+                      int32_t max_draft, mtg_draft_fn draft, mtg_commit_fn commit, void* user,
+                      int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats) {
+  if (!ctx) return MTG_ERR_INVALID;
+  Ctx& c = ctx->impl;
+  if (!ids_out || !n_ids_out || max_new <= 0 || first_seed < 0 || first_seed >= c.hp.vocab)
+    return c.fail(MTG_ERR_INVALID, "generate: bad arguments");
+  try {
+    penalty = std::max(1.0f, std::min(1.5f, penalty));
+    max_draft = std::max(0, std::min(max_draft, MTG_MAX_BATCH - 1));
+    std::vector<int32_t> ids(prior_ids, prior_ids + (prior_ids ? n_prior : 0));
+    const size_t first_new = ids.size();
+    ids.reserve(first_new + (size_t)max_new);
+    mtg_gen_stats st{};
+    int stop = 0;
+    auto emit = [&](int32_t id) {
+      ids.push_back(id);
+      if (id == eos) stop = 1;
+      else if ((int)(ids.size() - first_new) >= max_new) stop = 2;
+    };
+    int32_t proposal[MTG_MAX_BATCH], choice[MTG_MAX_BATCH], inputs[MTG_MAX_BATCH];
+    int32_t raw_choice = first_seed;
+    int steps = 0, rc = MTG_OK;
+    while (!stop) {
+      if (max_steps > 0 && steps >= max_steps) break;
+      const int32_t seed = raw_choice;
+      emit(seed);
+      if (stop) {
+        if (commit) commit(user, ids.data(), (int)ids.size(), c.past, 1);
+        break;
+      }
+      const int before = c.past;
+      const int budget = std::max(0, std::min({max_draft, max_new - (int)(ids.size() - first_new),
+                                               c.max_seq - c.past - 1}));
+      auto t0 = std::chrono::steady_clock::now();
+      int np = draft ? draft(user, ids.data(), (int)ids.size(), budget, proposal)
+                     : mtg_ngram_draft(ids.data(), (int)ids.size(), budget, proposal);
+      st.draft_seconds += seconds_since(t0);
+      np = std::max(0, std::min(np, budget));
+      for (int i = 0; i < np; ++i)
+        if (proposal[i] < 0 || proposal[i] >= c.hp.vocab) {
+          rc = c.fail(MTG_ERR_INVALID, "invalid draft token %d", proposal[i]);
+          break;
+        }
+      if (rc) break;
+      inputs[0] = seed;
+      std::copy(proposal, proposal + np, inputs + 1);
+      int32_t n_match = 0;
+      t0 = std::chrono::steady_clock::now();
+      rc = c.verify(inputs, np + 1, ids.data(), (int)ids.size() - 1, penalty, choice, &n_match,
+                    nullptr, nullptr);
+      st.verify_seconds += seconds_since(t0);
+      if (rc) break;
+      ++steps;
+      ++st.target_calls;
+      st.drafted_calls += np > 0;
+      st.proposed += np;
+      st.target_input_tokens += np + 1;
+      int keep = 1;
+      raw_choice = choice[0];
+      for (int i = 0; i < np && i < n_match; ++i) {
+        ++st.accepted;
+        emit(proposal[i]);
+        if (stop) break;  // the terminating token is emitted, not kept
+        ++keep;
+        raw_choice = choice[i + 1];
+      }
+      const int position = before + keep;
+      if (c.past != position) {
+        c.past = position;
+        ++st.rewinds;
+      }
+      if (commit) commit(user, ids.data(), (int)ids.size(), c.past, stop != 0);
+    }
+    st.stop_reason = stop;
+    st.next_seed = raw_choice;
+    const int n_new = (int)(ids.size() - first_new);
+    std::copy(ids.begin() + first_new, ids.end(), ids_out);
+    *n_ids_out = n_new;
+    if (stats) *stats = st;
+    return rc;
+  } catch (...) {
+    return c.fail(MTG_ERR_DEVICE, "generate: exception");
+  }
+}
+
+int mtg_generate(mtg_ctx* ctx, const float* fused, int32_t seq, int32_t max_new, int32_t eos,
+                 float penalty, int32_t max_draft, mtg_draft_fn draft, mtg_commit_fn commit,
+                 void* user, int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats) {
+  if (!ctx) return MTG_ERR_INVALID;
+  Ctx& c = ctx->impl;
+  if (!fused || seq <= 0 || max_new <= 0 || !ids_out || !n_ids_out)
+    return c.fail(MTG_ERR_INVALID, "generate: bad arguments");
+  try {
+    const int H = c.hp.hidden;
+    auto t0 = std::chrono::steady_clock::now();
+    std::vector<float> hidden((size_t)seq * H);
+    int rc = mtg_prefill(ctx, fused, seq, hidden.data());
+    if (rc) return rc;
+    std::vector<float> raw(c.hp.vocab);
+    if ((rc = c.logits_of(hidden.data() + (size_t)(seq - 1) * H, 1, raw.data()))) return rc;
+    const double prefill_s = seconds_since(t0);
+    const int32_t first = mtg_greedy_choice(raw.data(), c.hp.vocab, nullptr, 0, 1.0f);
+    rc = mtg_generate_from(ctx, first, nullptr, 0, max_new, 0, eos, penalty, max_draft, draft,
+                           commit, user, ids_out, n_ids_out, stats);
+    if (stats) stats->prefill_seconds = prefill_s;
+    return rc;
+  } catch (...) {
+    return c.fail(MTG_ERR_DEVICE, "generate: exception");
+  }
+}
+
+// Draft hook used by the long-context workloads: n-gram proposal over
+// prompt ++ ids (the reference drafter), completed from a seeded periodic token
+// stream aligned to the absolute position of the next token.
+int32_t mtg_stream_draft(void* user, const int32_t* ids, int32_t n_ids, int32_t budget,
+                         int32_t* out) {
+  const mtg_stream_drafter* d = (const mtg_stream_drafter*)user;
+  if (!d || budget <= 0) return 0;
+  std::vector<int32_t> hist(d->prompt, d->prompt + d->n_prompt);
+  hist.insert(hist.end(), ids, ids + n_ids);
+  int n = mtg_ngram_draft(hist.data(), (int)hist.size(), budget, out);
+  if (d->period > 0)
+    for (; n < budget; ++n) out[n] = d->stream[(size_t)(hist.size() + n) % (size_t)d->period];
+  return n;
+}
+
+// ---- kernel-level entry points ----
+struct mtg_q8_packed {
+  uint8_t* tiles = nullptr;
+  int k = 0, n = 0;
+};
+
+int mtg_q8_pack(const void* blocks, int32_t k, int32_t n, mtg_q8_packed** out) {
+  if (!blocks || !out || k <= 0 || n <= 0) return MTG_ERR_INVALID;
+  if (k % 64 || n % 16) return MTG_ERR_UNSUPPORTED;
+  auto* p = new (std::nothrow) mtg_q8_packed();
+  if (!p) return MTG_ERR_NOMEM;
+  p->k = k;
+  p->n = n;
+  const size_t raw = (size_t)n * (k / 32) * 34, tiles = (size_t)(n / 16) * (k / 64) * mtg::kUnitBytes;
+  uint8_t* staging = nullptr;
+  if (hipMalloc(&staging, raw) != hipSuccess || hipMalloc(&p->tiles, tiles) != hipSuccess ||
+      hipMemcpy(staging, blocks, raw, hipMemcpyHostToDevice) != hipSuccess) {
+    hipFree(staging);
+    hipFree(p->tiles);
+    delete p;
+    return MTG_ERR_DEVICE;
+  }
+  mtg::launch_q8_retile(nullptr, staging, n, k, p->tiles);
+  const hipError_t e = hipDeviceSynchronize();
+  hipFree(staging);
+  if (e != hipSuccess) {
+    hipFree(p->tiles);
+    delete p;
+    return MTG_ERR_DEVICE;
+  }
+  *out = p;
+  return MTG_OK;
+}
+
+void mtg_q8_free(mtg_q8_packed* p) {
+  if (!p) return;
+  hipFree(p->tiles);
+  delete p;
+}
+
+int mtg_q8_mul_mat_dev(const mtg_q8_packed* w, const float* x_dev, int32_t T, float* y_dev) {
+  if (!w || !x_dev || !y_dev || T <= 0 || T > MTG_MAX_BATCH) return MTG_ERR_INVALID;
+  mtg::StepDesc host{};
+  host.T = T;
+  host.groups = (T + 7) / 8;
+  mtg::StepDesc* desc = nullptr;
+  mtg::Panel panel{};
+  const size_t pairs = (size_t)w->k / 64;
+  if (hipMalloc(&desc, sizeof(host)) != hipSuccess) return MTG_ERR_DEVICE;
+  if (hipMalloc(&panel.codes, mtg::kMaxGroups * pairs * 1024) != hipSuccess ||
+      hipMalloc(&panel.scales, mtg::kMaxGroups * pairs * 64) != hipSuccess) {
+    hipFree(desc);
+    hipFree(panel.codes);
+    return MTG_ERR_DEVICE;
+  }
+  hipError_t e = hipMemcpy(desc, &host, sizeof(host), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemset(panel.codes, 0, mtg::kMaxGroups * pairs * 1024);
+  if (e == hipSuccess) {
+    mtg::launch_norm_quant(nullptr, desc, x_dev, w->k, nullptr, 0.0f, panel, nullptr);
+    mtg::launch_gemm_store(nullptr, host.groups, desc, w->tiles, w->n, w->k, panel, y_dev);
+    e = hipDeviceSynchronize();
+  }
+  hipFree(desc);
+  hipFree(panel.codes);
+  hipFree(panel.scales);
+  return e == hipSuccess ? MTG_OK : MTG_ERR_DEVICE;
+}
+
+int mtg_causal_context_dev(const float* v_dev, const float* p_dev, int32_t head_dim,
+                           int32_t kv_heads, int32_t heads, int32_t queries, int32_t kv_len,
+                           float* out_dev) {
+  if (!v_dev || !p_dev || !out_dev || head_dim <= 0 || kv_heads <= 0 || heads <= 0 ||
+      heads % kv_heads || queries < 2 || kv_len <= queries)
+    return MTG_ERR_UNSUPPORTED;  // the reference's cpu_causal_context returns nullptr here
+  mtg::launch_causal_context(nullptr, v_dev, p_dev, head_dim, kv_heads, heads, queries, kv_len,
+                             out_dev);
+  return hipDeviceSynchronize() == hipSuccess ? MTG_OK : MTG_ERR_DEVICE;
+}
+
+}  // extern "C"

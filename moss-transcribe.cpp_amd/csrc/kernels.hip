@@ -1,0 +1,760 @@
+// kernels.hip - gfx950 kernels of the speculative verify step.
+//
+// Reference ops replaced (moss-transcribe.cpp, via ggml's CPU backend):
+//   k_embed            get_rows / embed_rows_f32             src/generate.cpp:68-111
+//   k_norm_quant       rms_norm * gain, then the q8_0 activation conversion of
+//                      mul_mat (vec_dot_type Q8_0)            src/qwen3.cpp:27-30,80,196
+//   k_gemm_*           mul_mat(q8_0 W, f32 x) (+ add / silu*mul)
+//                                                             src/qwen3.cpp:92-97,192-193,204-216
+//   k_qk_rope_append   q/k rms_norm, rope_ext NEOX, cpy into the cache views
+//                                                             src/qwen3.cpp:105-139
+//   k_attn_split/combine  scores (F32), soft_max_ext(mask, 1/sqrt(hd)),
+//                      causal context at the valid length    src/qwen3.cpp:172-189,
+//                                                             src/cpu_context.cpp:13-32
+//   k_lm_head + k_accept  tied lm_head, cpu_greedy_choice, the accept loop
+//                                                             src/qwen3_decoder.cpp:174-205,
+//                                                             src/cpu_speculative.cpp:57-68,142-148
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "kernels.hpp"
+
+namespace mtg {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+namespace {
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// q8_0 activation conversion of one 32-element block held by 8 consecutive lanes
+// (4 elements each): d = amax/127 rounded to f16, codes = rint(x * 127/amax).
+// Returns the f32 value of the stored f16 scale.
+__device__ __forceinline__ float quant_block8(const float v[4], int8_t q[4]) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+  const float d = __fdiv_rn(amax, 127.0f);
+  const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+  for (int e = 0; e < 4; ++e) q[e] = (int8_t)rintf(__fmul_rn(v[e], id));
+  return __half2float(__float2half_rn(d));
+}
+
+// Panel position of element k of verify row t (see mtg_internal.hpp).
+__device__ __forceinline__ void panel_store4(Panel p, int bps, int t, int k, const int8_t q[4]) {
+  const int b = k >> 5, bp = b >> 1, par = b & 1, half = (k >> 4) & 1, byte = k & 15;
+  const int cg = t >> 3, j = par * 8 + (t & 7), g = 2 * par + half, lane = j + 16 * g;
+  uint32_t packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
+                    ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
+  *(uint32_t*)(p.codes + ((size_t)(cg * bps + bp)) * 1024 + lane * 16 + byte) = packed;
+}
+__device__ __forceinline__ void panel_store_scale(Panel p, int bps, int t, int block, float d) {
+  const int bp = block >> 1, par = block & 1, cg = t >> 3, j = par * 8 + (t & 7);
+  p.scales[(size_t)(cg * bps + bp) * 16 + j] = d;
+}
+
+// ------------------------------------------------------------- embed -------
+__global__ void k_embed(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ tiles,
+                        int hidden, const float* __restrict__ host_rows, float* __restrict__ x) {
+  const int t = blockIdx.x;
+  if (t >= desc->T) return;
+  float* xr = x + (size_t)t * hidden;
+  if (desc->use_embeds) {
+    for (int k = threadIdx.x; k < hidden; k += blockDim.x) xr[k] = host_rows[(size_t)t * hidden + k];
+    return;
+  }
+  const int n = desc->tokens[t];
+  const int bps = hidden / kPairK, tile = n >> 4, r = n & 15;
+  for (int k = threadIdx.x; k < hidden; k += blockDim.x) {
+    const int b = k >> 5, bp = b >> 1, par = b & 1, half = (k >> 4) & 1;
+    const uint8_t* unit = tiles + ((size_t)tile * bps + bp) * kUnitBytes;
+    const int lane = r + 16 * (2 * par + half);
+    const int8_t q = (int8_t)unit[lane * 16 + (k & 15)];
+    const float d = half_bits_to_float(((const uint16_t*)(unit + 1024))[par * 16 + r]);
+    xr[k] = d * (float)q;  // dequantize_row_q8_0
+  }
+}
+
+// --------------------------------------------------------- norm+quant -------
+// One workgroup per verify row; 256 threads, 8 lanes per 32-block.
+__global__ void k_norm_quant(const StepDesc* __restrict__ desc, const float* __restrict__ src,
+                             int K, const float* __restrict__ gain, float eps, Panel panel,
+                             float* __restrict__ normed_out) {
+  const int t = blockIdx.x;
+  if (t >= desc->T) return;
+  const float* xr = src + (size_t)t * K;
+  const int tid = threadIdx.x;
+  __shared__ double red[4];
+  float scale = 1.0f;
+  if (gain) {
+    double s = 0.0;
+    for (int k = tid; k < K; k += 256) {
+      const float v = xr[k];
+      s += (double)__fmul_rn(v, v);
+    }
+    s = wave_sum_d(s);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float mean = (float)(tot / (double)K);
+    scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+  }
+  const int bps = K / kPairK;
+  for (int base = 0; base < K; base += 1024) {
+    const int k0 = base + tid * 4;  // K is a multiple of 1024 or of 256 below
+    if (k0 >= K) break;             // whole 8-lane groups leave together (K % 32 == 0)
+    float v[4];
+    for (int e = 0; e < 4; ++e) {
+      float y = xr[k0 + e];
+      if (gain) y = __fmul_rn(__fmul_rn(y, scale), gain[k0 + e]);
+      v[e] = y;
+    }
+    if (normed_out)
+      for (int e = 0; e < 4; ++e) normed_out[(size_t)t * K + k0 + e] = v[e];
+    int8_t q[4];
+    const float d = quant_block8(v, q);
+    panel_store4(panel, bps, t, k0, q);
+    if ((tid & 7) == 0) panel_store_scale(panel, bps, t, k0 >> 5, d);
+  }
+}
+
+// ----------------------------------------------------------- GEMM core ------
+// One wave accumulates a 16-row tile over block pairs [bp0, bp1) for every
+// column group: acc[cg][r] holds rows 4*(lane/16)+r of column lane%16, split by
+// block parity (columns 0-7 even blocks, 8-15 odd blocks of rows t = col%8).
+template <int G>
+__device__ __forceinline__ void tile_accumulate(const uint8_t* __restrict__ tile, int bp0, int bp1,
+                                                const uint8_t* __restrict__ pcodes,
+                                                const float* __restrict__ pscales, int bps,
+                                                float acc[G][4]) {
+  const int lane = threadIdx.x & 63;
+  const int par = (lane & 15) >> 3;
+  const int srow = par * 16 + 4 * (lane >> 4);
+  const v4i zero = {0, 0, 0, 0};
+#pragma unroll 4
+  for (int bp = bp0; bp < bp1; ++bp) {
+    const uint8_t* unit = tile + (size_t)bp * kUnitBytes;
+    const v4i a = *(const v4i*)(unit + lane * 16);
+    const uint2 sw = *(const uint2*)(unit + 1024 + srow * 2);
+    float dw[4];
+    dw[0] = half_bits_to_float((uint16_t)(sw.x & 0xffff));
+    dw[1] = half_bits_to_float((uint16_t)(sw.x >> 16));
+    dw[2] = half_bits_to_float((uint16_t)(sw.y & 0xffff));
+    dw[3] = half_bits_to_float((uint16_t)(sw.y >> 16));
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg) {
+      const v4i b = *(const v4i*)(pcodes + ((size_t)(cg * bps + bp)) * 1024 + lane * 16);
+      const float dx = pscales[(size_t)(cg * bps + bp) * 16 + (lane & 15)];
+      const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, zero, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[cg][r] = fmaf((float)c[r], dw[r] * dx, acc[cg][r]);
+    }
+  }
+}
+
+// Split-K GEMM over one tile per workgroup: SPLIT waves each take a slice of
+// the block pairs; partial sums meet in LDS in wave order (deterministic).
+// EPI 0: store, 1: residual add, 2: swiglu (second matrix in w2).
+template <int EPI, int SPLIT, int G>
+__global__ void __launch_bounds__(SPLIT * 64)
+k_gemm(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w,
+       const uint8_t* __restrict__ w2, int n, int bps, Panel x, float* __restrict__ out) {
+  const int T = desc->T;
+  if ((T + 7) / 8 != G) return;  // launched once per supported group count
+  const int tile = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int bp0 = (bps * wave) / SPLIT, bp1 = (bps * (wave + 1)) / SPLIT;
+  constexpr int NM = EPI == 2 ? 2 : 1;
+  float acc[NM][G][4];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[m][cg][r] = 0.0f;
+  tile_accumulate<G>(w + (size_t)tile * bps * kUnitBytes, bp0, bp1, x.codes, x.scales, bps, acc[0]);
+  if (EPI == 2)
+    tile_accumulate<G>(w2 + (size_t)tile * bps * kUnitBytes, bp0, bp1, x.codes, x.scales, bps,
+                       acc[NM - 1]);
+  __shared__ float red[SPLIT > 1 ? SPLIT : 1][NM * G * 4][64];
+  if (SPLIT > 1) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][(m * G + cg) * 4 + r][lane] = acc[m][cg][r];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float s = red[0][(m * G + cg) * 4 + r][lane];
+          for (int wv = 1; wv < SPLIT; ++wv) s += red[wv][(m * G + cg) * 4 + r][lane];
+          acc[m][cg][r] = s;
+        }
+  }
+  // even + odd block halves of the same (row, t)
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[m][cg][r] += __shfl_xor(acc[m][cg][r], 8, 64);
+  if ((lane & 15) >= 8) return;
+#pragma unroll
+  for (int cg = 0; cg < G; ++cg) {
+    const int t = cg * 8 + (lane & 7);
+    if (t >= T) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = tile * 16 + 4 * (lane >> 4) + r;
+      float* dst = out + (size_t)t * n + row;
+      if (EPI == 0) {
+        *dst = acc[0][cg][r];
+      } else if (EPI == 1) {
+        *dst = *dst + acc[0][cg][r];
+      } else {
+        const float g = acc[0][cg][r], u = acc[NM - 1][cg][r];
+        const float silu = g / (1.0f + expf(-g));
+        *dst = silu * u;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------- q/k norm, rope, append ---
+// grid (16 rows, n_heads + 2*n_kv_heads units), one wave per unit; lane i owns
+// the NEOX pair (i, i + 64) of head_dim 128.
+__global__ void __launch_bounds__(64)
+k_qk_rope_append(const StepDesc* __restrict__ desc, const float* __restrict__ qkv, int n_heads,
+                 int n_kv_heads, const float* __restrict__ q_norm,
+                 const float* __restrict__ k_norm, float eps, const float* __restrict__ rope,
+                 float* __restrict__ q_out, KvLayer kv) {
+  const int t = blockIdx.x;
+  if (t >= desc->T) return;
+  const int u = blockIdx.y, i = threadIdx.x;
+  const int QN = n_heads * kHeadDim, KN = n_kv_heads * kHeadDim, N = QN + 2 * KN;
+  const int pos = desc->past + t;
+  const float* row = qkv + (size_t)t * N;
+  float x0, x1;
+  const bool is_q = u < n_heads, is_k = !is_q && u < n_heads + n_kv_heads;
+  const int col = is_q ? u * kHeadDim : is_k ? QN + (u - n_heads) * kHeadDim
+                                             : QN + KN + (u - n_heads - n_kv_heads) * kHeadDim;
+  x0 = row[col + i];
+  x1 = row[col + i + 64];
+  if (is_q || is_k) {
+    const float* g = is_q ? q_norm : k_norm;
+    double s = (double)__fmul_rn(x0, x0) + (double)__fmul_rn(x1, x1);
+    s = wave_sum_d(s);
+    const float mean = (float)(s / (double)kHeadDim);
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    const float y0 = __fmul_rn(__fmul_rn(x0, scale), g[i]);
+    const float y1 = __fmul_rn(__fmul_rn(x1, scale), g[i + 64]);
+    const float c = rope[(size_t)pos * kHeadDim + 2 * i], sn = rope[(size_t)pos * kHeadDim + 2 * i + 1];
+    x0 = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, sn));
+    x1 = __fadd_rn(__fmul_rn(y0, sn), __fmul_rn(y1, c));
+  }
+  if (is_q) {
+    float* q = q_out + ((size_t)t * n_heads + u) * kHeadDim;
+    q[i] = x0;
+    q[i + 64] = x1;
+    return;
+  }
+  const int h = is_k ? u - n_heads : u - n_heads - n_kv_heads;
+  void* base = is_k ? kv.k : kv.v;
+  const size_t off = ((size_t)h * kv.max_seq + pos) * kHeadDim;
+  if (kv.f16) {
+    __half* p = (__half*)base + off;
+    p[i] = __float2half_rn(x0);
+    p[i + 64] = __float2half_rn(x1);
+  } else {
+    float* p = (float*)base + off;
+    p[i] = x0;
+    p[i + 64] = x1;
+  }
+}
+
+// -------------------------------------------------------------- attention --
+// Split-KV GQA attention on v_mfma_f32_16x16x4f32. One workgroup = (kv head g,
+// split s), kAttnWaves waves; each wave takes 16-key tiles round-robin.
+// Query columns (16 per group cg): col j -> q head 2g + j/8, row t = 8*cg + j%8.
+// S^T = K . Q^T per tile (keys x queries), online softmax per column, then
+// O^T += V^T . P^T with P^T taken straight from the S^T accumulator layout.
+__device__ __forceinline__ float kv_load(const void* base, int f16, size_t idx) {
+  return f16 ? __half2float(((const __half*)base)[idx]) : ((const float*)base)[idx];
+}
+__device__ __forceinline__ v4f kv_load4(const void* base, int f16, size_t idx) {
+  if (f16) {
+    const uint2 raw = *(const uint2*)((const __half*)base + idx);
+    v4f r;
+    r[0] = half_bits_to_float((uint16_t)(raw.x & 0xffff));
+    r[1] = half_bits_to_float((uint16_t)(raw.x >> 16));
+    r[2] = half_bits_to_float((uint16_t)(raw.y & 0xffff));
+    r[3] = half_bits_to_float((uint16_t)(raw.y >> 16));
+    return r;
+  }
+  return *(const v4f*)((const float*)base + idx);
+}
+
+__global__ void __launch_bounds__(kAttnWaves * 64)
+k_attn_split(const StepDesc* __restrict__ desc, const float* __restrict__ q, int n_heads,
+             KvLayer kv, AttnWork work) {
+  const int g = blockIdx.x, split = blockIdx.y;
+  const int T = desc->T, past = desc->past, kvlen = past + T;
+  const int G = (T + 7) / 8;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int j = lane & 15, lg = lane >> 4;
+  const float scale = 1.0f / sqrtf((float)kHeadDim);
+  const size_t head_base = (size_t)g * kv.max_seq * kHeadDim;
+  const int ntiles = (kvlen + 15) / 16;
+  const int t0 = (ntiles * split) / kAttnSplits, t1 = (ntiles * (split + 1)) / kAttnSplits;
+  const bool f16kv = kv.f16 != 0;
+  __shared__ float s_m[kAttnWaves][16], s_l[kAttnWaves][16];
+  __shared__ float s_o[16][kHeadDim + 4];
+  for (int cg = 0; cg < G; ++cg) {
+    // this lane's query column
+    const int t = cg * 8 + (j & 7), hq = 2 * g + (j >> 3);
+    const bool qvalid = t < T;
+    v4f qf[8];
+    const float* qrow = q + ((size_t)(qvalid ? t : 0) * n_heads + hq) * kHeadDim;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      qf[c] = *(const v4f*)(qrow + 16 * c + 4 * lg);
+      if (f16kv)  // mul_mat(f16 K, f32 q) converts q to f16 first
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qf[c][e] = __half2float(__float2half_rn(qf[c][e]));
+    }
+    float m_run = -INFINITY, l_run = 0.0f;
+    v4f o[8];
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) o[cb] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int tile = t0 + wave; tile < t1; tile += kAttnWaves) {
+      const int key0 = tile * 16;
+      // S^T tile: A = K[key0 + j][perm d], B = Q^T[perm d][col j]
+      const int kk = min(key0 + j, kvlen - 1);
+      v4f s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const v4f kf = kv_load4(kv.k, kv.f16, head_base + (size_t)kk * kHeadDim + 16 * c + 4 * lg);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[e], qf[c][e], s, 0, 0, 0);
+      }
+      // lane holds S^T[key0 + 4*lg + r][col j]
+      float w[4], tmax = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = key0 + 4 * lg + r;
+        const bool ok = qvalid && key < kvlen && key <= past + t;
+        w[r] = ok ? s[r] * scale : -INFINITY;
+        tmax = fmaxf(tmax, w[r]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_new == -INFINITY ? 1.0f : expf(m_run - m_new);
+      float p[4], psum = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = w[r] == -INFINITY ? 0.0f : expf(w[r] - m_new);
+        if (f16kv) p[r] = __half2float(__float2half_rn(p[r]));
+        psum += p[r];
+      }
+      psum += __shfl_xor(psum, 16, 64);
+      psum += __shfl_xor(psum, 32, 64);
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) o[cb] *= alpha;
+      // O^T += V^T . P^T: step r uses key key0 + 4*lg + r from every lane group;
+      // lane (row i = j) loads V[key][4i..4i+3] and V[key][64+4i..+3]: component e
+      // of the first load is output block e (d = 4i+e), of the second block 4+e.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = min(key0 + 4 * lg + r, kvlen - 1);
+        const size_t vb = head_base + (size_t)key * kHeadDim + 4 * j;
+        const v4f v0 = kv_load4(kv.v, kv.f16, vb);
+        const v4f v1 = kv_load4(kv.v, kv.f16, vb + 64);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0[e], p[r], o[e], 0, 0, 0);
+          o[4 + e] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1[e], p[r], o[4 + e], 0, 0, 0);
+        }
+      }
+    }
+    // combine the waves of this workgroup (fixed order)
+    if (lg == 0) {
+      s_m[wave][j] = m_run;
+      s_l[wave][j] = l_run;
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int wv = 0; wv < kAttnWaves; ++wv) M = fmaxf(M, s_m[wv][j]);
+    const float myscale = (M == -INFINITY || m_run == -INFINITY) ? 0.0f : expf(m_run - M);
+    for (int wv = 0; wv < kAttnWaves; ++wv) {
+      if (wave == wv) {
+        // lane holds O^T rows (within block cb) 4*lg + r -> d = 4*(4*lg+r) + cb (cb<4)
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int d = (cb < 4) ? 4 * (4 * lg + r) + cb : 64 + 4 * (4 * lg + r) + (cb - 4);
+            const float val = o[cb][r] * myscale;
+            s_o[j][d] = wv == 0 ? val : s_o[j][d] + val;
+          }
+      }
+      __syncthreads();
+    }
+    // write the workgroup partial: (M, L) and O for the 16 columns
+    const size_t pbase = (((size_t)g * kAttnSplits + split) * kMaxGroups + cg) * 16;
+    if (threadIdx.x < 16) {
+      const int col = threadIdx.x;
+      float Mc = -INFINITY, L = 0.0f;
+      for (int wv = 0; wv < kAttnWaves; ++wv) Mc = fmaxf(Mc, s_m[wv][col]);
+      for (int wv = 0; wv < kAttnWaves; ++wv) {
+        const float mw = s_m[wv][col];
+        if (mw != -INFINITY) L += s_l[wv][col] * expf(mw - Mc);
+      }
+      work.part_ml[(pbase + col) * 2 + 0] = Mc;
+      work.part_ml[(pbase + col) * 2 + 1] = L;
+    }
+    for (int idx = threadIdx.x; idx < 16 * kHeadDim; idx += blockDim.x) {
+      const int col = idx / kHeadDim, d = idx % kHeadDim;
+      work.part_o[(pbase + col) * kHeadDim + d] = s_o[col][d];
+    }
+    __syncthreads();
+  }
+}
+
+// grid (n_heads, 16 rows), 128 threads (one per d). Merges the splits of one
+// (head, row), writes o (f32) and its q8_0 panel for the o-projection.
+__global__ void __launch_bounds__(128)
+k_attn_combine(const StepDesc* __restrict__ desc, AttnWork work, int n_heads, Panel o_panel,
+               float* __restrict__ o_out) {
+  const int hq = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+  if (t >= desc->T) return;
+  const int g = hq / 2, col = (hq & 1) * 8 + (t & 7), cg = t >> 3;
+  float M = -INFINITY;
+  for (int s = 0; s < kAttnSplits; ++s) {
+    const size_t pb = (((size_t)g * kAttnSplits + s) * kMaxGroups + cg) * 16 + col;
+    M = fmaxf(M, work.part_ml[pb * 2]);
+  }
+  float L = 0.0f, acc = 0.0f;
+  for (int s = 0; s < kAttnSplits; ++s) {
+    const size_t pb = (((size_t)g * kAttnSplits + s) * kMaxGroups + cg) * 16 + col;
+    const float m = work.part_ml[pb * 2];
+    if (m == -INFINITY) continue;
+    const float f = expf(m - M);
+    L += work.part_ml[pb * 2 + 1] * f;
+    acc += work.part_o[pb * kHeadDim + d] * f;
+  }
+  const float val = acc / L;
+  const int QN = n_heads * kHeadDim;
+  o_out[(size_t)t * QN + hq * kHeadDim + d] = val;
+  // q8_0 conversion of this head's 4 blocks: lanes 4*i..4*i+3 own d
+  __shared__ float s_v[kHeadDim];
+  s_v[d] = val;
+  __syncthreads();
+  if (d < 32) {
+    float v[4];
+    for (int e = 0; e < 4; ++e) v[e] = s_v[d * 4 + e];
+    int8_t qv[4];
+    const float ds = quant_block8(v, qv);
+    const int k = hq * kHeadDim + d * 4;
+    panel_store4(o_panel, QN / kPairK, t, k, qv);
+    if ((d & 7) == 0) panel_store_scale(o_panel, QN / kPairK, t, k >> 5, ds);
+  }
+}
+
+// ------------------------------------------------------- penalty bitmap -----
+__global__ void k_penalty_bitmap(const StepDesc* __restrict__ desc, int vocab,
+                                 uint32_t* __restrict__ bitmap) {
+  const int t = blockIdx.x;
+  if (t >= desc->T || !(desc->penalty > 1.0f)) return;
+  const int words = (vocab + 31) / 32;
+  uint32_t* row = bitmap + (size_t)t * words;
+  for (int i = threadIdx.x; i < words; i += blockDim.x) row[i] = 0u;
+  __syncthreads();
+  __threadfence_block();
+  const int end = desc->pen_base + t + 1;
+  const int begin = max(0, end - kPenaltyWindow);
+  for (int i = begin + (int)threadIdx.x; i < end; i += blockDim.x) {
+    const int id = desc->pen_ids[i];
+    if (id >= 0 && id < vocab) atomicOr(row + (id >> 5), 1u << (id & 31));
+  }
+}
+
+// --------------------------------------------------------------- lm_head ----
+// Grid-stride over 16-row tiles of the tied embedding; the activation panel is
+// staged in LDS once per workgroup. Each lane keeps the best (value, index) key
+// per verify row; ties keep the lowest index (first maximum).
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+  if (v == 0.0f) v = 0.0f;  // -0 and +0 compare equal in the reference
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+}
+
+template <int G>
+__global__ void __launch_bounds__(256)
+k_lm_head(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int vocab, int bps,
+          Panel x, const uint32_t* __restrict__ bitmap, float* __restrict__ logits,
+          uint64_t* __restrict__ part_keys) {
+  const int T = desc->T;
+  if ((T + 7) / 8 != G) return;
+  extern __shared__ v4i lds_v4[];  // 16-byte aligned for the 128-bit panel reads
+  uint8_t* lds = (uint8_t*)lds_v4;
+  uint8_t* lcodes = lds;
+  float* lscales = (float*)(lds + (size_t)G * bps * 1024);
+  for (int i = threadIdx.x; i < G * bps * 64; i += blockDim.x)
+    ((v4i*)lcodes)[i] = ((const v4i*)x.codes)[i];
+  for (int i = threadIdx.x; i < G * bps * 16; i += blockDim.x) lscales[i] = x.scales[i];
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n_tiles = vocab / 16;
+  const int nwaves = gridDim.x * 4;
+  const bool pen = desc->penalty > 1.0f;
+  const float penalty = desc->penalty;
+  const int words = (vocab + 31) / 32;
+  uint64_t best[G];
+#pragma unroll
+  for (int cg = 0; cg < G; ++cg) best[cg] = 0;
+  for (int tile = blockIdx.x * 4 + wave; tile < n_tiles; tile += nwaves) {
+    float acc[G][4];
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[cg][r] = 0.0f;
+    tile_accumulate<G>(w + (size_t)tile * bps * kUnitBytes, 0, bps, lcodes, lscales, bps, acc);
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[cg][r] += __shfl_xor(acc[cg][r], 8, 64);
+    if ((lane & 15) < 8) {
+#pragma unroll
+      for (int cg = 0; cg < G; ++cg) {
+        const int t = cg * 8 + (lane & 7);
+        if (t < T) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = tile * 16 + 4 * (lane >> 4) + r;
+            float v = acc[cg][r];
+            if (desc->write_logits) logits[(size_t)t * vocab + row] = v;
+            if (pen && ((bitmap[(size_t)t * words + (row >> 5)] >> (row & 31)) & 1u))
+              v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+            const uint64_t key = argmax_key(v, row);
+            best[cg] = key > best[cg] ? key : best[cg];
+          }
+        }
+      }
+    }
+  }
+  // lanes with the same row t: xor 16, 32 (and the odd-parity lanes hold 0)
+#pragma unroll
+  for (int cg = 0; cg < G; ++cg) {
+    uint64_t b = best[cg];
+    uint64_t o = shfl_xor_u64(b, 16);
+    b = o > b ? o : b;
+    o = shfl_xor_u64(b, 32);
+    b = o > b ? o : b;
+    o = shfl_xor_u64(b, 8);
+    b = o > b ? o : b;
+    best[cg] = b;
+  }
+  __shared__ uint64_t s_best[4][kMaxRows];
+  if (lane < 8)
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg) s_best[wave][cg * 8 + lane] = best[cg];
+  __syncthreads();
+  if (threadIdx.x < G * 8) {
+    uint64_t b = s_best[0][threadIdx.x];
+    for (int wv = 1; wv < 4; ++wv) b = s_best[wv][threadIdx.x] > b ? s_best[wv][threadIdx.x] : b;
+    part_keys[(size_t)blockIdx.x * kMaxRows + threadIdx.x] = b;
+  }
+}
+
+// ---------------------------------------------------------------- accept ----
+__global__ void __launch_bounds__(256)
+k_accept(const StepDesc* __restrict__ desc, const uint64_t* __restrict__ part_keys, int nparts,
+         StepResult* __restrict__ result) {
+  const int T = desc->T;
+  __shared__ uint64_t s_red[256];
+  __shared__ int32_t s_choice[kMaxRows];
+  for (int t = 0; t < T; ++t) {
+    uint64_t b = 0;
+    for (int i = threadIdx.x; i < nparts; i += 256) {
+      const uint64_t k = part_keys[(size_t)i * kMaxRows + t];
+      b = k > b ? k : b;
+    }
+    s_red[threadIdx.x] = b;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+      if (threadIdx.x < o) {
+        const uint64_t k = s_red[threadIdx.x + o];
+        if (k > s_red[threadIdx.x]) s_red[threadIdx.x] = k;
+      }
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) s_choice[t] = (int32_t)(0xffffffffu - (uint32_t)(s_red[0] & 0xffffffffu));
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    int m = 0;
+    while (m + 1 < T && desc->tokens[m + 1] == s_choice[m]) ++m;
+    for (int t = 0; t < kMaxRows; ++t) result->choice[t] = t < T ? s_choice[t] : -1;
+    result->n_match = m;
+  }
+}
+
+// ------------------------------------------------------ causal context -----
+// cpu_causal_context on device pointers: one thread per (head, query, f),
+// summing exactly the valid length in key order.
+__global__ void k_causal_context(const float* __restrict__ v, const float* __restrict__ p,
+                                 int head_dim, int kv_heads, int heads, int queries, int kv_len,
+                                 float* __restrict__ out) {
+  const size_t total = (size_t)heads * queries * head_dim;
+  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int f = (int)(i % head_dim), q = (int)((i / head_dim) % queries), h = (int)(i / ((size_t)head_dim * queries));
+  const int groups = heads / kv_heads, past = kv_len - queries;
+  const float* vr = v + (size_t)(h / groups) * kv_len * head_dim + f;
+  const float* pr = p + ((size_t)h * queries + q) * kv_len;
+  float acc = 0.0f;
+  for (int k = 0; k < past + q + 1; ++k) acc = __fadd_rn(acc, __fmul_rn(vr[(size_t)k * head_dim], pr[k]));
+  out[i] = acc;
+}
+
+// --------------------------------------------------------------- retile -----
+// ggml q8_0 rows (34-byte blocks) -> MFMA panel tiles. One thread per
+// (tile, pair, lane): 16 code bytes, and lanes < 32 also move one f16 scale.
+__global__ void k_q8_retile(const uint8_t* __restrict__ blocks, int n, int k,
+                            uint8_t* __restrict__ tiles) {
+  const int bps = k / kPairK, nb = k / 32;
+  const size_t units = (size_t)(n / 16) * bps;
+  const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (gid >= units * 64) return;
+  const int lane = (int)(gid & 63);
+  const size_t unit = gid >> 6;
+  const int tile = (int)(unit / bps), bp = (int)(unit % bps);
+  uint8_t* dst = tiles + unit * kUnitBytes;
+  {
+    const int row = tile * 16 + (lane & 15), g = lane >> 4;
+    const int block = 2 * bp + (g >> 1);
+    const uint8_t* src = blocks + ((size_t)row * nb + block) * 34 + 2 + (g & 1) * 16;
+    for (int b = 0; b < 16; ++b) dst[lane * 16 + b] = src[b];
+  }
+  if (lane < 32) {
+    const int par = lane >> 4, r = lane & 15;
+    const uint8_t* src = blocks + ((size_t)(tile * 16 + r) * nb + 2 * bp + par) * 34;
+    dst[1024 + (par * 16 + r) * 2] = src[0];
+    dst[1024 + (par * 16 + r) * 2 + 1] = src[1];
+  }
+}
+
+}  // namespace
+
+// ================================================================ launches ==
+void launch_embed(hipStream_t s, const StepDesc* desc, const uint8_t* embd_tiles, int hidden,
+                  const float* host_rows, float* x) {
+  hipLaunchKernelGGL(k_embed, dim3(kMaxRows), dim3(256), 0, s, desc, embd_tiles, hidden, host_rows, x);
+}
+
+void launch_norm_quant(hipStream_t s, const StepDesc* desc, const float* src, int K,
+                       const float* gain, float eps, Panel panel, float* normed_out) {
+  hipLaunchKernelGGL(k_norm_quant, dim3(kMaxRows), dim3(256), 0, s, desc, src, K, gain, eps, panel,
+                     normed_out);
+}
+
+template <int EPI, int SPLIT>
+static void gemm_launch(hipStream_t s, int G, const StepDesc* desc, const uint8_t* w,
+                        const uint8_t* w2, int n, int k, Panel x, float* out) {
+  const int tiles = n / 16, bps = k / kPairK;
+  if (G == 1)
+    hipLaunchKernelGGL((k_gemm<EPI, SPLIT, 1>), dim3(tiles), dim3(SPLIT * 64), 0, s, desc, w, w2, n,
+                       bps, x, out);
+  else
+    hipLaunchKernelGGL((k_gemm<EPI, SPLIT, 2>), dim3(tiles), dim3(SPLIT * 64), 0, s, desc, w, w2, n,
+                       bps, x, out);
+}
+
+void launch_gemm_store(hipStream_t s, int G, const StepDesc* desc, const uint8_t* w, int n, int k,
+                       Panel x, float* out) {
+  gemm_launch<0, 2>(s, G, desc, w, nullptr, n, k, x, out);
+}
+void launch_gemm_residual(hipStream_t s, int G, const StepDesc* desc, const uint8_t* w, int n,
+                          int k, Panel x, float* resid) {
+  gemm_launch<1, 8>(s, G, desc, w, nullptr, n, k, x, resid);
+}
+void launch_gemm_swiglu(hipStream_t s, int G, const StepDesc* desc, const uint8_t* wg,
+                        const uint8_t* wu, int n, int k, Panel x, float* act) {
+  gemm_launch<2, 4>(s, G, desc, wg, wu, n, k, x, act);
+}
+
+void launch_qk_rope_append(hipStream_t s, const StepDesc* desc, const float* qkv, int n_heads,
+                           int n_kv_heads, const float* q_norm, const float* k_norm, float eps,
+                           const float* rope, float* q_out, KvLayer kv) {
+  hipLaunchKernelGGL(k_qk_rope_append, dim3(kMaxRows, n_heads + 2 * n_kv_heads), dim3(64), 0, s,
+                     desc, qkv, n_heads, n_kv_heads, q_norm, k_norm, eps, rope, q_out, kv);
+}
+
+void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n_heads,
+                      int n_kv_heads, KvLayer kv, AttnWork work, Panel o_panel, float* o_out) {
+  hipLaunchKernelGGL(k_attn_split, dim3(n_kv_heads, kAttnSplits), dim3(kAttnWaves * 64), 0, s,
+                     desc, q, n_heads, kv, work);
+  hipLaunchKernelGGL(k_attn_combine, dim3(n_heads, kMaxRows), dim3(kHeadDim), 0, s, desc, work,
+                     n_heads, o_panel, o_out);
+}
+
+void launch_penalty_bitmap(hipStream_t s, const StepDesc* desc, int vocab, uint32_t* bitmap) {
+  hipLaunchKernelGGL(k_penalty_bitmap, dim3(kMaxRows), dim3(256), 0, s, desc, vocab, bitmap);
+}
+
+void launch_lm_head(hipStream_t s, int G, const StepDesc* desc, const uint8_t* w, int vocab,
+                    int k, Panel x, const uint32_t* bitmap, float* logits, uint64_t* part_keys) {
+  const int bps = k / kPairK;
+  const size_t lds = (size_t)G * bps * (1024 + 64);
+  if (G == 1)
+    hipLaunchKernelGGL(k_lm_head<1>, dim3(kLmWorkgroups), dim3(256), lds, s, desc, w, vocab, bps,
+                       x, bitmap, logits, part_keys);
+  else
+    hipLaunchKernelGGL(k_lm_head<2>, dim3(kLmWorkgroups), dim3(256), lds, s, desc, w, vocab, bps,
+                       x, bitmap, logits, part_keys);
+}
+
+void launch_accept(hipStream_t s, const StepDesc* desc, const uint64_t* part_keys,
+                   StepResult* result) {
+  hipLaunchKernelGGL(k_accept, dim3(1), dim3(256), 0, s, desc, part_keys, kLmWorkgroups, result);
+}
+
+void launch_causal_context(hipStream_t s, const float* v, const float* p, int head_dim,
+                           int kv_heads, int heads, int queries, int kv_len, float* out) {
+  const size_t total = (size_t)heads * queries * head_dim;
+  hipLaunchKernelGGL(k_causal_context, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, v, p,
+                     head_dim, kv_heads, heads, queries, kv_len, out);
+}
+
+void launch_q8_retile(hipStream_t s, const uint8_t* blocks, int n, int k, uint8_t* tiles) {
+  const size_t threads = (size_t)(n / 16) * (k / kPairK) * 64;
+  hipLaunchKernelGGL(k_q8_retile, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, blocks, n,
+                     k, tiles);
+}
+
+}  // namespace mtg

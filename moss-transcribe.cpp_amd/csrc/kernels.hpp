@@ -1,0 +1,62 @@
+// kernels.hpp - launch wrappers of the gfx950 kernels (defined in kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mtg_internal.hpp"
+
+namespace mtg {
+
+// Activation panel of one GEMM input (B operand, see mtg_internal.hpp).
+struct Panel {
+  uint8_t* codes;  // [group][pair][1024]
+  float* scales;   // [group][pair][16]
+};
+
+struct KvLayer {
+  void* k;  // [kv_head][max_seq][head_dim]
+  void* v;
+  int f16;
+  int max_seq;
+};
+
+struct AttnWork {
+  float* part_ml;  // [kv_head][split][group][16 cols][2]
+  float* part_o;   // [kv_head][split][group][16 cols][head_dim]
+};
+
+// x[t] = embeddings of desc->tokens (or the uploaded rows when desc->use_embeds).
+void launch_embed(hipStream_t s, const StepDesc* desc, const uint8_t* embd_tiles, int hidden,
+                  const float* host_rows, float* x);
+// panel <- q8_0(RMSNorm(src) * gain) (gain == nullptr: quantize src as is);
+// normed_out (nullable) receives the f32 normalized rows.
+void launch_norm_quant(hipStream_t s, const StepDesc* desc, const float* src, int K,
+                       const float* gain, float eps, Panel panel, float* normed_out);
+// out[t][n] = W . x[t] for all rows of a packed matrix (epilogue: store).
+void launch_gemm_store(hipStream_t s, int G, const StepDesc* desc, const uint8_t* w, int n, int k,
+                       Panel x, float* out);
+// x[t][n] += W . act[t] (o-proj and down-proj with residual).
+void launch_gemm_residual(hipStream_t s, int G, const StepDesc* desc, const uint8_t* w, int n, int k,
+                          Panel x, float* resid);
+// act[t][n] = silu(gate . x) * (up . x).
+void launch_gemm_swiglu(hipStream_t s, int G, const StepDesc* desc, const uint8_t* wg, const uint8_t* wu,
+                        int n, int k, Panel x, float* act);
+// q/k per-head RMSNorm + NEOX RoPE (host-built table), K/V append at past.
+void launch_qk_rope_append(hipStream_t s, const StepDesc* desc, const float* qkv, int n_heads,
+                           int n_kv_heads, const float* q_norm, const float* k_norm, float eps,
+                           const float* rope, float* q_out, KvLayer kv);
+void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n_heads,
+                      int n_kv_heads, KvLayer kv, AttnWork work, Panel o_panel, float* o_out);
+void launch_penalty_bitmap(hipStream_t s, const StepDesc* desc, int vocab, uint32_t* bitmap);
+void launch_lm_head(hipStream_t s, int G, const StepDesc* desc, const uint8_t* w, int vocab, int k,
+                    Panel x, const uint32_t* bitmap, float* logits, uint64_t* part_keys);
+void launch_accept(hipStream_t s, const StepDesc* desc, const uint64_t* part_keys,
+                   StepResult* result);
+// kernel-level entry points
+void launch_causal_context(hipStream_t s, const float* v, const float* p, int head_dim,
+                           int kv_heads, int heads, int queries, int kv_len, float* out);
+void launch_q8_retile(hipStream_t s, const uint8_t* blocks, int n, int k, uint8_t* tiles);
+
+}  // namespace mtg

@@ -1,0 +1,381 @@
+// runtime.cpp - device decoder state and the verify step (host side).
+//
+// Replaces Qwen3Decoder (src/qwen3_decoder.cpp:20-205) and the graph execution of
+// src/backend.cpp:216-240 for the verify path: weights are uploaded once and
+// re-tiled into MFMA panels, the KV cache stays resident in HBM, and one verify
+// step is a fixed kernel sequence replayed from a captured HIP graph (one graph per
+// column-group count and penalty mode); only the step descriptor goes in and
+// T + 2 ints come back per step.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "runtime.hpp"
+
+namespace mtg {
+
+namespace {
+
+size_t q8_tiles_bytes(int n, int k) { return (size_t)(n / 16) * (k / kPairK) * kUnitBytes; }
+
+}  // namespace
+
+Ctx::~Ctx() {
+  for (auto& g : graphs)
+    if (g.exec) hipGraphExecDestroy(g.exec);
+  for (void* p : allocations) hipFree(p);
+  if (desc_host) hipHostFree(desc_host);
+  if (result_host) hipHostFree(result_host);
+  if (stream) hipStreamDestroy(stream);
+}
+
+int Ctx::fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  error = buf;
+  return code;
+}
+
+int Ctx::check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MTG_OK;
+  return fail(MTG_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+void* Ctx::dalloc(size_t bytes, bool zero) {
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes ? bytes : 16) != hipSuccess) return nullptr;
+  allocations.push_back(p);
+  if (zero && hipMemset(p, 0, bytes ? bytes : 16) != hipSuccess) return nullptr;
+  return p;
+}
+
+int Ctx::upload_q8(const void* blocks, int n, int k, uint8_t* dst, uint8_t* staging) {
+  const size_t raw = (size_t)n * (k / 32) * 34;
+  int rc = check(hipMemcpyAsync(staging, blocks, raw, hipMemcpyHostToDevice, stream), "upload weights");
+  if (rc) return rc;
+  launch_q8_retile(stream, staging, n, k, dst);
+  rc = check(hipGetLastError(), "retile launch");
+  if (rc) return rc;
+  return check(hipStreamSynchronize(stream), "retile");
+}
+
+int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
+  hp = d->hp;
+  max_seq = max_seq_in;
+  kv_type = kv_type_in;
+  const int H = hp.hidden, D = hp.head_dim, NH = hp.n_heads, NKV = hp.n_kv_heads;
+  const int QN = NH * D, KN = NKV * D, F = hp.intermediate, L = hp.n_layers, V = hp.vocab;
+  if (d->weight_type != MTG_TYPE_Q8_0)
+    return fail(MTG_ERR_UNSUPPORTED, "weight type %d is not supported by this build", d->weight_type);
+  if (kv_type != MTG_TYPE_F32 && kv_type != MTG_TYPE_F16)
+    return fail(MTG_ERR_UNSUPPORTED, "kv type %d", kv_type);
+  if (D != kHeadDim || NH != 2 * NKV || H % kPairK || QN % kPairK || F % kPairK || V % 16 ||
+      H % 16 || F % 16 || L <= 0 || max_seq <= 0)
+    return fail(MTG_ERR_UNSUPPORTED,
+                "shape not supported: head_dim 128, n_heads = 2*n_kv_heads, hidden/intermediate "
+                "multiples of 64, vocab multiple of 16");
+  int rc = check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "stream");
+  if (rc) return rc;
+  if (hipHostMalloc((void**)&desc_host, sizeof(StepDesc), hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&result_host, sizeof(StepResult), hipHostMallocDefault) != hipSuccess)
+    return fail(MTG_ERR_NOMEM, "pinned host buffers");
+  std::memset(desc_host, 0, sizeof(StepDesc));
+
+  // weights
+  size_t staging_bytes = (size_t)V * (H / 32) * 34;
+  staging_bytes = std::max(staging_bytes, (size_t)F * (H / 32) * 34);
+  staging_bytes = std::max(staging_bytes, (size_t)H * (F / 32) * 34);
+  uint8_t* staging = (uint8_t*)dalloc(staging_bytes, false);
+  if (!staging) return fail(MTG_ERR_NOMEM, "staging buffer");
+  layers.resize(L);
+  const int NQKV = QN + 2 * KN;
+  for (int l = 0; l < L; ++l) {
+    const mtg_layer_tensors& s = d->layers[l];
+    Layer& y = layers[l];
+    y.wqkv = (uint8_t*)dalloc(q8_tiles_bytes(NQKV, H), false);
+    y.wo = (uint8_t*)dalloc(q8_tiles_bytes(H, QN), false);
+    y.wg = (uint8_t*)dalloc(q8_tiles_bytes(F, H), false);
+    y.wu = (uint8_t*)dalloc(q8_tiles_bytes(F, H), false);
+    y.wd = (uint8_t*)dalloc(q8_tiles_bytes(H, F), false);
+    y.attn_norm = (float*)dalloc(H * 4, false);
+    y.ffn_norm = (float*)dalloc(H * 4, false);
+    y.q_norm = (float*)dalloc(D * 4, false);
+    y.k_norm = (float*)dalloc(D * 4, false);
+    if (!y.wqkv || !y.wo || !y.wg || !y.wu || !y.wd || !y.attn_norm || !y.ffn_norm || !y.q_norm ||
+        !y.k_norm)
+      return fail(MTG_ERR_NOMEM, "layer %d weights", l);
+    if ((rc = upload_q8(s.attn_q, QN, H, y.wqkv, staging))) return rc;
+    if ((rc = upload_q8(s.attn_k, KN, H, y.wqkv + q8_tiles_bytes(QN, H), staging))) return rc;
+    if ((rc = upload_q8(s.attn_v, KN, H, y.wqkv + q8_tiles_bytes(QN + KN, H), staging))) return rc;
+    if ((rc = upload_q8(s.attn_o, H, QN, y.wo, staging))) return rc;
+    if ((rc = upload_q8(s.ffn_gate, F, H, y.wg, staging))) return rc;
+    if ((rc = upload_q8(s.ffn_up, F, H, y.wu, staging))) return rc;
+    if ((rc = upload_q8(s.ffn_down, H, F, y.wd, staging))) return rc;
+    if ((rc = check(hipMemcpy(y.attn_norm, s.attn_norm, H * 4, hipMemcpyHostToDevice), "norms")) ||
+        (rc = check(hipMemcpy(y.ffn_norm, s.ffn_norm, H * 4, hipMemcpyHostToDevice), "norms")) ||
+        (rc = check(hipMemcpy(y.q_norm, s.attn_q_norm, D * 4, hipMemcpyHostToDevice), "norms")) ||
+        (rc = check(hipMemcpy(y.k_norm, s.attn_k_norm, D * 4, hipMemcpyHostToDevice), "norms")))
+      return rc;
+  }
+  embd = (uint8_t*)dalloc(q8_tiles_bytes(V, H), false);
+  out_norm = (float*)dalloc(H * 4, false);
+  if (!embd || !out_norm) return fail(MTG_ERR_NOMEM, "token_embd");
+  if ((rc = upload_q8(d->token_embd, V, H, embd, staging))) return rc;
+  if ((rc = check(hipMemcpy(out_norm, d->output_norm, H * 4, hipMemcpyHostToDevice), "norms")))
+    return rc;
+  hipFree(staging);
+  allocations.erase(std::find(allocations.begin(), allocations.end(), (void*)staging));
+
+  // RoPE table: the float recurrence of ggml's rope cache, built once on the host.
+  std::vector<float> table((size_t)max_seq * D);
+  const float theta_scale = std::pow(hp.rope_base, -2.0f / (float)D);
+  for (int p = 0; p < max_seq; ++p) {
+    float theta = (float)p;
+    for (int i = 0; i < D / 2; ++i) {
+      table[(size_t)p * D + 2 * i] = std::cos(theta);
+      table[(size_t)p * D + 2 * i + 1] = std::sin(theta);
+      theta *= theta_scale;
+    }
+  }
+  rope = (float*)dalloc(table.size() * 4, false);
+  if (!rope) return fail(MTG_ERR_NOMEM, "rope table");
+  if ((rc = check(hipMemcpy(rope, table.data(), table.size() * 4, hipMemcpyHostToDevice), "rope")))
+    return rc;
+
+  // KV cache
+  const size_t es = kv_type == MTG_TYPE_F32 ? 4 : 2;
+  kv_layer_bytes = (size_t)NKV * max_seq * D * es;
+  kcache = (uint8_t*)dalloc(kv_layer_bytes * L, true);
+  vcache = (uint8_t*)dalloc(kv_layer_bytes * L, true);
+  if (!kcache || !vcache) return fail(MTG_ERR_NOMEM, "KV cache of %d positions", max_seq);
+
+  // activations and step buffers
+  const int R = kMaxRows;
+  x = (float*)dalloc((size_t)R * H * 4, true);
+  qkv = (float*)dalloc((size_t)R * NQKV * 4, true);
+  qbuf = (float*)dalloc((size_t)R * QN * 4, true);
+  obuf = (float*)dalloc((size_t)R * QN * 4, true);
+  act = (float*)dalloc((size_t)R * F * 4, true);
+  hid = (float*)dalloc((size_t)R * H * 4, true);
+  embeds_dev = (float*)dalloc((size_t)R * H * 4, true);
+  logits = (float*)dalloc((size_t)R * V * 4, true);
+  bitmap = (uint32_t*)dalloc((size_t)R * ((V + 31) / 32) * 4, true);
+  part_keys = (uint64_t*)dalloc((size_t)kLmWorkgroups * R * 8, true);
+  auto panel = [&](int K) {
+    Panel p;
+    p.codes = (uint8_t*)dalloc((size_t)kMaxGroups * (K / kPairK) * 1024, true);
+    p.scales = (float*)dalloc((size_t)kMaxGroups * (K / kPairK) * 16 * 4, true);
+    return p;
+  };
+  panel_h = panel(H);
+  panel_o = panel(QN);
+  panel_f = panel(F);
+  work.part_ml = (float*)dalloc((size_t)NKV * kAttnSplits * kMaxGroups * 16 * 2 * 4, true);
+  work.part_o = (float*)dalloc((size_t)NKV * kAttnSplits * kMaxGroups * 16 * D * 4, true);
+  desc_dev = (StepDesc*)dalloc(sizeof(StepDesc), true);
+  result_dev = (StepResult*)dalloc(sizeof(StepResult), true);
+  if (!x || !qkv || !qbuf || !obuf || !act || !hid || !embeds_dev || !logits || !bitmap ||
+      !part_keys || !panel_h.codes || !panel_h.scales || !panel_o.codes || !panel_o.scales ||
+      !panel_f.codes || !panel_f.scales || !work.part_ml || !work.part_o || !desc_dev || !result_dev)
+    return fail(MTG_ERR_NOMEM, "step buffers");
+  return check(hipDeviceSynchronize(), "init");
+}
+
+KvLayer Ctx::kv_layer(int l) const {
+  KvLayer k;
+  k.k = kcache + kv_layer_bytes * l;
+  k.v = vcache + kv_layer_bytes * l;
+  k.f16 = kv_type == MTG_TYPE_F16;
+  k.max_seq = max_seq;
+  return k;
+}
+
+// The kernel sequence of one step (src/qwen3_decoder.cpp:91-160 + 174-205).
+void Ctx::enqueue(int G, int mode) {
+  const int H = hp.hidden, NH = hp.n_heads, NKV = hp.n_kv_heads, D = hp.head_dim;
+  const int QN = NH * D, KN = NKV * D, F = hp.intermediate, V = hp.vocab;
+  const float eps = hp.rms_eps;
+  hipStream_t s = stream;
+  if (mode != kModeLogits) {
+    launch_embed(s, desc_dev, embd, H, embeds_dev, x);
+    for (int l = 0; l < hp.n_layers; ++l) {
+      const Layer& y = layers[l];
+      const KvLayer kv = kv_layer(l);
+      launch_norm_quant(s, desc_dev, x, H, y.attn_norm, eps, panel_h, nullptr);
+      launch_gemm_store(s, G, desc_dev, y.wqkv, QN + 2 * KN, H, panel_h, qkv);
+      launch_qk_rope_append(s, desc_dev, qkv, NH, NKV, y.q_norm, y.k_norm, eps, rope, qbuf, kv);
+      launch_attention(s, desc_dev, qbuf, NH, NKV, kv, work, panel_o, obuf);
+      launch_gemm_residual(s, G, desc_dev, y.wo, H, QN, panel_o, x);
+      launch_norm_quant(s, desc_dev, x, H, y.ffn_norm, eps, panel_h, nullptr);
+      launch_gemm_swiglu(s, G, desc_dev, y.wg, y.wu, F, H, panel_h, act);
+      launch_norm_quant(s, desc_dev, act, F, nullptr, eps, panel_f, nullptr);
+      launch_gemm_residual(s, G, desc_dev, y.wd, H, F, panel_f, x);
+    }
+    launch_norm_quant(s, desc_dev, x, H, out_norm, eps, panel_h, hid);
+  } else {
+    // logits of given final-normed rows: quantize them as they are
+    launch_norm_quant(s, desc_dev, embeds_dev, H, nullptr, eps, panel_h, nullptr);
+  }
+  if (mode == kModeAppend) return;
+  if (mode == kModeVerifyPenalty) launch_penalty_bitmap(s, desc_dev, V, bitmap);
+  launch_lm_head(s, G, desc_dev, embd, V, H, panel_h, bitmap, logits, part_keys);
+  launch_accept(s, desc_dev, part_keys, result_dev);
+}
+
+int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_out,
+             float* logits_out) {
+  const int G = (T + 7) / 8;
+  int rc = check(hipMemcpyAsync(desc_dev, desc_host, sizeof(StepDesc), hipMemcpyHostToDevice, stream),
+                 "step descriptor");
+  if (rc) return rc;
+  if (use_graphs) {
+    GraphSlot& slot = graphs[(G - 1) * kModes + mode];
+    if (!slot.exec) {
+      hipGraph_t g = nullptr;
+      if ((rc = check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "capture")))
+        return rc;
+      enqueue(G, mode);
+      if ((rc = check(hipStreamEndCapture(stream, &g), "end capture"))) return rc;
+      rc = check(hipGraphInstantiate(&slot.exec, g, nullptr, nullptr, 0), "instantiate");
+      hipGraphDestroy(g);
+      if (rc) return rc;
+    }
+    if ((rc = check(hipGraphLaunch(slot.exec, stream), "graph launch"))) return rc;
+  } else {
+    enqueue(G, mode);
+    if ((rc = check(hipGetLastError(), "kernel launch"))) return rc;
+  }
+  if (mode == kModeVerify || mode == kModeVerifyPenalty || mode == kModeLogits) {
+    if ((rc = check(hipMemcpyAsync(result_host, result_dev, sizeof(StepResult),
+                                   hipMemcpyDeviceToHost, stream), "result")))
+      return rc;
+  }
+  if (want_hidden && hidden_out &&
+      (rc = check(hipMemcpyAsync(hidden_out, hid, (size_t)T * hp.hidden * 4, hipMemcpyDeviceToHost,
+                                 stream), "hidden")))
+    return rc;
+  if (want_logits && logits_out &&
+      (rc = check(hipMemcpyAsync(logits_out, logits, (size_t)T * hp.vocab * 4,
+                                 hipMemcpyDeviceToHost, stream), "logits")))
+    return rc;
+  return check(hipStreamSynchronize(stream), "step");
+}
+
+void Ctx::fill_desc(int T, bool use_embeds, float penalty, const int32_t* tokens,
+                    const int32_t* history, int n_history, bool write_logits) {
+  StepDesc& d = *desc_host;
+  d.T = T;
+  d.past = past;
+  d.groups = (T + 7) / 8;
+  d.use_embeds = use_embeds ? 1 : 0;
+  d.penalty = penalty;
+  d.write_logits = write_logits ? 1 : 0;
+  for (int i = 0; i < kMaxRows; ++i) d.tokens[i] = (tokens && i < T) ? tokens[i] : 0;
+  d.n_pen = 0;
+  d.pen_base = 0;
+  if (penalty > 1.0f) {
+    // window of row i = last 100 of history ++ tokens[0..i]
+    const int nh = history ? n_history : 0;
+    const int start = std::max(0, nh + 1 - kPenaltyWindow);
+    int n = 0;
+    for (int i = start; i < nh; ++i) d.pen_ids[n++] = history[i];
+    for (int i = 0; i < T; ++i) d.pen_ids[n++] = tokens[i];
+    d.n_pen = n;
+    d.pen_base = nh - start;
+  }
+}
+
+int Ctx::verify(const int32_t* tokens, int T, const int32_t* history, int n_history,
+                float penalty, int32_t* choice_out, int32_t* n_match_out, float* hidden_out,
+                float* logits_out) {
+  if (!tokens || T <= 0 || T > kMaxRows || !choice_out || !n_match_out)
+    return fail(MTG_ERR_INVALID, "verify: bad arguments (T=%d)", T);
+  if (past + T > max_seq) return fail(MTG_ERR_CAPACITY, "sequence exceeds max_seq");
+  for (int i = 0; i < T; ++i)
+    if (tokens[i] < 0 || tokens[i] >= hp.vocab) return fail(MTG_ERR_INVALID, "token id %d", tokens[i]);
+  fill_desc(T, false, penalty, tokens, history, n_history, logits_out != nullptr);
+  const int mode = penalty > 1.0f ? kModeVerifyPenalty : kModeVerify;
+  int rc = run(mode, T, true, true, hidden_out, logits_out);
+  if (rc) return rc;
+  past += T;
+  for (int i = 0; i < T; ++i) choice_out[i] = result_host->choice[i];
+  *n_match_out = result_host->n_match;
+  return MTG_OK;
+}
+
+int Ctx::append(const float* embeds, int T, float* hidden_out) {
+  if (!embeds || T <= 0 || T > kMaxRows) return fail(MTG_ERR_INVALID, "append: bad arguments");
+  if (past + T > max_seq) return fail(MTG_ERR_CAPACITY, "sequence exceeds max_seq");
+  int rc = check(hipMemcpyAsync(embeds_dev, embeds, (size_t)T * hp.hidden * 4, hipMemcpyHostToDevice,
+                                stream), "embeddings");
+  if (rc) return rc;
+  fill_desc(T, true, 1.0f, nullptr, nullptr, 0, false);
+  if ((rc = run(kModeAppend, T, true, false, hidden_out, nullptr))) return rc;
+  past += T;
+  return MTG_OK;
+}
+
+int Ctx::logits_of(const float* hidden, int T, float* logits_out) {
+  if (!hidden || T <= 0 || !logits_out) return fail(MTG_ERR_INVALID, "logits: bad arguments");
+  for (int t0 = 0; t0 < T; t0 += kMaxRows) {
+    const int n = std::min(kMaxRows, T - t0);
+    int rc = check(hipMemcpyAsync(embeds_dev, hidden + (size_t)t0 * hp.hidden,
+                                  (size_t)n * hp.hidden * 4, hipMemcpyHostToDevice, stream),
+                   "hidden rows");
+    if (rc) return rc;
+    fill_desc(n, true, 1.0f, nullptr, nullptr, 0, true);
+    if ((rc = run(kModeLogits, n, false, true, nullptr, logits_out + (size_t)t0 * hp.vocab)))
+      return rc;
+  }
+  return MTG_OK;
+}
+
+int Ctx::embed(const int32_t* ids, int n, float* out) {
+  if (!ids || n <= 0 || !out) return fail(MTG_ERR_INVALID, "embed: bad arguments");
+  for (int i = 0; i < n; ++i)
+    if (ids[i] < 0 || ids[i] >= hp.vocab) return fail(MTG_ERR_INVALID, "token id %d", ids[i]);
+  for (int i0 = 0; i0 < n; i0 += kMaxRows) {
+    const int c = std::min(kMaxRows, n - i0);
+    fill_desc(c, false, 1.0f, ids + i0, nullptr, 0, false);
+    int rc = check(hipMemcpyAsync(desc_dev, desc_host, sizeof(StepDesc), hipMemcpyHostToDevice,
+                                  stream), "descriptor");
+    if (rc) return rc;
+    launch_embed(stream, desc_dev, embd, hp.hidden, embeds_dev, x);
+    if ((rc = check(hipMemcpyAsync(out + (size_t)i0 * hp.hidden, x, (size_t)c * hp.hidden * 4,
+                                   hipMemcpyDeviceToHost, stream), "embed rows")))
+      return rc;
+    if ((rc = check(hipStreamSynchronize(stream), "embed"))) return rc;
+  }
+  return MTG_OK;
+}
+
+int Ctx::kv_io(void* k, void* v, int n_pos, bool write) {
+  if (!k || !v || n_pos < 0 || n_pos > max_seq) return fail(MTG_ERR_INVALID, "kv: bad arguments");
+  const size_t es = kv_type == MTG_TYPE_F32 ? 4 : 2;
+  const size_t row = (size_t)hp.head_dim * es, chunk = row * n_pos;
+  for (int l = 0; l < hp.n_layers; ++l)
+    for (int h = 0; h < hp.n_kv_heads; ++h) {
+      const size_t dev_off = kv_layer_bytes * l + (size_t)h * max_seq * row;
+      const size_t host_off = ((size_t)l * hp.n_kv_heads + h) * chunk;
+      for (int which = 0; which < 2; ++which) {
+        uint8_t* dev = (which ? vcache : kcache) + dev_off;
+        uint8_t* host = (uint8_t*)(which ? v : k) + host_off;
+        const hipError_t e = write ? hipMemcpy(dev, host, chunk, hipMemcpyHostToDevice)
+                                   : hipMemcpy(host, dev, chunk, hipMemcpyDeviceToHost);
+        if (int rc = check(e, "kv copy")) return rc;
+      }
+    }
+  if (write) past = n_pos;
+  return MTG_OK;
+}
+
+}  // namespace mtg

@@ -1,0 +1,75 @@
+// runtime.hpp - the device decoder context behind the C ABI.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "mtg_internal.hpp"
+
+namespace mtg {
+
+enum { kModeVerify = 0, kModeVerifyPenalty = 1, kModeAppend = 2, kModeLogits = 3, kModes = 4 };
+
+struct Layer {
+  uint8_t *wqkv = nullptr, *wo = nullptr, *wg = nullptr, *wu = nullptr, *wd = nullptr;
+  float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+};
+
+struct GraphSlot {
+  hipGraphExec_t exec = nullptr;
+};
+
+struct Ctx {
+  mtg_hparams hp{};
+  int max_seq = 0, kv_type = MTG_TYPE_F32, past = 0;
+  bool use_graphs = true;
+  std::string error;
+  hipStream_t stream = nullptr;
+  std::vector<void*> allocations;
+  std::vector<Layer> layers;
+  uint8_t* embd = nullptr;
+  float* out_norm = nullptr;
+  float* rope = nullptr;
+  uint8_t *kcache = nullptr, *vcache = nullptr;
+  size_t kv_layer_bytes = 0;
+  float *x = nullptr, *qkv = nullptr, *qbuf = nullptr, *obuf = nullptr, *act = nullptr,
+        *hid = nullptr, *embeds_dev = nullptr, *logits = nullptr;
+  uint32_t* bitmap = nullptr;
+  uint64_t* part_keys = nullptr;
+  Panel panel_h{}, panel_o{}, panel_f{};
+  AttnWork work{};
+  StepDesc* desc_dev = nullptr;
+  StepResult* result_dev = nullptr;
+  StepDesc* desc_host = nullptr;      // pinned
+  StepResult* result_host = nullptr;  // pinned
+  GraphSlot graphs[2 * kModes];
+
+  ~Ctx();
+  int fail(int code, const char* fmt, ...);
+  int check(hipError_t e, const char* what);
+  void* dalloc(size_t bytes, bool zero);
+  int upload_q8(const void* blocks, int n, int k, uint8_t* dst, uint8_t* staging);
+  int init(const mtg_model_desc* d, int max_seq, int kv_type);
+  KvLayer kv_layer(int l) const;
+  void enqueue(int G, int mode);
+  void fill_desc(int T, bool use_embeds, float penalty, const int32_t* tokens,
+                 const int32_t* history, int n_history, bool write_logits);
+  int run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_out,
+          float* logits_out);
+  int verify(const int32_t* tokens, int T, const int32_t* history, int n_history, float penalty,
+             int32_t* choice_out, int32_t* n_match_out, float* hidden_out, float* logits_out);
+  int append(const float* embeds, int T, float* hidden_out);
+  int logits_of(const float* hidden, int T, float* logits_out);
+  int embed(const int32_t* ids, int n, float* out);
+  int kv_io(void* k, void* v, int n_pos, bool write);
+};
+
+}  // namespace mtg
+
+struct mtg_ctx {
+  mtg::Ctx impl;
+};

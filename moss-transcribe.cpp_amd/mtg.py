@@ -1,0 +1,333 @@
+"""ctypes binding of libmtg.so (include/mtg_verify.h).
+
+The Python layer is plumbing for tests and the benchmark: it passes host numpy
+arrays (and, for the *_dev entry points, device pointers from torch tensors) to
+the C ABI. The product path is the C++/HIP library; this module raises if it is
+missing instead of falling back to anything.
+"""
+import ctypes
+import os
+from ctypes import POINTER, c_float, c_int32, c_int64, c_uint16, c_uint64, c_void_p, c_double
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmtg.so")
+
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K = 0, 1, 8, 12
+MAX_BATCH = 16
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_DEVICE, ERR_CAPACITY, ERR_NOMEM, ERR_STATE = 0, -1, -2, -3, -4, -5, -6
+
+QWEN3_0_6B = dict(hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, intermediate=3072,
+                  n_layers=28, vocab=151936, rope_base=1e6, rms_eps=1e-6)
+
+
+class Hparams(ctypes.Structure):
+    _fields_ = [("hidden", c_int32), ("n_heads", c_int32), ("n_kv_heads", c_int32),
+                ("head_dim", c_int32), ("intermediate", c_int32), ("n_layers", c_int32),
+                ("vocab", c_int32), ("rope_base", c_float), ("rms_eps", c_float)]
+
+
+class LayerTensors(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_o",
+                                        "attn_q_norm", "attn_k_norm", "ffn_norm", "ffn_gate",
+                                        "ffn_up", "ffn_down")]
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [("hp", Hparams), ("weight_type", c_int32), ("token_embd", c_void_p),
+                ("output_norm", c_void_p), ("layers", POINTER(LayerTensors))]
+
+
+class GenStats(ctypes.Structure):
+    _fields_ = [("target_calls", c_int64), ("drafted_calls", c_int64), ("proposed", c_int64),
+                ("accepted", c_int64), ("target_input_tokens", c_int64), ("rewinds", c_int64),
+                ("prefill_seconds", c_double), ("verify_seconds", c_double),
+                ("draft_seconds", c_double), ("stop_reason", c_int32), ("next_seed", c_int32)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+class StreamDrafter(ctypes.Structure):
+    _fields_ = [("prompt", POINTER(c_int32)), ("n_prompt", c_int32),
+                ("stream", POINTER(c_int32)), ("period", c_int32)]
+
+
+DRAFT_FN = ctypes.CFUNCTYPE(c_int32, c_void_p, POINTER(c_int32), c_int32, c_int32, POINTER(c_int32))
+COMMIT_FN = ctypes.CFUNCTYPE(None, c_void_p, POINTER(c_int32), c_int32, c_int32, c_int32)
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "mtg_abi_version": (c_int32, []),
+    "mtg_create": (c_int32, [POINTER(ModelDesc), c_int32, c_int32, POINTER(c_void_p)]),
+    "mtg_destroy": (None, [c_void_p]),
+    "mtg_last_error": (ctypes.c_char_p, [c_void_p]),
+    "mtg_past_len": (c_int32, [c_void_p]),
+    "mtg_remaining": (c_int32, [c_void_p]),
+    "mtg_rewind": (c_int32, [c_void_p, c_int32]),
+    "mtg_embed": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
+    "mtg_prefill": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
+    "mtg_append": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
+    "mtg_logits": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
+    "mtg_verify": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_int32, c_float, c_void_p,
+                             c_void_p, c_void_p, c_void_p]),
+    "mtg_kv_write": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32]),
+    "mtg_kv_read": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32]),
+    "mtg_generate": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, c_int32,
+                               c_void_p, c_void_p, c_void_p, c_void_p, POINTER(c_int32),
+                               POINTER(GenStats)]),
+    "mtg_generate_from": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32,
+                                    c_int32, c_float, c_int32, c_void_p, c_void_p, c_void_p,
+                                    c_void_p, POINTER(c_int32), POINTER(GenStats)]),
+    "mtg_stream_draft": (c_int32, [c_void_p, POINTER(c_int32), c_int32, c_int32, POINTER(c_int32)]),
+    "mtg_set_graphs": (c_int32, [c_void_p, c_int32]),
+    "mtg_ngram_draft": (c_int32, [c_void_p, c_int32, c_int32, c_void_p]),
+    "mtg_greedy_choice": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_float]),
+    "mtg_q8_pack": (c_int32, [c_void_p, c_int32, c_int32, POINTER(c_void_p)]),
+    "mtg_q8_free": (None, [c_void_p]),
+    "mtg_q8_mul_mat_dev": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
+    "mtg_causal_context_dev": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
+                                         c_int32, c_void_p]),
+    "mtg_synth_create": (c_int32, [POINTER(Hparams), c_int32, c_uint64, c_float, c_float,
+                                   POINTER(c_void_p)]),
+    "mtg_synth_free": (None, [c_void_p]),
+    "mtg_synth_desc": (POINTER(ModelDesc), [c_void_p]),
+    "mtg_normal_fill": (None, [c_uint64, c_uint64, c_void_p, ctypes.c_size_t]),
+    "mtg_quantize_q8_0_weight": (None, [c_void_p, c_int64, c_void_p]),
+    "mtg_quantize_q4_k": (None, [c_void_p, c_int64, c_void_p]),
+    "mtg_dequantize": (None, [c_int32, c_void_p, c_int64, c_void_p]),
+    "mtg_row_bytes": (ctypes.c_size_t, [c_int32, c_int64]),
+    "mtg_f32_to_f16": (c_uint16, [c_float]),
+    "mtg_f16_to_f32": (c_float, [c_uint16]),
+}
+
+_lib = None
+
+
+class MtgError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("mtg error %d: %s" % (code, msg))
+        self.code = code
+
+
+def lib():
+    """Load libmtg.so (built by __graft_entry__.build()); raise if it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError("libmtg.so is not built: run __graft_entry__.build() (%s)" % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def ptr(a):
+    return None if a is None else a.ctypes.data_as(c_void_p)
+
+
+def i32(a):
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+
+
+def f32(a):
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def make_hparams(**kw):
+    d = dict(QWEN3_0_6B)
+    d.update(kw)
+    return Hparams(**d)
+
+
+class SynthModel:
+    """Seeded synthetic Qwen3 model held in host memory (ggml block layout)."""
+
+    def __init__(self, weight_type=TYPE_Q8_0, seed=0, std=0.02, gain_jitter=0.0, **hp):
+        self.hp = make_hparams(**hp)
+        out = c_void_p()
+        rc = lib().mtg_synth_create(ctypes.byref(self.hp), weight_type, seed, std, gain_jitter,
+                                    ctypes.byref(out))
+        if rc:
+            raise MtgError(rc, "synthetic model")
+        self.handle = out
+        self.desc = lib().mtg_synth_desc(out)
+        self.weight_type = weight_type
+
+    def close(self):
+        if self.handle:
+            lib().mtg_synth_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def matrix(self, ptr_, k, n):
+        """Copy of one weight matrix's raw block bytes (n rows of k)."""
+        nb = lib().mtg_row_bytes(self.weight_type, k) * n
+        return np.frombuffer(ctypes.string_at(ptr_, nb), dtype=np.uint8).copy()
+
+    def dequant_rows(self, ptr_, k, rows):
+        rb = lib().mtg_row_bytes(self.weight_type, k)
+        out = np.empty((len(rows), k), np.float32)
+        for i, r in enumerate(rows):
+            raw = ctypes.string_at(ptr_ + int(r) * rb, rb)
+            lib().mtg_dequantize(self.weight_type, raw, k, ptr(out[i]))
+        return out
+
+
+class Decoder:
+    """Device decoder context (mtg_ctx)."""
+
+    def __init__(self, model, max_seq, kv_type=TYPE_F32):
+        self.hp = model.hp
+        out = c_void_p()
+        rc = lib().mtg_create(model.desc, max_seq, kv_type, ctypes.byref(out))
+        if rc:
+            raise MtgError(rc, lib().mtg_last_error(None).decode())
+        self.ctx = out
+        self.kv_type = kv_type
+        self.max_seq = max_seq
+
+    def _chk(self, rc):
+        if rc:
+            raise MtgError(rc, lib().mtg_last_error(self.ctx).decode())
+
+    def close(self):
+        if self.ctx:
+            lib().mtg_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def past_len(self):
+        return lib().mtg_past_len(self.ctx)
+
+    def rewind(self, pos):
+        self._chk(lib().mtg_rewind(self.ctx, pos))
+
+    def set_graphs(self, on):
+        self._chk(lib().mtg_set_graphs(self.ctx, 1 if on else 0))
+
+    def embed(self, ids):
+        ids = i32(ids)
+        out = np.empty((len(ids), self.hp.hidden), np.float32)
+        self._chk(lib().mtg_embed(self.ctx, ptr(ids), len(ids), ptr(out)))
+        return out
+
+    def prefill(self, embeds, want_hidden=True):
+        embeds = f32(embeds)
+        S = embeds.shape[0]
+        hid = np.empty((S, self.hp.hidden), np.float32) if want_hidden else None
+        self._chk(lib().mtg_prefill(self.ctx, ptr(embeds), S, ptr(hid)))
+        return hid
+
+    def append(self, embeds):
+        embeds = f32(embeds)
+        T = embeds.shape[0]
+        hid = np.empty((T, self.hp.hidden), np.float32)
+        self._chk(lib().mtg_append(self.ctx, ptr(embeds), T, ptr(hid)))
+        return hid
+
+    def logits(self, hidden):
+        hidden = f32(hidden)
+        T = hidden.shape[0]
+        out = np.empty((T, self.hp.vocab), np.float32)
+        self._chk(lib().mtg_logits(self.ctx, ptr(hidden), T, ptr(out)))
+        return out
+
+    def verify(self, tokens, history=(), penalty=1.0, want_hidden=False, want_logits=False):
+        tokens = i32(tokens)
+        T = len(tokens)
+        hist = i32(history)
+        choice = np.empty(T, np.int32)
+        n_match = np.zeros(1, np.int32)
+        hid = np.empty((T, self.hp.hidden), np.float32) if want_hidden else None
+        lg = np.empty((T, self.hp.vocab), np.float32) if want_logits else None
+        self._chk(lib().mtg_verify(self.ctx, ptr(tokens), T, ptr(hist) if len(hist) else None,
+                                   len(hist), penalty, ptr(choice), ptr(n_match), ptr(hid), ptr(lg)))
+        return choice, int(n_match[0]), hid, lg
+
+    def kv_dtype(self):
+        return np.float32 if self.kv_type == TYPE_F32 else np.float16
+
+    def kv_read(self, n_pos):
+        shape = (self.hp.n_layers, self.hp.n_kv_heads, n_pos, self.hp.head_dim)
+        k = np.empty(shape, self.kv_dtype())
+        v = np.empty(shape, self.kv_dtype())
+        self._chk(lib().mtg_kv_read(self.ctx, ptr(k), ptr(v), n_pos))
+        return k, v
+
+    def kv_write(self, k, v):
+        k = np.ascontiguousarray(k, self.kv_dtype())
+        v = np.ascontiguousarray(v, self.kv_dtype())
+        self._chk(lib().mtg_kv_write(self.ctx, ptr(k), ptr(v), k.shape[2]))
+
+    def generate_from(self, first_seed, max_new, max_steps=0, eos=-1, penalty=1.0, max_draft=4,
+                      draft=None, user=None, prior=()):
+        """Run the speculative controller; draft is None (reference n-gram), a
+        (c function pointer, user pointer) pair, or a Python callable."""
+        out = np.empty(max_new, np.int32)
+        n = c_int32(0)
+        st = GenStats()
+        prior = i32(prior)
+        keep = None
+        fn = None
+        if callable(draft):
+            def _cb(_user, ids, n_ids, budget, dst, _f=draft):
+                props = list(_f([ids[i] for i in range(n_ids)], budget))[:budget]
+                for i, t in enumerate(props):
+                    dst[i] = int(t)
+                return len(props)
+            keep = DRAFT_FN(_cb)
+            fn = ctypes.cast(keep, c_void_p)
+        elif draft is not None:
+            fn = draft
+        self._chk(lib().mtg_generate_from(self.ctx, first_seed, ptr(prior) if len(prior) else None,
+                                          len(prior), max_new, max_steps, eos, penalty, max_draft,
+                                          fn, None, user, ptr(out), ctypes.byref(n),
+                                          ctypes.byref(st)))
+        del keep
+        return out[: n.value].copy(), st
+
+
+def stream_drafter(prompt, stream):
+    """(function pointer, user pointer, keepalive) for mtg_stream_draft."""
+    prompt = i32(prompt)
+    stream = i32(stream)
+    d = StreamDrafter(prompt.ctypes.data_as(POINTER(c_int32)), len(prompt),
+                      stream.ctypes.data_as(POINTER(c_int32)), len(stream))
+    fn = ctypes.cast(lib().mtg_stream_draft, c_void_p)
+    return fn, ctypes.cast(ctypes.pointer(d), c_void_p), (prompt, stream, d)
+
+
+def ngram_draft(history, maximum):
+    h = i32(history)
+    out = np.zeros(max(maximum, 1), np.int32)
+    n = lib().mtg_ngram_draft(ptr(h) if len(h) else None, len(h), maximum, ptr(out))
+    return [int(x) for x in out[:n]]
+
+
+def greedy_choice(raw, history, penalty):
+    raw = f32(raw)
+    h = i32(history)
+    return int(lib().mtg_greedy_choice(ptr(raw), len(raw), ptr(h) if len(h) else None, len(h),
+                                       penalty))
+
+
+def normal(seed, first, n):
+    out = np.empty(n, np.float32)
+    lib().mtg_normal_fill(seed, first, ptr(out), n)
+    return out

@@ -1,0 +1,813 @@
+// oracle.cpp - CPU restatement of the reference speculative verify path.
+//
+// TEST INFRASTRUCTURE ONLY: the parity checker for libmtg and the timed CPU
+// baseline of bench.py. Nothing in the product links or loads this file.
+//
+// The reference executes these ops through ggml's CPU backend, which is not
+// vendored in the reference tree (third_party/ggml is an empty submodule), so the
+// arithmetic below restates ggml's published CPU semantics as the reference uses
+// them. Where ggml's exact float summation order is not knowable here, the
+// oracle uses a plain sequential order; the per-block integer dots of q8_0 and
+// q4_K are exact by construction.
+#include "oracle.h"
+
+#include <omp.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <set>
+#include <vector>
+
+namespace {
+
+// ---------------------------------------------------------------- f16 -------
+// IEEE binary16 conversions, round-to-nearest-even, after the magic-number
+// method published by F. Giesen ("half <-> float conversions", 2012).
+uint16_t f2h(float value) {
+  uint32_t u;
+  std::memcpy(&u, &value, 4);
+  const uint32_t sign = u & 0x80000000u;
+  u ^= sign;
+  uint16_t out;
+  if (u >= (uint32_t)(127 + 16) << 23) {
+    out = (u > 0x7f800000u) ? 0x7e00 : 0x7c00;  // NaN -> quiet NaN, overflow -> inf
+  } else if (u < (uint32_t)113 << 23) {
+    // Result is subnormal or zero: let an FP add align the mantissa (RNE).
+    const uint32_t magic_u = (uint32_t)((127 - 15) + (23 - 10) + 1) << 23;
+    float magic, f;
+    std::memcpy(&magic, &magic_u, 4);
+    std::memcpy(&f, &u, 4);
+    f += magic;
+    uint32_t r;
+    std::memcpy(&r, &f, 4);
+    out = (uint16_t)(r - magic_u);
+  } else {
+    const uint32_t mant_odd = (u >> 13) & 1u;
+    u += ((uint32_t)(15 - 127) << 23) + 0xfffu;
+    u += mant_odd;
+    out = (uint16_t)(u >> 13);
+  }
+  return (uint16_t)(out | (sign >> 16));
+}
+
+float h2f(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu;
+  uint32_t man = h & 0x3ffu;
+  uint32_t bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else {
+      exp = 127 - 15 + 1;
+      while (!(man & 0x400u)) {
+        man <<= 1;
+        --exp;
+      }
+      man &= 0x3ffu;
+      bits = sign | (exp << 23) | (man << 13);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7f800000u | (man << 13);
+  } else {
+    bits = sign | ((exp + 112) << 23) | (man << 13);
+  }
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+// ------------------------------------------------------------ blocks -------
+#pragma pack(push, 1)
+struct BlockQ8 {  // ggml block_q8_0: 34 bytes (src/cpu_q8.cpp:17 relies on it)
+  uint16_t d;
+  int8_t qs[32];
+};
+struct BlockQ8K {  // ggml block_q8_K: activation side of the q4_K dot
+  float d;
+  int8_t qs[256];
+  int16_t bsums[16];
+};
+struct BlockQ4K {  // ggml block_q4_K: 144 bytes per 256 weights
+  uint16_t d;
+  uint16_t dmin;
+  uint8_t scales[12];
+  uint8_t qs[128];
+};
+#pragma pack(pop)
+static_assert(sizeof(BlockQ8) == 34, "q8_0 block");
+static_assert(sizeof(BlockQ4K) == 144, "q4_K block");
+
+// ggml x86 CPU activation quantizer (quantize_row_q8_0, AVX path):
+// amax over the block, d = amax/127 stored as f16, codes = round-half-even of
+// x * (127/amax). Used by ggml_mul_mat for vec_dot_type == Q8_0
+// (asserted by the reference at src/cpu_q8.cpp:23-24).
+void quantize_q8_0_act(const float* x, int64_t k, BlockQ8* y) {
+  for (int64_t b = 0; b < k / 32; ++b) {
+    const float* v = x + b * 32;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) amax = std::max(amax, std::fabs(v[j]));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    y[b].d = f2h(d);
+    for (int j = 0; j < 32; ++j) y[b].qs[j] = (int8_t)std::nearbyint(v[j] * id);
+  }
+}
+
+// ggml quantize_row_q8_K_ref: signed max, iscale = -127/max, nearest int,
+// clamp to 127, d = 1/iscale, bsums over 16-element groups.
+int nearest_int(float f) {
+  float val = f + 12582912.0f;
+  int i;
+  std::memcpy(&i, &val, 4);
+  return (i & 0x007fffff) - 0x00400000;
+}
+void quantize_q8_k_act(const float* x, int64_t k, BlockQ8K* y) {
+  for (int64_t b = 0; b < k / 256; ++b) {
+    const float* v = x + b * 256;
+    float max = 0.0f, amax = 0.0f;
+    for (int j = 0; j < 256; ++j) {
+      const float ax = std::fabs(v[j]);
+      if (ax > amax) {
+        amax = ax;
+        max = v[j];
+      }
+    }
+    if (amax == 0.0f) {
+      y[b].d = 0.0f;
+      std::memset(y[b].qs, 0, 256);
+      std::memset(y[b].bsums, 0, sizeof(y[b].bsums));
+      continue;
+    }
+    const float iscale = -127.0f / max;
+    for (int j = 0; j < 256; ++j) y[b].qs[j] = (int8_t)std::min(127, nearest_int(iscale * v[j]));
+    for (int g = 0; g < 16; ++g) {
+      int s = 0;
+      for (int i = 0; i < 16; ++i) s += y[b].qs[g * 16 + i];
+      y[b].bsums[g] = (int16_t)s;
+    }
+    y[b].d = 1.0f / iscale;
+  }
+}
+
+// q4_K 6-bit scale/min unpacking (GGUF q4_K format, get_scale_min_k4).
+void q4k_scale_min(int j, const uint8_t* q, int* sc, int* mn) {
+  if (j < 4) {
+    *sc = q[j] & 63;
+    *mn = q[j + 4] & 63;
+  } else {
+    *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+    *mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+int32_t q8_block_dot(const BlockQ8& a, const BlockQ8& b) {
+  int32_t s = 0;
+  for (int j = 0; j < 32; ++j) s += (int32_t)a.qs[j] * (int32_t)b.qs[j];
+  return s;
+}
+
+// mul_mat(q8_0 W, f32 x) as ggml runs it: x quantized to q8_0, then per block
+// y += (d_w * d_x) * isum with an exact int32 isum per 32-block.
+void mul_mat_q8(const BlockQ8* w, int k, int n, const float* x, int T, float* y) {
+  const int nb = k / 32;
+  std::vector<BlockQ8> xq((size_t)T * nb);
+  for (int t = 0; t < T; ++t) quantize_q8_0_act(x + (size_t)t * k, k, xq.data() + (size_t)t * nb);
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < n; ++r) {
+    const BlockQ8* wr = w + (size_t)r * nb;
+    for (int t = 0; t < T; ++t) {
+      const BlockQ8* xr = xq.data() + (size_t)t * nb;
+      float acc = 0.0f;
+      for (int b = 0; b < nb; ++b) {
+        const float d = h2f(wr[b].d) * h2f(xr[b].d);
+        acc += d * (float)q8_block_dot(wr[b], xr[b]);
+      }
+      y[(size_t)t * n + r] = acc;
+    }
+  }
+}
+
+// mul_mat(f16 W, f32 x): x converted to f16 (vec_dot_type F16), f32 accumulation.
+void mul_mat_f16(const uint16_t* w, int k, int n, const float* x, int T, float* y) {
+  std::vector<float> xh((size_t)T * k);
+  for (size_t i = 0; i < xh.size(); ++i) xh[i] = h2f(f2h(x[i]));
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < n; ++r) {
+    const uint16_t* wr = w + (size_t)r * k;
+    for (int t = 0; t < T; ++t) {
+      const float* xr = xh.data() + (size_t)t * k;
+      float acc = 0.0f;
+      for (int i = 0; i < k; ++i) acc += h2f(wr[i]) * xr[i];
+      y[(size_t)t * n + r] = acc;
+    }
+  }
+}
+
+// mul_mat(q4_K W, f32 x): x quantized to q8_K; per 256-superblock exact int32
+// sums sum_j sc_j * dot_j and sum_j mn_j * bsum_j, combined as
+// (d_w*d_x)*dot - (dmin_w*d_x)*min.
+void mul_mat_q4k(const BlockQ4K* w, int k, int n, const float* x, int T, float* y) {
+  const int nb = k / 256;
+  std::vector<BlockQ8K> xq((size_t)T * nb);
+  for (int t = 0; t < T; ++t) quantize_q8_k_act(x + (size_t)t * k, k, xq.data() + (size_t)t * nb);
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < n; ++r) {
+    const BlockQ4K* wr = w + (size_t)r * nb;
+    for (int t = 0; t < T; ++t) {
+      const BlockQ8K* xr = xq.data() + (size_t)t * nb;
+      float acc = 0.0f;
+      for (int b = 0; b < nb; ++b) {
+        int32_t dot = 0, mins = 0;
+        for (int s = 0; s < 8; ++s) {
+          int sc, mn;
+          q4k_scale_min(s, wr[b].scales, &sc, &mn);
+          const uint8_t* q = wr[b].qs + (s / 2) * 32;
+          int32_t sub = 0;
+          for (int l = 0; l < 32; ++l) {
+            const int v = (s & 1) ? (q[l] >> 4) : (q[l] & 0xF);
+            sub += v * xr[b].qs[s * 32 + l];
+          }
+          dot += sc * sub;
+          mins += mn * (xr[b].bsums[2 * s] + xr[b].bsums[2 * s + 1]);
+        }
+        const float d = h2f(wr[b].d) * xr[b].d;
+        const float dmin = h2f(wr[b].dmin) * xr[b].d;
+        acc += d * (float)dot;
+        acc -= dmin * (float)mins;
+      }
+      y[(size_t)t * n + r] = acc;
+    }
+  }
+}
+
+void mul_mat(int wtype, const void* w, int k, int n, const float* x, int T, float* y) {
+  if (wtype == MTG_TYPE_Q8_0) mul_mat_q8((const BlockQ8*)w, k, n, x, T, y);
+  else if (wtype == MTG_TYPE_F16) mul_mat_f16((const uint16_t*)w, k, n, x, T, y);
+  else mul_mat_q4k((const BlockQ4K*)w, k, n, x, T, y);
+}
+
+// ggml_rms_norm (x*x summed in double, mean cast to float, 1/sqrtf), then
+// ggml_mul by the gain as a separate op (src/qwen3.cpp:27-30).
+void rms_norm(const float* x, const float* w, int n, float eps, float* y) {
+  double sum = 0.0;
+  for (int i = 0; i < n; ++i) sum += (double)(x[i] * x[i]);
+  const float mean = (float)(sum / n);
+  const float scale = 1.0f / std::sqrt(mean + eps);
+  for (int i = 0; i < n; ++i) {
+    const float v = x[i] * scale;
+    y[i] = v * w[i];
+  }
+}
+
+// NEOX RoPE as ggml_rope_ext builds it (src/qwen3.cpp:108-118, mode NEOX):
+// theta_scale = powf(base, -2/n_dims); theta_0 = pos, theta_{i+1} = theta_i *
+// theta_scale in float; pairs (i, i + n_dims/2); ext_factor 0, attn_factor 1.
+void rope_table(int pos, int n_dims, float base, float* cs) {
+  const float theta_scale = std::pow(base, -2.0f / (float)n_dims);
+  float theta = (float)pos;
+  for (int i = 0; i < n_dims / 2; ++i) {
+    cs[2 * i] = std::cos(theta);
+    cs[2 * i + 1] = std::sin(theta);
+    theta *= theta_scale;
+  }
+}
+void rope_apply(float* x, int n_dims, const float* cs) {
+  const int half = n_dims / 2;
+  for (int i = 0; i < half; ++i) {
+    const float x0 = x[i], x1 = x[i + half];
+    const float c = cs[2 * i], s = cs[2 * i + 1];
+    x[i] = x0 * c - x1 * s;
+    x[i + half] = x0 * s + x1 * c;
+  }
+}
+
+// ggml_soft_max_ext(scores, mask, scale) row: scale, add mask, max, expf and a
+// double sum, multiply by (float)(1/sum) (op order of src/cpu_softmax.cpp:27-36
+// with the mask add of soft_max_ext).
+void softmax_row(const float* s, int n, float scale, const float* mask, float* out) {
+  std::vector<float> w(n);
+  for (int i = 0; i < n; ++i) {
+    w[i] = s[i] * scale;
+    if (mask) w[i] += mask[i];
+  }
+  float max = -INFINITY;
+  for (int i = 0; i < n; ++i) max = std::max(max, w[i]);
+  double sum = 0.0;
+  for (int i = 0; i < n; ++i) {
+    const float e = std::exp(w[i] - max);
+    sum += (double)e;
+    out[i] = e;
+  }
+  const float inv = (float)(1.0 / sum);
+  for (int i = 0; i < n; ++i) out[i] *= inv;
+}
+
+float silu(float g) { return g / (1.0f + std::exp(-g)); }
+
+}  // namespace
+
+// ------------------------------------------------------------- model -------
+struct orc_model {
+  mtg_hparams hp{};
+  int wtype = MTG_TYPE_Q8_0;
+  int kv_type = MTG_TYPE_F32;
+  int max_seq = 0, past = 0;
+  std::vector<std::vector<uint8_t>> wq, wk, wv, wo, wg, wu, wd;
+  std::vector<std::vector<float>> attn_norm, q_norm, k_norm, ffn_norm;
+  std::vector<uint8_t> embd;
+  std::vector<float> out_norm;
+  // KV cache [layer][kv_head][pos][head_dim], f32 or f16 bits.
+  std::vector<float> k32, v32;
+  std::vector<uint16_t> k16, v16;
+  size_t layer_stride = 0;  // elements per layer
+};
+
+namespace {
+size_t row_bytes(int type, int64_t k) {
+  if (type == MTG_TYPE_Q8_0) return (size_t)(k / 32) * 34;
+  if (type == MTG_TYPE_F16) return (size_t)k * 2;
+  if (type == MTG_TYPE_Q4_K) return (size_t)(k / 256) * 144;
+  return (size_t)k * 4;
+}
+std::vector<uint8_t> copy_matrix(const void* p, int type, int64_t k, int64_t n) {
+  const size_t bytes = row_bytes(type, k) * (size_t)n;
+  std::vector<uint8_t> v(bytes);
+  std::memcpy(v.data(), p, bytes);
+  return v;
+}
+
+void embed_row(const orc_model& m, int32_t id, float* out) {
+  const int H = m.hp.hidden;
+  const uint8_t* row = m.embd.data() + row_bytes(m.wtype, H) * (size_t)id;
+  if (m.wtype == MTG_TYPE_Q8_0) {
+    const BlockQ8* b = (const BlockQ8*)row;
+    for (int i = 0; i < H; ++i) out[i] = h2f(b[i / 32].d) * (float)b[i / 32].qs[i % 32];
+  } else if (m.wtype == MTG_TYPE_F16) {
+    const uint16_t* h = (const uint16_t*)row;
+    for (int i = 0; i < H; ++i) out[i] = h2f(h[i]);
+  } else {
+    const BlockQ4K* b = (const BlockQ4K*)row;
+    for (int sb = 0; sb < H / 256; ++sb) {
+      const float d = h2f(b[sb].d), dmin = h2f(b[sb].dmin);
+      for (int s = 0; s < 8; ++s) {
+        int sc, mn;
+        q4k_scale_min(s, b[sb].scales, &sc, &mn);
+        const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+        const uint8_t* q = b[sb].qs + (s / 2) * 32;
+        for (int l = 0; l < 32; ++l) {
+          const int v = (s & 1) ? (q[l] >> 4) : (q[l] & 0xF);
+          out[sb * 256 + s * 32 + l] = d1 * (float)v - m1;
+        }
+      }
+    }
+  }
+}
+
+inline float kv_get(const orc_model& m, bool is_k, size_t idx) {
+  if (m.kv_type == MTG_TYPE_F32) return is_k ? m.k32[idx] : m.v32[idx];
+  return h2f(is_k ? m.k16[idx] : m.v16[idx]);
+}
+inline void kv_set(orc_model& m, bool is_k, size_t idx, float v) {
+  if (m.kv_type == MTG_TYPE_F32) (is_k ? m.k32 : m.v32)[idx] = v;
+  else (is_k ? m.k16 : m.v16)[idx] = f2h(v);  // ggml_cpy f32 -> f16
+}
+
+// One qwen3_layer_forward over T rows at positions past..past+T-1
+// (src/qwen3.cpp:62-218 with the device-cache path, transposed-V semantics and
+// the causal-context op of src/cpu_context.cpp:13-32).
+void layer_forward(orc_model& m, int l, float* x, int T) {
+  const mtg_hparams& hp = m.hp;
+  const int H = hp.hidden, D = hp.head_dim, NH = hp.n_heads, NKV = hp.n_kv_heads;
+  const int QN = NH * D, KN = NKV * D, F = hp.intermediate;
+  const int past = m.past, kv = past + T, groups = NH / NKV;
+  std::vector<float> xn((size_t)T * H), q((size_t)T * QN), k((size_t)T * KN), v((size_t)T * KN);
+  for (int t = 0; t < T; ++t)
+    rms_norm(x + (size_t)t * H, m.attn_norm[l].data(), H, hp.rms_eps, xn.data() + (size_t)t * H);
+  mul_mat(m.wtype, m.wq[l].data(), H, QN, xn.data(), T, q.data());
+  mul_mat(m.wtype, m.wk[l].data(), H, KN, xn.data(), T, k.data());
+  mul_mat(m.wtype, m.wv[l].data(), H, KN, xn.data(), T, v.data());
+  // per-head q/k RMSNorm over head_dim, then NEOX RoPE at pos = past + t
+  std::vector<float> cs(D);
+  std::vector<float> tmp(D);
+  for (int t = 0; t < T; ++t) {
+    rope_table(past + t, D, hp.rope_base, cs.data());
+    for (int h = 0; h < NH; ++h) {
+      float* qh = q.data() + (size_t)t * QN + (size_t)h * D;
+      rms_norm(qh, m.q_norm[l].data(), D, hp.rms_eps, tmp.data());
+      rope_apply(tmp.data(), D, cs.data());
+      std::memcpy(qh, tmp.data(), D * sizeof(float));
+    }
+    for (int h = 0; h < NKV; ++h) {
+      float* kh = k.data() + (size_t)t * KN + (size_t)h * D;
+      rms_norm(kh, m.k_norm[l].data(), D, hp.rms_eps, tmp.data());
+      rope_apply(tmp.data(), D, cs.data());
+      std::memcpy(kh, tmp.data(), D * sizeof(float));
+    }
+  }
+  // KV store at past (src/qwen3.cpp:123-139)
+  const size_t base = (size_t)l * m.layer_stride;
+  for (int t = 0; t < T; ++t)
+    for (int h = 0; h < NKV; ++h)
+      for (int d = 0; d < D; ++d) {
+        const size_t idx = base + ((size_t)h * m.max_seq + (size_t)(past + t)) * D + d;
+        kv_set(m, true, idx, k[(size_t)t * KN + (size_t)h * D + d]);
+        kv_set(m, false, idx, v[(size_t)t * KN + (size_t)h * D + d]);
+      }
+  // eager GQA attention: scores K.Q (f32), soft_max_ext with scale 1/sqrt(D)
+  // and the causal mask, then the context at each query's valid length.
+  const float scale = 1.0f / std::sqrt((float)D);
+  const bool f16kv = m.kv_type == MTG_TYPE_F16;
+  std::vector<float> o((size_t)T * QN);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int h = 0; h < NH; ++h)
+    for (int t = 0; t < T; ++t) {
+      const int g = h / groups;
+      std::vector<float> s(kv), mask(kv), p(kv), qv(D);
+      const float* qh = q.data() + (size_t)t * QN + (size_t)h * D;
+      for (int d = 0; d < D; ++d) qv[d] = f16kv ? h2f(f2h(qh[d])) : qh[d];
+      for (int j = 0; j < kv; ++j) {
+        const size_t kb = base + ((size_t)g * m.max_seq + j) * D;
+        float acc = 0.0f;
+        for (int d = 0; d < D; ++d) acc += kv_get(m, true, kb + d) * qv[d];
+        s[j] = acc;
+        mask[j] = (T > 1 && j > past + t) ? -INFINITY : 0.0f;
+      }
+      softmax_row(s.data(), kv, scale, mask.data(), p.data());
+      if (f16kv)
+        for (int j = 0; j < kv; ++j) p[j] = h2f(f2h(p[j]));
+      float* oh = o.data() + (size_t)t * QN + (size_t)h * D;
+      const int valid = past + t + 1;
+      for (int d = 0; d < D; ++d) {
+        float acc = 0.0f;
+        for (int j = 0; j < valid; ++j)
+          acc += kv_get(m, false, base + ((size_t)g * m.max_seq + j) * D + d) * p[j];
+        oh[d] = acc;
+      }
+    }
+  // o-proj + residual, FFN pre-norm, SwiGLU, down + residual
+  std::vector<float> ao((size_t)T * H);
+  mul_mat(m.wtype, m.wo[l].data(), QN, H, o.data(), T, ao.data());
+  for (size_t i = 0; i < (size_t)T * H; ++i) x[i] = x[i] + ao[i];
+  for (int t = 0; t < T; ++t)
+    rms_norm(x + (size_t)t * H, m.ffn_norm[l].data(), H, hp.rms_eps, xn.data() + (size_t)t * H);
+  std::vector<float> g((size_t)T * F), u((size_t)T * F), act((size_t)T * F);
+  mul_mat(m.wtype, m.wg[l].data(), H, F, xn.data(), T, g.data());
+  mul_mat(m.wtype, m.wu[l].data(), H, F, xn.data(), T, u.data());
+  for (size_t i = 0; i < act.size(); ++i) act[i] = silu(g[i]) * u[i];
+  mul_mat(m.wtype, m.wd[l].data(), F, H, act.data(), T, ao.data());
+  for (size_t i = 0; i < (size_t)T * H; ++i) x[i] = x[i] + ao[i];
+}
+
+}  // namespace
+
+extern "C" {
+
+uint16_t orc_f32_to_f16(float f) { return f2h(f); }
+float orc_f16_to_f32(uint16_t h) { return h2f(h); }
+void orc_quantize_q8_0_act(const float* x, int64_t k, void* blocks) {
+  quantize_q8_0_act(x, k, (BlockQ8*)blocks);
+}
+void orc_quantize_q8_k_act(const float* x, int64_t k, void* blocks) {
+  quantize_q8_k_act(x, k, (BlockQ8K*)blocks);
+}
+int32_t orc_q8_0_block_dot(const void* a, const void* b) {
+  return q8_block_dot(*(const BlockQ8*)a, *(const BlockQ8*)b);
+}
+void orc_mul_mat(int32_t wtype, const void* w, int32_t k, int32_t n, const float* x, int32_t T,
+                 float* y) {
+  mul_mat(wtype, w, k, n, x, T, y);
+}
+void orc_rms_norm(const float* x, const float* w, int32_t n, float eps, float* y) {
+  rms_norm(x, w, n, eps, y);
+}
+void orc_rope_neox(float* x, int32_t n_dims, int32_t pos, float base) {
+  std::vector<float> cs(n_dims);
+  rope_table(pos, n_dims, base, cs.data());
+  rope_apply(x, n_dims, cs.data());
+}
+void orc_softmax(const float* s, int32_t n, float scale, const float* mask, float* out) {
+  softmax_row(s, n, scale, mask, out);
+}
+// cpu_causal_context (src/cpu_context.cpp:13-32): out[h][q][f] =
+// sum_{k < past+q+1} v[h/groups][k][f] * p[h][q][k], exactly the valid length.
+void orc_causal_context(const float* v, const float* p, int32_t head_dim, int32_t kv_heads,
+                        int32_t heads, int32_t queries, int32_t kv_len, float* out) {
+  const int groups = heads / kv_heads, past = kv_len - queries;
+  for (int h = 0; h < heads; ++h)
+    for (int q = 0; q < queries; ++q)
+      for (int f = 0; f < head_dim; ++f) {
+        float acc = 0.0f;
+        for (int k = 0; k < past + q + 1; ++k)
+          acc += v[((size_t)(h / groups) * kv_len + k) * head_dim + f] *
+                 p[((size_t)h * queries + q) * kv_len + k];
+        out[((size_t)h * queries + q) * head_dim + f] = acc;
+      }
+}
+
+void orc_set_threads(int n) {
+  if (n > 0) omp_set_num_threads(n);
+}
+
+int orc_create(const mtg_model_desc* desc, int32_t max_seq, int32_t kv_type, orc_model** out) {
+  if (!desc || !out || max_seq <= 0) return MTG_ERR_INVALID;
+  if (kv_type != MTG_TYPE_F32 && kv_type != MTG_TYPE_F16) return MTG_ERR_UNSUPPORTED;
+  const mtg_hparams& hp = desc->hp;
+  if (hp.hidden <= 0 || hp.n_layers <= 0 || hp.n_heads <= 0 || hp.n_kv_heads <= 0 ||
+      hp.head_dim <= 0 || hp.n_heads % hp.n_kv_heads)
+    return MTG_ERR_INVALID;
+  auto m = std::unique_ptr<orc_model>(new (std::nothrow) orc_model());
+  if (!m) return MTG_ERR_NOMEM;
+  m->hp = hp;
+  m->wtype = desc->weight_type;
+  m->kv_type = kv_type;
+  m->max_seq = max_seq;
+  const int H = hp.hidden, D = hp.head_dim, QN = hp.n_heads * D, KN = hp.n_kv_heads * D,
+            F = hp.intermediate;
+  for (int l = 0; l < hp.n_layers; ++l) {
+    const mtg_layer_tensors& L = desc->layers[l];
+    m->wq.push_back(copy_matrix(L.attn_q, m->wtype, H, QN));
+    m->wk.push_back(copy_matrix(L.attn_k, m->wtype, H, KN));
+    m->wv.push_back(copy_matrix(L.attn_v, m->wtype, H, KN));
+    m->wo.push_back(copy_matrix(L.attn_o, m->wtype, QN, H));
+    m->wg.push_back(copy_matrix(L.ffn_gate, m->wtype, H, F));
+    m->wu.push_back(copy_matrix(L.ffn_up, m->wtype, H, F));
+    m->wd.push_back(copy_matrix(L.ffn_down, m->wtype, F, H));
+    m->attn_norm.emplace_back(L.attn_norm, L.attn_norm + H);
+    m->q_norm.emplace_back(L.attn_q_norm, L.attn_q_norm + D);
+    m->k_norm.emplace_back(L.attn_k_norm, L.attn_k_norm + D);
+    m->ffn_norm.emplace_back(L.ffn_norm, L.ffn_norm + H);
+  }
+  m->embd = copy_matrix(desc->token_embd, m->wtype, H, hp.vocab);
+  m->out_norm.assign(desc->output_norm, desc->output_norm + H);
+  m->layer_stride = (size_t)hp.n_kv_heads * max_seq * D;
+  const size_t total = m->layer_stride * hp.n_layers;
+  if (kv_type == MTG_TYPE_F32) {
+    m->k32.assign(total, 0.0f);
+    m->v32.assign(total, 0.0f);
+  } else {
+    m->k16.assign(total, 0);
+    m->v16.assign(total, 0);
+  }
+  *out = m.release();
+  return MTG_OK;
+}
+
+void orc_destroy(orc_model* m) { delete m; }
+int32_t orc_past_len(const orc_model* m) { return m ? m->past : 0; }
+
+// CpuSpeculativeDecoder::rewind (src/cpu_speculative.cpp:40-42).
+int orc_rewind(orc_model* m, int32_t position) {
+  if (!m || position < 0 || position > m->past) return MTG_ERR_STATE;
+  m->past = position;
+  return MTG_OK;
+}
+
+// embed_rows_f32 host path: dequantize the selected token_embd rows
+// (src/generate.cpp:33-66).
+int orc_embed(orc_model* m, const int32_t* ids, int32_t n, float* out) {
+  if (!m || !ids || n <= 0 || !out) return MTG_ERR_INVALID;
+  for (int i = 0; i < n; ++i) {
+    if (ids[i] < 0 || ids[i] >= m->hp.vocab) return MTG_ERR_INVALID;
+    embed_row(*m, ids[i], out + (size_t)i * m->hp.hidden);
+  }
+  return MTG_OK;
+}
+
+// Qwen3Decoder::run (src/qwen3_decoder.cpp:91-160): 28 layers over T rows at
+// past, final RMSNorm * output_norm on every row, past += T.
+int orc_run(orc_model* m, const float* embeds, int32_t T, float* hidden_out) {
+  if (!m || !embeds || T <= 0) return MTG_ERR_INVALID;
+  if (m->past + T > m->max_seq) return MTG_ERR_CAPACITY;
+  const int H = m->hp.hidden;
+  std::vector<float> x(embeds, embeds + (size_t)T * H);
+  for (int l = 0; l < m->hp.n_layers; ++l) layer_forward(*m, l, x.data(), T);
+  m->past += T;
+  if (hidden_out)
+    for (int t = 0; t < T; ++t)
+      rms_norm(x.data() + (size_t)t * H, m->out_norm.data(), H, m->hp.rms_eps,
+               hidden_out + (size_t)t * H);
+  return MTG_OK;
+}
+
+int orc_prefill(orc_model* m, const float* embeds, int32_t S, float* hidden_out) {
+  if (!m) return MTG_ERR_INVALID;
+  m->past = 0;
+  return orc_run(m, embeds, S, hidden_out);
+}
+
+// logits_from_hidden (src/qwen3_decoder.cpp:174-205), row by row.
+int orc_logits(orc_model* m, const float* hidden, int32_t T, float* logits_out) {
+  if (!m || !hidden || T <= 0 || !logits_out) return MTG_ERR_INVALID;
+  mul_mat(m->wtype, m->embd.data(), m->hp.hidden, m->hp.vocab, hidden, T, logits_out);
+  return MTG_OK;
+}
+
+// cpu_ngram_draft (src/cpu_speculative.cpp:45-56): for n = min(16,|h|-1)..2
+// the latest earlier occurrence of the last-n suffix; up to `maximum` tokens
+// that follow it.
+int32_t orc_ngram_draft(const int32_t* h, int32_t size, int32_t maximum, int32_t* out) {
+  if (maximum <= 0 || size < 3) return 0;
+  for (int n = std::min<int>(16, size - 1); n >= 2; --n)
+    for (int start = size - n - 1; start >= 0; --start) {
+      if (std::equal(h + size - n, h + size, h + start)) {
+        const int begin = start + n;
+        const int count = std::min<int>(maximum, size - begin);
+        for (int i = 0; i < count; ++i) out[i] = h[begin + i];
+        return count;
+      }
+    }
+  return 0;
+}
+
+// cpu_greedy_choice (src/cpu_speculative.cpp:57-68): first maximum (strict >)
+// after dividing positive / multiplying negative logits of the distinct ids of
+// the last 100 history entries by the penalty.
+int32_t orc_greedy_choice(const float* raw, int32_t n, const int32_t* history, int32_t nh,
+                          float penalty) {
+  if (!raw || n <= 0) return -1;
+  std::vector<float> adj(raw, raw + n);
+  if (penalty > 1.0f) {
+    std::set<int32_t> recent;
+    for (int i = std::max(0, nh - 100); i < nh; ++i) recent.insert(history[i]);
+    for (int32_t id : recent)
+      if (id >= 0 && id < n) adj[id] = adj[id] > 0 ? adj[id] / penalty : adj[id] * penalty;
+  }
+  int best = 0;
+  for (int i = 1; i < n; ++i)
+    if (adj[i] > adj[best]) best = i;
+  return best;
+}
+
+// One verify step: append all T rows, logits of every row, greedy choice of
+// row i over history ++ tokens[0..i], leading matches.
+int orc_verify(orc_model* m, const int32_t* tokens, int32_t T, const int32_t* history,
+               int32_t n_history, float penalty, int32_t* choice_out, int32_t* n_match_out,
+               float* hidden_out, float* logits_out) {
+  if (!m || !tokens || T <= 0 || T > MTG_MAX_BATCH || !choice_out || !n_match_out)
+    return MTG_ERR_INVALID;
+  const int H = m->hp.hidden, V = m->hp.vocab;
+  std::vector<float> emb((size_t)T * H), hid((size_t)T * H), logits((size_t)T * V);
+  int rc = orc_embed(m, tokens, T, emb.data());
+  if (rc) return rc;
+  rc = orc_run(m, emb.data(), T, hid.data());
+  if (rc) return rc;
+  orc_logits(m, hid.data(), T, logits.data());
+  std::vector<int32_t> hist(history, history + (history ? n_history : 0));
+  int match = 0;
+  bool run = true;
+  for (int i = 0; i < T; ++i) {
+    hist.push_back(tokens[i]);
+    choice_out[i] = orc_greedy_choice(logits.data() + (size_t)i * V, V, hist.data(),
+                                      (int)hist.size(), penalty);
+    if (run && i + 1 < T && tokens[i + 1] == choice_out[i]) ++match;
+    else run = false;
+  }
+  *n_match_out = match;
+  if (hidden_out) std::memcpy(hidden_out, hid.data(), hid.size() * sizeof(float));
+  if (logits_out) std::memcpy(logits_out, logits.data(), logits.size() * sizeof(float));
+  return MTG_OK;
+}
+
+int orc_kv_write(orc_model* m, const void* k, const void* v, int32_t n_pos) {
+  if (!m || !k || !v || n_pos < 0 || n_pos > m->max_seq) return MTG_ERR_INVALID;
+  const int L = m->hp.n_layers, NKV = m->hp.n_kv_heads, D = m->hp.head_dim;
+  const size_t es = m->kv_type == MTG_TYPE_F32 ? 4 : 2;
+  for (int l = 0; l < L; ++l)
+    for (int h = 0; h < NKV; ++h) {
+      const size_t src = (((size_t)l * NKV + h) * n_pos) * D;
+      const size_t dst = (size_t)l * m->layer_stride + (size_t)h * m->max_seq * D;
+      if (es == 4) {
+        std::memcpy(&m->k32[dst], (const float*)k + src, (size_t)n_pos * D * 4);
+        std::memcpy(&m->v32[dst], (const float*)v + src, (size_t)n_pos * D * 4);
+      } else {
+        std::memcpy(&m->k16[dst], (const uint16_t*)k + src, (size_t)n_pos * D * 2);
+        std::memcpy(&m->v16[dst], (const uint16_t*)v + src, (size_t)n_pos * D * 2);
+      }
+    }
+  m->past = n_pos;
+  return MTG_OK;
+}
+
+int orc_kv_read(const orc_model* m, void* k, void* v, int32_t n_pos) {
+  if (!m || !k || !v || n_pos < 0 || n_pos > m->max_seq) return MTG_ERR_INVALID;
+  const int L = m->hp.n_layers, NKV = m->hp.n_kv_heads, D = m->hp.head_dim;
+  for (int l = 0; l < L; ++l)
+    for (int h = 0; h < NKV; ++h) {
+      const size_t dst = (((size_t)l * NKV + h) * n_pos) * D;
+      const size_t src = (size_t)l * m->layer_stride + (size_t)h * m->max_seq * D;
+      if (m->kv_type == MTG_TYPE_F32) {
+        std::memcpy((float*)k + dst, &m->k32[src], (size_t)n_pos * D * 4);
+        std::memcpy((float*)v + dst, &m->v32[src], (size_t)n_pos * D * 4);
+      } else {
+        std::memcpy((uint16_t*)k + dst, &m->k16[src], (size_t)n_pos * D * 2);
+        std::memcpy((uint16_t*)v + dst, &m->v16[src], (size_t)n_pos * D * 2);
+      }
+    }
+  return MTG_OK;
+}
+
+// The controller loop of cpu_speculative_generate (src/cpu_speculative.cpp:
+// 118-155), continuing from an existing target state: emit the seed (eos /
+// token_limit stops), budget = min(max_draft, max_new-|ids|, remaining-1), draft,
+// append seed+drafts, accept while the draft equals the greedy choice of the
+// previous row, the terminating token is emitted but not kept, logical rewind.
+int orc_controller(orc_target* tg, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
+                   int32_t max_new, int32_t max_steps, int32_t eos, float penalty,
+                   int32_t max_draft, mtg_draft_fn draft, void* user, int32_t* ids_out,
+                   int32_t* n_ids_out, mtg_gen_stats* stats) {
+  if (!tg || !tg->verify || !ids_out || !n_ids_out || max_new <= 0) return MTG_ERR_INVALID;
+  penalty = std::max(1.0f, std::min(1.5f, penalty));
+  std::vector<int32_t> ids(prior_ids, prior_ids + (prior_ids ? n_prior : 0));
+  const size_t first_new = ids.size();
+  mtg_gen_stats st{};
+  int stop = 0;
+  auto emit = [&](int32_t id) {
+    ids.push_back(id);
+    if (id == eos) stop = 1;
+    else if ((int)(ids.size() - first_new) >= max_new) stop = 2;
+  };
+  int32_t raw_choice = first_seed;
+  int steps = 0;
+  int rc = MTG_OK;
+  std::vector<int32_t> proposal(MTG_MAX_BATCH), choice(MTG_MAX_BATCH);
+  while (!stop) {
+    if (max_steps > 0 && steps >= max_steps) break;
+    const int32_t seed = raw_choice;
+    emit(seed);
+    if (stop) break;
+    const int before = tg->past;
+    const int remaining = tg->max_seq - tg->past;
+    const int budget = std::max(0, std::min({max_draft, max_new - (int)(ids.size() - first_new),
+                                              remaining - 1, MTG_MAX_BATCH - 1}));
+    int np = draft ? draft(user, ids.data(), (int)ids.size(), budget, proposal.data())
+                   : orc_ngram_draft(ids.data(), (int)ids.size(), budget, proposal.data());
+    np = std::max(0, std::min(np, budget));
+    for (int i = 0; i < np; ++i)
+      if (proposal[i] < 0 || proposal[i] >= tg->vocab) { rc = MTG_ERR_INVALID; break; }
+    if (rc) break;
+    std::vector<int32_t> inputs{seed};
+    inputs.insert(inputs.end(), proposal.begin(), proposal.begin() + np);
+    int32_t n_match = 0;
+    // history for row i = ids before the seed ++ inputs[0..i]
+    rc = tg->verify(tg, inputs.data(), (int)inputs.size(), ids.data(), (int)ids.size() - 1,
+                    penalty, choice.data(), &n_match);
+    if (rc) break;
+    tg->past += (int)inputs.size();
+    ++steps;
+    ++st.target_calls;
+    st.drafted_calls += np > 0;
+    st.proposed += np;
+    st.target_input_tokens += (int)inputs.size();
+    int keep = 1;
+    raw_choice = choice[0];
+    for (int i = 0; i < np; ++i) {
+      if (proposal[i] != choice[i]) break;
+      ++st.accepted;
+      emit(proposal[i]);
+      if (stop) break;
+      ++keep;
+      raw_choice = choice[i + 1];
+    }
+    const int position = before + keep;
+    if (tg->past != position) {
+      tg->past = position;
+      ++st.rewinds;
+    }
+  }
+  st.stop_reason = stop;
+  st.next_seed = raw_choice;
+  const int n_new = (int)(ids.size() - first_new);
+  std::memcpy(ids_out, ids.data() + first_new, (size_t)n_new * sizeof(int32_t));
+  *n_ids_out = n_new;
+  if (stats) *stats = st;
+  return rc;
+}
+
+namespace {
+int model_verify(orc_target* tg, const int32_t* tokens, int32_t T, const int32_t* history,
+                 int32_t n_history, float penalty, int32_t* choice_out, int32_t* n_match_out) {
+  orc_model* m = (orc_model*)tg->self;
+  m->past = tg->past;
+  return orc_verify(m, tokens, T, history, n_history, penalty, choice_out, n_match_out, nullptr,
+                    nullptr);
+}
+}  // namespace
+
+int orc_generate_from(orc_model* m, int32_t first_seed, const int32_t* prior_ids,
+                      int32_t n_prior, int32_t max_new, int32_t max_steps, int32_t eos,
+                      float penalty, int32_t max_draft, mtg_draft_fn draft, void* user,
+                      int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats) {
+  if (!m) return MTG_ERR_INVALID;
+  orc_target tg{m, model_verify, m->past, m->max_seq, m->hp.vocab};
+  const int rc = orc_controller(&tg, first_seed, prior_ids, n_prior, max_new, max_steps, eos,
+                                penalty, max_draft, draft, user, ids_out, n_ids_out, stats);
+  m->past = tg.past;
+  return rc;
+}
+
+}  // extern "C"
