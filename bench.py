@@ -109,7 +109,8 @@ def main():
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--eager", action="store_true", help="launch kernels without graph replay")
+    ap.add_argument("--exec", choices=["step", "graph", "eager"], default="step",
+                    help="persistent step kernel, per-op kernels from a graph, or eager per-op")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box here has one MI355X, and the verify path "
@@ -123,8 +124,7 @@ def main():
     n_prompt = cfg["blocks"] * AUDIO_ROWS + cfg["text"]
     max_seq = n_prompt + (args.warmup + steps + 2) * cfg["K"] + 16
     dec = mtg.Decoder(model, max_seq, cfg["kv"])
-    if args.eager:
-        dec.set_graphs(False)
+    dec.set_exec({"step": mtg.EXEC_STEP_KERNEL, "graph": mtg.EXEC_GRAPH, "eager": mtg.EXEC_EAGER}[args.exec])
     rows, text, stream = build_prompt(model, dec, cfg)
     hid = dec.prefill(rows)
     first = int(np.argmax(dec.logits(hid[-1:])[0]))
@@ -167,7 +167,7 @@ def main():
                                           "f32" if cfg["kv"] == mtg.TYPE_F32 else "f16"),
                    "verify_rows": cfg["K"], "context_start": ctx_start, "context_end": dec.past_len,
                    "accepted_per_step": st.accepted / max(n_steps, 1),
-                   "tokens": tokens, "graphs": not args.eager},
+                   "tokens": tokens, "exec": args.exec},
         "step_us": 1e3 * ms_step,
         "step_bytes": step_bytes,
         "step_hbm_fraction": step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS,

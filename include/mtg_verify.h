@@ -198,8 +198,19 @@ typedef struct mtg_stream_drafter {
 int32_t mtg_stream_draft(void* user, const int32_t* ids, int32_t n_ids, int32_t budget,
                          int32_t* out);
 
-/* 1 (default): replay each step from a captured HIP graph; 0: launch eagerly. */
-int mtg_set_graphs(mtg_ctx* ctx, int32_t enable);
+/* How a step runs on the device. MTG_EXEC_STEP_KERNEL (default where the shape
+ * allows): one persistent kernel per step. MTG_EXEC_GRAPH: the per-op kernels,
+ * replayed from a captured HIP graph. MTG_EXEC_EAGER: the per-op kernels launched
+ * one by one (profiling). All three produce the same results. */
+enum { MTG_EXEC_STEP_KERNEL = 0, MTG_EXEC_GRAPH = 1, MTG_EXEC_EAGER = 2 };
+int mtg_set_exec_mode(mtg_ctx* ctx, int32_t mode);
+int32_t mtg_exec_mode(const mtg_ctx* ctx);
+
+/* Diagnostics: copy an internal activation buffer of the last step (16 rows):
+ * the residual stream, the fused q|k|v projection, the attention output, the
+ * SwiGLU activation or the final-normed hidden rows. */
+enum { MTG_DEBUG_X = 0, MTG_DEBUG_QKV = 1, MTG_DEBUG_O = 2, MTG_DEBUG_ACT = 3, MTG_DEBUG_HIDDEN = 4 };
+int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes);
 
 /* Host policy functions (reference: cpu_ngram_draft, cpu_greedy_choice). */
 int32_t mtg_ngram_draft(const int32_t* history, int32_t n, int32_t maximum, int32_t* out);

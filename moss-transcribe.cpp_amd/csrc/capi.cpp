@@ -55,10 +55,33 @@ const char* mtg_last_error(const mtg_ctx* ctx) {
   return ctx ? ctx->impl.error.c_str() : g_create_error.c_str();
 }
 
-int mtg_set_graphs(mtg_ctx* ctx, int32_t enable) {
-  if (!ctx) return MTG_ERR_INVALID;
-  ctx->impl.use_graphs = enable != 0;
+int mtg_set_exec_mode(mtg_ctx* ctx, int32_t mode) {
+  if (!ctx || mode < MTG_EXEC_STEP_KERNEL || mode > MTG_EXEC_EAGER) return MTG_ERR_INVALID;
+  if (mode == MTG_EXEC_STEP_KERNEL && !ctx->impl.step_ok)
+    return ctx->impl.fail(MTG_ERR_UNSUPPORTED, "persistent step kernel unavailable for this shape");
+  ctx->impl.exec = mode;
   return MTG_OK;
+}
+
+int32_t mtg_exec_mode(const mtg_ctx* ctx) { return ctx ? ctx->impl.exec : -1; }
+
+int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes) {
+  if (!ctx || !out) return MTG_ERR_INVALID;
+  const Ctx& c = ctx->impl;
+  const int R = mtg::kMaxRows, H = c.hp.hidden, QN = c.hp.n_heads * c.hp.head_dim,
+            KN = c.hp.n_kv_heads * c.hp.head_dim, F = c.hp.intermediate;
+  const void* src = nullptr;
+  size_t size = 0;
+  switch (which) {
+    case MTG_DEBUG_X: src = c.x; size = (size_t)R * H * 4; break;
+    case MTG_DEBUG_QKV: src = c.qkv; size = (size_t)R * (QN + 2 * KN) * 4; break;
+    case MTG_DEBUG_O: src = c.obuf; size = (size_t)R * QN * 4; break;
+    case MTG_DEBUG_ACT: src = c.act; size = (size_t)R * F * 4; break;
+    case MTG_DEBUG_HIDDEN: src = c.hid; size = (size_t)R * H * 4; break;
+    default: return MTG_ERR_INVALID;
+  }
+  if (bytes < size) return MTG_ERR_INVALID;
+  return hipMemcpy(out, src, size, hipMemcpyDeviceToHost) == hipSuccess ? MTG_OK : MTG_ERR_DEVICE;
 }
 
 int32_t mtg_past_len(const mtg_ctx* ctx) { return ctx ? ctx->impl.past : 0; }

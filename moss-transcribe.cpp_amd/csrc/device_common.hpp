@@ -1,0 +1,357 @@
+// device_common.hpp - device helpers shared by the per-op kernels and the
+// persistent step kernel (q8_0 activation conversion, activation-panel layout,
+// the MFMA tile accumulator, KV loads, argmax keys).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "kernels.hpp"
+
+namespace mtg {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+namespace dev {
+
+// ---------------------------------------------------------------------------
+// Canonical arithmetic. The oracle (oracle/oracle.cpp) restates every one of
+// these orders, so device results equal the oracle's bit for bit:
+//  * exp: Cody-Waite reduction x = n ln2 + r, degree-7 Taylor polynomial in
+//    Horner form with fmaf, ldexp; 0 below -87, inf above 88.7.
+//  * q8_0 dot: K split in 4 slices of block pairs; per slice even and odd
+//    blocks accumulate acc = fmaf(isum, dw*dx, acc) in block order; slices add
+//    ((s0 + s1) + s2) + s3 per parity; result = even + odd.
+//  * row sums of squares (RMSNorm): 64 partials (lane l holds elements
+//    16l..16l+15 of a 1024 row, or l and l+64 of a 128 head), each a sequential
+//    double sum of float squares, reduced by the xor butterfly 32,16,8,4,2,1.
+//  * attention: keys in chunks of 64; score = fmaf chain over head_dim; per chunk
+//    max, p = exp(w - max), l = butterfly sum of p over the 64 keys, O = fmaf
+//    chain over the keys; chunks merged in order with f = exp(m_c - M),
+//    L = fmaf(l_c, f, L), O = fmaf(O_c, f, O), out = O / L.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float dev_expf(float x) {
+  if (x < -87.0f) return 0.0f;  // keeps every result a normal float
+  if (x > 88.7f) return INFINITY;
+  const float n = rintf(__fmul_rn(x, 1.44269504f));
+  float r = fmaf(n, -0.693145752f, x);
+  r = fmaf(n, -1.42860677e-06f, r);
+  float p = 1.98412698e-4f;             // 1/5040
+  p = fmaf(p, r, 1.38888889e-3f);       // 1/720
+  p = fmaf(p, r, 8.33333333e-3f);       // 1/120
+  p = fmaf(p, r, 4.16666667e-2f);       // 1/24
+  p = fmaf(p, r, 1.66666667e-1f);       // 1/6
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)n);
+}
+
+// Correctly rounded square root of a non-negative float. The hardware estimate
+// is within one ulp; the neighbour whose rounding interval holds x is chosen by
+// comparing x with the squared midpoints, all exact in double (a float has 24
+// significant bits, a midpoint 25, its square at most 50).
+__device__ __forceinline__ float dev_sqrtf(float x) {
+  if (!(x > 0.0f) || x == INFINITY) return __builtin_sqrtf(x);
+  float s = __builtin_sqrtf(x);
+  const float up = __uint_as_float(__float_as_uint(s) + 1u);
+  const float dn = __uint_as_float(__float_as_uint(s) - 1u);
+  const double xd = (double)x;
+  const double mu = ((double)s + (double)up) * 0.5, md = ((double)s + (double)dn) * 0.5;
+  if (xd > mu * mu) s = up;
+  else if (xd < md * md) s = dn;
+  return s;
+}
+
+// 1 / sqrt(mean + eps) of an RMSNorm row, correctly rounded at every step.
+__device__ __forceinline__ float dev_rms_scale(float mean, float eps) {
+  return __fdiv_rn(1.0f, dev_sqrtf(__fadd_rn(mean, eps)));
+}
+
+// silu(g) * u with the canonical exp and a correctly rounded division.
+__device__ __forceinline__ float dev_swiglu(float g, float u) {
+  return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, dev_expf(-g))), u);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// q8_0 activation conversion of one 32-element block held by 8 consecutive lanes
+// (4 elements each): d = amax/127 rounded to f16, codes = rint(x * 127/amax).
+// Returns the f32 value of the stored f16 scale.
+__device__ __forceinline__ float quant_block8(const float v[4], int8_t q[4]) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+  const float d = __fdiv_rn(amax, 127.0f);
+  const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+  for (int e = 0; e < 4; ++e) q[e] = (int8_t)rintf(__fmul_rn(v[e], id));
+  return __half2float(__float2half_rn(d));
+}
+
+// Panel position of element k of verify row t (see mtg_internal.hpp).
+__device__ __forceinline__ void panel_store4(Panel p, int bps, int t, int k, const int8_t q[4]) {
+  const int b = k >> 5, bp = b >> 1, par = b & 1, half = (k >> 4) & 1, byte = k & 15;
+  const int cg = t >> 3, j = par * 8 + (t & 7), g = 2 * par + half, lane = j + 16 * g;
+  uint32_t packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
+                    ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
+  *(uint32_t*)(p.codes + ((size_t)(cg * bps + bp)) * 1024 + lane * 16 + byte) = packed;
+}
+__device__ __forceinline__ void panel_store_scale(Panel p, int bps, int t, int block, float d) {
+  const int bp = block >> 1, par = block & 1, cg = t >> 3, j = par * 8 + (t & 7);
+  p.scales[(size_t)(cg * bps + bp) * 16 + j] = d;
+}
+
+// ----------------------------------------------------------- GEMM core ------
+// One wave accumulates a 16-row tile over block pairs [bp0, bp1) for every
+// column group: acc[cg][r] holds rows 4*(lane/16)+r of column lane%16, split by
+// block parity (columns 0-7 even blocks, 8-15 odd blocks of rows t = col%8).
+template <int G>
+__device__ __forceinline__ void tile_accumulate(const uint8_t* __restrict__ tile, int bp0, int bp1,
+                                                const uint8_t* __restrict__ pcodes,
+                                                const float* __restrict__ pscales, int bps,
+                                                float acc[G][4]) {
+  const int lane = threadIdx.x & 63;
+  const int par = (lane & 15) >> 3;
+  const int srow = par * 16 + 4 * (lane >> 4);
+  const v4i zero = {0, 0, 0, 0};
+#pragma unroll 4
+  for (int bp = bp0; bp < bp1; ++bp) {
+    const uint8_t* unit = tile + (size_t)bp * kUnitBytes;
+    const v4i a = *(const v4i*)(unit + lane * 16);
+    const uint2 sw = *(const uint2*)(unit + 1024 + srow * 2);
+    float dw[4];
+    dw[0] = half_bits_to_float((uint16_t)(sw.x & 0xffff));
+    dw[1] = half_bits_to_float((uint16_t)(sw.x >> 16));
+    dw[2] = half_bits_to_float((uint16_t)(sw.y & 0xffff));
+    dw[3] = half_bits_to_float((uint16_t)(sw.y >> 16));
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg) {
+      const v4i b = *(const v4i*)(pcodes + ((size_t)(cg * bps + bp)) * 1024 + lane * 16);
+      const float dx = pscales[(size_t)(cg * bps + bp) * 16 + (lane & 15)];
+      const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, zero, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[cg][r] = fmaf((float)c[r], dw[r] * dx, acc[cg][r]);
+    }
+  }
+}
+
+// One wave computes a whole tile in the canonical order: four slice
+// accumulators, summed ((s0 + s1) + s2) + s3, then even + odd parity.
+template <int G>
+__device__ __forceinline__ void tile_accumulate_canonical(const uint8_t* __restrict__ tile, int bps,
+                                                          const uint8_t* __restrict__ pcodes,
+                                                          const float* __restrict__ pscales,
+                                                          float acc[G][4]) {
+  float part[4][G][4];
+#pragma unroll
+  for (int sl = 0; sl < 4; ++sl) {
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[sl][cg][r] = 0.0f;
+    tile_accumulate<G>(tile, (bps * sl) / 4, (bps * (sl + 1)) / 4, pcodes, pscales, bps, part[sl]);
+  }
+#pragma unroll
+  for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = __fadd_rn(__fadd_rn(__fadd_rn(part[0][cg][r], part[1][cg][r]), part[2][cg][r]), part[3][cg][r]);
+      acc[cg][r] = __fadd_rn(v, __shfl_xor(v, 8, 64));
+    }
+}
+
+__device__ __forceinline__ float kv_load(const void* base, int f16, size_t idx) {
+  return f16 ? __half2float(((const __half*)base)[idx]) : ((const float*)base)[idx];
+}
+__device__ __forceinline__ v4f kv_load4(const void* base, int f16, size_t idx) {
+  if (f16) {
+    const uint2 raw = *(const uint2*)((const __half*)base + idx);
+    v4f r;
+    r[0] = half_bits_to_float((uint16_t)(raw.x & 0xffff));
+    r[1] = half_bits_to_float((uint16_t)(raw.x >> 16));
+    r[2] = half_bits_to_float((uint16_t)(raw.y & 0xffff));
+    r[3] = half_bits_to_float((uint16_t)(raw.y >> 16));
+    return r;
+  }
+  return *(const v4f*)((const float*)base + idx);
+}
+
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+  if (v == 0.0f) v = 0.0f;  // -0 and +0 compare equal in the reference
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+}
+
+
+// Device-coherent accesses for data exchanged between workgroups inside one
+// launch (they bypass the non-coherent caches; no cache maintenance needed).
+__device__ __forceinline__ uint32_t ld_coh_u32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh(const float* p) {
+  return __uint_as_float(__hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ void st_coh(float* p, float v) {
+  __hip_atomic_store((uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_coh_u64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh_u64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool COH>
+__device__ __forceinline__ void st_f(float* p, float v) {
+  if (COH) st_coh(p, v);
+  else *p = v;
+}
+
+__device__ __forceinline__ float wave_max_f(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float f16_round(float v) { return __half2float(__float2half_rn(v)); }
+
+// ------------------------------------------------------------- attention ----
+constexpr int kChunk = kChunkKeys;  // keys per attention chunk (canonical)
+
+// Where the keys and values of one kv head come from: the cache, except keys at
+// or after new_from, which are rows (key - new_from) of knew/vnew (LDS).
+struct AttnSrc {
+  const void* kc;
+  const void* vc;
+  int f16;
+  size_t head_base;  // element offset of the kv head in the cache
+  const float* knew;
+  const float* vnew;
+  int new_from;      // >= kvlen when every key is in the cache
+};
+
+// Scores, chunk softmax and P.V of keys [key0, key0+64) for ncol query columns
+// held in q (LDS, [col][128], already f16-rounded for an f16 cache). col ->
+// query row col_t(col) = col % T. Writes (m, l) and O of each column. 256
+// threads. LDS: vbuf [64][128], sp [kMaxCols][64].
+__device__ __forceinline__ v4f attn_row4(const AttnSrc& a, bool is_v, int key, int d) {
+  if (key >= a.new_from) return *(const v4f*)((is_v ? a.vnew : a.knew) + (key - a.new_from) * kHeadDim + d);
+  return kv_load4(is_v ? a.vc : a.kc, a.f16, a.head_base + (size_t)key * kHeadDim + d);
+}
+
+template <bool COH>
+__device__ void attn_chunk(const AttnSrc& a, const float* q, int ncol, int T, int past, int kvlen,
+                           int key0, float scale, float* vbuf, float* sp, float* out_ml,
+                           float* out_o) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // 1. V chunk -> LDS (zeros past kvlen)
+  for (int idx = tid; idx < kChunk * kHeadDim / 4; idx += 256) {
+    const int j = idx >> 5, d = (idx & 31) * 4, key = key0 + j;
+    const v4f v = key < kvlen ? attn_row4(a, true, key, d) : (v4f){0.f, 0.f, 0.f, 0.f};
+    *(v4f*)(vbuf + j * kHeadDim + d) = v;
+  }
+  // 2. scores: thread = (key, 8 columns)
+  {
+    const int key = key0 + lane, c0 = wave * 8;
+    const bool kvalid = key < kvlen;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    if (c0 < ncol && kvalid) {
+      for (int d = 0; d < kHeadDim; d += 4) {
+        const v4f kf = attn_row4(a, false, key, d);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const v4f qf = *(const v4f*)(q + (c0 + i) * kHeadDim + d);
+          acc[i] = fmaf(qf[0], kf[0], acc[i]);
+          acc[i] = fmaf(qf[1], kf[1], acc[i]);
+          acc[i] = fmaf(qf[2], kf[2], acc[i]);
+          acc[i] = fmaf(qf[3], kf[3], acc[i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int col = c0 + i;
+      if (col < ncol) {
+        const int t = col % T;
+        sp[col * kChunk + lane] = (kvalid && key <= past + t) ? __fmul_rn(acc[i], scale) : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+  // 3. chunk softmax per column (one wave per column, lane = key)
+  for (int col = wave; col < ncol; col += 4) {
+    const float w = sp[col * kChunk + lane];
+    const float m = wave_max_f(w);
+    float p = (m == -INFINITY || w == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(w, m));
+    if (a.f16) p = f16_round(p);
+    const float l = wave_sum_f(p);
+    sp[col * kChunk + lane] = p;
+    if (lane == 0) {
+      st_f<COH>(out_ml + col * 2, m);
+      st_f<COH>(out_ml + col * 2 + 1, l);
+    }
+  }
+  __syncthreads();
+  // 4. O[col][d] = sum over the 64 keys in order of p * v
+  {
+    const int d = tid & 127, c0 = (tid >> 7) * 16;
+    float o[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = 0.0f;
+    if (c0 < ncol) {
+      for (int j = 0; j < kChunk; ++j) {
+        const float v = vbuf[j * kHeadDim + d];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i] = fmaf(sp[(c0 + i < ncol ? c0 + i : 0) * kChunk + j], v, o[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (c0 + i < ncol) st_f<COH>(out_o + (c0 + i) * kHeadDim + d, o[i]);
+  }
+  __syncthreads();
+}
+
+// Merge the chunk partials of one query column (canonical order); returns
+// element d of the attention output. part_ml/part_o point at chunk 0 of the
+// column, consecutive chunks `stride_ml` / `stride_o` floats apart.
+template <bool COH>
+__device__ __forceinline__ float attn_merge(const float* part_ml, const float* part_o, int nch,
+                                            size_t stride_ml, size_t stride_o, int d) {
+  auto ld = [](const float* p) { return COH ? ld_coh(p) : *p; };
+  float M = -INFINITY;
+  for (int c = 0; c < nch; ++c) M = fmaxf(M, ld(part_ml + c * stride_ml));
+  float L = 0.0f, O = 0.0f;
+  for (int c = 0; c < nch; ++c) {
+    const float m = ld(part_ml + c * stride_ml);
+    if (m == -INFINITY) continue;
+    const float f = dev_expf(__fsub_rn(m, M));
+    L = fmaf(ld(part_ml + c * stride_ml + 1), f, L);
+    O = fmaf(ld(part_o + c * stride_o + d), f, O);
+  }
+  return __fdiv_rn(O, L);
+}
+
+}  // namespace dev
+}  // namespace mtg

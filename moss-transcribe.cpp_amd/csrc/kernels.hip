@@ -17,55 +17,12 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
-#include "kernels.hpp"
+#include "device_common.hpp"
 
 namespace mtg {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-
 namespace {
-
-__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
-  return __half2float(__ushort_as_half(h));
-}
-
-__device__ __forceinline__ double wave_sum_d(double v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// q8_0 activation conversion of one 32-element block held by 8 consecutive lanes
-// (4 elements each): d = amax/127 rounded to f16, codes = rint(x * 127/amax).
-// Returns the f32 value of the stored f16 scale.
-__device__ __forceinline__ float quant_block8(const float v[4], int8_t q[4]) {
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-  const float d = __fdiv_rn(amax, 127.0f);
-  const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-  for (int e = 0; e < 4; ++e) q[e] = (int8_t)rintf(__fmul_rn(v[e], id));
-  return __half2float(__float2half_rn(d));
-}
-
-// Panel position of element k of verify row t (see mtg_internal.hpp).
-__device__ __forceinline__ void panel_store4(Panel p, int bps, int t, int k, const int8_t q[4]) {
-  const int b = k >> 5, bp = b >> 1, par = b & 1, half = (k >> 4) & 1, byte = k & 15;
-  const int cg = t >> 3, j = par * 8 + (t & 7), g = 2 * par + half, lane = j + 16 * g;
-  uint32_t packed = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
-                    ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
-  *(uint32_t*)(p.codes + ((size_t)(cg * bps + bp)) * 1024 + lane * 16 + byte) = packed;
-}
-__device__ __forceinline__ void panel_store_scale(Panel p, int bps, int t, int block, float d) {
-  const int bp = block >> 1, par = block & 1, cg = t >> 3, j = par * 8 + (t & 7);
-  p.scales[(size_t)(cg * bps + bp) * 16 + j] = d;
-}
+using namespace dev;
 
 // ------------------------------------------------------------- embed -------
 __global__ void k_embed(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ tiles,
@@ -98,20 +55,24 @@ __global__ void k_norm_quant(const StepDesc* __restrict__ desc, const float* __r
   if (t >= desc->T) return;
   const float* xr = src + (size_t)t * K;
   const int tid = threadIdx.x;
-  __shared__ double red[4];
+  __shared__ float s_scale;
   float scale = 1.0f;
   if (gain) {
-    double s = 0.0;
-    for (int k = tid; k < K; k += 256) {
-      const float v = xr[k];
-      s += (double)__fmul_rn(v, v);
+    // canonical row sum (K == 1024): lane l sums elements 16l..16l+15, butterfly
+    if (tid < 64) {
+      double s = 0.0;
+      for (int e = 0; e < 16; ++e) {
+        const float v = xr[tid * 16 + e];
+        s += (double)__fmul_rn(v, v);
+      }
+      s = wave_sum_d(s);
+      if (tid == 0) {
+        const float mean = (float)(s / (double)K);
+        s_scale = dev_rms_scale(mean, eps);
+      }
     }
-    s = wave_sum_d(s);
-    if ((tid & 63) == 0) red[tid >> 6] = s;
     __syncthreads();
-    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
-    const float mean = (float)(tot / (double)K);
-    scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    scale = s_scale;
   }
   const int bps = K / kPairK;
   for (int base = 0; base < K; base += 1024) {
@@ -129,40 +90,6 @@ __global__ void k_norm_quant(const StepDesc* __restrict__ desc, const float* __r
     const float d = quant_block8(v, q);
     panel_store4(panel, bps, t, k0, q);
     if ((tid & 7) == 0) panel_store_scale(panel, bps, t, k0 >> 5, d);
-  }
-}
-
-// ----------------------------------------------------------- GEMM core ------
-// One wave accumulates a 16-row tile over block pairs [bp0, bp1) for every
-// column group: acc[cg][r] holds rows 4*(lane/16)+r of column lane%16, split by
-// block parity (columns 0-7 even blocks, 8-15 odd blocks of rows t = col%8).
-template <int G>
-__device__ __forceinline__ void tile_accumulate(const uint8_t* __restrict__ tile, int bp0, int bp1,
-                                                const uint8_t* __restrict__ pcodes,
-                                                const float* __restrict__ pscales, int bps,
-                                                float acc[G][4]) {
-  const int lane = threadIdx.x & 63;
-  const int par = (lane & 15) >> 3;
-  const int srow = par * 16 + 4 * (lane >> 4);
-  const v4i zero = {0, 0, 0, 0};
-#pragma unroll 4
-  for (int bp = bp0; bp < bp1; ++bp) {
-    const uint8_t* unit = tile + (size_t)bp * kUnitBytes;
-    const v4i a = *(const v4i*)(unit + lane * 16);
-    const uint2 sw = *(const uint2*)(unit + 1024 + srow * 2);
-    float dw[4];
-    dw[0] = half_bits_to_float((uint16_t)(sw.x & 0xffff));
-    dw[1] = half_bits_to_float((uint16_t)(sw.x >> 16));
-    dw[2] = half_bits_to_float((uint16_t)(sw.y & 0xffff));
-    dw[3] = half_bits_to_float((uint16_t)(sw.y >> 16));
-#pragma unroll
-    for (int cg = 0; cg < G; ++cg) {
-      const v4i b = *(const v4i*)(pcodes + ((size_t)(cg * bps + bp)) * 1024 + lane * 16);
-      const float dx = pscales[(size_t)(cg * bps + bp) * 16 + (lane & 15)];
-      const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, zero, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[cg][r] = fmaf((float)c[r], dw[r] * dx, acc[cg][r]);
-    }
   }
 }
 
@@ -207,7 +134,7 @@ k_gemm(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w,
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float s = red[0][(m * G + cg) * 4 + r][lane];
-          for (int wv = 1; wv < SPLIT; ++wv) s += red[wv][(m * G + cg) * 4 + r][lane];
+          for (int wv = 1; wv < SPLIT; ++wv) s = __fadd_rn(s, red[wv][(m * G + cg) * 4 + r][lane]);
           acc[m][cg][r] = s;
         }
   }
@@ -217,7 +144,7 @@ k_gemm(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w,
 #pragma unroll
     for (int cg = 0; cg < G; ++cg)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[m][cg][r] += __shfl_xor(acc[m][cg][r], 8, 64);
+      for (int r = 0; r < 4; ++r) acc[m][cg][r] = __fadd_rn(acc[m][cg][r], __shfl_xor(acc[m][cg][r], 8, 64));
   if ((lane & 15) >= 8) return;
 #pragma unroll
   for (int cg = 0; cg < G; ++cg) {
@@ -230,11 +157,9 @@ k_gemm(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w,
       if (EPI == 0) {
         *dst = acc[0][cg][r];
       } else if (EPI == 1) {
-        *dst = *dst + acc[0][cg][r];
+        *dst = __fadd_rn(*dst, acc[0][cg][r]);
       } else {
-        const float g = acc[0][cg][r], u = acc[NM - 1][cg][r];
-        const float silu = g / (1.0f + expf(-g));
-        *dst = silu * u;
+        *dst = dev_swiglu(acc[0][cg][r], acc[NM - 1][cg][r]);
       }
     }
   }
@@ -265,7 +190,7 @@ k_qk_rope_append(const StepDesc* __restrict__ desc, const float* __restrict__ qk
     double s = (double)__fmul_rn(x0, x0) + (double)__fmul_rn(x1, x1);
     s = wave_sum_d(s);
     const float mean = (float)(s / (double)kHeadDim);
-    const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    const float scale = dev_rms_scale(mean, eps);
     const float y0 = __fmul_rn(__fmul_rn(x0, scale), g[i]);
     const float y1 = __fmul_rn(__fmul_rn(x1, scale), g[i + 64]);
     const float c = rope[(size_t)pos * kHeadDim + 2 * i], sn = rope[(size_t)pos * kHeadDim + 2 * i + 1];
@@ -293,183 +218,54 @@ k_qk_rope_append(const StepDesc* __restrict__ desc, const float* __restrict__ qk
 }
 
 // -------------------------------------------------------------- attention --
-// Split-KV GQA attention on v_mfma_f32_16x16x4f32. One workgroup = (kv head g,
-// split s), kAttnWaves waves; each wave takes 16-key tiles round-robin.
-// Query columns (16 per group cg): col j -> q head 2g + j/8, row t = 8*cg + j%8.
-// S^T = K . Q^T per tile (keys x queries), online softmax per column, then
-// O^T += V^T . P^T with P^T taken straight from the S^T accumulator layout.
-__device__ __forceinline__ float kv_load(const void* base, int f16, size_t idx) {
-  return f16 ? __half2float(((const __half*)base)[idx]) : ((const float*)base)[idx];
-}
-__device__ __forceinline__ v4f kv_load4(const void* base, int f16, size_t idx) {
-  if (f16) {
-    const uint2 raw = *(const uint2*)((const __half*)base + idx);
-    v4f r;
-    r[0] = half_bits_to_float((uint16_t)(raw.x & 0xffff));
-    r[1] = half_bits_to_float((uint16_t)(raw.x >> 16));
-    r[2] = half_bits_to_float((uint16_t)(raw.y & 0xffff));
-    r[3] = half_bits_to_float((uint16_t)(raw.y >> 16));
-    return r;
-  }
-  return *(const v4f*)((const float*)base + idx);
-}
-
-__global__ void __launch_bounds__(kAttnWaves * 64)
-k_attn_split(const StepDesc* __restrict__ desc, const float* __restrict__ q, int n_heads,
-             KvLayer kv, AttnWork work) {
-  const int g = blockIdx.x, split = blockIdx.y;
+// One workgroup per (kv head g, chunk of 64 keys); query columns col = hl*T + t
+// for q heads 2g + hl. Canonical chunk arithmetic (device_common.hpp).
+__global__ void __launch_bounds__(256)
+k_attn_chunk(const StepDesc* __restrict__ desc, const float* __restrict__ q, int n_heads,
+             KvLayer kv, AttnWork work, int max_chunks) {
+  const int g = blockIdx.x, chunk = blockIdx.y;
   const int T = desc->T, past = desc->past, kvlen = past + T;
-  const int G = (T + 7) / 8;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int j = lane & 15, lg = lane >> 4;
-  const float scale = 1.0f / sqrtf((float)kHeadDim);
-  const size_t head_base = (size_t)g * kv.max_seq * kHeadDim;
-  const int ntiles = (kvlen + 15) / 16;
-  const int t0 = (ntiles * split) / kAttnSplits, t1 = (ntiles * (split + 1)) / kAttnSplits;
+  if (chunk * kChunk >= kvlen) return;
+  __shared__ float s_q[kMaxCols * kHeadDim];
+  __shared__ float s_v[kChunk * kHeadDim];
+  __shared__ float s_p[kMaxCols * kChunk];
+  const int ncol = 2 * T;
   const bool f16kv = kv.f16 != 0;
-  __shared__ float s_m[kAttnWaves][16], s_l[kAttnWaves][16];
-  __shared__ float s_o[16][kHeadDim + 4];
-  for (int cg = 0; cg < G; ++cg) {
-    // this lane's query column
-    const int t = cg * 8 + (j & 7), hq = 2 * g + (j >> 3);
-    const bool qvalid = t < T;
-    v4f qf[8];
-    const float* qrow = q + ((size_t)(qvalid ? t : 0) * n_heads + hq) * kHeadDim;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      qf[c] = *(const v4f*)(qrow + 16 * c + 4 * lg);
-      if (f16kv)  // mul_mat(f16 K, f32 q) converts q to f16 first
-#pragma unroll
-        for (int e = 0; e < 4; ++e) qf[c][e] = __half2float(__float2half_rn(qf[c][e]));
-    }
-    float m_run = -INFINITY, l_run = 0.0f;
-    v4f o[8];
-#pragma unroll
-    for (int cb = 0; cb < 8; ++cb) o[cb] = (v4f){0.f, 0.f, 0.f, 0.f};
-    for (int tile = t0 + wave; tile < t1; tile += kAttnWaves) {
-      const int key0 = tile * 16;
-      // S^T tile: A = K[key0 + j][perm d], B = Q^T[perm d][col j]
-      const int kk = min(key0 + j, kvlen - 1);
-      v4f s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const v4f kf = kv_load4(kv.k, kv.f16, head_base + (size_t)kk * kHeadDim + 16 * c + 4 * lg);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[e], qf[c][e], s, 0, 0, 0);
-      }
-      // lane holds S^T[key0 + 4*lg + r][col j]
-      float w[4], tmax = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = key0 + 4 * lg + r;
-        const bool ok = qvalid && key < kvlen && key <= past + t;
-        w[r] = ok ? s[r] * scale : -INFINITY;
-        tmax = fmaxf(tmax, w[r]);
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m_run, tmax);
-      const float alpha = m_new == -INFINITY ? 1.0f : expf(m_run - m_new);
-      float p[4], psum = 0.0f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[r] = w[r] == -INFINITY ? 0.0f : expf(w[r] - m_new);
-        if (f16kv) p[r] = __half2float(__float2half_rn(p[r]));
-        psum += p[r];
-      }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-#pragma unroll
-      for (int cb = 0; cb < 8; ++cb) o[cb] *= alpha;
-      // O^T += V^T . P^T: step r uses key key0 + 4*lg + r from every lane group;
-      // lane (row i = j) loads V[key][4i..4i+3] and V[key][64+4i..+3]: component e
-      // of the first load is output block e (d = 4i+e), of the second block 4+e.
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = min(key0 + 4 * lg + r, kvlen - 1);
-        const size_t vb = head_base + (size_t)key * kHeadDim + 4 * j;
-        const v4f v0 = kv_load4(kv.v, kv.f16, vb);
-        const v4f v1 = kv_load4(kv.v, kv.f16, vb + 64);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          o[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0[e], p[r], o[e], 0, 0, 0);
-          o[4 + e] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1[e], p[r], o[4 + e], 0, 0, 0);
-        }
-      }
-    }
-    // combine the waves of this workgroup (fixed order)
-    if (lg == 0) {
-      s_m[wave][j] = m_run;
-      s_l[wave][j] = l_run;
-    }
-    __syncthreads();
-    float M = -INFINITY;
-    for (int wv = 0; wv < kAttnWaves; ++wv) M = fmaxf(M, s_m[wv][j]);
-    const float myscale = (M == -INFINITY || m_run == -INFINITY) ? 0.0f : expf(m_run - M);
-    for (int wv = 0; wv < kAttnWaves; ++wv) {
-      if (wave == wv) {
-        // lane holds O^T rows (within block cb) 4*lg + r -> d = 4*(4*lg+r) + cb (cb<4)
-#pragma unroll
-        for (int cb = 0; cb < 8; ++cb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int d = (cb < 4) ? 4 * (4 * lg + r) + cb : 64 + 4 * (4 * lg + r) + (cb - 4);
-            const float val = o[cb][r] * myscale;
-            s_o[j][d] = wv == 0 ? val : s_o[j][d] + val;
-          }
-      }
-      __syncthreads();
-    }
-    // write the workgroup partial: (M, L) and O for the 16 columns
-    const size_t pbase = (((size_t)g * kAttnSplits + split) * kMaxGroups + cg) * 16;
-    if (threadIdx.x < 16) {
-      const int col = threadIdx.x;
-      float Mc = -INFINITY, L = 0.0f;
-      for (int wv = 0; wv < kAttnWaves; ++wv) Mc = fmaxf(Mc, s_m[wv][col]);
-      for (int wv = 0; wv < kAttnWaves; ++wv) {
-        const float mw = s_m[wv][col];
-        if (mw != -INFINITY) L += s_l[wv][col] * expf(mw - Mc);
-      }
-      work.part_ml[(pbase + col) * 2 + 0] = Mc;
-      work.part_ml[(pbase + col) * 2 + 1] = L;
-    }
-    for (int idx = threadIdx.x; idx < 16 * kHeadDim; idx += blockDim.x) {
-      const int col = idx / kHeadDim, d = idx % kHeadDim;
-      work.part_o[(pbase + col) * kHeadDim + d] = s_o[col][d];
-    }
-    __syncthreads();
+  for (int idx = threadIdx.x; idx < ncol * kHeadDim; idx += 256) {
+    const int col = idx / kHeadDim, d = idx % kHeadDim, hl = col / T, t = col % T;
+    const float v = q[((size_t)t * n_heads + 2 * g + hl) * kHeadDim + d];
+    s_q[idx] = f16kv ? f16_round(v) : v;  // mul_mat(f16 K, f32 q) converts q to f16
   }
+  __syncthreads();
+  AttnSrc a;
+  a.kc = kv.k;
+  a.vc = kv.v;
+  a.f16 = kv.f16;
+  a.head_base = (size_t)g * kv.max_seq * kHeadDim;
+  a.knew = nullptr;
+  a.vnew = nullptr;
+  a.new_from = kvlen;
+  const size_t item = (size_t)g * max_chunks + chunk;
+  attn_chunk<false>(a, s_q, ncol, T, past, kvlen, chunk * kChunk, __fdiv_rn(1.0f, dev_sqrtf((float)kHeadDim)), s_v,
+                    s_p, work.part_ml + item * kMaxCols * 2, work.part_o + item * kMaxCols * kHeadDim);
 }
 
-// grid (n_heads, 16 rows), 128 threads (one per d). Merges the splits of one
-// (head, row), writes o (f32) and its q8_0 panel for the o-projection.
+// grid (n_heads, 16 rows), 128 threads: merge the chunks of one (head, row),
+// write o (f32) and its q8_0 panel for the o-projection.
 __global__ void __launch_bounds__(128)
-k_attn_combine(const StepDesc* __restrict__ desc, AttnWork work, int n_heads, Panel o_panel,
-               float* __restrict__ o_out) {
+k_attn_combine(const StepDesc* __restrict__ desc, AttnWork work, int n_heads, int max_chunks,
+               Panel o_panel, float* __restrict__ o_out) {
   const int hq = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
-  if (t >= desc->T) return;
-  const int g = hq / 2, col = (hq & 1) * 8 + (t & 7), cg = t >> 3;
-  float M = -INFINITY;
-  for (int s = 0; s < kAttnSplits; ++s) {
-    const size_t pb = (((size_t)g * kAttnSplits + s) * kMaxGroups + cg) * 16 + col;
-    M = fmaxf(M, work.part_ml[pb * 2]);
-  }
-  float L = 0.0f, acc = 0.0f;
-  for (int s = 0; s < kAttnSplits; ++s) {
-    const size_t pb = (((size_t)g * kAttnSplits + s) * kMaxGroups + cg) * 16 + col;
-    const float m = work.part_ml[pb * 2];
-    if (m == -INFINITY) continue;
-    const float f = expf(m - M);
-    L += work.part_ml[pb * 2 + 1] * f;
-    acc += work.part_o[pb * kHeadDim + d] * f;
-  }
-  const float val = acc / L;
+  const int T = desc->T;
+  if (t >= T) return;
+  const int g = hq / 2, col = (hq & 1) * T + t;
+  const int nch = (desc->past + T + kChunk - 1) / kChunk;
+  const size_t item0 = (size_t)g * max_chunks;
+  const float val = attn_merge<false>(work.part_ml + item0 * kMaxCols * 2 + col * 2,
+                                      work.part_o + item0 * kMaxCols * kHeadDim + col * kHeadDim, nch,
+                                      (size_t)kMaxCols * 2, (size_t)kMaxCols * kHeadDim, d);
   const int QN = n_heads * kHeadDim;
   o_out[(size_t)t * QN + hq * kHeadDim + d] = val;
-  // q8_0 conversion of this head's 4 blocks: lanes 4*i..4*i+3 own d
   __shared__ float s_v[kHeadDim];
   s_v[d] = val;
   __syncthreads();
@@ -506,13 +302,6 @@ __global__ void k_penalty_bitmap(const StepDesc* __restrict__ desc, int vocab,
 // Grid-stride over 16-row tiles of the tied embedding; the activation panel is
 // staged in LDS once per workgroup. Each lane keeps the best (value, index) key
 // per verify row; ties keep the lowest index (first maximum).
-__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
-  if (v == 0.0f) v = 0.0f;  // -0 and +0 compare equal in the reference
-  uint32_t u = __float_as_uint(v);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
-}
-
 template <int G>
 __global__ void __launch_bounds__(256)
 k_lm_head(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int vocab, int bps,
@@ -539,15 +328,7 @@ k_lm_head(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int 
   for (int cg = 0; cg < G; ++cg) best[cg] = 0;
   for (int tile = blockIdx.x * 4 + wave; tile < n_tiles; tile += nwaves) {
     float acc[G][4];
-#pragma unroll
-    for (int cg = 0; cg < G; ++cg)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[cg][r] = 0.0f;
-    tile_accumulate<G>(w + (size_t)tile * bps * kUnitBytes, 0, bps, lcodes, lscales, bps, acc);
-#pragma unroll
-    for (int cg = 0; cg < G; ++cg)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[cg][r] += __shfl_xor(acc[cg][r], 8, 64);
+    tile_accumulate_canonical<G>(w + (size_t)tile * bps * kUnitBytes, bps, lcodes, lscales, acc);
     if ((lane & 15) < 8) {
 #pragma unroll
       for (int cg = 0; cg < G; ++cg) {
@@ -697,11 +478,11 @@ static void gemm_launch(hipStream_t s, int G, const StepDesc* desc, const uint8_
 
 void launch_gemm_store(hipStream_t s, int G, const StepDesc* desc, const uint8_t* w, int n, int k,
                        Panel x, float* out) {
-  gemm_launch<0, 2>(s, G, desc, w, nullptr, n, k, x, out);
+  gemm_launch<0, 4>(s, G, desc, w, nullptr, n, k, x, out);
 }
 void launch_gemm_residual(hipStream_t s, int G, const StepDesc* desc, const uint8_t* w, int n,
                           int k, Panel x, float* resid) {
-  gemm_launch<1, 8>(s, G, desc, w, nullptr, n, k, x, resid);
+  gemm_launch<1, 4>(s, G, desc, w, nullptr, n, k, x, resid);
 }
 void launch_gemm_swiglu(hipStream_t s, int G, const StepDesc* desc, const uint8_t* wg,
                         const uint8_t* wu, int n, int k, Panel x, float* act) {
@@ -717,10 +498,11 @@ void launch_qk_rope_append(hipStream_t s, const StepDesc* desc, const float* qkv
 
 void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n_heads,
                       int n_kv_heads, KvLayer kv, AttnWork work, Panel o_panel, float* o_out) {
-  hipLaunchKernelGGL(k_attn_split, dim3(n_kv_heads, kAttnSplits), dim3(kAttnWaves * 64), 0, s,
-                     desc, q, n_heads, kv, work);
+  const int max_chunks = (kv.max_seq + kChunk - 1) / kChunk;
+  hipLaunchKernelGGL(k_attn_chunk, dim3(n_kv_heads, max_chunks), dim3(256), 0, s, desc, q, n_heads,
+                     kv, work, max_chunks);
   hipLaunchKernelGGL(k_attn_combine, dim3(n_heads, kMaxRows), dim3(kHeadDim), 0, s, desc, work,
-                     n_heads, o_panel, o_out);
+                     n_heads, max_chunks, o_panel, o_out);
 }
 
 void launch_penalty_bitmap(hipStream_t s, const StepDesc* desc, int vocab, uint32_t* bitmap) {

@@ -29,8 +29,8 @@ constexpr int kUnitBytes = 1088;       // 1024 codes + 32 f16 scales
 constexpr int kPanelPairBytes = 1024;  // activation codes per (group, pair)
 constexpr int kMaxRows = MTG_MAX_BATCH;
 constexpr int kMaxGroups = 2;          // column groups of 8 rows
-constexpr int kAttnSplits = 16;        // split-KV workgroups per kv head
-constexpr int kAttnWaves = 8;          // waves per split workgroup
+constexpr int kChunkKeys = 64;         // keys per attention chunk
+constexpr int kMaxCols = 2 * MTG_MAX_BATCH;  // attention query columns (2 q heads x rows)
 constexpr int kHeadDim = 128;
 constexpr int kPenaltyWindow = 100;
 constexpr int kLmWorkgroups = 1024;    // lm_head grid (grid-stride over tiles)
@@ -54,7 +54,7 @@ struct StepDesc {
 struct StepResult {
   int32_t choice[kMaxRows];
   int32_t n_match;
-  int32_t pad;
+  int32_t err;  // nonzero: a grid-barrier wait of the step kernel ran out
 };
 
 }  // namespace mtg

@@ -179,15 +179,98 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
   panel_h = panel(H);
   panel_o = panel(QN);
   panel_f = panel(F);
-  work.part_ml = (float*)dalloc((size_t)NKV * kAttnSplits * kMaxGroups * 16 * 2 * 4, true);
-  work.part_o = (float*)dalloc((size_t)NKV * kAttnSplits * kMaxGroups * 16 * D * 4, true);
+  const size_t chunks = (size_t)NKV * ((max_seq + kChunkKeys - 1) / kChunkKeys);
+  work.part_ml = (float*)dalloc(chunks * kMaxCols * 2 * 4, true);
+  work.part_o = (float*)dalloc(chunks * kMaxCols * D * 4, true);
   desc_dev = (StepDesc*)dalloc(sizeof(StepDesc), true);
   result_dev = (StepResult*)dalloc(sizeof(StepResult), true);
   if (!x || !qkv || !qbuf || !obuf || !act || !hid || !embeds_dev || !logits || !bitmap ||
       !part_keys || !panel_h.codes || !panel_h.scales || !panel_o.codes || !panel_o.scales ||
       !panel_f.codes || !panel_f.scales || !work.part_ml || !work.part_o || !desc_dev || !result_dev)
     return fail(MTG_ERR_NOMEM, "step buffers");
+  if ((rc = init_step_kernel())) return rc;
   return check(hipDeviceSynchronize(), "init");
+}
+
+// Parameters of the persistent step kernel: one workgroup per CU, the layer
+// table and the per-workgroup partial buffers live in device memory.
+int Ctx::init_step_kernel() {
+  int dev = 0, cus = 0;
+  int rc = check(hipGetDevice(&dev), "device");
+  if (rc) return rc;
+  if ((rc = check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count")))
+    return rc;
+  const int H = hp.hidden, QN = hp.n_heads * hp.head_dim, F = hp.intermediate, V = hp.vocab;
+  nwg = cus - cus % hp.n_kv_heads;
+  bps_max = std::max(std::max(H, QN), F) / kPairK;
+  // The kernel's phases are written for these shapes (whole 1024-element norm
+  // rows, 16-row tiles covering each matrix); other shapes use the per-op kernels.
+  if (H != 1024 || nwg < hp.n_kv_heads || (QN + 2 * hp.n_kv_heads * hp.head_dim) % 16 || QN % 1024 ||
+      F % 1024) {
+    exec = kExecGraph;
+    return MTG_OK;
+  }
+  if (prepare_step_kernels(bps_max) != hipSuccess) {
+    (void)hipGetLastError();
+    exec = kExecGraph;
+    return MTG_OK;
+  }
+  std::vector<LayerDev> table(hp.n_layers);
+  for (int l = 0; l < hp.n_layers; ++l) {
+    const Layer& y = layers[l];
+    LayerDev& d = table[l];
+    d.wqkv = y.wqkv;
+    d.wo = y.wo;
+    d.wg = y.wg;
+    d.wu = y.wu;
+    d.wd = y.wd;
+    d.attn_norm = y.attn_norm;
+    d.ffn_norm = y.ffn_norm;
+    d.q_norm = y.q_norm;
+    d.k_norm = y.k_norm;
+    d.kc = kcache + kv_layer_bytes * l;
+    d.vc = vcache + kv_layer_bytes * l;
+  }
+  LayerDev* table_dev = (LayerDev*)dalloc(table.size() * sizeof(LayerDev), false);
+  StepParams P{};
+  P.H = H;
+  P.NH = hp.n_heads;
+  P.NKV = hp.n_kv_heads;
+  P.F = F;
+  P.V = V;
+  P.L = hp.n_layers;
+  P.max_seq = max_seq;
+  P.kv_f16 = kv_type == MTG_TYPE_F16;
+  P.bps_max = bps_max;
+  P.eps = hp.rms_eps;
+  P.layers = table_dev;
+  P.embd = embd;
+  P.out_norm = out_norm;
+  P.rope = rope;
+  P.embeds = embeds_dev;
+  P.x = x;
+  P.qkv = qkv;
+  P.o = obuf;
+  P.act = act;
+  P.hid = hid;
+  P.logits = logits;
+  P.max_chunks = (max_seq + kChunkKeys - 1) / kChunkKeys;
+  P.part_ml = work.part_ml;  // same layout as the per-op kernels
+  P.part_o = work.part_o;
+  P.bitmap = bitmap;
+  P.part_keys = (uint64_t*)dalloc((size_t)nwg * kMaxRows * 8, true);
+  P.result = result_dev;
+  P.flags = (uint32_t*)dalloc((size_t)nwg * 4, true);
+  P.err = &result_dev->err;
+  params_dev = (StepParams*)dalloc(sizeof(StepParams), false);
+  if (!table_dev || !P.part_ml || !P.part_o || !P.part_keys || !P.flags || !params_dev)
+    return fail(MTG_ERR_NOMEM, "step kernel buffers");
+  if ((rc = check(hipMemcpy(table_dev, table.data(), table.size() * sizeof(LayerDev),
+                            hipMemcpyHostToDevice), "layer table")) ||
+      (rc = check(hipMemcpy(params_dev, &P, sizeof(P), hipMemcpyHostToDevice), "step params")))
+    return rc;
+  step_ok = true;
+  return MTG_OK;
 }
 
 KvLayer Ctx::kv_layer(int l) const {
@@ -237,7 +320,14 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
   int rc = check(hipMemcpyAsync(desc_dev, desc_host, sizeof(StepDesc), hipMemcpyHostToDevice, stream),
                  "step descriptor");
   if (rc) return rc;
-  if (use_graphs) {
+  const bool step_mode = mode == kModeVerify || mode == kModeVerifyPenalty || mode == kModeAppend;
+  if (exec == kExecStep && step_ok && step_mode) {
+    const int smode = mode == kModeAppend ? kStepAppend : kStepVerify;
+    if ((rc = check(launch_step(stream, G, nwg, params_dev, desc_dev, epoch, smode, bps_max),
+                    "step kernel launch")))
+      return rc;
+    epoch += (uint32_t)step_barriers(hp.n_layers, smode);
+  } else if (exec != kExecEager) {
     GraphSlot& slot = graphs[(G - 1) * kModes + mode];
     if (!slot.exec) {
       hipGraph_t g = nullptr;
@@ -254,11 +344,9 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
     enqueue(G, mode);
     if ((rc = check(hipGetLastError(), "kernel launch"))) return rc;
   }
-  if (mode == kModeVerify || mode == kModeVerifyPenalty || mode == kModeLogits) {
-    if ((rc = check(hipMemcpyAsync(result_host, result_dev, sizeof(StepResult),
-                                   hipMemcpyDeviceToHost, stream), "result")))
-      return rc;
-  }
+  if ((rc = check(hipMemcpyAsync(result_host, result_dev, sizeof(StepResult), hipMemcpyDeviceToHost,
+                                 stream), "result")))
+    return rc;
   if (want_hidden && hidden_out &&
       (rc = check(hipMemcpyAsync(hidden_out, hid, (size_t)T * hp.hidden * 4, hipMemcpyDeviceToHost,
                                  stream), "hidden")))
@@ -267,7 +355,13 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
       (rc = check(hipMemcpyAsync(logits_out, logits, (size_t)T * hp.vocab * 4,
                                  hipMemcpyDeviceToHost, stream), "logits")))
     return rc;
-  return check(hipStreamSynchronize(stream), "step");
+  if ((rc = check(hipStreamSynchronize(stream), "step"))) return rc;
+  if (result_host->err) {
+    // a bounded barrier wait ran out: every workgroup left the kernel
+    (void)hipMemset(&result_dev->err, 0, sizeof(int32_t));
+    return fail(MTG_ERR_DEVICE, "step kernel: grid barrier wait timed out");
+  }
+  return MTG_OK;
 }
 
 void Ctx::fill_desc(int T, bool use_embeds, float penalty, const int32_t* tokens,

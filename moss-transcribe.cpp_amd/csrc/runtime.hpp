@@ -9,10 +9,14 @@
 
 #include "kernels.hpp"
 #include "mtg_internal.hpp"
+#include "step_kernel.hpp"
 
 namespace mtg {
 
 enum { kModeVerify = 0, kModeVerifyPenalty = 1, kModeAppend = 2, kModeLogits = 3, kModes = 4 };
+// How a step is executed: one persistent kernel, or the per-op kernels replayed
+// from a captured graph, or the per-op kernels launched one by one.
+enum { kExecStep = 0, kExecGraph = 1, kExecEager = 2 };
 
 struct Layer {
   uint8_t *wqkv = nullptr, *wo = nullptr, *wg = nullptr, *wu = nullptr, *wd = nullptr;
@@ -26,7 +30,12 @@ struct GraphSlot {
 struct Ctx {
   mtg_hparams hp{};
   int max_seq = 0, kv_type = MTG_TYPE_F32, past = 0;
-  bool use_graphs = true;
+  int exec = kExecStep;
+  // persistent step kernel
+  int nwg = 0, bps_max = 0;
+  bool step_ok = false;
+  uint32_t epoch = 0;
+  StepParams* params_dev = nullptr;
   std::string error;
   hipStream_t stream = nullptr;
   std::vector<void*> allocations;
@@ -66,6 +75,7 @@ struct Ctx {
   int logits_of(const float* hidden, int T, float* logits_out);
   int embed(const int32_t* ids, int n, float* out);
   int kv_io(void* k, void* v, int n_pos, bool write);
+  int init_step_kernel();
 };
 
 }  // namespace mtg

@@ -15,6 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmtg.so")
 
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K = 0, 1, 8, 12
+EXEC_STEP_KERNEL, EXEC_GRAPH, EXEC_EAGER = 0, 1, 2
 MAX_BATCH = 16
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_DEVICE, ERR_CAPACITY, ERR_NOMEM, ERR_STATE = 0, -1, -2, -3, -4, -5, -6
 
@@ -81,7 +82,9 @@ SIGNATURES = {
                                     c_int32, c_float, c_int32, c_void_p, c_void_p, c_void_p,
                                     c_void_p, POINTER(c_int32), POINTER(GenStats)]),
     "mtg_stream_draft": (c_int32, [c_void_p, POINTER(c_int32), c_int32, c_int32, POINTER(c_int32)]),
-    "mtg_set_graphs": (c_int32, [c_void_p, c_int32]),
+    "mtg_set_exec_mode": (c_int32, [c_void_p, c_int32]),
+    "mtg_exec_mode": (c_int32, [c_void_p]),
+    "mtg_debug_copy": (c_int32, [c_void_p, c_int32, c_void_p, ctypes.c_size_t]),
     "mtg_ngram_draft": (c_int32, [c_void_p, c_int32, c_int32, c_void_p]),
     "mtg_greedy_choice": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_float]),
     "mtg_q8_pack": (c_int32, [c_void_p, c_int32, c_int32, POINTER(c_void_p)]),
@@ -218,8 +221,17 @@ class Decoder:
     def rewind(self, pos):
         self._chk(lib().mtg_rewind(self.ctx, pos))
 
-    def set_graphs(self, on):
-        self._chk(lib().mtg_set_graphs(self.ctx, 1 if on else 0))
+    def set_exec(self, mode):
+        self._chk(lib().mtg_set_exec_mode(self.ctx, mode))
+
+    def debug_buffer(self, which, width):
+        out = np.empty((MAX_BATCH, width), np.float32)
+        self._chk(lib().mtg_debug_copy(self.ctx, which, ptr(out), out.nbytes))
+        return out
+
+    @property
+    def exec_mode(self):
+        return lib().mtg_exec_mode(self.ctx)
 
     def embed(self, ids):
         ids = i32(ids)

@@ -81,6 +81,42 @@ float h2f(uint16_t h) {
   return f;
 }
 
+// ------------------------------------------------------ canonical order ----
+// The float operation order the oracle fixes for every reduction whose order
+// ggml's SIMD code leaves machine-specific; the device kernels use the same
+// order, so both sides agree bit for bit (moss-transcribe.cpp_amd/csrc/
+// device_common.hpp states the same contract).
+
+// exp: Cody-Waite reduction x = n*ln2 + r (ln2 split in two floats),
+// degree-7 Taylor polynomial of e^r in Horner form with fmaf, ldexp.
+float exp_c(float x) {
+  if (x < -87.0f) return 0.0f;
+  if (x > 88.7f) return INFINITY;
+  const float n = std::nearbyint(x * 1.44269504f);
+  float r = std::fma(n, -0.693145752f, x);
+  r = std::fma(n, -1.42860677e-06f, r);
+  float p = 1.98412698e-4f;
+  p = std::fma(p, r, 1.38888889e-3f);
+  p = std::fma(p, r, 8.33333333e-3f);
+  p = std::fma(p, r, 4.16666667e-2f);
+  p = std::fma(p, r, 1.66666667e-1f);
+  p = std::fma(p, r, 0.5f);
+  p = std::fma(p, r, 1.0f);
+  p = std::fma(p, r, 1.0f);
+  return std::ldexp(p, (int)n);
+}
+
+// xor butterfly (32, 16, 8, 4, 2, 1) over 64 partials, as a wave reduces them.
+template <class F>
+F butterfly64(F v[64]) {
+  for (int o = 32; o > 0; o >>= 1) {
+    F w[64];
+    for (int l = 0; l < 64; ++l) w[l] = v[l] + v[l ^ o];
+    for (int l = 0; l < 64; ++l) v[l] = w[l];
+  }
+  return v[0];
+}
+
 // ------------------------------------------------------------ blocks -------
 #pragma pack(push, 1)
 struct BlockQ8 {  // ggml block_q8_0: 34 bytes (src/cpu_q8.cpp:17 relies on it)
@@ -171,10 +207,12 @@ int32_t q8_block_dot(const BlockQ8& a, const BlockQ8& b) {
   return s;
 }
 
-// mul_mat(q8_0 W, f32 x) as ggml runs it: x quantized to q8_0, then per block
-// y += (d_w * d_x) * isum with an exact int32 isum per 32-block.
+// mul_mat(q8_0 W, f32 x) as ggml runs it: x quantized to q8_0, then
+// y = sum over blocks of (d_w * d_x) * isum with an exact int32 isum per
+// 32-block. Canonical float order: K in 4 slices of block pairs, even and odd
+// blocks in separate fma chains per slice, slices added in order, even + odd.
 void mul_mat_q8(const BlockQ8* w, int k, int n, const float* x, int T, float* y) {
-  const int nb = k / 32;
+  const int nb = k / 32, bps = nb / 2;
   std::vector<BlockQ8> xq((size_t)T * nb);
   for (int t = 0; t < T; ++t) quantize_q8_0_act(x + (size_t)t * k, k, xq.data() + (size_t)t * nb);
 #pragma omp parallel for schedule(static)
@@ -182,12 +220,18 @@ void mul_mat_q8(const BlockQ8* w, int k, int n, const float* x, int T, float* y)
     const BlockQ8* wr = w + (size_t)r * nb;
     for (int t = 0; t < T; ++t) {
       const BlockQ8* xr = xq.data() + (size_t)t * nb;
-      float acc = 0.0f;
-      for (int b = 0; b < nb; ++b) {
-        const float d = h2f(wr[b].d) * h2f(xr[b].d);
-        acc += d * (float)q8_block_dot(wr[b], xr[b]);
+      float e[4], o[4];
+      for (int sl = 0; sl < 4; ++sl) {
+        e[sl] = o[sl] = 0.0f;
+        for (int bp = (bps * sl) / 4; bp < (bps * (sl + 1)) / 4; ++bp) {
+          const int b0 = 2 * bp, b1 = 2 * bp + 1;
+          e[sl] = std::fma((float)q8_block_dot(wr[b0], xr[b0]), h2f(wr[b0].d) * h2f(xr[b0].d), e[sl]);
+          o[sl] = std::fma((float)q8_block_dot(wr[b1], xr[b1]), h2f(wr[b1].d) * h2f(xr[b1].d), o[sl]);
+        }
       }
-      y[(size_t)t * n + r] = acc;
+      const float ev = ((e[0] + e[1]) + e[2]) + e[3];
+      const float ov = ((o[0] + o[1]) + o[2]) + o[3];
+      y[(size_t)t * n + r] = ev + ov;
     }
   }
 }
@@ -251,12 +295,31 @@ void mul_mat(int wtype, const void* w, int k, int n, const float* x, int T, floa
   else mul_mat_q4k((const BlockQ4K*)w, k, n, x, T, y);
 }
 
-// ggml_rms_norm (x*x summed in double, mean cast to float, 1/sqrtf), then
-// ggml_mul by the gain as a separate op (src/qwen3.cpp:27-30).
+// ggml_rms_norm (x*x in float, summed in double, mean cast to float,
+// 1/sqrtf), then ggml_mul by the gain as a separate op (src/qwen3.cpp:27-30).
+// Canonical double-sum order: 64 partials (16 consecutive elements each for a
+// 1024 row; elements l and l+64 for a 128 head) reduced by the butterfly.
+double sum_squares(const float* x, int n) {
+  double part[64];
+  if (n == 1024) {
+    for (int l = 0; l < 64; ++l) {
+      double s = 0.0;
+      for (int e = 0; e < 16; ++e) s += (double)(x[16 * l + e] * x[16 * l + e]);
+      part[l] = s;
+    }
+    return butterfly64(part);
+  }
+  if (n == 128) {
+    for (int l = 0; l < 64; ++l) part[l] = (double)(x[l] * x[l]) + (double)(x[l + 64] * x[l + 64]);
+    return butterfly64(part);
+  }
+  double s = 0.0;
+  for (int i = 0; i < n; ++i) s += (double)(x[i] * x[i]);
+  return s;
+}
+
 void rms_norm(const float* x, const float* w, int n, float eps, float* y) {
-  double sum = 0.0;
-  for (int i = 0; i < n; ++i) sum += (double)(x[i] * x[i]);
-  const float mean = (float)(sum / n);
+  const float mean = (float)(sum_squares(x, n) / n);
   const float scale = 1.0f / std::sqrt(mean + eps);
   for (int i = 0; i < n; ++i) {
     const float v = x[i] * scale;
@@ -307,7 +370,7 @@ void softmax_row(const float* s, int n, float scale, const float* mask, float* o
   for (int i = 0; i < n; ++i) out[i] *= inv;
 }
 
-float silu(float g) { return g / (1.0f + std::exp(-g)); }
+float swiglu(float g, float u) { return (g / (1.0f + exp_c(-g))) * u; }
 
 }  // namespace
 
@@ -418,35 +481,67 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
         kv_set(m, true, idx, k[(size_t)t * KN + (size_t)h * D + d]);
         kv_set(m, false, idx, v[(size_t)t * KN + (size_t)h * D + d]);
       }
-  // eager GQA attention: scores K.Q (f32), soft_max_ext with scale 1/sqrt(D)
-  // and the causal mask, then the context at each query's valid length.
+  // eager GQA attention (src/qwen3.cpp:157-189): scores K.Q in f32,
+  // soft_max_ext(scale 1/sqrt(D), causal mask), context over each query's valid
+  // length (src/cpu_context.cpp:13-32). Canonical order: keys in chunks of 64;
+  // score = fma chain over D; per chunk max, p = exp(w - max), l = butterfly
+  // sum of p, O = fma chain over the chunk's keys; chunks merged in order.
   const float scale = 1.0f / std::sqrt((float)D);
   const bool f16kv = m.kv_type == MTG_TYPE_F16;
+  const int nch = (kv + 63) / 64;
   std::vector<float> o((size_t)T * QN);
 #pragma omp parallel for collapse(2) schedule(static)
   for (int h = 0; h < NH; ++h)
     for (int t = 0; t < T; ++t) {
       const int g = h / groups;
-      std::vector<float> s(kv), mask(kv), p(kv), qv(D);
+      std::vector<float> qv(D), cm(nch), cl(nch), co((size_t)nch * D);
       const float* qh = q.data() + (size_t)t * QN + (size_t)h * D;
       for (int d = 0; d < D; ++d) qv[d] = f16kv ? h2f(f2h(qh[d])) : qh[d];
-      for (int j = 0; j < kv; ++j) {
-        const size_t kb = base + ((size_t)g * m.max_seq + j) * D;
-        float acc = 0.0f;
-        for (int d = 0; d < D; ++d) acc += kv_get(m, true, kb + d) * qv[d];
-        s[j] = acc;
-        mask[j] = (T > 1 && j > past + t) ? -INFINITY : 0.0f;
+      for (int c = 0; c < nch; ++c) {
+        float w[64], p[64];
+        float mx = -INFINITY;
+        for (int j = 0; j < 64; ++j) {
+          const int key = 64 * c + j;
+          if (key < kv && key <= past + t) {
+            const size_t kb = base + ((size_t)g * m.max_seq + key) * D;
+            float s = 0.0f;
+            for (int d = 0; d < D; ++d) s = std::fma(qv[d], kv_get(m, true, kb + d), s);
+            w[j] = s * scale;
+          } else {
+            w[j] = -INFINITY;
+          }
+          mx = std::max(mx, w[j]);
+        }
+        for (int j = 0; j < 64; ++j) {
+          p[j] = (mx == -INFINITY || w[j] == -INFINITY) ? 0.0f : exp_c(w[j] - mx);
+          if (f16kv) p[j] = h2f(f2h(p[j]));
+        }
+        float pl[64];
+        std::memcpy(pl, p, sizeof(pl));
+        cm[c] = mx;
+        cl[c] = butterfly64(pl);
+        for (int d = 0; d < D; ++d) {
+          float acc = 0.0f;
+          for (int j = 0; j < 64; ++j) {
+            const int key = 64 * c + j;
+            const float v = key < kv ? kv_get(m, false, base + ((size_t)g * m.max_seq + key) * D + d) : 0.0f;
+            acc = std::fma(p[j], v, acc);
+          }
+          co[(size_t)c * D + d] = acc;
+        }
       }
-      softmax_row(s.data(), kv, scale, mask.data(), p.data());
-      if (f16kv)
-        for (int j = 0; j < kv; ++j) p[j] = h2f(f2h(p[j]));
+      float M = -INFINITY;
+      for (int c = 0; c < nch; ++c) M = std::max(M, cm[c]);
       float* oh = o.data() + (size_t)t * QN + (size_t)h * D;
-      const int valid = past + t + 1;
       for (int d = 0; d < D; ++d) {
-        float acc = 0.0f;
-        for (int j = 0; j < valid; ++j)
-          acc += kv_get(m, false, base + ((size_t)g * m.max_seq + j) * D + d) * p[j];
-        oh[d] = acc;
+        float L = 0.0f, acc = 0.0f;
+        for (int c = 0; c < nch; ++c) {
+          if (cm[c] == -INFINITY) continue;
+          const float f = exp_c(cm[c] - M);
+          L = std::fma(cl[c], f, L);
+          acc = std::fma(co[(size_t)c * D + d], f, acc);
+        }
+        oh[d] = acc / L;
       }
     }
   // o-proj + residual, FFN pre-norm, SwiGLU, down + residual
@@ -458,7 +553,7 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
   std::vector<float> g((size_t)T * F), u((size_t)T * F), act((size_t)T * F);
   mul_mat(m.wtype, m.wg[l].data(), H, F, xn.data(), T, g.data());
   mul_mat(m.wtype, m.wu[l].data(), H, F, xn.data(), T, u.data());
-  for (size_t i = 0; i < act.size(); ++i) act[i] = silu(g[i]) * u[i];
+  for (size_t i = 0; i < act.size(); ++i) act[i] = swiglu(g[i], u[i]);
   mul_mat(m.wtype, m.wd[l].data(), F, H, act.data(), T, ao.data());
   for (size_t i = 0; i < (size_t)T * H; ++i) x[i] = x[i] + ao[i];
 }

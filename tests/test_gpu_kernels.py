@@ -67,11 +67,10 @@ def test_q8_gemm_matches_oracle(k, n, T):
         assert rc == 0
         y = yd.cpu().numpy()
         assert np.isfinite(y).all()
-        # per-block int32 dots are exact; only the float accumulation order across
-        # blocks differs from the oracle (1e-3 relative / 1e-4 absolute contract)
-        scale = np.abs(ref).max() + 1e-30
-        err = np.abs(y - ref)
-        assert (err <= 1e-4 + 1e-3 * np.abs(ref) + 1e-6 * scale).all(), (dist, err.max())
+        # per-block int32 dots are exact and the cross-block float order is the
+        # canonical one on both sides: bit-identical
+        err = np.abs(y.astype(np.float64) - ref)
+        assert np.array_equal(y, ref), (dist, int((y != ref).sum()), err.max())
 
 
 def test_q8_gemm_exact_when_sums_are_exact():
