@@ -212,6 +212,13 @@ int32_t mtg_exec_mode(const mtg_ctx* ctx);
 enum { MTG_DEBUG_X = 0, MTG_DEBUG_QKV = 1, MTG_DEBUG_O = 2, MTG_DEBUG_ACT = 3, MTG_DEBUG_HIDDEN = 4 };
 int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes);
 
+/* Profiling of the persistent step kernel: when enabled, workgroup 0 records a
+ * 100 MHz device clock at the start of the step and after every grid barrier
+ * (1 + 6 per layer + 1 for the lm_head), plus the end; read the marks of the
+ * last step with mtg_step_profile_read (returns how many were copied). */
+int mtg_step_profile(mtg_ctx* ctx, int32_t enable);
+int32_t mtg_step_profile_read(mtg_ctx* ctx, uint64_t* marks, int32_t n);
+
 /* Host policy functions (reference: cpu_ngram_draft, cpu_greedy_choice). */
 int32_t mtg_ngram_draft(const int32_t* history, int32_t n, int32_t maximum, int32_t* out);
 int32_t mtg_greedy_choice(const float* raw, int32_t n, const int32_t* history, int32_t n_history,

@@ -65,6 +65,28 @@ int mtg_set_exec_mode(mtg_ctx* ctx, int32_t mode) {
 
 int32_t mtg_exec_mode(const mtg_ctx* ctx) { return ctx ? ctx->impl.exec : -1; }
 
+int mtg_step_profile(mtg_ctx* ctx, int32_t enable) {
+  if (!ctx) return MTG_ERR_INVALID;
+  Ctx& c = ctx->impl;
+  if (!c.step_ok) return c.fail(MTG_ERR_UNSUPPORTED, "no step kernel");
+  if (enable && !c.timing_dev) {
+    c.timing_dev = (uint64_t*)c.dalloc(sizeof(uint64_t) * 1024, true);
+    if (!c.timing_dev) return c.fail(MTG_ERR_NOMEM, "timing buffer");
+  }
+  c.params_host.timing = enable ? c.timing_dev : nullptr;
+  return hipMemcpy(c.params_dev, &c.params_host, sizeof(c.params_host), hipMemcpyHostToDevice) == hipSuccess
+             ? MTG_OK
+             : MTG_ERR_DEVICE;
+}
+
+int32_t mtg_step_profile_read(mtg_ctx* ctx, uint64_t* marks, int32_t n) {
+  if (!ctx || !marks || !ctx->impl.timing_dev) return 0;
+  const int count = std::min<int>(n, std::min<int>(1024, mtg::step_barriers(ctx->impl.hp.n_layers, mtg::kStepVerify) + 2));
+  if (hipMemcpy(marks, ctx->impl.timing_dev, sizeof(uint64_t) * count, hipMemcpyDeviceToHost) != hipSuccess)
+    return 0;
+  return count;
+}
+
 int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes) {
   if (!ctx || !out) return MTG_ERR_INVALID;
   const Ctx& c = ctx->impl;

@@ -129,7 +129,7 @@ __device__ __forceinline__ void tile_accumulate(const uint8_t* __restrict__ tile
   const int srow = par * 16 + 4 * (lane >> 4);
   const v4i zero = {0, 0, 0, 0};
 #pragma unroll 4
-  for (int bp = bp0; bp < bp1; ++bp) {
+  for (int bp = bp0; bp < bp1; ++bp) {  // 4 pairs in flight per wave
     const uint8_t* unit = tile + (size_t)bp * kUnitBytes;
     const v4i a = *(const v4i*)(unit + lane * 16);
     const uint2 sw = *(const uint2*)(unit + 1024 + srow * 2);

@@ -261,14 +261,17 @@ int Ctx::init_step_kernel() {
   P.part_keys = (uint64_t*)dalloc((size_t)nwg * kMaxRows * 8, true);
   P.result = result_dev;
   P.flags = (uint32_t*)dalloc((size_t)nwg * 4, true);
+  P.release = (uint32_t*)dalloc(256, true);
   P.err = &result_dev->err;
+  P.timing = nullptr;
   params_dev = (StepParams*)dalloc(sizeof(StepParams), false);
-  if (!table_dev || !P.part_ml || !P.part_o || !P.part_keys || !P.flags || !params_dev)
+  if (!table_dev || !P.part_ml || !P.part_o || !P.part_keys || !P.flags || !P.release || !params_dev)
     return fail(MTG_ERR_NOMEM, "step kernel buffers");
   if ((rc = check(hipMemcpy(table_dev, table.data(), table.size() * sizeof(LayerDev),
                             hipMemcpyHostToDevice), "layer table")) ||
       (rc = check(hipMemcpy(params_dev, &P, sizeof(P), hipMemcpyHostToDevice), "step params")))
     return rc;
+  params_host = P;
   step_ok = true;
   return MTG_OK;
 }

@@ -36,6 +36,8 @@ struct Ctx {
   bool step_ok = false;
   uint32_t epoch = 0;
   StepParams* params_dev = nullptr;
+  StepParams params_host{};
+  uint64_t* timing_dev = nullptr;  // step-kernel phase clock marks (profiling)
   std::string error;
   hipStream_t stream = nullptr;
   std::vector<void*> allocations;

@@ -42,21 +42,44 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   return v;
 }
 
-// Grid barrier: each workgroup publishes the barrier number in its own word
-// after its coherent stores completed; wave 0 polls all words. Returns false
-// when the step was aborted (a bounded wait ran out here or elsewhere).
+__device__ __forceinline__ void mark(const StepParams& P, int slot) {
+  if (P.timing && blockIdx.x == 0 && threadIdx.x == 0) P.timing[slot] = wall_clock64();
+}
+
+// Grid barrier: each workgroup publishes the barrier number in its own arrival
+// word once its coherent stores completed; workgroup 0 gathers all words and
+// publishes the number in the release word, which the others poll with one
+// lane. Returns false when the step was aborted (a bounded wait ran out here or
+// elsewhere).
 __device__ bool grid_sync(const StepParams& P, uint32_t target, int* s_flag) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // this wave's stores are complete
   __syncthreads();
   if (threadIdx.x == 0) st_coh_u32(P.flags + blockIdx.x, target);
-  if (threadIdx.x < 64) {
+  if (blockIdx.x == 0) {
+    if (threadIdx.x < 64) {
+      unsigned spins = 0;
+      int ok = 1;
+      for (;;) {
+        uint32_t mn = 0xffffffffu;
+        for (int i = threadIdx.x; i < (int)gridDim.x; i += 64) mn = min(mn, ld_coh_u32(P.flags + i));
+        mn = wave_min_u32(mn);
+        if (mn >= target) break;
+        if (ld_coh_u32((const uint32_t*)P.err)) { ok = 0; break; }
+        if (++spins > kSpinLimit) {
+          st_coh_u32((uint32_t*)P.err, 1u);
+          ok = 0;
+          break;
+        }
+      }
+      if (threadIdx.x == 0) {
+        if (ok) st_coh_u32(P.release, target);
+        *s_flag = ok;
+      }
+    }
+  } else if (threadIdx.x == 0) {
     unsigned spins = 0;
     int ok = 1;
-    for (;;) {
-      uint32_t mn = 0xffffffffu;
-      for (int i = threadIdx.x; i < (int)gridDim.x; i += 64) mn = min(mn, ld_coh_u32(P.flags + i));
-      mn = wave_min_u32(mn);
-      if (mn >= target) break;
+    while (ld_coh_u32(P.release) < target) {
       if (ld_coh_u32((const uint32_t*)P.err)) { ok = 0; break; }
       if (++spins > kSpinLimit) {
         st_coh_u32((uint32_t*)P.err, 1u);
@@ -64,87 +87,170 @@ __device__ bool grid_sync(const StepParams& P, uint32_t target, int* s_flag) {
         break;
       }
     }
-    if (threadIdx.x == 0) *s_flag = ok;
+    *s_flag = ok;
   }
   __syncthreads();
   return *s_flag != 0;
 }
+#define SYNC_OR_RETURN()                     \
+  do {                                       \
+    if (!grid_sync(P, ++b, &s_flag)) return; \
+    mark(P, (int)(b - epoch));               \
+  } while (0)
 
 // ---------------------------------------------------------------- panels ----
-// Build the q8_0 activation panel of T rows of src (K columns) in LDS, optionally
-// after RMSNorm * gain (then K must be 1024: 4 half-block chunks per thread at
-// most). Chunk c (16 consecutive elements of one row) belongs to lane c%64 of a
-// wave pass, so the two halves of a 32-block sit in lanes l and l^1.
+// Build the q8_0 activation panel of T rows of src (K columns, K a multiple of
+// 1024) in LDS, optionally after RMSNorm * gain (then K == 1024). A wave pass is
+// 64 half-block chunks = 1024 consecutive floats of one row: they are fetched
+// with coalesced coherent loads into the wave's LDS scratch, then lane l takes
+// elements 16l..16l+15 (the two halves of a 32-block sit in lanes l and l^1).
 // normed_out (nullable) receives the f32 normalized rows.
+__device__ __forceinline__ void load_pass(const float* src, int K, int c0, float* sw, float v[16]) {
+  const int lane = threadIdx.x & 63, cpr = K / 16;
+  const float* base = src + (size_t)(c0 / cpr) * K + (c0 % cpr) * 16;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) sw[64 * e + lane] = ld_coh(base + 64 * e + lane);
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const v4f x = *(const v4f*)(sw + 16 * lane + 4 * q);
+    v[4 * q] = x[0];
+    v[4 * q + 1] = x[1];
+    v[4 * q + 2] = x[2];
+    v[4 * q + 3] = x[3];
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+}
+
+template <int G>
+__device__ __forceinline__ void quant_store(const float v[16], int t, int kc, int bps, uint8_t* pcodes,
+                                            float* pscales) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  const float d = __fdiv_rn(amax, 127.0f);
+  const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+  uint32_t packed[4];
+#pragma unroll
+  for (int w4 = 0; w4 < 4; ++w4) {
+    uint32_t u = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int8_t q = (int8_t)rintf(__fmul_rn(v[w4 * 4 + b], id));
+      u |= (uint32_t)(uint8_t)q << (8 * b);
+    }
+    packed[w4] = u;
+  }
+  const int blk = kc >> 1, half = kc & 1, bp = blk >> 1, par = blk & 1;
+  const int cg = t >> 3, j = par * 8 + (t & 7);
+  uint8_t* unit = pcodes + (size_t)(cg * bps + bp) * 1024;
+  *(uint4*)(unit + (j + 16 * (2 * par + half)) * 16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  *(uint4*)(unit + (j + 16 * (2 * (1 - par) + half)) * 16) = make_uint4(0u, 0u, 0u, 0u);
+  if (half == 0) pscales[(size_t)(cg * bps + bp) * 16 + j] = __half2float(__float2half_rn(d));
+}
+
 template <int G>
 __device__ void build_panel(const float* src, int K, int T, const float* gain, float eps,
-                            uint8_t* pcodes, float* pscales, double* s_part, float* normed_out) {
+                            uint8_t* pcodes, float* pscales, double* s_part, float* scratch,
+                            float* normed_out) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int cpr = K / 16, chunks = T * cpr, bps = K / kPairK;
   const int passes = (chunks + kThreads - 1) / kThreads;
-  float scale_row[4] = {1.f, 1.f, 1.f, 1.f};
+  float* sw = scratch + wave * 1024;
   if (gain) {
-    // pass 1: per-wave-pass sum of squares (each pass of a wave lies in one row)
-    for (int p = 0; p < passes; ++p) {
-      const int c = p * kThreads + tid;
+    // K == 1024: one wave pass = one row; at most 4 passes (T <= 16)
+    float v[4][16];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int c0 = p * kThreads + wave * 64;
+      if (p < passes && c0 < chunks) {
+        const float* base = src + (size_t)(c0 / cpr) * K + (c0 % cpr) * 16;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[p][e] = ld_coh(base + 64 * e + lane);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if (p >= passes) break;
+      const int c0 = p * kThreads + wave * 64;
       double s = 0.0;
-      if (c < chunks) {
-        const float* row = src + (size_t)(c / cpr) * K + (c % cpr) * 16;
-        for (int e = 0; e < 16; ++e) {
-          const float v = ld_coh(row + e);
-          s += (double)__fmul_rn(v, v);
+      if (c0 < chunks) {
+        // transpose the coalesced fetch through the wave's LDS scratch
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sw[64 * e + lane] = v[p][e];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const v4f x4 = *(const v4f*)(sw + 16 * lane + 4 * qq);
+          v[p][4 * qq] = x4[0];
+          v[p][4 * qq + 1] = x4[1];
+          v[p][4 * qq + 2] = x4[2];
+          v[p][4 * qq + 3] = x4[3];
         }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s += (double)__fmul_rn(v[p][e], v[p][e]);
       }
       s = wave_sum_d(s);
       if (lane == 0) s_part[p * kWaves + wave] = s;
     }
     __syncthreads();
-    for (int p = 0; p < passes; ++p) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
       const int c = p * kThreads + tid;
-      if (c >= chunks) continue;
-      const int t = c / cpr;
-      // sum the wave-pass partials of row t in pass order
-      double tot = 0.0;
-      const int first = t * cpr / 64, last = (t + 1) * cpr / 64;
-      for (int q = first; q < last; ++q) tot += s_part[q];
-      const float mean = (float)(tot / (double)K);
-      scale_row[p & 3] = dev_rms_scale(mean, eps);
+      if (p >= passes || c >= chunks) break;  // whole waves
+      const int t = c / cpr, kc = c % cpr, k0 = kc * 16;
+      const float mean = (float)(s_part[p * kWaves + wave] / (double)K);
+      const float scale = dev_rms_scale(mean, eps);
+      float y[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) y[e] = __fmul_rn(__fmul_rn(v[p][e], scale), gain[k0 + e]);
+      if (normed_out)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) normed_out[(size_t)t * K + k0 + e] = y[e];
+      quant_store<G>(y, t, kc, bps, pcodes, pscales);
     }
-  }
-  for (int p = 0; p < passes; ++p) {
-    const int c = p * kThreads + tid;
-    const bool active = c < chunks;  // whole wave passes share this (chunks % 64 == 0)
-    if (!active) break;
-    const int t = c / cpr, kc = c % cpr, k0 = kc * 16;
-    const float* row = src + (size_t)t * K + k0;
-    float v[16];
-    float amax = 0.0f;
-    for (int e = 0; e < 16; ++e) {
-      float y = ld_coh(row + e);
-      if (gain) y = __fmul_rn(__fmul_rn(y, scale_row[p & 3]), gain[k0 + e]);
-      v[e] = y;
-      amax = fmaxf(amax, fabsf(y));
-    }
-    if (normed_out)
-      for (int e = 0; e < 16; ++e) normed_out[(size_t)t * K + k0 + e] = v[e];
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    const float d = __fdiv_rn(amax, 127.0f);
-    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-    uint32_t packed[4];
-    for (int w4 = 0; w4 < 4; ++w4) {
-      uint32_t u = 0;
-      for (int b = 0; b < 4; ++b) {
-        const int8_t q = (int8_t)rintf(__fmul_rn(v[w4 * 4 + b], id));
-        u |= (uint32_t)(uint8_t)q << (8 * b);
+  } else {
+    for (int p0 = 0; p0 < passes; p0 += 4) {
+      // fetch up to four passes of this wave with independent coherent loads
+      float raw[4][16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c0 = (p0 + q) * kThreads + wave * 64;
+        if (p0 + q < passes && c0 < chunks) {
+          const float* base = src + (size_t)(c0 / cpr) * K + (c0 % cpr) * 16;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) raw[q][e] = ld_coh(base + 64 * e + lane);
+        }
       }
-      packed[w4] = u;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c0 = (p0 + q) * kThreads + wave * 64;
+        if (p0 + q >= passes || c0 >= chunks) break;  // whole waves
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sw[64 * e + lane] = raw[q][e];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        float v[16];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const v4f x4 = *(const v4f*)(sw + 16 * lane + 4 * qq);
+          v[4 * qq] = x4[0];
+          v[4 * qq + 1] = x4[1];
+          v[4 * qq + 2] = x4[2];
+          v[4 * qq + 3] = x4[3];
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        const int c = c0 + lane;
+        quant_store<G>(v, c / cpr, c % cpr, bps, pcodes, pscales);
+      }
     }
-    const int blk = kc >> 1, half = kc & 1, bp = blk >> 1, par = blk & 1;
-    const int cg = t >> 3, j = par * 8 + (t & 7);
-    uint8_t* unit = pcodes + (size_t)(cg * bps + bp) * 1024;
-    *(uint4*)(unit + (j + 16 * (2 * par + half)) * 16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    *(uint4*)(unit + (j + 16 * (2 * (1 - par) + half)) * 16) = make_uint4(0u, 0u, 0u, 0u);
-    if (half == 0) pscales[(size_t)(cg * bps + bp) * 16 + j] = __half2float(__float2half_rn(d));
   }
   __syncthreads();
 }
@@ -314,17 +420,57 @@ __device__ void attn_phase(const StepParams& P, const LayerDev& Ly, int T, int p
   }
 }
 
-// (head, row) items: merge the chunks into o[t][head*128 + d].
-__device__ void combine_phase(const StepParams& P, int T, int past) {
+// (head, row) items: merge the chunks into o[t][head*128 + d]. Each half
+// workgroup takes one item; the partials of up to 32 chunks are fetched with
+// independent coherent loads before the canonical merge runs over them.
+__device__ void combine_phase(const StepParams& P, int T, int past, float* s_ml) {
   const int items = P.NH * T, nch = (past + T + kChunk - 1) / kChunk;
   const int d = threadIdx.x & 127, half = threadIdx.x >> 7;
-  for (int item = 2 * blockIdx.x + half; item < items; item += 2 * gridDim.x) {
-    const int hq = item / T, t = item % T, g = hq / 2, col = (hq & 1) * T + t;
-    const size_t item0 = (size_t)g * P.max_chunks;
-    const float val = attn_merge<true>(P.part_ml + item0 * kMaxCols * 2 + col * 2,
-                                       P.part_o + item0 * kMaxCols * kHeadDim + col * kHeadDim, nch,
-                                       (size_t)kMaxCols * 2, (size_t)kMaxCols * kHeadDim, d);
-    st_coh(P.o + (size_t)t * P.NH * kHeadDim + hq * kHeadDim + d, val);
+  float* ml = s_ml + half * 64;  // [32 chunks][2]
+  for (int base = 2 * blockIdx.x; base < items; base += 2 * gridDim.x) {
+    const int item = base + half;
+    const bool active = item < items;
+    const int hq = active ? item / T : 0, t = active ? item % T : 0;
+    const int g = hq / 2, col = (hq & 1) * T + t;
+    const float* pml = P.part_ml + (size_t)g * P.max_chunks * kMaxCols * 2 + col * 2;
+    const float* po = P.part_o + (size_t)g * P.max_chunks * kMaxCols * kHeadDim + col * kHeadDim + d;
+    const size_t sml = (size_t)kMaxCols * 2, so = (size_t)kMaxCols * kHeadDim;
+    // pass 1: the maximum over all chunks
+    float M = -INFINITY;
+    for (int c0 = 0; c0 < nch; c0 += 64) {
+      const int c = c0 + (d & 63);
+      float m = -INFINITY;
+      if (active && d < 64 && c < nch) m = ld_coh(pml + c * sml);
+      M = fmaxf(M, m);
+    }
+    // M is reduced over the half workgroup's first wave-half... use LDS
+    __shared__ float s_max[2][2];
+    M = wave_max_f(M);
+    if ((threadIdx.x & 63) == 0 && ((threadIdx.x >> 6) & 1) == 0) s_max[half][0] = M;
+    __syncthreads();
+    M = s_max[half][0];
+    float L = 0.0f, O = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 32) {
+      const int nb = min(32, nch - c0);
+      if (active && d < 2 * nb) ml[d] = ld_coh(pml + (c0 + (d >> 1)) * sml + (d & 1));
+      float ov[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) ov[i] = (active && i < nb) ? ld_coh(po + (c0 + i) * so) : 0.0f;
+      __syncthreads();
+      if (active) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          if (i >= nb) break;
+          const float m = ml[2 * i];
+          if (m == -INFINITY) continue;
+          const float f = dev_expf(__fsub_rn(m, M));
+          L = fmaf(ml[2 * i + 1], f, L);
+          O = fmaf(ov[i], f, O);
+        }
+      }
+      __syncthreads();
+    }
+    if (active) st_coh(P.o + (size_t)t * P.NH * kHeadDim + hq * kHeadDim + d, __fdiv_rn(O, L));
   }
 }
 
@@ -426,12 +572,14 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   uint8_t* pcodes = lds;
   float* pscales = (float*)(lds + (size_t)G * bps_max * 1024);
   float* red = (float*)(lds + (size_t)G * bps_max * (1024 + 64));
+  float* scratch = red;  // panel builds and GEMM reductions never overlap in time
   __shared__ double s_part[64];
   __shared__ int s_flag;
   __shared__ uint64_t s_best[kWaves * kMaxRows];
   __shared__ uint64_t s_red[kThreads];
   __shared__ int32_t s_choice[kMaxRows];
   uint32_t b = epoch;
+  mark(P, 0);
 
   // embeddings (and the penalty bitmap)
   if ((int)blockIdx.x < T) {
@@ -462,44 +610,45 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       }
     }
   }
-  if (!grid_sync(P, ++b, &s_flag)) return;
+  SYNC_OR_RETURN();
 
   for (int l = 0; l < P.L; ++l) {
     const LayerDev& Ly = P.layers[l];
     // QKV
     if ((int)blockIdx.x < (QN + 2 * KN) / 16) {
-      build_panel<G>(P.x, H, T, Ly.attn_norm, P.eps, pcodes, pscales, s_part, nullptr);
+      build_panel<G>(P.x, H, T, Ly.attn_norm, P.eps, pcodes, pscales, s_part, scratch, nullptr);
       gemm_phase<G, EPI_STORE>(Ly.wqkv, nullptr, (QN + 2 * KN) / 16, H / kPairK, pcodes, pscales, red,
                                P.qkv, QN + 2 * KN, T);
     }
-    if (!grid_sync(P, ++b, &s_flag)) return;
+    SYNC_OR_RETURN();
     attn_phase(P, Ly, T, past, lds);
-    if (!grid_sync(P, ++b, &s_flag)) return;
-    combine_phase(P, T, past);
-    if (!grid_sync(P, ++b, &s_flag)) return;
+    SYNC_OR_RETURN();
+    combine_phase(P, T, past, (float*)lds);
+    SYNC_OR_RETURN();
     if ((int)blockIdx.x < H / 16) {
-      build_panel<G>(P.o, QN, T, nullptr, 0.0f, pcodes, pscales, s_part, nullptr);
+      build_panel<G>(P.o, QN, T, nullptr, 0.0f, pcodes, pscales, s_part, scratch, nullptr);
       gemm_phase<G, EPI_RESID>(Ly.wo, nullptr, H / 16, QN / kPairK, pcodes, pscales, red, P.x, H, T);
     }
-    if (!grid_sync(P, ++b, &s_flag)) return;
+    SYNC_OR_RETURN();
     if ((int)blockIdx.x < F / 16) {
-      build_panel<G>(P.x, H, T, Ly.ffn_norm, P.eps, pcodes, pscales, s_part, nullptr);
+      build_panel<G>(P.x, H, T, Ly.ffn_norm, P.eps, pcodes, pscales, s_part, scratch, nullptr);
       gemm_phase<G, EPI_SWIGLU>(Ly.wg, Ly.wu, F / 16, H / kPairK, pcodes, pscales, red, P.act, F, T);
     }
-    if (!grid_sync(P, ++b, &s_flag)) return;
+    SYNC_OR_RETURN();
     if ((int)blockIdx.x < H / 16) {
-      build_panel<G>(P.act, F, T, nullptr, 0.0f, pcodes, pscales, s_part, nullptr);
+      build_panel<G>(P.act, F, T, nullptr, 0.0f, pcodes, pscales, s_part, scratch, nullptr);
       gemm_phase<G, EPI_RESID>(Ly.wd, nullptr, H / 16, F / kPairK, pcodes, pscales, red, P.x, H, T);
     }
-    if (!grid_sync(P, ++b, &s_flag)) return;
+    SYNC_OR_RETURN();
   }
   // final RMSNorm * output_norm (workgroup 0 also returns the f32 rows)
-  build_panel<G>(P.x, H, T, P.out_norm, P.eps, pcodes, pscales, s_part,
+  build_panel<G>(P.x, H, T, P.out_norm, P.eps, pcodes, pscales, s_part, scratch,
                  blockIdx.x == 0 ? P.hid : nullptr);
   if (mode != kStepVerify) return;
   lm_head_phase<G>(P, desc, T, pcodes, pscales, s_best);
-  if (!grid_sync(P, ++b, &s_flag)) return;
+  SYNC_OR_RETURN();
   if (blockIdx.x == 0) accept_phase(P, desc, T, s_red, s_choice);
+  mark(P, (int)(b - epoch) + 1);
 }
 
 }  // namespace
@@ -508,7 +657,8 @@ int step_barriers(int n_layers, int mode) { return 1 + 6 * n_layers + (mode == k
 
 size_t step_lds_bytes(int G, int bps_max) {
   const size_t panel = (size_t)G * bps_max * (1024 + 64);
-  const size_t red = (size_t)kWaves * 2 * G * 4 * 64 * 4;
+  size_t red = (size_t)kWaves * 2 * G * 4 * 64 * 4;
+  if (red < (size_t)kWaves * 1024 * 4) red = (size_t)kWaves * 1024 * 4;  // panel-build scratch
   const size_t attn = ((size_t)kMaxCols * kHeadDim + 2 * kMaxRows * kHeadDim + kChunk * kHeadDim +
                        (size_t)kMaxCols * kChunk) * 4;
   return (panel > attn ? panel : attn) + red;

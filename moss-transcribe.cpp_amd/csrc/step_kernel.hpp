@@ -33,7 +33,9 @@ struct StepParams {
   uint64_t* part_keys;      // [nwg][16]
   StepResult* result;
   uint32_t* flags;          // [nwg] barrier arrival words
+  uint32_t* release;        // barrier release word (written by workgroup 0)
   int32_t* err;             // raised by a wait that ran out (inside *result)
+  uint64_t* timing;         // nullable: workgroup 0 records the clock after every barrier
 };
 
 int step_barriers(int n_layers, int mode);

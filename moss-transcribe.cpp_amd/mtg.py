@@ -85,6 +85,8 @@ SIGNATURES = {
     "mtg_set_exec_mode": (c_int32, [c_void_p, c_int32]),
     "mtg_exec_mode": (c_int32, [c_void_p]),
     "mtg_debug_copy": (c_int32, [c_void_p, c_int32, c_void_p, ctypes.c_size_t]),
+    "mtg_step_profile": (c_int32, [c_void_p, c_int32]),
+    "mtg_step_profile_read": (c_int32, [c_void_p, c_void_p, c_int32]),
     "mtg_ngram_draft": (c_int32, [c_void_p, c_int32, c_int32, c_void_p]),
     "mtg_greedy_choice": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_float]),
     "mtg_q8_pack": (c_int32, [c_void_p, c_int32, c_int32, POINTER(c_void_p)]),
@@ -228,6 +230,14 @@ class Decoder:
         out = np.empty((MAX_BATCH, width), np.float32)
         self._chk(lib().mtg_debug_copy(self.ctx, which, ptr(out), out.nbytes))
         return out
+
+    def step_profile(self, on):
+        self._chk(lib().mtg_step_profile(self.ctx, 1 if on else 0))
+
+    def step_marks(self):
+        out = np.zeros(1024, np.uint64)
+        n = lib().mtg_step_profile_read(self.ctx, ptr(out), 1024)
+        return out[:n].astype(np.int64)
 
     @property
     def exec_mode(self):
