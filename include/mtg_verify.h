@@ -10,19 +10,24 @@
  * moss-transcribe.cpp source tree):
  *   mtg_create/mtg_destroy    Qwen3Decoder::load, ~Qwen3Decoder     src/qwen3_decoder.cpp:16-85
  *   mtg_prefill               Qwen3Decoder::prefill                 src/qwen3_decoder.cpp:162-166
- *   mtg_append                CpuSpeculativeDecoder::append -> run  src/cpu_speculative.cpp:37-39, src/qwen3_decoder.cpp:91-160
+ *   mtg_append                CpuSpeculativeDecoder::append -> run  src/cpu_speculative.cpp:19-21,
+ *                                                                    src/qwen3_decoder.cpp:91-160
  *   mtg_logits                Qwen3Decoder::logits_from_hidden      src/qwen3_decoder.cpp:174-205
  *   mtg_embed                 embed_rows_f32                        src/generate.cpp:68-111
  *   mtg_verify                append + lazy logits + cpu_greedy_choice + accept loop
- *                                                                    src/cpu_speculative.cpp:127-148
+ *                                                                    src/cpu_speculative.cpp:109-130
  *   mtg_rewind/mtg_past_len   CpuSpeculativeDecoder::rewind, Qwen3Decoder::past_len
- *                                                                    src/cpu_speculative.cpp:40-43, src/qwen3_decoder.hpp:262
- *   mtg_remaining             CpuSpeculativeDecoder::remaining       src/cpu_speculative.cpp:43
- *   mtg_generate              cpu_speculative_generate               src/cpu_speculative.cpp:86-165
- *   mtg_ngram_draft           cpu_ngram_draft                        src/cpu_speculative.cpp:45-56
- *   mtg_greedy_choice         cpu_greedy_choice                      src/cpu_speculative.cpp:57-68
- *   mtg_q8_pack/mtg_q8_mul_mat  cpu_pack_q8 / cpu_decode_mul_mat     src/cpu_q8.hpp:131-145, src/cpu_q8.cpp:177-276
- *   mtg_causal_context        cpu_causal_context                     src/cpu_context.hpp:69-73, src/cpu_context.cpp:13-56
+ *                                                                    src/cpu_speculative.cpp:22-24,
+ *                                                                    src/qwen3_decoder.hpp:55
+ *   mtg_remaining             CpuSpeculativeDecoder::remaining       src/cpu_speculative.cpp:25
+ *   mtg_generate              cpu_speculative_generate               src/cpu_speculative.cpp:68-147
+ *   mtg_speculative_run       the loop of cpu_speculative_generate   src/cpu_speculative.cpp:89-137
+ *   mtg_ngram_draft           cpu_ngram_draft                        src/cpu_speculative.cpp:27-38
+ *   mtg_greedy_choice         cpu_greedy_choice                      src/cpu_speculative.cpp:39-50
+ *   mtg_q8_pack/mtg_q8_mul_mat  cpu_pack_q8 / cpu_decode_mul_mat     src/cpu_q8.hpp:13-27,
+ *                                                                    src/cpu_q8.cpp:30-129
+ *   mtg_causal_context        cpu_causal_context                     src/cpu_context.hpp:7-10,
+ *                                                                    src/cpu_context.cpp:13-56
  *   mtg_last_error            moss_transcribe_capi_last_error        include/moss_transcribe_capi.h:50-53
  *
  * Conventions: every function returns an int status (MTG_OK == 0, negative on
@@ -168,6 +173,38 @@ typedef struct mtg_gen_stats {
   int32_t next_seed;   /* greedy choice of the last kept row (the next step's seed) */
 } mtg_gen_stats;
 
+/* A decoder the controller drives (reference: the Qwen3Decoder that
+ * cpu_speculative_generate appends to and rewinds, src/cpu_speculative.cpp:17-26).
+ * verify runs T rows {seed, drafts} at *past (the controller then sets *past to
+ * past + T) and returns the greedy choice after every row and the number of
+ * leading drafts equal to the choice of the row before them, as mtg_verify does;
+ * the controller rewinds by writing *past. A nonzero return aborts the loop. */
+typedef int32_t (*mtg_target_verify_fn)(void* self, const int32_t* tokens, int32_t T,
+                                        const int32_t* history, int32_t n_history, float penalty,
+                                        int32_t* choice_out, int32_t* n_match_out);
+typedef struct mtg_target {
+  void* self;
+  mtg_target_verify_fn verify;
+  int32_t* past;   /* the target's past_len */
+  int32_t max_seq;
+  int32_t vocab;
+} mtg_target;
+
+/* The loop of cpu_speculative_generate over any target, continuing from its
+ * current state: emit the seed (eos / token-limit stops), budget =
+ * min(max_draft, max_new - emitted, max_seq - past - 1), draft (draft == NULL:
+ * mtg_ngram_draft), verify seed + drafts, emit the drafts that equal the greedy
+ * choice of the row before them (a stopping token is emitted but not kept),
+ * logical rewind to past + kept. first_seed: the greedy choice of the last row
+ * already in the target. prior_ids (nullable): ids committed before, visible to
+ * the drafter and the penalty window. max_steps <= 0: until a stop rule fires.
+ * Returns the verify callback's status or MTG_ERR_INVALID (bad draft id). */
+int mtg_speculative_run(const mtg_target* target, int32_t first_seed, const int32_t* prior_ids,
+                        int32_t n_prior, int32_t max_new, int32_t max_steps, int32_t eos,
+                        float penalty, int32_t max_draft, mtg_draft_fn draft,
+                        mtg_commit_fn commit, void* user, int32_t* ids_out, int32_t* n_ids_out,
+                        mtg_gen_stats* stats);
+
 /* cpu_speculative_generate on the device decoder: prefill `seq` fused rows, take
  * the first greedy seed, then loop {draft <= max_draft, verify, accept, rewind}
  * until eos or max_new tokens. draft == NULL uses mtg_ngram_draft. ids_out must
@@ -176,10 +213,7 @@ int mtg_generate(mtg_ctx* ctx, const float* fused, int32_t seq, int32_t max_new,
                  float penalty, int32_t max_draft, mtg_draft_fn draft, mtg_commit_fn commit,
                  void* user, int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats);
 
-/* Same loop, continuing from the current KV state instead of a prefill.
- * first_seed: the greedy choice of the last row already in the cache.
- * prior_ids (nullable): ids committed before, visible to the drafter and the
- * penalty window. max_steps <= 0: run until a stop rule fires. */
+/* mtg_speculative_run on the device decoder, from its current KV state. */
 int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids,
                       int32_t n_prior, int32_t max_new, int32_t max_steps, int32_t eos,
                       float penalty, int32_t max_draft, mtg_draft_fn draft, mtg_commit_fn commit,

@@ -109,7 +109,7 @@ int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes) {
 int32_t mtg_past_len(const mtg_ctx* ctx) { return ctx ? ctx->impl.past : 0; }
 int32_t mtg_remaining(const mtg_ctx* ctx) { return ctx ? ctx->impl.max_seq - ctx->impl.past : 0; }
 
-// CpuSpeculativeDecoder::rewind (src/cpu_speculative.cpp:40-42): logical only;
+// CpuSpeculativeDecoder::rewind (src/cpu_speculative.cpp:22-24): logical only;
 // positions >= past_len are never read again before being rewritten.
 int mtg_rewind(mtg_ctx* ctx, int32_t position) {
   if (!ctx) return MTG_ERR_INVALID;
@@ -187,7 +187,7 @@ int mtg_kv_read(mtg_ctx* ctx, void* k, void* v, int32_t n_pos) {
   return ctx->impl.kv_io(k, v, n_pos, false);
 }
 
-// cpu_ngram_draft (src/cpu_speculative.cpp:45-56).
+// cpu_ngram_draft (src/cpu_speculative.cpp:27-38).
 int32_t mtg_ngram_draft(const int32_t* h, int32_t size, int32_t maximum, int32_t* out) {
   if (!h || !out || maximum <= 0 || size < 3) return 0;
   for (int n = std::min<int>(16, size - 1); n >= 2; --n)
@@ -200,7 +200,7 @@ int32_t mtg_ngram_draft(const int32_t* h, int32_t size, int32_t maximum, int32_t
   return 0;
 }
 
-// cpu_greedy_choice (src/cpu_speculative.cpp:57-68).
+// cpu_greedy_choice (src/cpu_speculative.cpp:39-50).
 int32_t mtg_greedy_choice(const float* raw, int32_t n, const int32_t* history, int32_t nh,
                           float penalty) {
   if (!raw || n <= 0) return -1;
@@ -222,28 +222,29 @@ int32_t mtg_greedy_choice(const float* raw, int32_t n, const int32_t* history, i
   return best;
 }
 
-// The loop of cpu_speculative_generate (src/cpu_speculative.cpp:118-155) on the
-// device decoder. Differences: the draft width is a parameter (the reference
-// fixes 4), and all T logits rows come from one lm_head pass with on-device
-// choices instead of one lazily computed row at a time; the accepted tokens, the
-// kept KV rows and the rewinds are the same.
-int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
-                      int32_t max_new, int32_t max_steps, int32_t eos, float penalty,
-                      int32_t max_draft, mtg_draft_fn draft, mtg_commit_fn commit, void* user,
-                      int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats) {
-  if (!ctx) return MTG_ERR_INVALID;
-  Ctx& c = ctx->impl;
-  if (!ids_out || !n_ids_out || max_new <= 0 || first_seed < 0 || first_seed >= c.hp.vocab)
-    return c.fail(MTG_ERR_INVALID, "generate: bad arguments");
+// The loop of cpu_speculative_generate (src/cpu_speculative.cpp:89-137) over any
+// verify target. Differences from the reference: the draft width is a parameter
+// (the reference fixes 4, :104) and a target returns the greedy choice of every
+// row at once (the device computes all T logits rows in one lm_head pass)
+// instead of one lazily computed row at a time (:118-130); the emitted ids, the
+// kept KV rows, the rewinds and the counters are the same.
+int mtg_speculative_run(const mtg_target* tg, int32_t first_seed, const int32_t* prior_ids,
+                        int32_t n_prior, int32_t max_new, int32_t max_steps, int32_t eos,
+                        float penalty, int32_t max_draft, mtg_draft_fn draft,
+                        mtg_commit_fn commit, void* user, int32_t* ids_out, int32_t* n_ids_out,
+                        mtg_gen_stats* stats) {
+  if (!tg || !tg->verify || !tg->past || !ids_out || !n_ids_out || max_new <= 0 || n_prior < 0 ||
+      first_seed < 0 || first_seed >= tg->vocab)
+    return MTG_ERR_INVALID;
   try {
-    penalty = std::max(1.0f, std::min(1.5f, penalty));
+    penalty = std::max(1.0f, std::min(1.5f, penalty));  // :85-86
     max_draft = std::max(0, std::min(max_draft, MTG_MAX_BATCH - 1));
     std::vector<int32_t> ids(prior_ids, prior_ids + (prior_ids ? n_prior : 0));
     const size_t first_new = ids.size();
     ids.reserve(first_new + (size_t)max_new);
     mtg_gen_stats st{};
     int stop = 0;
-    auto emit = [&](int32_t id) {
+    auto emit = [&](int32_t id) {  // :90-98 (the loop guard needs the tokenizer)
       ids.push_back(id);
       if (id == eos) stop = 1;
       else if ((int)(ids.size() - first_new) >= max_new) stop = 2;
@@ -256,31 +257,30 @@ int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids
       const int32_t seed = raw_choice;
       emit(seed);
       if (stop) {
-        if (commit) commit(user, ids.data(), (int)ids.size(), c.past, 1);
+        if (commit) commit(user, ids.data(), (int)ids.size(), *tg->past, 1);
         break;
       }
-      const int before = c.past;
+      const int before = *tg->past;
       const int budget = std::max(0, std::min({max_draft, max_new - (int)(ids.size() - first_new),
-                                               c.max_seq - c.past - 1}));
+                                               tg->max_seq - before - 1}));
       auto t0 = std::chrono::steady_clock::now();
       int np = draft ? draft(user, ids.data(), (int)ids.size(), budget, proposal)
                      : mtg_ngram_draft(ids.data(), (int)ids.size(), budget, proposal);
       st.draft_seconds += seconds_since(t0);
       np = std::max(0, std::min(np, budget));
       for (int i = 0; i < np; ++i)
-        if (proposal[i] < 0 || proposal[i] >= c.hp.vocab) {
-          rc = c.fail(MTG_ERR_INVALID, "invalid draft token %d", proposal[i]);
-          break;
-        }
+        if (proposal[i] < 0 || proposal[i] >= tg->vocab) rc = MTG_ERR_INVALID;  // :108
       if (rc) break;
       inputs[0] = seed;
       std::copy(proposal, proposal + np, inputs + 1);
       int32_t n_match = 0;
       t0 = std::chrono::steady_clock::now();
-      rc = c.verify(inputs, np + 1, ids.data(), (int)ids.size() - 1, penalty, choice, &n_match,
-                    nullptr, nullptr);
+      // row i's penalty window: ids before the seed ++ inputs[0..i]
+      rc = tg->verify(tg->self, inputs, np + 1, ids.data(), (int)ids.size() - 1, penalty, choice,
+                      &n_match);
       st.verify_seconds += seconds_since(t0);
       if (rc) break;
+      *tg->past = before + np + 1;
       ++steps;
       ++st.target_calls;
       st.drafted_calls += np > 0;
@@ -291,16 +291,16 @@ int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids
       for (int i = 0; i < np && i < n_match; ++i) {
         ++st.accepted;
         emit(proposal[i]);
-        if (stop) break;  // the terminating token is emitted, not kept
+        if (stop) break;  // the terminating token is emitted, not kept (:128)
         ++keep;
         raw_choice = choice[i + 1];
       }
       const int position = before + keep;
-      if (c.past != position) {
-        c.past = position;
+      if (*tg->past != position) {  // :131-135
+        *tg->past = position;
         ++st.rewinds;
       }
-      if (commit) commit(user, ids.data(), (int)ids.size(), c.past, stop != 0);
+      if (commit) commit(user, ids.data(), (int)ids.size(), *tg->past, stop != 0);
     }
     st.stop_reason = stop;
     st.next_seed = raw_choice;
@@ -310,8 +310,34 @@ int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids
     if (stats) *stats = st;
     return rc;
   } catch (...) {
-    return c.fail(MTG_ERR_DEVICE, "generate: exception");
+    return MTG_ERR_NOMEM;
   }
+}
+
+namespace {
+int32_t ctx_verify(void* self, const int32_t* tokens, int32_t T, const int32_t* history,
+                   int32_t n_history, float penalty, int32_t* choice_out, int32_t* n_match_out) {
+  // Ctx::verify advances past by T itself; the controller sets it again.
+  return ((Ctx*)self)->verify(tokens, T, history, n_history, penalty, choice_out, n_match_out,
+                              nullptr, nullptr);
+}
+}  // namespace
+
+int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
+                      int32_t max_new, int32_t max_steps, int32_t eos, float penalty,
+                      int32_t max_draft, mtg_draft_fn draft, mtg_commit_fn commit, void* user,
+                      int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats) {
+  if (!ctx) return MTG_ERR_INVALID;
+  Ctx& c = ctx->impl;
+  if (!ids_out || !n_ids_out || max_new <= 0 || first_seed < 0 || first_seed >= c.hp.vocab)
+    return c.fail(MTG_ERR_INVALID, "generate: bad arguments");
+  mtg_target tg{&c, ctx_verify, &c.past, c.max_seq, c.hp.vocab};
+  c.error.clear();
+  const int rc = mtg_speculative_run(&tg, first_seed, prior_ids, n_prior, max_new, max_steps, eos,
+                                     penalty, max_draft, draft, commit, user, ids_out, n_ids_out,
+                                     stats);
+  if (rc && c.error.empty()) c.fail(rc, "generate: invalid draft token or argument");
+  return rc;
 }
 
 int mtg_generate(mtg_ctx* ctx, const float* fused, int32_t seq, int32_t max_new, int32_t eos,

@@ -13,7 +13,7 @@
 //                                                             src/cpu_context.cpp:13-32
 //   k_lm_head + k_accept  tied lm_head, cpu_greedy_choice, the accept loop
 //                                                             src/qwen3_decoder.cpp:174-205,
-//                                                             src/cpu_speculative.cpp:57-68,142-148
+//                                                             src/cpu_speculative.cpp:39-50,124-130
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 

@@ -20,7 +20,7 @@
 //   DOWN   q8_0(act) panel; 64 tiles; x += W_d act
 // then the final norm, the tied lm_head with fused argmax keys, and the
 // on-device acceptance (src/qwen3_decoder.cpp:129,174-205,
-// src/cpu_speculative.cpp:57-68,142-148).
+// src/cpu_speculative.cpp:39-50,124-130).
 //
 // Every barrier wait is bounded: a workgroup that waits too long raises the
 // error word and returns, every other workgroup sees it and returns too, and the

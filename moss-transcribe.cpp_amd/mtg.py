@@ -56,6 +56,15 @@ class StreamDrafter(ctypes.Structure):
 
 
 DRAFT_FN = ctypes.CFUNCTYPE(c_int32, c_void_p, POINTER(c_int32), c_int32, c_int32, POINTER(c_int32))
+TARGET_VERIFY_FN = ctypes.CFUNCTYPE(c_int32, c_void_p, POINTER(c_int32), c_int32, POINTER(c_int32),
+                                    c_int32, c_float, POINTER(c_int32), POINTER(c_int32))
+
+
+class Target(ctypes.Structure):
+    _fields_ = [("self", c_void_p), ("verify", TARGET_VERIFY_FN), ("past", POINTER(c_int32)),
+                ("max_seq", c_int32), ("vocab", c_int32)]
+
+
 COMMIT_FN = ctypes.CFUNCTYPE(None, c_void_p, POINTER(c_int32), c_int32, c_int32, c_int32)
 
 # name -> (restype, argtypes)
@@ -81,6 +90,9 @@ SIGNATURES = {
     "mtg_generate_from": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32,
                                     c_int32, c_float, c_int32, c_void_p, c_void_p, c_void_p,
                                     c_void_p, POINTER(c_int32), POINTER(GenStats)]),
+    "mtg_speculative_run": (c_int32, [POINTER(Target), c_int32, c_void_p, c_int32, c_int32, c_int32,
+                                      c_int32, c_float, c_int32, c_void_p, c_void_p, c_void_p,
+                                      c_void_p, POINTER(c_int32), POINTER(GenStats)]),
     "mtg_stream_draft": (c_int32, [c_void_p, POINTER(c_int32), c_int32, c_int32, POINTER(c_int32)]),
     "mtg_set_exec_mode": (c_int32, [c_void_p, c_int32]),
     "mtg_exec_mode": (c_int32, [c_void_p]),
@@ -323,6 +335,62 @@ class Decoder:
                                           ctypes.byref(st)))
         del keep
         return out[: n.value].copy(), st
+
+
+def _draft_pointer(draft):
+    """(function pointer, keepalive) for a Python drafter callable."""
+    if draft is None:
+        return None, None
+    if not callable(draft):
+        return draft, None
+
+    def _cb(_user, ids, n_ids, budget, dst, _f=draft):
+        props = list(_f([ids[i] for i in range(n_ids)], budget))[:budget]
+        for i, t in enumerate(props):
+            dst[i] = int(t)
+        return len(props)
+    keep = DRAFT_FN(_cb)
+    return ctypes.cast(keep, c_void_p), keep
+
+
+def speculative_run(verify_cb, first_seed, max_new, eos=-1, penalty=1.0, max_draft=4, past=0,
+                    max_seq=1 << 20, vocab=1 << 20, draft=None, prior=(), max_steps=0,
+                    commits=None):
+    """Drive the library's controller (mtg_speculative_run) with a Python target:
+    verify_cb(tokens, history, penalty, past) -> (choices, n_match). Returns
+    (ids, stats, past)."""
+    past_box = c_int32(past)
+
+    def _verify(_self, tokens, T, hist, nh, pen, choice_out, n_match_out):
+        try:
+            ch, nm = verify_cb([tokens[i] for i in range(T)], [hist[i] for i in range(nh)], pen,
+                               past_box.value)
+        except Exception:
+            return ERR_INVALID
+        for i in range(T):
+            choice_out[i] = int(ch[i])
+        n_match_out[0] = int(nm)
+        return OK
+    vfn = TARGET_VERIFY_FN(_verify)
+    tg = Target(None, vfn, ctypes.pointer(past_box), max_seq, vocab)
+    fn, keep = _draft_pointer(draft)
+    cfn = None
+    if commits is not None:
+        def _commit(_u, ids, n, past_len, stopped):
+            commits.append(([ids[i] for i in range(n)], past_len, stopped))
+        cfn_keep = COMMIT_FN(_commit)
+        cfn = ctypes.cast(cfn_keep, c_void_p)
+    out = np.empty(max_new, np.int32)
+    n = c_int32(0)
+    st = GenStats()
+    prior = i32(prior)
+    rc = lib().mtg_speculative_run(ctypes.byref(tg), first_seed, ptr(prior) if len(prior) else None,
+                                   len(prior), max_new, max_steps, eos, penalty, max_draft, fn, cfn,
+                                   None, ptr(out), ctypes.byref(n), ctypes.byref(st))
+    del keep, vfn
+    if rc:
+        raise MtgError(rc, "speculative_run")
+    return [int(x) for x in out[: n.value]], st, past_box.value
 
 
 def stream_drafter(prompt, stream):

@@ -563,6 +563,7 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
 extern "C" {
 
 uint16_t orc_f32_to_f16(float f) { return f2h(f); }
+float orc_exp(float x) { return exp_c(x); }
 float orc_f16_to_f32(uint16_t h) { return h2f(h); }
 void orc_quantize_q8_0_act(const float* x, int64_t k, void* blocks) {
   quantize_q8_0_act(x, k, (BlockQ8*)blocks);
@@ -655,7 +656,7 @@ int orc_create(const mtg_model_desc* desc, int32_t max_seq, int32_t kv_type, orc
 void orc_destroy(orc_model* m) { delete m; }
 int32_t orc_past_len(const orc_model* m) { return m ? m->past : 0; }
 
-// CpuSpeculativeDecoder::rewind (src/cpu_speculative.cpp:40-42).
+// CpuSpeculativeDecoder::rewind (src/cpu_speculative.cpp:22-24).
 int orc_rewind(orc_model* m, int32_t position) {
   if (!m || position < 0 || position > m->past) return MTG_ERR_STATE;
   m->past = position;
@@ -702,7 +703,7 @@ int orc_logits(orc_model* m, const float* hidden, int32_t T, float* logits_out) 
   return MTG_OK;
 }
 
-// cpu_ngram_draft (src/cpu_speculative.cpp:45-56): for n = min(16,|h|-1)..2
+// cpu_ngram_draft (src/cpu_speculative.cpp:27-38): for n = min(16,|h|-1)..2
 // the latest earlier occurrence of the last-n suffix; up to `maximum` tokens
 // that follow it.
 int32_t orc_ngram_draft(const int32_t* h, int32_t size, int32_t maximum, int32_t* out) {
@@ -719,7 +720,7 @@ int32_t orc_ngram_draft(const int32_t* h, int32_t size, int32_t maximum, int32_t
   return 0;
 }
 
-// cpu_greedy_choice (src/cpu_speculative.cpp:57-68): first maximum (strict >)
+// cpu_greedy_choice (src/cpu_speculative.cpp:39-50): first maximum (strict >)
 // after dividing positive / multiplying negative logits of the distinct ids of
 // the last 100 history entries by the penalty.
 int32_t orc_greedy_choice(const float* raw, int32_t n, const int32_t* history, int32_t nh,
@@ -807,7 +808,7 @@ int orc_kv_read(const orc_model* m, void* k, void* v, int32_t n_pos) {
 }
 
 // The controller loop of cpu_speculative_generate (src/cpu_speculative.cpp:
-// 118-155), continuing from an existing target state: emit the seed (eos /
+// 89-137), continuing from an existing target state: emit the seed (eos /
 // token_limit stops), budget = min(max_draft, max_new-|ids|, remaining-1), draft,
 // append seed+drafts, accept while the draft equals the greedy choice of the
 // previous row, the terminating token is emitted but not kept, logical rewind.

@@ -10,8 +10,8 @@
  *   lm_head             src/qwen3_decoder.cpp:174-205
  *   causal context      src/cpu_context.cpp:13-32
  *   softmax op order    src/cpu_softmax.cpp:27-36
- *   controller/policy   src/cpu_speculative.cpp:37-68, 86-165
- *   embedding rows      src/generate.cpp:33-66
+ *   controller/policy   src/cpu_speculative.cpp:19-50, 68-147
+ *   embedding rows      src/generate.cpp:33-111
  * Every function below names the reference lines it follows in oracle.cpp.
  */
 #ifndef MTG_ORACLE_H
@@ -72,6 +72,7 @@ int orc_generate_from(orc_model* m, int32_t first_seed, const int32_t* prior_ids
 
 /* primitives, exposed for unit tests */
 uint16_t orc_f32_to_f16(float f);
+float orc_exp(float x); /* the exp of attention and SiLU */
 float orc_f16_to_f32(uint16_t h);
 void orc_quantize_q8_0_act(const float* x, int64_t k, void* blocks);
 void orc_quantize_q8_k_act(const float* x, int64_t k, void* blocks);

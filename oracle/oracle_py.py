@@ -49,6 +49,7 @@ SIGNATURES = {
                                     c_float, c_int32, c_void_p, c_void_p, c_void_p,
                                     POINTER(c_int32), POINTER(mtg.GenStats)]),
     "orc_f32_to_f16": (c_uint16, [c_float]),
+    "orc_exp": (c_float, [c_float]),
     "orc_f16_to_f32": (c_float, [c_uint16]),
     "orc_quantize_q8_0_act": (None, [c_void_p, c_int64, c_void_p]),
     "orc_quantize_q8_k_act": (None, [c_void_p, c_int64, c_void_p]),

@@ -146,3 +146,25 @@ def test_step_kernel_matches_per_op_kernels():
         keep = int(rng.integers(1, T + 1))
         a.rewind(a.past_len - T + keep)
         b.rewind(b.past_len - T + keep)
+
+
+@pytest.mark.parametrize("penalty", [1.0, 1.25])
+def test_generated_token_stream_matches_oracle(penalty):
+    """The controller on the device decoder and on the oracle, fed the same
+    drafter (n-gram over prompt ++ ids, completed from a periodic stream), emit
+    the same ids with the same counters, step for step."""
+    print("token stream parity: penalty %.2f" % penalty, flush=True)
+    model, orc, dec, rng = _setup(2, 48, vocab=4096, max_seq=512, seed=7)
+    prompt = rng.integers(0, 4096, 20).astype(np.int32)
+    stream = rng.integers(0, 4096, 37).astype(np.int32)
+    fn, user, _keep = mtg.stream_drafter(prompt, stream)
+    first = int(rng.integers(0, 4096))
+    ids0, st0 = orc.generate_from(first, 200, max_steps=24, penalty=penalty, max_draft=7, draft=fn,
+                                  user=user)
+    ids1, st1 = dec.generate_from(first, 200, max_steps=24, penalty=penalty, max_draft=7, draft=fn,
+                                  user=user)
+    assert ids1.tolist() == ids0.tolist()
+    for k in ("target_calls", "drafted_calls", "proposed", "accepted", "target_input_tokens",
+              "rewinds", "next_seed"):
+        assert getattr(st1, k) == getattr(st0, k), k
+    assert dec.past_len == orc.past_len
