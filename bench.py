@@ -10,7 +10,15 @@ over all rows, on-device greedy choice and acceptance) plus the host controller.
 
 Prints one JSON line (metric, value = accepted tokens/s, ms_per_step, roofline of
 the dominant kernel, cpu_baseline = the oracle on the host cores).
+
+roofline: the step's device work (one persistent kernel per verify step) is timed
+with HIP events on the library's stream over the timed region; achieved = the
+algorithmic bytes of a step (q8_0 weights + KV read of past + T rows + KV write of
+T rows) / the mean event time. traffic: HBM bytes per launch from rocprofv3
+FETCH_SIZE + WRITE_SIZE (profiles/traffic.json), reported only when that file was
+measured on the current kernel sources, else null.
 """
+import hashlib
 import argparse
 import json
 import os
@@ -26,6 +34,31 @@ import mtg  # noqa: E402
 
 METRIC = "verify-step µs + accepted tok/s (q8_0, K=8, ctx 1.6k); % of HBM peak"
 HBM_PEAK_GBS = 8000.0
+KERNEL = "k_step"  # the dominant kernel: the whole verify step
+CSRC = os.path.join(ROOT, "moss-transcribe.cpp_amd", "csrc")
+TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def source_hash():
+    """Hash of the kernel and runtime sources, to tie a profile to a build."""
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(CSRC)):
+        if name.endswith((".hip", ".cpp", ".hpp")):
+            h.update(name.encode())
+            h.update(open(os.path.join(CSRC, name), "rb").read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(config):
+    """HBM bytes per step launch from the committed rocprofv3 counter summary,
+    if it was measured on these sources and this workload."""
+    try:
+        t = json.load(open(TRAFFIC))
+    except (OSError, ValueError):
+        return None
+    if t.get("source_hash") != source_hash() or t.get("config") != config:
+        return None
+    return t.get("traffic_bytes_per_launch")
 
 # (weight type, kv type, audio blocks, text ids, K rows, decode steps)
 CONFIGS = {
@@ -111,6 +144,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--exec", choices=["step", "graph", "eager"], default="step",
                     help="persistent step kernel, per-op kernels from a graph, or eager per-op")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="after the run, copy a buffer of this size 5 times (device to device) "
+                         "so that a counter profile of the same command can calibrate FETCH_SIZE "
+                         "and WRITE_SIZE against a known byte count")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box here has one MI355X, and the verify path "
@@ -139,16 +176,23 @@ def main():
     import ctypes
     hip = ctypes.CDLL("libamdhip64.so")
     hip.hipDeviceSynchronize()
+    dec.launch_timing(True)
     t0 = time.perf_counter()
     ids, st = dec.generate_from(st_w.next_seed, 1 << 20, max_steps=steps, max_draft=cfg["K"] - 1,
                                 draft=fn, user=user, prior=ids_w)
     hip.hipDeviceSynchronize()
     elapsed = time.perf_counter() - t0
+    dev_ms, launches, past_sum, rows_sum = dec.launch_timing_read()
+    dec.launch_timing(False)
     n_steps = int(st.target_calls)
     tokens = len(ids)
     ms_step = 1e3 * elapsed / max(n_steps, 1)
-    ctx_mean = ctx_start + (dec.past_len - ctx_start) / 2.0
-    step_bytes = weight_bytes(hp, cfg["wtype"]) + (ctx_mean + 2 * cfg["K"]) * kv_bytes_per_pos(hp, cfg["kv"])
+    kvpos = kv_bytes_per_pos(hp, cfg["kv"])
+    # algorithmic bytes of one launch: weights + KV read of past + T rows + KV write of T rows
+    bytes_launch = weight_bytes(hp, cfg["wtype"]) + (past_sum + 2 * rows_sum) / max(launches, 1) * kvpos
+    launch_s = dev_ms * 1e-3 / max(launches, 1)
+    achieved = bytes_launch / launch_s / 1e9
+    traffic = measured_traffic(args.config) if args.layers == 28 and args.exec == "step" else None
     out = {
         "metric": METRIC,
         "value": tokens / elapsed,
@@ -160,21 +204,40 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q8_0 int8 dots, f32 accumulate" if cfg["wtype"] == mtg.TYPE_Q8_0 else "f16/q4_K",
-        "data": "synthetic (seeded random weights and prompt rows)",
-        "config": {"workload": "config %d: Qwen3-0.6B-shaped verify, %d layers, K=%d, prompt %d rows, "
-                               "%s KV" % (args.config, hp.n_layers, cfg["K"], n_prompt,
-                                          "f32" if cfg["kv"] == mtg.TYPE_F32 else "f16"),
+        "dtype": {mtg.TYPE_Q8_0: "q8_0 (int8 dots, f32 accumulate)", mtg.TYPE_F16: "f16",
+                  mtg.TYPE_Q4_K: "q4_K"}[cfg["wtype"]],
+        "data": "synthetic: seeded random weights, seeded audio-like prompt rows and draft stream",
+        "config": {"workload": "Qwen3-0.6B-shaped verify step, %d layers, K=%d rows, %s weights, "
+                               "%s KV, %d-row prompt (%d audio + %d text), %d greedy steps"
+                               % (hp.n_layers, cfg["K"], {mtg.TYPE_Q8_0: "q8_0", mtg.TYPE_F16: "f16",
+                                                          mtg.TYPE_Q4_K: "q4_K"}[cfg["wtype"]],
+                                  "f32" if cfg["kv"] == mtg.TYPE_F32 else "f16", n_prompt,
+                                  cfg["blocks"] * AUDIO_ROWS, cfg["text"], n_steps),
                    "verify_rows": cfg["K"], "context_start": ctx_start, "context_end": dec.past_len,
                    "accepted_per_step": st.accepted / max(n_steps, 1),
                    "tokens": tokens, "exec": args.exec},
-        "step_us": 1e3 * ms_step,
-        "step_bytes": step_bytes,
-        "step_hbm_fraction": step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "verify_step_us": 1e3 * dev_ms / max(launches, 1),
+        "host_step_us": 1e3 * ms_step,
+        "step_bytes": bytes_launch,
+        "roofline": {"bound": "hbm", "kernel": KERNEL if args.exec == "step" else "per-op kernels",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic,
+                     "launch_us": launch_s * 1e6, "launches": launches},
+        "source_hash": source_hash(),
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(model, dec, cfg, st.next_seed,
                                            np.concatenate([ids_w, ids]), drafter, args.cpu_seconds)
+    if args.copy_probe_mib > 0:
+        import torch
+        n = args.copy_probe_mib << 18  # float32 elements
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        out["copy_probe_bytes"] = n * 4
     print(json.dumps(out))
 
 

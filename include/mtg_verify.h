@@ -253,6 +253,15 @@ int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes);
 int mtg_step_profile(mtg_ctx* ctx, int32_t enable);
 int32_t mtg_step_profile_read(mtg_ctx* ctx, uint64_t* marks, int32_t n);
 
+/* Launch timing: when enabled, every verify / append step's device work is
+ * bracketed by two HIP events on the context's stream; the read-out gives the
+ * summed event time, the number of timed steps and the sums of their past_len
+ * and row counts (so a caller can divide the algorithmic bytes per step by the
+ * measured time). Enabling resets the sums. */
+int mtg_launch_timing(mtg_ctx* ctx, int32_t enable);
+int mtg_launch_timing_read(const mtg_ctx* ctx, double* total_ms, int64_t* launches,
+                           int64_t* past_sum, int64_t* rows_sum);
+
 /* Host policy functions (reference: cpu_ngram_draft, cpu_greedy_choice). */
 int32_t mtg_ngram_draft(const int32_t* history, int32_t n, int32_t maximum, int32_t* out);
 int32_t mtg_greedy_choice(const float* raw, int32_t n, const int32_t* history, int32_t n_history,
@@ -265,6 +274,9 @@ typedef struct mtg_q8_packed mtg_q8_packed;
  * Returns MTG_ERR_UNSUPPORTED for other shapes (the caller keeps its own path). */
 int mtg_q8_pack(const void* blocks, int32_t k, int32_t n, mtg_q8_packed** out);
 void mtg_q8_free(mtg_q8_packed* p);
+/* Download the tiles and restore the n rows of q8_0 blocks they were packed from
+ * (reference: PackedQ8::round_trip_exact, src/cpu_q8.hpp:17). */
+int mtg_q8_unpack(const mtg_q8_packed* p, void* blocks);
 /* y_dev[t][n] = q8_0 dot of the packed rows with x_dev[t][:] (T x K floats,
  * quantized to q8_0 per 32-block on the device), T in 1..MTG_MAX_BATCH. */
 int mtg_q8_mul_mat_dev(const mtg_q8_packed* w, const float* x_dev, int32_t T, float* y_dev);

@@ -19,7 +19,7 @@ ORACLE_DIR = os.path.join(ROOT, "oracle")
 ORACLE_LIB = os.path.join(ORACLE_DIR, "liboracle.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["kernels.hip", "step_kernel.hip", "runtime.cpp", "capi.cpp", "synth.cpp"]
+SOURCES = ["kernels.hip", "step_kernel.hip", "runtime.cpp", "capi.cpp", "synth.cpp", "reference_api.cpp"]
 # -ffp-contract=off: elementwise ops round like the reference's scalar code;
 # fused multiply-adds are written explicitly (fmaf) where they are wanted.
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-pass-failed", "-Wno-unused-parameter", "-Wno-unused-value", "-Wno-unused-result",
@@ -59,6 +59,26 @@ def build_lib(verbose=False):
     return LIB
 
 
+CPP_TESTS = os.path.join(ROOT, "tests", "cpp")
+
+
+def build_cpp_tests():
+    """The C++ test drivers of the reference-named interface (tests/cpp), linked
+    against libmtg.so; binaries go to tests/cpp/bin (git-ignored)."""
+    out_dir = os.path.join(CPP_TESTS, "bin")
+    os.makedirs(out_dir, exist_ok=True)
+    outs = []
+    for name in sorted(os.listdir(CPP_TESTS)):
+        if not name.endswith(".cpp"):
+            continue
+        exe = os.path.join(out_dir, name[:-4])
+        _run(["g++", "-std=c++17", "-O1", "-Wall", "-I", os.path.join(ROOT, "include"),
+              os.path.join(CPP_TESTS, name), "-o", exe, "-L", PKG, "-lmtg",
+              "-Wl,-rpath," + PKG, "-Wl,-rpath-link,/opt/rocm/lib"])
+        outs.append(exe)
+    return outs
+
+
 def build_oracle():
     _run(["make", "-s", "-C", ORACLE_DIR, "liboracle.so"])
     return ORACLE_LIB
@@ -67,6 +87,7 @@ def build_oracle():
 def build_all(verbose=False):
     build_lib(verbose)
     build_oracle()
+    build_cpp_tests()
 
 
 if __name__ == "__main__":

@@ -79,6 +79,30 @@ int mtg_step_profile(mtg_ctx* ctx, int32_t enable) {
              : MTG_ERR_DEVICE;
 }
 
+int mtg_launch_timing(mtg_ctx* ctx, int32_t enable) {
+  if (!ctx) return MTG_ERR_INVALID;
+  Ctx& c = ctx->impl;
+  if (enable && !c.ev_start) {
+    if (int rc = c.check(hipEventCreate(&c.ev_start), "event")) return rc;
+    if (int rc = c.check(hipEventCreate(&c.ev_stop), "event")) return rc;
+  }
+  c.timing = enable != 0;
+  c.timing_ms = 0.0;
+  c.timing_launches = c.timing_past = c.timing_rows = 0;
+  return MTG_OK;
+}
+
+int mtg_launch_timing_read(const mtg_ctx* ctx, double* total_ms, int64_t* launches,
+                           int64_t* past_sum, int64_t* rows_sum) {
+  if (!ctx || !total_ms || !launches || !past_sum || !rows_sum) return MTG_ERR_INVALID;
+  const Ctx& c = ctx->impl;
+  *total_ms = c.timing_ms;
+  *launches = c.timing_launches;
+  *past_sum = c.timing_past;
+  *rows_sum = c.timing_rows;
+  return MTG_OK;
+}
+
 int32_t mtg_step_profile_read(mtg_ctx* ctx, uint64_t* marks, int32_t n) {
   if (!ctx || !marks || !ctx->impl.timing_dev) return 0;
   const int count = std::min<int>(n, std::min<int>(1024, mtg::step_barriers(ctx->impl.hp.n_layers, mtg::kStepVerify) + 2));
@@ -412,6 +436,31 @@ int mtg_q8_pack(const void* blocks, int32_t k, int32_t n, mtg_q8_packed** out) {
     return MTG_ERR_DEVICE;
   }
   *out = p;
+  return MTG_OK;
+}
+
+// Inverse of the re-tiling: download the tiles and restore n rows of ggml
+// block_q8_0 (lets a caller check that packing kept every byte).
+int mtg_q8_unpack(const mtg_q8_packed* p, void* blocks) {
+  if (!p || !blocks) return MTG_ERR_INVALID;
+  const int bps = p->k / 64, nb = p->k / 32;
+  const size_t units = (size_t)(p->n / 16) * bps;
+  std::vector<uint8_t> tiles(units * mtg::kUnitBytes);
+  if (hipMemcpy(tiles.data(), p->tiles, tiles.size(), hipMemcpyDeviceToHost) != hipSuccess)
+    return MTG_ERR_DEVICE;
+  uint8_t* out = (uint8_t*)blocks;
+  for (size_t u = 0; u < units; ++u) {
+    const int tile = (int)(u / bps), bp = (int)(u % bps);
+    const uint8_t* unit = tiles.data() + u * mtg::kUnitBytes;
+    for (int lane = 0; lane < 64; ++lane) {
+      const int row = tile * 16 + (lane & 15), g = lane >> 4, block = 2 * bp + (g >> 1);
+      std::memcpy(out + ((size_t)row * nb + block) * 34 + 2 + (g & 1) * 16, unit + lane * 16, 16);
+    }
+    for (int par = 0; par < 2; ++par)
+      for (int r = 0; r < 16; ++r)
+        std::memcpy(out + ((size_t)(tile * 16 + r) * nb + 2 * bp + par) * 34,
+                    unit + 1024 + (par * 16 + r) * 2, 2);
+  }
   return MTG_OK;
 }
 

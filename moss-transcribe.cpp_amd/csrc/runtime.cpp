@@ -30,6 +30,8 @@ Ctx::~Ctx() {
   for (auto& g : graphs)
     if (g.exec) hipGraphExecDestroy(g.exec);
   for (void* p : allocations) hipFree(p);
+  if (ev_start) hipEventDestroy(ev_start);
+  if (ev_stop) hipEventDestroy(ev_stop);
   if (desc_host) hipHostFree(desc_host);
   if (result_host) hipHostFree(result_host);
   if (stream) hipStreamDestroy(stream);
@@ -324,6 +326,8 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
                  "step descriptor");
   if (rc) return rc;
   const bool step_mode = mode == kModeVerify || mode == kModeVerifyPenalty || mode == kModeAppend;
+  const bool timed = timing && mode != kModeLogits;
+  if (timed && (rc = check(hipEventRecord(ev_start, stream), "timing event"))) return rc;
   if (exec == kExecStep && step_ok && step_mode) {
     const int smode = mode == kModeAppend ? kStepAppend : kStepVerify;
     if ((rc = check(launch_step(stream, G, nwg, params_dev, desc_dev, epoch, smode, bps_max),
@@ -347,6 +351,7 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
     enqueue(G, mode);
     if ((rc = check(hipGetLastError(), "kernel launch"))) return rc;
   }
+  if (timed && (rc = check(hipEventRecord(ev_stop, stream), "timing event"))) return rc;
   if ((rc = check(hipMemcpyAsync(result_host, result_dev, sizeof(StepResult), hipMemcpyDeviceToHost,
                                  stream), "result")))
     return rc;
@@ -359,6 +364,14 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
                                  hipMemcpyDeviceToHost, stream), "logits")))
     return rc;
   if ((rc = check(hipStreamSynchronize(stream), "step"))) return rc;
+  if (timed) {
+    float ms = 0.0f;
+    if ((rc = check(hipEventElapsedTime(&ms, ev_start, ev_stop), "timing"))) return rc;
+    timing_ms += ms;
+    ++timing_launches;
+    timing_past += desc_host->past;
+    timing_rows += T;
+  }
   if (result_host->err) {
     // a bounded barrier wait ran out: every workgroup left the kernel
     (void)hipMemset(&result_dev->err, 0, sizeof(int32_t));

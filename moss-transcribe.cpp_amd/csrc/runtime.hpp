@@ -38,6 +38,11 @@ struct Ctx {
   StepParams* params_dev = nullptr;
   StepParams params_host{};
   uint64_t* timing_dev = nullptr;  // step-kernel phase clock marks (profiling)
+  // launch timing: HIP events around every step's device work on `stream`
+  bool timing = false;
+  hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+  double timing_ms = 0.0;
+  int64_t timing_launches = 0, timing_past = 0, timing_rows = 0;
   std::string error;
   hipStream_t stream = nullptr;
   std::vector<void*> allocations;

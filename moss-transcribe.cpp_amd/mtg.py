@@ -98,11 +98,15 @@ SIGNATURES = {
     "mtg_exec_mode": (c_int32, [c_void_p]),
     "mtg_debug_copy": (c_int32, [c_void_p, c_int32, c_void_p, ctypes.c_size_t]),
     "mtg_step_profile": (c_int32, [c_void_p, c_int32]),
+    "mtg_launch_timing": (c_int32, [c_void_p, c_int32]),
+    "mtg_launch_timing_read": (c_int32, [c_void_p, POINTER(c_double), POINTER(c_int64),
+                                         POINTER(c_int64), POINTER(c_int64)]),
     "mtg_step_profile_read": (c_int32, [c_void_p, c_void_p, c_int32]),
     "mtg_ngram_draft": (c_int32, [c_void_p, c_int32, c_int32, c_void_p]),
     "mtg_greedy_choice": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_float]),
     "mtg_q8_pack": (c_int32, [c_void_p, c_int32, c_int32, POINTER(c_void_p)]),
     "mtg_q8_free": (None, [c_void_p]),
+    "mtg_q8_unpack": (c_int32, [c_void_p, c_void_p]),
     "mtg_q8_mul_mat_dev": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
     "mtg_causal_context_dev": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
                                          c_int32, c_void_p]),
@@ -245,6 +249,16 @@ class Decoder:
 
     def step_profile(self, on):
         self._chk(lib().mtg_step_profile(self.ctx, 1 if on else 0))
+
+    def launch_timing(self, on):
+        self._chk(lib().mtg_launch_timing(self.ctx, 1 if on else 0))
+
+    def launch_timing_read(self):
+        """(total ms, launches, sum of past_len, sum of rows) of the timed steps."""
+        ms, n, ps, rs = c_double(), c_int64(), c_int64(), c_int64()
+        self._chk(lib().mtg_launch_timing_read(self.ctx, ctypes.byref(ms), ctypes.byref(n),
+                                               ctypes.byref(ps), ctypes.byref(rs)))
+        return ms.value, n.value, ps.value, rs.value
 
     def step_marks(self):
         out = np.zeros(1024, np.uint64)

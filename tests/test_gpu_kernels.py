@@ -132,3 +132,19 @@ def test_causal_context_rejects_unsupported_layouts():
     assert L.mtg_causal_context_dev(z, z, 128, 8, 16, 1, 10, z) == mtg.ERR_UNSUPPORTED  # one query
     assert L.mtg_causal_context_dev(z, z, 128, 8, 12, 4, 10, z) == mtg.ERR_UNSUPPORTED  # heads % kv
     assert L.mtg_causal_context_dev(z, z, 128, 8, 16, 4, 4, z) == mtg.ERR_UNSUPPORTED   # no prefix
+
+
+@pytest.mark.parametrize("k,n", [(1024, 64), (3072, 1024), (1024, 151936)])
+def test_q8_pack_is_lossless(k, n):
+    """PackedQ8::round_trip_exact (src/cpu_q8.hpp:17): the tiles hold exactly the
+    q8_0 blocks they were packed from."""
+    rng = np.random.default_rng(k + n)
+    raw = _q8_weights(n, k, "normal" if n < 100000 else "extreme", rng)
+    packed = ctypes.c_void_p()
+    assert mtg.lib().mtg_q8_pack(mtg.ptr(raw), k, n, ctypes.byref(packed)) == 0
+    back = np.zeros_like(raw)
+    rc = mtg.lib().mtg_q8_unpack(packed, mtg.ptr(back))
+    mtg.lib().mtg_q8_free(packed)
+    assert rc == 0
+    assert np.array_equal(back, raw)
+    assert mtg.lib().mtg_q8_pack(mtg.ptr(raw), 1000, 64, ctypes.byref(packed)) == mtg.ERR_UNSUPPORTED
