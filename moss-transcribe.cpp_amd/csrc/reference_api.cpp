@@ -6,6 +6,7 @@
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <exception>
 #include <stdexcept>
 #include <string>
 
@@ -95,12 +96,16 @@ struct HookedTarget {
   std::vector<float> raw;     // logits of the last kept row (for `committed`)
   std::vector<float> logits;  // all rows of the last verify (only with `committed`)
   bool bad_draft = false;
+  // An exception thrown by a hook is held here, the loop is stopped at the next
+  // callback that can return an error, and cpu_speculative_generate rethrows it.
+  std::exception_ptr error;
 };
 
 int32_t hooked_verify(void* self, const int32_t* tokens, int32_t T, const int32_t* history,
                       int32_t n_history, float penalty, int32_t* choice, int32_t* n_match) {
   HookedTarget& h = *(HookedTarget*)self;
-  // apply the controller's logical rewind of the previous step to the context
+  if (h.error) return MTG_ERR_STATE;
+  // the controller's logical rewind reaches the context at commit; keep in step
   if (*h.past != h.dec->past_len() && !h.dec->rewind(*h.past)) return MTG_ERR_STATE;
   h.before = *h.past;
   const bool want_hidden = h.hooks && h.hooks->appended;
@@ -110,13 +115,26 @@ int32_t hooked_verify(void* self, const int32_t* tokens, int32_t T, const int32_
   const int rc = mtg_verify(h.dec->context(), tokens, T, history, n_history, penalty, choice,
                             n_match, want_hidden ? hid.data() : nullptr,
                             want_logits ? h.logits.data() : nullptr);
-  if (rc == MTG_OK && want_hidden) h.hooks->appended(std::vector<int32_t>(tokens, tokens + T), hid);
+  if (rc == MTG_OK && want_hidden) {
+    try {
+      h.hooks->appended(std::vector<int32_t>(tokens, tokens + T), hid);
+    } catch (...) {
+      h.error = std::current_exception();
+      return MTG_ERR_STATE;
+    }
+  }
   return rc;
 }
 
 int32_t hooked_draft(void* user, const int32_t* ids, int32_t n_ids, int32_t budget, int32_t* out) {
   HookedTarget& h = *(HookedTarget*)user;
-  auto proposal = h.hooks->draft(std::vector<int32_t>(ids, ids + n_ids), budget);
+  std::vector<int32_t> proposal;
+  try {
+    proposal = h.hooks->draft(std::vector<int32_t>(ids, ids + n_ids), budget);
+  } catch (...) {
+    h.error = std::current_exception();
+    return 0;
+  }
   if (proposal.size() > (size_t)budget) proposal.resize((size_t)budget);
   for (int32_t id : proposal)
     if (id < 0 || id >= h.vocab) h.bad_draft = true;
@@ -126,12 +144,18 @@ int32_t hooked_draft(void* user, const int32_t* ids, int32_t n_ids, int32_t budg
 
 void hooked_commit(void* user, const int32_t* ids, int32_t n_ids, int32_t past_len, int32_t stopped) {
   HookedTarget& h = *(HookedTarget*)user;
-  if (!h.hooks || !h.hooks->committed) return;
+  // the logical rewind of this step (src/cpu_speculative.cpp:131-135), before the hook
+  if (past_len < h.dec->past_len()) h.dec->rewind(past_len);
+  if (!h.hooks || !h.hooks->committed || h.error) return;
   const int row = past_len - h.before - 1;  // the last kept row of this step
   if (!h.logits.empty() && row >= 0 && (size_t)(row + 1) * h.vocab <= h.logits.size())
     h.raw.assign(h.logits.begin() + (size_t)row * h.vocab,
                  h.logits.begin() + (size_t)(row + 1) * h.vocab);
-  h.hooks->committed(*h.dec, std::vector<int32_t>(ids, ids + n_ids), h.raw, stopped != 0);
+  try {
+    h.hooks->committed(*h.dec, std::vector<int32_t>(ids, ids + n_ids), h.raw, stopped != 0);
+  } catch (...) {
+    h.error = std::current_exception();
+  }
 }
 }  // namespace
 
@@ -166,6 +190,7 @@ std::vector<int32_t> cpu_speculative_generate(GpuDecoder& dec, const std::vector
                                      hooked_commit, &h, ids.data(), &n, nullptr);
   // the controller moved `past`; mirror it into the context (a logical rewind)
   if (past <= dec.past_len()) dec.rewind(past);
+  if (h.error) std::rethrow_exception(h.error);
   if (rc == MTG_ERR_INVALID && h.bad_draft) throw std::runtime_error("invalid draft token");
   ids.resize((size_t)std::max(0, n));
   return ids;
