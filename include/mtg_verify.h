@@ -232,10 +232,11 @@ typedef struct mtg_stream_drafter {
 int32_t mtg_stream_draft(void* user, const int32_t* ids, int32_t n_ids, int32_t budget,
                          int32_t* out);
 
-/* How a step runs on the device. MTG_EXEC_STEP_KERNEL (default where the shape
- * allows): one persistent kernel per step. MTG_EXEC_GRAPH: the per-op kernels,
- * replayed from a captured HIP graph. MTG_EXEC_EAGER: the per-op kernels launched
- * one by one (profiling). All three produce the same results. */
+/* How a step runs on the device. MTG_EXEC_STEP_KERNEL (the default for the
+ * Qwen3-0.6B shape on a device with at least 256 CUs): one persistent dataflow
+ * kernel per step. MTG_EXEC_GRAPH (the default otherwise): the per-op kernels,
+ * replayed from a captured HIP graph. MTG_EXEC_EAGER: the per-op kernels
+ * launched one by one (profiling). All modes produce the same results. */
 enum { MTG_EXEC_STEP_KERNEL = 0, MTG_EXEC_GRAPH = 1, MTG_EXEC_EAGER = 2 };
 int mtg_set_exec_mode(mtg_ctx* ctx, int32_t mode);
 int32_t mtg_exec_mode(const mtg_ctx* ctx);
@@ -247,9 +248,11 @@ enum { MTG_DEBUG_X = 0, MTG_DEBUG_QKV = 1, MTG_DEBUG_O = 2, MTG_DEBUG_ACT = 3, M
 int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes);
 
 /* Profiling of the persistent step kernel: when enabled, workgroup 0 records a
- * 100 MHz device clock at the start of the step and after every grid barrier
- * (1 + 6 per layer + 1 for the lm_head), plus the end; read the marks of the
- * last step with mtg_step_profile_read (returns how many were copied). */
+ * 100 MHz device clock into up to 1024 slots: 0 at the start; for layer l at
+ * 3 + 12 l + {0, 1}: QKV inputs ready / QKV published, {2, 3}: attention,
+ * {4, 5}: o-proj, {6, 7}: down (when workgroup 0 has those roles); at 3 + 12 L
+ * the lm_head start, + 1 its end, + 2 / + 3 the acceptance (verify steps).
+ * mtg_step_profile_read copies the slots of the last step (returns the count). */
 int mtg_step_profile(mtg_ctx* ctx, int32_t enable);
 int32_t mtg_step_profile_read(mtg_ctx* ctx, uint64_t* marks, int32_t n);
 

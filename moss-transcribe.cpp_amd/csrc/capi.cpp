@@ -70,7 +70,7 @@ int mtg_step_profile(mtg_ctx* ctx, int32_t enable) {
   Ctx& c = ctx->impl;
   if (!c.step_ok) return c.fail(MTG_ERR_UNSUPPORTED, "no step kernel");
   if (enable && !c.timing_dev) {
-    c.timing_dev = (uint64_t*)c.dalloc(sizeof(uint64_t) * 1024, true);
+    c.timing_dev = (uint64_t*)c.dalloc(sizeof(uint64_t) * 8192, true);
     if (!c.timing_dev) return c.fail(MTG_ERR_NOMEM, "timing buffer");
   }
   c.params_host.timing = enable ? c.timing_dev : nullptr;
@@ -105,7 +105,7 @@ int mtg_launch_timing_read(const mtg_ctx* ctx, double* total_ms, int64_t* launch
 
 int32_t mtg_step_profile_read(mtg_ctx* ctx, uint64_t* marks, int32_t n) {
   if (!ctx || !marks || !ctx->impl.timing_dev) return 0;
-  const int count = std::min<int>(n, std::min<int>(1024, mtg::step_barriers(ctx->impl.hp.n_layers, mtg::kStepVerify) + 2));
+  const int count = std::min<int>(n, 8192);
   if (hipMemcpy(marks, ctx->impl.timing_dev, sizeof(uint64_t) * count, hipMemcpyDeviceToHost) != hipSuccess)
     return 0;
   return count;

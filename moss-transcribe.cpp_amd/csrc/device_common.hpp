@@ -78,14 +78,65 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
   return __half2float(__ushort_as_half(h));
 }
 
+// ------------------------------------------------------ lane exchanges ---
+// lane_xor<O>(v): the value of lane (lane ^ O) of a 64-lane wave, with VALU
+// lane moves instead of LDS permutes: DPP quad_perm (O = 1, 2), two bank-masked
+// row rotations (O = 4: lanes 0-3 / 8-11 of a row take lane + 4, the others
+// lane - 4), row_ror:8 (O = 8), and the gfx950 row / half-wave swaps (O = 16, 32:
+// each half keeps the value that crossed over).
+template <int O>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  const int x = (int)v;
+  if constexpr (O == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (O == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (O == 4) {
+    const int t = __builtin_amdgcn_update_dpp(x, x, 0x12C, 0xF, 0x5, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(t, x, 0x124, 0xF, 0xA, false);
+  } else if constexpr (O == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);
+  } else if constexpr (O == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? r[0] : r[1];
+  } else {
+    static_assert(O == 32, "lane_xor: 1, 2, 4, 8, 16 or 32");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? r[0] : r[1];
+  }
+}
+template <int O>
+__device__ __forceinline__ float lane_xor_f(float v) {
+  return __uint_as_float(lane_xor<O>(__float_as_uint(v)));
+}
+template <int O>
+__device__ __forceinline__ uint64_t lane_xor_u64(uint64_t v) {
+  return ((uint64_t)lane_xor<O>((uint32_t)(v >> 32)) << 32) | lane_xor<O>((uint32_t)v);
+}
+template <int O>
+__device__ __forceinline__ double lane_xor_d(double v) {
+  return __longlong_as_double((long long)lane_xor_u64<O>((uint64_t)__double_as_longlong(v)));
+}
+
+// xor butterfly 32, 16, 8, 4, 2, 1 (the canonical order of every wave sum)
 __device__ __forceinline__ double wave_sum_d(double v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v += lane_xor_d<32>(v);
+  v += lane_xor_d<16>(v);
+  v += lane_xor_d<8>(v);
+  v += lane_xor_d<4>(v);
+  v += lane_xor_d<2>(v);
+  v += lane_xor_d<1>(v);
   return v;
 }
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
-  return ((uint64_t)hi << 32) | lo;
+  switch (o) {
+    case 1: return lane_xor_u64<1>(v);
+    case 2: return lane_xor_u64<2>(v);
+    case 4: return lane_xor_u64<4>(v);
+    case 8: return lane_xor_u64<8>(v);
+    case 16: return lane_xor_u64<16>(v);
+    default: return lane_xor_u64<32>(v);
+  }
 }
 
 // q8_0 activation conversion of one 32-element block held by 8 consecutive lanes
@@ -93,9 +144,9 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
 // Returns the f32 value of the stored f16 scale.
 __device__ __forceinline__ float quant_block8(const float v[4], int8_t q[4]) {
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+  amax = fmaxf(amax, lane_xor_f<1>(amax));
+  amax = fmaxf(amax, lane_xor_f<2>(amax));
+  amax = fmaxf(amax, lane_xor_f<4>(amax));
   const float d = __fdiv_rn(amax, 127.0f);
   const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
   for (int e = 0; e < 4; ++e) q[e] = (int8_t)rintf(__fmul_rn(v[e], id));
@@ -170,7 +221,7 @@ __device__ __forceinline__ void tile_accumulate_canonical(const uint8_t* __restr
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float v = __fadd_rn(__fadd_rn(__fadd_rn(part[0][cg][r], part[1][cg][r]), part[2][cg][r]), part[3][cg][r]);
-      acc[cg][r] = __fadd_rn(v, __shfl_xor(v, 8, 64));
+      acc[cg][r] = __fadd_rn(v, lane_xor_f<8>(v));
     }
 }
 
@@ -225,11 +276,30 @@ __device__ __forceinline__ void st_f(float* p, float v) {
 }
 
 __device__ __forceinline__ float wave_max_f(float v) {
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  v = fmaxf(v, lane_xor_f<32>(v));
+  v = fmaxf(v, lane_xor_f<16>(v));
+  v = fmaxf(v, lane_xor_f<8>(v));
+  v = fmaxf(v, lane_xor_f<4>(v));
+  v = fmaxf(v, lane_xor_f<2>(v));
+  v = fmaxf(v, lane_xor_f<1>(v));
   return v;
 }
 __device__ __forceinline__ float wave_sum_f(float v) {
-  for (int o = 32; o > 0; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o, 64));
+  v = __fadd_rn(v, lane_xor_f<32>(v));
+  v = __fadd_rn(v, lane_xor_f<16>(v));
+  v = __fadd_rn(v, lane_xor_f<8>(v));
+  v = __fadd_rn(v, lane_xor_f<4>(v));
+  v = __fadd_rn(v, lane_xor_f<2>(v));
+  v = __fadd_rn(v, lane_xor_f<1>(v));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, lane_xor<32>(v));
+  v = min(v, lane_xor<16>(v));
+  v = min(v, lane_xor<8>(v));
+  v = min(v, lane_xor<4>(v));
+  v = min(v, lane_xor<2>(v));
+  v = min(v, lane_xor<1>(v));
   return v;
 }
 __device__ __forceinline__ float f16_round(float v) { return __half2float(__float2half_rn(v)); }

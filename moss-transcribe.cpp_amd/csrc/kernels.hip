@@ -144,7 +144,7 @@ k_gemm(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w,
 #pragma unroll
     for (int cg = 0; cg < G; ++cg)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[m][cg][r] = __fadd_rn(acc[m][cg][r], __shfl_xor(acc[m][cg][r], 8, 64));
+      for (int r = 0; r < 4; ++r) acc[m][cg][r] = __fadd_rn(acc[m][cg][r], lane_xor_f<8>(acc[m][cg][r]));
   if ((lane & 15) >= 8) return;
 #pragma unroll
   for (int cg = 0; cg < G; ++cg) {

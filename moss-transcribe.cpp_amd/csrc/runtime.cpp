@@ -202,21 +202,14 @@ int Ctx::init_step_kernel() {
   if (rc) return rc;
   if ((rc = check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count")))
     return rc;
-  const int H = hp.hidden, QN = hp.n_heads * hp.head_dim, F = hp.intermediate, V = hp.vocab;
-  nwg = cus - cus % hp.n_kv_heads;
-  bps_max = std::max(std::max(H, QN), F) / kPairK;
-  // The kernel's phases are written for these shapes (whole 1024-element norm
-  // rows, 16-row tiles covering each matrix); other shapes use the per-op kernels.
-  if (H != 1024 || nwg < hp.n_kv_heads || (QN + 2 * hp.n_kv_heads * hp.head_dim) % 16 || QN % 1024 ||
-      F % 1024) {
-    exec = kExecGraph;
-    return MTG_OK;
-  }
-  if (prepare_step_kernels(bps_max) != hipSuccess) {
+  const int H = hp.hidden, F = hp.intermediate, V = hp.vocab;
+  if (!step_kernel_supported(H, hp.n_heads, hp.n_kv_heads, hp.head_dim, F, cus) ||
+      prepare_step_kernels() != hipSuccess) {
     (void)hipGetLastError();
-    exec = kExecGraph;
+    exec = kExecGraph;  // other shapes and smaller devices: the per-op kernels
     return MTG_OK;
   }
+  nwg = step_kernel_workgroups();
   std::vector<LayerDev> table(hp.n_layers);
   for (int l = 0; l < hp.n_layers; ++l) {
     const Layer& y = layers[l];
@@ -243,7 +236,6 @@ int Ctx::init_step_kernel() {
   P.L = hp.n_layers;
   P.max_seq = max_seq;
   P.kv_f16 = kv_type == MTG_TYPE_F16;
-  P.bps_max = bps_max;
   P.eps = hp.rms_eps;
   P.layers = table_dev;
   P.embd = embd;
@@ -261,13 +253,16 @@ int Ctx::init_step_kernel() {
   P.part_o = work.part_o;
   P.bitmap = bitmap;
   P.part_keys = (uint64_t*)dalloc((size_t)nwg * kMaxRows * 8, true);
+  P.oq = (int8_t*)dalloc((size_t)kMaxRows * hp.n_heads * hp.head_dim, true);
+  P.oqs = (float*)dalloc((size_t)kMaxRows * hp.n_heads * hp.head_dim / 32 * 4, true);
+  P.aq = (int8_t*)dalloc((size_t)kMaxRows * F, true);
+  P.aqs = (float*)dalloc((size_t)kMaxRows * F / 32 * 4, true);
   P.result = result_dev;
   P.flags = (uint32_t*)dalloc((size_t)nwg * 4, true);
-  P.release = (uint32_t*)dalloc(256, true);
   P.err = &result_dev->err;
   P.timing = nullptr;
   params_dev = (StepParams*)dalloc(sizeof(StepParams), false);
-  if (!table_dev || !P.part_ml || !P.part_o || !P.part_keys || !P.flags || !P.release || !params_dev)
+  if (!table_dev || !P.part_ml || !P.part_o || !P.part_keys || !P.flags || !P.oq || !P.oqs || !P.aq || !P.aqs || !params_dev)
     return fail(MTG_ERR_NOMEM, "step kernel buffers");
   if ((rc = check(hipMemcpy(table_dev, table.data(), table.size() * sizeof(LayerDev),
                             hipMemcpyHostToDevice), "layer table")) ||
@@ -329,11 +324,14 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
   const bool timed = timing && mode != kModeLogits;
   if (timed && (rc = check(hipEventRecord(ev_start, stream), "timing event"))) return rc;
   if (exec == kExecStep && step_ok && step_mode) {
+    if (epoch > 0xF0000000u) {  // progress words restart before they could wrap
+      if ((rc = check(hipMemsetAsync(params_host.flags, 0, (size_t)nwg * 4, stream), "flags"))) return rc;
+      epoch = 0;
+    }
     const int smode = mode == kModeAppend ? kStepAppend : kStepVerify;
-    if ((rc = check(launch_step(stream, G, nwg, params_dev, desc_dev, epoch, smode, bps_max),
-                    "step kernel launch")))
+    if ((rc = check(launch_step(stream, G, params_dev, desc_dev, epoch, smode), "step kernel launch")))
       return rc;
-    epoch += (uint32_t)step_barriers(hp.n_layers, smode);
+    epoch += step_progress_per_step(hp.n_layers);
   } else if (exec != kExecEager) {
     GraphSlot& slot = graphs[(G - 1) * kModes + mode];
     if (!slot.exec) {

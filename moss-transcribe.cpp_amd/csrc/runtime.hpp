@@ -32,8 +32,8 @@ struct Ctx {
   int max_seq = 0, kv_type = MTG_TYPE_F32, past = 0;
   int exec = kExecStep;
   // persistent step kernel
-  int nwg = 0, bps_max = 0;
-  bool step_ok = false;
+  int nwg = 0;
+  bool step_ok = false;  // the persistent step kernel is usable for this model / device
   uint32_t epoch = 0;
   StepParams* params_dev = nullptr;
   StepParams params_host{};

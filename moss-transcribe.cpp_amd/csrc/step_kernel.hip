@@ -1,30 +1,34 @@
-// step_kernel.hip - the whole verify step as one persistent gfx950 kernel.
+// step_kernel.hip - the Qwen3-0.6B verify step as one persistent dataflow kernel (gfx950).
 //
-// One workgroup per CU (cooperative launch, so all are co-resident). The step is a
-// fixed sequence of phases; between phases every workgroup meets at a grid
-// barrier made of per-workgroup arrival words (no atomics, no cache-wide
-// writeback/invalidate). Data produced and consumed inside the launch (residual
-// stream, qkv, attention partials, o, act, argmax keys) moves through
-// device-coherent loads and stores, so no L2 maintenance is needed; weights and
-// the KV prefix are read with ordinary cached loads.
+// One 256-thread workgroup per CU (cooperative launch of exactly 256 workgroups).
+// Every workgroup owns fixed roles per layer:
+//   QKV   tile w of the fused q|k|v matrix (256 tiles of 16 rows, K = 1024)
+//   ATTN  items (kv head, 64-key chunk), numbered head-major; item i runs on
+//         workgroup (i + 64) mod 256, so the 192 workgroups without o/down
+//         tiles take the first items
+//   MERGE (q head, row) items on workgroups 160..255; the merged rows leave as
+//         q8_0 codes + scales (the o-proj's activation quantization)
+//   OPROJ tile w < 64 (K = 2048) and DOWN tile w < 64 (K = 3072)
+//   GATEUP rows 32j..32j+31 of gate and up on workgroup 64 + j (j < 96); the
+//         SwiGLU rows leave as q8_0 blocks (the down-proj's quantization)
+// (src/qwen3.cpp:62-218.) Instead of grid barriers, each workgroup publishes a
+// monotone progress word: after its work in a phase it announces the last phase
+// before its next work as done, so a phase it takes no part in never delays
+// anyone. A phase waits until every progress word has reached the phase before
+// it; this orders every reuse of the exchange buffers (x, q|k|v, attention
+// partials, o, act) globally.
 //
-// Per layer (src/qwen3.cpp:62-218):
-//   QKV    every WG: RMSNorm(x)*attn_norm -> q8_0 panel in LDS; one 16-row tile of
-//          the fused q|k|v matrix per WG (256 tiles)
-//   ATTN   WG = (kv head, split): q/k RMSNorm + NEOX RoPE of its rows in LDS, the
-//          new K/V rows appended to the cache by the split holding `past`,
-//          split-KV f32-MFMA attention with online softmax -> partial (m, l, O)
-//   COMB   (head, row) items: merge the splits -> o
-//   OPROJ  q8_0(o) panel; 64 tiles; x += W_o o
-//   GATEUP RMSNorm(x)*ffn_norm panel; 192 tile pairs; act = silu(g) * u
-//   DOWN   q8_0(act) panel; 64 tiles; x += W_d act
-// then the final norm, the tied lm_head with fused argmax keys, and the
-// on-device acceptance (src/qwen3_decoder.cpp:129,174-205,
-// src/cpu_speculative.cpp:39-50,124-130).
+// Latency hiding: after publishing, a workgroup issues the loads of the weights
+// (and, for attention, of its 64-key K and V slices) of its next phase into
+// registers, so the HBM stream of a phase overlaps the wait for its inputs.
+// Weights are re-tiled q8_0 MFMA panels read with non-temporal 16-byte loads;
+// exchange buffers move through 16-byte device-coherent (sc1) buffer accesses.
 //
-// Every barrier wait is bounded: a workgroup that waits too long raises the
-// error word and returns, every other workgroup sees it and returns too, and the
-// host reports the failure.
+// Arithmetic follows the canonical order shared with the oracle: the q8_0 GEMM
+// in 4 K-slices (one per wave) with exact int8 MFMA block dots; attention scores
+// and P.V as fma chains over head_dim / keys, which v_mfma_f32_16x16x4f32
+// computes exactly (its 4-term dot is a sequential fma chain); chunk softmax,
+// butterfly sums and the chunk merge as in device_common.hpp.
 #include "device_common.hpp"
 #include "step_kernel.hpp"
 
@@ -33,104 +37,292 @@ namespace mtg {
 namespace {
 using namespace dev;
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr unsigned kSpinLimit = 1u << 22;
+constexpr int kT = 256;                 // threads per workgroup
+constexpr int kNwg = 256;               // workgroups (one per CU)
+constexpr unsigned kSpin = 1u << 23;    // bounded waits
+// shapes the kernel is written for (Qwen3-0.6B)
+constexpr int cH = 1024, cQN = 2048, cNQKV = 4096, cF = 3072, cNH = 16, cNKV = 8, cHD = 128;
+constexpr int cBH = cH / kPairK, cBQ = cQN / kPairK, cBF = cF / kPairK;  // 16, 32, 48
+constexpr int cOTiles = cH / 16;         // 64 (o-proj and down tiles, on workgroups 0..63)
+constexpr int cGuBlocks = cF / 32;       // 96 (gate/up 32-row blocks, on workgroups 64..159)
+constexpr int kMergeWg0 = 160;           // merge items on workgroups 160..255
+constexpr int cQStride = 132;            // LDS row strides (conflict-free MFMA operand reads)
+constexpr int cPStride = 68;
 
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
-  return v;
+enum { kPhQkv = 0, kPhAttn = 1, kPhMerge = 2, kPhO = 3, kPhGu = 4, kPhD = 5, kPhases = 6 };
+
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ Rsrc mk_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+// device-coherent (agent scope) 16- and 4-byte accesses
+__device__ __forceinline__ v4f ldc4(Rsrc r, uint32_t off) {
+  return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 16));
+}
+__device__ __forceinline__ float ldc1(Rsrc r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 16));
+}
+__device__ __forceinline__ void stc4(Rsrc r, uint32_t off, v4f v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, (int)off, 0, 16);
+}
+__device__ __forceinline__ void stc1(Rsrc r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, (int)off, 0, 16);
+}
+
+// Global-address-space access to memory reached through the parameter block:
+// without the cast such pointers are generic and their loads become flat
+// loads, which also count against the LDS counter, so every LDS wait would
+// drain the prefetched weights.
+#define MTG_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ T gld(const void* p) { return *(const MTG_GLOBAL T*)p; }
+template <class T>
+__device__ __forceinline__ T gld_nt(const void* p) { return __builtin_nontemporal_load((const MTG_GLOBAL T*)p); }
+template <class T>
+__device__ __forceinline__ void gst(void* p, T v) { *(MTG_GLOBAL T*)p = v; }
+
+// Workgroup barrier that waits only for LDS traffic, so loads issued ahead of
+// it stay in flight.
+__device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+
+struct Ctl {
+  const StepParams* P;
+  uint32_t epoch;
+  uint32_t published;
+  int* s_ok;
+};
+
+// All of this thread's stores have completed; then workgroup w announces v.
+__device__ __forceinline__ void publish(Ctl& c, uint32_t v) {
+  if (v <= c.published) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  bar();
+  if (threadIdx.x == 0)
+    __hip_atomic_store(c.P->flags + blockIdx.x, c.epoch + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  c.published = v;
+}
+
+// Wait until every workgroup has announced at least v. Returns false when the
+// step is aborted (a bounded wait ran out here or elsewhere).
+__device__ __forceinline__ bool wait_all(Ctl& c, uint32_t v, int prof_slot = -1) {
+  const StepParams& P = *c.P;
+  if (threadIdx.x < 64) {
+    if (prof_slot >= 0 && P.timing && threadIdx.x == 0) P.timing[prof_slot] = wall_clock64();
+    const int lane = threadIdx.x;
+    const Rsrc rf = mk_rsrc(P.flags, kNwg * 4);
+    const Rsrc re = mk_rsrc(P.err, 4);
+    const uint32_t target = c.epoch + v;
+    unsigned spins = 0;
+    int ok = 1;
+    bool have = false;  // this lane's four words have reached the target
+    for (;;) {
+      if (!have) {  // only lanes still behind issue loads: less traffic on the words
+        const v4u f = __builtin_amdgcn_raw_buffer_load_b128(rf, lane * 16, 0, 16);
+        have = min(min(f.x, f.y), min(f.z, f.w)) >= target;
+      }
+      if (__all(have)) break;
+      if (__builtin_amdgcn_raw_buffer_load_b32(re, 0, 0, 16)) { ok = 0; break; }
+      if (++spins > kSpin) {
+        if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32(1u, re, 0, 0, 16);
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (prof_slot >= 0 && P.timing && lane == 0) P.timing[prof_slot + 1] = spins;
+    if (lane == 0) *c.s_ok = ok;
+  }
+  bar();
+  return *c.s_ok != 0;
 }
 
 __device__ __forceinline__ void mark(const StepParams& P, int slot) {
   if (P.timing && blockIdx.x == 0 && threadIdx.x == 0) P.timing[slot] = wall_clock64();
 }
+// every workgroup's marks of one layer: slots 1024 + 16 w + k
+__device__ __forceinline__ void wmark(const StepParams& P, int l, int k) {
+  if (P.timing && l == 1 && threadIdx.x == 0) P.timing[1024 + 16 * blockIdx.x + k] = wall_clock64();
+}
 
-// Grid barrier: each workgroup publishes the barrier number in its own arrival
-// word once its coherent stores completed; workgroup 0 gathers all words and
-// publishes the number in the release word, which the others poll with one
-// lane. Returns false when the step was aborted (a bounded wait ran out here or
-// elsewhere).
-__device__ bool grid_sync(const StepParams& P, uint32_t target, int* s_flag) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // this wave's stores are complete
-  __syncthreads();
-  if (threadIdx.x == 0) st_coh_u32(P.flags + blockIdx.x, target);
-  if (blockIdx.x == 0) {
-    if (threadIdx.x < 64) {
-      unsigned spins = 0;
-      int ok = 1;
-      for (;;) {
-        uint32_t mn = 0xffffffffu;
-        for (int i = threadIdx.x; i < (int)gridDim.x; i += 64) mn = min(mn, ld_coh_u32(P.flags + i));
-        mn = wave_min_u32(mn);
-        if (mn >= target) break;
-        if (ld_coh_u32((const uint32_t*)P.err)) { ok = 0; break; }
-        if (++spins > kSpinLimit) {
-          st_coh_u32((uint32_t*)P.err, 1u);
-          ok = 0;
-          break;
+// ----------------------------------------------------------- weight tiles ---
+// NP block pairs of one wave's K-slice of a 16-row tile, held in registers:
+// a[p] = the lane's 16 code bytes, s[p] = the 4 f16 row scales it needs.
+template <int NP>
+__device__ __forceinline__ void wt_load(const uint8_t* __restrict__ tile, int bp0, v4i* a, uint2* s) {
+  const int lane = threadIdx.x & 63;
+  const int srow = ((lane & 15) >> 3) * 16 + 4 * (lane >> 4);
+  // buffer loads: per-lane 32-bit offset + wave-uniform scalar offset per unit
+  const Rsrc r = mk_rsrc(tile, cBF * kUnitBytes);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int so = (bp0 + p) * kUnitBytes;
+    a[p] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, so, 2));
+    const v2u sv = __builtin_amdgcn_raw_buffer_load_b64(r, 1024 + srow * 2, so, 2);
+    s[p] = make_uint2(sv.x, sv.y);
+  }
+}
+
+// acc[cg][r] += the tile slice against the activation panel (canonical: per
+// block, acc = fma(isum, dw * dx, acc) in block-pair order).
+template <int G, int NP>
+__device__ __forceinline__ void wt_mma(const v4i* a, const uint2* sc, int bp0, int bps,
+                                       const uint8_t* __restrict__ pcodes,
+                                       const float* __restrict__ pscales, float acc[G][4]) {
+  const int lane = threadIdx.x & 63;
+  const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    float dw[4];
+    dw[0] = half_bits_to_float((uint16_t)(sc[p].x & 0xffff));
+    dw[1] = half_bits_to_float((uint16_t)(sc[p].x >> 16));
+    dw[2] = half_bits_to_float((uint16_t)(sc[p].y & 0xffff));
+    dw[3] = half_bits_to_float((uint16_t)(sc[p].y >> 16));
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg) {
+      const int bp = bp0 + p;
+      const v4i b = *(const v4i*)(pcodes + ((size_t)(cg * bps + bp)) * 1024 + lane * 16);
+      const float dx = pscales[(size_t)(cg * bps + bp) * 16 + (lane & 15)];
+      const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[p], b, zero, 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[cg][q] = fmaf((float)c[q], dw[q] * dx, acc[cg][q]);
+    }
+  }
+}
+
+// q8_0 code of v with the block's scale: d = amax / 127 rounded to f16,
+// code = rint(v * 127 / amax) (the activation quantizer of the q8_0 GEMMs).
+__device__ __forceinline__ float q8_scale(float amax) { return __half2float(__float2half_rn(__fdiv_rn(amax, 127.0f))); }
+__device__ __forceinline__ uint32_t q8_code(float v, float amax) {
+  const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+  return (uint32_t)(uint8_t)(int8_t)rintf(__fmul_rn(v, id));
+}
+
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+
+// The four waves' slice sums meet in LDS and are added in wave order, then the
+// even and odd block halves; wave 0 writes T x 16 outputs with 16-byte stores.
+template <int G, int NM, int EPI>
+__device__ __forceinline__ void gemm_finish(float acc[NM][G][4], float* red, Rsrc out, int n,
+                                            int tile, int T) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[((wave * NM + m) * G * 4 + cg * 4 + q) * 64 + lane] = acc[m][cg][q];
+  bar();
+  if (wave == 0) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float s = red[((0 * NM + m) * G * 4 + cg * 4 + q) * 64 + lane];
+#pragma unroll
+          for (int wv = 1; wv < 4; ++wv) s = __fadd_rn(s, red[((wv * NM + m) * G * 4 + cg * 4 + q) * 64 + lane]);
+          acc[m][cg][q] = __fadd_rn(s, lane_xor_f<8>(s));
+        }
+    if ((lane & 15) < 8) {
+#pragma unroll
+      for (int cg = 0; cg < G; ++cg) {
+        const int t = cg * 8 + (lane & 7);
+        if (t < T) {
+          const uint32_t off = (uint32_t)((t * n + tile * 16 + 4 * (lane >> 4)) * 4);
+          v4f v;
+          if (EPI == EPI_STORE) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = acc[0][cg][q];
+          } else if (EPI == EPI_RESID) {
+            const v4f x = ldc4(out, off);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = __fadd_rn(x[q], acc[0][cg][q]);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = dev_swiglu(acc[0][cg][q], acc[NM - 1][cg][q]);
+          }
+          stc4(out, off, v);
         }
       }
-      if (threadIdx.x == 0) {
-        if (ok) st_coh_u32(P.release, target);
-        *s_flag = ok;
-      }
     }
-  } else if (threadIdx.x == 0) {
-    unsigned spins = 0;
-    int ok = 1;
-    while (ld_coh_u32(P.release) < target) {
-      if (ld_coh_u32((const uint32_t*)P.err)) { ok = 0; break; }
-      if (++spins > kSpinLimit) {
-        st_coh_u32((uint32_t*)P.err, 1u);
-        ok = 0;
-        break;
-      }
-    }
-    *s_flag = ok;
   }
-  __syncthreads();
-  return *s_flag != 0;
-}
-#define SYNC_OR_RETURN()                     \
-  do {                                       \
-    if (!grid_sync(P, ++b, &s_flag)) return; \
-    mark(P, (int)(b - epoch));               \
-  } while (0)
-
-// ---------------------------------------------------------------- panels ----
-// Build the q8_0 activation panel of T rows of src (K columns, K a multiple of
-// 1024) in LDS, optionally after RMSNorm * gain (then K == 1024). A wave pass is
-// 64 half-block chunks = 1024 consecutive floats of one row: they are fetched
-// with coalesced coherent loads into the wave's LDS scratch, then lane l takes
-// elements 16l..16l+15 (the two halves of a 32-block sit in lanes l and l^1).
-// normed_out (nullable) receives the f32 normalized rows.
-__device__ __forceinline__ void load_pass(const float* src, int K, int c0, float* sw, float v[16]) {
-  const int lane = threadIdx.x & 63, cpr = K / 16;
-  const float* base = src + (size_t)(c0 / cpr) * K + (c0 % cpr) * 16;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) sw[64 * e + lane] = ld_coh(base + 64 * e + lane);
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const v4f x = *(const v4f*)(sw + 16 * lane + 4 * q);
-    v[4 * q] = x[0];
-    v[4 * q + 1] = x[1];
-    v[4 * q + 2] = x[2];
-    v[4 * q + 3] = x[3];
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  bar();
 }
 
+// Gate and up of rows 32j..32j+31 (two 16-row tiles; acc[0], acc[1] gate,
+// acc[2], acc[3] up): the wave slice sums meet in LDS in wave order, then the
+// even and odd halves, SwiGLU, and each row t's 32 values leave as one q8_0
+// block (the activation quantization of the down projection).
 template <int G>
-__device__ __forceinline__ void quant_store(const float v[16], int t, int kc, int bps, uint8_t* pcodes,
-                                            float* pscales) {
+__device__ __forceinline__ void gu_finish(float acc[4][G][4], float* red, const StepParams& P, int j,
+                                          int T) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[((wave * 4 + m) * G * 4 + cg * 4 + q) * 64 + lane] = acc[m][cg][q];
+  bar();
+  if (wave == 0) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float s = red[((0 * 4 + m) * G * 4 + cg * 4 + q) * 64 + lane];
+#pragma unroll
+          for (int wv = 1; wv < 4; ++wv) s = __fadd_rn(s, red[((wv * 4 + m) * G * 4 + cg * 4 + q) * 64 + lane]);
+          acc[m][cg][q] = __fadd_rn(s, lane_xor_f<8>(s));
+        }
+    const Rsrc rq = mk_rsrc(P.aq, kMaxRows * cF);
+    const Rsrc rs = mk_rsrc(P.aqs, kMaxRows * (cF / 32) * 4);
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg) {
+      float va[4], vb[4], amax = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        va[q] = dev_swiglu(acc[0][cg][q], acc[2][cg][q]);
+        vb[q] = dev_swiglu(acc[1][cg][q], acc[3][cg][q]);
+        amax = fmaxf(amax, fmaxf(fabsf(va[q]), fabsf(vb[q])));
+      }
+      // the block's 32 rows sit in lanes (lane & 15) + 16 m, m = 0..3
+      amax = fmaxf(amax, lane_xor_f<16>(amax));
+      amax = fmaxf(amax, lane_xor_f<32>(amax));
+      const int t = cg * 8 + (lane & 7);
+      if ((lane & 15) < 8 && t < T) {
+        uint32_t pa = 0, pb = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          pa |= q8_code(va[q], amax) << (8 * q);
+          pb |= q8_code(vb[q], amax) << (8 * q);
+        }
+        const int row = 32 * j + 4 * (lane >> 4);
+        __builtin_amdgcn_raw_buffer_store_b32(pa, rq, t * cF + row, 0, 16);
+        __builtin_amdgcn_raw_buffer_store_b32(pb, rq, t * cF + row + 16, 0, 16);
+        if (lane < 16) stc1(rs, (uint32_t)((t * (cF / 32) + j) * 4), q8_scale(amax));
+      }
+    }
+  }
+  bar();
+}
+
+// --------------------------------------------------------------- panels -----
+// 16 elements (a half q8_0 block) -> codes in the LDS panel; lanes l and l^1 hold
+// the two halves of one block.
+__device__ __forceinline__ void quant16(const float v[16], int t, int kc, int bps, uint8_t* pcodes,
+                                        float* pscales) {
   float amax = 0.0f;
 #pragma unroll
   for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(v[e]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, lane_xor_f<1>(amax));
   const float d = __fdiv_rn(amax, 127.0f);
   const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
   uint32_t packed[4];
@@ -152,359 +344,500 @@ __device__ __forceinline__ void quant_store(const float v[16], int t, int kc, in
   if (half == 0) pscales[(size_t)(cg * bps + bp) * 16 + j] = __half2float(__float2half_rn(d));
 }
 
-template <int G>
-__device__ void build_panel(const float* src, int K, int T, const float* gain, float eps,
-                            uint8_t* pcodes, float* pscales, double* s_part, float* scratch,
-                            float* normed_out) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int cpr = K / 16, chunks = T * cpr, bps = K / kPairK;
-  const int passes = (chunks + kThreads - 1) / kThreads;
-  float* sw = scratch + wave * 1024;
-  if (gain) {
-    // K == 1024: one wave pass = one row; at most 4 passes (T <= 16)
-    float v[4][16];
+// Panel of RMSNorm(x) * gain for T rows of 1024 (one wave per row): lane l
+// holds elements 16l..16l+15. normed_out (nullable): the f32 rows.
+__device__ void panel_norm(Rsrc x, int T, const float* __restrict__ gain, float eps, uint8_t* pcodes,
+                           float* pscales, float* normed_out) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float gv[16];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int c0 = p * kThreads + wave * 64;
-      if (p < passes && c0 < chunks) {
-        const float* base = src + (size_t)(c0 / cpr) * K + (c0 % cpr) * 16;
+  for (int i = 0; i < 4; ++i) {
+    const v4f g = gld<v4f>(gain + 16 * lane + 4 * i);
+    gv[4 * i] = g[0];
+    gv[4 * i + 1] = g[1];
+    gv[4 * i + 2] = g[2];
+    gv[4 * i + 3] = g[3];
+  }
+  for (int t0 = wave; t0 < T; t0 += 8) {
+    // two rows per pass: all loads issued before any arithmetic
+    float v[2][16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) v[p][e] = ld_coh(base + 64 * e + lane);
-      }
-    }
+    for (int j = 0; j < 2; ++j) {
+      const int t = t0 + 4 * j;
+      if (t < T) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      if (p >= passes) break;
-      const int c0 = p * kThreads + wave * 64;
-      double s = 0.0;
-      if (c0 < chunks) {
-        // transpose the coalesced fetch through the wave's LDS scratch
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sw[64 * e + lane] = v[p][e];
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const v4f x4 = *(const v4f*)(sw + 16 * lane + 4 * qq);
-          v[p][4 * qq] = x4[0];
-          v[p][4 * qq + 1] = x4[1];
-          v[p][4 * qq + 2] = x4[2];
-          v[p][4 * qq + 3] = x4[3];
+        for (int i = 0; i < 4; ++i) {
+          const v4f q = ldc4(x, (uint32_t)((t * cH + 16 * lane + 4 * i) * 4));
+          v[j][4 * i] = q[0];
+          v[j][4 * i + 1] = q[1];
+          v[j][4 * i + 2] = q[2];
+          v[j][4 * i + 3] = q[3];
         }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s += (double)__fmul_rn(v[p][e], v[p][e]);
       }
-      s = wave_sum_d(s);
-      if (lane == 0) s_part[p * kWaves + wave] = s;
     }
-    __syncthreads();
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int c = p * kThreads + tid;
-      if (p >= passes || c >= chunks) break;  // whole waves
-      const int t = c / cpr, kc = c % cpr, k0 = kc * 16;
-      const float mean = (float)(s_part[p * kWaves + wave] / (double)K);
-      const float scale = dev_rms_scale(mean, eps);
+    for (int j = 0; j < 2; ++j) {
+      const int t = t0 + 4 * j;
+      if (t >= T) break;
+      double s = 0.0;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s += (double)__fmul_rn(v[j][e], v[j][e]);
+      s = wave_sum_d(s);
+      const float scale = dev_rms_scale((float)(s / (double)cH), eps);
       float y[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) y[e] = __fmul_rn(__fmul_rn(v[p][e], scale), gain[k0 + e]);
+      for (int e = 0; e < 16; ++e) y[e] = __fmul_rn(__fmul_rn(v[j][e], scale), gv[e]);
       if (normed_out)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) normed_out[(size_t)t * K + k0 + e] = y[e];
-      quant_store<G>(y, t, kc, bps, pcodes, pscales);
+        for (int i = 0; i < 4; ++i) {
+          const v4f o = {y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]};
+          gst<v4f>(normed_out + (size_t)t * cH + 16 * lane + 4 * i, o);
+        }
+      quant16(y, t, lane, cBH, pcodes, pscales);
     }
+  }
+  bar();
+}
+
+// Panel of T rows of K floats quantized as they are (o: K = 2048, act: K = 3072).
+// Chunk c (16 floats) = bytes [64c, 64c + 64) of the row-major source.
+template <int K>
+__device__ void panel_plain(Rsrc src, int T, uint8_t* pcodes, float* pscales) {
+  constexpr int cpr = K / 16, bps = K / kPairK;
+  const int chunks = T * cpr;
+  for (int base = 0; base < chunks; base += 4 * kT) {
+    float v[4][16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = base + j * kT + threadIdx.x;
+      if (c < chunks) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const v4f q = ldc4(src, (uint32_t)(c * 64 + 16 * i));
+          v[j][4 * i] = q[0];
+          v[j][4 * i + 1] = q[1];
+          v[j][4 * i + 2] = q[2];
+          v[j][4 * i + 3] = q[3];
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = base + j * kT + threadIdx.x;
+      if (c < chunks)  // whole waves: chunks is a multiple of 64
+        quant16(v[j], c / cpr, c % cpr, bps, pcodes, pscales);
+    }
+  }
+  bar();
+}
+
+// Panel of T rows of K activations already quantized by their producer:
+// codes [t][K] int8, scales [t][K/32]. Thread = 16 codes (a half block).
+template <int K>
+__device__ void panel_from_q(const int8_t* codes, const float* scales, int T, uint8_t* pcodes,
+                             float* pscales) {
+  constexpr int cpr = K / 16, bps = K / kPairK;
+  const Rsrc rc = mk_rsrc(codes, kMaxRows * K);
+  const Rsrc rs = mk_rsrc(scales, kMaxRows * (K / 32) * 4);
+  const int chunks = T * cpr;
+  for (int base = 0; base < chunks; base += 4 * kT) {
+    v4u q[4];
+    float d[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = base + j * kT + threadIdx.x;
+      if (c < chunks) {
+        const int t = c / cpr, kc = c % cpr;
+        q[j] = __builtin_amdgcn_raw_buffer_load_b128(rc, t * K + kc * 16, 0, 16);
+        d[j] = ldc1(rs, (uint32_t)((t * (K / 32) + (kc >> 1)) * 4));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = base + j * kT + threadIdx.x;
+      if (c < chunks) {
+        const int t = c / cpr, kc = c % cpr;
+        const int blk = kc >> 1, half = kc & 1, bp = blk >> 1, par = blk & 1;
+        const int cg = t >> 3, jc = par * 8 + (t & 7);
+        uint8_t* unit = pcodes + (size_t)(cg * bps + bp) * 1024;
+        *(uint4*)(unit + (jc + 16 * (2 * par + half)) * 16) = make_uint4(q[j].x, q[j].y, q[j].z, q[j].w);
+        *(uint4*)(unit + (jc + 16 * (2 * (1 - par) + half)) * 16) = make_uint4(0u, 0u, 0u, 0u);
+        if (half == 0) pscales[(size_t)(cg * bps + bp) * 16 + jc] = d[j];
+      }
+    }
+  }
+  bar();
+}
+
+// ------------------------------------------------------------ attention -----
+// K and V of one 64-key chunk in MFMA operand layout. Wave w: scores of keys
+// 16w + (lane % 16), k-index lane / 16 (kreg[s] = K[key][4s + lane/16]); P.V for
+// head_dim tiles 2w and 2w+1 (vreg[h][s] = V[4s + lane/16][16(2w+h) + lane%16]).
+// Raw cache bits (f32, or f16 in the low half), zero outside [0, past).
+struct KvRegs {
+  uint32_t k[32];
+  uint32_t v[2][16];
+};
+
+__device__ __forceinline__ void kv_prefetch(const LayerDev& Ly, const StepParams& P, int g, int key0,
+                                            int past, KvRegs& r) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, kl = lane & 15, kk = lane >> 4;
+  const int es = P.kv_f16 ? 2 : 4;
+  // The kv head's rows [0, past). Every key-dependent part of an address is in
+  // the per-lane offset (the scalar offset is 0), so a key >= past lies beyond
+  // num_records and its load returns 0 without touching memory.
+  const size_t head = (size_t)g * P.max_seq * cHD * es;
+  const Rsrc rk = mk_rsrc(Ly.kc + head, (uint32_t)(past * cHD * es));
+  const Rsrc rv = mk_rsrc(Ly.vc + head, (uint32_t)(past * cHD * es));
+  // K: lane (kl, kk) of wave w holds K[key0 + 16w + kl][4s + kk]
+  const int kvo = ((key0 + 16 * wave + kl) * cHD + kk) * es;
+  // V: vreg[h][s] = V[key0 + 4s + kk][16(2w + h) + kl]
+  const int vvo = ((key0 + kk) * cHD + 32 * wave + kl) * es;
+  if (es == 2) {
+#pragma unroll
+    for (int s = 0; s < 32; ++s) r.k[s] = __builtin_amdgcn_raw_buffer_load_b16(rk, kvo + 4 * s * 2, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        r.v[h][s] = __builtin_amdgcn_raw_buffer_load_b16(rv, vvo + (4 * s * cHD + 16 * h) * 2, 0, 0);
   } else {
-    for (int p0 = 0; p0 < passes; p0 += 4) {
-      // fetch up to four passes of this wave with independent coherent loads
-      float raw[4][16];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c0 = (p0 + q) * kThreads + wave * 64;
-        if (p0 + q < passes && c0 < chunks) {
-          const float* base = src + (size_t)(c0 / cpr) * K + (c0 % cpr) * 16;
+    for (int s = 0; s < 32; ++s) r.k[s] = __builtin_amdgcn_raw_buffer_load_b32(rk, kvo + 4 * s * 4, 0, 0);
 #pragma unroll
-          for (int e = 0; e < 16; ++e) raw[q][e] = ld_coh(base + 64 * e + lane);
-        }
-      }
+    for (int s = 0; s < 16; ++s)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c0 = (p0 + q) * kThreads + wave * 64;
-        if (p0 + q >= passes || c0 >= chunks) break;  // whole waves
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sw[64 * e + lane] = raw[q][e];
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        float v[16];
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const v4f x4 = *(const v4f*)(sw + 16 * lane + 4 * qq);
-          v[4 * qq] = x4[0];
-          v[4 * qq + 1] = x4[1];
-          v[4 * qq + 2] = x4[2];
-          v[4 * qq + 3] = x4[3];
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        const int c = c0 + lane;
-        quant_store<G>(v, c / cpr, c % cpr, bps, pcodes, pscales);
-      }
-    }
-  }
-  __syncthreads();
-}
-
-// ------------------------------------------------------------------ GEMM ----
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
-
-// Tiles tile = blockIdx.x, +gridDim.x, ...; the 4 waves split K and meet in
-// LDS in wave order; the epilogue writes coherently.
-template <int G, int EPI>
-__device__ void gemm_phase(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
-                           int n_tiles, int bps, const uint8_t* pcodes, const float* pscales,
-                           float* red, float* out, int n, int T) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  constexpr int NM = EPI == EPI_SWIGLU ? 2 : 1;
-  const int bp0 = (bps * wave) / kWaves, bp1 = (bps * (wave + 1)) / kWaves;
-  for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-    float acc[NM][G][4];
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int cg = 0; cg < G; ++cg)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[m][cg][r] = 0.0f;
-    tile_accumulate<G>(w + (size_t)tile * bps * kUnitBytes, bp0, bp1, pcodes, pscales, bps, acc[0]);
-    if (EPI == EPI_SWIGLU)
-      tile_accumulate<G>(w2 + (size_t)tile * bps * kUnitBytes, bp0, bp1, pcodes, pscales, bps,
-                         acc[NM - 1]);
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int cg = 0; cg < G; ++cg)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[((wave * NM + m) * G * 4 + cg * 4 + r) * 64 + lane] = acc[m][cg][r];
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-      for (int m = 0; m < NM; ++m)
-#pragma unroll
-        for (int cg = 0; cg < G; ++cg)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float s = red[((0 * NM + m) * G * 4 + cg * 4 + r) * 64 + lane];
-            for (int wv = 1; wv < kWaves; ++wv) s = __fadd_rn(s, red[((wv * NM + m) * G * 4 + cg * 4 + r) * 64 + lane]);
-            acc[m][cg][r] = __fadd_rn(s, __shfl_xor(s, 8, 64));
-          }
-      if ((lane & 15) < 8) {
-#pragma unroll
-        for (int cg = 0; cg < G; ++cg) {
-          const int t = cg * 8 + (lane & 7);
-          if (t < T) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int row = tile * 16 + 4 * (lane >> 4) + r;
-              float* dst = out + (size_t)t * n + row;
-              if (EPI == EPI_STORE) {
-                st_coh(dst, acc[0][cg][r]);
-              } else if (EPI == EPI_RESID) {
-                st_coh(dst, __fadd_rn(ld_coh(dst), acc[0][cg][r]));
-              } else {
-                st_coh(dst, dev_swiglu(acc[0][cg][r], acc[NM - 1][cg][r]));
-              }
-            }
-          }
-        }
-      }
-    }
-    __syncthreads();
+      for (int h = 0; h < 2; ++h)
+        r.v[h][s] = __builtin_amdgcn_raw_buffer_load_b32(rv, vvo + (4 * s * cHD + 16 * h) * 4, 0, 0);
   }
 }
 
-// ------------------------------------------------------------- attention ----
-// q/k RMSNorm (head_dim 128) + NEOX RoPE of one row, one wave, lane i owns the
-// pair (i, i+64); returns the rotated pair.
-__device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, const float* g, float eps,
-                                               const float* rope_row, int i) {
-  double s = (double)__fmul_rn(x0, x0) + (double)__fmul_rn(x1, x1);
-  s = wave_sum_d(s);
-  const float mean = (float)(s / (double)kHeadDim);
-  const float scale = dev_rms_scale(mean, eps);
-  const float y0 = __fmul_rn(__fmul_rn(x0, scale), g[i]);
-  const float y1 = __fmul_rn(__fmul_rn(x1, scale), g[i + 64]);
-  const float c = rope_row[2 * i], sn = rope_row[2 * i + 1];
-  x0 = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, sn));
-  x1 = __fadd_rn(__fmul_rn(y0, sn), __fmul_rn(y1, c));
+__device__ __forceinline__ float kv_val(uint32_t bits, bool f16) {
+  return f16 ? half_bits_to_float((uint16_t)bits) : __uint_as_float(bits);
 }
 
-// Items (kv head g, chunk of 64 keys), grid-stride. Each workgroup stages the
-// roped q of heads 2g, 2g+1 and, when its chunk reaches the new keys, the new
-// K/V rows (q/k RMSNorm + NEOX RoPE from qkv); the workgroup whose chunk holds
-// position `past` also appends them to the cache for later steps.
-__device__ void attn_phase(const StepParams& P, const LayerDev& Ly, int T, int past, uint8_t* lds) {
-  const int NKV = P.NKV, NH = P.NH;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int NQKV = (NH + 2 * NKV) * kHeadDim;
+// One attention item: chunk `chunk` of kv head g over the ncol = 2T query
+// columns (col = hl*T + t for q head 2g + hl). LDS: q [32][132], knew/vnew
+// [16][132], sp [32][68].
+__device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& Ly, int T, int past, int g, int chunk,
+                          const KvRegs& kv, uint8_t* lds, bool prof) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kl = lane & 15, kk = lane >> 4;
   const bool f16kv = P.kv_f16 != 0;
-  const int kvlen = past + T, nch = (kvlen + kChunk - 1) / kChunk;
-  float* q_lds = (float*)lds;                  // [kMaxCols][128]
-  float* knew = q_lds + kMaxCols * kHeadDim;   // [16][128]
-  float* vnew = knew + kMaxRows * kHeadDim;    // [16][128]
-  float* vbuf = vnew + kMaxRows * kHeadDim;    // [64][128]
-  float* sp = vbuf + kChunk * kHeadDim;        // [kMaxCols][64]
-  const int ncol = 2 * T;
-  int staged_g = -1;
-  for (int item = blockIdx.x; item < NKV * nch; item += gridDim.x) {
-    const int g = item / nch, chunk = item % nch, key0 = chunk * kChunk;
-    const bool has_new = key0 + kChunk > past;
-    const bool appender = key0 <= past && past < key0 + kChunk;
-    if (g != staged_g || has_new) {
-      // q rows (col = hl*T + t) and, if needed, the new k / v rows
-      const int nrows = ncol + (has_new ? 2 * T : 0);
-      for (int r = wave; r < nrows; r += kWaves) {
-        int kind, t, col;
-        if (r < ncol) {
-          kind = 0;
-          t = r % T;
-          col = (2 * g + r / T) * kHeadDim;
-        } else if (r < ncol + T) {
-          kind = 1;
-          t = r - ncol;
-          col = (NH + g) * kHeadDim;
-        } else {
-          kind = 2;
-          t = r - ncol - T;
-          col = (NH + NKV + g) * kHeadDim;
-        }
-        const float* src = P.qkv + (size_t)t * NQKV + col;
-        float x0 = ld_coh(src + lane), x1 = ld_coh(src + lane + 64);
-        if (kind < 2)
-          norm_rope_pair(x0, x1, kind == 0 ? Ly.q_norm : Ly.k_norm, P.eps,
-                         P.rope + (size_t)(past + t) * kHeadDim, lane);
-        if (kind == 0) {
-          float* q = q_lds + r * kHeadDim;
-          q[lane] = f16kv ? f16_round(x0) : x0;
-          q[lane + 64] = f16kv ? f16_round(x1) : x1;
-        } else {
-          if (appender) {
-            const size_t off = ((size_t)g * P.max_seq + past + t) * kHeadDim;
-            uint8_t* cache = kind == 1 ? Ly.kc : Ly.vc;
-            if (f16kv) {
-              ((__half*)cache)[off + lane] = __float2half_rn(x0);
-              ((__half*)cache)[off + lane + 64] = __float2half_rn(x1);
-            } else {
-              ((float*)cache)[off + lane] = x0;
-              ((float*)cache)[off + lane + 64] = x1;
-            }
-          }
-          float* dst = (kind == 1 ? knew : vnew) + t * kHeadDim;
-          dst[lane] = f16kv ? f16_round(x0) : x0;
-          dst[lane + 64] = f16kv ? f16_round(x1) : x1;
+  const int kvlen = past + T, ncol = 2 * T, key0 = chunk * kChunk;
+  float* q_lds = (float*)lds;
+  float* knew = q_lds + kMaxCols * cQStride;
+  float* vnew = knew + kMaxRows * cQStride;
+  float* sp = vnew + kMaxRows * cQStride;
+  const bool has_new = key0 + kChunk > past;
+  const bool appender = key0 <= past && past < key0 + kChunk;
+  const Rsrc rq = mk_rsrc(P.qkv, kMaxRows * cNQKV * 4);
+  // 1. stage the roped q rows and, if this chunk reaches them, the new k / v rows
+  //    (per wave up to four rows at a time, every load issued before the math)
+  const int nrows = ncol + (has_new ? 2 * T : 0);
+  for (int r0 = wave; r0 < nrows; r0 += 16) {
+    float x0[4], x1[4], g0[4], g1[4], rc[4], rs[4];
+    int kind[4], tt[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = r0 + 4 * j;
+      kind[j] = r < ncol ? 0 : (r < ncol + T ? 1 : 2);
+      tt[j] = kind[j] == 0 ? r % T : (kind[j] == 1 ? r - ncol : r - ncol - T);
+      if (r < nrows) {
+        const int col = kind[j] == 0 ? (2 * g + r / T) * cHD
+                                     : (kind[j] == 1 ? (cNH + g) * cHD : (cNH + cNKV + g) * cHD);
+        const uint32_t base = (uint32_t)((tt[j] * cNQKV + col) * 4);
+        x0[j] = ldc1(rq, base + lane * 4);
+        x1[j] = ldc1(rq, base + (lane + 64) * 4);
+        if (kind[j] < 2) {
+          const float* gn = kind[j] == 0 ? Ly.q_norm : Ly.k_norm;
+          g0[j] = gld<float>(gn + lane);
+          g1[j] = gld<float>(gn + lane + 64);
+          const v2f cs = gld<v2f>(P.rope + (size_t)(past + tt[j]) * cHD + 2 * lane);
+          rc[j] = cs.x;
+          rs[j] = cs.y;
         }
       }
-      __syncthreads();
-      staged_g = has_new ? -1 : g;
     }
-    AttnSrc a;
-    a.kc = Ly.kc;
-    a.vc = Ly.vc;
-    a.f16 = P.kv_f16;
-    a.head_base = (size_t)g * P.max_seq * kHeadDim;
-    a.knew = knew;
-    a.vnew = vnew;
-    a.new_from = has_new ? past : kvlen;
-    const size_t pi = (size_t)g * P.max_chunks + chunk;
-    attn_chunk<true>(a, q_lds, ncol, T, past, kvlen, key0, __fdiv_rn(1.0f, dev_sqrtf((float)kHeadDim)), vbuf, sp,
-                     P.part_ml + pi * kMaxCols * 2, P.part_o + pi * kMaxCols * kHeadDim);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = r0 + 4 * j, t = tt[j];
+      if (r >= nrows) break;
+      float a0 = x0[j], a1 = x1[j];
+      if (kind[j] < 2) {
+        double sq = (double)__fmul_rn(a0, a0) + (double)__fmul_rn(a1, a1);
+        sq = wave_sum_d(sq);
+        const float scale = dev_rms_scale((float)(sq / (double)cHD), P.eps);
+        const float y0 = __fmul_rn(__fmul_rn(a0, scale), g0[j]);
+        const float y1 = __fmul_rn(__fmul_rn(a1, scale), g1[j]);
+        a0 = __fsub_rn(__fmul_rn(y0, rc[j]), __fmul_rn(y1, rs[j]));
+        a1 = __fadd_rn(__fmul_rn(y0, rs[j]), __fmul_rn(y1, rc[j]));
+      }
+      if (kind[j] > 0 && appender) {
+        const size_t off = ((size_t)g * P.max_seq + past + t) * cHD;
+        uint8_t* cache = kind[j] == 1 ? Ly.kc : Ly.vc;
+        if (f16kv) {
+          gst<uint16_t>((uint16_t*)cache + off + lane, __half_as_ushort(__float2half_rn(a0)));
+          gst<uint16_t>((uint16_t*)cache + off + lane + 64, __half_as_ushort(__float2half_rn(a1)));
+        } else {
+          gst<float>((float*)cache + off + lane, a0);
+          gst<float>((float*)cache + off + lane + 64, a1);
+        }
+      }
+      float* dst = kind[j] == 0 ? q_lds + r * cQStride : (kind[j] == 1 ? knew : vnew) + t * cQStride;
+      dst[lane] = f16kv ? f16_round(a0) : a0;
+      dst[lane + 64] = f16kv ? f16_round(a1) : a1;
+    }
+  }
+  bar();
+  if (prof) mark(P, 510);
+  // 2. operands: prefetched cache rows, new rows from LDS, zeros past kvlen
+  float ka[32], vb[2][16];
+#pragma unroll
+  for (int s = 0; s < 32; ++s) ka[s] = kv_val(kv.k[s], f16kv);
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int s = 0; s < 16; ++s) vb[h][s] = kv_val(kv.v[h][s], f16kv);
+  if (has_new) {  // keys >= past come from this step's rows; none past kvlen
+    const int key = key0 + 16 * wave + kl;
+#pragma unroll
+    for (int s = 0; s < 32; ++s)
+      if (key >= past) ka[s] = key < kvlen ? knew[(key - past) * cQStride + 4 * s + kk] : 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const int vk = key0 + 4 * s + kk;
+        if (vk >= past) vb[h][s] = vk < kvlen ? vnew[(vk - past) * cQStride + 16 * (2 * wave + h) + kl] : 0.0f;
+      }
+  }
+  if (prof) { bar(); mark(P, 511); }
+  // 3. scores S[key][col] = fma chain over head_dim, scaled and masked -> sp
+  const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)cHD));
+  for (int ct = 0; ct * 16 < ncol; ++ct) {
+    const int colb = ct * 16 + kl;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 32; ++s) {
+      const float b = colb < ncol ? q_lds[colb * cQStride + 4 * s + kk] : 0.0f;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[s], b, acc, 0, 0, 0);
+    }
+    if (colb < ncol) {
+      const int t = colb % T;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int kloc = 16 * wave + 4 * kk + q, key = key0 + kloc;
+        sp[colb * cPStride + kloc] = (key < kvlen && key <= past + t) ? __fmul_rn(acc[q], scale) : -INFINITY;
+      }
+    }
+  }
+  bar();
+  if (prof) mark(P, 512);
+  // 4. chunk softmax per column (one wave per column, lane = key)
+  const size_t pi = (size_t)g * P.max_chunks + chunk;
+  const Rsrc rml = mk_rsrc(P.part_ml + pi * kMaxCols * 2, kMaxCols * 2 * 4);
+  for (int col = wave; col < ncol; col += 4) {
+    const float w = sp[col * cPStride + lane];
+    const float m = wave_max_f(w);
+    float p = (m == -INFINITY || w == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(w, m));
+    if (f16kv) p = f16_round(p);
+    const float l = wave_sum_f(p);
+    sp[col * cPStride + lane] = p;
+    if (lane == 0) {
+      stc1(rml, (uint32_t)(col * 2 * 4), m);
+      stc1(rml, (uint32_t)((col * 2 + 1) * 4), l);
+    }
+  }
+  bar();
+  if (prof) mark(P, 513);
+  // 5. O[col][d] = fma chain over the chunk's keys of p * v
+  const Rsrc ro = mk_rsrc(P.part_o + pi * kMaxCols * cHD, kMaxCols * cHD * 4);
+  for (int ct = 0; ct * 16 < ncol; ++ct) {
+    const int cola = ct * 16 + kl;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const float a = cola < ncol ? sp[cola * cPStride + 4 * s + kk] : 0.0f;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[h][s], acc, 0, 0, 0);
+      }
+      const int d = 16 * (2 * wave + h) + kl;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = ct * 16 + 4 * kk + q;
+        if (col < ncol) stc1(ro, (uint32_t)((col * cHD + d) * 4), acc[q]);
+      }
+    }
+  }
+  bar();
+  if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); mark(P, 514); }
+}
+
+// Merge the chunk partials of (q head hq, row t) in chunk order; 128 threads,
+// thread = head_dim element d (two waves). The merged row leaves as four q8_0
+// blocks (32 lanes each). valid == false: the lanes only take part in the lane
+// exchanges.
+__device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, int hq, int t, int d,
+                                           bool valid) {
+  const int g = hq / 2, col = (hq & 1) * T + t;
+  const Rsrc rml = mk_rsrc(P.part_ml + (size_t)g * P.max_chunks * kMaxCols * 2,
+                           (uint32_t)P.max_chunks * kMaxCols * 2 * 4);
+  const Rsrc ro = mk_rsrc(P.part_o + (size_t)g * P.max_chunks * kMaxCols * cHD,
+                          (uint32_t)P.max_chunks * kMaxCols * cHD * 4);
+  // Chunk factors once per wave: lane c holds m_c, l_c and f_c = exp(m_c - M);
+  // every thread then reads them as wave-uniform values (readlane) while it runs
+  // the two chunk-ordered fma chains over its own O values.
+  const int lane = threadIdx.x & 63;
+  float out = 0.0f;
+  float M = -INFINITY;
+  for (int c0 = 0; c0 < nch; c0 += 64) {
+    const float m = (valid && c0 + lane < nch) ? ldc1(rml, (uint32_t)(((c0 + lane) * kMaxCols + col) * 2 * 4)) : -INFINITY;
+    M = fmaxf(M, wave_max_f(m));
+  }
+  float L = 0.0f, O = 0.0f;
+  for (int c0 = 0; c0 < nch; c0 += 64) {
+    const int cl = c0 + lane < nch ? c0 + lane : nch - 1;
+    const float m = valid ? ldc1(rml, (uint32_t)((cl * kMaxCols + col) * 2 * 4)) : -INFINITY;
+    const float l = valid ? ldc1(rml, (uint32_t)(((cl * kMaxCols + col) * 2 + 1) * 4)) : 0.0f;
+    const float f = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, M));
+    const int nb = min(64, nch - c0);
+    for (int i0 = 0; i0 < nb; i0 += 32) {
+      float o[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int c = c0 + i0 + i < nch ? c0 + i0 + i : nch - 1;
+        o[i] = valid ? ldc1(ro, (uint32_t)(((c * kMaxCols + col) * cHD + d) * 4)) : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        if (i0 + i >= nb) break;
+        const float mc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), i0 + i));
+        if (mc == -INFINITY) continue;
+        const float fc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), i0 + i));
+        const float lc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), i0 + i));
+        L = fmaf(lc, fc, L);
+        O = fmaf(o[i], fc, O);
+      }
+    }
+  }
+  if (valid) out = __fdiv_rn(O, L);
+  // q8_0 blocks of 32 consecutive d (32 lanes of one wave)
+  float amax = fabsf(out);
+  amax = fmaxf(amax, lane_xor_f<1>(amax));
+  amax = fmaxf(amax, lane_xor_f<2>(amax));
+  amax = fmaxf(amax, lane_xor_f<4>(amax));
+  amax = fmaxf(amax, lane_xor_f<8>(amax));
+  amax = fmaxf(amax, lane_xor_f<16>(amax));
+  if (valid) {
+    const Rsrc rq = mk_rsrc(P.oq, kMaxRows * cQN);
+    const Rsrc rs = mk_rsrc(P.oqs, kMaxRows * (cQN / 32) * 4);
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)q8_code(out, amax), rq, t * cQN + hq * cHD + d, 0, 16);
+    if ((d & 31) == 0) stc1(rs, (uint32_t)((t * (cQN / 32) + (hq * cHD + d) / 32) * 4), q8_scale(amax));
   }
 }
 
-// (head, row) items: merge the chunks into o[t][head*128 + d]. Each half
-// workgroup takes one item; the partials of up to 32 chunks are fetched with
-// independent coherent loads before the canonical merge runs over them.
-__device__ void combine_phase(const StepParams& P, int T, int past, float* s_ml) {
-  const int items = P.NH * T, nch = (past + T + kChunk - 1) / kChunk;
-  const int d = threadIdx.x & 127, half = threadIdx.x >> 7;
-  float* ml = s_ml + half * 64;  // [32 chunks][2]
-  for (int base = 2 * blockIdx.x; base < items; base += 2 * gridDim.x) {
-    const int item = base + half;
-    const bool active = item < items;
-    const int hq = active ? item / T : 0, t = active ? item % T : 0;
-    const int g = hq / 2, col = (hq & 1) * T + t;
-    const float* pml = P.part_ml + (size_t)g * P.max_chunks * kMaxCols * 2 + col * 2;
-    const float* po = P.part_o + (size_t)g * P.max_chunks * kMaxCols * kHeadDim + col * kHeadDim + d;
-    const size_t sml = (size_t)kMaxCols * 2, so = (size_t)kMaxCols * kHeadDim;
-    // pass 1: the maximum over all chunks
-    float M = -INFINITY;
-    for (int c0 = 0; c0 < nch; c0 += 64) {
-      const int c = c0 + (d & 63);
-      float m = -INFINITY;
-      if (active && d < 64 && c < nch) m = ld_coh(pml + c * sml);
-      M = fmaxf(M, m);
-    }
-    // M is reduced over the half workgroup's first wave-half... use LDS
-    __shared__ float s_max[2][2];
-    M = wave_max_f(M);
-    if ((threadIdx.x & 63) == 0 && ((threadIdx.x >> 6) & 1) == 0) s_max[half][0] = M;
-    __syncthreads();
-    M = s_max[half][0];
-    float L = 0.0f, O = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += 32) {
-      const int nb = min(32, nch - c0);
-      if (active && d < 2 * nb) ml[d] = ld_coh(pml + (c0 + (d >> 1)) * sml + (d & 1));
-      float ov[32];
-#pragma unroll
-      for (int i = 0; i < 32; ++i) ov[i] = (active && i < nb) ? ld_coh(po + (c0 + i) * so) : 0.0f;
-      __syncthreads();
-      if (active) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          if (i >= nb) break;
-          const float m = ml[2 * i];
-          if (m == -INFINITY) continue;
-          const float f = dev_expf(__fsub_rn(m, M));
-          L = fmaf(ml[2 * i + 1], f, L);
-          O = fmaf(ov[i], f, O);
-        }
-      }
-      __syncthreads();
-    }
-    if (active) st_coh(P.o + (size_t)t * P.NH * kHeadDim + hq * kHeadDim + d, __fdiv_rn(O, L));
-  }
-}
-
-// ------------------------------------------------------------- lm_head -----
+// ---------------------------------------------------------------- lm_head ---
+// Wave-strided tiles of the tied embedding; block pairs stream through an
+// 8-deep register ring; per tile the canonical 4-slice sums, the penalty and
+// 64-bit first-max keys.
 template <int G>
-__device__ void lm_head_phase(const StepParams& P, const StepDesc* desc, int T, const uint8_t* pcodes,
-                              const float* pscales, uint64_t* s_best) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int V = P.V, bps = P.H / kPairK, n_tiles = V / 16;
+__device__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const uint8_t* pcodes,
+                        const float* pscales, uint64_t* s_best) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int V = P.V, n_tiles = V / 16, gw = blockIdx.x * 4 + wave, nwaves = gridDim.x * 4;
   const bool pen = desc->penalty > 1.0f;
   const float penalty = desc->penalty;
   const int words = (V + 31) / 32;
   const bool write_logits = desc->write_logits != 0;
+  const Rsrc rb = mk_rsrc(P.bitmap, (uint32_t)(kMaxRows * words * 4));
+  const int srow = ((lane & 15) >> 3) * 16 + 4 * (lane >> 4);
+  const v4i zero = {0, 0, 0, 0};
   uint64_t best[G];
 #pragma unroll
   for (int cg = 0; cg < G; ++cg) best[cg] = 0;
-  const int nwaves = gridDim.x * kWaves;
-  for (int tile = blockIdx.x * kWaves + wave; tile < n_tiles; tile += nwaves) {
-    float acc[G][4];
-    tile_accumulate_canonical<G>(P.embd + (size_t)tile * bps * kUnitBytes, bps, pcodes, pscales, acc);
-    if ((lane & 15) < 8) {
+  const int my_tiles = gw < n_tiles ? (n_tiles - 1 - gw) / nwaves + 1 : 0;
+  const int units = my_tiles * cBH;  // (tile, pair) units of this wave, in order
+  constexpr int R = 8;
+  v4i ra[R];
+  uint2 rs[R];
+  const Rsrc re = mk_rsrc(P.embd, (uint32_t)((size_t)n_tiles * cBH * kUnitBytes));
+  auto issue = [&](int u, int slot) {
+    const int tile = gw + (u / cBH) * nwaves, bp = u % cBH;
+    const int so = (tile * cBH + bp) * kUnitBytes;
+    ra[slot] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(re, lane * 16, so, 2));
+    const v2u sv = __builtin_amdgcn_raw_buffer_load_b64(re, 1024 + srow * 2, so, 2);
+    rs[slot] = make_uint2(sv.x, sv.y);
+  };
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    if (i < units) issue(i, i);
+  float part[4][G][4];
+  for (int u0 = 0; u0 < units; u0 += R) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int u = u0 + i;
+      if (u >= units) break;
+      const int bp = u % cBH, sl = bp >> 2;
+      if (bp == 0) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) part[a][cg][q] = 0.0f;
+      }
+      float dw[4];
+      dw[0] = half_bits_to_float((uint16_t)(rs[i].x & 0xffff));
+      dw[1] = half_bits_to_float((uint16_t)(rs[i].x >> 16));
+      dw[2] = half_bits_to_float((uint16_t)(rs[i].y & 0xffff));
+      dw[3] = half_bits_to_float((uint16_t)(rs[i].y >> 16));
+      const v4i a = ra[i];
+      if (u + R < units) issue(u + R, i);
 #pragma unroll
       for (int cg = 0; cg < G; ++cg) {
-        const int t = cg * 8 + (lane & 7);
-        if (t < T) {
+        const v4i b = *(const v4i*)(pcodes + ((size_t)(cg * cBH + bp)) * 1024 + lane * 16);
+        const float dx = pscales[(size_t)(cg * cBH + bp) * 16 + (lane & 15)];
+        const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, zero, 0, 0, 0);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = tile * 16 + 4 * (lane >> 4) + r;
-            float v = acc[cg][r];
-            if (write_logits) P.logits[(size_t)t * V + row] = v;
-            if (pen && ((ld_coh_u32(P.bitmap + (size_t)t * words + (row >> 5)) >> (row & 31)) & 1u))
-              v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
-            const uint64_t key = argmax_key(v, row);
-            best[cg] = key > best[cg] ? key : best[cg];
+        for (int q = 0; q < 4; ++q) {
+          // the slice index is wave-uniform: select without dynamic indexing
+          const float add = dw[q] * dx;
+          if (sl == 0) part[0][cg][q] = fmaf((float)c[q], add, part[0][cg][q]);
+          else if (sl == 1) part[1][cg][q] = fmaf((float)c[q], add, part[1][cg][q]);
+          else if (sl == 2) part[2][cg][q] = fmaf((float)c[q], add, part[2][cg][q]);
+          else part[3][cg][q] = fmaf((float)c[q], add, part[3][cg][q]);
+        }
+      }
+      if (bp == cBH - 1) {
+        const int tile = gw + (u / cBH) * nwaves;
+#pragma unroll
+        for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float v = __fadd_rn(__fadd_rn(__fadd_rn(part[0][cg][q], part[1][cg][q]), part[2][cg][q]), part[3][cg][q]);
+            v = __fadd_rn(v, lane_xor_f<8>(v));
+            part[0][cg][q] = v;
+          }
+        if ((lane & 15) < 8) {
+#pragma unroll
+          for (int cg = 0; cg < G; ++cg) {
+            const int t = cg * 8 + (lane & 7);
+            if (t < T) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const int row = tile * 16 + 4 * (lane >> 4) + q;
+                float v = part[0][cg][q];
+                if (write_logits) gst<float>(P.logits + (size_t)t * V + row, v);
+                if (pen) {
+                  const uint32_t word = __builtin_amdgcn_raw_buffer_load_b32(rb, (t * words + (row >> 5)) * 4, 0, 16);
+                  if ((word >> (row & 31)) & 1u) v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+                }
+                const uint64_t key = argmax_key(v, row);
+                best[cg] = key > best[cg] ? key : best[cg];
+              }
+            }
           }
         }
       }
@@ -524,26 +857,25 @@ __device__ void lm_head_phase(const StepParams& P, const StepDesc* desc, int T, 
   if (lane < 8)
 #pragma unroll
     for (int cg = 0; cg < G; ++cg) s_best[wave * kMaxRows + cg * 8 + lane] = best[cg];
-  __syncthreads();
+  bar();
   if (threadIdx.x < G * 8) {
     uint64_t b = s_best[threadIdx.x];
-    for (int wv = 1; wv < kWaves; ++wv) b = s_best[wv * kMaxRows + threadIdx.x] > b ? s_best[wv * kMaxRows + threadIdx.x] : b;
+    for (int wv = 1; wv < 4; ++wv) b = s_best[wv * kMaxRows + threadIdx.x] > b ? s_best[wv * kMaxRows + threadIdx.x] : b;
     st_coh_u64(P.part_keys + (size_t)blockIdx.x * kMaxRows + threadIdx.x, b);
   }
-  __syncthreads();
 }
 
-__device__ void accept_phase(const StepParams& P, const StepDesc* desc, int T, uint64_t* s_red,
-                             int32_t* s_choice) {
+__device__ void accept(const StepParams& P, const StepDesc* desc, int T, uint64_t* s_red,
+                       int32_t* s_choice) {
   for (int t = 0; t < T; ++t) {
     uint64_t b = 0;
-    for (int i = threadIdx.x; i < (int)gridDim.x; i += kThreads) {
+    for (int i = threadIdx.x; i < (int)gridDim.x; i += kT) {
       const uint64_t k = ld_coh_u64(P.part_keys + (size_t)i * kMaxRows + t);
       b = k > b ? k : b;
     }
     s_red[threadIdx.x] = b;
     __syncthreads();
-    for (int o = kThreads / 2; o > 0; o >>= 1) {
+    for (int o = kT / 2; o > 0; o >>= 1) {
       if ((int)threadIdx.x < o && s_red[threadIdx.x + o] > s_red[threadIdx.x]) s_red[threadIdx.x] = s_red[threadIdx.x + o];
       __syncthreads();
     }
@@ -559,126 +891,257 @@ __device__ void accept_phase(const StepParams& P, const StepDesc* desc, int T, u
 }
 
 // ---------------------------------------------------------------- kernel ----
+__device__ __forceinline__ uint32_t ph(int l, int p) { return 2u + (uint32_t)(l * kPhases + p); }
+
 template <int G>
-__global__ void __launch_bounds__(kThreads, 1)
+__global__ void __launch_bounds__(kT, 1)
 k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uint32_t epoch,
-       int mode) {
+        int mode) {
   const StepParams& P = *Pp;
   extern __shared__ v4i lds_v4[];
   uint8_t* lds = (uint8_t*)lds_v4;
-  const int T = desc->T, past = desc->past;
-  const int H = P.H, QN = P.NH * kHeadDim, KN = P.NKV * kHeadDim, F = P.F;
-  const int bps_max = P.bps_max;
-  uint8_t* pcodes = lds;
-  float* pscales = (float*)(lds + (size_t)G * bps_max * 1024);
-  float* red = (float*)(lds + (size_t)G * bps_max * (1024 + 64));
-  float* scratch = red;  // panel builds and GEMM reductions never overlap in time
-  __shared__ double s_part[64];
-  __shared__ int s_flag;
-  __shared__ uint64_t s_best[kWaves * kMaxRows];
-  __shared__ uint64_t s_red[kThreads];
+  __shared__ int s_ok;
+  __shared__ uint64_t s_best[4 * kMaxRows];
+  __shared__ uint64_t s_red[kT];
   __shared__ int32_t s_choice[kMaxRows];
-  uint32_t b = epoch;
+  const int w = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int T = desc->T, past = desc->past, L = P.L;
+  const int nch = (past + T + kChunk - 1) / kChunk, n_items = cNKV * nch;
+  uint8_t* pcodes = lds;
+  float* pscales = (float*)(lds + (size_t)G * cBF * 1024);
+  float* red = (float*)(lds + (size_t)G * cBF * (1024 + 64));
+  Ctl c{&P, epoch, 0, &s_ok};
+#define RX mk_rsrc(P.x, kMaxRows * cH * 4)
+#define RQKV mk_rsrc(P.qkv, kMaxRows * cNQKV * 4)
+
+  // roles
+  const int first_item = (w + kNwg - 64) % kNwg;  // item i runs on workgroup (i + 64) % 256
+  const bool has_attn = first_item < n_items;
+  const int n_merge = cNH * T;                    // (head, row) items, in pairs
+  const bool has_merge = w >= kMergeWg0;
+  const bool od = w < cOTiles;                    // o-proj and down tiles
+  const bool gu = w >= cOTiles && w < cOTiles + cGuBlocks;  // gate/up rows 32j..32j+31
+  // phase mask of this workgroup (bit p = works in phase p)
+  const int mask = 1 | (has_attn ? 2 : 0) | (has_merge ? 4 : 0) | (od ? 8 | 32 : 0) | (gu ? 16 : 0);
+  auto next_done = [&](int l, int p) -> uint32_t {  // progress after working in phase p of layer l
+    for (int q = p + 1; q < kPhases; ++q)
+      if (mask & (1 << q)) return ph(l, q) - 1;
+    return ph(l, kPhases) - 1;  // next work: the next layer's QKV (or the lm_head)
+  };
   mark(P, 0);
 
-  // embeddings (and the penalty bitmap)
-  if ((int)blockIdx.x < T) {
-    const int t = blockIdx.x;
-    float* xr = P.x + (size_t)t * H;
+  // registers carried across phases
+  v4i qa[4];              // this layer's q|k|v tile slice
+  uint2 qs[4];
+  v4i ba[16];             // o-proj (8 pairs) then down (12), or gate A|B, up A|B (4 each)
+  uint2 bs[16];
+  KvRegs kv;              // K / V of the first attention item
+
+  // ---- embeddings (and the penalty bitmap) ----
+  if (w < T) {
+    const int t = w;
+    const int k = threadIdx.x * 4;
+    v4f e;
     if (desc->use_embeds) {
-      for (int k = threadIdx.x; k < H; k += kThreads) st_coh(xr + k, P.embeds[(size_t)t * H + k]);
+      e = gld<v4f>(P.embeds + (size_t)t * cH + k);
     } else {
-      const int n = desc->tokens[t], bps = H / kPairK, tile = n >> 4, r = n & 15;
-      for (int k = threadIdx.x; k < H; k += kThreads) {
-        const int bk = k >> 5, bp = bk >> 1, par = bk & 1, half = (k >> 4) & 1;
-        const uint8_t* unit = P.embd + ((size_t)tile * bps + bp) * kUnitBytes;
-        const int8_t q = (int8_t)unit[(r + 16 * (2 * par + half)) * 16 + (k & 15)];
-        const float d = half_bits_to_float(((const uint16_t*)(unit + 1024))[par * 16 + r]);
-        st_coh(xr + k, d * (float)q);
-      }
+      const int n = desc->tokens[t], tile = n >> 4, r = n & 15;
+      const int bk = k >> 5, bp = bk >> 1, par = bk & 1, half = (k >> 4) & 1;
+      const uint8_t* unit = P.embd + ((size_t)tile * cBH + bp) * kUnitBytes;
+      const uint32_t q4 = gld<uint32_t>(unit + (r + 16 * (2 * par + half)) * 16 + (k & 15));
+      const float d = half_bits_to_float(gld<uint16_t>(unit + 1024 + (par * 16 + r) * 2));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) e[i] = d * (float)(int8_t)(q4 >> (8 * i));
     }
+    stc4(RX, (uint32_t)((t * cH + k) * 4), e);
     if (mode == kStepVerify && desc->penalty > 1.0f) {
       const int words = (P.V + 31) / 32;
       uint32_t* row = P.bitmap + (size_t)t * words;
-      for (int i = threadIdx.x; i < words; i += kThreads) st_coh_u32(row + i, 0u);
+      for (int i = threadIdx.x; i < words; i += kT) st_coh_u32(row + i, 0u);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       __syncthreads();
       const int end = desc->pen_base + t + 1, begin = max(0, end - kPenaltyWindow);
-      for (int i = begin + (int)threadIdx.x; i < end; i += kThreads) {
+      for (int i = begin + (int)threadIdx.x; i < end; i += kT) {
         const int id = desc->pen_ids[i];
         if (id >= 0 && id < P.V) atomicOr(row + (id >> 5), 1u << (id & 31));
       }
     }
   }
-  SYNC_OR_RETURN();
+  publish(c, 1);
+  // prefetch layer 0: q|k|v tile and the first attention item's K / V
+  wt_load<4>(P.layers[0].wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+  if (has_attn) kv_prefetch(P.layers[0], P, first_item / nch, (first_item % nch) * kChunk, past, kv);
 
-  for (int l = 0; l < P.L; ++l) {
+  for (int l = 0; l < L; ++l) {
     const LayerDev& Ly = P.layers[l];
-    // QKV
-    if ((int)blockIdx.x < (QN + 2 * KN) / 16) {
-      build_panel<G>(P.x, H, T, Ly.attn_norm, P.eps, pcodes, pscales, s_part, scratch, nullptr);
-      gemm_phase<G, EPI_STORE>(Ly.wqkv, nullptr, (QN + 2 * KN) / 16, H / kPairK, pcodes, pscales, red,
-                               P.qkv, QN + 2 * KN, T);
+    // ---- QKV: tile w ----
+    if (!wait_all(c, ph(l, kPhQkv) - 1)) return;
+    mark(P, 3 + 12 * l + 0);
+    wmark(P, l, 0);
+    panel_norm(RX, T, Ly.attn_norm, P.eps, pcodes, pscales, nullptr);
+    {
+      float acc[1][G][4] = {};
+      wt_mma<G, 4>(qa, qs, 4 * wave, cBH, pcodes, pscales, acc[0]);
+      gemm_finish<G, 1, EPI_STORE>(acc, red, RQKV, cNQKV, w, T);
     }
-    SYNC_OR_RETURN();
-    attn_phase(P, Ly, T, past, lds);
-    SYNC_OR_RETURN();
-    combine_phase(P, T, past, (float*)lds);
-    SYNC_OR_RETURN();
-    if ((int)blockIdx.x < H / 16) {
-      build_panel<G>(P.o, QN, T, nullptr, 0.0f, pcodes, pscales, s_part, scratch, nullptr);
-      gemm_phase<G, EPI_RESID>(Ly.wo, nullptr, H / 16, QN / kPairK, pcodes, pscales, red, P.x, H, T);
+    publish(c, next_done(l, kPhQkv));
+    mark(P, 3 + 12 * l + 1);
+    wmark(P, l, 1);
+    if (od) wt_load<8>(Ly.wo + (size_t)w * cBQ * kUnitBytes, 8 * wave, ba, bs);
+    // ---- ATTN: items of this workgroup ----
+    if (has_attn) {
+      if (!wait_all(c, ph(l, kPhAttn) - 1, l == 1 ? 1024 + 16 * w + 14 : -1)) return;
+      mark(P, 3 + 12 * l + 2);
+      wmark(P, l, 2);
+      for (int item = first_item; item < n_items; item += kNwg) {
+        if (item != first_item) kv_prefetch(Ly, P, item / nch, (item % nch) * kChunk, past, kv);
+        attn_item(P, Ly, T, past, item / nch, item % nch, kv, lds, l == 1);
+      }
+      publish(c, next_done(l, kPhAttn));
+      mark(P, 3 + 12 * l + 3);
+      wmark(P, l, 3);
     }
-    SYNC_OR_RETURN();
-    if ((int)blockIdx.x < F / 16) {
-      build_panel<G>(P.x, H, T, Ly.ffn_norm, P.eps, pcodes, pscales, s_part, scratch, nullptr);
-      gemm_phase<G, EPI_SWIGLU>(Ly.wg, Ly.wu, F / 16, H / kPairK, pcodes, pscales, red, P.act, F, T);
+    if (gu) {  // gate / up tiles 2j, 2j + 1 of this layer
+      const int j = w - cOTiles;
+      wt_load<4>(Ly.wg + (size_t)(2 * j) * cBH * kUnitBytes, 4 * wave, ba, bs);
+      wt_load<4>(Ly.wg + (size_t)(2 * j + 1) * cBH * kUnitBytes, 4 * wave, ba + 4, bs + 4);
+      wt_load<4>(Ly.wu + (size_t)(2 * j) * cBH * kUnitBytes, 4 * wave, ba + 8, bs + 8);
+      wt_load<4>(Ly.wu + (size_t)(2 * j + 1) * cBH * kUnitBytes, 4 * wave, ba + 12, bs + 12);
     }
-    SYNC_OR_RETURN();
-    if ((int)blockIdx.x < H / 16) {
-      build_panel<G>(P.act, F, T, nullptr, 0.0f, pcodes, pscales, s_part, scratch, nullptr);
-      gemm_phase<G, EPI_RESID>(Ly.wd, nullptr, H / 16, F / kPairK, pcodes, pscales, red, P.x, H, T);
+    // ---- MERGE: (head, row) items, two at a time ----
+    if (has_merge) {
+      if (!wait_all(c, ph(l, kPhMerge) - 1)) return;
+      wmark(P, l, 4);
+      const int half = threadIdx.x >> 7;
+      for (int i0 = 2 * (w - kMergeWg0); i0 < n_merge; i0 += 2 * (kNwg - kMergeWg0)) {
+        const int item = i0 + half;
+        const bool valid = item < n_merge;
+        merge_item(P, T, nch, valid ? item / T : 0, valid ? item % T : 0, threadIdx.x & 127, valid);
+      }
+      publish(c, next_done(l, kPhMerge));
+      wmark(P, l, 5);
+      if (!gu && l + 1 < L) {  // nothing more in this layer: prefetch the next one
+        const LayerDev& Ln = P.layers[l + 1];
+        wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+        if (has_attn) kv_prefetch(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+      }
     }
-    SYNC_OR_RETURN();
+    // ---- O-proj: x += W_o o ----
+    if (od) {
+      if (!wait_all(c, ph(l, kPhO) - 1, l == 1 ? 1024 + 16 * w + 12 : -1)) return;
+      mark(P, 3 + 12 * l + 4);
+      wmark(P, l, 6);
+      panel_from_q<cQN>(P.oq, P.oqs, T, pcodes, pscales);
+      float acc[1][G][4] = {};
+      wt_mma<G, 8>(ba, bs, 8 * wave, cBQ, pcodes, pscales, acc[0]);
+      gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T);
+      publish(c, next_done(l, kPhO));
+      mark(P, 3 + 12 * l + 5);
+      wmark(P, l, 7);
+      wt_load<12>(Ly.wd + (size_t)w * cBF * kUnitBytes, 12 * wave, ba, bs);
+      // the next layer's attention K / V, so that they are in flight before the down wait
+      if (has_attn && l + 1 < L)
+        kv_prefetch(P.layers[l + 1], P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+    }
+    // ---- GATE/UP: act = silu(g) * u, as q8_0 blocks ----
+    if (gu) {
+      if (!wait_all(c, ph(l, kPhGu) - 1, l == 1 ? 1024 + 16 * w + 12 : -1)) return;
+      wmark(P, l, 8);
+      panel_norm(RX, T, Ly.ffn_norm, P.eps, pcodes, pscales, nullptr);
+      float acc[4][G][4] = {};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) wt_mma<G, 4>(ba + 4 * m, bs + 4 * m, 4 * wave, cBH, pcodes, pscales, acc[m]);
+      gu_finish<G>(acc, red, P, w - cOTiles, T);
+      publish(c, next_done(l, kPhGu));
+      wmark(P, l, 9);
+      if (l + 1 < L) {
+        const LayerDev& Ln = P.layers[l + 1];
+        wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+        if (has_attn) kv_prefetch(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+      }
+    }
+    // ---- DOWN: x += W_d act ----
+    if (od) {
+      if (!wait_all(c, ph(l, kPhD) - 1)) return;
+      mark(P, 3 + 12 * l + 6);
+      wmark(P, l, 10);
+      panel_from_q<cF>(P.aq, P.aqs, T, pcodes, pscales);
+      float acc[1][G][4] = {};
+      wt_mma<G, 12>(ba, bs, 12 * wave, cBF, pcodes, pscales, acc[0]);
+      gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T);
+      publish(c, next_done(l, kPhD));
+      mark(P, 3 + 12 * l + 7);
+      wmark(P, l, 11);
+      if (l + 1 < L) wt_load<4>(P.layers[l + 1].wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+    }
+    // workgroups with only q|k|v and attention work
+    if (!od && !gu && !has_merge && l + 1 < L) {
+      const LayerDev& Ln = P.layers[l + 1];
+      wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+      if (has_attn) kv_prefetch(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+    }
   }
-  // final RMSNorm * output_norm (workgroup 0 also returns the f32 rows)
-  build_panel<G>(P.x, H, T, P.out_norm, P.eps, pcodes, pscales, s_part, scratch,
-                 blockIdx.x == 0 ? P.hid : nullptr);
-  if (mode != kStepVerify) return;
-  lm_head_phase<G>(P, desc, T, pcodes, pscales, s_best);
-  SYNC_OR_RETURN();
-  if (blockIdx.x == 0) accept_phase(P, desc, T, s_red, s_choice);
-  mark(P, (int)(b - epoch) + 1);
+
+  // ---- final RMSNorm * output_norm, tied lm_head, acceptance ----
+  const uint32_t lm = ph(L, 0);
+  if (mode != kStepVerify) {
+    if (w == 0) {
+      if (!wait_all(c, lm - 1)) return;
+      panel_norm(RX, T, P.out_norm, P.eps, pcodes, pscales, P.hid);
+      mark(P, 2);
+    }
+    return;
+  }
+  if (!wait_all(c, lm - 1)) return;
+  mark(P, 3 + 12 * L);
+  panel_norm(RX, T, P.out_norm, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr);
+  lm_head<G>(P, desc, T, pcodes, pscales, s_best);
+  publish(c, lm);
+  mark(P, 4 + 12 * L);
+  if (w == 0) {
+    if (!wait_all(c, lm)) return;
+    mark(P, 5 + 12 * L);
+    accept(P, desc, T, s_red, s_choice);
+    mark(P, 6 + 12 * L);
+  }
+#undef RX
+#undef RQKV
 }
 
 }  // namespace
 
-int step_barriers(int n_layers, int mode) { return 1 + 6 * n_layers + (mode == kStepVerify ? 1 : 0); }
-
-size_t step_lds_bytes(int G, int bps_max) {
-  const size_t panel = (size_t)G * bps_max * (1024 + 64);
-  size_t red = (size_t)kWaves * 2 * G * 4 * 64 * 4;
-  if (red < (size_t)kWaves * 1024 * 4) red = (size_t)kWaves * 1024 * 4;  // panel-build scratch
-  const size_t attn = ((size_t)kMaxCols * kHeadDim + 2 * kMaxRows * kHeadDim + kChunk * kHeadDim +
-                       (size_t)kMaxCols * kChunk) * 4;
-  return (panel > attn ? panel : attn) + red;
+int step_kernel_supported(int hidden, int n_heads, int n_kv_heads, int head_dim, int intermediate,
+                          int cus) {
+  return hidden == cH && n_heads == cNH && n_kv_heads == cNKV && head_dim == cHD &&
+         intermediate == cF && cus >= kNwg;
 }
 
-hipError_t launch_step(hipStream_t s, int G, int nwg, const StepParams* P, const StepDesc* desc,
-                       uint32_t epoch, int mode, int bps_max) {
-  const size_t lds = step_lds_bytes(G, bps_max);
-  void* args[] = {(void*)&P, (void*)&desc, (void*)&epoch, (void*)&mode};
-  if (G == 1)
-    return hipLaunchCooperativeKernel((const void*)k_step<1>, dim3(nwg), dim3(kThreads), args, lds, s);
-  return hipLaunchCooperativeKernel((const void*)k_step<2>, dim3(nwg), dim3(kThreads), args, lds, s);
+int step_kernel_workgroups() { return kNwg; }
+
+uint32_t step_progress_per_step(int n_layers) { return 2u + (uint32_t)(n_layers * kPhases); }
+
+size_t step_lds_bytes(int G) {
+  const size_t panel = (size_t)G * cBF * (1024 + 64);
+  const size_t red = (size_t)4 * 4 * G * 4 * 64 * 4;
+  const size_t attn = ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride) * 4;
+  return (panel + red > attn ? panel + red : attn);
 }
 
-hipError_t prepare_step_kernels(int bps_max) {
+hipError_t prepare_step_kernels() {
   hipError_t e = hipFuncSetAttribute((const void*)k_step<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)step_lds_bytes(1, bps_max));
+                                     (int)step_lds_bytes(1));
   if (e != hipSuccess) return e;
   return hipFuncSetAttribute((const void*)k_step<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)step_lds_bytes(2, bps_max));
+                             (int)step_lds_bytes(2));
+}
+
+hipError_t launch_step(hipStream_t s, int G, const StepParams* P, const StepDesc* desc, uint32_t epoch,
+                        int mode) {
+  void* args[] = {(void*)&P, (void*)&desc, (void*)&epoch, (void*)&mode};
+  const size_t lds = step_lds_bytes(G);
+  if (G == 1)
+    return hipLaunchCooperativeKernel((const void*)k_step<1>, dim3(kNwg), dim3(kT), args, lds, s);
+  return hipLaunchCooperativeKernel((const void*)k_step<2>, dim3(kNwg), dim3(kT), args, lds, s);
 }
 
 }  // namespace mtg

@@ -20,7 +20,7 @@ struct LayerDev {
 
 // Constant for a context; lives in device memory.
 struct StepParams {
-  int H, NH, NKV, F, V, L, max_seq, kv_f16, bps_max, max_chunks;
+  int H, NH, NKV, F, V, L, max_seq, kv_f16, max_chunks;
   float eps;
   const LayerDev* layers;
   const uint8_t* embd;
@@ -29,19 +29,28 @@ struct StepParams {
   const float* embeds;  // host rows uploaded for append
   float *x, *qkv, *o, *act, *hid, *logits;
   float *part_ml, *part_o;  // [kv head][chunk][col][2] and [kv head][chunk][col][head_dim]
+  // q8_0 activations exchanged between phases: o (merge -> o-proj) and the
+  // SwiGLU output (gate/up -> down): codes [16][K] and f16-valued scales [16][K/32]
+  int8_t *oq, *aq;
+  float *oqs, *aqs;
   uint32_t* bitmap;
   uint64_t* part_keys;      // [nwg][16]
   StepResult* result;
-  uint32_t* flags;          // [nwg] barrier arrival words
-  uint32_t* release;        // barrier release word (written by workgroup 0)
+  uint32_t* flags;          // [nwg] progress words
   int32_t* err;             // raised by a wait that ran out (inside *result)
-  uint64_t* timing;         // nullable: workgroup 0 records the clock after every barrier
+  uint64_t* timing;         // nullable: phase clock marks (profiling)
 };
 
-int step_barriers(int n_layers, int mode);
-size_t step_lds_bytes(int G, int bps_max);
-hipError_t prepare_step_kernels(int bps_max);
-hipError_t launch_step(hipStream_t s, int G, int nwg, const StepParams* P, const StepDesc* desc,
-                       uint32_t epoch, int mode, int bps_max);
+// The Qwen3-0.6B verify step as one persistent dataflow kernel (256
+// workgroups with fixed, prefetching roles; step_kernel.hip). Progress words
+// advance by step_progress_per_step per launch.
+int step_kernel_supported(int hidden, int n_heads, int n_kv_heads, int head_dim, int intermediate,
+                          int cus);
+int step_kernel_workgroups();
+uint32_t step_progress_per_step(int n_layers);
+size_t step_lds_bytes(int G);
+hipError_t prepare_step_kernels();
+hipError_t launch_step(hipStream_t s, int G, const StepParams* P, const StepDesc* desc,
+                        uint32_t epoch, int mode);
 
 }  // namespace mtg

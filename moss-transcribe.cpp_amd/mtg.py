@@ -261,8 +261,8 @@ class Decoder:
         return ms.value, n.value, ps.value, rs.value
 
     def step_marks(self):
-        out = np.zeros(1024, np.uint64)
-        n = lib().mtg_step_profile_read(self.ctx, ptr(out), 1024)
+        out = np.zeros(8192, np.uint64)
+        n = lib().mtg_step_profile_read(self.ctx, ptr(out), 8192)
         return out[:n].astype(np.int64)
 
     @property

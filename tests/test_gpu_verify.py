@@ -1,9 +1,9 @@
 """Verify-step parity on the GPU against the oracle (same weights, same KV state).
 
-Every execution mode of the library (persistent step kernel, per-op kernels from a
-graph, per-op kernels launched eagerly) must match the oracle within the contract
-(logits 1e-3 relative / 1e-4 absolute) and return identical greedy choices and
-acceptance."""
+Every execution mode of the library (the Qwen3-0.6B dataflow step kernel,
+per-op kernels from a graph, per-op kernels launched eagerly) must match the oracle within the contract (logits 1e-3 relative
+/ 1e-4 absolute) and return identical greedy choices and acceptance; in fact they
+match bit for bit (shared canonical order)."""
 import numpy as np
 import pytest
 
