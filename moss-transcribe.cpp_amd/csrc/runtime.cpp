@@ -258,7 +258,7 @@ int Ctx::init_step_kernel() {
   P.aq = (int8_t*)dalloc((size_t)kMaxRows * F, true);
   P.aqs = (float*)dalloc((size_t)kMaxRows * F / 32 * 4, true);
   P.result = result_dev;
-  P.flags = (uint32_t*)dalloc((size_t)nwg * 4, true);
+  P.flags = (uint32_t*)dalloc((size_t)nwg * kFlagStride * 4, true);
   P.err = &result_dev->err;
   P.timing = nullptr;
   params_dev = (StepParams*)dalloc(sizeof(StepParams), false);
@@ -325,7 +325,7 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
   if (timed && (rc = check(hipEventRecord(ev_start, stream), "timing event"))) return rc;
   if (exec == kExecStep && step_ok && step_mode) {
     if (epoch > 0xF0000000u) {  // progress words restart before they could wrap
-      if ((rc = check(hipMemsetAsync(params_host.flags, 0, (size_t)nwg * 4, stream), "flags"))) return rc;
+      if ((rc = check(hipMemsetAsync(params_host.flags, 0, (size_t)nwg * kFlagStride * 4, stream), "flags"))) return rc;
       epoch = 0;
     }
     const int smode = mode == kModeAppend ? kStepAppend : kStepVerify;

@@ -103,7 +103,8 @@ __device__ __forceinline__ void publish(Ctl& c, uint32_t v) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   bar();
   if (threadIdx.x == 0)
-    __hip_atomic_store(c.P->flags + blockIdx.x, c.epoch + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(c.P->flags + blockIdx.x * kFlagStride, c.epoch + v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   c.published = v;
 }
 
@@ -114,17 +115,28 @@ __device__ __forceinline__ bool wait_all(Ctl& c, uint32_t v, int prof_slot = -1)
   if (threadIdx.x < 64) {
     if (prof_slot >= 0 && P.timing && threadIdx.x == 0) P.timing[prof_slot] = wall_clock64();
     const int lane = threadIdx.x;
-    const Rsrc rf = mk_rsrc(P.flags, kNwg * 4);
+    const Rsrc rf = mk_rsrc(P.flags, kNwg * kFlagStride * 4);
     const Rsrc re = mk_rsrc(P.err, 4);
     const uint32_t target = c.epoch + v;
     unsigned spins = 0;
     int ok = 1;
-    bool have = false;  // this lane's four words have reached the target
+    // lane j watches the words of workgroups j, j+64, j+128, j+192 and keeps a
+    // bit per word that has reached the target. The four loads issue back to
+    // back; a word already seen gets an offset past the buffer's end, which the
+    // range check answers with 0 and no memory request.
+    constexpr uint32_t kGone = 0x80000000u;
+    unsigned hv = 0;
+    bool have = false;
     for (;;) {
-      if (!have) {  // only lanes still behind issue loads: less traffic on the words
-        const v4u f = __builtin_amdgcn_raw_buffer_load_b128(rf, lane * 16, 0, 16);
-        have = min(min(f.x, f.y), min(f.z, f.w)) >= target;
-      }
+      uint32_t f[kNwg / 64];
+#pragma unroll
+      for (int k = 0; k < kNwg / 64; ++k)
+        f[k] = __builtin_amdgcn_raw_buffer_load_b32(
+            rf, (hv & (1u << k)) ? kGone : (uint32_t)((k * 64 + lane) * kFlagStride * 4), 0, 16);
+#pragma unroll
+      for (int k = 0; k < kNwg / 64; ++k)
+        if (f[k] >= target) hv |= 1u << k;
+      have = hv == (1u << (kNwg / 64)) - 1;
       if (__all(have)) break;
       if (__builtin_amdgcn_raw_buffer_load_b32(re, 0, 0, 16)) { ok = 0; break; }
       if (++spins > kSpin) {

@@ -36,7 +36,7 @@ struct StepParams {
   uint32_t* bitmap;
   uint64_t* part_keys;      // [nwg][16]
   StepResult* result;
-  uint32_t* flags;          // [nwg] progress words
+  uint32_t* flags;          // [nwg][kFlagStride] progress words, one per 128-byte line
   int32_t* err;             // raised by a wait that ran out (inside *result)
   uint64_t* timing;         // nullable: phase clock marks (profiling)
 };
@@ -47,6 +47,9 @@ struct StepParams {
 int step_kernel_supported(int hidden, int n_heads, int n_kv_heads, int head_dim, int intermediate,
                           int cus);
 int step_kernel_workgroups();
+// Words between two workgroups' progress words: each word owns a 128-byte line,
+// so a publish does not contend with the polls of its neighbours' words.
+constexpr int kFlagStride = 32;
 uint32_t step_progress_per_step(int n_layers);
 size_t step_lds_bytes(int G);
 hipError_t prepare_step_kernels();
