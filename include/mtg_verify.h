@@ -247,12 +247,17 @@ int32_t mtg_exec_mode(const mtg_ctx* ctx);
 enum { MTG_DEBUG_X = 0, MTG_DEBUG_QKV = 1, MTG_DEBUG_O = 2, MTG_DEBUG_ACT = 3, MTG_DEBUG_HIDDEN = 4 };
 int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes);
 
-/* Profiling of the persistent step kernel: when enabled, workgroup 0 records a
- * 100 MHz device clock into up to 1024 slots: 0 at the start; for layer l at
- * 3 + 12 l + {0, 1}: QKV inputs ready / QKV published, {2, 3}: attention,
- * {4, 5}: o-proj, {6, 7}: down (when workgroup 0 has those roles); at 3 + 12 L
- * the lm_head start, + 1 its end, + 2 / + 3 the acceptance (verify steps).
- * mtg_step_profile_read copies the slots of the last step (returns the count). */
+/* Profiling of the persistent step kernel: when enabled, the kernel records a
+ * 100 MHz device clock into MTG_PROFILE_SLOTS slots. Workgroup 0, slots 0..1023:
+ * 0 at the start; for layer l at 3 + 12 l + {0, 1}: QKV inputs ready / QKV
+ * published, {2, 3}: attention, {4, 5}: o-proj, {6, 7}: down (when workgroup 0
+ * has those roles); at 3 + 12 L the lm_head start, + 1 its end, + 2 / + 3 the
+ * acceptance (verify steps). Every workgroup w, layer 1, slots 1024 + 32 w + k:
+ * k = 0..11 ready / published of QKV, attention, merge, o-proj, gate-up, down;
+ * 12 / 13 first poll and poll count of the o-proj or gate-up wait, 14 / 15 of the
+ * attention wait; 16..23 the attention item's stages. mtg_step_profile_read
+ * copies the slots of the last step (returns the count). */
+#define MTG_PROFILE_SLOTS 9216
 int mtg_step_profile(mtg_ctx* ctx, int32_t enable);
 int32_t mtg_step_profile_read(mtg_ctx* ctx, uint64_t* marks, int32_t n);
 

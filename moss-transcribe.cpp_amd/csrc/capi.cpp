@@ -18,6 +18,8 @@
 using mtg::Ctx;
 
 namespace {
+
+constexpr int kProfileSlots = MTG_PROFILE_SLOTS;
 thread_local std::string g_create_error;
 
 double seconds_since(std::chrono::steady_clock::time_point t0) {
@@ -70,7 +72,7 @@ int mtg_step_profile(mtg_ctx* ctx, int32_t enable) {
   Ctx& c = ctx->impl;
   if (!c.step_ok) return c.fail(MTG_ERR_UNSUPPORTED, "no step kernel");
   if (enable && !c.timing_dev) {
-    c.timing_dev = (uint64_t*)c.dalloc(sizeof(uint64_t) * 8192, true);
+    c.timing_dev = (uint64_t*)c.dalloc(sizeof(uint64_t) * kProfileSlots, true);
     if (!c.timing_dev) return c.fail(MTG_ERR_NOMEM, "timing buffer");
   }
   c.params_host.timing = enable ? c.timing_dev : nullptr;
@@ -105,7 +107,7 @@ int mtg_launch_timing_read(const mtg_ctx* ctx, double* total_ms, int64_t* launch
 
 int32_t mtg_step_profile_read(mtg_ctx* ctx, uint64_t* marks, int32_t n) {
   if (!ctx || !marks || !ctx->impl.timing_dev) return 0;
-  const int count = std::min<int>(n, 8192);
+  const int count = std::min<int>(n, kProfileSlots);
   if (hipMemcpy(marks, ctx->impl.timing_dev, sizeof(uint64_t) * count, hipMemcpyDeviceToHost) != hipSuccess)
     return 0;
   return count;
@@ -339,6 +341,7 @@ int mtg_speculative_run(const mtg_target* tg, int32_t first_seed, const int32_t*
 }
 
 namespace {
+
 int32_t ctx_verify(void* self, const int32_t* tokens, int32_t T, const int32_t* history,
                    int32_t n_history, float penalty, int32_t* choice_out, int32_t* n_match_out) {
   // Ctx::verify advances past by T itself; the controller sets it again.

@@ -32,8 +32,8 @@ namespace dev {
 //    L = fmaf(l_c, f, L), O = fmaf(O_c, f, O), out = O / L.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float dev_expf(float x) {
-  if (x < -87.0f) return 0.0f;  // keeps every result a normal float
-  if (x > 88.7f) return INFINITY;
+  // straight-line code: the out-of-range cases are selected at the end, so that
+  // independent exponentials can interleave
   const float n = rintf(__fmul_rn(x, 1.44269504f));
   float r = fmaf(n, -0.693145752f, x);
   r = fmaf(n, -1.42860677e-06f, r);
@@ -45,7 +45,8 @@ __device__ __forceinline__ float dev_expf(float x) {
   p = fmaf(p, r, 0.5f);
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
-  return ldexpf(p, (int)n);
+  const float e = ldexpf(p, (int)fminf(fmaxf(n, -200.0f), 200.0f));
+  return x < -87.0f ? 0.0f : (x > 88.7f ? INFINITY : e);  // every result a normal float
 }
 
 // Correctly rounded square root of a non-negative float. The hardware estimate
@@ -53,15 +54,13 @@ __device__ __forceinline__ float dev_expf(float x) {
 // comparing x with the squared midpoints, all exact in double (a float has 24
 // significant bits, a midpoint 25, its square at most 50).
 __device__ __forceinline__ float dev_sqrtf(float x) {
-  if (!(x > 0.0f) || x == INFINITY) return __builtin_sqrtf(x);
-  float s = __builtin_sqrtf(x);
+  const float s = __builtin_sqrtf(x);
   const float up = __uint_as_float(__float_as_uint(s) + 1u);
   const float dn = __uint_as_float(__float_as_uint(s) - 1u);
   const double xd = (double)x;
   const double mu = ((double)s + (double)up) * 0.5, md = ((double)s + (double)dn) * 0.5;
-  if (xd > mu * mu) s = up;
-  else if (xd < md * md) s = dn;
-  return s;
+  const float r = xd > mu * mu ? up : (xd < md * md ? dn : s);
+  return (!(x > 0.0f) || x == INFINITY) ? s : r;  // selects, no branches
 }
 
 // 1 / sqrt(mean + eps) of an RMSNorm row, correctly rounded at every step.
@@ -118,15 +117,100 @@ __device__ __forceinline__ double lane_xor_d(double v) {
   return __longlong_as_double((long long)lane_xor_u64<O>((uint64_t)__double_as_longlong(v)));
 }
 
+// ------------------------------------------------------ wave reductions ---
+// A reduction step needs op(x_lane, x_partner), not the exchange itself; for a
+// commutative op (IEEE add, max) either operand order gives the same bits, so the
+// steps use cheaper lane moves than lane_xor and every lane still ends with the
+// value of the xor butterfly:
+//   * O = 32, 16: the half-wave / row swap of two copies leaves one member of
+//     each (lane, lane ^ O) pair in each register: op(a, b).
+//   * O = 8, 4, 2, 1 inside a 16-lane row: row_ror:O. ror 8 is xor 8; once the
+//     steps 8, 4, .. above O are done the values are symmetric under xor with
+//     those bits, and lane + O (mod 16) differs from lane ^ O only in them.
+// The DPP moves read with bound_ctrl, so the compiler may fold them into the op.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __uint_as_float(dpp_u<CTRL>(__float_as_uint(x)));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double x) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  return __longlong_as_double(
+      (long long)(((uint64_t)dpp_u<CTRL>((uint32_t)(b >> 32)) << 32) | dpp_u<CTRL>((uint32_t)b)));
+}
+constexpr int kDppRor8 = 0x128, kDppRor4 = 0x124, kDppRor2 = 0x122, kDppRor1 = 0x121;
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+// The members of every (lane, lane ^ O) pair, O = 16 or 32, one in a and one in b.
+template <int O>
+__device__ __forceinline__ void pair_split(uint32_t x, uint32_t& a, uint32_t& b) {
+  if constexpr (O == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    a = r[0];
+    b = r[1];
+  } else {
+    static_assert(O == 32, "pair_split: 16 or 32");
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    a = r[0];
+    b = r[1];
+  }
+}
+template <int O>
+__device__ __forceinline__ float pair_add_f(float v) {
+  uint32_t a, b;
+  pair_split<O>(__float_as_uint(v), a, b);
+  return __fadd_rn(__uint_as_float(a), __uint_as_float(b));
+}
+template <int O>
+__device__ __forceinline__ float pair_max_f(float v) {
+  uint32_t a, b;
+  pair_split<O>(__float_as_uint(v), a, b);
+  return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+template <int O>
+__device__ __forceinline__ double pair_add_d(double v) {
+  const uint64_t bits = (uint64_t)__double_as_longlong(v);
+  uint32_t alo, blo, ahi, bhi;
+  pair_split<O>((uint32_t)bits, alo, blo);
+  pair_split<O>((uint32_t)(bits >> 32), ahi, bhi);
+  return __longlong_as_double((long long)(((uint64_t)ahi << 32) | alo)) +
+         __longlong_as_double((long long)(((uint64_t)bhi << 32) | blo));
+}
+// max over non-negative floats (their bit patterns order as unsigned integers)
+template <int O>
+__device__ __forceinline__ uint32_t pair_max_u(uint32_t v) {
+  uint32_t a, b;
+  pair_split<O>(v, a, b);
+  return max(a, b);
+}
+
 // xor butterfly 32, 16, 8, 4, 2, 1 (the canonical order of every wave sum)
 __device__ __forceinline__ double wave_sum_d(double v) {
-  v += lane_xor_d<32>(v);
-  v += lane_xor_d<16>(v);
-  v += lane_xor_d<8>(v);
-  v += lane_xor_d<4>(v);
-  v += lane_xor_d<2>(v);
-  v += lane_xor_d<1>(v);
+  v = pair_add_d<32>(v);
+  v = pair_add_d<16>(v);
+  v += dpp_d<kDppRor8>(v);
+  v += dpp_d<kDppRor4>(v);
+  v += dpp_d<kDppRor2>(v);
+  v += dpp_d<kDppRor1>(v);
   return v;
+}
+// amax of non-negative values over 8 consecutive lanes (aligned groups)
+__device__ __forceinline__ float group8_max_nonneg(float v) {
+  uint32_t u = __float_as_uint(v);
+  u = max(u, dpp_u<kDppQuadXor1>(u));
+  u = max(u, dpp_u<kDppQuadXor2>(u));
+  u = max(u, dpp_u<kDppHalfMirror>(u));
+  return __uint_as_float(u);
+}
+// amax of non-negative values over 32 consecutive lanes (aligned halves)
+__device__ __forceinline__ float group32_max_nonneg(float v) {
+  uint32_t u = __float_as_uint(group8_max_nonneg(v));
+  u = max(u, dpp_u<kDppMirror>(u));
+  return __uint_as_float(pair_max_u<16>(u));
 }
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
   switch (o) {
@@ -143,10 +227,8 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
 // (4 elements each): d = amax/127 rounded to f16, codes = rint(x * 127/amax).
 // Returns the f32 value of the stored f16 scale.
 __device__ __forceinline__ float quant_block8(const float v[4], int8_t q[4]) {
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = fmaxf(amax, lane_xor_f<1>(amax));
-  amax = fmaxf(amax, lane_xor_f<2>(amax));
-  amax = fmaxf(amax, lane_xor_f<4>(amax));
+  const float amax =
+      group8_max_nonneg(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
   const float d = __fdiv_rn(amax, 127.0f);
   const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
   for (int e = 0; e < 4; ++e) q[e] = (int8_t)rintf(__fmul_rn(v[e], id));
@@ -221,7 +303,7 @@ __device__ __forceinline__ void tile_accumulate_canonical(const uint8_t* __restr
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float v = __fadd_rn(__fadd_rn(__fadd_rn(part[0][cg][r], part[1][cg][r]), part[2][cg][r]), part[3][cg][r]);
-      acc[cg][r] = __fadd_rn(v, lane_xor_f<8>(v));
+      acc[cg][r] = __fadd_rn(v, dpp_f<kDppRor8>(v));
     }
 }
 
@@ -276,30 +358,96 @@ __device__ __forceinline__ void st_f(float* p, float v) {
 }
 
 __device__ __forceinline__ float wave_max_f(float v) {
-  v = fmaxf(v, lane_xor_f<32>(v));
-  v = fmaxf(v, lane_xor_f<16>(v));
-  v = fmaxf(v, lane_xor_f<8>(v));
-  v = fmaxf(v, lane_xor_f<4>(v));
-  v = fmaxf(v, lane_xor_f<2>(v));
-  v = fmaxf(v, lane_xor_f<1>(v));
+  v = pair_max_f<32>(v);
+  v = pair_max_f<16>(v);
+  v = fmaxf(v, dpp_f<kDppRor8>(v));
+  v = fmaxf(v, dpp_f<kDppRor4>(v));
+  v = fmaxf(v, dpp_f<kDppRor2>(v));
+  v = fmaxf(v, dpp_f<kDppRor1>(v));
   return v;
 }
 __device__ __forceinline__ float wave_sum_f(float v) {
-  v = __fadd_rn(v, lane_xor_f<32>(v));
-  v = __fadd_rn(v, lane_xor_f<16>(v));
-  v = __fadd_rn(v, lane_xor_f<8>(v));
-  v = __fadd_rn(v, lane_xor_f<4>(v));
-  v = __fadd_rn(v, lane_xor_f<2>(v));
-  v = __fadd_rn(v, lane_xor_f<1>(v));
+  v = pair_add_f<32>(v);
+  v = pair_add_f<16>(v);
+  v = __fadd_rn(v, dpp_f<kDppRor8>(v));
+  v = __fadd_rn(v, dpp_f<kDppRor4>(v));
+  v = __fadd_rn(v, dpp_f<kDppRor2>(v));
+  v = __fadd_rn(v, dpp_f<kDppRor1>(v));
   return v;
 }
+// N values reduced side by side, step by step, each in the order of wave_sum_d /
+// wave_sum_f.
+template <int N>
+__device__ __forceinline__ void wave_sum_d_n(double* v) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = pair_add_d<32>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = pair_add_d<16>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_d<kDppRor8>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_d<kDppRor4>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_d<kDppRor2>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_d<kDppRor1>(v[i]);
+}
+template <int N>
+__device__ __forceinline__ void wave_sum_f_n(float* v) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = pair_add_f<32>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = pair_add_f<16>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = __fadd_rn(v[i], dpp_f<kDppRor8>(v[i]));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = __fadd_rn(v[i], dpp_f<kDppRor4>(v[i]));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = __fadd_rn(v[i], dpp_f<kDppRor2>(v[i]));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = __fadd_rn(v[i], dpp_f<kDppRor1>(v[i]));
+}
+// Order-preserving integer key of a float that is not NaN (signed compare), and
+// back; max is exact in any order.
+__device__ __forceinline__ int ord_key(float x) {
+  const int b = __float_as_int(x);
+  return b ^ ((b >> 31) & 0x7FFFFFFF);
+}
+__device__ __forceinline__ float ord_val(int k) { return __int_as_float(k ^ ((k >> 31) & 0x7FFFFFFF)); }
+template <int N>
+__device__ __forceinline__ void wave_max_i_n(int* v) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    uint32_t a, b;
+    pair_split<32>((uint32_t)v[i], a, b);
+    v[i] = max((int)a, (int)b);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    uint32_t a, b;
+    pair_split<16>((uint32_t)v[i], a, b);
+    v[i] = max((int)a, (int)b);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = max(v[i], (int)dpp_u<kDppRor8>((uint32_t)v[i]));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = max(v[i], (int)dpp_u<kDppRor4>((uint32_t)v[i]));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = max(v[i], (int)dpp_u<kDppRor2>((uint32_t)v[i]));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = max(v[i], (int)dpp_u<kDppRor1>((uint32_t)v[i]));
+}
+
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-  v = min(v, lane_xor<32>(v));
-  v = min(v, lane_xor<16>(v));
-  v = min(v, lane_xor<8>(v));
-  v = min(v, lane_xor<4>(v));
-  v = min(v, lane_xor<2>(v));
-  v = min(v, lane_xor<1>(v));
+  uint32_t a, b;
+  pair_split<32>(v, a, b);
+  v = min(a, b);
+  pair_split<16>(v, a, b);
+  v = min(a, b);
+  v = min(v, dpp_u<kDppRor8>(v));
+  v = min(v, dpp_u<kDppRor4>(v));
+  v = min(v, dpp_u<kDppRor2>(v));
+  v = min(v, dpp_u<kDppRor1>(v));
   return v;
 }
 __device__ __forceinline__ float f16_round(float v) { return __half2float(__float2half_rn(v)); }

@@ -103,7 +103,7 @@ k_gemm(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w,
   const int T = desc->T;
   if ((T + 7) / 8 != G) return;  // launched once per supported group count
   const int tile = blockIdx.x;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int bp0 = (bps * wave) / SPLIT, bp1 = (bps * (wave + 1)) / SPLIT;
   constexpr int NM = EPI == 2 ? 2 : 1;
   float acc[NM][G][4];
@@ -144,7 +144,7 @@ k_gemm(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w,
 #pragma unroll
     for (int cg = 0; cg < G; ++cg)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[m][cg][r] = __fadd_rn(acc[m][cg][r], lane_xor_f<8>(acc[m][cg][r]));
+      for (int r = 0; r < 4; ++r) acc[m][cg][r] = __fadd_rn(acc[m][cg][r], dpp_f<kDppRor8>(acc[m][cg][r]));
   if ((lane & 15) >= 8) return;
 #pragma unroll
   for (int cg = 0; cg < G; ++cg) {
@@ -317,7 +317,7 @@ k_lm_head(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int 
     ((v4i*)lcodes)[i] = ((const v4i*)x.codes)[i];
   for (int i = threadIdx.x; i < G * bps * 16; i += blockDim.x) lscales[i] = x.scales[i];
   __syncthreads();
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int n_tiles = vocab / 16;
   const int nwaves = gridDim.x * 4;
   const bool pen = desc->penalty > 1.0f;

@@ -203,7 +203,7 @@ int Ctx::init_step_kernel() {
   if ((rc = check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count")))
     return rc;
   const int H = hp.hidden, F = hp.intermediate, V = hp.vocab;
-  if (!step_kernel_supported(H, hp.n_heads, hp.n_kv_heads, hp.head_dim, F, cus) ||
+  if (!step_kernel_supported(H, hp.n_heads, hp.n_kv_heads, hp.head_dim, F, hp.n_layers, cus) ||
       prepare_step_kernels() != hipSuccess) {
     (void)hipGetLastError();
     exec = kExecGraph;  // other shapes and smaller devices: the per-op kernels
@@ -226,8 +226,8 @@ int Ctx::init_step_kernel() {
     d.kc = kcache + kv_layer_bytes * l;
     d.vc = vcache + kv_layer_bytes * l;
   }
-  LayerDev* table_dev = (LayerDev*)dalloc(table.size() * sizeof(LayerDev), false);
   StepParams P{};
+  for (int l = 0; l < hp.n_layers; ++l) P.layer[l] = table[l];
   P.H = H;
   P.NH = hp.n_heads;
   P.NKV = hp.n_kv_heads;
@@ -237,7 +237,6 @@ int Ctx::init_step_kernel() {
   P.max_seq = max_seq;
   P.kv_f16 = kv_type == MTG_TYPE_F16;
   P.eps = hp.rms_eps;
-  P.layers = table_dev;
   P.embd = embd;
   P.out_norm = out_norm;
   P.rope = rope;
@@ -262,11 +261,9 @@ int Ctx::init_step_kernel() {
   P.err = &result_dev->err;
   P.timing = nullptr;
   params_dev = (StepParams*)dalloc(sizeof(StepParams), false);
-  if (!table_dev || !P.part_ml || !P.part_o || !P.part_keys || !P.flags || !P.oq || !P.oqs || !P.aq || !P.aqs || !params_dev)
+  if (!P.part_ml || !P.part_o || !P.part_keys || !P.flags || !P.oq || !P.oqs || !P.aq || !P.aqs || !params_dev)
     return fail(MTG_ERR_NOMEM, "step kernel buffers");
-  if ((rc = check(hipMemcpy(table_dev, table.data(), table.size() * sizeof(LayerDev),
-                            hipMemcpyHostToDevice), "layer table")) ||
-      (rc = check(hipMemcpy(params_dev, &P, sizeof(P), hipMemcpyHostToDevice), "step params")))
+  if ((rc = check(hipMemcpy(params_dev, &P, sizeof(P), hipMemcpyHostToDevice), "step params")))
     return rc;
   params_host = P;
   step_ok = true;

@@ -90,6 +90,11 @@ __device__ __forceinline__ void gst(void* p, T v) { *(MTG_GLOBAL T*)p = v; }
 __device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 
+// Layer l's pointers (scalar loads from the parameter block; a read through a
+// generic pointer would be a flat load, and every use of it would wait for all
+// vector loads in flight, the prefetched weights included).
+__device__ __forceinline__ const LayerDev& layer_at(const StepParams& P, int l) { return P.layer[l]; }
+
 struct Ctl {
   const StepParams* P;
   uint32_t epoch;
@@ -102,9 +107,9 @@ __device__ __forceinline__ void publish(Ctl& c, uint32_t v) {
   if (v <= c.published) return;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   bar();
-  if (threadIdx.x == 0)
-    __hip_atomic_store(c.P->flags + blockIdx.x * kFlagStride, c.epoch + v, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0)  // device-coherent buffer store: no LDS-counter wait covers it
+    __builtin_amdgcn_raw_buffer_store_b32(c.epoch + v, mk_rsrc(c.P->flags, kNwg * kFlagStride * 4),
+                                          blockIdx.x * kFlagStride * 4, 0, 16);
   c.published = v;
 }
 
@@ -113,7 +118,7 @@ __device__ __forceinline__ void publish(Ctl& c, uint32_t v) {
 __device__ __forceinline__ bool wait_all(Ctl& c, uint32_t v, int prof_slot = -1) {
   const StepParams& P = *c.P;
   if (threadIdx.x < 64) {
-    if (prof_slot >= 0 && P.timing && threadIdx.x == 0) P.timing[prof_slot] = wall_clock64();
+    if (prof_slot >= 0 && P.timing && threadIdx.x == 0) gst<uint64_t>(P.timing + prof_slot, wall_clock64());
     const int lane = threadIdx.x;
     const Rsrc rf = mk_rsrc(P.flags, kNwg * kFlagStride * 4);
     const Rsrc re = mk_rsrc(P.err, 4);
@@ -146,7 +151,7 @@ __device__ __forceinline__ bool wait_all(Ctl& c, uint32_t v, int prof_slot = -1)
       }
       __builtin_amdgcn_s_sleep(1);
     }
-    if (prof_slot >= 0 && P.timing && lane == 0) P.timing[prof_slot + 1] = spins;
+    if (prof_slot >= 0 && P.timing && lane == 0) gst<uint64_t>(P.timing + prof_slot + 1, (uint64_t)spins);
     if (lane == 0) *c.s_ok = ok;
   }
   bar();
@@ -154,11 +159,12 @@ __device__ __forceinline__ bool wait_all(Ctl& c, uint32_t v, int prof_slot = -1)
 }
 
 __device__ __forceinline__ void mark(const StepParams& P, int slot) {
-  if (P.timing && blockIdx.x == 0 && threadIdx.x == 0) P.timing[slot] = wall_clock64();
+  if (P.timing && blockIdx.x == 0 && threadIdx.x == 0) gst<uint64_t>(P.timing + slot, wall_clock64());
 }
-// every workgroup's marks of one layer: slots 1024 + 16 w + k
+// every workgroup's marks of one layer: slots 1024 + 32 w + k
+__device__ __forceinline__ int wslot(int w, int k) { return 1024 + 32 * w + k; }
 __device__ __forceinline__ void wmark(const StepParams& P, int l, int k) {
-  if (P.timing && l == 1 && threadIdx.x == 0) P.timing[1024 + 16 * blockIdx.x + k] = wall_clock64();
+  if (P.timing && l == 1 && threadIdx.x == 0) gst<uint64_t>(P.timing + wslot(blockIdx.x, k), wall_clock64());
 }
 
 // ----------------------------------------------------------- weight tiles ---
@@ -221,7 +227,7 @@ enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 template <int G, int NM, int EPI>
 __device__ __forceinline__ void gemm_finish(float acc[NM][G][4], float* red, Rsrc out, int n,
                                             int tile, int T) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -239,7 +245,7 @@ __device__ __forceinline__ void gemm_finish(float acc[NM][G][4], float* red, Rsr
           float s = red[((0 * NM + m) * G * 4 + cg * 4 + q) * 64 + lane];
 #pragma unroll
           for (int wv = 1; wv < 4; ++wv) s = __fadd_rn(s, red[((wv * NM + m) * G * 4 + cg * 4 + q) * 64 + lane]);
-          acc[m][cg][q] = __fadd_rn(s, lane_xor_f<8>(s));
+          acc[m][cg][q] = __fadd_rn(s, dpp_f<kDppRor8>(s));
         }
     if ((lane & 15) < 8) {
 #pragma unroll
@@ -274,7 +280,7 @@ __device__ __forceinline__ void gemm_finish(float acc[NM][G][4], float* red, Rsr
 template <int G>
 __device__ __forceinline__ void gu_finish(float acc[4][G][4], float* red, const StepParams& P, int j,
                                           int T) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
 #pragma unroll
   for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -292,7 +298,7 @@ __device__ __forceinline__ void gu_finish(float acc[4][G][4], float* red, const 
           float s = red[((0 * 4 + m) * G * 4 + cg * 4 + q) * 64 + lane];
 #pragma unroll
           for (int wv = 1; wv < 4; ++wv) s = __fadd_rn(s, red[((wv * 4 + m) * G * 4 + cg * 4 + q) * 64 + lane]);
-          acc[m][cg][q] = __fadd_rn(s, lane_xor_f<8>(s));
+          acc[m][cg][q] = __fadd_rn(s, dpp_f<kDppRor8>(s));
         }
     const Rsrc rq = mk_rsrc(P.aq, kMaxRows * cF);
     const Rsrc rs = mk_rsrc(P.aqs, kMaxRows * (cF / 32) * 4);
@@ -306,8 +312,7 @@ __device__ __forceinline__ void gu_finish(float acc[4][G][4], float* red, const 
         amax = fmaxf(amax, fmaxf(fabsf(va[q]), fabsf(vb[q])));
       }
       // the block's 32 rows sit in lanes (lane & 15) + 16 m, m = 0..3
-      amax = fmaxf(amax, lane_xor_f<16>(amax));
-      amax = fmaxf(amax, lane_xor_f<32>(amax));
+      amax = __uint_as_float(pair_max_u<32>(pair_max_u<16>(__float_as_uint(amax))));
       const int t = cg * 8 + (lane & 7);
       if ((lane & 15) < 8 && t < T) {
         uint32_t pa = 0, pb = 0;
@@ -334,7 +339,7 @@ __device__ __forceinline__ void quant16(const float v[16], int t, int kc, int bp
   float amax = 0.0f;
 #pragma unroll
   for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(v[e]));
-  amax = fmaxf(amax, lane_xor_f<1>(amax));
+  amax = __uint_as_float(max(__float_as_uint(amax), dpp_u<kDppQuadXor1>(__float_as_uint(amax))));
   const float d = __fdiv_rn(amax, 127.0f);
   const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
   uint32_t packed[4];
@@ -360,7 +365,7 @@ __device__ __forceinline__ void quant16(const float v[16], int t, int kc, int bp
 // holds elements 16l..16l+15. normed_out (nullable): the f32 rows.
 __device__ void panel_norm(Rsrc x, int T, const float* __restrict__ gain, float eps, uint8_t* pcodes,
                            float* pscales, float* normed_out) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   float gv[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -529,12 +534,85 @@ __device__ __forceinline__ float kv_val(uint32_t bits, bool f16) {
   return f16 ? half_bits_to_float((uint16_t)bits) : __uint_as_float(bits);
 }
 
+// One staging pass of an attention item: wave `wave` takes rows r0 + 4 j,
+// j < NS (q rows, then the new k rows, then the new v rows), loads them all,
+// then norms (q, k) and ropes them side by side, writes them to LDS and, for the
+// workgroup that appends, the new k / v rows to the KV cache. Straight-line over
+// the NS slots; slots past the rows compute on zeros and store nothing.
+template <int NS>
+__device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& Ly, int T, int past, int g,
+                                           int r0, int nrows, bool appender, float* q_lds, float* knew,
+                                           float* vnew) {
+  const int lane = threadIdx.x & 63, ncol = 2 * T;
+  const bool f16kv = P.kv_f16 != 0;
+  const Rsrc rq = mk_rsrc(P.qkv, kMaxRows * cNQKV * 4);
+  float x0[NS], x1[NS], g0[NS], g1[NS], rc[NS], rs[NS];
+  int kind[NS], tt[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const int r = r0 + 4 * j;
+    kind[j] = r < ncol ? 0 : (r < ncol + T ? 1 : 2);
+    tt[j] = kind[j] == 0 ? r % T : (kind[j] == 1 ? r - ncol : r - ncol - T);
+    x0[j] = x1[j] = g0[j] = g1[j] = rc[j] = rs[j] = 0.0f;
+    if (r < nrows) {
+      const int col = kind[j] == 0 ? (2 * g + r / T) * cHD
+                                   : (kind[j] == 1 ? (cNH + g) * cHD : (cNH + cNKV + g) * cHD);
+      const uint32_t base = (uint32_t)((tt[j] * cNQKV + col) * 4);
+      x0[j] = ldc1(rq, base + lane * 4);
+      x1[j] = ldc1(rq, base + (lane + 64) * 4);
+      if (kind[j] < 2) {
+        const float* gn = kind[j] == 0 ? Ly.q_norm : Ly.k_norm;
+        g0[j] = gld<float>(gn + lane);
+        g1[j] = gld<float>(gn + lane + 64);
+        const v2f cs = gld<v2f>(P.rope + (size_t)(past + tt[j]) * cHD + 2 * lane);
+        rc[j] = cs.x;
+        rs[j] = cs.y;
+      }
+    }
+  }
+  double sq[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) sq[j] = (double)__fmul_rn(x0[j], x0[j]) + (double)__fmul_rn(x1[j], x1[j]);
+  wave_sum_d_n<NS>(sq);
+  float y0[NS], y1[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const float scale = dev_rms_scale((float)(sq[j] / (double)cHD), P.eps);
+    const float n0 = __fmul_rn(__fmul_rn(x0[j], scale), g0[j]);
+    const float n1 = __fmul_rn(__fmul_rn(x1[j], scale), g1[j]);
+    y0[j] = __fsub_rn(__fmul_rn(n0, rc[j]), __fmul_rn(n1, rs[j]));
+    y1[j] = __fadd_rn(__fmul_rn(n0, rs[j]), __fmul_rn(n1, rc[j]));
+  }
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const int r = r0 + 4 * j, t = tt[j];
+    if (r >= nrows) break;
+    const float a0 = kind[j] < 2 ? y0[j] : x0[j], a1 = kind[j] < 2 ? y1[j] : x1[j];
+    if (kind[j] > 0 && appender) {
+      const size_t off = ((size_t)g * P.max_seq + past + t) * cHD;
+      uint8_t* cache = kind[j] == 1 ? Ly.kc : Ly.vc;
+      if (f16kv) {
+        gst<uint16_t>((uint16_t*)cache + off + lane, __half_as_ushort(__float2half_rn(a0)));
+        gst<uint16_t>((uint16_t*)cache + off + lane + 64, __half_as_ushort(__float2half_rn(a1)));
+      } else {
+        gst<float>((float*)cache + off + lane, a0);
+        gst<float>((float*)cache + off + lane + 64, a1);
+      }
+    }
+    float* dst = kind[j] == 0 ? q_lds + r * cQStride : (kind[j] == 1 ? knew : vnew) + t * cQStride;
+    dst[lane] = f16kv ? f16_round(a0) : a0;
+    dst[lane + 64] = f16kv ? f16_round(a1) : a1;
+  }
+}
+
 // One attention item: chunk `chunk` of kv head g over the ncol = 2T query
 // columns (col = hl*T + t for q head 2g + hl). LDS: q [32][132], knew/vnew
 // [16][132], sp [32][68].
+template <int G>
 __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& Ly, int T, int past, int g, int chunk,
-                          const KvRegs& kv, uint8_t* lds, bool prof) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kl = lane & 15, kk = lane >> 4;
+                                          const KvRegs& kv, uint8_t* lds, bool prof) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, kl = lane & 15,
+            kk = lane >> 4;
   const bool f16kv = P.kv_f16 != 0;
   const int kvlen = past + T, ncol = 2 * T, key0 = chunk * kChunk;
   float* q_lds = (float*)lds;
@@ -543,66 +621,18 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   float* sp = vnew + kMaxRows * cQStride;
   const bool has_new = key0 + kChunk > past;
   const bool appender = key0 <= past && past < key0 + kChunk;
-  const Rsrc rq = mk_rsrc(P.qkv, kMaxRows * cNQKV * 4);
   // 1. stage the roped q rows and, if this chunk reaches them, the new k / v rows
-  //    (per wave up to four rows at a time, every load issued before the math)
+  //    (q rows: 4G per wave; with the new rows up to 8 per wave and pass)
   const int nrows = ncol + (has_new ? 2 * T : 0);
-  for (int r0 = wave; r0 < nrows; r0 += 16) {
-    float x0[4], x1[4], g0[4], g1[4], rc[4], rs[4];
-    int kind[4], tt[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = r0 + 4 * j;
-      kind[j] = r < ncol ? 0 : (r < ncol + T ? 1 : 2);
-      tt[j] = kind[j] == 0 ? r % T : (kind[j] == 1 ? r - ncol : r - ncol - T);
-      if (r < nrows) {
-        const int col = kind[j] == 0 ? (2 * g + r / T) * cHD
-                                     : (kind[j] == 1 ? (cNH + g) * cHD : (cNH + cNKV + g) * cHD);
-        const uint32_t base = (uint32_t)((tt[j] * cNQKV + col) * 4);
-        x0[j] = ldc1(rq, base + lane * 4);
-        x1[j] = ldc1(rq, base + (lane + 64) * 4);
-        if (kind[j] < 2) {
-          const float* gn = kind[j] == 0 ? Ly.q_norm : Ly.k_norm;
-          g0[j] = gld<float>(gn + lane);
-          g1[j] = gld<float>(gn + lane + 64);
-          const v2f cs = gld<v2f>(P.rope + (size_t)(past + tt[j]) * cHD + 2 * lane);
-          rc[j] = cs.x;
-          rs[j] = cs.y;
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = r0 + 4 * j, t = tt[j];
-      if (r >= nrows) break;
-      float a0 = x0[j], a1 = x1[j];
-      if (kind[j] < 2) {
-        double sq = (double)__fmul_rn(a0, a0) + (double)__fmul_rn(a1, a1);
-        sq = wave_sum_d(sq);
-        const float scale = dev_rms_scale((float)(sq / (double)cHD), P.eps);
-        const float y0 = __fmul_rn(__fmul_rn(a0, scale), g0[j]);
-        const float y1 = __fmul_rn(__fmul_rn(a1, scale), g1[j]);
-        a0 = __fsub_rn(__fmul_rn(y0, rc[j]), __fmul_rn(y1, rs[j]));
-        a1 = __fadd_rn(__fmul_rn(y0, rs[j]), __fmul_rn(y1, rc[j]));
-      }
-      if (kind[j] > 0 && appender) {
-        const size_t off = ((size_t)g * P.max_seq + past + t) * cHD;
-        uint8_t* cache = kind[j] == 1 ? Ly.kc : Ly.vc;
-        if (f16kv) {
-          gst<uint16_t>((uint16_t*)cache + off + lane, __half_as_ushort(__float2half_rn(a0)));
-          gst<uint16_t>((uint16_t*)cache + off + lane + 64, __half_as_ushort(__float2half_rn(a1)));
-        } else {
-          gst<float>((float*)cache + off + lane, a0);
-          gst<float>((float*)cache + off + lane + 64, a1);
-        }
-      }
-      float* dst = kind[j] == 0 ? q_lds + r * cQStride : (kind[j] == 1 ? knew : vnew) + t * cQStride;
-      dst[lane] = f16kv ? f16_round(a0) : a0;
-      dst[lane + 64] = f16kv ? f16_round(a1) : a1;
-    }
+  if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 21); }
+  if (!has_new) {
+    stage_pass<4 * G>(P, Ly, T, past, g, wave, nrows, appender, q_lds, knew, vnew);
+  } else {
+    for (int r0 = wave; r0 < nrows; r0 += 32)
+      stage_pass<8>(P, Ly, T, past, g, r0, nrows, appender, q_lds, knew, vnew);
   }
   bar();
-  if (prof) mark(P, 510);
+  if (prof) wmark(P, 1, 16);
   // 2. operands: prefetched cache rows, new rows from LDS, zeros past kvlen
   float ka[32], vb[2][16];
 #pragma unroll
@@ -624,7 +654,7 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
         if (vk >= past) vb[h][s] = vk < kvlen ? vnew[(vk - past) * cQStride + 16 * (2 * wave + h) + kl] : 0.0f;
       }
   }
-  if (prof) { bar(); mark(P, 511); }
+  if (prof) { bar(); wmark(P, 1, 17); }
   // 3. scores S[key][col] = fma chain over head_dim, scaled and masked -> sp
   const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)cHD));
   for (int ct = 0; ct * 16 < ncol; ++ct) {
@@ -645,24 +675,44 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
     }
   }
   bar();
-  if (prof) mark(P, 512);
+  if (prof) wmark(P, 1, 18);
   // 4. chunk softmax per column (one wave per column, lane = key)
   const size_t pi = (size_t)g * P.max_chunks + chunk;
   const Rsrc rml = mk_rsrc(P.part_ml + pi * kMaxCols * 2, kMaxCols * 2 * 4);
-  for (int col = wave; col < ncol; col += 4) {
-    const float w = sp[col * cPStride + lane];
-    const float m = wave_max_f(w);
-    float p = (m == -INFINITY || w == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(w, m));
+  // this wave's columns wave + 4 i (i < 4G) side by side; the max runs on
+  // order-preserving integer keys of the scores (no NaN here; the sign of a zero
+  // maximum does not change any exp(w - m))
+  constexpr int kCols = 4 * G;
+  float wv[kCols], lv[kCols];
+  int mk[kCols];
+#pragma unroll
+  for (int i = 0; i < kCols; ++i) {
+    const int col = wave + 4 * i;
+    wv[i] = col < ncol ? sp[col * cPStride + lane] : -INFINITY;
+    mk[i] = ord_key(wv[i]);
+  }
+  wave_max_i_n<kCols>(mk);
+#pragma unroll
+  for (int i = 0; i < kCols; ++i) {
+    const float m = ord_val(mk[i]);
+    float p = (m == -INFINITY || wv[i] == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(wv[i], m));
     if (f16kv) p = f16_round(p);
-    const float l = wave_sum_f(p);
-    sp[col * cPStride + lane] = p;
+    wv[i] = p;
+    lv[i] = p;
+  }
+  wave_sum_f_n<kCols>(lv);
+#pragma unroll
+  for (int i = 0; i < kCols; ++i) {
+    const int col = wave + 4 * i;
+    if (col >= ncol) break;
+    sp[col * cPStride + lane] = wv[i];
     if (lane == 0) {
-      stc1(rml, (uint32_t)(col * 2 * 4), m);
-      stc1(rml, (uint32_t)((col * 2 + 1) * 4), l);
+      stc1(rml, (uint32_t)(col * 2 * 4), ord_val(mk[i]));
+      stc1(rml, (uint32_t)((col * 2 + 1) * 4), lv[i]);
     }
   }
   bar();
-  if (prof) mark(P, 513);
+  if (prof) wmark(P, 1, 19);
   // 5. O[col][d] = fma chain over the chunk's keys of p * v
   const Rsrc ro = mk_rsrc(P.part_o + pi * kMaxCols * cHD, kMaxCols * cHD * 4);
   for (int ct = 0; ct * 16 < ncol; ++ct) {
@@ -684,7 +734,7 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
     }
   }
   bar();
-  if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); mark(P, 514); }
+  if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 20); }
 }
 
 // Merge the chunk partials of (q head hq, row t) in chunk order; 128 threads,
@@ -736,12 +786,7 @@ __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, 
   }
   if (valid) out = __fdiv_rn(O, L);
   // q8_0 blocks of 32 consecutive d (32 lanes of one wave)
-  float amax = fabsf(out);
-  amax = fmaxf(amax, lane_xor_f<1>(amax));
-  amax = fmaxf(amax, lane_xor_f<2>(amax));
-  amax = fmaxf(amax, lane_xor_f<4>(amax));
-  amax = fmaxf(amax, lane_xor_f<8>(amax));
-  amax = fmaxf(amax, lane_xor_f<16>(amax));
+  const float amax = group32_max_nonneg(fabsf(out));
   if (valid) {
     const Rsrc rq = mk_rsrc(P.oq, kMaxRows * cQN);
     const Rsrc rs = mk_rsrc(P.oqs, kMaxRows * (cQN / 32) * 4);
@@ -829,7 +874,7 @@ __device__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const 
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             float v = __fadd_rn(__fadd_rn(__fadd_rn(part[0][cg][q], part[1][cg][q]), part[2][cg][q]), part[3][cg][q]);
-            v = __fadd_rn(v, lane_xor_f<8>(v));
+            v = __fadd_rn(v, dpp_f<kDppRor8>(v));
             part[0][cg][q] = v;
           }
         if ((lane & 15) < 8) {
@@ -981,11 +1026,11 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   }
   publish(c, 1);
   // prefetch layer 0: q|k|v tile and the first attention item's K / V
-  wt_load<4>(P.layers[0].wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-  if (has_attn) kv_prefetch(P.layers[0], P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+  wt_load<4>(layer_at(P, 0).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+  if (has_attn) kv_prefetch(layer_at(P, 0), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
 
   for (int l = 0; l < L; ++l) {
-    const LayerDev& Ly = P.layers[l];
+    const LayerDev& Ly = layer_at(P, l);
     // ---- QKV: tile w ----
     if (!wait_all(c, ph(l, kPhQkv) - 1)) return;
     mark(P, 3 + 12 * l + 0);
@@ -1002,12 +1047,12 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     if (od) wt_load<8>(Ly.wo + (size_t)w * cBQ * kUnitBytes, 8 * wave, ba, bs);
     // ---- ATTN: items of this workgroup ----
     if (has_attn) {
-      if (!wait_all(c, ph(l, kPhAttn) - 1, l == 1 ? 1024 + 16 * w + 14 : -1)) return;
+      if (!wait_all(c, ph(l, kPhAttn) - 1, l == 1 ? wslot(w, 14) : -1)) return;
       mark(P, 3 + 12 * l + 2);
       wmark(P, l, 2);
       for (int item = first_item; item < n_items; item += kNwg) {
         if (item != first_item) kv_prefetch(Ly, P, item / nch, (item % nch) * kChunk, past, kv);
-        attn_item(P, Ly, T, past, item / nch, item % nch, kv, lds, l == 1);
+        attn_item<G>(P, Ly, T, past, item / nch, item % nch, kv, lds, l == 1 && P.timing != nullptr);
       }
       publish(c, next_done(l, kPhAttn));
       mark(P, 3 + 12 * l + 3);
@@ -1033,14 +1078,14 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       publish(c, next_done(l, kPhMerge));
       wmark(P, l, 5);
       if (!gu && l + 1 < L) {  // nothing more in this layer: prefetch the next one
-        const LayerDev& Ln = P.layers[l + 1];
+        const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
         if (has_attn) kv_prefetch(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
       }
     }
     // ---- O-proj: x += W_o o ----
     if (od) {
-      if (!wait_all(c, ph(l, kPhO) - 1, l == 1 ? 1024 + 16 * w + 12 : -1)) return;
+      if (!wait_all(c, ph(l, kPhO) - 1, l == 1 ? wslot(w, 12) : -1)) return;
       mark(P, 3 + 12 * l + 4);
       wmark(P, l, 6);
       panel_from_q<cQN>(P.oq, P.oqs, T, pcodes, pscales);
@@ -1053,11 +1098,11 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       wt_load<12>(Ly.wd + (size_t)w * cBF * kUnitBytes, 12 * wave, ba, bs);
       // the next layer's attention K / V, so that they are in flight before the down wait
       if (has_attn && l + 1 < L)
-        kv_prefetch(P.layers[l + 1], P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+        kv_prefetch(layer_at(P, l + 1), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
     }
     // ---- GATE/UP: act = silu(g) * u, as q8_0 blocks ----
     if (gu) {
-      if (!wait_all(c, ph(l, kPhGu) - 1, l == 1 ? 1024 + 16 * w + 12 : -1)) return;
+      if (!wait_all(c, ph(l, kPhGu) - 1, l == 1 ? wslot(w, 12) : -1)) return;
       wmark(P, l, 8);
       panel_norm(RX, T, Ly.ffn_norm, P.eps, pcodes, pscales, nullptr);
       float acc[4][G][4] = {};
@@ -1067,7 +1112,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       publish(c, next_done(l, kPhGu));
       wmark(P, l, 9);
       if (l + 1 < L) {
-        const LayerDev& Ln = P.layers[l + 1];
+        const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
         if (has_attn) kv_prefetch(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
       }
@@ -1084,11 +1129,11 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       publish(c, next_done(l, kPhD));
       mark(P, 3 + 12 * l + 7);
       wmark(P, l, 11);
-      if (l + 1 < L) wt_load<4>(P.layers[l + 1].wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+      if (l + 1 < L) wt_load<4>(layer_at(P, l + 1).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
     }
     // workgroups with only q|k|v and attention work
     if (!od && !gu && !has_merge && l + 1 < L) {
-      const LayerDev& Ln = P.layers[l + 1];
+      const LayerDev& Ln = layer_at(P, l + 1);
       wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
       if (has_attn) kv_prefetch(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
     }
@@ -1123,9 +1168,9 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
 }  // namespace
 
 int step_kernel_supported(int hidden, int n_heads, int n_kv_heads, int head_dim, int intermediate,
-                          int cus) {
+                          int n_layers, int cus) {
   return hidden == cH && n_heads == cNH && n_kv_heads == cNKV && head_dim == cHD &&
-         intermediate == cF && cus >= kNwg;
+         intermediate == cF && n_layers >= 1 && n_layers <= kStepMaxLayers && cus >= kNwg;
 }
 
 int step_kernel_workgroups() { return kNwg; }

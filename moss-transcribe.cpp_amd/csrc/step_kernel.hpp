@@ -18,11 +18,16 @@ struct LayerDev {
   uint8_t *kc, *vc;                          // KV cache of the layer
 };
 
+// Layers the step kernel's parameter block holds.
+constexpr int kStepMaxLayers = 48;
+
 // Constant for a context; lives in device memory.
 struct StepParams {
   int H, NH, NKV, F, V, L, max_seq, kv_f16, max_chunks;
   float eps;
-  const LayerDev* layers;
+  // The layer table sits inside the block: the kernel reads the block through a
+  // const restrict argument, so these pointers come in with scalar loads.
+  LayerDev layer[kStepMaxLayers];
   const uint8_t* embd;
   const float* out_norm;
   const float* rope;
@@ -45,7 +50,7 @@ struct StepParams {
 // workgroups with fixed, prefetching roles; step_kernel.hip). Progress words
 // advance by step_progress_per_step per launch.
 int step_kernel_supported(int hidden, int n_heads, int n_kv_heads, int head_dim, int intermediate,
-                          int cus);
+                          int n_layers, int cus);
 int step_kernel_workgroups();
 // Words between two workgroups' progress words: each word owns a 128-byte line,
 // so a publish does not contend with the polls of its neighbours' words.

@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(HERE, "libmtg.so")
 
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K = 0, 1, 8, 12
 EXEC_STEP_KERNEL, EXEC_GRAPH, EXEC_EAGER = 0, 1, 2
+PROFILE_SLOTS = 9216  # MTG_PROFILE_SLOTS
 MAX_BATCH = 16
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_DEVICE, ERR_CAPACITY, ERR_NOMEM, ERR_STATE = 0, -1, -2, -3, -4, -5, -6
 
@@ -261,8 +262,8 @@ class Decoder:
         return ms.value, n.value, ps.value, rs.value
 
     def step_marks(self):
-        out = np.zeros(8192, np.uint64)
-        n = lib().mtg_step_profile_read(self.ctx, ptr(out), 8192)
+        out = np.zeros(PROFILE_SLOTS, np.uint64)
+        n = lib().mtg_step_profile_read(self.ctx, ptr(out), PROFILE_SLOTS)
         return out[:n].astype(np.int64)
 
     @property
