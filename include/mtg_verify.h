@@ -252,7 +252,7 @@ int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes);
  * 0 at the start; for layer l at 3 + 12 l + {0, 1}: QKV inputs ready / QKV
  * published, {2, 3}: attention, {4, 5}: o-proj, {6, 7}: down (when workgroup 0
  * has those roles); at 3 + 12 L the lm_head start, + 1 its end, + 2 / + 3 the
- * acceptance (verify steps). Every workgroup w, layer 1, slots 1024 + 32 w + k:
+ * acceptance (verify steps), + 4 its keys loaded, + 5 its choices reduced. Every workgroup w, layer 1, slots 1024 + 32 w + k:
  * k = 0..11 ready / published of QKV, attention, merge, o-proj, gate-up, down;
  * 12 / 13 first poll and poll count of the o-proj or gate-up wait, 14 / 15 of the
  * attention wait; 16..23 the attention item's stages. mtg_step_profile_read

@@ -438,6 +438,26 @@ __device__ __forceinline__ void wave_max_i_n(int* v) {
   for (int i = 0; i < N; ++i) v[i] = max(v[i], (int)dpp_u<kDppRor1>((uint32_t)v[i]));
 }
 
+// max of a 64-bit key over the wave (exact in any order); both halves take the
+// same lane moves, so each pair of halves stays one lane's key
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  uint32_t alo, blo, ahi, bhi;
+  pair_split<32>((uint32_t)v, alo, blo);
+  pair_split<32>((uint32_t)(v >> 32), ahi, bhi);
+  v = max(((uint64_t)ahi << 32) | alo, ((uint64_t)bhi << 32) | blo);
+  pair_split<16>((uint32_t)v, alo, blo);
+  pair_split<16>((uint32_t)(v >> 32), ahi, bhi);
+  v = max(((uint64_t)ahi << 32) | alo, ((uint64_t)bhi << 32) | blo);
+  uint64_t o = ((uint64_t)dpp_u<kDppRor8>((uint32_t)(v >> 32)) << 32) | dpp_u<kDppRor8>((uint32_t)v);
+  v = max(v, o);
+  o = ((uint64_t)dpp_u<kDppRor4>((uint32_t)(v >> 32)) << 32) | dpp_u<kDppRor4>((uint32_t)v);
+  v = max(v, o);
+  o = ((uint64_t)dpp_u<kDppRor2>((uint32_t)(v >> 32)) << 32) | dpp_u<kDppRor2>((uint32_t)v);
+  v = max(v, o);
+  o = ((uint64_t)dpp_u<kDppRor1>((uint32_t)(v >> 32)) << 32) | dpp_u<kDppRor1>((uint32_t)v);
+  return max(v, o);
+}
+
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   uint32_t a, b;
   pair_split<32>(v, a, b);

@@ -56,6 +56,16 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
+// A pointer the whole wave shares, moved to scalar registers (a value that came
+// through a generic load or a call argument sits in vector registers, and a
+// buffer descriptor built from it would make every load a loop over lanes).
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t u = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return (T*)(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ Rsrc mk_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
 }
@@ -536,13 +546,12 @@ __device__ __forceinline__ float kv_val(uint32_t bits, bool f16) {
 
 // One staging pass of an attention item: wave `wave` takes rows r0 + 4 j,
 // j < NS (q rows, then the new k rows, then the new v rows), loads them all,
-// then norms (q, k) and ropes them side by side, writes them to LDS and, for the
-// workgroup that appends, the new k / v rows to the KV cache. Straight-line over
-// the NS slots; slots past the rows compute on zeros and store nothing.
+// then norms (q, k) and ropes them side by side and writes them to LDS.
+// Straight-line over the NS slots; slots past the rows compute on zeros and store
+// nothing.
 template <int NS>
 __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& Ly, int T, int past, int g,
-                                           int r0, int nrows, bool appender, float* q_lds, float* knew,
-                                           float* vnew) {
+                                           int r0, int nrows, float* q_lds, float* knew, float* vnew) {
   const int lane = threadIdx.x & 63, ncol = 2 * T;
   const bool f16kv = P.kv_f16 != 0;
   const Rsrc rq = mk_rsrc(P.qkv, kMaxRows * cNQKV * 4);
@@ -588,17 +597,6 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
     const int r = r0 + 4 * j, t = tt[j];
     if (r >= nrows) break;
     const float a0 = kind[j] < 2 ? y0[j] : x0[j], a1 = kind[j] < 2 ? y1[j] : x1[j];
-    if (kind[j] > 0 && appender) {
-      const size_t off = ((size_t)g * P.max_seq + past + t) * cHD;
-      uint8_t* cache = kind[j] == 1 ? Ly.kc : Ly.vc;
-      if (f16kv) {
-        gst<uint16_t>((uint16_t*)cache + off + lane, __half_as_ushort(__float2half_rn(a0)));
-        gst<uint16_t>((uint16_t*)cache + off + lane + 64, __half_as_ushort(__float2half_rn(a1)));
-      } else {
-        gst<float>((float*)cache + off + lane, a0);
-        gst<float>((float*)cache + off + lane + 64, a1);
-      }
-    }
     float* dst = kind[j] == 0 ? q_lds + r * cQStride : (kind[j] == 1 ? knew : vnew) + t * cQStride;
     dst[lane] = f16kv ? f16_round(a0) : a0;
     dst[lane + 64] = f16kv ? f16_round(a1) : a1;
@@ -626,10 +624,10 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   const int nrows = ncol + (has_new ? 2 * T : 0);
   if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 21); }
   if (!has_new) {
-    stage_pass<4 * G>(P, Ly, T, past, g, wave, nrows, appender, q_lds, knew, vnew);
+    stage_pass<4 * G>(P, Ly, T, past, g, wave, nrows, q_lds, knew, vnew);
   } else {
     for (int r0 = wave; r0 < nrows; r0 += 32)
-      stage_pass<8>(P, Ly, T, past, g, r0, nrows, appender, q_lds, knew, vnew);
+      stage_pass<8>(P, Ly, T, past, g, r0, nrows, q_lds, knew, vnew);
   }
   bar();
   if (prof) wmark(P, 1, 16);
@@ -733,6 +731,19 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
       }
     }
   }
+  // 6. the appending workgroup writes this step's k / v rows to the KV cache from
+  //    the staged rows (for an f16 cache they are f16 values already). Issued
+  //    last, so that no wait for the prefetched K / V above also waits for them.
+  if (appender) {
+    for (int i = threadIdx.x; i < 2 * T * cHD; i += kT) {
+      const int r = i / cHD, d = i % cHD, t = r % T;
+      const float v = (r < T ? knew : vnew)[t * cQStride + d];
+      const size_t off = ((size_t)g * P.max_seq + past + t) * cHD + d;
+      uint8_t* cache = r < T ? Ly.kc : Ly.vc;
+      if (f16kv) gst<uint16_t>((uint16_t*)cache + off, __half_as_ushort(__float2half_rn(v)));
+      else gst<float>((float*)cache + off, v);
+    }
+  }
   bar();
   if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 20); }
 }
@@ -802,13 +813,24 @@ __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, 
 template <int G>
 __device__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const uint8_t* pcodes,
                         const float* pscales, uint64_t* s_best) {
+  // a called function receives P's fields and T in vector registers: make the
+  // tile arithmetic wave-uniform again, or every buffer load with a scalar
+  // offset becomes a loop over its distinct values
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int V = P.V, n_tiles = V / 16, gw = blockIdx.x * 4 + wave, nwaves = gridDim.x * 4;
+  T = __builtin_amdgcn_readfirstlane(T);
+  const int V = __builtin_amdgcn_readfirstlane(P.V), n_tiles = V / 16, gw = blockIdx.x * 4 + wave,
+            nwaves = gridDim.x * 4;
   const bool pen = desc->penalty > 1.0f;
   const float penalty = desc->penalty;
   const int words = (V + 31) / 32;
   const bool write_logits = desc->write_logits != 0;
-  const Rsrc rb = mk_rsrc(P.bitmap, (uint32_t)(kMaxRows * words * 4));
+  float* const logits = uniform_ptr(P.logits);
+  const Rsrc rb = mk_rsrc(uniform_ptr(P.bitmap), (uint32_t)(kMaxRows * words * 4));
+  // the penalty bits of a tile's 16 rows share one word per verify row; it is
+  // loaded with the tile's first unit and used at its last
+  uint32_t pword[G];
+#pragma unroll
+  for (int cg = 0; cg < G; ++cg) pword[cg] = 0;
   const int srow = ((lane & 15) >> 3) * 16 + 4 * (lane >> 4);
   const v4i zero = {0, 0, 0, 0};
   uint64_t best[G];
@@ -819,25 +841,40 @@ __device__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const 
   constexpr int R = 8;
   v4i ra[R];
   uint2 rs[R];
-  const Rsrc re = mk_rsrc(P.embd, (uint32_t)((size_t)n_tiles * cBH * kUnitBytes));
+  const Rsrc re = mk_rsrc(uniform_ptr(P.embd), (uint32_t)((size_t)n_tiles * cBH * kUnitBytes));
+  // Every slot is refilled unconditionally, so each ring slot keeps its registers
+  // and only its own load is waited for. A unit past this wave's last one gets
+  // a per-lane offset past the buffer's end (the range check covers the per-lane
+  // offset, not the scalar one): zeros, no memory traffic, never used.
   auto issue = [&](int u, int slot) {
+    const bool in = u < units;
     const int tile = gw + (u / cBH) * nwaves, bp = u % cBH;
-    const int so = (tile * cBH + bp) * kUnitBytes;
-    ra[slot] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(re, lane * 16, so, 2));
-    const v2u sv = __builtin_amdgcn_raw_buffer_load_b64(re, 1024 + srow * 2, so, 2);
+    const int so = in ? (tile * cBH + bp) * kUnitBytes : 0;
+    const uint32_t gone = 0x80000000u;
+    ra[slot] = __builtin_bit_cast(
+        v4i, __builtin_amdgcn_raw_buffer_load_b128(re, in ? (uint32_t)(lane * 16) : gone, so, 2));
+    const v2u sv = __builtin_amdgcn_raw_buffer_load_b64(re, in ? (uint32_t)(1024 + srow * 2) : gone, so, 2);
     rs[slot] = make_uint2(sv.x, sv.y);
   };
 #pragma unroll
-  for (int i = 0; i < R; ++i)
-    if (i < units) issue(i, i);
+  for (int i = 0; i < R; ++i) issue(i, i);
   float part[4][G][4];
+  // units is a multiple of cBH, and cBH of R: a pass of R units is whole
+  static_assert(cBH % R == 0, "ring depth divides the pairs of a tile");
   for (int u0 = 0; u0 < units; u0 += R) {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int u = u0 + i;
-      if (u >= units) break;
       const int bp = u % cBH, sl = bp >> 2;
       if (bp == 0) {
+        if (pen) {
+          const int tile = gw + (u / cBH) * nwaves;
+#pragma unroll
+          for (int cg = 0; cg < G; ++cg) {
+            const int t = min(cg * 8 + (lane & 7), T - 1);
+            pword[cg] = __builtin_amdgcn_raw_buffer_load_b32(rb, (t * words + (tile >> 1)) * 4, 0, 16);
+          }
+        }
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -851,7 +888,7 @@ __device__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const 
       dw[2] = half_bits_to_float((uint16_t)(rs[i].y & 0xffff));
       dw[3] = half_bits_to_float((uint16_t)(rs[i].y >> 16));
       const v4i a = ra[i];
-      if (u + R < units) issue(u + R, i);
+      issue(u + R, i);
 #pragma unroll
       for (int cg = 0; cg < G; ++cg) {
         const v4i b = *(const v4i*)(pcodes + ((size_t)(cg * cBH + bp)) * 1024 + lane * 16);
@@ -886,11 +923,9 @@ __device__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const 
               for (int q = 0; q < 4; ++q) {
                 const int row = tile * 16 + 4 * (lane >> 4) + q;
                 float v = part[0][cg][q];
-                if (write_logits) gst<float>(P.logits + (size_t)t * V + row, v);
-                if (pen) {
-                  const uint32_t word = __builtin_amdgcn_raw_buffer_load_b32(rb, (t * words + (row >> 5)) * 4, 0, 16);
-                  if ((word >> (row & 31)) & 1u) v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
-                }
+                if (write_logits) gst<float>(logits + (size_t)t * V + row, v);
+                if (pen && ((pword[cg] >> (row & 31)) & 1u))
+                  v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
                 const uint64_t key = argmax_key(v, row);
                 best[cg] = key > best[cg] ? key : best[cg];
               }
@@ -922,28 +957,49 @@ __device__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const 
   }
 }
 
-__device__ void accept(const StepParams& P, const StepDesc* desc, int T, uint64_t* s_red,
-                       int32_t* s_choice) {
-  for (int t = 0; t < T; ++t) {
-    uint64_t b = 0;
-    for (int i = threadIdx.x; i < (int)gridDim.x; i += kT) {
-      const uint64_t k = ld_coh_u64(P.part_keys + (size_t)i * kMaxRows + t);
-      b = k > b ? k : b;
-    }
-    s_red[threadIdx.x] = b;
-    __syncthreads();
-    for (int o = kT / 2; o > 0; o >>= 1) {
-      if ((int)threadIdx.x < o && s_red[threadIdx.x + o] > s_red[threadIdx.x]) s_red[threadIdx.x] = s_red[threadIdx.x + o];
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) s_choice[t] = (int32_t)(0xffffffffu - (uint32_t)(s_red[0] & 0xffffffffu));
-    __syncthreads();
+// Greedy choice per verify row from the workgroups' best keys, then the longest
+// prefix of drafts that matches. Thread i holds workgroup i's keys of every row;
+// those loads and the draft tokens' are in flight together. Per row a wave max,
+// then the four waves.
+__device__ void accept(const uint64_t* part_keys, const int32_t* tokens, StepResult* result, int T, int nwg,
+                       uint64_t* s_red, int32_t* s_choice, int32_t* s_tok, uint64_t* timing, int slot) {
+  static_assert(kNwg <= kT, "one thread per workgroup's keys");
+  T = __builtin_amdgcn_readfirstlane(T);
+  nwg = __builtin_amdgcn_readfirstlane(nwg);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const Rsrc rk = mk_rsrc(uniform_ptr(part_keys), (uint32_t)(nwg * kMaxRows * 8));
+  const Rsrc rt = mk_rsrc(uniform_ptr(tokens), (uint32_t)(T * 4));
+  uint64_t key[kMaxRows];
+#pragma unroll
+  for (int h = 0; h < kMaxRows / 2; ++h) {
+    const v4u q = __builtin_amdgcn_raw_buffer_load_b128(
+        rk, (int)threadIdx.x < nwg ? (uint32_t)((threadIdx.x * kMaxRows + 2 * h) * 8) : 0x80000000u, 0, 16);
+    key[2 * h] = ((uint64_t)q.y << 32) | q.x;
+    key[2 * h + 1] = ((uint64_t)q.w << 32) | q.z;
   }
+  const int32_t tok = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(
+      rt, (int)threadIdx.x < T ? (uint32_t)(threadIdx.x * 4) : 0x80000000u, 0, 0);
+  if ((int)threadIdx.x < T) s_tok[threadIdx.x] = tok;
+  if (timing) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); if (threadIdx.x == 0) gst<uint64_t>(uniform_ptr(timing) + slot, wall_clock64()); }
+#pragma unroll
+  for (int t = 0; t < kMaxRows; ++t) {  // every row, so that key[] stays in registers
+    const uint64_t b = wave_max_u64(key[t]);
+    if (lane == 0) s_red[wave * kMaxRows + t] = b;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < T) {
+    uint64_t b = s_red[threadIdx.x];
+    for (int wv = 1; wv < kT / 64; ++wv) b = s_red[wv * kMaxRows + threadIdx.x] > b ? s_red[wv * kMaxRows + threadIdx.x] : b;
+    s_choice[threadIdx.x] = (int32_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
+  }
+  __syncthreads();
+  if (timing && threadIdx.x == 0) gst<uint64_t>(uniform_ptr(timing) + slot + 1, wall_clock64());
   if (threadIdx.x == 0) {
     int m = 0;
-    while (m + 1 < T && desc->tokens[m + 1] == s_choice[m]) ++m;
-    for (int t = 0; t < kMaxRows; ++t) P.result->choice[t] = t < T ? s_choice[t] : -1;
-    P.result->n_match = m;
+    while (m + 1 < T && s_tok[m + 1] == s_choice[m]) ++m;
+    StepResult* r = uniform_ptr(result);
+    for (int t = 0; t < kMaxRows; ++t) r->choice[t] = t < T ? s_choice[t] : -1;
+    r->n_match = m;
   }
 }
 
@@ -961,6 +1017,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   __shared__ uint64_t s_best[4 * kMaxRows];
   __shared__ uint64_t s_red[kT];
   __shared__ int32_t s_choice[kMaxRows];
+  __shared__ int32_t s_tok[kMaxRows];
   const int w = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int T = desc->T, past = desc->past, L = P.L;
   const int nch = (past + T + kChunk - 1) / kChunk, n_items = cNKV * nch;
@@ -1158,7 +1215,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   if (w == 0) {
     if (!wait_all(c, lm)) return;
     mark(P, 5 + 12 * L);
-    accept(P, desc, T, s_red, s_choice);
+    accept(P.part_keys, desc->tokens, P.result, T, kNwg, s_red, s_choice, s_tok, P.timing, 7 + 12 * L);
     mark(P, 6 + 12 * L);
   }
 #undef RX
