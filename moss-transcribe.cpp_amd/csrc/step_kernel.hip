@@ -640,17 +640,25 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
 #pragma unroll
     for (int s = 0; s < 16; ++s) vb[h][s] = kv_val(kv.v[h][s], f16kv);
   if (has_new) {  // keys >= past come from this step's rows; none past kvlen
+    // every lane reads a staged row (clamped row index) and keeps what applies,
+    // so that the reads are not each behind a lane mask and a wait
     const int key = key0 + 16 * wave + kl;
+    const bool kn = key >= past, kz = key >= kvlen;
+    const float* krow = knew + min(max(key - past, 0), T - 1) * cQStride + kk;
 #pragma unroll
-    for (int s = 0; s < 32; ++s)
-      if (key >= past) ka[s] = key < kvlen ? knew[(key - past) * cQStride + 4 * s + kk] : 0.0f;
+    for (int s = 0; s < 32; ++s) {
+      const float nv = krow[4 * s];
+      ka[s] = kz ? 0.0f : (kn ? nv : ka[s]);
+    }
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const int vk = key0 + 4 * s + kk;
-        if (vk >= past) vb[h][s] = vk < kvlen ? vnew[(vk - past) * cQStride + 16 * (2 * wave + h) + kl] : 0.0f;
-      }
+    for (int s = 0; s < 16; ++s) {
+      const int vk = key0 + 4 * s + kk;
+      const bool vn = vk >= past, vz = vk >= kvlen;
+      const float* vrow = vnew + min(max(vk - past, 0), T - 1) * cQStride + 32 * wave + kl;
+      const float n0 = vrow[0], n1 = vrow[16];
+      vb[0][s] = vz ? 0.0f : (vn ? n0 : vb[0][s]);
+      vb[1][s] = vz ? 0.0f : (vn ? n1 : vb[1][s]);
+    }
   }
   if (prof) { bar(); wmark(P, 1, 17); }
   // 3. scores S[key][col] = fma chain over head_dim, scaled and masked -> sp
@@ -761,28 +769,39 @@ __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, 
                           (uint32_t)P.max_chunks * kMaxCols * cHD * 4);
   // Chunk factors once per wave: lane c holds m_c, l_c and f_c = exp(m_c - M);
   // every thread then reads them as wave-uniform values (readlane) while it runs
-  // the two chunk-ordered fma chains over its own O values.
+  // the two chunk-ordered fma chains over its own O values. The first 64 chunks'
+  // (m, l) and the first 32 chunks' O are loaded together: one round trip at the
+  // usual context lengths.
   const int lane = threadIdx.x & 63;
   float out = 0.0f;
-  float M = -INFINITY;
-  for (int c0 = 0; c0 < nch; c0 += 64) {
-    const float m = (valid && c0 + lane < nch) ? ldc1(rml, (uint32_t)(((c0 + lane) * kMaxCols + col) * 2 * 4)) : -INFINITY;
-    M = fmaxf(M, wave_max_f(m));
-  }
+  auto ld_m = [&](int c) {
+    return valid && c < nch ? ldc1(rml, (uint32_t)((c * kMaxCols + col) * 2 * 4)) : -INFINITY;
+  };
+  auto ld_l = [&](int c) {
+    return valid && c < nch ? ldc1(rml, (uint32_t)(((c * kMaxCols + col) * 2 + 1) * 4)) : 0.0f;
+  };
+  float o[32];
+  auto ld_o = [&](int b0) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int c = min(b0 + i, nch - 1);
+      o[i] = valid ? ldc1(ro, (uint32_t)(((c * kMaxCols + col) * cHD + d) * 4)) : 0.0f;
+    }
+  };
+  float m = ld_m(lane), l = ld_l(lane);
+  ld_o(0);
+  float M = wave_max_f(m);
+  for (int c0 = 64; c0 < nch; c0 += 64) M = fmaxf(M, wave_max_f(ld_m(c0 + lane)));
   float L = 0.0f, O = 0.0f;
   for (int c0 = 0; c0 < nch; c0 += 64) {
-    const int cl = c0 + lane < nch ? c0 + lane : nch - 1;
-    const float m = valid ? ldc1(rml, (uint32_t)((cl * kMaxCols + col) * 2 * 4)) : -INFINITY;
-    const float l = valid ? ldc1(rml, (uint32_t)(((cl * kMaxCols + col) * 2 + 1) * 4)) : 0.0f;
+    if (c0 > 0) {
+      m = ld_m(c0 + lane);
+      l = ld_l(c0 + lane);
+    }
     const float f = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, M));
     const int nb = min(64, nch - c0);
     for (int i0 = 0; i0 < nb; i0 += 32) {
-      float o[32];
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        const int c = c0 + i0 + i < nch ? c0 + i0 + i : nch - 1;
-        o[i] = valid ? ldc1(ro, (uint32_t)(((c * kMaxCols + col) * cHD + d) * 4)) : 0.0f;
-      }
+      if (c0 + i0 > 0) ld_o(c0 + i0);
 #pragma unroll
       for (int i = 0; i < 32; ++i) {
         if (i0 + i >= nb) break;
