@@ -236,7 +236,7 @@ enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 // even and odd block halves; wave 0 writes T x 16 outputs with 16-byte stores.
 template <int G, int NM, int EPI>
 __device__ __forceinline__ void gemm_finish(float acc[NM][G][4], float* red, Rsrc out, int n,
-                                            int tile, int T) {
+                                            int tile, int T, float* xs = nullptr, bool xs_valid = false) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
 #pragma unroll
   for (int m = 0; m < NM; ++m)
@@ -268,9 +268,13 @@ __device__ __forceinline__ void gemm_finish(float acc[NM][G][4], float* red, Rsr
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] = acc[0][cg][q];
           } else if (EPI == EPI_RESID) {
-            const v4f x = ldc4(out, off);
+            // this workgroup is the only writer of its 16 residual columns: after
+            // the first time they come from its LDS copy, not from memory
+            v4f* xl = (v4f*)(xs + t * 16 + 4 * (lane >> 4));
+            const v4f x = xs_valid ? *xl : ldc4(out, off);
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] = __fadd_rn(x[q], acc[0][cg][q]);
+            *xl = v;
           } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] = dev_swiglu(acc[0][cg][q], acc[NM - 1][cg][q]);
@@ -1023,6 +1027,15 @@ __device__ void accept(const uint64_t* part_keys, const int32_t* tokens, StepRes
 }
 
 // ---------------------------------------------------------------- kernel ----
+// LDS: the GEMM panel + reduction space, or the attention's q / new rows /
+// probabilities (the phases reuse it), then the residual columns of the o-proj /
+// down tile ([8G rows][16], kept across phases).
+__host__ __device__ constexpr size_t step_lds_x_offset(int G) {
+  return ((size_t)G * cBF * (1024 + 64) + (size_t)4 * 4 * G * 4 * 64 * 4 >
+          ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride) * 4)
+             ? (size_t)G * cBF * (1024 + 64) + (size_t)4 * 4 * G * 4 * 64 * 4
+             : ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride) * 4;
+}
 __device__ __forceinline__ uint32_t ph(int l, int p) { return 2u + (uint32_t)(l * kPhases + p); }
 
 template <int G>
@@ -1043,6 +1056,8 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   uint8_t* pcodes = lds;
   float* pscales = (float*)(lds + (size_t)G * cBF * 1024);
   float* red = (float*)(lds + (size_t)G * cBF * (1024 + 64));
+  float* xs = (float*)(lds + step_lds_x_offset(G));  // this workgroup's residual columns
+  bool xs_valid = false;
   Ctl c{&P, epoch, 0, &s_ok};
 #define RX mk_rsrc(P.x, kMaxRows * cH * 4)
 #define RQKV mk_rsrc(P.qkv, kMaxRows * cNQKV * 4)
@@ -1087,6 +1102,12 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       for (int i = 0; i < 4; ++i) e[i] = d * (float)(int8_t)(q4 >> (8 * i));
     }
     stc4(RX, (uint32_t)((t * cH + k) * 4), e);
+  }
+  publish(c, 1);
+  // the penalty bitmap is read only by the lm_head: built after the publish (a
+  // later publish of this workgroup covers its stores)
+  if (w < T) {
+    const int t = w;
     if (mode == kStepVerify && desc->penalty > 1.0f) {
       const int words = (P.V + 31) / 32;
       uint32_t* row = P.bitmap + (size_t)t * words;
@@ -1100,7 +1121,6 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       }
     }
   }
-  publish(c, 1);
   // prefetch layer 0: q|k|v tile and the first attention item's K / V
   wt_load<4>(layer_at(P, 0).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
   if (has_attn) kv_prefetch(layer_at(P, 0), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
@@ -1167,7 +1187,9 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       panel_from_q<cQN>(P.oq, P.oqs, T, pcodes, pscales);
       float acc[1][G][4] = {};
       wt_mma<G, 8>(ba, bs, 8 * wave, cBQ, pcodes, pscales, acc[0]);
-      gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T);
+      gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T, xs, xs_valid);
+      xs_valid = true;
+      wmark(P, l, 24);
       publish(c, next_done(l, kPhO));
       mark(P, 3 + 12 * l + 5);
       wmark(P, l, 7);
@@ -1185,6 +1207,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
 #pragma unroll
       for (int m = 0; m < 4; ++m) wt_mma<G, 4>(ba + 4 * m, bs + 4 * m, 4 * wave, cBH, pcodes, pscales, acc[m]);
       gu_finish<G>(acc, red, P, w - cOTiles, T);
+      wmark(P, l, 24);
       publish(c, next_done(l, kPhGu));
       wmark(P, l, 9);
       if (l + 1 < L) {
@@ -1201,7 +1224,8 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       panel_from_q<cF>(P.aq, P.aqs, T, pcodes, pscales);
       float acc[1][G][4] = {};
       wt_mma<G, 12>(ba, bs, 12 * wave, cBF, pcodes, pscales, acc[0]);
-      gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T);
+      gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T, xs, xs_valid);
+      xs_valid = true;
       publish(c, next_done(l, kPhD));
       mark(P, 3 + 12 * l + 7);
       wmark(P, l, 11);
@@ -1253,12 +1277,7 @@ int step_kernel_workgroups() { return kNwg; }
 
 uint32_t step_progress_per_step(int n_layers) { return 2u + (uint32_t)(n_layers * kPhases); }
 
-size_t step_lds_bytes(int G) {
-  const size_t panel = (size_t)G * cBF * (1024 + 64);
-  const size_t red = (size_t)4 * 4 * G * 4 * 64 * 4;
-  const size_t attn = ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride) * 4;
-  return (panel + red > attn ? panel + red : attn);
-}
+size_t step_lds_bytes(int G) { return step_lds_x_offset(G) + (size_t)G * 8 * 16 * 4; }
 
 hipError_t prepare_step_kernels() {
   hipError_t e = hipFuncSetAttribute((const void*)k_step<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
