@@ -22,6 +22,18 @@ struct KvLayer {
   int max_seq;
 };
 
+// Activation of a GEMM whose weights are f16 or q4_K (kernels_wt.hip): the
+// f16-rounded rows [16][K], or the q8_K blocks of the rows.
+struct ActQ8K {
+  int8_t* qs;      // [16][K]
+  float* d;        // [16][K/256]
+  int32_t* bsums;  // [16][K/16]
+};
+struct WtAct {
+  float* f16v;  // [16][K]
+  ActQ8K q8k;
+};
+
 struct AttnWork {
   float* part_ml;  // [kv_head][split][group][16 cols][2]
   float* part_o;   // [kv_head][split][group][16 cols][head_dim]
@@ -58,5 +70,19 @@ void launch_accept(hipStream_t s, const StepDesc* desc, const uint64_t* part_key
 void launch_causal_context(hipStream_t s, const float* v, const float* p, int head_dim,
                            int kv_heads, int heads, int queries, int kv_len, float* out);
 void launch_q8_retile(hipStream_t s, const uint8_t* blocks, int n, int k, uint8_t* tiles);
+
+// ---- f16 / q4_K weights (kernels_wt.hip); weights in the GGUF row layout ----
+bool wt_shape_supported(int wtype, int k);
+// act <- the weight type's vec_dot_type of RMSNorm(src) * gain (gain == nullptr:
+// src as is); normed_out (nullable) receives the f32 normalized rows.
+void launch_act_wt(hipStream_t s, int wtype, const StepDesc* desc, const float* src, int K,
+                   const float* gain, float eps, const WtAct& act, float* normed_out);
+// epi 0: out = W act, 1: out += W act, 2: out = silu(W act) * (W2 act)
+void launch_gemm_wt(hipStream_t s, int wtype, int epi, const StepDesc* desc, const uint8_t* w,
+                    const uint8_t* w2, int n, int k, const WtAct& act, float* out);
+void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int vocab, int k,
+                       const WtAct& act, const uint32_t* bitmap, float* logits, uint64_t* part_keys);
+void launch_embed_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int hidden,
+                     const float* host_rows, float* x);
 
 }  // namespace mtg

@@ -1,0 +1,403 @@
+// kernels_wt.hip - the f16 and q4_K weight paths of the verify step (gfx950).
+//
+// Reference ops replaced (moss-transcribe.cpp through ggml's CPU backend; ggml
+// itself is absent, its published semantics are restated):
+//   k_act_f16 / k_act_q8k   rms_norm * gain, then mul_mat's conversion of the
+//                           activation to vec_dot_type (F16 for f16 weights,
+//                           Q8_K for q4_K)                src/qwen3.cpp:27-30,80,196
+//   k_gemm_f16 / k_gemm_q4k mul_mat(W, x) (+ add / silu*mul)
+//                                                         src/qwen3.cpp:92-97,192-193,204-216
+//   k_lm_head_wt            tied lm_head + cpu_greedy_choice keys
+//                                                         src/qwen3_decoder.cpp:174-205,
+//                                                         src/cpu_speculative.cpp:39-50
+//   k_embed_wt              get_rows / embed_rows_f32     src/generate.cpp:68-111
+//
+// Weights stay in the GGUF row layout: f16 [N][K] halves, q4_K [N][K/256] blocks
+// of 144 bytes. One wave computes one output row for all verify rows.
+//
+// Canonical orders (shared with the oracle, which restates them on the CPU):
+//   f16  : x rounded to f16; lane l of a wave takes the K/64 consecutive
+//          elements [l*K/64, (l+1)*K/64) in an fma chain from 0 (the products of
+//          two f16 values are exact in f32), then the 64 partials meet in the xor
+//          butterfly 32, 16, 8, 4, 2, 1.
+//   q4_K : x quantized to q8_K (ggml quantize_row_q8_K); per 256-superblock the
+//          exact int32 sums dot = sum_s sc_s * dot_s and mins = sum_s mn_s * bsum_s;
+//          then in superblock order acc = acc + (d_w*d_x)*dot, acc = acc -
+//          (dmin_w*d_x)*mins.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace mtg {
+
+namespace {
+using namespace dev;
+
+// 1 / sqrt(mean(x^2) + eps) of a hidden row (K == 1024), the canonical double sum:
+// lane l sums elements 16l..16l+15, then the butterfly. Called by wave 0.
+__device__ __forceinline__ float row_rms_scale(const float* xr, int K, float eps) {
+  const int lane = threadIdx.x & 63;
+  double s = 0.0;
+  for (int e = 0; e < 16; ++e) {
+    const float v = xr[lane * 16 + e];
+    s += (double)__fmul_rn(v, v);
+  }
+  s = wave_sum_d(s);
+  return dev_rms_scale((float)(s / (double)K), eps);
+}
+
+// exact integer wave sum (any order is exact)
+__device__ __forceinline__ int wave_sum_i(int v) {
+  uint32_t a, b;
+  pair_split<32>((uint32_t)v, a, b);
+  v = (int)a + (int)b;
+  pair_split<16>((uint32_t)v, a, b);
+  v = (int)a + (int)b;
+  v += (int)dpp_u<kDppRor8>((uint32_t)v);
+  v += (int)dpp_u<kDppRor4>((uint32_t)v);
+  v += (int)dpp_u<kDppRor2>((uint32_t)v);
+  v += (int)dpp_u<kDppRor1>((uint32_t)v);
+  return v;
+}
+
+// ------------------------------------------------------- activations ------
+// One workgroup (256 threads) per verify row. gain == nullptr: no norm (the
+// attention output and the SwiGLU product go in as they are).
+__global__ void __launch_bounds__(256)
+k_act_f16(const StepDesc* __restrict__ desc, const float* __restrict__ src, int K,
+          const float* __restrict__ gain, float eps, float* __restrict__ out,
+          float* __restrict__ normed_out) {
+  const int t = blockIdx.x;
+  if (t >= desc->T) return;
+  const float* xr = src + (size_t)t * K;
+  __shared__ float s_scale;
+  float scale = 1.0f;
+  if (gain) {
+    if (threadIdx.x < 64) {
+      const float sc = row_rms_scale(xr, K, eps);
+      if (threadIdx.x == 0) s_scale = sc;
+    }
+    __syncthreads();
+    scale = s_scale;
+  }
+  for (int k = threadIdx.x; k < K; k += 256) {
+    float y = xr[k];
+    if (gain) y = __fmul_rn(__fmul_rn(y, scale), gain[k]);
+    if (normed_out) normed_out[(size_t)t * K + k] = y;
+    out[(size_t)t * K + k] = f16_round(y);  // vec_dot_type F16
+  }
+}
+
+// ggml quantize_row_q8_K_ref per 256-block: the element of largest magnitude
+// (the first one on ties) gives max with its sign, iscale = -127/max, codes =
+// min(127, nearest(iscale*x)), d = 1/iscale, bsums over 16-element groups.
+__global__ void __launch_bounds__(256)
+k_act_q8k(const StepDesc* __restrict__ desc, const float* __restrict__ src, int K,
+          const float* __restrict__ gain, float eps, ActQ8K a, float* __restrict__ normed_out) {
+  const int t = blockIdx.x;
+  if (t >= desc->T) return;
+  const float* xr = src + (size_t)t * K;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __shared__ float s_scale;
+  __shared__ float s_y[256];
+  __shared__ uint64_t s_key[4];
+  float scale = 1.0f;
+  if (gain) {
+    if (tid < 64) {
+      const float sc = row_rms_scale(xr, K, eps);
+      if (tid == 0) s_scale = sc;
+    }
+    __syncthreads();
+    scale = s_scale;
+  }
+  for (int b = 0; b < K / 256; ++b) {
+    const int k = b * 256 + tid;
+    float y = xr[k];
+    if (gain) y = __fmul_rn(__fmul_rn(y, scale), gain[k]);
+    if (normed_out) normed_out[(size_t)t * K + k] = y;
+    s_y[tid] = y;
+    // first maximum of |y|: larger magnitude, then lower index
+    const uint64_t key = ((uint64_t)__float_as_uint(fabsf(y)) << 32) | (uint32_t)(255 - tid);
+    const uint64_t wk = wave_max_u64(key);
+    if (lane == 0) s_key[wave] = wk;
+    __syncthreads();
+    uint64_t best = s_key[0];
+    for (int w = 1; w < 4; ++w) best = s_key[w] > best ? s_key[w] : best;
+    const float maxv = s_y[255 - (int)(best & 0xffffffffu)];
+    int q = 0;
+    float d = 0.0f;
+    if ((best >> 32) != 0) {  // amax > 0
+      const float iscale = __fdiv_rn(-127.0f, maxv);
+      q = min(127, (int)rintf(__fmul_rn(iscale, y)));
+      d = __fdiv_rn(1.0f, iscale);
+    }
+    a.qs[(size_t)t * K + k] = (int8_t)q;
+    // bsums: the 16 lanes of a DPP row hold one group
+    int s = q;
+    s += (int)dpp_u<kDppRor8>((uint32_t)s);
+    s += (int)dpp_u<kDppRor4>((uint32_t)s);
+    s += (int)dpp_u<kDppRor2>((uint32_t)s);
+    s += (int)dpp_u<kDppRor1>((uint32_t)s);
+    if ((tid & 15) == 0) a.bsums[(size_t)t * (K / 16) + b * 16 + (tid >> 4)] = s;
+    if (tid == 0) a.d[(size_t)t * (K / 256) + b] = d;
+    __syncthreads();  // s_y / s_key are reused by the next block
+  }
+}
+
+// ------------------------------------------------------------ row dots ----
+// f16: res[t] (wave-uniform) = the canonical dot of row w[K] with xa[t][K].
+template <int SEG>
+__device__ __forceinline__ void f16_row_dots(const uint16_t* __restrict__ wrow,
+                                             const float* __restrict__ xa, int T, float* res) {
+  constexpr int K = SEG * 64;
+  const int lane = threadIdx.x & 63;
+  float wv[SEG];
+  const uint4* wp = (const uint4*)(wrow + lane * SEG);
+#pragma unroll
+  for (int i = 0; i < SEG / 8; ++i) {
+    const uint4 u = wp[i];
+    const uint32_t h[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      wv[8 * i + 2 * j] = half_bits_to_float((uint16_t)(h[j] & 0xffff));
+      wv[8 * i + 2 * j + 1] = half_bits_to_float((uint16_t)(h[j] >> 16));
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kMaxRows; ++t) {  // constant indices keep res[] in registers
+    if (t >= T) break;
+    const float4* xp = (const float4*)(xa + (size_t)t * K + lane * SEG);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SEG / 4; ++i) {
+      const float4 x4 = xp[i];
+      acc = fmaf(wv[4 * i + 0], x4.x, acc);
+      acc = fmaf(wv[4 * i + 1], x4.y, acc);
+      acc = fmaf(wv[4 * i + 2], x4.z, acc);
+      acc = fmaf(wv[4 * i + 3], x4.w, acc);
+    }
+    res[t] = wave_sum_f(acc);
+  }
+}
+
+// q4_K: lane l takes elements 4(l%8)..+3 of sub-block l/8 of each superblock.
+__device__ __forceinline__ void q4k_row_dots(const uint8_t* __restrict__ wrow, const ActQ8K& a,
+                                             int K, int T, float* res) {
+  const int lane = threadIdx.x & 63, s = lane >> 3, j0 = 4 * (lane & 7);
+  const int nb = K / 256;
+#pragma unroll
+  for (int t = 0; t < kMaxRows; ++t) res[t] = 0.0f;
+  for (int b = 0; b < nb; ++b) {
+    const uint8_t* blk = wrow + (size_t)b * 144;
+    const float dw = half_bits_to_float(*(const uint16_t*)blk);
+    const float dminw = half_bits_to_float(*(const uint16_t*)(blk + 2));
+    const uint8_t* sc12 = blk + 4;
+    int sc, mn;  // get_scale_min_k4 of sub-block s
+    if (s < 4) {
+      sc = sc12[s] & 63;
+      mn = sc12[s + 4] & 63;
+    } else {
+      sc = (sc12[s + 4] & 0xF) | ((sc12[s - 4] >> 6) << 4);
+      mn = (sc12[s + 4] >> 4) | ((sc12[s] >> 6) << 4);
+    }
+    const uint32_t qb = *(const uint32_t*)(blk + 16 + (s >> 1) * 32 + j0);
+    const int nib = (int)((s & 1) ? (qb >> 4) & 0x0F0F0F0Fu : qb & 0x0F0F0F0Fu);
+#pragma unroll
+    for (int t = 0; t < kMaxRows; ++t) {
+      if (t >= T) break;
+      const int xq = *(const int*)(a.qs + (size_t)t * K + b * 256 + s * 32 + j0);
+      const int part = __builtin_amdgcn_sdot4(nib, xq, 0, false);
+      const int dot = wave_sum_i(sc * part);
+      const int mcontrib =
+          (lane & 7) == 0
+              ? mn * (a.bsums[(size_t)t * (K / 16) + b * 16 + 2 * s] + a.bsums[(size_t)t * (K / 16) + b * 16 + 2 * s + 1])
+              : 0;
+      const int mins = wave_sum_i(mcontrib);
+      const float dx = a.d[(size_t)t * nb + b];
+      const float d = __fmul_rn(dw, dx), dmin = __fmul_rn(dminw, dx);
+      res[t] = __fadd_rn(res[t], __fmul_rn(d, (float)dot));
+      res[t] = __fsub_rn(res[t], __fmul_rn(dmin, (float)mins));
+    }
+  }
+}
+
+template <int WT, int SEG>
+__device__ __forceinline__ void row_dots(const uint8_t* w, int row, int K, const float* xa, const ActQ8K& a,
+                                         int T, float* res) {
+  if constexpr (WT == MTG_TYPE_F16)
+    f16_row_dots<SEG>((const uint16_t*)w + (size_t)row * K, xa, T, res);
+  else
+    q4k_row_dots(w + (size_t)row * (K / 256) * 144, a, K, T, res);
+}
+
+// ---------------------------------------------------------------- GEMM ----
+// EPI 0: store, 1: residual add, 2: silu(W x) * (W2 x). One wave per row.
+template <int WT, int SEG, int EPI>
+__global__ void __launch_bounds__(256)
+k_gemm_wt(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w,
+          const uint8_t* __restrict__ w2, int n, int K, const float* __restrict__ xa, ActQ8K a,
+          float* __restrict__ out) {
+  const int T = desc->T;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= n) return;
+  float r1[kMaxRows], r2[kMaxRows];
+  row_dots<WT, SEG>(w, row, K, xa, a, T, r1);
+  if (EPI == 2) row_dots<WT, SEG>(w2, row, K, xa, a, T, r2);
+  if (lane != 0) return;
+#pragma unroll
+  for (int t = 0; t < kMaxRows; ++t) {
+    if (t >= T) break;
+    float* dst = out + (size_t)t * n + row;
+    if (EPI == 0) *dst = r1[t];
+    else if (EPI == 1) *dst = __fadd_rn(*dst, r1[t]);
+    else *dst = dev_swiglu(r1[t], r2[t]);
+  }
+}
+
+// ------------------------------------------------------------- lm_head ----
+// Grid-stride over rows; per verify row the best 64-bit key (value bits, lowest
+// index on ties) of each workgroup goes to part_keys, as the q8_0 lm_head does.
+template <int WT, int SEG>
+__global__ void __launch_bounds__(256)
+k_lm_head_wt(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int vocab, int K,
+             const float* __restrict__ xa, ActQ8K a, const uint32_t* __restrict__ bitmap,
+             float* __restrict__ logits, uint64_t* __restrict__ part_keys) {
+  const int T = desc->T;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nwaves = gridDim.x * 4;
+  const bool pen = desc->penalty > 1.0f;
+  const float penalty = desc->penalty;
+  const int words = (vocab + 31) / 32;
+  uint64_t best[kMaxRows];
+#pragma unroll
+  for (int t = 0; t < kMaxRows; ++t) best[t] = 0;
+  float res[kMaxRows];
+  for (int row = blockIdx.x * 4 + wave; row < vocab; row += nwaves) {
+    row_dots<WT, SEG>(w, row, K, xa, a, T, res);
+#pragma unroll
+    for (int t = 0; t < kMaxRows; ++t) {
+      if (t >= T) break;
+      float v = res[t];
+      if (desc->write_logits && lane == 0) logits[(size_t)t * vocab + row] = v;
+      if (pen && ((bitmap[(size_t)t * words + (row >> 5)] >> (row & 31)) & 1u))
+        v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+      const uint64_t key = argmax_key(v, row);
+      best[t] = key > best[t] ? key : best[t];
+    }
+  }
+  __shared__ uint64_t s_best[4][kMaxRows];
+  if (lane == 0)
+#pragma unroll
+    for (int t = 0; t < kMaxRows; ++t) s_best[wave][t] = best[t];
+  __syncthreads();
+  if ((int)threadIdx.x < T) {
+    uint64_t b = s_best[0][threadIdx.x];
+    for (int wv = 1; wv < 4; ++wv) b = s_best[wv][threadIdx.x] > b ? s_best[wv][threadIdx.x] : b;
+    part_keys[(size_t)blockIdx.x * kMaxRows + threadIdx.x] = b;
+  }
+}
+
+// --------------------------------------------------------------- embed -----
+template <int WT>
+__global__ void k_embed_wt(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int hidden,
+                           const float* __restrict__ host_rows, float* __restrict__ x) {
+  const int t = blockIdx.x;
+  if (t >= desc->T) return;
+  float* xr = x + (size_t)t * hidden;
+  if (desc->use_embeds) {
+    for (int k = threadIdx.x; k < hidden; k += blockDim.x) xr[k] = host_rows[(size_t)t * hidden + k];
+    return;
+  }
+  const int n = desc->tokens[t];
+  for (int k = threadIdx.x; k < hidden; k += blockDim.x) {
+    if constexpr (WT == MTG_TYPE_F16) {
+      xr[k] = half_bits_to_float(((const uint16_t*)w)[(size_t)n * hidden + k]);
+    } else {  // dequantize_row_q4_K
+      const uint8_t* blk = w + ((size_t)n * (hidden / 256) + k / 256) * 144;
+      const int e = k % 256, s = e / 32, l = e % 32;
+      const uint8_t* sc12 = blk + 4;
+      int sc, mn;
+      if (s < 4) {
+        sc = sc12[s] & 63;
+        mn = sc12[s + 4] & 63;
+      } else {
+        sc = (sc12[s + 4] & 0xF) | ((sc12[s - 4] >> 6) << 4);
+        mn = (sc12[s + 4] >> 4) | ((sc12[s] >> 6) << 4);
+      }
+      const uint8_t qb = blk[16 + (s / 2) * 32 + l];
+      const int v = (s & 1) ? (qb >> 4) : (qb & 0xF);
+      const float d1 = __fmul_rn(half_bits_to_float(*(const uint16_t*)blk), (float)sc);
+      const float m1 = __fmul_rn(half_bits_to_float(*(const uint16_t*)(blk + 2)), (float)mn);
+      xr[k] = __fsub_rn(__fmul_rn(d1, (float)v), m1);
+    }
+  }
+}
+
+template <int WT, int EPI>
+void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_t* w2, int n, int k,
+             const WtAct& act, float* out) {
+  const dim3 grid((n + 3) / 4), block(256);
+  if constexpr (WT == MTG_TYPE_F16) {
+    if (k == 1024)
+      hipLaunchKernelGGL((k_gemm_wt<WT, 16, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
+    else if (k == 2048)
+      hipLaunchKernelGGL((k_gemm_wt<WT, 32, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
+    else
+      hipLaunchKernelGGL((k_gemm_wt<WT, 48, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
+  } else {
+    hipLaunchKernelGGL((k_gemm_wt<WT, 0, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
+  }
+}
+
+}  // namespace
+
+// ================================================================ launches ==
+bool wt_shape_supported(int wtype, int k) {
+  if (wtype == MTG_TYPE_F16) return k == 1024 || k == 2048 || k == 3072;
+  if (wtype == MTG_TYPE_Q4_K) return k % 256 == 0;
+  return false;
+}
+
+void launch_act_wt(hipStream_t s, int wtype, const StepDesc* desc, const float* src, int K,
+                   const float* gain, float eps, const WtAct& act, float* normed_out) {
+  if (wtype == MTG_TYPE_F16)
+    hipLaunchKernelGGL(k_act_f16, dim3(kMaxRows), dim3(256), 0, s, desc, src, K, gain, eps, act.f16v, normed_out);
+  else
+    hipLaunchKernelGGL(k_act_q8k, dim3(kMaxRows), dim3(256), 0, s, desc, src, K, gain, eps, act.q8k, normed_out);
+}
+
+void launch_gemm_wt(hipStream_t s, int wtype, int epi, const StepDesc* desc, const uint8_t* w,
+                    const uint8_t* w2, int n, int k, const WtAct& act, float* out) {
+  if (wtype == MTG_TYPE_F16) {
+    if (epi == 0) gemm_wt<MTG_TYPE_F16, 0>(s, desc, w, w2, n, k, act, out);
+    else if (epi == 1) gemm_wt<MTG_TYPE_F16, 1>(s, desc, w, w2, n, k, act, out);
+    else gemm_wt<MTG_TYPE_F16, 2>(s, desc, w, w2, n, k, act, out);
+  } else {
+    if (epi == 0) gemm_wt<MTG_TYPE_Q4_K, 0>(s, desc, w, w2, n, k, act, out);
+    else if (epi == 1) gemm_wt<MTG_TYPE_Q4_K, 1>(s, desc, w, w2, n, k, act, out);
+    else gemm_wt<MTG_TYPE_Q4_K, 2>(s, desc, w, w2, n, k, act, out);
+  }
+}
+
+void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int vocab, int k,
+                       const WtAct& act, const uint32_t* bitmap, float* logits, uint64_t* part_keys) {
+  const dim3 grid(kLmWorkgroups), block(256);
+  if (wtype == MTG_TYPE_F16)
+    hipLaunchKernelGGL((k_lm_head_wt<MTG_TYPE_F16, 16>), grid, block, 0, s, desc, w, vocab, k, act.f16v,
+                       act.q8k, bitmap, logits, part_keys);
+  else
+    hipLaunchKernelGGL((k_lm_head_wt<MTG_TYPE_Q4_K, 0>), grid, block, 0, s, desc, w, vocab, k, act.f16v,
+                       act.q8k, bitmap, logits, part_keys);
+}
+
+void launch_embed_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int hidden,
+                     const float* host_rows, float* x) {
+  if (wtype == MTG_TYPE_F16)
+    hipLaunchKernelGGL(k_embed_wt<MTG_TYPE_F16>, dim3(kMaxRows), dim3(256), 0, s, desc, w, hidden, host_rows, x);
+  else
+    hipLaunchKernelGGL(k_embed_wt<MTG_TYPE_Q4_K>, dim3(kMaxRows), dim3(256), 0, s, desc, w, hidden, host_rows, x);
+}
+
+}  // namespace mtg

@@ -70,14 +70,30 @@ int Ctx::upload_q8(const void* blocks, int n, int k, uint8_t* dst, uint8_t* stag
   return check(hipStreamSynchronize(stream), "retile");
 }
 
+size_t Ctx::weight_bytes(int n, int k) const {
+  if (wtype == MTG_TYPE_Q8_0) return q8_tiles_bytes(n, k);
+  if (wtype == MTG_TYPE_F16) return (size_t)n * k * 2;
+  return (size_t)n * (k / 256) * 144;  // q4_K
+}
+
+int Ctx::upload_weights(const void* src, int n, int k, uint8_t* dst, uint8_t* staging) {
+  if (wtype == MTG_TYPE_Q8_0) return upload_q8(src, n, k, dst, staging);
+  return check(hipMemcpy(dst, src, weight_bytes(n, k), hipMemcpyHostToDevice), "upload weights");
+}
+
 int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
   hp = d->hp;
   max_seq = max_seq_in;
   kv_type = kv_type_in;
   const int H = hp.hidden, D = hp.head_dim, NH = hp.n_heads, NKV = hp.n_kv_heads;
   const int QN = NH * D, KN = NKV * D, F = hp.intermediate, L = hp.n_layers, V = hp.vocab;
-  if (d->weight_type != MTG_TYPE_Q8_0)
-    return fail(MTG_ERR_UNSUPPORTED, "weight type %d is not supported by this build", d->weight_type);
+  wtype = d->weight_type;
+  if (wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16 && wtype != MTG_TYPE_Q4_K)
+    return fail(MTG_ERR_UNSUPPORTED, "weight type %d is not supported by this build", wtype);
+  if (wtype != MTG_TYPE_Q8_0 && (!wt_shape_supported(wtype, H) || !wt_shape_supported(wtype, QN) ||
+                                 !wt_shape_supported(wtype, F)))
+    return fail(MTG_ERR_UNSUPPORTED, "shape not supported for weight type %d (f16: K of 1024, 2048 or "
+                "3072; q4_K: K a multiple of 256)", wtype);
   if (kv_type != MTG_TYPE_F32 && kv_type != MTG_TYPE_F16)
     return fail(MTG_ERR_UNSUPPORTED, "kv type %d", kv_type);
   if (D != kHeadDim || NH != 2 * NKV || H % kPairK || QN % kPairK || F % kPairK || V % 16 ||
@@ -93,21 +109,24 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
   std::memset(desc_host, 0, sizeof(StepDesc));
 
   // weights
-  size_t staging_bytes = (size_t)V * (H / 32) * 34;
-  staging_bytes = std::max(staging_bytes, (size_t)F * (H / 32) * 34);
-  staging_bytes = std::max(staging_bytes, (size_t)H * (F / 32) * 34);
-  uint8_t* staging = (uint8_t*)dalloc(staging_bytes, false);
-  if (!staging) return fail(MTG_ERR_NOMEM, "staging buffer");
+  uint8_t* staging = nullptr;  // q8_0 rows before the re-tiling
+  if (wtype == MTG_TYPE_Q8_0) {
+    size_t staging_bytes = (size_t)V * (H / 32) * 34;
+    staging_bytes = std::max(staging_bytes, (size_t)F * (H / 32) * 34);
+    staging_bytes = std::max(staging_bytes, (size_t)H * (F / 32) * 34);
+    staging = (uint8_t*)dalloc(staging_bytes, false);
+    if (!staging) return fail(MTG_ERR_NOMEM, "staging buffer");
+  }
   layers.resize(L);
   const int NQKV = QN + 2 * KN;
   for (int l = 0; l < L; ++l) {
     const mtg_layer_tensors& s = d->layers[l];
     Layer& y = layers[l];
-    y.wqkv = (uint8_t*)dalloc(q8_tiles_bytes(NQKV, H), false);
-    y.wo = (uint8_t*)dalloc(q8_tiles_bytes(H, QN), false);
-    y.wg = (uint8_t*)dalloc(q8_tiles_bytes(F, H), false);
-    y.wu = (uint8_t*)dalloc(q8_tiles_bytes(F, H), false);
-    y.wd = (uint8_t*)dalloc(q8_tiles_bytes(H, F), false);
+    y.wqkv = (uint8_t*)dalloc(weight_bytes(NQKV, H), false);
+    y.wo = (uint8_t*)dalloc(weight_bytes(H, QN), false);
+    y.wg = (uint8_t*)dalloc(weight_bytes(F, H), false);
+    y.wu = (uint8_t*)dalloc(weight_bytes(F, H), false);
+    y.wd = (uint8_t*)dalloc(weight_bytes(H, F), false);
     y.attn_norm = (float*)dalloc(H * 4, false);
     y.ffn_norm = (float*)dalloc(H * 4, false);
     y.q_norm = (float*)dalloc(D * 4, false);
@@ -115,27 +134,29 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
     if (!y.wqkv || !y.wo || !y.wg || !y.wu || !y.wd || !y.attn_norm || !y.ffn_norm || !y.q_norm ||
         !y.k_norm)
       return fail(MTG_ERR_NOMEM, "layer %d weights", l);
-    if ((rc = upload_q8(s.attn_q, QN, H, y.wqkv, staging))) return rc;
-    if ((rc = upload_q8(s.attn_k, KN, H, y.wqkv + q8_tiles_bytes(QN, H), staging))) return rc;
-    if ((rc = upload_q8(s.attn_v, KN, H, y.wqkv + q8_tiles_bytes(QN + KN, H), staging))) return rc;
-    if ((rc = upload_q8(s.attn_o, H, QN, y.wo, staging))) return rc;
-    if ((rc = upload_q8(s.ffn_gate, F, H, y.wg, staging))) return rc;
-    if ((rc = upload_q8(s.ffn_up, F, H, y.wu, staging))) return rc;
-    if ((rc = upload_q8(s.ffn_down, H, F, y.wd, staging))) return rc;
+    if ((rc = upload_weights(s.attn_q, QN, H, y.wqkv, staging))) return rc;
+    if ((rc = upload_weights(s.attn_k, KN, H, y.wqkv + weight_bytes(QN, H), staging))) return rc;
+    if ((rc = upload_weights(s.attn_v, KN, H, y.wqkv + weight_bytes(QN + KN, H), staging))) return rc;
+    if ((rc = upload_weights(s.attn_o, H, QN, y.wo, staging))) return rc;
+    if ((rc = upload_weights(s.ffn_gate, F, H, y.wg, staging))) return rc;
+    if ((rc = upload_weights(s.ffn_up, F, H, y.wu, staging))) return rc;
+    if ((rc = upload_weights(s.ffn_down, H, F, y.wd, staging))) return rc;
     if ((rc = check(hipMemcpy(y.attn_norm, s.attn_norm, H * 4, hipMemcpyHostToDevice), "norms")) ||
         (rc = check(hipMemcpy(y.ffn_norm, s.ffn_norm, H * 4, hipMemcpyHostToDevice), "norms")) ||
         (rc = check(hipMemcpy(y.q_norm, s.attn_q_norm, D * 4, hipMemcpyHostToDevice), "norms")) ||
         (rc = check(hipMemcpy(y.k_norm, s.attn_k_norm, D * 4, hipMemcpyHostToDevice), "norms")))
       return rc;
   }
-  embd = (uint8_t*)dalloc(q8_tiles_bytes(V, H), false);
+  embd = (uint8_t*)dalloc(weight_bytes(V, H), false);
   out_norm = (float*)dalloc(H * 4, false);
   if (!embd || !out_norm) return fail(MTG_ERR_NOMEM, "token_embd");
-  if ((rc = upload_q8(d->token_embd, V, H, embd, staging))) return rc;
+  if ((rc = upload_weights(d->token_embd, V, H, embd, staging))) return rc;
   if ((rc = check(hipMemcpy(out_norm, d->output_norm, H * 4, hipMemcpyHostToDevice), "norms")))
     return rc;
-  hipFree(staging);
-  allocations.erase(std::find(allocations.begin(), allocations.end(), (void*)staging));
+  if (staging) {
+    hipFree(staging);
+    allocations.erase(std::find(allocations.begin(), allocations.end(), (void*)staging));
+  }
 
   // RoPE table: the float recurrence of ggml's rope cache, built once on the host.
   std::vector<float> table((size_t)max_seq * D);
@@ -181,6 +202,15 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
   panel_h = panel(H);
   panel_o = panel(QN);
   panel_f = panel(F);
+  if (wtype != MTG_TYPE_Q8_0) {
+    const int KM = std::max(H, std::max(QN, F));
+    wact.f16v = (float*)dalloc((size_t)R * KM * 4, true);
+    wact.q8k.qs = (int8_t*)dalloc((size_t)R * KM, true);
+    wact.q8k.d = (float*)dalloc((size_t)R * (KM / 256 + 1) * 4, true);
+    wact.q8k.bsums = (int32_t*)dalloc((size_t)R * (KM / 16) * 4, true);
+    if (!wact.f16v || !wact.q8k.qs || !wact.q8k.d || !wact.q8k.bsums)
+      return fail(MTG_ERR_NOMEM, "activation buffers");
+  }
   const size_t chunks = (size_t)NKV * ((max_seq + kChunkKeys - 1) / kChunkKeys);
   work.part_ml = (float*)dalloc(chunks * kMaxCols * 2 * 4, true);
   work.part_o = (float*)dalloc(chunks * kMaxCols * D * 4, true);
@@ -203,7 +233,8 @@ int Ctx::init_step_kernel() {
   if ((rc = check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count")))
     return rc;
   const int H = hp.hidden, F = hp.intermediate, V = hp.vocab;
-  if (!step_kernel_supported(H, hp.n_heads, hp.n_kv_heads, hp.head_dim, F, hp.n_layers, cus) ||
+  if (wtype != MTG_TYPE_Q8_0 ||  // the persistent kernel streams q8_0 panel tiles
+      !step_kernel_supported(H, hp.n_heads, hp.n_kv_heads, hp.head_dim, F, hp.n_layers, cus) ||
       prepare_step_kernels() != hipSuccess) {
     (void)hipGetLastError();
     exec = kExecGraph;  // other shapes and smaller devices: the per-op kernels
@@ -285,6 +316,10 @@ void Ctx::enqueue(int G, int mode) {
   const int QN = NH * D, KN = NKV * D, F = hp.intermediate, V = hp.vocab;
   const float eps = hp.rms_eps;
   hipStream_t s = stream;
+  if (wtype != MTG_TYPE_Q8_0) {
+    enqueue_wt(mode);
+    return;
+  }
   if (mode != kModeLogits) {
     launch_embed(s, desc_dev, embd, H, embeds_dev, x);
     for (int l = 0; l < hp.n_layers; ++l) {
@@ -308,6 +343,39 @@ void Ctx::enqueue(int G, int mode) {
   if (mode == kModeAppend) return;
   if (mode == kModeVerifyPenalty) launch_penalty_bitmap(s, desc_dev, V, bitmap);
   launch_lm_head(s, G, desc_dev, embd, V, H, panel_h, bitmap, logits, part_keys);
+  launch_accept(s, desc_dev, part_keys, result_dev);
+}
+
+// The same step for f16 / q4_K weights: the activation of every GEMM is converted
+// to the weight type's vec_dot_type first (kernels_wt.hip).
+void Ctx::enqueue_wt(int mode) {
+  const int H = hp.hidden, NH = hp.n_heads, NKV = hp.n_kv_heads, D = hp.head_dim;
+  const int QN = NH * D, KN = NKV * D, F = hp.intermediate, V = hp.vocab;
+  const float eps = hp.rms_eps;
+  hipStream_t s = stream;
+  if (mode != kModeLogits) {
+    launch_embed_wt(s, wtype, desc_dev, embd, H, embeds_dev, x);
+    for (int l = 0; l < hp.n_layers; ++l) {
+      const Layer& y = layers[l];
+      const KvLayer kv = kv_layer(l);
+      launch_act_wt(s, wtype, desc_dev, x, H, y.attn_norm, eps, wact, nullptr);
+      launch_gemm_wt(s, wtype, 0, desc_dev, y.wqkv, nullptr, QN + 2 * KN, H, wact, qkv);
+      launch_qk_rope_append(s, desc_dev, qkv, NH, NKV, y.q_norm, y.k_norm, eps, rope, qbuf, kv);
+      launch_attention(s, desc_dev, qbuf, NH, NKV, kv, work, panel_o, obuf);
+      launch_act_wt(s, wtype, desc_dev, obuf, QN, nullptr, eps, wact, nullptr);
+      launch_gemm_wt(s, wtype, 1, desc_dev, y.wo, nullptr, H, QN, wact, x);
+      launch_act_wt(s, wtype, desc_dev, x, H, y.ffn_norm, eps, wact, nullptr);
+      launch_gemm_wt(s, wtype, 2, desc_dev, y.wg, y.wu, F, H, wact, act);
+      launch_act_wt(s, wtype, desc_dev, act, F, nullptr, eps, wact, nullptr);
+      launch_gemm_wt(s, wtype, 1, desc_dev, y.wd, nullptr, H, F, wact, x);
+    }
+    launch_act_wt(s, wtype, desc_dev, x, H, out_norm, eps, wact, hid);
+  } else {
+    launch_act_wt(s, wtype, desc_dev, embeds_dev, H, nullptr, eps, wact, nullptr);
+  }
+  if (mode == kModeAppend) return;
+  if (mode == kModeVerifyPenalty) launch_penalty_bitmap(s, desc_dev, V, bitmap);
+  launch_lm_head_wt(s, wtype, desc_dev, embd, V, H, wact, bitmap, logits, part_keys);
   launch_accept(s, desc_dev, part_keys, result_dev);
 }
 
@@ -454,7 +522,8 @@ int Ctx::embed(const int32_t* ids, int n, float* out) {
     int rc = check(hipMemcpyAsync(desc_dev, desc_host, sizeof(StepDesc), hipMemcpyHostToDevice,
                                   stream), "descriptor");
     if (rc) return rc;
-    launch_embed(stream, desc_dev, embd, hp.hidden, embeds_dev, x);
+    if (wtype == MTG_TYPE_Q8_0) launch_embed(stream, desc_dev, embd, hp.hidden, embeds_dev, x);
+    else launch_embed_wt(stream, wtype, desc_dev, embd, hp.hidden, embeds_dev, x);
     if ((rc = check(hipMemcpyAsync(out + (size_t)i0 * hp.hidden, x, (size_t)c * hp.hidden * 4,
                                    hipMemcpyDeviceToHost, stream), "embed rows")))
       return rc;

@@ -30,6 +30,7 @@ struct GraphSlot {
 struct Ctx {
   mtg_hparams hp{};
   int max_seq = 0, kv_type = MTG_TYPE_F32, past = 0;
+  int wtype = MTG_TYPE_Q8_0;  // q8_0: MFMA panel tiles; f16 / q4_K: GGUF rows (kernels_wt.hip)
   int exec = kExecStep;
   // persistent step kernel
   int nwg = 0;
@@ -57,6 +58,7 @@ struct Ctx {
   uint32_t* bitmap = nullptr;
   uint64_t* part_keys = nullptr;
   Panel panel_h{}, panel_o{}, panel_f{};
+  WtAct wact{};  // f16 / q4_K weights: the activation of the next GEMM
   AttnWork work{};
   StepDesc* desc_dev = nullptr;
   StepResult* result_dev = nullptr;
@@ -69,9 +71,13 @@ struct Ctx {
   int check(hipError_t e, const char* what);
   void* dalloc(size_t bytes, bool zero);
   int upload_q8(const void* blocks, int n, int k, uint8_t* dst, uint8_t* staging);
+  // bytes of an n x k weight matrix on the device, and its upload
+  size_t weight_bytes(int n, int k) const;
+  int upload_weights(const void* src, int n, int k, uint8_t* dst, uint8_t* staging);
   int init(const mtg_model_desc* d, int max_seq, int kv_type);
   KvLayer kv_layer(int l) const;
   void enqueue(int G, int mode);
+  void enqueue_wt(int mode);
   void fill_desc(int T, bool use_embeds, float penalty, const int32_t* tokens,
                  const int32_t* history, int n_history, bool write_logits);
   int run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_out,

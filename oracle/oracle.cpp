@@ -236,18 +236,26 @@ void mul_mat_q8(const BlockQ8* w, int k, int n, const float* x, int T, float* y)
   }
 }
 
-// mul_mat(f16 W, f32 x): x converted to f16 (vec_dot_type F16), f32 accumulation.
+// mul_mat(f16 W, f32 x): x converted to f16 (vec_dot_type F16), f32 accumulation
+// (ggml vec_dot_f16). Canonical order: K in 64 consecutive segments, each an fma
+// chain from 0 (a product of two f16 values is exact in f32), the 64 partials
+// reduced by the xor butterfly. ggml's own SIMD order is not pinned.
 void mul_mat_f16(const uint16_t* w, int k, int n, const float* x, int T, float* y) {
   std::vector<float> xh((size_t)T * k);
   for (size_t i = 0; i < xh.size(); ++i) xh[i] = h2f(f2h(x[i]));
+  const int seg = k / 64;
 #pragma omp parallel for schedule(static)
   for (int r = 0; r < n; ++r) {
     const uint16_t* wr = w + (size_t)r * k;
     for (int t = 0; t < T; ++t) {
       const float* xr = xh.data() + (size_t)t * k;
-      float acc = 0.0f;
-      for (int i = 0; i < k; ++i) acc += h2f(wr[i]) * xr[i];
-      y[(size_t)t * n + r] = acc;
+      float part[64];
+      for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (int e = 0; e < seg; ++e) acc = std::fma(h2f(wr[l * seg + e]), xr[l * seg + e], acc);
+        part[l] = acc;
+      }
+      y[(size_t)t * n + r] = butterfly64(part);
     }
   }
 }

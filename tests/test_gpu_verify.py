@@ -17,8 +17,8 @@ EXEC_NAMES = {mtg.EXEC_STEP_KERNEL: "step", mtg.EXEC_GRAPH: "graph", mtg.EXEC_EA
 
 
 def _setup(n_layers, prefix, kv_type=mtg.TYPE_F32, vocab=4096, seed=0, max_seq=256, jitter=0.05,
-           exec_mode=mtg.EXEC_STEP_KERNEL):
-    model = mtg.SynthModel(mtg.TYPE_Q8_0, seed=seed, std=0.02, gain_jitter=jitter, n_layers=n_layers,
+           exec_mode=mtg.EXEC_STEP_KERNEL, wtype=mtg.TYPE_Q8_0):
+    model = mtg.SynthModel(wtype, seed=seed, std=0.02, gain_jitter=jitter, n_layers=n_layers,
                            vocab=vocab)
     orc = oracle_py.Oracle(model, max_seq, kv_type)
     dec = mtg.Decoder(model, max_seq, kv_type)
@@ -168,3 +168,61 @@ def test_generated_token_stream_matches_oracle(penalty):
               "rewinds", "next_seed"):
         assert getattr(st1, k) == getattr(st0, k), k
     assert dec.past_len == orc.past_len
+
+
+WTYPES = [mtg.TYPE_F16, mtg.TYPE_Q4_K]
+WT_NAMES = {mtg.TYPE_F16: "f16", mtg.TYPE_Q4_K: "q4_K"}
+WT_EXECS = [mtg.EXEC_GRAPH, mtg.EXEC_EAGER]  # the persistent kernel streams q8_0 only
+
+
+@pytest.mark.parametrize("exec_mode", WT_EXECS, ids=lambda e: EXEC_NAMES[e])
+@pytest.mark.parametrize("wtype", WTYPES, ids=lambda w: WT_NAMES[w])
+def test_f16_and_q4k_weights_verify_matches_oracle(wtype, exec_mode):
+    """f16 and q4_K weights (the non-quantized path and the k-quant path): hidden
+    rows, logits, choices, acceptance and the appended KV equal the oracle's, for
+    T = 1, 8, 16 in a row, with an f16 KV cache."""
+    print("weights %s parity: exec=%s" % (WT_NAMES[wtype], EXEC_NAMES[exec_mode]), flush=True)
+    model, orc, dec, rng = _setup(2, 40, kv_type=mtg.TYPE_F16, exec_mode=exec_mode, wtype=wtype)
+    for T in (1, 8, 16):
+        tokens = rng.integers(0, model.hp.vocab, T)
+        c0, m0, h0, l0 = orc.verify(tokens, want_hidden=True, want_logits=True)
+        c1, m1, h1, l1 = dec.verify(tokens, want_hidden=True, want_logits=True)
+        _close(h1, h0, "hidden T=%d" % T)
+        _close(l1, l0, "logits T=%d" % T)
+        assert np.array_equal(c1, c0) and m1 == m0
+    k0, v0 = orc.kv_read(orc.past_len)
+    k1, v1 = dec.kv_read(dec.past_len)
+    _close(k1, k0, "K cache")
+    _close(v1, v0, "V cache")
+
+
+@pytest.mark.parametrize("wtype", WTYPES, ids=lambda w: WT_NAMES[w])
+def test_f16_and_q4k_weights_penalty_prefill_and_stream(wtype):
+    """The same weight types through the GPU prefill, the repetition penalty and
+    the whole controller loop: token stream and counters equal the oracle's."""
+    print("weights %s: prefill, penalty, token stream" % WT_NAMES[wtype], flush=True)
+    model = mtg.SynthModel(wtype, seed=9, std=0.02, gain_jitter=0.05, n_layers=2, vocab=4096)
+    orc = oracle_py.Oracle(model, 512)
+    dec = mtg.Decoder(model, 512)
+    assert dec.exec_mode == mtg.EXEC_GRAPH
+    with pytest.raises(Exception):
+        dec.set_exec(mtg.EXEC_STEP_KERNEL)
+    rng = np.random.default_rng(10)
+    rows = orc.embed(rng.integers(0, 4096, 37))
+    ids = rng.integers(0, 4096, 5)
+    _close(dec.embed(ids), orc.embed(ids), "embed")
+    _close(dec.prefill(rows), orc.prefill(rows), "prefill hidden")
+    hist = rng.integers(0, 4096, 120).tolist()
+    tokens = rng.integers(0, 4096, 8)
+    c0, m0, _, l0 = orc.verify(tokens, history=hist, penalty=1.3, want_logits=True)
+    c1, m1, _, l1 = dec.verify(tokens, history=hist, penalty=1.3, want_logits=True)
+    _close(l1, l0, "logits with penalty")
+    assert np.array_equal(c1, c0) and m1 == m0
+    prompt = rng.integers(0, 4096, 20).astype(np.int32)
+    stream = rng.integers(0, 4096, 37).astype(np.int32)
+    fn, user, _keep = mtg.stream_drafter(prompt, stream)
+    first = int(rng.integers(0, 4096))
+    ids0, st0 = orc.generate_from(first, 200, max_steps=12, penalty=1.1, max_draft=7, draft=fn, user=user)
+    ids1, st1 = dec.generate_from(first, 200, max_steps=12, penalty=1.1, max_draft=7, draft=fn, user=user)
+    assert ids1.tolist() == ids0.tolist()
+    assert st1.accepted == st0.accepted and st1.proposed == st0.proposed

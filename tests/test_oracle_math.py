@@ -153,6 +153,20 @@ def test_f16_and_q4k_mul_mat_close_to_float64_of_quantized_operands(wtype):
     assert np.abs(wq - wf).max() <= (1e-3 if wtype == mtg.TYPE_F16 else 0.25) * np.abs(wf).max()
 
 
+def test_f16_mul_mat_exact_on_small_integers():
+    """Small-integer f16 weights and activations: every product and partial sum is
+    exact in f32, so any summation order gives the float64 value bit for bit; a
+    dropped, repeated or misplaced element does not."""
+    rng = np.random.default_rng(16)
+    for k in (1024, 2048, 3072):
+        n, T = 24, 5
+        w = rng.integers(-8, 9, (n, k)).astype(np.float16)
+        x = rng.integers(-8, 9, (T, k)).astype(np.float32)
+        got = oracle_py.mul_mat(mtg.TYPE_F16, w.view(np.uint8).reshape(-1).copy(), k, n, x)
+        want = x.astype(np.float64) @ w.astype(np.float64).T
+        assert np.array_equal(got.astype(np.float64), want)
+
+
 def test_rms_norm_matches_float64_closed_form():
     rng = np.random.default_rng(7)
     for n in (1024, 128, 96):
