@@ -161,6 +161,10 @@ def main():
     n_prompt = cfg["blocks"] * AUDIO_ROWS + cfg["text"]
     max_seq = n_prompt + (args.warmup + steps + 2) * cfg["K"] + 16
     dec = mtg.Decoder(model, max_seq, cfg["kv"])
+    if args.exec == "step" and dec.exec_mode != mtg.EXEC_STEP_KERNEL:
+        # the persistent kernel streams q8_0 only: f16 / q4_K weights run the
+        # per-op kernels from a captured graph
+        args.exec = "graph"
     dec.set_exec({"step": mtg.EXEC_STEP_KERNEL, "graph": mtg.EXEC_GRAPH, "eager": mtg.EXEC_EAGER}[args.exec])
     rows, text, stream = build_prompt(model, dec, cfg)
     hid = dec.prefill(rows)

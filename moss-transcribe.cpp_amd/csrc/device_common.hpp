@@ -501,7 +501,8 @@ __device__ void attn_chunk(const AttnSrc& a, const float* q, int ncol, int T, in
                            int key0, float scale, float* vbuf, float* sp, float* out_ml,
                            float* out_o) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  // 1. V chunk -> LDS (zeros past kvlen)
+  // 1. V chunk -> LDS (zeros past kvlen); unrolled so that the loads are in flight together
+#pragma unroll
   for (int idx = tid; idx < kChunk * kHeadDim / 4; idx += 256) {
     const int j = idx >> 5, d = (idx & 31) * 4, key = key0 + j;
     const v4f v = key < kvlen ? attn_row4(a, true, key, d) : (v4f){0.f, 0.f, 0.f, 0.f};
@@ -515,6 +516,7 @@ __device__ void attn_chunk(const AttnSrc& a, const float* q, int ncol, int T, in
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
     if (c0 < ncol && kvalid) {
+#pragma unroll 8
       for (int d = 0; d < kHeadDim; d += 4) {
         const v4f kf = attn_row4(a, false, key, d);
 #pragma unroll
@@ -573,20 +575,43 @@ __device__ void attn_chunk(const AttnSrc& a, const float* q, int ncol, int T, in
 
 // Merge the chunk partials of one query column (canonical order); returns
 // element d of the attention output. part_ml/part_o point at chunk 0 of the
-// column, consecutive chunks `stride_ml` / `stride_o` floats apart.
+// column, consecutive chunks `stride_ml` / `stride_o` floats apart. Lane c of a
+// wave loads (m, l) of chunk c0 + c, so a round of loads covers 64 chunks; the
+// O values come 16 chunks per round; f = exp(m_c - M) is computed once per
+// chunk and read by every thread (readlane) for the two chunk-ordered chains.
 template <bool COH>
 __device__ __forceinline__ float attn_merge(const float* part_ml, const float* part_o, int nch,
                                             size_t stride_ml, size_t stride_o, int d) {
   auto ld = [](const float* p) { return COH ? ld_coh(p) : *p; };
+  const int lane = threadIdx.x & 63;
   float M = -INFINITY;
-  for (int c = 0; c < nch; ++c) M = fmaxf(M, ld(part_ml + c * stride_ml));
+  for (int c0 = 0; c0 < nch; c0 += 64) {
+    const float m = c0 + lane < nch ? ld(part_ml + (size_t)(c0 + lane) * stride_ml) : -INFINITY;
+    M = fmaxf(M, wave_max_f(m));
+  }
   float L = 0.0f, O = 0.0f;
-  for (int c = 0; c < nch; ++c) {
-    const float m = ld(part_ml + c * stride_ml);
-    if (m == -INFINITY) continue;
-    const float f = dev_expf(__fsub_rn(m, M));
-    L = fmaf(ld(part_ml + c * stride_ml + 1), f, L);
-    O = fmaf(ld(part_o + c * stride_o + d), f, O);
+  for (int c0 = 0; c0 < nch; c0 += 64) {
+    const int c = c0 + lane;
+    const float m = c < nch ? ld(part_ml + (size_t)c * stride_ml) : -INFINITY;
+    const float l = c < nch ? ld(part_ml + (size_t)c * stride_ml + 1) : 0.0f;
+    const float f = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, M));
+    const int nb = min(64, nch - c0);
+    for (int i0 = 0; i0 < nb; i0 += 16) {
+      float o[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        o[i] = i0 + i < nb ? ld(part_o + (size_t)(c0 + i0 + i) * stride_o + d) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (i0 + i >= nb) break;
+        const float mc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), i0 + i));
+        if (mc == -INFINITY) continue;
+        const float fc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), i0 + i));
+        const float lc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), i0 + i));
+        L = fmaf(lc, fc, L);
+        O = fmaf(o[i], fc, O);
+      }
+    }
   }
   return __fdiv_rn(O, L);
 }
