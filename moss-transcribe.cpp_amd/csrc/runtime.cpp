@@ -394,7 +394,7 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
       epoch = 0;
     }
     const int smode = mode == kModeAppend ? kStepAppend : kStepVerify;
-    if ((rc = check(launch_step(stream, G, params_dev, desc_dev, epoch, smode), "step kernel launch")))
+    if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, params_dev, desc_dev, epoch, smode), "step kernel launch")))
       return rc;
     epoch += step_progress_per_step(hp.n_layers);
   } else if (exec != kExecEager) {

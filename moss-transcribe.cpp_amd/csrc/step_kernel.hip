@@ -510,11 +510,12 @@ struct KvRegs {
   uint32_t v[2][16];
 };
 
+template <int KVH>
 __device__ __forceinline__ void kv_prefetch(const LayerDev& Ly, const StepParams& P, int g, int key0,
                                             int past, KvRegs& r) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, kl = lane & 15, kk = lane >> 4;
-  const int es = P.kv_f16 ? 2 : 4;
+  constexpr int es = KVH ? 2 : 4;
   // The kv head's rows [0, past). Every key-dependent part of an address is in
   // the per-lane offset (the scalar offset is 0), so a key >= past lies beyond
   // num_records and its load returns 0 without touching memory.
@@ -525,7 +526,7 @@ __device__ __forceinline__ void kv_prefetch(const LayerDev& Ly, const StepParams
   const int kvo = ((key0 + 16 * wave + kl) * cHD + kk) * es;
   // V: vreg[h][s] = V[key0 + 4s + kk][16(2w + h) + kl]
   const int vvo = ((key0 + kk) * cHD + 32 * wave + kl) * es;
-  if (es == 2) {
+  if constexpr (KVH) {
 #pragma unroll
     for (int s = 0; s < 32; ++s) r.k[s] = __builtin_amdgcn_raw_buffer_load_b16(rk, kvo + 4 * s * 2, 0, 0);
 #pragma unroll
@@ -553,11 +554,11 @@ __device__ __forceinline__ float kv_val(uint32_t bits, bool f16) {
 // then norms (q, k) and ropes them side by side and writes them to LDS.
 // Straight-line over the NS slots; slots past the rows compute on zeros and store
 // nothing.
-template <int NS>
+template <int NS, int KVH>
 __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& Ly, int T, int past, int g,
                                            int r0, int nrows, float* q_lds, float* knew, float* vnew) {
   const int lane = threadIdx.x & 63, ncol = 2 * T;
-  const bool f16kv = P.kv_f16 != 0;
+  constexpr bool f16kv = KVH != 0;
   const Rsrc rq = mk_rsrc(P.qkv, kMaxRows * cNQKV * 4);
   float x0[NS], x1[NS], g0[NS], g1[NS], rc[NS], rs[NS];
   int kind[NS], tt[NS];
@@ -610,12 +611,12 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
 // One attention item: chunk `chunk` of kv head g over the ncol = 2T query
 // columns (col = hl*T + t for q head 2g + hl). LDS: q [32][132], knew/vnew
 // [16][132], sp [32][68].
-template <int G>
+template <int G, int KVH>
 __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& Ly, int T, int past, int g, int chunk,
                                           const KvRegs& kv, uint8_t* lds, bool prof) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, kl = lane & 15,
             kk = lane >> 4;
-  const bool f16kv = P.kv_f16 != 0;
+  constexpr bool f16kv = KVH != 0;
   const int kvlen = past + T, ncol = 2 * T, key0 = chunk * kChunk;
   float* q_lds = (float*)lds;
   float* knew = q_lds + kMaxCols * cQStride;
@@ -628,10 +629,10 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   const int nrows = ncol + (has_new ? 2 * T : 0);
   if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 21); }
   if (!has_new) {
-    stage_pass<4 * G>(P, Ly, T, past, g, wave, nrows, q_lds, knew, vnew);
+    stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, nrows, q_lds, knew, vnew);
   } else {
     for (int r0 = wave; r0 < nrows; r0 += 32)
-      stage_pass<8>(P, Ly, T, past, g, r0, nrows, q_lds, knew, vnew);
+      stage_pass<8, KVH>(P, Ly, T, past, g, r0, nrows, q_lds, knew, vnew);
   }
   bar();
   if (prof) wmark(P, 1, 16);
@@ -1038,7 +1039,7 @@ __host__ __device__ constexpr size_t step_lds_x_offset(int G) {
 }
 __device__ __forceinline__ uint32_t ph(int l, int p) { return 2u + (uint32_t)(l * kPhases + p); }
 
-template <int G>
+template <int G, int KVH>
 __global__ void __launch_bounds__(kT, 1)
 k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uint32_t epoch,
         int mode) {
@@ -1123,7 +1124,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   }
   // prefetch layer 0: q|k|v tile and the first attention item's K / V
   wt_load<4>(layer_at(P, 0).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-  if (has_attn) kv_prefetch(layer_at(P, 0), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+  if (has_attn) kv_prefetch<KVH>(layer_at(P, 0), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
 
   for (int l = 0; l < L; ++l) {
     const LayerDev& Ly = layer_at(P, l);
@@ -1147,8 +1148,8 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       mark(P, 3 + 12 * l + 2);
       wmark(P, l, 2);
       for (int item = first_item; item < n_items; item += kNwg) {
-        if (item != first_item) kv_prefetch(Ly, P, item / nch, (item % nch) * kChunk, past, kv);
-        attn_item<G>(P, Ly, T, past, item / nch, item % nch, kv, lds, l == 1 && P.timing != nullptr);
+        if (item != first_item) kv_prefetch<KVH>(Ly, P, item / nch, (item % nch) * kChunk, past, kv);
+        attn_item<G, KVH>(P, Ly, T, past, item / nch, item % nch, kv, lds, l == 1 && P.timing != nullptr);
       }
       publish(c, next_done(l, kPhAttn));
       mark(P, 3 + 12 * l + 3);
@@ -1176,7 +1177,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       if (!gu && l + 1 < L) {  // nothing more in this layer: prefetch the next one
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-        if (has_attn) kv_prefetch(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+        if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
       }
     }
     // ---- O-proj: x += W_o o ----
@@ -1196,7 +1197,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       wt_load<12>(Ly.wd + (size_t)w * cBF * kUnitBytes, 12 * wave, ba, bs);
       // the next layer's attention K / V, so that they are in flight before the down wait
       if (has_attn && l + 1 < L)
-        kv_prefetch(layer_at(P, l + 1), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+        kv_prefetch<KVH>(layer_at(P, l + 1), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
     }
     // ---- GATE/UP: act = silu(g) * u, as q8_0 blocks ----
     if (gu) {
@@ -1213,7 +1214,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       if (l + 1 < L) {
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-        if (has_attn) kv_prefetch(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+        if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
       }
     }
     // ---- DOWN: x += W_d act ----
@@ -1235,7 +1236,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     if (!od && !gu && !has_merge && l + 1 < L) {
       const LayerDev& Ln = layer_at(P, l + 1);
       wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-      if (has_attn) kv_prefetch(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+      if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
     }
   }
 
@@ -1280,20 +1281,23 @@ uint32_t step_progress_per_step(int n_layers) { return 2u + (uint32_t)(n_layers 
 size_t step_lds_bytes(int G) { return step_lds_x_offset(G) + (size_t)G * 8 * 16 * 4; }
 
 hipError_t prepare_step_kernels() {
-  hipError_t e = hipFuncSetAttribute((const void*)k_step<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)step_lds_bytes(1));
-  if (e != hipSuccess) return e;
-  return hipFuncSetAttribute((const void*)k_step<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)step_lds_bytes(2));
+  const void* fns[4] = {(const void*)k_step<1, 0>, (const void*)k_step<1, 1>, (const void*)k_step<2, 0>,
+                        (const void*)k_step<2, 1>};
+  for (int i = 0; i < 4; ++i) {
+    const hipError_t e =
+        hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)step_lds_bytes(1 + i / 2));
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
-hipError_t launch_step(hipStream_t s, int G, const StepParams* P, const StepDesc* desc, uint32_t epoch,
-                        int mode) {
+hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
+                        uint32_t epoch, int mode) {
   void* args[] = {(void*)&P, (void*)&desc, (void*)&epoch, (void*)&mode};
   const size_t lds = step_lds_bytes(G);
-  if (G == 1)
-    return hipLaunchCooperativeKernel((const void*)k_step<1>, dim3(kNwg), dim3(kT), args, lds, s);
-  return hipLaunchCooperativeKernel((const void*)k_step<2>, dim3(kNwg), dim3(kT), args, lds, s);
+  const void* fn = G == 1 ? (kv_f16 ? (const void*)k_step<1, 1> : (const void*)k_step<1, 0>)
+                          : (kv_f16 ? (const void*)k_step<2, 1> : (const void*)k_step<2, 0>);
+  return hipLaunchCooperativeKernel(fn, dim3(kNwg), dim3(kT), args, lds, s);
 }
 
 }  // namespace mtg
