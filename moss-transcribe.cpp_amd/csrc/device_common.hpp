@@ -458,6 +458,20 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return max(v, o);
 }
 
+// exact integer wave sum (any order is exact)
+__device__ __forceinline__ int wave_sum_i(int v) {
+  uint32_t a, b;
+  pair_split<32>((uint32_t)v, a, b);
+  v = (int)a + (int)b;
+  pair_split<16>((uint32_t)v, a, b);
+  v = (int)a + (int)b;
+  v += (int)dpp_u<kDppRor8>((uint32_t)v);
+  v += (int)dpp_u<kDppRor4>((uint32_t)v);
+  v += (int)dpp_u<kDppRor2>((uint32_t)v);
+  v += (int)dpp_u<kDppRor1>((uint32_t)v);
+  return v;
+}
+
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   uint32_t a, b;
   pair_split<32>(v, a, b);

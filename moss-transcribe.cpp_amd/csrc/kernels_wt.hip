@@ -48,20 +48,6 @@ __device__ __forceinline__ float row_rms_scale(const float* xr, int K, float eps
   return dev_rms_scale((float)(s / (double)K), eps);
 }
 
-// exact integer wave sum (any order is exact)
-__device__ __forceinline__ int wave_sum_i(int v) {
-  uint32_t a, b;
-  pair_split<32>((uint32_t)v, a, b);
-  v = (int)a + (int)b;
-  pair_split<16>((uint32_t)v, a, b);
-  v = (int)a + (int)b;
-  v += (int)dpp_u<kDppRor8>((uint32_t)v);
-  v += (int)dpp_u<kDppRor4>((uint32_t)v);
-  v += (int)dpp_u<kDppRor2>((uint32_t)v);
-  v += (int)dpp_u<kDppRor1>((uint32_t)v);
-  return v;
-}
-
 // ------------------------------------------------------- activations ------
 // One workgroup (256 threads) per verify row. gain == nullptr: no norm (the
 // attention output and the SwiGLU product go in as they are).

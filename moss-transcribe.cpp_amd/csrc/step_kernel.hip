@@ -290,10 +290,12 @@ __device__ __forceinline__ void gemm_finish(float acc[NM][G][4], float* red, Rsr
 // Gate and up of rows 32j..32j+31 (two 16-row tiles; acc[0], acc[1] gate,
 // acc[2], acc[3] up): the wave slice sums meet in LDS in wave order, then the
 // even and odd halves, SwiGLU, and each row t's 32 values leave as one q8_0
-// block (the activation quantization of the down projection).
+// block. Wave w finishes the values of row slot q = w of every tile (lane l
+// holds tile rows 4 (l / 16) + q for verify row t = 8 cg + l % 8), so the four
+// waves share the SwiGLU and quantization; the block maxima meet in LDS (amx).
 template <int G>
-__device__ __forceinline__ void gu_finish(float acc[4][G][4], float* red, const StepParams& P, int j,
-                                          int T) {
+__device__ __forceinline__ void gu_finish(float acc[4][G][4], float* red, float* amx, const StepParams& P,
+                                          int j, int T) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
 #pragma unroll
   for (int m = 0; m < 4; ++m)
@@ -302,44 +304,42 @@ __device__ __forceinline__ void gu_finish(float acc[4][G][4], float* red, const 
 #pragma unroll
       for (int q = 0; q < 4; ++q) red[((wave * 4 + m) * G * 4 + cg * 4 + q) * 64 + lane] = acc[m][cg][q];
   bar();
-  if (wave == 0) {
+  const int q = wave;
+  float va[G], vb[G];
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+  for (int cg = 0; cg < G; ++cg) {
+    float v4[4];
 #pragma unroll
-      for (int cg = 0; cg < G; ++cg)
+    for (int m = 0; m < 4; ++m) {
+      float s = red[((0 * 4 + m) * G * 4 + cg * 4 + q) * 64 + lane];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float s = red[((0 * 4 + m) * G * 4 + cg * 4 + q) * 64 + lane];
+      for (int wv = 1; wv < 4; ++wv) s = __fadd_rn(s, red[((wv * 4 + m) * G * 4 + cg * 4 + q) * 64 + lane]);
+      v4[m] = __fadd_rn(s, dpp_f<kDppRor8>(s));
+    }
+    va[cg] = dev_swiglu(v4[0], v4[2]);
+    vb[cg] = dev_swiglu(v4[1], v4[3]);
+    // this wave's part of the block maximum: its two values, over the lanes of
+    // the same t (xor 16, 32)
+    const float am = __uint_as_float(
+        pair_max_u<32>(pair_max_u<16>(__float_as_uint(fmaxf(fabsf(va[cg]), fabsf(vb[cg]))))));
+    if (lane < 16) amx[(wave * G + cg) * 16 + lane] = am;
+  }
+  bar();
+  const Rsrc rq = mk_rsrc(P.aq, kMaxRows * cF);
+  const Rsrc rs = mk_rsrc(P.aqs, kMaxRows * (cF / 32) * 4);
 #pragma unroll
-          for (int wv = 1; wv < 4; ++wv) s = __fadd_rn(s, red[((wv * 4 + m) * G * 4 + cg * 4 + q) * 64 + lane]);
-          acc[m][cg][q] = __fadd_rn(s, dpp_f<kDppRor8>(s));
-        }
-    const Rsrc rq = mk_rsrc(P.aq, kMaxRows * cF);
-    const Rsrc rs = mk_rsrc(P.aqs, kMaxRows * (cF / 32) * 4);
+  for (int cg = 0; cg < G; ++cg) {
+    const int t = cg * 8 + (lane & 7);
+    if ((lane & 15) < 8 && t < T) {
+      float amax = amx[(0 * G + cg) * 16 + (lane & 15)];
 #pragma unroll
-    for (int cg = 0; cg < G; ++cg) {
-      float va[4], vb[4], amax = 0.0f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        va[q] = dev_swiglu(acc[0][cg][q], acc[2][cg][q]);
-        vb[q] = dev_swiglu(acc[1][cg][q], acc[3][cg][q]);
-        amax = fmaxf(amax, fmaxf(fabsf(va[q]), fabsf(vb[q])));
-      }
-      // the block's 32 rows sit in lanes (lane & 15) + 16 m, m = 0..3
-      amax = __uint_as_float(pair_max_u<32>(pair_max_u<16>(__float_as_uint(amax))));
-      const int t = cg * 8 + (lane & 7);
-      if ((lane & 15) < 8 && t < T) {
-        uint32_t pa = 0, pb = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          pa |= q8_code(va[q], amax) << (8 * q);
-          pb |= q8_code(vb[q], amax) << (8 * q);
-        }
-        const int row = 32 * j + 4 * (lane >> 4);
-        __builtin_amdgcn_raw_buffer_store_b32(pa, rq, t * cF + row, 0, 16);
-        __builtin_amdgcn_raw_buffer_store_b32(pb, rq, t * cF + row + 16, 0, 16);
-        if (lane < 16) stc1(rs, (uint32_t)((t * (cF / 32) + j) * 4), q8_scale(amax));
-      }
+      for (int wv = 1; wv < 4; ++wv) amax = fmaxf(amax, amx[(wv * G + cg) * 16 + (lane & 15)]);
+      const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+      const int row = 32 * j + 4 * (lane >> 4) + q;
+      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(int8_t)rintf(__fmul_rn(va[cg], id)), rq, t * cF + row, 0, 16);
+      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(int8_t)rintf(__fmul_rn(vb[cg], id)), rq, t * cF + row + 16, 0,
+                                           16);
+      if (wave == 0 && lane < 16) stc1(rs, (uint32_t)((t * (cF / 32) + j) * 4), q8_scale(amax));
     }
   }
   bar();
@@ -1028,13 +1028,15 @@ __device__ void accept(const uint64_t* part_keys, const int32_t* tokens, StepRes
 }
 
 // ---------------------------------------------------------------- kernel ----
+// per column group: the wave slice sums of four tiles, then the SwiGLU block maxima
+constexpr size_t kRedBytes = (size_t)4 * 4 * 4 * 64 * 4 + 4 * 16 * 4;
 // LDS: the GEMM panel + reduction space, or the attention's q / new rows /
 // probabilities (the phases reuse it), then the residual columns of the o-proj /
 // down tile ([8G rows][16], kept across phases).
 __host__ __device__ constexpr size_t step_lds_x_offset(int G) {
-  return ((size_t)G * cBF * (1024 + 64) + (size_t)4 * 4 * G * 4 * 64 * 4 >
+  return ((size_t)G * cBF * (1024 + 64) + kRedBytes * G >
           ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride) * 4)
-             ? (size_t)G * cBF * (1024 + 64) + (size_t)4 * 4 * G * 4 * 64 * 4
+             ? (size_t)G * cBF * (1024 + 64) + kRedBytes * G
              : ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride) * 4;
 }
 __device__ __forceinline__ uint32_t ph(int l, int p) { return 2u + (uint32_t)(l * kPhases + p); }
@@ -1207,7 +1209,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       float acc[4][G][4] = {};
 #pragma unroll
       for (int m = 0; m < 4; ++m) wt_mma<G, 4>(ba + 4 * m, bs + 4 * m, 4 * wave, cBH, pcodes, pscales, acc[m]);
-      gu_finish<G>(acc, red, P, w - cOTiles, T);
+      gu_finish<G>(acc, red, red + 4 * 4 * G * 4 * 64, P, w - cOTiles, T);
       wmark(P, l, 24);
       publish(c, next_done(l, kPhGu));
       wmark(P, l, 9);
