@@ -1143,7 +1143,6 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     publish(c, next_done(l, kPhQkv));
     mark(P, 3 + 12 * l + 1);
     wmark(P, l, 1);
-    if (od) wt_load<8>(Ly.wo + (size_t)w * cBQ * kUnitBytes, 8 * wave, ba, bs);
     // ---- ATTN: items of this workgroup ----
     if (has_attn) {
       if (!wait_all(c, ph(l, kPhAttn) - 1, l == 1 ? wslot(w, 14) : -1)) return;
@@ -1157,6 +1156,9 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       mark(P, 3 + 12 * l + 3);
       wmark(P, l, 3);
     }
+    // the o-proj tile's weights: issued after the attention, so that no register
+    // holds them through it (the o-proj starts after the merge, well after they land)
+    if (od) wt_load<8>(Ly.wo + (size_t)w * cBQ * kUnitBytes, 8 * wave, ba, bs);
     if (gu) {  // gate / up tiles 2j, 2j + 1 of this layer
       const int j = w - cOTiles;
       wt_load<4>(Ly.wg + (size_t)(2 * j) * cBH * kUnitBytes, 4 * wave, ba, bs);
