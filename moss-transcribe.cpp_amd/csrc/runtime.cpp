@@ -107,6 +107,9 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
       hipHostMalloc((void**)&result_host, sizeof(StepResult), hipHostMallocDefault) != hipSuccess)
     return fail(MTG_ERR_NOMEM, "pinned host buffers");
   std::memset(desc_host, 0, sizeof(StepDesc));
+  std::memset(result_host, 0, sizeof(StepResult));
+  if (hipHostGetDevicePointer((void**)&result_map, result_host, 0) != hipSuccess)
+    return fail(MTG_ERR_DEVICE, "mapped result buffer");
 
   // weights
   uint8_t* staging = nullptr;  // q8_0 rows before the re-tiling
@@ -287,7 +290,7 @@ int Ctx::init_step_kernel() {
   P.oqs = (float*)dalloc((size_t)kMaxRows * hp.n_heads * hp.head_dim / 32 * 4, true);
   P.aq = (int8_t*)dalloc((size_t)kMaxRows * F, true);
   P.aqs = (float*)dalloc((size_t)kMaxRows * F / 32 * 4, true);
-  P.result = result_dev;
+  P.result = result_map;  // choices and n_match go straight to pinned host memory
   P.flags = (uint32_t*)dalloc((size_t)nwg * kFlagStride * 4, true);
   P.err = &result_dev->err;
   P.timing = nullptr;
@@ -394,6 +397,8 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
       epoch = 0;
     }
     const int smode = mode == kModeAppend ? kStepAppend : kStepVerify;
+    result_host->n_match = -1;  // the kernel's acceptance overwrites it
+    result_host->err = 0;
     if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, params_dev, desc_dev, epoch, smode), "step kernel launch")))
       return rc;
     epoch += step_progress_per_step(hp.n_layers);
@@ -415,8 +420,11 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
     if ((rc = check(hipGetLastError(), "kernel launch"))) return rc;
   }
   if (timed && (rc = check(hipEventRecord(ev_stop, stream), "timing event"))) return rc;
-  if ((rc = check(hipMemcpyAsync(result_host, result_dev, sizeof(StepResult), hipMemcpyDeviceToHost,
-                                 stream), "result")))
+  // the step kernel's verify writes its choices into the mapped host buffer; the
+  // other paths (per-op kernels, appends) bring the result over with a copy
+  const bool mapped = exec == kExecStep && step_ok && (mode == kModeVerify || mode == kModeVerifyPenalty);
+  if (!mapped && (rc = check(hipMemcpyAsync(result_host, result_dev, sizeof(StepResult),
+                                             hipMemcpyDeviceToHost, stream), "result")))
     return rc;
   if (want_hidden && hidden_out &&
       (rc = check(hipMemcpyAsync(hidden_out, hid, (size_t)T * hp.hidden * 4, hipMemcpyDeviceToHost,
@@ -435,9 +443,15 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
     timing_past += desc_host->past;
     timing_rows += T;
   }
+  if (mapped && result_host->n_match < 0) {
+    // the kernel left before its acceptance: a bounded wait ran out
+    (void)hipMemcpy(&result_host->err, &result_dev->err, sizeof(int32_t), hipMemcpyDeviceToHost);
+    if (!result_host->err) return fail(MTG_ERR_DEVICE, "step kernel: no result");
+  }
   if (result_host->err) {
     // a bounded barrier wait ran out: every workgroup left the kernel
     (void)hipMemset(&result_dev->err, 0, sizeof(int32_t));
+    result_host->err = 0;
     return fail(MTG_ERR_DEVICE, "step kernel: grid barrier wait timed out");
   }
   return MTG_OK;

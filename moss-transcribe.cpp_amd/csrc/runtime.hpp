@@ -64,6 +64,7 @@ struct Ctx {
   StepResult* result_dev = nullptr;
   StepDesc* desc_host = nullptr;      // pinned
   StepResult* result_host = nullptr;  // pinned
+  StepResult* result_map = nullptr;   // result_host as the device sees it (the step kernel writes it)
   GraphSlot graphs[2 * kModes];
 
   ~Ctx();
