@@ -835,7 +835,7 @@ __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, 
 // 8-deep register ring; per tile the canonical 4-slice sums, the penalty and
 // 64-bit first-max keys.
 template <int G>
-__device__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const uint8_t* pcodes,
+__device__ __forceinline__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const uint8_t* pcodes,
                         const float* pscales, uint64_t* s_best) {
   // a called function receives P's fields and T in vector registers: make the
   // tile arithmetic wave-uniform again, or every buffer load with a scalar
@@ -862,7 +862,7 @@ __device__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const 
   for (int cg = 0; cg < G; ++cg) best[cg] = 0;
   const int my_tiles = gw < n_tiles ? (n_tiles - 1 - gw) / nwaves + 1 : 0;
   const int units = my_tiles * cBH;  // (tile, pair) units of this wave, in order
-  constexpr int R = 8;
+  constexpr int R = 16;
   v4i ra[R];
   uint2 rs[R];
   const Rsrc re = mk_rsrc(uniform_ptr(P.embd), (uint32_t)((size_t)n_tiles * cBH * kUnitBytes));
