@@ -985,6 +985,7 @@ __device__ __forceinline__ void lm_head(const StepParams& P, const StepDesc* des
 // prefix of drafts that matches. Thread i holds workgroup i's keys of every row;
 // those loads and the draft tokens' are in flight together. Per row a wave max,
 // then the four waves.
+template <int G>
 __device__ void accept(const uint64_t* part_keys, const int32_t* tokens, StepResult* result, int T, int nwg,
                        uint64_t* s_red, int32_t* s_choice, int32_t* s_tok, uint64_t* timing, int slot) {
   static_assert(kNwg <= kT, "one thread per workgroup's keys");
@@ -993,9 +994,10 @@ __device__ void accept(const uint64_t* part_keys, const int32_t* tokens, StepRes
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const Rsrc rk = mk_rsrc(uniform_ptr(part_keys), (uint32_t)(nwg * kMaxRows * 8));
   const Rsrc rt = mk_rsrc(uniform_ptr(tokens), (uint32_t)(T * 4));
-  uint64_t key[kMaxRows];
+  constexpr int R = 8 * G;  // rows of this launch's column groups
+  uint64_t key[R];
 #pragma unroll
-  for (int h = 0; h < kMaxRows / 2; ++h) {
+  for (int h = 0; h < R / 2; ++h) {
     const v4u q = __builtin_amdgcn_raw_buffer_load_b128(
         rk, (int)threadIdx.x < nwg ? (uint32_t)((threadIdx.x * kMaxRows + 2 * h) * 8) : 0x80000000u, 0, 16);
     key[2 * h] = ((uint64_t)q.y << 32) | q.x;
@@ -1006,7 +1008,7 @@ __device__ void accept(const uint64_t* part_keys, const int32_t* tokens, StepRes
   if ((int)threadIdx.x < T) s_tok[threadIdx.x] = tok;
   if (timing) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); if (threadIdx.x == 0) gst<uint64_t>(uniform_ptr(timing) + slot, wall_clock64()); }
 #pragma unroll
-  for (int t = 0; t < kMaxRows; ++t) {  // every row, so that key[] stays in registers
+  for (int t = 0; t < R; ++t) {  // every row slot, so that key[] stays in registers
     const uint64_t b = wave_max_u64(key[t]);
     if (lane == 0) s_red[wave * kMaxRows + t] = b;
   }
@@ -1263,7 +1265,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   if (w == 0) {
     if (!wait_all(c, lm)) return;
     mark(P, 5 + 12 * L);
-    accept(P.part_keys, desc->tokens, P.result, T, kNwg, s_red, s_choice, s_tok, P.timing, 7 + 12 * L);
+    accept<G>(P.part_keys, desc->tokens, P.result, T, kNwg, s_red, s_choice, s_tok, P.timing, 7 + 12 * L);
     mark(P, 6 + 12 * L);
   }
 #undef RX
