@@ -151,7 +151,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box here has one MI355X, and the verify path "
-              "shards only across independent streams (see DESIGN.md).", file=sys.stderr)
+              "shards only across independent streams (one decoder per recording, one GPU each).", file=sys.stderr)
         sys.exit(2)
     cfg = CONFIGS[args.config]
     steps = args.steps if args.steps is not None else cfg["steps"]

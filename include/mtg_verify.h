@@ -247,6 +247,13 @@ int32_t mtg_exec_mode(const mtg_ctx* ctx);
 enum { MTG_DEBUG_X = 0, MTG_DEBUG_QKV = 1, MTG_DEBUG_O = 2, MTG_DEBUG_ACT = 3, MTG_DEBUG_HIDDEN = 4 };
 int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes);
 
+/* Failure-path check (no counterpart in the reference): the next step on the
+ * persistent kernel starts with its error word raised, so every bounded wait of
+ * that launch gives up at its first poll and every workgroup leaves, as after a
+ * wait that ran out. The step returns MTG_ERR_DEVICE without advancing past_len;
+ * the following steps run normally. */
+int mtg_debug_abort_next_step(mtg_ctx* ctx);
+
 /* Profiling of the persistent step kernel: when enabled, the kernel records a
  * 100 MHz device clock into MTG_PROFILE_SLOTS slots. Workgroup 0, slots 0..1023:
  * 0 at the start; for layer l at 3 + 12 l + {0, 1}: QKV inputs ready / QKV

@@ -113,6 +113,13 @@ int32_t mtg_step_profile_read(mtg_ctx* ctx, uint64_t* marks, int32_t n) {
   return count;
 }
 
+int mtg_debug_abort_next_step(mtg_ctx* ctx) {
+  if (!ctx) return MTG_ERR_INVALID;
+  if (!ctx->impl.step_ok) return ctx->impl.fail(MTG_ERR_UNSUPPORTED, "no step kernel");
+  ctx->impl.abort_next = true;
+  return MTG_OK;
+}
+
 int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes) {
   if (!ctx || !out) return MTG_ERR_INVALID;
   const Ctx& c = ctx->impl;

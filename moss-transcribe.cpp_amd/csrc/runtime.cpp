@@ -399,6 +399,11 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
     const int smode = mode == kModeAppend ? kStepAppend : kStepVerify;
     result_host->n_match = -1;  // the kernel's acceptance overwrites it
     result_host->err = 0;
+    if (abort_next) {
+      abort_next = false;
+      if ((rc = check(hipMemsetAsync(&result_dev->err, 1, sizeof(int32_t), stream), "abort")))
+        return rc;
+    }
     if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, params_dev, desc_dev, epoch, smode), "step kernel launch")))
       return rc;
     epoch += step_progress_per_step(hp.n_layers);

@@ -36,6 +36,7 @@ struct Ctx {
   int nwg = 0;
   bool step_ok = false;  // the persistent step kernel is usable for this model / device
   uint32_t epoch = 0;
+  bool abort_next = false;  // raise the error word before the next step-kernel launch
   StepParams* params_dev = nullptr;
   StepParams params_host{};
   uint64_t* timing_dev = nullptr;  // step-kernel phase clock marks (profiling)

@@ -430,38 +430,6 @@ __device__ void panel_norm(Rsrc x, int T, const float* __restrict__ gain, float 
   bar();
 }
 
-// Panel of T rows of K floats quantized as they are (o: K = 2048, act: K = 3072).
-// Chunk c (16 floats) = bytes [64c, 64c + 64) of the row-major source.
-template <int K>
-__device__ void panel_plain(Rsrc src, int T, uint8_t* pcodes, float* pscales) {
-  constexpr int cpr = K / 16, bps = K / kPairK;
-  const int chunks = T * cpr;
-  for (int base = 0; base < chunks; base += 4 * kT) {
-    float v[4][16];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = base + j * kT + threadIdx.x;
-      if (c < chunks) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const v4f q = ldc4(src, (uint32_t)(c * 64 + 16 * i));
-          v[j][4 * i] = q[0];
-          v[j][4 * i + 1] = q[1];
-          v[j][4 * i + 2] = q[2];
-          v[j][4 * i + 3] = q[3];
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = base + j * kT + threadIdx.x;
-      if (c < chunks)  // whole waves: chunks is a multiple of 64
-        quant16(v[j], c / cpr, c % cpr, bps, pcodes, pscales);
-    }
-  }
-  bar();
-}
-
 // Panel of T rows of K activations already quantized by their producer:
 // codes [t][K] int8, scales [t][K/32]. Thread = 16 codes (a half block).
 template <int K>

@@ -98,6 +98,7 @@ SIGNATURES = {
     "mtg_set_exec_mode": (c_int32, [c_void_p, c_int32]),
     "mtg_exec_mode": (c_int32, [c_void_p]),
     "mtg_debug_copy": (c_int32, [c_void_p, c_int32, c_void_p, ctypes.c_size_t]),
+    "mtg_debug_abort_next_step": (c_int32, [c_void_p]),
     "mtg_step_profile": (c_int32, [c_void_p, c_int32]),
     "mtg_launch_timing": (c_int32, [c_void_p, c_int32]),
     "mtg_launch_timing_read": (c_int32, [c_void_p, POINTER(c_double), POINTER(c_int64),
@@ -242,6 +243,9 @@ class Decoder:
 
     def set_exec(self, mode):
         self._chk(lib().mtg_set_exec_mode(self.ctx, mode))
+
+    def debug_abort_next_step(self):
+        self._chk(lib().mtg_debug_abort_next_step(self.ctx))
 
     def debug_buffer(self, which, width):
         out = np.empty((MAX_BATCH, width), np.float32)

@@ -33,7 +33,7 @@ def _setup(n_layers, prefix, kv_type=mtg.TYPE_F32, vocab=4096, seed=0, max_seq=2
 
 def _close(got, ref, what):
     """Device and oracle use the same canonical float order, so results are
-    bit-identical; the north-star tolerance (1e-3 rel / 1e-4 abs) is reported
+    bit-identical; the contract tolerance (1e-3 rel / 1e-4 abs) is reported
     in the message for context."""
     got = np.asarray(got)
     ref = np.asarray(ref)
@@ -226,3 +226,29 @@ def test_f16_and_q4k_weights_penalty_prefill_and_stream(wtype):
     ids1, st1 = dec.generate_from(first, 200, max_steps=12, penalty=1.1, max_draft=7, draft=fn, user=user)
     assert ids1.tolist() == ids0.tolist()
     assert st1.accepted == st0.accepted and st1.proposed == st0.proposed
+
+
+def test_step_kernel_abort_reports_and_recovers():
+    """Failure path of the persistent kernel, forced from the host: with its error
+    word raised before the launch, every bounded wait gives up at its first poll.
+    The step fails with MTG_ERR_DEVICE, past_len and the KV cache stay, and the next
+    step matches the oracle bit for bit."""
+    print("step kernel abort path", flush=True)
+    model, orc, dec, rng = _setup(2, 40)
+    tokens = rng.integers(0, model.hp.vocab, 8)
+    k_before, v_before = dec.kv_read(40)
+    dec.debug_abort_next_step()
+    with pytest.raises(mtg.MtgError) as exc:
+        dec.verify(tokens)
+    assert exc.value.code == mtg.ERR_DEVICE
+    assert dec.past_len == 40
+    k_after, v_after = dec.kv_read(40)
+    _close(k_after, k_before, "K cache after the aborted step")
+    _close(v_after, v_before, "V cache after the aborted step")
+    for T in (8, 3):
+        tokens = rng.integers(0, model.hp.vocab, T)
+        c0, m0, h0, l0 = orc.verify(tokens, want_hidden=True, want_logits=True)
+        c1, m1, h1, l1 = dec.verify(tokens, want_hidden=True, want_logits=True)
+        _close(h1, h0, "hidden after recovery")
+        _close(l1, l0, "logits after recovery")
+        assert np.array_equal(c1, c0) and m1 == m0
