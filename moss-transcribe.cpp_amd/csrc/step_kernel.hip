@@ -377,7 +377,7 @@ __device__ __forceinline__ void quant16(const float v[16], int t, int kc, int bp
 
 // Panel of RMSNorm(x) * gain for T rows of 1024 (one wave per row): lane l
 // holds elements 16l..16l+15. normed_out (nullable): the f32 rows.
-__device__ void panel_norm(Rsrc x, int T, const float* __restrict__ gain, float eps, uint8_t* pcodes,
+__device__ __forceinline__ void panel_norm(Rsrc x, int T, const float* __restrict__ gain, float eps, uint8_t* pcodes,
                            float* pscales, float* normed_out) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   float gv[16];
@@ -433,7 +433,7 @@ __device__ void panel_norm(Rsrc x, int T, const float* __restrict__ gain, float 
 // Panel of T rows of K activations already quantized by their producer:
 // codes [t][K] int8, scales [t][K/32]. Thread = 16 codes (a half block).
 template <int K>
-__device__ void panel_from_q(const int8_t* codes, const float* scales, int T, uint8_t* pcodes,
+__device__ __forceinline__ void panel_from_q(const int8_t* codes, const float* scales, int T, uint8_t* pcodes,
                              float* pscales) {
   constexpr int cpr = K / 16, bps = K / kPairK;
   const Rsrc rc = mk_rsrc(codes, kMaxRows * K);
@@ -513,6 +513,11 @@ __device__ __forceinline__ void kv_prefetch(const LayerDev& Ly, const StepParams
   }
 }
 
+// two floats as f16 bits (round to nearest even), the first in the low half
+__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+  return (uint32_t)__half_as_ushort(__float2half_rn(a)) | ((uint32_t)__half_as_ushort(__float2half_rn(b)) << 16);
+}
+
 __device__ __forceinline__ float kv_val(uint32_t bits, bool f16) {
   return f16 ? half_bits_to_float((uint16_t)bits) : __uint_as_float(bits);
 }
@@ -570,9 +575,13 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
     const int r = r0 + 4 * j, t = tt[j];
     if (r >= nrows) break;
     const float a0 = kind[j] < 2 ? y0[j] : x0[j], a1 = kind[j] < 2 ? y1[j] : x1[j];
+    // new k rows are kept permuted (element 4 s + kk at kk * 32 + s), so that a
+    // lane reads its 32 score operands of one key with 16-byte LDS reads
+    const int o0 = kind[j] == 1 ? (lane & 3) * 32 + (lane >> 2) : lane;
+    const int o1 = kind[j] == 1 ? o0 + 16 : lane + 64;
     float* dst = kind[j] == 0 ? q_lds + r * cQStride : (kind[j] == 1 ? knew : vnew) + t * cQStride;
-    dst[lane] = f16kv ? f16_round(a0) : a0;
-    dst[lane + 64] = f16kv ? f16_round(a1) : a1;
+    dst[o0] = f16kv ? f16_round(a0) : a0;
+    dst[o1] = f16kv ? f16_round(a1) : a1;
   }
 }
 
@@ -604,7 +613,8 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   }
   bar();
   if (prof) wmark(P, 1, 16);
-  // 2. operands: prefetched cache rows, new rows from LDS, zeros past kvlen
+  // 2. operands: prefetched cache rows (zero from `past` on: the loads' range
+  //    ends there), new rows [past, kvlen) from LDS
   float ka[32], vb[2][16];
 #pragma unroll
   for (int s = 0; s < 32; ++s) ka[s] = kv_val(kv.k[s], f16kv);
@@ -612,25 +622,68 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int s = 0; s < 16; ++s) vb[h][s] = kv_val(kv.v[h][s], f16kv);
-  if (has_new) {  // keys >= past come from this step's rows; none past kvlen
-    // every lane reads a staged row (clamped row index) and keeps what applies,
-    // so that the reads are not each behind a lane mask and a wait
-    const int key = key0 + 16 * wave + kl;
-    const bool kn = key >= past, kz = key >= kvlen;
-    const float* krow = knew + min(max(key - past, 0), T - 1) * cQStride + kk;
+  // a use of every operand register here makes the compiler wait for their loads
+  // before the stores below (the staging's loads, issued later, are complete, so
+  // this costs nothing); otherwise its first wait would come after the stores
+  // and would have to wait for them
 #pragma unroll
-    for (int s = 0; s < 32; ++s) {
-      const float nv = krow[4 * s];
-      ka[s] = kz ? 0.0f : (kn ? nv : ka[s]);
+  for (int s = 0; s < 32; ++s) asm volatile("" ::"v"(ka[s]));
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int s = 0; s < 16; ++s) asm volatile("" ::"v"(vb[h][s]));
+  // the appending workgroup writes this step's k / v rows to the KV cache from
+  // the staged rows (for an f16 cache they are f16 values already). Issued after
+  // the prefetched K / V are in registers (a wait for a load issued before these
+  // stores would wait for them too), so that their acknowledgement overlaps the
+  // scores instead of delaying the publish.
+  if (appender) {
+    // wave-uniform cache pointers (a per-lane choice between the two fields
+    // would load the pointer with a vector load before every store)
+    uint8_t* const kcp = uniform_ptr(Ly.kc);
+    uint8_t* const vcp = uniform_ptr(Ly.vc);
+    for (int i = threadIdx.x; i < T * (cHD / 4); i += kT) {  // 4 elements of one row
+      const int t = i / (cHD / 4), m = i % (cHD / 4), d = 4 * m;
+      const size_t off = ((size_t)g * P.max_seq + past + t) * cHD + d;
+      const float* kr = knew + t * cQStride + m;  // element 4 m + kk sits at kk * 32 + m
+      const v4f kq = {kr[0], kr[32], kr[64], kr[96]};
+      const v4f vq = *(const v4f*)(vnew + t * cQStride + d);
+      if (f16kv) {
+        const v2u kh = {pack_half2(kq[0], kq[1]), pack_half2(kq[2], kq[3])};
+        const v2u vh = {pack_half2(vq[0], vq[1]), pack_half2(vq[2], vq[3])};
+        gst<v2u>((uint16_t*)kcp + off, kh);
+        gst<v2u>((uint16_t*)vcp + off, vh);
+      } else {
+        gst<v4f>((float*)kcp + off, kq);
+        gst<v4f>((float*)vcp + off, vq);
+      }
     }
+  }
+  if (has_new) {
+    // score operands: the lane's key, all 32 values from one permuted row
+    const int key = key0 + 16 * wave + kl;
+    if (key >= past && key < kvlen) {
+      const float* kr = knew + (key - past) * cQStride + kk * 32;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const v4f q = *(const v4f*)(kr + 4 * i);
+        ka[4 * i] = q[0];
+        ka[4 * i + 1] = q[1];
+        ka[4 * i + 2] = q[2];
+        ka[4 * i + 3] = q[3];
+      }
+    }
+    // P.V operands: only the key groups that reach a new key
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
-      const int vk = key0 + 4 * s + kk;
-      const bool vn = vk >= past, vz = vk >= kvlen;
-      const float* vrow = vnew + min(max(vk - past, 0), T - 1) * cQStride + 32 * wave + kl;
-      const float n0 = vrow[0], n1 = vrow[16];
-      vb[0][s] = vz ? 0.0f : (vn ? n0 : vb[0][s]);
-      vb[1][s] = vz ? 0.0f : (vn ? n1 : vb[1][s]);
+      const int g0 = key0 + 4 * s;  // wave-uniform
+      if (g0 + 3 < past || g0 >= kvlen) continue;
+      const int vk = g0 + kk;
+      if (vk >= past && vk < kvlen) {
+        const float* vrow = vnew + (vk - past) * cQStride + 32 * wave + kl;
+        vb[0][s] = vrow[0];
+        vb[1][s] = vrow[16];
+      }
     }
   }
   if (prof) { bar(); wmark(P, 1, 17); }
@@ -710,19 +763,6 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
         const int col = ct * 16 + 4 * kk + q;
         if (col < ncol) stc1(ro, (uint32_t)((col * cHD + d) * 4), acc[q]);
       }
-    }
-  }
-  // 6. the appending workgroup writes this step's k / v rows to the KV cache from
-  //    the staged rows (for an f16 cache they are f16 values already). Issued
-  //    last, so that no wait for the prefetched K / V above also waits for them.
-  if (appender) {
-    for (int i = threadIdx.x; i < 2 * T * cHD; i += kT) {
-      const int r = i / cHD, d = i % cHD, t = r % T;
-      const float v = (r < T ? knew : vnew)[t * cQStride + d];
-      const size_t off = ((size_t)g * P.max_seq + past + t) * cHD + d;
-      uint8_t* cache = r < T ? Ly.kc : Ly.vc;
-      if (f16kv) gst<uint16_t>((uint16_t*)cache + off, __half_as_ushort(__float2half_rn(v)));
-      else gst<float>((float*)cache + off, v);
     }
   }
   bar();
@@ -1105,9 +1145,11 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     mark(P, 3 + 12 * l + 0);
     wmark(P, l, 0);
     panel_norm(RX, T, Ly.attn_norm, P.eps, pcodes, pscales, nullptr);
+    wmark(P, l, 25);
     {
       float acc[1][G][4] = {};
       wt_mma<G, 4>(qa, qs, 4 * wave, cBH, pcodes, pscales, acc[0]);
+      wmark(P, l, 26);
       gemm_finish<G, 1, EPI_STORE>(acc, red, RQKV, cNQKV, w, T);
     }
     publish(c, next_done(l, kPhQkv));
@@ -1146,6 +1188,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
         const bool valid = item < n_merge;
         merge_item(P, T, nch, valid ? item / T : 0, valid ? item % T : 0, threadIdx.x & 127, valid);
       }
+      wmark(P, l, 22);
       publish(c, next_done(l, kPhMerge));
       wmark(P, l, 5);
       if (!gu && l + 1 < L) {  // nothing more in this layer: prefetch the next one
@@ -1160,8 +1203,10 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       mark(P, 3 + 12 * l + 4);
       wmark(P, l, 6);
       panel_from_q<cQN>(P.oq, P.oqs, T, pcodes, pscales);
+      wmark(P, l, 27);
       float acc[1][G][4] = {};
       wt_mma<G, 8>(ba, bs, 8 * wave, cBQ, pcodes, pscales, acc[0]);
+      wmark(P, l, 28);
       gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T, xs, xs_valid);
       xs_valid = true;
       wmark(P, l, 24);
@@ -1178,9 +1223,11 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       if (!wait_all(c, ph(l, kPhGu) - 1, l == 1 ? wslot(w, 12) : -1)) return;
       wmark(P, l, 8);
       panel_norm(RX, T, Ly.ffn_norm, P.eps, pcodes, pscales, nullptr);
+      wmark(P, l, 27);
       float acc[4][G][4] = {};
 #pragma unroll
       for (int m = 0; m < 4; ++m) wt_mma<G, 4>(ba + 4 * m, bs + 4 * m, 4 * wave, cBH, pcodes, pscales, acc[m]);
+      wmark(P, l, 28);
       gu_finish<G>(acc, red, red + 4 * 4 * G * 4 * 64, P, w - cOTiles, T);
       wmark(P, l, 24);
       publish(c, next_done(l, kPhGu));
@@ -1197,8 +1244,10 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       mark(P, 3 + 12 * l + 6);
       wmark(P, l, 10);
       panel_from_q<cF>(P.aq, P.aqs, T, pcodes, pscales);
+      wmark(P, l, 29);
       float acc[1][G][4] = {};
       wt_mma<G, 12>(ba, bs, 12 * wave, cBF, pcodes, pscales, acc[0]);
+      wmark(P, l, 30);
       gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T, xs, xs_valid);
       xs_valid = true;
       publish(c, next_done(l, kPhD));
