@@ -774,17 +774,27 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
 // blocks (32 lanes each). valid == false: the lanes only take part in the lane
 // exchanges.
 __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, int hq, int t, int d,
-                                           bool valid) {
+                                           bool valid, bool prof, float* fl) {
+  // the item is uniform over each wave (two waves per item): made visibly so, or
+  // the buffer descriptors below would sit in vector registers and every load
+  // would become a loop over the distinct descriptors
+  hq = __builtin_amdgcn_readfirstlane(hq);
+  t = __builtin_amdgcn_readfirstlane(t);
+  T = __builtin_amdgcn_readfirstlane(T);
+  nch = __builtin_amdgcn_readfirstlane(nch);
+  valid = __builtin_amdgcn_readfirstlane((int)valid) != 0;
   const int g = hq / 2, col = (hq & 1) * T + t;
   const Rsrc rml = mk_rsrc(P.part_ml + (size_t)g * P.max_chunks * kMaxCols * 2,
                            (uint32_t)P.max_chunks * kMaxCols * 2 * 4);
   const Rsrc ro = mk_rsrc(P.part_o + (size_t)g * P.max_chunks * kMaxCols * cHD,
                           (uint32_t)P.max_chunks * kMaxCols * cHD * 4);
-  // Chunk factors once per wave: lane c holds m_c, l_c and f_c = exp(m_c - M);
-  // every thread then reads them as wave-uniform values (readlane) while it runs
-  // the two chunk-ordered fma chains over its own O values. The first 64 chunks'
-  // (m, l) and the first 32 chunks' O are loaded together: one round trip at the
-  // usual context lengths.
+  // Chunk factors once per wave: lane c holds m_c, l_c and f_c = exp(m_c - M),
+  // written to this wave's LDS slots (fl[0..63] factors, fl[64..127] sums); every
+  // thread then reads them back four chunks at a time (same address in all lanes)
+  // while it runs the two chunk-ordered fma chains over its own O values. A fully
+  // masked chunk (m = -inf) has f = 0, l = 0 and O = 0, so its fma terms add
+  // exact zeros. The first 64 chunks' (m, l) and the first 32 chunks' O are
+  // loaded together: one round trip at the usual context lengths.
   const int lane = threadIdx.x & 63;
   float out = 0.0f;
   auto ld_m = [&](int c) {
@@ -805,28 +815,35 @@ __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, 
   ld_o(0);
   float M = wave_max_f(m);
   for (int c0 = 64; c0 < nch; c0 += 64) M = fmaxf(M, wave_max_f(ld_m(c0 + lane)));
+  if (prof) wmark(P, 1, 23);
   float L = 0.0f, O = 0.0f;
   for (int c0 = 0; c0 < nch; c0 += 64) {
     if (c0 > 0) {
       m = ld_m(c0 + lane);
       l = ld_l(c0 + lane);
     }
-    const float f = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, M));
+    // LDS accesses of one wave execute in order: the reads below see these
+    // writes, and the next block's writes follow this block's reads
+    fl[lane] = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, M));
+    fl[64 + lane] = l;
     const int nb = min(64, nch - c0);
     for (int i0 = 0; i0 < nb; i0 += 32) {
       if (c0 + i0 > 0) ld_o(c0 + i0);
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
+      for (int i = 0; i < 32; i += 4) {
         if (i0 + i >= nb) break;
-        const float mc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), i0 + i));
-        if (mc == -INFINITY) continue;
-        const float fc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), i0 + i));
-        const float lc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), i0 + i));
-        L = fmaf(lc, fc, L);
-        O = fmaf(o[i], fc, O);
+        const v4f f4 = *(const v4f*)(fl + i0 + i);
+        const v4f l4 = *(const v4f*)(fl + 64 + i0 + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (i0 + i + j >= nb) break;
+          L = fmaf(l4[j], f4[j], L);
+          O = fmaf(o[i + j], f4[j], O);
+        }
       }
     }
   }
+  if (prof) wmark(P, 1, 31);
   if (valid) out = __fdiv_rn(O, L);
   // q8_0 blocks of 32 consecutive d (32 lanes of one wave)
   const float amax = group32_max_nonneg(fabsf(out));
@@ -1186,7 +1203,8 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       for (int i0 = 2 * (w - kMergeWg0); i0 < n_merge; i0 += 2 * (kNwg - kMergeWg0)) {
         const int item = i0 + half;
         const bool valid = item < n_merge;
-        merge_item(P, T, nch, valid ? item / T : 0, valid ? item % T : 0, threadIdx.x & 127, valid);
+        merge_item(P, T, nch, valid ? item / T : 0, valid ? item % T : 0, threadIdx.x & 127, valid,
+                   l == 1 && i0 == 2 * (w - kMergeWg0), (float*)lds + wave * 128);
       }
       wmark(P, l, 22);
       publish(c, next_done(l, kPhMerge));
