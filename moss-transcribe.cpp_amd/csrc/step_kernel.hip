@@ -161,7 +161,6 @@ __device__ __forceinline__ bool wait_all(Ctl& c, uint32_t v, int prof_slot = -1)
       }
       __builtin_amdgcn_s_sleep(1);
     }
-    if (prof_slot >= 0 && P.timing && lane == 0) gst<uint64_t>(P.timing + prof_slot + 1, (uint64_t)spins);
     if (lane == 0) *c.s_ok = ok;
   }
   bar();
@@ -377,10 +376,12 @@ __device__ __forceinline__ void quant16(const float v[16], int t, int kc, int bp
 
 // Panel of RMSNorm(x) * gain for T rows of 1024 (one wave per row): lane l
 // holds elements 16l..16l+15. normed_out (nullable): the f32 rows.
-__device__ __forceinline__ void panel_norm(Rsrc x, int T, const float* __restrict__ gain, float eps, uint8_t* pcodes,
-                           float* pscales, float* normed_out) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  float gv[16];
+// The 16 gain values of lane l (elements 16 l .. 16 l + 15) of a 1024 norm. The
+// layers' norms are loaded with the weights of the phase that uses them, before
+// its wait: a load from HBM issued just before the activation loads would hold
+// them up (loads complete in order).
+__device__ __forceinline__ void gain16_load(const float* __restrict__ gain, float (&gv)[16]) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const v4f g = gld<v4f>(gain + 16 * lane + 4 * i);
@@ -389,6 +390,11 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float* __restric
     gv[4 * i + 2] = g[2];
     gv[4 * i + 3] = g[3];
   }
+}
+
+__device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv)[16], float eps, uint8_t* pcodes,
+                                           float* pscales, float* normed_out, const StepParams* prof = nullptr) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   for (int t0 = wave; t0 < T; t0 += 8) {
     // two rows per pass: all loads issued before any arithmetic
     float v[2][16];
@@ -406,6 +412,7 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float* __restric
         }
       }
     }
+    if (prof && t0 == wave) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); wmark(*prof, 1, 13); }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int t = t0 + 4 * j;
@@ -431,38 +438,39 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float* __restric
 }
 
 // Panel of T rows of K activations already quantized by their producer:
-// codes [t][K] int8, scales [t][K/32]. Thread = 16 codes (a half block).
-template <int K>
+// codes [t][K] int8, scales [t][K/32]. Thread = 16 codes (a half block); every
+// load is issued before the first LDS write (one round trip).
+template <int K, int G>
 __device__ __forceinline__ void panel_from_q(const int8_t* codes, const float* scales, int T, uint8_t* pcodes,
-                             float* pscales) {
+                                             float* pscales) {
   constexpr int cpr = K / 16, bps = K / kPairK;
+  constexpr int NC = (8 * G * cpr + kT - 1) / kT;  // chunks per thread at the largest T
   const Rsrc rc = mk_rsrc(codes, kMaxRows * K);
   const Rsrc rs = mk_rsrc(scales, kMaxRows * (K / 32) * 4);
   const int chunks = T * cpr;
-  for (int base = 0; base < chunks; base += 4 * kT) {
-    v4u q[4];
-    float d[4];
+  v4u q[NC];
+  float d[NC];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = base + j * kT + threadIdx.x;
-      if (c < chunks) {
-        const int t = c / cpr, kc = c % cpr;
-        q[j] = __builtin_amdgcn_raw_buffer_load_b128(rc, t * K + kc * 16, 0, 16);
-        d[j] = ldc1(rs, (uint32_t)((t * (K / 32) + (kc >> 1)) * 4));
-      }
-    }
+  for (int j = 0; j < NC; ++j) {
+    const int c = j * kT + threadIdx.x;
+    // a chunk past the rows reads past the buffers' ends: zeros, no memory traffic
+    const int t = c / cpr, kc = c % cpr;
+    const bool in = c < chunks;
+    q[j] = __builtin_amdgcn_raw_buffer_load_b128(rc, in ? (uint32_t)(t * K + kc * 16) : 0x80000000u, 0, 16);
+    d[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         rs, in ? (uint32_t)((t * (K / 32) + (kc >> 1)) * 4) : 0x80000000u, 0, 16));
+  }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = base + j * kT + threadIdx.x;
-      if (c < chunks) {
-        const int t = c / cpr, kc = c % cpr;
-        const int blk = kc >> 1, half = kc & 1, bp = blk >> 1, par = blk & 1;
-        const int cg = t >> 3, jc = par * 8 + (t & 7);
-        uint8_t* unit = pcodes + (size_t)(cg * bps + bp) * 1024;
-        *(uint4*)(unit + (jc + 16 * (2 * par + half)) * 16) = make_uint4(q[j].x, q[j].y, q[j].z, q[j].w);
-        *(uint4*)(unit + (jc + 16 * (2 * (1 - par) + half)) * 16) = make_uint4(0u, 0u, 0u, 0u);
-        if (half == 0) pscales[(size_t)(cg * bps + bp) * 16 + jc] = d[j];
-      }
+  for (int j = 0; j < NC; ++j) {
+    const int c = j * kT + threadIdx.x;
+    if (c < chunks) {
+      const int t = c / cpr, kc = c % cpr;
+      const int blk = kc >> 1, half = kc & 1, bp = blk >> 1, par = blk & 1;
+      const int cg = t >> 3, jc = par * 8 + (t & 7);
+      uint8_t* unit = pcodes + (size_t)(cg * bps + bp) * 1024;
+      *(uint4*)(unit + (jc + 16 * (2 * par + half)) * 16) = make_uint4(q[j].x, q[j].y, q[j].z, q[j].w);
+      *(uint4*)(unit + (jc + 16 * (2 * (1 - par) + half)) * 16) = make_uint4(0u, 0u, 0u, 0u);
+      if (half == 0) pscales[(size_t)(cg * bps + bp) * 16 + jc] = d[j];
     }
   }
   bar();
@@ -529,7 +537,8 @@ __device__ __forceinline__ float kv_val(uint32_t bits, bool f16) {
 // nothing.
 template <int NS, int KVH>
 __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& Ly, int T, int past, int g,
-                                           int r0, int nrows, float* q_lds, float* knew, float* vnew) {
+                                           int r0, int nrows, float* q_lds, float* knew, float* vnew,
+                                           bool prof = false) {
   const int lane = threadIdx.x & 63, ncol = 2 * T;
   constexpr bool f16kv = KVH != 0;
   const Rsrc rq = mk_rsrc(P.qkv, kMaxRows * cNQKV * 4);
@@ -557,6 +566,7 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
       }
     }
   }
+  if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); wmark(P, 1, 15); }
   double sq[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) sq[j] = (double)__fmul_rn(x0[j], x0[j]) + (double)__fmul_rn(x1[j], x1[j]);
@@ -575,10 +585,10 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
     const int r = r0 + 4 * j, t = tt[j];
     if (r >= nrows) break;
     const float a0 = kind[j] < 2 ? y0[j] : x0[j], a1 = kind[j] < 2 ? y1[j] : x1[j];
-    // new k rows are kept permuted (element 4 s + kk at kk * 32 + s), so that a
-    // lane reads its 32 score operands of one key with 16-byte LDS reads
-    const int o0 = kind[j] == 1 ? (lane & 3) * 32 + (lane >> 2) : lane;
-    const int o1 = kind[j] == 1 ? o0 + 16 : lane + 64;
+    // q and new k rows are kept permuted (element 4 s + kk at kk * 32 + s), so that
+    // a lane reads its 32 score operands of one row with 16-byte LDS reads
+    const int o0 = kind[j] < 2 ? (lane & 3) * 32 + (lane >> 2) : lane;
+    const int o1 = kind[j] < 2 ? o0 + 16 : lane + 64;
     float* dst = kind[j] == 0 ? q_lds + r * cQStride : (kind[j] == 1 ? knew : vnew) + t * cQStride;
     dst[o0] = f16kv ? f16_round(a0) : a0;
     dst[o1] = f16kv ? f16_round(a1) : a1;
@@ -606,7 +616,7 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   const int nrows = ncol + (has_new ? 2 * T : 0);
   if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 21); }
   if (!has_new) {
-    stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, nrows, q_lds, knew, vnew);
+    stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, nrows, q_lds, knew, vnew, prof);
   } else {
     for (int r0 = wave; r0 < nrows; r0 += 32)
       stage_pass<8, KVH>(P, Ly, T, past, g, r0, nrows, q_lds, knew, vnew);
@@ -692,17 +702,25 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   for (int ct = 0; ct * 16 < ncol; ++ct) {
     const int colb = ct * 16 + kl;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
+    // the column's permuted q row: element 4 s + kk at kk * 32 + s
+    const float* qrow = q_lds + min(colb, ncol - 1) * cQStride + kk * 32;
 #pragma unroll
-    for (int s = 0; s < 32; ++s) {
-      const float b = colb < ncol ? q_lds[colb * cQStride + 4 * s + kk] : 0.0f;
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[s], b, acc, 0, 0, 0);
+    for (int i = 0; i < 8; ++i) {
+      const v4f q4 = *(const v4f*)(qrow + 4 * i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float b = colb < ncol ? q4[j] : 0.0f;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[4 * i + j], b, acc, 0, 0, 0);
+      }
     }
     if (colb < ncol) {
       const int t = colb % T;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        // key 16 w + 4 kk + q of the chunk sits at sp_pos(key) = q * 16 + 4 w + kk
         const int kloc = 16 * wave + 4 * kk + q, key = key0 + kloc;
-        sp[colb * cPStride + kloc] = (key < kvlen && key <= past + t) ? __fmul_rn(acc[q], scale) : -INFINITY;
+        sp[colb * cPStride + q * 16 + 4 * wave + kk] =
+            (key < kvlen && key <= past + t) ? __fmul_rn(acc[q], scale) : -INFINITY;
       }
     }
   }
@@ -715,12 +733,15 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   // order-preserving integer keys of the scores (no NaN here; the sign of a zero
   // maximum does not change any exp(w - m))
   constexpr int kCols = 4 * G;
+  // probabilities of a column are kept permuted (key 4 s + kk at kk * 16 + s), so
+  // that the P.V operands of a lane are 16 consecutive floats
+  const int sp_pos = (lane & 3) * 16 + (lane >> 2);
   float wv[kCols], lv[kCols];
   int mk[kCols];
 #pragma unroll
   for (int i = 0; i < kCols; ++i) {
     const int col = wave + 4 * i;
-    wv[i] = col < ncol ? sp[col * cPStride + lane] : -INFINITY;
+    wv[i] = col < ncol ? sp[col * cPStride + sp_pos] : -INFINITY;
     mk[i] = ord_key(wv[i]);
   }
   wave_max_i_n<kCols>(mk);
@@ -737,7 +758,7 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   for (int i = 0; i < kCols; ++i) {
     const int col = wave + 4 * i;
     if (col >= ncol) break;
-    sp[col * cPStride + lane] = wv[i];
+    sp[col * cPStride + sp_pos] = wv[i];
     if (lane == 0) {
       stc1(rml, (uint32_t)(col * 2 * 4), ord_val(mk[i]));
       stc1(rml, (uint32_t)((col * 2 + 1) * 4), lv[i]);
@@ -749,14 +770,21 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   const Rsrc ro = mk_rsrc(P.part_o + pi * kMaxCols * cHD, kMaxCols * cHD * 4);
   for (int ct = 0; ct * 16 < ncol; ++ct) {
     const int cola = ct * 16 + kl;
+    float pa[16];
+    {
+      const float* prow = sp + min(cola, ncol - 1) * cPStride + kk * 16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v4f p4 = *(const v4f*)(prow + 4 * i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pa[4 * i + j] = cola < ncol ? p4[j] : 0.0f;
+      }
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const float a = cola < ncol ? sp[cola * cPStride + 4 * s + kk] : 0.0f;
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[h][s], acc, 0, 0, 0);
-      }
+      for (int s = 0; s < 16; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s], vb[h][s], acc, 0, 0, 0);
       const int d = 16 * (2 * wave + h) + kl;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -1114,6 +1142,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   v4i ba[16];             // o-proj (8 pairs) then down (12), or gate A|B, up A|B (4 each)
   uint2 bs[16];
   KvRegs kv;              // K / V of the first attention item
+  float gq[16], gf[16];   // attn_norm / ffn_norm gains of the lane's 16 elements
 
   // ---- embeddings (and the penalty bitmap) ----
   if (w < T) {
@@ -1153,6 +1182,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   }
   // prefetch layer 0: q|k|v tile and the first attention item's K / V
   wt_load<4>(layer_at(P, 0).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+  gain16_load(layer_at(P, 0).attn_norm, gq);
   if (has_attn) kv_prefetch<KVH>(layer_at(P, 0), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
 
   for (int l = 0; l < L; ++l) {
@@ -1161,7 +1191,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     if (!wait_all(c, ph(l, kPhQkv) - 1)) return;
     mark(P, 3 + 12 * l + 0);
     wmark(P, l, 0);
-    panel_norm(RX, T, Ly.attn_norm, P.eps, pcodes, pscales, nullptr);
+    panel_norm(RX, T, gq, P.eps, pcodes, pscales, nullptr, (P.timing && l == 1) ? &P : nullptr);
     wmark(P, l, 25);
     {
       float acc[1][G][4] = {};
@@ -1194,6 +1224,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       wt_load<4>(Ly.wg + (size_t)(2 * j + 1) * cBH * kUnitBytes, 4 * wave, ba + 4, bs + 4);
       wt_load<4>(Ly.wu + (size_t)(2 * j) * cBH * kUnitBytes, 4 * wave, ba + 8, bs + 8);
       wt_load<4>(Ly.wu + (size_t)(2 * j + 1) * cBH * kUnitBytes, 4 * wave, ba + 12, bs + 12);
+      gain16_load(Ly.ffn_norm, gf);
     }
     // ---- MERGE: (head, row) items, two at a time ----
     if (has_merge) {
@@ -1212,6 +1243,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       if (!gu && l + 1 < L) {  // nothing more in this layer: prefetch the next one
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+        gain16_load(Ln.attn_norm, gq);
         if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
       }
     }
@@ -1220,7 +1252,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       if (!wait_all(c, ph(l, kPhO) - 1, l == 1 ? wslot(w, 12) : -1)) return;
       mark(P, 3 + 12 * l + 4);
       wmark(P, l, 6);
-      panel_from_q<cQN>(P.oq, P.oqs, T, pcodes, pscales);
+      panel_from_q<cQN, G>(P.oq, P.oqs, T, pcodes, pscales);
       wmark(P, l, 27);
       float acc[1][G][4] = {};
       wt_mma<G, 8>(ba, bs, 8 * wave, cBQ, pcodes, pscales, acc[0]);
@@ -1240,7 +1272,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     if (gu) {
       if (!wait_all(c, ph(l, kPhGu) - 1, l == 1 ? wslot(w, 12) : -1)) return;
       wmark(P, l, 8);
-      panel_norm(RX, T, Ly.ffn_norm, P.eps, pcodes, pscales, nullptr);
+      panel_norm(RX, T, gf, P.eps, pcodes, pscales, nullptr);
       wmark(P, l, 27);
       float acc[4][G][4] = {};
 #pragma unroll
@@ -1253,6 +1285,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       if (l + 1 < L) {
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+        gain16_load(Ln.attn_norm, gq);
         if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
       }
     }
@@ -1261,7 +1294,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       if (!wait_all(c, ph(l, kPhD) - 1)) return;
       mark(P, 3 + 12 * l + 6);
       wmark(P, l, 10);
-      panel_from_q<cF>(P.aq, P.aqs, T, pcodes, pscales);
+      panel_from_q<cF, G>(P.aq, P.aqs, T, pcodes, pscales);
       wmark(P, l, 29);
       float acc[1][G][4] = {};
       wt_mma<G, 12>(ba, bs, 12 * wave, cBF, pcodes, pscales, acc[0]);
@@ -1271,12 +1304,16 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       publish(c, next_done(l, kPhD));
       mark(P, 3 + 12 * l + 7);
       wmark(P, l, 11);
-      if (l + 1 < L) wt_load<4>(layer_at(P, l + 1).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+      if (l + 1 < L) {
+        wt_load<4>(layer_at(P, l + 1).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+        gain16_load(layer_at(P, l + 1).attn_norm, gq);
+      }
     }
     // workgroups with only q|k|v and attention work
     if (!od && !gu && !has_merge && l + 1 < L) {
       const LayerDev& Ln = layer_at(P, l + 1);
       wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+      gain16_load(Ln.attn_norm, gq);
       if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
     }
   }
@@ -1286,14 +1323,16 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   if (mode != kStepVerify) {
     if (w == 0) {
       if (!wait_all(c, lm - 1)) return;
-      panel_norm(RX, T, P.out_norm, P.eps, pcodes, pscales, P.hid);
+      gain16_load(P.out_norm, gq);
+      panel_norm(RX, T, gq, P.eps, pcodes, pscales, P.hid);
       mark(P, 2);
     }
     return;
   }
   if (!wait_all(c, lm - 1)) return;
   mark(P, 3 + 12 * L);
-  panel_norm(RX, T, P.out_norm, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr);
+  gain16_load(P.out_norm, gq);
+  panel_norm(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr);
   lm_head<G>(P, desc, T, pcodes, pscales, s_best);
   publish(c, lm);
   mark(P, 4 + 12 * L);
