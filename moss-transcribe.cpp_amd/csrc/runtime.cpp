@@ -404,7 +404,8 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
       if ((rc = check(hipMemsetAsync(&result_dev->err, 1, sizeof(int32_t), stream), "abort")))
         return rc;
     }
-    if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, params_dev, desc_dev, epoch, smode), "step kernel launch")))
+    if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, params_dev, desc_dev, epoch, smode,
+                                    params_host.timing != nullptr), "step kernel launch")))
       return rc;
     epoch += step_progress_per_step(hp.n_layers);
   } else if (exec != kExecEager) {

@@ -1096,10 +1096,14 @@ __host__ __device__ constexpr size_t step_lds_x_offset(int G) {
 }
 __device__ __forceinline__ uint32_t ph(int l, int p) { return 2u + (uint32_t)(l * kPhases + p); }
 
-template <int G, int KVH>
+// PROF: the profiled variant (clock marks into P.timing); the production
+// variant carries no marks at all (they would cost code size and registers)
+template <int G, int KVH, bool PROF>
 __global__ void __launch_bounds__(kT, 1)
 k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uint32_t epoch,
         int mode) {
+#define MARK(...) do { if constexpr (PROF) mark(__VA_ARGS__); } while (0)
+#define WMARK(...) do { if constexpr (PROF) wmark(__VA_ARGS__); } while (0)
   const StepParams& P = *Pp;
   extern __shared__ v4i lds_v4[];
   uint8_t* lds = (uint8_t*)lds_v4;
@@ -1134,7 +1138,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       if (mask & (1 << q)) return ph(l, q) - 1;
     return ph(l, kPhases) - 1;  // next work: the next layer's QKV (or the lm_head)
   };
-  mark(P, 0);
+  MARK(P, 0);
 
   // registers carried across phases
   v4i qa[4];              // this layer's q|k|v tile slice
@@ -1189,31 +1193,31 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     const LayerDev& Ly = layer_at(P, l);
     // ---- QKV: tile w ----
     if (!wait_all(c, ph(l, kPhQkv) - 1)) return;
-    mark(P, 3 + 12 * l + 0);
-    wmark(P, l, 0);
-    panel_norm(RX, T, gq, P.eps, pcodes, pscales, nullptr, (P.timing && l == 1) ? &P : nullptr);
-    wmark(P, l, 25);
+    MARK(P, 3 + 12 * l + 0);
+    WMARK(P, l, 0);
+    panel_norm(RX, T, gq, P.eps, pcodes, pscales, nullptr, (PROF && P.timing && l == 1) ? &P : nullptr);
+    WMARK(P, l, 25);
     {
       float acc[1][G][4] = {};
       wt_mma<G, 4>(qa, qs, 4 * wave, cBH, pcodes, pscales, acc[0]);
-      wmark(P, l, 26);
+      WMARK(P, l, 26);
       gemm_finish<G, 1, EPI_STORE>(acc, red, RQKV, cNQKV, w, T);
     }
     publish(c, next_done(l, kPhQkv));
-    mark(P, 3 + 12 * l + 1);
-    wmark(P, l, 1);
+    MARK(P, 3 + 12 * l + 1);
+    WMARK(P, l, 1);
     // ---- ATTN: items of this workgroup ----
     if (has_attn) {
-      if (!wait_all(c, ph(l, kPhAttn) - 1, l == 1 ? wslot(w, 14) : -1)) return;
-      mark(P, 3 + 12 * l + 2);
-      wmark(P, l, 2);
+      if (!wait_all(c, ph(l, kPhAttn) - 1, PROF && l == 1 ? wslot(w, 14) : -1)) return;
+      MARK(P, 3 + 12 * l + 2);
+      WMARK(P, l, 2);
       for (int item = first_item; item < n_items; item += kNwg) {
         if (item != first_item) kv_prefetch<KVH>(Ly, P, item / nch, (item % nch) * kChunk, past, kv);
-        attn_item<G, KVH>(P, Ly, T, past, item / nch, item % nch, kv, lds, l == 1 && P.timing != nullptr);
+        attn_item<G, KVH>(P, Ly, T, past, item / nch, item % nch, kv, lds, PROF && l == 1 && P.timing != nullptr);
       }
       publish(c, next_done(l, kPhAttn));
-      mark(P, 3 + 12 * l + 3);
-      wmark(P, l, 3);
+      MARK(P, 3 + 12 * l + 3);
+      WMARK(P, l, 3);
     }
     // the o-proj tile's weights: issued after the attention, so that no register
     // holds them through it (the o-proj starts after the merge, well after they land)
@@ -1229,17 +1233,17 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     // ---- MERGE: (head, row) items, two at a time ----
     if (has_merge) {
       if (!wait_all(c, ph(l, kPhMerge) - 1)) return;
-      wmark(P, l, 4);
+      WMARK(P, l, 4);
       const int half = threadIdx.x >> 7;
       for (int i0 = 2 * (w - kMergeWg0); i0 < n_merge; i0 += 2 * (kNwg - kMergeWg0)) {
         const int item = i0 + half;
         const bool valid = item < n_merge;
         merge_item(P, T, nch, valid ? item / T : 0, valid ? item % T : 0, threadIdx.x & 127, valid,
-                   l == 1 && i0 == 2 * (w - kMergeWg0), (float*)lds + wave * 128);
+                   PROF && l == 1 && i0 == 2 * (w - kMergeWg0), (float*)lds + wave * 128);
       }
-      wmark(P, l, 22);
+      WMARK(P, l, 22);
       publish(c, next_done(l, kPhMerge));
-      wmark(P, l, 5);
+      WMARK(P, l, 5);
       if (!gu && l + 1 < L) {  // nothing more in this layer: prefetch the next one
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
@@ -1249,20 +1253,20 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     }
     // ---- O-proj: x += W_o o ----
     if (od) {
-      if (!wait_all(c, ph(l, kPhO) - 1, l == 1 ? wslot(w, 12) : -1)) return;
-      mark(P, 3 + 12 * l + 4);
-      wmark(P, l, 6);
+      if (!wait_all(c, ph(l, kPhO) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return;
+      MARK(P, 3 + 12 * l + 4);
+      WMARK(P, l, 6);
       panel_from_q<cQN, G>(P.oq, P.oqs, T, pcodes, pscales);
-      wmark(P, l, 27);
+      WMARK(P, l, 27);
       float acc[1][G][4] = {};
       wt_mma<G, 8>(ba, bs, 8 * wave, cBQ, pcodes, pscales, acc[0]);
-      wmark(P, l, 28);
+      WMARK(P, l, 28);
       gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T, xs, xs_valid);
       xs_valid = true;
-      wmark(P, l, 24);
+      WMARK(P, l, 24);
       publish(c, next_done(l, kPhO));
-      mark(P, 3 + 12 * l + 5);
-      wmark(P, l, 7);
+      MARK(P, 3 + 12 * l + 5);
+      WMARK(P, l, 7);
       wt_load<12>(Ly.wd + (size_t)w * cBF * kUnitBytes, 12 * wave, ba, bs);
       // the next layer's attention K / V, so that they are in flight before the down wait
       if (has_attn && l + 1 < L)
@@ -1270,18 +1274,18 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     }
     // ---- GATE/UP: act = silu(g) * u, as q8_0 blocks ----
     if (gu) {
-      if (!wait_all(c, ph(l, kPhGu) - 1, l == 1 ? wslot(w, 12) : -1)) return;
-      wmark(P, l, 8);
+      if (!wait_all(c, ph(l, kPhGu) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return;
+      WMARK(P, l, 8);
       panel_norm(RX, T, gf, P.eps, pcodes, pscales, nullptr);
-      wmark(P, l, 27);
+      WMARK(P, l, 27);
       float acc[4][G][4] = {};
 #pragma unroll
       for (int m = 0; m < 4; ++m) wt_mma<G, 4>(ba + 4 * m, bs + 4 * m, 4 * wave, cBH, pcodes, pscales, acc[m]);
-      wmark(P, l, 28);
+      WMARK(P, l, 28);
       gu_finish<G>(acc, red, red + 4 * 4 * G * 4 * 64, P, w - cOTiles, T);
-      wmark(P, l, 24);
+      WMARK(P, l, 24);
       publish(c, next_done(l, kPhGu));
-      wmark(P, l, 9);
+      WMARK(P, l, 9);
       if (l + 1 < L) {
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
@@ -1292,18 +1296,18 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     // ---- DOWN: x += W_d act ----
     if (od) {
       if (!wait_all(c, ph(l, kPhD) - 1)) return;
-      mark(P, 3 + 12 * l + 6);
-      wmark(P, l, 10);
+      MARK(P, 3 + 12 * l + 6);
+      WMARK(P, l, 10);
       panel_from_q<cF, G>(P.aq, P.aqs, T, pcodes, pscales);
-      wmark(P, l, 29);
+      WMARK(P, l, 29);
       float acc[1][G][4] = {};
       wt_mma<G, 12>(ba, bs, 12 * wave, cBF, pcodes, pscales, acc[0]);
-      wmark(P, l, 30);
+      WMARK(P, l, 30);
       gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T, xs, xs_valid);
       xs_valid = true;
       publish(c, next_done(l, kPhD));
-      mark(P, 3 + 12 * l + 7);
-      wmark(P, l, 11);
+      MARK(P, 3 + 12 * l + 7);
+      WMARK(P, l, 11);
       if (l + 1 < L) {
         wt_load<4>(layer_at(P, l + 1).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
         gain16_load(layer_at(P, l + 1).attn_norm, gq);
@@ -1325,23 +1329,25 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
       if (!wait_all(c, lm - 1)) return;
       gain16_load(P.out_norm, gq);
       panel_norm(RX, T, gq, P.eps, pcodes, pscales, P.hid);
-      mark(P, 2);
+      MARK(P, 2);
     }
     return;
   }
   if (!wait_all(c, lm - 1)) return;
-  mark(P, 3 + 12 * L);
+  MARK(P, 3 + 12 * L);
   gain16_load(P.out_norm, gq);
   panel_norm(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr);
   lm_head<G>(P, desc, T, pcodes, pscales, s_best);
   publish(c, lm);
-  mark(P, 4 + 12 * L);
+  MARK(P, 4 + 12 * L);
   if (w == 0) {
     if (!wait_all(c, lm)) return;
-    mark(P, 5 + 12 * L);
-    accept<G>(P.part_keys, desc->tokens, P.result, T, kNwg, s_red, s_choice, s_tok, P.timing, 7 + 12 * L);
-    mark(P, 6 + 12 * L);
+    MARK(P, 5 + 12 * L);
+    accept<G>(P.part_keys, desc->tokens, P.result, T, kNwg, s_red, s_choice, s_tok, PROF ? P.timing : nullptr, 7 + 12 * L);
+    MARK(P, 6 + 12 * L);
   }
+#undef MARK
+#undef WMARK
 #undef RX
 #undef RQKV
 }
@@ -1360,24 +1366,34 @@ uint32_t step_progress_per_step(int n_layers) { return 2u + (uint32_t)(n_layers 
 
 size_t step_lds_bytes(int G) { return step_lds_x_offset(G) + (size_t)G * 8 * 16 * 4; }
 
+namespace {
+// [G - 1][f16 KV][profiled]
+const void* step_fn(int G, int kv_f16, bool prof) {
+  static const void* fns[2][2][2] = {
+      {{(const void*)k_step<1, 0, false>, (const void*)k_step<1, 0, true>},
+       {(const void*)k_step<1, 1, false>, (const void*)k_step<1, 1, true>}},
+      {{(const void*)k_step<2, 0, false>, (const void*)k_step<2, 0, true>},
+       {(const void*)k_step<2, 1, false>, (const void*)k_step<2, 1, true>}}};
+  return fns[G - 1][kv_f16 ? 1 : 0][prof ? 1 : 0];
+}
+}  // namespace
+
 hipError_t prepare_step_kernels() {
-  const void* fns[4] = {(const void*)k_step<1, 0>, (const void*)k_step<1, 1>, (const void*)k_step<2, 0>,
-                        (const void*)k_step<2, 1>};
-  for (int i = 0; i < 4; ++i) {
-    const hipError_t e =
-        hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)step_lds_bytes(1 + i / 2));
-    if (e != hipSuccess) return e;
-  }
+  for (int G = 1; G <= 2; ++G)
+    for (int kv = 0; kv < 2; ++kv)
+      for (int prof = 0; prof < 2; ++prof) {
+        const hipError_t e = hipFuncSetAttribute(step_fn(G, kv, prof != 0), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)step_lds_bytes(G));
+        if (e != hipSuccess) return e;
+      }
   return hipSuccess;
 }
 
 hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
-                        uint32_t epoch, int mode) {
+                        uint32_t epoch, int mode, bool profiled) {
   void* args[] = {(void*)&P, (void*)&desc, (void*)&epoch, (void*)&mode};
   const size_t lds = step_lds_bytes(G);
-  const void* fn = G == 1 ? (kv_f16 ? (const void*)k_step<1, 1> : (const void*)k_step<1, 0>)
-                          : (kv_f16 ? (const void*)k_step<2, 1> : (const void*)k_step<2, 0>);
-  return hipLaunchCooperativeKernel(fn, dim3(kNwg), dim3(kT), args, lds, s);
+  return hipLaunchCooperativeKernel(step_fn(G, kv_f16, profiled), dim3(kNwg), dim3(kT), args, lds, s);
 }
 
 }  // namespace mtg
