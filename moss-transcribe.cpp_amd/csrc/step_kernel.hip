@@ -595,6 +595,29 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
   }
 }
 
+// The new v rows of kv head g: wave w copies rows w + 4 j (j < NV, row < T) of
+// this step's v to LDS (f16-rounded for an f16 cache).
+template <int NV, int KVH>
+__device__ __forceinline__ void stage_v(const StepParams& P, int g, int T, float* vnew) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const Rsrc rq = mk_rsrc(P.qkv, kMaxRows * cNQKV * 4);
+  float x0[NV], x1[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int t = wave + 4 * j;
+    const uint32_t base = (uint32_t)((min(t, T - 1) * cNQKV + (cNH + cNKV + g) * cHD) * 4);
+    x0[j] = ldc1(rq, base + lane * 4);
+    x1[j] = ldc1(rq, base + (lane + 64) * 4);
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int t = wave + 4 * j;
+    if (t >= T) break;
+    vnew[t * cQStride + lane] = KVH ? f16_round(x0[j]) : x0[j];
+    vnew[t * cQStride + lane + 64] = KVH ? f16_round(x1[j]) : x1[j];
+  }
+}
+
 // One attention item: chunk `chunk` of kv head g over the ncol = 2T query
 // columns (col = hl*T + t for q head 2g + hl). LDS: q [32][132], knew/vnew
 // [16][132], sp [32][68].
@@ -613,13 +636,13 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   const bool appender = key0 <= past && past < key0 + kChunk;
   // 1. stage the roped q rows and, if this chunk reaches them, the new k / v rows
   //    (q rows: 4G per wave; with the new rows up to 8 per wave and pass)
-  const int nrows = ncol + (has_new ? 2 * T : 0);
   if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 21); }
   if (!has_new) {
-    stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, nrows, q_lds, knew, vnew, prof);
+    stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol, q_lds, knew, vnew, prof);
   } else {
-    for (int r0 = wave; r0 < nrows; r0 += 32)
-      stage_pass<8, KVH>(P, Ly, T, past, g, r0, nrows, q_lds, knew, vnew);
+    // q and new k rows are normed and roped; the new v rows are plain copies
+    stage_pass<6 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, q_lds, knew, vnew);
+    stage_v<2 * G, KVH>(P, g, T, vnew);
   }
   bar();
   if (prof) wmark(P, 1, 16);
