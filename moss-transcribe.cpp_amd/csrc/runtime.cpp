@@ -385,10 +385,14 @@ void Ctx::enqueue_wt(int mode) {
 int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_out,
              float* logits_out) {
   const int G = (T + 7) / 8;
-  int rc = check(hipMemcpyAsync(desc_dev, desc_host, sizeof(StepDesc), hipMemcpyHostToDevice, stream),
-                 "step descriptor");
-  if (rc) return rc;
+  int rc = MTG_OK;
   const bool step_mode = mode == kModeVerify || mode == kModeVerifyPenalty || mode == kModeAppend;
+  // the step kernel takes the descriptor as a kernel argument; the per-op kernels
+  // read it from device memory
+  if (!(exec == kExecStep && step_ok && step_mode) &&
+      (rc = check(hipMemcpyAsync(desc_dev, desc_host, sizeof(StepDesc), hipMemcpyHostToDevice, stream),
+                  "step descriptor")))
+    return rc;
   const bool timed = timing && mode != kModeLogits;
   if (timed && (rc = check(hipEventRecord(ev_start, stream), "timing event"))) return rc;
   if (exec == kExecStep && step_ok && step_mode) {
@@ -404,7 +408,7 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
       if ((rc = check(hipMemsetAsync(&result_dev->err, 1, sizeof(int32_t), stream), "abort")))
         return rc;
     }
-    if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, params_dev, desc_dev, epoch, smode,
+    if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, params_dev, desc_host, epoch, smode,
                                     params_host.timing != nullptr), "step kernel launch")))
       return rc;
     epoch += step_progress_per_step(hp.n_layers);

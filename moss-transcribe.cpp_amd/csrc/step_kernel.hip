@@ -911,8 +911,8 @@ __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, 
 // 8-deep register ring; per tile the canonical 4-slice sums, the penalty and
 // 64-bit first-max keys.
 template <int G>
-__device__ __forceinline__ void lm_head(const StepParams& P, const StepDesc* desc, int T, const uint8_t* pcodes,
-                        const float* pscales, uint64_t* s_best) {
+__device__ __forceinline__ void lm_head(const StepParams& P, float penalty, bool write_logits, int T,
+                                        const uint8_t* pcodes, const float* pscales, uint64_t* s_best) {
   // a called function receives P's fields and T in vector registers: make the
   // tile arithmetic wave-uniform again, or every buffer load with a scalar
   // offset becomes a loop over its distinct values
@@ -920,10 +920,8 @@ __device__ __forceinline__ void lm_head(const StepParams& P, const StepDesc* des
   T = __builtin_amdgcn_readfirstlane(T);
   const int V = __builtin_amdgcn_readfirstlane(P.V), n_tiles = V / 16, gw = blockIdx.x * 4 + wave,
             nwaves = gridDim.x * 4;
-  const bool pen = desc->penalty > 1.0f;
-  const float penalty = desc->penalty;
+  const bool pen = penalty > 1.0f;
   const int words = (V + 31) / 32;
-  const bool write_logits = desc->write_logits != 0;
   float* const logits = uniform_ptr(P.logits);
   const Rsrc rb = mk_rsrc(uniform_ptr(P.bitmap), (uint32_t)(kMaxRows * words * 4));
   // the penalty bits of a tile's 16 rows share one word per verify row; it is
@@ -1062,14 +1060,13 @@ __device__ __forceinline__ void lm_head(const StepParams& P, const StepDesc* des
 // those loads and the draft tokens' are in flight together. Per row a wave max,
 // then the four waves.
 template <int G>
-__device__ void accept(const uint64_t* part_keys, const int32_t* tokens, StepResult* result, int T, int nwg,
+__device__ void accept(const uint64_t* part_keys, int32_t tok, StepResult* result, int T, int nwg,
                        uint64_t* s_red, int32_t* s_choice, int32_t* s_tok, uint64_t* timing, int slot) {
   static_assert(kNwg <= kT, "one thread per workgroup's keys");
   T = __builtin_amdgcn_readfirstlane(T);
   nwg = __builtin_amdgcn_readfirstlane(nwg);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const Rsrc rk = mk_rsrc(uniform_ptr(part_keys), (uint32_t)(nwg * kMaxRows * 8));
-  const Rsrc rt = mk_rsrc(uniform_ptr(tokens), (uint32_t)(T * 4));
   constexpr int R = 8 * G;  // rows of this launch's column groups
   uint64_t key[R];
 #pragma unroll
@@ -1079,8 +1076,6 @@ __device__ void accept(const uint64_t* part_keys, const int32_t* tokens, StepRes
     key[2 * h] = ((uint64_t)q.y << 32) | q.x;
     key[2 * h + 1] = ((uint64_t)q.w << 32) | q.z;
   }
-  const int32_t tok = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(
-      rt, (int)threadIdx.x < T ? (uint32_t)(threadIdx.x * 4) : 0x80000000u, 0, 0);
   if ((int)threadIdx.x < T) s_tok[threadIdx.x] = tok;
   if (timing) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); if (threadIdx.x == 0) gst<uint64_t>(uniform_ptr(timing) + slot, wall_clock64()); }
 #pragma unroll
@@ -1123,7 +1118,7 @@ __device__ __forceinline__ uint32_t ph(int l, int p) { return 2u + (uint32_t)(l 
 // variant carries no marks at all (they would cost code size and registers)
 template <int G, int KVH, bool PROF>
 __global__ void __launch_bounds__(kT, 1)
-k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uint32_t epoch,
+k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoch,
         int mode) {
 #define MARK(...) do { if constexpr (PROF) mark(__VA_ARGS__); } while (0)
 #define WMARK(...) do { if constexpr (PROF) wmark(__VA_ARGS__); } while (0)
@@ -1136,7 +1131,11 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   __shared__ int32_t s_choice[kMaxRows];
   __shared__ int32_t s_tok[kMaxRows];
   const int w = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int T = desc->T, past = desc->past, L = P.L;
+  // The step descriptor arrives by value in the kernel arguments (no copy to
+  // device memory before the launch). Its fields are read in place; its address
+  // is never taken (that would give every thread a private copy).
+  const StepDesc& desc = desc_arg;
+  const int T = desc.T, past = desc.past, L = P.L;
   const int nch = (past + T + kChunk - 1) / kChunk, n_items = cNKV * nch;
   uint8_t* pcodes = lds;
   float* pscales = (float*)(lds + (size_t)G * cBF * 1024);
@@ -1176,10 +1175,10 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
     const int t = w;
     const int k = threadIdx.x * 4;
     v4f e;
-    if (desc->use_embeds) {
+    if (desc.use_embeds) {
       e = gld<v4f>(P.embeds + (size_t)t * cH + k);
     } else {
-      const int n = desc->tokens[t], tile = n >> 4, r = n & 15;
+      const int n = desc.tokens[t], tile = n >> 4, r = n & 15;
       const int bk = k >> 5, bp = bk >> 1, par = bk & 1, half = (k >> 4) & 1;
       const uint8_t* unit = P.embd + ((size_t)tile * cBH + bp) * kUnitBytes;
       const uint32_t q4 = gld<uint32_t>(unit + (r + 16 * (2 * par + half)) * 16 + (k & 15));
@@ -1194,15 +1193,15 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   // later publish of this workgroup covers its stores)
   if (w < T) {
     const int t = w;
-    if (mode == kStepVerify && desc->penalty > 1.0f) {
+    if (mode == kStepVerify && desc.penalty > 1.0f) {
       const int words = (P.V + 31) / 32;
       uint32_t* row = P.bitmap + (size_t)t * words;
       for (int i = threadIdx.x; i < words; i += kT) st_coh_u32(row + i, 0u);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       __syncthreads();
-      const int end = desc->pen_base + t + 1, begin = max(0, end - kPenaltyWindow);
+      const int end = desc.pen_base + t + 1, begin = max(0, end - kPenaltyWindow);
       for (int i = begin + (int)threadIdx.x; i < end; i += kT) {
-        const int id = desc->pen_ids[i];
+        const int id = desc.pen_ids[i];
         if (id >= 0 && id < P.V) atomicOr(row + (id >> 5), 1u << (id & 31));
       }
     }
@@ -1360,13 +1359,14 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc* __restrict__ desc, uin
   MARK(P, 3 + 12 * L);
   gain16_load(P.out_norm, gq);
   panel_norm(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr);
-  lm_head<G>(P, desc, T, pcodes, pscales, s_best);
+  lm_head<G>(P, desc_arg.penalty, desc_arg.write_logits != 0, T, pcodes, pscales, s_best);
   publish(c, lm);
   MARK(P, 4 + 12 * L);
   if (w == 0) {
     if (!wait_all(c, lm)) return;
     MARK(P, 5 + 12 * L);
-    accept<G>(P.part_keys, desc->tokens, P.result, T, kNwg, s_red, s_choice, s_tok, PROF ? P.timing : nullptr, 7 + 12 * L);
+    accept<G>(P.part_keys, (int)threadIdx.x < T ? desc_arg.tokens[threadIdx.x] : 0, P.result, T, kNwg, s_red,
+              s_choice, s_tok, PROF ? P.timing : nullptr, 7 + 12 * L);
     MARK(P, 6 + 12 * L);
   }
 #undef MARK
@@ -1414,7 +1414,8 @@ hipError_t prepare_step_kernels() {
 
 hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
                         uint32_t epoch, int mode, bool profiled) {
-  void* args[] = {(void*)&P, (void*)&desc, (void*)&epoch, (void*)&mode};
+  // desc: host memory; the launch copies it into the kernel arguments
+  void* args[] = {(void*)&P, (void*)desc, (void*)&epoch, (void*)&mode};
   const size_t lds = step_lds_bytes(G);
   return hipLaunchCooperativeKernel(step_fn(G, kv_f16, profiled), dim3(kNwg), dim3(kT), args, lds, s);
 }

@@ -58,7 +58,8 @@ constexpr int kFlagStride = 32;
 uint32_t step_progress_per_step(int n_layers);
 size_t step_lds_bytes(int G);
 hipError_t prepare_step_kernels();
-// profiled: the variant that writes clock marks into StepParams::timing
+// desc: the host copy of the step descriptor (passed by value as a kernel
+// argument). profiled: the variant that writes clock marks into StepParams::timing
 hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
                         uint32_t epoch, int mode, bool profiled);
 
