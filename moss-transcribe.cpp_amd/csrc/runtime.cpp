@@ -292,10 +292,12 @@ int Ctx::init_step_kernel() {
   P.aqs = (float*)dalloc((size_t)kMaxRows * F / 32 * 4, true);
   P.result = result_map;  // choices and n_match go straight to pinned host memory
   P.flags = (uint32_t*)dalloc((size_t)nwg * kFlagStride * 4, true);
+  P.qkvt = (uint32_t*)dalloc(qkvt_bytes(), true);
   P.err = &result_dev->err;
   P.timing = nullptr;
   params_dev = (StepParams*)dalloc(sizeof(StepParams), false);
-  if (!P.part_ml || !P.part_o || !P.part_keys || !P.flags || !P.oq || !P.oqs || !P.aq || !P.aqs || !params_dev)
+  if (!P.part_ml || !P.part_o || !P.part_keys || !P.flags || !P.qkvt || !P.oq || !P.oqs || !P.aq || !P.aqs ||
+      !params_dev)
     return fail(MTG_ERR_NOMEM, "step kernel buffers");
   if ((rc = check(hipMemcpy(params_dev, &P, sizeof(P), hipMemcpyHostToDevice), "step params")))
     return rc;
@@ -398,6 +400,8 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
   if (exec == kExecStep && step_ok && step_mode) {
     if (epoch > 0xF0000000u) {  // progress words restart before they could wrap
       if ((rc = check(hipMemsetAsync(params_host.flags, 0, (size_t)nwg * kFlagStride * 4, stream), "flags"))) return rc;
+      // the tags of the exchanged q|k|v values come from the same counter
+      if ((rc = check(hipMemsetAsync(params_host.qkvt, 0, qkvt_bytes(), stream), "tags"))) return rc;
       epoch = 0;
     }
     const int smode = mode == kModeAppend ? kStepAppend : kStepVerify;

@@ -75,6 +75,10 @@ struct Ctx {
   int upload_q8(const void* blocks, int n, int k, uint8_t* dst, uint8_t* staging);
   // bytes of an n x k weight matrix on the device, and its upload
   size_t weight_bytes(int n, int k) const;
+  // the step kernel's tagged q|k|v exchange: [rows][q|k|v] (value, tag) pairs
+  size_t qkvt_bytes() const {
+    return (size_t)kMaxRows * (hp.n_heads + 2 * hp.n_kv_heads) * hp.head_dim * 8;
+  }
   int upload_weights(const void* src, int n, int k, uint8_t* dst, uint8_t* staging);
   int init(const mtg_model_desc* d, int max_seq, int kv_type);
   KvLayer kv_layer(int l) const;

@@ -167,6 +167,36 @@ __device__ __forceinline__ bool wait_all(Ctl& c, uint32_t v, int prof_slot = -1)
   return *c.s_ok != 0;
 }
 
+// Values read from a tagged exchange buffer: each 8-byte pair is (value bits,
+// tag), written by one 8-byte part of a store, so a pair whose tag is the phase's
+// progress value holds that phase's value. Re-reads the pairs whose tag is not yet
+// `want` until all are (bounded, like wait_all). Per lane: N pairs at byte offsets
+// off[j] (live[j] false: not needed). When the wait runs out it raises the error
+// word and returns with what it has: the workgroup leaves at its next progress
+// wait, and the host discards the step (only positions from `past` on were
+// written). The workgroup does not leave from here: an exit from inside the
+// attention costs the whole kernel its register allocation.
+template <int N>
+__device__ __forceinline__ void tagged_wait(const StepParams& P, Rsrc r, v2u (&a)[N], const uint32_t (&off)[N],
+                                            const bool (&live)[N], uint32_t want) {
+  const Rsrc re = mk_rsrc(P.err, 4);
+  for (unsigned spins = 0;; ++spins) {
+    bool stale = false;
+#pragma unroll
+    for (int j = 0; j < N; ++j) stale |= live[j] && a[j].y != want;
+    if (!__any(stale)) return;
+    if (__builtin_amdgcn_raw_buffer_load_b32(re, 0, 0, 16)) return;
+    if (spins > kSpin) {
+      if ((threadIdx.x & 63) == 0) __builtin_amdgcn_raw_buffer_store_b32(1u, re, 0, 0, 16);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (live[j] && a[j].y != want) a[j] = __builtin_amdgcn_raw_buffer_load_b64(r, off[j], 0, 16);
+  }
+}
+
 __device__ __forceinline__ void mark(const StepParams& P, int slot) {
   if (P.timing && blockIdx.x == 0 && threadIdx.x == 0) gst<uint64_t>(P.timing + slot, wall_clock64());
 }
@@ -235,7 +265,8 @@ enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 // even and odd block halves; wave 0 writes T x 16 outputs with 16-byte stores.
 template <int G, int NM, int EPI>
 __device__ __forceinline__ void gemm_finish(float acc[NM][G][4], float* red, Rsrc out, int n,
-                                            int tile, int T, float* xs = nullptr, bool xs_valid = false) {
+                                            int tile, int T, float* xs = nullptr, bool xs_valid = false,
+                                            uint32_t tag = 0) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
 #pragma unroll
   for (int m = 0; m < NM; ++m)
@@ -278,7 +309,16 @@ __device__ __forceinline__ void gemm_finish(float acc[NM][G][4], float* red, Rsr
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] = dev_swiglu(acc[0][cg][q], acc[NM - 1][cg][q]);
           }
-          stc4(out, off, v);
+          if (EPI == EPI_STORE) {
+            // (value, tag) pairs, two per 16-byte store: readers check the tags
+            // instead of waiting for this workgroup's progress word
+            const v4u p0 = {__float_as_uint(v[0]), tag, __float_as_uint(v[1]), tag};
+            const v4u p1 = {__float_as_uint(v[2]), tag, __float_as_uint(v[3]), tag};
+            __builtin_amdgcn_raw_buffer_store_b128(p0, out, (int)(2 * off), 0, 16);
+            __builtin_amdgcn_raw_buffer_store_b128(p1, out, (int)(2 * off + 16), 0, 16);
+          } else {
+            stc4(out, off, v);
+          }
         }
       }
     }
@@ -537,25 +577,31 @@ __device__ __forceinline__ float kv_val(uint32_t bits, bool f16) {
 // nothing.
 template <int NS, int KVH>
 __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& Ly, int T, int past, int g,
-                                           int r0, int nrows, float* q_lds, float* knew, float* vnew,
-                                           bool prof = false) {
+                                           int r0, int nrows, uint32_t tag, float* q_lds, float* knew,
+                                           float* vnew, bool prof = false) {
   const int lane = threadIdx.x & 63, ncol = 2 * T;
   constexpr bool f16kv = KVH != 0;
-  const Rsrc rq = mk_rsrc(P.qkv, kMaxRows * cNQKV * 4);
+  const Rsrc rq = mk_rsrc(P.qkvt, kMaxRows * cNQKV * 8);
   float x0[NS], x1[NS], g0[NS], g1[NS], rc[NS], rs[NS];
   int kind[NS], tt[NS];
+  v2u pr[2 * NS];  // (value, tag) of elements lane and lane + 64 of each slot
+  uint32_t po[2 * NS];
+  bool live[2 * NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     const int r = r0 + 4 * j;
     kind[j] = r < ncol ? 0 : (r < ncol + T ? 1 : 2);
     tt[j] = kind[j] == 0 ? r % T : (kind[j] == 1 ? r - ncol : r - ncol - T);
-    x0[j] = x1[j] = g0[j] = g1[j] = rc[j] = rs[j] = 0.0f;
+    g0[j] = g1[j] = rc[j] = rs[j] = 0.0f;
+    live[2 * j] = live[2 * j + 1] = r < nrows;
+    const int col = kind[j] == 0 ? (2 * g + r / T) * cHD
+                                 : (kind[j] == 1 ? (cNH + g) * cHD : (cNH + cNKV + g) * cHD);
+    po[2 * j] = (uint32_t)((min(tt[j], kMaxRows - 1) * cNQKV + col + lane) * 8);
+    po[2 * j + 1] = po[2 * j] + 64 * 8;
+    pr[2 * j] = pr[2 * j + 1] = v2u{0u, tag};
     if (r < nrows) {
-      const int col = kind[j] == 0 ? (2 * g + r / T) * cHD
-                                   : (kind[j] == 1 ? (cNH + g) * cHD : (cNH + cNKV + g) * cHD);
-      const uint32_t base = (uint32_t)((tt[j] * cNQKV + col) * 4);
-      x0[j] = ldc1(rq, base + lane * 4);
-      x1[j] = ldc1(rq, base + (lane + 64) * 4);
+      pr[2 * j] = __builtin_amdgcn_raw_buffer_load_b64(rq, po[2 * j], 0, 16);
+      pr[2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b64(rq, po[2 * j + 1], 0, 16);
       if (kind[j] < 2) {
         const float* gn = kind[j] == 0 ? Ly.q_norm : Ly.k_norm;
         g0[j] = gld<float>(gn + lane);
@@ -565,6 +611,12 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
         rs[j] = cs.y;
       }
     }
+  }
+  tagged_wait<2 * NS>(P, rq, pr, po, live, tag);
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    x0[j] = __uint_as_float(pr[2 * j].x);
+    x1[j] = __uint_as_float(pr[2 * j + 1].x);
   }
   if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); wmark(P, 1, 15); }
   double sq[NS];
@@ -598,23 +650,29 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
 // The new v rows of kv head g: wave w copies rows w + 4 j (j < NV, row < T) of
 // this step's v to LDS (f16-rounded for an f16 cache).
 template <int NV, int KVH>
-__device__ __forceinline__ void stage_v(const StepParams& P, int g, int T, float* vnew) {
+__device__ __forceinline__ void stage_v(const StepParams& P, int g, int T, uint32_t tag, float* vnew) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const Rsrc rq = mk_rsrc(P.qkv, kMaxRows * cNQKV * 4);
-  float x0[NV], x1[NV];
+  const Rsrc rq = mk_rsrc(P.qkvt, kMaxRows * cNQKV * 8);
+  v2u pr[2 * NV];
+  uint32_t po[2 * NV];
+  bool live[2 * NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int t = wave + 4 * j;
-    const uint32_t base = (uint32_t)((min(t, T - 1) * cNQKV + (cNH + cNKV + g) * cHD) * 4);
-    x0[j] = ldc1(rq, base + lane * 4);
-    x1[j] = ldc1(rq, base + (lane + 64) * 4);
+    po[2 * j] = (uint32_t)((min(t, T - 1) * cNQKV + (cNH + cNKV + g) * cHD + lane) * 8);
+    po[2 * j + 1] = po[2 * j] + 64 * 8;
+    live[2 * j] = live[2 * j + 1] = t < T;
+    pr[2 * j] = __builtin_amdgcn_raw_buffer_load_b64(rq, po[2 * j], 0, 16);
+    pr[2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b64(rq, po[2 * j + 1], 0, 16);
   }
+  tagged_wait<2 * NV>(P, rq, pr, po, live, tag);
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int t = wave + 4 * j;
     if (t >= T) break;
-    vnew[t * cQStride + lane] = KVH ? f16_round(x0[j]) : x0[j];
-    vnew[t * cQStride + lane + 64] = KVH ? f16_round(x1[j]) : x1[j];
+    const float x0 = __uint_as_float(pr[2 * j].x), x1 = __uint_as_float(pr[2 * j + 1].x);
+    vnew[t * cQStride + lane] = KVH ? f16_round(x0) : x0;
+    vnew[t * cQStride + lane + 64] = KVH ? f16_round(x1) : x1;
   }
 }
 
@@ -623,7 +681,7 @@ __device__ __forceinline__ void stage_v(const StepParams& P, int g, int T, float
 // [16][132], sp [32][68].
 template <int G, int KVH>
 __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& Ly, int T, int past, int g, int chunk,
-                                          const KvRegs& kv, uint8_t* lds, bool prof) {
+                                          uint32_t tag, const KvRegs& kv, uint8_t* lds, bool prof) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, kl = lane & 15,
             kk = lane >> 4;
   constexpr bool f16kv = KVH != 0;
@@ -635,14 +693,16 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   const bool has_new = key0 + kChunk > past;
   const bool appender = key0 <= past && past < key0 + kChunk;
   // 1. stage the roped q rows and, if this chunk reaches them, the new k / v rows
-  //    (q rows: 4G per wave; with the new rows up to 8 per wave and pass)
+  //    (q rows: 4G per wave; with the new rows up to 8 per wave and pass). The
+  //    rows come from the tagged q|k|v buffer: no wait for the q|k|v phase's
+  //    progress, each value is checked by its tag.
   if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 21); }
   if (!has_new) {
-    stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol, q_lds, knew, vnew, prof);
+    stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol, tag, q_lds, knew, vnew, prof);
   } else {
     // q and new k rows are normed and roped; the new v rows are plain copies
-    stage_pass<6 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, q_lds, knew, vnew);
-    stage_v<2 * G, KVH>(P, g, T, vnew);
+    stage_pass<6 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, tag, q_lds, knew, vnew);
+    stage_v<2 * G, KVH>(P, g, T, tag, vnew);
   }
   bar();
   if (prof) wmark(P, 1, 16);
@@ -1144,7 +1204,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   bool xs_valid = false;
   Ctl c{&P, epoch, 0, &s_ok};
 #define RX mk_rsrc(P.x, kMaxRows * cH * 4)
-#define RQKV mk_rsrc(P.qkv, kMaxRows * cNQKV * 4)
+#define RQKVT mk_rsrc(P.qkvt, kMaxRows * cNQKV * 8)
 
   // roles
   const int first_item = (w + kNwg - 64) % kNwg;  // item i runs on workgroup (i + 64) % 256
@@ -1223,19 +1283,21 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       float acc[1][G][4] = {};
       wt_mma<G, 4>(qa, qs, 4 * wave, cBH, pcodes, pscales, acc[0]);
       WMARK(P, l, 26);
-      gemm_finish<G, 1, EPI_STORE>(acc, red, RQKV, cNQKV, w, T);
+      gemm_finish<G, 1, EPI_STORE>(acc, red, RQKVT, cNQKV, w, T, nullptr, false, c.epoch + ph(l, kPhQkv));
     }
-    publish(c, next_done(l, kPhQkv));
+    // the attention reads q|k|v by their tags: a workgroup with attention items
+    // announces its q|k|v tile together with its attention partials
+    if (!has_attn) publish(c, next_done(l, kPhQkv));
     MARK(P, 3 + 12 * l + 1);
     WMARK(P, l, 1);
     // ---- ATTN: items of this workgroup ----
     if (has_attn) {
-      if (!wait_all(c, ph(l, kPhAttn) - 1, PROF && l == 1 ? wslot(w, 14) : -1)) return;
       MARK(P, 3 + 12 * l + 2);
       WMARK(P, l, 2);
       for (int item = first_item; item < n_items; item += kNwg) {
         if (item != first_item) kv_prefetch<KVH>(Ly, P, item / nch, (item % nch) * kChunk, past, kv);
-        attn_item<G, KVH>(P, Ly, T, past, item / nch, item % nch, kv, lds, PROF && l == 1 && P.timing != nullptr);
+        attn_item<G, KVH>(P, Ly, T, past, item / nch, item % nch, c.epoch + ph(l, kPhQkv), kv, lds,
+                          PROF && l == 1 && P.timing != nullptr);
       }
       publish(c, next_done(l, kPhAttn));
       MARK(P, 3 + 12 * l + 3);
@@ -1372,7 +1434,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
 #undef MARK
 #undef WMARK
 #undef RX
-#undef RQKV
+#undef RQKVT
 }
 
 }  // namespace

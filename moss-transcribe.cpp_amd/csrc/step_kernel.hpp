@@ -42,6 +42,9 @@ struct StepParams {
   uint64_t* part_keys;      // [nwg][16]
   StepResult* result;
   uint32_t* flags;          // [nwg][kFlagStride] progress words, one per 128-byte line
+  // q|k|v of the step's rows as (value bits, tag) pairs, [16][4096][2]: the tag is
+  // the progress value of the phase that wrote it, so a reader needs no flag
+  uint32_t* qkvt;
   int32_t* err;             // raised by a wait that ran out (inside *result)
   uint64_t* timing;         // nullable: phase clock marks (profiling)
 };
