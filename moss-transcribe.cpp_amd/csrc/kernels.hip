@@ -219,35 +219,124 @@ k_qk_rope_append(const StepDesc* __restrict__ desc, const float* __restrict__ qk
 
 // -------------------------------------------------------------- attention --
 // One workgroup per (kv head g, chunk of 64 keys); query columns col = hl*T + t
-// for q heads 2g + hl. Canonical chunk arithmetic (device_common.hpp).
+// for q heads 2g + hl. Canonical chunk arithmetic (device_common.hpp) on
+// v_mfma_f32_16x16x4f32, whose 4-term dot is a sequential fma chain: scores are a
+// chain of 32 MFMAs over head_dim, P.V a chain of 16 over the chunk's keys.
+// The chunk's K and V come to LDS with 16-byte loads (as f32, zeros past kvlen);
+// q and K rows are kept permuted (element 4 s + kk at kk * 32 + s) and the
+// probabilities too (key 4 s + kk at kk * 16 + s), so that every MFMA operand of
+// a lane is one run of consecutive floats.
+constexpr int kAqStride = 132, kApStride = 68;
+constexpr size_t kAttnLds = (size_t)(kMaxCols * kAqStride + 2 * kChunk * kAqStride + kMaxCols * kApStride) * 4;
+
+__device__ __forceinline__ int attn_perm128(int d) { return (d & 3) * 32 + (d >> 2); }
+
 __global__ void __launch_bounds__(256)
 k_attn_chunk(const StepDesc* __restrict__ desc, const float* __restrict__ q, int n_heads,
              KvLayer kv, AttnWork work, int max_chunks) {
   const int g = blockIdx.x, chunk = blockIdx.y;
   const int T = desc->T, past = desc->past, kvlen = past + T;
-  if (chunk * kChunk >= kvlen) return;
-  __shared__ float s_q[kMaxCols * kHeadDim];
-  __shared__ float s_v[kChunk * kHeadDim];
-  __shared__ float s_p[kMaxCols * kChunk];
+  const int key0 = chunk * kChunk;
+  if (key0 >= kvlen) return;
+  extern __shared__ v4f attn_lds_v4[];
+  float* s_q = (float*)attn_lds_v4;                 // [32][132] permuted
+  float* s_k = s_q + kMaxCols * kAqStride;          // [64][132] permuted
+  float* s_v = s_k + kChunk * kAqStride;            // [64][132]
+  float* s_p = s_v + kChunk * kAqStride;            // [32][68] permuted
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, kl = lane & 15, kk = lane >> 4;
   const int ncol = 2 * T;
   const bool f16kv = kv.f16 != 0;
-  for (int idx = threadIdx.x; idx < ncol * kHeadDim; idx += 256) {
-    const int col = idx / kHeadDim, d = idx % kHeadDim, hl = col / T, t = col % T;
-    const float v = q[((size_t)t * n_heads + 2 * g + hl) * kHeadDim + d];
-    s_q[idx] = f16kv ? f16_round(v) : v;  // mul_mat(f16 K, f32 q) converts q to f16
+  // 1. q rows (f16-rounded for an f16 cache: mul_mat(f16 K, f32 q) converts q),
+  //    and the chunk's K / V rows, 4 consecutive elements per thread and pass
+  for (int idx = tid; idx < ncol * (kHeadDim / 4); idx += 256) {
+    const int col = idx / (kHeadDim / 4), d = (idx % (kHeadDim / 4)) * 4, hl = col / T, t = col % T;
+    const v4f v = *(const v4f*)(q + ((size_t)t * n_heads + 2 * g + hl) * kHeadDim + d);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_q[col * kAqStride + attn_perm128(d + e)] = f16kv ? f16_round(v[e]) : v[e];
+  }
+  const size_t head = (size_t)g * kv.max_seq * kHeadDim;
+#pragma unroll
+  for (int i = 0; i < kChunk * kHeadDim / 4 / 256; ++i) {
+    const int idx = i * 256 + tid, j = idx / (kHeadDim / 4), d = (idx % (kHeadDim / 4)) * 4;
+    const int key = key0 + j;
+    const bool in = key < kvlen;
+    const v4f kf = in ? kv_load4(kv.k, kv.f16, head + (size_t)key * kHeadDim + d) : (v4f){0.f, 0.f, 0.f, 0.f};
+    const v4f vf = in ? kv_load4(kv.v, kv.f16, head + (size_t)key * kHeadDim + d) : (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_k[j * kAqStride + attn_perm128(d + e)] = kf[e];
+    *(v4f*)(s_v + j * kAqStride + d) = vf;
   }
   __syncthreads();
-  AttnSrc a;
-  a.kc = kv.k;
-  a.vc = kv.v;
-  a.f16 = kv.f16;
-  a.head_base = (size_t)g * kv.max_seq * kHeadDim;
-  a.knew = nullptr;
-  a.vnew = nullptr;
-  a.new_from = kvlen;
+  // 2. scores of keys 16 wave + kl (A operand) for 16 columns per tile (B)
+  const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)kHeadDim));
+  for (int ct = 0; ct * 16 < ncol; ++ct) {
+    const int colb = ct * 16 + kl;
+    const float* krow = s_k + (16 * wave + kl) * kAqStride + kk * 32;
+    const float* qrow = s_q + min(colb, ncol - 1) * kAqStride + kk * 32;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const v4f k4 = *(const v4f*)(krow + 4 * i);
+      const v4f q4 = *(const v4f*)(qrow + 4 * i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[j], colb < ncol ? q4[j] : 0.0f, acc, 0, 0, 0);
+    }
+    if (colb < ncol) {
+      const int t = colb % T;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {  // key 16 wave + 4 kk + r sits at r * 16 + 4 wave + kk
+        const int key = key0 + 16 * wave + 4 * kk + r;
+        s_p[colb * kApStride + r * 16 + 4 * wave + kk] =
+            (key < kvlen && key <= past + t) ? __fmul_rn(acc[r], scale) : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+  // 3. chunk softmax per column (one wave per column, lane = key)
   const size_t item = (size_t)g * max_chunks + chunk;
-  attn_chunk<false>(a, s_q, ncol, T, past, kvlen, chunk * kChunk, __fdiv_rn(1.0f, dev_sqrtf((float)kHeadDim)), s_v,
-                    s_p, work.part_ml + item * kMaxCols * 2, work.part_o + item * kMaxCols * kHeadDim);
+  float* out_ml = work.part_ml + item * kMaxCols * 2;
+  float* out_o = work.part_o + item * kMaxCols * kHeadDim;
+  const int sp_pos = (lane & 3) * 16 + (lane >> 2);
+  for (int col = wave; col < ncol; col += 4) {
+    const float w = s_p[col * kApStride + sp_pos];
+    const float m = wave_max_f(w);
+    float p = (m == -INFINITY || w == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(w, m));
+    if (f16kv) p = f16_round(p);
+    const float l = wave_sum_f(p);
+    s_p[col * kApStride + sp_pos] = p;
+    if (lane == 0) {
+      out_ml[col * 2] = m;
+      out_ml[col * 2 + 1] = l;
+    }
+  }
+  __syncthreads();
+  // 4. O[col][d] = fma chain over the chunk's keys of p * v: wave w takes head_dim
+  //    tiles 2w, 2w + 1
+  for (int ct = 0; ct * 16 < ncol; ++ct) {
+    const int cola = ct * 16 + kl;
+    float pa[16];
+    const float* prow = s_p + min(cola, ncol - 1) * kApStride + kk * 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const v4f p4 = *(const v4f*)(prow + 4 * i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pa[4 * i + j] = cola < ncol ? p4[j] : 0.0f;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int d = 16 * (2 * wave + h) + kl;
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s2], s_v[(4 * s2 + kk) * kAqStride + d], acc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int col = ct * 16 + 4 * kk + r;
+        if (col < ncol) out_o[col * kHeadDim + d] = acc[r];
+      }
+    }
+  }
 }
 
 // grid (n_heads, 16 rows), 128 threads: merge the chunks of one (head, row),
@@ -496,10 +585,14 @@ void launch_qk_rope_append(hipStream_t s, const StepDesc* desc, const float* qkv
                      desc, qkv, n_heads, n_kv_heads, q_norm, k_norm, eps, rope, q_out, kv);
 }
 
+hipError_t prepare_kernels() {
+  return hipFuncSetAttribute((const void*)k_attn_chunk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnLds);
+}
+
 void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n_heads,
                       int n_kv_heads, KvLayer kv, AttnWork work, Panel o_panel, float* o_out) {
   const int max_chunks = (kv.max_seq + kChunk - 1) / kChunk;
-  hipLaunchKernelGGL(k_attn_chunk, dim3(n_kv_heads, max_chunks), dim3(256), 0, s, desc, q, n_heads,
+  hipLaunchKernelGGL(k_attn_chunk, dim3(n_kv_heads, max_chunks), dim3(256), kAttnLds, s, desc, q, n_heads,
                      kv, work, max_chunks);
   hipLaunchKernelGGL(k_attn_combine, dim3(n_heads, kMaxRows), dim3(kHeadDim), 0, s, desc, work,
                      n_heads, max_chunks, o_panel, o_out);

@@ -59,6 +59,9 @@ void launch_gemm_swiglu(hipStream_t s, int G, const StepDesc* desc, const uint8_
 void launch_qk_rope_append(hipStream_t s, const StepDesc* desc, const float* qkv, int n_heads,
                            int n_kv_heads, const float* q_norm, const float* k_norm, float eps,
                            const float* rope, float* q_out, KvLayer kv);
+// Launch attributes of the per-op kernels (the chunk attention's LDS); once per
+// context, before any launch or graph capture.
+hipError_t prepare_kernels();
 void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n_heads,
                       int n_kv_heads, KvLayer kv, AttnWork work, Panel o_panel, float* o_out);
 void launch_penalty_bitmap(hipStream_t s, const StepDesc* desc, int vocab, uint32_t* bitmap);
