@@ -62,6 +62,7 @@ void launch_qk_rope_append(hipStream_t s, const StepDesc* desc, const float* qkv
 // Launch attributes of the per-op kernels (the chunk attention's LDS); once per
 // context, before any launch or graph capture.
 hipError_t prepare_kernels();
+hipError_t prepare_kernels_wt();  // the same for the f16 / q4_K weight kernels
 void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n_heads,
                       int n_kv_heads, KvLayer kv, AttnWork work, Panel o_panel, float* o_out);
 void launch_penalty_bitmap(hipStream_t s, const StepDesc* desc, int vocab, uint32_t* bitmap);

@@ -24,6 +24,8 @@
 //          exact int32 sums dot = sum_s sc_s * dot_s and mins = sum_s mn_s * bsum_s;
 //          then in superblock order acc = acc + (d_w*d_x)*dot, acc = acc -
 //          (dmin_w*d_x)*mins.
+#include <algorithm>
+
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -321,6 +323,260 @@ __global__ void k_embed_wt(const StepDesc* __restrict__ desc, const uint8_t* __r
   }
 }
 
+// ------------------------------------------------- q4_K, task per lane ----
+// The workgroup stages the q8_K activation of every verify row in LDS; each wave
+// stages a batch of D weight rows (NM matrices) there, the next batch already in
+// flight in registers. Lane = task (row of the batch, superblock b, verify row t):
+// the exact int32 dot sum_s sc_s * dot_s over the superblock's 256 elements
+// (64 sdot4) and mins = sum_s mn_s * bsum_s, with no lane exchanges (integer sums
+// are exact in any order). A lane per (batch row, verify row) then runs the
+// canonical float chain over superblocks in order:
+//   acc = acc + (d_w*d_x)*dot,  acc = acc - (dmin_w*d_x)*mins.
+constexpr int kQ4MaxK = 3072;
+constexpr int kQ4Slots = (kQ4MaxK / 256 * 9 + 63) / 64;  // 16-byte weight pieces per lane and row
+constexpr int kQ4GemmD = 1, kQ4LmD = 4;                   // weight rows per wave and batch
+
+__host__ __device__ constexpr int q4_act_stride(int K) { return K + 16; }        // bytes; spreads LDS banks
+__host__ __device__ constexpr int q4_bs_stride(int K) { return K / 16 + 4; }     // ints
+__host__ __device__ constexpr size_t q4_lds_bytes(int K, int rows_per_wave) {
+  // act [16][K+16] + bsums [16][K/16+4] + dx [16][K/256] + per wave: the batch's
+  // weight rows and their (dot, mins) [rows][K/256][16][2]
+  return (size_t)kMaxRows * q4_act_stride(K) + (size_t)kMaxRows * q4_bs_stride(K) * 4 +
+         (size_t)kMaxRows * (K / 256) * 4 + 4 * (size_t)rows_per_wave * (K / 256) * (144 + kMaxRows * 8);
+}
+
+struct Q4Lds {
+  const int8_t* act;
+  const int* bs;
+  const float* dx;
+  uint8_t* w;  // this wave's weight rows
+  int* r;      // this wave's (dot, mins) results
+};
+
+__device__ __forceinline__ Q4Lds q4_stage(const ActQ8K& a, int K, int T, int rows_per_wave, uint8_t* lds) {
+  const int tid = threadIdx.x, wave = tid >> 6, nb = K / 256;
+  const int as = q4_act_stride(K), bst = q4_bs_stride(K);
+  int8_t* act = (int8_t*)lds;
+  int* bs = (int*)(lds + (size_t)kMaxRows * as);
+  float* dx = (float*)(bs + kMaxRows * bst);
+  uint8_t* wbase = (uint8_t*)(dx + kMaxRows * nb);
+  const int pa = K / 16, pb = K / 64;  // 16-byte pieces per row
+  for (int i = tid; i < T * pa; i += 256)
+    *(v4i*)(act + (size_t)(i / pa) * as + (i % pa) * 16) = ((const v4i*)a.qs)[i];
+  for (int i = tid; i < T * pb; i += 256) *(v4i*)(bs + (size_t)(i / pb) * bst + (i % pb) * 4) = ((const v4i*)a.bsums)[i];
+  for (int i = tid; i < T * nb; i += 256) dx[i] = a.d[i];
+  __syncthreads();
+  Q4Lds q;
+  q.act = act;
+  q.bs = bs;
+  q.dx = dx;
+  q.w = wbase + (size_t)wave * rows_per_wave * nb * 144;
+  q.r = (int*)(wbase + 4 * (size_t)rows_per_wave * nb * 144) + (size_t)wave * rows_per_wave * nb * kMaxRows * 2;
+  return q;
+}
+
+// get_scale_min_k4 of the 8 sub-blocks from the 12 packed bytes
+__device__ __forceinline__ void q4k_scales(const uint8_t* sc12, int sc[8], int mn[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sc[j] = sc12[j] & 63;
+    mn[j] = sc12[j + 4] & 63;
+  }
+#pragma unroll
+  for (int j = 4; j < 8; ++j) {
+    sc[j] = (sc12[j + 4] & 0xF) | ((sc12[j - 4] >> 6) << 4);
+    mn[j] = (sc12[j + 4] >> 4) | ((sc12[j] >> 6) << 4);
+  }
+}
+
+// Registers of one batch: rows row0 + d*rstride (d < D) of the NM matrices.
+template <int NM, int D>
+struct Q4Batch {
+  v4i v[NM][D][kQ4Slots];
+};
+
+template <int NM, int D>
+__device__ __forceinline__ void q4k_load(const uint8_t* const (&base)[NM], int n, int nb, int row0, int rstride,
+                                         Q4Batch<NM, D>& bt) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int row = row0 + d * rstride;
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int j = 0; j < kQ4Slots; ++j) {
+        const int i = lane + 64 * j;
+        if (row < n && i < nb * 9) bt.v[m][d][j] = ((const v4i*)(base[m] + (size_t)row * nb * 144))[i];
+      }
+  }
+}
+
+// The batch in registers to the wave's LDS rows, then every (row, superblock,
+// verify row) task; lane (d, t) = (lane >> 4, lane & 15) returns res[m] of batch
+// row d (d < D, in steps of 4 for D > 4) and verify row t < T.
+template <int NM, int D>
+__device__ __forceinline__ void q4k_batch(const Q4Batch<NM, D>& bt, int K, int T, const Q4Lds& q,
+                                          float (&res)[NM][(D + 3) / 4]) {
+  const int lane = threadIdx.x & 63, nb = K / 256;
+  const int as = q4_act_stride(K), bst = q4_bs_stride(K);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous batch's LDS reads are done
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int j = 0; j < kQ4Slots; ++j) {
+        const int i = lane + 64 * j;
+        if (i < nb * 9) ((v4i*)(q.w + (size_t)(m * D + d) * nb * 144))[i] = bt.v[m][d][j];
+      }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's LDS writes are done
+  const int ntask = NM * D * nb * T;
+  for (int task = lane; task < ntask; task += 64) {
+    const int rb = task / T, t = task - rb * T;  // rb = (m*D + d)*nb + b
+    const int b = rb % nb;
+    const uint8_t* blk = q.w + (size_t)rb * 144;
+    int sc[8], mn[8];
+    q4k_scales(blk + 4, sc, mn);
+    const v4i* xq = (const v4i*)(q.act + (size_t)t * as + b * 256);
+    const v4i* qs = (const v4i*)(blk + 16);
+    int dot = 0;
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {  // sub-blocks 2 mm (low nibbles) and 2 mm + 1 (high)
+      int d0 = 0, d1 = 0;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const v4i wq = qs[mm * 2 + i];
+        const v4i x0 = xq[(2 * mm) * 2 + i], x1 = xq[(2 * mm + 1) * 2 + i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          d0 = __builtin_amdgcn_sdot4(wq[e] & 0x0F0F0F0F, x0[e], d0, false);
+          d1 = __builtin_amdgcn_sdot4((wq[e] >> 4) & 0x0F0F0F0F, x1[e], d1, false);
+        }
+      }
+      dot += sc[2 * mm] * d0 + sc[2 * mm + 1] * d1;
+    }
+    const int* bsr = q.bs + (size_t)t * bst + b * 16;
+    int mins = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mins += mn[j] * (bsr[2 * j] + bsr[2 * j + 1]);
+    int* r = q.r + ((size_t)rb * kMaxRows + t) * 2;
+    r[0] = dot;
+    r[1] = mins;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const int t = lane & 15;
+#pragma unroll
+  for (int dd = 0; dd < (D + 3) / 4; ++dd) {
+    const int d = (lane >> 4) + 4 * dd;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      float acc = 0.0f;
+      if (t < T && d < D) {
+        for (int b = 0; b < nb; ++b) {
+          const int rb = (m * D + d) * nb + b;
+          const uint8_t* blk = q.w + (size_t)rb * 144;
+          const float dw = half_bits_to_float(*(const uint16_t*)blk);
+          const float dminw = half_bits_to_float(*(const uint16_t*)(blk + 2));
+          const float dxv = q.dx[t * nb + b];
+          const int* r = q.r + ((size_t)rb * kMaxRows + t) * 2;
+          const float dm = __fmul_rn(dw, dxv), dmin = __fmul_rn(dminw, dxv);
+          acc = __fadd_rn(acc, __fmul_rn(dm, (float)r[0]));
+          acc = __fsub_rn(acc, __fmul_rn(dmin, (float)r[1]));
+        }
+      }
+      res[m][dd] = acc;
+    }
+  }
+}
+
+// EPI 0: store, 1: residual add, 2: silu(W x) * (W2 x). Wave w of the grid owns
+// rows w + nwaves * (j*D + d).
+template <int EPI, int D>
+__global__ void __launch_bounds__(256)
+k_gemm_q4k(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
+           int n, int K, ActQ8K a, float* __restrict__ out) {
+  extern __shared__ v4i q4_lds_v4[];
+  constexpr int NM = EPI == 2 ? 2 : 1, DD = (D + 3) / 4;
+  const int T = desc->T, lane = threadIdx.x & 63, nb = K / 256;
+  const int nwaves = gridDim.x * 4;
+  const uint8_t* base[NM];
+  base[0] = w;
+  if (EPI == 2) base[NM - 1] = w2;
+  int row0 = blockIdx.x * 4 + (threadIdx.x >> 6);
+  Q4Batch<NM, D> bt;
+  q4k_load<NM, D>(base, n, nb, row0, nwaves, bt);  // before the staging: in flight meanwhile
+  const Q4Lds q = q4_stage(a, K, T, NM * D, (uint8_t*)q4_lds_v4);
+  for (; row0 < n; row0 += nwaves * D) {
+    const Q4Batch<NM, D> cur = bt;
+    if (row0 + nwaves * D < n) q4k_load<NM, D>(base, n, nb, row0 + nwaves * D, nwaves, bt);
+    float res[NM][DD];
+    q4k_batch<NM, D>(cur, K, T, q, res);
+    const int t = lane & 15;
+#pragma unroll
+    for (int dd = 0; dd < DD; ++dd) {
+      const int d = (lane >> 4) + 4 * dd, row = row0 + d * nwaves;
+      if (t < T && d < D && row < n) {
+        float* dst = out + (size_t)t * n + row;
+        if (EPI == 0) *dst = res[0][dd];
+        else if (EPI == 1) *dst = __fadd_rn(*dst, res[0][dd]);
+        else *dst = dev_swiglu(res[0][dd], res[NM - 1][dd]);
+      }
+    }
+  }
+}
+
+// q4_K lm_head over the rows of the tied embedding, distributed as in k_gemm_q4k;
+// per verify row the best 64-bit key (value bits, lowest index on ties) of each
+// workgroup goes to part_keys.
+__global__ void __launch_bounds__(256)
+k_lm_head_q4k(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int vocab, int K, ActQ8K a,
+              const uint32_t* __restrict__ bitmap, float* __restrict__ logits, uint64_t* __restrict__ part_keys) {
+  extern __shared__ v4i q4_lds_v4[];
+  constexpr int D = kQ4LmD, DD = (D + 3) / 4;
+  const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nb = K / 256;
+  const bool pen = desc->penalty > 1.0f;
+  const float penalty = desc->penalty;
+  const bool write_logits = desc->write_logits != 0;
+  const int words = (vocab + 31) / 32;
+  const int nwaves = gridDim.x * 4, t = lane & 15;
+  const uint8_t* base[1] = {w};
+  int row0 = blockIdx.x * 4 + wave;
+  Q4Batch<1, D> bt;
+  q4k_load<1, D>(base, vocab, nb, row0, nwaves, bt);
+  const Q4Lds q = q4_stage(a, K, T, D, (uint8_t*)q4_lds_v4);
+  uint64_t best = 0;  // lane (d, t): verify row t
+  for (; row0 < vocab; row0 += nwaves * D) {
+    const Q4Batch<1, D> cur = bt;
+    if (row0 + nwaves * D < vocab) q4k_load<1, D>(base, vocab, nb, row0 + nwaves * D, nwaves, bt);
+    float res[1][DD];
+    q4k_batch<1, D>(cur, K, T, q, res);
+#pragma unroll
+    for (int dd = 0; dd < DD; ++dd) {
+      const int d = (lane >> 4) + 4 * dd, row = row0 + d * nwaves;
+      if (t < T && d < D && row < vocab) {
+        float v = res[0][dd];
+        if (write_logits) logits[(size_t)t * vocab + row] = v;
+        if (pen && ((bitmap[(size_t)t * words + (row >> 5)] >> (row & 31)) & 1u))
+          v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+        const uint64_t key = argmax_key(v, row);
+        best = key > best ? key : best;
+      }
+    }
+  }
+  __shared__ uint64_t s_best[4][64];
+  s_best[wave][lane] = best;
+  __syncthreads();
+  if ((int)threadIdx.x < T) {
+    uint64_t b = 0;
+    for (int i = 0; i < 16; ++i) {
+      const uint64_t c = s_best[i >> 2][(i & 3) * 16 + threadIdx.x];
+      b = c > b ? c : b;
+    }
+    part_keys[(size_t)blockIdx.x * kMaxRows + threadIdx.x] = b;
+  }
+}
+
 template <int WT, int EPI>
 void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_t* w2, int n, int k,
              const WtAct& act, float* out) {
@@ -332,6 +588,11 @@ void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_
       hipLaunchKernelGGL((k_gemm_wt<WT, 32, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
     else
       hipLaunchKernelGGL((k_gemm_wt<WT, 48, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
+  } else if (k <= kQ4MaxK) {
+    constexpr int NM = EPI == 2 ? 2 : 1;
+    const int blocks = std::min((n + 4 * kQ4GemmD - 1) / (4 * kQ4GemmD), kLmWorkgroups);
+    hipLaunchKernelGGL((k_gemm_q4k<EPI, kQ4GemmD>), dim3(blocks), block, q4_lds_bytes(k, NM * kQ4GemmD), s, desc,
+                       w, w2, n, k, act.q8k, out);
   } else {
     hipLaunchKernelGGL((k_gemm_wt<WT, 0, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
   }
@@ -340,6 +601,18 @@ void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_
 }  // namespace
 
 // ================================================================ launches ==
+hipError_t prepare_kernels_wt() {
+  const void* fns[4] = {(const void*)k_gemm_q4k<0, kQ4GemmD>, (const void*)k_gemm_q4k<1, kQ4GemmD>,
+                        (const void*)k_gemm_q4k<2, kQ4GemmD>, (const void*)k_lm_head_q4k};
+  const int rows[4] = {kQ4GemmD, kQ4GemmD, 2 * kQ4GemmD, kQ4LmD};
+  for (int i = 0; i < 4; ++i) {
+    const hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)q4_lds_bytes(kQ4MaxK, rows[i]));
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 bool wt_shape_supported(int wtype, int k) {
   if (wtype == MTG_TYPE_F16) return k == 1024 || k == 2048 || k == 3072;
   if (wtype == MTG_TYPE_Q4_K) return k % 256 == 0;
@@ -373,6 +646,9 @@ void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uin
   if (wtype == MTG_TYPE_F16)
     hipLaunchKernelGGL((k_lm_head_wt<MTG_TYPE_F16, 16>), grid, block, 0, s, desc, w, vocab, k, act.f16v,
                        act.q8k, bitmap, logits, part_keys);
+  else if (k <= kQ4MaxK)
+    hipLaunchKernelGGL(k_lm_head_q4k, grid, block, q4_lds_bytes(k, kQ4LmD), s, desc, w, vocab, k, act.q8k, bitmap,
+                       logits, part_keys);
   else
     hipLaunchKernelGGL((k_lm_head_wt<MTG_TYPE_Q4_K, 0>), grid, block, 0, s, desc, w, vocab, k, act.f16v,
                        act.q8k, bitmap, logits, part_keys);

@@ -224,6 +224,7 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
       !panel_f.codes || !panel_f.scales || !work.part_ml || !work.part_o || !desc_dev || !result_dev)
     return fail(MTG_ERR_NOMEM, "step buffers");
   if ((rc = check(prepare_kernels(), "kernel attributes"))) return rc;
+  if ((rc = check(prepare_kernels_wt(), "kernel attributes"))) return rc;
   if ((rc = init_step_kernel())) return rc;
   return check(hipDeviceSynchronize(), "init");
 }
