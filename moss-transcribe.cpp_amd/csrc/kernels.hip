@@ -15,6 +15,8 @@
 //                                                             src/qwen3_decoder.cpp:174-205,
 //                                                             src/cpu_speculative.cpp:39-50,124-130
 #include <hip/hip_fp16.h>
+#include <algorithm>
+
 #include <hip/hip_runtime.h>
 
 #include "device_common.hpp"
@@ -339,6 +341,213 @@ k_attn_chunk(const StepDesc* __restrict__ desc, const float* __restrict__ q, int
   }
 }
 
+// ------------------------------------------------ attention, f16 cache ----
+// The same chunk arithmetic for an f16 cache, laid out for two workgroups per CU
+// and back-to-back MFMA chains. A workgroup keeps its q columns in registers and
+// walks the chunks blockIdx.y, blockIdx.y + gridDim.y, ..., the next chunk's K / V
+// rows in flight in registers while the current one computes. K / V sit in LDS
+// as f16: K rows permuted as above (element 4 i + kk at kk * 32 + i), V rows 65
+// words apart. In P.V lane (kl, kk) owns head_dim elements 8 kl + 2 wave + {0, 1},
+// read as one 32-bit word per MFMA pair; the 4 lanes kk of a key group and the
+// 16 lanes kl then hit 64 different banks.
+constexpr int kAkStrideH = 136;  // halves per permuted K row
+constexpr int kAvStrideW = 65;   // 32-bit words per V row
+constexpr size_t kAttnF16Lds =
+    (size_t)kMaxCols * kAqStride * 4 + (size_t)kChunk * kAkStrideH * 2 + (size_t)kChunk * kAvStrideW * 4;
+constexpr int kAttnF16Waves = 2 * 256;  // resident workgroups targeted by the grid (2 per CU)
+
+__device__ __forceinline__ float h_lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)w); }
+__device__ __forceinline__ float h_hi(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// K / V rows of the chunk at key0: thread piece p = i * 256 + tid is key p / 16,
+// halves 8 (p % 16) .. + 7; zeros past kvlen.
+__device__ __forceinline__ void attn_f16_load(const uint16_t* kb, const uint16_t* vb, int key0, int kvlen,
+                                              v4i (&pk)[4], v4i (&pv)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = i * 256 + (int)threadIdx.x, key = key0 + (p >> 4), d8 = (p & 15) * 8;
+    if (key < kvlen) {
+      pk[i] = *(const v4i*)(kb + (size_t)key * kHeadDim + d8);
+      pv[i] = *(const v4i*)(vb + (size_t)key * kHeadDim + d8);
+    } else {
+      pk[i] = (v4i){0, 0, 0, 0};
+      pv[i] = (v4i){0, 0, 0, 0};
+    }
+  }
+}
+
+template <int NCT>
+__device__ __forceinline__ void attn_f16_scores(const uint16_t* s_k, const float (&qreg)[2][32], float* s_p,
+                                                int key0, int kvlen, int past, int T, int ncol, float scale) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kl = lane & 15, kk = lane >> 4;
+  const uint16_t* krow = s_k + (16 * wave + kl) * kAkStrideH + kk * 32;
+  v4f acc[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) acc[ct] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const v4i kw = *(const v4i*)(krow + 8 * m);
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {  // head_dim elements 4 (8 m + h) + kk, in order
+      const uint32_t word = (uint32_t)kw[h >> 1];
+      const float kv = (h & 1) ? h_hi(word) : h_lo(word);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv, qreg[ct][8 * m + h], acc[ct], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int colb = ct * 16 + kl;
+    if (colb < ncol) {
+      const int t = colb % T;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {  // key 16 wave + 4 kk + r sits at r * 16 + 4 wave + kk
+        const int key = key0 + 16 * wave + 4 * kk + r;
+        s_p[colb * kApStride + r * 16 + 4 * wave + kk] =
+            (key < kvlen && key <= past + t) ? __fmul_rn(acc[ct][r], scale) : -INFINITY;
+      }
+    }
+  }
+}
+
+template <int NCT>
+__device__ __forceinline__ void attn_f16_pv(const uint32_t* s_v, const float* s_p, int ncol, float* out_o) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kl = lane & 15, kk = lane >> 4;
+  float pa[NCT][16];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int cola = ct * 16 + kl;
+    const float* prow = s_p + min(cola, ncol - 1) * kApStride + kk * 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const v4f p4 = *(const v4f*)(prow + 4 * i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pa[ct][4 * i + j] = cola < ncol ? p4[j] : 0.0f;
+    }
+  }
+  v4f acc[NCT][2];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) acc[ct][0] = acc[ct][1] = (v4f){0.f, 0.f, 0.f, 0.f};
+  const uint32_t* vcol = s_v + kk * kAvStrideW + 4 * kl + wave;
+#pragma unroll
+  for (int s2 = 0; s2 < 16; ++s2) {  // keys 4 s2 + kk, in order
+    const uint32_t word = vcol[4 * s2 * kAvStrideW];
+    const float v0 = h_lo(word), v1 = h_hi(word);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      acc[ct][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[ct][s2], v0, acc[ct][0], 0, 0, 0);
+      acc[ct][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[ct][s2], v1, acc[ct][1], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int col = ct * 16 + 4 * kk + r;
+      if (col < ncol) *(float2*)(out_o + col * kHeadDim + 8 * kl + 2 * wave) = make_float2(acc[ct][0][r], acc[ct][1][r]);
+    }
+}
+
+__global__ void __launch_bounds__(256, 2)
+k_attn_f16(const StepDesc* __restrict__ desc, const float* __restrict__ q, int n_heads, KvLayer kv,
+           AttnWork work, int max_chunks) {
+  const int g = blockIdx.x;
+  const int T = desc->T, past = desc->past, kvlen = past + T;
+  const int nch = (kvlen + kChunk - 1) / kChunk;
+  int chunk = blockIdx.y;
+  if (chunk >= nch) return;
+  extern __shared__ v4f attn_lds_v4[];
+  float* s_q = (float*)attn_lds_v4;  // [32][132] permuted; then the chunk's scores / probabilities
+  float* s_p = s_q;
+  uint16_t* s_k = (uint16_t*)(s_q + kMaxCols * kAqStride);  // [64][136] permuted
+  uint32_t* s_v = (uint32_t*)(s_k + kChunk * kAkStrideH);   // [64][65] words
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, kl = lane & 15, kk = lane >> 4;
+  const int ncol = 2 * T;
+  const uint16_t* kb = (const uint16_t*)kv.k + (size_t)g * kv.max_seq * kHeadDim;
+  const uint16_t* vb = (const uint16_t*)kv.v + (size_t)g * kv.max_seq * kHeadDim;
+  v4i pk[4], pv[4];
+  attn_f16_load(kb, vb, chunk * kChunk, kvlen, pk, pv);
+  // q columns, f16-rounded (mul_mat(f16 K, f32 q) converts q), into registers:
+  // lane (kl, kk) of column tile ct holds column 16 ct + kl, elements 4 i + kk
+  for (int idx = tid; idx < ncol * (kHeadDim / 4); idx += 256) {
+    const int col = idx / (kHeadDim / 4), d = (idx % (kHeadDim / 4)) * 4, hl = col / T, t = col % T;
+    const v4f v = *(const v4f*)(q + ((size_t)t * n_heads + 2 * g + hl) * kHeadDim + d);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_q[col * kAqStride + attn_perm128(d + e)] = f16_round(v[e]);
+  }
+  __syncthreads();
+  float qreg[2][32];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    const int col = ct * 16 + kl;
+    const float* qrow = s_q + min(col, ncol - 1) * kAqStride + kk * 32;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const v4f q4 = *(const v4f*)(qrow + 4 * i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qreg[ct][4 * i + j] = col < ncol ? q4[j] : 0.0f;
+    }
+  }
+  __syncthreads();  // s_q is s_p from here on
+  const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)kHeadDim));
+  const int sp_pos = (lane & 3) * 16 + (lane >> 2);
+  for (; chunk < nch; chunk += gridDim.y) {
+    const int key0 = chunk * kChunk;
+    // 1. the chunk's rows to LDS; the next chunk's loads go out
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = i * 256 + tid, j = p >> 4, d8 = (p & 15) * 8;
+      const uint32_t w0 = (uint32_t)pk[i][0], w1 = (uint32_t)pk[i][1], w2 = (uint32_t)pk[i][2],
+                     w3 = (uint32_t)pk[i][3];
+      // halves d8 + e and d8 + e + 4 are elements 4 (d8/4) + e and 4 (d8/4 + 1) + e
+      uint32_t* kr = (uint32_t*)(s_k + j * kAkStrideH + d8 / 4);
+      kr[0] = (w0 & 0xffffu) | (w2 << 16);
+      kr[16] = (w0 >> 16) | (w2 & 0xffff0000u);
+      kr[32] = (w1 & 0xffffu) | (w3 << 16);
+      kr[48] = (w1 >> 16) | (w3 & 0xffff0000u);
+      uint32_t* vr = s_v + j * kAvStrideW + d8 / 2;
+      vr[0] = (uint32_t)pv[i][0];
+      vr[1] = (uint32_t)pv[i][1];
+      vr[2] = (uint32_t)pv[i][2];
+      vr[3] = (uint32_t)pv[i][3];
+    }
+    if (chunk + (int)gridDim.y < nch) attn_f16_load(kb, vb, (chunk + gridDim.y) * kChunk, kvlen, pk, pv);
+    __syncthreads();
+    // 2. scores
+    if (ncol > 16)
+      attn_f16_scores<2>(s_k, qreg, s_p, key0, kvlen, past, T, ncol, scale);
+    else
+      attn_f16_scores<1>(s_k, qreg, s_p, key0, kvlen, past, T, ncol, scale);
+    __syncthreads();
+    // 3. chunk softmax per column (one wave per column, lane = key)
+    const size_t item = (size_t)g * max_chunks + chunk;
+    float* out_ml = work.part_ml + item * kMaxCols * 2;
+    float* out_o = work.part_o + item * kMaxCols * kHeadDim;
+    for (int col = wave; col < ncol; col += 4) {
+      const float w = s_p[col * kApStride + sp_pos];
+      const float m = wave_max_f(w);
+      float p = (m == -INFINITY || w == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(w, m));
+      p = f16_round(p);
+      const float l = wave_sum_f(p);
+      s_p[col * kApStride + sp_pos] = p;
+      if (lane == 0) {
+        out_ml[col * 2] = m;
+        out_ml[col * 2 + 1] = l;
+      }
+    }
+    __syncthreads();
+    // 4. O = fma chain over the chunk's keys of p * v
+    if (ncol > 16)
+      attn_f16_pv<2>(s_v, s_p, ncol, out_o);
+    else
+      attn_f16_pv<1>(s_v, s_p, ncol, out_o);
+    __syncthreads();  // s_k / s_v / s_p are rewritten by the next chunk
+  }
+}
+
 // grid (n_heads, 16 rows), 128 threads: merge the chunks of one (head, row),
 // write o (f32) and its q8_0 panel for the o-projection.
 __global__ void __launch_bounds__(128)
@@ -586,14 +795,24 @@ void launch_qk_rope_append(hipStream_t s, const StepDesc* desc, const float* qkv
 }
 
 hipError_t prepare_kernels() {
-  return hipFuncSetAttribute((const void*)k_attn_chunk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnLds);
+  const hipError_t e =
+      hipFuncSetAttribute((const void*)k_attn_chunk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnLds);
+  if (e != hipSuccess) return e;
+  return hipFuncSetAttribute((const void*)k_attn_f16, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)kAttnF16Lds);
 }
 
 void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n_heads,
                       int n_kv_heads, KvLayer kv, AttnWork work, Panel o_panel, float* o_out) {
   const int max_chunks = (kv.max_seq + kChunk - 1) / kChunk;
-  hipLaunchKernelGGL(k_attn_chunk, dim3(n_kv_heads, max_chunks), dim3(256), kAttnLds, s, desc, q, n_heads,
-                     kv, work, max_chunks);
+  if (kv.f16) {
+    const int ny = std::max(1, std::min(max_chunks, kAttnF16Waves / n_kv_heads));
+    hipLaunchKernelGGL(k_attn_f16, dim3(n_kv_heads, ny), dim3(256), kAttnF16Lds, s, desc, q, n_heads, kv, work,
+                       max_chunks);
+  } else {
+    hipLaunchKernelGGL(k_attn_chunk, dim3(n_kv_heads, max_chunks), dim3(256), kAttnLds, s, desc, q, n_heads,
+                       kv, work, max_chunks);
+  }
   hipLaunchKernelGGL(k_attn_combine, dim3(n_heads, kMaxRows), dim3(kHeadDim), 0, s, desc, work,
                      n_heads, max_chunks, o_panel, o_out);
 }

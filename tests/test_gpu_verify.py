@@ -196,6 +196,35 @@ def test_f16_and_q4k_weights_verify_matches_oracle(wtype, exec_mode):
     _close(v1, v0, "V cache")
 
 
+@pytest.mark.parametrize("exec_mode", WT_EXECS, ids=lambda e: EXEC_NAMES[e])
+@pytest.mark.parametrize("wtype", WTYPES, ids=lambda w: WT_NAMES[w])
+def test_long_f16_context_matches_oracle(wtype, exec_mode):
+    """A context of 8300 cached positions (130 chunks of 64 keys, more than the
+    chunk attention's workgroups per kv head, so each walks several chunks with
+    the next one's rows in flight): hidden rows and logits equal the oracle's for
+    T = 16, 5 and 12 (query columns that fill two, one and one and a half tiles)."""
+    print("long f16 context %s: exec=%s" % (WT_NAMES[wtype], EXEC_NAMES[exec_mode]), flush=True)
+    model = mtg.SynthModel(wtype, seed=11, std=0.02, gain_jitter=0.05, n_layers=1, vocab=4096)
+    hp = model.hp
+    prefix, max_seq = 8300, 8400
+    orc = oracle_py.Oracle(model, max_seq, mtg.TYPE_F16)
+    dec = mtg.Decoder(model, max_seq, mtg.TYPE_F16)
+    dec.set_exec(exec_mode)
+    rng = np.random.default_rng(12)
+    shape = (1, hp.n_kv_heads, prefix, hp.head_dim)
+    k = rng.normal(0.0, 1.0, shape).astype(np.float16)
+    v = rng.normal(0.0, 0.5, shape).astype(np.float16)
+    orc.kv_write(k, v)
+    dec.kv_write(k, v)
+    for T in (16, 5, 12):
+        tokens = rng.integers(0, hp.vocab, T)
+        c0, m0, h0, l0 = orc.verify(tokens, want_hidden=True, want_logits=True)
+        c1, m1, h1, l1 = dec.verify(tokens, want_hidden=True, want_logits=True)
+        _close(h1, h0, "hidden T=%d" % T)
+        _close(l1, l0, "logits T=%d" % T)
+        assert np.array_equal(c1, c0) and m1 == m0
+
+
 @pytest.mark.parametrize("wtype", WTYPES, ids=lambda w: WT_NAMES[w])
 def test_f16_and_q4k_weights_penalty_prefill_and_stream(wtype):
     """The same weight types through the GPU prefill, the repetition penalty and
