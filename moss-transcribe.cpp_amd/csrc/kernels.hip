@@ -802,9 +802,11 @@ hipError_t prepare_kernels() {
                              (int)kAttnF16Lds);
 }
 
-void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n_heads,
-                      int n_kv_heads, KvLayer kv, AttnWork work, Panel o_panel, float* o_out) {
-  const int max_chunks = (kv.max_seq + kChunk - 1) / kChunk;
+int attn_max_chunks(const KvLayer& kv) { return (kv.max_seq + kChunk - 1) / kChunk; }
+
+void launch_attn_chunks(hipStream_t s, const StepDesc* desc, const float* q, int n_heads, int n_kv_heads,
+                        KvLayer kv, AttnWork work) {
+  const int max_chunks = attn_max_chunks(kv);
   if (kv.f16) {
     const int ny = std::max(1, std::min(max_chunks, kAttnF16Waves / n_kv_heads));
     hipLaunchKernelGGL(k_attn_f16, dim3(n_kv_heads, ny), dim3(256), kAttnF16Lds, s, desc, q, n_heads, kv, work,
@@ -813,6 +815,12 @@ void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n
     hipLaunchKernelGGL(k_attn_chunk, dim3(n_kv_heads, max_chunks), dim3(256), kAttnLds, s, desc, q, n_heads,
                        kv, work, max_chunks);
   }
+}
+
+void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n_heads,
+                      int n_kv_heads, KvLayer kv, AttnWork work, Panel o_panel, float* o_out) {
+  const int max_chunks = attn_max_chunks(kv);
+  launch_attn_chunks(s, desc, q, n_heads, n_kv_heads, kv, work);
   hipLaunchKernelGGL(k_attn_combine, dim3(n_heads, kMaxRows), dim3(kHeadDim), 0, s, desc, work,
                      n_heads, max_chunks, o_panel, o_out);
 }

@@ -65,6 +65,11 @@ hipError_t prepare_kernels();
 hipError_t prepare_kernels_wt();  // the same for the f16 / q4_K weight kernels
 void launch_attention(hipStream_t s, const StepDesc* desc, const float* q, int n_heads,
                       int n_kv_heads, KvLayer kv, AttnWork work, Panel o_panel, float* o_out);
+// The chunk half of launch_attention: (m, l, o) partials of every (kv head, chunk)
+// into work; attn_max_chunks is the chunk capacity of the cache (work's stride).
+void launch_attn_chunks(hipStream_t s, const StepDesc* desc, const float* q, int n_heads, int n_kv_heads,
+                        KvLayer kv, AttnWork work);
+int attn_max_chunks(const KvLayer& kv);
 void launch_penalty_bitmap(hipStream_t s, const StepDesc* desc, int vocab, uint32_t* bitmap);
 void launch_lm_head(hipStream_t s, int G, const StepDesc* desc, const uint8_t* w, int vocab, int k,
                     Panel x, const uint32_t* bitmap, float* logits, uint64_t* part_keys);
@@ -81,6 +86,10 @@ bool wt_shape_supported(int wtype, int k);
 // src as is); normed_out (nullable) receives the f32 normalized rows.
 void launch_act_wt(hipStream_t s, int wtype, const StepDesc* desc, const float* src, int K,
                    const float* gain, float eps, const WtAct& act, float* normed_out);
+// The merge half of the attention for f16 / q4_K weights: the attention output
+// rows go straight to the o-projection's vec_dot_type in act.
+void launch_attn_combine_wt(hipStream_t s, int wtype, const StepDesc* desc, AttnWork work, int n_heads,
+                            int max_chunks, const WtAct& act);
 // epi 0: out = W act, 1: out += W act, 2: out = silu(W act) * (W2 act)
 void launch_gemm_wt(hipStream_t s, int wtype, int epi, const StepDesc* desc, const uint8_t* w,
                     const uint8_t* w2, int n, int k, const WtAct& act, float* out);

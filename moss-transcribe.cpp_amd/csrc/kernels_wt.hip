@@ -51,87 +51,147 @@ __device__ __forceinline__ float row_rms_scale(const float* xr, int K, float eps
 }
 
 // ------------------------------------------------------- activations ------
-// One workgroup (256 threads) per verify row. gain == nullptr: no norm (the
-// attention output and the SwiGLU product go in as they are).
+// Grid (16 rows, K / 256), 256 threads: one element per thread. gain == nullptr:
+// no norm (the SwiGLU product goes in as it is); otherwise every workgroup of a
+// row recomputes the row's RMS scale (same order, same value).
 __global__ void __launch_bounds__(256)
 k_act_f16(const StepDesc* __restrict__ desc, const float* __restrict__ src, int K,
           const float* __restrict__ gain, float eps, float* __restrict__ out,
           float* __restrict__ normed_out) {
-  const int t = blockIdx.x;
+  const int t = blockIdx.x, k = blockIdx.y * 256 + threadIdx.x;
   if (t >= desc->T) return;
   const float* xr = src + (size_t)t * K;
   __shared__ float s_scale;
-  float scale = 1.0f;
+  float y = xr[k];
   if (gain) {
     if (threadIdx.x < 64) {
       const float sc = row_rms_scale(xr, K, eps);
       if (threadIdx.x == 0) s_scale = sc;
     }
     __syncthreads();
-    scale = s_scale;
+    y = __fmul_rn(__fmul_rn(y, s_scale), gain[k]);
   }
-  for (int k = threadIdx.x; k < K; k += 256) {
-    float y = xr[k];
-    if (gain) y = __fmul_rn(__fmul_rn(y, scale), gain[k]);
-    if (normed_out) normed_out[(size_t)t * K + k] = y;
-    out[(size_t)t * K + k] = f16_round(y);  // vec_dot_type F16
-  }
+  if (normed_out) normed_out[(size_t)t * K + k] = y;
+  out[(size_t)t * K + k] = f16_round(y);  // vec_dot_type F16
 }
 
-// ggml quantize_row_q8_K_ref per 256-block: the element of largest magnitude
-// (the first one on ties) gives max with its sign, iscale = -127/max, codes =
-// min(127, nearest(iscale*x)), d = 1/iscale, bsums over 16-element groups.
+// ggml quantize_row_q8_K_ref of one 256-block held one element per thread of a
+// 256-thread workgroup: the element of largest magnitude (the first one on ties)
+// gives max with its sign, iscale = -127/max, codes = min(127, nearest(iscale*x)),
+// d = 1/iscale, bsums over 16-element groups.
+__device__ __forceinline__ void q8k_block256(float y, const ActQ8K& a, int t, int K, int b) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __shared__ float s_y[256];
+  __shared__ uint64_t s_key[4];
+  s_y[tid] = y;
+  // first maximum of |y|: larger magnitude, then lower index
+  const uint64_t key = ((uint64_t)__float_as_uint(fabsf(y)) << 32) | (uint32_t)(255 - tid);
+  const uint64_t wk = wave_max_u64(key);
+  if (lane == 0) s_key[wave] = wk;
+  __syncthreads();
+  uint64_t best = s_key[0];
+  for (int w = 1; w < 4; ++w) best = s_key[w] > best ? s_key[w] : best;
+  const float maxv = s_y[255 - (int)(best & 0xffffffffu)];
+  int q = 0;
+  float d = 0.0f;
+  if ((best >> 32) != 0) {  // amax > 0
+    const float iscale = __fdiv_rn(-127.0f, maxv);
+    q = min(127, (int)rintf(__fmul_rn(iscale, y)));
+    d = __fdiv_rn(1.0f, iscale);
+  }
+  a.qs[(size_t)t * K + b * 256 + tid] = (int8_t)q;
+  // bsums: the 16 lanes of a DPP row hold one group
+  int s = q;
+  s += (int)dpp_u<kDppRor8>((uint32_t)s);
+  s += (int)dpp_u<kDppRor4>((uint32_t)s);
+  s += (int)dpp_u<kDppRor2>((uint32_t)s);
+  s += (int)dpp_u<kDppRor1>((uint32_t)s);
+  if ((tid & 15) == 0) a.bsums[(size_t)t * (K / 16) + b * 16 + (tid >> 4)] = s;
+  if (tid == 0) a.d[(size_t)t * (K / 256) + b] = d;
+}
+
+// Grid (16 rows, K / 256), 256 threads: block blockIdx.y of row blockIdx.x.
 __global__ void __launch_bounds__(256)
 k_act_q8k(const StepDesc* __restrict__ desc, const float* __restrict__ src, int K,
           const float* __restrict__ gain, float eps, ActQ8K a, float* __restrict__ normed_out) {
-  const int t = blockIdx.x;
+  const int t = blockIdx.x, b = blockIdx.y, k = b * 256 + threadIdx.x;
   if (t >= desc->T) return;
   const float* xr = src + (size_t)t * K;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   __shared__ float s_scale;
-  __shared__ float s_y[256];
-  __shared__ uint64_t s_key[4];
-  float scale = 1.0f;
+  float y = xr[k];
   if (gain) {
-    if (tid < 64) {
+    if (threadIdx.x < 64) {
       const float sc = row_rms_scale(xr, K, eps);
-      if (tid == 0) s_scale = sc;
+      if (threadIdx.x == 0) s_scale = sc;
     }
     __syncthreads();
-    scale = s_scale;
+    y = __fmul_rn(__fmul_rn(y, s_scale), gain[k]);
   }
-  for (int b = 0; b < K / 256; ++b) {
-    const int k = b * 256 + tid;
-    float y = xr[k];
-    if (gain) y = __fmul_rn(__fmul_rn(y, scale), gain[k]);
-    if (normed_out) normed_out[(size_t)t * K + k] = y;
-    s_y[tid] = y;
-    // first maximum of |y|: larger magnitude, then lower index
-    const uint64_t key = ((uint64_t)__float_as_uint(fabsf(y)) << 32) | (uint32_t)(255 - tid);
-    const uint64_t wk = wave_max_u64(key);
-    if (lane == 0) s_key[wave] = wk;
-    __syncthreads();
-    uint64_t best = s_key[0];
-    for (int w = 1; w < 4; ++w) best = s_key[w] > best ? s_key[w] : best;
-    const float maxv = s_y[255 - (int)(best & 0xffffffffu)];
-    int q = 0;
-    float d = 0.0f;
-    if ((best >> 32) != 0) {  // amax > 0
-      const float iscale = __fdiv_rn(-127.0f, maxv);
-      q = min(127, (int)rintf(__fmul_rn(iscale, y)));
-      d = __fdiv_rn(1.0f, iscale);
+  if (normed_out) normed_out[(size_t)t * K + k] = y;
+  q8k_block256(y, a, t, K, b);
+}
+
+// ------------------------------------------------- attention merge + act ---
+// The chunk merge of the attention output (attn_merge's arithmetic: M = max of
+// the chunk maxima, then the chunk-ordered chains L = fma(l_c, f_c, L) and
+// O = fma(o_c, f_c, O), f_c = exp(m_c - M), out = O / L) with the loads of 64
+// chunks in flight per thread, fused with the conversion of the row to the
+// o-projection's vec_dot_type. Grid (n_heads / 2, 16 rows), 256 threads: thread
+// (hl, d) = (tid / 128, tid % 128) takes head 2 blockIdx.x + hl, so one
+// workgroup holds one q8_K block (256 elements) of the row.
+__device__ __forceinline__ float attn_merge64(const float* part_ml, const float* part_o, int nch,
+                                              size_t stride_ml, size_t stride_o, int d) {
+  const int lane = threadIdx.x & 63;
+  float M = -INFINITY;
+  for (int c0 = 0; c0 < nch; c0 += 256) {
+    float m[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = c0 + 64 * r + lane;
+      m[r] = c < nch ? part_ml[(size_t)c * stride_ml] : -INFINITY;
     }
-    a.qs[(size_t)t * K + k] = (int8_t)q;
-    // bsums: the 16 lanes of a DPP row hold one group
-    int s = q;
-    s += (int)dpp_u<kDppRor8>((uint32_t)s);
-    s += (int)dpp_u<kDppRor4>((uint32_t)s);
-    s += (int)dpp_u<kDppRor2>((uint32_t)s);
-    s += (int)dpp_u<kDppRor1>((uint32_t)s);
-    if ((tid & 15) == 0) a.bsums[(size_t)t * (K / 16) + b * 16 + (tid >> 4)] = s;
-    if (tid == 0) a.d[(size_t)t * (K / 256) + b] = d;
-    __syncthreads();  // s_y / s_key are reused by the next block
+    M = fmaxf(M, wave_max_f(fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]))));
   }
+  float L = 0.0f, O = 0.0f;
+  for (int c0 = 0; c0 < nch; c0 += 64) {
+    const int c = c0 + lane, nb = min(64, nch - c0);
+    const float m = c < nch ? part_ml[(size_t)c * stride_ml] : -INFINITY;
+    const float l = c < nch ? part_ml[(size_t)c * stride_ml + 1] : 0.0f;
+    float o[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) o[i] = i < nb ? part_o[(size_t)(c0 + i) * stride_o + d] : 0.0f;
+    const float f = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, M));
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const float mc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), i));
+      if (i < nb && mc != -INFINITY) {
+        const float fc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), i));
+        const float lc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), i));
+        L = fmaf(lc, fc, L);
+        O = fmaf(o[i], fc, O);
+      }
+    }
+  }
+  return __fdiv_rn(O, L);
+}
+
+template <int WT>
+__global__ void __launch_bounds__(256)
+k_attn_combine_wt(const StepDesc* __restrict__ desc, AttnWork work, int n_heads, int max_chunks, WtAct act) {
+  const int g = blockIdx.x, t = blockIdx.y, hl = threadIdx.x >> 7, d = threadIdx.x & 127;
+  const int T = desc->T;
+  if (t >= T) return;
+  const int col = hl * T + t;  // q head 2 g + hl shares kv head g
+  const int nch = (desc->past + T + kChunk - 1) / kChunk;
+  const size_t item0 = (size_t)g * max_chunks;
+  const float val = attn_merge64(work.part_ml + item0 * kMaxCols * 2 + col * 2,
+                                 work.part_o + item0 * kMaxCols * kHeadDim + col * kHeadDim, nch,
+                                 (size_t)kMaxCols * 2, (size_t)kMaxCols * kHeadDim, d);
+  const int QN = n_heads * kHeadDim;
+  if constexpr (WT == MTG_TYPE_F16)
+    act.f16v[(size_t)t * QN + g * 256 + threadIdx.x] = f16_round(val);
+  else
+    q8k_block256(val, act.q8k, t, QN, g);
 }
 
 // ------------------------------------------------------------ row dots ----
@@ -621,10 +681,22 @@ bool wt_shape_supported(int wtype, int k) {
 
 void launch_act_wt(hipStream_t s, int wtype, const StepDesc* desc, const float* src, int K,
                    const float* gain, float eps, const WtAct& act, float* normed_out) {
+  const dim3 grid(kMaxRows, K / 256);
   if (wtype == MTG_TYPE_F16)
-    hipLaunchKernelGGL(k_act_f16, dim3(kMaxRows), dim3(256), 0, s, desc, src, K, gain, eps, act.f16v, normed_out);
+    hipLaunchKernelGGL(k_act_f16, grid, dim3(256), 0, s, desc, src, K, gain, eps, act.f16v, normed_out);
   else
-    hipLaunchKernelGGL(k_act_q8k, dim3(kMaxRows), dim3(256), 0, s, desc, src, K, gain, eps, act.q8k, normed_out);
+    hipLaunchKernelGGL(k_act_q8k, grid, dim3(256), 0, s, desc, src, K, gain, eps, act.q8k, normed_out);
+}
+
+void launch_attn_combine_wt(hipStream_t s, int wtype, const StepDesc* desc, AttnWork work, int n_heads,
+                            int max_chunks, const WtAct& act) {
+  const dim3 grid(n_heads / 2, kMaxRows);
+  if (wtype == MTG_TYPE_F16)
+    hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_F16>, grid, dim3(256), 0, s, desc, work, n_heads, max_chunks,
+                       act);
+  else
+    hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_Q4_K>, grid, dim3(256), 0, s, desc, work, n_heads, max_chunks,
+                       act);
 }
 
 void launch_gemm_wt(hipStream_t s, int wtype, int epi, const StepDesc* desc, const uint8_t* w,

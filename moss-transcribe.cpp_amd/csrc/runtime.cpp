@@ -368,8 +368,8 @@ void Ctx::enqueue_wt(int mode) {
       launch_act_wt(s, wtype, desc_dev, x, H, y.attn_norm, eps, wact, nullptr);
       launch_gemm_wt(s, wtype, 0, desc_dev, y.wqkv, nullptr, QN + 2 * KN, H, wact, qkv);
       launch_qk_rope_append(s, desc_dev, qkv, NH, NKV, y.q_norm, y.k_norm, eps, rope, qbuf, kv);
-      launch_attention(s, desc_dev, qbuf, NH, NKV, kv, work, panel_o, obuf);
-      launch_act_wt(s, wtype, desc_dev, obuf, QN, nullptr, eps, wact, nullptr);
+      launch_attn_chunks(s, desc_dev, qbuf, NH, NKV, kv, work);
+      launch_attn_combine_wt(s, wtype, desc_dev, work, NH, attn_max_chunks(kv), wact);
       launch_gemm_wt(s, wtype, 1, desc_dev, y.wo, nullptr, H, QN, wact, x);
       launch_act_wt(s, wtype, desc_dev, x, H, y.ffn_norm, eps, wact, nullptr);
       launch_gemm_wt(s, wtype, 2, desc_dev, y.wg, y.wu, F, H, wact, act);
