@@ -1,6 +1,6 @@
 // step_kernel.hip - the Qwen3-0.6B verify step as one persistent dataflow kernel (gfx950).
 //
-// One 256-thread workgroup per CU (cooperative launch of exactly 256 workgroups).
+// One 256-thread workgroup per CU (exactly 256 workgroups, all resident together).
 // Every workgroup owns fixed roles per layer:
 //   QKV   tile w of the fused q|k|v matrix (256 tiles of 16 rows, K = 1024)
 //   ATTN  items (kv head, 64-key chunk), numbered head-major; item i runs on
@@ -1479,7 +1479,13 @@ hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, co
   // desc: host memory; the launch copies it into the kernel arguments
   void* args[] = {(void*)&P, (void*)desc, (void*)&epoch, (void*)&mode};
   const size_t lds = step_lds_bytes(G);
-  return hipLaunchCooperativeKernel(step_fn(G, kv_f16, profiled), dim3(kNwg), dim3(kT), args, lds, s);
+  // A plain launch: one workgroup per CU (the kernel's registers and LDS allow
+  // no second), so on an idle device the whole grid is resident at once. The
+  // cooperative launch guarantees that too, at 15 us more per step. Every wait
+  // in the kernel is bounded: if another kernel holds CUs, the late workgroups
+  // join when it ends, and a wait that outlasts its bound ends the step with an
+  // error instead of a hang.
+  return hipLaunchKernel(step_fn(G, kv_f16, profiled), dim3(kNwg), dim3(kT), args, lds, s);
 }
 
 }  // namespace mtg
