@@ -48,6 +48,7 @@ constexpr int cGuBlocks = cF / 32;       // 96 (gate/up 32-row blocks, on workgr
 constexpr int kMergeWg0 = 160;           // merge items on workgroups 160..255
 constexpr int cQStride = 132;            // LDS row strides (conflict-free MFMA operand reads)
 constexpr int cPStride = 68;
+constexpr int kStageFloats = cH + cH / 4;  // one padded row image per wave (panel_norm)
 
 enum { kPhQkv = 0, kPhAttn = 1, kPhMerge = 2, kPhO = 3, kPhGu = 4, kPhD = 5, kPhases = 6 };
 
@@ -432,24 +433,29 @@ __device__ __forceinline__ void gain16_load(const float* __restrict__ gain, floa
   }
 }
 
+// COAL: the rows come with coalesced loads (lane l: 16 bytes at 16 l + 1024 i)
+// and reach their lanes through this wave's LDS row image (element e at
+// e + 4 (e / 16): the 16-byte reads of 16 consecutive elements per lane are free
+// of bank conflicts; LDS accesses of one wave execute in order, no barrier).
+// Otherwise each lane loads its own 64 bytes (every load instruction then
+// touches all 32 lines of a row, ~20 % slower in a 256-workgroup broadcast, but
+// no LDS image and fewer registers: the 16-row variant keeps that form).
+template <bool COAL>
 __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv)[16], float eps, uint8_t* pcodes,
-                                           float* pscales, float* normed_out, const StepParams* prof = nullptr) {
+                                           float* pscales, float* normed_out, float* stage,
+                                           const StepParams* prof = nullptr) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  float* stg = stage + wave * kStageFloats;
   for (int t0 = wave; t0 < T; t0 += 8) {
-    // two rows per pass: all loads issued before any arithmetic
-    float v[2][16];
+    // two rows per pass, all loads issued before any arithmetic
+    v4f raw[2][4];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int t = t0 + 4 * j;
       if (t < T) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const v4f q = ldc4(x, (uint32_t)((t * cH + 16 * lane + 4 * i) * 4));
-          v[j][4 * i] = q[0];
-          v[j][4 * i + 1] = q[1];
-          v[j][4 * i + 2] = q[2];
-          v[j][4 * i + 3] = q[3];
-        }
+        for (int i = 0; i < 4; ++i)
+          raw[j][i] = ldc4(x, (uint32_t)((t * cH + (COAL ? 4 * lane + 256 * i : 16 * lane + 4 * i)) * 4));
       }
     }
     if (prof && t0 == wave) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); wmark(*prof, 1, 13); }
@@ -457,14 +463,38 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv)[16],
     for (int j = 0; j < 2; ++j) {
       const int t = t0 + 4 * j;
       if (t >= T) break;
+      float v[1][16];
+      if constexpr (COAL) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e0 = 4 * lane + 256 * i;
+          *(v4f*)(stg + e0 + 4 * (e0 >> 4)) = raw[j][i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const v4f q = *(const v4f*)(stg + 20 * lane + 4 * i);
+          v[0][4 * i] = q[0];
+          v[0][4 * i + 1] = q[1];
+          v[0][4 * i + 2] = q[2];
+          v[0][4 * i + 3] = q[3];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[0][4 * i] = raw[j][i][0];
+          v[0][4 * i + 1] = raw[j][i][1];
+          v[0][4 * i + 2] = raw[j][i][2];
+          v[0][4 * i + 3] = raw[j][i][3];
+        }
+      }
       double s = 0.0;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s += (double)__fmul_rn(v[j][e], v[j][e]);
+      for (int e = 0; e < 16; ++e) s += (double)__fmul_rn(v[0][e], v[0][e]);
       s = wave_sum_d(s);
       const float scale = dev_rms_scale((float)(s / (double)cH), eps);
       float y[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) y[e] = __fmul_rn(__fmul_rn(v[j][e], scale), gv[e]);
+      for (int e = 0; e < 16; ++e) y[e] = __fmul_rn(__fmul_rn(v[0][e], scale), gv[e]);
       if (normed_out)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -1172,6 +1202,11 @@ __host__ __device__ constexpr size_t step_lds_x_offset(int G) {
              ? (size_t)G * cBF * (1024 + 64) + kRedBytes * G
              : ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride) * 4;
 }
+// after the residual columns: each wave's row image for the norm panel (8-row
+// variant only)
+__host__ __device__ constexpr size_t step_lds_stage_offset(int G) {
+  return step_lds_x_offset(G) + (size_t)G * 8 * 16 * 4;
+}
 __device__ __forceinline__ uint32_t ph(int l, int p) { return 2u + (uint32_t)(l * kPhases + p); }
 
 // PROF: the profiled variant (clock marks into P.timing); the production
@@ -1201,6 +1236,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   float* pscales = (float*)(lds + (size_t)G * cBF * 1024);
   float* red = (float*)(lds + (size_t)G * cBF * (1024 + 64));
   float* xs = (float*)(lds + step_lds_x_offset(G));  // this workgroup's residual columns
+  float* stg = (float*)(lds + step_lds_stage_offset(G));
   bool xs_valid = false;
   Ctl c{&P, epoch, 0, &s_ok};
 #define RX mk_rsrc(P.x, kMaxRows * cH * 4)
@@ -1277,7 +1313,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     if (!wait_all(c, ph(l, kPhQkv) - 1)) return;
     MARK(P, 3 + 12 * l + 0);
     WMARK(P, l, 0);
-    panel_norm(RX, T, gq, P.eps, pcodes, pscales, nullptr, (PROF && P.timing && l == 1) ? &P : nullptr);
+    panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, nullptr, stg, (PROF && P.timing && l == 1) ? &P : nullptr);
     WMARK(P, l, 25);
     {
       float acc[1][G][4] = {};
@@ -1360,7 +1396,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     if (gu) {
       if (!wait_all(c, ph(l, kPhGu) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return;
       WMARK(P, l, 8);
-      panel_norm(RX, T, gf, P.eps, pcodes, pscales, nullptr);
+      panel_norm<G == 1>(RX, T, gf, P.eps, pcodes, pscales, nullptr, stg);
       WMARK(P, l, 27);
       float acc[4][G][4] = {};
 #pragma unroll
@@ -1412,7 +1448,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     if (w == 0) {
       if (!wait_all(c, lm - 1)) return;
       gain16_load(P.out_norm, gq);
-      panel_norm(RX, T, gq, P.eps, pcodes, pscales, P.hid);
+      panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, P.hid, stg);
       MARK(P, 2);
     }
     return;
@@ -1420,7 +1456,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   if (!wait_all(c, lm - 1)) return;
   MARK(P, 3 + 12 * L);
   gain16_load(P.out_norm, gq);
-  panel_norm(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr);
+  panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr, stg);
   lm_head<G>(P, desc_arg.penalty, desc_arg.write_logits != 0, T, pcodes, pscales, s_best);
   publish(c, lm);
   MARK(P, 4 + 12 * L);
@@ -1449,7 +1485,7 @@ int step_kernel_workgroups() { return kNwg; }
 
 uint32_t step_progress_per_step(int n_layers) { return 2u + (uint32_t)(n_layers * kPhases); }
 
-size_t step_lds_bytes(int G) { return step_lds_x_offset(G) + (size_t)G * 8 * 16 * 4; }
+size_t step_lds_bytes(int G) { return step_lds_stage_offset(G) + (G == 1 ? (size_t)4 * kStageFloats * 4 : 0); }
 
 namespace {
 // [G - 1][f16 KV][profiled]
