@@ -23,14 +23,14 @@ struct KvLayer {
 };
 
 // Activation of a GEMM whose weights are f16 or q4_K (kernels_wt.hip): the
-// f16-rounded rows [16][K], or the q8_K blocks of the rows.
+// rows as f16 [16][K], or the q8_K blocks of the rows.
 struct ActQ8K {
   int8_t* qs;      // [16][K]
   float* d;        // [16][K/256]
   int32_t* bsums;  // [16][K/16]
 };
 struct WtAct {
-  float* f16v;  // [16][K]
+  uint16_t* f16h;  // [16][K] f16 bits
   ActQ8K q8k;
 };
 

@@ -56,7 +56,7 @@ __device__ __forceinline__ float row_rms_scale(const float* xr, int K, float eps
 // row recomputes the row's RMS scale (same order, same value).
 __global__ void __launch_bounds__(256)
 k_act_f16(const StepDesc* __restrict__ desc, const float* __restrict__ src, int K,
-          const float* __restrict__ gain, float eps, float* __restrict__ out,
+          const float* __restrict__ gain, float eps, uint16_t* __restrict__ out,
           float* __restrict__ normed_out) {
   const int t = blockIdx.x, k = blockIdx.y * 256 + threadIdx.x;
   if (t >= desc->T) return;
@@ -72,7 +72,7 @@ k_act_f16(const StepDesc* __restrict__ desc, const float* __restrict__ src, int 
     y = __fmul_rn(__fmul_rn(y, s_scale), gain[k]);
   }
   if (normed_out) normed_out[(size_t)t * K + k] = y;
-  out[(size_t)t * K + k] = f16_round(y);  // vec_dot_type F16
+  out[(size_t)t * K + k] = __half_as_ushort(__float2half_rn(y));  // vec_dot_type F16
 }
 
 // ggml quantize_row_q8_K_ref of one 256-block held one element per thread of a
@@ -189,47 +189,12 @@ k_attn_combine_wt(const StepDesc* __restrict__ desc, AttnWork work, int n_heads,
                                  (size_t)kMaxCols * 2, (size_t)kMaxCols * kHeadDim, d);
   const int QN = n_heads * kHeadDim;
   if constexpr (WT == MTG_TYPE_F16)
-    act.f16v[(size_t)t * QN + g * 256 + threadIdx.x] = f16_round(val);
+    act.f16h[(size_t)t * QN + g * 256 + threadIdx.x] = __half_as_ushort(__float2half_rn(val));
   else
     q8k_block256(val, act.q8k, t, QN, g);
 }
 
 // ------------------------------------------------------------ row dots ----
-// f16: res[t] (wave-uniform) = the canonical dot of row w[K] with xa[t][K].
-template <int SEG>
-__device__ __forceinline__ void f16_row_dots(const uint16_t* __restrict__ wrow,
-                                             const float* __restrict__ xa, int T, float* res) {
-  constexpr int K = SEG * 64;
-  const int lane = threadIdx.x & 63;
-  float wv[SEG];
-  const uint4* wp = (const uint4*)(wrow + lane * SEG);
-#pragma unroll
-  for (int i = 0; i < SEG / 8; ++i) {
-    const uint4 u = wp[i];
-    const uint32_t h[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      wv[8 * i + 2 * j] = half_bits_to_float((uint16_t)(h[j] & 0xffff));
-      wv[8 * i + 2 * j + 1] = half_bits_to_float((uint16_t)(h[j] >> 16));
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < kMaxRows; ++t) {  // constant indices keep res[] in registers
-    if (t >= T) break;
-    const float4* xp = (const float4*)(xa + (size_t)t * K + lane * SEG);
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < SEG / 4; ++i) {
-      const float4 x4 = xp[i];
-      acc = fmaf(wv[4 * i + 0], x4.x, acc);
-      acc = fmaf(wv[4 * i + 1], x4.y, acc);
-      acc = fmaf(wv[4 * i + 2], x4.z, acc);
-      acc = fmaf(wv[4 * i + 3], x4.w, acc);
-    }
-    res[t] = wave_sum_f(acc);
-  }
-}
-
 // q4_K: lane l takes elements 4(l%8)..+3 of sub-block l/8 of each superblock.
 __device__ __forceinline__ void q4k_row_dots(const uint8_t* __restrict__ wrow, const ActQ8K& a,
                                              int K, int T, float* res) {
@@ -274,10 +239,8 @@ __device__ __forceinline__ void q4k_row_dots(const uint8_t* __restrict__ wrow, c
 template <int WT, int SEG>
 __device__ __forceinline__ void row_dots(const uint8_t* w, int row, int K, const float* xa, const ActQ8K& a,
                                          int T, float* res) {
-  if constexpr (WT == MTG_TYPE_F16)
-    f16_row_dots<SEG>((const uint16_t*)w + (size_t)row * K, xa, T, res);
-  else
-    q4k_row_dots(w + (size_t)row * (K / 256) * 144, a, K, T, res);
+  static_assert(WT == MTG_TYPE_Q4_K, "f16 rows go through k_gemm_f16 / k_lm_head_f16");
+  q4k_row_dots(w + (size_t)row * (K / 256) * 144, a, K, T, res);
 }
 
 // ---------------------------------------------------------------- GEMM ----
@@ -637,24 +600,234 @@ k_lm_head_q4k(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
   }
 }
 
+// ------------------------------------------------------ f16, row groups ----
+// The workgroup stages the f16 activation rows [T][K] in LDS once; a wave takes
+// NR weight rows (of each of NM matrices) at a time, the next group's rows in
+// flight in registers. Lane l runs the canonical fma chain over its K/64
+// elements for every (matrix, row, verify row) output; the 64 lane partials of
+// an output meet in LDS (row stride 65 words: conflict-free both ways) and one
+// lane adds them in the pairing of the xor butterfly 32, 16, 8, 4, 2, 1 (the same
+// additions as wave_sum_f: IEEE sums commute). Lane j < 16 NR ends with the
+// outputs of row j / 16, verify row j % 16.
+template <int SEG, int NM, int NR>
+struct F16Group {
+  v4i w[NM][NR][SEG / 8];  // the lane's K/64 halves of each row, 8 per piece
+};
+
+__host__ __device__ constexpr size_t f16_lds_bytes(int K, int nm_nr) {
+  return (size_t)kMaxRows * K * 2 + 4 * (size_t)nm_nr * kMaxRows * 65 * 4;
+}
+
+template <int SEG, int NM, int NR>
+__device__ __forceinline__ void f16_load(const uint16_t* const (&base)[NM], int n, int row0,
+                                         F16Group<SEG, NM, NR>& g) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int row = row0 + r;
+#pragma unroll
+      for (int c = 0; c < SEG / 8; ++c)
+        if (row < n) g.w[m][r][c] = *(const v4i*)(base[m] + (size_t)row * (SEG * 64) + lane * SEG + 8 * c);
+    }
+}
+
+__device__ __forceinline__ float h_lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)w); }
+__device__ __forceinline__ float h_hi(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+template <int SEG, int NM, int NR>
+__device__ __forceinline__ void f16_group(const F16Group<SEG, NM, NR>& g, const uint16_t* s_x, int T, float* s_p,
+                                          float (&res)[NM]) {
+  constexpr int K = SEG * 64, NC = SEG / 8;
+  const int lane = threadIdx.x & 63;
+  float wf[NM][NR][SEG];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t u = (uint32_t)g.w[m][r][c][q];
+          wf[m][r][8 * c + 2 * q] = h_lo(u);
+          wf[m][r][8 * c + 2 * q + 1] = h_hi(u);
+        }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous group's partial reads are done
+#pragma unroll
+  for (int t = 0; t < kMaxRows; ++t) {  // constant indices keep the sums in registers
+    if (t >= T) break;
+    float acc[NM][NR];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int r = 0; r < NR; ++r) acc[m][r] = 0.0f;
+    const uint16_t* xr = s_x + t * K + lane * SEG;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const v4i xv = *(const v4i*)(xr + 8 * c);
+      float xf[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        xf[2 * q] = h_lo((uint32_t)xv[q]);
+        xf[2 * q + 1] = h_hi((uint32_t)xv[q]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int r = 0; r < NR; ++r) acc[m][r] = fmaf(wf[m][r][8 * c + e], xf[e], acc[m][r]);
+    }
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int r = 0; r < NR; ++r) s_p[((m * NR + r) * kMaxRows + t) * 65 + lane] = acc[m][r];
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's partial writes are done
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    float v[64];
+    const float* col = s_p + ((m * NR) * kMaxRows + lane) * 65;
+    if (lane < NR * kMaxRows && (lane & 15) < T) {
+#pragma unroll
+      for (int i = 0; i < 64; ++i) v[i] = col[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 64; ++i) v[i] = 0.0f;
+    }
+#pragma unroll
+    for (int h = 32; h >= 1; h >>= 1)
+#pragma unroll
+      for (int i = 0; i < h; ++i) v[i] = v[i] + v[i + h];
+    res[m] = v[0];
+  }
+}
+
+// EPI 0: store, 1: residual add, 2: silu(W x) * (W2 x)
+template <int EPI, int SEG, int NR>
+__global__ void __launch_bounds__(256)
+k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int n,
+           const uint16_t* __restrict__ xh, float* __restrict__ out) {
+  constexpr int K = SEG * 64, NM = EPI == 2 ? 2 : 1;
+  extern __shared__ v4i f16_lds_v4[];
+  uint16_t* s_x = (uint16_t*)f16_lds_v4;
+  const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float* s_p = (float*)(s_x + kMaxRows * K) + wave * (NM * NR * kMaxRows * 65);
+  const int ngroups = (n + NR - 1) / NR, nwaves = gridDim.x * 4;
+  const uint16_t* base[NM];
+  base[0] = (const uint16_t*)w;
+  if (NM == 2) base[NM - 1] = (const uint16_t*)w2;
+  int g = blockIdx.x * 4 + wave;
+  F16Group<SEG, NM, NR> bt;
+  f16_load<SEG, NM, NR>(base, n, g * NR, bt);  // in flight during the staging
+  for (int i = threadIdx.x; i < T * K / 8; i += 256) ((v4i*)s_x)[i] = ((const v4i*)xh)[i];
+  __syncthreads();
+  const int r = lane >> 4, t = lane & 15;
+  for (; g < ngroups; g += nwaves) {
+    const F16Group<SEG, NM, NR> cur = bt;
+    if (g + nwaves < ngroups) f16_load<SEG, NM, NR>(base, n, (g + nwaves) * NR, bt);
+    float res[NM];
+    f16_group<SEG, NM, NR>(cur, s_x, T, s_p, res);
+    const int row = g * NR + r;
+    if (r < NR && t < T && row < n) {
+      float* dst = out + (size_t)t * n + row;
+      if (EPI == 0) *dst = res[0];
+      else if (EPI == 1) *dst = __fadd_rn(*dst, res[0]);
+      else *dst = dev_swiglu(res[0], res[NM - 1]);
+    }
+  }
+}
+
+// f16 lm_head over the rows of the tied embedding, grouped as in k_gemm_f16; per
+// verify row the best 64-bit key (value bits, lowest index on ties) of each
+// workgroup goes to part_keys.
+constexpr int kF16LmNR = 4;
+__global__ void __launch_bounds__(256)
+k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int vocab,
+              const uint16_t* __restrict__ xh, const uint32_t* __restrict__ bitmap, float* __restrict__ logits,
+              uint64_t* __restrict__ part_keys) {
+  constexpr int SEG = 16, K = SEG * 64, NR = kF16LmNR;
+  extern __shared__ v4i f16_lds_v4[];
+  uint16_t* s_x = (uint16_t*)f16_lds_v4;
+  const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float* s_p = (float*)(s_x + kMaxRows * K) + wave * (NR * kMaxRows * 65);
+  const bool pen = desc->penalty > 1.0f;
+  const float penalty = desc->penalty;
+  const bool write_logits = desc->write_logits != 0;
+  const int words = (vocab + 31) / 32;
+  const int ngroups = (vocab + NR - 1) / NR, nwaves = gridDim.x * 4;
+  const uint16_t* base[1] = {(const uint16_t*)w};
+  int g = blockIdx.x * 4 + wave;
+  F16Group<SEG, 1, NR> bt;
+  f16_load<SEG, 1, NR>(base, vocab, g * NR, bt);
+  for (int i = threadIdx.x; i < T * K / 8; i += 256) ((v4i*)s_x)[i] = ((const v4i*)xh)[i];
+  __syncthreads();
+  const int r = lane >> 4, t = lane & 15;
+  uint64_t best = 0;  // lane (r, t): verify row t
+  for (; g < ngroups; g += nwaves) {
+    const F16Group<SEG, 1, NR> cur = bt;
+    if (g + nwaves < ngroups) f16_load<SEG, 1, NR>(base, vocab, (g + nwaves) * NR, bt);
+    float res[1];
+    f16_group<SEG, 1, NR>(cur, s_x, T, s_p, res);
+    const int row = g * NR + r;
+    if (t < T && row < vocab) {
+      float v = res[0];
+      if (write_logits) logits[(size_t)t * vocab + row] = v;
+      if (pen && ((bitmap[(size_t)t * words + (row >> 5)] >> (row & 31)) & 1u))
+        v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+      const uint64_t key = argmax_key(v, row);
+      best = key > best ? key : best;
+    }
+  }
+  __shared__ uint64_t s_best[4][64];
+  s_best[wave][lane] = best;
+  __syncthreads();
+  if ((int)threadIdx.x < T) {
+    uint64_t b = 0;
+    for (int i = 0; i < 16; ++i) {
+      const uint64_t c = s_best[i >> 2][(i & 3) * 16 + threadIdx.x];
+      b = c > b ? c : b;
+    }
+    part_keys[(size_t)blockIdx.x * kMaxRows + threadIdx.x] = b;
+  }
+}
+
+// weight rows per wave and group of the f16 GEMM (NM * NR * 16 partial rows of LDS per wave)
+constexpr int f16_nr(int epi, int seg) { return seg == 16 ? (epi == 2 ? 2 : 4) : 1; }
+
 template <int WT, int EPI>
 void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_t* w2, int n, int k,
              const WtAct& act, float* out) {
   const dim3 grid((n + 3) / 4), block(256);
   if constexpr (WT == MTG_TYPE_F16) {
-    if (k == 1024)
-      hipLaunchKernelGGL((k_gemm_wt<WT, 16, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
-    else if (k == 2048)
-      hipLaunchKernelGGL((k_gemm_wt<WT, 32, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
-    else
-      hipLaunchKernelGGL((k_gemm_wt<WT, 48, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
+    constexpr int NM = EPI == 2 ? 2 : 1;
+    if (k == 1024) {
+      constexpr int NR = f16_nr(EPI, 16);
+      const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kLmWorkgroups);
+      hipLaunchKernelGGL((k_gemm_f16<EPI, 16, NR>), dim3(blocks), block, f16_lds_bytes(k, NM * NR), s, desc, w, w2,
+                         n, act.f16h, out);
+    } else if (k == 2048) {
+      constexpr int NR = f16_nr(EPI, 32);
+      const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kLmWorkgroups);
+      hipLaunchKernelGGL((k_gemm_f16<EPI, 32, NR>), dim3(blocks), block, f16_lds_bytes(k, NM * NR), s, desc, w, w2,
+                         n, act.f16h, out);
+    } else {
+      constexpr int NR = f16_nr(EPI, 48);
+      const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kLmWorkgroups);
+      hipLaunchKernelGGL((k_gemm_f16<EPI, 48, NR>), dim3(blocks), block, f16_lds_bytes(k, NM * NR), s, desc, w, w2,
+                         n, act.f16h, out);
+    }
   } else if (k <= kQ4MaxK) {
     constexpr int NM = EPI == 2 ? 2 : 1;
     const int blocks = std::min((n + 4 * kQ4GemmD - 1) / (4 * kQ4GemmD), kLmWorkgroups);
     hipLaunchKernelGGL((k_gemm_q4k<EPI, kQ4GemmD>), dim3(blocks), block, q4_lds_bytes(k, NM * kQ4GemmD), s, desc,
                        w, w2, n, k, act.q8k, out);
   } else {
-    hipLaunchKernelGGL((k_gemm_wt<WT, 0, EPI>), grid, block, 0, s, desc, w, w2, n, k, act.f16v, act.q8k, out);
+    hipLaunchKernelGGL((k_gemm_wt<WT, 0, EPI>), grid, block, 0, s, desc, w, w2, n, k, nullptr, act.q8k, out);
   }
 }
 
@@ -670,7 +843,20 @@ hipError_t prepare_kernels_wt() {
                                              (int)q4_lds_bytes(kQ4MaxK, rows[i]));
     if (e != hipSuccess) return e;
   }
-  return hipSuccess;
+#define MTG_F16_ATTR(EPI, SEG)                                                                              \
+  {                                                                                                          \
+    constexpr int NR = f16_nr(EPI, SEG), NM = EPI == 2 ? 2 : 1;                                              \
+    const hipError_t e = hipFuncSetAttribute((const void*)k_gemm_f16<EPI, SEG, NR>,                          \
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,                     \
+                                             (int)f16_lds_bytes(SEG * 64, NM * NR));                         \
+    if (e != hipSuccess) return e;                                                                           \
+  }
+  MTG_F16_ATTR(0, 16) MTG_F16_ATTR(1, 16) MTG_F16_ATTR(2, 16)
+  MTG_F16_ATTR(0, 32) MTG_F16_ATTR(1, 32) MTG_F16_ATTR(2, 32)
+  MTG_F16_ATTR(0, 48) MTG_F16_ATTR(1, 48) MTG_F16_ATTR(2, 48)
+#undef MTG_F16_ATTR
+  return hipFuncSetAttribute((const void*)k_lm_head_f16, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)f16_lds_bytes(1024, kF16LmNR));
 }
 
 bool wt_shape_supported(int wtype, int k) {
@@ -683,7 +869,7 @@ void launch_act_wt(hipStream_t s, int wtype, const StepDesc* desc, const float* 
                    const float* gain, float eps, const WtAct& act, float* normed_out) {
   const dim3 grid(kMaxRows, K / 256);
   if (wtype == MTG_TYPE_F16)
-    hipLaunchKernelGGL(k_act_f16, grid, dim3(256), 0, s, desc, src, K, gain, eps, act.f16v, normed_out);
+    hipLaunchKernelGGL(k_act_f16, grid, dim3(256), 0, s, desc, src, K, gain, eps, act.f16h, normed_out);
   else
     hipLaunchKernelGGL(k_act_q8k, grid, dim3(256), 0, s, desc, src, K, gain, eps, act.q8k, normed_out);
 }
@@ -716,13 +902,13 @@ void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uin
                        const WtAct& act, const uint32_t* bitmap, float* logits, uint64_t* part_keys) {
   const dim3 grid(kLmWorkgroups), block(256);
   if (wtype == MTG_TYPE_F16)
-    hipLaunchKernelGGL((k_lm_head_wt<MTG_TYPE_F16, 16>), grid, block, 0, s, desc, w, vocab, k, act.f16v,
-                       act.q8k, bitmap, logits, part_keys);
+    hipLaunchKernelGGL(k_lm_head_f16, grid, block, f16_lds_bytes(1024, kF16LmNR), s, desc, w, vocab, act.f16h,
+                       bitmap, logits, part_keys);
   else if (k <= kQ4MaxK)
     hipLaunchKernelGGL(k_lm_head_q4k, grid, block, q4_lds_bytes(k, kQ4LmD), s, desc, w, vocab, k, act.q8k, bitmap,
                        logits, part_keys);
   else
-    hipLaunchKernelGGL((k_lm_head_wt<MTG_TYPE_Q4_K, 0>), grid, block, 0, s, desc, w, vocab, k, act.f16v,
+    hipLaunchKernelGGL((k_lm_head_wt<MTG_TYPE_Q4_K, 0>), grid, block, 0, s, desc, w, vocab, k, nullptr,
                        act.q8k, bitmap, logits, part_keys);
 }
 

@@ -207,11 +207,11 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
   panel_f = panel(F);
   if (wtype != MTG_TYPE_Q8_0) {
     const int KM = std::max(H, std::max(QN, F));
-    wact.f16v = (float*)dalloc((size_t)R * KM * 4, true);
+    wact.f16h = (uint16_t*)dalloc((size_t)R * KM * 2, true);
     wact.q8k.qs = (int8_t*)dalloc((size_t)R * KM, true);
     wact.q8k.d = (float*)dalloc((size_t)R * (KM / 256 + 1) * 4, true);
     wact.q8k.bsums = (int32_t*)dalloc((size_t)R * (KM / 16) * 4, true);
-    if (!wact.f16v || !wact.q8k.qs || !wact.q8k.d || !wact.q8k.bsums)
+    if (!wact.f16h || !wact.q8k.qs || !wact.q8k.d || !wact.q8k.bsums)
       return fail(MTG_ERR_NOMEM, "activation buffers");
   }
   const size_t chunks = (size_t)NKV * ((max_seq + kChunkKeys - 1) / kChunkKeys);
