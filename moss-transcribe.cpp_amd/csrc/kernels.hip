@@ -451,6 +451,43 @@ __device__ __forceinline__ void attn_f16_pv(const uint32_t* s_v, const float* s_
     }
 }
 
+// Chunk softmax of this wave's columns wave + 4 i (i < NC) side by side (lane =
+// key): the maximum on order-preserving integer keys (exact in any order; the
+// sign of a zero maximum changes no exp(w - m)), the sum in wave_sum_f's order.
+template <int NC>
+__device__ __forceinline__ void attn_f16_softmax(float* s_p, int ncol, float* out_ml) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sp_pos = (lane & 3) * 16 + (lane >> 2);
+  float wv[NC], lv[NC];
+  int mk[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int col = wave + 4 * i;
+    wv[i] = col < ncol ? s_p[col * kApStride + sp_pos] : -INFINITY;
+    mk[i] = ord_key(wv[i]);
+  }
+  wave_max_i_n<NC>(mk);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const float m = ord_val(mk[i]);
+    const float p = f16_round((m == -INFINITY || wv[i] == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(wv[i], m)));
+    wv[i] = p;
+    lv[i] = p;
+  }
+  wave_sum_f_n<NC>(lv);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int col = wave + 4 * i;
+    if (col < ncol) {
+      s_p[col * kApStride + sp_pos] = wv[i];
+      if (lane == 0) {
+        out_ml[col * 2] = ord_val(mk[i]);
+        out_ml[col * 2 + 1] = lv[i];
+      }
+    }
+  }
+}
+
 __global__ void __launch_bounds__(256, 2)
 k_attn_f16(const StepDesc* __restrict__ desc, const float* __restrict__ q, int n_heads, KvLayer kv,
            AttnWork work, int max_chunks) {
@@ -493,7 +530,6 @@ k_attn_f16(const StepDesc* __restrict__ desc, const float* __restrict__ q, int n
   }
   __syncthreads();  // s_q is s_p from here on
   const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)kHeadDim));
-  const int sp_pos = (lane & 3) * 16 + (lane >> 2);
   for (; chunk < nch; chunk += gridDim.y) {
     const int key0 = chunk * kChunk;
     // 1. the chunk's rows to LDS; the next chunk's loads go out
@@ -522,22 +558,14 @@ k_attn_f16(const StepDesc* __restrict__ desc, const float* __restrict__ q, int n
     else
       attn_f16_scores<1>(s_k, qreg, s_p, key0, kvlen, past, T, ncol, scale);
     __syncthreads();
-    // 3. chunk softmax per column (one wave per column, lane = key)
+    // 3. chunk softmax per column (lane = key), a wave's columns side by side
     const size_t item = (size_t)g * max_chunks + chunk;
     float* out_ml = work.part_ml + item * kMaxCols * 2;
     float* out_o = work.part_o + item * kMaxCols * kHeadDim;
-    for (int col = wave; col < ncol; col += 4) {
-      const float w = s_p[col * kApStride + sp_pos];
-      const float m = wave_max_f(w);
-      float p = (m == -INFINITY || w == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(w, m));
-      p = f16_round(p);
-      const float l = wave_sum_f(p);
-      s_p[col * kApStride + sp_pos] = p;
-      if (lane == 0) {
-        out_ml[col * 2] = m;
-        out_ml[col * 2 + 1] = l;
-      }
-    }
+    if (ncol > 16)
+      attn_f16_softmax<kMaxCols / 4>(s_p, ncol, out_ml);
+    else
+      attn_f16_softmax<4>(s_p, ncol, out_ml);
     __syncthreads();
     // 4. O = fma chain over the chunk's keys of p * v
     if (ncol > 16)
