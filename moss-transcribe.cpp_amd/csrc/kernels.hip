@@ -703,26 +703,35 @@ __global__ void __launch_bounds__(256)
 k_accept(const StepDesc* __restrict__ desc, const uint64_t* __restrict__ part_keys, int nparts,
          StepResult* __restrict__ result) {
   const int T = desc->T;
-  __shared__ uint64_t s_red[256];
+  __shared__ uint64_t s_red[4][kMaxRows];
   __shared__ int32_t s_choice[kMaxRows];
-  for (int t = 0; t < T; ++t) {
-    uint64_t b = 0;
-    for (int i = threadIdx.x; i < nparts; i += 256) {
-      const uint64_t k = part_keys[(size_t)i * kMaxRows + t];
-      b = k > b ? k : b;
-    }
-    s_red[threadIdx.x] = b;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-      if (threadIdx.x < o) {
-        const uint64_t k = s_red[threadIdx.x + o];
-        if (k > s_red[threadIdx.x]) s_red[threadIdx.x] = k;
-      }
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) s_choice[t] = (int32_t)(0xffffffffu - (uint32_t)(s_red[0] & 0xffffffffu));
-    __syncthreads();
+  // thread (j, t) = (tid / 16, tid % 16) takes the keys of verify row t in the
+  // parts j, j + 16, ... (a wave reads 512 contiguous bytes per pass); the
+  // maxima meet over lanes xor 16 and 32, then over the four waves
+  const int t = threadIdx.x & 15, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint64_t b = 0;
+#pragma unroll 8
+  for (int i = threadIdx.x >> 4; i < nparts; i += 16) {
+    const uint64_t k = part_keys[(size_t)i * kMaxRows + t];
+    b = k > b ? k : b;
   }
+  {
+    uint32_t alo, blo, ahi, bhi;
+    pair_split<32>((uint32_t)b, alo, blo);
+    pair_split<32>((uint32_t)(b >> 32), ahi, bhi);
+    b = max(((uint64_t)ahi << 32) | alo, ((uint64_t)bhi << 32) | blo);
+    pair_split<16>((uint32_t)b, alo, blo);
+    pair_split<16>((uint32_t)(b >> 32), ahi, bhi);
+    b = max(((uint64_t)ahi << 32) | alo, ((uint64_t)bhi << 32) | blo);
+  }
+  if (lane < 16) s_red[wave][lane] = b;
+  __syncthreads();
+  if ((int)threadIdx.x < T) {
+    uint64_t m = s_red[0][threadIdx.x];
+    for (int w = 1; w < 4; ++w) m = s_red[w][threadIdx.x] > m ? s_red[w][threadIdx.x] : m;
+    s_choice[threadIdx.x] = (int32_t)(0xffffffffu - (uint32_t)(m & 0xffffffffu));
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
     int m = 0;
     while (m + 1 < T && desc->tokens[m + 1] == s_choice[m]) ++m;
