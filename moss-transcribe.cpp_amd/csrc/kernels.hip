@@ -451,39 +451,62 @@ __device__ __forceinline__ void attn_f16_pv(const uint32_t* s_v, const float* s_
     }
 }
 
-// Chunk softmax of this wave's columns wave + 4 i (i < NC) side by side (lane =
-// key): the maximum on order-preserving integer keys (exact in any order; the
-// sign of a zero maximum changes no exp(w - m)), the sum in wave_sum_f's order.
+// Chunk softmax of this wave's columns wave + 4 c (c < NC): lane (c, j) =
+// (lane / LG, lane % LG), LG = 64 / NC lanes per column, holds keys j + LG a
+// (a < NC) of column c. The maximum runs on order-preserving integer keys (exact
+// in any order; the sign of a zero maximum changes no exp(w - m)). The sum keeps
+// wave_sum_f's pairing over the keys: the partners at xor 32 .. LG sit in the
+// same lane (a ^ (32 / LG) .. a ^ 1), those at xor LG / 2 .. 1 in lanes j ^ 8
+// (LG = 16: a row rotation by 8 is that exchange), j ^ 4, j ^ 2, j ^ 1.
+__device__ __forceinline__ int sp_key_pos(int key) { return (key & 3) * 16 + (key >> 2); }
+// the value of lane ^ 4 within groups of 8 lanes: a row rotation right by n
+// gives lane l the value of lane l - n (mod 16), so lanes with bit 2 clear take
+// the rotation by 12 (lane l + 4) and the others the rotation by 4 (lane l - 4)
+__device__ __forceinline__ uint32_t lane_xor4(uint32_t v) {
+  const uint32_t from_up = dpp_u<0x12C>(v), from_dn = dpp_u<0x124>(v);
+  return (threadIdx.x & 4) ? from_dn : from_up;
+}
 template <int NC>
 __device__ __forceinline__ void attn_f16_softmax(float* s_p, int ncol, float* out_ml) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sp_pos = (lane & 3) * 16 + (lane >> 2);
-  float wv[NC], lv[NC];
-  int mk[NC];
+  static_assert(NC == 4 || NC == 8, "4 or 8 columns per wave");
+  constexpr int LG = 64 / NC;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, c = lane / LG, j = lane % LG;
+  const int col = wave + 4 * c;
+  const bool live = col < ncol;
+  float* row = s_p + min(col, ncol - 1) * kApStride;
+  float w[NC];
+  int mk = ord_key(-INFINITY);
 #pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int col = wave + 4 * i;
-    wv[i] = col < ncol ? s_p[col * kApStride + sp_pos] : -INFINITY;
-    mk[i] = ord_key(wv[i]);
+  for (int a = 0; a < NC; ++a) {
+    w[a] = live ? row[sp_key_pos(j + LG * a)] : -INFINITY;
+    mk = max(mk, ord_key(w[a]));
   }
-  wave_max_i_n<NC>(mk);
+  if (LG == 16) mk = max(mk, (int)dpp_u<kDppRor8>((uint32_t)mk));
+  mk = max(mk, (int)lane_xor4((uint32_t)mk));
+  mk = max(mk, (int)dpp_u<kDppQuadXor2>((uint32_t)mk));
+  mk = max(mk, (int)dpp_u<kDppQuadXor1>((uint32_t)mk));
+  const float m = ord_val(mk);
+  float p[NC], v[NC];
 #pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const float m = ord_val(mk[i]);
-    const float p = f16_round((m == -INFINITY || wv[i] == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(wv[i], m)));
-    wv[i] = p;
-    lv[i] = p;
+  for (int a = 0; a < NC; ++a) {
+    p[a] = f16_round((m == -INFINITY || w[a] == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(w[a], m)));
+    v[a] = p[a];
   }
-  wave_sum_f_n<NC>(lv);
 #pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int col = wave + 4 * i;
-    if (col < ncol) {
-      s_p[col * kApStride + sp_pos] = wv[i];
-      if (lane == 0) {
-        out_ml[col * 2] = ord_val(mk[i]);
-        out_ml[col * 2 + 1] = lv[i];
-      }
+  for (int h = NC / 2; h >= 1; h /= 2)
+#pragma unroll
+    for (int a = 0; a < h; ++a) v[a] = __fadd_rn(v[a], v[a + h]);
+  float l = v[0];
+  if (LG == 16) l = __fadd_rn(l, dpp_f<kDppRor8>(l));
+  l = __fadd_rn(l, __uint_as_float(lane_xor4(__float_as_uint(l))));
+  l = __fadd_rn(l, dpp_f<kDppQuadXor2>(l));
+  l = __fadd_rn(l, dpp_f<kDppQuadXor1>(l));
+  if (live) {
+#pragma unroll
+    for (int a = 0; a < NC; ++a) row[sp_key_pos(j + LG * a)] = p[a];
+    if (j == 0) {
+      out_ml[col * 2] = m;
+      out_ml[col * 2 + 1] = l;
     }
   }
 }
