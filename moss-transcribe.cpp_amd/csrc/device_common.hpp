@@ -407,6 +407,16 @@ __device__ __forceinline__ void wave_sum_f_n(float* v) {
 #pragma unroll
   for (int i = 0; i < N; ++i) v[i] = __fadd_rn(v[i], dpp_f<kDppRor1>(v[i]));
 }
+// Position of key k of a 64-key chunk in a permuted probability row (key
+// 4 s + kk at kk * 16 + s).
+__device__ __forceinline__ int sp_key_pos(int key) { return (key & 3) * 16 + (key >> 2); }
+// The value of lane ^ 4 within groups of 8 lanes: a row rotation right by n
+// gives lane l the value of lane l - n (mod 16), so lanes with bit 2 clear take
+// the rotation by 12 (lane l + 4) and the others the rotation by 4 (lane l - 4).
+__device__ __forceinline__ uint32_t lane_xor4(uint32_t v) {
+  const uint32_t from_up = dpp_u<0x12C>(v), from_dn = dpp_u<0x124>(v);
+  return (threadIdx.x & 4) ? from_dn : from_up;
+}
 // Order-preserving integer key of a float that is not NaN (signed compare), and
 // back; max is exact in any order.
 __device__ __forceinline__ int ord_key(float x) {

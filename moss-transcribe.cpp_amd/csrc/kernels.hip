@@ -458,14 +458,6 @@ __device__ __forceinline__ void attn_f16_pv(const uint32_t* s_v, const float* s_
 // wave_sum_f's pairing over the keys: the partners at xor 32 .. LG sit in the
 // same lane (a ^ (32 / LG) .. a ^ 1), those at xor LG / 2 .. 1 in lanes j ^ 8
 // (LG = 16: a row rotation by 8 is that exchange), j ^ 4, j ^ 2, j ^ 1.
-__device__ __forceinline__ int sp_key_pos(int key) { return (key & 3) * 16 + (key >> 2); }
-// the value of lane ^ 4 within groups of 8 lanes: a row rotation right by n
-// gives lane l the value of lane l - n (mod 16), so lanes with bit 2 clear take
-// the rotation by 12 (lane l + 4) and the others the rotation by 4 (lane l - 4)
-__device__ __forceinline__ uint32_t lane_xor4(uint32_t v) {
-  const uint32_t from_up = dpp_u<0x12C>(v), from_dn = dpp_u<0x124>(v);
-  return (threadIdx.x & 4) ? from_dn : from_up;
-}
 template <int NC>
 __device__ __forceinline__ void attn_f16_softmax(float* s_p, int ncol, float* out_ml) {
   static_assert(NC == 4 || NC == 8, "4 or 8 columns per wave");

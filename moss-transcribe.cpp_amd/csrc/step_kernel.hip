@@ -842,39 +842,56 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   // 4. chunk softmax per column (one wave per column, lane = key)
   const size_t pi = (size_t)g * P.max_chunks + chunk;
   const Rsrc rml = mk_rsrc(P.part_ml + pi * kMaxCols * 2, kMaxCols * 2 * 4);
-  // this wave's columns wave + 4 i (i < 4G) side by side; the max runs on
-  // order-preserving integer keys of the scores (no NaN here; the sign of a zero
-  // maximum does not change any exp(w - m))
-  constexpr int kCols = 4 * G;
-  // probabilities of a column are kept permuted (key 4 s + kk at kk * 16 + s), so
-  // that the P.V operands of a lane are 16 consecutive floats
-  const int sp_pos = (lane & 3) * 16 + (lane >> 2);
-  float wv[kCols], lv[kCols];
-  int mk[kCols];
+  // this wave's columns wave + 4 c (c < NC = 4G): lane (c, j) = (lane / LG,
+  // lane % LG), LG = 64 / NC, holds keys j + LG a (a < NC) of column c. The max
+  // runs on order-preserving integer keys of the scores (exact in any order; no
+  // NaN here; the sign of a zero maximum changes no exp(w - m)). The sum keeps
+  // wave_sum_f's pairing over the keys: the partners at xor 32 .. LG sit in the
+  // same lane, those at xor LG / 2 .. 1 in lanes j ^ 8 (LG = 16: a row rotation
+  // by 8), j ^ 4, j ^ 2, j ^ 1. Probabilities of a column are kept permuted (key
+  // 4 s + kk at kk * 16 + s), so that the P.V operands of a lane are 16
+  // consecutive floats.
+  {
+    constexpr int NC = 4 * G, LG = 64 / NC;
+    const int c = lane / LG, j = lane % LG, col = wave + 4 * c;
+    const bool live = col < ncol;
+    float* row = sp + min(col, ncol - 1) * cPStride;
+    float w[NC];
+    int mk = ord_key(-INFINITY);
 #pragma unroll
-  for (int i = 0; i < kCols; ++i) {
-    const int col = wave + 4 * i;
-    wv[i] = col < ncol ? sp[col * cPStride + sp_pos] : -INFINITY;
-    mk[i] = ord_key(wv[i]);
-  }
-  wave_max_i_n<kCols>(mk);
+    for (int a = 0; a < NC; ++a) {
+      w[a] = live ? row[sp_key_pos(j + LG * a)] : -INFINITY;
+      mk = max(mk, ord_key(w[a]));
+    }
+    if (LG == 16) mk = max(mk, (int)dpp_u<kDppRor8>((uint32_t)mk));
+    mk = max(mk, (int)lane_xor4((uint32_t)mk));
+    mk = max(mk, (int)dpp_u<kDppQuadXor2>((uint32_t)mk));
+    mk = max(mk, (int)dpp_u<kDppQuadXor1>((uint32_t)mk));
+    const float m = ord_val(mk);
+    float pv[NC], v[NC];
 #pragma unroll
-  for (int i = 0; i < kCols; ++i) {
-    const float m = ord_val(mk[i]);
-    float p = (m == -INFINITY || wv[i] == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(wv[i], m));
-    if (f16kv) p = f16_round(p);
-    wv[i] = p;
-    lv[i] = p;
-  }
-  wave_sum_f_n<kCols>(lv);
+    for (int a = 0; a < NC; ++a) {
+      float p = (m == -INFINITY || w[a] == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(w[a], m));
+      if (f16kv) p = f16_round(p);
+      pv[a] = p;
+      v[a] = p;
+    }
 #pragma unroll
-  for (int i = 0; i < kCols; ++i) {
-    const int col = wave + 4 * i;
-    if (col >= ncol) break;
-    sp[col * cPStride + sp_pos] = wv[i];
-    if (lane == 0) {
-      stc1(rml, (uint32_t)(col * 2 * 4), ord_val(mk[i]));
-      stc1(rml, (uint32_t)((col * 2 + 1) * 4), lv[i]);
+    for (int h = NC / 2; h >= 1; h /= 2)
+#pragma unroll
+      for (int a = 0; a < h; ++a) v[a] = __fadd_rn(v[a], v[a + h]);
+    float l = v[0];
+    if (LG == 16) l = __fadd_rn(l, dpp_f<kDppRor8>(l));
+    l = __fadd_rn(l, __uint_as_float(lane_xor4(__float_as_uint(l))));
+    l = __fadd_rn(l, dpp_f<kDppQuadXor2>(l));
+    l = __fadd_rn(l, dpp_f<kDppQuadXor1>(l));
+    if (live) {
+#pragma unroll
+      for (int a = 0; a < NC; ++a) row[sp_key_pos(j + LG * a)] = pv[a];
+      if (j == 0) {
+        stc1(rml, (uint32_t)(col * 2 * 4), m);
+        stc1(rml, (uint32_t)((col * 2 + 1) * 4), l);
+      }
     }
   }
   bar();
