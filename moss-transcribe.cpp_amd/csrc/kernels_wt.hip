@@ -600,6 +600,156 @@ k_lm_head_q4k(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
   }
 }
 
+// ------------------------------------------------ q4_K lm_head, int8 MFMA ----
+// Tile = 16 rows of the tied embedding, all 16 verify rows. Per superblock the
+// exact int32 sums come from v_mfma_i32_16x16x32_i8, one sub-block (32 elements)
+// per instruction, accumulated over the superblock's 8 sub-blocks:
+//   A = the nibbles q (0..15) of row l % 16, elements 8 (l / 16) .. + 7, times a
+//       small factor (bytewise exact: every product fits a byte);
+//   B = the q8_K codes x of verify row l % 16, the same elements.
+// With the 6-bit scale split as sc = 8 hi + lo (hi, lo <= 7, q * hi <= 105):
+//   dot  = sum_s sc_s sum_e q x = 8 * sum_s (hi_s q) . x + sum_s (lo_s q) . x
+//   mins = sum_s mn_s bsum_s     =     sum_s (mn_s 1) . x
+// Lane l then holds rows 4 (l / 16) + r (r < 4) of verify row l % 16 and runs the
+// canonical float chain over the superblocks (d, dmin of its rows from LDS).
+__host__ __device__ constexpr size_t q4m_lds_bytes(int K) {
+  return q4_lds_bytes(K, 0) + 4 * (size_t)16 * 2 * 4;  // + per wave: d|dmin [16][2]
+}
+
+// get_scale_min_k4 of the 8 sub-blocks from the 12 packed bytes held in three
+// words (byte i in word i / 4)
+__device__ __forceinline__ void q4k_scales_w(uint32_t w0, uint32_t w1, uint32_t w2, int sc[8], int mn[8]) {
+  const uint32_t wd[3] = {w0, w1, w2};
+  auto by = [&](int i) { return (int)((wd[i >> 2] >> (8 * (i & 3))) & 0xffu); };
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sc[j] = by(j) & 63;
+    mn[j] = by(j + 4) & 63;
+  }
+#pragma unroll
+  for (int j = 4; j < 8; ++j) {
+    sc[j] = (by(j + 4) & 0xF) | ((by(j - 4) >> 6) << 4);
+    mn[j] = (by(j + 4) >> 4) | ((by(j) >> 6) << 4);
+  }
+}
+
+template <int NB>
+struct Q4Tile {
+  uint32_t q[NB][4][2];  // per superblock, pair mm: the lane's 8 nibble bytes
+  v4i head[NB];          // the lane's row's d, dmin and 12 scale bytes
+};
+
+template <int NB>
+__device__ __forceinline__ void q4m_load(const uint8_t* w, int n_tiles, int tile, Q4Tile<NB>& tl) {
+  const int lane = threadIdx.x & 63, row = lane & 15, g = lane >> 4;
+  if (tile >= n_tiles) return;
+  const uint8_t* rb = w + ((size_t)tile * 16 + row) * NB * 144;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+      const uint2 u = *(const uint2*)(rb + b * 144 + 16 + 32 * mm + 8 * g);
+      tl.q[b][mm][0] = u.x;
+      tl.q[b][mm][1] = u.y;
+    }
+    tl.head[b] = *(const v4i*)(rb + b * 144);
+  }
+}
+
+// res[r]: row 4 (lane / 16) + r of the tile, verify row lane % 16
+template <int NB>
+__device__ __forceinline__ void q4m_tile(const Q4Tile<NB>& tl, const Q4Lds& q, int K, float* s_d, float (&res)[4]) {
+  const int lane = threadIdx.x & 63, t = lane & 15, g = lane >> 4;
+  const int as = q4_act_stride(K);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) res[r] = 0.0f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const v4i h = tl.head[b];
+    int sc[8], mn[8];
+    q4k_scales_w((uint32_t)h[1], (uint32_t)h[2], (uint32_t)h[3], sc, mn);
+    v4i ahi = {0, 0, 0, 0}, alo = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
+    const int8_t* xa = q.act + (size_t)t * as + b * 256 + 8 * g;
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {  // sub-block 2 mm + hi: the low or high nibbles
+        const int s = 2 * mm + hi;
+        const uint32_t q0 = hi ? (tl.q[b][mm][0] >> 4) & 0x0F0F0F0Fu : tl.q[b][mm][0] & 0x0F0F0F0Fu;
+        const uint32_t q1 = hi ? (tl.q[b][mm][1] >> 4) & 0x0F0F0F0Fu : tl.q[b][mm][1] & 0x0F0F0F0Fu;
+        const uint32_t fh = (uint32_t)(sc[s] >> 3), fl = (uint32_t)(sc[s] & 7), fm = (uint32_t)mn[s] * 0x01010101u;
+        const long bv = *(const long*)(xa + 32 * s);
+        ahi = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)(((uint64_t)(q1 * fh) << 32) | (q0 * fh)), bv, ahi, 0, 0, 0);
+        alo = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)(((uint64_t)(q1 * fl) << 32) | (q0 * fl)), bv, alo, 0, 0, 0);
+        amn = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)(((uint64_t)fm << 32) | fm), bv, amn, 0, 0, 0);
+      }
+    }
+    // d, dmin of the tile's rows through the wave's LDS slot (lanes 0..15 own them)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (g == 0) {
+      s_d[t * 2] = half_bits_to_float((uint16_t)((uint32_t)h[0] & 0xffffu));
+      s_d[t * 2 + 1] = half_bits_to_float((uint16_t)((uint32_t)h[0] >> 16));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const float dxv = q.dx[t * NB + b];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int dot = 8 * ahi[r] + alo[r];
+      const float dm = __fmul_rn(s_d[(4 * g + r) * 2], dxv), dmin = __fmul_rn(s_d[(4 * g + r) * 2 + 1], dxv);
+      res[r] = __fadd_rn(res[r], __fmul_rn(dm, (float)dot));
+      res[r] = __fsub_rn(res[r], __fmul_rn(dmin, (float)amn[r]));
+    }
+  }
+}
+
+template <int NB>
+__global__ void __launch_bounds__(256)
+k_lm_head_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int vocab, ActQ8K a,
+              const uint32_t* __restrict__ bitmap, float* __restrict__ logits, uint64_t* __restrict__ part_keys) {
+  constexpr int K = NB * 256;
+  extern __shared__ v4i q4_lds_v4[];
+  const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = lane & 15, g = lane >> 4;
+  const bool pen = desc->penalty > 1.0f;
+  const float penalty = desc->penalty;
+  const bool write_logits = desc->write_logits != 0;
+  const int words = (vocab + 31) / 32, n_tiles = vocab / 16, nwaves = gridDim.x * 4;
+  int tile = blockIdx.x * 4 + wave;
+  Q4Tile<NB> nx;
+  q4m_load<NB>(w, n_tiles, tile, nx);
+  const Q4Lds q = q4_stage(a, K, T, 0, (uint8_t*)q4_lds_v4);
+  float* s_d = (float*)((uint8_t*)q4_lds_v4 + q4_lds_bytes(K, 0)) + wave * 16 * 2;
+  uint64_t best = 0;  // lane (g, t): verify row t
+  for (; tile < n_tiles; tile += nwaves) {
+    const Q4Tile<NB> cur = nx;
+    if (tile + nwaves < n_tiles) q4m_load<NB>(w, n_tiles, tile + nwaves, nx);
+    float res[4];
+    q4m_tile<NB>(cur, q, K, s_d, res);
+    if (t < T) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = tile * 16 + 4 * g + r;
+        float v = res[r];
+        if (write_logits) logits[(size_t)t * vocab + row] = v;
+        if (pen && ((bitmap[(size_t)t * words + (row >> 5)] >> (row & 31)) & 1u))
+          v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+        const uint64_t key = argmax_key(v, row);
+        best = key > best ? key : best;
+      }
+    }
+  }
+  __shared__ uint64_t s_best[4][64];
+  s_best[wave][lane] = best;
+  __syncthreads();
+  if ((int)threadIdx.x < T) {
+    uint64_t b = 0;
+    for (int i = 0; i < 16; ++i) {
+      const uint64_t c = s_best[i >> 2][(i & 3) * 16 + threadIdx.x];
+      b = c > b ? c : b;
+    }
+    part_keys[(size_t)blockIdx.x * kMaxRows + threadIdx.x] = b;
+  }
+}
+
 // ------------------------------------------------------ f16, row groups ----
 // The workgroup stages the f16 activation rows [T][K] in LDS once; a wave takes
 // NR weight rows (of each of NM matrices) at a time, the next group's rows in
@@ -904,6 +1054,9 @@ void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uin
   if (wtype == MTG_TYPE_F16)
     hipLaunchKernelGGL(k_lm_head_f16, grid, block, f16_lds_bytes(1024, kF16LmNR), s, desc, w, vocab, act.f16h,
                        bitmap, logits, part_keys);
+  else if (k == 1024 && vocab % 16 == 0)
+    hipLaunchKernelGGL(k_lm_head_q4m<4>, grid, block, q4m_lds_bytes(k), s, desc, w, vocab, act.q8k, bitmap, logits,
+                       part_keys);
   else if (k <= kQ4MaxK)
     hipLaunchKernelGGL(k_lm_head_q4k, grid, block, q4_lds_bytes(k, kQ4LmD), s, desc, w, vocab, k, act.q8k, bitmap,
                        logits, part_keys);
