@@ -383,11 +383,11 @@ __device__ __forceinline__ Q4Lds q4_stage(const ActQ8K& a, int K, int T, int row
   int* bs = (int*)(lds + (size_t)kMaxRows * as);
   float* dx = (float*)(bs + kMaxRows * bst);
   uint8_t* wbase = (uint8_t*)(dx + kMaxRows * nb);
-  const int pa = K / 16, pb = K / 64;  // 16-byte pieces per row
-  for (int i = tid; i < T * pa; i += 256)
+  const int pa = K / 16, pb = K / 64, nt = blockDim.x;  // 16-byte pieces per row
+  for (int i = tid; i < T * pa; i += nt)
     *(v4i*)(act + (size_t)(i / pa) * as + (i % pa) * 16) = ((const v4i*)a.qs)[i];
-  for (int i = tid; i < T * pb; i += 256) *(v4i*)(bs + (size_t)(i / pb) * bst + (i % pb) * 4) = ((const v4i*)a.bsums)[i];
-  for (int i = tid; i < T * nb; i += 256) dx[i] = a.d[i];
+  for (int i = tid; i < T * pb; i += nt) *(v4i*)(bs + (size_t)(i / pb) * bst + (i % pb) * 4) = ((const v4i*)a.bsums)[i];
+  for (int i = tid; i < T * nb; i += nt) dx[i] = a.d[i];
   __syncthreads();
   Q4Lds q;
   q.act = act;
@@ -656,11 +656,13 @@ __device__ __forceinline__ void q4m_load(const uint8_t* w, int n_tiles, int tile
   }
 }
 
-// res[r]: row 4 (lane / 16) + r of the tile, verify row lane % 16
+// res[r]: row 4 (lane / 16) + r of the tile, verify row lane % 16. The q8_K codes
+// and scales come from the workgroup's LDS copy (xq / dxp in LDS, row stride as)
+// or, for a single tile, straight from the activation buffers.
 template <int NB>
-__device__ __forceinline__ void q4m_tile(const Q4Tile<NB>& tl, const Q4Lds& q, int K, float* s_d, float (&res)[4]) {
+__device__ __forceinline__ void q4m_tile(const Q4Tile<NB>& tl, const int8_t* xq, int as, const float* dxp,
+                                         float* s_d, float (&res)[4]) {
   const int lane = threadIdx.x & 63, t = lane & 15, g = lane >> 4;
-  const int as = q4_act_stride(K);
 #pragma unroll
   for (int r = 0; r < 4; ++r) res[r] = 0.0f;
 #pragma unroll
@@ -669,7 +671,7 @@ __device__ __forceinline__ void q4m_tile(const Q4Tile<NB>& tl, const Q4Lds& q, i
     int sc[8], mn[8];
     q4k_scales_w((uint32_t)h[1], (uint32_t)h[2], (uint32_t)h[3], sc, mn);
     v4i ahi = {0, 0, 0, 0}, alo = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
-    const int8_t* xa = q.act + (size_t)t * as + b * 256 + 8 * g;
+    const int8_t* xa = xq + (size_t)t * as + b * 256 + 8 * g;
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
 #pragma unroll
@@ -691,13 +693,43 @@ __device__ __forceinline__ void q4m_tile(const Q4Tile<NB>& tl, const Q4Lds& q, i
       s_d[t * 2 + 1] = half_bits_to_float((uint16_t)((uint32_t)h[0] >> 16));
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const float dxv = q.dx[t * NB + b];
+    const float dxv = dxp[t * NB + b];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int dot = 8 * ahi[r] + alo[r];
       const float dm = __fmul_rn(s_d[(4 * g + r) * 2], dxv), dmin = __fmul_rn(s_d[(4 * g + r) * 2 + 1], dxv);
       res[r] = __fadd_rn(res[r], __fmul_rn(dm, (float)dot));
       res[r] = __fsub_rn(res[r], __fmul_rn(dmin, (float)amn[r]));
+    }
+  }
+}
+
+// q4_K GEMM on the same tiles: one 64-thread workgroup per 16-row tile (and per
+// matrix pair for EPI 2); the activation operands come straight from the q8_K
+// buffers (every tile reads them, from L2). EPI 0: store, 1: residual add,
+// 2: silu(W x) * (W2 x).
+template <int EPI, int NB>
+__global__ void __launch_bounds__(64)
+k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int n,
+           ActQ8K a, float* __restrict__ out) {
+  constexpr int K = NB * 256, NM = EPI == 2 ? 2 : 1;
+  extern __shared__ v4i q4_lds_v4[];
+  const int T = desc->T, lane = threadIdx.x & 63, t = lane & 15, g = lane >> 4;
+  const int tile = blockIdx.x, n_tiles = n / 16;
+  Q4Tile<NB> tl[NM];
+  q4m_load<NB>(w, n_tiles, tile, tl[0]);
+  if (NM == 2) q4m_load<NB>(w2, n_tiles, tile, tl[NM - 1]);
+  float* s_d = (float*)q4_lds_v4;
+  float res[NM][4];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) q4m_tile<NB>(tl[m], a.qs, K, a.d, s_d, res[m]);
+  if (t < T) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float* dst = out + (size_t)t * n + tile * 16 + 4 * g + r;
+      if (EPI == 0) *dst = res[0][r];
+      else if (EPI == 1) *dst = __fadd_rn(*dst, res[0][r]);
+      else *dst = dev_swiglu(res[0][r], res[NM - 1][r]);
     }
   }
 }
@@ -723,7 +755,7 @@ k_lm_head_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
     const Q4Tile<NB> cur = nx;
     if (tile + nwaves < n_tiles) q4m_load<NB>(w, n_tiles, tile + nwaves, nx);
     float res[4];
-    q4m_tile<NB>(cur, q, K, s_d, res);
+    q4m_tile<NB>(cur, q.act, q4_act_stride(K), q.dx, s_d, res);
     if (t < T) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -971,6 +1003,15 @@ void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_
       hipLaunchKernelGGL((k_gemm_f16<EPI, 48, NR>), dim3(blocks), block, f16_lds_bytes(k, NM * NR), s, desc, w, w2,
                          n, act.f16h, out);
     }
+  } else if (n % 16 == 0 && (k == 1024 || k == 2048 || (k == 3072 && EPI != 2))) {
+    // (the two-matrix tile at K = 3072 would spill: that shape takes the kernel below)
+    const size_t lds = 16 * 2 * 4;  // d|dmin of the tile's rows
+    if (k == 1024)
+      hipLaunchKernelGGL((k_gemm_q4m<EPI, 4>), dim3(n / 16), dim3(64), lds, s, desc, w, w2, n, act.q8k, out);
+    else if (k == 2048)
+      hipLaunchKernelGGL((k_gemm_q4m<EPI, 8>), dim3(n / 16), dim3(64), lds, s, desc, w, w2, n, act.q8k, out);
+    else if constexpr (EPI != 2)
+      hipLaunchKernelGGL((k_gemm_q4m<EPI, 12>), dim3(n / 16), dim3(64), lds, s, desc, w, w2, n, act.q8k, out);
   } else if (k <= kQ4MaxK) {
     constexpr int NM = EPI == 2 ? 2 : 1;
     const int blocks = std::min((n + 4 * kQ4GemmD - 1) / (4 * kQ4GemmD), kLmWorkgroups);
