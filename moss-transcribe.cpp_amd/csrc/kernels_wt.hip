@@ -704,25 +704,101 @@ __device__ __forceinline__ void q4m_tile(const Q4Tile<NB>& tl, const int8_t* xq,
   }
 }
 
-// q4_K GEMM on the same tiles: one 64-thread workgroup per 16-row tile (and per
-// matrix pair for EPI 2); the activation operands come straight from the q8_K
-// buffers (every tile reads them, from L2). EPI 0: store, 1: residual add,
-// 2: silu(W x) * (W2 x).
+// q4_K GEMM on the same tiles: one 256-thread workgroup per 16-row tile (and per
+// matrix pair for EPI 2). Wave w takes superblocks w, w + 4, ...: their exact
+// int32 sums (dot, mins) of every (row, verify row) and the rows' d, dmin go to
+// LDS, and wave 0 runs the canonical float chain over the superblocks in order.
+// The activation operands come straight from the q8_K buffers (every tile reads
+// them, from L2). EPI 0: store, 1: residual add, 2: silu(W x) * (W2 x).
+__host__ __device__ constexpr size_t q4g_lds_bytes(int nb, int nm) {
+  return (size_t)nm * nb * (2 * 4 * 64 * 4 + 16 * 2 * 4);  // [m][b] (dot, mins) [2][4][64] + d|dmin [16][2]
+}
+
 template <int EPI, int NB>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(256)
 k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int n,
            ActQ8K a, float* __restrict__ out) {
-  constexpr int K = NB * 256, NM = EPI == 2 ? 2 : 1;
+  constexpr int K = NB * 256, NM = EPI == 2 ? 2 : 1, NBW = (NB + 3) / 4;
   extern __shared__ v4i q4_lds_v4[];
-  const int T = desc->T, lane = threadIdx.x & 63, t = lane & 15, g = lane >> 4;
-  const int tile = blockIdx.x, n_tiles = n / 16;
-  Q4Tile<NB> tl[NM];
-  q4m_load<NB>(w, n_tiles, tile, tl[0]);
-  if (NM == 2) q4m_load<NB>(w2, n_tiles, tile, tl[NM - 1]);
-  float* s_d = (float*)q4_lds_v4;
+  int* s_i = (int*)q4_lds_v4;                                 // [m][b][2][4][64]
+  float* s_dd = (float*)(s_i + NM * NB * 2 * 4 * 64);        // [m][b][16][2]
+  const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = lane & 15, g = lane >> 4;
+  const int row = lane & 15, tile = blockIdx.x;
+  const uint8_t* const base[2] = {w, w2};
+  // this wave's superblocks: loads first, all of them
+  uint32_t qw[NM][NBW][4][2];
+  v4i head[NM][NBW];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int b = wave + 4 * j;
+      if (b < NB) {
+        const uint8_t* rb = base[m] + ((size_t)tile * 16 + row) * NB * 144 + b * 144;
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+          const uint2 u = *(const uint2*)(rb + 16 + 32 * mm + 8 * g);
+          qw[m][j][mm][0] = u.x;
+          qw[m][j][mm][1] = u.y;
+        }
+        head[m][j] = *(const v4i*)rb;
+      }
+    }
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int b = wave + 4 * j;
+      if (b >= NB) continue;
+      const v4i h = head[m][j];
+      int sc[8], mn[8];
+      q4k_scales_w((uint32_t)h[1], (uint32_t)h[2], (uint32_t)h[3], sc, mn);
+      v4i ahi = {0, 0, 0, 0}, alo = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
+      const int8_t* xa = a.qs + (size_t)t * K + b * 256 + 8 * g;
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm)
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+          const int s = 2 * mm + hi;
+          const uint32_t q0 = hi ? (qw[m][j][mm][0] >> 4) & 0x0F0F0F0Fu : qw[m][j][mm][0] & 0x0F0F0F0Fu;
+          const uint32_t q1 = hi ? (qw[m][j][mm][1] >> 4) & 0x0F0F0F0Fu : qw[m][j][mm][1] & 0x0F0F0F0Fu;
+          const uint32_t fh = (uint32_t)(sc[s] >> 3), fl = (uint32_t)(sc[s] & 7), fm = (uint32_t)mn[s] * 0x01010101u;
+          const long bv = *(const long*)(xa + 32 * s);
+          ahi = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)(((uint64_t)(q1 * fh) << 32) | (q0 * fh)), bv, ahi, 0, 0, 0);
+          alo = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)(((uint64_t)(q1 * fl) << 32) | (q0 * fl)), bv, alo, 0, 0, 0);
+          amn = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)(((uint64_t)fm << 32) | fm), bv, amn, 0, 0, 0);
+        }
+      int* si = s_i + ((m * NB + b) * 2) * 4 * 64;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        si[r * 64 + lane] = 8 * ahi[r] + alo[r];
+        si[(4 + r) * 64 + lane] = amn[r];
+      }
+      if (g == 0) {
+        float* dd = s_dd + ((m * NB + b) * 16 + row) * 2;
+        dd[0] = half_bits_to_float((uint16_t)((uint32_t)h[0] & 0xffffu));
+        dd[1] = half_bits_to_float((uint16_t)((uint32_t)h[0] >> 16));
+      }
+    }
+  __syncthreads();
+  if (wave != 0) return;
   float res[NM][4];
 #pragma unroll
-  for (int m = 0; m < NM; ++m) q4m_tile<NB>(tl[m], a.qs, K, a.d, s_d, res[m]);
+  for (int m = 0; m < NM; ++m) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) res[m][r] = 0.0f;
+    for (int b = 0; b < NB; ++b) {
+      const float dxv = a.d[t * NB + b];
+      const int* si = s_i + ((m * NB + b) * 2) * 4 * 64;
+      const float* dd = s_dd + (m * NB + b) * 16 * 2;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float dm = __fmul_rn(dd[(4 * g + r) * 2], dxv), dmin = __fmul_rn(dd[(4 * g + r) * 2 + 1], dxv);
+        res[m][r] = __fadd_rn(res[m][r], __fmul_rn(dm, (float)si[r * 64 + lane]));
+        res[m][r] = __fsub_rn(res[m][r], __fmul_rn(dmin, (float)si[(4 + r) * 64 + lane]));
+      }
+    }
+  }
   if (t < T) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -1003,15 +1079,17 @@ void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_
       hipLaunchKernelGGL((k_gemm_f16<EPI, 48, NR>), dim3(blocks), block, f16_lds_bytes(k, NM * NR), s, desc, w, w2,
                          n, act.f16h, out);
     }
-  } else if (n % 16 == 0 && (k == 1024 || k == 2048 || (k == 3072 && EPI != 2))) {
-    // (the two-matrix tile at K = 3072 would spill: that shape takes the kernel below)
-    const size_t lds = 16 * 2 * 4;  // d|dmin of the tile's rows
+  } else if (n % 16 == 0 && (k == 1024 || k == 2048 || k == 3072)) {
+    constexpr int NM = EPI == 2 ? 2 : 1;
     if (k == 1024)
-      hipLaunchKernelGGL((k_gemm_q4m<EPI, 4>), dim3(n / 16), dim3(64), lds, s, desc, w, w2, n, act.q8k, out);
+      hipLaunchKernelGGL((k_gemm_q4m<EPI, 4>), dim3(n / 16), block, q4g_lds_bytes(4, NM), s, desc, w, w2, n, act.q8k,
+                         out);
     else if (k == 2048)
-      hipLaunchKernelGGL((k_gemm_q4m<EPI, 8>), dim3(n / 16), dim3(64), lds, s, desc, w, w2, n, act.q8k, out);
-    else if constexpr (EPI != 2)
-      hipLaunchKernelGGL((k_gemm_q4m<EPI, 12>), dim3(n / 16), dim3(64), lds, s, desc, w, w2, n, act.q8k, out);
+      hipLaunchKernelGGL((k_gemm_q4m<EPI, 8>), dim3(n / 16), block, q4g_lds_bytes(8, NM), s, desc, w, w2, n, act.q8k,
+                         out);
+    else
+      hipLaunchKernelGGL((k_gemm_q4m<EPI, 12>), dim3(n / 16), block, q4g_lds_bytes(12, NM), s, desc, w, w2, n,
+                         act.q8k, out);
   } else if (k <= kQ4MaxK) {
     constexpr int NM = EPI == 2 ? 2 : 1;
     const int blocks = std::min((n + 4 * kQ4GemmD - 1) / (4 * kQ4GemmD), kLmWorkgroups);
