@@ -369,8 +369,10 @@ __device__ __forceinline__ void attn_f16_load(const uint16_t* kb, const uint16_t
   for (int i = 0; i < 4; ++i) {
     const int p = i * 256 + (int)threadIdx.x, key = key0 + (p >> 4), d8 = (p & 15) * 8;
     if (key < kvlen) {
-      pk[i] = *(const v4i*)(kb + (size_t)key * kHeadDim + d8);
-      pv[i] = *(const v4i*)(vb + (size_t)key * kHeadDim + d8);
+      // streamed once per step: kept out of the caches, which then still hold the
+      // chunk partials when the merge (same XCD: kv head g) reads them
+      pk[i] = __builtin_nontemporal_load((const v4i*)(kb + (size_t)key * kHeadDim + d8));
+      pv[i] = __builtin_nontemporal_load((const v4i*)(vb + (size_t)key * kHeadDim + d8));
     } else {
       pk[i] = (v4i){0, 0, 0, 0};
       pv[i] = (v4i){0, 0, 0, 0};
