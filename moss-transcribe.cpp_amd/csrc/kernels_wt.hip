@@ -5,15 +5,21 @@
 //   k_act_f16 / k_act_q8k   rms_norm * gain, then mul_mat's conversion of the
 //                           activation to vec_dot_type (F16 for f16 weights,
 //                           Q8_K for q4_K)                src/qwen3.cpp:27-30,80,196
-//   k_gemm_f16 / k_gemm_q4k mul_mat(W, x) (+ add / silu*mul)
+//   k_gemm_f16 / k_gemm_q4m mul_mat(W, x) (+ add / silu*mul); k_gemm_q4k and
+//                           k_gemm_wt for other q4_K shapes
 //                                                         src/qwen3.cpp:92-97,192-193,204-216
-//   k_lm_head_wt            tied lm_head + cpu_greedy_choice keys
+//   k_lm_head_f16 / k_lm_head_q4m
+//                           tied lm_head + cpu_greedy_choice keys
 //                                                         src/qwen3_decoder.cpp:174-205,
 //                                                         src/cpu_speculative.cpp:39-50
+//   k_attn_combine_wt       the attention's chunk merge, written as the
+//                           o-projection's activation     src/qwen3.cpp:172-189
 //   k_embed_wt              get_rows / embed_rows_f32     src/generate.cpp:68-111
 //
 // Weights stay in the GGUF row layout: f16 [N][K] halves, q4_K [N][K/256] blocks
-// of 144 bytes. One wave computes one output row for all verify rows.
+// of 144 bytes. The f16 kernels stage the activation in LDS and give a wave a
+// group of rows; the q4_K kernels compute the exact integer sums of 16-row tiles
+// on int8 MFMA.
 //
 // Canonical orders (shared with the oracle, which restates them on the CPU):
 //   f16  : x rounded to f16; lane l of a wave takes the K/64 consecutive
