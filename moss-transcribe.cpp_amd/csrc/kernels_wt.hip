@@ -1026,15 +1026,18 @@ k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
   const int ngroups = (vocab + NR - 1) / NR, nwaves = gridDim.x * 4;
   const uint16_t* base[1] = {(const uint16_t*)w};
   int g = blockIdx.x * 4 + wave;
-  F16Group<SEG, 1, NR> bt;
+  // two groups in flight ahead of the one being computed
+  F16Group<SEG, 1, NR> bt, bt2;
   f16_load<SEG, 1, NR>(base, vocab, g * NR, bt);
+  if (g + nwaves < ngroups) f16_load<SEG, 1, NR>(base, vocab, (g + nwaves) * NR, bt2);
   for (int i = threadIdx.x; i < T * K / 8; i += 256) ((v4i*)s_x)[i] = ((const v4i*)xh)[i];
   __syncthreads();
   const int r = lane >> 4, t = lane & 15;
   uint64_t best = 0;  // lane (r, t): verify row t
   for (; g < ngroups; g += nwaves) {
     const F16Group<SEG, 1, NR> cur = bt;
-    if (g + nwaves < ngroups) f16_load<SEG, 1, NR>(base, vocab, (g + nwaves) * NR, bt);
+    bt = bt2;
+    if (g + 2 * nwaves < ngroups) f16_load<SEG, 1, NR>(base, vocab, (g + 2 * nwaves) * NR, bt2);
     float res[1];
     f16_group<SEG, 1, NR>(cur, s_x, T, s_p, res);
     const int row = g * NR + r;
@@ -1062,6 +1065,10 @@ k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
 
 // weight rows per wave and group of the f16 GEMM (NM * NR * 16 partial rows of LDS per wave)
 constexpr int f16_nr(int epi, int seg) { return seg == 16 ? (epi == 2 ? 2 : 4) : 1; }
+// at most one workgroup per CU (its LDS admits no second): more groups go to the
+// waves' loops, with the next group in flight, instead of a second round of
+// workgroups that would stage the activation again
+constexpr int kF16GemmWorkgroups = 256;
 
 template <int WT, int EPI>
 void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_t* w2, int n, int k,
@@ -1071,17 +1078,17 @@ void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_
     constexpr int NM = EPI == 2 ? 2 : 1;
     if (k == 1024) {
       constexpr int NR = f16_nr(EPI, 16);
-      const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kLmWorkgroups);
+      const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kF16GemmWorkgroups);
       hipLaunchKernelGGL((k_gemm_f16<EPI, 16, NR>), dim3(blocks), block, f16_lds_bytes(k, NM * NR), s, desc, w, w2,
                          n, act.f16h, out);
     } else if (k == 2048) {
       constexpr int NR = f16_nr(EPI, 32);
-      const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kLmWorkgroups);
+      const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kF16GemmWorkgroups);
       hipLaunchKernelGGL((k_gemm_f16<EPI, 32, NR>), dim3(blocks), block, f16_lds_bytes(k, NM * NR), s, desc, w, w2,
                          n, act.f16h, out);
     } else {
       constexpr int NR = f16_nr(EPI, 48);
-      const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kLmWorkgroups);
+      const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kF16GemmWorkgroups);
       hipLaunchKernelGGL((k_gemm_f16<EPI, 48, NR>), dim3(blocks), block, f16_lds_bytes(k, NM * NR), s, desc, w, w2,
                          n, act.f16h, out);
     }
