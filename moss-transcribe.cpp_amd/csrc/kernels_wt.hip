@@ -710,8 +710,8 @@ __device__ __forceinline__ void q4m_tile(const Q4Tile<NB>& tl, const int8_t* xq,
   }
 }
 
-// q4_K GEMM on the same tiles: one 256-thread workgroup per 16-row tile (and per
-// matrix pair for EPI 2). Wave w takes superblocks w, w + 4, ...: their exact
+// q4_K GEMM on the same tiles: one workgroup of 4 or 8 waves per 16-row tile (and
+// per matrix pair for EPI 2). Wave w takes superblocks w, w + NW, ...: their exact
 // int32 sums (dot, mins) of every (row, verify row) and the rows' d, dmin go to
 // LDS, and wave 0 runs the canonical float chain over the superblocks in order.
 // The activation operands come straight from the q8_K buffers (every tile reads
@@ -720,11 +720,15 @@ __host__ __device__ constexpr size_t q4g_lds_bytes(int nb, int nm) {
   return (size_t)nm * nb * (2 * 4 * 64 * 4 + 16 * 2 * 4);  // [m][b] (dot, mins) [2][4][64] + d|dmin [16][2]
 }
 
+// waves per tile: 8 for the long rows (K >= 2048), whose few tiles would leave
+// most of the machine idle with 4
+__host__ __device__ constexpr int q4g_waves(int nb) { return nb >= 8 ? 8 : 4; }
+
 template <int EPI, int NB>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * q4g_waves(NB))
 k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int n,
            ActQ8K a, float* __restrict__ out) {
-  constexpr int K = NB * 256, NM = EPI == 2 ? 2 : 1, NBW = (NB + 3) / 4;
+  constexpr int K = NB * 256, NM = EPI == 2 ? 2 : 1, NW = q4g_waves(NB), NBW = (NB + NW - 1) / NW;
   extern __shared__ v4i q4_lds_v4[];
   int* s_i = (int*)q4_lds_v4;                                 // [m][b][2][4][64]
   float* s_dd = (float*)(s_i + NM * NB * 2 * 4 * 64);        // [m][b][16][2]
@@ -738,7 +742,7 @@ k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
   for (int m = 0; m < NM; ++m)
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
-      const int b = wave + 4 * j;
+      const int b = wave + NW * j;
       if (b < NB) {
         const uint8_t* rb = base[m] + ((size_t)tile * 16 + row) * NB * 144 + b * 144;
 #pragma unroll
@@ -754,7 +758,7 @@ k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
   for (int m = 0; m < NM; ++m)
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
-      const int b = wave + 4 * j;
+      const int b = wave + NW * j;
       if (b >= NB) continue;
       const v4i h = head[m][j];
       int sc[8], mn[8];
@@ -1095,14 +1099,14 @@ void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_
   } else if (n % 16 == 0 && (k == 1024 || k == 2048 || k == 3072)) {
     constexpr int NM = EPI == 2 ? 2 : 1;
     if (k == 1024)
-      hipLaunchKernelGGL((k_gemm_q4m<EPI, 4>), dim3(n / 16), block, q4g_lds_bytes(4, NM), s, desc, w, w2, n, act.q8k,
-                         out);
+      hipLaunchKernelGGL((k_gemm_q4m<EPI, 4>), dim3(n / 16), dim3(64 * q4g_waves(4)), q4g_lds_bytes(4, NM), s, desc,
+                         w, w2, n, act.q8k, out);
     else if (k == 2048)
-      hipLaunchKernelGGL((k_gemm_q4m<EPI, 8>), dim3(n / 16), block, q4g_lds_bytes(8, NM), s, desc, w, w2, n, act.q8k,
-                         out);
+      hipLaunchKernelGGL((k_gemm_q4m<EPI, 8>), dim3(n / 16), dim3(64 * q4g_waves(8)), q4g_lds_bytes(8, NM), s, desc,
+                         w, w2, n, act.q8k, out);
     else
-      hipLaunchKernelGGL((k_gemm_q4m<EPI, 12>), dim3(n / 16), block, q4g_lds_bytes(12, NM), s, desc, w, w2, n,
-                         act.q8k, out);
+      hipLaunchKernelGGL((k_gemm_q4m<EPI, 12>), dim3(n / 16), dim3(64 * q4g_waves(12)), q4g_lds_bytes(12, NM), s,
+                         desc, w, w2, n, act.q8k, out);
   } else if (k <= kQ4MaxK) {
     constexpr int NM = EPI == 2 ? 2 : 1;
     const int blocks = std::min((n + 4 * kQ4GemmD - 1) / (4 * kQ4GemmD), kLmWorkgroups);
