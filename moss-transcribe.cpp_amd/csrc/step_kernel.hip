@@ -1043,7 +1043,7 @@ __device__ __forceinline__ void lm_head(const StepParams& P, float penalty, bool
   for (int cg = 0; cg < G; ++cg) best[cg] = 0;
   const int my_tiles = gw < n_tiles ? (n_tiles - 1 - gw) / nwaves + 1 : 0;
   const int units = my_tiles * cBH;  // (tile, pair) units of this wave, in order
-  constexpr int R = 16;
+  constexpr int R = 16;  // units of loads in flight per wave
   v4i ra[R];
   uint2 rs[R];
   const Rsrc re = mk_rsrc(uniform_ptr(P.embd), (uint32_t)((size_t)n_tiles * cBH * kUnitBytes));
@@ -1064,12 +1064,13 @@ __device__ __forceinline__ void lm_head(const StepParams& P, float penalty, bool
 #pragma unroll
   for (int i = 0; i < R; ++i) issue(i, i);
   float part[4][G][4];
-  // units is a multiple of cBH, and cBH of R: a pass of R units is whole
-  static_assert(cBH % R == 0, "ring depth divides the pairs of a tile");
+  // A pass of R units may end inside a tile; the last pass stops at this wave's
+  // last unit (units is wave-uniform, so the whole wave leaves together).
   for (int u0 = 0; u0 < units; u0 += R) {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int u = u0 + i;
+      if (u >= units) break;
       const int bp = u % cBH, sl = bp >> 2;
       if (bp == 0) {
         if (pen) {
