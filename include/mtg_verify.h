@@ -296,6 +296,19 @@ int mtg_q8_unpack(const mtg_q8_packed* p, void* blocks);
  * quantized to q8_0 per 32-block on the device), T in 1..MTG_MAX_BATCH. */
 int mtg_q8_mul_mat_dev(const mtg_q8_packed* w, const float* x_dev, int32_t T, float* y_dev);
 
+/* mtg_q8_mul_mat_dev without any allocation (no counterpart in the reference;
+ * for callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The descriptor and the
+ * activation panel live in one static device array per GPU (about 137 KiB, held
+ * until the process ends) instead of per-call hipMalloc; K is limited to 4096
+ * (MTG_ERR_CAPACITY above, with the reason in mtg_last_error(NULL)). The call
+ * enqueues three kernels on `stream` (NULL: the default stream) and returns
+ * without waiting; the caller synchronizes. Every call on one GPU shares the
+ * array, so calls that overlap on one GPU (other streams, other threads) race:
+ * serialize them. */
+int mtg_q8_mul_mat_dev_noalloc(const mtg_q8_packed* w, const float* x_dev, int32_t T, float* y_dev,
+                               void* stream);
+
 /* out_dev[h][q][f] = sum_{k <= past+q} v[h/groups][k][f] * p[h][q][k]
  * v_dev: [kv_heads][kv_len][head_dim] f32, p_dev: [heads][queries][kv_len] f32,
  * past = kv_len - queries; each query reads exactly its valid length. */

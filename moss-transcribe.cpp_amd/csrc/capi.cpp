@@ -421,6 +421,19 @@ struct mtg_q8_packed {
   int k = 0, n = 0;
 };
 
+}  // extern "C"
+
+namespace mtg {
+void set_call_error(const std::string& msg) { g_create_error = msg; }
+const uint8_t* q8_packed_view(const mtg_q8_packed* p, int* k, int* n) {
+  *k = p->k;
+  *n = p->n;
+  return p->tiles;
+}
+}  // namespace mtg
+
+extern "C" {
+
 int mtg_q8_pack(const void* blocks, int32_t k, int32_t n, mtg_q8_packed** out) {
   if (!blocks || !out || k <= 0 || n <= 0) return MTG_ERR_INVALID;
   if (k % 64 || n % 16) return MTG_ERR_UNSUPPORTED;

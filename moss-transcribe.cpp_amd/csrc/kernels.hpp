@@ -5,9 +5,16 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <string>
+
 #include "mtg_internal.hpp"
 
 namespace mtg {
+
+// Error text of the calls without a context (mtg_last_error(NULL)).
+void set_call_error(const std::string& msg);
+// Device tiles and shape of a packed q8_0 matrix.
+const uint8_t* q8_packed_view(const mtg_q8_packed* p, int* k, int* n);
 
 // Activation panel of one GEMM input (B operand, see mtg_internal.hpp).
 struct Panel {

@@ -110,6 +110,7 @@ SIGNATURES = {
     "mtg_q8_free": (None, [c_void_p]),
     "mtg_q8_unpack": (c_int32, [c_void_p, c_void_p]),
     "mtg_q8_mul_mat_dev": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
+    "mtg_q8_mul_mat_dev_noalloc": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p]),
     "mtg_causal_context_dev": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
                                          c_int32, c_void_p]),
     "mtg_synth_create": (c_int32, [POINTER(Hparams), c_int32, c_uint64, c_float, c_float,
