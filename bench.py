@@ -17,11 +17,24 @@ algorithmic bytes of a step (q8_0 weights + KV read of past + T rows + KV write 
 T rows) / the mean event time. traffic: HBM bytes per launch from rocprofv3
 FETCH_SIZE + WRITE_SIZE (profiles/traffic.json), reported only when that file was
 measured on the current kernel sources, else null.
+
+cpu_baseline (reference protocol, cpu-lab/moss_causal_context_bench.cpp:184-222:
+one discarded warmup pair, then 5 alternating measured pairs, median and range):
+the KV cache is snapshotted at the start of the timed region; the oracle (the CPU
+restatement of the reference path, C++/OpenMP, one thread per core of this
+process's CPU share, pinned) and the GPU each verify the same batch (the first
+K ids of the timed stream) from that state, alternating; their choices must be
+equal. Then the oracle replays the GPU's timed steps from the snapshot, as many as
+fit the --cpu-seconds budget; its ids must equal the GPU's prefix. value =
+committed tokens / time of that replay. The CPU leg runs after the GPU
+measurement, and a failure in it is reported inside cpu_baseline without losing
+the GPU fields.
 """
-import hashlib
 import argparse
+import hashlib
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -31,12 +44,17 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [os.path.join(ROOT, "moss-transcribe.cpp_amd"), os.path.join(ROOT, "oracle")]
 
 import mtg  # noqa: E402
+from workloads import AUDIO_ROWS, CONFIGS, WNAME, build_prompt, prompt_rows  # noqa: E402
 
 METRIC = "verify-step µs + accepted tok/s (q8_0, K=8, ctx 1.6k); % of HBM peak"
 HBM_PEAK_GBS = 8000.0
 KERNEL = "k_step"  # the dominant kernel: the whole verify step
 CSRC = os.path.join(ROOT, "moss-transcribe.cpp_amd", "csrc")
 TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
 
 
 def source_hash():
@@ -60,17 +78,6 @@ def measured_traffic(config):
         return None
     return t.get("traffic_bytes_per_launch")
 
-# (weight type, kv type, audio blocks, text ids, K rows, decode steps)
-CONFIGS = {
-    1: dict(wtype=mtg.TYPE_Q8_0, kv=mtg.TYPE_F32, blocks=0, text=512, K=4, steps=1),
-    2: dict(wtype=mtg.TYPE_Q8_0, kv=mtg.TYPE_F32, blocks=4, text=100, K=8, steps=256),
-    3: dict(wtype=mtg.TYPE_Q8_0, kv=mtg.TYPE_F16, blocks=10, text=250, K=16, steps=128),
-    4: dict(wtype=mtg.TYPE_F16, kv=mtg.TYPE_F16, blocks=20, text=500, K=8, steps=128),
-    5: dict(wtype=mtg.TYPE_Q4_K, kv=mtg.TYPE_F16, blocks=43, text=259, K=16, steps=64),
-}
-AUDIO_ROWS = 375
-STREAM_PERIOD = 37
-
 
 def weight_bytes(hp, wtype):
     H, D, F = hp.hidden, hp.head_dim, hp.intermediate
@@ -84,53 +91,92 @@ def kv_bytes_per_pos(hp, kv):
     return hp.n_layers * 2 * hp.n_kv_heads * hp.head_dim * (4 if kv == mtg.TYPE_F32 else 2)
 
 
-def build_prompt(model, dec, cfg):
-    """Fused prompt rows: audio blocks (N(0,1) scaled to the embedding RMS) + text ids."""
-    hp = model.hp
-    rng = np.random.default_rng(1)
-    text = rng.integers(0, hp.vocab, cfg["text"]).astype(np.int32)
-    sample = dec.embed(np.arange(0, hp.vocab, max(1, hp.vocab // 2048))[:2048])
-    rms = float(np.sqrt((sample.astype(np.float64) ** 2).mean()))
-    n_audio = cfg["blocks"] * AUDIO_ROWS
-    audio = mtg.normal(1, 0, n_audio * hp.hidden).reshape(n_audio, hp.hidden) * np.float32(rms)
-    rows = np.concatenate([audio, dec.embed(text)]) if n_audio else dec.embed(text)
-    stream = np.random.default_rng(2).integers(0, hp.vocab, STREAM_PERIOD).astype(np.int32)
-    return rows.astype(np.float32), text, stream
+def cpu_threads():
+    """Threads for the CPU leg: one per core of this process's CPU share
+    (OMP_NUM_THREADS when the environment sets it lower than the affinity mask)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return n
 
 
-def cpu_baseline(model, dec, cfg, first_seed, prior, drafter, budget_s):
-    """The oracle (CPU restatement of the reference path) on this host's cores,
-    from the same KV state, on a bounded number of verify steps."""
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(model, dec, cfg, snap, budget_s):
+    """The oracle beside the GPU from the KV state at the start of the timed run.
+    snap: (k, v, ctx_start, first_seed, prior ids, GPU timed ids, GPU steps, drafter)."""
+    k, v, ctx_start, seed0, prior, gpu_ids, gpu_steps, drafter = snap
+    threads = cpu_threads()
+    # the host as this process sees it, before the OpenMP runtime pins the threads
+    host = {"cpu_model": cpu_model(), "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
+    # pinning: read by the OpenMP runtime when the oracle library loads
+    os.environ.setdefault("OMP_PROC_BIND", "close")
+    os.environ.setdefault("OMP_PLACES", "cores")
     import oracle_py
-    threads = len(os.sched_getaffinity(0))
     oracle_py.lib().orc_set_threads(threads)
     orc = oracle_py.Oracle(model, dec.max_seq, cfg["kv"])
-    past = dec.past_len
-    k, v = dec.kv_read(past)
-    orc.kv_write(k, v)
-    fn, user, _keep = drafter
-    # one warm step, then steps until the budget is used
-    t0 = time.perf_counter()
-    ids, st = orc.generate_from(first_seed, 1 << 20, max_steps=1, penalty=1.0, max_draft=cfg["K"] - 1,
-                                draft=fn, user=user, prior=prior)
-    seed = st.next_seed
-    prior = np.concatenate([prior, ids])
-    steps = tokens = 0
-    t_steps = 0.0
-    while t_steps < budget_s or steps < 2:
-        t1 = time.perf_counter()
-        ids, st = orc.generate_from(seed, 1 << 20, max_steps=1, penalty=1.0,
-                                    max_draft=cfg["K"] - 1, draft=fn, user=user, prior=prior)
-        t_steps += time.perf_counter() - t1
-        steps += 1
-        tokens += len(ids)
-        seed = st.next_seed
-        prior = np.concatenate([prior, ids])
-    orc.close()
-    return {"value": tokens / t_steps, "unit": "tok/s", "cores": threads, "kind": "port",
-            "ms_per_step": 1e3 * t_steps / steps,
-            "sample": "%d verify steps (K=%d) of the same workload from the GPU's KV state, "
-                      "oracle C++/OpenMP on %d host threads" % (steps, cfg["K"], threads)}
+    try:
+        orc.kv_write(k, v)
+        K = cfg["K"]
+        tokens = np.asarray(gpu_ids[:K], np.int32)
+        if len(tokens) < 1:
+            raise RuntimeError("the timed run emitted no ids")
+        hist = np.asarray(prior, np.int32)
+        gpu_ms, cpu_ms = [], []
+        for pair in range(6):  # pair 0 is the discarded warmup
+            dec.rewind(ctx_start)
+            t0 = time.perf_counter()
+            c_gpu, m_gpu, _, _ = dec.verify(tokens, history=hist)
+            t1 = time.perf_counter()
+            orc.rewind(ctx_start)
+            t2 = time.perf_counter()
+            c_cpu, m_cpu, _, _ = orc.verify(tokens, history=hist)
+            t3 = time.perf_counter()
+            if not (np.array_equal(c_gpu, c_cpu) and m_gpu == m_cpu):
+                raise RuntimeError("pair %d: GPU choices %s / %d differ from the oracle's %s / %d"
+                                   % (pair, c_gpu.tolist(), m_gpu, c_cpu.tolist(), m_cpu))
+            if pair:
+                gpu_ms.append(1e3 * (t1 - t0))
+                cpu_ms.append(1e3 * (t3 - t2))
+        log("cpu leg: pairs done, CPU verify median %.1f ms" % statistics.median(cpu_ms))
+        # replay of the GPU's timed steps, bounded by the time budget
+        n_steps = int(max(2, min(gpu_steps, budget_s / (statistics.median(cpu_ms) * 1e-3))))
+        orc.rewind(ctx_start)
+        fn, user, _keep = drafter
+        t0 = time.perf_counter()
+        ids, st = orc.generate_from(seed0, 1 << 20, max_steps=n_steps, penalty=1.0, max_draft=K - 1,
+                                    draft=fn, user=user, prior=prior)
+        t_replay = time.perf_counter() - t0
+        same = bool(np.array_equal(ids, np.asarray(gpu_ids[:len(ids)], np.int32)))
+        if not same:
+            raise RuntimeError("oracle replay of %d steps emitted ids that differ from the GPU's" % n_steps)
+        log("cpu leg: replayed %d steps in %.1f s, ids identical to the GPU's" % (n_steps, t_replay))
+        return {"value": len(ids) / t_replay, "unit": "tok/s", "cores": threads, "kind": "port",
+                "sample": "first %d of the GPU's timed verify steps (K=%d, context %d+), replayed by the "
+                          "oracle (C++/OpenMP restatement of the reference path) from the same KV "
+                          "snapshot; %d ids, identical to the GPU's" % (n_steps, K, ctx_start, len(ids)),
+                "ms_per_step": 1e3 * t_replay / n_steps,
+                "pairs": {"protocol": "1 warmup + 5 alternating GPU/CPU pairs, same verify batch "
+                                      "(T=%d at past %d), choices equal in every pair" % (len(tokens), ctx_start),
+                          "cpu_verify_ms_median": statistics.median(cpu_ms),
+                          "cpu_verify_ms_range": [min(cpu_ms), max(cpu_ms)],
+                          "gpu_verify_ms_median": statistics.median(gpu_ms),
+                          "gpu_verify_ms_range": [min(gpu_ms), max(gpu_ms)]},
+                "host": dict(host, threads=threads, OMP_PROC_BIND=os.environ.get("OMP_PROC_BIND"),
+                             OMP_PLACES=os.environ.get("OMP_PLACES")),
+                "stream_identical": same}
+    finally:
+        orc.close()
 
 
 def main():
@@ -151,14 +197,15 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box here has one MI355X, and the verify path "
-              "shards only across independent streams (one decoder per recording, one GPU each).", file=sys.stderr)
+              "shards only across independent streams (one decoder per recording, one GPU each).",
+              file=sys.stderr)
         sys.exit(2)
     cfg = CONFIGS[args.config]
     steps = args.steps if args.steps is not None else cfg["steps"]
     t_setup = time.perf_counter()
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0, n_layers=args.layers)
     hp = model.hp
-    n_prompt = cfg["blocks"] * AUDIO_ROWS + cfg["text"]
+    n_prompt = prompt_rows(cfg)
     max_seq = n_prompt + (args.warmup + steps + 2) * cfg["K"] + 16
     dec = mtg.Decoder(model, max_seq, cfg["kv"])
     if args.exec == "step" and dec.exec_mode != mtg.EXEC_STEP_KERNEL:
@@ -166,17 +213,18 @@ def main():
         # per-op kernels from a captured graph
         args.exec = "graph"
     dec.set_exec({"step": mtg.EXEC_STEP_KERNEL, "graph": mtg.EXEC_GRAPH, "eager": mtg.EXEC_EAGER}[args.exec])
-    rows, text, stream = build_prompt(model, dec, cfg)
+    rows, text, stream = build_prompt(model, dec.embed, cfg)
     hid = dec.prefill(rows)
     first = int(np.argmax(dec.logits(hid[-1:])[0]))
     drafter = mtg.stream_drafter(text, stream)
     fn, user, _keep = drafter
-    print("setup %.1fs: prompt %d rows, max_seq %d" % (time.perf_counter() - t_setup, n_prompt, max_seq),
-          file=sys.stderr, flush=True)
+    log("setup %.1fs: prompt %d rows, max_seq %d" % (time.perf_counter() - t_setup, n_prompt, max_seq))
     # warmup
     ids_w, st_w = dec.generate_from(first, 1 << 20, max_steps=args.warmup, max_draft=cfg["K"] - 1,
                                     draft=fn, user=user)
     ctx_start = dec.past_len
+    # KV snapshot for the CPU leg (outside the timed region)
+    snap_kv = dec.kv_read(ctx_start) if not args.no_cpu else None
     import ctypes
     hip = ctypes.CDLL("libamdhip64.so")
     hip.hipDeviceSynchronize()
@@ -190,6 +238,8 @@ def main():
     dec.launch_timing(False)
     n_steps = int(st.target_calls)
     tokens = len(ids)
+    log("timed: %d steps, %d tokens in %.3f s (%.1f us per launch)"
+        % (n_steps, tokens, elapsed, 1e3 * dev_ms / max(launches, 1)))
     ms_step = 1e3 * elapsed / max(n_steps, 1)
     kvpos = kv_bytes_per_pos(hp, cfg["kv"])
     # algorithmic bytes of one launch: weights + KV read of past + T rows + KV write of T rows
@@ -213,8 +263,7 @@ def main():
         "data": "synthetic: seeded random weights, seeded audio-like prompt rows and draft stream",
         "config": {"workload": "Qwen3-0.6B-shaped verify step, %d layers, K=%d rows, %s weights, "
                                "%s KV, %d-row prompt (%d audio + %d text), %d greedy steps"
-                               % (hp.n_layers, cfg["K"], {mtg.TYPE_Q8_0: "q8_0", mtg.TYPE_F16: "f16",
-                                                          mtg.TYPE_Q4_K: "q4_K"}[cfg["wtype"]],
+                               % (hp.n_layers, cfg["K"], WNAME[cfg["wtype"]],
                                   "f32" if cfg["kv"] == mtg.TYPE_F32 else "f16", n_prompt,
                                   cfg["blocks"] * AUDIO_ROWS, cfg["text"], n_steps),
                    "verify_rows": cfg["K"], "context_start": ctx_start, "context_end": dec.past_len,
@@ -231,8 +280,12 @@ def main():
         "source_hash": source_hash(),
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(model, dec, cfg, st.next_seed,
-                                           np.concatenate([ids_w, ids]), drafter, args.cpu_seconds)
+        try:
+            snap = (snap_kv[0], snap_kv[1], ctx_start, st_w.next_seed, ids_w, ids, n_steps, drafter)
+            out["cpu_baseline"] = cpu_baseline(model, dec, cfg, snap, args.cpu_seconds)
+        except Exception as e:  # the GPU fields stay; the failure is reported in place
+            out["cpu_baseline"] = {"value": None, "unit": "tok/s", "error": "%s: %s" % (type(e).__name__, e)}
+            log("cpu leg failed: %s" % e)
     if args.copy_probe_mib > 0:
         import torch
         n = args.copy_probe_mib << 18  # float32 elements
@@ -242,7 +295,7 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         out["copy_probe_bytes"] = n * 4
-    print(json.dumps(out))
+    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

@@ -169,7 +169,7 @@ typedef void (*mtg_commit_fn)(void* user, const int32_t* ids, int32_t n_ids, int
 typedef struct mtg_gen_stats {
   int64_t target_calls, drafted_calls, proposed, accepted, target_input_tokens, rewinds;
   double prefill_seconds, verify_seconds, draft_seconds;
-  int32_t stop_reason; /* 0 none/error, 1 eos, 2 token_limit */
+  int32_t stop_reason; /* 0 none/error, 1 eos, 2 token_limit, 3 KV cache full */
   int32_t next_seed;   /* greedy choice of the last kept row (the next step's seed) */
 } mtg_gen_stats;
 
@@ -253,6 +253,15 @@ int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes);
  * wait that ran out. The step returns MTG_ERR_DEVICE without advancing past_len;
  * the following steps run normally. */
 int mtg_debug_abort_next_step(mtg_ctx* ctx);
+
+/* Bounded waits (no counterpart in the reference): every wait of the persistent
+ * step kernel gives up after a poll limit or 50 ms of device clock, raising the
+ * error word so that every workgroup leaves; the step then runs again on the
+ * per-op kernels (which need no co-resident workgroups) and
+ * mtg_step_fallbacks counts it. mtg_debug_wait_limit sets the poll limit (<= 0:
+ * the default, 2^23) so that a test can force that path from the host. */
+int mtg_debug_wait_limit(mtg_ctx* ctx, int32_t polls);
+int64_t mtg_step_fallbacks(const mtg_ctx* ctx);
 
 /* Profiling of the persistent step kernel: when enabled, the kernel records a
  * 100 MHz device clock into MTG_PROFILE_SLOTS slots. Workgroup 0, slots 0..1023:

@@ -120,6 +120,17 @@ int mtg_debug_abort_next_step(mtg_ctx* ctx) {
   return MTG_OK;
 }
 
+int mtg_debug_wait_limit(mtg_ctx* ctx, int32_t polls) {
+  if (!ctx) return MTG_ERR_INVALID;
+  Ctx& c = ctx->impl;
+  if (!c.step_ok) return c.fail(MTG_ERR_UNSUPPORTED, "no step kernel");
+  c.params_host.wait_polls = polls > 0 ? (uint32_t)polls : mtg::kWaitPolls;
+  return c.check(hipMemcpy(c.params_dev, &c.params_host, sizeof(c.params_host), hipMemcpyHostToDevice),
+                 "step params");
+}
+
+int64_t mtg_step_fallbacks(const mtg_ctx* ctx) { return ctx ? ctx->impl.step_fallbacks : 0; }
+
 int mtg_debug_copy(mtg_ctx* ctx, int32_t which, void* out, size_t bytes) {
   if (!ctx || !out) return MTG_ERR_INVALID;
   const Ctx& c = ctx->impl;
@@ -294,6 +305,12 @@ int mtg_speculative_run(const mtg_target* tg, int32_t first_seed, const int32_t*
         break;
       }
       const int before = *tg->past;
+      if (tg->max_seq - before < 1) {
+        // no room for the seed's row: the reference's append fails and its loop
+        // breaks with the seed emitted (src/cpu_speculative.cpp:113-114)
+        stop = 3;
+        break;
+      }
       const int budget = std::max(0, std::min({max_draft, max_new - (int)(ids.size() - first_new),
                                                tg->max_seq - before - 1}));
       auto t0 = std::chrono::steady_clock::now();

@@ -296,6 +296,8 @@ int Ctx::init_step_kernel() {
   P.flags = (uint32_t*)dalloc((size_t)nwg * kFlagStride * 4, true);
   P.qkvt = (uint32_t*)dalloc(qkvt_bytes(), true);
   P.err = &result_dev->err;
+  P.wait_polls = kWaitPolls;
+  P.wait_ticks = kWaitTicks;
   P.timing = nullptr;
   params_dev = (StepParams*)dalloc(sizeof(StepParams), false);
   if (!P.part_ml || !P.part_o || !P.part_keys || !P.flags || !P.qkvt || !P.oq || !P.oqs || !P.aq || !P.aqs ||
@@ -391,15 +393,12 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
   const int G = (T + 7) / 8;
   int rc = MTG_OK;
   const bool step_mode = mode == kModeVerify || mode == kModeVerifyPenalty || mode == kModeAppend;
-  // the step kernel takes the descriptor as a kernel argument; the per-op kernels
-  // read it from device memory
-  if (!(exec == kExecStep && step_ok && step_mode) &&
-      (rc = check(hipMemcpyAsync(desc_dev, desc_host, sizeof(StepDesc), hipMemcpyHostToDevice, stream),
-                  "step descriptor")))
-    return rc;
+  const bool on_step = exec == kExecStep && step_ok && step_mode;
   const bool timed = timing && mode != kModeLogits;
   if (timed && (rc = check(hipEventRecord(ev_start, stream), "timing event"))) return rc;
-  if (exec == kExecStep && step_ok && step_mode) {
+  bool aborting = false;
+  if (on_step) {
+    // the step kernel takes the descriptor as a kernel argument
     if (epoch > 0xF0000000u) {  // progress words restart before they could wrap
       if ((rc = check(hipMemsetAsync(params_host.flags, 0, (size_t)nwg * kFlagStride * 4, stream), "flags"))) return rc;
       // the tags of the exchanged q|k|v values come from the same counter
@@ -411,6 +410,7 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
     result_host->err = 0;
     if (abort_next) {
       abort_next = false;
+      aborting = true;
       if ((rc = check(hipMemsetAsync(&result_dev->err, 1, sizeof(int32_t), stream), "abort")))
         return rc;
     }
@@ -418,40 +418,42 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
                                     params_host.timing != nullptr), "step kernel launch")))
       return rc;
     epoch += step_progress_per_step(hp.n_layers);
-  } else if (exec != kExecEager) {
-    GraphSlot& slot = graphs[(G - 1) * kModes + mode];
-    if (!slot.exec) {
-      hipGraph_t g = nullptr;
-      if ((rc = check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "capture")))
-        return rc;
-      enqueue(G, mode);
-      if ((rc = check(hipStreamEndCapture(stream, &g), "end capture"))) return rc;
-      rc = check(hipGraphInstantiate(&slot.exec, g, nullptr, nullptr, 0), "instantiate");
-      hipGraphDestroy(g);
-      if (rc) return rc;
-    }
-    if ((rc = check(hipGraphLaunch(slot.exec, stream), "graph launch"))) return rc;
   } else {
-    enqueue(G, mode);
-    if ((rc = check(hipGetLastError(), "kernel launch"))) return rc;
+    if ((rc = enqueue_per_op(G, mode))) return rc;
   }
   if (timed && (rc = check(hipEventRecord(ev_stop, stream), "timing event"))) return rc;
   // the step kernel's verify writes its choices into the mapped host buffer; the
   // other paths (per-op kernels, appends) bring the result over with a copy
-  const bool mapped = exec == kExecStep && step_ok && (mode == kModeVerify || mode == kModeVerifyPenalty);
+  const bool mapped = on_step && (mode == kModeVerify || mode == kModeVerifyPenalty);
   if (!mapped && (rc = check(hipMemcpyAsync(result_host, result_dev, sizeof(StepResult),
                                              hipMemcpyDeviceToHost, stream), "result")))
     return rc;
-  if (want_hidden && hidden_out &&
-      (rc = check(hipMemcpyAsync(hidden_out, hid, (size_t)T * hp.hidden * 4, hipMemcpyDeviceToHost,
-                                 stream), "hidden")))
-    return rc;
-  if (want_logits && logits_out &&
-      (rc = check(hipMemcpyAsync(logits_out, logits, (size_t)T * hp.vocab * 4,
-                                 hipMemcpyDeviceToHost, stream), "logits")))
-    return rc;
   if ((rc = check(hipStreamSynchronize(stream), "step"))) return rc;
-  if (timed) {
+  if (mapped && result_host->n_match < 0) {
+    // the kernel left before its acceptance: a bounded wait ran out
+    (void)hipMemcpy(&result_host->err, &result_dev->err, sizeof(int32_t), hipMemcpyDeviceToHost);
+    if (!result_host->err) return fail(MTG_ERR_DEVICE, "step kernel: no result");
+  }
+  if (result_host->err) {
+    // a bounded wait ran out and every workgroup left the kernel; only positions
+    // from `past` on were written, so the step can run again
+    (void)hipMemset(&result_dev->err, 0, sizeof(int32_t));
+    result_host->err = 0;
+    if (aborting || !on_step)
+      return fail(MTG_ERR_DEVICE, "step kernel: a bounded wait ran out (step abandoned)");
+    // the same step on the per-op kernels (its workgroups need no co-residency)
+    ++step_fallbacks;
+    if ((rc = enqueue_per_op(G, mode))) return rc;
+    if ((rc = check(hipMemcpyAsync(result_host, result_dev, sizeof(StepResult), hipMemcpyDeviceToHost,
+                                   stream), "result")))
+      return rc;
+    if ((rc = check(hipStreamSynchronize(stream), "fallback step"))) return rc;
+    if (timed) {
+      ++timing_launches;  // counted, not timed: the event pair covers the abandoned launch
+      timing_past += desc_host->past;
+      timing_rows += T;
+    }
+  } else if (timed) {
     float ms = 0.0f;
     if ((rc = check(hipEventElapsedTime(&ms, ev_start, ev_stop), "timing"))) return rc;
     timing_ms += ms;
@@ -459,18 +461,36 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
     timing_past += desc_host->past;
     timing_rows += T;
   }
-  if (mapped && result_host->n_match < 0) {
-    // the kernel left before its acceptance: a bounded wait ran out
-    (void)hipMemcpy(&result_host->err, &result_dev->err, sizeof(int32_t), hipMemcpyDeviceToHost);
-    if (!result_host->err) return fail(MTG_ERR_DEVICE, "step kernel: no result");
-  }
-  if (result_host->err) {
-    // a bounded barrier wait ran out: every workgroup left the kernel
-    (void)hipMemset(&result_dev->err, 0, sizeof(int32_t));
-    result_host->err = 0;
-    return fail(MTG_ERR_DEVICE, "step kernel: grid barrier wait timed out");
-  }
+  if (want_hidden && hidden_out &&
+      (rc = check(hipMemcpy(hidden_out, hid, (size_t)T * hp.hidden * 4, hipMemcpyDeviceToHost), "hidden")))
+    return rc;
+  if (want_logits && logits_out &&
+      (rc = check(hipMemcpy(logits_out, logits, (size_t)T * hp.vocab * 4, hipMemcpyDeviceToHost), "logits")))
+    return rc;
   return MTG_OK;
+}
+
+// The per-op kernels of one step: the descriptor goes to device memory, then
+// the captured graph (or the eager sequence) runs on the stream.
+int Ctx::enqueue_per_op(int G, int mode) {
+  int rc = check(hipMemcpyAsync(desc_dev, desc_host, sizeof(StepDesc), hipMemcpyHostToDevice, stream),
+                 "step descriptor");
+  if (rc) return rc;
+  if (exec == kExecEager) {
+    enqueue(G, mode);
+    return check(hipGetLastError(), "kernel launch");
+  }
+  GraphSlot& slot = graphs[(G - 1) * kModes + mode];
+  if (!slot.exec) {
+    hipGraph_t g = nullptr;
+    if ((rc = check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "capture"))) return rc;
+    enqueue(G, mode);
+    if ((rc = check(hipStreamEndCapture(stream, &g), "end capture"))) return rc;
+    rc = check(hipGraphInstantiate(&slot.exec, g, nullptr, nullptr, 0), "instantiate");
+    hipGraphDestroy(g);
+    if (rc) return rc;
+  }
+  return check(hipGraphLaunch(slot.exec, stream), "graph launch");
 }
 
 void Ctx::fill_desc(int T, bool use_embeds, float penalty, const int32_t* tokens,

@@ -37,6 +37,7 @@ struct Ctx {
   bool step_ok = false;  // the persistent step kernel is usable for this model / device
   uint32_t epoch = 0;
   bool abort_next = false;  // raise the error word before the next step-kernel launch
+  int64_t step_fallbacks = 0;  // steps rerun on the per-op kernels after a wait ran out
   StepParams* params_dev = nullptr;
   StepParams params_host{};
   uint64_t* timing_dev = nullptr;  // step-kernel phase clock marks (profiling)
@@ -88,6 +89,7 @@ struct Ctx {
                  const int32_t* history, int n_history, bool write_logits);
   int run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_out,
           float* logits_out);
+  int enqueue_per_op(int G, int mode);
   int verify(const int32_t* tokens, int T, const int32_t* history, int n_history, float penalty,
              int32_t* choice_out, int32_t* n_match_out, float* hidden_out, float* logits_out);
   int append(const float* embeds, int T, float* hidden_out);

@@ -39,7 +39,6 @@ using namespace dev;
 
 constexpr int kT = 256;                 // threads per workgroup
 constexpr int kNwg = 256;               // workgroups (one per CU)
-constexpr unsigned kSpin = 1u << 23;    // bounded waits
 // shapes the kernel is written for (Qwen3-0.6B)
 constexpr int cH = 1024, cQN = 2048, cNQKV = 4096, cF = 3072, cNH = 16, cNKV = 8, cHD = 128;
 constexpr int cBH = cH / kPairK, cBQ = cQN / kPairK, cBF = cF / kPairK;  // 16, 32, 48
@@ -113,6 +112,18 @@ struct Ctl {
   int* s_ok;
 };
 
+// A wait's bound: P.wait_polls polls, or P.wait_ticks of the device clock from
+// its 256th poll on (read only every 256 polls, so a short wait never reads it).
+__device__ __forceinline__ bool wait_expired(const StepParams& P, unsigned spins, uint64_t& t0) {
+  if (spins > P.wait_polls) return true;
+  if ((spins & 255u) == 0u) {
+    const uint64_t now = wall_clock64();
+    if (spins == 256u) t0 = now;
+    else if (now - t0 > (uint64_t)P.wait_ticks) return true;
+  }
+  return false;
+}
+
 // All of this thread's stores have completed; then workgroup w announces v.
 __device__ __forceinline__ void publish(Ctl& c, uint32_t v) {
   if (v <= c.published) return;
@@ -135,6 +146,7 @@ __device__ __forceinline__ bool wait_all(Ctl& c, uint32_t v, int prof_slot = -1)
     const Rsrc re = mk_rsrc(P.err, 4);
     const uint32_t target = c.epoch + v;
     unsigned spins = 0;
+    uint64_t t0 = 0;
     int ok = 1;
     // lane j watches the words of workgroups j, j+64, j+128, j+192 and keeps a
     // bit per word that has reached the target. The four loads issue back to
@@ -155,7 +167,7 @@ __device__ __forceinline__ bool wait_all(Ctl& c, uint32_t v, int prof_slot = -1)
       have = hv == (1u << (kNwg / 64)) - 1;
       if (__all(have)) break;
       if (__builtin_amdgcn_raw_buffer_load_b32(re, 0, 0, 16)) { ok = 0; break; }
-      if (++spins > kSpin) {
+      if (wait_expired(P, ++spins, t0)) {
         if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32(1u, re, 0, 0, 16);
         ok = 0;
         break;
@@ -181,13 +193,14 @@ template <int N>
 __device__ __forceinline__ void tagged_wait(const StepParams& P, Rsrc r, v2u (&a)[N], const uint32_t (&off)[N],
                                             const bool (&live)[N], uint32_t want) {
   const Rsrc re = mk_rsrc(P.err, 4);
+  uint64_t t0 = 0;
   for (unsigned spins = 0;; ++spins) {
     bool stale = false;
 #pragma unroll
     for (int j = 0; j < N; ++j) stale |= live[j] && a[j].y != want;
     if (!__any(stale)) return;
     if (__builtin_amdgcn_raw_buffer_load_b32(re, 0, 0, 16)) return;
-    if (spins > kSpin) {
+    if (spins > 0 && wait_expired(P, spins, t0)) {
       if ((threadIdx.x & 63) == 0) __builtin_amdgcn_raw_buffer_store_b32(1u, re, 0, 0, 16);
       return;
     }

@@ -20,6 +20,9 @@ struct LayerDev {
 
 // Layers the step kernel's parameter block holds.
 constexpr int kStepMaxLayers = 48;
+// Default wait bounds: 2^23 polls, 50 ms.
+constexpr uint32_t kWaitPolls = 1u << 23;
+constexpr uint32_t kWaitTicks = 5000000u;
 
 // Constant for a context; lives in device memory.
 struct StepParams {
@@ -46,6 +49,9 @@ struct StepParams {
   // the progress value of the phase that wrote it, so a reader needs no flag
   uint32_t* qkvt;
   int32_t* err;             // raised by a wait that ran out (inside *result)
+  // bounds of every wait: polls, and device-clock ticks (100 MHz) measured from
+  // the wait's 256th poll, checked every 256 polls
+  uint32_t wait_polls, wait_ticks;
   uint64_t* timing;         // nullable: phase clock marks (profiling)
 };
 

@@ -99,6 +99,8 @@ SIGNATURES = {
     "mtg_exec_mode": (c_int32, [c_void_p]),
     "mtg_debug_copy": (c_int32, [c_void_p, c_int32, c_void_p, ctypes.c_size_t]),
     "mtg_debug_abort_next_step": (c_int32, [c_void_p]),
+    "mtg_debug_wait_limit": (c_int32, [c_void_p, c_int32]),
+    "mtg_step_fallbacks": (c_int64, [c_void_p]),
     "mtg_step_profile": (c_int32, [c_void_p, c_int32]),
     "mtg_launch_timing": (c_int32, [c_void_p, c_int32]),
     "mtg_launch_timing_read": (c_int32, [c_void_p, POINTER(c_double), POINTER(c_int64),
@@ -247,6 +249,13 @@ class Decoder:
 
     def debug_abort_next_step(self):
         self._chk(lib().mtg_debug_abort_next_step(self.ctx))
+
+    def debug_wait_limit(self, polls):
+        self._chk(lib().mtg_debug_wait_limit(self.ctx, polls))
+
+    @property
+    def step_fallbacks(self):
+        return lib().mtg_step_fallbacks(self.ctx)
 
     def debug_buffer(self, which, width):
         out = np.empty((MAX_BATCH, width), np.float32)

@@ -335,6 +335,114 @@ void rms_norm(const float* x, const float* w, int n, float eps, float* y) {
   }
 }
 
+// ------------------------------------------------- ggml generic order ------
+// The second order of the oracle (orc_set_order(m, ORC_ORDER_GGML_GENERIC)):
+// the float order of ggml's generic (scalar) CPU kernels, the portable C path of
+// the same ops (the reference's Xeon runs ggml's x86 SIMD kernels, whose order is
+// machine-specific and not reproducible here). Integer block dots stay exact;
+// what changes is every float reduction: sequential block sums, double
+// accumulation where ggml's scalar code accumulates in double, soft_max_ext over
+// the common length with the causal mask, and the context at each query's valid
+// length (src/qwen3.cpp:157-189, src/cpu_context.cpp:13-32). It measures how far
+// the canonical order is from an independent, published one.
+
+// ggml_vec_dot_q8_0_q8_0 (generic): sumf += (float)isum * (d_w * d_x), block by block.
+void mul_mat_q8_generic(const BlockQ8* w, int k, int n, const float* x, int T, float* y) {
+  const int nb = k / 32;
+  std::vector<BlockQ8> xq((size_t)T * nb);
+  for (int t = 0; t < T; ++t) quantize_q8_0_act(x + (size_t)t * k, k, xq.data() + (size_t)t * nb);
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < n; ++r) {
+    const BlockQ8* wr = w + (size_t)r * nb;
+    for (int t = 0; t < T; ++t) {
+      const BlockQ8* xr = xq.data() + (size_t)t * nb;
+      float sumf = 0.0f;
+      for (int b = 0; b < nb; ++b) {
+        const float isum = (float)q8_block_dot(wr[b], xr[b]);
+        sumf = sumf + isum * (h2f(wr[b].d) * h2f(xr[b].d));
+      }
+      y[(size_t)t * n + r] = sumf;
+    }
+  }
+}
+
+// ggml_vec_dot_f16 (generic): x rounded to f16, sum of (double)(w * x) in order.
+void mul_mat_f16_generic(const uint16_t* w, int k, int n, const float* x, int T, float* y) {
+  std::vector<float> xh((size_t)T * k);
+  for (size_t i = 0; i < xh.size(); ++i) xh[i] = h2f(f2h(x[i]));
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < n; ++r) {
+    const uint16_t* wr = w + (size_t)r * k;
+    for (int t = 0; t < T; ++t) {
+      const float* xr = xh.data() + (size_t)t * k;
+      double sumf = 0.0;
+      for (int i = 0; i < k; ++i) sumf += (double)(h2f(wr[i]) * xr[i]);
+      y[(size_t)t * n + r] = (float)sumf;
+    }
+  }
+}
+
+// ggml_vec_dot_q4_K_q8_K (generic): per superblock eight int32 lane sums
+// aux[l] = sum over sub-blocks j and 8-element groups g of sc_j * q4 * q8 at
+// element 32 j + 8 g + l; sums[l] += d * aux[l] (float, d = d_w * d_x);
+// sumf -= dmin * sum_j bsum_j * mn_(j/2); at the end sumf += sums[0..7].
+void mul_mat_q4k_generic(const BlockQ4K* w, int k, int n, const float* x, int T, float* y) {
+  const int nb = k / 256;
+  std::vector<BlockQ8K> xq((size_t)T * nb);
+  for (int t = 0; t < T; ++t) quantize_q8_k_act(x + (size_t)t * k, k, xq.data() + (size_t)t * nb);
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < n; ++r) {
+    const BlockQ4K* wr = w + (size_t)r * nb;
+    for (int t = 0; t < T; ++t) {
+      const BlockQ8K* xr = xq.data() + (size_t)t * nb;
+      float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      float sumf = 0.0f;
+      for (int b = 0; b < nb; ++b) {
+        int32_t aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int32_t sumi = 0;
+        for (int s = 0; s < 8; ++s) {
+          int sc, mn;
+          q4k_scale_min(s, wr[b].scales, &sc, &mn);
+          sumi += (xr[b].bsums[2 * s] + xr[b].bsums[2 * s + 1]) * mn;
+          const uint8_t* q = wr[b].qs + (s / 2) * 32;
+          for (int g = 0; g < 4; ++g)
+            for (int l = 0; l < 8; ++l) {
+              const int e = 8 * g + l;
+              const int v = (s & 1) ? (q[e] >> 4) : (q[e] & 0xF);
+              aux[l] += sc * (v * xr[b].qs[s * 32 + e]);
+            }
+        }
+        const float d = h2f(wr[b].d) * xr[b].d;
+        for (int l = 0; l < 8; ++l) sums[l] = sums[l] + d * (float)aux[l];
+        const float dmin = h2f(wr[b].dmin) * xr[b].d;
+        sumf = sumf - dmin * (float)sumi;
+      }
+      for (int l = 0; l < 8; ++l) sumf = sumf + sums[l];
+      y[(size_t)t * n + r] = sumf;
+    }
+  }
+}
+
+void mul_mat_generic(int wtype, const void* w, int k, int n, const float* x, int T, float* y) {
+  if (wtype == MTG_TYPE_Q8_0) mul_mat_q8_generic((const BlockQ8*)w, k, n, x, T, y);
+  else if (wtype == MTG_TYPE_F16) mul_mat_f16_generic((const uint16_t*)w, k, n, x, T, y);
+  else mul_mat_q4k_generic((const BlockQ4K*)w, k, n, x, T, y);
+}
+
+// ggml_compute_forward_rms_norm_f32 (generic): sum of (double)(x*x) in order,
+// mean = (float)(sum / n), scale = 1.0f / sqrtf(mean + eps), y = x * scale; then
+// ggml_mul by the gain (src/qwen3.cpp:27-30).
+void rms_norm_generic(const float* x, const float* w, int n, float eps, float* y) {
+  double sum = 0.0;
+  for (int i = 0; i < n; ++i) sum += (double)(x[i] * x[i]);
+  const float mean = (float)(sum / n);
+  const float scale = 1.0f / std::sqrt(mean + eps);
+  for (int i = 0; i < n; ++i) {
+    const float v = x[i] * scale;
+    y[i] = v * w[i];
+  }
+}
+
 // NEOX RoPE as ggml_rope_ext builds it (src/qwen3.cpp:108-118, mode NEOX):
 // theta_scale = powf(base, -2/n_dims); theta_0 = pos, theta_{i+1} = theta_i *
 // theta_scale in float; pairs (i, i + n_dims/2); ext_factor 0, attn_factor 1.
@@ -379,6 +487,8 @@ void softmax_row(const float* s, int n, float scale, const float* mask, float* o
 }
 
 float swiglu(float g, float u) { return (g / (1.0f + exp_c(-g))) * u; }
+// ggml_silu_f32 (x / (1 + expf(-x))) times up, with the C library's expf.
+float swiglu_generic(float g, float u) { return (g / (1.0f + std::exp(-g))) * u; }
 
 }  // namespace
 
@@ -388,6 +498,7 @@ struct orc_model {
   int wtype = MTG_TYPE_Q8_0;
   int kv_type = MTG_TYPE_F32;
   int max_seq = 0, past = 0;
+  int order = ORC_ORDER_CANONICAL;  // float order of every reduction (orc_set_order)
   std::vector<std::vector<uint8_t>> wq, wk, wv, wo, wg, wu, wd;
   std::vector<std::vector<float>> attn_norm, q_norm, k_norm, ffn_norm;
   std::vector<uint8_t> embd;
@@ -448,6 +559,56 @@ inline void kv_set(orc_model& m, bool is_k, size_t idx, float v) {
   else (is_k ? m.k16 : m.v16)[idx] = f2h(v);  // ggml_cpy f32 -> f16
 }
 
+void norm_op(const orc_model& m, const float* x, const float* w, int n, float* y) {
+  if (m.order == ORC_ORDER_GGML_GENERIC) rms_norm_generic(x, w, n, m.hp.rms_eps, y);
+  else rms_norm(x, w, n, m.hp.rms_eps, y);
+}
+void gemm_op(const orc_model& m, const void* w, int k, int n, const float* x, int T, float* y) {
+  if (m.order == ORC_ORDER_GGML_GENERIC) mul_mat_generic(m.wtype, w, k, n, x, T, y);
+  else mul_mat(m.wtype, w, k, n, x, T, y);
+}
+
+// The eager attention in ggml's generic order (src/qwen3.cpp:157-189): scores
+// = mul_mat(K, q) with ggml_vec_dot_f32 (double accumulation; an f16 cache takes
+// q rounded to f16 and ggml_vec_dot_f16), soft_max_ext(scores, mask, 1/sqrt(D))
+// over the common length past + T with the causal mask (0 / -inf), then
+// cpu_causal_context: out[f] = dot(V[0..past+t][f], P[t][0..past+t]) at the
+// valid length (src/cpu_context.cpp:13-32), again a double-accumulated dot.
+void attention_generic(const orc_model& m, int l, const float* q, int T, float* o) {
+  const mtg_hparams& hp = m.hp;
+  const int D = hp.head_dim, NH = hp.n_heads, NKV = hp.n_kv_heads, QN = NH * D;
+  const int past = m.past, kv = past + T, groups = NH / NKV;
+  const size_t base = (size_t)l * m.layer_stride;
+  const bool f16kv = m.kv_type == MTG_TYPE_F16;
+  const float scale = 1.0f / std::sqrt((float)D);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int h = 0; h < NH; ++h)
+    for (int t = 0; t < T; ++t) {
+      const int g = h / groups;
+      std::vector<float> qv(D), sc(kv), mask(kv), p(kv);
+      const float* qh = q + (size_t)t * QN + (size_t)h * D;
+      for (int d = 0; d < D; ++d) qv[d] = f16kv ? h2f(f2h(qh[d])) : qh[d];
+      for (int j = 0; j < kv; ++j) {
+        const size_t kb = base + ((size_t)g * m.max_seq + j) * D;
+        double acc = 0.0;
+        for (int d = 0; d < D; ++d) acc += (double)(kv_get(m, true, kb + d) * qv[d]);
+        sc[j] = (float)acc;
+        mask[j] = j <= past + t ? 0.0f : -INFINITY;
+      }
+      softmax_row(sc.data(), kv, scale, mask.data(), p.data());
+      if (f16kv)
+        for (int j = 0; j < kv; ++j) p[j] = h2f(f2h(p[j]));
+      float* oh = o + (size_t)t * QN + (size_t)h * D;
+      const int valid = past + t + 1;
+      for (int d = 0; d < D; ++d) {
+        double acc = 0.0;
+        for (int j = 0; j < valid; ++j)
+          acc += (double)(kv_get(m, false, base + ((size_t)g * m.max_seq + j) * D + d) * p[j]);
+        oh[d] = (float)acc;
+      }
+    }
+}
+
 // One qwen3_layer_forward over T rows at positions past..past+T-1
 // (src/qwen3.cpp:62-218 with the device-cache path, transposed-V semantics and
 // the causal-context op of src/cpu_context.cpp:13-32).
@@ -457,11 +618,10 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
   const int QN = NH * D, KN = NKV * D, F = hp.intermediate;
   const int past = m.past, kv = past + T, groups = NH / NKV;
   std::vector<float> xn((size_t)T * H), q((size_t)T * QN), k((size_t)T * KN), v((size_t)T * KN);
-  for (int t = 0; t < T; ++t)
-    rms_norm(x + (size_t)t * H, m.attn_norm[l].data(), H, hp.rms_eps, xn.data() + (size_t)t * H);
-  mul_mat(m.wtype, m.wq[l].data(), H, QN, xn.data(), T, q.data());
-  mul_mat(m.wtype, m.wk[l].data(), H, KN, xn.data(), T, k.data());
-  mul_mat(m.wtype, m.wv[l].data(), H, KN, xn.data(), T, v.data());
+  for (int t = 0; t < T; ++t) norm_op(m, x + (size_t)t * H, m.attn_norm[l].data(), H, xn.data() + (size_t)t * H);
+  gemm_op(m, m.wq[l].data(), H, QN, xn.data(), T, q.data());
+  gemm_op(m, m.wk[l].data(), H, KN, xn.data(), T, k.data());
+  gemm_op(m, m.wv[l].data(), H, KN, xn.data(), T, v.data());
   // per-head q/k RMSNorm over head_dim, then NEOX RoPE at pos = past + t
   std::vector<float> cs(D);
   std::vector<float> tmp(D);
@@ -469,13 +629,13 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
     rope_table(past + t, D, hp.rope_base, cs.data());
     for (int h = 0; h < NH; ++h) {
       float* qh = q.data() + (size_t)t * QN + (size_t)h * D;
-      rms_norm(qh, m.q_norm[l].data(), D, hp.rms_eps, tmp.data());
+      norm_op(m, qh, m.q_norm[l].data(), D, tmp.data());
       rope_apply(tmp.data(), D, cs.data());
       std::memcpy(qh, tmp.data(), D * sizeof(float));
     }
     for (int h = 0; h < NKV; ++h) {
       float* kh = k.data() + (size_t)t * KN + (size_t)h * D;
-      rms_norm(kh, m.k_norm[l].data(), D, hp.rms_eps, tmp.data());
+      norm_op(m, kh, m.k_norm[l].data(), D, tmp.data());
       rope_apply(tmp.data(), D, cs.data());
       std::memcpy(kh, tmp.data(), D * sizeof(float));
     }
@@ -498,6 +658,8 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
   const bool f16kv = m.kv_type == MTG_TYPE_F16;
   const int nch = (kv + 63) / 64;
   std::vector<float> o((size_t)T * QN);
+  if (m.order == ORC_ORDER_GGML_GENERIC) attention_generic(m, l, q.data(), T, o.data());
+  else
 #pragma omp parallel for collapse(2) schedule(static)
   for (int h = 0; h < NH; ++h)
     for (int t = 0; t < T; ++t) {
@@ -554,15 +716,15 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
     }
   // o-proj + residual, FFN pre-norm, SwiGLU, down + residual
   std::vector<float> ao((size_t)T * H);
-  mul_mat(m.wtype, m.wo[l].data(), QN, H, o.data(), T, ao.data());
+  gemm_op(m, m.wo[l].data(), QN, H, o.data(), T, ao.data());
   for (size_t i = 0; i < (size_t)T * H; ++i) x[i] = x[i] + ao[i];
-  for (int t = 0; t < T; ++t)
-    rms_norm(x + (size_t)t * H, m.ffn_norm[l].data(), H, hp.rms_eps, xn.data() + (size_t)t * H);
+  for (int t = 0; t < T; ++t) norm_op(m, x + (size_t)t * H, m.ffn_norm[l].data(), H, xn.data() + (size_t)t * H);
   std::vector<float> g((size_t)T * F), u((size_t)T * F), act((size_t)T * F);
-  mul_mat(m.wtype, m.wg[l].data(), H, F, xn.data(), T, g.data());
-  mul_mat(m.wtype, m.wu[l].data(), H, F, xn.data(), T, u.data());
-  for (size_t i = 0; i < act.size(); ++i) act[i] = swiglu(g[i], u[i]);
-  mul_mat(m.wtype, m.wd[l].data(), F, H, act.data(), T, ao.data());
+  gemm_op(m, m.wg[l].data(), H, F, xn.data(), T, g.data());
+  gemm_op(m, m.wu[l].data(), H, F, xn.data(), T, u.data());
+  const bool generic = m.order == ORC_ORDER_GGML_GENERIC;
+  for (size_t i = 0; i < act.size(); ++i) act[i] = generic ? swiglu_generic(g[i], u[i]) : swiglu(g[i], u[i]);
+  gemm_op(m, m.wd[l].data(), F, H, act.data(), T, ao.data());
   for (size_t i = 0; i < (size_t)T * H; ++i) x[i] = x[i] + ao[i];
 }
 
@@ -585,6 +747,10 @@ int32_t orc_q8_0_block_dot(const void* a, const void* b) {
 void orc_mul_mat(int32_t wtype, const void* w, int32_t k, int32_t n, const float* x, int32_t T,
                  float* y) {
   mul_mat(wtype, w, k, n, x, T, y);
+}
+void orc_mul_mat_generic(int32_t wtype, const void* w, int32_t k, int32_t n, const float* x, int32_t T,
+                         float* y) {
+  mul_mat_generic(wtype, w, k, n, x, T, y);
 }
 void orc_rms_norm(const float* x, const float* w, int32_t n, float eps, float* y) {
   rms_norm(x, w, n, eps, y);
@@ -693,8 +859,7 @@ int orc_run(orc_model* m, const float* embeds, int32_t T, float* hidden_out) {
   m->past += T;
   if (hidden_out)
     for (int t = 0; t < T; ++t)
-      rms_norm(x.data() + (size_t)t * H, m->out_norm.data(), H, m->hp.rms_eps,
-               hidden_out + (size_t)t * H);
+      norm_op(*m, x.data() + (size_t)t * H, m->out_norm.data(), H, hidden_out + (size_t)t * H);
   return MTG_OK;
 }
 
@@ -707,7 +872,13 @@ int orc_prefill(orc_model* m, const float* embeds, int32_t S, float* hidden_out)
 // logits_from_hidden (src/qwen3_decoder.cpp:174-205), row by row.
 int orc_logits(orc_model* m, const float* hidden, int32_t T, float* logits_out) {
   if (!m || !hidden || T <= 0 || !logits_out) return MTG_ERR_INVALID;
-  mul_mat(m->wtype, m->embd.data(), m->hp.hidden, m->hp.vocab, hidden, T, logits_out);
+  gemm_op(*m, m->embd.data(), m->hp.hidden, m->hp.vocab, hidden, T, logits_out);
+  return MTG_OK;
+}
+
+int orc_set_order(orc_model* m, int32_t order) {
+  if (!m || (order != ORC_ORDER_CANONICAL && order != ORC_ORDER_GGML_GENERIC)) return MTG_ERR_INVALID;
+  m->order = order;
   return MTG_OK;
 }
 
@@ -846,6 +1017,10 @@ int orc_controller(orc_target* tg, int32_t first_seed, const int32_t* prior_ids,
     if (stop) break;
     const int before = tg->past;
     const int remaining = tg->max_seq - tg->past;
+    if (remaining < 1) {  // append of the seed fails: break (src/cpu_speculative.cpp:113-114)
+      stop = 3;
+      break;
+    }
     const int budget = std::max(0, std::min({max_draft, max_new - (int)(ids.size() - first_new),
                                               remaining - 1, MTG_MAX_BATCH - 1}));
     int np = draft ? draft(user, ids.data(), (int)ids.size(), budget, proposal.data())

@@ -27,6 +27,15 @@ extern "C" {
 typedef struct orc_model orc_model;
 
 int orc_create(const mtg_model_desc* desc, int32_t max_seq, int32_t kv_type, orc_model** out);
+
+/* Float order of every reduction of the step. CANONICAL (the default): the order
+ * the device kernels share with the oracle bit for bit (64-key attention chunks
+ * merged in order, 4-slice q8_0 sums, butterfly sums). GGML_GENERIC: the order of
+ * ggml's generic scalar CPU kernels (sequential block sums, double-accumulated
+ * dots, soft_max_ext over the whole row then the context at the valid length),
+ * an independent published order to measure the canonical one against. */
+enum { ORC_ORDER_CANONICAL = 0, ORC_ORDER_GGML_GENERIC = 1 };
+int orc_set_order(orc_model* m, int32_t order);
 void orc_destroy(orc_model* m);
 int32_t orc_past_len(const orc_model* m);
 int orc_rewind(orc_model* m, int32_t position);
@@ -79,6 +88,9 @@ void orc_quantize_q8_k_act(const float* x, int64_t k, void* blocks);
 int32_t orc_q8_0_block_dot(const void* a, const void* b);
 void orc_mul_mat(int32_t wtype, const void* w, int32_t k, int32_t n, const float* x, int32_t T,
                  float* y);
+/* the same product in ggml's generic scalar order (ORC_ORDER_GGML_GENERIC) */
+void orc_mul_mat_generic(int32_t wtype, const void* w, int32_t k, int32_t n, const float* x, int32_t T,
+                         float* y);
 void orc_rms_norm(const float* x, const float* w, int32_t n, float eps, float* y);
 void orc_rope_neox(float* x, int32_t n_dims, int32_t pos, float base);
 void orc_softmax(const float* s, int32_t n, float scale, const float* mask, float* out);

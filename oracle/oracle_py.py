@@ -53,6 +53,8 @@ SIGNATURES = {
     "orc_f16_to_f32": (c_float, [c_uint16]),
     "orc_quantize_q8_0_act": (None, [c_void_p, c_int64, c_void_p]),
     "orc_quantize_q8_k_act": (None, [c_void_p, c_int64, c_void_p]),
+    "orc_set_order": (c_int32, [c_void_p, c_int32]),
+    "orc_mul_mat_generic": (None, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
     "orc_q8_0_block_dot": (c_int32, [c_void_p, c_void_p]),
     "orc_mul_mat": (None, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
     "orc_rms_norm": (None, [c_void_p, c_void_p, c_int32, c_float, c_void_p]),
@@ -93,11 +95,31 @@ def quantize_q8_0_act(x):
     return out
 
 
+Q8K_BLOCK = np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bsums", "<i2", 16)])
+
+
+def quantize_q8_k_act(x):
+    x = f32(x)
+    out = np.zeros(x.size // 256, Q8K_BLOCK)
+    assert out.itemsize == 4 + 256 + 32
+    lib().orc_quantize_q8_k_act(ptr(x), x.size, ptr(out))
+    return out
+
+
 def mul_mat(wtype, w_bytes, k, n, x):
     x = f32(x)
     T = x.shape[0]
     y = np.empty((T, n), np.float32)
     lib().orc_mul_mat(wtype, ptr(w_bytes), k, n, ptr(x), T, ptr(y))
+    return y
+
+
+def mul_mat_generic(wtype, w_bytes, k, n, x):
+    """mul_mat in ggml's generic scalar order (sequential block sums)."""
+    x = f32(x)
+    T = x.shape[0]
+    y = np.empty((T, n), np.float32)
+    lib().orc_mul_mat_generic(wtype, ptr(w_bytes), k, n, ptr(x), T, ptr(y))
     return y
 
 
@@ -189,6 +211,15 @@ class Oracle:
         if rc:
             raise RuntimeError("orc_create failed: %d" % rc)
         self.m = out
+
+    ORDER_CANONICAL, ORDER_GGML_GENERIC = 0, 1
+
+    def set_order(self, order):
+        """Float order of the step's reductions: ORDER_CANONICAL (the device's) or
+        ORDER_GGML_GENERIC (ggml's generic scalar kernels)."""
+        rc = lib().orc_set_order(self.m, order)
+        if rc:
+            raise RuntimeError("orc_set_order %d" % rc)
 
     def close(self):
         if self.m:

@@ -281,3 +281,31 @@ def test_step_kernel_abort_reports_and_recovers():
         _close(h1, h0, "hidden after recovery")
         _close(l1, l0, "logits after recovery")
         assert np.array_equal(c1, c0) and m1 == m0
+
+
+def test_step_kernel_wait_timeout_falls_back_to_per_op_kernels():
+    """A wait that runs out (forced from the host with a 1-poll limit on the
+    kernel's own bounded waits) abandons the launch; the same step then runs on the
+    per-op kernels in the same call, so the caller sees a normal result, equal to
+    the oracle's bit for bit, and the fallback counter advances."""
+    print("step kernel wait-timeout fallback", flush=True)
+    model, orc, dec, rng = _setup(2, 40)
+    before = dec.step_fallbacks
+    dec.debug_wait_limit(1)
+    try:
+        for T in (8, 5):
+            tokens = rng.integers(0, model.hp.vocab, T)
+            c0, m0, h0, l0 = orc.verify(tokens, want_hidden=True, want_logits=True)
+            c1, m1, h1, l1 = dec.verify(tokens, want_hidden=True, want_logits=True)
+            _close(h1, h0, "hidden after the fallback")
+            _close(l1, l0, "logits after the fallback")
+            assert np.array_equal(c1, c0) and m1 == m0
+            assert dec.past_len == orc.past_len
+    finally:
+        dec.debug_wait_limit(0)
+    assert dec.step_fallbacks > before
+    tokens = rng.integers(0, model.hp.vocab, 8)
+    c0, m0, _, l0 = orc.verify(tokens, want_logits=True)
+    c1, m1, _, l1 = dec.verify(tokens, want_logits=True)
+    _close(l1, l0, "logits with the default bound")
+    assert np.array_equal(c1, c0) and m1 == m0

@@ -269,3 +269,57 @@ def test_exp_is_within_two_ulps_of_float64():
     assert L().orc_exp(0.0) == 1.0
     assert L().orc_exp(-87.5) == 0.0 and L().orc_exp(-1000.0) == 0.0
     assert L().orc_exp(89.0) == np.inf
+
+
+def test_q8_k_activation_quantizer_rules():
+    """ggml's quantize_row_q8_K (the vec_dot_type of q4_K): the scale comes from the
+    SIGNED value of the first element of largest magnitude (strict '>' scan), so
+    that element always maps to -127 and d = 1/iscale carries the opposite sign;
+    codes are round-half-even of iscale * x, at most +127; bsums are the sums of
+    16-code groups; an all-zero block gives d = 0 and zero codes. Each planted case
+    tells the rule apart from a plausible alternative (amax/127 scaling, last
+    occurrence on ties, half-away rounding)."""
+    def q(block):
+        return oracle_py.quantize_q8_k_act(np.asarray(block, np.float32))[0]
+    # signed max: the largest |x| is negative -> iscale > 0, d < 0 ... and positive
+    b = np.zeros(256, np.float32)
+    b[7], b[20] = -4.0, 3.0
+    r = q(b)
+    assert r["qs"][7] == -127 and r["d"] == np.float32(1.0) / (np.float32(-127.0) / np.float32(-4.0))
+    assert r["d"] > 0 and r["qs"][20] == int(np.rint(np.float32(31.75) * np.float32(3.0)))  # 95.25 -> 95
+    b[7], b[20] = 4.0, -3.0
+    r = q(b)
+    assert r["qs"][7] == -127 and r["qs"][20] == 95 and r["d"] < 0
+    # a tie in magnitude: the FIRST occurrence sets the sign; the opposite-sign
+    # extreme lands on +127 exactly (the clamp's bound, never 128)
+    b = np.zeros(256, np.float32)
+    b[3], b[10] = -5.0, 5.0
+    r = q(b)
+    assert r["qs"][3] == -127 and r["qs"][10] == 127
+    b[3], b[10] = 5.0, -5.0
+    r = q(b)
+    assert r["qs"][3] == -127 and r["qs"][10] == 127
+    # rounding ties: max = -127 gives iscale = 1 exactly, so x = k + 0.5 is a tie
+    b = np.zeros(256, np.float32)
+    b[0] = -127.0
+    b[1:8] = [0.5, 1.5, 2.5, -0.5, -3.5, 126.5, -126.5]
+    r = q(b)
+    assert r["qs"][:8].tolist() == [-127, 0, 2, 2, 0, -4, 126, -126]
+    # bsums = sums of the 16-code groups (int16), on random blocks
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal(256 * 32) * 10.0 ** rng.integers(-4, 3, 256 * 32)).astype(np.float32)
+    x[256:512] = 0.0
+    blocks = oracle_py.quantize_q8_k_act(x)
+    qs = blocks["qs"].astype(np.int64)
+    assert np.array_equal(blocks["bsums"], qs.reshape(-1, 16, 16).sum(axis=2))
+    assert blocks["d"][1] == 0 and (blocks["qs"][1] == 0).all()
+    assert qs.max() <= 127 and qs.min() >= -127
+    # the codes are the nearest integers: |x - d * code| <= |d| / 2 (+ rounding of
+    # the float product), and the extreme element of every block is -127
+    xb = x.reshape(-1, 256).astype(np.float64)
+    d = blocks["d"].astype(np.float64)[:, None]
+    err = np.abs(xb - d * qs)
+    assert (err <= np.abs(d) * (0.5 + 1e-5) + 1e-30).all()
+    nz = np.abs(xb).max(axis=1) > 0
+    first = np.abs(xb).argmax(axis=1)  # numpy: first occurrence
+    assert (qs[nz, first[nz]] == -127).all()

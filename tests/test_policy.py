@@ -221,3 +221,35 @@ def test_stream_drafter_aligns_to_absolute_position():
     assert n == 4
     # n-gram part [3, 1, 2] (latest earlier occurrence of the suffix 1,2), then stream
     assert out[:4].tolist() == [3, 1, 2, stream[(8 + 3) % 37]]
+
+
+@pytest.mark.parametrize("impl", ["libmtg", "oracle"])
+def test_controller_stops_when_the_cache_is_full(impl):
+    """A full KV cache ends the loop the way the reference's failed append does
+    (src/cpu_speculative.cpp:113-114): the seed is emitted, no verify call is made,
+    the status is OK and stop_reason says why (3)."""
+    gold = [1, 2, 1, 2, 1, 2, 1, 2, 1, 2, 1, 2, 1, 2, 1, 2, 9]
+    calls = []
+
+    def verify(tokens, hist, penalty, past):
+        calls.append((len(tokens), past))
+        return _scripted(gold)(tokens, hist, penalty, past)
+    kw = dict(max_draft=4, past=6, max_seq=10)
+    if impl == "libmtg":
+        ids, st, past = mtg.speculative_run(verify, gold[0], 100, eos=9, **kw)
+    else:
+        ids, st, past = oracle_py.run_controller(verify, gold[0], 100, 9, **kw)
+    # every call fits: past + T <= max_seq, and the last one leaves no free position
+    assert all(p + t <= 10 for t, p in calls)
+    assert past == 10
+    assert st.stop_reason == 3
+    # the seed of the step that found no room is emitted (and not kept)
+    assert ids == gold[:len(ids)] and len(ids) == 10 - 6 + 1
+    # a full cache from the start: only the seed, no verify call
+    calls.clear()
+    kw["past"] = 10
+    if impl == "libmtg":
+        ids, st, past = mtg.speculative_run(verify, gold[0], 100, eos=9, **kw)
+    else:
+        ids, st, past = oracle_py.run_controller(verify, gold[0], 100, 9, **kw)
+    assert ids == [gold[0]] and calls == [] and st.stop_reason == 3 and past == 10
