@@ -719,12 +719,58 @@ __device__ __forceinline__ void stage_v(const StepParams& P, int g, int T, uint3
   }
 }
 
+// This step's k / v rows of kv head g, staged in LDS (knew: normed, roped and
+// permuted, vnew: plain; f16-rounded for an f16 cache), written to the KV cache
+// at positions past .. past + T - 1 with 16-byte stores.
+template <int KVH>
+__device__ __forceinline__ void kv_append(const StepParams& P, const LayerDev& Ly, int T, int past, int g,
+                                          const float* knew, const float* vnew) {
+  constexpr bool f16kv = KVH != 0;
+  // wave-uniform cache pointers (a per-lane choice between the two fields
+  // would load the pointer with a vector load before every store)
+  uint8_t* const kcp = uniform_ptr(Ly.kc);
+  uint8_t* const vcp = uniform_ptr(Ly.vc);
+  for (int i = threadIdx.x; i < T * (cHD / 4); i += kT) {  // 4 elements of one row
+    const int t = i / (cHD / 4), m = i % (cHD / 4), d = 4 * m;
+    const size_t off = ((size_t)g * P.max_seq + past + t) * cHD + d;
+    const float* kr = knew + t * cQStride + m;  // element 4 m + kk sits at kk * 32 + m
+    const v4f kq = {kr[0], kr[32], kr[64], kr[96]};
+    const v4f vq = *(const v4f*)(vnew + t * cQStride + d);
+    if (f16kv) {
+      const v2u kh = {pack_half2(kq[0], kq[1]), pack_half2(kq[2], kq[3])};
+      const v2u vh = {pack_half2(vq[0], vq[1]), pack_half2(vq[2], vq[3])};
+      gst<v2u>((uint16_t*)kcp + off, kh);
+      gst<v2u>((uint16_t*)vcp + off, vh);
+    } else {
+      gst<v4f>((float*)kcp + off, kq);
+      gst<v4f>((float*)vcp + off, vq);
+    }
+  }
+}
+
+// The KV append of kv head g by a workgroup without attention items: the new k
+// rows normed and roped and the new v rows, staged from the tagged q|k|v buffer
+// as the attention items stage them, then written to the cache. Nothing in this
+// step reads them from the cache (the items take new rows from their own
+// staging), so this runs beside the attention, off its critical path.
+template <int G, int KVH>
+__device__ __forceinline__ void append_item(const StepParams& P, const LayerDev& Ly, int T, int past, int g,
+                                            uint32_t tag, uint8_t* lds) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ncol = 2 * T;
+  float* q_lds = (float*)lds;
+  float* knew = q_lds + kMaxCols * cQStride;
+  float* vnew = knew + kMaxRows * cQStride;
+  stage_pass<4 * G, KVH>(P, Ly, T, past, g, ncol + wave, ncol + 2 * T, tag, q_lds, knew, vnew);
+  bar();
+  kv_append<KVH>(P, Ly, T, past, g, knew, vnew);
+}
+
 // One attention item: chunk `chunk` of kv head g over the ncol = 2T query
 // columns (col = hl*T + t for q head 2g + hl). LDS: q [32][132], knew/vnew
 // [16][132], sp [32][68].
 template <int G, int KVH>
 __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& Ly, int T, int past, int g, int chunk,
-                                          uint32_t tag, const KvRegs& kv, uint8_t* lds, bool prof) {
+                                          uint32_t tag, const KvRegs& kv, uint8_t* lds, bool self_append, bool prof) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, kl = lane & 15,
             kk = lane >> 4;
   constexpr bool f16kv = KVH != 0;
@@ -744,7 +790,8 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
     stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol, tag, q_lds, knew, vnew, prof);
   } else {
     // q and new k rows are normed and roped; the new v rows are plain copies
-    stage_pass<6 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, tag, q_lds, knew, vnew);
+    stage_pass<6 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, tag, q_lds, knew, vnew, prof);
+    if (prof) wmark(P, 1, 14);
     stage_v<2 * G, KVH>(P, g, T, tag, vnew);
   }
   bar();
@@ -768,33 +815,13 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int s = 0; s < 16; ++s) asm volatile("" ::"v"(vb[h][s]));
-  // the appending workgroup writes this step's k / v rows to the KV cache from
-  // the staged rows (for an f16 cache they are f16 values already). Issued after
-  // the prefetched K / V are in registers (a wait for a load issued before these
+  // Without a helper workgroup (every workgroup holds attention items), the
+  // appending item writes this step's k / v rows to the KV cache from the staged
+  // rows (for an f16 cache they are f16 values already). Issued after the
+  // prefetched K / V are in registers (a wait for a load issued before these
   // stores would wait for them too), so that their acknowledgement overlaps the
   // scores instead of delaying the publish.
-  if (appender) {
-    // wave-uniform cache pointers (a per-lane choice between the two fields
-    // would load the pointer with a vector load before every store)
-    uint8_t* const kcp = uniform_ptr(Ly.kc);
-    uint8_t* const vcp = uniform_ptr(Ly.vc);
-    for (int i = threadIdx.x; i < T * (cHD / 4); i += kT) {  // 4 elements of one row
-      const int t = i / (cHD / 4), m = i % (cHD / 4), d = 4 * m;
-      const size_t off = ((size_t)g * P.max_seq + past + t) * cHD + d;
-      const float* kr = knew + t * cQStride + m;  // element 4 m + kk sits at kk * 32 + m
-      const v4f kq = {kr[0], kr[32], kr[64], kr[96]};
-      const v4f vq = *(const v4f*)(vnew + t * cQStride + d);
-      if (f16kv) {
-        const v2u kh = {pack_half2(kq[0], kq[1]), pack_half2(kq[2], kq[3])};
-        const v2u vh = {pack_half2(vq[0], vq[1]), pack_half2(vq[2], vq[3])};
-        gst<v2u>((uint16_t*)kcp + off, kh);
-        gst<v2u>((uint16_t*)vcp + off, vh);
-      } else {
-        gst<v4f>((float*)kcp + off, kq);
-        gst<v4f>((float*)vcp + off, vq);
-      }
-    }
-  }
+  if (appender && self_append) kv_append<KVH>(P, Ly, T, past, g, knew, vnew);
   if (has_new) {
     // score operands: the lane's key, all 32 values from one permuted row
     const int key = key0 + 16 * wave + kl;
@@ -1276,6 +1303,11 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   // roles
   const int first_item = (w + kNwg - 64) % kNwg;  // item i runs on workgroup (i + 64) % 256
   const bool has_attn = first_item < n_items;
+  // KV append helpers: when 8 workgroups hold no attention item, workgroup
+  // (n_items + 64 + g) mod 256 appends kv head g's new rows
+  const bool helpers = n_items + cNKV <= kNwg;
+  const int help_g = (w - n_items - 64 + 2 * kNwg) % kNwg;
+  const bool helper = helpers && help_g < cNKV;
   const int n_merge = cNH * T;                    // (head, row) items, in pairs
   const bool has_merge = w >= kMergeWg0;
   const bool od = w < cOTiles;                    // o-proj and down tiles
@@ -1357,13 +1389,14 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     if (!has_attn) publish(c, next_done(l, kPhQkv));
     MARK(P, 3 + 12 * l + 1);
     WMARK(P, l, 1);
+    if (helper) append_item<G, KVH>(P, Ly, T, past, help_g, c.epoch + ph(l, kPhQkv), lds);
     // ---- ATTN: items of this workgroup ----
     if (has_attn) {
       MARK(P, 3 + 12 * l + 2);
       WMARK(P, l, 2);
       for (int item = first_item; item < n_items; item += kNwg) {
         if (item != first_item) kv_prefetch<KVH>(Ly, P, item / nch, (item % nch) * kChunk, past, kv);
-        attn_item<G, KVH>(P, Ly, T, past, item / nch, item % nch, c.epoch + ph(l, kPhQkv), kv, lds,
+        attn_item<G, KVH>(P, Ly, T, past, item / nch, item % nch, c.epoch + ph(l, kPhQkv), kv, lds, !helpers,
                           PROF && l == 1 && P.timing != nullptr);
       }
       publish(c, next_done(l, kPhAttn));
@@ -1419,9 +1452,15 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       MARK(P, 3 + 12 * l + 5);
       WMARK(P, l, 7);
       wt_load<12>(Ly.wd + (size_t)w * cBF * kUnitBytes, 12 * wave, ba, bs);
-      // the next layer's attention K / V, so that they are in flight before the down wait
-      if (has_attn && l + 1 < L)
-        kv_prefetch<KVH>(layer_at(P, l + 1), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+      // the next layer's q|k|v tile and attention K / V, so that they are in flight
+      // before the down wait (issued after the down phase, the tile's loads would
+      // hold up the residual rows of the next q|k|v panel: loads complete in order)
+      if (l + 1 < L) {
+        wt_load<4>(layer_at(P, l + 1).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+        gain16_load(layer_at(P, l + 1).attn_norm, gq);
+        if (has_attn)
+          kv_prefetch<KVH>(layer_at(P, l + 1), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+      }
     }
     // ---- GATE/UP: act = silu(g) * u, as q8_0 blocks ----
     if (gu) {
@@ -1459,10 +1498,6 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       publish(c, next_done(l, kPhD));
       MARK(P, 3 + 12 * l + 7);
       WMARK(P, l, 11);
-      if (l + 1 < L) {
-        wt_load<4>(layer_at(P, l + 1).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-        gain16_load(layer_at(P, l + 1).attn_norm, gq);
-      }
     }
     // workgroups with only q|k|v and attention work
     if (!od && !gu && !has_merge && l + 1 < L) {
