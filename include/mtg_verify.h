@@ -125,9 +125,17 @@ int mtg_rewind(mtg_ctx* ctx, int32_t position);
 int mtg_embed(mtg_ctx* ctx, const int32_t* ids, int32_t n, float* out);
 
 /* reset + run S rows; hidden_out (nullable) receives the final-normed hidden of
- * every row (S x hidden). Rows are processed in verify batches of up to
- * MTG_MAX_BATCH, each causal over everything before it. */
+ * every row (S x hidden). With q8_0 weights the rows go through the decoder in
+ * blocks of up to 2,048 (each weight matrix streamed once per block, causal
+ * attention over the cache); otherwise in verify batches of up to
+ * MTG_MAX_BATCH. Both give the same bits. */
 int mtg_prefill(mtg_ctx* ctx, const float* embeds, int32_t S, float* hidden_out);
+/* blocks != 0 (the default): the block prefill where it applies; 0: verify-size
+ * batches (no counterpart in the reference; for comparing the two paths). */
+int mtg_prefill_mode(mtg_ctx* ctx, int32_t blocks);
+/* Device time of the last block prefill in ms (HIP events on the context's
+ * stream, uploads of the rows included). */
+double mtg_last_prefill_ms(const mtg_ctx* ctx);
 
 /* Append T (1..MTG_MAX_BATCH) embedding rows at past_len; past_len += T.
  * hidden_out (nullable) receives T x hidden final-normed rows. */

@@ -183,22 +183,20 @@ int mtg_append(mtg_ctx* ctx, const float* embeds, int32_t T, float* hidden_out) 
 
 int mtg_prefill(mtg_ctx* ctx, const float* embeds, int32_t S, float* hidden_out) {
   if (!ctx) return MTG_ERR_INVALID;
-  if (!embeds || S <= 0) return ctx->impl.fail(MTG_ERR_INVALID, "prefill: bad arguments");
-  if (S > ctx->impl.max_seq) return ctx->impl.fail(MTG_ERR_CAPACITY, "prefill exceeds max_seq");
   try {
-    ctx->impl.past = 0;
-    const int H = ctx->impl.hp.hidden;
-    for (int s0 = 0; s0 < S; s0 += MTG_MAX_BATCH) {
-      const int n = std::min(MTG_MAX_BATCH, S - s0);
-      const int rc = ctx->impl.append(embeds + (size_t)s0 * H, n,
-                                      hidden_out ? hidden_out + (size_t)s0 * H : nullptr);
-      if (rc) return rc;
-    }
-    return MTG_OK;
+    return ctx->impl.prefill(embeds, S, hidden_out);
   } catch (...) {
     return ctx->impl.fail(MTG_ERR_DEVICE, "prefill: exception");
   }
 }
+
+int mtg_prefill_mode(mtg_ctx* ctx, int32_t blocks) {
+  if (!ctx) return MTG_ERR_INVALID;
+  ctx->impl.prefill_fast_enabled = blocks != 0;
+  return MTG_OK;
+}
+
+double mtg_last_prefill_ms(const mtg_ctx* ctx) { return ctx ? ctx->impl.last_prefill_ms : 0.0; }
 
 int mtg_logits(mtg_ctx* ctx, const float* hidden, int32_t T, float* logits_out) {
   if (!ctx) return MTG_ERR_INVALID;

@@ -87,6 +87,24 @@ void launch_causal_context(hipStream_t s, const float* v, const float* p, int he
                            int kv_heads, int heads, int queries, int kv_len, float* out);
 void launch_q8_retile(hipStream_t s, const uint8_t* blocks, int n, int k, uint8_t* tiles);
 
+// ---- prompt prefill over S rows (prefill.hip); activations in the compact
+// q8_0 layout codes [S][K] int8 + scales [S][K/32] ----
+enum { PF_EPI_STORE = 0, PF_EPI_RESID = 1, PF_EPI_SWIGLU = 2 };
+int pf_max_context();  // positions the prefill attention supports
+hipError_t prepare_kernels_pf();
+// RMSNorm(src) * gain (hidden 1024) -> q8_0 codes / scales; normed_out (nullable)
+void launch_pf_norm_quant(hipStream_t s, const float* src, int S, const float* gain, float eps, int8_t* codes,
+                          float* scales, float* normed_out);
+void launch_pf_quant(hipStream_t s, const float* src, int S, int K, int8_t* codes, float* scales);
+// out[s][n] (= / += / swiglu with w2) q8_0 GEMM of packed tiles (N % 32 == 0)
+void launch_pf_gemm(hipStream_t s, int epi, const uint8_t* w, const uint8_t* w2, int N, int K, const int8_t* codes,
+                    const float* scales, int S, float* out);
+void launch_pf_qk_rope(hipStream_t s, const float* qkv, int S, int past0, int n_heads, int n_kv_heads,
+                       const float* q_norm, const float* k_norm, float eps, const float* rope, float* q_out,
+                       KvLayer kv);
+void launch_pf_attn(hipStream_t s, const float* q, int n_heads, int n_kv_heads, KvLayer kv, int past0, int S,
+                    int8_t* ocodes, float* oscales);
+
 // ---- f16 / q4_K weights (kernels_wt.hip); weights in the GGUF row layout ----
 bool wt_shape_supported(int wtype, int k);
 // act <- the weight type's vec_dot_type of RMSNorm(src) * gain (gain == nullptr:

@@ -225,6 +225,7 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
     return fail(MTG_ERR_NOMEM, "step buffers");
   if ((rc = check(prepare_kernels(), "kernel attributes"))) return rc;
   if ((rc = check(prepare_kernels_wt(), "kernel attributes"))) return rc;
+  if ((rc = check(prepare_kernels_pf(), "kernel attributes"))) return rc;
   if ((rc = init_step_kernel())) return rc;
   return check(hipDeviceSynchronize(), "init");
 }
@@ -544,6 +545,85 @@ int Ctx::append(const float* embeds, int T, float* hidden_out) {
   fill_desc(T, true, 1.0f, nullptr, nullptr, 0, false);
   if ((rc = run(kModeAppend, T, true, false, hidden_out, nullptr))) return rc;
   past += T;
+  return MTG_OK;
+}
+
+// Qwen3Decoder::prefill (src/qwen3_decoder.cpp:162-166): the fused prompt rows
+// run from position 0; hidden_out (nullable) gets every row's final-normed
+// hidden state.
+int Ctx::prefill(const float* embeds, int S, float* hidden_out) {
+  if (!embeds || S <= 0) return fail(MTG_ERR_INVALID, "prefill: bad arguments");
+  if (S > max_seq) return fail(MTG_ERR_CAPACITY, "prefill exceeds max_seq");
+  past = 0;
+  const bool blocks = prefill_fast_enabled && wtype == MTG_TYPE_Q8_0 && S <= pf_max_context() &&
+                      hp.hidden == 1024 && hp.head_dim == kHeadDim;
+  if (blocks) return prefill_blocks(embeds, S, hidden_out);
+  const int H = hp.hidden;
+  for (int s0 = 0; s0 < S; s0 += kMaxRows) {
+    const int n = std::min(kMaxRows, S - s0);
+    const int rc = append(embeds + (size_t)s0 * H, n, hidden_out ? hidden_out + (size_t)s0 * H : nullptr);
+    if (rc) return rc;
+  }
+  return MTG_OK;
+}
+
+// The prompt in blocks of kPfRows rows: per layer RMSNorm + q8_0 conversion, the
+// fused q|k|v GEMM, q/k norm + RoPE + KV append, causal attention over the cache,
+// o-proj + residual, RMSNorm, gate/up + SwiGLU, q8_0, down + residual; each
+// weight matrix is streamed once per block. Same arithmetic as the verify path.
+int Ctx::prefill_blocks(const float* embeds, int S, float* hidden_out) {
+  const int H = hp.hidden, NH = hp.n_heads, NKV = hp.n_kv_heads, D = hp.head_dim;
+  const int QN = NH * D, KN = NKV * D, NQKV = QN + 2 * KN, F = hp.intermediate;
+  const float eps = hp.rms_eps;
+  const int R = kPfRows;
+  if (!pf.x) {
+    pf.x = (float*)dalloc((size_t)R * H * 4, false);
+    pf.qkv = (float*)dalloc((size_t)R * NQKV * 4, false);
+    pf.q = (float*)dalloc((size_t)R * QN * 4, false);
+    pf.act = (float*)dalloc((size_t)R * F * 4, false);
+    pf.hid = (float*)dalloc((size_t)R * H * 4, false);
+    const int KM = std::max(H, std::max(QN, F));
+    pf.codes = (int8_t*)dalloc((size_t)R * KM, false);
+    pf.scales = (float*)dalloc((size_t)R * (KM / 32) * 4, false);
+    if (!pf.x || !pf.qkv || !pf.q || !pf.act || !pf.hid || !pf.codes || !pf.scales)
+      return fail(MTG_ERR_NOMEM, "prefill buffers");
+  }
+  hipStream_t s = stream;
+  int rc = MTG_OK;
+  if (!ev_start && (rc = check(hipEventCreate(&ev_start), "event"))) return rc;
+  if (!ev_stop && (rc = check(hipEventCreate(&ev_stop), "event"))) return rc;
+  if ((rc = check(hipEventRecord(ev_start, s), "event"))) return rc;
+  for (int c0 = 0; c0 < S; c0 += R) {
+    const int n = std::min(R, S - c0);
+    if ((rc = check(hipMemcpyAsync(pf.x, embeds + (size_t)c0 * H, (size_t)n * H * 4, hipMemcpyHostToDevice, s),
+                    "prompt rows")))
+      return rc;
+    for (int l = 0; l < hp.n_layers; ++l) {
+      const Layer& y = layers[l];
+      const KvLayer kv = kv_layer(l);
+      launch_pf_norm_quant(s, pf.x, n, y.attn_norm, eps, pf.codes, pf.scales, nullptr);
+      launch_pf_gemm(s, PF_EPI_STORE, y.wqkv, nullptr, NQKV, H, pf.codes, pf.scales, n, pf.qkv);
+      launch_pf_qk_rope(s, pf.qkv, n, c0, NH, NKV, y.q_norm, y.k_norm, eps, rope, pf.q, kv);
+      launch_pf_attn(s, pf.q, NH, NKV, kv, c0, n, pf.codes, pf.scales);
+      launch_pf_gemm(s, PF_EPI_RESID, y.wo, nullptr, H, QN, pf.codes, pf.scales, n, pf.x);
+      launch_pf_norm_quant(s, pf.x, n, y.ffn_norm, eps, pf.codes, pf.scales, nullptr);
+      launch_pf_gemm(s, PF_EPI_SWIGLU, y.wg, y.wu, F, H, pf.codes, pf.scales, n, pf.act);
+      launch_pf_quant(s, pf.act, n, F, pf.codes, pf.scales);
+      launch_pf_gemm(s, PF_EPI_RESID, y.wd, nullptr, H, F, pf.codes, pf.scales, n, pf.x);
+    }
+    launch_pf_norm_quant(s, pf.x, n, out_norm, eps, pf.codes, pf.scales, pf.hid);
+    if ((rc = check(hipGetLastError(), "prefill launch"))) return rc;
+    if (hidden_out &&
+        (rc = check(hipMemcpyAsync(hidden_out + (size_t)c0 * H, pf.hid, (size_t)n * H * 4, hipMemcpyDeviceToHost, s),
+                    "hidden rows")))
+      return rc;
+  }
+  if ((rc = check(hipEventRecord(ev_stop, s), "event"))) return rc;
+  if ((rc = check(hipStreamSynchronize(s), "prefill"))) return rc;
+  float ms = 0.0f;
+  if ((rc = check(hipEventElapsedTime(&ms, ev_start, ev_stop), "event"))) return rc;
+  last_prefill_ms = ms;
+  past = S;
   return MTG_OK;
 }
 

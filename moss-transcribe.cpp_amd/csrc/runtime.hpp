@@ -68,6 +68,16 @@ struct Ctx {
   StepResult* result_host = nullptr;  // pinned
   StepResult* result_map = nullptr;   // result_host as the device sees it (the step kernel writes it)
   GraphSlot graphs[2 * kModes];
+  // prompt prefill over blocks of up to kPfRows rows (prefill.hip), allocated at
+  // the first prefill
+  static constexpr int kPfRows = 2048;
+  struct PfBuffers {
+    float *x = nullptr, *qkv = nullptr, *q = nullptr, *act = nullptr, *hid = nullptr;
+    int8_t* codes = nullptr;
+    float* scales = nullptr;
+  } pf;
+  bool prefill_fast_enabled = true;
+  double last_prefill_ms = 0.0;  // device time of the last prefill (HIP events)
 
   ~Ctx();
   int fail(int code, const char* fmt, ...);
@@ -93,6 +103,10 @@ struct Ctx {
   int verify(const int32_t* tokens, int T, const int32_t* history, int n_history, float penalty,
              int32_t* choice_out, int32_t* n_match_out, float* hidden_out, float* logits_out);
   int append(const float* embeds, int T, float* hidden_out);
+  // reset + S prompt rows; the block path when the weights are q8_0 and the
+  // context fits the prefill attention, else verify-size appends
+  int prefill(const float* embeds, int S, float* hidden_out);
+  int prefill_blocks(const float* embeds, int S, float* hidden_out);
   int logits_of(const float* hidden, int T, float* logits_out);
   int embed(const int32_t* ids, int n, float* out);
   int kv_io(void* k, void* v, int n_pos, bool write);

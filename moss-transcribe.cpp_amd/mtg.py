@@ -79,6 +79,8 @@ SIGNATURES = {
     "mtg_rewind": (c_int32, [c_void_p, c_int32]),
     "mtg_embed": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
     "mtg_prefill": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
+    "mtg_prefill_mode": (c_int32, [c_void_p, c_int32]),
+    "mtg_last_prefill_ms": (c_double, [c_void_p]),
     "mtg_append": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
     "mtg_logits": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
     "mtg_verify": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_int32, c_float, c_void_p,
@@ -296,6 +298,13 @@ class Decoder:
         hid = np.empty((S, self.hp.hidden), np.float32) if want_hidden else None
         self._chk(lib().mtg_prefill(self.ctx, ptr(embeds), S, ptr(hid)))
         return hid
+
+    def prefill_mode(self, blocks):
+        self._chk(lib().mtg_prefill_mode(self.ctx, 1 if blocks else 0))
+
+    @property
+    def last_prefill_ms(self):
+        return lib().mtg_last_prefill_ms(self.ctx)
 
     def append(self, embeds):
         embeds = f32(embeds)
