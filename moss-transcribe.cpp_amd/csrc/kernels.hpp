@@ -96,7 +96,7 @@ hipError_t prepare_kernels_pf();
 void launch_pf_norm_quant(hipStream_t s, const float* src, int S, const float* gain, float eps, int8_t* codes,
                           float* scales, float* normed_out);
 void launch_pf_quant(hipStream_t s, const float* src, int S, int K, int8_t* codes, float* scales);
-// out[s][n] (= / += / swiglu with w2) q8_0 GEMM of packed tiles (N % 32 == 0)
+// out[s][n] (= / += / swiglu with w2) q8_0 GEMM of packed tiles (N % 64 == 0)
 void launch_pf_gemm(hipStream_t s, int epi, const uint8_t* w, const uint8_t* w2, int N, int K, const int8_t* codes,
                     const float* scales, int S, float* out);
 void launch_pf_qk_rope(hipStream_t s, const float* qkv, int S, int past0, int n_heads, int n_kv_heads,

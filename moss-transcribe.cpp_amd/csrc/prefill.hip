@@ -8,11 +8,12 @@
 //   k_pf_norm_quant  RMSNorm * gain and the q8_0 activation conversion, compact
 //                    layout: codes [S][K] int8, scales [S][K/32] (f16 values)
 //   k_pf_gemm        q8_0 weight tiles x activation rows on v_mfma_i32_16x16x64_i8
-//                    (block-diagonal B operand: two exact per-block int32 dots per
-//                    MFMA), epilogue store / residual add / SwiGLU
+//                    (block-diagonal B operand from LDS-staged codes: two exact
+//                    per-block int32 dots per MFMA), epilogue store / residual
+//                    add / SwiGLU
 //   k_pf_quant       q8_0 conversion of f32 rows (the SwiGLU output)
 //   k_pf_qk_rope     q/k RMSNorm + NEOX RoPE, K/V written into the cache
-//   k_pf_attn        causal attention of 16 query rows x 2 q heads per
+//   k_pf_attn        causal attention of 16 query rows of one q head per
 //                    workgroup over the cache, in two passes over the 64-key
 //                    chunks, writing the o-projection's q8_0 activation
 // Every reduction follows the canonical order of device_common.hpp, so hidden
@@ -127,112 +128,139 @@ k_pf_quant(const float* __restrict__ src, int S, int K, int8_t* __restrict__ cod
 }
 
 // ----------------------------------------------------------------- GEMM ----
-// out[s][n] for weight tiles tile0 .. tile0 + TPW - 1 (16 rows each) and the 64
-// activation rows of blockIdx.y; wave w takes rows s0 + 16 w .. + 15 as two
-// column groups of 8. Per block pair the lane's B operand holds 16 code bytes of
-// row (8 cg + j % 8), block 2 bp + j / 8, when (lane / 16) / 2 == j / 8 (j =
-// lane % 16), else zeros, so each MFMA returns the exact int32 dot of every
-// (weight row, activation row, block). EPI_SWIGLU: TPW tiles of w (gate) and the
-// same TPW tiles of w2 (up).
+// out[s][n] for the 64 weight rows of blockIdx.x (wave w: tile 4 blockIdx.x + w;
+// for SwiGLU waves 0, 1 take gate tiles 2 blockIdx.x + {0, 1} and waves 2, 3 the
+// same tiles of the up matrix, meeting in LDS for the epilogue) and the 64
+// activation rows of blockIdx.y (8 column groups of 8). The block pairs run in
+// order; per pair the activation codes of the 64 rows are staged in LDS (the
+// next pair's already in flight in registers), and each wave's B operand of
+// column group cg holds 16 code bytes of row 8 cg + j % 8, block 2 bp + j / 8,
+// when (lane / 16) / 2 == j / 8 (j = lane % 16), else zeros, so each MFMA returns
+// the exact int32 dot of every (weight row, activation row, block). The K-slices
+// run one after the other, so one accumulator per slice and a running total
+// give ((s0 + s1) + s2) + s3 per parity, then even + odd.
 enum { PF_STORE = 0, PF_RESID = 1, PF_SWIGLU = 2 };
+constexpr int kPfRowBytes = 80;  // LDS stride of a staged 64-byte code row (bank spread)
 
-template <int EPI, int TPW>
+template <int EPI>
 __global__ void __launch_bounds__(256)
 k_pf_gemm(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int N, int K,
           const int8_t* __restrict__ codes, const float* __restrict__ scales, int S, float* __restrict__ out) {
-  constexpr int NM = EPI == PF_SWIGLU ? 2 : 1;
-  constexpr int NT = NM * TPW;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int tile0 = blockIdx.x * TPW;
-  const int s0 = blockIdx.y * 64 + 16 * wave;
+  constexpr bool GLU = EPI == PF_SWIGLU;
+  __shared__ __align__(16) uint8_t s_codes[2][64 * kPfRowBytes];
+  __shared__ float s_dx[2][64 * 2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tile = GLU ? blockIdx.x * 2 + (wave & 1) : blockIdx.x * 4 + wave;
+  const uint8_t* mat = (GLU && wave >= 2) ? w2 : w;
+  const int s0 = blockIdx.y * 64;
   const int bps = K / kPairK;
   const int j = lane & 15, g = lane >> 4, par = j >> 3;
   const bool holds = (g >> 1) == par;
   const int srow = par * 16 + 4 * (lane >> 4);
-  int rows[2];
-  bool rin[2];
-#pragma unroll
-  for (int cg = 0; cg < 2; ++cg) {
-    rows[cg] = s0 + 8 * cg + (j & 7);
-    rin[cg] = rows[cg] < S;
-  }
   const v4i zero = {0, 0, 0, 0};
-  float part[4][NT][2][4];
+  // staging: thread t loads 16 bytes of row t / 4 (part t % 4); threads < 128 a scale
+  const int st_row = tid >> 2, st_part = tid & 3;
+  const bool st_in = s0 + st_row < S;
+  const int sc_row = tid >> 1, sc_par = tid & 1;
+  const bool sc_in = tid < 128 && s0 + sc_row < S;
+  auto fetch = [&](int bp, v4i& c, float& d) {
+    c = st_in ? *(const v4i*)(codes + (size_t)(s0 + st_row) * K + 64 * bp + 16 * st_part) : zero;
+    d = sc_in ? scales[(size_t)(s0 + sc_row) * (K / 32) + 2 * bp + sc_par] : 0.0f;
+  };
+  auto stage = [&](int buf, const v4i& c, float d) {
+    *(v4i*)(s_codes[buf] + st_row * kPfRowBytes + 16 * st_part) = c;
+    if (tid < 128) s_dx[buf][sc_row * 2 + sc_par] = d;
+  };
+  v4i nc;
+  float nd;
+  fetch(0, nc, nd);
+  stage(0, nc, nd);
+  float part[8][4], tot[8][4];
 #pragma unroll
-  for (int sl = 0; sl < 4; ++sl)
+  for (int cg = 0; cg < 8; ++cg)
 #pragma unroll
-    for (int m = 0; m < NT; ++m)
+    for (int q = 0; q < 4; ++q) part[cg][q] = tot[cg][q] = 0.0f;
+  // the weight unit of the next pair is in flight while a pair computes
+  const uint8_t* wtile = mat + (size_t)tile * bps * kUnitBytes;
+  v4i na = __builtin_nontemporal_load((const v4i*)(wtile + lane * 16));
+  uint2 nsw = *(const uint2*)(wtile + 1024 + srow * 2);
+  int sl = 0, sl_end = bps / 4;
+  for (int bp = 0; bp < bps; ++bp) {
+    const int buf = bp & 1;
+    if (bp + 1 < bps) fetch(bp + 1, nc, nd);
+    const v4i a = na;
+    const uint2 sw = nsw;
+    if (bp + 1 < bps) {
+      const uint8_t* unit = wtile + (size_t)(bp + 1) * kUnitBytes;
+      na = __builtin_nontemporal_load((const v4i*)(unit + lane * 16));
+      nsw = *(const uint2*)(unit + 1024 + srow * 2);
+    }
+    float dw[4];
+    dw[0] = half_bits_to_float((uint16_t)(sw.x & 0xffff));
+    dw[1] = half_bits_to_float((uint16_t)(sw.x >> 16));
+    dw[2] = half_bits_to_float((uint16_t)(sw.y & 0xffff));
+    dw[3] = half_bits_to_float((uint16_t)(sw.y >> 16));
+    __syncthreads();  // the staged pair bp is complete
 #pragma unroll
-      for (int cg = 0; cg < 2; ++cg)
+    for (int cg = 0; cg < 8; ++cg) {
+      const int row = 8 * cg + (j & 7);
+      const v4i b = holds ? *(const v4i*)(s_codes[buf] + row * kPfRowBytes + 32 * par + 16 * (g & 1)) : zero;
+      const float dx = s_dx[buf][row * 2 + par];
+      const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, zero, 0, 0, 0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) part[sl][m][cg][q] = 0.0f;
+      for (int q = 0; q < 4; ++q) part[cg][q] = fmaf((float)c[q], dw[q] * dx, part[cg][q]);
+    }
+    if (bp + 1 == sl_end) {  // a K-slice ends: fold it into the running total
 #pragma unroll
-  for (int sl = 0; sl < 4; ++sl) {
-    const int bp1 = (bps * (sl + 1)) / 4;
-#pragma unroll 2
-    for (int bp = (bps * sl) / 4; bp < bp1; ++bp) {
-      v4i b[2];
-      float dx[2];
+      for (int cg = 0; cg < 8; ++cg)
 #pragma unroll
-      for (int cg = 0; cg < 2; ++cg) {
-        b[cg] = (holds && rin[cg])
-                    ? *(const v4i*)(codes + (size_t)rows[cg] * K + 64 * bp + 32 * par + 16 * (g & 1))
-                    : zero;
-        dx[cg] = rin[cg] ? scales[(size_t)rows[cg] * (K / 32) + 2 * bp + par] : 0.0f;
-      }
-#pragma unroll
-      for (int m = 0; m < NT; ++m) {
-        const uint8_t* mat = m < TPW ? w : w2;
-        const uint8_t* unit = mat + ((size_t)(tile0 + m % TPW) * bps + bp) * kUnitBytes;
-        const v4i a = __builtin_nontemporal_load((const v4i*)(unit + lane * 16));
-        const uint2 sw = *(const uint2*)(unit + 1024 + srow * 2);
-        float dw[4];
-        dw[0] = half_bits_to_float((uint16_t)(sw.x & 0xffff));
-        dw[1] = half_bits_to_float((uint16_t)(sw.x >> 16));
-        dw[2] = half_bits_to_float((uint16_t)(sw.y & 0xffff));
-        dw[3] = half_bits_to_float((uint16_t)(sw.y >> 16));
-#pragma unroll
-        for (int cg = 0; cg < 2; ++cg) {
-          const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[cg], zero, 0, 0, 0);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) part[sl][m][cg][q] = fmaf((float)c[q], dw[q] * dx[cg], part[sl][m][cg][q]);
+        for (int q = 0; q < 4; ++q) {
+          tot[cg][q] = sl == 0 ? part[cg][q] : __fadd_rn(tot[cg][q], part[cg][q]);
+          part[cg][q] = 0.0f;
         }
-      }
+      ++sl;
+      sl_end = (bps * (sl + 1)) / 4;
+    }
+    if (bp + 1 < bps) stage(buf ^ 1, nc, nd);  // the other buffer: read two steps ago, behind the barrier
+  }
+#pragma unroll
+  for (int cg = 0; cg < 8; ++cg)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) tot[cg][q] = __fadd_rn(tot[cg][q], dpp_f<kDppRor8>(tot[cg][q]));  // even + odd
+  if constexpr (GLU) {
+    // the up waves hand their values to the gate waves of the same tile
+    __syncthreads();
+    __shared__ __align__(16) float s_up[2 * 8 * 64 * 4];  // [2 tiles][8 cg][64 lanes][4]
+    if (wave >= 2)
+#pragma unroll
+      for (int cg = 0; cg < 8; ++cg)
+        *(v4f*)(s_up + (((wave & 1) * 8 + cg) * 64 + lane) * 4) = (v4f){tot[cg][0], tot[cg][1], tot[cg][2], tot[cg][3]};
+    __syncthreads();
+    if (wave >= 2) return;
+#pragma unroll
+    for (int cg = 0; cg < 8; ++cg) {
+      const v4f u = *(const v4f*)(s_up + (((wave & 1) * 8 + cg) * 64 + lane) * 4);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) tot[cg][q] = dev_swiglu(tot[cg][q], u[q]);
     }
   }
-  float acc[NT][2][4];
-#pragma unroll
-  for (int m = 0; m < NT; ++m)
-#pragma unroll
-    for (int cg = 0; cg < 2; ++cg)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float v = __fadd_rn(__fadd_rn(__fadd_rn(part[0][m][cg][q], part[1][m][cg][q]), part[2][m][cg][q]),
-                                  part[3][m][cg][q]);
-        acc[m][cg][q] = __fadd_rn(v, dpp_f<kDppRor8>(v));  // even + odd parity
-      }
   if (j < 8) {
+    const int n = tile * 16 + 4 * (lane >> 4);
 #pragma unroll
-    for (int cg = 0; cg < 2; ++cg) {
-      if (!rin[cg]) continue;
-      const size_t rowoff = (size_t)rows[cg] * N;
+    for (int cg = 0; cg < 8; ++cg) {
+      const int row = s0 + 8 * cg + j;
+      if (row >= S) continue;
+      float* dst = out + (size_t)row * N + n;
+      v4f v;
+      if (EPI == PF_RESID) {
+        const v4f x = *(const v4f*)dst;
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        const int n = (tile0 + t) * 16 + 4 * (lane >> 4);
-        v4f v;
-        if (EPI == PF_STORE) {
+        for (int q = 0; q < 4; ++q) v[q] = __fadd_rn(x[q], tot[cg][q]);
+      } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = acc[t][cg][q];
-        } else if (EPI == PF_RESID) {
-          const v4f x = *(const v4f*)(out + rowoff + n);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = __fadd_rn(x[q], acc[t][cg][q]);
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = dev_swiglu(acc[t][cg][q], acc[TPW + t][cg][q]);
-        }
-        *(v4f*)(out + rowoff + n) = v;
+        for (int q = 0; q < 4; ++q) v[q] = tot[cg][q];
       }
+      *(v4f*)dst = v;
     }
   }
 }
@@ -286,53 +314,74 @@ k_pf_qk_rope(const float* __restrict__ qkv, int S, int past0, int n_heads, int n
 }
 
 // ------------------------------------------------------------ attention ----
-// grid (n_kv_heads, ceil(S / 16)): workgroup (g, qb) takes query rows
-// r0 = 16 qb .. r0 + 15 (positions past0 + r0 + t) of q heads 2 g and 2 g + 1,
-// columns col = 16 hl + t. Keys 0 .. past0 + r0 + 15 come from the cache (this
-// block's rows were appended by k_pf_qk_rope). The output rows leave as the
+// grid (n_heads / kPfHeads, ceil(S / kPfRows)): a workgroup takes query rows
+// r0 .. r0 + kPfRows - 1 (positions past0 + r0 + t) of the kPfHeads q heads of
+// one kv head, columns col = kPfRows hl + t; the blocks with the most chunks are
+// numbered first. Keys 0 .. past0 + r0 + kPfRows - 1 come from the cache (this block's
+// rows were appended by k_pf_qk_rope). The output rows leave as the
 // o-projection's q8_0 activation: codes [S][n_heads * 128], scales [S][n_heads * 4].
 __device__ __forceinline__ int pf_perm128(int d) { return (d & 3) * 32 + (d >> 2); }
 
-// K (and V) rows of chunk key0 into LDS as f32: K permuted (element 4 s + kk at
-// kk * 32 + s), V plain; zeros past kvlen.
-template <bool WITH_V>
-__device__ __forceinline__ void pf_load_chunk(const KvLayer& kv, size_t head, int key0, int kvlen, float* s_k,
-                                              float* s_v) {
-  const int tid = threadIdx.x;
+// K and V of the 64-key chunk at key0 in MFMA operand layout, loaded straight
+// into registers (f32, or f16 widened; zeros past kvlen). Wave w: scores of keys
+// 16 w + kl, k[m] = K[key0 + 16 w + kl][4 m + kk] (m < 32, the fma chain over
+// head_dim in order); P.V of head_dim tiles 2 w, 2 w + 1,
+// v[h][s] = V[key0 + 4 s + kk][16 (2 w + h) + kl] (s < 16, the chain over keys).
+constexpr int kPfHeads = 2;     // q heads per workgroup (one kv head's group)
+constexpr int kPfRowTiles = 2;  // query rows per workgroup / 16
+constexpr int kPfRows = 16 * kPfRowTiles;
+constexpr int kPfCols = kPfHeads * kPfRows;  // column tile ct: q head ct / kPfRowTiles, rows 16 (ct % kPfRowTiles) + kl
+
+typedef __amdgpu_buffer_rsrc_t PfRsrc;
+// A buffer descriptor over kv head rows [0, kvlen): loads past its end return 0.
+// The range check covers the per-lane offset only, so every key-dependent part
+// of an address goes there (the scalar offset stays 0).
+__device__ __forceinline__ PfRsrc pf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+template <int KVH>
+__device__ __forceinline__ float pf_kv(PfRsrc r, uint32_t voff, uint32_t soff) {
+  if constexpr (KVH)
+    return half_bits_to_float((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0));
+  else
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+template <int KVH>
+__device__ __forceinline__ void pf_load_k(PfRsrc rk, int key0, float (&k)[32]) {
+  constexpr int es = KVH ? 2 : 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kl = lane & 15, kk = lane >> 4;
+  const uint32_t voff = (uint32_t)(((key0 + 16 * wave + kl) * kHeadDim + kk) * es);
 #pragma unroll
-  for (int i = 0; i < kChunk * kHeadDim / 4 / 256; ++i) {
-    const int idx = i * 256 + tid, jk = idx / (kHeadDim / 4), d = (idx % (kHeadDim / 4)) * 4;
-    const int key = key0 + jk;
-    const bool in = key < kvlen;
-    const v4f kf = in ? kv_load4(kv.k, kv.f16, head + (size_t)key * kHeadDim + d) : (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int m = 0; m < 32; ++m) k[m] = pf_kv<KVH>(rk, voff + 4 * m * es, 0);
+}
+template <int KVH>
+__device__ __forceinline__ void pf_load_v(PfRsrc rv, int key0, float (&v)[2][16]) {
+  constexpr int es = KVH ? 2 : 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kl = lane & 15, kk = lane >> 4;
+  const uint32_t voff = (uint32_t)(((key0 + kk) * kHeadDim + 32 * wave + kl) * es);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s_k[jk * kPfQStride + pf_perm128(d + e)] = kf[e];
-    if (WITH_V) {
-      const v4f vf = in ? kv_load4(kv.v, kv.f16, head + (size_t)key * kHeadDim + d) : (v4f){0.f, 0.f, 0.f, 0.f};
-      *(v4f*)(s_v + jk * kPfQStride + d) = vf;
-    }
-  }
+  for (int s2 = 0; s2 < 16; ++s2)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) v[h][s2] = pf_kv<KVH>(rv, voff + (4 * s2 * kHeadDim + 16 * h) * es, 0);
 }
 
 // Scores of keys 16 wave + 4 kk + r (r < 4) for columns 16 ct + kl, scaled and
-// masked: acc[ct][r]. The fma chain over head_dim is 32 chained MFMAs.
-__device__ __forceinline__ void pf_scores(const float* s_q, const float* s_k, int key0, int kvlen, int past0,
-                                          int r0, int nq, float scale, float (&w)[2][4]) {
+// masked: the fma chain over head_dim is 32 chained MFMAs.
+template <int NCT>
+__device__ __forceinline__ void pf_scores(const float* s_q, const float (&k)[32], int key0, int kvlen, int past0,
+                                          int r0, int nq, float scale, float (&w)[NCT][4]) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kl = lane & 15, kk = lane >> 4;
-  const float* krow = s_k + (16 * wave + kl) * kPfQStride + kk * 32;
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
+  for (int ct = 0; ct < NCT; ++ct) {
     const float* qrow = s_q + (ct * 16 + kl) * kPfQStride + kk * 32;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const v4f k4 = *(const v4f*)(krow + 4 * i);
       const v4f q4 = *(const v4f*)(qrow + 4 * i);
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[jj], q4[jj], acc, 0, 0, 0);
+      for (int jj = 0; jj < 4; ++jj) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[4 * i + jj], q4[jj], acc, 0, 0, 0);
     }
-    // the MFMA's column kl is this lane's column; rows are keys 16 wave + 4 kk + r
-    const int t = kl;  // column 16 ct + kl is query row kl of head 2 g + ct
+    const int t = 16 * (ct % kPfRowTiles) + kl;  // column 16 ct + kl: row t of q head ct / kPfRowTiles
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int key = key0 + 16 * wave + 4 * kk + r;
@@ -341,108 +390,112 @@ __device__ __forceinline__ void pf_scores(const float* s_q, const float* s_k, in
   }
 }
 
-constexpr int kPfMaxChunks = 320;  // 20,480 positions
 constexpr size_t kPfAttnLds =
-    ((size_t)32 * kPfQStride + 2 * (size_t)kChunk * kPfQStride + 32 * kPfPStride + (size_t)kPfMaxChunks * 32 +
-     4 * 32 + 3 * 32) * 4;
+    ((size_t)kPfCols * kPfQStride + kPfCols * kPfPStride + 4 * kPfCols + 3 * kPfCols) * 4;
 
+template <int KVH>
 __global__ void __launch_bounds__(256)
-k_pf_attn(const float* __restrict__ q, int n_heads, KvLayer kv, int past0, int S, int8_t* __restrict__ ocodes,
-          float* __restrict__ oscales) {
-  const int g = blockIdx.x, r0 = blockIdx.y * 16;
-  const int nq = min(16, S - r0);
+k_pf_attn(const float* __restrict__ q, int n_heads, int n_kv_heads, KvLayer kv, int past0, int S,
+          int8_t* __restrict__ ocodes, float* __restrict__ oscales) {
+  constexpr int NCT = kPfCols / 16, NC = kPfCols;
+  // the query blocks with the most chunks start first
+  const int hq0 = blockIdx.x * kPfHeads, g = hq0 / (n_heads / n_kv_heads);
+  const int r0 = (gridDim.y - 1 - blockIdx.y) * kPfRows;
+  const int nq = min(kPfRows, S - r0);
   const int kvlen = past0 + S;
   const int last = past0 + r0 + nq - 1;  // the block's last query position
   const int nch = last / kChunk + 1;
   extern __shared__ v4f pf_lds_v4[];
-  float* s_q = (float*)pf_lds_v4;                  // [32][132] permuted
-  float* s_k = s_q + 32 * kPfQStride;              // [64][132] permuted
-  float* s_v = s_k + kChunk * kPfQStride;          // [64][132]
-  float* s_p = s_v + kChunk * kPfQStride;          // [32][68] permuted keys
-  float* s_m = s_p + 32 * kPfPStride;              // [chunk][32] column maxima
-  float* s_wm = s_m + kPfMaxChunks * 32;           // [4 waves][32]
-  float* s_l = s_wm + 4 * 32;                      // [32] chunk sums
-  float* s_f = s_l + 32;                           // [32] chunk factors
-  float* s_M = s_f + 32;                           // [32] column maxima over all chunks
+  float* s_q = (float*)pf_lds_v4;                  // [NC][132] permuted
+  float* s_p = s_q + NC * kPfQStride;              // [NC][68] permuted keys
+  float* s_wm = s_p + NC * kPfPStride;             // [4 waves][NC]
+  float* s_l = s_wm + 4 * NC;                      // [NC] chunk sums
+  float* s_f = s_l + NC;                           // [NC] chunk factors
+  float* s_M = s_f + NC;                           // [NC] column maxima over all chunks
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, kl = lane & 15, kk = lane >> 4;
-  const bool f16kv = kv.f16 != 0;
+  constexpr bool f16kv = KVH != 0;
   // q rows (f16-rounded for an f16 cache: mul_mat(f16 K, f32 q) converts q)
-  for (int idx = tid; idx < 32 * (kHeadDim / 4); idx += 256) {
-    const int col = idx / (kHeadDim / 4), d = (idx % (kHeadDim / 4)) * 4, hl = col >> 4, t = col & 15;
+  for (int idx = tid; idx < NC * (kHeadDim / 4); idx += 256) {
+    const int col = idx / (kHeadDim / 4), d = (idx % (kHeadDim / 4)) * 4, hl = col / kPfRows, t = col % kPfRows;
     v4f v = {0.f, 0.f, 0.f, 0.f};
-    if (t < nq) v = *(const v4f*)(q + ((size_t)(r0 + t) * n_heads + 2 * g + hl) * kHeadDim + d);
+    if (t < nq) v = *(const v4f*)(q + ((size_t)(r0 + t) * n_heads + hq0 + hl) * kHeadDim + d);
 #pragma unroll
     for (int e = 0; e < 4; ++e) s_q[col * kPfQStride + pf_perm128(d + e)] = f16kv ? f16_round(v[e]) : v[e];
   }
-  const size_t head = (size_t)g * kv.max_seq * kHeadDim;
+  constexpr int es = KVH ? 2 : 4;
+  const size_t head = (size_t)g * kv.max_seq * kHeadDim * es;
+  const uint32_t kvbytes = (uint32_t)kvlen * kHeadDim * es;
+  const PfRsrc rk = pf_rsrc((const uint8_t*)kv.k + head, kvbytes);
+  const PfRsrc rv = pf_rsrc((const uint8_t*)kv.v + head, kvbytes);
   const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)kHeadDim));
-  // pass 1: chunk maxima per column
-  for (int c = 0; c < nch; ++c) {
-    __syncthreads();
-    pf_load_chunk<false>(kv, head, c * kChunk, kvlen, s_k, s_v);
-    __syncthreads();
-    float w[2][4];
-    pf_scores(s_q, s_k, c * kChunk, kvlen, past0, r0, nq, scale, w);
+  float kr[32], vr[2][16];
+  // pass 1: each column's maximum over all chunks (exact in any order)
+  pf_load_k<KVH>(rk, 0, kr);
+  __syncthreads();
+  int colmax[NCT];  // per column tile: the lane's column kl
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      int mk = max(max(ord_key(w[ct][0]), ord_key(w[ct][1])), max(ord_key(w[ct][2]), ord_key(w[ct][3])));
-      uint32_t a, b;
-      pair_split<16>((uint32_t)mk, a, b);  // lanes kk and kk ^ 1 (same column)
-      mk = max((int)a, (int)b);
-      pair_split<32>((uint32_t)mk, a, b);  // kk ^ 2
-      mk = max((int)a, (int)b);
-      if (kk == 0) s_wm[wave * 32 + ct * 16 + kl] = ord_val(mk);
-    }
-    __syncthreads();
-    if (tid < 32)
-      s_m[c * 32 + tid] = fmaxf(fmaxf(s_wm[tid], s_wm[32 + tid]), fmaxf(s_wm[64 + tid], s_wm[96 + tid]));
+  for (int ct = 0; ct < NCT; ++ct) colmax[ct] = ord_key(-INFINITY);
+  for (int c = 0; c < nch; ++c) {
+    float w[NCT][4];
+    pf_scores<NCT>(s_q, kr, c * kChunk, kvlen, past0, r0, nq, scale, w);
+    if (c + 1 < nch) pf_load_k<KVH>(rk, (c + 1) * kChunk, kr);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) colmax[ct] = max(colmax[ct], ord_key(w[ct][r]));
+  }
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    uint32_t a, b;
+    pair_split<16>((uint32_t)colmax[ct], a, b);  // the lanes kk of one column
+    colmax[ct] = max((int)a, (int)b);
+    pair_split<32>((uint32_t)colmax[ct], a, b);
+    colmax[ct] = max((int)a, (int)b);
+    if (kk == 0) s_wm[wave * NC + ct * 16 + kl] = ord_val(colmax[ct]);
   }
   __syncthreads();
-  if (tid < 32) {  // the columns' overall maxima (exact in any order)
-    float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, s_m[c * 32 + tid]);
-    s_M[tid] = M;
-  }
+  if (tid < NC)
+    s_M[tid] = fmaxf(fmaxf(s_wm[tid], s_wm[NC + tid]), fmaxf(s_wm[2 * NC + tid], s_wm[3 * NC + tid]));
   // pass 2: probabilities, chunk sums, P.V, merged in chunk order
-  float O[2][2][4], L[2][4];
+  float O[NCT][2][4], L[NCT][4];
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
+  for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       L[ct][r] = 0.0f;
       O[ct][0][r] = O[ct][1][r] = 0.0f;
     }
   const int sp_pos = (lane & 3) * 16 + (lane >> 2);
+  pf_load_k<KVH>(rk, 0, kr);
+  pf_load_v<KVH>(rv, 0, vr);
   for (int c = 0; c < nch; ++c) {
-    __syncthreads();
-    pf_load_chunk<true>(kv, head, c * kChunk, kvlen, s_k, s_v);
-    __syncthreads();
-    float w[2][4];
-    pf_scores(s_q, s_k, c * kChunk, kvlen, past0, r0, nq, scale, w);
+    float w[NCT][4];
+    pf_scores<NCT>(s_q, kr, c * kChunk, kvlen, past0, r0, nq, scale, w);
+    if (c + 1 < nch) pf_load_k<KVH>(rk, (c + 1) * kChunk, kr);
+    __syncthreads();  // the previous chunk's probabilities are consumed
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
+    for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
       for (int r = 0; r < 4; ++r)  // key 16 wave + 4 kk + r sits at r * 16 + 4 wave + kk
         s_p[(ct * 16 + kl) * kPfPStride + r * 16 + 4 * wave + kk] = w[ct][r];
     __syncthreads();
     // chunk softmax per column (one wave per column, lane = key)
-    for (int col = wave; col < 32; col += 4) {
+    for (int col = wave; col < NC; col += 4) {
       const float wv = s_p[col * kPfPStride + sp_pos];
-      const float m = s_m[c * 32 + col];
+      const float m = wave_max_f(wv);
       float p = (m == -INFINITY || wv == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(wv, m));
       if (f16kv) p = f16_round(p);
       const float l = wave_sum_f(p);
       s_p[col * kPfPStride + sp_pos] = p;
-      if (lane == 0) s_l[col] = l;
-    }
-    if (tid < 32) {
-      const float m = s_m[c * 32 + tid];
-      s_f[tid] = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, s_M[tid]));
+      if (lane == 0) {
+        s_l[col] = l;
+        s_f[col] = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, s_M[col]));
+      }
     }
     __syncthreads();
     // O_c[col][d]: fma chain over the chunk's keys; wave w takes head_dim tiles 2w, 2w+1
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
+    for (int ct = 0; ct < NCT; ++ct) {
       float pa[16];
       const float* prow = s_p + (ct * 16 + kl) * kPfPStride + kk * 16;
 #pragma unroll
@@ -453,16 +506,11 @@ k_pf_attn(const float* __restrict__ q, int n_heads, KvLayer kv, int past0, int S
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int d = 16 * (2 * wave + h) + kl;
         v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s2 = 0; s2 < 16; ++s2)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s2], s_v[(4 * s2 + kk) * kPfQStride + d], acc, 0, 0, 0);
+        for (int s2 = 0; s2 < 16; ++s2) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s2], vr[h][s2], acc, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float f = s_f[ct * 16 + 4 * kk + r];
-          O[ct][h][r] = fmaf(acc[r], f, O[ct][h][r]);
-        }
+        for (int r = 0; r < 4; ++r) O[ct][h][r] = fmaf(acc[r], s_f[ct * 16 + 4 * kk + r], O[ct][h][r]);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -470,14 +518,15 @@ k_pf_attn(const float* __restrict__ q, int n_heads, KvLayer kv, int past0, int S
         L[ct][r] = fmaf(s_l[col], s_f[col], L[ct][r]);
       }
     }
+    if (c + 1 < nch) pf_load_v<KVH>(rv, (c + 1) * kChunk, vr);
   }
   // out = O / L, then the q8_0 blocks of 32 head_dim elements (wave w: block w)
   const int QN = n_heads * kHeadDim;
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
+  for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int t = 4 * kk + r;  // query row of column 16 ct + 4 kk + r
+      const int t = 16 * (ct % kPfRowTiles) + 4 * kk + r;  // query row of column 16 ct + 4 kk + r
       const float o0 = __fdiv_rn(O[ct][0][r], L[ct][r]);
       const float o1 = __fdiv_rn(O[ct][1][r], L[ct][r]);
       float amax = fmaxf(fabsf(o0), fabsf(o1));
@@ -489,11 +538,11 @@ k_pf_attn(const float* __restrict__ q, int n_heads, KvLayer kv, int past0, int S
       amax = __uint_as_float(u);
       if (t < nq) {
         const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-        const size_t rowoff = (size_t)(r0 + t) * QN + (2 * g + ct) * kHeadDim;
+        const size_t rowoff = (size_t)(r0 + t) * QN + (hq0 + ct / kPfRowTiles) * kHeadDim;
         ocodes[rowoff + 32 * wave + kl] = (int8_t)rintf(__fmul_rn(o0, id));
         ocodes[rowoff + 32 * wave + 16 + kl] = (int8_t)rintf(__fmul_rn(o1, id));
         if (kl == 0)
-          oscales[(size_t)(r0 + t) * (QN / 32) + ((2 * g + ct) * kHeadDim) / 32 + wave] =
+          oscales[(size_t)(r0 + t) * (QN / 32) + ((hq0 + ct / kPfRowTiles) * kHeadDim) / 32 + wave] =
               __half2float(__float2half_rn(__fdiv_rn(amax, 127.0f)));
       }
     }
@@ -502,7 +551,9 @@ k_pf_attn(const float* __restrict__ q, int n_heads, KvLayer kv, int past0, int S
 }  // namespace
 
 // ================================================================ launches ==
-int pf_max_context() { return kPfMaxChunks * kChunk; }
+// The buffer descriptors of the attention cover a kv head's rows with a 32-bit
+// byte count.
+int pf_max_context() { return (int)(0x7fffffffu / (kHeadDim * 4)); }
 
 void launch_pf_norm_quant(hipStream_t s, const float* src, int S, const float* gain, float eps, int8_t* codes,
                           float* scales, float* normed_out) {
@@ -516,13 +567,13 @@ void launch_pf_quant(hipStream_t s, const float* src, int S, int K, int8_t* code
 
 void launch_pf_gemm(hipStream_t s, int epi, const uint8_t* w, const uint8_t* w2, int N, int K, const int8_t* codes,
                     const float* scales, int S, float* out) {
-  const dim3 blocks((unsigned)(N / 16 / 2), (unsigned)((S + 63) / 64));
+  const dim3 blocks((unsigned)(epi == PF_SWIGLU ? N / 32 : N / 64), (unsigned)((S + 63) / 64));
   if (epi == PF_STORE)
-    hipLaunchKernelGGL((k_pf_gemm<PF_STORE, 2>), blocks, dim3(256), 0, s, w, w2, N, K, codes, scales, S, out);
+    hipLaunchKernelGGL(k_pf_gemm<PF_STORE>, blocks, dim3(256), 0, s, w, w2, N, K, codes, scales, S, out);
   else if (epi == PF_RESID)
-    hipLaunchKernelGGL((k_pf_gemm<PF_RESID, 2>), blocks, dim3(256), 0, s, w, w2, N, K, codes, scales, S, out);
+    hipLaunchKernelGGL(k_pf_gemm<PF_RESID>, blocks, dim3(256), 0, s, w, w2, N, K, codes, scales, S, out);
   else
-    hipLaunchKernelGGL((k_pf_gemm<PF_SWIGLU, 2>), blocks, dim3(256), 0, s, w, w2, N, K, codes, scales, S, out);
+    hipLaunchKernelGGL(k_pf_gemm<PF_SWIGLU>, blocks, dim3(256), 0, s, w, w2, N, K, codes, scales, S, out);
 }
 
 void launch_pf_qk_rope(hipStream_t s, const float* qkv, int S, int past0, int n_heads, int n_kv_heads,
@@ -534,12 +585,20 @@ void launch_pf_qk_rope(hipStream_t s, const float* qkv, int S, int past0, int n_
 
 void launch_pf_attn(hipStream_t s, const float* q, int n_heads, int n_kv_heads, KvLayer kv, int past0, int S,
                     int8_t* ocodes, float* oscales) {
-  hipLaunchKernelGGL(k_pf_attn, dim3((unsigned)n_kv_heads, (unsigned)((S + 15) / 16)), dim3(256), kPfAttnLds, s, q,
-                     n_heads, kv, past0, S, ocodes, oscales);
+  const dim3 grid((unsigned)(n_heads / kPfHeads), (unsigned)((S + kPfRows - 1) / kPfRows));
+  if (kv.f16)
+    hipLaunchKernelGGL(k_pf_attn<1>, grid, dim3(256), kPfAttnLds, s, q, n_heads, n_kv_heads, kv, past0, S, ocodes,
+                       oscales);
+  else
+    hipLaunchKernelGGL(k_pf_attn<0>, grid, dim3(256), kPfAttnLds, s, q, n_heads, n_kv_heads, kv, past0, S, ocodes,
+                       oscales);
 }
 
 hipError_t prepare_kernels_pf() {
-  return hipFuncSetAttribute((const void*)k_pf_attn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfAttnLds);
+  hipError_t e = hipFuncSetAttribute((const void*)k_pf_attn<0>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)kPfAttnLds);
+  if (e != hipSuccess) return e;
+  return hipFuncSetAttribute((const void*)k_pf_attn<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfAttnLds);
 }
 
 }  // namespace mtg
