@@ -333,7 +333,32 @@ int mtg_causal_context_dev(const float* v_dev, const float* p_dev, int32_t head_
                            int32_t kv_heads, int32_t heads, int32_t queries, int32_t kv_len,
                            float* out_dev);
 
-/* ---- synthetic model (workload generator; stands in for the GGUF loader) ---- */
+/* ---- GGUF model files (reference: ModelLoader::load / read_config,
+ * src/model_loader.cpp:21-169; tensor names src/qwen3.cpp:33-56,
+ * src/qwen3_decoder.cpp:53-57) ---- */
+
+typedef struct mtg_gguf mtg_gguf;
+/* Map and parse a GGUF (v2 / v3) file: header, metadata, tensor table, every
+ * tensor's data range checked against the file. On failure the reason is in
+ * mtg_gguf_error(NULL) (and mtg_last_error(NULL)). */
+int mtg_gguf_open(const char* path, mtg_gguf** out);
+void mtg_gguf_close(mtg_gguf* g);
+const char* mtg_gguf_error(const mtg_gguf* g);
+int64_t mtg_gguf_n_tensors(const mtg_gguf* g);
+/* One tensor by name: ggml type, ne[4], data in the mapping, bytes. */
+int mtg_gguf_tensor(const mtg_gguf* g, const char* name, int32_t* type, int64_t* ne, const void** data,
+                    size_t* bytes);
+/* The Qwen3 decoder of the file: hyper-parameters from the mtd.text.* keys
+ * (the reference's defaults where absent), every tensor found by name and
+ * checked for shape and for one weight type (q8_0, f16 or q4_K); f16 norm
+ * gains are widened to f32. NULL on failure (mtg_gguf_error). The description
+ * stays valid until mtg_gguf_close. */
+const mtg_model_desc* mtg_gguf_model(mtg_gguf* g);
+/* mtg_gguf_open + mtg_gguf_model + mtg_create; the file is unmapped before
+ * returning. */
+int mtg_create_from_gguf(const char* path, int32_t max_seq, int32_t kv_type, mtg_ctx** out);
+
+/* ---- synthetic model (workload generator for the benchmark and tests) ---- */
 
 typedef struct mtg_synth_model mtg_synth_model;
 /* Seeded N(0, std) weights quantized to weight_type, norm gains

@@ -20,7 +20,7 @@ ORACLE_LIB = os.path.join(ORACLE_DIR, "liboracle.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 SOURCES = ["kernels.hip", "kernels_wt.hip", "step_kernel.hip", "noalloc.hip", "prefill.hip", "runtime.cpp", "capi.cpp",
-           "synth.cpp", "reference_api.cpp"]
+           "synth.cpp", "gguf.cpp", "reference_api.cpp"]
 # -ffp-contract=off: elementwise ops round like the reference's scalar code;
 # fused multiply-adds are written explicitly (fmaf) where they are wanted.
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-pass-failed", "-Wno-unused-parameter", "-Wno-unused-value", "-Wno-unused-result",

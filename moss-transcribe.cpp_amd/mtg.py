@@ -117,6 +117,14 @@ SIGNATURES = {
     "mtg_q8_mul_mat_dev_noalloc": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p]),
     "mtg_causal_context_dev": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
                                          c_int32, c_void_p]),
+    "mtg_gguf_open": (c_int32, [ctypes.c_char_p, POINTER(c_void_p)]),
+    "mtg_gguf_close": (None, [c_void_p]),
+    "mtg_gguf_error": (ctypes.c_char_p, [c_void_p]),
+    "mtg_gguf_n_tensors": (c_int64, [c_void_p]),
+    "mtg_gguf_tensor": (c_int32, [c_void_p, ctypes.c_char_p, POINTER(c_int32), POINTER(c_int64),
+                                  POINTER(c_void_p), POINTER(ctypes.c_size_t)]),
+    "mtg_gguf_model": (POINTER(ModelDesc), [c_void_p]),
+    "mtg_create_from_gguf": (c_int32, [ctypes.c_char_p, c_int32, c_int32, POINTER(c_void_p)]),
     "mtg_synth_create": (c_int32, [POINTER(Hparams), c_int32, c_uint64, c_float, c_float,
                                    POINTER(c_void_p)]),
     "mtg_synth_free": (None, [c_void_p]),
@@ -211,6 +219,45 @@ class SynthModel:
         return out
 
 
+class GgufModel:
+    """A mapped GGUF file (mtg_gguf) and its decoder description."""
+
+    def __init__(self, path):
+        out = c_void_p()
+        rc = lib().mtg_gguf_open(os.fsencode(path), ctypes.byref(out))
+        if rc:
+            raise MtgError(rc, lib().mtg_gguf_error(None).decode())
+        self.handle = out
+        d = lib().mtg_gguf_model(out)
+        if not d:
+            msg = lib().mtg_gguf_error(out).decode()
+            self.close()
+            raise MtgError(ERR_INVALID, msg)
+        self.desc = d
+        self.hp = d.contents.hp
+        self.weight_type = d.contents.weight_type
+
+    def tensor(self, name):
+        """(ggml type, ne[4], raw bytes) of one tensor."""
+        t, ne, data, nb = c_int32(), (c_int64 * 4)(), c_void_p(), ctypes.c_size_t()
+        rc = lib().mtg_gguf_tensor(self.handle, name.encode(), ctypes.byref(t), ne, ctypes.byref(data),
+                                   ctypes.byref(nb))
+        if rc:
+            raise KeyError(name)
+        return t.value, list(ne), ctypes.string_at(data, nb.value)
+
+    def close(self):
+        if self.handle:
+            lib().mtg_gguf_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Decoder:
     """Device decoder context (mtg_ctx)."""
 
@@ -223,6 +270,25 @@ class Decoder:
         self.ctx = out
         self.kv_type = kv_type
         self.max_seq = max_seq
+
+    @classmethod
+    def from_gguf(cls, path, max_seq, kv_type=TYPE_F32):
+        """A decoder whose weights come from a GGUF file (mtg_create_from_gguf);
+        the file's hyper-parameters are read with mtg_gguf_open first."""
+        g = GgufModel(path)
+        hp = Hparams()
+        ctypes.memmove(ctypes.byref(hp), ctypes.byref(g.hp), ctypes.sizeof(Hparams))
+        g.close()
+        self = cls.__new__(cls)
+        self.hp = hp
+        out = c_void_p()
+        rc = lib().mtg_create_from_gguf(os.fsencode(path), max_seq, kv_type, ctypes.byref(out))
+        if rc:
+            raise MtgError(rc, lib().mtg_last_error(None).decode())
+        self.ctx = out
+        self.kv_type = kv_type
+        self.max_seq = max_seq
+        return self
 
     def _chk(self, rc):
         if rc:

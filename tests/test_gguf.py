@@ -1,0 +1,159 @@
+"""The GGUF loader (csrc/gguf.cpp; reference ModelLoader::load / read_config,
+src/model_loader.cpp:21-169) on the CPU: files written by tests/gguf_writer.py
+from a seeded synthetic model must give back every tensor byte for byte, the
+hyper-parameters, the weight type and f32 norm gains (f16 ones widened); damaged
+or foreign files must fail with a reason, never crash. The device decoder built
+from a file is checked against the one built from the model in
+test_gpu_gguf.py."""
+import ctypes
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import gguf_writer
+import mtg
+
+
+@pytest.fixture(scope="module", params=[mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_Q4_K], ids=["q8_0", "f16", "q4_K"])
+def model(request):
+    m = mtg.SynthModel(request.param, seed=7, std=0.02, gain_jitter=0.05, n_layers=2, vocab=2048)
+    yield m
+    m.close()
+
+
+def _desc_bytes(desc, hp, wt):
+    """Every tensor of a model description as bytes, in a fixed order."""
+    d = desc.contents
+    H, D = hp.hidden, hp.head_dim
+    QN, KN, F = hp.n_heads * D, hp.n_kv_heads * D, hp.intermediate
+    rb = lambda k: mtg.lib().mtg_row_bytes(wt, k)
+    out = [ctypes.string_at(d.token_embd, rb(H) * hp.vocab), ctypes.string_at(d.output_norm, 4 * H)]
+    for i in range(hp.n_layers):
+        L = d.layers[i]
+        out += [ctypes.string_at(L.attn_norm, 4 * H), ctypes.string_at(L.attn_q, rb(H) * QN),
+                ctypes.string_at(L.attn_k, rb(H) * KN), ctypes.string_at(L.attn_v, rb(H) * KN),
+                ctypes.string_at(L.attn_o, rb(QN) * H), ctypes.string_at(L.attn_q_norm, 4 * D),
+                ctypes.string_at(L.attn_k_norm, 4 * D), ctypes.string_at(L.ffn_norm, 4 * H),
+                ctypes.string_at(L.ffn_gate, rb(H) * F), ctypes.string_at(L.ffn_up, rb(H) * F),
+                ctypes.string_at(L.ffn_down, rb(F) * H)]
+    return out
+
+
+@pytest.mark.parametrize("alignment", [32, 64])
+def test_round_trip(model, tmp_path, alignment):
+    path = str(tmp_path / "m.gguf")
+    gguf_writer.write_model(path, model, alignment=alignment)
+    g = mtg.GgufModel(path)
+    hp = g.hp
+    for f in ("hidden", "n_heads", "n_kv_heads", "head_dim", "intermediate", "n_layers", "vocab"):
+        assert getattr(hp, f) == getattr(model.hp, f), f
+    assert hp.rms_eps == np.float32(model.hp.rms_eps) and hp.rope_base == np.float32(model.hp.rope_base)
+    assert g.weight_type == model.weight_type
+    assert mtg.lib().mtg_gguf_n_tensors(g.handle) == 2 + 11 * model.hp.n_layers
+    got = _desc_bytes(g.desc, hp, g.weight_type)
+    want = _desc_bytes(model.desc, model.hp, model.weight_type)
+    assert len(got) == len(want)
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert a == b, i
+    t, ne, raw = g.tensor("qwen3.blk.1.ffn_down.weight")
+    assert t == model.weight_type and ne[:2] == [model.hp.intermediate, model.hp.hidden]
+    g.close()
+
+
+def test_f16_norm_gains_are_widened(model, tmp_path):
+    path = str(tmp_path / "m16.gguf")
+    gguf_writer.write_model(path, model, f16_norms=True)
+    g = mtg.GgufModel(path)
+    H = model.hp.hidden
+    got = np.frombuffer(ctypes.string_at(g.desc.contents.layers[0].attn_norm, 4 * H), np.float32)
+    src = np.frombuffer(ctypes.string_at(model.desc.contents.layers[0].attn_norm, 4 * H), np.float32)
+    assert np.array_equal(got, src.astype(np.float16).astype(np.float32))
+    g.close()
+
+
+def test_defaults_when_metadata_is_absent(tmp_path):
+    """read_config's defaults (src/model_loader.cpp:118-128) are the Qwen3-0.6B
+    dims: a file without mtd.text.* keys is read with them, so a 2-layer file
+    fails on the missing layer 2 tensors, with the name in the message."""
+    m = mtg.SynthModel(mtg.TYPE_Q8_0, seed=8, n_layers=2, vocab=151936)
+    path = str(tmp_path / "nometa.gguf")
+    gguf_writer.write(path, [], [(n, t, ne, d) for n, t, ne, d in gguf_writer.model_tensors(m)])
+    with pytest.raises(mtg.MtgError) as e:
+        mtg.GgufModel(path)
+    assert "qwen3.blk.2." in str(e.value)
+    m.close()
+
+
+def _expect_failure(path, needle):
+    with pytest.raises(mtg.MtgError) as e:
+        mtg.GgufModel(path)
+    assert needle in str(e.value), str(e.value)
+    out = ctypes.c_void_p()
+    rc = mtg.lib().mtg_create_from_gguf(os.fsencode(path), 64, mtg.TYPE_F32, ctypes.byref(out))
+    assert rc != 0 and not out.value
+    assert needle in mtg.lib().mtg_last_error(None).decode()
+
+
+def test_damaged_and_foreign_files_fail_with_a_reason(tmp_path):
+    m = mtg.SynthModel(mtg.TYPE_Q8_0, seed=9, n_layers=1, vocab=512)
+    good = str(tmp_path / "good.gguf")
+    gguf_writer.write_model(good, m)
+    raw = open(good, "rb").read()
+    # bad magic
+    p = str(tmp_path / "magic.gguf")
+    open(p, "wb").write(b"GGUX" + raw[4:])
+    _expect_failure(p, "bad magic")
+    # truncated inside the metadata, and inside the tensor data
+    for cut, needle in ((200, "truncated"), (len(raw) - 1000, "outside the file")):
+        p = str(tmp_path / ("cut%d.gguf" % cut))
+        open(p, "wb").write(raw[:cut])
+        _expect_failure(p, needle)
+    # a missing tensor
+    p = str(tmp_path / "missing.gguf")
+    gguf_writer.write_model(p, m, edit=lambda ts: [t for t in ts if t[0] != "qwen3.blk.0.attn_o.weight"])
+    _expect_failure(p, "missing tensor qwen3.blk.0.attn_o.weight")
+    # a wrong shape
+    def transpose_q(ts):
+        return [(n, t, ne[::-1] if n == "qwen3.blk.0.attn_q.weight" else ne, d) for n, t, ne, d in ts]
+    p = str(tmp_path / "shape.gguf")
+    gguf_writer.write_model(p, m, edit=transpose_q)
+    _expect_failure(p, "shape")
+    # a matrix of another type than token_embd (f16 bytes of the same size class)
+    def f16_gate(ts):
+        out = []
+        for n, t, ne, d in ts:
+            if n == "qwen3.blk.0.ffn_gate.weight":
+                t, d = 1, np.zeros(ne[0] * ne[1], np.float16).tobytes()
+            out.append((n, t, ne, d))
+        return out
+    p = str(tmp_path / "mixed.gguf")
+    gguf_writer.write_model(p, m, edit=f16_gate)
+    _expect_failure(p, "mixed weight types")
+    # an unsupported weight type everywhere (Q6_K geometry: 210 bytes per 256)
+    def q6k(ts):
+        out = []
+        for n, t, ne, d in ts:
+            if t == 8:
+                t, d = 14, b"\0" * (ne[0] // 256 * 210 * ne[1])
+            out.append((n, t, ne, d))
+        return out
+    p = str(tmp_path / "q6k.gguf")
+    gguf_writer.write_model(p, m, edit=q6k)
+    _expect_failure(p, "not supported")
+    # a data offset that is not aligned
+    p = str(tmp_path / "align.gguf")
+    gguf_writer.write_model(p, m)
+    b = bytearray(open(p, "rb").read())
+    name = b"qwen3.output_norm.weight"
+    i = b.index(struct.pack("<Q", len(name)) + name) + 8 + len(name)
+    n_dims = struct.unpack_from("<I", b, i)[0]
+    off_pos = i + 4 + 8 * n_dims + 4
+    struct.pack_into("<Q", b, off_pos, struct.unpack_from("<Q", b, off_pos)[0] + 4)
+    open(p, "wb").write(bytes(b))
+    _expect_failure(p, "outside the file")
+    # not a file
+    with pytest.raises(mtg.MtgError):
+        mtg.GgufModel(str(tmp_path / "absent.gguf"))
+    m.close()
