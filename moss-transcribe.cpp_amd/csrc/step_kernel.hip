@@ -453,12 +453,16 @@ __device__ __forceinline__ void gain16_load(const float* __restrict__ gain, floa
 // Otherwise each lane loads its own 64 bytes (every load instruction then
 // touches all 32 lines of a row, ~20 % slower in a 256-workgroup broadcast, but
 // no LDS image and fewer registers: the 16-row variant keeps that form).
+// gain_late (nullable): the gains are loaded here, after the rows, instead of
+// coming prefetched in gv (the 16-row variant: 16 fewer registers held across
+// the phases, for 0.3 us more per panel).
 template <bool COAL>
-__device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv)[16], float eps, uint8_t* pcodes,
+__device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv_in)[16], float eps, uint8_t* pcodes,
                                            float* pscales, float* normed_out, float* stage,
-                                           const StepParams* prof = nullptr) {
+                                           const float* gain_late = nullptr, const StepParams* prof = nullptr) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   float* stg = stage + wave * kStageFloats;
+  float gv[16];
   for (int t0 = wave; t0 < T; t0 += 8) {
     // two rows per pass, all loads issued before any arithmetic
     v4f raw[2][4];
@@ -470,6 +474,12 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv)[16],
         for (int i = 0; i < 4; ++i)
           raw[j][i] = ldc4(x, (uint32_t)((t * cH + (COAL ? 4 * lane + 256 * i : 16 * lane + 4 * i)) * 4));
       }
+    }
+    if (gain_late) {
+      if (t0 == wave) gain16_load(gain_late, gv);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) gv[e] = gv_in[e];
     }
     if (prof && t0 == wave) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); wmark(*prof, 1, 13); }
 #pragma unroll
@@ -1367,7 +1377,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   }
   // prefetch layer 0: q|k|v tile and the first attention item's K / V
   wt_load<4>(layer_at(P, 0).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-  gain16_load(layer_at(P, 0).attn_norm, gq);
+  if constexpr (G == 1) gain16_load(layer_at(P, 0).attn_norm, gq);
   if (has_attn) kv_prefetch<KVH>(layer_at(P, 0), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
 
   for (int l = 0; l < L; ++l) {
@@ -1376,7 +1386,8 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     if (!wait_all(c, ph(l, kPhQkv) - 1)) return;
     MARK(P, 3 + 12 * l + 0);
     WMARK(P, l, 0);
-    panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, nullptr, stg, (PROF && P.timing && l == 1) ? &P : nullptr);
+    panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, nullptr, stg, G == 1 ? nullptr : Ly.attn_norm,
+                       (PROF && P.timing && l == 1) ? &P : nullptr);
     WMARK(P, l, 25);
     {
       float acc[1][G][4] = {};
@@ -1412,7 +1423,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       wt_load<4>(Ly.wg + (size_t)(2 * j + 1) * cBH * kUnitBytes, 4 * wave, ba + 4, bs + 4);
       wt_load<4>(Ly.wu + (size_t)(2 * j) * cBH * kUnitBytes, 4 * wave, ba + 8, bs + 8);
       wt_load<4>(Ly.wu + (size_t)(2 * j + 1) * cBH * kUnitBytes, 4 * wave, ba + 12, bs + 12);
-      gain16_load(Ly.ffn_norm, gf);
+      if constexpr (G == 1) gain16_load(Ly.ffn_norm, gf);
     }
     // ---- MERGE: (head, row) items, two at a time ----
     if (has_merge) {
@@ -1431,7 +1442,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       if (!gu && l + 1 < L) {  // nothing more in this layer: prefetch the next one
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-        gain16_load(Ln.attn_norm, gq);
+        if constexpr (G == 1) gain16_load(Ln.attn_norm, gq);
         if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
       }
     }
@@ -1457,7 +1468,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       // hold up the residual rows of the next q|k|v panel: loads complete in order)
       if (l + 1 < L) {
         wt_load<4>(layer_at(P, l + 1).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-        gain16_load(layer_at(P, l + 1).attn_norm, gq);
+        if constexpr (G == 1) gain16_load(layer_at(P, l + 1).attn_norm, gq);
         if (has_attn)
           kv_prefetch<KVH>(layer_at(P, l + 1), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
       }
@@ -1466,7 +1477,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     if (gu) {
       if (!wait_all(c, ph(l, kPhGu) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return;
       WMARK(P, l, 8);
-      panel_norm<G == 1>(RX, T, gf, P.eps, pcodes, pscales, nullptr, stg);
+      panel_norm<G == 1>(RX, T, gf, P.eps, pcodes, pscales, nullptr, stg, G == 1 ? nullptr : Ly.ffn_norm);
       WMARK(P, l, 27);
       float acc[4][G][4] = {};
 #pragma unroll
@@ -1479,7 +1490,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       if (l + 1 < L) {
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-        gain16_load(Ln.attn_norm, gq);
+        if constexpr (G == 1) gain16_load(Ln.attn_norm, gq);
         if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
       }
     }
@@ -1503,7 +1514,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     if (!od && !gu && !has_merge && l + 1 < L) {
       const LayerDev& Ln = layer_at(P, l + 1);
       wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
-      gain16_load(Ln.attn_norm, gq);
+      if constexpr (G == 1) gain16_load(Ln.attn_norm, gq);
       if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
     }
   }
@@ -1513,16 +1524,16 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   if (mode != kStepVerify) {
     if (w == 0) {
       if (!wait_all(c, lm - 1)) return;
-      gain16_load(P.out_norm, gq);
-      panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, P.hid, stg);
+      if constexpr (G == 1) gain16_load(P.out_norm, gq);
+      panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, P.hid, stg, G == 1 ? nullptr : P.out_norm);
       MARK(P, 2);
     }
     return;
   }
   if (!wait_all(c, lm - 1)) return;
   MARK(P, 3 + 12 * L);
-  gain16_load(P.out_norm, gq);
-  panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr, stg);
+  if constexpr (G == 1) gain16_load(P.out_norm, gq);
+  panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr, stg, G == 1 ? nullptr : P.out_norm);
   lm_head<G>(P, desc_arg.penalty, desc_arg.write_logits != 0, T, pcodes, pscales, s_best);
   publish(c, lm);
   MARK(P, 4 + 12 * L);
