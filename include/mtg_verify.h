@@ -227,6 +227,21 @@ int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids
                       float penalty, int32_t max_draft, mtg_draft_fn draft, mtg_commit_fn commit,
                       void* user, int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats);
 
+/* mtg_generate_from with the whole loop on the device (reference
+ * cpu_speculative_generate, src/cpu_speculative.cpp:68-147, with
+ * cpu_ngram_draft, :27-38): a controller kernel between the verify steps commits
+ * each step's accepted ids, applies the stop rules, drafts the next step and
+ * writes its descriptor, so the host neither drafts nor waits per step (it looks
+ * at the state every 8 steps). Same ids, counters, stop reason and KV position
+ * as mtg_generate_from with draft == NULL. No draft or commit hooks; stats carry
+ * no draft time (verify_seconds is the whole run). MTG_ERR_UNSUPPORTED unless
+ * the step kernel runs this model (q8_0 weights, MTG_EXEC_STEP_KERNEL) and
+ * max_draft <= 7. A step abandoned on a bounded wait is finished by the host
+ * controller from the same state. */
+int mtg_generate_device(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
+                        int32_t max_new, int32_t max_steps, int32_t eos, float penalty, int32_t max_draft,
+                        int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats);
+
 /* Draft hook for long-context workloads (pass mtg_stream_draft as `draft` and a
  * mtg_stream_drafter as `user`): the reference n-gram proposal over
  * prompt ++ ids, completed up to the budget from a periodic token stream

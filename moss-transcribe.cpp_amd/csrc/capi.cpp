@@ -389,6 +389,74 @@ int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids
   return rc;
 }
 
+int mtg_generate_device(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
+                        int32_t max_new, int32_t max_steps, int32_t eos, float penalty, int32_t max_draft,
+                        int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats) {
+  if (!ctx) return MTG_ERR_INVALID;
+  Ctx& c = ctx->impl;
+  if (!ids_out || !n_ids_out || max_new <= 0 || n_prior < 0 || (n_prior > 0 && !prior_ids) || first_seed < 0 ||
+      first_seed >= c.hp.vocab)
+    return c.fail(MTG_ERR_INVALID, "generate_device: bad arguments");
+  for (int i = 0; i < n_prior; ++i)
+    if (prior_ids[i] < 0 || prior_ids[i] >= c.hp.vocab) return c.fail(MTG_ERR_INVALID, "prior id %d", prior_ids[i]);
+  c.error.clear();
+  try {
+    mtg::GenState g{};
+    g.first_new = n_prior;
+    g.max_new = max_new;
+    g.max_steps = max_steps;
+    g.eos = eos;
+    g.max_draft = std::max(0, std::min(max_draft, MTG_MAX_BATCH - 1));  // :85-86
+    g.max_seq = c.max_seq;
+    g.penalty = std::max(1.0f, std::min(1.5f, penalty));
+    g.n_ids = n_prior;
+    g.past = c.past;
+    g.raw_choice = first_seed;
+    const int cap = n_prior + max_new + 1;
+    std::vector<int32_t> ids((size_t)cap);
+    std::copy(prior_ids, prior_ids + n_prior, ids.begin());
+    const auto t0 = std::chrono::steady_clock::now();
+    int rc = c.generate_device(g, ids.data(), cap);
+    if (rc) return rc;
+    mtg_gen_stats st{};
+    st.target_calls = g.target_calls;
+    st.drafted_calls = g.drafted_calls;
+    st.proposed = g.proposed;
+    st.accepted = g.accepted;
+    st.target_input_tokens = g.target_input_tokens;
+    st.rewinds = g.rewinds;
+    st.stop_reason = g.stop;
+    st.next_seed = g.raw_choice;
+    int n_new = g.n_ids - n_prior;
+    if (g.err) {
+      // a step of the device loop was abandoned (a bounded wait ran out): the host
+      // controller finishes from the same state, its steps with the per-op fallback
+      int32_t more = 0;
+      mtg_gen_stats rest{};
+      const int left_steps = max_steps > 0 ? max_steps - g.steps : 0;  // >= 1: the abandoned step did not count
+      rc = mtg_generate_from(ctx, g.raw_choice, ids.data(), g.n_ids, max_new - n_new, left_steps, eos, penalty,
+                             max_draft, nullptr, nullptr, nullptr, ids.data() + g.n_ids, &more, &rest);
+      if (rc) return rc;
+      n_new += more;
+      st.target_calls += rest.target_calls;
+      st.drafted_calls += rest.drafted_calls;
+      st.proposed += rest.proposed;
+      st.accepted += rest.accepted;
+      st.target_input_tokens += rest.target_input_tokens;
+      st.rewinds += rest.rewinds;
+      st.stop_reason = rest.stop_reason;
+      st.next_seed = rest.next_seed;
+    }
+    st.verify_seconds = seconds_since(t0);
+    std::copy(ids.begin() + n_prior, ids.begin() + n_prior + n_new, ids_out);
+    *n_ids_out = n_new;
+    if (stats) *stats = st;
+    return MTG_OK;
+  } catch (...) {
+    return c.fail(MTG_ERR_NOMEM, "generate_device: out of host memory");
+  }
+}
+
 int mtg_generate(mtg_ctx* ctx, const float* fused, int32_t seq, int32_t max_new, int32_t eos,
                  float penalty, int32_t max_draft, mtg_draft_fn draft, mtg_commit_fn commit,
                  void* user, int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats) {

@@ -123,4 +123,11 @@ void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uin
 void launch_embed_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int hidden,
                      const float* host_rows, float* x);
 
+// ---- the speculative controller on the device (generate.hip) ----
+// One controller pass: commit the previous step's result from res_map (the
+// mapped result buffer the step kernel writes; step_err: its error word), apply
+// the stop rules, draft and write the next descriptor (T = 0 once stopped).
+void launch_gen_ctrl(hipStream_t s, GenState* g, int32_t* ids, StepDesc* desc, StepResult* res_map,
+                     const int32_t* step_err);
+
 }  // namespace mtg

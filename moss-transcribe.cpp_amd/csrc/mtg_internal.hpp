@@ -57,4 +57,25 @@ struct StepResult {
   int32_t err;  // nonzero: a grid-barrier wait of the step kernel ran out
 };
 
+// The device-side speculative controller's state (generate.hip): set up by
+// the host, advanced by k_gen_ctrl between verify steps.
+struct GenState {
+  // set by the host
+  int32_t first_new;  // committed ids before the run (prior ids)
+  int32_t max_new, max_steps, eos, max_draft, max_seq;
+  float penalty;
+  // the controller's state
+  int32_t n_ids;       // committed ids
+  int32_t past;        // KV position
+  int32_t raw_choice;  // seed of the next step
+  int32_t steps;
+  int32_t done;        // the loop ended: stop gives the reason (0: the step limit)
+  int32_t stop;        // 1 eos, 2 token limit, 3 KV cache full
+  int32_t err;         // a step left before its acceptance (its seed is undone)
+  int32_t pending;     // a step was issued and its result is not yet taken
+  int32_t before, np;  // position and draft count of that step
+  int32_t proposal[kMaxRows];
+  int64_t target_calls, drafted_calls, proposed, accepted, target_input_tokens, rewinds;
+};
+
 }  // namespace mtg

@@ -30,6 +30,9 @@ Ctx::~Ctx() {
   for (auto& g : graphs)
     if (g.exec) hipGraphExecDestroy(g.exec);
   for (void* p : allocations) hipFree(p);
+  if (gen_ids_dev) hipFree(gen_ids_dev);
+  if (gen_state_dev) hipFree(gen_state_dev);
+  if (gen_state_host) hipHostFree(gen_state_host);
   if (ev_start) hipEventDestroy(ev_start);
   if (ev_stop) hipEventDestroy(ev_stop);
   if (desc_host) hipHostFree(desc_host);
@@ -679,6 +682,75 @@ int Ctx::kv_io(void* k, void* v, int n_pos, bool write) {
       }
     }
   if (write) past = n_pos;
+  return MTG_OK;
+}
+
+}  // namespace mtg
+
+namespace mtg {
+
+// The controller on the device: [k_gen_ctrl, step kernel] pairs enqueued in
+// chunks of kChunkSteps, the state looked at once per chunk. A step that leaves
+// before its acceptance ends the run with g.err set and that step undone.
+int Ctx::generate_device(GenState& g, int32_t* ids, int cap) {
+  constexpr int kChunkSteps = 8;
+  int rc = MTG_OK;
+  if (!step_ok || exec != kExecStep || g.max_draft + 1 > 8)
+    return fail(MTG_ERR_UNSUPPORTED, "device generation needs the step kernel and max_draft <= 7");
+  if (cap > gen_cap) {
+    if (gen_ids_dev) (void)hipFree(gen_ids_dev);
+    gen_ids_dev = nullptr;
+    gen_cap = 0;
+    if ((rc = check(hipMalloc((void**)&gen_ids_dev, (size_t)cap * 4), "generation ids"))) return rc;
+    gen_cap = cap;
+  }
+  if (!gen_state_dev && (rc = check(hipMalloc((void**)&gen_state_dev, sizeof(GenState)), "generation state")))
+    return rc;
+  if (!gen_state_host &&
+      (rc = check(hipHostMalloc((void**)&gen_state_host, sizeof(GenState), hipHostMallocDefault), "generation state")))
+    return rc;
+  *gen_state_host = g;
+  if ((rc = check(hipMemcpyAsync(gen_state_dev, gen_state_host, sizeof(GenState), hipMemcpyHostToDevice, stream),
+                  "generation state")))
+    return rc;
+  if (g.n_ids > 0 && (rc = check(hipMemcpyAsync(gen_ids_dev, ids, (size_t)g.n_ids * 4, hipMemcpyHostToDevice, stream),
+                                 "generation ids")))
+    return rc;
+  const uint32_t pps = step_progress_per_step(hp.n_layers);
+  const int kv_f16 = kv_type == MTG_TYPE_F16;
+  StepDesc unused{};
+  result_host->err = 0;
+  for (;;) {
+    if (epoch > 0xF0000000u - (uint32_t)kChunkSteps * pps) {  // progress words restart before they could wrap
+      if ((rc = check(hipMemsetAsync(params_host.flags, 0, (size_t)nwg * kFlagStride * 4, stream), "flags"))) return rc;
+      if ((rc = check(hipMemsetAsync(params_host.qkvt, 0, qkvt_bytes(), stream), "tags"))) return rc;
+      epoch = 0;
+    }
+    for (int i = 0; i < kChunkSteps; ++i) {
+      launch_gen_ctrl(stream, gen_state_dev, gen_ids_dev, desc_dev, result_map, &result_dev->err);
+      if ((rc = check(hipGetLastError(), "controller launch"))) return rc;
+      if ((rc = check(launch_step(stream, 1, kv_f16, params_dev, &unused, epoch, kStepVerify, false, desc_dev),
+                      "step kernel launch")))
+        return rc;
+      epoch += pps;
+    }
+    // the last step of the chunk is taken by the next chunk's first controller
+    // pass, or by the closing pass below
+    if ((rc = check(hipMemcpyAsync(gen_state_host, gen_state_dev, sizeof(GenState), hipMemcpyDeviceToHost, stream),
+                    "generation state")))
+      return rc;
+    if ((rc = check(hipStreamSynchronize(stream), "generation"))) return rc;
+    if (gen_state_host->done) break;
+  }
+  g = *gen_state_host;
+  if ((rc = check(hipMemcpy(ids, gen_ids_dev, (size_t)g.n_ids * 4, hipMemcpyDeviceToHost), "generation ids")))
+    return rc;
+  if (g.err) {
+    // the abandoned step wrote only positions from its `before` on
+    (void)hipMemset(&result_dev->err, 0, sizeof(int32_t));
+    ++step_fallbacks;
+  }
+  past = g.past;
   return MTG_OK;
 }
 

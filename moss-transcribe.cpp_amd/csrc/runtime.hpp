@@ -111,6 +111,14 @@ struct Ctx {
   int embed(const int32_t* ids, int n, float* out);
   int kv_io(void* k, void* v, int n_pos, bool write);
   int init_step_kernel();
+  // the speculative controller on the device (generate.hip): runs from state g
+  // (first_new / limits / n_ids / past / raw_choice set) over ids[0, n_ids), with
+  // room for cap ids; returns with g and ids as the device left them
+  GenState* gen_state_dev = nullptr;  // device copies, grown on demand
+  int32_t* gen_ids_dev = nullptr;
+  int gen_cap = 0;
+  GenState* gen_state_host = nullptr;  // pinned
+  int generate_device(GenState& g, int32_t* ids, int cap);
 };
 
 }  // namespace mtg

@@ -1277,12 +1277,22 @@ __host__ __device__ constexpr size_t step_lds_stage_offset(int G) {
 }
 __device__ __forceinline__ uint32_t ph(int l, int p) { return 2u + (uint32_t)(l * kPhases + p); }
 
+// The step descriptor: the kernel argument, or (DEV) the one in device memory
+// that the device-side controller wrote.
+template <bool DEV>
+__device__ __forceinline__ const StepDesc& step_desc(const StepDesc& arg, const StepDesc* dev);
+template <>
+__device__ __forceinline__ const StepDesc& step_desc<false>(const StepDesc& arg, const StepDesc*) { return arg; }
+template <>
+__device__ __forceinline__ const StepDesc& step_desc<true>(const StepDesc&, const StepDesc* dev) { return *dev; }
+
 // PROF: the profiled variant (clock marks into P.timing); the production
-// variant carries no marks at all (they would cost code size and registers)
-template <int G, int KVH, bool PROF>
+// variant carries no marks at all (they would cost code size and registers).
+// DEV: the descriptor comes from desc_dev (T == 0 there: nothing to do).
+template <int G, int KVH, bool PROF, bool DEV = false>
 __global__ void __launch_bounds__(kT, 1)
 k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoch,
-        int mode) {
+        int mode, const StepDesc* __restrict__ desc_dev) {
 #define MARK(...) do { if constexpr (PROF) mark(__VA_ARGS__); } while (0)
 #define WMARK(...) do { if constexpr (PROF) wmark(__VA_ARGS__); } while (0)
   const StepParams& P = *Pp;
@@ -1297,8 +1307,9 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   // The step descriptor arrives by value in the kernel arguments (no copy to
   // device memory before the launch). Its fields are read in place; its address
   // is never taken (that would give every thread a private copy).
-  const StepDesc& desc = desc_arg;
+  const StepDesc& desc = step_desc<DEV>(desc_arg, desc_dev);
   const int T = desc.T, past = desc.past, L = P.L;
+  if (DEV && T == 0) return;  // the controller has stopped
   const int nch = (past + T + kChunk - 1) / kChunk, n_items = cNKV * nch;
   uint8_t* pcodes = lds;
   float* pscales = (float*)(lds + (size_t)G * cBF * 1024);
@@ -1534,13 +1545,13 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   MARK(P, 3 + 12 * L);
   if constexpr (G == 1) gain16_load(P.out_norm, gq);
   panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr, stg, G == 1 ? nullptr : P.out_norm);
-  lm_head<G>(P, desc_arg.penalty, desc_arg.write_logits != 0, T, pcodes, pscales, s_best);
+  lm_head<G>(P, desc.penalty, desc.write_logits != 0, T, pcodes, pscales, s_best);
   publish(c, lm);
   MARK(P, 4 + 12 * L);
   if (w == 0) {
     if (!wait_all(c, lm)) return;
     MARK(P, 5 + 12 * L);
-    accept<G>(P.part_keys, (int)threadIdx.x < T ? desc_arg.tokens[threadIdx.x] : 0, P.result, T, kNwg, s_red,
+    accept<G>(P.part_keys, (int)threadIdx.x < T ? desc.tokens[threadIdx.x] : 0, P.result, T, kNwg, s_red,
               s_choice, s_tok, PROF ? P.timing : nullptr, 7 + 12 * L);
     MARK(P, 6 + 12 * L);
   }
@@ -1574,6 +1585,10 @@ const void* step_fn(int G, int kv_f16, bool prof) {
        {(const void*)k_step<2, 1, false>, (const void*)k_step<2, 1, true>}}};
   return fns[G - 1][kv_f16 ? 1 : 0][prof ? 1 : 0];
 }
+// the 8-row variants that read the descriptor from device memory
+const void* step_fn_dev(int kv_f16) {
+  return kv_f16 ? (const void*)k_step<1, 1, false, true> : (const void*)k_step<1, 0, false, true>;
+}
 }  // namespace
 
 hipError_t prepare_step_kernels() {
@@ -1584,13 +1599,23 @@ hipError_t prepare_step_kernels() {
                                                  (int)step_lds_bytes(G));
         if (e != hipSuccess) return e;
       }
+  for (int kv = 0; kv < 2; ++kv) {
+    const hipError_t e = hipFuncSetAttribute(step_fn_dev(kv), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)step_lds_bytes(1));
+    if (e != hipSuccess) return e;
+  }
   return hipSuccess;
 }
 
 hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
-                        uint32_t epoch, int mode, bool profiled) {
-  // desc: host memory; the launch copies it into the kernel arguments
-  void* args[] = {(void*)&P, (void*)desc, (void*)&epoch, (void*)&mode};
+                        uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev) {
+  // desc: host memory; the launch copies it into the kernel arguments. desc_dev
+  // (8-row verify only): the kernel reads the descriptor there instead.
+  void* args[] = {(void*)&P, (void*)desc, (void*)&epoch, (void*)&mode, (void*)&desc_dev};
+  if (desc_dev) {
+    if (G != 1 || profiled) return hipErrorInvalidValue;
+    return hipLaunchKernel(step_fn_dev(kv_f16), dim3(kNwg), dim3(kT), args, step_lds_bytes(1), s);
+  }
   const size_t lds = step_lds_bytes(G);
   // A plain launch: one workgroup per CU (the kernel's registers and LDS allow
   // no second), so on an idle device the whole grid is resident at once. The

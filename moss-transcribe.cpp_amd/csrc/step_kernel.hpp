@@ -70,6 +70,6 @@ hipError_t prepare_step_kernels();
 // desc: the host copy of the step descriptor (passed by value as a kernel
 // argument). profiled: the variant that writes clock marks into StepParams::timing
 hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
-                        uint32_t epoch, int mode, bool profiled);
+                        uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev = nullptr);
 
 }  // namespace mtg
