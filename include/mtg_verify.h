@@ -373,6 +373,68 @@ const mtg_model_desc* mtg_gguf_model(mtg_gguf* g);
  * returning. */
 int mtg_create_from_gguf(const char* path, int32_t max_seq, int32_t kv_type, mtg_ctx** out);
 
+/* ---- Whisper encoder + audio adaptor (reference: WhisperEncoder,
+ * src/whisper_encoder.cpp:64-209, and AudioAdaptor, src/audio_adaptor.cpp:22-97)
+ * ---- */
+
+typedef struct mtg_encoder_hparams {
+  int32_t n_mels;    /* mtd.audio.mel_bins (80) */
+  int32_t n_frames;  /* mel frames of one chunk (3000); the encoder emits (n_frames - 1) / 2 + 1 rows */
+  int32_t d_model;   /* mtd.audio.d_model (1024) */
+  int32_t n_layers;  /* mtd.audio.n_layers (24) */
+  int32_t n_heads;   /* mtd.audio.n_heads (16, head_dim 64) */
+  int32_t ffn;       /* mtd.audio.ffn (4096) */
+  int32_t merge;     /* mtd.audio_merge_size (4): frames per adaptor row */
+  int32_t hidden;    /* the adaptor's output width, text hidden (1024) */
+  float adaptor_eps; /* mtd.adaptor_norm_eps (1e-6); the encoder's LayerNorms use 1e-5 */
+} mtg_encoder_hparams;
+
+/* One encoder layer, names of the reference GGUF (src/whisper_encoder.cpp:76-94):
+ * the projection and FFN matrices in the weight type, [out][in] rows of GGUF
+ * blocks; norms and biases f32. */
+typedef struct mtg_encoder_layer {
+  const float *attn_ln_w, *attn_ln_b;   /* enc.blk.N.attn_ln.{w,b} [d] */
+  const void *q_w, *k_w, *v_w, *o_w;    /* enc.blk.N.attn_{q,k,v,out}.w [d][d] */
+  const float *q_b, *v_b, *o_b;         /* their biases [d] (attn_k has none) */
+  const float *ffn_ln_w, *ffn_ln_b;     /* enc.blk.N.ffn_ln.{w,b} */
+  const void* fc1_w;                    /* enc.blk.N.ffn_1.w [ffn][d] */
+  const float* fc1_b;
+  const void* fc2_w;                    /* enc.blk.N.ffn_2.w [d][ffn] */
+  const float* fc2_b;
+} mtg_encoder_layer;
+
+typedef struct mtg_encoder_desc {
+  mtg_encoder_hparams hp;
+  int32_t weight_type;                  /* MTG_TYPE_Q8_0 */
+  const float *conv1_w, *conv1_b;       /* enc.conv1.{w,b}: [d][n_mels][3], [d] */
+  const float *conv2_w, *conv2_b;       /* enc.conv2.{w,b}: [d][d][3], [d] (stride 2) */
+  const float* pos_embd;                /* enc.pos_embd [rows][d] */
+  const float *ln_post_w, *ln_post_b;   /* enc.ln_post.{w,b} */
+  const mtg_encoder_layer* layers;
+  const void* ad_fc1_w;                 /* adaptor.fc1.w [hidden][d * merge] */
+  const float* ad_fc1_b;
+  const void* ad_fc2_w;                 /* adaptor.fc2.w [hidden][hidden] */
+  const float* ad_fc2_b;
+  const float *ad_ln_w, *ad_ln_b;       /* adaptor.ln.{w,b} */
+} mtg_encoder_desc;
+
+typedef struct mtg_encoder mtg_encoder;
+/* Upload an encoder + adaptor. q8_0 weights, head_dim 64, d_model and ffn
+ * multiples of 64, hidden a multiple of 64 (else MTG_ERR_UNSUPPORTED). */
+int mtg_encoder_create(const mtg_encoder_desc* desc, mtg_encoder** out);
+void mtg_encoder_destroy(mtg_encoder* e);
+const char* mtg_encoder_error(const mtg_encoder* e);
+/* WhisperEncoder::encode: mel [n_mels][n_frames] (frames fastest) through the
+ * conv stem, the layers and ln_post. The rows stay on the device for
+ * mtg_encoder_adapt; out (nullable) receives them, [rows][d]. */
+int mtg_encoder_encode(mtg_encoder* e, const float* mel, float* out, int32_t* rows_out);
+/* AudioAdaptor::apply on T encoder rows: rows (nullable: the last encode's rows
+ * on the device), trimmed to a multiple of merge, merge consecutive rows per
+ * adaptor row, fc1 + SiLU, fc2, LayerNorm -> out [N][hidden], N = T / merge. */
+int mtg_encoder_adapt(mtg_encoder* e, const float* rows, int32_t T, float* out, int32_t* n_out);
+/* device time of the last encode / adapt call, ms (HIP events) */
+double mtg_encoder_last_ms(const mtg_encoder* e);
+
 /* ---- synthetic model (workload generator for the benchmark and tests) ---- */
 
 typedef struct mtg_synth_model mtg_synth_model;

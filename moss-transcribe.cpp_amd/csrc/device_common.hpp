@@ -69,6 +69,30 @@ __device__ __forceinline__ float dev_rms_scale(float mean, float eps) {
 }
 
 // silu(g) * u with the canonical exp and a correctly rounded division.
+// erf by its Maclaurin series in double, a fixed number of terms per range of
+// |z| (the oracle evaluates the same operations); +-1 from |z| >= 4.
+__device__ __forceinline__ double dev_erf_series(double z) {
+  const double a = fabs(z);
+  if (a >= 4.0) return z < 0.0 ? -1.0 : 1.0;
+  const int terms = a < 1.0 ? 28 : (a < 2.0 ? 44 : (a < 3.0 ? 60 : 76));
+  const double a2 = __dmul_rn(a, a);
+  double term = a, sum = 0.0;
+  for (int n = 0; n < terms; ++n) {
+    sum = __dadd_rn(sum, __ddiv_rn(term, (double)(2 * n + 1)));
+    term = -__ddiv_rn(__dmul_rn(term, a2), (double)(n + 1));
+  }
+  const double r = __dmul_rn(sum, 1.1283791670955126);  // 2 / sqrt(pi)
+  return z < 0.0 ? -r : r;
+}
+// ggml_gelu_erf: 0.5 x (1 + erf(x / sqrt 2)), evaluated left to right
+__device__ __forceinline__ float dev_gelu_erf(float x) {
+  const float z = __fmul_rn(x, 0.70710678118654752440f);
+  const float e = (float)dev_erf_series((double)z);
+  return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, e));
+}
+// ggml_silu: x / (1 + exp(-x))
+__device__ __forceinline__ float dev_silu(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, dev_expf(-x))); }
+
 __device__ __forceinline__ float dev_swiglu(float g, float u) {
   return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, dev_expf(-g))), u);
 }

@@ -89,7 +89,8 @@ void launch_q8_retile(hipStream_t s, const uint8_t* blocks, int n, int k, uint8_
 
 // ---- prompt prefill over S rows (prefill.hip); activations in the compact
 // q8_0 layout codes [S][K] int8 + scales [S][K/32] ----
-enum { PF_EPI_STORE = 0, PF_EPI_RESID = 1, PF_EPI_SWIGLU = 2 };
+enum { PF_EPI_STORE = 0, PF_EPI_RESID = 1, PF_EPI_SWIGLU = 2, PF_EPI_BIAS = 3, PF_EPI_BIAS_GELU = 4,
+       PF_EPI_BIAS_SILU = 5, PF_EPI_BIAS_RESID = 6 };
 int pf_max_context();  // positions the prefill attention supports
 hipError_t prepare_kernels_pf();
 // RMSNorm(src) * gain (hidden 1024) -> q8_0 codes / scales; normed_out (nullable)
@@ -97,8 +98,10 @@ void launch_pf_norm_quant(hipStream_t s, const float* src, int S, const float* g
                           float* scales, float* normed_out);
 void launch_pf_quant(hipStream_t s, const float* src, int S, int K, int8_t* codes, float* scales);
 // out[s][n] (= / += / swiglu with w2) q8_0 GEMM of packed tiles (N % 64 == 0)
+// epi: PF_EPI_*; bias [N] for the PF_EPI_BIAS* epilogues (out = act(W x + b),
+// or out += W x + b)
 void launch_pf_gemm(hipStream_t s, int epi, const uint8_t* w, const uint8_t* w2, int N, int K, const int8_t* codes,
-                    const float* scales, int S, float* out);
+                    const float* scales, int S, float* out, const float* bias = nullptr);
 void launch_pf_qk_rope(hipStream_t s, const float* qkv, int S, int past0, int n_heads, int n_kv_heads,
                        const float* q_norm, const float* k_norm, float eps, const float* rope, float* q_out,
                        KvLayer kv);

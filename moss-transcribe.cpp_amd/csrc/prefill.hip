@@ -139,13 +139,14 @@ k_pf_quant(const float* __restrict__ src, int S, int K, int8_t* __restrict__ cod
 // the exact int32 dot of every (weight row, activation row, block). The K-slices
 // run one after the other, so one accumulator per slice and a running total
 // give ((s0 + s1) + s2) + s3 per parity, then even + odd.
-enum { PF_STORE = 0, PF_RESID = 1, PF_SWIGLU = 2 };
+enum { PF_STORE = 0, PF_RESID = 1, PF_SWIGLU = 2, PF_BIAS = 3, PF_BIAS_GELU = 4, PF_BIAS_SILU = 5, PF_BIAS_RESID = 6 };
 constexpr int kPfRowBytes = 80;  // LDS stride of a staged 64-byte code row (bank spread)
 
 template <int EPI>
 __global__ void __launch_bounds__(256)
 k_pf_gemm(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int N, int K,
-          const int8_t* __restrict__ codes, const float* __restrict__ scales, int S, float* __restrict__ out) {
+          const int8_t* __restrict__ codes, const float* __restrict__ scales, int S, float* __restrict__ out,
+          const float* __restrict__ bias) {
   constexpr bool GLU = EPI == PF_SWIGLU;
   __shared__ __align__(16) uint8_t s_codes[2][64 * kPfRowBytes];
   __shared__ float s_dx[2][64 * 2];
@@ -256,6 +257,18 @@ k_pf_gemm(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int N, 
         const v4f x = *(const v4f*)dst;
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = __fadd_rn(x[q], tot[cg][q]);
+      } else if (EPI >= PF_BIAS) {
+        // linear = mul_mat + bias, then the activation or the residual add
+        const v4f b = *(const v4f*)(bias + n);
+        v4f x{};
+        if (EPI == PF_BIAS_RESID) x = *(const v4f*)dst;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float y = __fadd_rn(tot[cg][q], b[q]);
+          v[q] = EPI == PF_BIAS_GELU ? dev_gelu_erf(y)
+                 : EPI == PF_BIAS_SILU ? dev_silu(y)
+                 : EPI == PF_BIAS_RESID ? __fadd_rn(x[q], y) : y;
+        }
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = tot[cg][q];
@@ -566,14 +579,20 @@ void launch_pf_quant(hipStream_t s, const float* src, int S, int K, int8_t* code
 }
 
 void launch_pf_gemm(hipStream_t s, int epi, const uint8_t* w, const uint8_t* w2, int N, int K, const int8_t* codes,
-                    const float* scales, int S, float* out) {
+                    const float* scales, int S, float* out, const float* bias) {
   const dim3 blocks((unsigned)(epi == PF_SWIGLU ? N / 32 : N / 64), (unsigned)((S + 63) / 64));
-  if (epi == PF_STORE)
-    hipLaunchKernelGGL(k_pf_gemm<PF_STORE>, blocks, dim3(256), 0, s, w, w2, N, K, codes, scales, S, out);
-  else if (epi == PF_RESID)
-    hipLaunchKernelGGL(k_pf_gemm<PF_RESID>, blocks, dim3(256), 0, s, w, w2, N, K, codes, scales, S, out);
-  else
-    hipLaunchKernelGGL(k_pf_gemm<PF_SWIGLU>, blocks, dim3(256), 0, s, w, w2, N, K, codes, scales, S, out);
+#define MTG_PF_GEMM(E) \
+  hipLaunchKernelGGL(k_pf_gemm<E>, blocks, dim3(256), 0, s, w, w2, N, K, codes, scales, S, out, bias)
+  switch (epi) {
+    case PF_STORE: MTG_PF_GEMM(PF_STORE); break;
+    case PF_RESID: MTG_PF_GEMM(PF_RESID); break;
+    case PF_SWIGLU: MTG_PF_GEMM(PF_SWIGLU); break;
+    case PF_BIAS: MTG_PF_GEMM(PF_BIAS); break;
+    case PF_BIAS_GELU: MTG_PF_GEMM(PF_BIAS_GELU); break;
+    case PF_BIAS_SILU: MTG_PF_GEMM(PF_BIAS_SILU); break;
+    default: MTG_PF_GEMM(PF_BIAS_RESID); break;
+  }
+#undef MTG_PF_GEMM
 }
 
 void launch_pf_qk_rope(hipStream_t s, const float* qkv, int S, int past0, int n_heads, int n_kv_heads,

@@ -140,6 +140,40 @@ SIGNATURES = {
     "mtg_f16_to_f32": (c_float, [c_uint16]),
 }
 
+# ---- Whisper encoder + audio adaptor (mtg_encoder_*) ----
+class EncoderHparams(ctypes.Structure):
+    _fields_ = [("n_mels", c_int32), ("n_frames", c_int32), ("d_model", c_int32), ("n_layers", c_int32),
+                ("n_heads", c_int32), ("ffn", c_int32), ("merge", c_int32), ("hidden", c_int32),
+                ("adaptor_eps", c_float)]
+
+
+class EncoderLayer(ctypes.Structure):
+    _fields_ = [("attn_ln_w", c_void_p), ("attn_ln_b", c_void_p), ("q_w", c_void_p), ("k_w", c_void_p),
+                ("v_w", c_void_p), ("o_w", c_void_p), ("q_b", c_void_p), ("v_b", c_void_p), ("o_b", c_void_p),
+                ("ffn_ln_w", c_void_p), ("ffn_ln_b", c_void_p), ("fc1_w", c_void_p), ("fc1_b", c_void_p),
+                ("fc2_w", c_void_p), ("fc2_b", c_void_p)]
+
+
+class EncoderDesc(ctypes.Structure):
+    _fields_ = [("hp", EncoderHparams), ("weight_type", c_int32), ("conv1_w", c_void_p), ("conv1_b", c_void_p),
+                ("conv2_w", c_void_p), ("conv2_b", c_void_p), ("pos_embd", c_void_p), ("ln_post_w", c_void_p),
+                ("ln_post_b", c_void_p), ("layers", POINTER(EncoderLayer)), ("ad_fc1_w", c_void_p),
+                ("ad_fc1_b", c_void_p), ("ad_fc2_w", c_void_p), ("ad_fc2_b", c_void_p), ("ad_ln_w", c_void_p),
+                ("ad_ln_b", c_void_p)]
+
+
+ENCODER_DEFAULTS = dict(n_mels=80, n_frames=3000, d_model=1024, n_layers=24, n_heads=16, ffn=4096, merge=4,
+                        hidden=1024, adaptor_eps=1e-6)
+
+SIGNATURES.update({
+    "mtg_encoder_create": (c_int32, [POINTER(EncoderDesc), POINTER(c_void_p)]),
+    "mtg_encoder_destroy": (None, [c_void_p]),
+    "mtg_encoder_error": (ctypes.c_char_p, [c_void_p]),
+    "mtg_encoder_encode": (c_int32, [c_void_p, c_void_p, c_void_p, POINTER(c_int32)]),
+    "mtg_encoder_adapt": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, POINTER(c_int32)]),
+    "mtg_encoder_last_ms": (c_double, [c_void_p]),
+})
+
 _lib = None
 
 
@@ -538,3 +572,115 @@ def normal(seed, first, n):
     out = np.empty(n, np.float32)
     lib().mtg_normal_fill(seed, first, ptr(out), n)
     return out
+
+
+class SynthEncoder:
+    """Seeded synthetic Whisper encoder + adaptor in host memory: f32 conv stem,
+    positional embedding, norms and biases; q8_0 projection / FFN / adaptor
+    matrices (the reference converter's types), from the shared normal stream."""
+
+    def __init__(self, seed=0, std=0.02, **hp):
+        d = dict(ENCODER_DEFAULTS)
+        d.update(hp)
+        self.hp = EncoderHparams(**d)
+        self._keep = []
+        self._next = 0
+        self.seed = seed
+        h = self.hp
+        D, F, M, H, IN = h.d_model, h.ffn, h.n_mels, h.hidden, h.d_model * h.merge
+        R = (h.n_frames - 1) // 2 + 1
+        self.rows = R
+        desc = EncoderDesc()
+        desc.hp = self.hp
+        desc.weight_type = TYPE_Q8_0
+        desc.conv1_w = self._f(D * M * 3, std)
+        desc.conv1_b = self._f(D, std)
+        desc.conv2_w = self._f(D * D * 3, std)
+        desc.conv2_b = self._f(D, std)
+        desc.pos_embd = self._f(R * D, 0.2)
+        desc.ln_post_w = self._f(D, 0.05, 1.0)
+        desc.ln_post_b = self._f(D, 0.05)
+        layers = (EncoderLayer * max(1, h.n_layers))()
+        for i in range(h.n_layers):
+            L = layers[i]
+            L.attn_ln_w, L.attn_ln_b = self._f(D, 0.05, 1.0), self._f(D, 0.05)
+            L.q_w, L.k_w, L.v_w, L.o_w = (self._q(D, D, std) for _ in range(4))
+            L.q_b, L.v_b, L.o_b = (self._f(D, std) for _ in range(3))
+            L.ffn_ln_w, L.ffn_ln_b = self._f(D, 0.05, 1.0), self._f(D, 0.05)
+            L.fc1_w, L.fc1_b = self._q(F, D, std), self._f(F, std)
+            L.fc2_w, L.fc2_b = self._q(D, F, std), self._f(D, std)
+        self._keep.append(layers)
+        desc.layers = layers
+        desc.ad_fc1_w, desc.ad_fc1_b = self._q(H, IN, std), self._f(H, std)
+        desc.ad_fc2_w, desc.ad_fc2_b = self._q(H, H, std), self._f(H, std)
+        desc.ad_ln_w, desc.ad_ln_b = self._f(H, 0.05, 1.0), self._f(H, 0.05)
+        self.desc = desc
+
+    def _normal(self, n):
+        out = normal(self.seed, self._next, n)
+        self._next += n
+        return out
+
+    def _f(self, n, std, mean=0.0):
+        a = (self._normal(n) * np.float32(std) + np.float32(mean)).astype(np.float32)
+        self._keep.append(a)
+        return a.ctypes.data
+
+    def _q(self, n, k, std):
+        x = self._normal(n * k) * np.float32(std)
+        blocks = np.empty(n * (k // 32) * 34, np.uint8)
+        lib().mtg_quantize_q8_0_weight(ptr(x), n * k, ptr(blocks))
+        self._keep.append(blocks)
+        return blocks.ctypes.data
+
+    def mel(self, seed=1):
+        """A mel chunk [n_mels][n_frames] shaped like log-mel features."""
+        h = self.hp
+        return (normal(seed, 0, h.n_mels * h.n_frames) * np.float32(0.5)).reshape(h.n_mels, h.n_frames)
+
+
+class Encoder:
+    """Device encoder + adaptor (mtg_encoder)."""
+
+    def __init__(self, synth):
+        self.hp = synth.hp
+        self.rows = synth.rows
+        out = c_void_p()
+        rc = lib().mtg_encoder_create(ctypes.byref(synth.desc), ctypes.byref(out))
+        if rc:
+            raise MtgError(rc, "encoder create")
+        self.h = out
+
+    def _chk(self, rc):
+        if rc:
+            raise MtgError(rc, lib().mtg_encoder_error(self.h).decode())
+
+    def encode(self, mel, want_rows=True):
+        mel = f32(mel)
+        out = np.empty((self.rows, self.hp.d_model), np.float32) if want_rows else None
+        n = c_int32(0)
+        self._chk(lib().mtg_encoder_encode(self.h, ptr(mel), ptr(out), ctypes.byref(n)))
+        return out
+
+    def adapt(self, T, rows=None):
+        n_out = T // self.hp.merge
+        out = np.empty((max(1, n_out), self.hp.hidden), np.float32)
+        n = c_int32(0)
+        r = None if rows is None else f32(rows)
+        self._chk(lib().mtg_encoder_adapt(self.h, ptr(r), T, ptr(out), ctypes.byref(n)))
+        return out[: n.value]
+
+    @property
+    def last_ms(self):
+        return lib().mtg_encoder_last_ms(self.h)
+
+    def close(self):
+        if self.h:
+            lib().mtg_encoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

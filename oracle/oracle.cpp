@@ -1090,3 +1090,297 @@ int orc_generate_from(orc_model* m, int32_t first_seed, const int32_t* prior_ids
 }
 
 }  // extern "C"
+
+// ===================================================== Whisper encoder ======
+// WhisperEncoder::encode (src/whisper_encoder.cpp:103-209) and
+// AudioAdaptor::apply (src/audio_adaptor.cpp:38-97) with the same canonical
+// orders as the decoder step: q8_0 linears as mul_mat_q8, the attention's
+// 64-key chunks merged in order, double sums over 64 partials + butterfly.
+namespace {
+
+// erf by its Maclaurin series in double, a fixed number of terms per range of
+// |z| (the device evaluates the same operations); erf(z) = +-1 from |z| >= 4,
+// where 1 - erf(4) = 1.5e-8 no longer moves a float.
+double erf_series(double z) {
+  const double a = std::fabs(z);
+  if (a >= 4.0) return z < 0.0 ? -1.0 : 1.0;
+  const int terms = a < 1.0 ? 28 : (a < 2.0 ? 44 : (a < 3.0 ? 60 : 76));
+  const double a2 = a * a;
+  double term = a, sum = 0.0;
+  for (int n = 0; n < terms; ++n) {
+    sum = sum + term / (double)(2 * n + 1);
+    term = -(term * a2) / (double)(n + 1);
+  }
+  const double r = sum * 1.1283791670955126;  // 2 / sqrt(pi)
+  return z < 0.0 ? -r : r;
+}
+
+// ggml_gelu_erf (0.5 x (1 + erf(x / sqrt 2)), src/whisper_encoder.cpp:119-123)
+float gelu_erf(float x) {
+  const float z = x * 0.70710678118654752440f;
+  const float e = (float)erf_series((double)z);
+  return (0.5f * x) * (1.0f + e);
+}
+
+// 64 partials of n / 64 consecutive elements (sequential double sums), butterfly
+double sum64(const double* v, int n) {
+  double part[64];
+  const int per = n / 64;
+  for (int l = 0; l < 64; ++l) {
+    double s = 0.0;
+    for (int e = 0; e < per; ++e) s += v[l * per + e];
+    part[l] = s;
+  }
+  return butterfly64(part);
+}
+
+// layer_norm (src/ggml_extend.hpp:57-63): ggml_norm (mean and variance summed in
+// double, scale = 1 / sqrtf(variance + eps)), then * w, then + b. n: a multiple of 64.
+void layer_norm(const float* x, const float* w, const float* b, int n, float eps, float* y) {
+  std::vector<double> t((size_t)n);
+  for (int i = 0; i < n; ++i) t[i] = (double)x[i];
+  const float mean = (float)(sum64(t.data(), n) / (double)n);
+  for (int i = 0; i < n; ++i) {
+    const float v = x[i] - mean;
+    y[i] = v;
+    t[i] = (double)(v * v);
+  }
+  const float variance = (float)(sum64(t.data(), n) / (double)n);
+  const float scale = 1.0f / std::sqrt(variance + eps);
+  for (int i = 0; i < n; ++i) y[i] = (y[i] * scale) * w[i] + b[i];
+}
+
+// conv1d_ph_f32 (src/whisper_encoder.cpp:32-44): f32 im2col (pad 1, kernel 3)
+// and mul_mat; canonical order: one fma chain per output over (ic, k), k fastest.
+void conv1d(const float* w, int ic, int oc, const float* x, int L, int stride, float* y) {
+  const int OL = (L - 1) / stride + 1;
+#pragma omp parallel for schedule(static)
+  for (int t = 0; t < OL; ++t)
+    for (int o = 0; o < oc; ++o) {
+      const float* wr = w + (size_t)o * ic * 3;
+      float acc = 0.0f;
+      for (int c = 0; c < ic; ++c)
+        for (int k = 0; k < 3; ++k) {
+          const int xi = t * stride + k - 1;
+          const float xv = (xi >= 0 && xi < L) ? x[(size_t)c * L + xi] : 0.0f;
+          acc = std::fma(wr[c * 3 + k], xv, acc);
+        }
+      y[(size_t)t * oc + o] = acc;
+    }
+}
+
+// the encoder's bidirectional attention (src/whisper_encoder.cpp:164-180):
+// scores K.Q, soft_max_ext with scale 1/sqrt(head_dim) and no mask, context
+// V.P. Canonical order as the decoder step: 64-key chunks, score = fma chain
+// over head_dim, chunk max, p = exp(w - max), l = butterfly, O = fma chain over
+// the chunk's keys, chunks merged in order with f = exp(m_c - M).
+void enc_attention(const float* q, const float* k, const float* v, int T, int NH, int D, float* out) {
+  const int W = NH * D, nch = (T + 63) / 64;
+  const float scale = 1.0f / std::sqrt((float)D);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int h = 0; h < NH; ++h)
+    for (int t = 0; t < T; ++t) {
+      std::vector<float> cm(nch), cl(nch), co((size_t)nch * D);
+      const float* qh = q + (size_t)t * W + (size_t)h * D;
+      for (int c = 0; c < nch; ++c) {
+        float wv[64], p[64];
+        float mx = -INFINITY;
+        for (int j = 0; j < 64; ++j) {
+          const int key = 64 * c + j;
+          if (key < T) {
+            const float* kr = k + (size_t)key * W + (size_t)h * D;
+            float s = 0.0f;
+            for (int d = 0; d < D; ++d) s = std::fma(qh[d], kr[d], s);
+            wv[j] = s * scale;
+          } else {
+            wv[j] = -INFINITY;
+          }
+          mx = std::max(mx, wv[j]);
+        }
+        for (int j = 0; j < 64; ++j) p[j] = wv[j] == -INFINITY ? 0.0f : exp_c(wv[j] - mx);
+        float pl[64];
+        std::memcpy(pl, p, sizeof(pl));
+        cm[c] = mx;
+        cl[c] = butterfly64(pl);
+        for (int d = 0; d < D; ++d) {
+          float acc = 0.0f;
+          for (int j = 0; j < 64; ++j) {
+            const int key = 64 * c + j;
+            const float vv = key < T ? v[(size_t)key * W + (size_t)h * D + d] : 0.0f;
+            acc = std::fma(p[j], vv, acc);
+          }
+          co[(size_t)c * D + d] = acc;
+        }
+      }
+      float M = -INFINITY;
+      for (int c = 0; c < nch; ++c) M = std::max(M, cm[c]);
+      float* oh = out + (size_t)t * W + (size_t)h * D;
+      for (int d = 0; d < D; ++d) {
+        float L = 0.0f, acc = 0.0f;
+        for (int c = 0; c < nch; ++c) {
+          const float f = exp_c(cm[c] - M);
+          L = std::fma(cl[c], f, L);
+          acc = std::fma(co[(size_t)c * D + d], f, acc);
+        }
+        oh[d] = acc / L;
+      }
+    }
+}
+
+// linear (src/ggml_extend.hpp:50-55): mul_mat (q8_0) then + bias
+void linear_q8(const std::vector<BlockQ8>& w, const float* bias, int k, int n, const float* x, int T, float* y) {
+  mul_mat_q8(w.data(), k, n, x, T, y);
+  if (bias)
+    for (int t = 0; t < T; ++t)
+      for (int i = 0; i < n; ++i) y[(size_t)t * n + i] = y[(size_t)t * n + i] + bias[i];
+}
+
+struct EncLayer {
+  std::vector<float> attn_ln_w, attn_ln_b, q_b, v_b, o_b, ffn_ln_w, ffn_ln_b, fc1_b, fc2_b;
+  std::vector<BlockQ8> q_w, k_w, v_w, o_w, fc1_w, fc2_w;
+};
+
+std::vector<float> copy_f(const float* p, size_t n) { return std::vector<float>(p, p + n); }
+std::vector<BlockQ8> copy_q8(const void* p, size_t n, size_t k) {
+  const BlockQ8* b = (const BlockQ8*)p;
+  return std::vector<BlockQ8>(b, b + n * (k / 32));
+}
+
+}  // namespace
+
+struct orc_encoder {
+  mtg_encoder_hparams hp;
+  std::vector<float> conv1_w, conv1_b, conv2_w, conv2_b, pos, ln_post_w, ln_post_b;
+  std::vector<EncLayer> layers;
+  std::vector<BlockQ8> ad_fc1_w, ad_fc2_w;
+  std::vector<float> ad_fc1_b, ad_fc2_b, ad_ln_w, ad_ln_b;
+  std::vector<float> last;  // the last encode's rows
+  int last_rows = 0;
+};
+
+extern "C" {
+
+float orc_gelu_erf(float x) { return gelu_erf(x); }
+void orc_layer_norm(const float* x, const float* w, const float* b, int32_t n, float eps, float* y) {
+  layer_norm(x, w, b, n, eps, y);
+}
+void orc_conv1d(const float* w, int32_t ic, int32_t oc, const float* x, int32_t L, int32_t stride, float* y) {
+  conv1d(w, ic, oc, x, L, stride, y);
+}
+void orc_enc_attention(const float* q, const float* k, const float* v, int32_t T, int32_t n_heads,
+                       int32_t head_dim, float* out) {
+  enc_attention(q, k, v, T, n_heads, head_dim, out);
+}
+
+int orc_encoder_create(const mtg_encoder_desc* d, orc_encoder** out) {
+  if (!d || !out || d->weight_type != MTG_TYPE_Q8_0) return MTG_ERR_INVALID;
+  const mtg_encoder_hparams& hp = d->hp;
+  const size_t D = hp.d_model, F = hp.ffn, M = hp.n_mels, R = (size_t)(hp.n_frames - 1) / 2 + 1;
+  auto e = std::make_unique<orc_encoder>();
+  e->hp = hp;
+  e->conv1_w = copy_f(d->conv1_w, D * M * 3);
+  e->conv1_b = copy_f(d->conv1_b, D);
+  e->conv2_w = copy_f(d->conv2_w, D * D * 3);
+  e->conv2_b = copy_f(d->conv2_b, D);
+  e->pos = copy_f(d->pos_embd, R * D);
+  e->ln_post_w = copy_f(d->ln_post_w, D);
+  e->ln_post_b = copy_f(d->ln_post_b, D);
+  for (int l = 0; l < hp.n_layers; ++l) {
+    const mtg_encoder_layer& s = d->layers[l];
+    EncLayer L;
+    L.attn_ln_w = copy_f(s.attn_ln_w, D);
+    L.attn_ln_b = copy_f(s.attn_ln_b, D);
+    L.q_w = copy_q8(s.q_w, D, D);
+    L.k_w = copy_q8(s.k_w, D, D);
+    L.v_w = copy_q8(s.v_w, D, D);
+    L.o_w = copy_q8(s.o_w, D, D);
+    L.q_b = copy_f(s.q_b, D);
+    L.v_b = copy_f(s.v_b, D);
+    L.o_b = copy_f(s.o_b, D);
+    L.ffn_ln_w = copy_f(s.ffn_ln_w, D);
+    L.ffn_ln_b = copy_f(s.ffn_ln_b, D);
+    L.fc1_w = copy_q8(s.fc1_w, F, D);
+    L.fc1_b = copy_f(s.fc1_b, F);
+    L.fc2_w = copy_q8(s.fc2_w, D, F);
+    L.fc2_b = copy_f(s.fc2_b, D);
+    e->layers.push_back(std::move(L));
+  }
+  const size_t H = hp.hidden, IN = D * hp.merge;
+  e->ad_fc1_w = copy_q8(d->ad_fc1_w, H, IN);
+  e->ad_fc1_b = copy_f(d->ad_fc1_b, H);
+  e->ad_fc2_w = copy_q8(d->ad_fc2_w, H, H);
+  e->ad_fc2_b = copy_f(d->ad_fc2_b, H);
+  e->ad_ln_w = copy_f(d->ad_ln_w, H);
+  e->ad_ln_b = copy_f(d->ad_ln_b, H);
+  *out = e.release();
+  return MTG_OK;
+}
+
+void orc_encoder_destroy(orc_encoder* e) { delete e; }
+
+int orc_encoder_encode(orc_encoder* e, const float* mel, float* out, int32_t* rows_out) {
+  if (!e || !mel) return MTG_ERR_INVALID;
+  const mtg_encoder_hparams& hp = e->hp;
+  const int D = hp.d_model, F = hp.ffn, NF = hp.n_frames, NH = hp.n_heads, hd = D / NH;
+  const int R = (NF - 1) / 2 + 1;
+  // conv stem: conv1 + bias, gelu; conv2 (stride 2) + bias, gelu; + pos_embd
+  std::vector<float> c1((size_t)NF * D), c1t((size_t)D * NF), x((size_t)R * D);
+  conv1d(e->conv1_w.data(), hp.n_mels, D, mel, NF, 1, c1.data());
+  for (int t = 0; t < NF; ++t)
+    for (int o = 0; o < D; ++o) c1t[(size_t)o * NF + t] = gelu_erf(c1[(size_t)t * D + o] + e->conv1_b[o]);
+  conv1d(e->conv2_w.data(), D, D, c1t.data(), NF, 2, x.data());
+  for (int t = 0; t < R; ++t)
+    for (int o = 0; o < D; ++o) {
+      const size_t i = (size_t)t * D + o;
+      x[i] = gelu_erf(x[i] + e->conv2_b[o]) + e->pos[i];
+    }
+  std::vector<float> xn((size_t)R * D), q((size_t)R * D), k((size_t)R * D), v((size_t)R * D), a((size_t)R * D),
+      f((size_t)R * F);
+  for (const EncLayer& L : e->layers) {
+    for (int t = 0; t < R; ++t)
+      layer_norm(x.data() + (size_t)t * D, L.attn_ln_w.data(), L.attn_ln_b.data(), D, 1e-5f, xn.data() + (size_t)t * D);
+    linear_q8(L.q_w, L.q_b.data(), D, D, xn.data(), R, q.data());
+    linear_q8(L.k_w, nullptr, D, D, xn.data(), R, k.data());
+    linear_q8(L.v_w, L.v_b.data(), D, D, xn.data(), R, v.data());
+    enc_attention(q.data(), k.data(), v.data(), R, NH, hd, a.data());
+    linear_q8(L.o_w, L.o_b.data(), D, D, a.data(), R, q.data());
+    for (size_t i = 0; i < x.size(); ++i) x[i] = x[i] + q[i];
+    for (int t = 0; t < R; ++t)
+      layer_norm(x.data() + (size_t)t * D, L.ffn_ln_w.data(), L.ffn_ln_b.data(), D, 1e-5f, xn.data() + (size_t)t * D);
+    linear_q8(L.fc1_w, L.fc1_b.data(), D, F, xn.data(), R, f.data());
+    for (float& y : f) y = gelu_erf(y);
+    linear_q8(L.fc2_w, L.fc2_b.data(), F, D, f.data(), R, q.data());
+    for (size_t i = 0; i < x.size(); ++i) x[i] = x[i] + q[i];
+  }
+  e->last.assign((size_t)R * D, 0.0f);
+  for (int t = 0; t < R; ++t)
+    layer_norm(x.data() + (size_t)t * D, e->ln_post_w.data(), e->ln_post_b.data(), D, 1e-5f,
+               e->last.data() + (size_t)t * D);
+  e->last_rows = R;
+  if (out) std::memcpy(out, e->last.data(), e->last.size() * sizeof(float));
+  if (rows_out) *rows_out = R;
+  return MTG_OK;
+}
+
+int orc_encoder_adapt(orc_encoder* e, const float* rows, int32_t T, float* out, int32_t* n_out) {
+  if (!e || !out || T < 0) return MTG_ERR_INVALID;
+  const mtg_encoder_hparams& hp = e->hp;
+  if (!rows) {
+    if (T > e->last_rows) return MTG_ERR_INVALID;
+    rows = e->last.data();
+  }
+  const int D = hp.d_model, H = hp.hidden, IN = D * hp.merge, N = T / hp.merge;
+  if (n_out) *n_out = N;
+  if (N <= 0) return MTG_OK;
+  // [D * merge, N]: merge consecutive rows per adaptor row (a plain view)
+  std::vector<float> h1((size_t)N * H), h2((size_t)N * H);
+  linear_q8(e->ad_fc1_w, e->ad_fc1_b.data(), IN, H, rows, N, h1.data());
+  for (float& y : h1) y = y / (1.0f + exp_c(-y));  // ggml_silu
+  linear_q8(e->ad_fc2_w, e->ad_fc2_b.data(), H, H, h1.data(), N, h2.data());
+  for (int t = 0; t < N; ++t)
+    layer_norm(h2.data() + (size_t)t * H, e->ad_ln_w.data(), e->ad_ln_b.data(), H, hp.adaptor_eps,
+               out + (size_t)t * H);
+  return MTG_OK;
+}
+
+}  // extern "C"

@@ -97,6 +97,22 @@ void orc_softmax(const float* s, int32_t n, float scale, const float* mask, floa
 void orc_causal_context(const float* v, const float* p, int32_t head_dim, int32_t kv_heads,
                         int32_t heads, int32_t queries, int32_t kv_len, float* out);
 
+/* ---- Whisper encoder + audio adaptor (src/whisper_encoder.cpp:103-209,
+ * src/audio_adaptor.cpp:38-97) ---- */
+typedef struct orc_encoder orc_encoder;
+int orc_encoder_create(const mtg_encoder_desc* desc, orc_encoder** out);
+void orc_encoder_destroy(orc_encoder* e);
+int orc_encoder_encode(orc_encoder* e, const float* mel, float* out, int32_t* rows_out);
+int orc_encoder_adapt(orc_encoder* e, const float* rows, int32_t T, float* out, int32_t* n_out);
+/* its parts */
+float orc_gelu_erf(float x);
+void orc_layer_norm(const float* x, const float* w, const float* b, int32_t n, float eps, float* y);
+/* y [OL][oc] = conv1d of x [ic][L] with w [oc][ic][3], pad 1, stride s (no bias) */
+void orc_conv1d(const float* w, int32_t ic, int32_t oc, const float* x, int32_t L, int32_t stride, float* y);
+/* unmasked multi-head attention, q / k / v / out [T][n_heads * head_dim] */
+void orc_enc_attention(const float* q, const float* k, const float* v, int32_t T, int32_t n_heads,
+                       int32_t head_dim, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,6 +62,14 @@ SIGNATURES = {
     "orc_softmax": (None, [c_void_p, c_int32, c_float, c_void_p, c_void_p]),
     "orc_causal_context": (None, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
                                   c_void_p]),
+    "orc_encoder_create": (c_int32, [POINTER(mtg.EncoderDesc), POINTER(c_void_p)]),
+    "orc_encoder_destroy": (None, [c_void_p]),
+    "orc_encoder_encode": (c_int32, [c_void_p, c_void_p, c_void_p, POINTER(c_int32)]),
+    "orc_encoder_adapt": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, POINTER(c_int32)]),
+    "orc_gelu_erf": (c_float, [c_float]),
+    "orc_layer_norm": (None, [c_void_p, c_void_p, c_void_p, c_int32, c_float, c_void_p]),
+    "orc_conv1d": (None, [c_void_p, c_int32, c_int32, c_void_p, c_int32, c_int32, c_void_p]),
+    "orc_enc_attention": (None, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p]),
 }
 
 _lib = None
@@ -310,3 +318,72 @@ class Oracle:
         if rc:
             raise RuntimeError("orc_generate_from %d" % rc)
         return out[: n.value].copy(), st
+
+
+class OracleEncoder:
+    """CPU restatement of the Whisper encoder + adaptor (orc_encoder_*)."""
+
+    def __init__(self, synth):
+        self.hp = synth.hp
+        self.rows = synth.rows
+        out = c_void_p()
+        rc = lib().orc_encoder_create(ctypes.byref(synth.desc), ctypes.byref(out))
+        if rc:
+            raise RuntimeError("orc_encoder_create %d" % rc)
+        self.h = out
+
+    def encode(self, mel):
+        mel = np.ascontiguousarray(mel, np.float32)
+        out = np.empty((self.rows, self.hp.d_model), np.float32)
+        n = c_int32(0)
+        assert lib().orc_encoder_encode(self.h, ptr(mel), ptr(out), ctypes.byref(n)) == 0
+        return out
+
+    def adapt(self, T, rows=None):
+        out = np.empty((max(1, T // self.hp.merge), self.hp.hidden), np.float32)
+        n = c_int32(0)
+        r = None if rows is None else np.ascontiguousarray(rows, np.float32)
+        assert lib().orc_encoder_adapt(self.h, ptr(r), T, ptr(out), ctypes.byref(n)) == 0
+        return out[: n.value]
+
+    def close(self):
+        if self.h:
+            lib().orc_encoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def gelu_erf(x):
+    return float(lib().orc_gelu_erf(float(x)))
+
+
+def layer_norm(x, w, b, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_layer_norm(ptr(x), ptr(np.ascontiguousarray(w, np.float32)), ptr(np.ascontiguousarray(b, np.float32)),
+                         x.size, eps, ptr(y))
+    return y
+
+
+def conv1d(w, x, stride):
+    """w [oc][ic][3], x [ic][L] -> [OL][oc]"""
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    oc, ic, _ = w.shape
+    L = x.shape[1]
+    y = np.empty(((L - 1) // stride + 1, oc), np.float32)
+    lib().orc_conv1d(ptr(w), ic, oc, ptr(x), L, stride, ptr(y))
+    return y
+
+
+def enc_attention(q, k, v, n_heads):
+    q, k, v = (np.ascontiguousarray(a, np.float32) for a in (q, k, v))
+    T, W = q.shape
+    out = np.empty_like(q)
+    lib().orc_enc_attention(ptr(q), ptr(k), ptr(v), T, n_heads, W // n_heads, ptr(out))
+    return out

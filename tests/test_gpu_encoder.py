@@ -1,0 +1,80 @@
+"""The Whisper encoder + audio adaptor on the device (csrc/encoder.hip; reference
+WhisperEncoder::encode, src/whisper_encoder.cpp:103-209, AudioAdaptor::apply,
+src/audio_adaptor.cpp:38-97) against the oracle: encoder rows and adaptor rows
+bit-identical (the kernels keep the oracle's order of every reduction), at a
+short chunk and at the full 3,000-frame chunk (1,500 rows); the 24-layer
+encoder is timed and checked for determinism."""
+import numpy as np
+import pytest
+
+import mtg
+import oracle_py
+
+pytestmark = pytest.mark.gpu
+
+
+def _same(got, ref, what):
+    got, ref = np.asarray(got), np.asarray(ref)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    if np.array_equal(got.view(np.uint8), ref.view(np.uint8)):
+        return
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    raise AssertionError("%s: not bit-identical: %d elements differ, max err %.3g at %s"
+                         % (what, int((got != ref).sum()), err.max(), np.unravel_index(err.argmax(), err.shape)))
+
+
+@pytest.mark.parametrize("n_frames,n_layers", [(160, 2), (333, 1)])
+def test_encoder_and_adaptor_match_oracle(n_frames, n_layers):
+    print("encoder vs oracle: %d frames, %d layers" % (n_frames, n_layers), flush=True)
+    syn = mtg.SynthEncoder(seed=3, n_frames=n_frames, n_layers=n_layers, ffn=2048)
+    dev = mtg.Encoder(syn)
+    orc = oracle_py.OracleEncoder(syn)
+    mel = syn.mel(seed=4)
+    rows = dev.encode(mel)
+    _same(rows, orc.encode(mel), "encoder rows")
+    for T in (syn.rows, syn.rows - 3, 4, 3):
+        _same(dev.adapt(T), orc.adapt(T), "adaptor rows, T=%d" % T)
+    # the adaptor on rows the caller hands over
+    other = (mtg.normal(8, 0, syn.rows * 1024).reshape(syn.rows, 1024) * np.float32(0.7)).astype(np.float32)
+    _same(dev.adapt(syn.rows, rows=other), orc.adapt(syn.rows, rows=other), "adaptor on host rows")
+    dev.close()
+    orc.close()
+
+
+def test_full_chunk_two_layers_matches_oracle():
+    """3,000 mel frames (1,500 rows, full width: d 1024, 16 heads, ffn 4096):
+    the conv stem, attention over all 1,500 rows and the adaptor's 375 rows."""
+    syn = mtg.SynthEncoder(seed=11, n_layers=2)
+    dev = mtg.Encoder(syn)
+    orc = oracle_py.OracleEncoder(syn)
+    mel = syn.mel(seed=12)
+    rows = dev.encode(mel)
+    print("full chunk, 2 layers: encode %.2f ms" % dev.last_ms, flush=True)
+    _same(rows, orc.encode(mel), "encoder rows")
+    _same(dev.adapt(1500), orc.adapt(1500), "adaptor rows")
+    _same(dev.adapt(552), orc.adapt(552), "adaptor rows of a trimmed chunk")
+    dev.close()
+    orc.close()
+
+
+def test_full_encoder_24_layers_timed_and_deterministic():
+    syn = mtg.SynthEncoder(seed=21)
+    dev = mtg.Encoder(syn)
+    mel = syn.mel(seed=22)
+    a = dev.encode(mel)
+    ms = []
+    for _ in range(3):
+        b = dev.encode(mel)
+        ms.append(dev.last_ms)
+        _same(b, a, "repeated encode")
+    ad = dev.adapt(1500)
+    print("24-layer encoder, 3,000 frames -> 1,500 rows: %.2f ms (min of 3), adaptor %.3f ms"
+          % (min(ms), dev.last_ms), flush=True)
+    assert np.isfinite(a).all() and np.isfinite(ad).all()
+    # ln_post's output rows: (y - b) / w has mean 0 and variance 1 per row
+    d = syn.desc
+    w = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_float * 1024).from_address(d.ln_post_w))
+    bb = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_float * 1024).from_address(d.ln_post_b))
+    z = (a.astype(np.float64) - bb) / w
+    assert np.abs(z.mean(axis=1)).max() < 1e-4 and np.abs(z.var(axis=1) - 1).max() < 1e-2
+    dev.close()
