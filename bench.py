@@ -57,13 +57,17 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+# the sources the step kernel is built from (its launch included)
+STEP_SOURCES = ("step_kernel.hip", "step_kernel.hpp", "device_common.hpp", "kernels.hpp", "mtg_internal.hpp",
+                "runtime.cpp", "runtime.hpp")
+
+
 def source_hash():
-    """Hash of the kernel and runtime sources, to tie a profile to a build."""
+    """Hash of the step kernel's sources, to tie a counter profile of it to a build."""
     h = hashlib.sha256()
-    for name in sorted(os.listdir(CSRC)):
-        if name.endswith((".hip", ".cpp", ".hpp")):
-            h.update(name.encode())
-            h.update(open(os.path.join(CSRC, name), "rb").read())
+    for name in STEP_SOURCES:
+        h.update(name.encode())
+        h.update(open(os.path.join(CSRC, name), "rb").read())
     return h.hexdigest()[:16]
 
 

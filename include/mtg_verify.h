@@ -434,6 +434,14 @@ int mtg_encoder_encode(mtg_encoder* e, const float* mel, float* out, int32_t* ro
 int mtg_encoder_adapt(mtg_encoder* e, const float* rows, int32_t T, float* out, int32_t* n_out);
 /* device time of the last encode / adapt call, ms (HIP events) */
 double mtg_encoder_last_ms(const mtg_encoder* e);
+/* The encoder + adaptor tensors of a mapped GGUF file (enc.*, adaptor.*) and the
+ * mtd.audio.* keys with read_config's defaults (src/model_loader.cpp:130-144);
+ * n_frames = 2 * mtd.audio.max_src_pos. f16 vectors are widened to f32. NULL on
+ * failure (mtg_gguf_error). Valid until mtg_gguf_close. */
+const mtg_encoder_desc* mtg_gguf_encoder(mtg_gguf* g);
+/* mtg_gguf_open + mtg_gguf_encoder + mtg_encoder_create; errors in
+ * mtg_gguf_error(NULL). */
+int mtg_encoder_create_from_gguf(const char* path, mtg_encoder** out);
 
 /* ---- synthetic model (workload generator for the benchmark and tests) ---- */
 

@@ -18,6 +18,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <deque>
 #include <map>
 #include <memory>
 #include <new>
@@ -147,6 +148,10 @@ struct mtg_gguf {
   mtg_model_desc desc{};
   std::vector<mtg_layer_tensors> layers;
   std::vector<std::vector<float>> widened;  // f16 norm gains as f32
+  // the encoder view, built by mtg_gguf_encoder
+  mtg_encoder_desc enc{};
+  std::vector<mtg_encoder_layer> enc_layers;
+  std::deque<std::vector<float>> enc_widened;  // f16 vectors as f32 (stable addresses)
   ~mtg_gguf() {
     if (map) munmap(map, size);
   }
@@ -419,6 +424,139 @@ const mtg_model_desc* mtg_gguf_model(mtg_gguf* g) {
     g->fail(MTG_ERR_NOMEM, "out of memory");
     return nullptr;
   }
+}
+
+// The Whisper encoder + adaptor tensors (reference WhisperEncoder /
+// AudioAdaptor constructors, src/whisper_encoder.cpp:64-95,
+// src/audio_adaptor.cpp:22-34) and the mtd.audio.* / adaptor keys with
+// read_config's defaults (src/model_loader.cpp:130-144).
+const mtg_encoder_desc* mtg_gguf_encoder(mtg_gguf* g) {
+  if (!g) return nullptr;
+  try {
+    mtg_encoder_hparams hp{};
+    hp.n_mels = (int32_t)g->get_u("mtd.audio.mel_bins", 80);
+    hp.d_model = (int32_t)g->get_u("mtd.audio.d_model", 1024);
+    hp.n_layers = (int32_t)g->get_u("mtd.audio.n_layers", 24);
+    hp.n_heads = (int32_t)g->get_u("mtd.audio.n_heads", 16);
+    hp.ffn = (int32_t)g->get_u("mtd.audio.ffn", 4096);
+    const int64_t src_pos = (int64_t)g->get_u("mtd.audio.max_src_pos", 1500);
+    hp.n_frames = (int32_t)(2 * src_pos);
+    hp.merge = (int32_t)g->get_u("mtd.audio_merge_size", 4);
+    hp.hidden = (int32_t)g->get_u("mtd.text.hidden", 1024);
+    hp.adaptor_eps = (float)g->get_f("mtd.adaptor_norm_eps", 1e-6);
+    if (hp.n_mels <= 0 || hp.d_model <= 0 || hp.n_layers < 0 || hp.n_heads <= 0 || hp.ffn <= 0 || src_pos <= 0 ||
+        hp.merge <= 0 || hp.hidden <= 0) {
+      g->fail(MTG_ERR_INVALID, "bad mtd.audio.* hyper-parameters");
+      return nullptr;
+    }
+    const int64_t D = hp.d_model, F = hp.ffn, M = hp.n_mels, H = hp.hidden, IN = D * hp.merge;
+    const TensorInfo* q0 = nullptr;
+    auto find = [&](const std::string& name, const TensorInfo** t) -> bool {
+      auto it = g->tensors.find(name);
+      if (it == g->tensors.end()) {
+        g->fail(MTG_ERR_INVALID, "missing tensor " + name);
+        return false;
+      }
+      *t = &it->second;
+      return true;
+    };
+    uint32_t wtype = MTG_TYPE_Q8_0;
+    if (hp.n_layers > 0) {
+      if (!find("enc.blk.0.attn_q.w", &q0)) return nullptr;
+      wtype = q0->type;
+    }
+    if (wtype != MTG_TYPE_Q8_0) {
+      g->fail(MTG_ERR_UNSUPPORTED, std::string("encoder weight type ") + type_name(wtype) + " is not supported: q8_0");
+      return nullptr;
+    }
+    auto matrix = [&](const std::string& name, int64_t k, int64_t n, const void** out) -> bool {
+      const TensorInfo* t = nullptr;
+      if (!find(name, &t)) return false;
+      if (t->type != wtype) {
+        g->fail(MTG_ERR_UNSUPPORTED, name + " is " + type_name(t->type) + ": the encoder matrices must be q8_0");
+        return false;
+      }
+      if (t->n_dims != 2 || (int64_t)t->ne[0] != k || (int64_t)t->ne[1] != n) {
+        g->fail(MTG_ERR_INVALID, name + ": shape [" + std::to_string(t->ne[0]) + ", " + std::to_string(t->ne[1]) +
+                                     "], expected [" + std::to_string(k) + ", " + std::to_string(n) + "]");
+        return false;
+      }
+      *out = t->data;
+      return true;
+    };
+    // f32 (or f16, widened) tensor of n elements in any shape
+    auto vec = [&](const std::string& name, int64_t n, const float** out) -> bool {
+      const TensorInfo* t = nullptr;
+      if (!find(name, &t)) return false;
+      if ((int64_t)(t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]) != n) {
+        g->fail(MTG_ERR_INVALID, name + ": expected " + std::to_string(n) + " elements");
+        return false;
+      }
+      if (t->type == 0) {
+        *out = (const float*)t->data;
+      } else if (t->type == 1) {
+        g->enc_widened.emplace_back((size_t)n);
+        const uint16_t* h = (const uint16_t*)t->data;
+        for (int64_t i = 0; i < n; ++i) g->enc_widened.back()[(size_t)i] = mtg_f16_to_f32(h[i]);
+        *out = g->enc_widened.back().data();
+      } else {
+        g->fail(MTG_ERR_UNSUPPORTED, name + ": must be f32 or f16");
+        return false;
+      }
+      return true;
+    };
+    g->enc_widened.clear();
+    mtg_encoder_desc& e = g->enc;
+    e = mtg_encoder_desc{};
+    if (!vec("enc.conv1.w", D * M * 3, &e.conv1_w) || !vec("enc.conv1.b", D, &e.conv1_b) ||
+        !vec("enc.conv2.w", D * D * 3, &e.conv2_w) || !vec("enc.conv2.b", D, &e.conv2_b) ||
+        !vec("enc.pos_embd", src_pos * D, &e.pos_embd) || !vec("enc.ln_post.w", D, &e.ln_post_w) ||
+        !vec("enc.ln_post.b", D, &e.ln_post_b))
+      return nullptr;
+    g->enc_layers.assign((size_t)hp.n_layers, mtg_encoder_layer{});
+    for (int i = 0; i < hp.n_layers; ++i) {
+      mtg_encoder_layer& L = g->enc_layers[(size_t)i];
+      const std::string b = "enc.blk." + std::to_string(i) + ".";
+      if (!vec(b + "attn_ln.w", D, &L.attn_ln_w) || !vec(b + "attn_ln.b", D, &L.attn_ln_b) ||
+          !matrix(b + "attn_q.w", D, D, &L.q_w) || !vec(b + "attn_q.b", D, &L.q_b) ||
+          !matrix(b + "attn_k.w", D, D, &L.k_w) || !matrix(b + "attn_v.w", D, D, &L.v_w) ||
+          !vec(b + "attn_v.b", D, &L.v_b) || !matrix(b + "attn_out.w", D, D, &L.o_w) ||
+          !vec(b + "attn_out.b", D, &L.o_b) || !vec(b + "ffn_ln.w", D, &L.ffn_ln_w) ||
+          !vec(b + "ffn_ln.b", D, &L.ffn_ln_b) || !matrix(b + "ffn_1.w", D, F, &L.fc1_w) ||
+          !vec(b + "ffn_1.b", F, &L.fc1_b) || !matrix(b + "ffn_2.w", F, D, &L.fc2_w) ||
+          !vec(b + "ffn_2.b", D, &L.fc2_b))
+        return nullptr;
+    }
+    if (!matrix("adaptor.fc1.w", IN, H, &e.ad_fc1_w) || !vec("adaptor.fc1.b", H, &e.ad_fc1_b) ||
+        !matrix("adaptor.fc2.w", H, H, &e.ad_fc2_w) || !vec("adaptor.fc2.b", H, &e.ad_fc2_b) ||
+        !vec("adaptor.ln.w", H, &e.ad_ln_w) || !vec("adaptor.ln.b", H, &e.ad_ln_b))
+      return nullptr;
+    e.hp = hp;
+    e.weight_type = (int32_t)wtype;
+    e.layers = g->enc_layers.data();
+    return &e;
+  } catch (...) {
+    g->fail(MTG_ERR_NOMEM, "out of memory");
+    return nullptr;
+  }
+}
+
+int mtg_encoder_create_from_gguf(const char* path, mtg_encoder** out) {
+  if (!out) return MTG_ERR_INVALID;
+  *out = nullptr;
+  mtg_gguf* g = nullptr;
+  int rc = mtg_gguf_open(path, &g);
+  if (rc) return rc;
+  const mtg_encoder_desc* d = mtg_gguf_encoder(g);
+  if (!d) {
+    g_gguf_error = g->error;
+    rc = g->code ? g->code : MTG_ERR_INVALID;
+    mtg_gguf_close(g);
+    return rc;
+  }
+  rc = mtg_encoder_create(d, out);
+  mtg_gguf_close(g);  // the encoder holds its own copies
+  return rc;
 }
 
 int mtg_create_from_gguf(const char* path, int32_t max_seq, int32_t kv_type, mtg_ctx** out) {

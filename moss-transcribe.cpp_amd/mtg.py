@@ -172,6 +172,8 @@ SIGNATURES.update({
     "mtg_encoder_encode": (c_int32, [c_void_p, c_void_p, c_void_p, POINTER(c_int32)]),
     "mtg_encoder_adapt": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, POINTER(c_int32)]),
     "mtg_encoder_last_ms": (c_double, [c_void_p]),
+    "mtg_gguf_encoder": (POINTER(EncoderDesc), [c_void_p]),
+    "mtg_encoder_create_from_gguf": (c_int32, [ctypes.c_char_p, POINTER(c_void_p)]),
 })
 
 _lib = None
@@ -256,14 +258,18 @@ class SynthModel:
 
 
 class GgufModel:
-    """A mapped GGUF file (mtg_gguf) and its decoder description."""
+    """A mapped GGUF file (mtg_gguf) and its decoder description (decoder=False:
+    the file is not required to hold a decoder)."""
 
-    def __init__(self, path):
+    def __init__(self, path, decoder=True):
         out = c_void_p()
         rc = lib().mtg_gguf_open(os.fsencode(path), ctypes.byref(out))
         if rc:
             raise MtgError(rc, lib().mtg_gguf_error(None).decode())
         self.handle = out
+        if not decoder:
+            self.desc = self.hp = self.weight_type = None
+            return
         d = lib().mtg_gguf_model(out)
         if not d:
             msg = lib().mtg_gguf_error(out).decode()
@@ -272,6 +278,13 @@ class GgufModel:
         self.desc = d
         self.hp = d.contents.hp
         self.weight_type = d.contents.weight_type
+
+    def encoder(self):
+        """The file's encoder + adaptor description (mtg_gguf_encoder)."""
+        d = lib().mtg_gguf_encoder(self.handle)
+        if not d:
+            raise MtgError(ERR_INVALID, lib().mtg_gguf_error(self.handle).decode())
+        return d
 
     def tensor(self, name):
         """(ggml type, ne[4], raw bytes) of one tensor."""
@@ -650,6 +663,22 @@ class Encoder:
         if rc:
             raise MtgError(rc, "encoder create")
         self.h = out
+
+    @classmethod
+    def from_gguf(cls, path):
+        g = GgufModel(path, decoder=False)
+        hp = EncoderHparams()
+        ctypes.memmove(ctypes.byref(hp), ctypes.byref(g.encoder().contents.hp), ctypes.sizeof(EncoderHparams))
+        g.close()
+        self = cls.__new__(cls)
+        self.hp = hp
+        self.rows = (hp.n_frames - 1) // 2 + 1
+        out = c_void_p()
+        rc = lib().mtg_encoder_create_from_gguf(os.fsencode(path), ctypes.byref(out))
+        if rc:
+            raise MtgError(rc, lib().mtg_gguf_error(None).decode())
+        self.h = out
+        return self
 
     def _chk(self, rc):
         if rc:

@@ -115,3 +115,59 @@ def write_model(path, model, f16_norms=False, alignment=32, extra_kv=(), edit=No
     if alignment != 32:
         kv.append(("general.alignment", U32, alignment))
     write(path, kv, tensors, alignment)
+
+
+def encoder_tensors(syn):
+    """The encoder + adaptor tensors of a SynthEncoder with their GGUF names
+    (src/whisper_encoder.cpp:71-94, src/audio_adaptor.cpp:28-33)."""
+    h, d = syn.hp, syn.desc
+    D, F, M, H, IN = h.d_model, h.ffn, h.n_mels, h.hidden, h.d_model * h.merge
+    R = syn.rows
+    rb = lambda k: mtg.lib().mtg_row_bytes(8, k)
+
+    def f32(p, ne):
+        return (0, ne, ctypes.string_at(p, 4 * int(np.prod(ne))))
+
+    def q8(p, k, n):
+        return (8, [k, n], ctypes.string_at(p, rb(k) * n))
+
+    out = [("enc.conv1.w",) + f32(d.conv1_w, [3, M, D]), ("enc.conv1.b",) + f32(d.conv1_b, [D]),
+           ("enc.conv2.w",) + f32(d.conv2_w, [3, D, D]), ("enc.conv2.b",) + f32(d.conv2_b, [D]),
+           ("enc.pos_embd",) + f32(d.pos_embd, [D, R])]
+    for i in range(h.n_layers):
+        L = d.layers[i]
+        b = "enc.blk.%d." % i
+        out += [(b + "attn_ln.w",) + f32(L.attn_ln_w, [D]), (b + "attn_ln.b",) + f32(L.attn_ln_b, [D]),
+                (b + "attn_q.w",) + q8(L.q_w, D, D), (b + "attn_q.b",) + f32(L.q_b, [D]),
+                (b + "attn_k.w",) + q8(L.k_w, D, D), (b + "attn_v.w",) + q8(L.v_w, D, D),
+                (b + "attn_v.b",) + f32(L.v_b, [D]), (b + "attn_out.w",) + q8(L.o_w, D, D),
+                (b + "attn_out.b",) + f32(L.o_b, [D]), (b + "ffn_ln.w",) + f32(L.ffn_ln_w, [D]),
+                (b + "ffn_ln.b",) + f32(L.ffn_ln_b, [D]), (b + "ffn_1.w",) + q8(L.fc1_w, D, F),
+                (b + "ffn_1.b",) + f32(L.fc1_b, [F]), (b + "ffn_2.w",) + q8(L.fc2_w, F, D),
+                (b + "ffn_2.b",) + f32(L.fc2_b, [D])]
+    out += [("enc.ln_post.w",) + f32(d.ln_post_w, [D]), ("enc.ln_post.b",) + f32(d.ln_post_b, [D]),
+            ("adaptor.fc1.w",) + q8(d.ad_fc1_w, IN, H), ("adaptor.fc1.b",) + f32(d.ad_fc1_b, [H]),
+            ("adaptor.fc2.w",) + q8(d.ad_fc2_w, H, H), ("adaptor.fc2.b",) + f32(d.ad_fc2_b, [H]),
+            ("adaptor.ln.w",) + f32(d.ad_ln_w, [H]), ("adaptor.ln.b",) + f32(d.ad_ln_b, [H])]
+    return out
+
+
+def encoder_metadata(syn):
+    h = syn.hp
+    return [("mtd.audio.mel_bins", U32, h.n_mels), ("mtd.audio.d_model", U32, h.d_model),
+            ("mtd.audio.n_layers", U32, h.n_layers), ("mtd.audio.n_heads", U32, h.n_heads),
+            ("mtd.audio.ffn", U32, h.ffn), ("mtd.audio.max_src_pos", U32, syn.rows),
+            ("mtd.audio_merge_size", U32, h.merge), ("mtd.adaptor_input_dim", U32, h.d_model * h.merge),
+            ("mtd.adaptor_norm_eps", F32, h.adaptor_eps), ("mtd.audio.act", STR, "gelu")]
+
+
+def write_encoder(path, syn, model=None, edit=None):
+    """A GGUF file with a SynthEncoder's tensors (and a SynthModel's decoder, if given)."""
+    tensors = encoder_tensors(syn)
+    kv = encoder_metadata(syn) + [("mtd.text.hidden", U32, syn.hp.hidden)]
+    if model is not None:
+        tensors = model_tensors(model) + tensors
+        kv = model_metadata(model) + encoder_metadata(syn)
+    if edit is not None:
+        tensors = edit(tensors)
+    write(path, kv, tensors)

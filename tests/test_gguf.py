@@ -157,3 +157,68 @@ def test_damaged_and_foreign_files_fail_with_a_reason(tmp_path):
     with pytest.raises(mtg.MtgError):
         mtg.GgufModel(str(tmp_path / "absent.gguf"))
     m.close()
+
+
+def _enc_bytes(desc, syn):
+    h = syn.hp
+    D, F, M, H, IN = h.d_model, h.ffn, h.n_mels, h.hidden, h.d_model * h.merge
+    rb = lambda k: mtg.lib().mtg_row_bytes(8, k)
+    d = desc.contents if hasattr(desc, "contents") else desc
+    fs = lambda p, n: ctypes.string_at(p, 4 * n)
+    out = [fs(d.conv1_w, D * M * 3), fs(d.conv1_b, D), fs(d.conv2_w, D * D * 3), fs(d.conv2_b, D),
+           fs(d.pos_embd, syn.rows * D), fs(d.ln_post_w, D), fs(d.ln_post_b, D),
+           ctypes.string_at(d.ad_fc1_w, rb(IN) * H), fs(d.ad_fc1_b, H), ctypes.string_at(d.ad_fc2_w, rb(H) * H),
+           fs(d.ad_fc2_b, H), fs(d.ad_ln_w, H), fs(d.ad_ln_b, H)]
+    for i in range(h.n_layers):
+        L = d.layers[i]
+        out += [fs(L.attn_ln_w, D), fs(L.attn_ln_b, D), ctypes.string_at(L.q_w, rb(D) * D),
+                ctypes.string_at(L.k_w, rb(D) * D), ctypes.string_at(L.v_w, rb(D) * D),
+                ctypes.string_at(L.o_w, rb(D) * D), fs(L.q_b, D), fs(L.v_b, D), fs(L.o_b, D), fs(L.ffn_ln_w, D),
+                fs(L.ffn_ln_b, D), ctypes.string_at(L.fc1_w, rb(D) * F), fs(L.fc1_b, F),
+                ctypes.string_at(L.fc2_w, rb(F) * D), fs(L.fc2_b, D)]
+    return out
+
+
+def test_encoder_tensors_round_trip(tmp_path):
+    """The encoder + adaptor of a file with the decoder too (the converter's
+    layout): every tensor byte for byte, the mtd.audio.* hyper-parameters, and
+    the reference defaults when the keys are absent."""
+    syn = mtg.SynthEncoder(seed=4, n_mels=16, n_frames=96, d_model=128, n_layers=2, n_heads=2, ffn=256, merge=4,
+                           hidden=128)
+    m = mtg.SynthModel(mtg.TYPE_Q8_0, seed=2, n_layers=1, vocab=512, hidden=128, n_heads=2, n_kv_heads=1,
+                       intermediate=256)
+    path = str(tmp_path / "full.gguf")
+    gguf_writer.write_encoder(path, syn, model=m)
+    g = mtg.GgufModel(path)
+    e = g.encoder().contents
+    for f in ("n_mels", "n_frames", "d_model", "n_layers", "n_heads", "ffn", "merge", "hidden"):
+        assert getattr(e.hp, f) == getattr(syn.hp, f), f
+    assert e.hp.adaptor_eps == np.float32(syn.hp.adaptor_eps) and e.weight_type == mtg.TYPE_Q8_0
+    got, want = _enc_bytes(e, syn), _enc_bytes(syn.desc, syn)
+    assert len(got) == len(want)
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert a == b, i
+    g.close()
+    # without the mtd.audio.* keys: read_config's defaults (24 layers of d 1024)
+    p2 = str(tmp_path / "nokeys.gguf")
+    gguf_writer.write(p2, [], gguf_writer.encoder_tensors(syn))
+    out = ctypes.c_void_p()
+    assert mtg.lib().mtg_gguf_open(os.fsencode(p2), ctypes.byref(out)) == 0
+    assert not mtg.lib().mtg_gguf_encoder(out)
+    assert "enc.conv1.w: expected" in mtg.lib().mtg_gguf_error(out).decode()
+    mtg.lib().mtg_gguf_close(out)
+    # a missing adaptor tensor, an f16 projection
+    p3 = str(tmp_path / "missing.gguf")
+    gguf_writer.write_encoder(p3, syn, edit=lambda ts: [t for t in ts if t[0] != "adaptor.fc2.b"])
+    enc = ctypes.c_void_p()
+    assert mtg.lib().mtg_encoder_create_from_gguf(os.fsencode(p3), ctypes.byref(enc)) != 0
+    assert "missing tensor adaptor.fc2.b" in mtg.lib().mtg_gguf_error(None).decode()
+
+    def f16_k(ts):
+        return [(n, 1, ne, np.zeros(ne[0] * ne[1], np.float16).tobytes()) if n == "enc.blk.0.attn_k.w" else (n, t, ne, dd)
+                for n, t, ne, dd in ts]
+    p4 = str(tmp_path / "f16k.gguf")
+    gguf_writer.write_encoder(p4, syn, edit=f16_k)
+    assert mtg.lib().mtg_encoder_create_from_gguf(os.fsencode(p4), ctypes.byref(enc)) != 0
+    assert "must be q8_0" in mtg.lib().mtg_gguf_error(None).decode()
+    m.close()

@@ -60,3 +60,16 @@ def test_full_size_q8_0_file(tmp_path):
     print("full-size q8_0 GGUF: %.0f MB written in %.1f s" % (os.path.getsize(path) / 1e6, t1 - t0), flush=True)
     _compare(model, path, mtg.TYPE_F32, 100, 8)
     model.close()
+
+
+def test_encoder_from_gguf_equals_encoder_from_model(tmp_path):
+    syn = mtg.SynthEncoder(seed=31, n_frames=160, n_layers=2, ffn=2048)
+    path = str(tmp_path / "enc.gguf")
+    gguf_writer.write_encoder(path, syn)
+    a = mtg.Encoder(syn)
+    b = mtg.Encoder.from_gguf(path)
+    mel = syn.mel(seed=32)
+    _same(b.encode(mel), a.encode(mel), "encoder rows")
+    _same(b.adapt(80), a.adapt(80), "adaptor rows")
+    a.close()
+    b.close()
