@@ -70,16 +70,32 @@ __device__ __forceinline__ float dev_rms_scale(float mean, float eps) {
 
 // silu(g) * u with the canonical exp and a correctly rounded division.
 // erf by its Maclaurin series in double, a fixed number of terms per range of
-// |z| (the oracle evaluates the same operations); +-1 from |z| >= 4.
+// |z| (the oracle evaluates the same operations); +-1 from |z| >= 4. The
+// divisions by n + 1 and 2 n + 1 are multiplications by their double
+// reciprocals, rounded once at compile time (the oracle's table holds the same
+// values).
+template <int N>
+struct ErfRecip {
+  double inv_next[N], inv_odd[N];
+  constexpr ErfRecip() : inv_next(), inv_odd() {
+    for (int n = 0; n < N; ++n) {
+      inv_next[n] = 1.0 / (double)(n + 1);
+      inv_odd[n] = 1.0 / (double)(2 * n + 1);
+    }
+  }
+};
+__constant__ constexpr ErfRecip<76> kErfRecip{};
 __device__ __forceinline__ double dev_erf_series(double z) {
+  const ErfRecip<76>& tab = kErfRecip;
   const double a = fabs(z);
   if (a >= 4.0) return z < 0.0 ? -1.0 : 1.0;
   const int terms = a < 1.0 ? 28 : (a < 2.0 ? 44 : (a < 3.0 ? 60 : 76));
   const double a2 = __dmul_rn(a, a);
   double term = a, sum = 0.0;
+#pragma unroll 4
   for (int n = 0; n < terms; ++n) {
-    sum = __dadd_rn(sum, __ddiv_rn(term, (double)(2 * n + 1)));
-    term = -__ddiv_rn(__dmul_rn(term, a2), (double)(n + 1));
+    sum = __dadd_rn(sum, __dmul_rn(term, tab.inv_odd[n]));
+    term = -__dmul_rn(__dmul_rn(term, a2), tab.inv_next[n]);
   }
   const double r = __dmul_rn(sum, 1.1283791670955126);  // 2 / sqrt(pi)
   return z < 0.0 ? -r : r;

@@ -35,8 +35,8 @@ namespace {
 using namespace dev;
 
 constexpr int kEncHd = 64;      // head_dim
-constexpr int kEncRows = 16;    // query rows per attention workgroup
-constexpr int kEncMaxChunks = 64;  // rows <= 4096
+constexpr int kEncRows = 64;    // query rows per attention workgroup
+constexpr int kEncMaxChunks = 32;  // rows <= 2048
 constexpr int kConvTile = 64;   // outputs per conv workgroup: 64 rows x 64 channels
 constexpr int kConvIcb = 16;    // input channels staged per step
 
@@ -164,103 +164,155 @@ k_enc_ln(const float* __restrict__ src, int S, const float* __restrict__ w, cons
 }
 
 // ------------------------------------------------------------ attention ----
-// Rows r0 .. r0 + 15 of head blockIdx.x over all T rows (no mask), q / k / v /
-// out [T][W] (W = heads * 64). Thread (r, g) = (tid / 16, tid % 16): scores of
-// keys 4 g .. 4 g + 3 of a chunk, then context elements 4 g .. 4 g + 3.
+// Rows r0 .. r0 + 63 of head blockIdx.x over all T rows (no mask), q / k / v /
+// out [T][W] (W = heads * 64). Thread (tr, tk) = (tid / 16, tid % 16) holds a
+// 4 x 4 register tile: the scores of rows 4 tr + i and keys 4 tk + j of a chunk
+// (fma chains over head_dim from 16-byte LDS reads), then the context of rows
+// 4 tr + i and elements 4 tk + e (fma chains over the chunk's keys). Pass 1
+// takes every chunk's row maxima; pass 2 recomputes the scores, p = exp(w - m_c),
+// l_c (fold-in-half over the 64 keys, the butterfly's order), O_c, and merges
+// the chunks in order.
+constexpr int kAS = kEncHd + 4;  // LDS row stride, floats (16-byte rows)
 __global__ void __launch_bounds__(256)
 k_enc_attn(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, int T, int W,
            float* __restrict__ out) {
-  __shared__ float qs[kEncRows][kEncHd + 1];
-  __shared__ float ks[64][kEncHd + 1];
-  __shared__ __align__(16) float vs[64][kEncHd + 4];
-  __shared__ float ps[kEncRows][64 + 1];
-  __shared__ float cm[kEncRows][kEncMaxChunks];
+  __shared__ __align__(16) float qs[kEncRows][kAS];
+  __shared__ __align__(16) float kv[64][kAS];  // the chunk's K, then its V
+  __shared__ __align__(16) float ps[kEncRows][kAS];
+  __shared__ float cm[kEncRows][kEncMaxChunks + 1];
   __shared__ float cl[kEncRows];
   const int h = blockIdx.x, r0 = blockIdx.y * kEncRows;
-  const int tid = threadIdx.x, r = tid >> 4, g = tid & 15;
+  const int tid = threadIdx.x, tr = tid >> 4, tk = tid & 15;
   const int nch = (T + 63) / 64;
   const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)kEncHd));
-  for (int i = tid; i < kEncRows * kEncHd; i += 256) {
-    const int rr = i / kEncHd, d = i % kEncHd;
-    qs[rr][d] = r0 + rr < T ? q[(size_t)(r0 + rr) * W + h * kEncHd + d] : 0.0f;
-  }
-  auto stage = [&](float (*dst)[kEncHd + 1], const float* src, int key0) {
-    for (int i = tid; i < 64 * kEncHd; i += 256) {
-      const int j = i / kEncHd, d = i % kEncHd;
-      dst[j][d] = key0 + j < T ? src[(size_t)(key0 + j) * W + h * kEncHd + d] : 0.0f;
+  const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  // 64 rows x 64 floats of src from row0 (zeros past T) into dst
+  auto stage = [&](float (*dst)[kAS], const float* src, int row0) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int i = tid + 256 * x, rr = i >> 4, d4 = i & 15;
+      *(v4f*)&dst[rr][4 * d4] =
+          row0 + rr < T ? *(const v4f*)(src + (size_t)(row0 + rr) * W + h * kEncHd + 4 * d4) : zero4;
     }
   };
-  // scores w[e] of keys key0 + 4 g + e: fma chains over d, scaled, masked past T
-  auto scores = [&](int key0, float (&wv)[4]) {
+  auto scores = [&](int key0, float (&w)[4][4]) {
+    float acc[4][4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float s = 0.0f;
-      for (int d = 0; d < kEncHd; ++d) s = fmaf(qs[r][d], ks[4 * g + e][d], s);
-      wv[e] = key0 + 4 * g + e < T ? __fmul_rn(s, scale) : -INFINITY;
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    for (int d0 = 0; d0 < kEncHd; d0 += 4) {
+      v4f qv[4], kx[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qv[i] = *(const v4f*)&qs[4 * tr + i][d0];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) kx[j] = *(const v4f*)&kv[4 * tk + j][d0];
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(qv[i][dd], kx[j][dd], acc[i][j]);
     }
-  };
-  auto row_max16 = [&](float m) {  // over the 16 threads of row r (consecutive lanes)
 #pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
-    return m;
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[i][j] = key0 + 4 * tk + j < T ? __fmul_rn(acc[i][j], scale) : -INFINITY;
   };
-  // pass 1: chunk maxima
+  stage(qs, q, r0);
+  // pass 1: chunk maxima per row (over the 16 threads of a row group)
   for (int c = 0; c < nch; ++c) {
     __syncthreads();
-    stage(ks, k, 64 * c);
+    stage(kv, k, 64 * c);
     __syncthreads();
-    float wv[4];
-    scores(64 * c, wv);
-    const float m = row_max16(fmaxf(fmaxf(wv[0], wv[1]), fmaxf(wv[2], wv[3])));
-    if (g == 0) cm[r][c] = m;
+    float w[4][4];
+    scores(64 * c, w);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float m = fmaxf(fmaxf(w[i][0], w[i][1]), fmaxf(w[i][2], w[i][3]));
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+      if (tk == 0) cm[4 * tr + i][c] = m;
+    }
   }
   __syncthreads();
-  float M = -INFINITY;
-  for (int c = 0; c < nch; ++c) M = fmaxf(M, cm[r][c]);
-  // pass 2: p = exp(w - m_c), l_c (fold-in-half sum = the butterfly), O_c, merge
-  float L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float M[4], L[4], O[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    M[i] = -INFINITY;
+    for (int c = 0; c < nch; ++c) M[i] = fmaxf(M[i], cm[4 * tr + i][c]);
+    L[i] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) O[i][e] = 0.0f;
+  }
+  // pass 2
   for (int c = 0; c < nch; ++c) {
     __syncthreads();
-    stage(ks, k, 64 * c);
-    for (int i = tid; i < 64 * kEncHd; i += 256) {
-      const int j = i / kEncHd, d = i % kEncHd;
-      vs[j][d] = 64 * c + j < T ? v[(size_t)(64 * c + j) * W + h * kEncHd + d] : 0.0f;
-    }
+    stage(kv, k, 64 * c);
     __syncthreads();
-    float wv[4];
-    scores(64 * c, wv);
-    const float mc = cm[r][c];
+    float w[4][4];
+    scores(64 * c, w);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) ps[r][4 * g + e] = wv[e] == -INFINITY ? 0.0f : dev_expf(__fsub_rn(wv[e], mc));
-    __syncthreads();
-    if (g == 0) {
+    for (int i = 0; i < 4; ++i) {
+      const float mc = cm[4 * tr + i][c];
+      v4f p4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) p4[j] = w[i][j] == -INFINITY ? 0.0f : dev_expf(__fsub_rn(w[i][j], mc));
+      *(v4f*)&ps[4 * tr + i][4 * tk] = p4;
+    }
+    __syncthreads();  // K consumed, p complete
+    stage(kv, v, 64 * c);
+    if (tid < kEncRows) {
       float t[64];
 #pragma unroll
-      for (int j = 0; j < 64; ++j) t[j] = ps[r][j];
+      for (int j = 0; j < 64; j += 4) {
+        const v4f p4 = *(const v4f*)&ps[tid][j];
+        t[j] = p4[0];
+        t[j + 1] = p4[1];
+        t[j + 2] = p4[2];
+        t[j + 3] = p4[3];
+      }
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1)
 #pragma unroll
         for (int j = 0; j < o; ++j) t[j] = __fadd_rn(t[j], t[j + o]);
-      cl[r] = t[0];
+      cl[tid] = t[0];
     }
-    float oc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = 0; j < 64; ++j) {
-      const float p = ps[r][j];
-      const v4f vv = *(const v4f*)&vs[j][4 * g];
+    __syncthreads();  // V staged, l_c ready
+    float oc[4][4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) oc[e] = fmaf(p, vv[e], oc[e]);
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) oc[i][e] = 0.0f;
+    for (int j0 = 0; j0 < 64; j0 += 4) {
+      v4f pv[4], vv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pv[i] = *(const v4f*)&ps[4 * tr + i][j0];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) vv[jj] = *(const v4f*)&kv[j0 + jj][4 * tk];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) oc[i][e] = fmaf(pv[i][jj], vv[jj][e], oc[i][e]);
     }
-    __syncthreads();
-    const float f = dev_expf(__fsub_rn(mc, M));
-    L = fmaf(cl[r], f, L);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) O[e] = fmaf(oc[e], f, O[e]);
+    for (int i = 0; i < 4; ++i) {
+      const float f = dev_expf(__fsub_rn(cm[4 * tr + i][c], M[i]));
+      L[i] = fmaf(cl[4 * tr + i], f, L[i]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) O[i][e] = fmaf(oc[i][e], f, O[i][e]);
+    }
   }
-  if (r0 + r < T) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = r0 + 4 * tr + i;
+    if (row >= T) continue;
     v4f o4;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o4[e] = __fdiv_rn(O[e], L);
-    *(v4f*)(out + (size_t)(r0 + r) * W + h * kEncHd + 4 * g) = o4;
+    for (int e = 0; e < 4; ++e) o4[e] = __fdiv_rn(O[i][e], L[i]);
+    *(v4f*)(out + (size_t)row * W + h * kEncHd + 4 * tk) = o4;
   }
 }
 

@@ -1100,7 +1100,19 @@ namespace {
 
 // erf by its Maclaurin series in double, a fixed number of terms per range of
 // |z| (the device evaluates the same operations); erf(z) = +-1 from |z| >= 4,
-// where 1 - erf(4) = 1.5e-8 no longer moves a float.
+// where 1 - erf(4) = 1.5e-8 no longer moves a float. The divisions by n + 1 and
+// 2 n + 1 are multiplications by their double reciprocals (a shared table).
+constexpr int kErfTerms = 76;
+struct ErfTable {
+  double inv_next[kErfTerms], inv_odd[kErfTerms];
+  constexpr ErfTable() : inv_next(), inv_odd() {
+    for (int n = 0; n < kErfTerms; ++n) {
+      inv_next[n] = 1.0 / (double)(n + 1);
+      inv_odd[n] = 1.0 / (double)(2 * n + 1);
+    }
+  }
+};
+constexpr ErfTable kErf{};
 double erf_series(double z) {
   const double a = std::fabs(z);
   if (a >= 4.0) return z < 0.0 ? -1.0 : 1.0;
@@ -1108,8 +1120,8 @@ double erf_series(double z) {
   const double a2 = a * a;
   double term = a, sum = 0.0;
   for (int n = 0; n < terms; ++n) {
-    sum = sum + term / (double)(2 * n + 1);
-    term = -(term * a2) / (double)(n + 1);
+    sum = sum + term * kErf.inv_odd[n];
+    term = -(term * a2) * kErf.inv_next[n];
   }
   const double r = sum * 1.1283791670955126;  // 2 / sqrt(pi)
   return z < 0.0 ? -r : r;
