@@ -1,5 +1,5 @@
-"""The drop-in loader snippet of INTEGRATION.md reads the tensors the reference's
-loader reads, in the field order of mtg_layer_tensors.
+"""The drop-in loader snippet of the repository's integration guide reads the
+tensors the reference's loader reads, in the field order of mtg_layer_tensors.
 
 Expected names (data, cited): qwen3_load_layer reads prefix + ".blk.<i>." + one of
 the eleven names below with prefix "qwen3" (src/qwen3.cpp:33-56), and
@@ -28,7 +28,7 @@ def _snippet():
     for b in blocks:
         if "mtg_desc_from_loader" in b:
             return b
-    raise AssertionError("INTEGRATION.md has no loader snippet")
+    raise AssertionError("the integration guide has no loader snippet")
 
 
 def _struct_fields():

@@ -14,8 +14,7 @@ length; src/qwen3.cpp:157-189, src/cpu_context.cpp:13-32).
   exceeds delta while delta < d: differences grow layer by layer to the size of
   one quantization step (~1 % of the row's magnitude) and stay there. The test
   asserts that bound and that the greedy choices agree wherever the top-2 margin
-  exceeds twice the largest logit difference; the printed numbers are the ones
-  DESIGN.md reports.
+  exceeds twice the largest logit difference, and prints the measured distances.
 """
 import os
 
