@@ -541,11 +541,18 @@ __device__ __forceinline__ void panel_from_q(const int8_t* codes, const float* s
   const Rsrc rc = mk_rsrc(codes, kMaxRows * K);
   const Rsrc rs = mk_rsrc(scales, kMaxRows * (K / 32) * 4);
   const int chunks = T * cpr;
+  // the thread index through an empty asm: the chunk addresses below are then
+  // computed here, on every call. As loop invariants of the layer loop they were
+  // hoisted out of it and, in the 16-row variant, spilled to scratch; each
+  // reload then waited for all the panel's loads before it (one round trip per
+  // chunk: 8 us more per down panel).
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   v4u q[NC];
   float d[NC];
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
-    const int c = j * kT + threadIdx.x;
+    const int c = j * kT + tid;
     // a chunk past the rows reads past the buffers' ends: zeros, no memory traffic
     const int t = c / cpr, kc = c % cpr;
     const bool in = c < chunks;
@@ -555,7 +562,7 @@ __device__ __forceinline__ void panel_from_q(const int8_t* codes, const float* s
   }
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
-    const int c = j * kT + threadIdx.x;
+    const int c = j * kT + tid;
     if (c < chunks) {
       const int t = c / cpr, kc = c % cpr;
       const int blk = kc >> 1, half = kc & 1, bp = blk >> 1, par = blk & 1;
