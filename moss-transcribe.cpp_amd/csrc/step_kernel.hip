@@ -784,10 +784,14 @@ __device__ __forceinline__ void append_item(const StepParams& P, const LayerDev&
 
 // One attention item: chunk `chunk` of kv head g over the ncol = 2T query
 // columns (col = hl*T + t for q head 2g + hl). LDS: q [32][132], knew/vnew
-// [16][132], sp [32][68].
+// [16][132], sp [32][68]. stage: stage the q rows (the first item of a
+// workgroup; later items of the same kv head find them in LDS), with the new k /
+// v rows if stage_new. next_chunk >= 0: the K / V of that chunk of the same head
+// are loaded into kv once this item's operands are out of it.
 template <int G, int KVH>
 __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& Ly, int T, int past, int g, int chunk,
-                                          uint32_t tag, const KvRegs& kv, uint8_t* lds, bool self_append, bool prof) {
+                                          uint32_t tag, KvRegs& kv, uint8_t* lds, bool self_append, bool prof,
+                                          bool stage, bool stage_new, int next_chunk) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, kl = lane & 15,
             kk = lane >> 4;
   constexpr bool f16kv = KVH != 0;
@@ -803,15 +807,17 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   //    rows come from the tagged q|k|v buffer: no wait for the q|k|v phase's
   //    progress, each value is checked by its tag.
   if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 21); }
-  if (!has_new) {
-    stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol, tag, q_lds, knew, vnew, prof);
-  } else {
-    // q and new k rows are normed and roped; the new v rows are plain copies
-    stage_pass<6 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, tag, q_lds, knew, vnew, prof);
-    if (prof) wmark(P, 1, 14);
-    stage_v<2 * G, KVH>(P, g, T, tag, vnew);
+  if (stage) {
+    if (!stage_new) {
+      stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol, tag, q_lds, knew, vnew, prof);
+    } else {
+      // q and new k rows are normed and roped; the new v rows are plain copies
+      stage_pass<6 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, tag, q_lds, knew, vnew, prof);
+      if (prof) wmark(P, 1, 14);
+      stage_v<2 * G, KVH>(P, g, T, tag, vnew);
+    }
+    bar();
   }
-  bar();
   if (prof) wmark(P, 1, 16);
   // 2. operands: prefetched cache rows (zero from `past` on: the loads' range
   //    ends there), new rows [past, kvlen) from LDS
@@ -839,6 +845,8 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   // stores would wait for them too), so that their acknowledgement overlaps the
   // scores instead of delaying the publish.
   if (appender && self_append) kv_append<KVH>(P, Ly, T, past, g, knew, vnew);
+  // the next chunk's K / V: in flight during this chunk's arithmetic
+  if (next_chunk >= 0) kv_prefetch<KVH>(Ly, P, g, next_chunk * kChunk, past, kv);
   if (has_new) {
     // score operands: the lane's key, all 32 values from one permuted row
     const int key = key0 + 16 * wave + kl;
@@ -868,29 +876,42 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   }
   if (prof) { bar(); wmark(P, 1, 17); }
   // 3. scores S[key][col] = fma chain over head_dim, scaled and masked -> sp
+  // (the G column tiles' chains run interleaved: 2 T <= 16 G columns)
   const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)cHD));
-  for (int ct = 0; ct * 16 < ncol; ++ct) {
-    const int colb = ct * 16 + kl;
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
-    // the column's permuted q row: element 4 s + kk at kk * 32 + s
-    const float* qrow = q_lds + min(colb, ncol - 1) * cQStride + kk * 32;
+  {
+    v4f acc[G];
+    const float* qrow[G];
+#pragma unroll
+    for (int ct = 0; ct < G; ++ct) {
+      acc[ct] = v4f{0.f, 0.f, 0.f, 0.f};
+      // the column's permuted q row: element 4 s + kk at kk * 32 + s
+      qrow[ct] = q_lds + min(ct * 16 + kl, ncol - 1) * cQStride + kk * 32;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const v4f q4 = *(const v4f*)(qrow + 4 * i);
+      v4f q4[G];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float b = colb < ncol ? q4[j] : 0.0f;
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[4 * i + j], b, acc, 0, 0, 0);
-      }
+      for (int ct = 0; ct < G; ++ct) q4[ct] = *(const v4f*)(qrow[ct] + 4 * i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int ct = 0; ct < G; ++ct) {
+          const float b = ct * 16 + kl < ncol ? q4[ct][j] : 0.0f;
+          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[4 * i + j], b, acc[ct], 0, 0, 0);
+        }
     }
-    if (colb < ncol) {
-      const int t = colb % T;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        // key 16 w + 4 kk + q of the chunk sits at sp_pos(key) = q * 16 + 4 w + kk
-        const int kloc = 16 * wave + 4 * kk + q, key = key0 + kloc;
-        sp[colb * cPStride + q * 16 + 4 * wave + kk] =
-            (key < kvlen && key <= past + t) ? __fmul_rn(acc[q], scale) : -INFINITY;
+    for (int ct = 0; ct < G; ++ct) {
+      const int colb = ct * 16 + kl;
+      if (colb < ncol) {
+        const int t = colb % T;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          // key 16 w + 4 kk + q of the chunk sits at sp_pos(key) = q * 16 + 4 w + kk
+          const int kloc = 16 * wave + 4 * kk + q, key = key0 + kloc;
+          sp[colb * cPStride + q * 16 + 4 * wave + kk] =
+              (key < kvlen && key <= past + t) ? __fmul_rn(acc[ct][q], scale) : -INFINITY;
+        }
       }
     }
   }
@@ -955,30 +976,43 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   if (prof) wmark(P, 1, 19);
   // 5. O[col][d] = fma chain over the chunk's keys of p * v
   const Rsrc ro = mk_rsrc(P.part_o + pi * kMaxCols * cHD, kMaxCols * cHD * 4);
-  for (int ct = 0; ct * 16 < ncol; ++ct) {
-    const int cola = ct * 16 + kl;
-    float pa[16];
-    {
+  {
+    // the 2 G chains (column tile, head_dim tile) run interleaved
+    float pa[G][16];
+#pragma unroll
+    for (int ct = 0; ct < G; ++ct) {
+      const int cola = ct * 16 + kl;
       const float* prow = sp + min(cola, ncol - 1) * cPStride + kk * 16;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const v4f p4 = *(const v4f*)(prow + 4 * i);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pa[4 * i + j] = cola < ncol ? p4[j] : 0.0f;
+        for (int j = 0; j < 4; ++j) pa[ct][4 * i + j] = cola < ncol ? p4[j] : 0.0f;
       }
     }
+    v4f acc[G][2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int ct = 0; ct < G; ++ct)
 #pragma unroll
-      for (int s = 0; s < 16; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s], vb[h][s], acc, 0, 0, 0);
-      const int d = 16 * (2 * wave + h) + kl;
+      for (int h = 0; h < 2; ++h) acc[ct][h] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int col = ct * 16 + 4 * kk + q;
-        if (col < ncol) stc1(ro, (uint32_t)((col * cHD + d) * 4), acc[q]);
+    for (int s = 0; s < 16; ++s)
+#pragma unroll
+      for (int ct = 0; ct < G; ++ct)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          acc[ct][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[ct][s], vb[h][s], acc[ct][h], 0, 0, 0);
+#pragma unroll
+    for (int ct = 0; ct < G; ++ct)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int d = 16 * (2 * wave + h) + kl;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = ct * 16 + 4 * kk + q;
+          if (col < ncol) stc1(ro, (uint32_t)((col * cHD + d) * 4), acc[ct][h][q]);
+        }
       }
-    }
   }
   bar();
   if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 20); }
@@ -1329,8 +1363,28 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
 #define RQKVT mk_rsrc(P.qkvt, kMaxRows * cNQKV * 8)
 
   // roles
-  const int first_item = (w + kNwg - 64) % kNwg;  // item i runs on workgroup (i + 64) % 256
-  const bool has_attn = first_item < n_items;
+  // Attention items are (kv head, 64-key chunk). Up to 256 items: item i =
+  // (head i / nch, chunk i % nch) on workgroup (i + 64) % 256. Beyond that, each
+  // kv head has 32 slots of m = ceil(nch / 32) consecutive chunks, slot s =
+  // (head s / 32, chunks m (s % 32) ..) on workgroup (s + 64) % 256: the chunks of
+  // a workgroup share their q rows (staged once) and each chunk's K / V loads are
+  // issued during the previous chunk's arithmetic.
+  const int slot = (w + kNwg - 64) % kNwg;
+  int att_g, att_c0, att_c1;
+  if (n_items <= kNwg) {
+    att_g = slot / nch;
+    att_c0 = slot % nch;
+    att_c1 = att_c0 + 1;
+  } else {
+    const int m = (nch + 31) / 32;
+    att_g = slot / 32;
+    att_c0 = (slot % 32) * m;
+    att_c1 = min(att_c0 + m, nch);
+  }
+  const bool has_attn = n_items <= kNwg ? slot < n_items : att_c0 < nch;
+  // chunks run from the last down: the first one staged holds the new rows if any does
+  const int att_first = att_c1 - 1;
+  const bool att_new = att_c1 * kChunk > past;
   // KV append helpers: when 8 workgroups hold no attention item, workgroup
   // (n_items + 64 + g) mod 256 appends kv head g's new rows
   const bool helpers = n_items + cNKV <= kNwg;
@@ -1396,7 +1450,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   // prefetch layer 0: q|k|v tile and the first attention item's K / V
   wt_load<4>(layer_at(P, 0).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
   if constexpr (G == 1) gain16_load(layer_at(P, 0).attn_norm, gq);
-  if (has_attn) kv_prefetch<KVH>(layer_at(P, 0), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+  if (has_attn) kv_prefetch<KVH>(layer_at(P, 0), P, att_g, att_first * kChunk, past, kv);
 
   for (int l = 0; l < L; ++l) {
     const LayerDev& Ly = layer_at(P, l);
@@ -1423,11 +1477,10 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     if (has_attn) {
       MARK(P, 3 + 12 * l + 2);
       WMARK(P, l, 2);
-      for (int item = first_item; item < n_items; item += kNwg) {
-        if (item != first_item) kv_prefetch<KVH>(Ly, P, item / nch, (item % nch) * kChunk, past, kv);
-        attn_item<G, KVH>(P, Ly, T, past, item / nch, item % nch, c.epoch + ph(l, kPhQkv), kv, lds, !helpers,
-                          PROF && l == 1 && P.timing != nullptr);
-      }
+      for (int ch = att_first; ch >= att_c0; --ch)
+        attn_item<G, KVH>(P, Ly, T, past, att_g, ch, c.epoch + ph(l, kPhQkv), kv, lds, !helpers,
+                          PROF && l == 1 && P.timing != nullptr, ch == att_first, att_new,
+                          ch > att_c0 ? ch - 1 : -1);
       publish(c, next_done(l, kPhAttn));
       MARK(P, 3 + 12 * l + 3);
       WMARK(P, l, 3);
@@ -1461,7 +1514,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
         if constexpr (G == 1) gain16_load(Ln.attn_norm, gq);
-        if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+        if (has_attn) kv_prefetch<KVH>(Ln, P, att_g, att_first * kChunk, past, kv);
       }
     }
     // ---- O-proj: x += W_o o ----
@@ -1488,7 +1541,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
         wt_load<4>(layer_at(P, l + 1).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
         if constexpr (G == 1) gain16_load(layer_at(P, l + 1).attn_norm, gq);
         if (has_attn)
-          kv_prefetch<KVH>(layer_at(P, l + 1), P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+          kv_prefetch<KVH>(layer_at(P, l + 1), P, att_g, att_first * kChunk, past, kv);
       }
     }
     // ---- GATE/UP: act = silu(g) * u, as q8_0 blocks ----
@@ -1509,7 +1562,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
         if constexpr (G == 1) gain16_load(Ln.attn_norm, gq);
-        if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+        if (has_attn) kv_prefetch<KVH>(Ln, P, att_g, att_first * kChunk, past, kv);
       }
     }
     // ---- DOWN: x += W_d act ----
@@ -1533,7 +1586,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       const LayerDev& Ln = layer_at(P, l + 1);
       wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
       if constexpr (G == 1) gain16_load(Ln.attn_norm, gq);
-      if (has_attn) kv_prefetch<KVH>(Ln, P, first_item / nch, (first_item % nch) * kChunk, past, kv);
+      if (has_attn) kv_prefetch<KVH>(Ln, P, att_g, att_first * kChunk, past, kv);
     }
   }
 

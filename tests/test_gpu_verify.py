@@ -225,6 +225,48 @@ def test_long_f16_context_matches_oracle(wtype, exec_mode):
         assert np.array_equal(c1, c0) and m1 == m0
 
 
+# (cached prefix, T, KV type): more than 32 chunks of 64 keys per kv head, so each
+# workgroup of the step kernel's attention walks 2 or 4 chunks of one head with the
+# q rows staged once. The new rows lie in one chunk (2050 + 16), straddle two
+# chunks on two workgroups (2040 + 16: chunks 31 | 32) or two chunks of one
+# workgroup (4030 + 9: chunks 62, 63), or end a 97-chunk context (6200 + 4).
+CHUNK_GROUPS = [(2050, 16, mtg.TYPE_F32), (2040, 16, mtg.TYPE_F16), (4030, 9, mtg.TYPE_F16),
+                (6200, 4, mtg.TYPE_F32), (3000, 1, mtg.TYPE_F16)]
+
+
+@pytest.mark.parametrize("case", CHUNK_GROUPS, ids=["%d+%d-%s" % (p, t, "f32" if k == mtg.TYPE_F32 else "f16")
+                                                    for p, t, k in CHUNK_GROUPS])
+def test_step_kernel_chunk_groups_match_oracle(case):
+    prefix, T, kv = case
+    print("step kernel, chunk groups: prefix %d, T=%d, kv %d" % case, flush=True)
+    model = mtg.SynthModel(mtg.TYPE_Q8_0, seed=13, std=0.02, gain_jitter=0.05, n_layers=2, vocab=4096)
+    hp = model.hp
+    max_seq = prefix + 2 * T + 8
+    orc = oracle_py.Oracle(model, max_seq, kv)
+    dec = mtg.Decoder(model, max_seq, kv)
+    dec.set_exec(mtg.EXEC_STEP_KERNEL)
+    rng = np.random.default_rng(prefix + T)
+    dt = np.float32 if kv == mtg.TYPE_F32 else np.float16
+    shape = (hp.n_layers, hp.n_kv_heads, prefix, hp.head_dim)
+    k = rng.normal(0.0, 1.0, shape).astype(dt)
+    v = rng.normal(0.0, 0.5, shape).astype(dt)
+    orc.kv_write(k, v)
+    dec.kv_write(k, v)
+    for step in range(2):
+        tokens = rng.integers(0, hp.vocab, T)
+        c0, m0, h0, l0 = orc.verify(tokens, want_hidden=True, want_logits=True)
+        c1, m1, h1, l1 = dec.verify(tokens, want_hidden=True, want_logits=True)
+        _close(h1, h0, "hidden, step %d" % step)
+        _close(l1, l0, "logits, step %d" % step)
+        assert np.array_equal(c1, c0) and m1 == m0
+    n = dec.past_len
+    assert n == orc.past_len
+    k0, v0 = orc.kv_read(n)
+    k1, v1 = dec.kv_read(n)
+    _close(k1[:, :, prefix:], k0[:, :, prefix:], "K cache (new rows)")
+    _close(v1[:, :, prefix:], v0[:, :, prefix:], "V cache (new rows)")
+
+
 @pytest.mark.parametrize("wtype", WTYPES, ids=lambda w: WT_NAMES[w])
 def test_f16_and_q4k_weights_penalty_prefill_and_stream(wtype):
     """The same weight types through the GPU prefill, the repetition penalty and
