@@ -577,57 +577,69 @@ __device__ __forceinline__ void panel_from_q(const int8_t* codes, const float* s
 }
 
 // ------------------------------------------------------------ attention -----
-// K and V of one 64-key chunk in MFMA operand layout. Wave w: scores of keys
-// 16w + (lane % 16), k-index lane / 16 (kreg[s] = K[key][4s + lane/16]); P.V for
-// head_dim tiles 2w and 2w+1 (vreg[h][s] = V[4s + lane/16][16(2w+h) + lane%16]).
-// Raw cache bits (f32, or f16 in the low half), zero outside [0, past).
+// K and V of one 64-key chunk, raw cache bytes in 16-byte pieces: piece p =
+// j * 256 + thread (j < NP) is bytes 16 p .. 16 p + 15 of the chunk's rows, K
+// pieces first, then V (NP = 8 for an f32 cache, 4 for f16). Coalesced: a wave's
+// load covers 1 KB of consecutive rows. (Loading the MFMA operand layout
+// directly, an element per lane and load, made every load touch 16 cache lines:
+// the address unit, not the memory, then set the time.) Zero from row `past`
+// on: the loads' range ends there.
 struct KvRegs {
-  uint32_t k[32];
-  uint32_t v[2][16];
+  v4u p[16];
 };
 
 template <int KVH>
 __device__ __forceinline__ void kv_prefetch(const LayerDev& Ly, const StepParams& P, int g, int key0,
                                             int past, KvRegs& r) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63, kl = lane & 15, kk = lane >> 4;
-  constexpr int es = KVH ? 2 : 4;
-  // The kv head's rows [0, past). Every key-dependent part of an address is in
-  // the per-lane offset (the scalar offset is 0), so a key >= past lies beyond
-  // num_records and its load returns 0 without touching memory.
+  constexpr int es = KVH ? 2 : 4, NP = KVH ? 4 : 8;
   const size_t head = (size_t)g * P.max_seq * cHD * es;
   const Rsrc rk = mk_rsrc(Ly.kc + head, (uint32_t)(past * cHD * es));
   const Rsrc rv = mk_rsrc(Ly.vc + head, (uint32_t)(past * cHD * es));
-  // K: lane (kl, kk) of wave w holds K[key0 + 16w + kl][4s + kk]
-  const int kvo = ((key0 + 16 * wave + kl) * cHD + kk) * es;
-  // V: vreg[h][s] = V[key0 + 4s + kk][16(2w + h) + kl]
-  const int vvo = ((key0 + kk) * cHD + 32 * wave + kl) * es;
-  if constexpr (KVH) {
+  // the whole offset per lane (scalar offset 0): a piece at or past `past` lies
+  // beyond num_records and reads 0 without touching memory
+  const uint32_t o0 = (uint32_t)(key0 * cHD * es) + 16u * threadIdx.x;
 #pragma unroll
-    for (int s = 0; s < 32; ++s) r.k[s] = __builtin_amdgcn_raw_buffer_load_b16(rk, kvo + 4 * s * 2, 0, 0);
+  for (int j = 0; j < NP; ++j) {
+    r.p[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, o0 + 16u * kT * j, 0, 0);
+    r.p[NP + j] = __builtin_amdgcn_raw_buffer_load_b128(rv, o0 + 16u * kT * j, 0, 0);
+  }
+}
+
+// LDS rows of the chunk's K and V as f32, padded so that the operand reads of
+// attn_item are free of bank conflicts: K row key at key * kKStride, V row at
+// key * kVStride.
+constexpr int kKStride = cHD + 4, kVStride = cHD + 16;
+constexpr int kKvLdsFloats = kChunk * (kKStride + kVStride);
+
+template <int KVH>
+__device__ __forceinline__ void kv_to_lds(const KvRegs& r, float* ks, float* vs) {
+  constexpr int NP = KVH ? 4 : 8;
 #pragma unroll
-    for (int s = 0; s < 16; ++s)
+  for (int j = 0; j < NP; ++j) {
+    const int p = j * kT + threadIdx.x;
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        r.v[h][s] = __builtin_amdgcn_raw_buffer_load_b16(rv, vvo + (4 * s * cHD + 16 * h) * 2, 0, 0);
-  } else {
-#pragma unroll
-    for (int s = 0; s < 32; ++s) r.k[s] = __builtin_amdgcn_raw_buffer_load_b32(rk, kvo + 4 * s * 4, 0, 0);
-#pragma unroll
-    for (int s = 0; s < 16; ++s)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        r.v[h][s] = __builtin_amdgcn_raw_buffer_load_b32(rv, vvo + (4 * s * cHD + 16 * h) * 4, 0, 0);
+    for (int t = 0; t < 2; ++t) {
+      const v4u q = r.p[t * NP + j];
+      float* base = t == 0 ? ks : vs;
+      const int stride = t == 0 ? kKStride : kVStride;
+      if constexpr (KVH != 0) {  // 8 halves: elements 8 (p % 16) .. of row p / 16
+        float* d = base + (p / 16) * stride + 8 * (p % 16);
+        const v4f lo = {half_bits_to_float((uint16_t)q.x), half_bits_to_float((uint16_t)(q.x >> 16)),
+                        half_bits_to_float((uint16_t)q.y), half_bits_to_float((uint16_t)(q.y >> 16))};
+        const v4f hi = {half_bits_to_float((uint16_t)q.z), half_bits_to_float((uint16_t)(q.z >> 16)),
+                        half_bits_to_float((uint16_t)q.w), half_bits_to_float((uint16_t)(q.w >> 16))};
+        *(v4f*)d = lo;
+        *(v4f*)(d + 4) = hi;
+      } else {  // 4 floats: elements 4 (p % 32) .. of row p / 32
+        *(v4u*)(base + (p / 32) * stride + 4 * (p % 32)) = q;
+      }
+    }
   }
 }
 
 // two floats as f16 bits (round to nearest even), the first in the low half
 __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
   return (uint32_t)__half_as_ushort(__float2half_rn(a)) | ((uint32_t)__half_as_ushort(__float2half_rn(b)) << 16);
-}
-
-__device__ __forceinline__ float kv_val(uint32_t bits, bool f16) {
-  return f16 ? half_bits_to_float((uint16_t)bits) : __uint_as_float(bits);
 }
 
 // One staging pass of an attention item: wave `wave` takes rows r0 + 4 j,
@@ -784,7 +796,7 @@ __device__ __forceinline__ void append_item(const StepParams& P, const LayerDev&
 
 // One attention item: chunk `chunk` of kv head g over the ncol = 2T query
 // columns (col = hl*T + t for q head 2g + hl). LDS: q [32][132], knew/vnew
-// [16][132], sp [32][68]. stage: stage the q rows (the first item of a
+// [16][132], sp [32][68], the chunk's K [64][132] and V [64][144]. stage: stage the q rows (the first item of a
 // workgroup; later items of the same kv head find them in LDS), with the new k /
 // v rows if stage_new. next_chunk >= 0: the K / V of that chunk of the same head
 // are loaded into kv once this item's operands are out of it.
@@ -800,6 +812,8 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   float* knew = q_lds + kMaxCols * cQStride;
   float* vnew = knew + kMaxRows * cQStride;
   float* sp = vnew + kMaxRows * cQStride;
+  float* ks = sp + kMaxCols * cPStride;
+  float* vs = ks + kChunk * kKStride;
   const bool has_new = key0 + kChunk > past;
   const bool appender = key0 <= past && past < key0 + kChunk;
   // 1. stage the roped q rows and, if this chunk reaches them, the new k / v rows
@@ -807,6 +821,9 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   //    rows come from the tagged q|k|v buffer: no wait for the q|k|v phase's
   //    progress, each value is checked by its tag.
   if (prof) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); bar(); wmark(P, 1, 21); }
+  // this chunk's K / V into the LDS rows (ordered before the operand reads by
+  // the barrier below)
+  kv_to_lds<KVH>(kv, ks, vs);
   if (stage) {
     if (!stage_new) {
       stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol, tag, q_lds, knew, vnew, prof);
@@ -816,37 +833,27 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
       if (prof) wmark(P, 1, 14);
       stage_v<2 * G, KVH>(P, g, T, tag, vnew);
     }
-    bar();
   }
+  bar();
   if (prof) wmark(P, 1, 16);
-  // 2. operands: prefetched cache rows (zero from `past` on: the loads' range
-  //    ends there), new rows [past, kvlen) from LDS
-  float ka[32], vb[2][16];
-#pragma unroll
-  for (int s = 0; s < 32; ++s) ka[s] = kv_val(kv.k[s], f16kv);
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int s = 0; s < 16; ++s) vb[h][s] = kv_val(kv.v[h][s], f16kv);
-  // a use of every operand register here makes the compiler wait for their loads
-  // before the stores below (the staging's loads, issued later, are complete, so
-  // this costs nothing); otherwise its first wait would come after the stores
-  // and would have to wait for them
-#pragma unroll
-  for (int s = 0; s < 32; ++s) asm volatile("" ::"v"(ka[s]));
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int s = 0; s < 16; ++s) asm volatile("" ::"v"(vb[h][s]));
-  // Without a helper workgroup (every workgroup holds attention items), the
-  // appending item writes this step's k / v rows to the KV cache from the staged
-  // rows (for an f16 cache they are f16 values already). Issued after the
-  // prefetched K / V are in registers (a wait for a load issued before these
-  // stores would wait for them too), so that their acknowledgement overlaps the
-  // scores instead of delaying the publish.
-  if (appender && self_append) kv_append<KVH>(P, Ly, T, past, g, knew, vnew);
   // the next chunk's K / V: in flight during this chunk's arithmetic
   if (next_chunk >= 0) kv_prefetch<KVH>(Ly, P, g, next_chunk * kChunk, past, kv);
+  // 2. operands: cache rows from the LDS rows (zero from `past` on), new rows
+  //    [past, kvlen) from the staged rows. Lane (kl, kk) of wave w: K[16 w + kl]
+  //    [4 s + kk] (s < 32) for the scores, V[4 s + kk][16 (2 w + h) + kl] (s < 16)
+  //    for P.V.
+  float ka[32], vb[2][16];
+#pragma unroll
+  for (int s = 0; s < 32; ++s) ka[s] = ks[(16 * wave + kl) * kKStride + 4 * s + kk];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int s = 0; s < 16; ++s) vb[h][s] = vs[(4 * s + kk) * kVStride + 16 * (2 * wave + h) + kl];
+  // Without a helper workgroup (every workgroup holds attention items), the
+  // appending item writes this step's k / v rows to the KV cache from the staged
+  // rows (for an f16 cache they are f16 values already); their acknowledgement
+  // overlaps the scores instead of delaying the publish.
+  if (appender && self_append) kv_append<KVH>(P, Ly, T, past, g, knew, vnew);
   if (has_new) {
     // score operands: the lane's key, all 32 values from one permuted row
     const int key = key0 + 16 * wave + kl;
@@ -1305,11 +1312,11 @@ constexpr size_t kRedBytes = (size_t)4 * 4 * 4 * 64 * 4 + 4 * 16 * 4;
 // LDS: the GEMM panel + reduction space, or the attention's q / new rows /
 // probabilities (the phases reuse it), then the residual columns of the o-proj /
 // down tile ([8G rows][16], kept across phases).
+constexpr size_t kAttnLdsBytes =
+    ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride + kKvLdsFloats) * 4;
 __host__ __device__ constexpr size_t step_lds_x_offset(int G) {
-  return ((size_t)G * cBF * (1024 + 64) + kRedBytes * G >
-          ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride) * 4)
-             ? (size_t)G * cBF * (1024 + 64) + kRedBytes * G
-             : ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride) * 4;
+  return ((size_t)G * cBF * (1024 + 64) + kRedBytes * G > kAttnLdsBytes) ? (size_t)G * cBF * (1024 + 64) + kRedBytes * G
+                                                                         : kAttnLdsBytes;
 }
 // after the residual columns: each wave's row image for the norm panel (8-row
 // variant only)
@@ -1479,7 +1486,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       WMARK(P, l, 2);
       for (int ch = att_first; ch >= att_c0; --ch)
         attn_item<G, KVH>(P, Ly, T, past, att_g, ch, c.epoch + ph(l, kPhQkv), kv, lds, !helpers,
-                          PROF && l == 1 && P.timing != nullptr, ch == att_first, att_new,
+                          PROF && l == 1 && P.timing != nullptr && ch == att_first, ch == att_first, att_new,
                           ch > att_c0 ? ch - 1 : -1);
       publish(c, next_done(l, kPhAttn));
       MARK(P, 3 + 12 * l + 3);
