@@ -85,16 +85,20 @@ k_act_f16(const StepDesc* __restrict__ desc, const float* __restrict__ src, int 
 // 256-thread workgroup: the element of largest magnitude (the first one on ties)
 // gives max with its sign, iscale = -127/max, codes = min(127, nearest(iscale*x)),
 // d = 1/iscale, bsums over 16-element groups.
+// Threads 0..255 hold the block; in a larger workgroup the others pass the
+// barrier only.
 __device__ __forceinline__ void q8k_block256(float y, const ActQ8K& a, int t, int K, int b) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const bool active = tid < 256;
   __shared__ float s_y[256];
   __shared__ uint64_t s_key[4];
-  s_y[tid] = y;
+  if (active) s_y[tid] = y;
   // first maximum of |y|: larger magnitude, then lower index
   const uint64_t key = ((uint64_t)__float_as_uint(fabsf(y)) << 32) | (uint32_t)(255 - tid);
   const uint64_t wk = wave_max_u64(key);
-  if (lane == 0) s_key[wave] = wk;
+  if (active && lane == 0) s_key[wave] = wk;
   __syncthreads();
+  if (!active) return;
   uint64_t best = s_key[0];
   for (int w = 1; w < 4; ++w) best = s_key[w] > best ? s_key[w] : best;
   const float maxv = s_y[255 - (int)(best & 0xffffffffu)];
@@ -140,64 +144,99 @@ k_act_q8k(const StepDesc* __restrict__ desc, const float* __restrict__ src, int 
 // ------------------------------------------------- attention merge + act ---
 // The chunk merge of the attention output (attn_merge's arithmetic: M = max of
 // the chunk maxima, then the chunk-ordered chains L = fma(l_c, f_c, L) and
-// O = fma(o_c, f_c, O), f_c = exp(m_c - M), out = O / L) with the loads of 64
-// chunks in flight per thread, fused with the conversion of the row to the
-// o-projection's vec_dot_type. Grid (n_heads / 2, 16 rows), 256 threads: thread
-// (hl, d) = (tid / 128, tid % 128) takes head 2 blockIdx.x + hl, so one
-// workgroup holds one q8_K block (256 elements) of the row.
-__device__ __forceinline__ float attn_merge64(const float* part_ml, const float* part_o, int nch,
-                                              size_t stride_ml, size_t stride_o, int d) {
-  const int lane = threadIdx.x & 63;
-  float M = -INFINITY;
-  for (int c0 = 0; c0 < nch; c0 += 256) {
-    float m[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = c0 + 64 * r + lane;
-      m[r] = c < nch ? part_ml[(size_t)c * stride_ml] : -INFINITY;
-    }
-    M = fmaxf(M, wave_max_f(fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]))));
-  }
-  float L = 0.0f, O = 0.0f;
-  for (int c0 = 0; c0 < nch; c0 += 64) {
-    const int c = c0 + lane, nb = min(64, nch - c0);
-    const float m = c < nch ? part_ml[(size_t)c * stride_ml] : -INFINITY;
-    const float l = c < nch ? part_ml[(size_t)c * stride_ml + 1] : 0.0f;
-    float o[64];
-#pragma unroll
-    for (int i = 0; i < 64; ++i) o[i] = i < nb ? part_o[(size_t)(c0 + i) * stride_o + d] : 0.0f;
-    const float f = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, M));
-#pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      const float mc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), i));
-      if (i < nb && mc != -INFINITY) {
-        const float fc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), i));
-        const float lc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), i));
-        L = fmaf(lc, fc, L);
-        O = fmaf(o[i], fc, O);
-      }
-    }
-  }
-  return __fdiv_rn(O, L);
-}
+// O = fma(o_c, f_c, O), f_c = exp(m_c - M), out = O / L), fused with the
+// conversion of the row to the o-projection's vec_dot_type. Grid (n_heads / 2,
+// 16 rows), kCombSeg x 256 threads: thread (seg, hl, d) = (tid / 256, tid / 128
+// % 2, tid % 128) takes q head 2 blockIdx.x + hl, element d, and the chunks of
+// segment seg. Every segment's partials are loaded at once (one round trip for
+// up to kCombPass chunks); the chains then run segment after segment, each
+// continuing from the previous one's (L, O) in LDS, so the order stays the
+// chunk order. A fully masked chunk (m = -inf) has f = 0, l = 0 and O = 0: its
+// fma terms add exact zeros.
+constexpr int kCombSeg = 4, kCombPer = 80, kCombPass = kCombSeg * kCombPer;
 
 template <int WT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256 * kCombSeg)
 k_attn_combine_wt(const StepDesc* __restrict__ desc, AttnWork work, int n_heads, int max_chunks, WtAct act) {
-  const int g = blockIdx.x, t = blockIdx.y, hl = threadIdx.x >> 7, d = threadIdx.x & 127;
+  const int g = blockIdx.x, t = blockIdx.y;
+  const int seg = threadIdx.x >> 8, tid = threadIdx.x & 255, hl = tid >> 7, d = tid & 127, lane = tid & 63;
   const int T = desc->T;
   if (t >= T) return;
   const int col = hl * T + t;  // q head 2 g + hl shares kv head g
   const int nch = (desc->past + T + kChunk - 1) / kChunk;
+  constexpr uint32_t so = kMaxCols * kHeadDim * 4, sml = kMaxCols * 2 * 4;  // bytes per chunk
   const size_t item0 = (size_t)g * max_chunks;
-  const float val = attn_merge64(work.part_ml + item0 * kMaxCols * 2 + col * 2,
-                                 work.part_o + item0 * kMaxCols * kHeadDim + col * kHeadDim, nch,
-                                 (size_t)kMaxCols * 2, (size_t)kMaxCols * kHeadDim, d);
+  // a chunk >= nch reads past num_records: zeros, no memory traffic
+  const auto ro = __builtin_amdgcn_make_buffer_rsrc(work.part_o + item0 * kMaxCols * kHeadDim, 0,
+                                                    (int)(nch * so), 0x00020000);
+  const auto rml = __builtin_amdgcn_make_buffer_rsrc(work.part_ml + item0 * kMaxCols * 2, 0, (int)(nch * sml),
+                                                     0x00020000);
+  __shared__ float s_f[2][kCombPass], s_l[2][kCombPass];
+  __shared__ float s_L[256], s_O[256];
+  // waves 0 and 2 (segment 0, d < 64) compute M and the chunk factors of q head hl
+  const bool factors = seg == 0 && d < 64;
+  float M = -INFINITY;
+  if (factors)
+    for (int c0 = 0; c0 < nch; c0 += 64) {
+      const float m = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rml, (c0 + lane) * sml + col * 8, 0, 0));
+      M = fmaxf(M, wave_max_f(c0 + lane < nch ? m : -INFINITY));
+    }
+  float L = 0.0f, O = 0.0f;
+  for (int p0 = 0; p0 < nch; p0 += kCombPass) {
+    const int c_lo = p0 + seg * kCombPer;
+    float o[kCombPer];
+#pragma unroll
+    for (int i = 0; i < kCombPer; ++i)
+      o[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           ro, (uint32_t)(c_lo + i) * so + (col * kHeadDim + d) * 4, 0, 0));
+    if (factors)
+      for (int c = lane; c < kCombPass; c += 64) {
+        const uint32_t off = (uint32_t)(p0 + c) * sml + col * 8;
+        const bool in = p0 + c < nch;
+        const float m = in ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rml, off, 0, 0))
+                           : -INFINITY;
+        const float l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rml, off + 4, 0, 0));
+        s_f[hl][c] = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, M));
+        s_l[hl][c] = in ? l : 0.0f;
+      }
+    __syncthreads();
+    for (int sg = 0; sg < kCombSeg; ++sg) {
+      if (seg == sg) {
+        if (sg > 0 || p0 > 0) {
+          L = s_L[tid];
+          O = s_O[tid];
+        }
+        // groups of 4 chunks up to the last one; the chunks past nch in the last
+        // group have f = l = o = 0 (exact zero terms)
+        const int n = nch - c_lo;
+        if (n > 0) {
+#pragma unroll
+          for (int i = 0; i < kCombPer; i += 4) {
+            if (i < n) {
+              const v4f f4 = *(const v4f*)&s_f[hl][seg * kCombPer + i];
+              const v4f l4 = *(const v4f*)&s_l[hl][seg * kCombPer + i];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                L = fmaf(l4[j], f4[j], L);
+                O = fmaf(o[i + j], f4[j], O);
+              }
+            }
+          }
+          s_L[tid] = L;
+          s_O[tid] = O;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const float val = __fdiv_rn(s_O[tid], s_L[tid]);
   const int QN = n_heads * kHeadDim;
-  if constexpr (WT == MTG_TYPE_F16)
-    act.f16h[(size_t)t * QN + g * 256 + threadIdx.x] = __half_as_ushort(__float2half_rn(val));
-  else
+  if constexpr (WT == MTG_TYPE_F16) {
+    if (seg == 0) act.f16h[(size_t)t * QN + g * 256 + tid] = __half_as_ushort(__float2half_rn(val));
+  } else {
     q8k_block256(val, act.q8k, t, QN, g);
+  }
 }
 
 // ------------------------------------------------------------ row dots ----
@@ -1162,13 +1201,11 @@ void launch_act_wt(hipStream_t s, int wtype, const StepDesc* desc, const float* 
 
 void launch_attn_combine_wt(hipStream_t s, int wtype, const StepDesc* desc, AttnWork work, int n_heads,
                             int max_chunks, const WtAct& act) {
-  const dim3 grid(n_heads / 2, kMaxRows);
+  const dim3 grid(n_heads / 2, kMaxRows), block(256 * kCombSeg);
   if (wtype == MTG_TYPE_F16)
-    hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_F16>, grid, dim3(256), 0, s, desc, work, n_heads, max_chunks,
-                       act);
+    hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_F16>, grid, block, 0, s, desc, work, n_heads, max_chunks, act);
   else
-    hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_Q4_K>, grid, dim3(256), 0, s, desc, work, n_heads, max_chunks,
-                       act);
+    hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_Q4_K>, grid, block, 0, s, desc, work, n_heads, max_chunks, act);
 }
 
 void launch_gemm_wt(hipStream_t s, int wtype, int epi, const StepDesc* desc, const uint8_t* w,
