@@ -836,8 +836,6 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   }
   bar();
   if (prof) wmark(P, 1, 16);
-  // the next chunk's K / V: in flight during this chunk's arithmetic
-  if (next_chunk >= 0) kv_prefetch<KVH>(Ly, P, g, next_chunk * kChunk, past, kv);
   // 2. operands: cache rows from the LDS rows (zero from `past` on), new rows
   //    [past, kvlen) from the staged rows. Lane (kl, kk) of wave w: K[16 w + kl]
   //    [4 s + kk] (s < 32) for the scores, V[4 s + kk][16 (2 w + h) + kl] (s < 16)
@@ -881,6 +879,11 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
       }
     }
   }
+  // the next chunk's K / V: in flight during this chunk's arithmetic. Issued
+  // after the operand reads: a wait that the compiler puts before writes of
+  // registers (conservative where earlier loads wrote them) would otherwise wait
+  // for these loads too.
+  if (next_chunk >= 0) kv_prefetch<KVH>(Ly, P, g, next_chunk * kChunk, past, kv);
   if (prof) { bar(); wmark(P, 1, 17); }
   // 3. scores S[key][col] = fma chain over head_dim, scaled and masked -> sp
   // (the G column tiles' chains run interleaved: 2 T <= 16 G columns)
@@ -1112,9 +1115,9 @@ __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, 
 }
 
 // ---------------------------------------------------------------- lm_head ---
-// Wave-strided tiles of the tied embedding; block pairs stream through an
-// 8-deep register ring; per tile the canonical 4-slice sums, the penalty and
-// 64-bit first-max keys.
+// Wave-strided tiles of the tied embedding; a tile's 16 block pairs stream
+// through a register ring one tile ahead; per tile the canonical 4-slice sums,
+// the penalty and 64-bit first-max keys.
 template <int G>
 __device__ __forceinline__ void lm_head(const StepParams& P, float penalty, bool write_logits, int T,
                                         const uint8_t* pcodes, const float* pscales, uint64_t* s_best) {
@@ -1140,100 +1143,91 @@ __device__ __forceinline__ void lm_head(const StepParams& P, float penalty, bool
 #pragma unroll
   for (int cg = 0; cg < G; ++cg) best[cg] = 0;
   const int my_tiles = gw < n_tiles ? (n_tiles - 1 - gw) / nwaves + 1 : 0;
-  const int units = my_tiles * cBH;  // (tile, pair) units of this wave, in order
-  constexpr int R = 16;  // units of loads in flight per wave
-  v4i ra[R];
-  uint2 rs[R];
+  // The activation panel is the same for every tile: its operands stay in
+  // registers (no LDS read, and no LDS latency, per unit).
+  v4i pb[cBH][G];
+  float pdx[cBH][G];
+#pragma unroll
+  for (int bp = 0; bp < cBH; ++bp)
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg) {
+      pb[bp][cg] = *(const v4i*)(pcodes + ((size_t)(cg * cBH + bp)) * 1024 + lane * 16);
+      pdx[bp][cg] = pscales[(size_t)(cg * cBH + bp) * 16 + (lane & 15)];
+    }
+  // A ring of one tile of loads in flight per wave: slot bp holds block pair bp
+  // of the tile being computed and is refilled with block pair bp of the next
+  // tile. Past this wave's last tile a load gets a per-lane offset past the
+  // buffer's end (the range check covers the per-lane offset, not the scalar
+  // one): zeros, no memory traffic, never used.
+  v4i ra[cBH];
+  uint2 rs[cBH];
   const Rsrc re = mk_rsrc(uniform_ptr(P.embd), (uint32_t)((size_t)n_tiles * cBH * kUnitBytes));
-  // Every slot is refilled unconditionally, so each ring slot keeps its registers
-  // and only its own load is waited for. A unit past this wave's last one gets
-  // a per-lane offset past the buffer's end (the range check covers the per-lane
-  // offset, not the scalar one): zeros, no memory traffic, never used.
-  auto issue = [&](int u, int slot) {
-    const bool in = u < units;
-    const int tile = gw + (u / cBH) * nwaves, bp = u % cBH;
-    const int so = in ? (tile * cBH + bp) * kUnitBytes : 0;
+  auto issue = [&](int ti, int bp) {
+    const bool in = ti < my_tiles;
+    const int so = in ? ((gw + ti * nwaves) * cBH + bp) * kUnitBytes : 0;
     const uint32_t gone = 0x80000000u;
-    ra[slot] = __builtin_bit_cast(
+    ra[bp] = __builtin_bit_cast(
         v4i, __builtin_amdgcn_raw_buffer_load_b128(re, in ? (uint32_t)(lane * 16) : gone, so, 2));
     const v2u sv = __builtin_amdgcn_raw_buffer_load_b64(re, in ? (uint32_t)(1024 + srow * 2) : gone, so, 2);
-    rs[slot] = make_uint2(sv.x, sv.y);
+    rs[bp] = make_uint2(sv.x, sv.y);
   };
 #pragma unroll
-  for (int i = 0; i < R; ++i) issue(i, i);
-  float part[4][G][4];
-  // A pass of R units may end inside a tile; the last pass stops at this wave's
-  // last unit (units is wave-uniform, so the whole wave leaves together).
-  for (int u0 = 0; u0 < units; u0 += R) {
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const int u = u0 + i;
-      if (u >= units) break;
-      const int bp = u % cBH, sl = bp >> 2;
-      if (bp == 0) {
-        if (pen) {
-          const int tile = gw + (u / cBH) * nwaves;
-#pragma unroll
-          for (int cg = 0; cg < G; ++cg) {
-            const int t = min(cg * 8 + (lane & 7), T - 1);
-            pword[cg] = __builtin_amdgcn_raw_buffer_load_b32(rb, (t * words + (tile >> 1)) * 4, 0, 16);
-          }
-        }
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-          for (int cg = 0; cg < G; ++cg)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) part[a][cg][q] = 0.0f;
-      }
-      float dw[4];
-      dw[0] = half_bits_to_float((uint16_t)(rs[i].x & 0xffff));
-      dw[1] = half_bits_to_float((uint16_t)(rs[i].x >> 16));
-      dw[2] = half_bits_to_float((uint16_t)(rs[i].y & 0xffff));
-      dw[3] = half_bits_to_float((uint16_t)(rs[i].y >> 16));
-      const v4i a = ra[i];
-      issue(u + R, i);
+  for (int bp = 0; bp < cBH; ++bp) issue(0, bp);
+  for (int ti = 0; ti < my_tiles; ++ti) {
+    const int tile = gw + ti * nwaves;
+    if (pen) {
 #pragma unroll
       for (int cg = 0; cg < G; ++cg) {
-        const v4i b = *(const v4i*)(pcodes + ((size_t)(cg * cBH + bp)) * 1024 + lane * 16);
-        const float dx = pscales[(size_t)(cg * cBH + bp) * 16 + (lane & 15)];
-        const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, zero, 0, 0, 0);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          // the slice index is wave-uniform: select without dynamic indexing
-          const float add = dw[q] * dx;
-          if (sl == 0) part[0][cg][q] = fmaf((float)c[q], add, part[0][cg][q]);
-          else if (sl == 1) part[1][cg][q] = fmaf((float)c[q], add, part[1][cg][q]);
-          else if (sl == 2) part[2][cg][q] = fmaf((float)c[q], add, part[2][cg][q]);
-          else part[3][cg][q] = fmaf((float)c[q], add, part[3][cg][q]);
-        }
+        const int t = min(cg * 8 + (lane & 7), T - 1);
+        pword[cg] = __builtin_amdgcn_raw_buffer_load_b32(rb, (t * words + (tile >> 1)) * 4, 0, 16);
       }
-      if (bp == cBH - 1) {
-        const int tile = gw + (u / cBH) * nwaves;
+    }
+    float part[4][G][4];
 #pragma unroll
-        for (int cg = 0; cg < G; ++cg)
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) part[a][cg][q] = 0.0f;
+#pragma unroll
+    for (int bp = 0; bp < cBH; ++bp) {
+      const int sl = bp >> 2;  // the K slice of this block pair
+      float dw[4];
+      dw[0] = half_bits_to_float((uint16_t)(rs[bp].x & 0xffff));
+      dw[1] = half_bits_to_float((uint16_t)(rs[bp].x >> 16));
+      dw[2] = half_bits_to_float((uint16_t)(rs[bp].y & 0xffff));
+      dw[3] = half_bits_to_float((uint16_t)(rs[bp].y >> 16));
+      const v4i a = ra[bp];
+      issue(ti + 1, bp);
+#pragma unroll
+      for (int cg = 0; cg < G; ++cg) {
+        const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, pb[bp][cg], zero, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) part[sl][cg][q] = fmaf((float)c[q], dw[q] * pdx[bp][cg], part[sl][cg][q]);
+      }
+    }
+#pragma unroll
+    for (int cg = 0; cg < G; ++cg)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v = __fadd_rn(__fadd_rn(__fadd_rn(part[0][cg][q], part[1][cg][q]), part[2][cg][q]), part[3][cg][q]);
+        v = __fadd_rn(v, dpp_f<kDppRor8>(v));
+        part[0][cg][q] = v;
+      }
+    if ((lane & 15) < 8) {
+#pragma unroll
+      for (int cg = 0; cg < G; ++cg) {
+        const int t = cg * 8 + (lane & 7);
+        if (t < T) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            float v = __fadd_rn(__fadd_rn(__fadd_rn(part[0][cg][q], part[1][cg][q]), part[2][cg][q]), part[3][cg][q]);
-            v = __fadd_rn(v, dpp_f<kDppRor8>(v));
-            part[0][cg][q] = v;
-          }
-        if ((lane & 15) < 8) {
-#pragma unroll
-          for (int cg = 0; cg < G; ++cg) {
-            const int t = cg * 8 + (lane & 7);
-            if (t < T) {
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const int row = tile * 16 + 4 * (lane >> 4) + q;
-                float v = part[0][cg][q];
-                if (write_logits) gst<float>(logits + (size_t)t * V + row, v);
-                if (pen && ((pword[cg] >> (row & 31)) & 1u))
-                  v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
-                const uint64_t key = argmax_key(v, row);
-                best[cg] = key > best[cg] ? key : best[cg];
-              }
-            }
+            const int row = tile * 16 + 4 * (lane >> 4) + q;
+            float v = part[0][cg][q];
+            if (write_logits) gst<float>(logits + (size_t)t * V + row, v);
+            if (pen && ((pword[cg] >> (row & 31)) & 1u))
+              v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+            const uint64_t key = argmax_key(v, row);
+            best[cg] = key > best[cg] ? key : best[cg];
           }
         }
       }
