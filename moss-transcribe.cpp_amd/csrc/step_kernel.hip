@@ -44,7 +44,8 @@ constexpr int cH = 1024, cQN = 2048, cNQKV = 4096, cF = 3072, cNH = 16, cNKV = 8
 constexpr int cBH = cH / kPairK, cBQ = cQN / kPairK, cBF = cF / kPairK;  // 16, 32, 48
 constexpr int cOTiles = cH / 16;         // 64 (o-proj and down tiles, on workgroups 0..63)
 constexpr int cGuBlocks = cF / 32;       // 96 (gate/up 32-row blocks, on workgroups 64..159)
-constexpr int kMergeWg0 = 160;           // merge items on workgroups 160..255
+constexpr int kMergeWg0 = 160;           // merge items on workgroups 160..255 (then 64..159)
+constexpr int kMergeSlots = kNwg - kMergeWg0 + cGuBlocks;
 constexpr int cQStride = 132;            // LDS row strides (conflict-free MFMA operand reads)
 constexpr int cPStride = 68;
 constexpr int kStageFloats = cH + cH / 4;  // one padded row image per wave (panel_norm)
@@ -1391,10 +1392,13 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   const bool helpers = n_items + cNKV <= kNwg;
   const int help_g = (w - n_items - 64 + 2 * kNwg) % kNwg;
   const bool helper = helpers && help_g < cNKV;
-  const int n_merge = cNH * T;                    // (head, row) items, in pairs
-  const bool has_merge = w >= kMergeWg0;
   const bool od = w < cOTiles;                    // o-proj and down tiles
   const bool gu = w >= cOTiles && w < cOTiles + cGuBlocks;  // gate/up rows 32j..32j+31
+  const int n_merge = cNH * T;                    // (head, row) items, in pairs
+  // merge pair slots: workgroups 160..255, then the gate/up workgroups (their own
+  // phase comes after the o-proj), so that 16 rows need one round, not two
+  const int merge_slot = w >= kMergeWg0 ? w - kMergeWg0 : (gu ? kNwg - kMergeWg0 + (w - cOTiles) : -1);
+  const bool has_merge = w >= kMergeWg0 || (merge_slot >= 0 && 2 * merge_slot < n_merge);
   // phase mask of this workgroup (bit p = works in phase p)
   const int mask = 1 | (has_attn ? 2 : 0) | (has_merge ? 4 : 0) | (od ? 8 | 32 : 0) | (gu ? 16 : 0);
   auto next_done = [&](int l, int p) -> uint32_t {  // progress after working in phase p of layer l
@@ -1502,11 +1506,11 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       if (!wait_all(c, ph(l, kPhMerge) - 1)) return;
       WMARK(P, l, 4);
       const int half = threadIdx.x >> 7;
-      for (int i0 = 2 * (w - kMergeWg0); i0 < n_merge; i0 += 2 * (kNwg - kMergeWg0)) {
+      for (int i0 = 2 * merge_slot; i0 < n_merge; i0 += 2 * kMergeSlots) {
         const int item = i0 + half;
         const bool valid = item < n_merge;
         merge_item(P, T, nch, valid ? item / T : 0, valid ? item % T : 0, threadIdx.x & 127, valid,
-                   PROF && l == 1 && i0 == 2 * (w - kMergeWg0), (float*)lds + wave * 128);
+                   PROF && l == 1 && i0 == 2 * merge_slot, (float*)lds + wave * 128);
       }
       WMARK(P, l, 22);
       publish(c, next_done(l, kPhMerge));
