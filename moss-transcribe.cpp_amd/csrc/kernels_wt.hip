@@ -1014,7 +1014,9 @@ __device__ __forceinline__ void f16_group(const F16Group<SEG, NM, NR>& g, const 
   }
 }
 
-// EPI 0: store, 1: residual add, 2: silu(W x) * (W2 x)
+// EPI 0: store, 1: residual add, 2: silu(W x) * (W2 x) written as f16 (the
+// down projection's vec_dot_type: out then holds f16 rows [T][n], in place of
+// the float rows and their conversion by k_act_f16, which gives the same bits)
 template <int EPI, int SEG, int NR>
 __global__ void __launch_bounds__(256)
 k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int n,
@@ -1044,7 +1046,13 @@ k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
       float* dst = out + (size_t)t * n + row;
       if (EPI == 0) *dst = res[0];
       else if (EPI == 1) *dst = __fadd_rn(*dst, res[0]);
-      else *dst = dev_swiglu(res[0], res[NM - 1]);
+      else {
+        // the float product first: the compiler would otherwise fold the multiply
+        // and the conversion into one fma_mix, rounding once instead of twice
+        float v = dev_swiglu(res[0], res[NM - 1]);
+        asm volatile("" : "+v"(v));
+        ((uint16_t*)out)[(size_t)t * n + row] = __half_as_ushort(__float2half_rn(v));
+      }
     }
   }
 }

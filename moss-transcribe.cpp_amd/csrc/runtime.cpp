@@ -379,8 +379,15 @@ void Ctx::enqueue_wt(int mode) {
       launch_gemm_wt(s, wtype, 1, desc_dev, y.wo, nullptr, H, QN, wact, x);
       launch_act_wt(s, wtype, desc_dev, x, H, y.ffn_norm, eps, wact, nullptr);
       launch_gemm_wt(s, wtype, 2, desc_dev, y.wg, y.wu, F, H, wact, act);
-      launch_act_wt(s, wtype, desc_dev, act, F, nullptr, eps, wact, nullptr);
-      launch_gemm_wt(s, wtype, 1, desc_dev, y.wd, nullptr, H, F, wact, x);
+      if (wtype == MTG_TYPE_F16) {
+        // the f16 gate/up GEMM leaves the SwiGLU rows as f16 in act's memory
+        WtAct down_in = wact;
+        down_in.f16h = (uint16_t*)act;
+        launch_gemm_wt(s, wtype, 1, desc_dev, y.wd, nullptr, H, F, down_in, x);
+      } else {
+        launch_act_wt(s, wtype, desc_dev, act, F, nullptr, eps, wact, nullptr);
+        launch_gemm_wt(s, wtype, 1, desc_dev, y.wd, nullptr, H, F, wact, x);
+      }
     }
     launch_act_wt(s, wtype, desc_dev, x, H, out_norm, eps, wact, hid);
   } else {
