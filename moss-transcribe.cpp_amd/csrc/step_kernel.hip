@@ -721,29 +721,42 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
 }
 
 // The new v rows of kv head g: wave w copies rows w + 4 j (j < NV, row < T) of
-// this step's v to LDS (f16-rounded for an f16 cache).
-template <int NV, int KVH>
-__device__ __forceinline__ void stage_v(const StepParams& P, int g, int T, uint32_t tag, float* vnew) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const Rsrc rq = mk_rsrc(P.qkvt, kMaxRows * cNQKV * 8);
+// this step's v to LDS (f16-rounded for an f16 cache). stage_v_issue sends the
+// loads (before the q / k staging, so that both are in flight together);
+// stage_v_finish checks their tags and writes the rows.
+template <int NV>
+struct VStage {
   v2u pr[2 * NV];
   uint32_t po[2 * NV];
   bool live[2 * NV];
+};
+
+template <int NV>
+__device__ __forceinline__ void stage_v_issue(const StepParams& P, int g, int T, VStage<NV>& v) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const Rsrc rq = mk_rsrc(P.qkvt, kMaxRows * cNQKV * 8);
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int t = wave + 4 * j;
-    po[2 * j] = (uint32_t)((min(t, T - 1) * cNQKV + (cNH + cNKV + g) * cHD + lane) * 8);
-    po[2 * j + 1] = po[2 * j] + 64 * 8;
-    live[2 * j] = live[2 * j + 1] = t < T;
-    pr[2 * j] = __builtin_amdgcn_raw_buffer_load_b64(rq, po[2 * j], 0, 16);
-    pr[2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b64(rq, po[2 * j + 1], 0, 16);
+    v.po[2 * j] = (uint32_t)((min(t, T - 1) * cNQKV + (cNH + cNKV + g) * cHD + lane) * 8);
+    v.po[2 * j + 1] = v.po[2 * j] + 64 * 8;
+    v.live[2 * j] = v.live[2 * j + 1] = t < T;
+    v.pr[2 * j] = __builtin_amdgcn_raw_buffer_load_b64(rq, v.po[2 * j], 0, 16);
+    v.pr[2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b64(rq, v.po[2 * j + 1], 0, 16);
   }
-  tagged_wait<2 * NV>(P, rq, pr, po, live, tag);
+}
+
+template <int NV, int KVH>
+__device__ __forceinline__ void stage_v_finish(const StepParams& P, int T, uint32_t tag, VStage<NV>& v,
+                                               float* vnew) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const Rsrc rq = mk_rsrc(P.qkvt, kMaxRows * cNQKV * 8);
+  tagged_wait<2 * NV>(P, rq, v.pr, v.po, v.live, tag);
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int t = wave + 4 * j;
     if (t >= T) break;
-    const float x0 = __uint_as_float(pr[2 * j].x), x1 = __uint_as_float(pr[2 * j + 1].x);
+    const float x0 = __uint_as_float(v.pr[2 * j].x), x1 = __uint_as_float(v.pr[2 * j + 1].x);
     vnew[t * cQStride + lane] = KVH ? f16_round(x0) : x0;
     vnew[t * cQStride + lane + 64] = KVH ? f16_round(x1) : x1;
   }
@@ -830,9 +843,11 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
       stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol, tag, q_lds, knew, vnew, prof);
     } else {
       // q and new k rows are normed and roped; the new v rows are plain copies
+      VStage<2 * G> vst;
+      stage_v_issue<2 * G>(P, g, T, vst);
       stage_pass<6 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, tag, q_lds, knew, vnew, prof);
       if (prof) wmark(P, 1, 14);
-      stage_v<2 * G, KVH>(P, g, T, tag, vnew);
+      stage_v_finish<2 * G, KVH>(P, T, tag, vst, vnew);
     }
   }
   bar();
