@@ -462,18 +462,22 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv_in)[1
                                            float* pscales, float* normed_out, float* stage,
                                            const float* gain_late = nullptr, const StepParams* prof = nullptr) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  float* stg = stage + wave * kStageFloats;
   float gv[16];
   for (int t0 = wave; t0 < T; t0 += 8) {
-    // two rows per pass, all loads issued before any arithmetic
+    // two rows per pass (t0 and t0 + 4), all loads issued before any arithmetic;
+    // their arithmetic runs side by side (the double sums are dependent chains)
+    const bool two = t0 + 4 < T;
     v4f raw[2][4];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int t = t0 + 4 * j;
-      if (t < T) {
+      if (j == 0 || two) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           raw[j][i] = ldc4(x, (uint32_t)((t * cH + (COAL ? 4 * lane + 256 * i : 16 * lane + 4 * i)) * 4));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) raw[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
       }
     }
     if (gain_late) {
@@ -483,49 +487,65 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv_in)[1
       for (int e = 0; e < 16; ++e) gv[e] = gv_in[e];
     }
     if (prof && t0 == wave) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); wmark(*prof, 1, 13); }
+    float v[2][16];
+    if constexpr (COAL) {
+      // one row image per row and wave (LDS accesses of a wave execute in order)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int t = t0 + 4 * j;
-      if (t >= T) break;
-      float v[1][16];
-      if constexpr (COAL) {
+      for (int j = 0; j < 2; ++j) {
+        float* stg = stage + (2 * wave + j) * kStageFloats;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e0 = 4 * lane + 256 * i;
           *(v4f*)(stg + e0 + 4 * (e0 >> 4)) = raw[j][i];
         }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float* stg = stage + (2 * wave + j) * kStageFloats;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const v4f q = *(const v4f*)(stg + 20 * lane + 4 * i);
-          v[0][4 * i] = q[0];
-          v[0][4 * i + 1] = q[1];
-          v[0][4 * i + 2] = q[2];
-          v[0][4 * i + 3] = q[3];
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[0][4 * i] = raw[j][i][0];
-          v[0][4 * i + 1] = raw[j][i][1];
-          v[0][4 * i + 2] = raw[j][i][2];
-          v[0][4 * i + 3] = raw[j][i][3];
+          v[j][4 * i] = q[0];
+          v[j][4 * i + 1] = q[1];
+          v[j][4 * i + 2] = q[2];
+          v[j][4 * i + 3] = q[3];
         }
       }
-      double s = 0.0;
+    } else {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s += (double)__fmul_rn(v[0][e], v[0][e]);
-      s = wave_sum_d(s);
-      const float scale = dev_rms_scale((float)(s / (double)cH), eps);
-      float y[16];
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) y[e] = __fmul_rn(__fmul_rn(v[0][e], scale), gv[e]);
+        for (int i = 0; i < 4; ++i) {
+          v[j][4 * i] = raw[j][i][0];
+          v[j][4 * i + 1] = raw[j][i][1];
+          v[j][4 * i + 2] = raw[j][i][2];
+          v[j][4 * i + 3] = raw[j][i][3];
+        }
+    }
+    double s[2] = {0.0, 0.0};
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) s[j] += (double)__fmul_rn(v[j][e], v[j][e]);
+    wave_sum_d_n<2>(s);
+    float y[2][16];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float scale = dev_rms_scale((float)(s[j] / (double)cH), eps);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) y[j][e] = __fmul_rn(__fmul_rn(v[j][e], scale), gv[e]);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int t = t0 + 4 * j;
+      if (j == 1 && !two) break;
       if (normed_out)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const v4f o = {y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]};
+          const v4f o = {y[j][4 * i], y[j][4 * i + 1], y[j][4 * i + 2], y[j][4 * i + 3]};
           gst<v4f>(normed_out + (size_t)t * cH + 16 * lane + 4 * i, o);
         }
-      quant16(y, t, lane, cBH, pcodes, pscales);
+      quant16(y[j], t, lane, cBH, pcodes, pscales);
     }
   }
   bar();
@@ -1328,7 +1348,7 @@ __host__ __device__ constexpr size_t step_lds_x_offset(int G) {
   return ((size_t)G * cBF * (1024 + 64) + kRedBytes * G > kAttnLdsBytes) ? (size_t)G * cBF * (1024 + 64) + kRedBytes * G
                                                                          : kAttnLdsBytes;
 }
-// after the residual columns: each wave's row image for the norm panel (8-row
+// after the residual columns: two row images per wave for the norm panel (8-row
 // variant only)
 __host__ __device__ constexpr size_t step_lds_stage_offset(int G) {
   return step_lds_x_offset(G) + (size_t)G * 8 * 16 * 4;
@@ -1653,7 +1673,7 @@ int step_kernel_workgroups() { return kNwg; }
 
 uint32_t step_progress_per_step(int n_layers) { return 2u + (uint32_t)(n_layers * kPhases); }
 
-size_t step_lds_bytes(int G) { return step_lds_stage_offset(G) + (G == 1 ? (size_t)4 * kStageFloats * 4 : 0); }
+size_t step_lds_bytes(int G) { return step_lds_stage_offset(G) + (G == 1 ? (size_t)8 * kStageFloats * 4 : 0); }
 
 namespace {
 // [G - 1][f16 KV][profiled]
