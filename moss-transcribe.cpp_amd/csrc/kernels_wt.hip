@@ -763,8 +763,13 @@ __host__ __device__ constexpr size_t q4g_lds_bytes(int nb, int nm) {
 // most of the machine idle with 4
 __host__ __device__ constexpr int q4g_waves(int nb) { return nb >= 8 ? 8 : 4; }
 
+// Every load of a workgroup goes out at its start, in one round trip: the weights,
+// the activation codes of the wave's superblocks, and (wave 0) the chain's
+// activation scales and the residual values of EPI 1. (Left to the compiler, the
+// activation loads went out one sub-block at a time, each waited for before its
+// MFMA.)
 template <int EPI, int NB>
-__global__ void __launch_bounds__(64 * q4g_waves(NB))
+__global__ void __launch_bounds__(64 * q4g_waves(NB), 1)
 k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int n,
            ActQ8K a, float* __restrict__ out) {
   constexpr int K = NB * 256, NM = EPI == 2 ? 2 : 1, NW = q4g_waves(NB), NBW = (NB + NW - 1) / NW;
@@ -774,7 +779,6 @@ k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
   const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = lane & 15, g = lane >> 4;
   const int row = lane & 15, tile = blockIdx.x;
   const uint8_t* const base[2] = {w, w2};
-  // this wave's superblocks: loads first, all of them
   uint32_t qw[NM][NBW][4][2];
   v4i head[NM][NBW];
 #pragma unroll
@@ -793,6 +797,20 @@ k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
         head[m][j] = *(const v4i*)rb;
       }
     }
+  long xv[NBW][8];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    const int b = wave + NW * j;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) xv[j][s] = b < NB ? *(const long*)(a.qs + (size_t)t * K + b * 256 + 8 * g + 32 * s) : 0;
+  }
+  float dxv[NB], xres[4];
+  if (wave == 0) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) dxv[b] = a.d[t * NB + b];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xres[r] = EPI == 1 && t < T ? out[(size_t)t * n + tile * 16 + 4 * g + r] : 0.0f;
+  }
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -803,7 +821,6 @@ k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
       int sc[8], mn[8];
       q4k_scales_w((uint32_t)h[1], (uint32_t)h[2], (uint32_t)h[3], sc, mn);
       v4i ahi = {0, 0, 0, 0}, alo = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
-      const int8_t* xa = a.qs + (size_t)t * K + b * 256 + 8 * g;
 #pragma unroll
       for (int mm = 0; mm < 4; ++mm)
 #pragma unroll
@@ -812,7 +829,7 @@ k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
           const uint32_t q0 = hi ? (qw[m][j][mm][0] >> 4) & 0x0F0F0F0Fu : qw[m][j][mm][0] & 0x0F0F0F0Fu;
           const uint32_t q1 = hi ? (qw[m][j][mm][1] >> 4) & 0x0F0F0F0Fu : qw[m][j][mm][1] & 0x0F0F0F0Fu;
           const uint32_t fh = (uint32_t)(sc[s] >> 3), fl = (uint32_t)(sc[s] & 7), fm = (uint32_t)mn[s] * 0x01010101u;
-          const long bv = *(const long*)(xa + 32 * s);
+          const long bv = xv[j][s];
           ahi = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)(((uint64_t)(q1 * fh) << 32) | (q0 * fh)), bv, ahi, 0, 0, 0);
           alo = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)(((uint64_t)(q1 * fl) << 32) | (q0 * fl)), bv, alo, 0, 0, 0);
           amn = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)(((uint64_t)fm << 32) | fm), bv, amn, 0, 0, 0);
@@ -836,13 +853,13 @@ k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
   for (int m = 0; m < NM; ++m) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) res[m][r] = 0.0f;
+#pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const float dxv = a.d[t * NB + b];
       const int* si = s_i + ((m * NB + b) * 2) * 4 * 64;
       const float* dd = s_dd + (m * NB + b) * 16 * 2;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float dm = __fmul_rn(dd[(4 * g + r) * 2], dxv), dmin = __fmul_rn(dd[(4 * g + r) * 2 + 1], dxv);
+        const float dm = __fmul_rn(dd[(4 * g + r) * 2], dxv[b]), dmin = __fmul_rn(dd[(4 * g + r) * 2 + 1], dxv[b]);
         res[m][r] = __fadd_rn(res[m][r], __fmul_rn(dm, (float)si[r * 64 + lane]));
         res[m][r] = __fsub_rn(res[m][r], __fmul_rn(dmin, (float)si[(4 + r) * 64 + lane]));
       }
@@ -853,7 +870,7 @@ k_gemm_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
     for (int r = 0; r < 4; ++r) {
       float* dst = out + (size_t)t * n + tile * 16 + 4 * g + r;
       if (EPI == 0) *dst = res[0][r];
-      else if (EPI == 1) *dst = __fadd_rn(*dst, res[0][r]);
+      else if (EPI == 1) *dst = __fadd_rn(xres[r], res[0][r]);
       else *dst = dev_swiglu(res[0][r], res[NM - 1][r]);
     }
   }
