@@ -342,7 +342,7 @@ k_attn_chunk(const StepDesc* __restrict__ desc, const float* __restrict__ q, int
 }
 
 // ------------------------------------------------ attention, f16 cache ----
-// The same chunk arithmetic for an f16 cache, laid out for two workgroups per CU
+// The same chunk arithmetic for an f16 cache, laid out for three workgroups per CU
 // and back-to-back MFMA chains. A workgroup keeps its q columns in registers and
 // walks the chunks blockIdx.y, blockIdx.y + gridDim.y, ..., the next chunk's K / V
 // rows in flight in registers while the current one computes. K / V sit in LDS
@@ -354,7 +354,7 @@ constexpr int kAkStrideH = 136;  // halves per permuted K row
 constexpr int kAvStrideW = 65;   // 32-bit words per V row
 constexpr size_t kAttnF16Lds =
     (size_t)kMaxCols * kAqStride * 4 + (size_t)kChunk * kAkStrideH * 2 + (size_t)kChunk * kAvStrideW * 4;
-constexpr int kAttnF16Waves = 2 * 256;  // resident workgroups targeted by the grid (2 per CU)
+constexpr int kAttnF16Waves = 3 * 256;  // resident workgroups targeted by the grid (3 per CU)
 
 __device__ __forceinline__ float h_lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)w); }
 __device__ __forceinline__ float h_hi(uint32_t w) {
@@ -505,7 +505,7 @@ __device__ __forceinline__ void attn_f16_softmax(float* s_p, int ncol, float* ou
   }
 }
 
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256, 3)
 k_attn_f16(const StepDesc* __restrict__ desc, const float* __restrict__ q, int n_heads, KvLayer kv,
            AttnWork work, int max_chunks) {
   const int g = blockIdx.x;
