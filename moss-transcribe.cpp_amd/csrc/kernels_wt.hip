@@ -42,6 +42,7 @@ namespace mtg {
 
 namespace {
 using namespace dev;
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 // 1 / sqrt(mean(x^2) + eps) of a hidden row (K == 1024), the canonical double sum:
 // lane l sums elements 16l..16l+15, then the butterfly. Called by wave 0.
@@ -173,15 +174,28 @@ k_attn_combine_wt(const StepDesc* __restrict__ desc, AttnWork work, int n_heads,
                                                      0x00020000);
   __shared__ float s_f[2][kCombPass], s_l[2][kCombPass];
   __shared__ float s_L[256], s_O[256];
-  // waves 0 and 2 (segment 0, d < 64) compute M and the chunk factors of q head hl
+  // waves 0 and 2 (segment 0, d < 64) compute M and the chunk factors of q head hl;
+  // the (m, l) of the first pass stay in their registers (one round trip)
   const bool factors = seg == 0 && d < 64;
-  float M = -INFINITY;
-  if (factors)
-    for (int c0 = 0; c0 < nch; c0 += 64) {
+  constexpr int kMl = kCombPass / 64;
+  float M = -INFINITY, m1[kMl], l1[kMl];
+  if (factors) {
+#pragma unroll
+    for (int i = 0; i < kMl; ++i) {
+      const uint32_t off = (uint32_t)(64 * i + lane) * sml + col * 8;
+      const v2u ml = __builtin_amdgcn_raw_buffer_load_b64(rml, off, 0, 0);  // past nch: zeros
+      const bool in = 64 * i + lane < nch;
+      m1[i] = in ? __uint_as_float(ml.x) : -INFINITY;
+      l1[i] = in ? __uint_as_float(ml.y) : 0.0f;
+      M = fmaxf(M, m1[i]);
+    }
+    for (int c0 = kCombPass; c0 < nch; c0 += 64) {
       const float m = __builtin_bit_cast(
           float, __builtin_amdgcn_raw_buffer_load_b32(rml, (c0 + lane) * sml + col * 8, 0, 0));
-      M = fmaxf(M, wave_max_f(c0 + lane < nch ? m : -INFINITY));
+      M = fmaxf(M, c0 + lane < nch ? m : -INFINITY);
     }
+    M = wave_max_f(M);
+  }
   float L = 0.0f, O = 0.0f;
   for (int p0 = 0; p0 < nch; p0 += kCombPass) {
     const int c_lo = p0 + seg * kCombPer;
@@ -190,16 +204,22 @@ k_attn_combine_wt(const StepDesc* __restrict__ desc, AttnWork work, int n_heads,
     for (int i = 0; i < kCombPer; ++i)
       o[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                            ro, (uint32_t)(c_lo + i) * so + (col * kHeadDim + d) * 4, 0, 0));
-    if (factors)
-      for (int c = lane; c < kCombPass; c += 64) {
-        const uint32_t off = (uint32_t)(p0 + c) * sml + col * 8;
-        const bool in = p0 + c < nch;
-        const float m = in ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rml, off, 0, 0))
-                           : -INFINITY;
-        const float l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rml, off + 4, 0, 0));
+    if (factors) {
+#pragma unroll
+      for (int i = 0; i < kMl; ++i) {
+        const int c = 64 * i + lane;
+        float m = m1[i], l = l1[i];
+        if (p0 > 0) {
+          const uint32_t off = (uint32_t)(p0 + c) * sml + col * 8;
+          const v2u ml = __builtin_amdgcn_raw_buffer_load_b64(rml, off, 0, 0);
+          const bool in = p0 + c < nch;
+          m = in ? __uint_as_float(ml.x) : -INFINITY;
+          l = in ? __uint_as_float(ml.y) : 0.0f;
+        }
         s_f[hl][c] = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, M));
-        s_l[hl][c] = in ? l : 0.0f;
+        s_l[hl][c] = l;
       }
+    }
     __syncthreads();
     for (int sg = 0; sg < kCombSeg; ++sg) {
       if (seg == sg) {
