@@ -69,14 +69,16 @@ k_act_f16(const StepDesc* __restrict__ desc, const float* __restrict__ src, int 
   if (t >= desc->T) return;
   const float* xr = src + (size_t)t * K;
   __shared__ float s_scale;
+  // the element and its gain load together with wave 0's row (one round trip)
   float y = xr[k];
+  const float gk = gain ? gain[k] : 0.0f;
   if (gain) {
     if (threadIdx.x < 64) {
       const float sc = row_rms_scale(xr, K, eps);
       if (threadIdx.x == 0) s_scale = sc;
     }
     __syncthreads();
-    y = __fmul_rn(__fmul_rn(y, s_scale), gain[k]);
+    y = __fmul_rn(__fmul_rn(y, s_scale), gk);
   }
   if (normed_out) normed_out[(size_t)t * K + k] = y;
   out[(size_t)t * K + k] = __half_as_ushort(__float2half_rn(y));  // vec_dot_type F16
@@ -129,14 +131,16 @@ k_act_q8k(const StepDesc* __restrict__ desc, const float* __restrict__ src, int 
   if (t >= desc->T) return;
   const float* xr = src + (size_t)t * K;
   __shared__ float s_scale;
+  // the element and its gain load together with wave 0's row (one round trip)
   float y = xr[k];
+  const float gk = gain ? gain[k] : 0.0f;
   if (gain) {
     if (threadIdx.x < 64) {
       const float sc = row_rms_scale(xr, K, eps);
       if (threadIdx.x == 0) s_scale = sc;
     }
     __syncthreads();
-    y = __fmul_rn(__fmul_rn(y, s_scale), gain[k]);
+    y = __fmul_rn(__fmul_rn(y, s_scale), gk);
   }
   if (normed_out) normed_out[(size_t)t * K + k] = y;
   q8k_block256(y, a, t, K, b);
