@@ -522,15 +522,25 @@ k_attn_f16(const StepDesc* __restrict__ desc, const float* __restrict__ q, int n
   const int ncol = 2 * T;
   const uint16_t* kb = (const uint16_t*)kv.k + (size_t)g * kv.max_seq * kHeadDim;
   const uint16_t* vb = (const uint16_t*)kv.v + (size_t)g * kv.max_seq * kHeadDim;
+  // q columns, f16-rounded (mul_mat(f16 K, f32 q) converts q), into registers:
+  // lane (kl, kk) of column tile ct holds column 16 ct + kl, elements 4 i + kk.
+  // The q loads go out first, all of them, then the first chunk's K / V: the
+  // staging below waits for q only (loads complete in order).
+  constexpr int kQPieces = kMaxCols * (kHeadDim / 4) / 256;
+  v4f qv[kQPieces];
+#pragma unroll
+  for (int j = 0; j < kQPieces; ++j) {
+    const int idx = tid + 256 * j, col = idx / (kHeadDim / 4), d = (idx % (kHeadDim / 4)) * 4;
+    if (col < ncol) qv[j] = *(const v4f*)(q + ((size_t)(col % T) * n_heads + 2 * g + col / T) * kHeadDim + d);
+  }
   v4i pk[4], pv[4];
   attn_f16_load(kb, vb, chunk * kChunk, kvlen, pk, pv);
-  // q columns, f16-rounded (mul_mat(f16 K, f32 q) converts q), into registers:
-  // lane (kl, kk) of column tile ct holds column 16 ct + kl, elements 4 i + kk
-  for (int idx = tid; idx < ncol * (kHeadDim / 4); idx += 256) {
-    const int col = idx / (kHeadDim / 4), d = (idx % (kHeadDim / 4)) * 4, hl = col / T, t = col % T;
-    const v4f v = *(const v4f*)(q + ((size_t)t * n_heads + 2 * g + hl) * kHeadDim + d);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s_q[col * kAqStride + attn_perm128(d + e)] = f16_round(v[e]);
+  for (int j = 0; j < kQPieces; ++j) {
+    const int idx = tid + 256 * j, col = idx / (kHeadDim / 4), d = (idx % (kHeadDim / 4)) * 4;
+    if (col < ncol)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s_q[col * kAqStride + attn_perm128(d + e)] = f16_round(qv[j][e]);
   }
   __syncthreads();
   float qreg[2][32];

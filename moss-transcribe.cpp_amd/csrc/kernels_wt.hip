@@ -44,6 +44,24 @@ namespace {
 using namespace dev;
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
+// Copy of n 16-byte pieces src[i] (i = tid, tid + nt, ...; at most MAXJ per thread)
+// to dst(i), with every load of the thread issued before the first store: one
+// memory round trip (a load / store loop waits for each load in turn).
+template <int MAXJ, class Dst>
+__device__ __forceinline__ void stage_pieces(const v4i* __restrict__ src, int n, int tid, int nt, Dst dst) {
+  v4i r[MAXJ];
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) {
+    const int i = tid + j * nt;
+    if (i < n) r[j] = src[i];
+  }
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) {
+    const int i = tid + j * nt;
+    if (i < n) *dst(i) = r[j];
+  }
+}
+
 // 1 / sqrt(mean(x^2) + eps) of a hidden row (K == 1024), the canonical double sum:
 // lane l sums elements 16l..16l+15, then the butterfly. Called by wave 0.
 __device__ __forceinline__ float row_rms_scale(const float* xr, int K, float eps) {
@@ -452,11 +470,22 @@ __device__ __forceinline__ Q4Lds q4_stage(const ActQ8K& a, int K, int T, int row
   int* bs = (int*)(lds + (size_t)kMaxRows * as);
   float* dx = (float*)(bs + kMaxRows * bst);
   uint8_t* wbase = (uint8_t*)(dx + kMaxRows * nb);
-  const int pa = K / 16, pb = K / 64, nt = blockDim.x;  // 16-byte pieces per row
-  for (int i = tid; i < T * pa; i += nt)
-    *(v4i*)(act + (size_t)(i / pa) * as + (i % pa) * 16) = ((const v4i*)a.qs)[i];
-  for (int i = tid; i < T * pb; i += nt) *(v4i*)(bs + (size_t)(i / pb) * bst + (i % pb) * 4) = ((const v4i*)a.bsums)[i];
-  for (int i = tid; i < T * nb; i += nt) dx[i] = a.d[i];
+  const int pa = K / 16, pb = K / 64, nt = 256;  // 16-byte pieces per row; 256-thread workgroups
+  // the scales first (one load each), then the codes and group sums with every
+  // load in flight before the first LDS write
+  float dxr[(kMaxRows * kQ4MaxK / 256 + 255) / 256];
+#pragma unroll
+  for (int j = 0; j < (kMaxRows * kQ4MaxK / 256 + 255) / 256; ++j)
+    if (tid + j * nt < T * nb) dxr[j] = a.d[tid + j * nt];
+  stage_pieces<kMaxRows * kQ4MaxK / 16 / 256>((const v4i*)a.qs, T * pa, tid, nt, [&](int i) {
+    return (v4i*)(act + (size_t)(i / pa) * as + (i % pa) * 16);
+  });
+  stage_pieces<kMaxRows * kQ4MaxK / 64 / 256>((const v4i*)a.bsums, T * pb, tid, nt, [&](int i) {
+    return (v4i*)(bs + (size_t)(i / pb) * bst + (i % pb) * 4);
+  });
+#pragma unroll
+  for (int j = 0; j < (kMaxRows * kQ4MaxK / 256 + 255) / 256; ++j)
+    if (tid + j * nt < T * nb) dx[tid + j * nt] = dxr[j];
   __syncthreads();
   Q4Lds q;
   q.act = act;
@@ -1074,7 +1103,8 @@ k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
   int g = blockIdx.x * 4 + wave;
   F16Group<SEG, NM, NR> bt;
   f16_load<SEG, NM, NR>(base, n, g * NR, bt);  // in flight during the staging
-  for (int i = threadIdx.x; i < T * K / 8; i += 256) ((v4i*)s_x)[i] = ((const v4i*)xh)[i];
+  stage_pieces<kMaxRows * K / 8 / 256>((const v4i*)xh, T * K / 8, threadIdx.x, 256,
+                                       [&](int i) { return (v4i*)s_x + i; });
   __syncthreads();
   const int r = lane >> 4, t = lane & 15;
   for (; g < ngroups; g += nwaves) {
@@ -1122,7 +1152,8 @@ k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
   F16Group<SEG, 1, NR> bt, bt2;
   f16_load<SEG, 1, NR>(base, vocab, g * NR, bt);
   if (g + nwaves < ngroups) f16_load<SEG, 1, NR>(base, vocab, (g + nwaves) * NR, bt2);
-  for (int i = threadIdx.x; i < T * K / 8; i += 256) ((v4i*)s_x)[i] = ((const v4i*)xh)[i];
+  stage_pieces<kMaxRows * K / 8 / 256>((const v4i*)xh, T * K / 8, threadIdx.x, 256,
+                                       [&](int i) { return (v4i*)s_x + i; });
   __syncthreads();
   const int r = lane >> 4, t = lane & 15;
   uint64_t best = 0;  // lane (r, t): verify row t
