@@ -186,13 +186,23 @@ k_enc_attn(const float* __restrict__ q, const float* __restrict__ k, const float
   const int nch = (T + 63) / 64;
   const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)kEncHd));
   const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-  // 64 rows x 64 floats of src from row0 (zeros past T) into dst
-  auto stage = [&](float (*dst)[kAS], const float* src, int row0) {
+  // 64 rows x 64 floats of src from row0 (zeros past T): load4 issues the four
+  // 16-byte loads of this thread (rows past T read row T - 1 and are zeroed after
+  // the load, so no branch splits them), store4 writes them to dst. A chunk's
+  // loads go out one chunk ahead and land during the previous chunk's arithmetic.
+  auto load4 = [&](const float* src, int row0, v4f (&r)[4]) {
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
       const int i = tid + 256 * x, rr = i >> 4, d4 = i & 15;
-      *(v4f*)&dst[rr][4 * d4] =
-          row0 + rr < T ? *(const v4f*)(src + (size_t)(row0 + rr) * W + h * kEncHd + 4 * d4) : zero4;
+      r[x] = *(const v4f*)(src + (size_t)min(row0 + rr, T - 1) * W + h * kEncHd + 4 * d4);
+      if (row0 + rr >= T) r[x] = zero4;
+    }
+  };
+  auto store4 = [&](float (*dst)[kAS], const v4f (&r)[4]) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int i = tid + 256 * x, rr = i >> 4, d4 = i & 15;
+      *(v4f*)&dst[rr][4 * d4] = r[x];
     }
   };
   auto scores = [&](int key0, float (&w)[4][4]) {
@@ -219,12 +229,16 @@ k_enc_attn(const float* __restrict__ q, const float* __restrict__ k, const float
 #pragma unroll
       for (int j = 0; j < 4; ++j) w[i][j] = key0 + 4 * tk + j < T ? __fmul_rn(acc[i][j], scale) : -INFINITY;
   };
-  stage(qs, q, r0);
+  v4f kr[4], vr[4];
+  load4(q, r0, vr);
+  load4(k, 0, kr);
+  store4(qs, vr);
   // pass 1: chunk maxima per row (over the 16 threads of a row group)
   for (int c = 0; c < nch; ++c) {
     __syncthreads();
-    stage(kv, k, 64 * c);
+    store4(kv, kr);
     __syncthreads();
+    if (c + 1 < nch) load4(k, 64 * (c + 1), kr);
     float w[4][4];
     scores(64 * c, w);
 #pragma unroll
@@ -246,10 +260,13 @@ k_enc_attn(const float* __restrict__ q, const float* __restrict__ k, const float
     for (int e = 0; e < 4; ++e) O[i][e] = 0.0f;
   }
   // pass 2
+  load4(k, 0, kr);
+  load4(v, 0, vr);
   for (int c = 0; c < nch; ++c) {
     __syncthreads();
-    stage(kv, k, 64 * c);
+    store4(kv, kr);
     __syncthreads();
+    if (c + 1 < nch) load4(k, 64 * (c + 1), kr);
     float w[4][4];
     scores(64 * c, w);
 #pragma unroll
@@ -261,7 +278,8 @@ k_enc_attn(const float* __restrict__ q, const float* __restrict__ k, const float
       *(v4f*)&ps[4 * tr + i][4 * tk] = p4;
     }
     __syncthreads();  // K consumed, p complete
-    stage(kv, v, 64 * c);
+    store4(kv, vr);
+    if (c + 1 < nch) load4(v, 64 * (c + 1), vr);
     if (tid < kEncRows) {
       float t[64];
 #pragma unroll
