@@ -119,6 +119,10 @@ void launch_act_wt(hipStream_t s, int wtype, const StepDesc* desc, const float* 
 void launch_attn_combine_wt(hipStream_t s, int wtype, const StepDesc* desc, AttnWork work, int n_heads,
                             int max_chunks, const WtAct& act);
 // epi 0: out = W act, 1: out += W act, 2: out = silu(W act) * (W2 act)
+// f16 weights, K = 1024, EPI 0 or 2: out = W (RMSNorm(x) * gain), the norm computed
+// in the GEMM (the activation k_act_f16 would write, without its launch)
+void launch_gemm_f16_norm(hipStream_t s, int epi, const StepDesc* desc, const uint8_t* w, const uint8_t* w2, int n,
+                          const float* x, const float* gain, float eps, float* out);
 void launch_gemm_wt(hipStream_t s, int wtype, int epi, const StepDesc* desc, const uint8_t* w,
                     const uint8_t* w2, int n, int k, const WtAct& act, float* out);
 void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int vocab, int k,

@@ -1084,14 +1084,64 @@ __device__ __forceinline__ void f16_group(const F16Group<SEG, NM, NR>& g, const 
   }
 }
 
+// The f16 activation rows of a K = 1024 GEMM computed in the workgroup from the
+// residual rows x: RMSNorm(x) * gain rounded to f16, k_act_f16's arithmetic (lane l
+// sums the squares of elements 16 l .. 16 l + 15 in double, the butterfly, the
+// correctly rounded 1 / sqrt, y = (x * scale) * gain, then f16), written to s_x.
+// Wave w takes rows w, w + 4, w + 8, w + 12, their double sums side by side.
+__device__ __forceinline__ void f16_norm_rows(const float* __restrict__ x, const float* __restrict__ gain, float eps,
+                                              int T, uint16_t* s_x) {
+  constexpr int K = 1024;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  v4f raw[4][4], gv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = min(wave + 4 * j, T - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) raw[j][i] = *(const v4f*)(x + (size_t)t * K + 16 * lane + 4 * i);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) gv[i] = *(const v4f*)(gain + 16 * lane + 4 * i);
+  double sq[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sq[j] += (double)__fmul_rn(raw[j][e >> 2][e & 3], raw[j][e >> 2][e & 3]);
+  wave_sum_d_n<4>(sq);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = wave + 4 * j;
+    if (t >= T) break;
+    const float scale = dev_rms_scale((float)(sq[j] / (double)K), eps);
+    uint32_t h[8];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      float y0 = __fmul_rn(__fmul_rn(raw[j][e >> 2][e & 3], scale), gv[e >> 2][e & 3]);
+      float y1 = __fmul_rn(__fmul_rn(raw[j][(e + 1) >> 2][(e + 1) & 3], scale), gv[(e + 1) >> 2][(e + 1) & 3]);
+      // the float products first: the compiler would otherwise fold the last
+      // multiply and the conversion into one fma_mix (one rounding, not two)
+      asm volatile("" : "+v"(y0), "+v"(y1));
+      h[e / 2] = (uint32_t)__half_as_ushort(__float2half_rn(y0)) |
+                 ((uint32_t)__half_as_ushort(__float2half_rn(y1)) << 16);
+    }
+    uint4* dst = (uint4*)(s_x + t * K + 16 * lane);
+    dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
+    dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+  }
+}
+
 // EPI 0: store, 1: residual add, 2: silu(W x) * (W2 x) written as f16 (the
 // down projection's vec_dot_type: out then holds f16 rows [T][n], in place of
-// the float rows and their conversion by k_act_f16, which gives the same bits)
-template <int EPI, int SEG, int NR>
+// the float rows and their conversion by k_act_f16, which gives the same bits).
+// NORM (K = 1024): the activation is RMSNorm(xn) * gain of the residual rows xn,
+// computed here (f16_norm_rows) instead of by a k_act_f16 launch before.
+template <int EPI, int SEG, int NR, bool NORM = false>
 __global__ void __launch_bounds__(256)
 k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int n,
-           const uint16_t* __restrict__ xh, float* __restrict__ out) {
+           const uint16_t* __restrict__ xh, float* __restrict__ out, const float* __restrict__ xn = nullptr,
+           const float* __restrict__ gain = nullptr, float eps = 0.0f) {
   constexpr int K = SEG * 64, NM = EPI == 2 ? 2 : 1;
+  static_assert(!NORM || K == 1024, "the norm prologue covers the hidden rows");
   extern __shared__ v4i f16_lds_v4[];
   uint16_t* s_x = (uint16_t*)f16_lds_v4;
   const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1103,8 +1153,11 @@ k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
   int g = blockIdx.x * 4 + wave;
   F16Group<SEG, NM, NR> bt;
   f16_load<SEG, NM, NR>(base, n, g * NR, bt);  // in flight during the staging
-  stage_pieces<kMaxRows * K / 8 / 256>((const v4i*)xh, T * K / 8, threadIdx.x, 256,
-                                       [&](int i) { return (v4i*)s_x + i; });
+  if constexpr (NORM)
+    f16_norm_rows(xn, gain, eps, T, s_x);
+  else
+    stage_pieces<kMaxRows * K / 8 / 256>((const v4i*)xh, T * K / 8, threadIdx.x, 256,
+                                         [&](int i) { return (v4i*)s_x + i; });
   __syncthreads();
   const int r = lane >> 4, t = lane & 15;
   for (; g < ngroups; g += nwaves) {
@@ -1236,6 +1289,17 @@ void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_
   }
 }
 
+// The f16 GEMM of a K = 1024 matrix whose activation is RMSNorm(x) * gain (EPI 0
+// or 2): the norm runs in the GEMM's workgroups.
+template <int EPI>
+void gemm_f16_norm(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_t* w2, int n, const float* x,
+                   const float* gain, float eps, float* out) {
+  constexpr int NM = EPI == 2 ? 2 : 1, NR = f16_nr(EPI, 16);
+  const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kF16GemmWorkgroups);
+  hipLaunchKernelGGL((k_gemm_f16<EPI, 16, NR, true>), dim3(blocks), dim3(256), f16_lds_bytes(1024, NM * NR), s, desc,
+                     w, w2, n, nullptr, out, x, gain, eps);
+}
+
 }  // namespace
 
 // ================================================================ launches ==
@@ -1260,6 +1324,13 @@ hipError_t prepare_kernels_wt() {
   MTG_F16_ATTR(0, 32) MTG_F16_ATTR(1, 32) MTG_F16_ATTR(2, 32)
   MTG_F16_ATTR(0, 48) MTG_F16_ATTR(1, 48) MTG_F16_ATTR(2, 48)
 #undef MTG_F16_ATTR
+  for (int epi = 0; epi <= 2; epi += 2) {
+    const int nm_nr = epi == 2 ? 2 * f16_nr(2, 16) : f16_nr(0, 16);
+    const hipError_t e = hipFuncSetAttribute(
+        epi == 2 ? (const void*)k_gemm_f16<2, 16, f16_nr(2, 16), true> : (const void*)k_gemm_f16<0, 16, f16_nr(0, 16), true>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)f16_lds_bytes(1024, nm_nr));
+    if (e != hipSuccess) return e;
+  }
   return hipFuncSetAttribute((const void*)k_lm_head_f16, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)f16_lds_bytes(1024, kF16LmNR));
 }
@@ -1286,6 +1357,12 @@ void launch_attn_combine_wt(hipStream_t s, int wtype, const StepDesc* desc, Attn
     hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_F16>, grid, block, 0, s, desc, work, n_heads, max_chunks, act);
   else
     hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_Q4_K>, grid, block, 0, s, desc, work, n_heads, max_chunks, act);
+}
+
+void launch_gemm_f16_norm(hipStream_t s, int epi, const StepDesc* desc, const uint8_t* w, const uint8_t* w2, int n,
+                          const float* x, const float* gain, float eps, float* out) {
+  if (epi == 2) gemm_f16_norm<2>(s, desc, w, w2, n, x, gain, eps, out);
+  else gemm_f16_norm<0>(s, desc, w, w2, n, x, gain, eps, out);
 }
 
 void launch_gemm_wt(hipStream_t s, int wtype, int epi, const StepDesc* desc, const uint8_t* w,

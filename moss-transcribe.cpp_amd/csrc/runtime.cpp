@@ -371,14 +371,22 @@ void Ctx::enqueue_wt(int mode) {
     for (int l = 0; l < hp.n_layers; ++l) {
       const Layer& y = layers[l];
       const KvLayer kv = kv_layer(l);
-      launch_act_wt(s, wtype, desc_dev, x, H, y.attn_norm, eps, wact, nullptr);
-      launch_gemm_wt(s, wtype, 0, desc_dev, y.wqkv, nullptr, QN + 2 * KN, H, wact, qkv);
+      if (wtype == MTG_TYPE_F16 && H == 1024) {  // the norm inside the f16 GEMM
+        launch_gemm_f16_norm(s, 0, desc_dev, y.wqkv, nullptr, QN + 2 * KN, x, y.attn_norm, eps, qkv);
+      } else {
+        launch_act_wt(s, wtype, desc_dev, x, H, y.attn_norm, eps, wact, nullptr);
+        launch_gemm_wt(s, wtype, 0, desc_dev, y.wqkv, nullptr, QN + 2 * KN, H, wact, qkv);
+      }
       launch_qk_rope_append(s, desc_dev, qkv, NH, NKV, y.q_norm, y.k_norm, eps, rope, qbuf, kv);
       launch_attn_chunks(s, desc_dev, qbuf, NH, NKV, kv, work);
       launch_attn_combine_wt(s, wtype, desc_dev, work, NH, attn_max_chunks(kv), wact);
       launch_gemm_wt(s, wtype, 1, desc_dev, y.wo, nullptr, H, QN, wact, x);
-      launch_act_wt(s, wtype, desc_dev, x, H, y.ffn_norm, eps, wact, nullptr);
-      launch_gemm_wt(s, wtype, 2, desc_dev, y.wg, y.wu, F, H, wact, act);
+      if (wtype == MTG_TYPE_F16 && H == 1024) {
+        launch_gemm_f16_norm(s, 2, desc_dev, y.wg, y.wu, F, x, y.ffn_norm, eps, act);
+      } else {
+        launch_act_wt(s, wtype, desc_dev, x, H, y.ffn_norm, eps, wact, nullptr);
+        launch_gemm_wt(s, wtype, 2, desc_dev, y.wg, y.wu, F, H, wact, act);
+      }
       if (wtype == MTG_TYPE_F16) {
         // the f16 gate/up GEMM leaves the SwiGLU rows as f16 in act's memory
         WtAct down_in = wact;
