@@ -31,6 +31,7 @@
 //          then in superblock order acc = acc + (d_w*d_x)*dot, acc = acc -
 //          (dmin_w*d_x)*mins.
 #include <algorithm>
+#include <type_traits>
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -982,19 +983,29 @@ k_lm_head_q4m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
 // NR weight rows (of each of NM matrices) at a time, the next group's rows in
 // flight in registers. Lane l runs the canonical fma chain over its K/64
 // elements for every (matrix, row, verify row) output; the 64 lane partials of
-// an output meet in LDS (row stride 65 words: conflict-free both ways) and one
+// an output meet in LDS as one row of kF16PStride words (lane writes: consecutive
+// words; one lane then reads the row with 16-byte loads, conflict-free) and that
 // lane adds them in the pairing of the xor butterfly 32, 16, 8, 4, 2, 1 (the same
 // additions as wave_sum_f: IEEE sums commute). Lane j < 16 NR ends with the
 // outputs of row j / 16, verify row j % 16.
+//
+// Order of the memory traffic: the activation loads are issued first, then the
+// weight rows (loads complete in order, so the activation's arrival, its LDS
+// writes and the norm prologue's arithmetic overlap the weights' flight), then
+// the residual values an EPI 1 store adds to.
 template <int SEG, int NM, int NR>
 struct F16Group {
   v4i w[NM][NR][SEG / 8];  // the lane's K/64 halves of each row, 8 per piece
 };
 
+constexpr int kF16PStride = 68;  // words per partial row (a multiple of 4 for 16-byte reads)
+
 __host__ __device__ constexpr size_t f16_lds_bytes(int K, int nm_nr) {
-  return (size_t)kMaxRows * K * 2 + 4 * (size_t)nm_nr * kMaxRows * 65 * 4;
+  return (size_t)kMaxRows * K * 2 + 4 * (size_t)nm_nr * kMaxRows * kF16PStride * 4;
 }
 
+// rows past n are clamped to row n - 1 (loaded, never stored): no branches
+// between the loads
 template <int SEG, int NM, int NR>
 __device__ __forceinline__ void f16_load(const uint16_t* const (&base)[NM], int n, int row0,
                                          F16Group<SEG, NM, NR>& g) {
@@ -1003,10 +1014,10 @@ __device__ __forceinline__ void f16_load(const uint16_t* const (&base)[NM], int 
   for (int m = 0; m < NM; ++m)
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      const int row = row0 + r;
+      const int row = min(row0 + r, n - 1);
 #pragma unroll
       for (int c = 0; c < SEG / 8; ++c)
-        if (row < n) g.w[m][r][c] = *(const v4i*)(base[m] + (size_t)row * (SEG * 64) + lane * SEG + 8 * c);
+        g.w[m][r][c] = *(const v4i*)(base[m] + (size_t)row * (SEG * 64) + lane * SEG + 8 * c);
     }
 }
 
@@ -1015,10 +1026,15 @@ __device__ __forceinline__ float h_hi(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
 }
 
-template <int SEG, int NM, int NR>
+// verify rows per pass of f16_group (their fma chains interleaved; measured best
+// for every row group here, one to six rows per wave)
+constexpr int kF16TT = 2;
+
+template <int SEG, int NM, int NR, int TT = kF16TT>
 __device__ __forceinline__ void f16_group(const F16Group<SEG, NM, NR>& g, const uint16_t* s_x, int T, float* s_p,
                                           float (&res)[NM]) {
   constexpr int K = SEG * 64, NC = SEG / 8;
+  static_assert(kMaxRows % TT == 0, "passes of TT rows cover the LDS rows");
   const int lane = threadIdx.x & 63;
   float wf[NM][NR][SEG];
 #pragma unroll
@@ -1034,44 +1050,76 @@ __device__ __forceinline__ void f16_group(const F16Group<SEG, NM, NR>& g, const 
           wf[m][r][8 * c + 2 * q + 1] = h_hi(u);
         }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous group's partial reads are done
+  // a pass takes verify rows t0 .. t0 + TT - 1; rows from T on (stale LDS rows,
+  // inside the kMaxRows staged) are computed and their partials written to slots
+  // the sums never read
+  const uint16_t* xr = s_x + lane * SEG;
+  v4i xv[TT][NC], xnext[TT][NC];
 #pragma unroll
-  for (int t = 0; t < kMaxRows; ++t) {  // constant indices keep the sums in registers
-    if (t >= T) break;
-    float acc[NM][NR];
+  for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-    for (int m = 0; m < NM; ++m)
+    for (int c = 0; c < NC; ++c) xv[tt][c] = *(const v4i*)(xr + tt * K + 8 * c);
 #pragma unroll
-      for (int r = 0; r < NR; ++r) acc[m][r] = 0.0f;
-    const uint16_t* xr = s_x + t * K + lane * SEG;
+  for (int t0 = 0; t0 < kMaxRows; t0 += TT) {  // constant indices keep the sums in registers
+    if (t0 >= T) break;
+    if (t0 + TT < T) {  // the next pass's activation in flight during this one's chains
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) xnext[tt][c] = *(const v4i*)(xr + (t0 + TT + tt) * K + 8 * c);
+    }
+    float acc[TT][NM][NR];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[tt][m][r] = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const v4i xv = *(const v4i*)(xr + 8 * c);
-      float xf[8];
+      float xf[TT][8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        xf[2 * q] = h_lo((uint32_t)xv[q]);
-        xf[2 * q + 1] = h_hi((uint32_t)xv[q]);
-      }
+      for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          xf[tt][2 * q] = h_lo((uint32_t)xv[tt][c][q]);
+          xf[tt][2 * q + 1] = h_hi((uint32_t)xv[tt][c][q]);
+        }
 #pragma unroll
       for (int e = 0; e < 8; ++e)
 #pragma unroll
-        for (int m = 0; m < NM; ++m)
+        for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-          for (int r = 0; r < NR; ++r) acc[m][r] = fmaf(wf[m][r][8 * c + e], xf[e], acc[m][r]);
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < NR; ++r) acc[tt][m][r] = fmaf(wf[m][r][8 * c + e], xf[tt][e], acc[tt][m][r]);
     }
 #pragma unroll
-    for (int m = 0; m < NM; ++m)
+    for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-      for (int r = 0; r < NR; ++r) s_p[((m * NR + r) * kMaxRows + t) * 65 + lane] = acc[m][r];
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+          s_p[((m * NR + r) * kMaxRows + t0 + tt) * kF16PStride + lane] = acc[tt][m][r];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) xv[tt][c] = xnext[tt][c];
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's partial writes are done
 #pragma unroll
   for (int m = 0; m < NM; ++m) {
     float v[64];
-    const float* col = s_p + ((m * NR) * kMaxRows + lane) * 65;
+    const v4f* col = (const v4f*)(s_p + ((m * NR) * kMaxRows + lane) * kF16PStride);
     if (lane < NR * kMaxRows && (lane & 15) < T) {
 #pragma unroll
-      for (int i = 0; i < 64; ++i) v[i] = col[i];
+      for (int i = 0; i < 16; ++i) {
+        const v4f q = col[i];
+        v[4 * i] = q[0];
+        v[4 * i + 1] = q[1];
+        v[4 * i + 2] = q[2];
+        v[4 * i + 3] = q[3];
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < 64; ++i) v[i] = 0.0f;
@@ -1089,52 +1137,85 @@ __device__ __forceinline__ void f16_group(const F16Group<SEG, NM, NR>& g, const 
 // sums the squares of elements 16 l .. 16 l + 15 in double, the butterfly, the
 // correctly rounded 1 / sqrt, y = (x * scale) * gain, then f16), written to s_x.
 // Wave w takes rows w, w + 4, w + 8, w + 12, their double sums side by side.
-__device__ __forceinline__ void f16_norm_rows(const float* __restrict__ x, const float* __restrict__ gain, float eps,
-                                              int T, uint16_t* s_x) {
-  constexpr int K = 1024;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+// load() issues the loads of all kMaxRows rows of x (rows from T on are in the
+// buffer and never stored: the loads need not wait for the step descriptor's T),
+// store() waits for them and writes rows 0 .. T - 1.
+struct F16NormRows {
   v4f raw[4][4], gv[4];
+
+  __device__ __forceinline__ void load(const float* __restrict__ x, const float* __restrict__ gain) {
+    constexpr int K = 1024;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = min(wave + 4 * j, T - 1);
+    for (int j = 0; j < 4; ++j) {
+      const int t = wave + 4 * j;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) raw[j][i] = *(const v4f*)(x + (size_t)t * K + 16 * lane + 4 * i);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) gv[i] = *(const v4f*)(gain + 16 * lane + 4 * i);
-  double sq[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-  for (int e = 0; e < 16; ++e)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sq[j] += (double)__fmul_rn(raw[j][e >> 2][e & 3], raw[j][e >> 2][e & 3]);
-  wave_sum_d_n<4>(sq);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = wave + 4 * j;
-    if (t >= T) break;
-    const float scale = dev_rms_scale((float)(sq[j] / (double)K), eps);
-    uint32_t h[8];
-#pragma unroll
-    for (int e = 0; e < 16; e += 2) {
-      float y0 = __fmul_rn(__fmul_rn(raw[j][e >> 2][e & 3], scale), gv[e >> 2][e & 3]);
-      float y1 = __fmul_rn(__fmul_rn(raw[j][(e + 1) >> 2][(e + 1) & 3], scale), gv[(e + 1) >> 2][(e + 1) & 3]);
-      // the float products first: the compiler would otherwise fold the last
-      // multiply and the conversion into one fma_mix (one rounding, not two)
-      asm volatile("" : "+v"(y0), "+v"(y1));
-      h[e / 2] = (uint32_t)__half_as_ushort(__float2half_rn(y0)) |
-                 ((uint32_t)__half_as_ushort(__float2half_rn(y1)) << 16);
+      for (int i = 0; i < 4; ++i) raw[j][i] = *(const v4f*)(x + (size_t)t * K + 16 * lane + 4 * i);
     }
-    uint4* dst = (uint4*)(s_x + t * K + 16 * lane);
-    dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
-    dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gv[i] = *(const v4f*)(gain + 16 * lane + 4 * i);
   }
-}
+
+  __device__ __forceinline__ void store(float eps, int T, uint16_t* s_x) {
+    constexpr int K = 1024;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    double sq[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sq[j] += (double)__fmul_rn(raw[j][e >> 2][e & 3], raw[j][e >> 2][e & 3]);
+    wave_sum_d_n<4>(sq);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = wave + 4 * j;
+      if (t >= T) break;
+      const float scale = dev_rms_scale((float)(sq[j] / (double)K), eps);
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) {
+        float y0 = __fmul_rn(__fmul_rn(raw[j][e >> 2][e & 3], scale), gv[e >> 2][e & 3]);
+        float y1 = __fmul_rn(__fmul_rn(raw[j][(e + 1) >> 2][(e + 1) & 3], scale), gv[(e + 1) >> 2][(e + 1) & 3]);
+        // the float products first: the compiler would otherwise fold the last
+        // multiply and the conversion into one fma_mix (one rounding, not two)
+        asm volatile("" : "+v"(y0), "+v"(y1));
+        h[e / 2] = (uint32_t)__half_as_ushort(__float2half_rn(y0)) |
+                   ((uint32_t)__half_as_ushort(__float2half_rn(y1)) << 16);
+      }
+      uint4* dst = (uint4*)(s_x + t * K + 16 * lane);
+      dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
+      dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+    }
+  }
+};
+
+// The f16 activation rows [T][K] copied to LDS: load() issues every load of the
+// thread (all kMaxRows rows of the buffer, without waiting for T), store() writes
+// rows 0 .. T - 1 (one memory round trip).
+template <int K>
+struct F16StageRows {
+  static constexpr int kPieces = kMaxRows * K / 8 / 256;
+  v4i r[kPieces];
+
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ xh) {
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) r[j] = ((const v4i*)xh)[(int)threadIdx.x + 256 * j];
+  }
+
+  __device__ __forceinline__ void store(int T, uint16_t* s_x) {
+    const int n = T * K / 8;
+#pragma unroll
+    for (int j = 0; j < kPieces; ++j) {
+      const int i = (int)threadIdx.x + 256 * j;
+      if (i < n) ((v4i*)s_x)[i] = r[j];
+    }
+  }
+};
 
 // EPI 0: store, 1: residual add, 2: silu(W x) * (W2 x) written as f16 (the
 // down projection's vec_dot_type: out then holds f16 rows [T][n], in place of
 // the float rows and their conversion by k_act_f16, which gives the same bits).
 // NORM (K = 1024): the activation is RMSNorm(xn) * gain of the residual rows xn,
-// computed here (f16_norm_rows) instead of by a k_act_f16 launch before.
+// computed here (F16NormRows) instead of by a k_act_f16 launch before.
 template <int EPI, int SEG, int NR, bool NORM = false>
 __global__ void __launch_bounds__(256)
 k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int n,
@@ -1145,31 +1226,39 @@ k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
   extern __shared__ v4i f16_lds_v4[];
   uint16_t* s_x = (uint16_t*)f16_lds_v4;
   const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float* s_p = (float*)(s_x + kMaxRows * K) + wave * (NM * NR * kMaxRows * 65);
+  float* s_p = (float*)(s_x + kMaxRows * K) + wave * (NM * NR * kMaxRows * kF16PStride);
   const int ngroups = (n + NR - 1) / NR, nwaves = gridDim.x * 4;
   const uint16_t* base[NM];
   base[0] = (const uint16_t*)w;
   if (NM == 2) base[NM - 1] = (const uint16_t*)w2;
-  int g = blockIdx.x * 4 + wave;
-  F16Group<SEG, NM, NR> bt;
-  f16_load<SEG, NM, NR>(base, n, g * NR, bt);  // in flight during the staging
-  if constexpr (NORM)
-    f16_norm_rows(xn, gain, eps, T, s_x);
-  else
-    stage_pieces<kMaxRows * K / 8 / 256>((const v4i*)xh, T * K / 8, threadIdx.x, 256,
-                                         [&](int i) { return (v4i*)s_x + i; });
-  __syncthreads();
   const int r = lane >> 4, t = lane & 15;
-  for (; g < ngroups; g += nwaves) {
+  int g = blockIdx.x * 4 + wave;
+  typename std::conditional<NORM, F16NormRows, F16StageRows<K>>::type act;
+  if constexpr (NORM)
+    act.load(xn, gain);
+  else
+    act.load(xh);
+  F16Group<SEG, NM, NR> bt;
+  f16_load<SEG, NM, NR>(base, n, g * NR, bt);
+  float old = 0.0f;  // EPI 1: the value the first group's output adds to
+  if (EPI == 1 && g < ngroups && r < NR && t < T && g * NR + r < n) old = out[(size_t)t * n + g * NR + r];
+  if constexpr (NORM)
+    act.store(eps, T, s_x);
+  else
+    act.store(T, s_x);
+  __syncthreads();
+  for (bool first = true; g < ngroups; g += nwaves, first = false) {
     const F16Group<SEG, NM, NR> cur = bt;
+    const int row = g * NR + r;
+    const bool mine = r < NR && t < T && row < n;
+    if (EPI == 1 && !first && mine) old = out[(size_t)t * n + row];
     if (g + nwaves < ngroups) f16_load<SEG, NM, NR>(base, n, (g + nwaves) * NR, bt);
     float res[NM];
     f16_group<SEG, NM, NR>(cur, s_x, T, s_p, res);
-    const int row = g * NR + r;
-    if (r < NR && t < T && row < n) {
+    if (mine) {
       float* dst = out + (size_t)t * n + row;
       if (EPI == 0) *dst = res[0];
-      else if (EPI == 1) *dst = __fadd_rn(*dst, res[0]);
+      else if (EPI == 1) *dst = __fadd_rn(old, res[0]);
       else {
         // the float product first: the compiler would otherwise fold the multiply
         // and the conversion into one fma_mix, rounding once instead of twice
@@ -1193,7 +1282,7 @@ k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
   extern __shared__ v4i f16_lds_v4[];
   uint16_t* s_x = (uint16_t*)f16_lds_v4;
   const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float* s_p = (float*)(s_x + kMaxRows * K) + wave * (NR * kMaxRows * 65);
+  float* s_p = (float*)(s_x + kMaxRows * K) + wave * (NR * kMaxRows * kF16PStride);
   const bool pen = desc->penalty > 1.0f;
   const float penalty = desc->penalty;
   const bool write_logits = desc->write_logits != 0;
@@ -1240,7 +1329,7 @@ k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
 }
 
 // weight rows per wave and group of the f16 GEMM (NM * NR * 16 partial rows of LDS per wave)
-constexpr int f16_nr(int epi, int seg) { return seg == 16 ? (epi == 2 ? 2 : 4) : 1; }
+constexpr int f16_nr(int epi, int seg) { return seg == 16 ? (epi == 2 ? 3 : 4) : 1; }
 // at most one workgroup per CU (its LDS admits no second): more groups go to the
 // waves' loops, with the next group in flight, instead of a second round of
 // workgroups that would stage the activation again
