@@ -68,6 +68,28 @@ __device__ __forceinline__ float dev_rms_scale(float mean, float eps) {
   return __fdiv_rn(1.0f, dev_sqrtf(__fadd_rn(mean, eps)));
 }
 
+// The RMSNorm scales dev_rms_scale(s[j] / K) of N rows whose double sums of
+// squares every lane of the wave holds: lane j < N evaluates row j's (the same
+// operations in any lane), every lane reads them back. N times fewer instructions
+// than each lane evaluating all N. Every lane of the wave must be active.
+template <int N, int K>
+__device__ __forceinline__ void rms_scales(const double (&s)[N], float eps, float (&scale)[N]) {
+  static_assert(N <= 64, "one row per lane");
+  const int lane = threadIdx.x & 63;
+  double mine = s[0];
+#pragma unroll
+  for (int j = 1; j < N; ++j) mine = lane == j ? s[j] : mine;
+  const int sc = __builtin_bit_cast(int, dev_rms_scale((float)(mine / (double)K), eps));
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    // held in a vector register: N scalar registers live through the row loop
+    // would add to the scalar spills of the larger kernels
+    float v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, j));
+    asm volatile("" : "+v"(v));
+    scale[j] = v;
+  }
+}
+
 // silu(g) * u with the canonical exp and a correctly rounded division.
 // erf by its Maclaurin series in double, a fixed number of terms per range of
 // |z| (the oracle evaluates the same operations); +-1 from |z| >= 4. The

@@ -1165,11 +1165,13 @@ struct F16NormRows {
 #pragma unroll
       for (int j = 0; j < 4; ++j) sq[j] += (double)__fmul_rn(raw[j][e >> 2][e & 3], raw[j][e >> 2][e & 3]);
     wave_sum_d_n<4>(sq);
+    float sc[4];
+    rms_scales<4, K>(sq, eps, sc);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int t = wave + 4 * j;
       if (t >= T) break;
-      const float scale = dev_rms_scale((float)(sq[j] / (double)K), eps);
+      const float scale = sc[j];
       uint32_t h[8];
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {

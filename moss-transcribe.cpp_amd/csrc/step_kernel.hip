@@ -528,13 +528,18 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv_in)[1
 #pragma unroll
       for (int j = 0; j < 2; ++j) s[j] += (double)__fmul_rn(v[j][e], v[j][e]);
     wave_sum_d_n<2>(s);
+    float scale[2];
+    if constexpr (COAL) {
+      rms_scales<2, cH>(s, eps, scale);
+    } else {  // the 16-row variant: every lane evaluates them (fewer scalar spills there)
+      scale[0] = dev_rms_scale((float)(s[0] / (double)cH), eps);
+      scale[1] = dev_rms_scale((float)(s[1] / (double)cH), eps);
+    }
     float y[2][16];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const float scale = dev_rms_scale((float)(s[j] / (double)cH), eps);
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) y[j][e] = __fmul_rn(__fmul_rn(v[j][e], scale), gv[e]);
-    }
+      for (int e = 0; e < 16; ++e) y[j][e] = __fmul_rn(__fmul_rn(v[j][e], scale[j]), gv[e]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int t = t0 + 4 * j;
@@ -716,12 +721,18 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
 #pragma unroll
   for (int j = 0; j < NS; ++j) sq[j] = (double)__fmul_rn(x0[j], x0[j]) + (double)__fmul_rn(x1[j], x1[j]);
   wave_sum_d_n<NS>(sq);
+  float scale[NS];
+  if constexpr (NS <= 6) {
+    rms_scales<NS, cHD>(sq, P.eps, scale);
+  } else {  // the 16-row variant: every lane evaluates them (fewer scalar spills there)
+#pragma unroll
+    for (int j = 0; j < NS; ++j) scale[j] = dev_rms_scale((float)(sq[j] / (double)cHD), P.eps);
+  }
   float y0[NS], y1[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
-    const float scale = dev_rms_scale((float)(sq[j] / (double)cHD), P.eps);
-    const float n0 = __fmul_rn(__fmul_rn(x0[j], scale), g0[j]);
-    const float n1 = __fmul_rn(__fmul_rn(x1[j], scale), g1[j]);
+    const float n0 = __fmul_rn(__fmul_rn(x0[j], scale[j]), g0[j]);
+    const float n1 = __fmul_rn(__fmul_rn(x1[j], scale[j]), g1[j]);
     y0[j] = __fsub_rn(__fmul_rn(n0, rc[j]), __fmul_rn(n1, rs[j]));
     y1[j] = __fadd_rn(__fmul_rn(n0, rs[j]), __fmul_rn(n1, rc[j]));
   }
