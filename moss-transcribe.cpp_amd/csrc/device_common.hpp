@@ -68,28 +68,6 @@ __device__ __forceinline__ float dev_rms_scale(float mean, float eps) {
   return __fdiv_rn(1.0f, dev_sqrtf(__fadd_rn(mean, eps)));
 }
 
-// The RMSNorm scales dev_rms_scale(s[j] / K) of N rows whose double sums of
-// squares every lane of the wave holds: lane j < N evaluates row j's (the same
-// operations in any lane), every lane reads them back. N times fewer instructions
-// than each lane evaluating all N. Every lane of the wave must be active.
-template <int N, int K>
-__device__ __forceinline__ void rms_scales(const double (&s)[N], float eps, float (&scale)[N]) {
-  static_assert(N <= 64, "one row per lane");
-  const int lane = threadIdx.x & 63;
-  double mine = s[0];
-#pragma unroll
-  for (int j = 1; j < N; ++j) mine = lane == j ? s[j] : mine;
-  const int sc = __builtin_bit_cast(int, dev_rms_scale((float)(mine / (double)K), eps));
-#pragma unroll
-  for (int j = 0; j < N; ++j) {
-    // held in a vector register: N scalar registers live through the row loop
-    // would add to the scalar spills of the larger kernels
-    float v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, j));
-    asm volatile("" : "+v"(v));
-    scale[j] = v;
-  }
-}
-
 // silu(g) * u with the canonical exp and a correctly rounded division.
 // erf by its Maclaurin series in double, a fixed number of terms per range of
 // |z| (the oracle evaluates the same operations); +-1 from |z| >= 4. The
@@ -454,6 +432,68 @@ __device__ __forceinline__ void wave_sum_d_n(double* v) {
 #pragma unroll
   for (int i = 0; i < N; ++i) v[i] += dpp_d<kDppRor1>(v[i]);
 }
+// a + b of the members of every (lane, lane ^ O) pair of two double registers
+// at once (O = 32: half-wave swap, O = 16: swap of 16-lane rows): lanes whose
+// bit O is clear end with a's pair sum, the others with b's.
+template <int O>
+__device__ __forceinline__ double swap_add_d(double a, double b) {
+  const uint64_t ab = (uint64_t)__double_as_longlong(a), bb = (uint64_t)__double_as_longlong(b);
+  uint32_t lo[2], hi[2];
+  if constexpr (O == 32) {
+    const auto l = __builtin_amdgcn_permlane32_swap((uint32_t)ab, (uint32_t)bb, false, false);
+    const auto h = __builtin_amdgcn_permlane32_swap((uint32_t)(ab >> 32), (uint32_t)(bb >> 32), false, false);
+    lo[0] = l[0], lo[1] = l[1], hi[0] = h[0], hi[1] = h[1];
+  } else {
+    static_assert(O == 16, "swap_add_d: 16 or 32");
+    const auto l = __builtin_amdgcn_permlane16_swap((uint32_t)ab, (uint32_t)bb, false, false);
+    const auto h = __builtin_amdgcn_permlane16_swap((uint32_t)(ab >> 32), (uint32_t)(bb >> 32), false, false);
+    lo[0] = l[0], lo[1] = l[1], hi[0] = h[0], hi[1] = h[1];
+  }
+  return __longlong_as_double((long long)(((uint64_t)hi[0] << 32) | lo[0])) +
+         __longlong_as_double((long long)(((uint64_t)hi[1] << 32) | lo[1]));
+}
+
+// The RMSNorm scales dev_rms_scale(S_j / K) of N rows (N even), S_j the wave sum
+// of the lanes' double partials v[j] in wave_sum_d's pairing. The rows travel
+// packed across the lanes: one half-wave swap reduces rows 2k and 2k + 1 together
+// (row 2k then in lanes 0-31, row 2k + 1 in 32-63), one row swap two such
+// registers (four rows, one per 16-lane row: 4q, 4q + 2, 4q + 1, 4q + 3), the DPP
+// steps the rest. Lane q of each 16-lane row evaluates register q's scale there
+// (the same operations in any lane); every lane reads the N scales back. Every
+// lane of the wave must be active.
+template <int N, int K>
+__device__ __forceinline__ void rms_scales(const double (&v)[N], float eps, float (&scale)[N]) {
+  static_assert(N % 2 == 0 && N <= 32, "an even number of rows, at most 32");
+  constexpr int P = N / 2, Q = (P + 1) / 2;
+  double a[P], r[Q];
+#pragma unroll
+  for (int k = 0; k < P; ++k) a[k] = swap_add_d<32>(v[2 * k], v[2 * k + 1]);
+#pragma unroll
+  for (int q = 0; q < Q; ++q) r[q] = 2 * q + 1 < P ? swap_add_d<16>(a[2 * q], a[2 * q + 1]) : pair_add_d<16>(a[2 * q]);
+#pragma unroll
+  for (int q = 0; q < Q; ++q) r[q] += dpp_d<kDppRor8>(r[q]);
+#pragma unroll
+  for (int q = 0; q < Q; ++q) r[q] += dpp_d<kDppRor4>(r[q]);
+#pragma unroll
+  for (int q = 0; q < Q; ++q) r[q] += dpp_d<kDppRor2>(r[q]);
+#pragma unroll
+  for (int q = 0; q < Q; ++q) r[q] += dpp_d<kDppRor1>(r[q]);
+  const int lane = threadIdx.x & 63;
+  double mine = r[0];
+#pragma unroll
+  for (int q = 1; q < Q; ++q) mine = (lane & 15) == q ? r[q] : mine;
+  const int sc = __builtin_bit_cast(int, dev_rms_scale((float)(mine / (double)K), eps));
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int w = j % 4, src = j / 4 + (w == 0 ? 0 : w == 1 ? 32 : w == 2 ? 16 : 48);
+    // held in a vector register: N scalar registers live through the row loop
+    // would add to the scalar spills of the larger kernels
+    float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(sc, src));
+    asm volatile("" : "+v"(x));
+    scale[j] = x;
+  }
+}
+
 template <int N>
 __device__ __forceinline__ void wave_sum_f_n(float* v) {
 #pragma unroll

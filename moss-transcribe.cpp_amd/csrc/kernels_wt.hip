@@ -1164,7 +1164,6 @@ struct F16NormRows {
     for (int e = 0; e < 16; ++e)
 #pragma unroll
       for (int j = 0; j < 4; ++j) sq[j] += (double)__fmul_rn(raw[j][e >> 2][e & 3], raw[j][e >> 2][e & 3]);
-    wave_sum_d_n<4>(sq);
     float sc[4];
     rms_scales<4, K>(sq, eps, sc);
 #pragma unroll

@@ -527,14 +527,8 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv_in)[1
     for (int e = 0; e < 16; ++e)
 #pragma unroll
       for (int j = 0; j < 2; ++j) s[j] += (double)__fmul_rn(v[j][e], v[j][e]);
-    wave_sum_d_n<2>(s);
     float scale[2];
-    if constexpr (COAL) {
-      rms_scales<2, cH>(s, eps, scale);
-    } else {  // the 16-row variant: every lane evaluates them (fewer scalar spills there)
-      scale[0] = dev_rms_scale((float)(s[0] / (double)cH), eps);
-      scale[1] = dev_rms_scale((float)(s[1] / (double)cH), eps);
-    }
+    rms_scales<2, cH>(s, eps, scale);
     float y[2][16];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -720,14 +714,8 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
   double sq[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) sq[j] = (double)__fmul_rn(x0[j], x0[j]) + (double)__fmul_rn(x1[j], x1[j]);
-  wave_sum_d_n<NS>(sq);
   float scale[NS];
-  if constexpr (NS <= 6) {
-    rms_scales<NS, cHD>(sq, P.eps, scale);
-  } else {  // the 16-row variant: every lane evaluates them (fewer scalar spills there)
-#pragma unroll
-    for (int j = 0; j < NS; ++j) scale[j] = dev_rms_scale((float)(sq[j] / (double)cHD), P.eps);
-  }
+  rms_scales<NS, cHD>(sq, P.eps, scale);
   float y0[NS], y1[NS];
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
