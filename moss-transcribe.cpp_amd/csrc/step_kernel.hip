@@ -670,8 +670,9 @@ __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
 template <int NS, int KVH>
 __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& Ly, int T, int past, int g,
                                            int r0, int nrows, uint32_t tag, float* q_lds, float* knew,
-                                           float* vnew, bool prof = false) {
-  const int lane = threadIdx.x & 63, ncol = 2 * T;
+                                           float* vnew, bool prof = false, int hsel = -1) {
+  // hsel >= 0: the q rows are those of q head 2 g + hsel only (T of them)
+  const int lane = threadIdx.x & 63, ncol = hsel < 0 ? 2 * T : T;
   constexpr bool f16kv = KVH != 0;
   const Rsrc rq = mk_rsrc(P.qkvt, kMaxRows * cNQKV * 8);
   float x0[NS], x1[NS], g0[NS], g1[NS], rc[NS], rs[NS];
@@ -686,7 +687,7 @@ __device__ __forceinline__ void stage_pass(const StepParams& P, const LayerDev& 
     tt[j] = kind[j] == 0 ? r % T : (kind[j] == 1 ? r - ncol : r - ncol - T);
     g0[j] = g1[j] = rc[j] = rs[j] = 0.0f;
     live[2 * j] = live[2 * j + 1] = r < nrows;
-    const int col = kind[j] == 0 ? (2 * g + r / T) * cHD
+    const int col = kind[j] == 0 ? (2 * g + (hsel < 0 ? r / T : hsel)) * cHD
                                  : (kind[j] == 1 ? (cNH + g) * cHD : (cNH + cNKV + g) * cHD);
     po[2 * j] = (uint32_t)((min(tt[j], kMaxRows - 1) * cNQKV + col + lane) * 8);
     po[2 * j + 1] = po[2 * j] + 64 * 8;
@@ -832,15 +833,19 @@ __device__ __forceinline__ void append_item(const StepParams& P, const LayerDev&
 // [16][132], sp [32][68], the chunk's K [64][132] and V [64][144]. stage: stage the q rows (the first item of a
 // workgroup; later items of the same kv head find them in LDS), with the new k /
 // v rows if stage_new. next_chunk >= 0: the K / V of that chunk of the same head
-// are loaded into kv once this item's operands are out of it.
+// are loaded into kv once this item's operands are out of it. hsel >= 0: the item
+// covers q head 2g + hsel only (its T columns, the partials' columns hsel T + t;
+// another workgroup takes the other head): the last chunk's item is split when
+// free workgroups exist, so that each half norms and ropes 2T rows, not 3T.
 template <int G, int KVH>
 __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& Ly, int T, int past, int g, int chunk,
                                           uint32_t tag, KvRegs& kv, uint8_t* lds, bool self_append, bool prof,
-                                          bool stage, bool stage_new, int next_chunk) {
+                                          bool stage, bool stage_new, int next_chunk, int hsel) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, kl = lane & 15,
             kk = lane >> 4;
   constexpr bool f16kv = KVH != 0;
-  const int kvlen = past + T, ncol = 2 * T, key0 = chunk * kChunk;
+  // ncol local columns; column c of this item is column c + col_off of the chunk's partials
+  const int kvlen = past + T, ncol = hsel < 0 ? 2 * T : T, col_off = hsel == 1 ? T : 0, key0 = chunk * kChunk;
   float* q_lds = (float*)lds;
   float* knew = q_lds + kMaxCols * cQStride;
   float* vnew = knew + kMaxRows * cQStride;
@@ -859,12 +864,15 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
   kv_to_lds<KVH>(kv, ks, vs);
   if (stage) {
     if (!stage_new) {
-      stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol, tag, q_lds, knew, vnew, prof);
+      stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol, tag, q_lds, knew, vnew, prof, hsel);
     } else {
       // q and new k rows are normed and roped; the new v rows are plain copies
       VStage<2 * G> vst;
       stage_v_issue<2 * G>(P, g, T, vst);
-      stage_pass<6 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, tag, q_lds, knew, vnew, prof);
+      if (hsel >= 0)  // T q rows + T k rows: at most 4G per wave (T <= 8 G)
+        stage_pass<4 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, tag, q_lds, knew, vnew, prof, hsel);
+      else
+        stage_pass<6 * G, KVH>(P, Ly, T, past, g, wave, ncol + T, tag, q_lds, knew, vnew, prof);
       if (prof) wmark(P, 1, 14);
       stage_v_finish<2 * G, KVH>(P, T, tag, vst, vnew);
     }
@@ -1012,8 +1020,8 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
 #pragma unroll
       for (int a = 0; a < NC; ++a) row[sp_key_pos(j + LG * a)] = pv[a];
       if (j == 0) {
-        stc1(rml, (uint32_t)(col * 2 * 4), m);
-        stc1(rml, (uint32_t)((col * 2 + 1) * 4), l);
+        stc1(rml, (uint32_t)((col + col_off) * 2 * 4), m);
+        stc1(rml, (uint32_t)(((col + col_off) * 2 + 1) * 4), l);
       }
     }
   }
@@ -1055,7 +1063,7 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int col = ct * 16 + 4 * kk + q;
-          if (col < ncol) stc1(ro, (uint32_t)((col * cHD + d) * 4), acc[ct][h][q]);
+          if (col < ncol) stc1(ro, (uint32_t)(((col + col_off) * cHD + d) * 4), acc[ct][h][q]);
         }
       }
   }
@@ -1417,15 +1425,30 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     att_c0 = (slot % 32) * m;
     att_c1 = min(att_c0 + m, nch);
   }
-  const bool has_attn = n_items <= kNwg ? slot < n_items : att_c0 < nch;
-  // chunks run from the last down: the first one staged holds the new rows if any does
-  const int att_first = att_c1 - 1;
-  const bool att_new = att_c1 * kChunk > past;
+  bool has_attn = n_items <= kNwg ? slot < n_items : att_c0 < nch;
   // KV append helpers: when 8 workgroups hold no attention item, workgroup
   // (n_items + 64 + g) mod 256 appends kv head g's new rows
   const bool helpers = n_items + cNKV <= kNwg;
   const int help_g = (w - n_items - 64 + 2 * kNwg) % kNwg;
   const bool helper = helpers && help_g < cNKV;
+  // split last chunk: when 8 more workgroups are free, kv head g's last chunk (it
+  // holds the new keys) runs as two items, q head 2g on its own workgroup and q head
+  // 2g + 1 on workgroup (n_items + 72 + g) mod 256
+  int att_hsel = -1;
+  if (n_items + 2 * cNKV <= kNwg) {
+    const int split_g = (w - n_items - 64 - cNKV + 3 * kNwg) % kNwg;
+    if (has_attn && att_c0 == nch - 1) att_hsel = 0;
+    if (split_g < cNKV) {
+      has_attn = true;
+      att_g = split_g;
+      att_c0 = nch - 1;
+      att_c1 = nch;
+      att_hsel = 1;
+    }
+  }
+  // chunks run from the last down: the first one staged holds the new rows if any does
+  const int att_first = att_c1 - 1;
+  const bool att_new = att_c1 * kChunk > past;
   const bool od = w < cOTiles;                    // o-proj and down tiles
   const bool gu = w >= cOTiles && w < cOTiles + cGuBlocks;  // gate/up rows 32j..32j+31
   const int n_merge = cNH * T;                    // (head, row) items, in pairs
@@ -1519,7 +1542,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
       for (int ch = att_first; ch >= att_c0; --ch)
         attn_item<G, KVH>(P, Ly, T, past, att_g, ch, c.epoch + ph(l, kPhQkv), kv, lds, !helpers,
                           PROF && l == 1 && P.timing != nullptr && ch == att_first, ch == att_first, att_new,
-                          ch > att_c0 ? ch - 1 : -1);
+                          ch > att_c0 ? ch - 1 : -1, att_hsel);
       publish(c, next_done(l, kPhAttn));
       MARK(P, 3 + 12 * l + 3);
       WMARK(P, l, 3);
