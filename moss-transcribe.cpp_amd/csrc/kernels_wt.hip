@@ -1000,8 +1000,8 @@ struct F16Group {
 
 constexpr int kF16PStride = 68;  // words per partial row (a multiple of 4 for 16-byte reads)
 
-__host__ __device__ constexpr size_t f16_lds_bytes(int K, int nm_nr) {
-  return (size_t)kMaxRows * K * 2 + 4 * (size_t)nm_nr * kMaxRows * kF16PStride * 4;
+__host__ __device__ constexpr size_t f16_lds_bytes(int K, int nm_nr, int nwv = 4) {
+  return (size_t)kMaxRows * K * 2 + (size_t)nwv * nm_nr * kMaxRows * kF16PStride * 4;
 }
 
 // rows past n are clamped to row n - 1 (loaded, never stored): no branches
@@ -1136,19 +1136,23 @@ __device__ __forceinline__ void f16_group(const F16Group<SEG, NM, NR>& g, const 
 // residual rows x: RMSNorm(x) * gain rounded to f16, k_act_f16's arithmetic (lane l
 // sums the squares of elements 16 l .. 16 l + 15 in double, the butterfly, the
 // correctly rounded 1 / sqrt, y = (x * scale) * gain, then f16), written to s_x.
-// Wave w takes rows w, w + 4, w + 8, w + 12, their double sums side by side.
+// Wave w of NWV takes rows w, w + NWV, .. (16 / NWV of them), their double sums
+// side by side.
 // load() issues the loads of all kMaxRows rows of x (rows from T on are in the
 // buffer and never stored: the loads need not wait for the step descriptor's T),
 // store() waits for them and writes rows 0 .. T - 1.
+template <int NWV>
 struct F16NormRows {
-  v4f raw[4][4], gv[4];
+  static constexpr int RW = kMaxRows / NWV;  // rows per wave
+  static_assert(kMaxRows % NWV == 0 && RW % 2 == 0, "an even number of rows per wave");
+  v4f raw[RW][4], gv[4];
 
   __device__ __forceinline__ void load(const float* __restrict__ x, const float* __restrict__ gain) {
     constexpr int K = 1024;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = wave + 4 * j;
+    for (int j = 0; j < RW; ++j) {
+      const int t = wave + NWV * j;
 #pragma unroll
       for (int i = 0; i < 4; ++i) raw[j][i] = *(const v4f*)(x + (size_t)t * K + 16 * lane + 4 * i);
     }
@@ -1159,16 +1163,18 @@ struct F16NormRows {
   __device__ __forceinline__ void store(float eps, int T, uint16_t* s_x) {
     constexpr int K = 1024;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    double sq[4] = {0.0, 0.0, 0.0, 0.0};
+    double sq[RW];
+#pragma unroll
+    for (int j = 0; j < RW; ++j) sq[j] = 0.0;
 #pragma unroll
     for (int e = 0; e < 16; ++e)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sq[j] += (double)__fmul_rn(raw[j][e >> 2][e & 3], raw[j][e >> 2][e & 3]);
-    float sc[4];
-    rms_scales<4, K>(sq, eps, sc);
+      for (int j = 0; j < RW; ++j) sq[j] += (double)__fmul_rn(raw[j][e >> 2][e & 3], raw[j][e >> 2][e & 3]);
+    float sc[RW];
+    rms_scales<RW, K>(sq, eps, sc);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = wave + 4 * j;
+    for (int j = 0; j < RW; ++j) {
+      const int t = wave + NWV * j;
       if (t >= T) break;
       const float scale = sc[j];
       uint32_t h[8];
@@ -1192,21 +1198,21 @@ struct F16NormRows {
 // The f16 activation rows [T][K] copied to LDS: load() issues every load of the
 // thread (all kMaxRows rows of the buffer, without waiting for T), store() writes
 // rows 0 .. T - 1 (one memory round trip).
-template <int K>
+template <int K, int NT>
 struct F16StageRows {
-  static constexpr int kPieces = kMaxRows * K / 8 / 256;
+  static constexpr int kPieces = kMaxRows * K / 8 / NT;
   v4i r[kPieces];
 
   __device__ __forceinline__ void load(const uint16_t* __restrict__ xh) {
 #pragma unroll
-    for (int j = 0; j < kPieces; ++j) r[j] = ((const v4i*)xh)[(int)threadIdx.x + 256 * j];
+    for (int j = 0; j < kPieces; ++j) r[j] = ((const v4i*)xh)[(int)threadIdx.x + NT * j];
   }
 
   __device__ __forceinline__ void store(int T, uint16_t* s_x) {
     const int n = T * K / 8;
 #pragma unroll
     for (int j = 0; j < kPieces; ++j) {
-      const int i = (int)threadIdx.x + 256 * j;
+      const int i = (int)threadIdx.x + NT * j;
       if (i < n) ((v4i*)s_x)[i] = r[j];
     }
   }
@@ -1216,9 +1222,10 @@ struct F16StageRows {
 // down projection's vec_dot_type: out then holds f16 rows [T][n], in place of
 // the float rows and their conversion by k_act_f16, which gives the same bits).
 // NORM (K = 1024): the activation is RMSNorm(xn) * gain of the residual rows xn,
-// computed here (F16NormRows) instead of by a k_act_f16 launch before.
-template <int EPI, int SEG, int NR, bool NORM = false>
-__global__ void __launch_bounds__(256)
+// computed here (F16NormRows) instead of by a k_act_f16 launch before. NWV waves
+// per workgroup (one workgroup per CU: its LDS admits no second).
+template <int EPI, int SEG, int NR, bool NORM = false, int NWV = 4>
+__global__ void __launch_bounds__(64 * NWV)
 k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int n,
            const uint16_t* __restrict__ xh, float* __restrict__ out, const float* __restrict__ xn = nullptr,
            const float* __restrict__ gain = nullptr, float eps = 0.0f) {
@@ -1228,13 +1235,13 @@ k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
   uint16_t* s_x = (uint16_t*)f16_lds_v4;
   const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   float* s_p = (float*)(s_x + kMaxRows * K) + wave * (NM * NR * kMaxRows * kF16PStride);
-  const int ngroups = (n + NR - 1) / NR, nwaves = gridDim.x * 4;
+  const int ngroups = (n + NR - 1) / NR, nwaves = gridDim.x * NWV;
   const uint16_t* base[NM];
   base[0] = (const uint16_t*)w;
   if (NM == 2) base[NM - 1] = (const uint16_t*)w2;
   const int r = lane >> 4, t = lane & 15;
-  int g = blockIdx.x * 4 + wave;
-  typename std::conditional<NORM, F16NormRows, F16StageRows<K>>::type act;
+  int g = blockIdx.x * NWV + wave;
+  typename std::conditional<NORM, F16NormRows<NWV>, F16StageRows<K, 64 * NWV>>::type act;
   if constexpr (NORM)
     act.load(xn, gain);
   else
@@ -1380,14 +1387,20 @@ void gemm_wt(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_
 }
 
 // The f16 GEMM of a K = 1024 matrix whose activation is RMSNorm(x) * gain (EPI 0
-// or 2): the norm runs in the GEMM's workgroups.
+// or 2): the norm runs in the GEMM's workgroups. q|k|v (EPI 0) runs 8 waves of
+// 2 rows per workgroup: two waves per SIMD share the fma issue (a lone wave leaves
+// about half of it idle), measured 6.8 -> 6.4 us at T = 8; gate/up keeps 4 waves
+// of 3 rows per matrix (its 8-wave form, 1 row per matrix, was slower).
+constexpr int f16n_nwv(int epi) { return epi == 2 ? 4 : 8; }
+constexpr int f16n_nr(int epi) { return epi == 2 ? f16_nr(2, 16) : 2; }
+
 template <int EPI>
 void gemm_f16_norm(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_t* w2, int n, const float* x,
                    const float* gain, float eps, float* out) {
-  constexpr int NM = EPI == 2 ? 2 : 1, NR = f16_nr(EPI, 16);
-  const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, kF16GemmWorkgroups);
-  hipLaunchKernelGGL((k_gemm_f16<EPI, 16, NR, true>), dim3(blocks), dim3(256), f16_lds_bytes(1024, NM * NR), s, desc,
-                     w, w2, n, nullptr, out, x, gain, eps);
+  constexpr int NM = EPI == 2 ? 2 : 1, NR = f16n_nr(EPI), NWV = f16n_nwv(EPI);
+  const int blocks = std::min(((n + NR - 1) / NR + NWV - 1) / NWV, kF16GemmWorkgroups);
+  hipLaunchKernelGGL((k_gemm_f16<EPI, 16, NR, true, NWV>), dim3(blocks), dim3(64 * NWV),
+                     f16_lds_bytes(1024, NM * NR, NWV), s, desc, w, w2, n, nullptr, out, x, gain, eps);
 }
 
 }  // namespace
@@ -1415,10 +1428,11 @@ hipError_t prepare_kernels_wt() {
   MTG_F16_ATTR(0, 48) MTG_F16_ATTR(1, 48) MTG_F16_ATTR(2, 48)
 #undef MTG_F16_ATTR
   for (int epi = 0; epi <= 2; epi += 2) {
-    const int nm_nr = epi == 2 ? 2 * f16_nr(2, 16) : f16_nr(0, 16);
+    const int nm_nr = epi == 2 ? 2 * f16n_nr(2) : f16n_nr(0);
     const hipError_t e = hipFuncSetAttribute(
-        epi == 2 ? (const void*)k_gemm_f16<2, 16, f16_nr(2, 16), true> : (const void*)k_gemm_f16<0, 16, f16_nr(0, 16), true>,
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int)f16_lds_bytes(1024, nm_nr));
+        epi == 2 ? (const void*)k_gemm_f16<2, 16, f16n_nr(2), true, f16n_nwv(2)>
+                 : (const void*)k_gemm_f16<0, 16, f16n_nr(0), true, f16n_nwv(0)>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)f16_lds_bytes(1024, nm_nr, epi == 2 ? f16n_nwv(2) : f16n_nwv(0)));
     if (e != hipSuccess) return e;
   }
   return hipFuncSetAttribute((const void*)k_lm_head_f16, hipFuncAttributeMaxDynamicSharedMemorySize,
