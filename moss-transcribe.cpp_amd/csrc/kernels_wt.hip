@@ -1280,13 +1280,16 @@ k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
 
 // f16 lm_head over the rows of the tied embedding, grouped as in k_gemm_f16; per
 // verify row the best 64-bit key (value bits, lowest index on ties) of each
-// workgroup goes to part_keys.
-constexpr int kF16LmNR = 4;
-__global__ void __launch_bounds__(256)
+// workgroup goes to part_keys (kLmWorkgroups slots per verify row: a grid of
+// kLmWorkgroups / PK workgroups writes its key in the first of its PK slots and
+// the smallest key, 0, in the others). NWV waves of NR rows per group.
+constexpr int kF16LmNWV = 8, kF16LmNR = 2, kF16LmBlocks = kLmWorkgroups / 4;  // 98.5 -> 78.5 us at T = 8 (vs 4 waves x 4 rows, 1,024 workgroups)
+template <int NWV, int NR>
+__global__ void __launch_bounds__(64 * NWV)
 k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int vocab,
               const uint16_t* __restrict__ xh, const uint32_t* __restrict__ bitmap, float* __restrict__ logits,
               uint64_t* __restrict__ part_keys) {
-  constexpr int SEG = 16, K = SEG * 64, NR = kF16LmNR;
+  constexpr int SEG = 16, K = SEG * 64, NT = 64 * NWV;
   extern __shared__ v4i f16_lds_v4[];
   uint16_t* s_x = (uint16_t*)f16_lds_v4;
   const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1295,15 +1298,15 @@ k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
   const float penalty = desc->penalty;
   const bool write_logits = desc->write_logits != 0;
   const int words = (vocab + 31) / 32;
-  const int ngroups = (vocab + NR - 1) / NR, nwaves = gridDim.x * 4;
+  const int ngroups = (vocab + NR - 1) / NR, nwaves = gridDim.x * NWV;
   const uint16_t* base[1] = {(const uint16_t*)w};
-  int g = blockIdx.x * 4 + wave;
+  int g = blockIdx.x * NWV + wave;
   // two groups in flight ahead of the one being computed
   F16Group<SEG, 1, NR> bt, bt2;
   f16_load<SEG, 1, NR>(base, vocab, g * NR, bt);
   if (g + nwaves < ngroups) f16_load<SEG, 1, NR>(base, vocab, (g + nwaves) * NR, bt2);
-  stage_pieces<kMaxRows * K / 8 / 256>((const v4i*)xh, T * K / 8, threadIdx.x, 256,
-                                       [&](int i) { return (v4i*)s_x + i; });
+  stage_pieces<kMaxRows * K / 8 / NT>((const v4i*)xh, T * K / 8, threadIdx.x, NT,
+                                      [&](int i) { return (v4i*)s_x + i; });
   __syncthreads();
   const int r = lane >> 4, t = lane & 15;
   uint64_t best = 0;  // lane (r, t): verify row t
@@ -1314,7 +1317,7 @@ k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
     float res[1];
     f16_group<SEG, 1, NR>(cur, s_x, T, s_p, res);
     const int row = g * NR + r;
-    if (t < T && row < vocab) {
+    if (r < NR && t < T && row < vocab) {
       float v = res[0];
       if (write_logits) logits[(size_t)t * vocab + row] = v;
       if (pen && ((bitmap[(size_t)t * words + (row >> 5)] >> (row & 31)) & 1u))
@@ -1323,16 +1326,17 @@ k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
       best = key > best ? key : best;
     }
   }
-  __shared__ uint64_t s_best[4][64];
+  __shared__ uint64_t s_best[NWV][64];
   s_best[wave][lane] = best;
   __syncthreads();
   if ((int)threadIdx.x < T) {
     uint64_t b = 0;
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < 4 * NWV; ++i) {
       const uint64_t c = s_best[i >> 2][(i & 3) * 16 + threadIdx.x];
       b = c > b ? c : b;
     }
-    part_keys[(size_t)blockIdx.x * kMaxRows + threadIdx.x] = b;
+    const int pk = kLmWorkgroups / gridDim.x;
+    for (int k = 0; k < pk; ++k) part_keys[((size_t)blockIdx.x * pk + k) * kMaxRows + threadIdx.x] = k == 0 ? b : 0;
   }
 }
 
@@ -1435,8 +1439,9 @@ hipError_t prepare_kernels_wt() {
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)f16_lds_bytes(1024, nm_nr, epi == 2 ? f16n_nwv(2) : f16n_nwv(0)));
     if (e != hipSuccess) return e;
   }
-  return hipFuncSetAttribute((const void*)k_lm_head_f16, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)f16_lds_bytes(1024, kF16LmNR));
+  return hipFuncSetAttribute((const void*)k_lm_head_f16<kF16LmNWV, kF16LmNR>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)f16_lds_bytes(1024, kF16LmNR, kF16LmNWV));
 }
 
 bool wt_shape_supported(int wtype, int k) {
@@ -1486,7 +1491,8 @@ void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uin
                        const WtAct& act, const uint32_t* bitmap, float* logits, uint64_t* part_keys) {
   const dim3 grid(kLmWorkgroups), block(256);
   if (wtype == MTG_TYPE_F16)
-    hipLaunchKernelGGL(k_lm_head_f16, grid, block, f16_lds_bytes(1024, kF16LmNR), s, desc, w, vocab, act.f16h,
+    hipLaunchKernelGGL((k_lm_head_f16<kF16LmNWV, kF16LmNR>), dim3(kF16LmBlocks), dim3(64 * kF16LmNWV),
+                       f16_lds_bytes(1024, kF16LmNR, kF16LmNWV), s, desc, w, vocab, act.f16h,
                        bitmap, logits, part_keys);
   else if (k == 1024 && vocab % 16 == 0)
     hipLaunchKernelGGL(k_lm_head_q4m<4>, grid, block, q4m_lds_bytes(k), s, desc, w, vocab, act.q8k, bitmap, logits,
