@@ -12,6 +12,9 @@
 #include "oracle.h"
 
 #include <omp.h>
+#ifdef __AVX2__
+#include <immintrin.h>
+#endif
 
 #include <algorithm>
 #include <cmath>
@@ -207,6 +210,39 @@ int32_t q8_block_dot(const BlockQ8& a, const BlockQ8& b) {
   return s;
 }
 
+// Exact int32 dots of nb consecutive 32-element int8 blocks (any order of the
+// integer adds gives the same sum). With AVX2: |w| (as unsigned) times x with
+// w's sign by vpmaddubsw (a pair sum is at most 2 * 128 * 127, no saturation:
+// activation codes lie in [-127, 127]), vpmaddwd to int32, then eight blocks'
+// horizontal sums at once.
+void block_dots(const int8_t* w, const int8_t* x, int nb, int32_t* out) {
+  int b = 0;
+#ifdef __AVX2__
+  const __m256i ones = _mm256_set1_epi16(1);
+  for (; b + 8 <= nb; b += 8) {
+    __m256i s[8];
+    for (int i = 0; i < 8; ++i) {
+      const __m256i wv = _mm256_loadu_si256((const __m256i*)(w + (size_t)(b + i) * 32));
+      const __m256i xv = _mm256_loadu_si256((const __m256i*)(x + (size_t)(b + i) * 32));
+      const __m256i p = _mm256_maddubs_epi16(_mm256_sign_epi8(wv, wv), _mm256_sign_epi8(xv, wv));
+      s[i] = _mm256_madd_epi16(p, ones);
+    }
+    const __m256i h01 = _mm256_hadd_epi32(s[0], s[1]), h23 = _mm256_hadd_epi32(s[2], s[3]);
+    const __m256i h45 = _mm256_hadd_epi32(s[4], s[5]), h67 = _mm256_hadd_epi32(s[6], s[7]);
+    const __m256i h0123 = _mm256_hadd_epi32(h01, h23), h4567 = _mm256_hadd_epi32(h45, h67);
+    // lanes: [0123 low halves | 0123 high halves], the same for 4567
+    const __m256i lo = _mm256_permute2x128_si256(h0123, h4567, 0x20);
+    const __m256i hi = _mm256_permute2x128_si256(h0123, h4567, 0x31);
+    _mm256_storeu_si256((__m256i*)(out + b), _mm256_add_epi32(lo, hi));
+  }
+#endif
+  for (; b < nb; ++b) {
+    int32_t s = 0;
+    for (int j = 0; j < 32; ++j) s += (int32_t)w[(size_t)b * 32 + j] * (int32_t)x[(size_t)b * 32 + j];
+    out[b] = s;
+  }
+}
+
 // mul_mat(q8_0 W, f32 x) as ggml runs it: x quantized to q8_0, then
 // y = sum over blocks of (d_w * d_x) * isum with an exact int32 isum per
 // 32-block. Canonical float order: K in 4 slices of block pairs, even and odd
@@ -215,23 +251,43 @@ void mul_mat_q8(const BlockQ8* w, int k, int n, const float* x, int T, float* y)
   const int nb = k / 32, bps = nb / 2;
   std::vector<BlockQ8> xq((size_t)T * nb);
   for (int t = 0; t < T; ++t) quantize_q8_0_act(x + (size_t)t * k, k, xq.data() + (size_t)t * nb);
-#pragma omp parallel for schedule(static)
-  for (int r = 0; r < n; ++r) {
-    const BlockQ8* wr = w + (size_t)r * nb;
-    for (int t = 0; t < T; ++t) {
-      const BlockQ8* xr = xq.data() + (size_t)t * nb;
-      float e[4], o[4];
-      for (int sl = 0; sl < 4; ++sl) {
-        e[sl] = o[sl] = 0.0f;
-        for (int bp = (bps * sl) / 4; bp < (bps * (sl + 1)) / 4; ++bp) {
-          const int b0 = 2 * bp, b1 = 2 * bp + 1;
-          e[sl] = std::fma((float)q8_block_dot(wr[b0], xr[b0]), h2f(wr[b0].d) * h2f(xr[b0].d), e[sl]);
-          o[sl] = std::fma((float)q8_block_dot(wr[b1], xr[b1]), h2f(wr[b1].d) * h2f(xr[b1].d), o[sl]);
-        }
+  // activation codes and scales unpacked once; per row the weight codes and
+  // scales once, the exact int32 block sums of every row t, then the chains
+  std::vector<int8_t> xc((size_t)T * k);
+  std::vector<float> xd((size_t)T * nb);
+  for (size_t i = 0; i < xq.size(); ++i) {
+    std::memcpy(&xc[i * 32], xq[i].qs, 32);
+    xd[i] = h2f(xq[i].d);
+  }
+#pragma omp parallel
+  {
+    std::vector<int8_t> wc(k);
+    std::vector<float> wd(nb);
+    std::vector<int32_t> isum((size_t)T * nb);
+#pragma omp for schedule(static)
+    for (int r = 0; r < n; ++r) {
+      const BlockQ8* wr = w + (size_t)r * nb;
+      for (int b = 0; b < nb; ++b) {
+        std::memcpy(&wc[(size_t)b * 32], wr[b].qs, 32);
+        wd[b] = h2f(wr[b].d);
       }
-      const float ev = ((e[0] + e[1]) + e[2]) + e[3];
-      const float ov = ((o[0] + o[1]) + o[2]) + o[3];
-      y[(size_t)t * n + r] = ev + ov;
+      for (int t = 0; t < T; ++t) block_dots(wc.data(), &xc[(size_t)t * k], nb, &isum[(size_t)t * nb]);
+      for (int t = 0; t < T; ++t) {
+        const float* xdt = &xd[(size_t)t * nb];
+        const int32_t* is = &isum[(size_t)t * nb];
+        float e[4], o[4];
+        for (int sl = 0; sl < 4; ++sl) {
+          e[sl] = o[sl] = 0.0f;
+          for (int bp = (bps * sl) / 4; bp < (bps * (sl + 1)) / 4; ++bp) {
+            const int b0 = 2 * bp, b1 = 2 * bp + 1;
+            e[sl] = std::fma((float)is[b0], wd[b0] * xdt[b0], e[sl]);
+            o[sl] = std::fma((float)is[b1], wd[b1] * xdt[b1], o[sl]);
+          }
+        }
+        const float ev = ((e[0] + e[1]) + e[2]) + e[3];
+        const float ov = ((o[0] + o[1]) + o[2]) + o[3];
+        y[(size_t)t * n + r] = ev + ov;
+      }
     }
   }
 }
@@ -244,18 +300,23 @@ void mul_mat_f16(const uint16_t* w, int k, int n, const float* x, int T, float* 
   std::vector<float> xh((size_t)T * k);
   for (size_t i = 0; i < xh.size(); ++i) xh[i] = h2f(f2h(x[i]));
   const int seg = k / 64;
-#pragma omp parallel for schedule(static)
-  for (int r = 0; r < n; ++r) {
-    const uint16_t* wr = w + (size_t)r * k;
-    for (int t = 0; t < T; ++t) {
-      const float* xr = xh.data() + (size_t)t * k;
-      float part[64];
-      for (int l = 0; l < 64; ++l) {
-        float acc = 0.0f;
-        for (int e = 0; e < seg; ++e) acc = std::fma(h2f(wr[l * seg + e]), xr[l * seg + e], acc);
-        part[l] = acc;
+#pragma omp parallel
+  {
+    std::vector<float> wf(k);  // the row decoded once
+#pragma omp for schedule(static)
+    for (int r = 0; r < n; ++r) {
+      const uint16_t* wr = w + (size_t)r * k;
+      for (int i = 0; i < k; ++i) wf[i] = h2f(wr[i]);
+      for (int t = 0; t < T; ++t) {
+        const float* xr = xh.data() + (size_t)t * k;
+        float part[64];
+        for (int l = 0; l < 64; ++l) {
+          float acc = 0.0f;
+          for (int e = 0; e < seg; ++e) acc = std::fma(wf[l * seg + e], xr[l * seg + e], acc);
+          part[l] = acc;
+        }
+        y[(size_t)t * n + r] = butterfly64(part);
       }
-      y[(size_t)t * n + r] = butterfly64(part);
     }
   }
 }
@@ -665,21 +726,29 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
     for (int t = 0; t < T; ++t) {
       const int g = h / groups;
       std::vector<float> qv(D), cm(nch), cl(nch), co((size_t)nch * D);
+      // the chunk's K transposed ([d][key]) and V ([key][d]), zeros past kv: the
+      // chains below run over d (scores) and over the keys (P.V) in order, 64
+      // scores or D outputs side by side
+      std::vector<float> kt((size_t)D * 64), vc((size_t)64 * D);
       const float* qh = q.data() + (size_t)t * QN + (size_t)h * D;
       for (int d = 0; d < D; ++d) qv[d] = f16kv ? h2f(f2h(qh[d])) : qh[d];
       for (int c = 0; c < nch; ++c) {
-        float w[64], p[64];
+        for (int j = 0; j < 64; ++j) {
+          const int key = 64 * c + j;
+          const size_t kb = base + ((size_t)g * m.max_seq + key) * D;
+          for (int d = 0; d < D; ++d) {
+            kt[(size_t)d * 64 + j] = key < kv ? kv_get(m, true, kb + d) : 0.0f;
+            vc[(size_t)j * D + d] = key < kv ? kv_get(m, false, kb + d) : 0.0f;
+          }
+        }
+        float s[64], w[64], p[64];
+        for (int j = 0; j < 64; ++j) s[j] = 0.0f;
+        for (int d = 0; d < D; ++d)
+          for (int j = 0; j < 64; ++j) s[j] = std::fma(qv[d], kt[(size_t)d * 64 + j], s[j]);
         float mx = -INFINITY;
         for (int j = 0; j < 64; ++j) {
           const int key = 64 * c + j;
-          if (key < kv && key <= past + t) {
-            const size_t kb = base + ((size_t)g * m.max_seq + key) * D;
-            float s = 0.0f;
-            for (int d = 0; d < D; ++d) s = std::fma(qv[d], kv_get(m, true, kb + d), s);
-            w[j] = s * scale;
-          } else {
-            w[j] = -INFINITY;
-          }
+          w[j] = (key < kv && key <= past + t) ? s[j] * scale : -INFINITY;
           mx = std::max(mx, w[j]);
         }
         for (int j = 0; j < 64; ++j) {
@@ -690,15 +759,10 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
         std::memcpy(pl, p, sizeof(pl));
         cm[c] = mx;
         cl[c] = butterfly64(pl);
-        for (int d = 0; d < D; ++d) {
-          float acc = 0.0f;
-          for (int j = 0; j < 64; ++j) {
-            const int key = 64 * c + j;
-            const float v = key < kv ? kv_get(m, false, base + ((size_t)g * m.max_seq + key) * D + d) : 0.0f;
-            acc = std::fma(p[j], v, acc);
-          }
-          co[(size_t)c * D + d] = acc;
-        }
+        float* oc = &co[(size_t)c * D];
+        for (int d = 0; d < D; ++d) oc[d] = 0.0f;
+        for (int j = 0; j < 64; ++j)
+          for (int d = 0; d < D; ++d) oc[d] = std::fma(p[j], vc[(size_t)j * D + d], oc[d]);
       }
       float M = -INFINITY;
       for (int c = 0; c < nch; ++c) M = std::max(M, cm[c]);
