@@ -719,65 +719,95 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
   const bool f16kv = m.kv_type == MTG_TYPE_F16;
   const int nch = (kv + 63) / 64;
   std::vector<float> o((size_t)T * QN);
-  if (m.order == ORC_ORDER_GGML_GENERIC) attention_generic(m, l, q.data(), T, o.data());
-  else
-#pragma omp parallel for collapse(2) schedule(static)
-  for (int h = 0; h < NH; ++h)
-    for (int t = 0; t < T; ++t) {
-      const int g = h / groups;
-      std::vector<float> qv(D), cm(nch), cl(nch), co((size_t)nch * D);
-      // the chunk's K transposed ([d][key]) and V ([key][d]), zeros past kv: the
-      // chains below run over d (scores) and over the keys (P.V) in order, 64
-      // scores or D outputs side by side
+  if (m.order == ORC_ORDER_GGML_GENERIC) {
+    attention_generic(m, l, q.data(), T, o.data());
+  } else {
+    // per (kv head, chunk): the chunk's K transposed ([d][key]) and V ([key][d])
+    // decoded once, zeros past kv, then every query of the kv head: the chains
+    // run over d (scores) and over the keys (P.V) in order, 64 scores or D
+    // outputs side by side; then per (head, row) the chunks merged in order
+    std::vector<float> qv((size_t)T * QN);
+    for (size_t i = 0; i < qv.size(); ++i) qv[i] = f16kv ? h2f(f2h(q[i])) : q[i];
+    std::vector<float> cm((size_t)NH * T * nch), cl((size_t)NH * T * nch), co((size_t)NH * T * nch * D);
+#pragma omp parallel
+    {
       std::vector<float> kt((size_t)D * 64), vc((size_t)64 * D);
-      const float* qh = q.data() + (size_t)t * QN + (size_t)h * D;
-      for (int d = 0; d < D; ++d) qv[d] = f16kv ? h2f(f2h(qh[d])) : qh[d];
-      for (int c = 0; c < nch; ++c) {
-        for (int j = 0; j < 64; ++j) {
-          const int key = 64 * c + j;
-          const size_t kb = base + ((size_t)g * m.max_seq + key) * D;
-          for (int d = 0; d < D; ++d) {
-            kt[(size_t)d * 64 + j] = key < kv ? kv_get(m, true, kb + d) : 0.0f;
-            vc[(size_t)j * D + d] = key < kv ? kv_get(m, false, kb + d) : 0.0f;
-          }
-        }
-        float s[64], w[64], p[64];
-        for (int j = 0; j < 64; ++j) s[j] = 0.0f;
-        for (int d = 0; d < D; ++d)
-          for (int j = 0; j < 64; ++j) s[j] = std::fma(qv[d], kt[(size_t)d * 64 + j], s[j]);
-        float mx = -INFINITY;
-        for (int j = 0; j < 64; ++j) {
-          const int key = 64 * c + j;
-          w[j] = (key < kv && key <= past + t) ? s[j] * scale : -INFINITY;
-          mx = std::max(mx, w[j]);
-        }
-        for (int j = 0; j < 64; ++j) {
-          p[j] = (mx == -INFINITY || w[j] == -INFINITY) ? 0.0f : exp_c(w[j] - mx);
-          if (f16kv) p[j] = h2f(f2h(p[j]));
-        }
-        float pl[64];
-        std::memcpy(pl, p, sizeof(pl));
-        cm[c] = mx;
-        cl[c] = butterfly64(pl);
-        float* oc = &co[(size_t)c * D];
-        for (int d = 0; d < D; ++d) oc[d] = 0.0f;
-        for (int j = 0; j < 64; ++j)
-          for (int d = 0; d < D; ++d) oc[d] = std::fma(p[j], vc[(size_t)j * D + d], oc[d]);
-      }
-      float M = -INFINITY;
-      for (int c = 0; c < nch; ++c) M = std::max(M, cm[c]);
-      float* oh = o.data() + (size_t)t * QN + (size_t)h * D;
-      for (int d = 0; d < D; ++d) {
-        float L = 0.0f, acc = 0.0f;
+#pragma omp for collapse(2) schedule(dynamic)
+      for (int g = 0; g < NKV; ++g)
         for (int c = 0; c < nch; ++c) {
-          if (cm[c] == -INFINITY) continue;
-          const float f = exp_c(cm[c] - M);
-          L = std::fma(cl[c], f, L);
-          acc = std::fma(co[(size_t)c * D + d], f, acc);
+          float* __restrict__ ktp = kt.data();
+          float* __restrict__ vcp = vc.data();
+          for (int j = 0; j < 64; ++j) {
+            const int key = 64 * c + j;
+            const size_t kb = base + ((size_t)g * m.max_seq + key) * D;
+            if (key >= kv) {
+              for (int d = 0; d < D; ++d) ktp[(size_t)d * 64 + j] = vcp[(size_t)j * D + d] = 0.0f;
+            } else if (m.kv_type == MTG_TYPE_F32) {
+              for (int d = 0; d < D; ++d) {
+                ktp[(size_t)d * 64 + j] = m.k32[kb + d];
+                vcp[(size_t)j * D + d] = m.v32[kb + d];
+              }
+            } else {
+              for (int d = 0; d < D; ++d) {
+                ktp[(size_t)d * 64 + j] = h2f(m.k16[kb + d]);
+                vcp[(size_t)j * D + d] = h2f(m.v16[kb + d]);
+              }
+            }
+          }
+          for (int h = g * groups; h < (g + 1) * groups; ++h)
+            for (int t = 0; t < T; ++t) {
+              const float* qh = &qv[(size_t)t * QN + (size_t)h * D];
+              float s[64], w[64], p[64];
+              for (int j = 0; j < 64; ++j) s[j] = 0.0f;
+              for (int d = 0; d < D; ++d) {
+                const float qd = qh[d];
+                const float* __restrict__ kd = ktp + (size_t)d * 64;
+                for (int j = 0; j < 64; ++j) s[j] = std::fma(qd, kd[j], s[j]);
+              }
+              float mx = -INFINITY;
+              for (int j = 0; j < 64; ++j) {
+                const int key = 64 * c + j;
+                w[j] = (key < kv && key <= past + t) ? s[j] * scale : -INFINITY;
+                mx = std::max(mx, w[j]);
+              }
+              for (int j = 0; j < 64; ++j) {
+                p[j] = (mx == -INFINITY || w[j] == -INFINITY) ? 0.0f : exp_c(w[j] - mx);
+                if (f16kv) p[j] = h2f(f2h(p[j]));
+              }
+              float pl[64];
+              std::memcpy(pl, p, sizeof(pl));
+              const size_t it = ((size_t)h * T + t) * nch + c;
+              cm[it] = mx;
+              cl[it] = butterfly64(pl);
+              float* __restrict__ oc = &co[it * D];
+              for (int d = 0; d < D; ++d) oc[d] = 0.0f;
+              for (int j = 0; j < 64; ++j) {
+                const float pj = p[j];
+                const float* __restrict__ vj = vcp + (size_t)j * D;
+                for (int d = 0; d < D; ++d) oc[d] = std::fma(pj, vj[d], oc[d]);
+              }
+            }
         }
-        oh[d] = acc / L;
-      }
     }
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int h = 0; h < NH; ++h)
+      for (int t = 0; t < T; ++t) {
+        const size_t i0 = ((size_t)h * T + t) * nch;
+        float M = -INFINITY;
+        for (int c = 0; c < nch; ++c) M = std::max(M, cm[i0 + c]);
+        float* oh = o.data() + (size_t)t * QN + (size_t)h * D;
+        for (int d = 0; d < D; ++d) {
+          float L = 0.0f, acc = 0.0f;
+          for (int c = 0; c < nch; ++c) {
+            if (cm[i0 + c] == -INFINITY) continue;
+            const float f = exp_c(cm[i0 + c] - M);
+            L = std::fma(cl[i0 + c], f, L);
+            acc = std::fma(co[(i0 + c) * D + d], f, acc);
+          }
+          oh[d] = acc / L;
+        }
+      }
+  }
   // o-proj + residual, FFN pre-norm, SwiGLU, down + residual
   std::vector<float> ao((size_t)T * H);
   gemm_op(m, m.wo[l].data(), QN, H, o.data(), T, ao.data());
