@@ -282,6 +282,115 @@ k_attn_combine_wt(const StepDesc* __restrict__ desc, AttnWork work, int n_heads,
   }
 }
 
+// The same merge for an f16 o-projection activation, which needs no 256-element
+// block per workgroup: grid (n_heads / 2, 16 rows, 4 quarters of head_dim), one
+// wave per segment, lane (hl, e) = (lane / 32, lane % 32) takes q head
+// 2 blockIdx.x + hl, element 32 blockIdx.z + e. Waves 0 and 1 compute the chunk
+// factors of q heads 2 blockIdx.x and 2 blockIdx.x + 1. Four times the workgroups
+// of k_attn_combine_wt, a quarter of the partial loads each.
+constexpr int kCombDq = 32;
+
+__global__ void __launch_bounds__(64 * kCombSeg)
+k_attn_combine_f16q(const StepDesc* __restrict__ desc, AttnWork work, int n_heads, int max_chunks, WtAct act) {
+  const int g = blockIdx.x, t = blockIdx.y;
+  const int seg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int hl = lane >> 5, d = kCombDq * (int)blockIdx.z + (lane & 31);
+  const int T = desc->T;
+  if (t >= T) return;
+  const int col = hl * T + t;  // q head 2 g + hl shares kv head g
+  const int nch = (desc->past + T + kChunk - 1) / kChunk;
+  constexpr uint32_t so = kMaxCols * kHeadDim * 4, sml = kMaxCols * 2 * 4;  // bytes per chunk
+  const size_t item0 = (size_t)g * max_chunks;
+  // a chunk >= nch reads past num_records: zeros, no memory traffic
+  const auto ro = __builtin_amdgcn_make_buffer_rsrc(work.part_o + item0 * kMaxCols * kHeadDim, 0,
+                                                    (int)(nch * so), 0x00020000);
+  const auto rml = __builtin_amdgcn_make_buffer_rsrc(work.part_ml + item0 * kMaxCols * 2, 0, (int)(nch * sml),
+                                                     0x00020000);
+  __shared__ float s_f[2][kCombPass], s_l[2][kCombPass];
+  __shared__ float s_L[64], s_O[64];
+  // waves 0 and 1 compute M and the chunk factors of q head fh = seg; the (m, l)
+  // of the first pass stay in their registers (one round trip)
+  const bool factors = seg < 2;
+  const int fcol = seg * T + t;
+  constexpr int kMl = kCombPass / 64;
+  float M = -INFINITY, m1[kMl], l1[kMl];
+  if (factors) {
+#pragma unroll
+    for (int i = 0; i < kMl; ++i) {
+      const uint32_t off = (uint32_t)(64 * i + lane) * sml + fcol * 8;
+      const v2u ml = __builtin_amdgcn_raw_buffer_load_b64(rml, off, 0, 0);  // past nch: zeros
+      const bool in = 64 * i + lane < nch;
+      m1[i] = in ? __uint_as_float(ml.x) : -INFINITY;
+      l1[i] = in ? __uint_as_float(ml.y) : 0.0f;
+      M = fmaxf(M, m1[i]);
+    }
+    for (int c0 = kCombPass; c0 < nch; c0 += 64) {
+      const float m = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rml, (c0 + lane) * sml + fcol * 8, 0, 0));
+      M = fmaxf(M, c0 + lane < nch ? m : -INFINITY);
+    }
+    M = wave_max_f(M);
+  }
+  float L = 0.0f, O = 0.0f;
+  for (int p0 = 0; p0 < nch; p0 += kCombPass) {
+    const int c_lo = p0 + seg * kCombPer;
+    float o[kCombPer];
+#pragma unroll
+    for (int i = 0; i < kCombPer; ++i)
+      o[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           ro, (uint32_t)(c_lo + i) * so + (col * kHeadDim + d) * 4, 0, 0));
+    if (factors) {
+#pragma unroll
+      for (int i = 0; i < kMl; ++i) {
+        const int c = 64 * i + lane;
+        float m = m1[i], l = l1[i];
+        if (p0 > 0) {
+          const uint32_t off = (uint32_t)(p0 + c) * sml + fcol * 8;
+          const v2u ml = __builtin_amdgcn_raw_buffer_load_b64(rml, off, 0, 0);
+          const bool in = p0 + c < nch;
+          m = in ? __uint_as_float(ml.x) : -INFINITY;
+          l = in ? __uint_as_float(ml.y) : 0.0f;
+        }
+        s_f[seg][c] = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, M));
+        s_l[seg][c] = l;
+      }
+    }
+    __syncthreads();
+    for (int sg = 0; sg < kCombSeg; ++sg) {
+      if (seg == sg) {
+        if (sg > 0 || p0 > 0) {
+          L = s_L[lane];
+          O = s_O[lane];
+        }
+        // groups of 4 chunks up to the last one; the chunks past nch in the last
+        // group have f = l = o = 0 (exact zero terms)
+        const int n = nch - c_lo;
+        if (n > 0) {
+#pragma unroll
+          for (int i = 0; i < kCombPer; i += 4) {
+            if (i < n) {
+              const v4f f4 = *(const v4f*)&s_f[hl][seg * kCombPer + i];
+              const v4f l4 = *(const v4f*)&s_l[hl][seg * kCombPer + i];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                L = fmaf(l4[j], f4[j], L);
+                O = fmaf(o[i + j], f4[j], O);
+              }
+            }
+          }
+          s_L[lane] = L;
+          s_O[lane] = O;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (seg == 0) {
+    const float val = __fdiv_rn(s_O[lane], s_L[lane]);
+    act.f16h[(size_t)t * n_heads * kHeadDim + g * 256 + hl * kHeadDim + d] = __half_as_ushort(__float2half_rn(val));
+  }
+}
+
 // ------------------------------------------------------------ row dots ----
 // q4_K: lane l takes elements 4(l%8)..+3 of sub-block l/8 of each superblock.
 __device__ __forceinline__ void q4k_row_dots(const uint8_t* __restrict__ wrow, const ActQ8K& a,
@@ -1463,7 +1572,8 @@ void launch_attn_combine_wt(hipStream_t s, int wtype, const StepDesc* desc, Attn
                             int max_chunks, const WtAct& act) {
   const dim3 grid(n_heads / 2, kMaxRows), block(256 * kCombSeg);
   if (wtype == MTG_TYPE_F16)
-    hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_F16>, grid, block, 0, s, desc, work, n_heads, max_chunks, act);
+    hipLaunchKernelGGL(k_attn_combine_f16q, dim3(n_heads / 2, kMaxRows, kHeadDim / kCombDq), dim3(64 * kCombSeg), 0,
+                       s, desc, work, n_heads, max_chunks, act);
   else
     hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_Q4_K>, grid, block, 0, s, desc, work, n_heads, max_chunks, act);
 }
