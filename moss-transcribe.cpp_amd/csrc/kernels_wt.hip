@@ -12,7 +12,8 @@
 //                           tied lm_head + cpu_greedy_choice keys
 //                                                         src/qwen3_decoder.cpp:174-205,
 //                                                         src/cpu_speculative.cpp:39-50
-//   k_attn_combine_wt       the attention's chunk merge, written as the
+//   k_attn_combine_wt / k_attn_combine_f16q
+//                           the attention's chunk merge, written as the
 //                           o-projection's activation     src/qwen3.cpp:172-189
 //   k_embed_wt              get_rows / embed_rows_f32     src/generate.cpp:68-111
 //
