@@ -838,6 +838,9 @@ void orc_quantize_q8_k_act(const float* x, int64_t k, void* blocks) {
 int32_t orc_q8_0_block_dot(const void* a, const void* b) {
   return q8_block_dot(*(const BlockQ8*)a, *(const BlockQ8*)b);
 }
+void orc_q8_0_block_dots(const int8_t* w, const int8_t* x, int32_t nb, int32_t* out) {
+  block_dots(w, x, nb, out);
+}
 void orc_mul_mat(int32_t wtype, const void* w, int32_t k, int32_t n, const float* x, int32_t T,
                  float* y) {
   mul_mat(wtype, w, k, n, x, T, y);

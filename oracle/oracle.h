@@ -86,6 +86,8 @@ float orc_f16_to_f32(uint16_t h);
 void orc_quantize_q8_0_act(const float* x, int64_t k, void* blocks);
 void orc_quantize_q8_k_act(const float* x, int64_t k, void* blocks);
 int32_t orc_q8_0_block_dot(const void* a, const void* b);
+/* the canonical q8_0 GEMM's exact int32 dots of nb consecutive 32-code blocks (x in [-127, 127]) */
+void orc_q8_0_block_dots(const int8_t* w, const int8_t* x, int32_t nb, int32_t* out);
 void orc_mul_mat(int32_t wtype, const void* w, int32_t k, int32_t n, const float* x, int32_t T,
                  float* y);
 /* the same product in ggml's generic scalar order (ORC_ORDER_GGML_GENERIC) */

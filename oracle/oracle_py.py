@@ -56,6 +56,7 @@ SIGNATURES = {
     "orc_set_order": (c_int32, [c_void_p, c_int32]),
     "orc_mul_mat_generic": (None, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
     "orc_q8_0_block_dot": (c_int32, [c_void_p, c_void_p]),
+    "orc_q8_0_block_dots": (None, [c_void_p, c_void_p, c_int32, c_void_p]),
     "orc_mul_mat": (None, [c_int32, c_void_p, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
     "orc_rms_norm": (None, [c_void_p, c_void_p, c_int32, c_float, c_void_p]),
     "orc_rope_neox": (None, [c_void_p, c_int32, c_int32, c_float]),

@@ -51,6 +51,28 @@ def test_q8_0_block_dot_is_the_exact_integer_sum():
     assert L().orc_q8_0_block_dot(mtg.ptr(a), mtg.ptr(b)) == 524288
 
 
+def test_q8_0_gemm_block_dots_are_the_exact_integer_sums():
+    """The GEMM's eight-blocks-at-a-time int8 dots (|w| x sign(w) x in 16-bit pair
+    sums) against the exact sums: weights over the whole int8 range (-128 included),
+    activation codes in [-127, 127] as the q8_0 quantizer makes them, block counts
+    around the eight-block step, and the largest pair sums."""
+    rng = np.random.default_rng(3)
+    for nb in (1, 7, 8, 9, 16, 31, 32, 33, 96):
+        for trial in range(20):
+            w = rng.integers(-128, 128, 32 * nb).astype(np.int8)
+            x = rng.integers(-127, 128, 32 * nb).astype(np.int8)
+            if trial == 0:
+                w[:] = -128
+                x[:] = np.where(np.arange(32 * nb) % 2 == 0, 127, -127)
+            if trial == 1:
+                w[:] = -128
+                x[:] = -127
+            out = np.zeros(nb, np.int32)
+            L().orc_q8_0_block_dots(mtg.ptr(w), mtg.ptr(x), nb, mtg.ptr(out))
+            want = (w.astype(np.int64) * x.astype(np.int64)).reshape(nb, 32).sum(axis=1)
+            assert np.array_equal(out.astype(np.int64), want), (nb, trial)
+
+
 def test_q8_0_activation_quantizer_rules():
     """d = amax/127 stored as f16; codes = round-half-even(x * 127/amax); zero
     blocks give d = 0 and zero codes; |code| <= 127 and the amax element maps to
