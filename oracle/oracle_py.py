@@ -213,7 +213,9 @@ class Oracle:
     """CPU decoder state (orc_model) over a SynthModel's host tensors."""
 
     def __init__(self, model, max_seq, kv_type=mtg.TYPE_F32):
-        self.hp = model.hp
+        # a copy: a parsed file's hyper-parameters live in the file handle's memory
+        self.hp = mtg.Hparams()
+        ctypes.memmove(ctypes.byref(self.hp), ctypes.byref(model.hp), ctypes.sizeof(mtg.Hparams))
         self.kv_type = kv_type
         out = c_void_p()
         rc = lib().orc_create(model.desc, max_seq, kv_type, ctypes.byref(out))

@@ -222,3 +222,67 @@ def test_encoder_tensors_round_trip(tmp_path):
     assert mtg.lib().mtg_encoder_create_from_gguf(os.fsencode(p4), ctypes.byref(enc)) != 0
     assert "must be q8_0" in mtg.lib().mtg_gguf_error(None).decode()
     m.close()
+
+
+def test_hand_assembled_file():
+    """A GGUF v3 file assembled here byte by byte from the published layout (not by
+    tests/gguf_writer.py): header, metadata of several types (a string array, a
+    64-bit integer, general.alignment = 64), two tensor infos whose data offsets are
+    relative to the 64-byte aligned data section. The loader must return each
+    tensor's type, ne and bytes."""
+    import tempfile
+
+    def s(x):
+        return struct.pack("<Q", len(x)) + x
+    kv = [s(b"general.architecture") + struct.pack("<I", 8) + s(b"qwen3"),
+          s(b"tokenizer.ggml.tokens") + struct.pack("<IIQ", 9, 8, 2) + s(b"a") + s(b"bc"),
+          s(b"general.alignment") + struct.pack("<II", 4, 64),
+          s(b"mtd.text.vocab_size") + struct.pack("<IQ", 10, 2)]
+    q8 = bytes(range(68))                                # two q8_0 rows of 32: 2 x 34 bytes
+    f32 = np.arange(3, dtype=np.float32).tobytes()
+    infos = (s(b"w.q8") + struct.pack("<I2QIQ", 2, 32, 2, 8, 0) +
+             s(b"v.f32") + struct.pack("<I1QIQ", 1, 3, 0, 128))
+    head = b"GGUF" + struct.pack("<IQQ", 3, 2, len(kv)) + b"".join(kv) + infos
+    data_start = (len(head) + 63) // 64 * 64
+    blob = head + b"\0" * (data_start - len(head)) + q8 + b"\0" * (128 - len(q8)) + f32
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "hand.gguf")
+        open(path, "wb").write(blob)
+        g = mtg.GgufModel(path, decoder=False)
+        assert mtg.lib().mtg_gguf_n_tensors(g.handle) == 2
+        t, ne, raw = g.tensor("w.q8")
+        assert (t, ne, raw) == (8, [32, 2, 1, 1], q8)
+        t, ne, raw = g.tensor("v.f32")
+        assert (t, ne, raw) == (0, [3, 1, 1, 1], f32)
+        with pytest.raises(KeyError):
+            g.tensor("absent")
+        g.close()
+
+
+@pytest.mark.parametrize("kv_type", [mtg.TYPE_F32, mtg.TYPE_F16], ids=["f32kv", "f16kv"])
+def test_oracle_from_parsed_file_equals_oracle_from_model(model, tmp_path, kv_type):
+    """The decoder description mtg_gguf_model builds from a file drives the oracle
+    to the same hidden rows, logits and choices as the in-memory model it was
+    written from (the device decoder from the same file is compared with this
+    oracle in test_gpu_gguf.py)."""
+    import oracle_py
+
+    path = str(tmp_path / "m.gguf")
+    gguf_writer.write_model(path, model)
+    g = mtg.GgufModel(path)
+    a = oracle_py.Oracle(model, 64, kv_type)
+    b = oracle_py.Oracle(g, 64, kv_type)
+    g.close()
+    rng = np.random.default_rng(5)
+    ids = rng.integers(0, model.hp.vocab, 20)
+    rows = a.embed(ids)
+    assert np.array_equal(b.embed(ids), rows)
+    assert np.array_equal(b.prefill(rows).view(np.uint32), a.prefill(rows).view(np.uint32))
+    tokens = rng.integers(0, model.hp.vocab, 5)
+    ca, ma, ha, la = a.verify(tokens, want_hidden=True, want_logits=True)
+    cb, mb, hb, lb = b.verify(tokens, want_hidden=True, want_logits=True)
+    assert np.array_equal(hb.view(np.uint32), ha.view(np.uint32))
+    assert np.array_equal(lb.view(np.uint32), la.view(np.uint32))
+    assert np.array_equal(cb, ca) and mb == ma
+    a.close()
+    b.close()

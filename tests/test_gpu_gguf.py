@@ -1,8 +1,12 @@
-"""Device decoders built from GGUF files (mtg_create_from_gguf) against decoders
-built from the same seeded model in memory: prefill hidden rows, verify hidden
-rows, logits and choices bit-identical, for q8_0, f16 and q4_K weights, and at
-full size (28 layers, 151,936-row vocabulary) for a q8_0 file named and typed
-the way the reference's converter writes one."""
+"""Device decoders built from GGUF files (mtg_create_from_gguf) against the oracle
+built from the parsed file (mtg_gguf_model's description of the same file): the
+embedding rows, the prefill's hidden rows and KV cache, the verify steps' hidden
+rows, logits and choices, bit for bit, for q8_0, f16 and q4_K weights and both KV
+types, and at full size (28 layers, 151,936-row vocabulary) for a q8_0 file named
+and typed the way the reference's converter writes one
+(src/model_loader.cpp:21-169, scripts/convert_moss_transcribe_to_gguf.py:242-259).
+The encoder read from a file is compared with the oracle's encoder over the same
+seeded model."""
 import os
 import time
 
@@ -11,65 +15,117 @@ import pytest
 
 import gguf_writer
 import mtg
+import oracle_py
 
 pytestmark = pytest.mark.gpu
 
 
-def _same(a, b, what):
-    assert np.array_equal(np.asarray(a).view(np.uint8), np.asarray(b).view(np.uint8)), what
+def _same(got, ref, what):
+    got, ref = np.asarray(got), np.asarray(ref)
+    if np.array_equal(got.view(np.uint8), ref.view(np.uint8)):
+        return
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    raise AssertionError("%s: not bit-identical: %d elements differ, max err %.3g"
+                         % (what, int((got != ref).sum()), err.max()))
 
 
-def _compare(model, path, kv_type, prefix, T):
-    a = mtg.Decoder(model, prefix + 2 * T + 8, kv_type)
-    b = mtg.Decoder.from_gguf(path, prefix + 2 * T + 8, kv_type)
+def _threads():
+    oracle_py.lib().orc_set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+
+
+def _compare_with_oracle(path, kv_type, prefix, T, hp_ref):
+    """The decoder mtg_create_from_gguf builds from `path` against the oracle
+    built from mtg_gguf_model's description of the same file."""
+    g = mtg.GgufModel(path)
     for f in ("hidden", "n_heads", "n_kv_heads", "head_dim", "intermediate", "n_layers", "vocab"):
-        assert getattr(b.hp, f) == getattr(model.hp, f), f
+        assert getattr(g.hp, f) == getattr(hp_ref, f), f
+    max_seq = prefix + 2 * T + 8
+    orc = oracle_py.Oracle(g, max_seq, kv_type)
+    g.close()  # the oracle holds copies of the tensors
+    dec = mtg.Decoder.from_gguf(path, max_seq, kv_type)
     rng = np.random.default_rng(prefix + T)
-    ids = rng.integers(0, model.hp.vocab, prefix)
-    rows = a.embed(ids)
-    _same(b.embed(ids), rows, "embedding rows")
-    _same(b.prefill(rows), a.prefill(rows), "prefill hidden")
-    for _ in range(2):
-        tokens = rng.integers(0, model.hp.vocab, T)
-        c0, m0, h0, l0 = a.verify(tokens, want_hidden=True, want_logits=True)
-        c1, m1, h1, l1 = b.verify(tokens, want_hidden=True, want_logits=True)
-        _same(h1, h0, "verify hidden")
-        _same(l1, l0, "logits")
-        assert np.array_equal(c1, c0) and m1 == m0
-    a.close()
-    b.close()
+    ids = rng.integers(0, hp_ref.vocab, prefix)
+    rows = orc.embed(ids)
+    _same(dec.embed(ids), rows, "embedding rows")
+    _same(dec.prefill(rows), orc.prefill(rows), "prefill hidden")
+    k0, v0 = orc.kv_read(prefix)
+    k1, v1 = dec.kv_read(prefix)
+    _same(k1, k0, "K cache after the prefill")
+    _same(v1, v0, "V cache after the prefill")
+    for step in range(2):
+        tokens = rng.integers(0, hp_ref.vocab, T)
+        hist = rng.integers(0, hp_ref.vocab, 40) if step else ()
+        pen = 1.3 if step else 1.0
+        c0, m0, h0, l0 = orc.verify(tokens, history=hist, penalty=pen, want_hidden=True, want_logits=True)
+        c1, m1, h1, l1 = dec.verify(tokens, history=hist, penalty=pen, want_hidden=True, want_logits=True)
+        _same(h1, h0, "verify hidden, step %d" % step)
+        _same(l1, l0, "logits, step %d" % step)
+        assert np.array_equal(c1, c0) and m1 == m0, "choices, step %d" % step
+    assert dec.past_len == orc.past_len == prefix + 2 * T
+    dec.close()
+    orc.close()
 
 
 @pytest.mark.parametrize("kv_type", [mtg.TYPE_F32, mtg.TYPE_F16], ids=["f32kv", "f16kv"])
 @pytest.mark.parametrize("wtype", [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_Q4_K], ids=["q8_0", "f16", "q4_K"])
-def test_decoder_from_gguf_equals_decoder_from_model(wtype, kv_type, tmp_path):
-    print("decoder from a GGUF file: weight type %d kv %d" % (wtype, kv_type), flush=True)
+def test_decoder_from_gguf_matches_oracle(wtype, kv_type, tmp_path):
+    print("decoder from a GGUF file against the oracle: weight type %d kv %d" % (wtype, kv_type), flush=True)
+    _threads()
     model = mtg.SynthModel(wtype, seed=21, std=0.02, gain_jitter=0.05, n_layers=2, vocab=4096)
     path = str(tmp_path / "m.gguf")
     gguf_writer.write_model(path, model)
-    _compare(model, path, kv_type, 40, 8)
+    hp = model.hp
+    model.close()  # nothing below reads the in-memory model
+    _compare_with_oracle(path, kv_type, 40, 8, hp)
+
+
+def test_decoder_from_gguf_f16_norms_matches_oracle(tmp_path):
+    """Norm gains stored as f16 (the converter's f16 output type) are widened to
+    f32 by the loader; the oracle reads the same widened description."""
+    _threads()
+    model = mtg.SynthModel(mtg.TYPE_Q8_0, seed=22, std=0.02, gain_jitter=0.05, n_layers=2, vocab=4096)
+    path = str(tmp_path / "m16.gguf")
+    gguf_writer.write_model(path, model, f16_norms=True)
+    hp = model.hp
     model.close()
+    _compare_with_oracle(path, mtg.TYPE_F32, 33, 4, hp)
 
 
-def test_full_size_q8_0_file(tmp_path):
+def test_full_size_q8_0_file_matches_oracle(tmp_path):
+    print("full-size q8_0 GGUF against the oracle", flush=True)
+    _threads()
     model = mtg.SynthModel(mtg.TYPE_Q8_0, seed=0, std=0.02, gain_jitter=0.0)
     path = str(tmp_path / "qwen3-0.6b-q8_0.gguf")
     t0 = time.perf_counter()
     gguf_writer.write_model(path, model)
     t1 = time.perf_counter()
     print("full-size q8_0 GGUF: %.0f MB written in %.1f s" % (os.path.getsize(path) / 1e6, t1 - t0), flush=True)
-    _compare(model, path, mtg.TYPE_F32, 100, 8)
+    hp = model.hp
+    assert (hp.n_layers, hp.hidden, hp.vocab) == (28, 1024, 151936)
     model.close()
+    _compare_with_oracle(path, mtg.TYPE_F32, 100, 8, hp)
 
 
-def test_encoder_from_gguf_equals_encoder_from_model(tmp_path):
+class _ParsedEncoder:
+    """mtg_gguf_encoder's description of a file, in the form OracleEncoder reads."""
+
+    def __init__(self, g):
+        self.desc = g.encoder().contents
+        self.hp = self.desc.hp
+        self.rows = (self.hp.n_frames - 1) // 2 + 1
+
+
+def test_encoder_from_gguf_matches_oracle(tmp_path):
     syn = mtg.SynthEncoder(seed=31, n_frames=160, n_layers=2, ffn=2048)
     path = str(tmp_path / "enc.gguf")
     gguf_writer.write_encoder(path, syn)
-    a = mtg.Encoder(syn)
-    b = mtg.Encoder.from_gguf(path)
     mel = syn.mel(seed=32)
-    _same(b.encode(mel), a.encode(mel), "encoder rows")
-    _same(b.adapt(80), a.adapt(80), "adaptor rows")
-    a.close()
+    del syn
+    g = mtg.GgufModel(path, decoder=False)
+    ref = oracle_py.OracleEncoder(_ParsedEncoder(g))  # copies the tensors
+    g.close()
+    b = mtg.Encoder.from_gguf(path)
+    _same(b.encode(mel), ref.encode(mel), "encoder rows")
+    _same(b.adapt(80), ref.adapt(80), "adaptor rows")
     b.close()
+    ref.close()
