@@ -233,6 +233,7 @@ def main():
     hip = ctypes.CDLL("libamdhip64.so")
     hip.hipDeviceSynchronize()
     dec.launch_timing(True)
+    fallbacks0 = dec.step_fallbacks
     t0 = time.perf_counter()
     ids, st = dec.generate_from(st_w.next_seed, 1 << 20, max_steps=steps, max_draft=cfg["K"] - 1,
                                 draft=fn, user=user, prior=ids_w)
@@ -240,6 +241,11 @@ def main():
     elapsed = time.perf_counter() - t0
     dev_ms, launches, past_sum, rows_sum = dec.launch_timing_read()
     dec.launch_timing(False)
+    # steps whose persistent kernel gave up on a bounded wait and ran again on the
+    # per-op kernels (their event time covers both launches)
+    fallbacks = dec.step_fallbacks - fallbacks0
+    if fallbacks:
+        log("WARNING: %d of %d timed steps fell back to the per-op kernels" % (fallbacks, launches))
     n_steps = int(st.target_calls)
     tokens = len(ids)
     log("timed: %d steps, %d tokens in %.3f s (%.1f us per launch)"
@@ -280,9 +286,13 @@ def main():
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
                      "traffic": traffic,
-                     "launch_us": launch_s * 1e6, "launches": launches},
+                     "launch_us": launch_s * 1e6, "launches": launches,
+                     "fallback_steps": fallbacks},
         "source_hash": source_hash(),
     }
+    if fallbacks:
+        out["roofline"]["flag"] = ("%d timed steps reran on the per-op kernels after a bounded wait ran "
+                                   "out; their time includes both launches" % fallbacks)
     if not args.no_cpu:
         try:
             snap = (snap_kv[0], snap_kv[1], ctx_start, st_w.next_seed, ids_w, ids, n_steps, drafter)

@@ -304,7 +304,9 @@ int32_t mtg_step_profile_read(mtg_ctx* ctx, uint64_t* marks, int32_t n);
  * bracketed by two HIP events on the context's stream; the read-out gives the
  * summed event time, the number of timed steps and the sums of their past_len
  * and row counts (so a caller can divide the algorithmic bytes per step by the
- * measured time). Enabling resets the sums. */
+ * measured time). A step whose persistent kernel gave up on a bounded wait counts
+ * once, with the time of the abandoned launch plus that of its rerun on the
+ * per-op kernels (mtg_step_fallbacks counts such steps). Enabling resets the sums. */
 int mtg_launch_timing(mtg_ctx* ctx, int32_t enable);
 int mtg_launch_timing_read(const mtg_ctx* ctx, double* total_ms, int64_t* launches,
                            int64_t* past_sum, int64_t* rows_sum);

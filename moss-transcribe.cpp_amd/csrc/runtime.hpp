@@ -32,6 +32,9 @@ struct Ctx {
   int max_seq = 0, kv_type = MTG_TYPE_F32, past = 0;
   int wtype = MTG_TYPE_Q8_0;  // q8_0: MFMA panel tiles; f16 / q4_K: GGUF rows (kernels_wt.hip)
   int exec = kExecStep;
+  // rocprofv3 collects hardware counters in this process (ROCPROF_COUNTER_COLLECTION):
+  // the per-op kernels then launch one by one instead of from a graph
+  bool counter_collection = false;
   // persistent step kernel
   int nwg = 0;
   bool step_ok = false;  // the persistent step kernel is usable for this model / device
