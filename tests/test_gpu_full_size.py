@@ -3,9 +3,10 @@
 workloads, two verify steps each (the second with the repetition penalty), device
 against the oracle bit for bit.
 
-The cached prefix is seeded random K/V written to both sides (the same rows in
-every layer): the verify arithmetic does not depend on how the cache was filled,
-and prefill parity is covered at small sizes (test_gpu_verify.py)."""
+The cached prefix is seeded random K/V written to both sides, different in every
+layer: the verify arithmetic does not depend on how the cache was filled, and
+prefill parity is covered at small sizes (test_gpu_verify.py) and on the full
+1,600-row prompt (test_gpu_streams.py)."""
 import os
 
 import numpy as np
@@ -50,10 +51,11 @@ def test_full_size_verify_matches_oracle(case):
     dec.set_exec(exec_mode)
     rng = np.random.default_rng(prefix + T)
     dt = np.float32 if kv == mtg.TYPE_F32 else np.float16
-    one = (1, hp.n_kv_heads, prefix, hp.head_dim)
-    k = np.broadcast_to(rng.standard_normal(one, dtype=np.float32).astype(dt), (hp.n_layers,) + one[1:])
-    v = np.broadcast_to((0.5 * rng.standard_normal(one, dtype=np.float32)).astype(dt),
-                        (hp.n_layers,) + one[1:])
+    # distinct seeded rows in every layer, so that a layer reading another layer's
+    # cache (a wrong layer stride or table entry) changes the result
+    shape = (hp.n_layers, hp.n_kv_heads, prefix, hp.head_dim)
+    k = rng.standard_normal(shape, dtype=np.float32).astype(dt)
+    v = (0.5 * rng.standard_normal(shape, dtype=np.float32)).astype(dt)
     orc.kv_write(k, v)
     dec.kv_write(k, v)
     del k, v

@@ -334,6 +334,7 @@ def test_step_kernel_wait_timeout_falls_back_to_per_op_kernels():
     model, orc, dec, rng = _setup(2, 40)
     before = dec.step_fallbacks
     dec.debug_wait_limit(1)
+    dec.launch_timing(True)
     try:
         for T in (8, 5):
             tokens = rng.integers(0, model.hp.vocab, T)
@@ -343,11 +344,56 @@ def test_step_kernel_wait_timeout_falls_back_to_per_op_kernels():
             _close(l1, l0, "logits after the fallback")
             assert np.array_equal(c1, c0) and m1 == m0
             assert dec.past_len == orc.past_len
+        # both steps are timed: each counts once, with the abandoned launch and
+        # the per-op rerun inside its time
+        ms, launches, past_sum, rows_sum = dec.launch_timing_read()
+        assert launches == 2 and rows_sum == 13 and past_sum == 40 + 48 and ms > 0.0
     finally:
+        dec.launch_timing(False)
         dec.debug_wait_limit(0)
-    assert dec.step_fallbacks > before
+    assert dec.step_fallbacks == before + 2
     tokens = rng.integers(0, model.hp.vocab, 8)
     c0, m0, _, l0 = orc.verify(tokens, want_logits=True)
     c1, m1, _, l1 = dec.verify(tokens, want_logits=True)
     _close(l1, l0, "logits with the default bound")
     assert np.array_equal(c1, c0) and m1 == m0
+
+
+@pytest.mark.parametrize("kv_type", [mtg.TYPE_F32, mtg.TYPE_F16], ids=["f32kv", "f16kv"])
+@pytest.mark.parametrize("exec_mode", EXECS, ids=lambda e: EXEC_NAMES[e])
+@pytest.mark.parametrize("prefix", [60, 2100])
+def test_nan_poisoned_discarded_kv_is_never_read(prefix, exec_mode, kv_type):
+    """cpu-lab/moss_speculative_gate.cpp:216-229 poisons a decoder's whole discarded
+    capacity after every commit. Here, before each step, every cache position from
+    past_len on (all layers and heads, both sides) is set to NaN; then T rows are
+    verified, and the rewind keeps part of them. Hidden rows, logits, choices and
+    the appended KV must be finite and bit-identical to the oracle's. Prefix 60
+    puts the new keys across a 64-key chunk boundary; prefix 2,100 runs the step
+    kernel's chunk groups (more than 32 chunks per kv head)."""
+    print("NaN-poisoned discarded KV: prefix %d exec %s kv %d" % (prefix, EXEC_NAMES[exec_mode], kv_type),
+          flush=True)
+    max_seq = prefix + 40
+    model, orc, dec, rng = _setup(2, prefix, kv_type=kv_type, exec_mode=exec_mode, max_seq=max_seq)
+    for step, (T, keep) in enumerate(((8, 3), (5, 5), (16, 1), (4, 2))):
+        past = dec.past_len
+        assert orc.past_len == past
+        k, v = orc.kv_read(max_seq)
+        k[:, :, past:] = np.nan
+        v[:, :, past:] = np.nan
+        orc.kv_write(k, v)
+        dec.kv_write(k, v)
+        orc.rewind(past)
+        dec.rewind(past)
+        tokens = rng.integers(0, model.hp.vocab, T)
+        c0, m0, h0, l0 = orc.verify(tokens, want_hidden=True, want_logits=True)
+        c1, m1, h1, l1 = dec.verify(tokens, want_hidden=True, want_logits=True)
+        assert np.isfinite(h1).all() and np.isfinite(l1).all(), "step %d read a poisoned position" % step
+        _close(h1, h0, "hidden, step %d" % step)
+        _close(l1, l0, "logits, step %d" % step)
+        assert np.array_equal(c1, c0) and m1 == m0
+        k0, v0 = orc.kv_read(past + T)
+        k1, v1 = dec.kv_read(past + T)
+        _close(k1, k0, "K cache, step %d" % step)
+        _close(v1, v0, "V cache, step %d" % step)
+        orc.rewind(past + keep)
+        dec.rewind(past + keep)

@@ -96,6 +96,18 @@ def test_q8_0_activation_quantizer_rules():
     blk[1:6] = [0.5, 1.5, 2.5, -0.5, -3.5]
     qt = oracle_py.quantize_q8_0_act(blk)
     assert qt["qs"][0][:6].tolist() == [127, 0, 2, 2, 0, -4]
+    # the multiplier: x * (127 / amax) (ggml's x86 quantize_row_q8_0) and x * (1 / d)
+    # with d = amax / 127 (ggml's generic rule) round apart on this block: -81.49999
+    # against -81.5, so the oracle's code tells the two rules apart
+    f = np.float32
+    amax, xv = f(0.5413191), f(-0.3473819)
+    x86 = np.rint(xv * (f(127) / amax))
+    generic = np.rint(xv * (f(1) / (amax / f(127))))
+    assert (x86, generic) == (-81.0, -82.0)
+    blk = np.zeros(32, np.float32)
+    blk[0], blk[1] = amax, xv
+    qn = oracle_py.quantize_q8_0_act(blk)
+    assert qn["qs"][0][:2].tolist() == [127, -81]
 
 
 def _q8_matrix(n, k, rng, exp_range=(-2, 1), code_range=(-4, 5)):
