@@ -46,6 +46,14 @@ constexpr int cOTiles = cH / 16;         // 64 (o-proj and down tiles, on workgr
 constexpr int cGuBlocks = cF / 32;       // 96 (gate/up 32-row blocks, on workgroups 64..159)
 constexpr int kMergeWg0 = 160;           // merge items on workgroups 160..255 (then 64..159)
 constexpr int kMergeSlots = kNwg - kMergeWg0 + cGuBlocks;
+// LDS stride of one activation-panel unit (the 1024 code bytes of a block pair as
+// the MFMA B operand): 16 bytes of padding put the 16 units a wave's lanes write at
+// once (a row's 64 half blocks) on different banks; without it every 16-byte
+// write of a panel build was a 32-way bank conflict.
+constexpr int kPanelUnit = 1024 + 16;
+// the panel's f32 block scales: one row of 16 (8 even-, 8 odd-block columns) per
+// unit, 17 floats apart for the same reason
+constexpr int kScaleStride = 17;
 constexpr int cQStride = 132;            // LDS row strides (conflict-free MFMA operand reads)
 constexpr int cPStride = 68;
 constexpr int kStageFloats = cH + cH / 4;  // one padded row image per wave (panel_norm)
@@ -257,8 +265,8 @@ __device__ __forceinline__ void wt_mma(const v4i* a, const uint2* sc, int bp0, i
 #pragma unroll
     for (int cg = 0; cg < G; ++cg) {
       const int bp = bp0 + p;
-      const v4i b = *(const v4i*)(pcodes + ((size_t)(cg * bps + bp)) * 1024 + lane * 16);
-      const float dx = pscales[(size_t)(cg * bps + bp) * 16 + (lane & 15)];
+      const v4i b = *(const v4i*)(pcodes + ((size_t)(cg * bps + bp)) * kPanelUnit + lane * 16);
+      const float dx = pscales[(size_t)(cg * bps + bp) * kScaleStride + (lane & 15)];
       const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[p], b, zero, 0, 0, 0);
 #pragma unroll
       for (int q = 0; q < 4; ++q) acc[cg][q] = fmaf((float)c[q], dw[q] * dx, acc[cg][q]);
@@ -381,6 +389,10 @@ __device__ __forceinline__ void gu_finish(float acc[4][G][4], float* red, float*
   bar();
   const Rsrc rq = mk_rsrc(P.aq, kMaxRows * cF);
   const Rsrc rs = mk_rsrc(P.aqs, kMaxRows * (cF / 32) * 4);
+  // The block's 32 codes of each verify row meet in LDS (the reduction space is
+  // free now) and leave as two 16-byte stores: byte stores from 96 producers
+  // into shared lines cost more to acknowledge and to read back.
+  uint8_t* cl = (uint8_t*)red;
 #pragma unroll
   for (int cg = 0; cg < G; ++cg) {
     const int t = cg * 8 + (lane & 7);
@@ -389,12 +401,17 @@ __device__ __forceinline__ void gu_finish(float acc[4][G][4], float* red, float*
 #pragma unroll
       for (int wv = 1; wv < 4; ++wv) amax = fmaxf(amax, amx[(wv * G + cg) * 16 + (lane & 15)]);
       const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-      const int row = 32 * j + 4 * (lane >> 4) + q;
-      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(int8_t)rintf(__fmul_rn(va[cg], id)), rq, t * cF + row, 0, 16);
-      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(int8_t)rintf(__fmul_rn(vb[cg], id)), rq, t * cF + row + 16, 0,
-                                           16);
+      const int r = 4 * (lane >> 4) + q;
+      cl[t * 32 + r] = (uint8_t)(int8_t)rintf(__fmul_rn(va[cg], id));
+      cl[t * 32 + r + 16] = (uint8_t)(int8_t)rintf(__fmul_rn(vb[cg], id));
       if (wave == 0 && lane < 16) stc1(rs, (uint32_t)((t * (cF / 32) + j) * 4), q8_scale(amax));
     }
+  }
+  bar();
+  if ((int)threadIdx.x < 2 * T) {
+    const int t = threadIdx.x >> 1, h = threadIdx.x & 1;
+    const v4u v = *(const v4u*)(cl + t * 32 + 16 * h);
+    __builtin_amdgcn_raw_buffer_store_b128(v, rq, t * cF + 32 * j + 16 * h, 0, 16);
   }
   bar();
 }
@@ -423,10 +440,10 @@ __device__ __forceinline__ void quant16(const float v[16], int t, int kc, int bp
   }
   const int blk = kc >> 1, half = kc & 1, bp = blk >> 1, par = blk & 1;
   const int cg = t >> 3, j = par * 8 + (t & 7);
-  uint8_t* unit = pcodes + (size_t)(cg * bps + bp) * 1024;
+  uint8_t* unit = pcodes + (size_t)(cg * bps + bp) * kPanelUnit;
   *(uint4*)(unit + (j + 16 * (2 * par + half)) * 16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
   *(uint4*)(unit + (j + 16 * (2 * (1 - par) + half)) * 16) = make_uint4(0u, 0u, 0u, 0u);
-  if (half == 0) pscales[(size_t)(cg * bps + bp) * 16 + j] = __half2float(__float2half_rn(d));
+  if (half == 0) pscales[(size_t)(cg * bps + bp) * kScaleStride + j] = __half2float(__float2half_rn(d));
 }
 
 // Panel of RMSNorm(x) * gain for T rows of 1024 (one wave per row): lane l
@@ -587,10 +604,10 @@ __device__ __forceinline__ void panel_from_q(const int8_t* codes, const float* s
       const int t = c / cpr, kc = c % cpr;
       const int blk = kc >> 1, half = kc & 1, bp = blk >> 1, par = blk & 1;
       const int cg = t >> 3, jc = par * 8 + (t & 7);
-      uint8_t* unit = pcodes + (size_t)(cg * bps + bp) * 1024;
+      uint8_t* unit = pcodes + (size_t)(cg * bps + bp) * kPanelUnit;
       *(uint4*)(unit + (jc + 16 * (2 * par + half)) * 16) = make_uint4(q[j].x, q[j].y, q[j].z, q[j].w);
       *(uint4*)(unit + (jc + 16 * (2 * (1 - par) + half)) * 16) = make_uint4(0u, 0u, 0u, 0u);
-      if (half == 0) pscales[(size_t)(cg * bps + bp) * 16 + jc] = d[j];
+      if (half == 0) pscales[(size_t)(cg * bps + bp) * kScaleStride + jc] = d[j];
     }
   }
   bar();
@@ -1149,10 +1166,15 @@ __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, 
   if (valid) out = __fdiv_rn(O, L);
   // q8_0 blocks of 32 consecutive d (32 lanes of one wave)
   const float amax = group32_max_nonneg(fabsf(out));
+  // the codes of d .. d + 3 packed into lane d (d % 4 == 0) with quad permutes:
+  // one 4-byte store per four lanes instead of byte stores into shared lines
+  const uint32_t code = valid ? q8_code(out, amax) : 0u;
+  const uint32_t packed = code | (dpp_u<0x39>(code) << 8) | (dpp_u<kDppQuadXor2>(code) << 16) |
+                          (dpp_u<0x93>(code) << 24);
   if (valid) {
     const Rsrc rq = mk_rsrc(P.oq, kMaxRows * cQN);
     const Rsrc rs = mk_rsrc(P.oqs, kMaxRows * (cQN / 32) * 4);
-    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)q8_code(out, amax), rq, t * cQN + hq * cHD + d, 0, 16);
+    if ((d & 3) == 0) __builtin_amdgcn_raw_buffer_store_b32(packed, rq, t * cQN + hq * cHD + d, 0, 16);
     if ((d & 31) == 0) stc1(rs, (uint32_t)((t * (cQN / 32) + (hq * cHD + d) / 32) * 4), q8_scale(amax));
   }
 }
@@ -1194,8 +1216,8 @@ __device__ __forceinline__ void lm_head(const StepParams& P, float penalty, bool
   for (int bp = 0; bp < cBH; ++bp)
 #pragma unroll
     for (int cg = 0; cg < G; ++cg) {
-      pb[bp][cg] = *(const v4i*)(pcodes + ((size_t)(cg * cBH + bp)) * 1024 + lane * 16);
-      pdx[bp][cg] = pscales[(size_t)(cg * cBH + bp) * 16 + (lane & 15)];
+      pb[bp][cg] = *(const v4i*)(pcodes + ((size_t)(cg * cBH + bp)) * kPanelUnit + lane * 16);
+      pdx[bp][cg] = pscales[(size_t)(cg * cBH + bp) * kScaleStride + (lane & 15)];
     }
   // A ring of one tile of loads in flight per wave: slot bp holds block pair bp
   // of the tile being computed and is refilled with block pair bp of the next
@@ -1352,8 +1374,9 @@ constexpr size_t kRedBytes = (size_t)4 * 4 * 4 * 64 * 4 + 4 * 16 * 4;
 constexpr size_t kAttnLdsBytes =
     ((size_t)kMaxCols * cQStride + 2 * kMaxRows * cQStride + kMaxCols * cPStride + kKvLdsFloats) * 4;
 __host__ __device__ constexpr size_t step_lds_x_offset(int G) {
-  return ((size_t)G * cBF * (1024 + 64) + kRedBytes * G > kAttnLdsBytes) ? (size_t)G * cBF * (1024 + 64) + kRedBytes * G
-                                                                         : kAttnLdsBytes;
+  return ((size_t)G * cBF * (kPanelUnit + 4 * kScaleStride) + kRedBytes * G > kAttnLdsBytes)
+             ? (size_t)G * cBF * (kPanelUnit + 4 * kScaleStride) + kRedBytes * G
+             : kAttnLdsBytes;
 }
 // after the residual columns: two row images per wave for the norm panel (8-row
 // variant only)
@@ -1397,8 +1420,8 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   if (DEV && T == 0) return;  // the controller has stopped
   const int nch = (past + T + kChunk - 1) / kChunk, n_items = cNKV * nch;
   uint8_t* pcodes = lds;
-  float* pscales = (float*)(lds + (size_t)G * cBF * 1024);
-  float* red = (float*)(lds + (size_t)G * cBF * (1024 + 64));
+  float* pscales = (float*)(lds + (size_t)G * cBF * kPanelUnit);
+  float* red = (float*)(lds + (size_t)G * cBF * (kPanelUnit + 4 * kScaleStride));
   float* xs = (float*)(lds + step_lds_x_offset(G));  // this workgroup's residual columns
   float* stg = (float*)(lds + step_lds_stage_offset(G));
   bool xs_valid = false;
