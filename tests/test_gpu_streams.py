@@ -3,13 +3,18 @@ softmax stress rows through the device attention.
 
 * The 1,600-row prompt of the K=8 q8_0 workload (4 x 375 audio rows + 100 text
   ids) is prefilled on the device and by the oracle: hidden rows and the whole KV
-  cache bit-identical. Then 64 greedy steps with the stream drafter on both sides:
-  identical ids and counters. The top-2 logit margins of the committed stream are
+  cache bit-identical. Then all 256 greedy steps of the workload with the stream
+  drafter on both sides: identical ids and counters. The top-2 logit margins of the committed stream are
   printed, and the choices of the oracle in ggml's generic order are compared with
-  the device's on the same steps (they must agree wherever the margin exceeds the
-  largest logit difference between the two orders).
+  the device's on the first 64 committed rows (they must agree wherever the margin
+  exceeds the largest logit difference between the two orders, and they agree on
+  every one of those rows).
 * The K=16 f16-KV workload at a 4,000-row prompt: 16 greedy steps from the same KV
   state on both sides, identical ids and counters.
+* The f16-weight workload (8,000-row prompt, K=8) and the q4_K workload (16,384-row
+  prompt, K=16), both with an f16 cache, on the per-op kernels: the prompt
+  prefilled on the device, 16 greedy steps on both sides from that KV state,
+  identical ids, counters and appended KV rows.
 * Attention on scores of +-10000 and -inf (tests/test_cpu_softmax.cpp:40-46), made
   by planting keys of magnitude 10^4 in the cache: bit-identical to the oracle.
 """
@@ -40,13 +45,14 @@ def _log(msg):
     print(msg, flush=True)
 
 
-@pytest.mark.timeout(400)
+@pytest.mark.timeout(600)
 def test_full_size_prefill_and_stream_k8_q8_0_ctx1600():
     cfg = CONFIGS[2]
     oracle_py.lib().orc_set_threads(THREADS)
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
     hp = model.hp
-    n_prompt, steps, K = prompt_rows(cfg), 64, cfg["K"]
+    n_prompt, steps, K = prompt_rows(cfg), cfg["steps"], cfg["K"]
+    assert steps == 256
     max_seq = n_prompt + (steps + 4) * K
     dec = mtg.Decoder(model, max_seq, cfg["kv"])
     orc = oracle_py.Oracle(model, max_seq, cfg["kv"])
@@ -82,7 +88,10 @@ def test_full_size_prefill_and_stream_k8_q8_0_ctx1600():
     del k, v
     gen.set_order(gen.ORDER_GGML_GENERIC)
     dec.rewind(n_prompt)
-    seq = np.concatenate([[first], ids1]).astype(np.int32)
+    # the input at position n_prompt + i is committed id i (the first seed is id 0),
+    # and the row of input i chooses id i + 1
+    seq = ids1.astype(np.int32)
+    assert seq[0] == first
     margins, agree, diffs = [], 0, []
     windows = min(8, len(seq) // K)
     for wi in range(windows):
@@ -97,6 +106,9 @@ def test_full_size_prefill_and_stream_k8_q8_0_ctx1600():
         margins.extend(m.tolist())
         safe = m > 2 * d
         assert np.array_equal(c1[safe], c2[safe]), (wi, c1.tolist(), c2.tolist(), m.tolist(), d)
+        # the device's choices are the committed stream's next ids
+        n = min(K, len(seq) - 1 - wi * K)
+        assert np.array_equal(c1[:n], seq[wi * K + 1:wi * K + 1 + n]), wi
         agree += int((c1 == c2).sum())
     gen.close()
     m = np.array(margins)
@@ -104,21 +116,37 @@ def test_full_size_prefill_and_stream_k8_q8_0_ctx1600():
          "device vs generic order: max |dlogit| %.3g, choices equal in %d of %d rows"
          % (len(m), m.min(), np.percentile(m, 1), np.percentile(m, 5), np.median(m), int((m < 0.04).sum()),
             max(diffs), agree, len(m)))
+    # The generic-order oracle run over the whole stream from the same prefill
+    # (tests/order_stream.py, on the CPU) commits the same ids as the canonical
+    # order up to id 165, so every row replayed here chooses the same id in both.
+    assert agree == len(m) == windows * K
     dec.close()
     orc.close()
     model.close()
 
 
-@pytest.mark.timeout(300)
-def test_full_size_stream_k16_f16kv_ctx4000():
-    cfg = CONFIGS[3]
+STREAM16 = [(3, "k16-q8_0-f16kv-ctx4000-step"), (4, "k8-f16-f16kv-ctx8000-graph"),
+            (5, "k16-q4_K-f16kv-ctx16384-graph")]
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("cfg_id", [c for c, _ in STREAM16], ids=[n for _, n in STREAM16])
+def test_full_size_stream_16_steps(cfg_id):
+    """16 greedy steps of a workload at full size from the device's prefilled KV
+    state, on the device and on the oracle: identical ids, counters and appended
+    KV rows. The q8_0 workload runs the persistent step kernel, the f16 and q4_K
+    workloads the per-op kernels from a graph."""
+    cfg = CONFIGS[cfg_id]
     oracle_py.lib().orc_set_threads(THREADS)
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
     n_prompt, steps, K = prompt_rows(cfg), 16, cfg["K"]
     max_seq = n_prompt + (steps + 4) * K
     dec = mtg.Decoder(model, max_seq, cfg["kv"])
+    want_exec = mtg.EXEC_STEP_KERNEL if cfg["wtype"] == mtg.TYPE_Q8_0 else mtg.EXEC_GRAPH
+    dec.set_exec(want_exec)
+    assert dec.exec_mode == want_exec
     rows, text, stream = build_prompt(model, dec.embed, cfg)
-    _log("config-3 stream: device prefill of %d rows" % n_prompt)
+    _log("config-%d stream: device prefill of %d rows" % (cfg_id, n_prompt))
     hid = dec.prefill(rows)
     first = int(np.argmax(dec.logits(hid[-1:])[0]))
     orc = oracle_py.Oracle(model, max_seq, cfg["kv"])
@@ -126,16 +154,19 @@ def test_full_size_stream_k16_f16kv_ctx4000():
     orc.kv_write(k, v)
     del k, v
     fn, user, _keep = mtg.stream_drafter(text, stream)
-    _log("config-3 stream: %d greedy steps on both sides" % steps)
+    _log("config-%d stream: %d greedy steps on both sides" % (cfg_id, steps))
     ids1, st1 = dec.generate_from(first, 1 << 20, max_steps=steps, max_draft=K - 1, draft=fn, user=user)
     ids0, st0 = orc.generate_from(first, 1 << 20, max_steps=steps, max_draft=K - 1, draft=fn, user=user)
     assert ids1.tolist() == ids0.tolist()
-    assert st1.accepted == st0.accepted and st1.proposed == st0.proposed and st1.rewinds == st0.rewinds
+    for f in ("target_calls", "drafted_calls", "proposed", "accepted", "target_input_tokens", "rewinds"):
+        assert getattr(st1, f) == getattr(st0, f), f
+    assert st1.target_calls == steps
+    assert dec.past_len == orc.past_len
     k0, v0 = orc.kv_read(orc.past_len)
     k1, v1 = dec.kv_read(dec.past_len)
     _same(k1[:, :, n_prompt:], k0[:, :, n_prompt:], "K rows appended by the steps")
     _same(v1[:, :, n_prompt:], v0[:, :, n_prompt:], "V rows appended by the steps")
-    _log("config-3 stream: %d ids, %d accepted drafts" % (len(ids1), st1.accepted))
+    _log("config-%d stream: %d ids, %d accepted drafts" % (cfg_id, len(ids1), st1.accepted))
     dec.close()
     orc.close()
     model.close()
