@@ -235,9 +235,10 @@ int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids
  * at the state every 8 steps). Same ids, counters, stop reason and KV position
  * as mtg_generate_from with draft == NULL. No draft or commit hooks; stats carry
  * no draft time (verify_seconds is the whole run). MTG_ERR_UNSUPPORTED unless
- * the step kernel runs this model (q8_0 weights, MTG_EXEC_STEP_KERNEL) and
- * max_draft <= 7. A step abandoned on a bounded wait is finished by the host
- * controller from the same state. */
+ * the step kernel runs this model (q8_0 weights, MTG_EXEC_STEP_KERNEL);
+ * max_draft is clamped to MTG_MAX_BATCH - 1 as in mtg_generate_from (above 7 the
+ * 16-row step kernel runs every step). A step abandoned on a bounded wait is
+ * finished by the host controller from the same state. */
 int mtg_generate_device(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
                         int32_t max_new, int32_t max_steps, int32_t eos, float penalty, int32_t max_draft,
                         int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats);
@@ -254,6 +255,18 @@ typedef struct mtg_stream_drafter {
 } mtg_stream_drafter;
 int32_t mtg_stream_draft(void* user, const int32_t* ids, int32_t n_ids, int32_t budget,
                          int32_t* out);
+
+/* mtg_generate_device with the stream drafter run by the device controller: the
+ * draft hook the reference loop calls every step (CpuSpeculativeHooks::draft,
+ * src/cpu_speculative.cpp:105) as mtg_generate_from calls it with
+ * draft = mtg_stream_draft and user = drafter: the n-gram proposal over
+ * prompt ++ committed ids, completed from the periodic stream. The drafter's
+ * arrays are copied to the device at the call. drafter == NULL: mtg_generate_device.
+ * Same ids, counters, stop reason and KV position as that host loop. */
+int mtg_generate_device_stream(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
+                               int32_t max_new, int32_t max_steps, int32_t eos, float penalty, int32_t max_draft,
+                               const mtg_stream_drafter* drafter, int32_t* ids_out, int32_t* n_ids_out,
+                               mtg_gen_stats* stats);
 
 /* How a step runs on the device. MTG_EXEC_STEP_KERNEL (the default for the
  * Qwen3-0.6B shape on a device with at least 256 CUs): one persistent dataflow

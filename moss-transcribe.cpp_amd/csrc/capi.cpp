@@ -392,6 +392,14 @@ int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids
 int mtg_generate_device(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
                         int32_t max_new, int32_t max_steps, int32_t eos, float penalty, int32_t max_draft,
                         int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats) {
+  return mtg_generate_device_stream(ctx, first_seed, prior_ids, n_prior, max_new, max_steps, eos, penalty, max_draft,
+                                    nullptr, ids_out, n_ids_out, stats);
+}
+
+int mtg_generate_device_stream(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
+                               int32_t max_new, int32_t max_steps, int32_t eos, float penalty, int32_t max_draft,
+                               const mtg_stream_drafter* drafter, int32_t* ids_out, int32_t* n_ids_out,
+                               mtg_gen_stats* stats) {
   if (!ctx) return MTG_ERR_INVALID;
   Ctx& c = ctx->impl;
   if (!ids_out || !n_ids_out || max_new <= 0 || n_prior < 0 || (n_prior > 0 && !prior_ids) || first_seed < 0 ||
@@ -399,6 +407,17 @@ int mtg_generate_device(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_i
     return c.fail(MTG_ERR_INVALID, "generate_device: bad arguments");
   for (int i = 0; i < n_prior; ++i)
     if (prior_ids[i] < 0 || prior_ids[i] >= c.hp.vocab) return c.fail(MTG_ERR_INVALID, "prior id %d", prior_ids[i]);
+  if (drafter && (drafter->n_prompt < 0 || drafter->period < 0 || (drafter->n_prompt > 0 && !drafter->prompt) ||
+                  (drafter->period > 0 && !drafter->stream)))
+    return c.fail(MTG_ERR_INVALID, "generate_device: bad stream drafter");
+  if (drafter) {
+    for (int i = 0; i < drafter->n_prompt; ++i)
+      if (drafter->prompt[i] < 0 || drafter->prompt[i] >= c.hp.vocab)
+        return c.fail(MTG_ERR_INVALID, "drafter prompt id %d", drafter->prompt[i]);
+    for (int i = 0; i < drafter->period; ++i)
+      if (drafter->stream[i] < 0 || drafter->stream[i] >= c.hp.vocab)
+        return c.fail(MTG_ERR_INVALID, "drafter stream id %d", drafter->stream[i]);
+  }
   c.error.clear();
   try {
     mtg::GenState g{};
@@ -412,11 +431,14 @@ int mtg_generate_device(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_i
     g.n_ids = n_prior;
     g.past = c.past;
     g.raw_choice = first_seed;
+    g.n_prompt = drafter ? drafter->n_prompt : 0;
+    g.period = drafter ? drafter->period : 0;
     const int cap = n_prior + max_new + 1;
     std::vector<int32_t> ids((size_t)cap);
     std::copy(prior_ids, prior_ids + n_prior, ids.begin());
     const auto t0 = std::chrono::steady_clock::now();
-    int rc = c.generate_device(g, ids.data(), cap);
+    int rc = c.generate_device(g, ids.data(), cap, drafter ? drafter->prompt : nullptr,
+                               drafter ? drafter->stream : nullptr);
     if (rc) return rc;
     mtg_gen_stats st{};
     st.target_calls = g.target_calls;
@@ -435,7 +457,9 @@ int mtg_generate_device(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_i
       mtg_gen_stats rest{};
       const int left_steps = max_steps > 0 ? max_steps - g.steps : 0;  // >= 1: the abandoned step did not count
       rc = mtg_generate_from(ctx, g.raw_choice, ids.data(), g.n_ids, max_new - n_new, left_steps, eos, penalty,
-                             max_draft, nullptr, nullptr, nullptr, ids.data() + g.n_ids, &more, &rest);
+                             max_draft, drafter ? mtg_stream_draft : nullptr, nullptr,
+                             drafter ? const_cast<mtg_stream_drafter*>(drafter) : nullptr, ids.data() + g.n_ids,
+                             &more, &rest);
       if (rc) return rc;
       n_new += more;
       st.target_calls += rest.target_calls;

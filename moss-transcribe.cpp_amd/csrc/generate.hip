@@ -7,7 +7,9 @@
 //   2. applies the stop rules (:90-98, :109-114): eos, the token limit, a full
 //      KV cache, a step limit;
 //   3. drafts the next step with cpu_ngram_draft (:27-38) over the committed ids
-//      and writes the next step descriptor (seed + drafts, position, repetition
+//      (with the stream drafter: over prompt ++ committed ids, the proposal
+//      completed from a periodic token stream, as mtg_stream_draft does) and
+//      writes the next step descriptor (seed + drafts, position, repetition
 //      penalty window) to device memory.
 // The step kernel's device-descriptor variant reads that descriptor; once the
 // controller stops it writes T = 0 and the remaining launches return at once.
@@ -45,7 +47,8 @@ __device__ __forceinline__ void emit(GenState* g, int32_t* ids, int32_t id) {
 
 __global__ void __launch_bounds__(kGenThreads)
 k_gen_ctrl(GenState* __restrict__ g, int32_t* __restrict__ ids, StepDesc* __restrict__ desc,
-           StepResult* __restrict__ res, const int32_t* __restrict__ step_err) {
+           StepResult* __restrict__ res, const int32_t* __restrict__ step_err, const int32_t* __restrict__ prompt,
+           const int32_t* __restrict__ stream) {
   __shared__ int s_go, s_n, s_budget, s_seed, s_before;
   __shared__ int s_red[kGenThreads / 64];
   __shared__ int32_t s_ids[kGenLdsIds];
@@ -121,21 +124,25 @@ k_gen_ctrl(GenState* __restrict__ g, int32_t* __restrict__ ids, StepDesc* __rest
     if (tid == 0) desc->T = 0;
     return;
   }
-  // 3. cpu_ngram_draft over ids[0, n): the longest suffix n-gram (16 .. 2) that
-  // occurred before, at its latest start; the ids that followed it are the draft
-  const int n = s_n, budget = s_budget;
-  const bool staged = n <= kGenLdsIds;
+  // 3. cpu_ngram_draft over the history h = prompt ++ ids[0, n): the longest
+  // suffix n-gram (16 .. 2) that occurred before, at its latest start; the ids that
+  // followed it are the draft, completed up to the budget from the stream
+  // (position of h's next id + k, modulo the period) when there is one
+  const int n = s_n, budget = s_budget, n_prompt = g->n_prompt, period = g->period;
+  const int nh_all = n_prompt + n;
+  const bool staged = nh_all <= kGenLdsIds;
   if (staged)
-    for (int i = tid; i < n; i += kGenThreads) s_ids[i] = ids[i];
+    for (int i = tid; i < nh_all; i += kGenThreads) s_ids[i] = i < n_prompt ? prompt[i] : ids[i - n_prompt];
   __syncthreads();
-  auto id_at = [&](int i) { return staged ? s_ids[i] : ids[i]; };
+  auto hist_at = [&](int i) { return staged ? s_ids[i] : (i < n_prompt ? prompt[i] : ids[i - n_prompt]); };
+  auto id_at = [&](int i) { return hist_at(n_prompt + i); };  // committed id i
   int begin = -1;
-  if (budget > 0 && n >= 3) {
-    for (int len = min(16, n - 1); len >= 2; --len) {
+  if (budget > 0 && nh_all >= 3) {
+    for (int len = min(16, nh_all - 1); len >= 2; --len) {
       int best = -1;
-      for (int start = n - len - 1 - tid; start >= 0; start -= kGenThreads) {
+      for (int start = nh_all - len - 1 - tid; start >= 0; start -= kGenThreads) {
         bool eq = true;
-        for (int j = 0; j < len && eq; ++j) eq = id_at(start + j) == id_at(n - len + j);
+        for (int j = 0; j < len && eq; ++j) eq = hist_at(start + j) == hist_at(nh_all - len + j);
         if (eq) {
           best = start;  // this thread's starts descend: the first match is its latest
           break;
@@ -148,7 +155,8 @@ k_gen_ctrl(GenState* __restrict__ g, int32_t* __restrict__ ids, StepDesc* __rest
       }
     }
   }
-  const int np = begin >= 0 ? min(budget, n - begin) : 0;
+  const int n_gram = begin >= 0 ? min(budget, nh_all - begin) : 0;
+  const int np = period > 0 ? budget : n_gram;
   // the step descriptor: rows {seed, drafts} at `before`; the penalty window of
   // row i is the last 100 ids before the seed ++ rows 0..i (fill_desc's layout)
   const int T = np + 1, nh = n - 1;
@@ -156,7 +164,10 @@ k_gen_ctrl(GenState* __restrict__ g, int32_t* __restrict__ ids, StepDesc* __rest
   const int pstart = max(0, nh + 1 - kPenaltyWindow);
   const int nwin = nh - pstart;
   if (tid < kMaxRows) {
-    const int32_t tok = tid == 0 ? s_seed : (tid < T ? id_at(begin + tid - 1) : 0);
+    int32_t tok = 0;
+    if (tid == 0) tok = s_seed;
+    else if (tid - 1 < n_gram) tok = hist_at(begin + tid - 1);
+    else if (tid < T) tok = stream[(nh_all + tid - 1) % period];
     desc->tokens[tid] = tok;
     if (tid >= 1 && tid < T) g->proposal[tid - 1] = tok;
     if (pen && tid < T) desc->pen_ids[nwin + tid] = tok;
@@ -166,7 +177,7 @@ k_gen_ctrl(GenState* __restrict__ g, int32_t* __restrict__ ids, StepDesc* __rest
   if (tid == 0) {
     desc->T = T;
     desc->past = s_before;
-    desc->groups = 1;
+    desc->groups = (T + 7) / 8;
     desc->use_embeds = 0;
     desc->penalty = g->penalty;
     desc->n_pen = pen ? nwin + T : 0;
@@ -182,8 +193,8 @@ k_gen_ctrl(GenState* __restrict__ g, int32_t* __restrict__ ids, StepDesc* __rest
 }  // namespace
 
 void launch_gen_ctrl(hipStream_t s, GenState* g, int32_t* ids, StepDesc* desc, StepResult* res_map,
-                     const int32_t* step_err) {
-  k_gen_ctrl<<<1, kGenThreads, 0, s>>>(g, ids, desc, res_map, step_err);
+                     const int32_t* step_err, const int32_t* prompt, const int32_t* stream) {
+  k_gen_ctrl<<<1, kGenThreads, 0, s>>>(g, ids, desc, res_map, step_err, prompt, stream);
 }
 
 }  // namespace mtg

@@ -135,6 +135,6 @@ void launch_embed_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8
 // mapped result buffer the step kernel writes; step_err: its error word), apply
 // the stop rules, draft and write the next descriptor (T = 0 once stopped).
 void launch_gen_ctrl(hipStream_t s, GenState* g, int32_t* ids, StepDesc* desc, StepResult* res_map,
-                     const int32_t* step_err);
+                     const int32_t* step_err, const int32_t* prompt, const int32_t* stream);
 
 }  // namespace mtg

@@ -64,6 +64,10 @@ struct GenState {
   int32_t first_new;  // committed ids before the run (prior ids)
   int32_t max_new, max_steps, eos, max_draft, max_seq;
   float penalty;
+  // the stream drafter (mtg_stream_draft): text ids before generation, prepended to
+  // the committed ids for the n-gram search, and a periodic stream that completes
+  // the proposal (n_prompt = period = 0: the plain n-gram drafter)
+  int32_t n_prompt, period;
   // the controller's state
   int32_t n_ids;       // committed ids
   int32_t past;        // KV position

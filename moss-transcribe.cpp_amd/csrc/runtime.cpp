@@ -32,6 +32,7 @@ Ctx::~Ctx() {
     if (g.exec) hipGraphExecDestroy(g.exec);
   for (void* p : allocations) hipFree(p);
   if (gen_ids_dev) hipFree(gen_ids_dev);
+  if (gen_aux_dev) hipFree(gen_aux_dev);
   if (gen_state_dev) hipFree(gen_state_dev);
   if (gen_state_host) hipHostFree(gen_state_host);
   if (ev_start) hipEventDestroy(ev_start);
@@ -725,11 +726,33 @@ namespace mtg {
 // The controller on the device: [k_gen_ctrl, step kernel] pairs enqueued in
 // chunks of kChunkSteps, the state looked at once per chunk. A step that leaves
 // before its acceptance ends the run with g.err set and that step undone.
-int Ctx::generate_device(GenState& g, int32_t* ids, int cap) {
+int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prompt_ids,
+                         const int32_t* stream_ids) {
   constexpr int kChunkSteps = 8;
   int rc = MTG_OK;
-  if (!step_ok || exec != kExecStep || g.max_draft + 1 > 8)
-    return fail(MTG_ERR_UNSUPPORTED, "device generation needs the step kernel and max_draft <= 7");
+  if (!step_ok || exec != kExecStep || g.max_draft + 1 > kMaxRows)
+    return fail(MTG_ERR_UNSUPPORTED, "device generation needs the step kernel and max_draft <= %d", kMaxRows - 1);
+  // the 16-row step variant when a step can hold more than 8 rows
+  const int G = g.max_draft + 1 > 8 ? 2 : 1;
+  // the stream drafter's prompt ids and stream period, in one device buffer
+  const size_t aux = (size_t)g.n_prompt + (size_t)g.period;
+  if (aux > (size_t)gen_aux_cap) {
+    if (gen_aux_dev) (void)hipFree(gen_aux_dev);
+    gen_aux_dev = nullptr;
+    gen_aux_cap = 0;
+    if ((rc = check(hipMalloc((void**)&gen_aux_dev, aux * 4), "drafter ids"))) return rc;
+    gen_aux_cap = (int)aux;
+  }
+  if (g.n_prompt > 0 &&
+      (rc = check(hipMemcpyAsync(gen_aux_dev, prompt_ids, (size_t)g.n_prompt * 4, hipMemcpyHostToDevice, stream),
+                  "drafter prompt")))
+    return rc;
+  if (g.period > 0 && (rc = check(hipMemcpyAsync(gen_aux_dev + g.n_prompt, stream_ids, (size_t)g.period * 4,
+                                                 hipMemcpyHostToDevice, stream),
+                                  "drafter stream")))
+    return rc;
+  const int32_t* prompt_dev = g.n_prompt > 0 ? gen_aux_dev : nullptr;
+  const int32_t* stream_dev = g.period > 0 ? gen_aux_dev + g.n_prompt : nullptr;
   if (cap > gen_cap) {
     if (gen_ids_dev) (void)hipFree(gen_ids_dev);
     gen_ids_dev = nullptr;
@@ -760,9 +783,10 @@ int Ctx::generate_device(GenState& g, int32_t* ids, int cap) {
       epoch = 0;
     }
     for (int i = 0; i < kChunkSteps; ++i) {
-      launch_gen_ctrl(stream, gen_state_dev, gen_ids_dev, desc_dev, result_map, &result_dev->err);
+      launch_gen_ctrl(stream, gen_state_dev, gen_ids_dev, desc_dev, result_map, &result_dev->err, prompt_dev,
+                      stream_dev);
       if ((rc = check(hipGetLastError(), "controller launch"))) return rc;
-      if ((rc = check(launch_step(stream, 1, kv_f16, params_dev, &unused, epoch, kStepVerify, false, desc_dev),
+      if ((rc = check(launch_step(stream, G, kv_f16, params_dev, &unused, epoch, kStepVerify, false, desc_dev),
                       "step kernel launch")))
         return rc;
       epoch += pps;

@@ -120,8 +120,10 @@ struct Ctx {
   GenState* gen_state_dev = nullptr;  // device copies, grown on demand
   int32_t* gen_ids_dev = nullptr;
   int gen_cap = 0;
+  int32_t* gen_aux_dev = nullptr;  // the stream drafter's prompt ids, then its stream period
+  int gen_aux_cap = 0;
   GenState* gen_state_host = nullptr;  // pinned
-  int generate_device(GenState& g, int32_t* ids, int cap);
+  int generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prompt_ids, const int32_t* stream_ids);
 };
 
 }  // namespace mtg

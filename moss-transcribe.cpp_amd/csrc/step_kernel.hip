@@ -1730,9 +1730,12 @@ const void* step_fn(int G, int kv_f16, bool prof) {
        {(const void*)k_step<2, 1, false>, (const void*)k_step<2, 1, true>}}};
   return fns[G - 1][kv_f16 ? 1 : 0][prof ? 1 : 0];
 }
-// the 8-row variants that read the descriptor from device memory
-const void* step_fn_dev(int kv_f16) {
-  return kv_f16 ? (const void*)k_step<1, 1, false, true> : (const void*)k_step<1, 0, false, true>;
+// the 8- and 16-row variants that read the descriptor from device memory
+const void* step_fn_dev(int G, int kv_f16) {
+  static const void* fns[2][2] = {
+      {(const void*)k_step<1, 0, false, true>, (const void*)k_step<1, 1, false, true>},
+      {(const void*)k_step<2, 0, false, true>, (const void*)k_step<2, 1, false, true>}};
+  return fns[G - 1][kv_f16 ? 1 : 0];
 }
 }  // namespace
 
@@ -1744,22 +1747,23 @@ hipError_t prepare_step_kernels() {
                                                  (int)step_lds_bytes(G));
         if (e != hipSuccess) return e;
       }
-  for (int kv = 0; kv < 2; ++kv) {
-    const hipError_t e = hipFuncSetAttribute(step_fn_dev(kv), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             (int)step_lds_bytes(1));
-    if (e != hipSuccess) return e;
-  }
+  for (int G = 1; G <= 2; ++G)
+    for (int kv = 0; kv < 2; ++kv) {
+      const hipError_t e = hipFuncSetAttribute(step_fn_dev(G, kv), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)step_lds_bytes(G));
+      if (e != hipSuccess) return e;
+    }
   return hipSuccess;
 }
 
 hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
                         uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev) {
   // desc: host memory; the launch copies it into the kernel arguments. desc_dev
-  // (8-row verify only): the kernel reads the descriptor there instead.
+  // (verify steps of up to 8 G rows): the kernel reads the descriptor there instead.
   void* args[] = {(void*)&P, (void*)desc, (void*)&epoch, (void*)&mode, (void*)&desc_dev};
   if (desc_dev) {
-    if (G != 1 || profiled) return hipErrorInvalidValue;
-    return hipLaunchKernel(step_fn_dev(kv_f16), dim3(kNwg), dim3(kT), args, step_lds_bytes(1), s);
+    if (G < 1 || G > 2 || profiled) return hipErrorInvalidValue;
+    return hipLaunchKernel(step_fn_dev(G, kv_f16), dim3(kNwg), dim3(kT), args, step_lds_bytes(G), s);
   }
   const size_t lds = step_lds_bytes(G);
   // A plain launch: one workgroup per CU (the kernel's registers and LDS allow

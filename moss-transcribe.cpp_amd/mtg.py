@@ -92,6 +92,9 @@ SIGNATURES = {
                                POINTER(GenStats)]),
     "mtg_generate_device": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32, c_int32,
                                       c_float, c_int32, c_void_p, POINTER(c_int32), POINTER(GenStats)]),
+    "mtg_generate_device_stream": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32, c_int32,
+                                             c_float, c_int32, c_void_p, c_void_p, POINTER(c_int32),
+                                             POINTER(GenStats)]),
     "mtg_generate_from": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32,
                                     c_int32, c_float, c_int32, c_void_p, c_void_p, c_void_p,
                                     c_void_p, POINTER(c_int32), POINTER(GenStats)]),
@@ -489,15 +492,24 @@ class Decoder:
         del keep
         return out[: n.value].copy(), st
 
-    def generate_device(self, first_seed, max_new, max_steps=0, eos=-1, penalty=1.0, max_draft=4, prior=()):
-        """The speculative controller on the device (reference n-gram drafter)."""
+    def generate_device(self, first_seed, max_new, max_steps=0, eos=-1, penalty=1.0, max_draft=4, prior=(),
+                        stream=None):
+        """The speculative controller on the device: the reference n-gram drafter,
+        or (stream = a stream_drafter() triple) the stream drafter run by the
+        controller kernel (mtg_generate_device_stream)."""
         out = np.empty(max_new, np.int32)
         n = c_int32(0)
         st = GenStats()
         prior = i32(prior)
-        self._chk(lib().mtg_generate_device(self.ctx, first_seed, ptr(prior) if len(prior) else None, len(prior),
-                                            max_new, max_steps, eos, penalty, max_draft, ptr(out),
-                                            ctypes.byref(n), ctypes.byref(st)))
+        if stream is None:
+            self._chk(lib().mtg_generate_device(self.ctx, first_seed, ptr(prior) if len(prior) else None,
+                                                len(prior), max_new, max_steps, eos, penalty, max_draft, ptr(out),
+                                                ctypes.byref(n), ctypes.byref(st)))
+        else:
+            _fn, user, _keep = stream
+            self._chk(lib().mtg_generate_device_stream(self.ctx, first_seed, ptr(prior) if len(prior) else None,
+                                                       len(prior), max_new, max_steps, eos, penalty, max_draft,
+                                                       user, ptr(out), ctypes.byref(n), ctypes.byref(st)))
         return out[: n.value].copy(), st
 
 

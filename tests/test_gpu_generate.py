@@ -69,6 +69,58 @@ def test_device_loop_equals_host_loop_and_oracle(penalty, max_draft, kv_type):
     assert a.past_len == b.past_len
 
 
+@pytest.mark.parametrize("penalty,max_draft,kv_type", [(1.0, 15, mtg.TYPE_F32), (1.25, 15, mtg.TYPE_F16),
+                                                       (1.0, 11, mtg.TYPE_F16)], ids=["p1-d15", "p1.25-d15-f16kv",
+                                                                                      "p1-d11-f16kv"])
+def test_device_loop_16_rows_equals_host_loop_and_oracle(penalty, max_draft, kv_type):
+    """More than 7 drafts per step: every step of the device loop runs the 16-row
+    step kernel, whatever its row count; ids, counters and KV position equal the
+    host loop's and the oracle's."""
+    print("device loop, 16 rows: penalty %.2f max_draft %d kv %d" % (penalty, max_draft, kv_type), flush=True)
+    model, orc, a, b, rng = _setup(40, 800, kv_type)
+    prior = _prior(rng, model.hp.vocab)
+    first = int(prior[-1])
+    kw = dict(max_steps=0, eos=-1, penalty=penalty, max_draft=max_draft, prior=prior)
+    dev = a.generate_device(first, 300, **kw)
+    host = b.generate_from(first, 300, **kw)
+    ref = orc.generate_from(first, 300, **kw)
+    _same_run(dev, host, "device vs host")
+    _same_run(dev, ref, "device vs oracle")
+    assert dev[1].drafted_calls > 0
+    assert a.past_len == b.past_len == orc.past_len
+
+
+@pytest.mark.parametrize("max_draft,period", [(7, 37), (15, 37), (15, 0), (5, 11)],
+                         ids=["d7-p37", "d15-p37", "d15-ngram", "d5-p11"])
+def test_device_stream_drafter_equals_host_hook_and_oracle(max_draft, period):
+    """The draft hook of the reference loop (called every step,
+    src/cpu_speculative.cpp:105) as the long-context workloads use it: the stream
+    drafter (n-gram over prompt ++ ids, completed from a periodic stream) run by
+    the device controller, against the host loop and the oracle's controller
+    calling mtg_stream_draft as their hook."""
+    print("device stream drafter: max_draft %d period %d" % (max_draft, period), flush=True)
+    model, orc, a, b, rng = _setup(50, 900)
+    vocab = model.hp.vocab
+    prompt = rng.integers(0, vocab, 30).astype(np.int32)
+    stream = rng.integers(0, vocab, max(period, 1)).astype(np.int32)[:period]
+    drafter = mtg.stream_drafter(prompt, stream)
+    fn, user, _keep = drafter
+    first = int(rng.integers(0, vocab))
+    for penalty in (1.0, 1.2):
+        a.rewind(50)
+        b.rewind(50)
+        orc.rewind(50)
+        kw = dict(max_steps=24, eos=-1, penalty=penalty, max_draft=max_draft)
+        dev = a.generate_device(first, 400, stream=drafter, **kw)
+        host = b.generate_from(first, 400, draft=fn, user=user, **kw)
+        ref = orc.generate_from(first, 400, draft=fn, user=user, **kw)
+        _same_run(dev, host, "device vs host, penalty %.1f" % penalty)
+        _same_run(dev, ref, "device vs oracle, penalty %.1f" % penalty)
+        assert a.past_len == b.past_len == orc.past_len
+        if period:
+            assert dev[1].proposed == dev[1].target_calls * max_draft
+
+
 def test_device_loop_stop_rules():
     """eos (stop 1), the token limit (2), a full KV cache (3) and a step limit (0)."""
     print("device loop: stop rules", flush=True)
@@ -134,9 +186,6 @@ def test_device_loop_finishes_on_the_host_after_an_abandoned_step():
 
 def test_device_loop_unsupported_cases():
     model, orc, a, b, rng = _setup(10, 100)
-    with pytest.raises(mtg.MtgError) as e:
-        a.generate_device(5, 10, max_draft=8)
-    assert e.value.code == mtg.ERR_UNSUPPORTED
     a.set_exec(mtg.EXEC_GRAPH)
     with pytest.raises(mtg.MtgError) as e:
         a.generate_device(5, 10)
@@ -166,7 +215,50 @@ def test_full_size_device_loop_k8_ctx1600():
         times[name] = (time.perf_counter() - t0) / max(1, runs[name][1].target_calls)
     _same_run(runs["device"], runs["host"], "full size")
     st = runs["device"][1]
+    assert a.past_len == b.past_len
+    # the same with the workload's own drafter (the stream drafter) on both loops
+    _, text2, stream = build_prompt(model, a.embed, cfg)
+    drafter = mtg.stream_drafter(text2, stream)
+    fn, user, _keep = drafter
+    for d in (a, b):
+        d.rewind(n)
+    runs["device_stream"] = a.generate_device(first, 1 << 12, max_steps=64, max_draft=cfg["K"] - 1, stream=drafter)
+    runs["host_stream"] = b.generate_from(first, 1 << 12, max_steps=64, max_draft=cfg["K"] - 1, draft=fn, user=user)
+    _same_run(runs["device_stream"], runs["host_stream"], "full size, stream drafter")
     print("full-size K=8 loop: %d steps, %d ids, %d accepted; %.1f us/step on the device loop, %.1f on the host loop"
           % (st.target_calls, len(runs["device"][0]), st.accepted, 1e6 * times["device"], 1e6 * times["host"]),
           flush=True)
     assert a.past_len == b.past_len
+
+
+def test_full_size_device_loop_k16_f16kv_ctx4000():
+    """The K=16 f16-KV workload at full size on the device loop with its stream
+    drafter (the 16-row step kernel): 16 steps against the host loop and the
+    oracle from the same prefilled KV state."""
+    import os
+    from workloads import CONFIGS, build_prompt, prompt_rows
+    cfg = CONFIGS[3]
+    oracle_py.lib().orc_set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
+    n = prompt_rows(cfg)
+    max_seq = n + 20 * cfg["K"]
+    a = mtg.Decoder(model, max_seq, cfg["kv"])
+    b = mtg.Decoder(model, max_seq, cfg["kv"])
+    rows, text, stream = build_prompt(model, a.embed, cfg)
+    hid = a.prefill(rows)
+    first = int(np.argmax(a.logits(hid[-1:])[0]))
+    k, v = a.kv_read(n)
+    b.kv_write(k, v)
+    orc = oracle_py.Oracle(model, max_seq, cfg["kv"])
+    orc.kv_write(k, v)
+    del k, v
+    drafter = mtg.stream_drafter(text, stream)
+    fn, user, _keep = drafter
+    kw = dict(max_steps=16, max_draft=cfg["K"] - 1)
+    dev = a.generate_device(first, 1 << 12, stream=drafter, **kw)
+    host = b.generate_from(first, 1 << 12, draft=fn, user=user, **kw)
+    ref = orc.generate_from(first, 1 << 12, draft=fn, user=user, **kw)
+    _same_run(dev, host, "K=16 device vs host")
+    _same_run(dev, ref, "K=16 device vs oracle")
+    assert dev[1].target_calls == 16 and a.past_len == b.past_len == orc.past_len
+    print("full-size K=16 device loop: %d ids, %d accepted drafts" % (len(dev[0]), dev[1].accepted), flush=True)
