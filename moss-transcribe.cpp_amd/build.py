@@ -19,7 +19,7 @@ ORACLE_DIR = os.path.join(ROOT, "oracle")
 ORACLE_LIB = os.path.join(ORACLE_DIR, "liboracle.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["kernels.hip", "kernels_wt.hip", "step_kernel.hip", "noalloc.hip", "prefill.hip", "generate.hip", "encoder.hip", "runtime.cpp", "capi.cpp",
+SOURCES = ["kernels.hip", "kernels_wt.hip", "step_kernel.hip", "noalloc.hip", "prefill.hip", "prefill_wt.hip", "generate.hip", "encoder.hip", "runtime.cpp", "capi.cpp",
            "synth.cpp", "gguf.cpp", "reference_api.cpp"]
 # -ffp-contract=off: elementwise ops round like the reference's scalar code;
 # fused multiply-adds are written explicitly (fmaf) where they are wanted.

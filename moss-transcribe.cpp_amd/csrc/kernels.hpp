@@ -105,8 +105,18 @@ void launch_pf_gemm(hipStream_t s, int epi, const uint8_t* w, const uint8_t* w2,
 void launch_pf_qk_rope(hipStream_t s, const float* qkv, int S, int past0, int n_heads, int n_kv_heads,
                        const float* q_norm, const float* k_norm, float eps, const float* rope, float* q_out,
                        KvLayer kv);
+// ofl == nullptr: the output rows as q8_0 codes / scales; otherwise as f32 rows in ofl
 void launch_pf_attn(hipStream_t s, const float* q, int n_heads, int n_kv_heads, KvLayer kv, int past0, int S,
-                    int8_t* ocodes, float* oscales);
+                    int8_t* ocodes, float* oscales, float* ofl = nullptr);
+// ---- the block prefill for f16 / q4_K weights (prefill_wt.hip); activations
+// [S][K] f16 or q8_K blocks in act (the compact layouts of WtAct, S rows) ----
+// act <- the weight type's vec_dot_type of RMSNorm(src) * gain (gain == nullptr:
+// src as is), S rows of K
+void launch_pf_act_wt(hipStream_t s, int wtype, const float* src, int S, int K, const float* gain, float eps,
+                      const WtAct& act);
+// out[s][n] (= / += / swiglu with w2) for f16 or q4_K weights in the GGUF row layout
+void launch_pf_gemm_wt(hipStream_t s, int wtype, int epi, const uint8_t* w, const uint8_t* w2, int N, int K,
+                       const WtAct& act, int S, float* out);
 
 // ---- f16 / q4_K weights (kernels_wt.hip); weights in the GGUF row layout ----
 bool wt_shape_supported(int wtype, int k);

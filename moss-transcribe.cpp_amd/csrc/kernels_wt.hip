@@ -64,18 +64,6 @@ __device__ __forceinline__ void stage_pieces(const v4i* __restrict__ src, int n,
   }
 }
 
-// 1 / sqrt(mean(x^2) + eps) of a hidden row (K == 1024), the canonical double sum:
-// lane l sums elements 16l..16l+15, then the butterfly. Called by wave 0.
-__device__ __forceinline__ float row_rms_scale(const float* xr, int K, float eps) {
-  const int lane = threadIdx.x & 63;
-  double s = 0.0;
-  for (int e = 0; e < 16; ++e) {
-    const float v = xr[lane * 16 + e];
-    s += (double)__fmul_rn(v, v);
-  }
-  s = wave_sum_d(s);
-  return dev_rms_scale((float)(s / (double)K), eps);
-}
 
 // ------------------------------------------------------- activations ------
 // Grid (16 rows, K / 256), 256 threads: one element per thread. gain == nullptr:
@@ -104,44 +92,6 @@ k_act_f16(const StepDesc* __restrict__ desc, const float* __restrict__ src, int 
   out[(size_t)t * K + k] = __half_as_ushort(__float2half_rn(y));  // vec_dot_type F16
 }
 
-// ggml quantize_row_q8_K_ref of one 256-block held one element per thread of a
-// 256-thread workgroup: the element of largest magnitude (the first one on ties)
-// gives max with its sign, iscale = -127/max, codes = min(127, nearest(iscale*x)),
-// d = 1/iscale, bsums over 16-element groups.
-// Threads 0..255 hold the block; in a larger workgroup the others pass the
-// barrier only.
-__device__ __forceinline__ void q8k_block256(float y, const ActQ8K& a, int t, int K, int b) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const bool active = tid < 256;
-  __shared__ float s_y[256];
-  __shared__ uint64_t s_key[4];
-  if (active) s_y[tid] = y;
-  // first maximum of |y|: larger magnitude, then lower index
-  const uint64_t key = ((uint64_t)__float_as_uint(fabsf(y)) << 32) | (uint32_t)(255 - tid);
-  const uint64_t wk = wave_max_u64(key);
-  if (active && lane == 0) s_key[wave] = wk;
-  __syncthreads();
-  if (!active) return;
-  uint64_t best = s_key[0];
-  for (int w = 1; w < 4; ++w) best = s_key[w] > best ? s_key[w] : best;
-  const float maxv = s_y[255 - (int)(best & 0xffffffffu)];
-  int q = 0;
-  float d = 0.0f;
-  if ((best >> 32) != 0) {  // amax > 0
-    const float iscale = __fdiv_rn(-127.0f, maxv);
-    q = min(127, (int)rintf(__fmul_rn(iscale, y)));
-    d = __fdiv_rn(1.0f, iscale);
-  }
-  a.qs[(size_t)t * K + b * 256 + tid] = (int8_t)q;
-  // bsums: the 16 lanes of a DPP row hold one group
-  int s = q;
-  s += (int)dpp_u<kDppRor8>((uint32_t)s);
-  s += (int)dpp_u<kDppRor4>((uint32_t)s);
-  s += (int)dpp_u<kDppRor2>((uint32_t)s);
-  s += (int)dpp_u<kDppRor1>((uint32_t)s);
-  if ((tid & 15) == 0) a.bsums[(size_t)t * (K / 16) + b * 16 + (tid >> 4)] = s;
-  if (tid == 0) a.d[(size_t)t * (K / 256) + b] = d;
-}
 
 // Grid (16 rows, K / 256), 256 threads: block blockIdx.y of row blockIdx.x.
 __global__ void __launch_bounds__(256)
@@ -825,22 +775,6 @@ __host__ __device__ constexpr size_t q4m_lds_bytes(int K) {
   return q4_lds_bytes(K, 0) + 4 * (size_t)16 * 2 * 4;  // + per wave: d|dmin [16][2]
 }
 
-// get_scale_min_k4 of the 8 sub-blocks from the 12 packed bytes held in three
-// words (byte i in word i / 4)
-__device__ __forceinline__ void q4k_scales_w(uint32_t w0, uint32_t w1, uint32_t w2, int sc[8], int mn[8]) {
-  const uint32_t wd[3] = {w0, w1, w2};
-  auto by = [&](int i) { return (int)((wd[i >> 2] >> (8 * (i & 3))) & 0xffu); };
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    sc[j] = by(j) & 63;
-    mn[j] = by(j + 4) & 63;
-  }
-#pragma unroll
-  for (int j = 4; j < 8; ++j) {
-    sc[j] = (by(j + 4) & 0xF) | ((by(j - 4) >> 6) << 4);
-    mn[j] = (by(j + 4) >> 4) | ((by(j) >> 6) << 4);
-  }
-}
 
 template <int NB>
 struct Q4Tile {

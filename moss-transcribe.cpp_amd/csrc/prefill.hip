@@ -406,10 +406,12 @@ __device__ __forceinline__ void pf_scores(const float* s_q, const float (&k)[32]
 constexpr size_t kPfAttnLds =
     ((size_t)kPfCols * kPfQStride + kPfCols * kPfPStride + 4 * kPfCols + 3 * kPfCols) * 4;
 
-template <int KVH>
+// OUTF: the output rows as f32 [S][n_heads * 128] in ofl (the f16 / q4_K weight
+// paths convert them to their vec_dot_type), instead of q8_0 codes.
+template <int KVH, bool OUTF = false>
 __global__ void __launch_bounds__(256)
 k_pf_attn(const float* __restrict__ q, int n_heads, int n_kv_heads, KvLayer kv, int past0, int S,
-          int8_t* __restrict__ ocodes, float* __restrict__ oscales) {
+          int8_t* __restrict__ ocodes, float* __restrict__ oscales, float* __restrict__ ofl) {
   constexpr int NCT = kPfCols / 16, NC = kPfCols;
   // the query blocks with the most chunks start first
   const int hq0 = blockIdx.x * kPfHeads, g = hq0 / (n_heads / n_kv_heads);
@@ -542,6 +544,14 @@ k_pf_attn(const float* __restrict__ q, int n_heads, int n_kv_heads, KvLayer kv, 
       const int t = 16 * (ct % kPfRowTiles) + 4 * kk + r;  // query row of column 16 ct + 4 kk + r
       const float o0 = __fdiv_rn(O[ct][0][r], L[ct][r]);
       const float o1 = __fdiv_rn(O[ct][1][r], L[ct][r]);
+      if constexpr (OUTF) {
+        if (t < nq) {
+          float* orow = ofl + (size_t)(r0 + t) * QN + (hq0 + ct / kPfRowTiles) * kHeadDim + 32 * wave + kl;
+          orow[0] = o0;
+          orow[16] = o1;
+        }
+        continue;
+      }
       float amax = fmaxf(fabsf(o0), fabsf(o1));
       uint32_t u = __float_as_uint(amax);  // max over the 16 lanes kl of this row
       u = max(u, dpp_u<kDppRor8>(u));
@@ -603,21 +613,29 @@ void launch_pf_qk_rope(hipStream_t s, const float* qkv, int S, int past0, int n_
 }
 
 void launch_pf_attn(hipStream_t s, const float* q, int n_heads, int n_kv_heads, KvLayer kv, int past0, int S,
-                    int8_t* ocodes, float* oscales) {
+                    int8_t* ocodes, float* oscales, float* ofl) {
   const dim3 grid((unsigned)(n_heads / kPfHeads), (unsigned)((S + kPfRows - 1) / kPfRows));
-  if (kv.f16)
-    hipLaunchKernelGGL(k_pf_attn<1>, grid, dim3(256), kPfAttnLds, s, q, n_heads, n_kv_heads, kv, past0, S, ocodes,
-                       oscales);
-  else
-    hipLaunchKernelGGL(k_pf_attn<0>, grid, dim3(256), kPfAttnLds, s, q, n_heads, n_kv_heads, kv, past0, S, ocodes,
-                       oscales);
+#define MTG_PF_ATTN(KVH, OUTF)                                                                                 \
+  hipLaunchKernelGGL((k_pf_attn<KVH, OUTF>), grid, dim3(256), kPfAttnLds, s, q, n_heads, n_kv_heads, kv, past0, S, \
+                     ocodes, oscales, ofl)
+  if (ofl) {
+    if (kv.f16) MTG_PF_ATTN(1, true);
+    else MTG_PF_ATTN(0, true);
+  } else {
+    if (kv.f16) MTG_PF_ATTN(1, false);
+    else MTG_PF_ATTN(0, false);
+  }
+#undef MTG_PF_ATTN
 }
 
 hipError_t prepare_kernels_pf() {
-  hipError_t e = hipFuncSetAttribute((const void*)k_pf_attn<0>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)kPfAttnLds);
-  if (e != hipSuccess) return e;
-  return hipFuncSetAttribute((const void*)k_pf_attn<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfAttnLds);
+  const void* fns[] = {(const void*)k_pf_attn<0, false>, (const void*)k_pf_attn<1, false>,
+                       (const void*)k_pf_attn<0, true>, (const void*)k_pf_attn<1, true>};
+  for (const void* f : fns) {
+    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfAttnLds);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace mtg

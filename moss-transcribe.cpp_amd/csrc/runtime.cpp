@@ -592,9 +592,10 @@ int Ctx::prefill(const float* embeds, int S, float* hidden_out) {
   if (!embeds || S <= 0) return fail(MTG_ERR_INVALID, "prefill: bad arguments");
   if (S > max_seq) return fail(MTG_ERR_CAPACITY, "prefill exceeds max_seq");
   past = 0;
-  const bool blocks = prefill_fast_enabled && wtype == MTG_TYPE_Q8_0 && S <= pf_max_context() &&
-                      hp.hidden == 1024 && hp.head_dim == kHeadDim;
-  if (blocks) return prefill_blocks(embeds, S, hidden_out);
+  const bool blocks = prefill_fast_enabled && S <= pf_max_context() && hp.hidden == 1024 &&
+                      hp.head_dim == kHeadDim;
+  if (blocks) return wtype == MTG_TYPE_Q8_0 ? prefill_blocks(embeds, S, hidden_out)
+                                            : prefill_blocks_wt(embeds, S, hidden_out);
   const int H = hp.hidden;
   for (int s0 = 0; s0 < S; s0 += kMaxRows) {
     const int n = std::min(kMaxRows, S - s0);
@@ -647,6 +648,80 @@ int Ctx::prefill_blocks(const float* embeds, int S, float* hidden_out) {
       launch_pf_gemm(s, PF_EPI_SWIGLU, y.wg, y.wu, F, H, pf.codes, pf.scales, n, pf.act);
       launch_pf_quant(s, pf.act, n, F, pf.codes, pf.scales);
       launch_pf_gemm(s, PF_EPI_RESID, y.wd, nullptr, H, F, pf.codes, pf.scales, n, pf.x);
+    }
+    launch_pf_norm_quant(s, pf.x, n, out_norm, eps, pf.codes, pf.scales, pf.hid);
+    if ((rc = check(hipGetLastError(), "prefill launch"))) return rc;
+    if (hidden_out &&
+        (rc = check(hipMemcpyAsync(hidden_out + (size_t)c0 * H, pf.hid, (size_t)n * H * 4, hipMemcpyDeviceToHost, s),
+                    "hidden rows")))
+      return rc;
+  }
+  if ((rc = check(hipEventRecord(ev_stop, s), "event"))) return rc;
+  if ((rc = check(hipStreamSynchronize(s), "prefill"))) return rc;
+  float ms = 0.0f;
+  if ((rc = check(hipEventElapsedTime(&ms, ev_start, ev_stop), "event"))) return rc;
+  last_prefill_ms = ms;
+  past = S;
+  return MTG_OK;
+}
+
+// The block prefill for f16 and q4_K weights (prefill_wt.hip): the same layer
+// sequence as prefill_blocks, with each GEMM's activation in the weight type's
+// vec_dot_type (f16 rows or q8_K blocks) and the attention output as f32 rows.
+int Ctx::prefill_blocks_wt(const float* embeds, int S, float* hidden_out) {
+  const int H = hp.hidden, NH = hp.n_heads, NKV = hp.n_kv_heads, D = hp.head_dim;
+  const int QN = NH * D, KN = NKV * D, NQKV = QN + 2 * KN, F = hp.intermediate;
+  const float eps = hp.rms_eps;
+  const int R = kPfRows;
+  const int KM = std::max(H, std::max(QN, F));
+  if (!pf.x) {
+    pf.x = (float*)dalloc((size_t)R * H * 4, false);
+    pf.qkv = (float*)dalloc((size_t)R * NQKV * 4, false);
+    pf.q = (float*)dalloc((size_t)R * QN * 4, false);
+    pf.act = (float*)dalloc((size_t)R * F * 4, false);
+    pf.hid = (float*)dalloc((size_t)R * H * 4, false);
+    pf.codes = (int8_t*)dalloc((size_t)R * KM, false);
+    pf.scales = (float*)dalloc((size_t)R * (KM / 32) * 4, false);
+    if (!pf.x || !pf.qkv || !pf.q || !pf.act || !pf.hid || !pf.codes || !pf.scales)
+      return fail(MTG_ERR_NOMEM, "prefill buffers");
+  }
+  if (!pf.o) {
+    pf.o = (float*)dalloc((size_t)R * QN * 4, false);
+    if (wtype == MTG_TYPE_F16) {
+      pf.wact.f16h = (uint16_t*)dalloc((size_t)R * KM * 2, false);
+    } else {
+      pf.wact.q8k.qs = (int8_t*)dalloc((size_t)R * KM, false);
+      pf.wact.q8k.d = (float*)dalloc((size_t)R * (KM / 256) * 4, false);
+      pf.wact.q8k.bsums = (int32_t*)dalloc((size_t)R * (KM / 16) * 4, false);
+    }
+    if (!pf.o || (wtype == MTG_TYPE_F16 ? !pf.wact.f16h
+                                        : (!pf.wact.q8k.qs || !pf.wact.q8k.d || !pf.wact.q8k.bsums)))
+      return fail(MTG_ERR_NOMEM, "prefill buffers");
+  }
+  hipStream_t s = stream;
+  int rc = MTG_OK;
+  if (!ev_start && (rc = check(hipEventCreate(&ev_start), "event"))) return rc;
+  if (!ev_stop && (rc = check(hipEventCreate(&ev_stop), "event"))) return rc;
+  if ((rc = check(hipEventRecord(ev_start, s), "event"))) return rc;
+  const WtAct& A = pf.wact;
+  for (int c0 = 0; c0 < S; c0 += R) {
+    const int n = std::min(R, S - c0);
+    if ((rc = check(hipMemcpyAsync(pf.x, embeds + (size_t)c0 * H, (size_t)n * H * 4, hipMemcpyHostToDevice, s),
+                    "prompt rows")))
+      return rc;
+    for (int l = 0; l < hp.n_layers; ++l) {
+      const Layer& y = layers[l];
+      const KvLayer kv = kv_layer(l);
+      launch_pf_act_wt(s, wtype, pf.x, n, H, y.attn_norm, eps, A);
+      launch_pf_gemm_wt(s, wtype, PF_EPI_STORE, y.wqkv, nullptr, NQKV, H, A, n, pf.qkv);
+      launch_pf_qk_rope(s, pf.qkv, n, c0, NH, NKV, y.q_norm, y.k_norm, eps, rope, pf.q, kv);
+      launch_pf_attn(s, pf.q, NH, NKV, kv, c0, n, nullptr, nullptr, pf.o);
+      launch_pf_act_wt(s, wtype, pf.o, n, QN, nullptr, eps, A);
+      launch_pf_gemm_wt(s, wtype, PF_EPI_RESID, y.wo, nullptr, H, QN, A, n, pf.x);
+      launch_pf_act_wt(s, wtype, pf.x, n, H, y.ffn_norm, eps, A);
+      launch_pf_gemm_wt(s, wtype, PF_EPI_SWIGLU, y.wg, y.wu, F, H, A, n, pf.act);
+      launch_pf_act_wt(s, wtype, pf.act, n, F, nullptr, eps, A);
+      launch_pf_gemm_wt(s, wtype, PF_EPI_RESID, y.wd, nullptr, H, F, A, n, pf.x);
     }
     launch_pf_norm_quant(s, pf.x, n, out_norm, eps, pf.codes, pf.scales, pf.hid);
     if ((rc = check(hipGetLastError(), "prefill launch"))) return rc;

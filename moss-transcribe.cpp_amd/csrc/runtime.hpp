@@ -78,6 +78,9 @@ struct Ctx {
     float *x = nullptr, *qkv = nullptr, *q = nullptr, *act = nullptr, *hid = nullptr;
     int8_t* codes = nullptr;
     float* scales = nullptr;
+    // f16 / q4_K weights: the attention output rows and the GEMM activation
+    float* o = nullptr;
+    WtAct wact{};
   } pf;
   bool prefill_fast_enabled = true;
   double last_prefill_ms = 0.0;  // device time of the last prefill (HIP events)
@@ -110,6 +113,7 @@ struct Ctx {
   // context fits the prefill attention, else verify-size appends
   int prefill(const float* embeds, int S, float* hidden_out);
   int prefill_blocks(const float* embeds, int S, float* hidden_out);
+  int prefill_blocks_wt(const float* embeds, int S, float* hidden_out);
   int logits_of(const float* hidden, int T, float* logits_out);
   int embed(const int32_t* ids, int n, float* out);
   int kv_io(void* k, void* v, int n_pos, bool write);
