@@ -194,6 +194,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--exec", choices=["step", "graph", "eager"], default="step",
                     help="persistent step kernel, per-op kernels from a graph, or eager per-op")
+    ap.add_argument("--prefill-runs", type=int, default=0,
+                    help="only prefill the workload's prompt this many times (block prefill) and print "
+                         "its device time; for kernel traces of the prefill")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, copy a buffer of this size 5 times (device to device) "
                          "so that a counter profile of the same command can calibrate FETCH_SIZE "
@@ -218,6 +221,15 @@ def main():
         args.exec = "graph"
     dec.set_exec({"step": mtg.EXEC_STEP_KERNEL, "graph": mtg.EXEC_GRAPH, "eager": mtg.EXEC_EAGER}[args.exec])
     rows, text, stream = build_prompt(model, dec.embed, cfg)
+    if args.prefill_runs > 0:
+        times = []
+        for _ in range(args.prefill_runs):
+            dec.prefill(rows, want_hidden=False)
+            times.append(dec.last_prefill_ms)
+        print(json.dumps({"metric": "block prefill device ms", "value": min(times), "unit": "ms",
+                          "runs_ms": times, "rows": int(rows.shape[0]), "config": args.config,
+                          "weights": WNAME[cfg["wtype"]], "higher_is_better": False}), flush=True)
+        return
     hid = dec.prefill(rows)
     first = int(np.argmax(dec.logits(hid[-1:])[0]))
     drafter = mtg.stream_drafter(text, stream)

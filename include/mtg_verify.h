@@ -125,10 +125,10 @@ int mtg_rewind(mtg_ctx* ctx, int32_t position);
 int mtg_embed(mtg_ctx* ctx, const int32_t* ids, int32_t n, float* out);
 
 /* reset + run S rows; hidden_out (nullable) receives the final-normed hidden of
- * every row (S x hidden). With q8_0 weights the rows go through the decoder in
- * blocks of up to 2,048 (each weight matrix streamed once per block, causal
- * attention over the cache); otherwise in verify batches of up to
- * MTG_MAX_BATCH. Both give the same bits. */
+ * every row (S x hidden). The rows go through the decoder in blocks of up to
+ * 2,048 (each weight matrix streamed once per block, causal attention over the
+ * cache), for q8_0, f16 and q4_K weights; with mtg_prefill_mode(ctx, 0) in verify
+ * batches of up to MTG_MAX_BATCH. Both give the same bits. */
 int mtg_prefill(mtg_ctx* ctx, const float* embeds, int32_t S, float* hidden_out);
 /* blocks != 0 (the default): the block prefill where it applies; 0: verify-size
  * batches (no counterpart in the reference; for comparing the two paths). */
