@@ -6,7 +6,10 @@ audio rows N(0,1) scaled to the RMS of the token embeddings, then 100 random
 text ids), greedy decoding with K = 8 verify rows per step (seed + 7 drafts)
 from an n-gram drafter over prompt ++ committed ids, completed from a seeded
 37-token periodic stream. A step = one verify pass (append K rows, tied lm_head
-over all rows, on-device greedy choice and acceptance) plus the host controller.
+over all rows, on-device greedy choice and acceptance) plus the host controller
+(--loop device: the device loop instead, a controller kernel between the step
+kernels that commits the accepted ids, applies the stop rules and drafts the next
+step with the same stream drafter, the host looking at the state every 8 steps).
 
 Prints one JSON line (metric, value = accepted tokens/s, ms_per_step, roofline of
 the dominant kernel, cpu_baseline = the oracle on the host cores).
@@ -194,6 +197,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--exec", choices=["step", "graph", "eager"], default="step",
                     help="persistent step kernel, per-op kernels from a graph, or eager per-op")
+    ap.add_argument("--loop", choices=["device", "host"], default="host",
+                    help="the speculative controller on the device (a controller kernel between the step "
+                         "kernels, the stream drafter run there) or on the host; per-op execution always "
+                         "runs the host loop")
     ap.add_argument("--prefill-runs", type=int, default=0,
                     help="only prefill the workload's prompt this many times (block prefill) and print "
                          "its device time; for kernel traces of the prefill")
@@ -235,9 +242,15 @@ def main():
     drafter = mtg.stream_drafter(text, stream)
     fn, user, _keep = drafter
     log("setup %.1fs: prompt %d rows, max_seq %d" % (time.perf_counter() - t_setup, n_prompt, max_seq))
-    # warmup
-    ids_w, st_w = dec.generate_from(first, 1 << 20, max_steps=args.warmup, max_draft=cfg["K"] - 1,
-                                    draft=fn, user=user)
+    # warmup, on the same controller as the timed steps (its buffers and events are
+    # made by the first call)
+    loop = args.loop if args.exec == "step" else "host"
+    if loop == "device":
+        ids_w, st_w = dec.generate_device(first, 1 << 20, max_steps=args.warmup, max_draft=cfg["K"] - 1,
+                                          stream=drafter)
+    else:
+        ids_w, st_w = dec.generate_from(first, 1 << 20, max_steps=args.warmup, max_draft=cfg["K"] - 1,
+                                        draft=fn, user=user)
     ctx_start = dec.past_len
     # KV snapshot for the CPU leg (outside the timed region)
     snap_kv = dec.kv_read(ctx_start) if not args.no_cpu else None
@@ -247,8 +260,12 @@ def main():
     dec.launch_timing(True)
     fallbacks0 = dec.step_fallbacks
     t0 = time.perf_counter()
-    ids, st = dec.generate_from(st_w.next_seed, 1 << 20, max_steps=steps, max_draft=cfg["K"] - 1,
-                                draft=fn, user=user, prior=ids_w)
+    if loop == "device":
+        ids, st = dec.generate_device(st_w.next_seed, 1 << 20, max_steps=steps, max_draft=cfg["K"] - 1,
+                                      prior=ids_w, stream=drafter)
+    else:
+        ids, st = dec.generate_from(st_w.next_seed, 1 << 20, max_steps=steps, max_draft=cfg["K"] - 1,
+                                    draft=fn, user=user, prior=ids_w)
     hip.hipDeviceSynchronize()
     elapsed = time.perf_counter() - t0
     dev_ms, launches, past_sum, rows_sum = dec.launch_timing_read()
@@ -290,7 +307,7 @@ def main():
                                   cfg["blocks"] * AUDIO_ROWS, cfg["text"], n_steps),
                    "verify_rows": cfg["K"], "context_start": ctx_start, "context_end": dec.past_len,
                    "accepted_per_step": st.accepted / max(n_steps, 1),
-                   "tokens": tokens, "exec": args.exec},
+                   "tokens": tokens, "exec": args.exec, "loop": loop},
         "verify_step_us": 1e3 * dev_ms / max(launches, 1),
         "host_step_us": 1e3 * ms_step,
         "step_bytes": bytes_launch,

@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cstring>
+#include <memory>
 #include <new>
 #include <set>
 #include <vector>
@@ -433,11 +434,18 @@ int mtg_generate_device_stream(mtg_ctx* ctx, int32_t first_seed, const int32_t* 
     g.raw_choice = first_seed;
     g.n_prompt = drafter ? drafter->n_prompt : 0;
     g.period = drafter ? drafter->period : 0;
-    const int cap = n_prior + max_new + 1;
-    std::vector<int32_t> ids((size_t)cap);
-    std::copy(prior_ids, prior_ids + n_prior, ids.begin());
+    // room for the prior ids and every id the run can emit: max_new, or fewer
+    // when a step limit bounds the run (each step emits at most max_draft + 1)
+    int64_t most = max_new;
+    if (max_steps > 0) most = std::min<int64_t>(most, (int64_t)max_steps * (g.max_draft + 1));
+    const int cap = n_prior + (int)most + 1;
+    // the controller kernel packs positions of prompt ++ ids into 26 bits
+    if ((int64_t)g.n_prompt + cap >= (1 << 26))
+      return c.fail(MTG_ERR_INVALID, "generate_device: prompt and ids exceed 2^26 positions");
+    std::unique_ptr<int32_t[]> ids(new int32_t[(size_t)cap]);  // not cleared: only written ids are read
+    std::copy(prior_ids, prior_ids + n_prior, ids.get());
     const auto t0 = std::chrono::steady_clock::now();
-    int rc = c.generate_device(g, ids.data(), cap, drafter ? drafter->prompt : nullptr,
+    int rc = c.generate_device(g, ids.get(), cap, drafter ? drafter->prompt : nullptr,
                                drafter ? drafter->stream : nullptr);
     if (rc) return rc;
     mtg_gen_stats st{};
@@ -456,9 +464,9 @@ int mtg_generate_device_stream(mtg_ctx* ctx, int32_t first_seed, const int32_t* 
       int32_t more = 0;
       mtg_gen_stats rest{};
       const int left_steps = max_steps > 0 ? max_steps - g.steps : 0;  // >= 1: the abandoned step did not count
-      rc = mtg_generate_from(ctx, g.raw_choice, ids.data(), g.n_ids, max_new - n_new, left_steps, eos, penalty,
+      rc = mtg_generate_from(ctx, g.raw_choice, ids.get(), g.n_ids, max_new - n_new, left_steps, eos, penalty,
                              max_draft, drafter ? mtg_stream_draft : nullptr, nullptr,
-                             drafter ? const_cast<mtg_stream_drafter*>(drafter) : nullptr, ids.data() + g.n_ids,
+                             drafter ? const_cast<mtg_stream_drafter*>(drafter) : nullptr, ids.get() + g.n_ids,
                              &more, &rest);
       if (rc) return rc;
       n_new += more;
@@ -472,7 +480,7 @@ int mtg_generate_device_stream(mtg_ctx* ctx, int32_t first_seed, const int32_t* 
       st.next_seed = rest.next_seed;
     }
     st.verify_seconds = seconds_since(t0);
-    std::copy(ids.begin() + n_prior, ids.begin() + n_prior + n_new, ids_out);
+    std::copy(ids.get() + n_prior, ids.get() + n_prior + n_new, ids_out);
     *n_ids_out = n_new;
     if (stats) *stats = st;
     return MTG_OK;

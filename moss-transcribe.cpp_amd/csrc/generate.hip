@@ -136,24 +136,23 @@ k_gen_ctrl(GenState* __restrict__ g, int32_t* __restrict__ ids, StepDesc* __rest
   __syncthreads();
   auto hist_at = [&](int i) { return staged ? s_ids[i] : (i < n_prompt ? prompt[i] : ids[i - n_prompt]); };
   auto id_at = [&](int i) { return hist_at(n_prompt + i); };  // committed id i
+  // One pass over the ends e (2 <= e < |h|) of the candidate n-grams instead of
+  // one pass per length: c(e), the length (at most 16) of the common suffix of
+  // h[0, e) and h, is >= len exactly when the len-gram ending at e matches h's
+  // suffix. The longest matching length is then the largest c(e) >= 2, and its
+  // latest start belongs to the largest e with that c(e): the draft begins at e.
   int begin = -1;
   if (budget > 0 && nh_all >= 3) {
-    for (int len = min(16, nh_all - 1); len >= 2; --len) {
-      int best = -1;
-      for (int start = nh_all - len - 1 - tid; start >= 0; start -= kGenThreads) {
-        bool eq = true;
-        for (int j = 0; j < len && eq; ++j) eq = hist_at(start + j) == hist_at(nh_all - len + j);
-        if (eq) {
-          best = start;  // this thread's starts descend: the first match is its latest
-          break;
-        }
-      }
-      best = block_max(best, s_red);
-      if (best >= 0) {
-        begin = best + len;
-        break;
-      }
+    const int lmax = min(16, nh_all - 1);
+    int key = -1;  // c(e) << 26 | e, the largest over this thread's ends
+    for (int e = nh_all - 1 - tid; e >= 2; e -= kGenThreads) {
+      int c = 0;
+      while (c < lmax && c < e && hist_at(e - 1 - c) == hist_at(nh_all - 1 - c)) ++c;
+      if (c >= 2) key = max(key, (c << 26) | e);
+      if (c == lmax) break;  // this thread's later ends are smaller
     }
+    key = block_max(key, s_red);
+    if (key >= 0) begin = key & ((1 << 26) - 1);
   }
   const int n_gram = begin >= 0 ? min(budget, nh_all - begin) : 0;
   const int np = period > 0 ? budget : n_gram;
@@ -186,6 +185,9 @@ k_gen_ctrl(GenState* __restrict__ g, int32_t* __restrict__ ids, StepDesc* __rest
     g->np = np;
     g->before = s_before;
     g->pending = 1;
+    ++g->issued;
+    g->issued_rows += T;
+    g->issued_past += s_before;
     res->n_match = -1;  // the step's acceptance overwrites it
   }
 }

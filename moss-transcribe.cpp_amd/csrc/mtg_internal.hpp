@@ -80,6 +80,9 @@ struct GenState {
   int32_t before, np;  // position and draft count of that step
   int32_t proposal[kMaxRows];
   int64_t target_calls, drafted_calls, proposed, accepted, target_input_tokens, rewinds;
+  // steps issued so far, their rows and the sum of their start positions (the
+  // host's launch timing counts the launches that ran a step)
+  int64_t issued, issued_rows, issued_past;
 };
 
 }  // namespace mtg

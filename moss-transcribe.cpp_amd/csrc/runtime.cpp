@@ -35,6 +35,8 @@ Ctx::~Ctx() {
   if (gen_aux_dev) hipFree(gen_aux_dev);
   if (gen_state_dev) hipFree(gen_state_dev);
   if (gen_state_host) hipHostFree(gen_state_host);
+  for (auto& e : gen_events)
+    if (e) hipEventDestroy(e);
   if (ev_start) hipEventDestroy(ev_start);
   if (ev_stop) hipEventDestroy(ev_stop);
   if (desc_host) hipHostFree(desc_host);
@@ -851,27 +853,60 @@ int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prom
   const int kv_f16 = kv_type == MTG_TYPE_F16;
   StepDesc unused{};
   result_host->err = 0;
+  // launch timing: an event pair around every step launch of a chunk; after the
+  // chunk, the launches that ran a step (the first `issued` ones) are counted
+  if (timing && !gen_events[0]) {
+    for (auto& e : gen_events)
+      if ((rc = check(hipEventCreate(&e), "event"))) return rc;
+  }
+  int64_t issued0 = g.issued, rows0 = g.issued_rows, past0 = g.issued_past;
   for (;;) {
     if (epoch > 0xF0000000u - (uint32_t)kChunkSteps * pps) {  // progress words restart before they could wrap
       if ((rc = check(hipMemsetAsync(params_host.flags, 0, (size_t)nwg * kFlagStride * 4, stream), "flags"))) return rc;
       if ((rc = check(hipMemsetAsync(params_host.qkvt, 0, qkvt_bytes(), stream), "tags"))) return rc;
       epoch = 0;
     }
-    for (int i = 0; i < kChunkSteps; ++i) {
+    // with a step limit, a chunk holds no more steps than are left to issue, and
+    // the chunk that issues the last one closes with one more controller pass,
+    // which takes that step's result. Otherwise the last step of a chunk is taken
+    // by the next chunk's first controller pass.
+    int steps = kChunkSteps;
+    if (g.max_steps > 0) steps = (int)std::min<int64_t>(kChunkSteps, std::max<int64_t>(0, g.max_steps - issued0));
+    const bool closing = g.max_steps > 0 && issued0 + steps >= g.max_steps;
+    for (int i = 0; i < steps; ++i) {
       launch_gen_ctrl(stream, gen_state_dev, gen_ids_dev, desc_dev, result_map, &result_dev->err, prompt_dev,
                       stream_dev);
       if ((rc = check(hipGetLastError(), "controller launch"))) return rc;
+      if (timing && (rc = check(hipEventRecord(gen_events[2 * i], stream), "timing event"))) return rc;
       if ((rc = check(launch_step(stream, G, kv_f16, params_dev, &unused, epoch, kStepVerify, false, desc_dev),
                       "step kernel launch")))
         return rc;
+      if (timing && (rc = check(hipEventRecord(gen_events[2 * i + 1], stream), "timing event"))) return rc;
       epoch += pps;
     }
-    // the last step of the chunk is taken by the next chunk's first controller
-    // pass, or by the closing pass below
+    if (closing) {
+      launch_gen_ctrl(stream, gen_state_dev, gen_ids_dev, desc_dev, result_map, &result_dev->err, prompt_dev,
+                      stream_dev);
+      if ((rc = check(hipGetLastError(), "controller launch"))) return rc;
+    }
     if ((rc = check(hipMemcpyAsync(gen_state_host, gen_state_dev, sizeof(GenState), hipMemcpyDeviceToHost, stream),
                     "generation state")))
       return rc;
     if ((rc = check(hipStreamSynchronize(stream), "generation"))) return rc;
+    if (timing) {
+      const int ran = (int)std::min<int64_t>(kChunkSteps, gen_state_host->issued - issued0);
+      for (int i = 0; i < ran; ++i) {
+        float ms = 0.0f;
+        if ((rc = check(hipEventElapsedTime(&ms, gen_events[2 * i], gen_events[2 * i + 1]), "timing"))) return rc;
+        timing_ms += ms;
+      }
+      timing_launches += ran;
+      timing_rows += gen_state_host->issued_rows - rows0;
+      timing_past += gen_state_host->issued_past - past0;
+    }
+    issued0 = gen_state_host->issued;
+    rows0 = gen_state_host->issued_rows;
+    past0 = gen_state_host->issued_past;
     if (gen_state_host->done) break;
   }
   g = *gen_state_host;

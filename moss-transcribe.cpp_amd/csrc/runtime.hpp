@@ -126,6 +126,7 @@ struct Ctx {
   int gen_cap = 0;
   int32_t* gen_aux_dev = nullptr;  // the stream drafter's prompt ids, then its stream period
   int gen_aux_cap = 0;
+  hipEvent_t gen_events[16] = {};  // launch timing of the device loop: a pair per step of a chunk
   GenState* gen_state_host = nullptr;  // pinned
   int generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prompt_ids, const int32_t* stream_ids);
 };
