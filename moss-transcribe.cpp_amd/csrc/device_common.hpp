@@ -106,6 +106,43 @@ __device__ __forceinline__ float dev_gelu_erf(float x) {
   const float e = (float)dev_erf_series((double)z);
   return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, e));
 }
+// dev_gelu_erf of N values at once: the N erf series run in lock step, each
+// element stopping at its own term count, so every element sees exactly the
+// operations of dev_gelu_erf; the N independent chains hide the latency of the
+// dependent double multiplies.
+template <int N>
+__device__ __forceinline__ void dev_gelu_erf_n(float (&x)[N]) {
+  const ErfRecip<76>& tab = kErfRecip;
+  double a2[N], term[N], sum[N];
+  int terms[N], tmax = 0;
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const double a = fabs((double)__fmul_rn(x[e], 0.70710678118654752440f));
+    terms[e] = a >= 4.0 ? 0 : (a < 1.0 ? 28 : (a < 2.0 ? 44 : (a < 3.0 ? 60 : 76)));
+    tmax = max(tmax, terms[e]);
+    a2[e] = __dmul_rn(a, a);
+    term[e] = a;
+    sum[e] = 0.0;
+  }
+  for (int n = 0; n < tmax; ++n) {
+    const double io = tab.inv_odd[n], in = tab.inv_next[n];
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const double s1 = __dadd_rn(sum[e], __dmul_rn(term[e], io));
+      const double t1 = -__dmul_rn(__dmul_rn(term[e], a2[e]), in);
+      const bool live = n < terms[e];
+      sum[e] = live ? s1 : sum[e];
+      term[e] = live ? t1 : term[e];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const float z = __fmul_rn(x[e], 0.70710678118654752440f);
+    const double r = terms[e] == 0 ? 1.0 : __dmul_rn(sum[e], 1.1283791670955126);
+    const float er = (float)(z < 0.0f ? -r : r);
+    x[e] = __fmul_rn(__fmul_rn(0.5f, x[e]), __fadd_rn(1.0f, er));
+  }
+}
 // ggml_silu: x / (1 + exp(-x))
 __device__ __forceinline__ float dev_silu(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, dev_expf(-x))); }
 

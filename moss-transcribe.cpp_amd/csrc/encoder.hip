@@ -2,17 +2,18 @@
 // (reference WhisperEncoder::encode, src/whisper_encoder.cpp:103-209, and
 // AudioAdaptor::apply, src/audio_adaptor.cpp:38-97).
 //
-//   conv stem  k_enc_conv: conv1d (kernel 3, pad 1) as one fma chain per output
-//              over (input channel, tap), + bias, GELU (erf); conv2 (stride 2)
-//              also adds the positional embedding and writes [rows][d]
+//   conv stem  k_enc_conv_mma: conv1d (kernel 3, pad 1) on f32 MFMA, one fma
+//              chain per output over (input channel, tap), + bias, GELU (erf);
+//              conv2 (stride 2) also adds the positional embedding and writes
+//              [rows][d]
 //   layers     k_enc_ln: LayerNorm (mean and variance as double sums over 64
 //              lane partials, butterfly) -> q8_0 codes for the next GEMM;
 //              q / k / v / out / fc1 / fc2 on the block GEMM of the prefill
 //              (q8_0 weights x q8_0 activations, int8 MFMA) with bias, GELU or
-//              residual epilogues; k_enc_attn: bidirectional attention of 16
-//              query rows of one head per workgroup over all rows in 64-key
-//              chunks (two passes: chunk maxima, then exp / sums / context
-//              merged in chunk order)
+//              residual epilogues; k_enc_attn_mma: bidirectional attention
+//              on f32 MFMA, 16 query rows of one head per wave over all rows
+//              in 64-key chunks (two passes: row maxima, then exp / sums /
+//              context merged in chunk order)
 //   adaptor    merge consecutive rows (a view), fc1 + SiLU, fc2, LayerNorm
 // Every reduction keeps the oracle's order (oracle/oracle.cpp, encoder
 // section), so results equal it bit for bit.
@@ -35,67 +36,118 @@ namespace {
 using namespace dev;
 
 constexpr int kEncHd = 64;      // head_dim
-constexpr int kEncRows = 64;    // query rows per attention workgroup
+constexpr int kEncRows = 64;    // query rows per attention workgroup (16 per wave)
 constexpr int kEncMaxChunks = 32;  // rows <= 2048
 constexpr int kConvTile = 64;   // outputs per conv workgroup: 64 rows x 64 channels
 constexpr int kConvIcb = 16;    // input channels staged per step
 
 // ------------------------------------------------------------- conv stem ---
-// out = gelu(conv(x) + b) (+ pos): x [IC][L] (frames fastest), w [OC][IC][3].
-// Thread (tx, ty): rows t0 + tx + 16 i, channels o0 + ty + 16 j (i, j < 4).
+// out = gelu(conv(x) + b) (+ pos) on f32 MFMA: the conv as a GEMM over
+// n = 3 c + k (input channel c, tap k), out[t][o] = sum_n w[o][n] X[n][t] with
+// X[n][t] = x[c][t * STRIDE + k - 1] (0 outside the frames). One MFMA chain per
+// 16 x 16 output tile over n in order is the canonical fma chain (tap fastest).
+// Workgroup: outputs o0 .. o0 + 63 x t0 .. t0 + 63; wave w: channels
+// o0 + 16 w + i (A = w rows) x four 16-row tiles of t (B = X columns). Per block
+// of 16 input channels (48 values of n) the w slab (element n = 4 s + g at
+// g * 12 + s) and the x rows are staged in LDS; the next block's loads are in
+// flight during the current block's MFMAs.
 // TRANS: out [OC][OL] (conv2's input layout), else out [OL][OC].
+constexpr int kCvNb = 3 * kConvIcb;  // values of n per staged block
+constexpr int kCvWs = kCvNb + 4;     // w slab row stride (floats)
 template <int STRIDE, bool TRANS>
 __global__ void __launch_bounds__(256)
-k_enc_conv(const float* __restrict__ w, const float* __restrict__ b, const float* __restrict__ x, int IC, int L,
-           int OC, const float* __restrict__ pos, float* __restrict__ out) {
+k_enc_conv_mma(const float* __restrict__ w, const float* __restrict__ b, const float* __restrict__ x, int IC, int L,
+               int OC, const float* __restrict__ pos, float* __restrict__ out) {
   constexpr int XW = kConvTile * STRIDE + 2;
-  __shared__ float xs[kConvIcb][XW];
-  __shared__ float ws[kConvTile][kConvIcb * 3 + 1];
+  constexpr int XN = (kConvIcb * XW + 255) / 256;  // x values per thread and block
+  __shared__ __align__(16) float xs[kConvIcb * XW];
+  __shared__ __align__(16) float ws[kConvTile * kCvWs];
   const int OL = (L - 1) / STRIDE + 1;
   const int t0 = blockIdx.x * kConvTile, o0 = blockIdx.y * kConvTile;
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, g = lane >> 4;
   const int p0 = t0 * STRIDE - 1;  // the input position of tap 0 of row t0
-  for (int ic0 = 0; ic0 < IC; ic0 += kConvIcb) {
-    for (int i = tid; i < kConvIcb * XW; i += 256) {
-      const int c = i / XW, q = i % XW, p = p0 + q;
-      xs[c][q] = (p >= 0 && p < L) ? x[(size_t)(ic0 + c) * L + p] : 0.0f;
-    }
-    for (int i = tid; i < kConvTile * kConvIcb * 3; i += 256) {
-      const int o = i / (kConvIcb * 3), e = i % (kConvIcb * 3);
-      ws[o][e] = w[((size_t)(o0 + o) * IC + ic0) * 3 + e];
-    }
-    __syncthreads();
-    for (int c = 0; c < kConvIcb; ++c)
+  // this lane's x offsets in the staged block: n = 4 s + g -> (c, k) = (n / 3, n % 3)
+  int xo[12];
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        float xv[4], wv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) xv[i] = xs[c][(tx + 16 * i) * STRIDE + k];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) wv[j] = ws[ty + 16 * j][c * 3 + k];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(wv[j], xv[i], acc[i][j]);
-      }
-    __syncthreads();
+  for (int s = 0; s < 12; ++s) {
+    const int n = 4 * s + g;
+    xo[s] = (n / 3) * XW + n % 3 + j * STRIDE;
   }
+  v4f wr[3];
+  float xr[XN];
+  auto load = [&](int ic0) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = t0 + tx + 16 * i;
-    if (t >= OL) continue;
+    for (int u = 0; u < 3; ++u) {
+      const int i = tid + 256 * u, o = i / (kCvNb / 4), q = i % (kCvNb / 4);
+      wr[u] = *(const v4f*)(w + (size_t)(o0 + o) * IC * 3 + (size_t)ic0 * 3 + 4 * q);
+    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int o = o0 + ty + 16 * j;
-      float y = dev_gelu_erf(__fadd_rn(acc[i][j], b[o]));
-      if (pos) y = __fadd_rn(y, pos[(size_t)t * OC + o]);
-      if (TRANS) out[(size_t)o * OL + t] = y;
-      else out[(size_t)t * OC + o] = y;
+    for (int u = 0; u < XN; ++u) {
+      const int i = tid + 256 * u, c = i / XW, p = p0 + i % XW;
+      xr[u] = (i < kConvIcb * XW && p >= 0 && p < L) ? x[(size_t)(ic0 + min(c, kConvIcb - 1)) * L + min(max(p, 0), L - 1)]
+                                                      : 0.0f;
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const int i = tid + 256 * u, o = i / (kCvNb / 4), q = i % (kCvNb / 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ws[o * kCvWs + e * 12 + q] = wr[u][e];  // n = 4 q + e
+    }
+#pragma unroll
+    for (int u = 0; u < XN; ++u) {
+      const int i = tid + 256 * u;
+      if (i < kConvIcb * XW) xs[i] = xr[u];
+    }
+  };
+  v4f acc[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) acc[tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  load(0);
+  for (int ic0 = 0; ic0 < IC; ic0 += kConvIcb) {
+    __syncthreads();  // the previous block's operands are consumed
+    stage();
+    __syncthreads();
+    if (ic0 + kConvIcb < IC) load(ic0 + kConvIcb);
+    v4f a[3];
+    const float* wrow = ws + (16 * wave + j) * kCvWs + g * 12;
+#pragma unroll
+    for (int u = 0; u < 3; ++u) a[u] = *(const v4f*)(wrow + 4 * u);
+#pragma unroll
+    for (int s = 0; s < 12; ++s)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s >> 2][s & 3], xs[xo[s] + 16 * tt * STRIDE], acc[tt], 0, 0,
+                                                       0);
+  }
+  // acc[tt][r]: output channel o0 + 16 wave + 4 g + r, row t0 + 16 tt + j
+  const int ob = o0 + 16 * wave + 4 * g;
+  const v4f bias = *(const v4f*)(b + ob);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = __fadd_rn(acc[2 * h + e / 4][e % 4], bias[e % 4]);
+    dev_gelu_erf_n<8>(y);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = t0 + 16 * (2 * h + u) + j;
+      if (t >= OL) continue;
+      v4f v;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = y[4 * u + r];
+      if (pos) {
+        const v4f pv = *(const v4f*)(pos + (size_t)t * OC + ob);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = __fadd_rn(v[r], pv[r]);
+      }
+      if constexpr (TRANS) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) out[(size_t)(ob + r) * OL + t] = v[r];
+      } else {
+        *(v4f*)(out + (size_t)t * OC + ob) = v;
+      }
     }
   }
 }
@@ -164,173 +216,208 @@ k_enc_ln(const float* __restrict__ src, int S, const float* __restrict__ w, cons
 }
 
 // ------------------------------------------------------------ attention ----
-// Rows r0 .. r0 + 63 of head blockIdx.x over all T rows (no mask), q / k / v /
-// out [T][W] (W = heads * 64). Thread (tr, tk) = (tid / 16, tid % 16) holds a
-// 4 x 4 register tile: the scores of rows 4 tr + i and keys 4 tk + j of a chunk
-// (fma chains over head_dim from 16-byte LDS reads), then the context of rows
-// 4 tr + i and elements 4 tk + e (fma chains over the chunk's keys). Pass 1
-// takes every chunk's row maxima; pass 2 recomputes the scores, p = exp(w - m_c),
-// l_c (fold-in-half over the 64 keys, the butterfly's order), O_c, and merges
-// the chunks in order.
-constexpr int kAS = kEncHd + 4;  // LDS row stride, floats (16-byte rows)
-__global__ void __launch_bounds__(256)
-k_enc_attn(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, int T, int W,
-           float* __restrict__ out) {
-  __shared__ __align__(16) float qs[kEncRows][kAS];
-  __shared__ __align__(16) float kv[64][kAS];  // the chunk's K, then its V
-  __shared__ __align__(16) float ps[kEncRows][kAS];
-  __shared__ float cm[kEncRows][kEncMaxChunks + 1];
-  __shared__ float cl[kEncRows];
+// Bidirectional attention on f32 MFMA (v_mfma_f32_16x16x4f32, whose 4-term dot
+// is the sequential fma chain fma(a3, b3, fma(a2, b2, fma(a1, b1, fma(a0, b0, c))))).
+// Workgroup = head blockIdx.x, rows r0 .. r0 + 63; wave w owns the 16 query rows
+// r0 + 16 w + j (j = lane % 16) over all keys, in 64-key chunks staged in LDS by
+// the whole workgroup (double-buffered, the next chunk's loads in flight during
+// the current chunk's arithmetic).
+//   scores: key tile t (16 keys) is one MFMA chain over head_dim, A = K rows,
+//     B = this wave's q rows (registers). A row i of tile t is key
+//     16 t + 4 (i % 4) + i / 4, so the output register r of lane (g, j)
+//     (g = lane / 16) holds the score of key 16 t + 4 r + g: key 4 m + g with
+//     m = 4 t + r, which is where the P.V MFMA m (keys 4 m .. 4 m + 3, in order)
+//     wants its B operand. The probabilities never leave the registers.
+//   chunk sum: the xor butterfly over the chunk's keys: levels 32 and 16 (t),
+//     8 and 4 (r) inside the lane, 2 and 1 (g) across lanes xor 32 and 16.
+//   P.V: head_dim tile dt is one MFMA chain over the chunk's keys, A = V^T.
+// Pass 1 takes each row's maximum over all keys; pass 2 recomputes the scores,
+// the chunk maxima m_c, p = exp(w - m_c), l_c and O_c, and merges the chunks in
+// order with f = exp(m_c - M): L = fma(l_c, f, L), O = fma(O_c, f, O).
+// LDS: K rows at slot 16 t + 4 g + r for key 16 t + 4 r + g, element 4 s + kk at
+// kk * 16 + s; V^T rows d with key 4 m + g at g * 16 + m. Rows 68 floats apart.
+constexpr int kEaStride = 68;
+constexpr int kEaBuf = 64 * kEaStride;  // floats per staged chunk (K or V^T)
+constexpr size_t kEaLds = (size_t)4 * kEaBuf * 4;  // K and V^T, two buffers each
+
+__device__ __forceinline__ void ea_load_k(const float* __restrict__ k, int key0, int T, int W, int h, v4f (&r)[4]) {
+  const int tid = threadIdx.x, key = tid >> 2, q = tid & 3;
+  const float* src = k + (size_t)min(key0 + key, T - 1) * W + h * kEncHd + 16 * q;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) r[x] = *(const v4f*)(src + 4 * x);
+}
+// K row key (element 16 q + 4 x + e = 4 s + kk with s = 4 q + x, kk = e) to slot
+// 16 t + 4 g + r of key 16 t + 4 r + g; rows past T are zero
+__device__ __forceinline__ void ea_store_k(float* s_k, int key0, int T, const v4f (&r)[4]) {
+  const int tid = threadIdx.x, key = tid >> 2, q = tid & 3;
+  const int slot = (key & ~15) | ((key & 3) << 2) | ((key >> 2) & 3);
+  const bool live = key0 + key < T;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v4f o;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) o[x] = live ? r[x][e] : 0.0f;
+    *(v4f*)(s_k + slot * kEaStride + e * 16 + 4 * q) = o;
+  }
+}
+// V: thread (g, mq, u) loads keys 4 (4 mq + x) + g, elements 4 u .. 4 u + 3
+__device__ __forceinline__ void ea_load_v(const float* __restrict__ v, int key0, int T, int W, int h, v4f (&r)[4]) {
+  const int tid = threadIdx.x, u = tid & 15, mq = (tid >> 4) & 3, g = tid >> 6;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const int key = 4 * (4 * mq + x) + g;
+    r[x] = *(const v4f*)(v + (size_t)min(key0 + key, T - 1) * W + h * kEncHd + 4 * u);
+  }
+}
+__device__ __forceinline__ void ea_store_v(float* s_v, int key0, int T, const v4f (&r)[4]) {
+  const int tid = threadIdx.x, u = tid & 15, mq = (tid >> 4) & 3, g = tid >> 6;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v4f o;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) o[x] = key0 + 4 * (4 * mq + x) + g < T ? r[x][e] : 0.0f;
+    *(v4f*)(s_v + (4 * u + e) * kEaStride + g * 16 + 4 * mq) = o;
+  }
+}
+
+__global__ void __launch_bounds__(256, 2)
+k_enc_attn_mma(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, int T, int W,
+               float* __restrict__ out) {
+  extern __shared__ v4f ea_lds_v4[];
+  float* s_k = (float*)ea_lds_v4;  // [2][kEaBuf]
+  float* s_v = s_k + 2 * kEaBuf;   // [2][kEaBuf]
   const int h = blockIdx.x, r0 = blockIdx.y * kEncRows;
-  const int tid = threadIdx.x, tr = tid >> 4, tk = tid & 15;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, g = lane >> 4;
   const int nch = (T + 63) / 64;
   const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)kEncHd));
-  const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-  // 64 rows x 64 floats of src from row0 (zeros past T): load4 issues the four
-  // 16-byte loads of this thread (rows past T read row T - 1 and are zeroed after
-  // the load, so no branch splits them), store4 writes them to dst. A chunk's
-  // loads go out one chunk ahead and land during the previous chunk's arithmetic.
-  auto load4 = [&](const float* src, int row0, v4f (&r)[4]) {
+  // the B operand of the scores: q[row][4 s + g], s < 16 (rows past T: zeros)
+  const int row = r0 + 16 * wave + j;
+  float qb[16];
+  {
+    const float* qr = q + (size_t)min(row, T - 1) * W + h * kEncHd + g;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int i = tid + 256 * x, rr = i >> 4, d4 = i & 15;
-      r[x] = *(const v4f*)(src + (size_t)min(row0 + rr, T - 1) * W + h * kEncHd + 4 * d4);
-      if (row0 + rr >= T) r[x] = zero4;
-    }
-  };
-  auto store4 = [&](float (*dst)[kAS], const v4f (&r)[4]) {
+    for (int s = 0; s < 16; ++s) qb[s] = row < T ? qr[4 * s] : 0.0f;
+  }
+  // scores of the staged chunk at key0: w[t][r] = key 16 t + 4 r + g, row j
+  auto scores = [&](const float* sk, int key0, float (&w)[4][4]) {
+    v4f acc[4];
+    v4f a[4][4];
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int i = tid + 256 * x, rr = i >> 4, d4 = i & 15;
-      *(v4f*)&dst[rr][4 * d4] = r[x];
-    }
-  };
-  auto scores = [&](int key0, float (&w)[4][4]) {
-    float acc[4][4];
+    for (int t = 0; t < 4; ++t) {
+      acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      const float* kr = sk + (16 * t + j) * kEaStride + g * 16;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-    for (int d0 = 0; d0 < kEncHd; d0 += 4) {
-      v4f qv[4], kx[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) qv[i] = *(const v4f*)&qs[4 * tr + i][d0];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) kx[j] = *(const v4f*)&kv[4 * tk + j][d0];
-#pragma unroll
-      for (int dd = 0; dd < 4; ++dd)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(qv[i][dd], kx[j][dd], acc[i][j]);
+      for (int x = 0; x < 4; ++x) a[t][x] = *(const v4f*)(kr + 4 * x);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int s = 0; s < 16; ++s)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) w[i][j] = key0 + 4 * tk + j < T ? __fmul_rn(acc[i][j], scale) : -INFINITY;
+      for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s >> 2][s & 3], qb[s], acc[t], 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[t][r] = key0 + 16 * t + 4 * r + g < T ? __fmul_rn(acc[t][r], scale) : -INFINITY;
   };
   v4f kr[4], vr[4];
-  load4(q, r0, vr);
-  load4(k, 0, kr);
-  store4(qs, vr);
-  // pass 1: chunk maxima per row (over the 16 threads of a row group)
-  for (int c = 0; c < nch; ++c) {
-    __syncthreads();
-    store4(kv, kr);
-    __syncthreads();
-    if (c + 1 < nch) load4(k, 64 * (c + 1), kr);
-    float w[4][4];
-    scores(64 * c, w);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float m = fmaxf(fmaxf(w[i][0], w[i][1]), fmaxf(w[i][2], w[i][3]));
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
-      if (tk == 0) cm[4 * tr + i][c] = m;
-    }
-  }
+  // chunk n of the whole walk: n < nch is pass 1 (K only), n >= nch pass 2 (K and V)
+  ea_load_k(k, 0, T, W, h, kr);
+  ea_store_k(s_k, 0, T, kr);
   __syncthreads();
-  float M[4], L[4], O[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    M[i] = -INFINITY;
-    for (int c = 0; c < nch; ++c) M[i] = fmaxf(M[i], cm[4 * tr + i][c]);
-    L[i] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) O[i][e] = 0.0f;
-  }
-  // pass 2
-  load4(k, 0, kr);
-  load4(v, 0, vr);
-  for (int c = 0; c < nch; ++c) {
-    __syncthreads();
-    store4(kv, kr);
-    __syncthreads();
-    if (c + 1 < nch) load4(k, 64 * (c + 1), kr);
+  float M = -INFINITY;
+  for (int n = 0; n < nch; ++n) {
+    const int nx = n + 1 < nch ? n + 1 : 0;  // the next staged chunk (pass 2 starts at chunk 0)
+    ea_load_k(k, 64 * nx, T, W, h, kr);
+    if (n + 1 == nch) ea_load_v(v, 0, T, W, h, vr);
     float w[4][4];
-    scores(64 * c, w);
+    scores(s_k + (n & 1) * kEaBuf, 64 * n, w);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float mc = cm[4 * tr + i][c];
-      v4f p4;
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) p4[j] = w[i][j] == -INFINITY ? 0.0f : dev_expf(__fsub_rn(w[i][j], mc));
-      *(v4f*)&ps[4 * tr + i][4 * tk] = p4;
-    }
-    __syncthreads();  // K consumed, p complete
-    store4(kv, vr);
-    if (c + 1 < nch) load4(v, 64 * (c + 1), vr);
-    if (tid < kEncRows) {
-      float t[64];
-#pragma unroll
-      for (int j = 0; j < 64; j += 4) {
-        const v4f p4 = *(const v4f*)&ps[tid][j];
-        t[j] = p4[0];
-        t[j + 1] = p4[1];
-        t[j + 2] = p4[2];
-        t[j + 3] = p4[3];
-      }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1)
-#pragma unroll
-        for (int j = 0; j < o; ++j) t[j] = __fadd_rn(t[j], t[j + o]);
-      cl[tid] = t[0];
-    }
-    __syncthreads();  // V staged, l_c ready
-    float oc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) oc[i][e] = 0.0f;
-    for (int j0 = 0; j0 < 64; j0 += 4) {
-      v4f pv[4], vv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pv[i] = *(const v4f*)&ps[4 * tr + i][j0];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) vv[jj] = *(const v4f*)&kv[j0 + jj][4 * tk];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) oc[i][e] = fmaf(pv[i][jj], vv[jj][e], oc[i][e]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float f = dev_expf(__fsub_rn(cm[4 * tr + i][c], M[i]));
-      L[i] = fmaf(cl[4 * tr + i], f, L[i]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) O[i][e] = fmaf(oc[i][e], f, O[i][e]);
-    }
+      for (int r = 0; r < 4; ++r) M = fmaxf(M, w[t][r]);
+    ea_store_k(s_k + ((n + 1) & 1) * kEaBuf, 64 * nx, T, kr);
+    if (n + 1 == nch) ea_store_v(s_v + ((n + 1) & 1) * kEaBuf, 0, T, vr);
+    __syncthreads();
   }
+  M = pair_max_f<32>(M);
+  M = pair_max_f<16>(M);
+  float L = 0.0f;
+  v4f O[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = r0 + 4 * tr + i;
-    if (row >= T) continue;
-    v4f o4;
+  for (int dt = 0; dt < 4; ++dt) O[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = 0; c < nch; ++c) {
+    const int b = (nch + c) & 1;
+    const bool more = c + 1 < nch;
+    if (more) {
+      ea_load_k(k, 64 * (c + 1), T, W, h, kr);
+      ea_load_v(v, 64 * (c + 1), T, W, h, vr);
+    }
+    float w[4][4];
+    scores(s_k + b * kEaBuf, 64 * c, w);
+    float mc = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o4[e] = __fdiv_rn(O[i][e], L[i]);
-    *(v4f*)(out + (size_t)row * W + h * kEncHd + 4 * tk) = o4;
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mc = fmaxf(mc, w[t][r]);
+    mc = pair_max_f<32>(mc);
+    mc = pair_max_f<16>(mc);
+    float p[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[t][r] = w[t][r] == -INFINITY ? 0.0f : dev_expf(__fsub_rn(w[t][r], mc));
+    // l_c: key levels 32, 16 (t), 8, 4 (r) in the lane, 2, 1 (g) across lanes
+    float lc;
+    {
+      float u[2][4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) u[t][r] = __fadd_rn(p[t][r], p[t + 2][r]);
+      float x[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = __fadd_rn(u[0][r], u[1][r]);
+      const float y0 = __fadd_rn(x[0], x[2]), y1 = __fadd_rn(x[1], x[3]);
+      lc = pair_add_f<32>(__fadd_rn(y0, y1));
+      lc = pair_add_f<16>(lc);
+    }
+    // O_c: head_dim tiles dt, A = V^T rows 16 dt + j, B = p (key 4 m + g at p[m / 4][m % 4])
+    const float* sv = s_v + b * kEaBuf;
+    v4f oc[4];
+    v4f av[4][4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      oc[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      const float* vrow = sv + (16 * dt + j) * kEaStride + g * 16;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) av[dt][x] = *(const v4f*)(vrow + 4 * x);
+    }
+#pragma unroll
+    for (int m = 0; m < 16; ++m)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        oc[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[dt][m >> 2][m & 3], p[m >> 2][m & 3], oc[dt], 0, 0, 0);
+    const float f = dev_expf(__fsub_rn(mc, M));
+    L = fmaf(lc, f, L);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) O[dt][r] = fmaf(oc[dt][r], f, O[dt][r]);
+    if (more) {
+      ea_store_k(s_k + (b ^ 1) * kEaBuf, 64 * (c + 1), T, kr);
+      ea_store_v(s_v + (b ^ 1) * kEaBuf, 64 * (c + 1), T, vr);
+    }
+    __syncthreads();
+  }
+  // O[dt][r] is element 16 dt + 4 g + r of row j
+  if (row < T) {
+    float* orow = out + (size_t)row * W + h * kEncHd + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      v4f o4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o4[r] = __fdiv_rn(O[dt][r], L);
+      *(v4f*)(orow + 16 * dt) = o4;
+    }
   }
 }
 
@@ -453,6 +540,10 @@ int mtg_encoder_create(const mtg_encoder_desc* d, mtg_encoder** out) {
   int rc = e->check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "stream");
   if (!rc) rc = e->check(hipEventCreate(&e->ev0), "event");
   if (!rc) rc = e->check(hipEventCreate(&e->ev1), "event");
+  if (!rc)
+    rc = e->check(hipFuncSetAttribute((const void*)k_enc_attn_mma, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)kEaLds),
+                  "attention LDS");
   // staging for the raw q8_0 rows of the largest matrix
   size_t raw_max = (size_t)std::max(F, std::max(D, H)) * (std::max(F, IN) / 32) * 34;
   uint8_t* staging = rc ? nullptr : (uint8_t*)e->dalloc(raw_max);
@@ -536,9 +627,9 @@ int mtg_encoder_encode(mtg_encoder* e, const float* mel, float* out, int32_t* ro
   if (rc) return rc;
   if ((rc = e->check(hipEventRecord(e->ev0, s), "event"))) return rc;
   // conv stem
-  hipLaunchKernelGGL((k_enc_conv<1, true>), dim3((NF + kConvTile - 1) / kConvTile, D / kConvTile), dim3(256), 0, s,
+  hipLaunchKernelGGL((k_enc_conv_mma<1, true>), dim3((NF + kConvTile - 1) / kConvTile, D / kConvTile), dim3(256), 0, s,
                      e->conv1_w, e->conv1_b, e->mel, M, NF, D, (const float*)nullptr, e->c1);
-  hipLaunchKernelGGL((k_enc_conv<2, false>), dim3((R + kConvTile - 1) / kConvTile, D / kConvTile), dim3(256), 0, s,
+  hipLaunchKernelGGL((k_enc_conv_mma<2, false>), dim3((R + kConvTile - 1) / kConvTile, D / kConvTile), dim3(256), 0, s,
                      e->conv2_w, e->conv2_b, e->c1, D, NF, D, e->pos, e->x);
   const dim3 agrid((unsigned)hp.n_heads, (unsigned)((R + kEncRows - 1) / kEncRows));
   for (const mtg_encoder::Layer& L : e->layers) {
@@ -546,7 +637,7 @@ int mtg_encoder_encode(mtg_encoder* e, const float* mel, float* out, int32_t* ro
     e->gemm(PF_EPI_BIAS, L.q_w, D, D, R, e->q, L.q_b);
     e->gemm(PF_EPI_STORE, L.k_w, D, D, R, e->k, nullptr);
     e->gemm(PF_EPI_BIAS, L.v_w, D, D, R, e->v, L.v_b);
-    hipLaunchKernelGGL(k_enc_attn, agrid, dim3(256), 0, s, e->q, e->k, e->v, R, D, e->a);
+    hipLaunchKernelGGL(k_enc_attn_mma, agrid, dim3(256), kEaLds, s, e->q, e->k, e->v, R, D, e->a);
     e->quant(e->a, R, D);
     e->gemm(PF_EPI_BIAS_RESID, L.o_w, D, D, R, e->x, L.o_b);
     e->ln(e->x, R, L.ffn_ln_w, L.ffn_ln_b, 1e-5f, true, nullptr);

@@ -245,33 +245,66 @@ k_pf_gemm(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int N, 
       for (int q = 0; q < 4; ++q) tot[cg][q] = dev_swiglu(tot[cg][q], u[q]);
     }
   }
-  if (j < 8) {
-    const int n = tile * 16 + 4 * (lane >> 4);
+  // lanes j and j + 8 hold the same sums: lane j takes row groups 0..3 of
+  // rows s0 + 8 cg + j, lane j + 8 groups 4..7
+  {
+    const int n = tile * 16 + 4 * (lane >> 4), hi = j >> 3;
+    // a mask the compiler cannot see through: a plain select between tot[c] and
+    // tot[4 + c] becomes a lane-dependent index into tot, which moves tot to
+    // scratch memory for the whole kernel
+    uint32_t m = 0u - (uint32_t)hi;
+    asm volatile("" : "+v"(m));
+    float y[4][4];
 #pragma unroll
-    for (int cg = 0; cg < 8; ++cg) {
-      const int row = s0 + 8 * cg + j;
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t lo = __float_as_uint(tot[c][q]);
+        y[c][q] = __uint_as_float(lo ^ ((lo ^ __float_as_uint(tot[4 + c][q])) & m));
+      }
+    if constexpr (EPI >= PF_BIAS) {
+      // linear = mul_mat + bias, then the activation or the residual add
+      const v4f b = *(const v4f*)(bias + n);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) y[c][q] = __fadd_rn(y[c][q], b[q]);
+      if constexpr (EPI == PF_BIAS_GELU) {
+#pragma unroll
+        for (int c = 0; c < 4; c += 2) {
+          float g[8];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            g[q] = y[c][q];
+            g[4 + q] = y[c + 1][q];
+          }
+          dev_gelu_erf_n<8>(g);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            y[c][q] = g[q];
+            y[c + 1][q] = g[4 + q];
+          }
+        }
+      }
+      if constexpr (EPI == PF_BIAS_SILU)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) y[c][q] = dev_silu(y[c][q]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int row = s0 + 8 * (4 * hi + c) + (j & 7);
       if (row >= S) continue;
       float* dst = out + (size_t)row * N + n;
       v4f v;
-      if (EPI == PF_RESID) {
+      if constexpr (EPI == PF_RESID || EPI == PF_BIAS_RESID) {
         const v4f x = *(const v4f*)dst;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = __fadd_rn(x[q], tot[cg][q]);
-      } else if (EPI >= PF_BIAS) {
-        // linear = mul_mat + bias, then the activation or the residual add
-        const v4f b = *(const v4f*)(bias + n);
-        v4f x{};
-        if (EPI == PF_BIAS_RESID) x = *(const v4f*)dst;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float y = __fadd_rn(tot[cg][q], b[q]);
-          v[q] = EPI == PF_BIAS_GELU ? dev_gelu_erf(y)
-                 : EPI == PF_BIAS_SILU ? dev_silu(y)
-                 : EPI == PF_BIAS_RESID ? __fadd_rn(x[q], y) : y;
-        }
+        for (int q = 0; q < 4; ++q) v[q] = __fadd_rn(x[q], y[c][q]);
       } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = tot[cg][q];
+        for (int q = 0; q < 4; ++q) v[q] = y[c][q];
       }
       *(v4f*)dst = v;
     }

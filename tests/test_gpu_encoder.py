@@ -2,8 +2,10 @@
 WhisperEncoder::encode, src/whisper_encoder.cpp:103-209, AudioAdaptor::apply,
 src/audio_adaptor.cpp:38-97) against the oracle: encoder rows and adaptor rows
 bit-identical (the kernels keep the oracle's order of every reduction), at a
-short chunk and at the full 3,000-frame chunk (1,500 rows); the 24-layer
-encoder is timed and checked for determinism."""
+short chunk, at the full 3,000-frame chunk (1,500 rows) with 2 layers, and for
+the whole 24-layer encoder (also timed and checked for determinism)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -57,7 +59,10 @@ def test_full_chunk_two_layers_matches_oracle():
     orc.close()
 
 
-def test_full_encoder_24_layers_timed_and_deterministic():
+@pytest.mark.timeout(900)
+def test_full_encoder_24_layers_matches_oracle():
+    """The whole 24-layer encoder on the full 3,000-frame chunk and the adaptor's
+    375 rows: bit-identical to the oracle, repeated encodes identical, timed."""
     syn = mtg.SynthEncoder(seed=21)
     dev = mtg.Encoder(syn)
     mel = syn.mel(seed=22)
@@ -71,6 +76,12 @@ def test_full_encoder_24_layers_timed_and_deterministic():
     print("24-layer encoder, 3,000 frames -> 1,500 rows: %.2f ms (min of 3), adaptor %.3f ms"
           % (min(ms), dev.last_ms), flush=True)
     assert np.isfinite(a).all() and np.isfinite(ad).all()
+    oracle_py.lib().orc_set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    orc = oracle_py.OracleEncoder(syn)
+    print("24-layer encoder: the oracle's encode", flush=True)
+    _same(a, orc.encode(mel), "24-layer encoder rows")
+    _same(ad, orc.adapt(1500), "adaptor rows after 24 layers")
+    orc.close()
     # ln_post's output rows: (y - b) / w has mean 0 and variance 1 per row
     d = syn.desc
     w = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_float * 1024).from_address(d.ln_post_w))
