@@ -13,9 +13,9 @@
 //                    add / SwiGLU
 //   k_pf_quant       q8_0 conversion of f32 rows (the SwiGLU output)
 //   k_pf_qk_rope     q/k RMSNorm + NEOX RoPE, K/V written into the cache
-//   k_pf_attn        causal attention of 16 query rows of one q head per
-//                    workgroup over the cache, in two passes over the 64-key
-//                    chunks, writing the o-projection's q8_0 activation
+//   k_pf_attn_mma    causal attention on f32 MFMA, 16 query rows of one q
+//                    head per wave over the cache, in two passes over the
+//                    64-key chunks, writing the o-projection's q8_0 activation
 // Every reduction follows the canonical order of device_common.hpp, so hidden
 // rows and the KV cache equal the verify path's and the oracle's bit for bit:
 //   * GEMM: per output, 4 K-slices of block pairs, even / odd fma chains per
@@ -36,8 +36,6 @@ namespace {
 using namespace dev;
 
 constexpr int kH = 1024;         // hidden (the RMSNorm partials assume 1024)
-constexpr int kPfQStride = 132;  // LDS row strides (floats)
-constexpr int kPfPStride = 68;
 
 // ---------------------------------------------------------- activations ----
 // One wave per row of 1024: lane l holds elements 16 l .. 16 l + 15 (the
@@ -362,246 +360,305 @@ k_pf_qk_rope(const float* __restrict__ qkv, int S, int past0, int n_heads, int n
 // ------------------------------------------------------------ attention ----
 // grid (n_heads / kPfHeads, ceil(S / kPfRows)): a workgroup takes query rows
 // r0 .. r0 + kPfRows - 1 (positions past0 + r0 + t) of the kPfHeads q heads of
-// one kv head, columns col = kPfRows hl + t; the blocks with the most chunks are
-// numbered first. Keys 0 .. past0 + r0 + kPfRows - 1 come from the cache (this block's
-// rows were appended by k_pf_qk_rope). The output rows leave as the
-// o-projection's q8_0 activation: codes [S][n_heads * 128], scales [S][n_heads * 4].
-__device__ __forceinline__ int pf_perm128(int d) { return (d & 3) * 32 + (d >> 2); }
-
-// K and V of the 64-key chunk at key0 in MFMA operand layout, loaded straight
-// into registers (f32, or f16 widened; zeros past kvlen). Wave w: scores of keys
-// 16 w + kl, k[m] = K[key0 + 16 w + kl][4 m + kk] (m < 32, the fma chain over
-// head_dim in order); P.V of head_dim tiles 2 w, 2 w + 1,
-// v[h][s] = V[key0 + 4 s + kk][16 (2 w + h) + kl] (s < 16, the chain over keys).
+// one kv head; the blocks with the most chunks are numbered first. Keys
+// 0 .. past0 + r0 + kPfRows - 1 come from the cache (this block's rows were
+// appended by k_pf_qk_rope). The output rows leave as the o-projection's q8_0
+// activation: codes [S][n_heads * 128], scales [S][n_heads * 4].
 constexpr int kPfHeads = 2;     // q heads per workgroup (one kv head's group)
 constexpr int kPfRowTiles = 2;  // query rows per workgroup / 16
 constexpr int kPfRows = 16 * kPfRowTiles;
-constexpr int kPfCols = kPfHeads * kPfRows;  // column tile ct: q head ct / kPfRowTiles, rows 16 (ct % kPfRowTiles) + kl
 
-typedef __amdgpu_buffer_rsrc_t PfRsrc;
-// A buffer descriptor over kv head rows [0, kvlen): loads past its end return 0.
-// The range check covers the per-lane offset only, so every key-dependent part
-// of an address goes there (the scalar offset stays 0).
-__device__ __forceinline__ PfRsrc pf_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
-template <int KVH>
-__device__ __forceinline__ float pf_kv(PfRsrc r, uint32_t voff, uint32_t soff) {
-  if constexpr (KVH)
-    return half_bits_to_float((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0));
-  else
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
-}
-template <int KVH>
-__device__ __forceinline__ void pf_load_k(PfRsrc rk, int key0, float (&k)[32]) {
-  constexpr int es = KVH ? 2 : 4;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kl = lane & 15, kk = lane >> 4;
-  const uint32_t voff = (uint32_t)(((key0 + 16 * wave + kl) * kHeadDim + kk) * es);
-#pragma unroll
-  for (int m = 0; m < 32; ++m) k[m] = pf_kv<KVH>(rk, voff + 4 * m * es, 0);
-}
-template <int KVH>
-__device__ __forceinline__ void pf_load_v(PfRsrc rv, int key0, float (&v)[2][16]) {
-  constexpr int es = KVH ? 2 : 4;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kl = lane & 15, kk = lane >> 4;
-  const uint32_t voff = (uint32_t)(((key0 + kk) * kHeadDim + 32 * wave + kl) * es);
-#pragma unroll
-  for (int s2 = 0; s2 < 16; ++s2)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) v[h][s2] = pf_kv<KVH>(rv, voff + (4 * s2 * kHeadDim + 16 * h) * es, 0);
-}
+// ------------------------------------------------ attention on f32 MFMA ----
+// k_pf_attn_mma: the causal attention of k_pf_attn with the chunk softmax kept in
+// registers. Workgroup = the two q heads of one kv head x 32 query rows; wave w
+// owns the 16 rows r0 + 16 (w & 1) + j (j = lane % 16) of q head hq0 + w / 2.
+//   scores: key tile t (16 keys) is one chain of 32 MFMAs over head_dim,
+//     A = K rows, B = the wave's q rows (registers). Row i of the A operand is
+//     key 16 t + 4 (i % 4) + i / 4, so output register r of lane (g, j)
+//     (g = lane / 16) holds key 16 t + 4 r + g: the B operand of P.V MFMA
+//     m = 4 t + r (keys 4 m .. 4 m + 3 in order) with no data movement.
+//   chunk max and sum: in-lane over t and r, then across lanes xor 32, 16 (the
+//     sum in the butterfly's pairing: key levels 32, 16, 8, 4 in the lane, 2, 1
+//     across lanes).
+//   P.V: head_dim tile dt (16) is one chain of 16 MFMAs over the chunk's keys,
+//     A = V^T.
+// The chunks go through LDS: K rows at slot 16 t + 4 g + r for key 16 t + 4 r + g,
+// element 4 s + g at g * 32 + s; V^T rows d with key 4 m + g at g * 16 + m. Pass 1
+// (row maxima) double-buffers K in the two regions; pass 2 holds K in one and
+// V^T in the other, the next chunk's loads in flight during the arithmetic.
+// A wave skips the chunks that lie wholly after its last row (their terms are
+// exact zeros of the merge).
+constexpr int kPaKs = kHeadDim + 4;              // K slab row stride (floats)
+constexpr int kPaVs = 64 + 4;                    // V^T slab row stride
+constexpr int kPaRegion = kHeadDim * kPaVs;      // floats per region (>= 64 * kPaKs)
+constexpr size_t kPaLds = (size_t)2 * kPaRegion * 4;
+static_assert(64 * kPaKs <= kPaRegion, "K slab fits a region");
 
-// Scores of keys 16 wave + 4 kk + r (r < 4) for columns 16 ct + kl, scaled and
-// masked: the fma chain over head_dim is 32 chained MFMAs.
-template <int NCT>
-__device__ __forceinline__ void pf_scores(const float* s_q, const float (&k)[32], int key0, int kvlen, int past0,
-                                          int r0, int nq, float scale, float (&w)[NCT][4]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kl = lane & 15, kk = lane >> 4;
+// this thread's share of a chunk of K (keys key0 ..): key tid / 4, elements
+// 32 (tid % 4) .. + 31; of V: keys 4 (4 mq + x) + g (x < 4), elements 8 u .. 8 u + 7
+// with (g, mq, u) = (tid / 64, tid / 16 % 4, tid % 16). Rows past kvlen read row
+// kvlen - 1 and are zeroed at the store.
+template <int KVH>
+struct PaRegs {
+  v4f r[8];
+};
+template <int KVH>
+__device__ __forceinline__ void pa_load_k(const uint8_t* kh, int key0, int kvlen, PaRegs<KVH>& R) {
+  constexpr int es = KVH ? 2 : 4;
+  const int tid = threadIdx.x, key = min(key0 + (tid >> 2), kvlen - 1), q = tid & 3;
+  const uint8_t* src = kh + ((size_t)key * kHeadDim + 32 * q) * es;
+  if constexpr (KVH) {
 #pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) {
-    const float* qrow = s_q + (ct * 16 + kl) * kPfQStride + kk * 32;
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int x = 0; x < 4; ++x) {
+      const v4i h = *(const v4i*)(src + 16 * x);  // 8 halves: elements 32 q + 8 x ..
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const v4f q4 = *(const v4f*)(qrow + 4 * i);
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[4 * i + jj], q4[jj], acc, 0, 0, 0);
+      for (int e = 0; e < 4; ++e) {
+        R.r[2 * x + e / 2][2 * (e % 2)] = half_bits_to_float((uint16_t)((uint32_t)h[e] & 0xffff));
+        R.r[2 * x + e / 2][2 * (e % 2) + 1] = half_bits_to_float((uint16_t)((uint32_t)h[e] >> 16));
+      }
     }
-    const int t = 16 * (ct % kPfRowTiles) + kl;  // column 16 ct + kl: row t of q head ct / kPfRowTiles
+  } else {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = key0 + 16 * wave + 4 * kk + r;
-      w[ct][r] = (t < nq && key < kvlen && key <= past0 + r0 + t) ? __fmul_rn(acc[r], scale) : -INFINITY;
+    for (int x = 0; x < 8; ++x) R.r[x] = *(const v4f*)(src + 16 * x);
+  }
+}
+template <int KVH>
+__device__ __forceinline__ void pa_store_k(float* s, int key0, int kvlen, const PaRegs<KVH>& R) {
+  const int tid = threadIdx.x, key = tid >> 2, q = tid & 3;
+  const int slot = (key & ~15) | ((key & 3) << 2) | ((key >> 2) & 3);
+  const bool live = key0 + key < kvlen;
+  // R.r[x][e] is element 32 q + 4 x + e = 4 s + g with s = 8 q + x, g = e
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4f o;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) o[x] = live ? R.r[4 * h + x][e] : 0.0f;
+      *(v4f*)(s + slot * kPaKs + e * 32 + 8 * q + 4 * h) = o;
+    }
+}
+template <int KVH>
+__device__ __forceinline__ void pa_load_v(const uint8_t* vh, int key0, int kvlen, PaRegs<KVH>& R) {
+  constexpr int es = KVH ? 2 : 4;
+  const int tid = threadIdx.x, u = tid & 15, mq = (tid >> 4) & 3, g = tid >> 6;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const int key = min(key0 + 4 * (4 * mq + x) + g, kvlen - 1);
+    const uint8_t* src = vh + ((size_t)key * kHeadDim + 8 * u) * es;
+    if constexpr (KVH) {
+      const v4i h = *(const v4i*)src;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        R.r[2 * x + e / 2][2 * (e % 2)] = half_bits_to_float((uint16_t)((uint32_t)h[e] & 0xffff));
+        R.r[2 * x + e / 2][2 * (e % 2) + 1] = half_bits_to_float((uint16_t)((uint32_t)h[e] >> 16));
+      }
+    } else {
+      R.r[2 * x] = *(const v4f*)src;
+      R.r[2 * x + 1] = *(const v4f*)(src + 16);
     }
   }
 }
+template <int KVH>
+__device__ __forceinline__ void pa_store_v(float* s, int key0, int kvlen, const PaRegs<KVH>& R) {
+  const int tid = threadIdx.x, u = tid & 15, mq = (tid >> 4) & 3, g = tid >> 6;
+  // R.r[2 x + e / 4][e % 4] is element 8 u + e of key 4 (4 mq + x) + g
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    v4f o;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) o[x] = key0 + 4 * (4 * mq + x) + g < kvlen ? R.r[2 * x + e / 4][e % 4] : 0.0f;
+    *(v4f*)(s + (8 * u + e) * kPaVs + g * 16 + 4 * mq) = o;
+  }
+}
 
-constexpr size_t kPfAttnLds =
-    ((size_t)kPfCols * kPfQStride + kPfCols * kPfPStride + 4 * kPfCols + 3 * kPfCols) * 4;
-
-// OUTF: the output rows as f32 [S][n_heads * 128] in ofl (the f16 / q4_K weight
-// paths convert them to their vec_dot_type), instead of q8_0 codes.
-template <int KVH, bool OUTF = false>
-__global__ void __launch_bounds__(256)
-k_pf_attn(const float* __restrict__ q, int n_heads, int n_kv_heads, KvLayer kv, int past0, int S,
-          int8_t* __restrict__ ocodes, float* __restrict__ oscales, float* __restrict__ ofl) {
-  constexpr int NCT = kPfCols / 16, NC = kPfCols;
-  // the query blocks with the most chunks start first
-  const int hq0 = blockIdx.x * kPfHeads, g = hq0 / (n_heads / n_kv_heads);
-  const int r0 = (gridDim.y - 1 - blockIdx.y) * kPfRows;
-  const int nq = min(kPfRows, S - r0);
+template <int KVH, bool OUTF>
+__global__ void __launch_bounds__(256, 2)
+k_pf_attn_mma(const float* __restrict__ q, int n_heads, int n_kv_heads, KvLayer kv, int past0, int S,
+              int8_t* __restrict__ ocodes, float* __restrict__ oscales, float* __restrict__ ofl) {
+  extern __shared__ v4f pa_lds_v4[];
+  float* reg0 = (float*)pa_lds_v4;
+  float* reg1 = reg0 + kPaRegion;
+  const int hq0 = blockIdx.x * kPfHeads, g_kv = hq0 / (n_heads / n_kv_heads);
+  const int r0 = (gridDim.y - 1 - blockIdx.y) * kPfRows;  // the blocks with the most chunks start first
   const int kvlen = past0 + S;
-  const int last = past0 + r0 + nq - 1;  // the block's last query position
-  const int nch = last / kChunk + 1;
-  extern __shared__ v4f pf_lds_v4[];
-  float* s_q = (float*)pf_lds_v4;                  // [NC][132] permuted
-  float* s_p = s_q + NC * kPfQStride;              // [NC][68] permuted keys
-  float* s_wm = s_p + NC * kPfPStride;             // [4 waves][NC]
-  float* s_l = s_wm + 4 * NC;                      // [NC] chunk sums
-  float* s_f = s_l + NC;                           // [NC] chunk factors
-  float* s_M = s_f + NC;                           // [NC] column maxima over all chunks
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, kl = lane & 15, kk = lane >> 4;
-  constexpr bool f16kv = KVH != 0;
-  // q rows (f16-rounded for an f16 cache: mul_mat(f16 K, f32 q) converts q)
-  for (int idx = tid; idx < NC * (kHeadDim / 4); idx += 256) {
-    const int col = idx / (kHeadDim / 4), d = (idx % (kHeadDim / 4)) * 4, hl = col / kPfRows, t = col % kPfRows;
-    v4f v = {0.f, 0.f, 0.f, 0.f};
-    if (t < nq) v = *(const v4f*)(q + ((size_t)(r0 + t) * n_heads + hq0 + hl) * kHeadDim + d);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s_q[col * kPfQStride + pf_perm128(d + e)] = f16kv ? f16_round(v[e]) : v[e];
-  }
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, g = lane >> 4;
+  const int hq = hq0 + (wave >> 1), rw = r0 + 16 * (wave & 1);  // this wave's head and first row
+  const int row = rw + j;
+  const int nch = min(past0 + r0 + kPfRows - 1, kvlen - 1) / kChunk + 1;  // the workgroup's chunks
+  const int wlast = min(past0 + rw + 15, kvlen - 1);                    // this wave's last key
   constexpr int es = KVH ? 2 : 4;
-  const size_t head = (size_t)g * kv.max_seq * kHeadDim * es;
-  const uint32_t kvbytes = (uint32_t)kvlen * kHeadDim * es;
-  const PfRsrc rk = pf_rsrc((const uint8_t*)kv.k + head, kvbytes);
-  const PfRsrc rv = pf_rsrc((const uint8_t*)kv.v + head, kvbytes);
+  const uint8_t* kh = (const uint8_t*)kv.k + (size_t)g_kv * kv.max_seq * kHeadDim * es;
+  const uint8_t* vh = (const uint8_t*)kv.v + (size_t)g_kv * kv.max_seq * kHeadDim * es;
   const float scale = __fdiv_rn(1.0f, dev_sqrtf((float)kHeadDim));
-  float kr[32], vr[2][16];
-  // pass 1: each column's maximum over all chunks (exact in any order)
-  pf_load_k<KVH>(rk, 0, kr);
-  __syncthreads();
-  int colmax[NCT];  // per column tile: the lane's column kl
+  // B operand of the scores: q[row][4 s + g] (f16-rounded for an f16 cache)
+  float qb[32];
+  {
+    const float* qr = q + ((size_t)min(row, S - 1) * n_heads + hq) * kHeadDim + g;
 #pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) colmax[ct] = ord_key(-INFINITY);
-  for (int c = 0; c < nch; ++c) {
-    float w[NCT][4];
-    pf_scores<NCT>(s_q, kr, c * kChunk, kvlen, past0, r0, nq, scale, w);
-    if (c + 1 < nch) pf_load_k<KVH>(rk, (c + 1) * kChunk, kr);
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) colmax[ct] = max(colmax[ct], ord_key(w[ct][r]));
-  }
-#pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) {
-    uint32_t a, b;
-    pair_split<16>((uint32_t)colmax[ct], a, b);  // the lanes kk of one column
-    colmax[ct] = max((int)a, (int)b);
-    pair_split<32>((uint32_t)colmax[ct], a, b);
-    colmax[ct] = max((int)a, (int)b);
-    if (kk == 0) s_wm[wave * NC + ct * 16 + kl] = ord_val(colmax[ct]);
-  }
-  __syncthreads();
-  if (tid < NC)
-    s_M[tid] = fmaxf(fmaxf(s_wm[tid], s_wm[NC + tid]), fmaxf(s_wm[2 * NC + tid], s_wm[3 * NC + tid]));
-  // pass 2: probabilities, chunk sums, P.V, merged in chunk order
-  float O[NCT][2][4], L[NCT][4];
-#pragma unroll
-  for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      L[ct][r] = 0.0f;
-      O[ct][0][r] = O[ct][1][r] = 0.0f;
+    for (int s = 0; s < 32; ++s) {
+      const float v = row < S ? qr[4 * s] : 0.0f;
+      qb[s] = KVH ? f16_round(v) : v;
     }
-  const int sp_pos = (lane & 3) * 16 + (lane >> 2);
-  pf_load_k<KVH>(rk, 0, kr);
-  pf_load_v<KVH>(rv, 0, vr);
-  for (int c = 0; c < nch; ++c) {
-    float w[NCT][4];
-    pf_scores<NCT>(s_q, kr, c * kChunk, kvlen, past0, r0, nq, scale, w);
-    if (c + 1 < nch) pf_load_k<KVH>(rk, (c + 1) * kChunk, kr);
-    __syncthreads();  // the previous chunk's probabilities are consumed
+  }
+  const int pos = past0 + row;  // this row's last key
+  auto scores = [&](const float* sk, int key0, float (&w)[4][4]) {
+    v4f acc[4];
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct)
+    for (int t = 0; t < 4; ++t) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r)  // key 16 wave + 4 kk + r sits at r * 16 + 4 wave + kk
-        s_p[(ct * 16 + kl) * kPfPStride + r * 16 + 4 * wave + kk] = w[ct][r];
-    __syncthreads();
-    // chunk softmax per column (one wave per column, lane = key)
-    for (int col = wave; col < NC; col += 4) {
-      const float wv = s_p[col * kPfPStride + sp_pos];
-      const float m = wave_max_f(wv);
-      float p = (m == -INFINITY || wv == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(wv, m));
-      if (f16kv) p = f16_round(p);
-      const float l = wave_sum_f(p);
-      s_p[col * kPfPStride + sp_pos] = p;
-      if (lane == 0) {
-        s_l[col] = l;
-        s_f[col] = m == -INFINITY ? 0.0f : dev_expf(__fsub_rn(m, s_M[col]));
-      }
+    for (int x = 0; x < 8; ++x) {
+      v4f a[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) a[t] = *(const v4f*)(sk + (16 * t + j) * kPaKs + g * 32 + 4 * x);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][e], qb[4 * x + e], acc[t], 0, 0, 0);
     }
-    __syncthreads();
-    // O_c[col][d]: fma chain over the chunk's keys; wave w takes head_dim tiles 2w, 2w+1
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
-      float pa[16];
-      const float* prow = s_p + (ct * 16 + kl) * kPfPStride + kk * 16;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const v4f p4 = *(const v4f*)(prow + 4 * i);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) pa[4 * i + jj] = p4[jj];
-      }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s2 = 0; s2 < 16; ++s2) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s2], vr[h][s2], acc, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) O[ct][h][r] = fmaf(acc[r], s_f[ct * 16 + 4 * kk + r], O[ct][h][r]);
-      }
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int col = ct * 16 + 4 * kk + r;
-        L[ct][r] = fmaf(s_l[col], s_f[col], L[ct][r]);
+        const int key = key0 + 16 * t + 4 * r + g;
+        w[t][r] = (row < S && key <= pos) ? __fmul_rn(acc[t][r], scale) : -INFINITY;
       }
+  };
+  PaRegs<KVH> R;
+  // pass 1: row maxima over all chunks; K double-buffered in the two regions
+  pa_load_k<KVH>(kh, 0, kvlen, R);
+  pa_store_k<KVH>(reg0, 0, kvlen, R);
+  __syncthreads();
+  float M = -INFINITY;
+  for (int c = 0; c < nch; ++c) {
+    const bool last = c + 1 == nch;
+    pa_load_k<KVH>(kh, last ? 0 : 64 * (c + 1), kvlen, R);  // pass 2 starts again at chunk 0
+    if (64 * c <= wlast) {
+      float w[4][4];
+      scores((c & 1) ? reg1 : reg0, 64 * c, w);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) M = fmaxf(M, w[t][r]);
     }
-    if (c + 1 < nch) pf_load_v<KVH>(rv, (c + 1) * kChunk, vr);
+    pa_store_k<KVH>(((c + 1) & 1) ? reg1 : reg0, last ? 0 : 64 * (c + 1), kvlen, R);
+    __syncthreads();
   }
-  // out = O / L, then the q8_0 blocks of 32 head_dim elements (wave w: block w)
-  const int QN = n_heads * kHeadDim;
+  M = pair_max_f<32>(M);
+  M = pair_max_f<16>(M);
+  // pass 2: K of chunk 0 sits in region nch & 1; V^T goes to the other region
+  float* sk = (nch & 1) ? reg1 : reg0;
+  float* sv = (nch & 1) ? reg0 : reg1;
+  pa_load_v<KVH>(vh, 0, kvlen, R);
+  pa_store_v<KVH>(sv, 0, kvlen, R);
+  __syncthreads();
+  float L = 0.0f;
+  v4f O[8];
 #pragma unroll
-  for (int ct = 0; ct < NCT; ++ct)
+  for (int dt = 0; dt < 8; ++dt) O[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = 0; c < nch; ++c) {
+    const bool more = c + 1 < nch, live = 64 * c <= wlast;
+    if (more) pa_load_k<KVH>(kh, 64 * (c + 1), kvlen, R);
+    float p[4][4];
+    float mc = -INFINITY, lc = 0.0f;
+    if (live) {
+      float w[4][4];
+      scores(sk, 64 * c, w);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * (ct % kPfRowTiles) + 4 * kk + r;  // query row of column 16 ct + 4 kk + r
-      const float o0 = __fdiv_rn(O[ct][0][r], L[ct][r]);
-      const float o1 = __fdiv_rn(O[ct][1][r], L[ct][r]);
-      if constexpr (OUTF) {
-        if (t < nq) {
-          float* orow = ofl + (size_t)(r0 + t) * QN + (hq0 + ct / kPfRowTiles) * kHeadDim + 32 * wave + kl;
-          orow[0] = o0;
-          orow[16] = o1;
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mc = fmaxf(mc, w[t][r]);
+      mc = pair_max_f<32>(mc);
+      mc = pair_max_f<16>(mc);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float pv = (mc == -INFINITY || w[t][r] == -INFINITY) ? 0.0f : dev_expf(__fsub_rn(w[t][r], mc));
+          p[t][r] = KVH ? f16_round(pv) : pv;
         }
-        continue;
+      float u[2][4], x4[4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) u[t][r] = __fadd_rn(p[t][r], p[t + 2][r]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x4[r] = __fadd_rn(u[0][r], u[1][r]);
+      lc = pair_add_f<32>(__fadd_rn(__fadd_rn(x4[0], x4[2]), __fadd_rn(x4[1], x4[3])));
+      lc = pair_add_f<16>(lc);
+    }
+    __syncthreads();  // K of chunk c is consumed
+    if (more) {
+      pa_store_k<KVH>(sk, 64 * (c + 1), kvlen, R);
+      pa_load_v<KVH>(vh, 64 * (c + 1), kvlen, R);
+    }
+    if (live) {
+      v4f oc[8];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) oc[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        v4f av[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) av[dt] = *(const v4f*)(sv + (16 * dt + j) * kPaVs + g * 16 + 4 * x);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt)
+            oc[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[dt][e], p[x][e], oc[dt], 0, 0, 0);
       }
-      float amax = fmaxf(fabsf(o0), fabsf(o1));
-      uint32_t u = __float_as_uint(amax);  // max over the 16 lanes kl of this row
-      u = max(u, dpp_u<kDppRor8>(u));
-      u = max(u, dpp_u<kDppRor4>(u));
-      u = max(u, dpp_u<kDppRor2>(u));
-      u = max(u, dpp_u<kDppRor1>(u));
-      amax = __uint_as_float(u);
-      if (t < nq) {
-        const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
-        const size_t rowoff = (size_t)(r0 + t) * QN + (hq0 + ct / kPfRowTiles) * kHeadDim;
-        ocodes[rowoff + 32 * wave + kl] = (int8_t)rintf(__fmul_rn(o0, id));
-        ocodes[rowoff + 32 * wave + 16 + kl] = (int8_t)rintf(__fmul_rn(o1, id));
-        if (kl == 0)
-          oscales[(size_t)(r0 + t) * (QN / 32) + ((hq0 + ct / kPfRowTiles) * kHeadDim) / 32 + wave] =
+      const float f = mc == -INFINITY ? 0.0f : dev_expf(__fsub_rn(mc, M));
+      L = fmaf(lc, f, L);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) O[dt][r] = fmaf(oc[dt][r], f, O[dt][r]);
+    }
+    __syncthreads();  // V^T of chunk c is consumed, K of chunk c + 1 is staged
+    if (more) pa_store_v<KVH>(sv, 64 * (c + 1), kvlen, R);
+  }
+  // O[dt][r]: element 16 dt + 4 g + r of row `row`
+  const int QN = n_heads * kHeadDim;
+  float o[8][4];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[dt][r] = __fdiv_rn(O[dt][r], L);
+  if constexpr (OUTF) {
+    if (row < S) {
+      float* orow = ofl + (size_t)row * QN + hq * kHeadDim + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) *(v4f*)(orow + 16 * dt) = v4f{o[dt][0], o[dt][1], o[dt][2], o[dt][3]};
+    }
+  } else {
+    // q8_0 block b = elements 32 b .. 32 b + 31 = tiles 2 b, 2 b + 1 over the four lane groups
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      uint32_t u = 0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) u = max(u, __float_as_uint(fabsf(o[2 * b + h][r])));
+      u = pair_max_u<32>(u);
+      u = pair_max_u<16>(u);
+      const float amax = __uint_as_float(u);
+      const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+      if (row < S) {
+        const size_t rowoff = (size_t)row * QN + hq * kHeadDim;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            word |= (uint32_t)(uint8_t)(int8_t)rintf(__fmul_rn(o[2 * b + h][r], id)) << (8 * r);
+          *(uint32_t*)(ocodes + rowoff + 16 * (2 * b + h) + 4 * g) = word;
+        }
+        if (g == 0)
+          oscales[(size_t)row * (QN / 32) + (hq * kHeadDim) / 32 + b] =
               __half2float(__float2half_rn(__fdiv_rn(amax, 127.0f)));
       }
     }
+  }
 }
 
 }  // namespace
@@ -648,8 +705,8 @@ void launch_pf_qk_rope(hipStream_t s, const float* qkv, int S, int past0, int n_
 void launch_pf_attn(hipStream_t s, const float* q, int n_heads, int n_kv_heads, KvLayer kv, int past0, int S,
                     int8_t* ocodes, float* oscales, float* ofl) {
   const dim3 grid((unsigned)(n_heads / kPfHeads), (unsigned)((S + kPfRows - 1) / kPfRows));
-#define MTG_PF_ATTN(KVH, OUTF)                                                                                 \
-  hipLaunchKernelGGL((k_pf_attn<KVH, OUTF>), grid, dim3(256), kPfAttnLds, s, q, n_heads, n_kv_heads, kv, past0, S, \
+#define MTG_PF_ATTN(KVH, OUTF)                                                                                \
+  hipLaunchKernelGGL((k_pf_attn_mma<KVH, OUTF>), grid, dim3(256), kPaLds, s, q, n_heads, n_kv_heads, kv, past0, S, \
                      ocodes, oscales, ofl)
   if (ofl) {
     if (kv.f16) MTG_PF_ATTN(1, true);
@@ -662,10 +719,10 @@ void launch_pf_attn(hipStream_t s, const float* q, int n_heads, int n_kv_heads, 
 }
 
 hipError_t prepare_kernels_pf() {
-  const void* fns[] = {(const void*)k_pf_attn<0, false>, (const void*)k_pf_attn<1, false>,
-                       (const void*)k_pf_attn<0, true>, (const void*)k_pf_attn<1, true>};
+  const void* fns[] = {(const void*)k_pf_attn_mma<0, false>, (const void*)k_pf_attn_mma<1, false>,
+                       (const void*)k_pf_attn_mma<0, true>, (const void*)k_pf_attn_mma<1, true>};
   for (const void* f : fns) {
-    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfAttnLds);
+    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPaLds);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
