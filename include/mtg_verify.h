@@ -420,7 +420,7 @@ typedef struct mtg_encoder_layer {
 
 typedef struct mtg_encoder_desc {
   mtg_encoder_hparams hp;
-  int32_t weight_type;                  /* MTG_TYPE_Q8_0 */
+  int32_t weight_type;                  /* of every matrix: MTG_TYPE_Q8_0, _F16 or _Q4_K */
   const float *conv1_w, *conv1_b;       /* enc.conv1.{w,b}: [d][n_mels][3], [d] */
   const float *conv2_w, *conv2_b;       /* enc.conv2.{w,b}: [d][d][3], [d] (stride 2) */
   const float* pos_embd;                /* enc.pos_embd [rows][d] */
@@ -434,8 +434,11 @@ typedef struct mtg_encoder_desc {
 } mtg_encoder_desc;
 
 typedef struct mtg_encoder mtg_encoder;
-/* Upload an encoder + adaptor. q8_0 weights, head_dim 64, d_model and ffn
- * multiples of 64, hidden a multiple of 64 (else MTG_ERR_UNSUPPORTED). */
+/* Upload an encoder + adaptor. Weights q8_0 (the converter's q8_0 dtype), f16
+ * (its f16 dtype) or q4_K (`cli quantize q4_k`, src/cli.cpp:106-130) in the GGUF
+ * block layout; head_dim 64, d_model and hidden 1,024, ffn a multiple of 64
+ * (f16: the K of every matrix 1,024, 2,048, 3,072 or 4,096; q4_K: multiples of
+ * 256), else MTG_ERR_UNSUPPORTED. */
 int mtg_encoder_create(const mtg_encoder_desc* desc, mtg_encoder** out);
 void mtg_encoder_destroy(mtg_encoder* e);
 const char* mtg_encoder_error(const mtg_encoder* e);

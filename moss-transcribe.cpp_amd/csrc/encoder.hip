@@ -452,6 +452,11 @@ struct mtg_encoder {
         *f = nullptr, *out_rows = nullptr, *in_rows = nullptr, *h1 = nullptr, *h2 = nullptr, *ad_out = nullptr;
   int8_t* codes = nullptr;
   float* scales = nullptr;
+  // f16 / q4_K matrices (GGUF row layout): the GEMMs' activation (f16 values or
+  // q8_K blocks) and the LayerNorm rows it is made from
+  int wtype = MTG_TYPE_Q8_0;
+  WtAct act{};
+  float* xn = nullptr;
 
   ~mtg_encoder() {
     for (void* p : allocs) (void)hipFree(p);
@@ -509,11 +514,40 @@ struct mtg_encoder {
     rc = check(hipStreamSynchronize(stream), "retile");
     return d;
   }
-  void quant(const float* src, int S, int K) { launch_pf_quant(stream, src, S, K, codes, scales); }
-  void gemm(int epi, const uint8_t* w, int N, int K, int S, float* out, const float* bias) {
-    launch_pf_gemm(stream, epi, w, nullptr, N, K, codes, scales, S, out, bias);
+  // an n x kk matrix: q8_0 re-tiled for the int8 MFMA GEMM, f16 / q4_K as they are
+  uint8_t* up_w(const void* src, int n, int kk, uint8_t* staging, int& rc) {
+    if (wtype == MTG_TYPE_Q8_0) return up_q8(src, n, kk, staging, rc);
+    if (rc) return nullptr;
+    if (!src) {
+      rc = fail(MTG_ERR_INVALID, "a tensor pointer is NULL");
+      return nullptr;
+    }
+    const size_t bytes = (size_t)n * (wtype == MTG_TYPE_F16 ? (size_t)kk * 2 : (size_t)(kk / 256) * 144);
+    uint8_t* d = (uint8_t*)dalloc(bytes);
+    if (!d) {
+      rc = fail(MTG_ERR_NOMEM, "device memory");
+      return nullptr;
+    }
+    rc = check(hipMemcpy(d, src, bytes, hipMemcpyHostToDevice), "upload");
+    return d;
   }
+  // src rows as the next GEMM's activation
+  void quant(const float* src, int S, int K) {
+    if (wtype == MTG_TYPE_Q8_0) launch_pf_quant(stream, src, S, K, codes, scales);
+    else launch_pf_act_wt(stream, wtype, src, S, K, nullptr, 0.0f, act);
+  }
+  void gemm(int epi, const uint8_t* w, int N, int K, int S, float* out, const float* bias) {
+    if (wtype == MTG_TYPE_Q8_0) launch_pf_gemm(stream, epi, w, nullptr, N, K, codes, scales, S, out, bias);
+    else launch_pf_gemm_wt(stream, wtype, epi, w, nullptr, N, K, act, S, out, bias);
+  }
+  // LayerNorm of S rows of d_model: as the next GEMM's activation (q8), or as f32
+  // rows in yout
   void ln(const float* src, int S, const float* w, const float* b, float eps, bool q8, float* yout) {
+    if (q8 && wtype != MTG_TYPE_Q8_0) {
+      hipLaunchKernelGGL(k_enc_ln, dim3((S + 3) / 4), dim3(256), 0, stream, src, S, w, b, eps, nullptr, nullptr, xn);
+      quant(xn, S, hp.d_model);
+      return;
+    }
     hipLaunchKernelGGL(k_enc_ln, dim3((S + 3) / 4), dim3(256), 0, stream, src, S, w, b, eps, q8 ? codes : nullptr,
                        q8 ? scales : nullptr, yout);
   }
@@ -525,7 +559,12 @@ int mtg_encoder_create(const mtg_encoder_desc* d, mtg_encoder** out) {
   if (!d || !out) return MTG_ERR_INVALID;
   *out = nullptr;
   const mtg_encoder_hparams& hp = d->hp;
-  if (d->weight_type != MTG_TYPE_Q8_0 || hp.d_model != 1024 || hp.hidden != 1024 || hp.n_heads <= 0 ||
+  const int wt = d->weight_type;
+  const bool wt_ok = wt == MTG_TYPE_Q8_0 ||
+                     ((wt == MTG_TYPE_F16 || wt == MTG_TYPE_Q4_K) && pf_gemm_wt_supported(wt, hp.d_model) &&
+                      pf_gemm_wt_supported(wt, hp.ffn) && pf_gemm_wt_supported(wt, hp.hidden) &&
+                      pf_gemm_wt_supported(wt, hp.d_model * hp.merge));
+  if (!wt_ok || hp.d_model != 1024 || hp.hidden != 1024 || hp.n_heads <= 0 ||
       hp.d_model / hp.n_heads != kEncHd || hp.d_model % hp.n_heads || hp.ffn % 64 || hp.n_mels % kConvIcb ||
       hp.n_mels <= 0 || hp.merge <= 0 || hp.n_layers < 0 || hp.n_frames < 2 ||
       (hp.n_frames - 1) / 2 + 1 > 64 * kEncMaxChunks)
@@ -534,6 +573,7 @@ int mtg_encoder_create(const mtg_encoder_desc* d, mtg_encoder** out) {
   mtg_encoder* e = new (std::nothrow) mtg_encoder();
   if (!e) return MTG_ERR_NOMEM;
   e->hp = hp;
+  e->wtype = wt;
   const int D = hp.d_model, F = hp.ffn, M = hp.n_mels, NF = hp.n_frames, R = (NF - 1) / 2 + 1, H = hp.hidden,
             IN = D * hp.merge;
   e->rows = R;
@@ -560,24 +600,24 @@ int mtg_encoder_create(const mtg_encoder_desc* d, mtg_encoder** out) {
     mtg_encoder::Layer L{};
     L.attn_ln_w = e->up_f(s.attn_ln_w, D, rc);
     L.attn_ln_b = e->up_f(s.attn_ln_b, D, rc);
-    L.q_w = e->up_q8(s.q_w, D, D, staging, rc);
-    L.k_w = e->up_q8(s.k_w, D, D, staging, rc);
-    L.v_w = e->up_q8(s.v_w, D, D, staging, rc);
-    L.o_w = e->up_q8(s.o_w, D, D, staging, rc);
+    L.q_w = e->up_w(s.q_w, D, D, staging, rc);
+    L.k_w = e->up_w(s.k_w, D, D, staging, rc);
+    L.v_w = e->up_w(s.v_w, D, D, staging, rc);
+    L.o_w = e->up_w(s.o_w, D, D, staging, rc);
     L.q_b = e->up_f(s.q_b, D, rc);
     L.v_b = e->up_f(s.v_b, D, rc);
     L.o_b = e->up_f(s.o_b, D, rc);
     L.ffn_ln_w = e->up_f(s.ffn_ln_w, D, rc);
     L.ffn_ln_b = e->up_f(s.ffn_ln_b, D, rc);
-    L.fc1_w = e->up_q8(s.fc1_w, F, D, staging, rc);
+    L.fc1_w = e->up_w(s.fc1_w, F, D, staging, rc);
     L.fc1_b = e->up_f(s.fc1_b, F, rc);
-    L.fc2_w = e->up_q8(s.fc2_w, D, F, staging, rc);
+    L.fc2_w = e->up_w(s.fc2_w, D, F, staging, rc);
     L.fc2_b = e->up_f(s.fc2_b, D, rc);
     e->layers.push_back(L);
   }
-  e->ad_fc1_w = e->up_q8(d->ad_fc1_w, H, IN, staging, rc);
+  e->ad_fc1_w = e->up_w(d->ad_fc1_w, H, IN, staging, rc);
   e->ad_fc1_b = e->up_f(d->ad_fc1_b, H, rc);
-  e->ad_fc2_w = e->up_q8(d->ad_fc2_w, H, H, staging, rc);
+  e->ad_fc2_w = e->up_w(d->ad_fc2_w, H, H, staging, rc);
   e->ad_fc2_b = e->up_f(d->ad_fc2_b, H, rc);
   e->ad_ln_w = e->up_f(d->ad_ln_w, H, rc);
   e->ad_ln_b = e->up_f(d->ad_ln_b, H, rc);
@@ -600,6 +640,19 @@ int mtg_encoder_create(const mtg_encoder_desc* d, mtg_encoder** out) {
     const size_t KC = std::max((size_t)R * std::max(F, D), (size_t)N * IN);
     e->codes = (int8_t*)e->dalloc(KC);
     e->scales = (float*)e->dalloc(KC / 32 * 4);
+    if (wt == MTG_TYPE_F16) {
+      e->act.f16h = (uint16_t*)e->dalloc(KC * 2);
+      if (!e->act.f16h) rc = e->fail(MTG_ERR_NOMEM, "device memory");
+    } else if (wt == MTG_TYPE_Q4_K) {
+      e->act.q8k.qs = (int8_t*)e->dalloc(KC);
+      e->act.q8k.d = (float*)e->dalloc(KC / 256 * 4);
+      e->act.q8k.bsums = (int32_t*)e->dalloc(KC / 16 * 4);
+      if (!e->act.q8k.qs || !e->act.q8k.d || !e->act.q8k.bsums) rc = e->fail(MTG_ERR_NOMEM, "device memory");
+    }
+    if (wt != MTG_TYPE_Q8_0) {
+      e->xn = (float*)e->dalloc(RD * 4);
+      if (!e->xn) rc = e->fail(MTG_ERR_NOMEM, "device memory");
+    }
     if (!e->mel || !e->c1 || !e->x || !e->q || !e->k || !e->v || !e->a || !e->f || !e->out_rows || !e->in_rows ||
         !e->h1 || !e->h2 || !e->ad_out || !e->codes || !e->scales)
       rc = e->fail(MTG_ERR_NOMEM, "device memory");

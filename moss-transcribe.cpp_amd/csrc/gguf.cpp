@@ -460,20 +460,22 @@ const mtg_encoder_desc* mtg_gguf_encoder(mtg_gguf* g) {
       *t = &it->second;
       return true;
     };
-    uint32_t wtype = MTG_TYPE_Q8_0;
-    if (hp.n_layers > 0) {
-      if (!find("enc.blk.0.attn_q.w", &q0)) return nullptr;
-      wtype = q0->type;
-    }
-    if (wtype != MTG_TYPE_Q8_0) {
-      g->fail(MTG_ERR_UNSUPPORTED, std::string("encoder weight type ") + type_name(wtype) + " is not supported: q8_0");
+    // the matrices' type: the converter writes q8_0 or f16 (--dtype), and
+    // `cli quantize q4_k` turns the encoder and adaptor matrices into q4_K
+    // (src/cli.cpp:106-130); all of them share it
+    if (!find(hp.n_layers > 0 ? "enc.blk.0.attn_q.w" : "adaptor.fc1.w", &q0)) return nullptr;
+    const uint32_t wtype = q0->type;
+    if (wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16 && wtype != MTG_TYPE_Q4_K) {
+      g->fail(MTG_ERR_UNSUPPORTED,
+              std::string("encoder weight type ") + type_name(wtype) + " is not supported: q8_0, f16 or q4_K");
       return nullptr;
     }
     auto matrix = [&](const std::string& name, int64_t k, int64_t n, const void** out) -> bool {
       const TensorInfo* t = nullptr;
       if (!find(name, &t)) return false;
       if (t->type != wtype) {
-        g->fail(MTG_ERR_UNSUPPORTED, name + " is " + type_name(t->type) + ": the encoder matrices must be q8_0");
+        g->fail(MTG_ERR_UNSUPPORTED, name + " is " + type_name(t->type) + ": the encoder matrices must all be " +
+                                         type_name(wtype));
         return false;
       }
       if (t->n_dims != 2 || (int64_t)t->ne[0] != k || (int64_t)t->ne[1] != n) {

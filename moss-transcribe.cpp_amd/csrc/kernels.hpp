@@ -114,9 +114,12 @@ void launch_pf_attn(hipStream_t s, const float* q, int n_heads, int n_kv_heads, 
 // src as is), S rows of K
 void launch_pf_act_wt(hipStream_t s, int wtype, const float* src, int S, int K, const float* gain, float eps,
                       const WtAct& act);
-// out[s][n] (= / += / swiglu with w2) for f16 or q4_K weights in the GGUF row layout
+// out[s][n] (= / += / swiglu with w2, or the encoder's bias epilogues PF_EPI_BIAS*)
+// for f16 or q4_K weights in the GGUF row layout
 void launch_pf_gemm_wt(hipStream_t s, int wtype, int epi, const uint8_t* w, const uint8_t* w2, int N, int K,
-                       const WtAct& act, int S, float* out);
+                       const WtAct& act, int S, float* out, const float* bias = nullptr);
+// the K this GEMM takes: f16 1,024 / 2,048 / 3,072 / 4,096; q4_K any multiple of 256
+int pf_gemm_wt_supported(int wtype, int K);
 
 // ---- f16 / q4_K weights (kernels_wt.hip); weights in the GGUF row layout ----
 bool wt_shape_supported(int wtype, int k);

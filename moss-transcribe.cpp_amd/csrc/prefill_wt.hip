@@ -50,19 +50,33 @@ k_pf_act_wt(const float* __restrict__ src, int S, int K, const float* __restrict
 
 // The rows of the output tile that this lane holds (the MFMA result layout:
 // lane (n, g) = (lane % 16, lane / 16) holds weight rows 4 g + r, r < 4, of the
-// wave's 16, for activation row n of the column tile), after the epilogue.
+// wave's 16, for activation row n of the column tile), after the epilogue
+// (epi: store, residual add, or the encoder's linear = mul_mat + bias, then GELU,
+// SiLU or the residual add; the SwiGLU is applied before this).
 // n0: the first of the 4 weight rows in the output's row space.
-template <int EPI>
-__device__ __forceinline__ void pf_store4(float* out, int N, int t, int n0, const float (&v)[4]) {
+__device__ __forceinline__ void pf_store4(int epi, float* out, int N, int t, int n0, const float (&v)[4],
+                                          const float* bias) {
   float* dst = out + (size_t)t * N + n0;
+  float y[4] = {v[0], v[1], v[2], v[3]};
+  if (epi >= PF_EPI_BIAS) {
+    const v4f b = *(const v4f*)(bias + n0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) y[q] = __fadd_rn(y[q], b[q]);
+    if (epi == PF_EPI_BIAS_GELU) {
+      dev_gelu_erf_n<4>(y);
+    } else if (epi == PF_EPI_BIAS_SILU) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) y[q] = dev_silu(y[q]);
+    }
+  }
   v4f o;
-  if (EPI == PF_EPI_RESID) {
+  if (epi == PF_EPI_RESID || epi == PF_EPI_BIAS_RESID) {
     const v4f x = *(const v4f*)dst;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) o[q] = __fadd_rn(x[q], v[q]);
+    for (int q = 0; q < 4; ++q) o[q] = __fadd_rn(x[q], y[q]);
   } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) o[q] = v[q];
+    for (int q = 0; q < 4; ++q) o[q] = y[q];
   }
   *(v4f*)dst = o;
 }
@@ -85,13 +99,12 @@ __device__ __forceinline__ void pf_store4(float* out, int N, int t, int n0, cons
 // segment's rows already in flight in registers.
 __device__ __forceinline__ int bitrev6(int k) { return (int)(__builtin_bitreverse32((uint32_t)k) >> 26); }
 
-template <int EPI, int L>
+template <bool GLU, int L>
 __global__ void __launch_bounds__(256)
 k_pf_gemm_f16(const uint16_t* __restrict__ w, const uint16_t* __restrict__ w2, int N,
-              const uint16_t* __restrict__ x, int S, float* __restrict__ out) {
+              const uint16_t* __restrict__ x, int S, float* __restrict__ out, int epi, const float* __restrict__ bias) {
   constexpr int K = 64 * L, LS = L + 4, NP = L / 8;  // 16-byte pieces (8 halves) per row and segment
   constexpr int NPIECE = 2 * 64 * NP, PPT = (NPIECE + 255) / 256;
-  constexpr bool GLU = EPI == PF_EPI_SWIGLU;
   __shared__ __align__(16) float s_w[2][64 * LS];
   __shared__ __align__(16) float s_x[2][64 * LS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, kk = lane >> 4;
@@ -202,7 +215,7 @@ k_pf_gemm_f16(const uint16_t* __restrict__ w, const uint16_t* __restrict__ w2, i
       float v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) v[q] = dev_swiglu(res[ct][q], u[q]);
-      pf_store4<PF_EPI_STORE>(out, N, t, 32 * blockIdx.x + 16 * (wave & 1) + 4 * g, v);
+      pf_store4(PF_EPI_STORE, out, N, t, 32 * blockIdx.x + 16 * (wave & 1) + 4 * g, v, nullptr);
     }
   } else {
 #pragma unroll
@@ -210,7 +223,7 @@ k_pf_gemm_f16(const uint16_t* __restrict__ w, const uint16_t* __restrict__ w2, i
       const int t = s0 + 16 * ct + n;
       if (t >= S) continue;
       const float v[4] = {res[ct][0], res[ct][1], res[ct][2], res[ct][3]};
-      pf_store4<EPI>(out, N, t, 64 * blockIdx.x + 16 * wave + 4 * g, v);
+      pf_store4(epi, out, N, t, 64 * blockIdx.x + 16 * wave + 4 * g, v, bias);
     }
   }
 }
@@ -228,11 +241,10 @@ k_pf_gemm_f16(const uint16_t* __restrict__ w, const uint16_t* __restrict__ w2, i
 // (dmin_w d_x) mins.
 constexpr int kQ4RowStride = 288;
 
-template <int EPI>
+template <bool GLU>
 __global__ void __launch_bounds__(256)
 k_pf_gemm_q4k(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int N, int K, ActQ8K a, int S,
-              float* __restrict__ out) {
-  constexpr bool GLU = EPI == PF_EPI_SWIGLU;
+              float* __restrict__ out, int epi, const float* __restrict__ bias) {
   __shared__ __align__(16) int8_t s_q[2][64 * kQ4RowStride];
   __shared__ float s_dx[2][64];
   __shared__ float s_dw[4][16 * 2];  // per wave: d, dmin of its 16 weight rows
@@ -345,14 +357,14 @@ k_pf_gemm_q4k(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int
       float v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) v[q] = dev_swiglu(res[ct][q], u[q]);
-      pf_store4<PF_EPI_STORE>(out, N, t, 32 * blockIdx.x + 16 * (wave & 1) + 4 * g, v);
+      pf_store4(PF_EPI_STORE, out, N, t, 32 * blockIdx.x + 16 * (wave & 1) + 4 * g, v, nullptr);
     }
   } else {
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       const int t = s0 + 16 * ct + row;
       if (t >= S) continue;
-      pf_store4<EPI>(out, N, t, 64 * blockIdx.x + 16 * wave + 4 * g, res[ct]);
+      pf_store4(epi, out, N, t, 64 * blockIdx.x + 16 * wave + 4 * g, res[ct], bias);
     }
   }
 }
@@ -370,31 +382,36 @@ void launch_pf_act_wt(hipStream_t s, int wtype, const float* src, int S, int K, 
 }
 
 void launch_pf_gemm_wt(hipStream_t s, int wtype, int epi, const uint8_t* w, const uint8_t* w2, int N, int K,
-                       const WtAct& act, int S, float* out) {
-  const dim3 grid((unsigned)(epi == PF_EPI_SWIGLU ? N / 32 : N / 64), (unsigned)((S + 63) / 64));
+                       const WtAct& act, int S, float* out, const float* bias) {
+  const bool glu = epi == PF_EPI_SWIGLU;
+  const dim3 grid((unsigned)(glu ? N / 32 : N / 64), (unsigned)((S + 63) / 64));
   if (wtype == MTG_TYPE_Q4_K) {
-#define MTG_PF_Q4(E) hipLaunchKernelGGL(k_pf_gemm_q4k<E>, grid, dim3(256), 0, s, w, w2, N, K, act.q8k, S, out)
-    if (epi == PF_EPI_STORE) MTG_PF_Q4(PF_EPI_STORE);
-    else if (epi == PF_EPI_RESID) MTG_PF_Q4(PF_EPI_RESID);
-    else MTG_PF_Q4(PF_EPI_SWIGLU);
-#undef MTG_PF_Q4
+    if (glu)
+      hipLaunchKernelGGL(k_pf_gemm_q4k<true>, grid, dim3(256), 0, s, w, w2, N, K, act.q8k, S, out, epi, bias);
+    else
+      hipLaunchKernelGGL(k_pf_gemm_q4k<false>, grid, dim3(256), 0, s, w, w2, N, K, act.q8k, S, out, epi, bias);
     return;
   }
   const uint16_t* wh = (const uint16_t*)w;
   const uint16_t* w2h = (const uint16_t*)w2;
-#define MTG_PF_F16(E, L) \
-  hipLaunchKernelGGL((k_pf_gemm_f16<E, L>), grid, dim3(256), 0, s, wh, w2h, N, act.f16h, S, out)
-#define MTG_PF_F16_K(E)                        \
+#define MTG_PF_F16(G, L) \
+  hipLaunchKernelGGL((k_pf_gemm_f16<G, L>), grid, dim3(256), 0, s, wh, w2h, N, act.f16h, S, out, epi, bias)
+#define MTG_PF_F16_K(G)                        \
   switch (K) {                                 \
-    case 1024: MTG_PF_F16(E, 16); break;       \
-    case 2048: MTG_PF_F16(E, 32); break;       \
-    default: MTG_PF_F16(E, 48); break;         \
+    case 1024: MTG_PF_F16(G, 16); break;       \
+    case 2048: MTG_PF_F16(G, 32); break;       \
+    case 3072: MTG_PF_F16(G, 48); break;       \
+    default: MTG_PF_F16(G, 64); break;         \
   }
-  if (epi == PF_EPI_STORE) { MTG_PF_F16_K(PF_EPI_STORE); }
-  else if (epi == PF_EPI_RESID) { MTG_PF_F16_K(PF_EPI_RESID); }
-  else { MTG_PF_F16_K(PF_EPI_SWIGLU); }
+  if (glu) { MTG_PF_F16_K(true); }
+  else { MTG_PF_F16_K(false); }
 #undef MTG_PF_F16_K
 #undef MTG_PF_F16
+}
+
+int pf_gemm_wt_supported(int wtype, int K) {
+  if (wtype == MTG_TYPE_Q4_K) return K % 256 == 0;
+  return K == 1024 || K == 2048 || K == 3072 || K == 4096;
 }
 
 }  // namespace mtg

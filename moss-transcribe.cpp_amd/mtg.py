@@ -601,23 +601,25 @@ def normal(seed, first, n):
 
 class SynthEncoder:
     """Seeded synthetic Whisper encoder + adaptor in host memory: f32 conv stem,
-    positional embedding, norms and biases; q8_0 projection / FFN / adaptor
-    matrices (the reference converter's types), from the shared normal stream."""
+    positional embedding, norms and biases; q8_0 (the converter's q8_0 dtype), f16
+    (its f16 dtype) or q4_K (`cli quantize q4_k`) projection / FFN / adaptor
+    matrices, from the shared normal stream."""
 
-    def __init__(self, seed=0, std=0.02, **hp):
+    def __init__(self, seed=0, std=0.02, wtype=TYPE_Q8_0, **hp):
         d = dict(ENCODER_DEFAULTS)
         d.update(hp)
         self.hp = EncoderHparams(**d)
         self._keep = []
         self._next = 0
         self.seed = seed
+        self.wtype = wtype
         h = self.hp
         D, F, M, H, IN = h.d_model, h.ffn, h.n_mels, h.hidden, h.d_model * h.merge
         R = (h.n_frames - 1) // 2 + 1
         self.rows = R
         desc = EncoderDesc()
         desc.hp = self.hp
-        desc.weight_type = TYPE_Q8_0
+        desc.weight_type = wtype
         desc.conv1_w = self._f(D * M * 3, std)
         desc.conv1_b = self._f(D, std)
         desc.conv2_w = self._f(D * D * 3, std)
@@ -652,9 +654,16 @@ class SynthEncoder:
         return a.ctypes.data
 
     def _q(self, n, k, std):
-        x = self._normal(n * k) * np.float32(std)
-        blocks = np.empty(n * (k // 32) * 34, np.uint8)
-        lib().mtg_quantize_q8_0_weight(ptr(x), n * k, ptr(blocks))
+        x = (self._normal(n * k) * np.float32(std)).astype(np.float32)
+        if self.wtype == TYPE_F16:
+            blocks = x.astype(np.float16).view(np.uint8)
+        elif self.wtype == TYPE_Q4_K:
+            blocks = np.empty(n * (k // 256) * 144, np.uint8)
+            lib().mtg_quantize_q4_k(ptr(x), n * k, ptr(blocks))
+        else:
+            blocks = np.empty(n * (k // 32) * 34, np.uint8)
+            lib().mtg_quantize_q8_0_weight(ptr(x), n * k, ptr(blocks))
+        blocks = np.ascontiguousarray(blocks)
         self._keep.append(blocks)
         return blocks.ctypes.data
 

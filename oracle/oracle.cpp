@@ -1336,9 +1336,11 @@ void enc_attention(const float* q, const float* k, const float* v, int T, int NH
     }
 }
 
-// linear (src/ggml_extend.hpp:50-55): mul_mat (q8_0) then + bias
-void linear_q8(const std::vector<BlockQ8>& w, const float* bias, int k, int n, const float* x, int T, float* y) {
-  mul_mat_q8(w.data(), k, n, x, T, y);
+// linear (src/ggml_extend.hpp:50-55): mul_mat (q8_0, f16 or q4_K weights, the
+// decoder's canonical orders) then + bias
+void linear_wt(int wtype, const std::vector<uint8_t>& w, const float* bias, int k, int n, const float* x, int T,
+               float* y) {
+  mul_mat(wtype, w.data(), k, n, x, T, y);
   if (bias)
     for (int t = 0; t < T; ++t)
       for (int i = 0; i < n; ++i) y[(size_t)t * n + i] = y[(size_t)t * n + i] + bias[i];
@@ -1346,22 +1348,25 @@ void linear_q8(const std::vector<BlockQ8>& w, const float* bias, int k, int n, c
 
 struct EncLayer {
   std::vector<float> attn_ln_w, attn_ln_b, q_b, v_b, o_b, ffn_ln_w, ffn_ln_b, fc1_b, fc2_b;
-  std::vector<BlockQ8> q_w, k_w, v_w, o_w, fc1_w, fc2_w;
+  std::vector<uint8_t> q_w, k_w, v_w, o_w, fc1_w, fc2_w;
 };
 
 std::vector<float> copy_f(const float* p, size_t n) { return std::vector<float>(p, p + n); }
-std::vector<BlockQ8> copy_q8(const void* p, size_t n, size_t k) {
-  const BlockQ8* b = (const BlockQ8*)p;
-  return std::vector<BlockQ8>(b, b + n * (k / 32));
+// the bytes of an n x k matrix of wtype (ggml block layouts)
+std::vector<uint8_t> copy_w(int wtype, const void* p, size_t n, size_t k) {
+  const size_t row = wtype == MTG_TYPE_F16 ? k * 2 : wtype == MTG_TYPE_Q4_K ? k / 256 * 144 : k / 32 * 34;
+  const uint8_t* b = (const uint8_t*)p;
+  return std::vector<uint8_t>(b, b + n * row);
 }
 
 }  // namespace
 
 struct orc_encoder {
   mtg_encoder_hparams hp;
+  int wtype = MTG_TYPE_Q8_0;
   std::vector<float> conv1_w, conv1_b, conv2_w, conv2_b, pos, ln_post_w, ln_post_b;
   std::vector<EncLayer> layers;
-  std::vector<BlockQ8> ad_fc1_w, ad_fc2_w;
+  std::vector<uint8_t> ad_fc1_w, ad_fc2_w;
   std::vector<float> ad_fc1_b, ad_fc2_b, ad_ln_w, ad_ln_b;
   std::vector<float> last;  // the last encode's rows
   int last_rows = 0;
@@ -1382,11 +1387,14 @@ void orc_enc_attention(const float* q, const float* k, const float* v, int32_t T
 }
 
 int orc_encoder_create(const mtg_encoder_desc* d, orc_encoder** out) {
-  if (!d || !out || d->weight_type != MTG_TYPE_Q8_0) return MTG_ERR_INVALID;
+  if (!d || !out) return MTG_ERR_INVALID;
+  const int wt = d->weight_type;
+  if (wt != MTG_TYPE_Q8_0 && wt != MTG_TYPE_F16 && wt != MTG_TYPE_Q4_K) return MTG_ERR_INVALID;
   const mtg_encoder_hparams& hp = d->hp;
   const size_t D = hp.d_model, F = hp.ffn, M = hp.n_mels, R = (size_t)(hp.n_frames - 1) / 2 + 1;
   auto e = std::make_unique<orc_encoder>();
   e->hp = hp;
+  e->wtype = wt;
   e->conv1_w = copy_f(d->conv1_w, D * M * 3);
   e->conv1_b = copy_f(d->conv1_b, D);
   e->conv2_w = copy_f(d->conv2_w, D * D * 3);
@@ -1399,25 +1407,25 @@ int orc_encoder_create(const mtg_encoder_desc* d, orc_encoder** out) {
     EncLayer L;
     L.attn_ln_w = copy_f(s.attn_ln_w, D);
     L.attn_ln_b = copy_f(s.attn_ln_b, D);
-    L.q_w = copy_q8(s.q_w, D, D);
-    L.k_w = copy_q8(s.k_w, D, D);
-    L.v_w = copy_q8(s.v_w, D, D);
-    L.o_w = copy_q8(s.o_w, D, D);
+    L.q_w = copy_w(wt, s.q_w, D, D);
+    L.k_w = copy_w(wt, s.k_w, D, D);
+    L.v_w = copy_w(wt, s.v_w, D, D);
+    L.o_w = copy_w(wt, s.o_w, D, D);
     L.q_b = copy_f(s.q_b, D);
     L.v_b = copy_f(s.v_b, D);
     L.o_b = copy_f(s.o_b, D);
     L.ffn_ln_w = copy_f(s.ffn_ln_w, D);
     L.ffn_ln_b = copy_f(s.ffn_ln_b, D);
-    L.fc1_w = copy_q8(s.fc1_w, F, D);
+    L.fc1_w = copy_w(wt, s.fc1_w, F, D);
     L.fc1_b = copy_f(s.fc1_b, F);
-    L.fc2_w = copy_q8(s.fc2_w, D, F);
+    L.fc2_w = copy_w(wt, s.fc2_w, D, F);
     L.fc2_b = copy_f(s.fc2_b, D);
     e->layers.push_back(std::move(L));
   }
   const size_t H = hp.hidden, IN = D * hp.merge;
-  e->ad_fc1_w = copy_q8(d->ad_fc1_w, H, IN);
+  e->ad_fc1_w = copy_w(wt, d->ad_fc1_w, H, IN);
   e->ad_fc1_b = copy_f(d->ad_fc1_b, H);
-  e->ad_fc2_w = copy_q8(d->ad_fc2_w, H, H);
+  e->ad_fc2_w = copy_w(wt, d->ad_fc2_w, H, H);
   e->ad_fc2_b = copy_f(d->ad_fc2_b, H);
   e->ad_ln_w = copy_f(d->ad_ln_w, H);
   e->ad_ln_b = copy_f(d->ad_ln_b, H);
@@ -1448,17 +1456,17 @@ int orc_encoder_encode(orc_encoder* e, const float* mel, float* out, int32_t* ro
   for (const EncLayer& L : e->layers) {
     for (int t = 0; t < R; ++t)
       layer_norm(x.data() + (size_t)t * D, L.attn_ln_w.data(), L.attn_ln_b.data(), D, 1e-5f, xn.data() + (size_t)t * D);
-    linear_q8(L.q_w, L.q_b.data(), D, D, xn.data(), R, q.data());
-    linear_q8(L.k_w, nullptr, D, D, xn.data(), R, k.data());
-    linear_q8(L.v_w, L.v_b.data(), D, D, xn.data(), R, v.data());
+    linear_wt(e->wtype, L.q_w, L.q_b.data(), D, D, xn.data(), R, q.data());
+    linear_wt(e->wtype, L.k_w, nullptr, D, D, xn.data(), R, k.data());
+    linear_wt(e->wtype, L.v_w, L.v_b.data(), D, D, xn.data(), R, v.data());
     enc_attention(q.data(), k.data(), v.data(), R, NH, hd, a.data());
-    linear_q8(L.o_w, L.o_b.data(), D, D, a.data(), R, q.data());
+    linear_wt(e->wtype, L.o_w, L.o_b.data(), D, D, a.data(), R, q.data());
     for (size_t i = 0; i < x.size(); ++i) x[i] = x[i] + q[i];
     for (int t = 0; t < R; ++t)
       layer_norm(x.data() + (size_t)t * D, L.ffn_ln_w.data(), L.ffn_ln_b.data(), D, 1e-5f, xn.data() + (size_t)t * D);
-    linear_q8(L.fc1_w, L.fc1_b.data(), D, F, xn.data(), R, f.data());
+    linear_wt(e->wtype, L.fc1_w, L.fc1_b.data(), D, F, xn.data(), R, f.data());
     for (float& y : f) y = gelu_erf(y);
-    linear_q8(L.fc2_w, L.fc2_b.data(), F, D, f.data(), R, q.data());
+    linear_wt(e->wtype, L.fc2_w, L.fc2_b.data(), F, D, f.data(), R, q.data());
     for (size_t i = 0; i < x.size(); ++i) x[i] = x[i] + q[i];
   }
   e->last.assign((size_t)R * D, 0.0f);
@@ -1483,9 +1491,9 @@ int orc_encoder_adapt(orc_encoder* e, const float* rows, int32_t T, float* out, 
   if (N <= 0) return MTG_OK;
   // [D * merge, N]: merge consecutive rows per adaptor row (a plain view)
   std::vector<float> h1((size_t)N * H), h2((size_t)N * H);
-  linear_q8(e->ad_fc1_w, e->ad_fc1_b.data(), IN, H, rows, N, h1.data());
+  linear_wt(e->wtype, e->ad_fc1_w, e->ad_fc1_b.data(), IN, H, rows, N, h1.data());
   for (float& y : h1) y = y / (1.0f + exp_c(-y));  // ggml_silu
-  linear_q8(e->ad_fc2_w, e->ad_fc2_b.data(), H, H, h1.data(), N, h2.data());
+  linear_wt(e->wtype, e->ad_fc2_w, e->ad_fc2_b.data(), H, H, h1.data(), N, h2.data());
   for (int t = 0; t < N; ++t)
     layer_norm(h2.data() + (size_t)t * H, e->ad_ln_w.data(), e->ad_ln_b.data(), H, hp.adaptor_eps,
                out + (size_t)t * H);

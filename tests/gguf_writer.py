@@ -123,13 +123,14 @@ def encoder_tensors(syn):
     h, d = syn.hp, syn.desc
     D, F, M, H, IN = h.d_model, h.ffn, h.n_mels, h.hidden, h.d_model * h.merge
     R = syn.rows
-    rb = lambda k: mtg.lib().mtg_row_bytes(8, k)
+    wt = getattr(syn, "wtype", mtg.TYPE_Q8_0)  # the matrices' type (q8_0, f16 or q4_K)
+    rb = lambda k: mtg.lib().mtg_row_bytes(wt, k)
 
     def f32(p, ne):
         return (0, ne, ctypes.string_at(p, 4 * int(np.prod(ne))))
 
     def q8(p, k, n):
-        return (8, [k, n], ctypes.string_at(p, rb(k) * n))
+        return (wt, [k, n], ctypes.string_at(p, rb(k) * n))
 
     out = [("enc.conv1.w",) + f32(d.conv1_w, [3, M, D]), ("enc.conv1.b",) + f32(d.conv1_b, [D]),
            ("enc.conv2.w",) + f32(d.conv2_w, [3, D, D]), ("enc.conv2.b",) + f32(d.conv2_b, [D]),

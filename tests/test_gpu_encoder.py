@@ -2,8 +2,9 @@
 WhisperEncoder::encode, src/whisper_encoder.cpp:103-209, AudioAdaptor::apply,
 src/audio_adaptor.cpp:38-97) against the oracle: encoder rows and adaptor rows
 bit-identical (the kernels keep the oracle's order of every reduction), at a
-short chunk, at the full 3,000-frame chunk (1,500 rows) with 2 layers, and for
-the whole 24-layer encoder (also timed and checked for determinism)."""
+short chunk and at the full 3,000-frame chunk (1,500 rows) with 2 layers for
+q8_0, f16 and q4_K matrices, and for the whole 24-layer q8_0 encoder (also timed
+and checked for determinism)."""
 import os
 
 import numpy as np
@@ -25,10 +26,15 @@ def _same(got, ref, what):
                          % (what, int((got != ref).sum()), err.max(), np.unravel_index(err.argmax(), err.shape)))
 
 
+WTYPES = [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_Q4_K]
+WT_IDS = ["q8_0", "f16", "q4_K"]
+
+
+@pytest.mark.parametrize("wtype", WTYPES, ids=WT_IDS)
 @pytest.mark.parametrize("n_frames,n_layers", [(160, 2), (333, 1)])
-def test_encoder_and_adaptor_match_oracle(n_frames, n_layers):
-    print("encoder vs oracle: %d frames, %d layers" % (n_frames, n_layers), flush=True)
-    syn = mtg.SynthEncoder(seed=3, n_frames=n_frames, n_layers=n_layers, ffn=2048)
+def test_encoder_and_adaptor_match_oracle(n_frames, n_layers, wtype):
+    print("encoder vs oracle: %d frames, %d layers, weights %d" % (n_frames, n_layers, wtype), flush=True)
+    syn = mtg.SynthEncoder(seed=3, wtype=wtype, n_frames=n_frames, n_layers=n_layers, ffn=2048)
     dev = mtg.Encoder(syn)
     orc = oracle_py.OracleEncoder(syn)
     mel = syn.mel(seed=4)
@@ -43,15 +49,17 @@ def test_encoder_and_adaptor_match_oracle(n_frames, n_layers):
     orc.close()
 
 
-def test_full_chunk_two_layers_matches_oracle():
+@pytest.mark.parametrize("wtype", WTYPES, ids=WT_IDS)
+def test_full_chunk_two_layers_matches_oracle(wtype):
     """3,000 mel frames (1,500 rows, full width: d 1024, 16 heads, ffn 4096):
-    the conv stem, attention over all 1,500 rows and the adaptor's 375 rows."""
-    syn = mtg.SynthEncoder(seed=11, n_layers=2)
+    the conv stem, attention over all 1,500 rows and the adaptor's 375 rows, for
+    q8_0, f16 and q4_K matrices."""
+    syn = mtg.SynthEncoder(seed=11, wtype=wtype, n_layers=2)
     dev = mtg.Encoder(syn)
     orc = oracle_py.OracleEncoder(syn)
     mel = syn.mel(seed=12)
     rows = dev.encode(mel)
-    print("full chunk, 2 layers: encode %.2f ms" % dev.last_ms, flush=True)
+    print("full chunk, 2 layers, weights %d: encode %.2f ms" % (wtype, dev.last_ms), flush=True)
     _same(rows, orc.encode(mel), "encoder rows")
     _same(dev.adapt(1500), orc.adapt(1500), "adaptor rows")
     _same(dev.adapt(552), orc.adapt(552), "adaptor rows of a trimmed chunk")

@@ -115,8 +115,9 @@ class _ParsedEncoder:
         self.rows = (self.hp.n_frames - 1) // 2 + 1
 
 
-def test_encoder_from_gguf_matches_oracle(tmp_path):
-    syn = mtg.SynthEncoder(seed=31, n_frames=160, n_layers=2, ffn=2048)
+@pytest.mark.parametrize("wtype", [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_Q4_K], ids=["q8_0", "f16", "q4_K"])
+def test_encoder_from_gguf_matches_oracle(tmp_path, wtype):
+    syn = mtg.SynthEncoder(seed=31, wtype=wtype, n_frames=160, n_layers=2, ffn=2048)
     path = str(tmp_path / "enc.gguf")
     gguf_writer.write_encoder(path, syn)
     mel = syn.mel(seed=32)
