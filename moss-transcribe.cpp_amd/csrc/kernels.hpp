@@ -7,6 +7,7 @@
 
 #include <string>
 
+#include "gen_ctrl.hpp"
 #include "mtg_internal.hpp"
 
 namespace mtg {
@@ -144,10 +145,10 @@ void launch_embed_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8
                      const float* host_rows, float* x);
 
 // ---- the speculative controller on the device (generate.hip) ----
-// One controller pass: commit the previous step's result from res_map (the
-// mapped result buffer the step kernel writes; step_err: its error word), apply
-// the stop rules, draft and write the next descriptor (T = 0 once stopped).
-void launch_gen_ctrl(hipStream_t s, GenState* g, int32_t* ids, StepDesc* desc, StepResult* res_map,
-                     const int32_t* step_err, const int32_t* prompt, const int32_t* stream);
+// One controller pass (gen_ctrl.hpp) as its own launch: commit a pending step's
+// result from res_map (the mapped result buffer the step kernel writes; step_err:
+// its error word), apply the stop rules, draft and write the next descriptor
+// (T = 0 once stopped). A device loop runs it once, before its first step.
+void launch_gen_ctrl(hipStream_t s, const GenCtl& c, const StepResult* res_map, const int32_t* step_err);
 
 }  // namespace mtg

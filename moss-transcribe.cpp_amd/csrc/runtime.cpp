@@ -35,7 +35,10 @@ Ctx::~Ctx() {
   if (gen_aux_dev) hipFree(gen_aux_dev);
   if (gen_state_dev) hipFree(gen_state_dev);
   if (gen_state_host) hipHostFree(gen_state_host);
-  for (auto& e : gen_events)
+  for (auto& slot : gen_events)
+    for (auto& e : slot)
+      if (e) hipEventDestroy(e);
+  for (auto& e : gen_chunk_ev)
     if (e) hipEventDestroy(e);
   if (ev_start) hipEventDestroy(ev_start);
   if (ev_stop) hipEventDestroy(ev_stop);
@@ -800,9 +803,10 @@ int Ctx::kv_io(void* k, void* v, int n_pos, bool write) {
 
 namespace mtg {
 
-// The controller on the device: [k_gen_ctrl, step kernel] pairs enqueued in
-// chunks of kChunkSteps, the state looked at once per chunk. A step that leaves
-// before its acceptance ends the run with g.err set and that step undone.
+// The controller on the device: one k_gen_ctrl pass, then step launches in
+// chunks of kChunkSteps (each runs the controller pass on its own outcome), the
+// state looked at once per chunk. A step that leaves before its acceptance ends
+// the run with g.err set and that step undone.
 int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prompt_ids,
                          const int32_t* stream_ids) {
   constexpr int kChunkSteps = 8;
@@ -840,7 +844,8 @@ int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prom
   if (!gen_state_dev && (rc = check(hipMalloc((void**)&gen_state_dev, sizeof(GenState)), "generation state")))
     return rc;
   if (!gen_state_host &&
-      (rc = check(hipHostMalloc((void**)&gen_state_host, sizeof(GenState), hipHostMallocDefault), "generation state")))
+      (rc = check(hipHostMalloc((void**)&gen_state_host, 2 * sizeof(GenState), hipHostMallocDefault),
+                  "generation state")))
     return rc;
   *gen_state_host = g;
   if ((rc = check(hipMemcpyAsync(gen_state_dev, gen_state_host, sizeof(GenState), hipMemcpyHostToDevice, stream),
@@ -853,62 +858,89 @@ int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prom
   const int kv_f16 = kv_type == MTG_TYPE_F16;
   StepDesc unused{};
   result_host->err = 0;
-  // launch timing: an event pair around every step launch of a chunk; after the
-  // chunk, the launches that ran a step (the first `issued` ones) are counted
-  if (timing && !gen_events[0]) {
-    for (auto& e : gen_events)
-      if ((rc = check(hipEventCreate(&e), "event"))) return rc;
+  // launch timing: an event pair around every step launch of a chunk; once the
+  // chunk's state is back, the launches that ran a step (the first ones) count
+  if (!gen_chunk_ev[0]) {
+    for (auto& e : gen_chunk_ev)
+      if ((rc = check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "event"))) return rc;
   }
-  int64_t issued0 = g.issued, rows0 = g.issued_rows, past0 = g.issued_past;
-  for (;;) {
+  if (timing && !gen_events[0][0]) {
+    for (auto& slot : gen_events)
+      for (auto& e : slot)
+        if ((rc = check(hipEventCreate(&e), "event"))) return rc;
+  }
+  int64_t rows0 = g.issued_rows, past0 = g.issued_past;
+  int64_t steps0 = g.steps, err0 = g.err;
+  const GenCtl ctl{gen_state_dev, gen_ids_dev, desc_dev, prompt_dev, stream_dev};
+  // the first controller pass issues the first step; every step launch then runs
+  // the pass on its own outcome (commit, stop rules, the next step's draft)
+  launch_gen_ctrl(stream, ctl, result_map, &result_dev->err);
+  if ((rc = check(hipGetLastError(), "controller launch"))) return rc;
+  int64_t launched = 0;
+  int chunk_steps[2] = {0, 0};
+  // one chunk of step launches (with a step limit, no more than steps are left)
+  // and the copy of the state behind it, into slot `slot`
+  auto issue = [&](int slot) -> int {
     if (epoch > 0xF0000000u - (uint32_t)kChunkSteps * pps) {  // progress words restart before they could wrap
       if ((rc = check(hipMemsetAsync(params_host.flags, 0, (size_t)nwg * kFlagStride * 4, stream), "flags"))) return rc;
       if ((rc = check(hipMemsetAsync(params_host.qkvt, 0, qkvt_bytes(), stream), "tags"))) return rc;
       epoch = 0;
     }
-    // with a step limit, a chunk holds no more steps than are left to issue, and
-    // the chunk that issues the last one closes with one more controller pass,
-    // which takes that step's result. Otherwise the last step of a chunk is taken
-    // by the next chunk's first controller pass.
     int steps = kChunkSteps;
-    if (g.max_steps > 0) steps = (int)std::min<int64_t>(kChunkSteps, std::max<int64_t>(0, g.max_steps - issued0));
-    const bool closing = g.max_steps > 0 && issued0 + steps >= g.max_steps;
+    if (g.max_steps > 0) steps = (int)std::min<int64_t>(kChunkSteps, std::max<int64_t>(0, g.max_steps - launched));
     for (int i = 0; i < steps; ++i) {
-      launch_gen_ctrl(stream, gen_state_dev, gen_ids_dev, desc_dev, result_map, &result_dev->err, prompt_dev,
-                      stream_dev);
-      if ((rc = check(hipGetLastError(), "controller launch"))) return rc;
-      if (timing && (rc = check(hipEventRecord(gen_events[2 * i], stream), "timing event"))) return rc;
-      if ((rc = check(launch_step(stream, G, kv_f16, params_dev, &unused, epoch, kStepVerify, false, desc_dev),
+      if (timing && (rc = check(hipEventRecord(gen_events[slot][2 * i], stream), "timing event"))) return rc;
+      if ((rc = check(launch_step(stream, G, kv_f16, params_dev, &unused, epoch, kStepVerify, false, desc_dev, &ctl),
                       "step kernel launch")))
         return rc;
-      if (timing && (rc = check(hipEventRecord(gen_events[2 * i + 1], stream), "timing event"))) return rc;
+      if (timing && (rc = check(hipEventRecord(gen_events[slot][2 * i + 1], stream), "timing event"))) return rc;
       epoch += pps;
     }
-    if (closing) {
-      launch_gen_ctrl(stream, gen_state_dev, gen_ids_dev, desc_dev, result_map, &result_dev->err, prompt_dev,
-                      stream_dev);
-      if ((rc = check(hipGetLastError(), "controller launch"))) return rc;
-    }
-    if ((rc = check(hipMemcpyAsync(gen_state_host, gen_state_dev, sizeof(GenState), hipMemcpyDeviceToHost, stream),
+    launched += steps;
+    chunk_steps[slot] = steps;
+    if ((rc = check(hipMemcpyAsync(gen_state_host + slot, gen_state_dev, sizeof(GenState), hipMemcpyDeviceToHost,
+                                   stream),
                     "generation state")))
       return rc;
-    if ((rc = check(hipStreamSynchronize(stream), "generation"))) return rc;
+    return check(hipEventRecord(gen_chunk_ev[slot], stream), "chunk event");
+  };
+  auto limit_reached = [&]() { return g.max_steps > 0 && launched >= g.max_steps; };
+  // Two chunks in flight: the next chunk is enqueued before the host waits for
+  // the current one's state, so the device does not idle at a chunk boundary.
+  // Launches after the loop has stopped return at once.
+  if ((rc = issue(0))) return rc;
+  int cur = 0;
+  for (;;) {
+    const bool next = !limit_reached();
+    if (next && (rc = issue(cur ^ 1))) return rc;
+    if ((rc = check(hipEventSynchronize(gen_chunk_ev[cur]), "generation"))) return rc;
+    const GenState& st = gen_state_host[cur];
+    // the launches of the chunk that ran a step come first: each committed one
+    // step, or left with the error that ended the loop
+    const int64_t ran = std::min<int64_t>(chunk_steps[cur], (st.steps - steps0) + (st.err - err0));
     if (timing) {
-      const int ran = (int)std::min<int64_t>(kChunkSteps, gen_state_host->issued - issued0);
-      for (int i = 0; i < ran; ++i) {
+      for (int i = 0; i < (int)ran; ++i) {
         float ms = 0.0f;
-        if ((rc = check(hipEventElapsedTime(&ms, gen_events[2 * i], gen_events[2 * i + 1]), "timing"))) return rc;
+        if ((rc = check(hipEventElapsedTime(&ms, gen_events[cur][2 * i], gen_events[cur][2 * i + 1]), "timing")))
+          return rc;
         timing_ms += ms;
       }
       timing_launches += ran;
-      timing_rows += gen_state_host->issued_rows - rows0;
-      timing_past += gen_state_host->issued_past - past0;
+      timing_rows += st.issued_rows - rows0;
+      timing_past += st.issued_past - past0;
     }
-    issued0 = gen_state_host->issued;
-    rows0 = gen_state_host->issued_rows;
-    past0 = gen_state_host->issued_past;
-    if (gen_state_host->done) break;
+    steps0 = st.steps;
+    err0 = st.err;
+    rows0 = st.issued_rows;
+    past0 = st.issued_past;
+    if (st.done || !next) break;  // without a next chunk the last step's pass has stopped the loop
+    cur ^= 1;
   }
+  // the chunk still in flight runs launches that return at once; the state is final
+  if ((rc = check(hipStreamSynchronize(stream), "generation"))) return rc;
+  if ((rc = check(hipMemcpy(gen_state_host, gen_state_dev, sizeof(GenState), hipMemcpyDeviceToHost),
+                  "generation state")))
+    return rc;
   g = *gen_state_host;
   if ((rc = check(hipMemcpy(ids, gen_ids_dev, (size_t)g.n_ids * 4, hipMemcpyDeviceToHost), "generation ids")))
     return rc;

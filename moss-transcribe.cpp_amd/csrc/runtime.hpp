@@ -126,8 +126,12 @@ struct Ctx {
   int gen_cap = 0;
   int32_t* gen_aux_dev = nullptr;  // the stream drafter's prompt ids, then its stream period
   int gen_aux_cap = 0;
-  hipEvent_t gen_events[16] = {};  // launch timing of the device loop: a pair per step of a chunk
-  GenState* gen_state_host = nullptr;  // pinned
+  // the device loop keeps two chunks of step launches in flight: per chunk slot an
+  // event pair per launch (launch timing), the event after its state copy, and
+  // the pinned copy of the state
+  hipEvent_t gen_events[2][16] = {};
+  hipEvent_t gen_chunk_ev[2] = {};
+  GenState* gen_state_host = nullptr;  // pinned, [2]
   int generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prompt_ids, const int32_t* stream_ids);
 };
 

@@ -1326,7 +1326,8 @@ __device__ __forceinline__ void lm_head(const StepParams& P, float penalty, bool
 // then the four waves.
 template <int G>
 __device__ void accept(const uint64_t* part_keys, int32_t tok, StepResult* result, int T, int nwg,
-                       uint64_t* s_red, int32_t* s_choice, int32_t* s_tok, uint64_t* timing, int slot) {
+                       uint64_t* s_red, int32_t* s_choice, int32_t* s_tok, int32_t* s_nmatch, uint64_t* timing,
+                       int slot) {
   static_assert(kNwg <= kT, "one thread per workgroup's keys");
   T = __builtin_amdgcn_readfirstlane(T);
   nwg = __builtin_amdgcn_readfirstlane(nwg);
@@ -1362,6 +1363,7 @@ __device__ void accept(const uint64_t* part_keys, int32_t tok, StepResult* resul
     StepResult* r = uniform_ptr(result);
     for (int t = 0; t < kMaxRows; ++t) r->choice[t] = t < T ? s_choice[t] : -1;
     r->n_match = m;
+    *s_nmatch = m;
   }
 }
 
@@ -1394,30 +1396,22 @@ __device__ __forceinline__ const StepDesc& step_desc<false>(const StepDesc& arg,
 template <>
 __device__ __forceinline__ const StepDesc& step_desc<true>(const StepDesc&, const StepDesc* dev) { return *dev; }
 
-// PROF: the profiled variant (clock marks into P.timing); the production
-// variant carries no marks at all (they would cost code size and registers).
-// DEV: the descriptor comes from desc_dev (T == 0 there: nothing to do).
-template <int G, int KVH, bool PROF, bool DEV = false>
-__global__ void __launch_bounds__(kT, 1)
-k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoch,
-        int mode, const StepDesc* __restrict__ desc_dev) {
+// The step itself; the kernel below adds the device loop's controller pass. The
+// return value matters in workgroup 0 only: true once its acceptance is done.
+template <int G, int KVH, bool PROF, bool DEV>
+__device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, const StepDesc& desc_arg,
+                                          uint32_t epoch, int mode, const StepDesc* __restrict__ desc_dev,
+                                          uint8_t* lds, int& s_ok, uint64_t* s_best, uint64_t* s_red,
+                                          int32_t* s_choice, int32_t* s_tok, int32_t* s_nmatch) {
 #define MARK(...) do { if constexpr (PROF) mark(__VA_ARGS__); } while (0)
 #define WMARK(...) do { if constexpr (PROF) wmark(__VA_ARGS__); } while (0)
   const StepParams& P = *Pp;
-  extern __shared__ v4i lds_v4[];
-  uint8_t* lds = (uint8_t*)lds_v4;
-  __shared__ int s_ok;
-  __shared__ uint64_t s_best[4 * kMaxRows];
-  __shared__ uint64_t s_red[kT];
-  __shared__ int32_t s_choice[kMaxRows];
-  __shared__ int32_t s_tok[kMaxRows];
   const int w = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // The step descriptor arrives by value in the kernel arguments (no copy to
   // device memory before the launch). Its fields are read in place; its address
   // is never taken (that would give every thread a private copy).
   const StepDesc& desc = step_desc<DEV>(desc_arg, desc_dev);
   const int T = desc.T, past = desc.past, L = P.L;
-  if (DEV && T == 0) return;  // the controller has stopped
   const int nch = (past + T + kChunk - 1) / kChunk, n_items = cNKV * nch;
   uint8_t* pcodes = lds;
   float* pscales = (float*)(lds + (size_t)G * cBF * kPanelUnit);
@@ -1540,7 +1534,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   for (int l = 0; l < L; ++l) {
     const LayerDev& Ly = layer_at(P, l);
     // ---- QKV: tile w ----
-    if (!wait_all(c, ph(l, kPhQkv) - 1)) return;
+    if (!wait_all(c, ph(l, kPhQkv) - 1)) return false;
     MARK(P, 3 + 12 * l + 0);
     WMARK(P, l, 0);
     panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, nullptr, stg, G == 1 ? nullptr : Ly.attn_norm,
@@ -1583,7 +1577,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     }
     // ---- MERGE: (head, row) items, two at a time ----
     if (has_merge) {
-      if (!wait_all(c, ph(l, kPhMerge) - 1)) return;
+      if (!wait_all(c, ph(l, kPhMerge) - 1)) return false;
       WMARK(P, l, 4);
       const int half = threadIdx.x >> 7;
       for (int i0 = 2 * merge_slot; i0 < n_merge; i0 += 2 * kMergeSlots) {
@@ -1604,7 +1598,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     }
     // ---- O-proj: x += W_o o ----
     if (od) {
-      if (!wait_all(c, ph(l, kPhO) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return;
+      if (!wait_all(c, ph(l, kPhO) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return false;
       MARK(P, 3 + 12 * l + 4);
       WMARK(P, l, 6);
       panel_from_q<cQN, G>(P.oq, P.oqs, T, pcodes, pscales);
@@ -1631,7 +1625,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     }
     // ---- GATE/UP: act = silu(g) * u, as q8_0 blocks ----
     if (gu) {
-      if (!wait_all(c, ph(l, kPhGu) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return;
+      if (!wait_all(c, ph(l, kPhGu) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return false;
       WMARK(P, l, 8);
       panel_norm<G == 1>(RX, T, gf, P.eps, pcodes, pscales, nullptr, stg, G == 1 ? nullptr : Ly.ffn_norm);
       WMARK(P, l, 27);
@@ -1652,7 +1646,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
     }
     // ---- DOWN: x += W_d act ----
     if (od) {
-      if (!wait_all(c, ph(l, kPhD) - 1)) return;
+      if (!wait_all(c, ph(l, kPhD) - 1)) return false;
       MARK(P, 3 + 12 * l + 6);
       WMARK(P, l, 10);
       panel_from_q<cF, G>(P.aq, P.aqs, T, pcodes, pscales);
@@ -1679,14 +1673,14 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   const uint32_t lm = ph(L, 0);
   if (mode != kStepVerify) {
     if (w == 0) {
-      if (!wait_all(c, lm - 1)) return;
+      if (!wait_all(c, lm - 1)) return false;
       if constexpr (G == 1) gain16_load(P.out_norm, gq);
       panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, P.hid, stg, G == 1 ? nullptr : P.out_norm);
       MARK(P, 2);
     }
-    return;
+    return false;
   }
-  if (!wait_all(c, lm - 1)) return;
+  if (!wait_all(c, lm - 1)) return false;
   MARK(P, 3 + 12 * L);
   if constexpr (G == 1) gain16_load(P.out_norm, gq);
   panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr, stg, G == 1 ? nullptr : P.out_norm);
@@ -1694,16 +1688,54 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   publish(c, lm);
   MARK(P, 4 + 12 * L);
   if (w == 0) {
-    if (!wait_all(c, lm)) return;
+    if (!wait_all(c, lm)) return false;
     MARK(P, 5 + 12 * L);
     accept<G>(P.part_keys, (int)threadIdx.x < T ? desc.tokens[threadIdx.x] : 0, P.result, T, kNwg, s_red,
-              s_choice, s_tok, PROF ? P.timing : nullptr, 7 + 12 * L);
+              s_choice, s_tok, s_nmatch, PROF ? P.timing : nullptr, 7 + 12 * L);
     MARK(P, 6 + 12 * L);
+    return true;
   }
+  return false;
 #undef MARK
 #undef WMARK
 #undef RX
 #undef RQKVT
+}
+
+static_assert(step_lds_stage_offset(1) >= (size_t)kGenLdsIds * 4, "the controller pass stages ids in the step's LDS");
+
+// PROF: the profiled variant (clock marks into P.timing); the production
+// variant carries no marks at all (they would cost code size and registers).
+// DEV: the descriptor comes from desc_dev (nothing to do once T == 0 there or
+// gc.g->done is set); with gc.g, workgroup 0 then runs the device loop's
+// controller pass on this step's outcome: the acceptance done, or (the
+// workgroup left at a wait that ran out) a failed step, in which case the
+// descriptor stays as it is (other workgroups may still read it) and the next
+// launches return on g->done.
+template <int G, int KVH, bool PROF, bool DEV = false>
+__global__ void __launch_bounds__(kT, 1)
+k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoch,
+        int mode, const StepDesc* __restrict__ desc_dev, GenCtl gc) {
+  extern __shared__ v4i lds_v4[];
+  uint8_t* lds = (uint8_t*)lds_v4;
+  __shared__ int s_ok;
+  __shared__ uint64_t s_best[4 * kMaxRows];
+  __shared__ uint64_t s_red[kT];
+  __shared__ int32_t s_choice[kMaxRows];
+  __shared__ int32_t s_tok[kMaxRows];
+  __shared__ int32_t s_nmatch;
+  if constexpr (DEV) {
+    if (desc_dev->T == 0 || (gc.g && gc.g->done)) return;  // the controller has stopped
+  }
+  const bool accepted = step_body<G, KVH, PROF, DEV>(Pp, desc_arg, epoch, mode, desc_dev, lds, s_ok, s_best, s_red,
+                                                     s_choice, s_tok, &s_nmatch);
+  if constexpr (DEV) {
+    if (gc.g && blockIdx.x == 0) {
+      __syncthreads();
+      const GenStepOutcome prev{!accepted, s_choice, s_nmatch};
+      gen_ctrl_pass(gc, prev, accepted, (int32_t*)lds, (int*)s_red, (int*)(s_red + 8));
+    }
+  }
 }
 
 }  // namespace
@@ -1757,10 +1789,12 @@ hipError_t prepare_step_kernels() {
 }
 
 hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
-                        uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev) {
+                        uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev, const GenCtl* gc) {
   // desc: host memory; the launch copies it into the kernel arguments. desc_dev
   // (verify steps of up to 8 G rows): the kernel reads the descriptor there instead.
-  void* args[] = {(void*)&P, (void*)desc, (void*)&epoch, (void*)&mode, (void*)&desc_dev};
+  GenCtl ctl{};
+  if (gc) ctl = *gc;
+  void* args[] = {(void*)&P, (void*)desc, (void*)&epoch, (void*)&mode, (void*)&desc_dev, (void*)&ctl};
   if (desc_dev) {
     if (G < 1 || G > 2 || profiled) return hipErrorInvalidValue;
     return hipLaunchKernel(step_fn_dev(G, kv_f16), dim3(kNwg), dim3(kT), args, step_lds_bytes(G), s);

@@ -5,6 +5,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "gen_ctrl.hpp"
 #include "mtg_internal.hpp"
 
 namespace mtg {
@@ -68,8 +69,12 @@ uint32_t step_progress_per_step(int n_layers);
 size_t step_lds_bytes(int G);
 hipError_t prepare_step_kernels();
 // desc: the host copy of the step descriptor (passed by value as a kernel
-// argument). profiled: the variant that writes clock marks into StepParams::timing
+// argument). profiled: the variant that writes clock marks into StepParams::timing.
+// desc_dev: the variant that reads the descriptor from device memory (a device
+// loop); with gc, its workgroup 0 then runs the controller pass on the step's
+// outcome (gen_ctrl.hpp), and the launch returns at once once gc->g->done is set.
 hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
-                        uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev = nullptr);
+                        uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev = nullptr,
+                        const GenCtl* gc = nullptr);
 
 }  // namespace mtg
