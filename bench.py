@@ -90,7 +90,7 @@ def weight_bytes(hp, wtype):
     H, D, F = hp.hidden, hp.head_dim, hp.intermediate
     layer = (H * (hp.n_heads * D) * 2 + H * (hp.n_kv_heads * D) * 2 + 3 * H * F) * hp.n_layers
     params = layer + hp.vocab * H
-    per = {mtg.TYPE_Q8_0: 34 / 32, mtg.TYPE_F16: 2.0, mtg.TYPE_Q4_K: 144 / 256}[wtype]
+    per = {mtg.TYPE_Q8_0: 34 / 32, mtg.TYPE_F16: 2.0, mtg.TYPE_F32: 4.0, mtg.TYPE_Q4_K: 144 / 256}[wtype]
     return params * per
 
 
@@ -204,6 +204,9 @@ def main():
     ap.add_argument("--prefill-runs", type=int, default=0,
                     help="only prefill the workload's prompt this many times (block prefill) and print "
                          "its device time; for kernel traces of the prefill")
+    ap.add_argument("--weights", choices=["q8_0", "f16", "f32", "q4_K"], default=None,
+                    help="run the workload with another weight type than its own (e.g. f32, the "
+                         "converter's default dtype); not a bench line of the workload")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, copy a buffer of this size 5 times (device to device) "
                          "so that a counter profile of the same command can calibrate FETCH_SIZE "
@@ -214,7 +217,9 @@ def main():
               "shards only across independent streams (one decoder per recording, one GPU each).",
               file=sys.stderr)
         sys.exit(2)
-    cfg = CONFIGS[args.config]
+    cfg = dict(CONFIGS[args.config])
+    if args.weights is not None:
+        cfg["wtype"] = {v: k for k, v in WNAME.items()}[args.weights]
     steps = args.steps if args.steps is not None else cfg["steps"]
     t_setup = time.perf_counter()
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0, n_layers=args.layers)
@@ -285,7 +290,8 @@ def main():
     bytes_launch = weight_bytes(hp, cfg["wtype"]) + (past_sum + 2 * rows_sum) / max(launches, 1) * kvpos
     launch_s = dev_ms * 1e-3 / max(launches, 1)
     achieved = bytes_launch / launch_s / 1e9
-    traffic = measured_traffic(args.config) if args.layers == 28 and args.exec == "step" else None
+    traffic = (measured_traffic(args.config) if args.layers == 28 and args.exec == "step" and args.weights is None
+               else None)
     out = {
         "metric": METRIC,
         "value": tokens / elapsed,
@@ -297,7 +303,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {mtg.TYPE_Q8_0: "q8_0 (int8 dots, f32 accumulate)", mtg.TYPE_F16: "f16",
+        "dtype": {mtg.TYPE_Q8_0: "q8_0 (int8 dots, f32 accumulate)", mtg.TYPE_F16: "f16", mtg.TYPE_F32: "f32",
                   mtg.TYPE_Q4_K: "q4_K"}[cfg["wtype"]],
         "data": "synthetic: seeded random weights, seeded audio-like prompt rows and draft stream",
         "config": {"workload": "Qwen3-0.6B-shaped verify step, %d layers, K=%d rows, %s weights, "

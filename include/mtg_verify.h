@@ -99,7 +99,7 @@ typedef struct mtg_layer_tensors {
 
 typedef struct mtg_model_desc {
   mtg_hparams hp;
-  int32_t weight_type;              /* MTG_TYPE_Q8_0, MTG_TYPE_F16 or MTG_TYPE_Q4_K */
+  int32_t weight_type;              /* MTG_TYPE_Q8_0, MTG_TYPE_F16, MTG_TYPE_F32 or MTG_TYPE_Q4_K */
   const void* token_embd;           /* N = vocab, K = hidden; also the tied lm_head */
   const float* output_norm;         /* [hidden] */
   const mtg_layer_tensors* layers;  /* n_layers entries */
@@ -380,7 +380,7 @@ int mtg_gguf_tensor(const mtg_gguf* g, const char* name, int32_t* type, int64_t*
                     size_t* bytes);
 /* The Qwen3 decoder of the file: hyper-parameters from the mtd.text.* keys
  * (the reference's defaults where absent), every tensor found by name and
- * checked for shape and for one weight type (q8_0, f16 or q4_K); f16 norm
+ * checked for shape and for one weight type (q8_0, f16, f32 or q4_K); f16 norm
  * gains are widened to f32. NULL on failure (mtg_gguf_error). The description
  * stays valid until mtg_gguf_close. */
 const mtg_model_desc* mtg_gguf_model(mtg_gguf* g);
@@ -420,7 +420,7 @@ typedef struct mtg_encoder_layer {
 
 typedef struct mtg_encoder_desc {
   mtg_encoder_hparams hp;
-  int32_t weight_type;                  /* of every matrix: MTG_TYPE_Q8_0, _F16 or _Q4_K */
+  int32_t weight_type;                  /* of every matrix: MTG_TYPE_Q8_0, _F16, _F32 or _Q4_K */
   const float *conv1_w, *conv1_b;       /* enc.conv1.{w,b}: [d][n_mels][3], [d] */
   const float *conv2_w, *conv2_b;       /* enc.conv2.{w,b}: [d][d][3], [d] (stride 2) */
   const float* pos_embd;                /* enc.pos_embd [rows][d] */

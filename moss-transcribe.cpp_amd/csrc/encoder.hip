@@ -514,7 +514,7 @@ struct mtg_encoder {
     rc = check(hipStreamSynchronize(stream), "retile");
     return d;
   }
-  // an n x kk matrix: q8_0 re-tiled for the int8 MFMA GEMM, f16 / q4_K as they are
+  // an n x kk matrix: q8_0 re-tiled for the int8 MFMA GEMM, f16 / f32 / q4_K as they are
   uint8_t* up_w(const void* src, int n, int kk, uint8_t* staging, int& rc) {
     if (wtype == MTG_TYPE_Q8_0) return up_q8(src, n, kk, staging, rc);
     if (rc) return nullptr;
@@ -522,7 +522,9 @@ struct mtg_encoder {
       rc = fail(MTG_ERR_INVALID, "a tensor pointer is NULL");
       return nullptr;
     }
-    const size_t bytes = (size_t)n * (wtype == MTG_TYPE_F16 ? (size_t)kk * 2 : (size_t)(kk / 256) * 144);
+    const size_t bytes = (size_t)n * (wtype == MTG_TYPE_F16   ? (size_t)kk * 2
+                                      : wtype == MTG_TYPE_F32 ? (size_t)kk * 4
+                                                              : (size_t)(kk / 256) * 144);
     uint8_t* d = (uint8_t*)dalloc(bytes);
     if (!d) {
       rc = fail(MTG_ERR_NOMEM, "device memory");
@@ -561,7 +563,8 @@ int mtg_encoder_create(const mtg_encoder_desc* d, mtg_encoder** out) {
   const mtg_encoder_hparams& hp = d->hp;
   const int wt = d->weight_type;
   const bool wt_ok = wt == MTG_TYPE_Q8_0 ||
-                     ((wt == MTG_TYPE_F16 || wt == MTG_TYPE_Q4_K) && pf_gemm_wt_supported(wt, hp.d_model) &&
+                     ((wt == MTG_TYPE_F16 || wt == MTG_TYPE_F32 || wt == MTG_TYPE_Q4_K) &&
+                      pf_gemm_wt_supported(wt, hp.d_model) &&
                       pf_gemm_wt_supported(wt, hp.ffn) && pf_gemm_wt_supported(wt, hp.hidden) &&
                       pf_gemm_wt_supported(wt, hp.d_model * hp.merge));
   if (!wt_ok || hp.d_model != 1024 || hp.hidden != 1024 || hp.n_heads <= 0 ||
@@ -643,6 +646,9 @@ int mtg_encoder_create(const mtg_encoder_desc* d, mtg_encoder** out) {
     if (wt == MTG_TYPE_F16) {
       e->act.f16h = (uint16_t*)e->dalloc(KC * 2);
       if (!e->act.f16h) rc = e->fail(MTG_ERR_NOMEM, "device memory");
+    } else if (wt == MTG_TYPE_F32) {
+      e->act.f32 = (float*)e->dalloc(KC * 4);
+      if (!e->act.f32) rc = e->fail(MTG_ERR_NOMEM, "device memory");
     } else if (wt == MTG_TYPE_Q4_K) {
       e->act.q8k.qs = (int8_t*)e->dalloc(KC);
       e->act.q8k.d = (float*)e->dalloc(KC / 256 * 4);

@@ -359,9 +359,9 @@ const mtg_model_desc* mtg_gguf_model(mtg_gguf* g) {
     const TensorInfo* embd = nullptr;
     if (!find("token_embd.weight", &embd)) return nullptr;
     const uint32_t wtype = embd->type;
-    if (wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16 && wtype != MTG_TYPE_Q4_K) {
+    if (wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16 && wtype != MTG_TYPE_F32 && wtype != MTG_TYPE_Q4_K) {
       g->fail(MTG_ERR_UNSUPPORTED, std::string("weight type ") + type_name(wtype) + " (" + std::to_string(wtype) +
-                                       ") is not supported: q8_0, f16 or q4_K");
+                                       ") is not supported: q8_0, f16, f32 or q4_K");
       return nullptr;
     }
     auto matrix = [&](const std::string& name, int64_t k, int64_t n, const void** out) -> bool {
@@ -460,14 +460,14 @@ const mtg_encoder_desc* mtg_gguf_encoder(mtg_gguf* g) {
       *t = &it->second;
       return true;
     };
-    // the matrices' type: the converter writes q8_0 or f16 (--dtype), and
+    // the matrices' type: the converter writes f32, f16 or q8_0 (--dtype), and
     // `cli quantize q4_k` turns the encoder and adaptor matrices into q4_K
     // (src/cli.cpp:106-130); all of them share it
     if (!find(hp.n_layers > 0 ? "enc.blk.0.attn_q.w" : "adaptor.fc1.w", &q0)) return nullptr;
     const uint32_t wtype = q0->type;
-    if (wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16 && wtype != MTG_TYPE_Q4_K) {
-      g->fail(MTG_ERR_UNSUPPORTED,
-              std::string("encoder weight type ") + type_name(wtype) + " is not supported: q8_0, f16 or q4_K");
+    if (wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16 && wtype != MTG_TYPE_F32 && wtype != MTG_TYPE_Q4_K) {
+      g->fail(MTG_ERR_UNSUPPORTED, std::string("encoder weight type ") + type_name(wtype) +
+                                       " is not supported: q8_0, f16, f32 or q4_K");
       return nullptr;
     }
     auto matrix = [&](const std::string& name, int64_t k, int64_t n, const void** out) -> bool {

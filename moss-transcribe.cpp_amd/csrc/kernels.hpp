@@ -40,6 +40,7 @@ struct ActQ8K {
 struct WtAct {
   uint16_t* f16h;  // [16][K] f16 bits
   ActQ8K q8k;
+  float* f32;  // [16][K] the rows as they are (f32 weights)
 };
 
 struct AttnWork {
@@ -119,7 +120,7 @@ void launch_pf_act_wt(hipStream_t s, int wtype, const float* src, int S, int K, 
 // for f16 or q4_K weights in the GGUF row layout
 void launch_pf_gemm_wt(hipStream_t s, int wtype, int epi, const uint8_t* w, const uint8_t* w2, int N, int K,
                        const WtAct& act, int S, float* out, const float* bias = nullptr);
-// the K this GEMM takes: f16 1,024 / 2,048 / 3,072 / 4,096; q4_K any multiple of 256
+// the K this GEMM takes: f16 and f32 1,024 / 2,048 / 3,072 / 4,096; q4_K any multiple of 256
 int pf_gemm_wt_supported(int wtype, int K);
 
 // ---- f16 / q4_K weights (kernels_wt.hip); weights in the GGUF row layout ----

@@ -68,10 +68,12 @@ __device__ __forceinline__ void stage_pieces(const v4i* __restrict__ src, int n,
 // ------------------------------------------------------- activations ------
 // Grid (16 rows, K / 256), 256 threads: one element per thread. gain == nullptr:
 // no norm (the SwiGLU product goes in as it is); otherwise every workgroup of a
-// row recomputes the row's RMS scale (same order, same value).
+// row recomputes the row's RMS scale (same order, same value). F32: the rows go
+// out as they are (vec_dot_type F32), otherwise as f16.
+template <bool F32>
 __global__ void __launch_bounds__(256)
 k_act_f16(const StepDesc* __restrict__ desc, const float* __restrict__ src, int K,
-          const float* __restrict__ gain, float eps, uint16_t* __restrict__ out,
+          const float* __restrict__ gain, float eps, uint16_t* __restrict__ out, float* __restrict__ out32,
           float* __restrict__ normed_out) {
   const int t = blockIdx.x, k = blockIdx.y * 256 + threadIdx.x;
   if (t >= desc->T) return;
@@ -89,7 +91,8 @@ k_act_f16(const StepDesc* __restrict__ desc, const float* __restrict__ src, int 
     y = __fmul_rn(__fmul_rn(y, s_scale), gk);
   }
   if (normed_out) normed_out[(size_t)t * K + k] = y;
-  out[(size_t)t * K + k] = __half_as_ushort(__float2half_rn(y));  // vec_dot_type F16
+  if constexpr (F32) out32[(size_t)t * K + k] = y;
+  else out[(size_t)t * K + k] = __half_as_ushort(__float2half_rn(y));  // vec_dot_type F16
 }
 
 
@@ -241,6 +244,7 @@ k_attn_combine_wt(const StepDesc* __restrict__ desc, AttnWork work, int n_heads,
 // of k_attn_combine_wt, a quarter of the partial loads each.
 constexpr int kCombDq = 32;
 
+template <bool F32>
 __global__ void __launch_bounds__(64 * kCombSeg)
 k_attn_combine_f16q(const StepDesc* __restrict__ desc, AttnWork work, int n_heads, int max_chunks, WtAct act) {
   const int g = blockIdx.x, t = blockIdx.y;
@@ -338,7 +342,9 @@ k_attn_combine_f16q(const StepDesc* __restrict__ desc, AttnWork work, int n_head
   }
   if (seg == 0) {
     const float val = __fdiv_rn(s_O[lane], s_L[lane]);
-    act.f16h[(size_t)t * n_heads * kHeadDim + g * 256 + hl * kHeadDim + d] = __half_as_ushort(__float2half_rn(val));
+    const size_t i = (size_t)t * n_heads * kHeadDim + g * 256 + hl * kHeadDim + d;
+    if constexpr (F32) act.f32[i] = val;
+    else act.f16h[i] = __half_as_ushort(__float2half_rn(val));
   }
 }
 
@@ -473,6 +479,8 @@ __global__ void k_embed_wt(const StepDesc* __restrict__ desc, const uint8_t* __r
   for (int k = threadIdx.x; k < hidden; k += blockDim.x) {
     if constexpr (WT == MTG_TYPE_F16) {
       xr[k] = half_bits_to_float(((const uint16_t*)w)[(size_t)n * hidden + k]);
+    } else if constexpr (WT == MTG_TYPE_F32) {
+      xr[k] = ((const float*)w)[(size_t)n * hidden + k];
     } else {  // dequantize_row_q4_K
       const uint8_t* blk = w + ((size_t)n * (hidden / 256) + k / 256) * 144;
       const int e = k % 256, s = e / 32, l = e % 32;
@@ -1384,6 +1392,164 @@ k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, 
   }
 }
 
+// ------------------------------------------------------------- f32 rows ----
+// f32 weights (vec_dot_type F32: the activation rows as they are). A wave takes
+// NR rows of each of the NM matrices; lane l holds elements [l SEG, (l + 1) SEG)
+// of each row and runs their fma chain from 0 for one verify row after the other,
+// then wave_sum_f_n reduces the NM * NR partials of that verify row side by side
+// (the xor butterfly 32, 16, .. 1: the f16 order's segments and tree, each step
+// of a chain one rounding). The activation rows come from memory (at most
+// 16 x 3,072 floats: cache-resident); the next group's weights are in flight
+// during the current group's chains.
+template <int SEG, int NM, int NR>
+struct F32Group {
+  v4f w[NM][NR][SEG / 4];
+};
+
+template <int SEG, int NM, int NR>
+__device__ __forceinline__ void f32_load(const float* const (&base)[NM], int n, int row0, F32Group<SEG, NM, NR>& g) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int row = min(row0 + r, n - 1);  // rows past n: loaded, never stored
+#pragma unroll
+      for (int p = 0; p < SEG / 4; ++p)
+        g.w[m][r][p] = *(const v4f*)(base[m] + (size_t)row * (SEG * 64) + lane * SEG + 4 * p);
+    }
+}
+
+// acc[m * NR + r] <- the dot of row r of matrix m with verify row t (every lane)
+template <int SEG, int NM, int NR>
+__device__ __forceinline__ void f32_dots(const F32Group<SEG, NM, NR>& g, const float* __restrict__ x, int t,
+                                         float (&acc)[NM * NR]) {
+  const int lane = threadIdx.x & 63;
+  v4f xv[SEG / 4];
+#pragma unroll
+  for (int p = 0; p < SEG / 4; ++p) xv[p] = *(const v4f*)(x + (size_t)t * (SEG * 64) + lane * SEG + 4 * p);
+#pragma unroll
+  for (int i = 0; i < NM * NR; ++i) acc[i] = 0.0f;
+#pragma unroll
+  for (int p = 0; p < SEG / 4; ++p)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[m * NR + r] = fmaf(g.w[m][r][p][e], xv[p][e], acc[m * NR + r]);
+  wave_sum_f_n<NM * NR>(acc);
+}
+
+// EPI 0: store, 1: residual add, 2: silu(W x) * (W2 x) (f32 rows: the down
+// projection's activation as it is). Lane r < NR stores row r of the group.
+template <int EPI, int SEG, int NR>
+__global__ void __launch_bounds__(256)
+k_gemm_f32(const StepDesc* __restrict__ desc, const float* __restrict__ w, const float* __restrict__ w2, int n,
+           const float* __restrict__ x, float* __restrict__ out) {
+  constexpr int NM = EPI == 2 ? 2 : 1;
+  const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int ngroups = (n + NR - 1) / NR, nwaves = gridDim.x * 4;
+  const float* base[NM];
+  base[0] = w;
+  if (NM == 2) base[NM - 1] = w2;
+  int g = blockIdx.x * 4 + wave;
+  F32Group<SEG, NM, NR> nxt;
+  if (g < ngroups) f32_load<SEG, NM, NR>(base, n, g * NR, nxt);
+  for (; g < ngroups; g += nwaves) {
+    const F32Group<SEG, NM, NR> cur = nxt;
+    if (g + nwaves < ngroups) f32_load<SEG, NM, NR>(base, n, (g + nwaves) * NR, nxt);
+    const int row = g * NR + lane;
+    for (int t = 0; t < T; ++t) {
+      float acc[NM * NR];
+      f32_dots<SEG, NM, NR>(cur, x, t, acc);
+      float v0 = acc[0], v1 = acc[NM * NR - NR];
+#pragma unroll
+      for (int r = 1; r < NR; ++r)
+        if (lane == r) {
+          v0 = acc[r];
+          v1 = acc[NM * NR - NR + r];
+        }
+      if (lane < NR && row < n) {
+        float* dst = out + (size_t)t * n + row;
+        if (EPI == 0) *dst = v0;
+        else if (EPI == 1) *dst = __fadd_rn(*dst, v0);
+        else *dst = dev_swiglu(v0, v1);
+      }
+    }
+  }
+}
+
+// f32 lm_head over the rows of the tied embedding, grouped as in k_gemm_f32; per
+// verify row the best 64-bit key of the workgroup goes to part_keys
+// (kLmWorkgroups workgroups, one slot each).
+template <int SEG, int NR>
+__global__ void __launch_bounds__(256)
+k_lm_head_f32(const StepDesc* __restrict__ desc, const float* __restrict__ w, int vocab, const float* __restrict__ x,
+              const uint32_t* __restrict__ bitmap, float* __restrict__ logits, uint64_t* __restrict__ part_keys) {
+  const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const bool pen = desc->penalty > 1.0f;
+  const float penalty = desc->penalty;
+  const bool write_logits = desc->write_logits != 0;
+  const int words = (vocab + 31) / 32;
+  const int ngroups = (vocab + NR - 1) / NR, nwaves = gridDim.x * 4;
+  const float* base[1] = {w};
+  int g = blockIdx.x * 4 + wave;
+  F32Group<SEG, 1, NR> nxt;
+  if (g < ngroups) f32_load<SEG, 1, NR>(base, vocab, g * NR, nxt);
+  uint64_t best = 0;  // lane t: verify row t
+  for (; g < ngroups; g += nwaves) {
+    const F32Group<SEG, 1, NR> cur = nxt;
+    if (g + nwaves < ngroups) f32_load<SEG, 1, NR>(base, vocab, (g + nwaves) * NR, nxt);
+    for (int t = 0; t < T; ++t) {
+      float acc[NR];
+      f32_dots<SEG, 1, NR>(cur, x, t, acc);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int row = g * NR + r;
+        if (row < vocab) {
+          float v = acc[r];
+          if (write_logits && lane == 0) logits[(size_t)t * vocab + row] = v;
+          if (pen && ((bitmap[(size_t)t * words + (row >> 5)] >> (row & 31)) & 1u))
+            v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+          const uint64_t key = argmax_key(v, row);
+          if (lane == t) best = key > best ? key : best;
+        }
+      }
+    }
+  }
+  __shared__ uint64_t s_best[4][64];
+  s_best[wave][lane] = best;
+  __syncthreads();
+  if ((int)threadIdx.x < T) {
+    uint64_t b = 0;
+    for (int i = 0; i < 4; ++i) b = s_best[i][threadIdx.x] > b ? s_best[i][threadIdx.x] : b;
+    part_keys[(size_t)blockIdx.x * kMaxRows + threadIdx.x] = b;
+  }
+}
+
+// weight rows per wave and group of the f32 GEMM: NM * NR * K / 64 <= 64 weight
+// floats per lane (twice that with the next group in flight)
+constexpr int f32_nr(int nm, int seg) { return seg == 16 ? 4 / nm : seg == 32 ? (nm == 1 ? 2 : 1) : 1; }
+
+template <int EPI>
+void gemm_f32(hipStream_t s, const StepDesc* desc, const uint8_t* w, const uint8_t* w2, int n, int k, const float* x,
+              float* out) {
+  constexpr int NM = EPI == 2 ? 2 : 1;
+  const float* wf = (const float*)w;
+  const float* w2f = (const float*)w2;
+#define MTG_F32_GEMM(SEG)                                                                                    \
+  {                                                                                                          \
+    constexpr int NR = f32_nr(NM, SEG);                                                                      \
+    const int blocks = std::min(((n + NR - 1) / NR + 3) / 4, 4 * kLmWorkgroups);                             \
+    hipLaunchKernelGGL((k_gemm_f32<EPI, SEG, NR>), dim3(blocks), dim3(256), 0, s, desc, wf, w2f, n, x, out); \
+  }
+  if (k == 1024) MTG_F32_GEMM(16)
+  else if (k == 2048) MTG_F32_GEMM(32)
+  else MTG_F32_GEMM(48)
+#undef MTG_F32_GEMM
+}
+
 // weight rows per wave and group of the f16 GEMM (NM * NR * 16 partial rows of LDS per wave)
 constexpr int f16_nr(int epi, int seg) { return seg == 16 ? (epi == 2 ? 3 : 4) : 1; }
 // at most one workgroup per CU (its LDS admits no second): more groups go to the
@@ -1489,7 +1655,7 @@ hipError_t prepare_kernels_wt() {
 }
 
 bool wt_shape_supported(int wtype, int k) {
-  if (wtype == MTG_TYPE_F16) return k == 1024 || k == 2048 || k == 3072;
+  if (wtype == MTG_TYPE_F16 || wtype == MTG_TYPE_F32) return k == 1024 || k == 2048 || k == 3072;
   if (wtype == MTG_TYPE_Q4_K) return k % 256 == 0;
   return false;
 }
@@ -1498,7 +1664,11 @@ void launch_act_wt(hipStream_t s, int wtype, const StepDesc* desc, const float* 
                    const float* gain, float eps, const WtAct& act, float* normed_out) {
   const dim3 grid(kMaxRows, K / 256);
   if (wtype == MTG_TYPE_F16)
-    hipLaunchKernelGGL(k_act_f16, grid, dim3(256), 0, s, desc, src, K, gain, eps, act.f16h, normed_out);
+    hipLaunchKernelGGL(k_act_f16<false>, grid, dim3(256), 0, s, desc, src, K, gain, eps, act.f16h, nullptr,
+                       normed_out);
+  else if (wtype == MTG_TYPE_F32)
+    hipLaunchKernelGGL(k_act_f16<true>, grid, dim3(256), 0, s, desc, src, K, gain, eps, nullptr, act.f32,
+                       normed_out);
   else
     hipLaunchKernelGGL(k_act_q8k, grid, dim3(256), 0, s, desc, src, K, gain, eps, act.q8k, normed_out);
 }
@@ -1507,8 +1677,11 @@ void launch_attn_combine_wt(hipStream_t s, int wtype, const StepDesc* desc, Attn
                             int max_chunks, const WtAct& act) {
   const dim3 grid(n_heads / 2, kMaxRows), block(256 * kCombSeg);
   if (wtype == MTG_TYPE_F16)
-    hipLaunchKernelGGL(k_attn_combine_f16q, dim3(n_heads / 2, kMaxRows, kHeadDim / kCombDq), dim3(64 * kCombSeg), 0,
-                       s, desc, work, n_heads, max_chunks, act);
+    hipLaunchKernelGGL(k_attn_combine_f16q<false>, dim3(n_heads / 2, kMaxRows, kHeadDim / kCombDq),
+                       dim3(64 * kCombSeg), 0, s, desc, work, n_heads, max_chunks, act);
+  else if (wtype == MTG_TYPE_F32)
+    hipLaunchKernelGGL(k_attn_combine_f16q<true>, dim3(n_heads / 2, kMaxRows, kHeadDim / kCombDq),
+                       dim3(64 * kCombSeg), 0, s, desc, work, n_heads, max_chunks, act);
   else
     hipLaunchKernelGGL(k_attn_combine_wt<MTG_TYPE_Q4_K>, grid, block, 0, s, desc, work, n_heads, max_chunks, act);
 }
@@ -1525,6 +1698,10 @@ void launch_gemm_wt(hipStream_t s, int wtype, int epi, const StepDesc* desc, con
     if (epi == 0) gemm_wt<MTG_TYPE_F16, 0>(s, desc, w, w2, n, k, act, out);
     else if (epi == 1) gemm_wt<MTG_TYPE_F16, 1>(s, desc, w, w2, n, k, act, out);
     else gemm_wt<MTG_TYPE_F16, 2>(s, desc, w, w2, n, k, act, out);
+  } else if (wtype == MTG_TYPE_F32) {
+    if (epi == 0) gemm_f32<0>(s, desc, w, w2, n, k, act.f32, out);
+    else if (epi == 1) gemm_f32<1>(s, desc, w, w2, n, k, act.f32, out);
+    else gemm_f32<2>(s, desc, w, w2, n, k, act.f32, out);
   } else {
     if (epi == 0) gemm_wt<MTG_TYPE_Q4_K, 0>(s, desc, w, w2, n, k, act, out);
     else if (epi == 1) gemm_wt<MTG_TYPE_Q4_K, 1>(s, desc, w, w2, n, k, act, out);
@@ -1539,7 +1716,18 @@ void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uin
     hipLaunchKernelGGL((k_lm_head_f16<kF16LmNWV, kF16LmNR>), dim3(kF16LmBlocks), dim3(64 * kF16LmNWV),
                        f16_lds_bytes(1024, kF16LmNR, kF16LmNWV), s, desc, w, vocab, act.f16h,
                        bitmap, logits, part_keys);
-  else if (k == 1024 && vocab % 16 == 0)
+  else if (wtype == MTG_TYPE_F32) {
+    const float* wf = (const float*)w;
+    if (k == 1024)
+      hipLaunchKernelGGL((k_lm_head_f32<16, 4>), grid, block, 0, s, desc, wf, vocab, act.f32, bitmap, logits,
+                         part_keys);
+    else if (k == 2048)
+      hipLaunchKernelGGL((k_lm_head_f32<32, 2>), grid, block, 0, s, desc, wf, vocab, act.f32, bitmap, logits,
+                         part_keys);
+    else
+      hipLaunchKernelGGL((k_lm_head_f32<48, 1>), grid, block, 0, s, desc, wf, vocab, act.f32, bitmap, logits,
+                         part_keys);
+  } else if (k == 1024 && vocab % 16 == 0)
     hipLaunchKernelGGL(k_lm_head_q4m<4>, grid, block, q4m_lds_bytes(k), s, desc, w, vocab, act.q8k, bitmap, logits,
                        part_keys);
   else if (k <= kQ4MaxK)
@@ -1554,6 +1742,8 @@ void launch_embed_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8
                      const float* host_rows, float* x) {
   if (wtype == MTG_TYPE_F16)
     hipLaunchKernelGGL(k_embed_wt<MTG_TYPE_F16>, dim3(kMaxRows), dim3(256), 0, s, desc, w, hidden, host_rows, x);
+  else if (wtype == MTG_TYPE_F32)
+    hipLaunchKernelGGL(k_embed_wt<MTG_TYPE_F32>, dim3(kMaxRows), dim3(256), 0, s, desc, w, hidden, host_rows, x);
   else
     hipLaunchKernelGGL(k_embed_wt<MTG_TYPE_Q4_K>, dim3(kMaxRows), dim3(256), 0, s, desc, w, hidden, host_rows, x);
 }

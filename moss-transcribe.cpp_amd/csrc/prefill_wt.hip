@@ -11,6 +11,8 @@
 // with prefill.hip's q/k norm + RoPE + KV append and causal attention (its f32
 // output variant) in between. Outputs equal the oracle's and the verify path's
 // bit for bit (the same orders as the per-op kernels of kernels_wt.hip).
+#include <type_traits>
+
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -26,7 +28,7 @@ using namespace dev;
 template <int WT>
 __global__ void __launch_bounds__(256)
 k_pf_act_wt(const float* __restrict__ src, int S, int K, const float* __restrict__ gain, float eps,
-            uint16_t* __restrict__ f16_out, ActQ8K a) {
+            uint16_t* __restrict__ f16_out, ActQ8K a, float* __restrict__ f32_out) {
   const int t = blockIdx.x, b = blockIdx.y, k = b * 256 + threadIdx.x;
   if (t >= S) return;
   const float* xr = src + (size_t)t * K;
@@ -43,6 +45,8 @@ k_pf_act_wt(const float* __restrict__ src, int S, int K, const float* __restrict
   }
   if constexpr (WT == MTG_TYPE_F16) {
     f16_out[(size_t)t * K + k] = __half_as_ushort(__float2half_rn(y));  // vec_dot_type F16
+  } else if constexpr (WT == MTG_TYPE_F32) {
+    f32_out[(size_t)t * K + k] = y;  // vec_dot_type F32: the row as it is
   } else {
     q8k_block256(y, a, t, K, b);
   }
@@ -81,7 +85,7 @@ __device__ __forceinline__ void pf_store4(int epi, float* out, int N, int t, int
   *(v4f*)dst = o;
 }
 
-// ------------------------------------------------------------- f16 GEMM ----
+// ------------------------------------------------------- f16 / f32 GEMM ----
 // out[s][n] for 64 weight rows x 64 activation rows per workgroup (wave w: the
 // 16-row tile 4 blockIdx.x + w; for the SwiGLU epilogue waves 0, 1 take gate rows
 // 32 blockIdx.x + 16 w and waves 2, 3 the same rows of up, meeting in LDS).
@@ -97,20 +101,28 @@ __device__ __forceinline__ void pf_store4(int epi, float* out, int N, int t, int
 // Every segment's weight and activation rows are staged in LDS as f32 (row stride
 // L + 4 floats: the operand reads of a wave hit 64 distinct banks), the next
 // segment's rows already in flight in registers.
+// F32: f32 weights and activations (vec_dot_type F32), the same segments, MFMA
+// chains and tree: each step of a segment's chain is one fma of two f32 values,
+// as the oracle's mul_mat_f32 and the per-op k_gemm_f32 take it.
 __device__ __forceinline__ int bitrev6(int k) { return (int)(__builtin_bitreverse32((uint32_t)k) >> 26); }
 
-template <bool GLU, int L>
+template <bool GLU, int L, bool F32 = false>
 __global__ void __launch_bounds__(256)
-k_pf_gemm_f16(const uint16_t* __restrict__ w, const uint16_t* __restrict__ w2, int N,
-              const uint16_t* __restrict__ x, int S, float* __restrict__ out, int epi, const float* __restrict__ bias) {
-  constexpr int K = 64 * L, LS = L + 4, NP = L / 8;  // 16-byte pieces (8 halves) per row and segment
+k_pf_gemm_f16(const void* __restrict__ wv, const void* __restrict__ w2v, int N, const void* __restrict__ xv, int S,
+              float* __restrict__ out, int epi, const float* __restrict__ bias) {
+  using E = typename std::conditional<F32, float, uint16_t>::type;
+  constexpr int EP = 16 / (int)sizeof(E);  // elements per 16-byte piece
+  constexpr int K = 64 * L, LS = L + 4, NP = L / EP;  // pieces per row and segment
   constexpr int NPIECE = 2 * 64 * NP, PPT = (NPIECE + 255) / 256;
+  const E* w = (const E*)wv;
+  const E* w2 = (const E*)w2v;
+  const E* x = (const E*)xv;
   __shared__ __align__(16) float s_w[2][64 * LS];
   __shared__ __align__(16) float s_x[2][64 * LS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, kk = lane >> 4;
   const int s0 = blockIdx.y * 64;
   // weight row r (< 64) of the workgroup
-  auto wrow = [&](int r) -> const uint16_t* {
+  auto wrow = [&](int r) -> const E* {
     if constexpr (GLU) return (r < 32 ? w : w2) + (size_t)(32 * blockIdx.x + (r & 31)) * K;
     return w + (size_t)(64 * blockIdx.x + r) * K;
   };
@@ -122,9 +134,9 @@ k_pf_gemm_f16(const uint16_t* __restrict__ w, const uint16_t* __restrict__ w2, i
       if (p < NPIECE) {
         const int half = p / (64 * NP), q = p % (64 * NP), r = q / NP, j = q % NP;
         if (half == 0)
-          reg[i] = *(const uint4*)(wrow(r) + seg * L + 8 * j);
+          reg[i] = *(const uint4*)(wrow(r) + seg * L + EP * j);
         else
-          reg[i] = s0 + r < S ? *(const uint4*)(x + (size_t)(s0 + r) * K + seg * L + 8 * j) : make_uint4(0, 0, 0, 0);
+          reg[i] = s0 + r < S ? *(const uint4*)(x + (size_t)(s0 + r) * K + seg * L + EP * j) : make_uint4(0, 0, 0, 0);
       }
     }
   };
@@ -134,8 +146,12 @@ k_pf_gemm_f16(const uint16_t* __restrict__ w, const uint16_t* __restrict__ w2, i
       const int p = tid + 256 * i;
       if (p < NPIECE) {
         const int half = p / (64 * NP), q = p % (64 * NP), r = q / NP, j = q % NP;
-        float* dst = (half ? s_x[buf] : s_w[buf]) + r * LS + 8 * j;
+        float* dst = (half ? s_x[buf] : s_w[buf]) + r * LS + EP * j;
         const uint32_t u[4] = {reg[i].x, reg[i].y, reg[i].z, reg[i].w};
+        if constexpr (F32) {
+          *(v4f*)dst = v4f{__uint_as_float(u[0]), __uint_as_float(u[1]), __uint_as_float(u[2]), __uint_as_float(u[3])};
+          continue;
+        }
         v4f lo, hi;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -376,9 +392,14 @@ void launch_pf_act_wt(hipStream_t s, int wtype, const float* src, int S, int K, 
                       const WtAct& act) {
   const dim3 grid((unsigned)S, (unsigned)(K / 256));
   if (wtype == MTG_TYPE_F16)
-    hipLaunchKernelGGL(k_pf_act_wt<MTG_TYPE_F16>, grid, dim3(256), 0, s, src, S, K, gain, eps, act.f16h, act.q8k);
+    hipLaunchKernelGGL(k_pf_act_wt<MTG_TYPE_F16>, grid, dim3(256), 0, s, src, S, K, gain, eps, act.f16h, act.q8k,
+                       act.f32);
+  else if (wtype == MTG_TYPE_F32)
+    hipLaunchKernelGGL(k_pf_act_wt<MTG_TYPE_F32>, grid, dim3(256), 0, s, src, S, K, gain, eps, act.f16h, act.q8k,
+                       act.f32);
   else
-    hipLaunchKernelGGL(k_pf_act_wt<MTG_TYPE_Q4_K>, grid, dim3(256), 0, s, src, S, K, gain, eps, act.f16h, act.q8k);
+    hipLaunchKernelGGL(k_pf_act_wt<MTG_TYPE_Q4_K>, grid, dim3(256), 0, s, src, S, K, gain, eps, act.f16h, act.q8k,
+                       act.f32);
 }
 
 void launch_pf_gemm_wt(hipStream_t s, int wtype, int epi, const uint8_t* w, const uint8_t* w2, int N, int K,
@@ -392,10 +413,13 @@ void launch_pf_gemm_wt(hipStream_t s, int wtype, int epi, const uint8_t* w, cons
       hipLaunchKernelGGL(k_pf_gemm_q4k<false>, grid, dim3(256), 0, s, w, w2, N, K, act.q8k, S, out, epi, bias);
     return;
   }
-  const uint16_t* wh = (const uint16_t*)w;
-  const uint16_t* w2h = (const uint16_t*)w2;
-#define MTG_PF_F16(G, L) \
-  hipLaunchKernelGGL((k_pf_gemm_f16<G, L>), grid, dim3(256), 0, s, wh, w2h, N, act.f16h, S, out, epi, bias)
+  const bool f32 = wtype == MTG_TYPE_F32;
+  const void* xa = f32 ? (const void*)act.f32 : (const void*)act.f16h;
+#define MTG_PF_F16(G, L)                                                                                       \
+  if (f32)                                                                                                     \
+    hipLaunchKernelGGL((k_pf_gemm_f16<G, L, true>), grid, dim3(256), 0, s, w, w2, N, xa, S, out, epi, bias); \
+  else                                                                                                         \
+    hipLaunchKernelGGL((k_pf_gemm_f16<G, L, false>), grid, dim3(256), 0, s, w, w2, N, xa, S, out, epi, bias)
 #define MTG_PF_F16_K(G)                        \
   switch (K) {                                 \
     case 1024: MTG_PF_F16(G, 16); break;       \

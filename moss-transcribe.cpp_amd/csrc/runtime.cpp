@@ -83,6 +83,7 @@ int Ctx::upload_q8(const void* blocks, int n, int k, uint8_t* dst, uint8_t* stag
 size_t Ctx::weight_bytes(int n, int k) const {
   if (wtype == MTG_TYPE_Q8_0) return q8_tiles_bytes(n, k);
   if (wtype == MTG_TYPE_F16) return (size_t)n * k * 2;
+  if (wtype == MTG_TYPE_F32) return (size_t)n * k * 4;
   return (size_t)n * (k / 256) * 144;  // q4_K
 }
 
@@ -98,11 +99,11 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
   const int H = hp.hidden, D = hp.head_dim, NH = hp.n_heads, NKV = hp.n_kv_heads;
   const int QN = NH * D, KN = NKV * D, F = hp.intermediate, L = hp.n_layers, V = hp.vocab;
   wtype = d->weight_type;
-  if (wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16 && wtype != MTG_TYPE_Q4_K)
+  if (wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16 && wtype != MTG_TYPE_F32 && wtype != MTG_TYPE_Q4_K)
     return fail(MTG_ERR_UNSUPPORTED, "weight type %d is not supported by this build", wtype);
   if (wtype != MTG_TYPE_Q8_0 && (!wt_shape_supported(wtype, H) || !wt_shape_supported(wtype, QN) ||
                                  !wt_shape_supported(wtype, F)))
-    return fail(MTG_ERR_UNSUPPORTED, "shape not supported for weight type %d (f16: K of 1024, 2048 or "
+    return fail(MTG_ERR_UNSUPPORTED, "shape not supported for weight type %d (f16, f32: K of 1024, 2048 or "
                 "3072; q4_K: K a multiple of 256)", wtype);
   if (kv_type != MTG_TYPE_F32 && kv_type != MTG_TYPE_F16)
     return fail(MTG_ERR_UNSUPPORTED, "kv type %d", kv_type);
@@ -224,7 +225,8 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
     wact.q8k.qs = (int8_t*)dalloc((size_t)R * KM, true);
     wact.q8k.d = (float*)dalloc((size_t)R * (KM / 256 + 1) * 4, true);
     wact.q8k.bsums = (int32_t*)dalloc((size_t)R * (KM / 16) * 4, true);
-    if (!wact.f16h || !wact.q8k.qs || !wact.q8k.d || !wact.q8k.bsums)
+    wact.f32 = (float*)dalloc((size_t)R * KM * 4, true);
+    if (!wact.f16h || !wact.q8k.qs || !wact.q8k.d || !wact.q8k.bsums || !wact.f32)
       return fail(MTG_ERR_NOMEM, "activation buffers");
   }
   const size_t chunks = (size_t)NKV * ((max_seq + kChunkKeys - 1) / kChunkKeys);
@@ -397,10 +399,12 @@ void Ctx::enqueue_wt(int mode) {
         launch_act_wt(s, wtype, desc_dev, x, H, y.ffn_norm, eps, wact, nullptr);
         launch_gemm_wt(s, wtype, 2, desc_dev, y.wg, y.wu, F, H, wact, act);
       }
-      if (wtype == MTG_TYPE_F16) {
-        // the f16 gate/up GEMM leaves the SwiGLU rows as f16 in act's memory
+      if (wtype == MTG_TYPE_F16 || wtype == MTG_TYPE_F32) {
+        // the f16 gate/up GEMM leaves the SwiGLU rows as f16 in act's memory, the
+        // f32 one as the f32 rows the down projection takes as they are
         WtAct down_in = wact;
         down_in.f16h = (uint16_t*)act;
+        down_in.f32 = act;
         launch_gemm_wt(s, wtype, 1, desc_dev, y.wd, nullptr, H, F, down_in, x);
       } else {
         launch_act_wt(s, wtype, desc_dev, act, F, nullptr, eps, wact, nullptr);
@@ -692,16 +696,18 @@ int Ctx::prefill_blocks_wt(const float* embeds, int S, float* hidden_out) {
   }
   if (!pf.o) {
     pf.o = (float*)dalloc((size_t)R * QN * 4, false);
+    bool ok = true;
     if (wtype == MTG_TYPE_F16) {
-      pf.wact.f16h = (uint16_t*)dalloc((size_t)R * KM * 2, false);
+      ok = (pf.wact.f16h = (uint16_t*)dalloc((size_t)R * KM * 2, false)) != nullptr;
+    } else if (wtype == MTG_TYPE_F32) {
+      ok = (pf.wact.f32 = (float*)dalloc((size_t)R * KM * 4, false)) != nullptr;
     } else {
       pf.wact.q8k.qs = (int8_t*)dalloc((size_t)R * KM, false);
       pf.wact.q8k.d = (float*)dalloc((size_t)R * (KM / 256) * 4, false);
       pf.wact.q8k.bsums = (int32_t*)dalloc((size_t)R * (KM / 16) * 4, false);
+      ok = pf.wact.q8k.qs && pf.wact.q8k.d && pf.wact.q8k.bsums;
     }
-    if (!pf.o || (wtype == MTG_TYPE_F16 ? !pf.wact.f16h
-                                        : (!pf.wact.q8k.qs || !pf.wact.q8k.d || !pf.wact.q8k.bsums)))
-      return fail(MTG_ERR_NOMEM, "prefill buffers");
+    if (!pf.o || !ok) return fail(MTG_ERR_NOMEM, "prefill buffers");
   }
   hipStream_t s = stream;
   int rc = MTG_OK;

@@ -239,6 +239,7 @@ const void* make_matrix(mtg_synth_model& m, int type, int64_t k, int64_t n, uint
     uint8_t* dst = base + rb * (size_t)r;
     if (type == MTG_TYPE_Q8_0) mtg_quantize_q8_0_weight(row.data(), k, dst);
     else if (type == MTG_TYPE_Q4_K) mtg_quantize_q4_k(row.data(), k, dst);
+    else if (type == MTG_TYPE_F32) std::memcpy(dst, row.data(), (size_t)k * 4);
     else {
       uint16_t* h = (uint16_t*)dst;
       for (int64_t i = 0; i < k; ++i) h[i] = mtg_f32_to_f16(row[i]);
@@ -261,7 +262,8 @@ extern "C" {
 int mtg_synth_create(const mtg_hparams* hp, int32_t weight_type, uint64_t seed, float std,
                      float gain_jitter, mtg_synth_model** out) {
   if (!hp || !out) return MTG_ERR_INVALID;
-  if (weight_type != MTG_TYPE_Q8_0 && weight_type != MTG_TYPE_F16 && weight_type != MTG_TYPE_Q4_K)
+  if (weight_type != MTG_TYPE_Q8_0 && weight_type != MTG_TYPE_F16 && weight_type != MTG_TYPE_F32 &&
+      weight_type != MTG_TYPE_Q4_K)
     return MTG_ERR_UNSUPPORTED;
   const int64_t H = hp->hidden, D = hp->head_dim, QN = (int64_t)hp->n_heads * D,
                 KN = (int64_t)hp->n_kv_heads * D, F = hp->intermediate;

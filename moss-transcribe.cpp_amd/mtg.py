@@ -657,6 +657,8 @@ class SynthEncoder:
         x = (self._normal(n * k) * np.float32(std)).astype(np.float32)
         if self.wtype == TYPE_F16:
             blocks = x.astype(np.float16).view(np.uint8)
+        elif self.wtype == TYPE_F32:
+            blocks = x.view(np.uint8)
         elif self.wtype == TYPE_Q4_K:
             blocks = np.empty(n * (k // 256) * 144, np.uint8)
             lib().mtg_quantize_q4_k(ptr(x), n * k, ptr(blocks))

@@ -21,7 +21,7 @@ CONFIGS = {
 }
 AUDIO_ROWS = 375
 STREAM_PERIOD = 37
-WNAME = {mtg.TYPE_Q8_0: "q8_0", mtg.TYPE_F16: "f16", mtg.TYPE_Q4_K: "q4_K"}
+WNAME = {mtg.TYPE_Q8_0: "q8_0", mtg.TYPE_F16: "f16", mtg.TYPE_F32: "f32", mtg.TYPE_Q4_K: "q4_K"}
 
 
 def prompt_rows(cfg):

@@ -321,6 +321,27 @@ void mul_mat_f16(const uint16_t* w, int k, int n, const float* x, int T, float* 
   }
 }
 
+// mul_mat(f32 W, f32 x): vec_dot_type F32, x as it is (ggml vec_dot_f32).
+// Canonical order: the f16 one's segments and butterfly, each segment an fma
+// chain from 0 (every step rounds once: fma(w, x, acc)).
+void mul_mat_f32(const float* w, int k, int n, const float* x, int T, float* y) {
+  const int seg = k / 64;
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < n; ++r) {
+    const float* wr = w + (size_t)r * k;
+    for (int t = 0; t < T; ++t) {
+      const float* xr = x + (size_t)t * k;
+      float part[64];
+      for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (int e = 0; e < seg; ++e) acc = std::fma(wr[l * seg + e], xr[l * seg + e], acc);
+        part[l] = acc;
+      }
+      y[(size_t)t * n + r] = butterfly64(part);
+    }
+  }
+}
+
 // mul_mat(q4_K W, f32 x): x quantized to q8_K; per 256-superblock exact int32
 // sums sum_j sc_j * dot_j and sum_j mn_j * bsum_j, combined as
 // (d_w*d_x)*dot - (dmin_w*d_x)*min.
@@ -361,6 +382,7 @@ void mul_mat_q4k(const BlockQ4K* w, int k, int n, const float* x, int T, float* 
 void mul_mat(int wtype, const void* w, int k, int n, const float* x, int T, float* y) {
   if (wtype == MTG_TYPE_Q8_0) mul_mat_q8((const BlockQ8*)w, k, n, x, T, y);
   else if (wtype == MTG_TYPE_F16) mul_mat_f16((const uint16_t*)w, k, n, x, T, y);
+  else if (wtype == MTG_TYPE_F32) mul_mat_f32((const float*)w, k, n, x, T, y);
   else mul_mat_q4k((const BlockQ4K*)w, k, n, x, T, y);
 }
 
@@ -484,9 +506,24 @@ void mul_mat_q4k_generic(const BlockQ4K* w, int k, int n, const float* x, int T,
   }
 }
 
+// ggml_vec_dot_f32 (generic): sum of (double)(w * x) in order.
+void mul_mat_f32_generic(const float* w, int k, int n, const float* x, int T, float* y) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < n; ++r) {
+    const float* wr = w + (size_t)r * k;
+    for (int t = 0; t < T; ++t) {
+      const float* xr = x + (size_t)t * k;
+      double sumf = 0.0;
+      for (int i = 0; i < k; ++i) sumf += (double)(wr[i] * xr[i]);
+      y[(size_t)t * n + r] = (float)sumf;
+    }
+  }
+}
+
 void mul_mat_generic(int wtype, const void* w, int k, int n, const float* x, int T, float* y) {
   if (wtype == MTG_TYPE_Q8_0) mul_mat_q8_generic((const BlockQ8*)w, k, n, x, T, y);
   else if (wtype == MTG_TYPE_F16) mul_mat_f16_generic((const uint16_t*)w, k, n, x, T, y);
+  else if (wtype == MTG_TYPE_F32) mul_mat_f32_generic((const float*)w, k, n, x, T, y);
   else mul_mat_q4k_generic((const BlockQ4K*)w, k, n, x, T, y);
 }
 
@@ -593,6 +630,8 @@ void embed_row(const orc_model& m, int32_t id, float* out) {
   } else if (m.wtype == MTG_TYPE_F16) {
     const uint16_t* h = (const uint16_t*)row;
     for (int i = 0; i < H; ++i) out[i] = h2f(h[i]);
+  } else if (m.wtype == MTG_TYPE_F32) {
+    std::memcpy(out, row, (size_t)H * 4);
   } else {
     const BlockQ4K* b = (const BlockQ4K*)row;
     for (int sb = 0; sb < H / 256; ++sb) {
@@ -1354,7 +1393,10 @@ struct EncLayer {
 std::vector<float> copy_f(const float* p, size_t n) { return std::vector<float>(p, p + n); }
 // the bytes of an n x k matrix of wtype (ggml block layouts)
 std::vector<uint8_t> copy_w(int wtype, const void* p, size_t n, size_t k) {
-  const size_t row = wtype == MTG_TYPE_F16 ? k * 2 : wtype == MTG_TYPE_Q4_K ? k / 256 * 144 : k / 32 * 34;
+  const size_t row = wtype == MTG_TYPE_F16   ? k * 2
+                     : wtype == MTG_TYPE_F32  ? k * 4
+                     : wtype == MTG_TYPE_Q4_K ? k / 256 * 144
+                                              : k / 32 * 34;
   const uint8_t* b = (const uint8_t*)p;
   return std::vector<uint8_t>(b, b + n * row);
 }
@@ -1389,7 +1431,7 @@ void orc_enc_attention(const float* q, const float* k, const float* v, int32_t T
 int orc_encoder_create(const mtg_encoder_desc* d, orc_encoder** out) {
   if (!d || !out) return MTG_ERR_INVALID;
   const int wt = d->weight_type;
-  if (wt != MTG_TYPE_Q8_0 && wt != MTG_TYPE_F16 && wt != MTG_TYPE_Q4_K) return MTG_ERR_INVALID;
+  if (wt != MTG_TYPE_Q8_0 && wt != MTG_TYPE_F16 && wt != MTG_TYPE_F32 && wt != MTG_TYPE_Q4_K) return MTG_ERR_INVALID;
   const mtg_encoder_hparams& hp = d->hp;
   const size_t D = hp.d_model, F = hp.ffn, M = hp.n_mels, R = (size_t)(hp.n_frames - 1) / 2 + 1;
   auto e = std::make_unique<orc_encoder>();

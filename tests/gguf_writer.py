@@ -123,7 +123,7 @@ def encoder_tensors(syn):
     h, d = syn.hp, syn.desc
     D, F, M, H, IN = h.d_model, h.ffn, h.n_mels, h.hidden, h.d_model * h.merge
     R = syn.rows
-    wt = getattr(syn, "wtype", mtg.TYPE_Q8_0)  # the matrices' type (q8_0, f16 or q4_K)
+    wt = getattr(syn, "wtype", mtg.TYPE_Q8_0)  # the matrices' type (q8_0, f16, f32 or q4_K)
     rb = lambda k: mtg.lib().mtg_row_bytes(wt, k)
 
     def f32(p, ne):

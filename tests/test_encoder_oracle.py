@@ -133,7 +133,7 @@ def _act_q8k(x):
 
 def _weights(wtype, addr, n, k):
     """A matrix of the synthetic encoder: q8_0 as (codes, scales) for the exact
-    block dots, f16 and q4_K dequantized to float64 by the library's decoder."""
+    block dots, f16, f32 and q4_K dequantized to float64 by the library's decoder."""
     if wtype == mtg.TYPE_Q8_0:
         return wtype, _q8(addr, n, k)
     nbytes = mtg.lib().mtg_row_bytes(wtype, k) * n
@@ -153,6 +153,8 @@ def _linear(W, b, x):
         y = np.einsum("tnb,nb,tb->tn", dots, dw[:, :, 0], dx[:, :, 0])
     elif wtype == mtg.TYPE_F16:
         y = x.astype(np.float32).astype(np.float16).astype(np.float64) @ m.T  # vec_dot_type F16
+    elif wtype == mtg.TYPE_F32:
+        y = x.astype(np.float32).astype(np.float64) @ m.T  # vec_dot_type F32
     else:
         y = _act_q8k(x) @ m.T
     return y if b is None else y + b
@@ -224,10 +226,10 @@ def _rel_rms(a, b):
 # within float32 rounding of a rounding boundary: a code that flips between the
 # float32 and the float64 evaluation moves a row by one quantization step, and
 # attention spreads it to every row (another seed's second layer shows 2e-3).
-ENC_CASES = [(mtg.TYPE_Q8_0, 5, 128), (mtg.TYPE_F16, 6, 256), (mtg.TYPE_Q4_K, 6, 256)]
+ENC_CASES = [(mtg.TYPE_Q8_0, 5, 128), (mtg.TYPE_F16, 6, 256), (mtg.TYPE_F32, 6, 256), (mtg.TYPE_Q4_K, 6, 256)]
 
 
-@pytest.mark.parametrize("wtype,seed,d", ENC_CASES, ids=["q8_0", "f16", "q4_K"])
+@pytest.mark.parametrize("wtype,seed,d", ENC_CASES, ids=["q8_0", "f16", "f32", "q4_K"])
 def test_small_encoder_and_adaptor_match_float64(wtype, seed, d):
     syn = mtg.SynthEncoder(seed=seed, wtype=wtype, n_mels=16, n_frames=96, d_model=d, n_layers=2,
                            n_heads=d // 64, ffn=2 * d, merge=4, hidden=d)

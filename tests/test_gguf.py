@@ -16,7 +16,7 @@ import gguf_writer
 import mtg
 
 
-@pytest.fixture(scope="module", params=[mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_Q4_K], ids=["q8_0", "f16", "q4_K"])
+@pytest.fixture(scope="module", params=[mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_F32, mtg.TYPE_Q4_K], ids=["q8_0", "f16", "f32", "q4_K"])
 def model(request):
     m = mtg.SynthModel(request.param, seed=7, std=0.02, gain_jitter=0.05, n_layers=2, vocab=2048)
     yield m
@@ -224,10 +224,10 @@ def test_encoder_tensors_round_trip(tmp_path):
     m.close()
 
 
-@pytest.mark.parametrize("wtype", [mtg.TYPE_F16, mtg.TYPE_Q4_K], ids=["f16", "q4_K"])
-def test_encoder_f16_and_q4k_round_trip(tmp_path, wtype):
-    """An encoder whose matrices are f16 (the converter's f16 dtype) or q4_K (cli
-    quantize q4_k): the description carries the type and every tensor byte for
+@pytest.mark.parametrize("wtype", [mtg.TYPE_F16, mtg.TYPE_F32, mtg.TYPE_Q4_K], ids=["f16", "f32", "q4_K"])
+def test_encoder_f16_f32_and_q4k_round_trip(tmp_path, wtype):
+    """An encoder whose matrices are f16 or f32 (the converter's f16 and default f32
+    dtypes) or q4_K (cli quantize q4_k): the description carries the type and every tensor byte for
     byte; a q8_0 matrix among them is refused by name."""
     syn = mtg.SynthEncoder(seed=4, wtype=wtype, n_mels=16, n_frames=96, d_model=256, n_layers=2, n_heads=4,
                            ffn=512, merge=4, hidden=256)

@@ -26,8 +26,8 @@ def _same(got, ref, what):
                          % (what, int((got != ref).sum()), err.max(), np.unravel_index(err.argmax(), err.shape)))
 
 
-WTYPES = [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_Q4_K]
-WT_IDS = ["q8_0", "f16", "q4_K"]
+WTYPES = [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_F32, mtg.TYPE_Q4_K]
+WT_IDS = ["q8_0", "f16", "f32", "q4_K"]
 
 
 @pytest.mark.parametrize("wtype", WTYPES, ids=WT_IDS)

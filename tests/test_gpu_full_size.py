@@ -25,6 +25,8 @@ CASES = [
     ("q8_0-f32kv-T8-ctx1600-graph", mtg.TYPE_Q8_0, mtg.TYPE_F32, 8, 1600, mtg.EXEC_GRAPH),
     ("f16-f16kv-T8-ctx8000-graph", mtg.TYPE_F16, mtg.TYPE_F16, 8, 8000, mtg.EXEC_GRAPH),
     ("q4_K-f16kv-T16-ctx16384-graph", mtg.TYPE_Q4_K, mtg.TYPE_F16, 16, 16384, mtg.EXEC_GRAPH),
+    # the converter's default dtype: every matrix f32 (2.4 GB of weights)
+    ("f32-f32kv-T8-ctx1600-graph", mtg.TYPE_F32, mtg.TYPE_F32, 8, 1600, mtg.EXEC_GRAPH),
 ]
 
 

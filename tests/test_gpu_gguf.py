@@ -67,7 +67,7 @@ def _compare_with_oracle(path, kv_type, prefix, T, hp_ref):
 
 
 @pytest.mark.parametrize("kv_type", [mtg.TYPE_F32, mtg.TYPE_F16], ids=["f32kv", "f16kv"])
-@pytest.mark.parametrize("wtype", [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_Q4_K], ids=["q8_0", "f16", "q4_K"])
+@pytest.mark.parametrize("wtype", [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_F32, mtg.TYPE_Q4_K], ids=["q8_0", "f16", "f32", "q4_K"])
 def test_decoder_from_gguf_matches_oracle(wtype, kv_type, tmp_path):
     print("decoder from a GGUF file against the oracle: weight type %d kv %d" % (wtype, kv_type), flush=True)
     _threads()
@@ -115,7 +115,7 @@ class _ParsedEncoder:
         self.rows = (self.hp.n_frames - 1) // 2 + 1
 
 
-@pytest.mark.parametrize("wtype", [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_Q4_K], ids=["q8_0", "f16", "q4_K"])
+@pytest.mark.parametrize("wtype", [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_F32, mtg.TYPE_Q4_K], ids=["q8_0", "f16", "f32", "q4_K"])
 def test_encoder_from_gguf_matches_oracle(tmp_path, wtype):
     syn = mtg.SynthEncoder(seed=31, wtype=wtype, n_frames=160, n_layers=2, ffn=2048)
     path = str(tmp_path / "enc.gguf")

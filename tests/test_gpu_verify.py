@@ -170,15 +170,15 @@ def test_generated_token_stream_matches_oracle(penalty):
     assert dec.past_len == orc.past_len
 
 
-WTYPES = [mtg.TYPE_F16, mtg.TYPE_Q4_K]
-WT_NAMES = {mtg.TYPE_F16: "f16", mtg.TYPE_Q4_K: "q4_K"}
+WTYPES = [mtg.TYPE_F16, mtg.TYPE_F32, mtg.TYPE_Q4_K]
+WT_NAMES = {mtg.TYPE_F16: "f16", mtg.TYPE_F32: "f32", mtg.TYPE_Q4_K: "q4_K"}
 WT_EXECS = [mtg.EXEC_GRAPH, mtg.EXEC_EAGER]  # the persistent kernel streams q8_0 only
 
 
 @pytest.mark.parametrize("exec_mode", WT_EXECS, ids=lambda e: EXEC_NAMES[e])
 @pytest.mark.parametrize("wtype", WTYPES, ids=lambda w: WT_NAMES[w])
-def test_f16_and_q4k_weights_verify_matches_oracle(wtype, exec_mode):
-    """f16 and q4_K weights (the non-quantized path and the k-quant path): hidden
+def test_f16_f32_and_q4k_weights_verify_matches_oracle(wtype, exec_mode):
+    """f16, f32 and q4_K weights (the converter's dtypes and the k-quant path): hidden
     rows, logits, choices, acceptance and the appended KV equal the oracle's, for
     T = 1, 8, 16 in a row, with an f16 KV cache."""
     print("weights %s parity: exec=%s" % (WT_NAMES[wtype], EXEC_NAMES[exec_mode]), flush=True)

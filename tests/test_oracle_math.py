@@ -154,8 +154,8 @@ def test_q8_0_mul_mat_close_to_float64_of_quantized_operands():
     assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
 
 
-@pytest.mark.parametrize("wtype", [mtg.TYPE_F16, mtg.TYPE_Q4_K])
-def test_f16_and_q4k_mul_mat_close_to_float64_of_quantized_operands(wtype):
+@pytest.mark.parametrize("wtype", [mtg.TYPE_F16, mtg.TYPE_F32, mtg.TYPE_Q4_K])
+def test_f16_f32_and_q4k_mul_mat_close_to_float64_of_quantized_operands(wtype):
     rng = np.random.default_rng(6)
     k, n, T = 1024, 32, 3
     wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
@@ -163,6 +163,8 @@ def test_f16_and_q4k_mul_mat_close_to_float64_of_quantized_operands(wtype):
     raw = np.empty(nb, np.uint8)
     if wtype == mtg.TYPE_F16:
         raw[:] = wf.astype(np.float16).view(np.uint8).reshape(-1)
+    elif wtype == mtg.TYPE_F32:
+        raw[:] = wf.view(np.uint8).reshape(-1)
     else:
         mtg.lib().mtg_quantize_q4_k(mtg.ptr(wf), wf.size, mtg.ptr(raw))
     wq = np.empty((n, k), np.float32)
@@ -171,6 +173,9 @@ def test_f16_and_q4k_mul_mat_close_to_float64_of_quantized_operands(wtype):
     got = oracle_py.mul_mat(wtype, raw, k, n, x).astype(np.float64)
     if wtype == mtg.TYPE_F16:
         xa = x.astype(np.float16).astype(np.float64)  # vec_dot_type F16
+        tol = 1e-5
+    elif wtype == mtg.TYPE_F32:
+        xa = x.astype(np.float64)  # vec_dot_type F32: x as it is
         tol = 1e-5
     else:
         # q8_K activations: 256-blocks, scale max/-127, codes nearest
@@ -184,7 +189,8 @@ def test_f16_and_q4k_mul_mat_close_to_float64_of_quantized_operands(wtype):
     want = xa @ wq.astype(np.float64).T
     assert np.abs(got - want).max() <= tol * np.abs(want).max()
     # the dequantized weights themselves are close to the float input
-    assert np.abs(wq - wf).max() <= (1e-3 if wtype == mtg.TYPE_F16 else 0.25) * np.abs(wf).max()
+    bound = {mtg.TYPE_F16: 1e-3, mtg.TYPE_F32: 0.0}.get(wtype, 0.25)
+    assert np.abs(wq - wf).max() <= bound * np.abs(wf).max()
 
 
 def test_f16_mul_mat_exact_on_small_integers():
@@ -199,6 +205,53 @@ def test_f16_mul_mat_exact_on_small_integers():
         got = oracle_py.mul_mat(mtg.TYPE_F16, w.view(np.uint8).reshape(-1).copy(), k, n, x)
         want = x.astype(np.float64) @ w.astype(np.float64).T
         assert np.array_equal(got.astype(np.float64), want)
+
+
+def test_f32_mul_mat_exact_on_small_integers():
+    """f32 weights: small-integer operands make every fma exact, so the result is
+    the float64 dot bit for bit whatever the order; an element dropped, repeated,
+    misplaced or taken from the wrong operand changes it."""
+    rng = np.random.default_rng(17)
+    for k in (1024, 2048, 3072):
+        n, T = 24, 5
+        w = rng.integers(-64, 65, (n, k)).astype(np.float32)
+        x = rng.integers(-64, 65, (T, k)).astype(np.float32)
+        got = oracle_py.mul_mat(mtg.TYPE_F32, w.view(np.uint8).reshape(-1).copy(), k, n, x)
+        want = x.astype(np.float64) @ w.astype(np.float64).T
+        assert np.array_equal(got.astype(np.float64), want)
+
+
+def _f32_planted(k, cells):
+    """A one-row f32 matrix and activation with w[i] * x[i] planted at the given
+    elements (i: (w, x)), zeros elsewhere."""
+    w = np.zeros((1, k), np.float32)
+    x = np.zeros((1, k), np.float32)
+    for i, (a, b) in cells.items():
+        w[0, i], x[0, i] = a, b
+    return oracle_py.mul_mat(mtg.TYPE_F32, w.view(np.uint8).reshape(-1).copy(), k, 1, x)[0, 0]
+
+
+def test_f32_mul_mat_order_planted():
+    """Planted rows where the candidate orders give different floats:
+    * one fused multiply-add per element: -(1 + 2^-11) then (1 + 2^-12)^2 in one
+      segment gives 2^-24 with fma, 0 with a rounded product then an add;
+    * segments of K/64 consecutive elements: 2^24 and 1 in segment 0 and -2^24 in
+      segment 1 give 0 (2^24 + 1 rounds to 2^24 inside the chain); with elements
+      dealt to the lanes in turn the 1 would meet the cancelled pair last: 1;
+    * the xor butterfly: partials 2^24, 1, -2^24 in segments 0, 1, 2 give 1
+      (segments 0 and 2 meet before segment 1 joins); a sequential sum gives 0."""
+    one = np.float32(1.0)
+    a = np.float32(1.0 + 2.0 ** -12)
+    for k in (1024, 2048, 3072):
+        seg = k // 64
+        assert _f32_planted(k, {0: (one, -np.float32(1.0 + 2.0 ** -11)), 1: (a, a)}) == np.float32(2.0 ** -24)
+        # the same pair in the last segment, at its last two elements
+        assert _f32_planted(k, {k - 2: (one, -np.float32(1.0 + 2.0 ** -11)), k - 1: (a, a)}) == np.float32(2.0 ** -24)
+        big = np.float32(2.0 ** 24)
+        assert _f32_planted(k, {0: (one, big), 1: (one, one), seg: (one, -big)}) == 0.0
+        assert _f32_planted(k, {0: (one, big), seg: (one, one), 2 * seg: (one, -big)}) == 1.0
+        # pairs at distance 32 segments meet first: 2^24 in segment 5, -2^24 in 37, 1 in 4
+        assert _f32_planted(k, {5 * seg: (one, big), 37 * seg: (one, -big), 4 * seg: (one, one)}) == 1.0
 
 
 def test_rms_norm_matches_float64_closed_form():

@@ -54,7 +54,7 @@ def test_generic_order_matches_independent_float64_model():
     m.close()
 
 
-@pytest.mark.parametrize("wtype", [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_Q4_K])
+@pytest.mark.parametrize("wtype", [mtg.TYPE_Q8_0, mtg.TYPE_F16, mtg.TYPE_F32, mtg.TYPE_Q4_K])
 def test_one_gemm_within_contract_at_every_step_shape(wtype):
     rng = np.random.default_rng(61)
     shapes = [(1024, 4096), (2048, 1024), (1024, 3072), (3072, 1024), (1024, 151936)]
@@ -67,6 +67,8 @@ def test_one_gemm_within_contract_at_every_step_shape(wtype):
             mtg.lib().mtg_quantize_q8_0_weight(mtg.ptr(w), w.size, mtg.ptr(raw))
         elif wtype == mtg.TYPE_F16:
             raw[:] = w.astype(np.float16).view(np.uint8).reshape(-1)
+        elif wtype == mtg.TYPE_F32:
+            raw[:] = w.view(np.uint8).reshape(-1)
         else:
             mtg.lib().mtg_quantize_q4_k(mtg.ptr(w), w.size, mtg.ptr(raw))
         x = rng.standard_normal((8, k)).astype(np.float32)
