@@ -709,6 +709,111 @@ void attention_generic(const orc_model& m, int l, const float* q, int T, float* 
     }
 }
 
+// Eager GQA attention of T query rows at positions past .. past + T - 1 over a
+// cache of NKV heads x max_seq positions x D (f32, or f16 bits when f16kv)
+// holding keys [0, past + T): scores K.Q in f32, soft_max_ext(scale 1/sqrt(D),
+// causal mask), context over each query's valid length (src/qwen3.cpp:157-189,
+// src/cpu_context.cpp:13-32). q, o: [T][NH * D]. Canonical order: keys in chunks
+// of 64; score = fma chain over D; per chunk max, p = exp(w - max) (f16-rounded
+// for an f16 cache, whose q is f16-rounded too), l = butterfly sum of p, O = fma
+// chain over the chunk's keys; the chunks merged in order: M = max of the chunk
+// maxima, f = exp(m_c - M), L = fma(l_c, f, L), O = fma(O_c, f, O), out = O / L.
+void attention_canonical(const void* kc, const void* vc, bool f16kv, int max_seq, int past, int T, int NH, int NKV,
+                         int D, const float* q, float* o) {
+  const int QN = NH * D, groups = NH / NKV, kv = past + T;
+  const float scale = 1.0f / std::sqrt((float)D);
+  const int nch = (kv + 63) / 64;
+  const float* k32 = (const float*)kc;
+  const float* v32 = (const float*)vc;
+  const uint16_t* k16 = (const uint16_t*)kc;
+  const uint16_t* v16 = (const uint16_t*)vc;
+  // per (kv head, chunk): the chunk's K transposed ([d][key]) and V ([key][d])
+  // decoded once, zeros past kv, then every query of the kv head: the chains
+  // run over d (scores) and over the keys (P.V) in order, 64 scores or D
+  // outputs side by side; then per (head, row) the chunks merged in order
+  std::vector<float> qv((size_t)T * QN);
+  for (size_t i = 0; i < qv.size(); ++i) qv[i] = f16kv ? h2f(f2h(q[i])) : q[i];
+  std::vector<float> cm((size_t)NH * T * nch), cl((size_t)NH * T * nch), co((size_t)NH * T * nch * D);
+#pragma omp parallel
+  {
+    std::vector<float> kt((size_t)D * 64), vt((size_t)64 * D);
+#pragma omp for collapse(2) schedule(dynamic)
+    for (int g = 0; g < NKV; ++g)
+      for (int c = 0; c < nch; ++c) {
+        float* __restrict__ ktp = kt.data();
+        float* __restrict__ vcp = vt.data();
+        for (int j = 0; j < 64; ++j) {
+          const int key = 64 * c + j;
+          const size_t kb = ((size_t)g * max_seq + key) * D;
+          if (key >= kv) {
+            for (int d = 0; d < D; ++d) ktp[(size_t)d * 64 + j] = vcp[(size_t)j * D + d] = 0.0f;
+          } else if (!f16kv) {
+            for (int d = 0; d < D; ++d) {
+              ktp[(size_t)d * 64 + j] = k32[kb + d];
+              vcp[(size_t)j * D + d] = v32[kb + d];
+            }
+          } else {
+            for (int d = 0; d < D; ++d) {
+              ktp[(size_t)d * 64 + j] = h2f(k16[kb + d]);
+              vcp[(size_t)j * D + d] = h2f(v16[kb + d]);
+            }
+          }
+        }
+        for (int h = g * groups; h < (g + 1) * groups; ++h)
+          for (int t = 0; t < T; ++t) {
+            const float* qh = &qv[(size_t)t * QN + (size_t)h * D];
+            float s[64], w[64], p[64];
+            for (int j = 0; j < 64; ++j) s[j] = 0.0f;
+            for (int d = 0; d < D; ++d) {
+              const float qd = qh[d];
+              const float* __restrict__ kd = ktp + (size_t)d * 64;
+              for (int j = 0; j < 64; ++j) s[j] = std::fma(qd, kd[j], s[j]);
+            }
+            float mx = -INFINITY;
+            for (int j = 0; j < 64; ++j) {
+              const int key = 64 * c + j;
+              w[j] = (key < kv && key <= past + t) ? s[j] * scale : -INFINITY;
+              mx = std::max(mx, w[j]);
+            }
+            for (int j = 0; j < 64; ++j) {
+              p[j] = (mx == -INFINITY || w[j] == -INFINITY) ? 0.0f : exp_c(w[j] - mx);
+              if (f16kv) p[j] = h2f(f2h(p[j]));
+            }
+            float pl[64];
+            std::memcpy(pl, p, sizeof(pl));
+            const size_t it = ((size_t)h * T + t) * nch + c;
+            cm[it] = mx;
+            cl[it] = butterfly64(pl);
+            float* __restrict__ oc = &co[it * D];
+            for (int d = 0; d < D; ++d) oc[d] = 0.0f;
+            for (int j = 0; j < 64; ++j) {
+              const float pj = p[j];
+              const float* __restrict__ vj = vcp + (size_t)j * D;
+              for (int d = 0; d < D; ++d) oc[d] = std::fma(pj, vj[d], oc[d]);
+            }
+          }
+      }
+  }
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int h = 0; h < NH; ++h)
+    for (int t = 0; t < T; ++t) {
+      const size_t i0 = ((size_t)h * T + t) * nch;
+      float M = -INFINITY;
+      for (int c = 0; c < nch; ++c) M = std::max(M, cm[i0 + c]);
+      float* oh = o + (size_t)t * QN + (size_t)h * D;
+      for (int d = 0; d < D; ++d) {
+        float L = 0.0f, acc = 0.0f;
+        for (int c = 0; c < nch; ++c) {
+          if (cm[i0 + c] == -INFINITY) continue;
+          const float f = exp_c(cm[i0 + c] - M);
+          L = std::fma(cl[i0 + c], f, L);
+          acc = std::fma(co[(i0 + c) * D + d], f, acc);
+        }
+        oh[d] = acc / L;
+      }
+    }
+}
+
 // One qwen3_layer_forward over T rows at positions past..past+T-1
 // (src/qwen3.cpp:62-218 with the device-cache path, transposed-V semantics and
 // the causal-context op of src/cpu_context.cpp:13-32).
@@ -716,7 +821,7 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
   const mtg_hparams& hp = m.hp;
   const int H = hp.hidden, D = hp.head_dim, NH = hp.n_heads, NKV = hp.n_kv_heads;
   const int QN = NH * D, KN = NKV * D, F = hp.intermediate;
-  const int past = m.past, kv = past + T, groups = NH / NKV;
+  const int past = m.past;
   std::vector<float> xn((size_t)T * H), q((size_t)T * QN), k((size_t)T * KN), v((size_t)T * KN);
   for (int t = 0; t < T; ++t) norm_op(m, x + (size_t)t * H, m.attn_norm[l].data(), H, xn.data() + (size_t)t * H);
   gemm_op(m, m.wq[l].data(), H, QN, xn.data(), T, q.data());
@@ -749,103 +854,15 @@ void layer_forward(orc_model& m, int l, float* x, int T) {
         kv_set(m, true, idx, k[(size_t)t * KN + (size_t)h * D + d]);
         kv_set(m, false, idx, v[(size_t)t * KN + (size_t)h * D + d]);
       }
-  // eager GQA attention (src/qwen3.cpp:157-189): scores K.Q in f32,
-  // soft_max_ext(scale 1/sqrt(D), causal mask), context over each query's valid
-  // length (src/cpu_context.cpp:13-32). Canonical order: keys in chunks of 64;
-  // score = fma chain over D; per chunk max, p = exp(w - max), l = butterfly
-  // sum of p, O = fma chain over the chunk's keys; chunks merged in order.
-  const float scale = 1.0f / std::sqrt((float)D);
-  const bool f16kv = m.kv_type == MTG_TYPE_F16;
-  const int nch = (kv + 63) / 64;
+  // eager GQA attention (src/qwen3.cpp:157-189)
   std::vector<float> o((size_t)T * QN);
   if (m.order == ORC_ORDER_GGML_GENERIC) {
     attention_generic(m, l, q.data(), T, o.data());
   } else {
-    // per (kv head, chunk): the chunk's K transposed ([d][key]) and V ([key][d])
-    // decoded once, zeros past kv, then every query of the kv head: the chains
-    // run over d (scores) and over the keys (P.V) in order, 64 scores or D
-    // outputs side by side; then per (head, row) the chunks merged in order
-    std::vector<float> qv((size_t)T * QN);
-    for (size_t i = 0; i < qv.size(); ++i) qv[i] = f16kv ? h2f(f2h(q[i])) : q[i];
-    std::vector<float> cm((size_t)NH * T * nch), cl((size_t)NH * T * nch), co((size_t)NH * T * nch * D);
-#pragma omp parallel
-    {
-      std::vector<float> kt((size_t)D * 64), vc((size_t)64 * D);
-#pragma omp for collapse(2) schedule(dynamic)
-      for (int g = 0; g < NKV; ++g)
-        for (int c = 0; c < nch; ++c) {
-          float* __restrict__ ktp = kt.data();
-          float* __restrict__ vcp = vc.data();
-          for (int j = 0; j < 64; ++j) {
-            const int key = 64 * c + j;
-            const size_t kb = base + ((size_t)g * m.max_seq + key) * D;
-            if (key >= kv) {
-              for (int d = 0; d < D; ++d) ktp[(size_t)d * 64 + j] = vcp[(size_t)j * D + d] = 0.0f;
-            } else if (m.kv_type == MTG_TYPE_F32) {
-              for (int d = 0; d < D; ++d) {
-                ktp[(size_t)d * 64 + j] = m.k32[kb + d];
-                vcp[(size_t)j * D + d] = m.v32[kb + d];
-              }
-            } else {
-              for (int d = 0; d < D; ++d) {
-                ktp[(size_t)d * 64 + j] = h2f(m.k16[kb + d]);
-                vcp[(size_t)j * D + d] = h2f(m.v16[kb + d]);
-              }
-            }
-          }
-          for (int h = g * groups; h < (g + 1) * groups; ++h)
-            for (int t = 0; t < T; ++t) {
-              const float* qh = &qv[(size_t)t * QN + (size_t)h * D];
-              float s[64], w[64], p[64];
-              for (int j = 0; j < 64; ++j) s[j] = 0.0f;
-              for (int d = 0; d < D; ++d) {
-                const float qd = qh[d];
-                const float* __restrict__ kd = ktp + (size_t)d * 64;
-                for (int j = 0; j < 64; ++j) s[j] = std::fma(qd, kd[j], s[j]);
-              }
-              float mx = -INFINITY;
-              for (int j = 0; j < 64; ++j) {
-                const int key = 64 * c + j;
-                w[j] = (key < kv && key <= past + t) ? s[j] * scale : -INFINITY;
-                mx = std::max(mx, w[j]);
-              }
-              for (int j = 0; j < 64; ++j) {
-                p[j] = (mx == -INFINITY || w[j] == -INFINITY) ? 0.0f : exp_c(w[j] - mx);
-                if (f16kv) p[j] = h2f(f2h(p[j]));
-              }
-              float pl[64];
-              std::memcpy(pl, p, sizeof(pl));
-              const size_t it = ((size_t)h * T + t) * nch + c;
-              cm[it] = mx;
-              cl[it] = butterfly64(pl);
-              float* __restrict__ oc = &co[it * D];
-              for (int d = 0; d < D; ++d) oc[d] = 0.0f;
-              for (int j = 0; j < 64; ++j) {
-                const float pj = p[j];
-                const float* __restrict__ vj = vcp + (size_t)j * D;
-                for (int d = 0; d < D; ++d) oc[d] = std::fma(pj, vj[d], oc[d]);
-              }
-            }
-        }
-    }
-#pragma omp parallel for collapse(2) schedule(static)
-    for (int h = 0; h < NH; ++h)
-      for (int t = 0; t < T; ++t) {
-        const size_t i0 = ((size_t)h * T + t) * nch;
-        float M = -INFINITY;
-        for (int c = 0; c < nch; ++c) M = std::max(M, cm[i0 + c]);
-        float* oh = o.data() + (size_t)t * QN + (size_t)h * D;
-        for (int d = 0; d < D; ++d) {
-          float L = 0.0f, acc = 0.0f;
-          for (int c = 0; c < nch; ++c) {
-            if (cm[i0 + c] == -INFINITY) continue;
-            const float f = exp_c(cm[i0 + c] - M);
-            L = std::fma(cl[i0 + c], f, L);
-            acc = std::fma(co[(i0 + c) * D + d], f, acc);
-          }
-          oh[d] = acc / L;
-        }
-      }
+    const bool f16kv = m.kv_type == MTG_TYPE_F16;
+    const void* kc = f16kv ? (const void*)(m.k16.data() + base) : (const void*)(m.k32.data() + base);
+    const void* vc = f16kv ? (const void*)(m.v16.data() + base) : (const void*)(m.v32.data() + base);
+    attention_canonical(kc, vc, f16kv, m.max_seq, past, T, NH, NKV, D, q.data(), o.data());
   }
   // o-proj + residual, FFN pre-norm, SwiGLU, down + residual
   std::vector<float> ao((size_t)T * H);
@@ -913,6 +930,11 @@ void orc_causal_context(const float* v, const float* p, int32_t head_dim, int32_
                  p[((size_t)h * queries + q) * kv_len + k];
         out[((size_t)h * queries + q) * head_dim + f] = acc;
       }
+}
+
+void orc_attention(const void* k, const void* v, int32_t f16kv, int32_t max_seq, int32_t past, int32_t T,
+                   int32_t heads, int32_t kv_heads, int32_t head_dim, const float* q, float* out) {
+  attention_canonical(k, v, f16kv != 0, max_seq, past, T, heads, kv_heads, head_dim, q, out);
 }
 
 void orc_set_threads(int n) {

@@ -98,6 +98,12 @@ void orc_rope_neox(float* x, int32_t n_dims, int32_t pos, float base);
 void orc_softmax(const float* s, int32_t n, float scale, const float* mask, float* out);
 void orc_causal_context(const float* v, const float* p, int32_t head_dim, int32_t kv_heads,
                         int32_t heads, int32_t queries, int32_t kv_len, float* out);
+/* The decoder step's attention in the canonical order (chunks of 64 keys merged
+ * in order): T query rows q [T][heads * head_dim] at positions
+ * past .. past + T - 1 over k, v [kv_heads][max_seq][head_dim] holding keys
+ * [0, past + T) (f32, or f16 bits when f16kv; q then rounded to f16). */
+void orc_attention(const void* k, const void* v, int32_t f16kv, int32_t max_seq, int32_t past, int32_t T,
+                   int32_t heads, int32_t kv_heads, int32_t head_dim, const float* q, float* out);
 
 /* ---- Whisper encoder + audio adaptor (src/whisper_encoder.cpp:103-209,
  * src/audio_adaptor.cpp:38-97) ---- */

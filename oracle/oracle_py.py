@@ -63,6 +63,8 @@ SIGNATURES = {
     "orc_softmax": (None, [c_void_p, c_int32, c_float, c_void_p, c_void_p]),
     "orc_causal_context": (None, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
                                   c_void_p]),
+    "orc_attention": (None, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                             c_void_p, c_void_p]),
     "orc_encoder_create": (c_int32, [POINTER(mtg.EncoderDesc), POINTER(c_void_p)]),
     "orc_encoder_destroy": (None, [c_void_p]),
     "orc_encoder_encode": (c_int32, [c_void_p, c_void_p, c_void_p, POINTER(c_int32)]),
@@ -157,6 +159,20 @@ def causal_context(v, p, kv_heads, heads, queries, kv_len, head_dim):
     v, p = f32(v), f32(p)
     out = np.empty((heads, queries, head_dim), np.float32)
     lib().orc_causal_context(ptr(v), ptr(p), head_dim, kv_heads, heads, queries, kv_len, ptr(out))
+    return out
+
+
+def attention(q, k, v, past):
+    """The decoder step's canonical attention: q [T][heads][head_dim] (float32),
+    k, v [kv_heads][max_seq][head_dim] float32 or float16 holding keys
+    [0, past + T). Returns [T][heads][head_dim]."""
+    q = f32(q)
+    T, heads, hd = q.shape
+    f16kv = k.dtype == np.float16
+    k, v = np.ascontiguousarray(k), np.ascontiguousarray(v)
+    assert k.dtype == v.dtype and k.shape == v.shape and k.shape[1] >= past + T
+    out = np.empty((T, heads, hd), np.float32)
+    lib().orc_attention(ptr(k), ptr(v), int(f16kv), k.shape[1], past, T, heads, k.shape[0], hd, ptr(q), ptr(out))
     return out
 
 

@@ -229,9 +229,12 @@ def test_long_f16_context_matches_oracle(wtype, exec_mode):
 # workgroup of the step kernel's attention walks 2 or 4 chunks of one head with the
 # q rows staged once. The new rows lie in one chunk (2050 + 16), straddle two
 # chunks on two workgroups (2040 + 16: chunks 31 | 32) or two chunks of one
-# workgroup (4030 + 9: chunks 62, 63), or end a 97-chunk context (6200 + 4).
+# workgroup (4030 + 9: chunks 62, 63), or end a 97-chunk context (6200 + 4); a
+# 96-chunk context (6130 + 8: three chunks per workgroup) and a 194-chunk one
+# (12400 + 16: seven).
 CHUNK_GROUPS = [(2050, 16, mtg.TYPE_F32), (2040, 16, mtg.TYPE_F16), (4030, 9, mtg.TYPE_F16),
-                (6200, 4, mtg.TYPE_F32), (3000, 1, mtg.TYPE_F16)]
+                (6200, 4, mtg.TYPE_F32), (3000, 1, mtg.TYPE_F16), (6130, 8, mtg.TYPE_F16),
+                (12400, 16, mtg.TYPE_F16)]
 
 
 @pytest.mark.parametrize("case", CHUNK_GROUPS, ids=["%d+%d-%s" % (p, t, "f32" if k == mtg.TYPE_F32 else "f16")

@@ -410,3 +410,86 @@ def test_q8_k_activation_quantizer_rules():
     nz = np.abs(xb).max(axis=1) > 0
     first = np.abs(xb).argmax(axis=1)  # numpy: first occurrence
     assert (qs[nz, first[nz]] == -127).all()
+
+
+def _attention_f64(q, k, v, past):
+    """Causal softmax attention in float64: q [T][H][D], k, v [G][S][D]."""
+    T, H, D = q.shape
+    G = k.shape[0]
+    out = np.empty((T, H, D))
+    for h in range(H):
+        g = h // (H // G)
+        kk = k[g, :past + T].astype(np.float64)
+        vv = v[g, :past + T].astype(np.float64)
+        s = q[:, h, :].astype(np.float64) @ kk.T / np.sqrt(D)
+        for t in range(T):
+            s[t, past + t + 1:] = -np.inf
+        s -= s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        out[:, h, :] = (p / p.sum(axis=1, keepdims=True)) @ vv
+    return out
+
+
+# (cached prefix, T): 26 chunks; 33 chunks, the last one reached by the last rows
+# only; 63, 96, 97, 140 and 194 chunks (the step kernel's attention items take 2 to
+# 7 chunks of a kv head each beyond 32 chunks; the per-op kernels stride over them)
+LONG_CASES = [(1650, 8), (2040, 16), (4000, 16), (6140, 4), (6200, 4), (8950, 9), (12400, 16)]
+
+
+@pytest.mark.parametrize("past,T", LONG_CASES)
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_attention_long_context_close_to_float64(past, T, kv):
+    """The step's attention in the canonical order (chunks of 64 keys, each with its
+    own maximum, merged in order with f = exp(m_c - M)) against float64 causal
+    softmax attention. The keys of each chunk are scaled by a factor between 0.3
+    and 3, so that the chunk maxima differ and every merge factor matters: a factor
+    taken the wrong way round, a chunk dropped or counted twice, or a mask off by
+    one row moves the result far beyond the bound."""
+    rng = np.random.default_rng(past + T)
+    G, H, D = 2, 4, 128
+    S = past + T + 7
+    q = rng.standard_normal((T, H, D)).astype(np.float32)
+    k = rng.standard_normal((G, S, D)).astype(np.float32)
+    nch = (past + T + 63) // 64
+    k *= np.repeat(rng.uniform(0.3, 3.0, (G, nch + 1)), 64, axis=1)[:, :S, None].astype(np.float32)
+    v = rng.standard_normal((G, S, D)).astype(np.float32)
+    if kv == "f16":
+        q16, k, v = q.astype(np.float16).astype(np.float32), k.astype(np.float16), v.astype(np.float16)
+        ref = _attention_f64(q16, k.astype(np.float32), v.astype(np.float32), past)
+        tol = 3e-3  # probabilities rounded to f16
+    else:
+        ref = _attention_f64(q, k, v, past)
+        tol = 2e-5
+    got = oracle_py.attention(q, k, v, past).astype(np.float64)
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err <= tol, err
+
+
+@pytest.mark.parametrize("past,T", LONG_CASES)
+def test_attention_long_context_exact_on_planted_keys(past, T):
+    """Scores of exactly +50 ("hot" keys) or -150 (probability exp(-200), which
+    flushes to 0): every chunk maximum that holds a hot key is 50, so every merge
+    factor is 1 or 0, l is the count of hot keys and O the sum of their
+    small-integer v rows: all exact, so the output is (sum / count) rounded once,
+    in any order. A chunk missing from the merge or counted twice, or a key past a
+    row's causal limit changes it."""
+    rng = np.random.default_rng(7 * past + T)
+    G, H, D = 2, 4, 128
+    S = past + T
+    a = np.float32(np.sqrt(128.0))  # q = a e0 and k[0] = +-50 or -150: score k[0]
+    q = np.zeros((T, H, D), np.float32)
+    q[:, :, 0] = a
+    k = np.zeros((G, S, D), np.float32)
+    hot = rng.random((G, S)) < 0.05
+    hot[:, rng.integers(0, S, 3)] = True
+    k[:, :, 0] = np.where(hot, 50.0, -150.0)
+    v = rng.integers(-8, 9, (G, S, D)).astype(np.float32)
+    got = oracle_py.attention(q, k, v, past)
+    for t in range(T):
+        for h in range(H):
+            g = h // (H // G)
+            sel = hot[g, :past + t + 1]
+            if not sel.any():
+                continue  # a row without a hot key: every p is 0 (0 / 0)
+            want = (v[g, :past + t + 1][sel].astype(np.float64).sum(axis=0) / sel.sum()).astype(np.float32)
+            assert np.array_equal(got[t, h], want), (t, h)
