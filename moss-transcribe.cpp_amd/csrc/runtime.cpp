@@ -105,6 +105,8 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
                                  !wt_shape_supported(wtype, F)))
     return fail(MTG_ERR_UNSUPPORTED, "shape not supported for weight type %d (f16, f32: K of 1024, 2048 or "
                 "3072; q4_K: K a multiple of 256)", wtype);
+  if ((wtype == MTG_TYPE_F16 || wtype == MTG_TYPE_F32) && H != 1024)
+    return fail(MTG_ERR_UNSUPPORTED, "f16 and f32 weights need hidden 1024 (their lm_head kernels)");
   if (kv_type != MTG_TYPE_F32 && kv_type != MTG_TYPE_F16)
     return fail(MTG_ERR_UNSUPPORTED, "kv type %d", kv_type);
   if (D != kHeadDim || NH != 2 * NKV || H % kPairK || QN % kPairK || F % kPairK || V % 16 ||

@@ -302,6 +302,18 @@ def test_f16_and_q4k_weights_penalty_prefill_and_stream(wtype):
     assert st1.accepted == st0.accepted and st1.proposed == st0.proposed
 
 
+@pytest.mark.parametrize("wtype", [mtg.TYPE_F16, mtg.TYPE_F32], ids=["f16", "f32"])
+def test_f16_and_f32_weights_refuse_other_hidden_sizes(wtype):
+    """The f16 and f32 lm_head kernels take K = 1,024: a model of hidden 2,048 with
+    those weights is refused with MTG_ERR_UNSUPPORTED (the q8_0 and q4_K paths take
+    it)."""
+    model = mtg.SynthModel(wtype, seed=1, std=0.02, n_layers=1, vocab=256, hidden=2048)
+    with pytest.raises(mtg.MtgError) as exc:
+        mtg.Decoder(model, 64, mtg.TYPE_F32)
+    assert exc.value.code == mtg.ERR_UNSUPPORTED
+    model.close()
+
+
 def test_step_kernel_abort_reports_and_recovers():
     """Failure path of the persistent kernel, forced from the host: with its error
     word raised before the launch, every bounded wait gives up at its first poll.
