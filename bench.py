@@ -47,7 +47,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [os.path.join(ROOT, "moss-transcribe.cpp_amd"), os.path.join(ROOT, "oracle")]
 
 import mtg  # noqa: E402
-from workloads import AUDIO_ROWS, CONFIGS, WNAME, build_prompt, prompt_rows  # noqa: E402
+from workloads import AUDIO_ROWS, WORKLOADS, WNAME, build_prompt, prompt_rows  # noqa: E402
 
 METRIC = "verify-step µs + accepted tok/s (q8_0, K=8, ctx 1.6k); % of HBM peak"
 HBM_PEAK_GBS = 8000.0
@@ -217,7 +217,7 @@ def main():
               "shards only across independent streams (one decoder per recording, one GPU each).",
               file=sys.stderr)
         sys.exit(2)
-    cfg = dict(CONFIGS[args.config])
+    cfg = dict(WORKLOADS[args.config])
     if args.weights is not None:
         cfg["wtype"] = {v: k for k, v in WNAME.items()}[args.weights]
     steps = args.steps if args.steps is not None else cfg["steps"]

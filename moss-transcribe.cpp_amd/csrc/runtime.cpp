@@ -100,7 +100,7 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
   const int QN = NH * D, KN = NKV * D, F = hp.intermediate, L = hp.n_layers, V = hp.vocab;
   wtype = d->weight_type;
   if (wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16 && wtype != MTG_TYPE_F32 && wtype != MTG_TYPE_Q4_K)
-    return fail(MTG_ERR_UNSUPPORTED, "weight type %d is not supported by this build", wtype);
+    return fail(MTG_ERR_UNSUPPORTED, "weight type %d is not supported", wtype);
   if (wtype != MTG_TYPE_Q8_0 && (!wt_shape_supported(wtype, H) || !wt_shape_supported(wtype, QN) ||
                                  !wt_shape_supported(wtype, F)))
     return fail(MTG_ERR_UNSUPPORTED, "shape not supported for weight type %d (f16, f32: K of 1024, 2048 or "

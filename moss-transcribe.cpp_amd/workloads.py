@@ -12,7 +12,7 @@ import numpy as np
 import mtg
 
 # (weight type, kv type, audio blocks, text ids, K rows, decode steps)
-CONFIGS = {
+WORKLOADS = {
     1: dict(wtype=mtg.TYPE_Q8_0, kv=mtg.TYPE_F32, blocks=0, text=512, K=4, steps=1),
     2: dict(wtype=mtg.TYPE_Q8_0, kv=mtg.TYPE_F32, blocks=4, text=100, K=8, steps=256),
     3: dict(wtype=mtg.TYPE_Q8_0, kv=mtg.TYPE_F16, blocks=10, text=250, K=16, steps=128),

@@ -1,7 +1,7 @@
 // oracle.cpp - CPU restatement of the reference speculative verify path.
 //
-// TEST INFRASTRUCTURE ONLY: the parity checker for libmtg and the timed CPU
-// baseline of bench.py. Nothing in the product links or loads this file.
+// TEST INFRASTRUCTURE ONLY: the oracle libmtg's parity tests compare against, and
+// the timed CPU baseline of bench.py. Nothing in the product links or loads this file.
 //
 // The reference executes these ops through ggml's CPU backend, which is not
 // vendored in the reference tree (third_party/ggml is an empty submodule), so the

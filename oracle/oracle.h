@@ -1,8 +1,9 @@
 /* oracle.h - CPU restatement of moss-transcribe.cpp's speculative verify path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the parity checker for libmtg and the
- * timed CPU baseline of bench.py. Only tests/, __graft_entry__.smoke() and the
- * bench's cpu_baseline leg load it; the product never does.
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle libmtg's parity tests
+ * compare against, and the timed CPU baseline of bench.py. Only tests/,
+ * __graft_entry__.smoke() and the bench's cpu_baseline leg load it; the product
+ * never does.
  *
  * It restates, in plain C++ loops, the arithmetic the reference runs through ggml's
  * CPU backend (ggml itself is an un-vendored submodule and cannot be built):

@@ -20,7 +20,7 @@ sys.path[:0] = [os.path.join(ROOT, "moss-transcribe.cpp_amd"), os.path.join(ROOT
 
 import mtg  # noqa: E402
 import oracle_py  # noqa: E402
-from workloads import CONFIGS, build_prompt, prompt_rows  # noqa: E402
+from workloads import WORKLOADS, build_prompt, prompt_rows  # noqa: E402
 
 
 def main():
@@ -29,7 +29,7 @@ def main():
     ap.add_argument("--threads", type=int, default=len(os.sched_getaffinity(0)))
     args = ap.parse_args()
     oracle_py.lib().orc_set_threads(args.threads)
-    cfg = CONFIGS[2]
+    cfg = WORKLOADS[2]
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
     n_prompt, K = prompt_rows(cfg), cfg["K"]
     max_seq = n_prompt + (args.steps + 4) * K

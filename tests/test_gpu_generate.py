@@ -197,8 +197,8 @@ def test_full_size_device_loop_k8_ctx1600():
     KV, the 1,600-row prompt): 64 steps of the device loop against the host loop,
     the same ids and counters; both are timed."""
     import time
-    from workloads import CONFIGS, build_prompt, prompt_rows
-    cfg = CONFIGS[2]
+    from workloads import WORKLOADS, build_prompt, prompt_rows
+    cfg = WORKLOADS[2]
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
     n = prompt_rows(cfg)
     a = mtg.Decoder(model, n + 600, cfg["kv"])
@@ -236,8 +236,8 @@ def test_full_size_device_loop_k16_f16kv_ctx4000():
     drafter (the 16-row step kernel): 16 steps against the host loop and the
     oracle from the same prefilled KV state."""
     import os
-    from workloads import CONFIGS, build_prompt, prompt_rows
-    cfg = CONFIGS[3]
+    from workloads import WORKLOADS, build_prompt, prompt_rows
+    cfg = WORKLOADS[3]
     oracle_py.lib().orc_set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
     n = prompt_rows(cfg)

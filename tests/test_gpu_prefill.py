@@ -11,7 +11,7 @@ import pytest
 
 import mtg
 import oracle_py
-from workloads import CONFIGS, build_prompt, prompt_rows
+from workloads import WORKLOADS, build_prompt, prompt_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -95,7 +95,7 @@ def test_full_size_prefill_paths_and_time(cfg_id):
     one, the 16,384-row q4_K one): block prefill and 16-row batches give the same
     hidden rows and KV cache; both are timed."""
     import time
-    cfg = CONFIGS[cfg_id]
+    cfg = WORKLOADS[cfg_id]
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
     n = prompt_rows(cfg)
     a = mtg.Decoder(model, n + 64, cfg["kv"])

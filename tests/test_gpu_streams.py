@@ -25,7 +25,7 @@ import pytest
 
 import mtg
 import oracle_py
-from workloads import CONFIGS, build_prompt, prompt_rows
+from workloads import WORKLOADS, build_prompt, prompt_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -47,7 +47,7 @@ def _log(msg):
 
 @pytest.mark.timeout(600)
 def test_full_size_prefill_and_stream_k8_q8_0_ctx1600():
-    cfg = CONFIGS[2]
+    cfg = WORKLOADS[2]
     oracle_py.lib().orc_set_threads(THREADS)
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
     hp = model.hp
@@ -136,7 +136,7 @@ def test_full_size_stream_16_steps(cfg_id):
     state, on the device and on the oracle: identical ids, counters and appended
     KV rows. The q8_0 workload runs the persistent step kernel, the f16 and q4_K
     workloads the per-op kernels from a graph."""
-    cfg = CONFIGS[cfg_id]
+    cfg = WORKLOADS[cfg_id]
     oracle_py.lib().orc_set_threads(THREADS)
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
     n_prompt, steps, K = prompt_rows(cfg), 16, cfg["K"]
