@@ -227,8 +227,8 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
     wact.q8k.qs = (int8_t*)dalloc((size_t)R * KM, true);
     wact.q8k.d = (float*)dalloc((size_t)R * (KM / 256 + 1) * 4, true);
     wact.q8k.bsums = (int32_t*)dalloc((size_t)R * (KM / 16) * 4, true);
-    wact.f32 = (float*)dalloc((size_t)R * KM * 4, true);
-    if (!wact.f16h || !wact.q8k.qs || !wact.q8k.d || !wact.q8k.bsums || !wact.f32)
+    if (wtype == MTG_TYPE_F32) wact.f32 = (float*)dalloc((size_t)R * KM * 4, true);
+    if (!wact.f16h || !wact.q8k.qs || !wact.q8k.d || !wact.q8k.bsums || (wtype == MTG_TYPE_F32 && !wact.f32))
       return fail(MTG_ERR_NOMEM, "activation buffers");
   }
   const size_t chunks = (size_t)NKV * ((max_seq + kChunkKeys - 1) / kChunkKeys);
