@@ -111,7 +111,9 @@ int mtg_abi_version(void);
 
 /* Upload weights (re-tiled for the gfx950 kernels) and allocate a KV cache of
  * max_seq positions of kv_type (MTG_TYPE_F32 or MTG_TYPE_F16). The host tensors
- * may be freed after the call. */
+ * may be freed after the call. A context owns one HIP stream on the current
+ * device; its calls are not synchronized with each other, so one host thread
+ * uses it at a time (distinct contexts may run side by side). */
 int mtg_create(const mtg_model_desc* desc, int32_t max_seq, int32_t kv_type, mtg_ctx** out);
 void mtg_destroy(mtg_ctx* ctx);
 const char* mtg_last_error(const mtg_ctx* ctx);
@@ -127,7 +129,7 @@ int mtg_embed(mtg_ctx* ctx, const int32_t* ids, int32_t n, float* out);
 /* reset + run S rows; hidden_out (nullable) receives the final-normed hidden of
  * every row (S x hidden). The rows go through the decoder in blocks of up to
  * 2,048 (each weight matrix streamed once per block, causal attention over the
- * cache), for q8_0, f16 and q4_K weights; with mtg_prefill_mode(ctx, 0) in verify
+ * cache), for every weight type; with mtg_prefill_mode(ctx, 0) in verify
  * batches of up to MTG_MAX_BATCH. Both give the same bits. */
 int mtg_prefill(mtg_ctx* ctx, const float* embeds, int32_t S, float* hidden_out);
 /* blocks != 0 (the default): the block prefill where it applies; 0: verify-size
