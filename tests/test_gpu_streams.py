@@ -9,12 +9,12 @@ softmax stress rows through the device attention.
   the device's on the first 64 committed rows (they must agree wherever the margin
   exceeds the largest logit difference between the two orders, and they agree on
   every one of those rows).
-* The K=16 f16-KV workload at a 4,000-row prompt: 16 greedy steps from the same KV
-  state on both sides, identical ids and counters.
-* The f16-weight workload (8,000-row prompt, K=8) and the q4_K workload (16,384-row
-  prompt, K=16), both with an f16 cache, on the per-op kernels: the prompt
-  prefilled on the device, 16 greedy steps on both sides from that KV state,
-  identical ids, counters and appended KV rows.
+* The K=16 f16-KV workload at a 4,000-row prompt: all 128 greedy steps from the same
+  KV state on both sides, identical ids and counters.
+* The f16-weight workload (8,000-row prompt, K=8, 128 steps) and the q4_K workload
+  (16,384-row prompt, K=16, 64 steps), both with an f16 cache, on the per-op kernels:
+  the prompt prefilled on the device, every greedy step of the workload on both sides
+  from that KV state, identical ids, counters and appended KV rows.
 * Attention on scores of +-10000 and -inf (tests/test_cpu_softmax.cpp:40-46), made
   by planting keys of magnitude 10^4 in the cache: bit-identical to the oracle.
 """
@@ -125,21 +125,21 @@ def test_full_size_prefill_and_stream_k8_q8_0_ctx1600():
     model.close()
 
 
-STREAM16 = [(3, "k16-q8_0-f16kv-ctx4000-step"), (4, "k8-f16-f16kv-ctx8000-graph"),
-            (5, "k16-q4_K-f16kv-ctx16384-graph")]
+STREAMS = [(3, "k16-q8_0-f16kv-ctx4000-step"), (4, "k8-f16-f16kv-ctx8000-graph"),
+           (5, "k16-q4_K-f16kv-ctx16384-graph")]
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("cfg_id", [c for c, _ in STREAM16], ids=[n for _, n in STREAM16])
-def test_full_size_stream_16_steps(cfg_id):
-    """16 greedy steps of a workload at full size from the device's prefilled KV
-    state, on the device and on the oracle: identical ids, counters and appended
-    KV rows. The q8_0 workload runs the persistent step kernel, the f16 and q4_K
-    workloads the per-op kernels from a graph."""
+@pytest.mark.parametrize("cfg_id", [c for c, _ in STREAMS], ids=[n for _, n in STREAMS])
+def test_full_size_stream_all_steps(cfg_id):
+    """Every greedy step of a workload (128, 128 and 64) at full size from the
+    device's prefilled KV state, on the device and on the oracle: identical ids,
+    counters and appended KV rows. The q8_0 workload runs the persistent step kernel,
+    the f16 and q4_K workloads the per-op kernels from a graph."""
     cfg = WORKLOADS[cfg_id]
     oracle_py.lib().orc_set_threads(THREADS)
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
-    n_prompt, steps, K = prompt_rows(cfg), 16, cfg["K"]
+    n_prompt, steps, K = prompt_rows(cfg), cfg["steps"], cfg["K"]
     max_seq = n_prompt + (steps + 4) * K
     dec = mtg.Decoder(model, max_seq, cfg["kv"])
     want_exec = mtg.EXEC_STEP_KERNEL if cfg["wtype"] == mtg.TYPE_Q8_0 else mtg.EXEC_GRAPH
