@@ -3,8 +3,9 @@ WhisperEncoder::encode, src/whisper_encoder.cpp:103-209, AudioAdaptor::apply,
 src/audio_adaptor.cpp:38-97) against the oracle: encoder rows and adaptor rows
 bit-identical (the kernels keep the oracle's order of every reduction), at a
 short chunk and at the full 3,000-frame chunk (1,500 rows) with 2 layers for
-q8_0, f16 and q4_K matrices, and for the whole 24-layer q8_0 encoder (also timed
-and checked for determinism)."""
+q8_0, f16, f32 and q4_K matrices, and for the whole 24-layer q8_0 encoder (also timed
+and checked for determinism); and the whole path from mel frames to token ids
+(encoder, adaptor, fused prompt, prefill, speculative steps) on both sides."""
 import os
 
 import numpy as np
@@ -97,3 +98,56 @@ def test_full_encoder_24_layers_matches_oracle():
     z = (a.astype(np.float64) - bb) / w
     assert np.abs(z.mean(axis=1)).max() < 1e-4 and np.abs(z.var(axis=1) - 1).max() < 1e-2
     dev.close()
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("exec_mode", [mtg.EXEC_STEP_KERNEL, mtg.EXEC_GRAPH], ids=["step", "graph"])
+def test_audio_to_tokens_matches_oracle(exec_mode):
+    """The whole transcription path on both sides, from mel frames to token ids: a
+    3,000-frame chunk through the encoder (2 layers) and the adaptor (375 rows), the
+    prompt fused as the reference's fuse_embeds does (src/generate.cpp:113-178: the
+    ids embedded, the k-th position holding the audio token id replaced by adaptor
+    row k), the decoder's prefill of the fused rows (2 layers, hidden 1024), the first
+    greedy id from the last row's logits, then 24 speculative steps with the n-gram
+    drafter. Every intermediate and the committed ids are equal."""
+    print("audio to tokens: exec %d" % exec_mode, flush=True)
+    oracle_py.lib().orc_set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    syn = mtg.SynthEncoder(seed=21, n_layers=2)
+    model = mtg.SynthModel(mtg.TYPE_Q8_0, seed=22, std=0.02, gain_jitter=0.05, n_layers=2, vocab=4096)
+    assert syn.hp.hidden == model.hp.hidden
+    enc, oenc = mtg.Encoder(syn), oracle_py.OracleEncoder(syn)
+    mel = syn.mel(seed=23)
+    _same(enc.encode(mel), oenc.encode(mel), "encoder rows")
+    a1, a0 = enc.adapt(syn.rows), oenc.adapt(syn.rows)
+    _same(a1, a0, "adaptor rows")
+    n_audio = a1.shape[0]
+    rng = np.random.default_rng(24)
+    audio_id = 4000
+    prefix = rng.integers(0, audio_id, 12)
+    suffix = rng.integers(0, audio_id, 40)
+    ids = np.concatenate([prefix, np.full(n_audio, audio_id), suffix]).astype(np.int32)
+    max_seq = len(ids) + 24 * 8 + 16
+    dec = mtg.Decoder(model, max_seq, mtg.TYPE_F32)
+    dec.set_exec(exec_mode)
+    orc = oracle_py.Oracle(model, max_seq, mtg.TYPE_F32)
+
+    def fuse(embed, audio):  # the k-th audio position takes audio row k
+        rows = embed(ids).copy()
+        rows[ids == audio_id] = audio
+        return rows
+
+    f1, f0 = fuse(dec.embed, a1), fuse(orc.embed, a0)
+    _same(f1, f0, "fused prompt rows")
+    h1, h0 = dec.prefill(f1), orc.prefill(f0)
+    _same(h1, h0, "prefill hidden rows")
+    l1, l0 = dec.logits(h1[-1:]), orc.logits(h0[-1:])
+    _same(l1, l0, "logits of the last prompt row")
+    first = int(np.argmax(l1[0]))
+    ids1, st1 = dec.generate_from(first, 1 << 20, max_steps=24, max_draft=7)
+    ids0, st0 = orc.generate_from(first, 1 << 20, max_steps=24, max_draft=7)
+    assert ids1.tolist() == ids0.tolist()
+    for f in ("target_calls", "drafted_calls", "proposed", "accepted", "target_input_tokens", "rewinds"):
+        assert getattr(st1, f) == getattr(st0, f), f
+    print("audio to tokens: %d prompt rows (%d audio), %d ids" % (len(ids), n_audio, len(ids1)), flush=True)
+    for x in (dec, orc, enc, oenc, model):
+        x.close()
