@@ -343,7 +343,10 @@ class OracleEncoder:
     """CPU restatement of the Whisper encoder + adaptor (orc_encoder_*)."""
 
     def __init__(self, synth):
-        self.hp = synth.hp
+        # a copy: synth.hp may be a view into memory its owner frees (a GGUF file's
+        # description is released by mtg_gguf_close)
+        self.hp = mtg.EncoderHparams()
+        ctypes.memmove(ctypes.byref(self.hp), ctypes.byref(synth.hp), ctypes.sizeof(mtg.EncoderHparams))
         self.rows = synth.rows
         out = c_void_p()
         rc = lib().orc_encoder_create(ctypes.byref(synth.desc), ctypes.byref(out))

@@ -130,3 +130,57 @@ def test_encoder_from_gguf_matches_oracle(tmp_path, wtype):
     _same(b.adapt(80), ref.adapt(80), "adaptor rows")
     b.close()
     ref.close()
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("wtype", [mtg.TYPE_Q8_0, mtg.TYPE_F32], ids=["q8_0", "f32"])
+def test_one_file_audio_to_tokens_matches_oracle(tmp_path, wtype):
+    """One GGUF file holding the decoder and the encoder + adaptor (as the
+    reference's converter writes them, q8_0 or its default f32), read once by the
+    device (mtg_create_from_gguf, mtg_encoder_create_from_gguf) and once parsed for
+    the oracle: a 3,000-frame chunk through the encoder and the adaptor, the prompt
+    fused as fuse_embeds does (src/generate.cpp:113-178), the prefill and 16
+    speculative steps give the same rows and ids on both sides."""
+    print("one file, audio to tokens: weights %d" % wtype, flush=True)
+    _threads()
+    syn = mtg.SynthEncoder(seed=41, wtype=wtype, n_layers=2)
+    model = mtg.SynthModel(wtype, seed=42, std=0.02, gain_jitter=0.05, n_layers=2, vocab=4096)
+    path = str(tmp_path / "moss.gguf")
+    gguf_writer.write_encoder(path, syn, model=model)
+    mel = syn.mel(seed=43)
+    model.close()
+    del syn, model
+    g = mtg.GgufModel(path)
+    oenc = oracle_py.OracleEncoder(_ParsedEncoder(g))  # copies the tensors
+    rng = np.random.default_rng(44)
+    audio_id = 4000
+    n_audio = oenc.rows // oenc.hp.merge
+    ids = np.concatenate([rng.integers(0, audio_id, 9), np.full(n_audio, audio_id),
+                          rng.integers(0, audio_id, 30)]).astype(np.int32)
+    max_seq = len(ids) + 16 * 8 + 16
+    orc = oracle_py.Oracle(g, max_seq, mtg.TYPE_F32)
+    g.close()
+    enc = mtg.Encoder.from_gguf(path)
+    dec = mtg.Decoder.from_gguf(path, max_seq, mtg.TYPE_F32)
+    _same(enc.encode(mel), oenc.encode(mel), "encoder rows")
+    a1, a0 = enc.adapt(oenc.rows), oenc.adapt(oenc.rows)
+    _same(a1, a0, "adaptor rows")
+    assert a1.shape[0] == n_audio
+
+    def fuse(embed, audio):
+        rows = embed(ids).copy()
+        rows[ids == audio_id] = audio
+        return rows
+
+    h1, h0 = dec.prefill(fuse(dec.embed, a1)), orc.prefill(fuse(orc.embed, a0))
+    _same(h1, h0, "prefill hidden rows")
+    first = int(np.argmax(dec.logits(h1[-1:])[0]))
+    assert first == int(np.argmax(orc.logits(h0[-1:])[0]))
+    ids1, st1 = dec.generate_from(first, 1 << 20, max_steps=16, max_draft=7)
+    ids0, st0 = orc.generate_from(first, 1 << 20, max_steps=16, max_draft=7)
+    assert ids1.tolist() == ids0.tolist()
+    for f in ("target_calls", "proposed", "accepted", "rewinds"):
+        assert getattr(st1, f) == getattr(st0, f), f
+    print("one file, audio to tokens: %d prompt rows (%d audio), %d ids" % (len(ids), n_audio, len(ids1)), flush=True)
+    for x in (dec, orc, enc, oenc):
+        x.close()
