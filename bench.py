@@ -264,6 +264,7 @@ def main():
     hip.hipDeviceSynchronize()
     dec.launch_timing(True)
     fallbacks0 = dec.step_fallbacks
+    runs0 = dec.step_kernel_runs
     t0 = time.perf_counter()
     if loop == "device":
         ids, st = dec.generate_device(st_w.next_seed, 1 << 20, max_steps=steps, max_draft=cfg["K"] - 1,
@@ -278,6 +279,17 @@ def main():
     # steps whose persistent kernel gave up on a bounded wait and ran again on the
     # per-op kernels (their event time covers both launches)
     fallbacks = dec.step_fallbacks - fallbacks0
+    # the path the timed steps took: in step mode, steps past the persistent
+    # kernel's KV length limit (f16 weights) run on the per-op graph
+    runs = dec.step_kernel_runs - runs0
+    if args.exec != "step":
+        path = args.exec
+    elif runs + fallbacks >= launches:
+        path = "step"
+    elif runs + fallbacks == 0:
+        path = "graph"
+    else:
+        path = "step+graph"
     if fallbacks:
         log("WARNING: %d of %d timed steps fell back to the per-op kernels" % (fallbacks, launches))
     n_steps = int(st.target_calls)
@@ -291,7 +303,7 @@ def main():
     launch_s = dev_ms * 1e-3 / max(launches, 1)
     achieved = bytes_launch / launch_s / 1e9
     traffic = (measured_traffic(args.config) if args.layers == 28 and args.exec == "step" and args.weights is None
-               else None)
+               and runs > 0 else None)
     out = {
         "metric": METRIC,
         "value": tokens / elapsed,
@@ -313,11 +325,12 @@ def main():
                                   cfg["blocks"] * AUDIO_ROWS, cfg["text"], n_steps),
                    "verify_rows": cfg["K"], "context_start": ctx_start, "context_end": dec.past_len,
                    "accepted_per_step": st.accepted / max(n_steps, 1),
-                   "tokens": tokens, "exec": args.exec, "loop": loop},
+                   "tokens": tokens, "exec": args.exec, "path": path, "loop": loop},
         "verify_step_us": 1e3 * dev_ms / max(launches, 1),
         "host_step_us": 1e3 * ms_step,
         "step_bytes": bytes_launch,
-        "roofline": {"bound": "hbm", "kernel": KERNEL if args.exec == "step" else "per-op kernels",
+        "roofline": {"bound": "hbm", "kernel": KERNEL if path == "step" else
+                     ("per-op kernels" if path in ("graph", "eager") else KERNEL + " + per-op kernels"),
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
                      "traffic": traffic,

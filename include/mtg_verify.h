@@ -271,13 +271,25 @@ int mtg_generate_device_stream(mtg_ctx* ctx, int32_t first_seed, const int32_t* 
                                mtg_gen_stats* stats);
 
 /* How a step runs on the device. MTG_EXEC_STEP_KERNEL (the default for the
- * Qwen3-0.6B shape on a device with at least 256 CUs): one persistent dataflow
- * kernel per step. MTG_EXEC_GRAPH (the default otherwise): the per-op kernels,
- * replayed from a captured HIP graph. MTG_EXEC_EAGER: the per-op kernels
- * launched one by one (profiling). All modes produce the same results. */
+ * Qwen3-0.6B shape with q8_0 or f16 weights on a device with at least 256 CUs):
+ * one persistent dataflow kernel per step (f16 weights: steps of up to 8 rows;
+ * longer ones take the per-op graph). MTG_EXEC_GRAPH (the default otherwise): the
+ * per-op kernels, replayed from a captured HIP graph. MTG_EXEC_EAGER: the per-op
+ * kernels launched one by one (profiling). All modes produce the same results. */
 enum { MTG_EXEC_STEP_KERNEL = 0, MTG_EXEC_GRAPH = 1, MTG_EXEC_EAGER = 2 };
 int mtg_set_exec_mode(mtg_ctx* ctx, int32_t mode);
 int32_t mtg_exec_mode(const mtg_ctx* ctx);
+
+/* Path selection by context length (no counterpart in the reference, which has
+ * one CPU path): in MTG_EXEC_STEP_KERNEL mode a verify / append step whose KV
+ * length (past_len + rows) exceeds max_keys runs on the per-op graph instead of
+ * the persistent kernel. max_keys <= 0 restores the default: no limit for q8_0
+ * weights; 3,584 for f16 weights, whose per-op attention (three workgroups per CU)
+ * overtakes the persistent kernel's at longer contexts on MI355X. The device loop
+ * (mtg_generate_device) always runs the persistent kernel. mtg_step_kernel_runs
+ * counts the steps that ran to their end on the persistent kernel. */
+int mtg_set_step_max_keys(mtg_ctx* ctx, int32_t max_keys);
+int64_t mtg_step_kernel_runs(const mtg_ctx* ctx);
 
 /* Diagnostics: copy an internal activation buffer of the last step (16 rows):
  * the residual stream, the fused q|k|v projection, the attention output, the

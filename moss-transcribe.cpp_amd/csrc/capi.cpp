@@ -68,6 +68,14 @@ int mtg_set_exec_mode(mtg_ctx* ctx, int32_t mode) {
 
 int32_t mtg_exec_mode(const mtg_ctx* ctx) { return ctx ? ctx->impl.exec : -1; }
 
+int mtg_set_step_max_keys(mtg_ctx* ctx, int32_t max_keys) {
+  if (!ctx) return MTG_ERR_INVALID;
+  ctx->impl.step_max_keys = max_keys > 0 ? max_keys : 0;
+  return MTG_OK;
+}
+
+int64_t mtg_step_kernel_runs(const mtg_ctx* ctx) { return ctx ? ctx->impl.step_runs : 0; }
+
 int mtg_step_profile(mtg_ctx* ctx, int32_t enable) {
   if (!ctx) return MTG_ERR_INVALID;
   Ctx& c = ctx->impl;

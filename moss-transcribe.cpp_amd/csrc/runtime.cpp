@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <limits>
 #include <string>
 #include <vector>
 
@@ -256,7 +257,8 @@ int Ctx::init_step_kernel() {
   if ((rc = check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count")))
     return rc;
   const int H = hp.hidden, F = hp.intermediate, V = hp.vocab;
-  if (wtype != MTG_TYPE_Q8_0 ||  // the persistent kernel streams q8_0 panel tiles
+  // the persistent kernel streams q8_0 panel tiles, or f16 rows (8-row steps)
+  if ((wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16) || (wtype == MTG_TYPE_F16 && V > kStepF16MaxVocab) ||
       !step_kernel_supported(H, hp.n_heads, hp.n_kv_heads, hp.head_dim, F, hp.n_layers, cus) ||
       prepare_step_kernels() != hipSuccess) {
     (void)hipGetLastError();
@@ -310,6 +312,11 @@ int Ctx::init_step_kernel() {
   P.oqs = (float*)dalloc((size_t)kMaxRows * hp.n_heads * hp.head_dim / 32 * 4, true);
   P.aq = (int8_t*)dalloc((size_t)kMaxRows * F, true);
   P.aqs = (float*)dalloc((size_t)kMaxRows * F / 32 * 4, true);
+  if (wtype == MTG_TYPE_F16) {
+    P.oh = (uint16_t*)dalloc((size_t)kMaxRows * hp.n_heads * hp.head_dim * 2, true);
+    P.ah = (uint16_t*)dalloc((size_t)kMaxRows * F * 2, true);
+    if (!P.oh || !P.ah) return fail(MTG_ERR_NOMEM, "step kernel buffers");
+  }
   P.result = result_map;  // choices and n_match go straight to pinned host memory
   P.flags = (uint32_t*)dalloc((size_t)nwg * kFlagStride * 4, true);
   P.qkvt = (uint32_t*)dalloc(qkvt_bytes(), true);
@@ -428,7 +435,12 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
   const int G = (T + 7) / 8;
   int rc = MTG_OK;
   const bool step_mode = mode == kModeVerify || mode == kModeVerifyPenalty || mode == kModeAppend;
-  const bool on_step = exec == kExecStep && step_ok && step_mode;
+  // the f16-weight variant of the step kernel runs steps of up to 8 rows; longer
+  // ones, and steps beyond the KV length limit, take the per-op kernels
+  const int max_keys = step_max_keys > 0 ? step_max_keys
+                                         : (wtype == MTG_TYPE_F16 ? kStepF16MaxKeys : std::numeric_limits<int>::max());
+  const bool on_step = exec == kExecStep && step_ok && step_mode && (wtype == MTG_TYPE_Q8_0 || G == 1) &&
+                       (int64_t)past + T <= max_keys;
   const bool timed = timing && mode != kModeLogits;
   if (timed && (rc = check(hipEventRecord(ev_start, stream), "timing event"))) return rc;
   bool aborting = false;
@@ -449,7 +461,7 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
       if ((rc = check(hipMemsetAsync(&result_dev->err, 1, sizeof(int32_t), stream), "abort")))
         return rc;
     }
-    if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, params_dev, desc_host, epoch, smode,
+    if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, wtype == MTG_TYPE_F16, params_dev, desc_host, epoch, smode,
                                     params_host.timing != nullptr), "step kernel launch")))
       return rc;
     epoch += step_progress_per_step(hp.n_layers);
@@ -469,6 +481,7 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
     (void)hipMemcpy(&result_host->err, &result_dev->err, sizeof(int32_t), hipMemcpyDeviceToHost);
     if (!result_host->err) return fail(MTG_ERR_DEVICE, "step kernel: no result");
   }
+  if (on_step && !result_host->err) ++step_runs;
   if (result_host->err) {
     // a bounded wait ran out and every workgroup left the kernel; only positions
     // from `past` on were written, so the step can run again
@@ -821,6 +834,8 @@ int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prom
   int rc = MTG_OK;
   if (!step_ok || exec != kExecStep || g.max_draft + 1 > kMaxRows)
     return fail(MTG_ERR_UNSUPPORTED, "device generation needs the step kernel and max_draft <= %d", kMaxRows - 1);
+  if (wtype == MTG_TYPE_F16 && g.max_draft + 1 > 8)
+    return fail(MTG_ERR_UNSUPPORTED, "device generation with f16 weights needs max_draft <= 7 (8-row steps)");
   // the 16-row step variant when a step can hold more than 8 rows
   const int G = g.max_draft + 1 > 8 ? 2 : 1;
   // the stream drafter's prompt ids and stream period, in one device buffer
@@ -878,6 +893,7 @@ int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prom
         if ((rc = check(hipEventCreate(&e), "event"))) return rc;
   }
   int64_t rows0 = g.issued_rows, past0 = g.issued_past;
+  const int64_t steps_begin = g.steps;
   int64_t steps0 = g.steps, err0 = g.err;
   const GenCtl ctl{gen_state_dev, gen_ids_dev, desc_dev, prompt_dev, stream_dev};
   // the first controller pass issues the first step; every step launch then runs
@@ -898,7 +914,8 @@ int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prom
     if (g.max_steps > 0) steps = (int)std::min<int64_t>(kChunkSteps, std::max<int64_t>(0, g.max_steps - launched));
     for (int i = 0; i < steps; ++i) {
       if (timing && (rc = check(hipEventRecord(gen_events[slot][2 * i], stream), "timing event"))) return rc;
-      if ((rc = check(launch_step(stream, G, kv_f16, params_dev, &unused, epoch, kStepVerify, false, desc_dev, &ctl),
+      if ((rc = check(launch_step(stream, G, kv_f16, wtype == MTG_TYPE_F16, params_dev, &unused, epoch, kStepVerify,
+                                  false, desc_dev, &ctl),
                       "step kernel launch")))
         return rc;
       if (timing && (rc = check(hipEventRecord(gen_events[slot][2 * i + 1], stream), "timing event"))) return rc;
@@ -957,6 +974,7 @@ int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prom
     (void)hipMemset(&result_dev->err, 0, sizeof(int32_t));
     ++step_fallbacks;
   }
+  step_runs += g.steps - steps_begin;
   past = g.past;
   return MTG_OK;
 }

@@ -41,6 +41,8 @@ struct Ctx {
   uint32_t epoch = 0;
   bool abort_next = false;  // raise the error word before the next step-kernel launch
   int64_t step_fallbacks = 0;  // steps rerun on the per-op kernels after a wait ran out
+  int64_t step_runs = 0;       // steps that ran to their end on the persistent kernel
+  int step_max_keys = 0;       // KV length limit of the persistent kernel (0: the weight type's default)
   StepParams* params_dev = nullptr;
   StepParams params_host{};
   uint64_t* timing_dev = nullptr;  // step-kernel phase clock marks (profiling)

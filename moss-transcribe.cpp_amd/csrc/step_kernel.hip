@@ -416,6 +416,11 @@ __device__ __forceinline__ void gu_finish(float acc[4][G][4], float* red, float*
   bar();
 }
 
+// two floats as f16 bits (round to nearest even), the first in the low half
+__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+  return (uint32_t)__half_as_ushort(__float2half_rn(a)) | ((uint32_t)__half_as_ushort(__float2half_rn(b)) << 16);
+}
+
 // --------------------------------------------------------------- panels -----
 // 16 elements (a half q8_0 block) -> codes in the LDS panel; lanes l and l^1 hold
 // the two halves of one block.
@@ -474,7 +479,9 @@ __device__ __forceinline__ void gain16_load(const float* __restrict__ gain, floa
 // gain_late (nullable): the gains are loaded here, after the rows, instead of
 // coming prefetched in gv (the 16-row variant: 16 fewer registers held across
 // the phases, for 0.3 us more per panel).
-template <bool COAL>
+// HOUT: the normed rows leave as f16 rows [t][1024] at pcodes (the f16 GEMMs'
+// vec_dot_type; lane l writes its elements 16 l .. 16 l + 15) instead of q8_0 codes.
+template <bool COAL, bool HOUT = false>
 __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv_in)[16], float eps, uint8_t* pcodes,
                                            float* pscales, float* normed_out, float* stage,
                                            const float* gain_late = nullptr, const StepParams* prof = nullptr) {
@@ -561,7 +568,22 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv_in)[1
           const v4f o = {y[j][4 * i], y[j][4 * i + 1], y[j][4 * i + 2], y[j][4 * i + 3]};
           gst<v4f>(normed_out + (size_t)t * cH + 16 * lane + 4 * i, o);
         }
-      quant16(y[j], t, lane, cBH, pcodes, pscales);
+      if constexpr (HOUT) {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          // the float products first: the compiler would otherwise fold the last
+          // multiply and the conversion into one fma_mix (one rounding, not two)
+          float a = y[j][e], b = y[j][e + 1];
+          asm volatile("" : "+v"(a), "+v"(b));
+          h[e / 2] = pack_half2(a, b);
+        }
+        uint4* dst = (uint4*)((uint16_t*)pcodes + t * cH + 16 * lane);
+        dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
+        dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+      } else {
+        quant16(y[j], t, lane, cBH, pcodes, pscales);
+      }
     }
   }
   bar();
@@ -672,11 +694,6 @@ __device__ __forceinline__ void kv_to_lds(const KvRegs& r, float* ks, float* vs)
       }
     }
   }
-}
-
-// two floats as f16 bits (round to nearest even), the first in the low half
-__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
-  return (uint32_t)__half_as_ushort(__float2half_rn(a)) | ((uint32_t)__half_as_ushort(__float2half_rn(b)) << 16);
 }
 
 // One staging pass of an attention item: wave `wave` takes rows r0 + 4 j,
@@ -1090,8 +1107,10 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
 
 // Merge the chunk partials of (q head hq, row t) in chunk order; 128 threads,
 // thread = head_dim element d (two waves). The merged row leaves as four q8_0
-// blocks (32 lanes each). valid == false: the lanes only take part in the lane
-// exchanges.
+// blocks (32 lanes each), or (HOUT) as f16 values (the f16 o-projection's
+// vec_dot_type), two per 4-byte store. valid == false: the lanes only take part
+// in the lane exchanges.
+template <bool HOUT = false>
 __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, int hq, int t, int d,
                                            bool valid, bool prof, float* fl) {
   // the item is uniform over each wave (two waves per item): made visibly so, or
@@ -1164,6 +1183,15 @@ __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, 
   }
   if (prof) wmark(P, 1, 31);
   if (valid) out = __fdiv_rn(O, L);
+  if constexpr (HOUT) {
+    // lane d (even) stores elements d and d + 1
+    const uint32_t h = (uint32_t)__half_as_ushort(__float2half_rn(out));
+    const uint32_t pair = h | (dpp_u<kDppQuadXor1>(h) << 16);
+    if (valid && (d & 1) == 0)
+      __builtin_amdgcn_raw_buffer_store_b32(pair, mk_rsrc(P.oh, kMaxRows * cQN * 2),
+                                            (t * cQN + hq * cHD + d) * 2, 0, 16);
+    return;
+  }
   // q8_0 blocks of 32 consecutive d (32 lanes of one wave)
   const float amax = group32_max_nonneg(fabsf(out));
   // the codes of d .. d + 3 packed into lane d (d % 4 == 0) with quad permutes:
@@ -1367,6 +1395,271 @@ __device__ void accept(const uint64_t* part_keys, int32_t tok, StepResult* resul
   }
 }
 
+// ----------------------------------------------------------- f16 weights ---
+// f16 weights (vec_dot_type F16) stay in the GGUF row layout, [N][K] halves, and
+// the GEMM phases of the f16 variant spread over all 256 workgroups: q|k|v rows
+// 16 w + 4 wave + r (r < 4), o-proj and down row 4 w + wave, gate and up rows
+// 12 w + 3 wave + r (r < 3). Canonical order (mul_mat_f16 of the oracle): the
+// activation rounded to f16; lane l runs the fma chain from 0 over elements
+// [l K/64, (l + 1) K/64) (the product of two f16 values is exact in f32, and the
+// compiler folds the conversions into v_fma_mix_f32); the 64 lane partials of an
+// output meet in LDS and one lane adds them in the pairing of the xor butterfly
+// 32, 16, 8, 4, 2, 1. The variant runs 8-row steps (T <= 8).
+constexpr int kHT = 8;                 // verify-row slots
+constexpr int kHP = 68;                // words per partial row in LDS (16-byte reads)
+constexpr int cGuRows = cF / kNwg;     // 12 gate and 12 up rows per workgroup
+static_assert(cNQKV == 16 * kNwg && cH == 4 * kNwg && cGuRows == 12, "row split of the f16 variant");
+
+template <int SEG, int NM, int NR>
+struct HRows {
+  v4i w[NM][NR][SEG / 8];  // the lane's SEG halves of each row, 8 per piece
+};
+
+// NR consecutive rows starting at rows[m] (wave-uniform) of each matrix, K = 64 SEG:
+// lane l's SEG halves, non-temporal 16-byte loads.
+template <int SEG, int NM, int NR>
+__device__ __forceinline__ void h_load(const uint16_t* const (&rows)[NM], HRows<SEG, NM, NR>& g) {
+  constexpr int K = SEG * 64;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    const Rsrc r = mk_rsrc(rows[m], (uint32_t)(NR * K * 2));
+#pragma unroll
+    for (int rr = 0; rr < NR; ++rr)
+#pragma unroll
+      for (int c = 0; c < SEG / 8; ++c)
+        g.w[m][rr][c] = __builtin_bit_cast(
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(rr * K * 2 + lane * SEG * 2 + 16 * c), 0, 2));
+  }
+}
+
+// The NM x NR x T outputs of a wave's rows against the f16 activation rows s_x
+// [kHT][K] (LDS). TT verify rows per pass, their NM NR TT chains interleaved (the
+// variant has one wave per SIMD: independent chains keep the fma issue busy); the
+// activation comes in 8-element pieces, the next piece in flight during the current
+// one's chains. Rows from T on in the last pass are computed from stale LDS rows
+// and their partials written to slots no sum reads. s_p: this wave's NM NR kHT
+// partial rows. Lane j < kHT NR ends with res[m] = output (row j / kHT, verify row
+// j % kHT).
+template <int SEG, int NM, int NR, int TT>
+__device__ __forceinline__ void h_dots(const HRows<SEG, NM, NR>& g, const uint16_t* s_x, int T, float* s_p,
+                                       float (&res)[NM]) {
+  constexpr int K = SEG * 64, NC = SEG / 8;
+  static_assert(kHT % TT == 0, "passes of TT rows cover the slots");
+  const int lane = threadIdx.x & 63;
+  float wf[NM][NR][SEG];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t u = (uint32_t)g.w[m][r][c][q];
+          wf[m][r][8 * c + 2 * q] = half_bits_to_float((uint16_t)u);
+          wf[m][r][8 * c + 2 * q + 1] = half_bits_to_float((uint16_t)(u >> 16));
+        }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous call's partial reads are done
+  const uint16_t* xr = s_x + lane * SEG;
+#pragma unroll
+  for (int t0 = 0; t0 < kHT; t0 += TT) {
+    if (t0 >= T) break;
+    float acc[TT][NM][NR];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[tt][m][r] = 0.0f;
+    v4i xa[TT], xb[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) xa[tt] = *(const v4i*)(xr + (t0 + tt) * K);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      if (c + 1 < NC) {
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) xb[tt] = *(const v4i*)(xr + (t0 + tt) * K + 8 * (c + 1));
+      }
+      float xf[TT][8];
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t u = (uint32_t)xa[tt][q];
+          xf[tt][2 * q] = half_bits_to_float((uint16_t)u);
+          xf[tt][2 * q + 1] = half_bits_to_float((uint16_t)(u >> 16));
+        }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < NR; ++r) acc[tt][m][r] = fmaf(wf[m][r][8 * c + e], xf[tt][e], acc[tt][m][r]);
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) xa[tt] = xb[tt];
+    }
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) s_p[((m * NR + r) * kHT + t0 + tt) * kHP + lane] = acc[tt][m][r];
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's partial writes are done
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    float v[64];
+    const v4f* col = (const v4f*)(s_p + ((m * NR) * kHT + lane) * kHP);
+    if (lane < NR * kHT && (lane % kHT) < T) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const v4f q = col[i];
+        v[4 * i] = q[0];
+        v[4 * i + 1] = q[1];
+        v[4 * i + 2] = q[2];
+        v[4 * i + 3] = q[3];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 64; ++i) v[i] = 0.0f;
+    }
+#pragma unroll
+    for (int h = 32; h >= 1; h >>= 1)
+#pragma unroll
+      for (int i = 0; i < h; ++i) v[i] = v[i] + v[i + h];
+    res[m] = v[0];
+  }
+}
+
+// verify rows per pass of each f16 phase
+constexpr int kTTQkv = 4, kTTO = 8, kTTGu = 4, kTTD = 8, kTTLm = 4;
+
+// f16 rows [T][K] of an exchange buffer (written by other workgroups in this
+// launch) into s_x: every device-coherent 16-byte load of the thread issued before
+// the first LDS write (one round trip); pieces past the T rows read past the
+// range (zeros, no memory traffic) and are not written.
+template <int K>
+__device__ __forceinline__ void stage_h(const uint16_t* src, int T, uint16_t* s_x) {
+  constexpr int NP = kHT * K / 8 / kT;
+  const Rsrc r = mk_rsrc(src, (uint32_t)(T * K * 2));
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));  // addresses computed here, not hoisted out of the layer loop
+  v4u q[NP];
+#pragma unroll
+  for (int j = 0; j < NP; ++j) q[j] = __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)((j * kT + tid) * 16), 0, 16);
+  const int n = T * K / 8;
+#pragma unroll
+  for (int j = 0; j < NP; ++j)
+    if (j * kT + tid < n) ((v4u*)s_x)[j * kT + tid] = q[j];
+  bar();
+}
+
+// The residual add of the o-proj / down output of row 4 w + wave: lane t < T holds
+// verify row t. The workgroup is the only writer of its 4 columns: after the first
+// time they come from its LDS copy xs ([kHT][16], columns 0..3); each row's 4 new
+// values leave as one 16-byte store.
+__device__ __forceinline__ void resid_h(float v, Rsrc x, int T, float* xs, bool xs_valid) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int col = 4 * blockIdx.x + wave;
+  if (lane < T) {
+    const float old = xs_valid ? xs[lane * 16 + wave] : ldc1(x, (uint32_t)((lane * cH + col) * 4));
+    xs[lane * 16 + wave] = __fadd_rn(old, v);
+  }
+  bar();
+  if ((int)threadIdx.x < T)
+    stc4(x, (uint32_t)((threadIdx.x * cH + 4 * blockIdx.x) * 4), *(const v4f*)(xs + threadIdx.x * 16));
+  bar();
+}
+
+// The tied f16 lm_head: wave gw takes row pairs (groups) gw, gw + 1024, .. of the
+// embedding, three groups in flight; per group the canonical dots (h_dots), the
+// penalty and 64-bit first-max keys. The penalty words of the workgroup's groups
+// (its 8 rows of a group index share one bitmap word) are staged in LDS first.
+constexpr int kHLmMax = 80;  // groups per wave at most (151,936-row vocabulary: 75)
+static_assert(kStepF16MaxVocab <= 2 * 4 * kNwg * kHLmMax, "the f16 lm_head's penalty words cover the vocabulary");
+
+__device__ __forceinline__ void lm_head_h(const StepParams& P, float penalty, bool write_logits, int T,
+                                          const uint16_t* s_x, float* s_p, uint32_t* s_pen, uint64_t* s_best) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  T = __builtin_amdgcn_readfirstlane(T);
+  const int V = __builtin_amdgcn_readfirstlane(P.V), ngroups = V / 2, nwaves = kNwg * 4;
+  const int gw = blockIdx.x * 4 + wave;
+  const bool pen = penalty > 1.0f;
+  const int words = (V + 31) / 32;
+  float* const logits = uniform_ptr(P.logits);
+  const int my = gw < ngroups ? (ngroups - 1 - gw) / nwaves + 1 : 0;
+  if (pen) {
+    // group i of the workgroup's waves covers rows 8 blockIdx.x + 2048 i + 0..7:
+    // bitmap word 2 blockIdx.x / 8 + 64 i
+    const int g0 = blockIdx.x * 4, n_i = g0 < ngroups ? (ngroups - 1 - g0) / nwaves + 1 : 0;
+    const Rsrc rb = mk_rsrc(uniform_ptr(P.bitmap), (uint32_t)(kMaxRows * words * 4));
+    constexpr int NJ = (kHT * kHLmMax + kT - 1) / kT;
+    uint32_t pw[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int k = j * kT + (int)threadIdx.x, t = k / kHLmMax, i = k % kHLmMax;
+      const bool in = t < T && i < n_i;
+      pw[j] = __builtin_amdgcn_raw_buffer_load_b32(
+          rb, in ? (uint32_t)((t * words + ((2 * g0) >> 5) + i * (2 * nwaves / 32)) * 4) : 0x80000000u, 0, 16);
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int k = j * kT + (int)threadIdx.x;
+      if (k < kHT * kHLmMax) s_pen[k] = pw[j];
+    }
+    bar();
+  }
+  const Rsrc re = mk_rsrc(uniform_ptr((const uint16_t*)P.embd), (uint32_t)((size_t)V * cH * 2));
+  auto issue = [&](int i, HRows<16, 1, 2>& h) {
+    const bool in = i < my;
+    const uint32_t base = in ? (uint32_t)((gw + i * nwaves) * 2 * cH * 2) : 0u;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        h.w[0][r][c] = __builtin_bit_cast(
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                     re, in ? base + (uint32_t)(r * cH * 2 + lane * 32 + 16 * c) : 0x80000000u, 0, 2));
+  };
+  uint64_t best = 0;  // lane j < 16: verify row j % 8
+  auto group = [&](HRows<16, 1, 2>& h, int i) {
+    float res[1];
+    h_dots<16, 1, 2, kTTLm>(h, s_x, T, s_p, res);
+    issue(i + 3, h);
+    const int t = lane & 7, row = 2 * (gw + i * nwaves) + (lane >> 3);
+    if (lane < 16 && t < T) {
+      float v = res[0];
+      if (write_logits) gst<float>(logits + (size_t)t * V + row, v);
+      if (pen && ((s_pen[t * kHLmMax + i] >> (row & 31)) & 1u)) v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
+      const uint64_t key = argmax_key(v, row);
+      best = key > best ? key : best;
+    }
+  };
+  HRows<16, 1, 2> r0, r1, r2;
+  issue(0, r0);
+  issue(1, r1);
+  issue(2, r2);
+  for (int i = 0; i < my; i += 3) {
+    group(r0, i);
+    if (i + 1 < my) group(r1, i + 1);
+    if (i + 2 < my) group(r2, i + 2);
+  }
+  {
+    const uint64_t o = shfl_xor_u64(best, 8);
+    best = o > best ? o : best;
+  }
+  if (lane < kHT) s_best[wave * kMaxRows + lane] = best;
+  bar();
+  if ((int)threadIdx.x < kHT) {
+    uint64_t b = s_best[threadIdx.x];
+    for (int wv = 1; wv < 4; ++wv) b = s_best[wv * kMaxRows + threadIdx.x] > b ? s_best[wv * kMaxRows + threadIdx.x] : b;
+    st_coh_u64(P.part_keys + (size_t)blockIdx.x * kMaxRows + threadIdx.x, b);
+  }
+}
+
 // ---------------------------------------------------------------- kernel ----
 // per column group: the wave slice sums of four tiles, then the SwiGLU block maxima
 constexpr size_t kRedBytes = (size_t)4 * 4 * 4 * 64 * 4 + 4 * 16 * 4;
@@ -1396,15 +1689,27 @@ __device__ __forceinline__ const StepDesc& step_desc<false>(const StepDesc& arg,
 template <>
 __device__ __forceinline__ const StepDesc& step_desc<true>(const StepDesc&, const StepDesc* dev) { return *dev; }
 
+// LDS of the f16 variant's GEMM phases (inside the attention's region, before the
+// residual columns): the activation rows [kHT][K <= 3072] f16, each wave's partial
+// rows (at most 6 x kHT), the gate/up outputs gathered for their stores, the
+// lm_head's penalty words.
+constexpr size_t kHxBytes = (size_t)kHT * cF * 2;
+constexpr size_t kHpWave = (size_t)6 * kHT * kHP * 4;
+constexpr size_t kHgOff = kHxBytes + 4 * kHpWave;
+constexpr size_t kHpenOff = kHgOff + 256;
+static_assert(kHpenOff + (size_t)kHT * kHLmMax * 4 <= kAttnLdsBytes, "f16 GEMM LDS inside the attention's region");
+
 // The step itself; the kernel below adds the device loop's controller pass. The
 // return value matters in workgroup 0 only: true once its acceptance is done.
-template <int G, int KVH, bool PROF, bool DEV>
+// WF: 0 q8_0 weights (MFMA panel tiles), 1 f16 weights (GGUF rows; 8-row steps).
+template <int G, int KVH, bool PROF, bool DEV, int WF>
 __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, const StepDesc& desc_arg,
                                           uint32_t epoch, int mode, const StepDesc* __restrict__ desc_dev,
                                           uint8_t* lds, int& s_ok, uint64_t* s_best, uint64_t* s_red,
                                           int32_t* s_choice, int32_t* s_tok, int32_t* s_nmatch) {
 #define MARK(...) do { if constexpr (PROF) mark(__VA_ARGS__); } while (0)
 #define WMARK(...) do { if constexpr (PROF) wmark(__VA_ARGS__); } while (0)
+  static_assert(WF == 0 || G == 1, "the f16 variant runs 8-row steps");
   const StepParams& P = *Pp;
   const int w = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // The step descriptor arrives by value in the kernel arguments (no copy to
@@ -1418,6 +1723,11 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
   float* red = (float*)(lds + (size_t)G * cBF * (kPanelUnit + 4 * kScaleStride));
   float* xs = (float*)(lds + step_lds_x_offset(G));  // this workgroup's residual columns
   float* stg = (float*)(lds + step_lds_stage_offset(G));
+  // the f16 variant's GEMM space
+  uint16_t* s_x = (uint16_t*)lds;
+  float* s_p = (float*)(lds + kHxBytes + wave * kHpWave);
+  uint16_t* s_h = (uint16_t*)(lds + kHgOff);
+  uint32_t* s_pen = (uint32_t*)(lds + kHpenOff);
   bool xs_valid = false;
   Ctl c{&P, epoch, 0, &s_ok};
 #define RX mk_rsrc(P.x, kMaxRows * cH * 4)
@@ -1466,12 +1776,15 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
   // chunks run from the last down: the first one staged holds the new rows if any does
   const int att_first = att_c1 - 1;
   const bool att_new = att_c1 * kChunk > past;
-  const bool od = w < cOTiles;                    // o-proj and down tiles
-  const bool gu = w >= cOTiles && w < cOTiles + cGuBlocks;  // gate/up rows 32j..32j+31
+  // o-proj and down tiles, gate/up rows 32j..32j+31 (the f16 variant: every
+  // workgroup has rows of all three)
+  const bool gu_blk = w >= cOTiles && w < cOTiles + cGuBlocks;
+  const bool od = WF ? true : w < cOTiles;
+  const bool gu = WF ? true : gu_blk;
   const int n_merge = cNH * T;                    // (head, row) items, in pairs
   // merge pair slots: workgroups 160..255, then the gate/up workgroups (their own
   // phase comes after the o-proj), so that 16 rows need one round, not two
-  const int merge_slot = w >= kMergeWg0 ? w - kMergeWg0 : (gu ? kNwg - kMergeWg0 + (w - cOTiles) : -1);
+  const int merge_slot = w >= kMergeWg0 ? w - kMergeWg0 : (gu_blk ? kNwg - kMergeWg0 + (w - cOTiles) : -1);
   const bool has_merge = w >= kMergeWg0 || (merge_slot >= 0 && 2 * merge_slot < n_merge);
   // phase mask of this workgroup (bit p = works in phase p)
   const int mask = 1 | (has_attn ? 2 : 0) | (has_merge ? 4 : 0) | (od ? 8 | 32 : 0) | (gu ? 16 : 0);
@@ -1489,6 +1802,15 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
   uint2 bs[16];
   KvRegs kv;              // K / V of the first attention item
   float gq[16], gf[16];   // attn_norm / ffn_norm gains of the lane's 16 elements
+  // the f16 variant's rows: q|k|v, o-proj, gate|up, down
+  HRows<16, 1, 4> hqkv;
+  HRows<32, 1, 1> ho;
+  HRows<16, 2, 3> hgu;
+  HRows<48, 1, 1> hd;
+  auto h_qkv_load = [&](const LayerDev& Ly) {
+    const uint16_t* r[1] = {(const uint16_t*)Ly.wqkv + (size_t)(16 * w + 4 * wave) * cH};
+    h_load<16, 1, 4>(r, hqkv);
+  };
 
   // ---- embeddings (and the penalty bitmap) ----
   if (w < T) {
@@ -1497,6 +1819,10 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     v4f e;
     if (desc.use_embeds) {
       e = gld<v4f>(P.embeds + (size_t)t * cH + k);
+    } else if constexpr (WF == 1) {
+      const v2u h = gld<v2u>((const uint16_t*)P.embd + (size_t)desc.tokens[t] * cH + k);
+      e = v4f{half_bits_to_float((uint16_t)h.x), half_bits_to_float((uint16_t)(h.x >> 16)),
+              half_bits_to_float((uint16_t)h.y), half_bits_to_float((uint16_t)(h.y >> 16))};
     } else {
       const int n = desc.tokens[t], tile = n >> 4, r = n & 15;
       const int bk = k >> 5, bp = bk >> 1, par = bk & 1, half = (k >> 4) & 1;
@@ -1527,7 +1853,8 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     }
   }
   // prefetch layer 0: q|k|v tile and the first attention item's K / V
-  wt_load<4>(layer_at(P, 0).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+  if constexpr (WF == 1) h_qkv_load(layer_at(P, 0));
+  else wt_load<4>(layer_at(P, 0).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
   if constexpr (G == 1) gain16_load(layer_at(P, 0).attn_norm, gq);
   if (has_attn) kv_prefetch<KVH>(layer_at(P, 0), P, att_g, att_first * kChunk, past, kv);
 
@@ -1537,10 +1864,24 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     if (!wait_all(c, ph(l, kPhQkv) - 1)) return false;
     MARK(P, 3 + 12 * l + 0);
     WMARK(P, l, 0);
-    panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, nullptr, stg, G == 1 ? nullptr : Ly.attn_norm,
-                       (PROF && P.timing && l == 1) ? &P : nullptr);
-    WMARK(P, l, 25);
-    {
+    if constexpr (WF == 1) {
+      panel_norm<true, true>(RX, T, gq, P.eps, (uint8_t*)s_x, nullptr, nullptr, stg, nullptr,
+                             (PROF && P.timing && l == 1) ? &P : nullptr);
+      WMARK(P, l, 25);
+      float res[1];
+      h_dots<16, 1, 4, kTTQkv>(hqkv, s_x, T, s_p, res);
+      WMARK(P, l, 26);
+      // (value, tag) pairs of rows 16 w + 4 wave + lane / 8, verify row lane % 8
+      const int lane = threadIdx.x & 63, t = lane & 7;
+      if (lane < 4 * kHT && t < T) {
+        const v2u pr = {__float_as_uint(res[0]), c.epoch + ph(l, kPhQkv)};
+        __builtin_amdgcn_raw_buffer_store_b64(pr, RQKVT, (t * cNQKV + 16 * w + 4 * wave + (lane >> 3)) * 8, 0, 16);
+      }
+      bar();
+    } else {
+      panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, nullptr, stg, G == 1 ? nullptr : Ly.attn_norm,
+                         (PROF && P.timing && l == 1) ? &P : nullptr);
+      WMARK(P, l, 25);
       float acc[1][G][4] = {};
       wt_mma<G, 4>(qa, qs, 4 * wave, cBH, pcodes, pscales, acc[0]);
       WMARK(P, l, 26);
@@ -1566,8 +1907,16 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     }
     // the o-proj tile's weights: issued after the attention, so that no register
     // holds them through it (the o-proj starts after the merge, well after they land)
-    if (od) wt_load<8>(Ly.wo + (size_t)w * cBQ * kUnitBytes, 8 * wave, ba, bs);
-    if (gu) {  // gate / up tiles 2j, 2j + 1 of this layer
+    if constexpr (WF == 1) {
+      const uint16_t* ro[1] = {(const uint16_t*)Ly.wo + (size_t)(4 * w + wave) * cQN};
+      h_load<32, 1, 1>(ro, ho);
+      const uint16_t* rg[2] = {(const uint16_t*)Ly.wg + (size_t)(cGuRows * w + 3 * wave) * cH,
+                               (const uint16_t*)Ly.wu + (size_t)(cGuRows * w + 3 * wave) * cH};
+      h_load<16, 2, 3>(rg, hgu);
+      gain16_load(Ly.ffn_norm, gf);
+    }
+    if (WF == 0 && od) wt_load<8>(Ly.wo + (size_t)w * cBQ * kUnitBytes, 8 * wave, ba, bs);
+    if (WF == 0 && gu) {  // gate / up tiles 2j, 2j + 1 of this layer
       const int j = w - cOTiles;
       wt_load<4>(Ly.wg + (size_t)(2 * j) * cBH * kUnitBytes, 4 * wave, ba, bs);
       wt_load<4>(Ly.wg + (size_t)(2 * j + 1) * cBH * kUnitBytes, 4 * wave, ba + 4, bs + 4);
@@ -1583,8 +1932,8 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
       for (int i0 = 2 * merge_slot; i0 < n_merge; i0 += 2 * kMergeSlots) {
         const int item = i0 + half;
         const bool valid = item < n_merge;
-        merge_item(P, T, nch, valid ? item / T : 0, valid ? item % T : 0, threadIdx.x & 127, valid,
-                   PROF && l == 1 && i0 == 2 * merge_slot, (float*)lds + wave * 128);
+        merge_item<WF == 1>(P, T, nch, valid ? item / T : 0, valid ? item % T : 0, threadIdx.x & 127, valid,
+                            PROF && l == 1 && i0 == 2 * merge_slot, (float*)lds + wave * 128);
       }
       WMARK(P, l, 22);
       publish(c, next_done(l, kPhMerge));
@@ -1601,22 +1950,37 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
       if (!wait_all(c, ph(l, kPhO) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return false;
       MARK(P, 3 + 12 * l + 4);
       WMARK(P, l, 6);
-      panel_from_q<cQN, G>(P.oq, P.oqs, T, pcodes, pscales);
-      WMARK(P, l, 27);
-      float acc[1][G][4] = {};
-      wt_mma<G, 8>(ba, bs, 8 * wave, cBQ, pcodes, pscales, acc[0]);
-      WMARK(P, l, 28);
-      gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T, xs, xs_valid);
+      if constexpr (WF == 1) {
+        stage_h<cQN>(P.oh, T, s_x);
+        WMARK(P, l, 27);
+        float res[1];
+        h_dots<32, 1, 1, kTTO>(ho, s_x, T, s_p, res);
+        WMARK(P, l, 28);
+        resid_h(res[0], RX, T, xs, xs_valid);
+      } else {
+        panel_from_q<cQN, G>(P.oq, P.oqs, T, pcodes, pscales);
+        WMARK(P, l, 27);
+        float acc[1][G][4] = {};
+        wt_mma<G, 8>(ba, bs, 8 * wave, cBQ, pcodes, pscales, acc[0]);
+        WMARK(P, l, 28);
+        gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T, xs, xs_valid);
+      }
       xs_valid = true;
       WMARK(P, l, 24);
       publish(c, next_done(l, kPhO));
       MARK(P, 3 + 12 * l + 5);
       WMARK(P, l, 7);
-      wt_load<12>(Ly.wd + (size_t)w * cBF * kUnitBytes, 12 * wave, ba, bs);
+      if constexpr (WF == 1) {
+        const uint16_t* rd[1] = {(const uint16_t*)Ly.wd + (size_t)(4 * w + wave) * cF};
+        h_load<48, 1, 1>(rd, hd);
+      } else {
+        wt_load<12>(Ly.wd + (size_t)w * cBF * kUnitBytes, 12 * wave, ba, bs);
+      }
       // the next layer's q|k|v tile and attention K / V, so that they are in flight
       // before the down wait (issued after the down phase, the tile's loads would
-      // hold up the residual rows of the next q|k|v panel: loads complete in order)
-      if (l + 1 < L) {
+      // hold up the residual rows of the next q|k|v panel: loads complete in order);
+      // the f16 variant issues them after its gate/up phase
+      if (WF == 0 && l + 1 < L) {
         wt_load<4>(layer_at(P, l + 1).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
         if constexpr (G == 1) gain16_load(layer_at(P, l + 1).attn_norm, gq);
         if (has_attn)
@@ -1627,19 +1991,44 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     if (gu) {
       if (!wait_all(c, ph(l, kPhGu) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return false;
       WMARK(P, l, 8);
-      panel_norm<G == 1>(RX, T, gf, P.eps, pcodes, pscales, nullptr, stg, G == 1 ? nullptr : Ly.ffn_norm);
-      WMARK(P, l, 27);
-      float acc[4][G][4] = {};
+      if constexpr (WF == 1) {
+        panel_norm<true, true>(RX, T, gf, P.eps, (uint8_t*)s_x, nullptr, nullptr, stg);
+        WMARK(P, l, 27);
+        float res[2];
+        h_dots<16, 2, 3, kTTGu>(hgu, s_x, T, s_p, res);
+        WMARK(P, l, 28);
+        // SwiGLU rows as f16 (the down projection's vec_dot_type); the workgroup's
+        // 12 values of each verify row meet in LDS and leave as three 8-byte stores
+        const int lane = threadIdx.x & 63, t = lane & 7;
+        if (lane < 3 * kHT && t < T) {
+          float v = dev_swiglu(res[0], res[1]);
+          // the float product first (no fma_mix: one rounding instead of two)
+          asm volatile("" : "+v"(v));
+          s_h[t * cGuRows + 3 * wave + (lane >> 3)] = __half_as_ushort(__float2half_rn(v));
+        }
+        bar();
+        if ((int)threadIdx.x < 3 * T) {
+          const int tt = threadIdx.x / 3, pc = threadIdx.x % 3;
+          const v2u v = *(const v2u*)(s_h + tt * cGuRows + 4 * pc);
+          __builtin_amdgcn_raw_buffer_store_b64(v, mk_rsrc(P.ah, kMaxRows * cF * 2),
+                                                (tt * cF + cGuRows * w + 4 * pc) * 2, 0, 16);
+        }
+      } else {
+        panel_norm<G == 1>(RX, T, gf, P.eps, pcodes, pscales, nullptr, stg, G == 1 ? nullptr : Ly.ffn_norm);
+        WMARK(P, l, 27);
+        float acc[4][G][4] = {};
 #pragma unroll
-      for (int m = 0; m < 4; ++m) wt_mma<G, 4>(ba + 4 * m, bs + 4 * m, 4 * wave, cBH, pcodes, pscales, acc[m]);
-      WMARK(P, l, 28);
-      gu_finish<G>(acc, red, red + 4 * 4 * G * 4 * 64, P, w - cOTiles, T);
+        for (int m = 0; m < 4; ++m) wt_mma<G, 4>(ba + 4 * m, bs + 4 * m, 4 * wave, cBH, pcodes, pscales, acc[m]);
+        WMARK(P, l, 28);
+        gu_finish<G>(acc, red, red + 4 * 4 * G * 4 * 64, P, w - cOTiles, T);
+      }
       WMARK(P, l, 24);
       publish(c, next_done(l, kPhGu));
       WMARK(P, l, 9);
       if (l + 1 < L) {
         const LayerDev& Ln = layer_at(P, l + 1);
-        wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
+        if constexpr (WF == 1) h_qkv_load(Ln);
+        else wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
         if constexpr (G == 1) gain16_load(Ln.attn_norm, gq);
         if (has_attn) kv_prefetch<KVH>(Ln, P, att_g, att_first * kChunk, past, kv);
       }
@@ -1649,12 +2038,21 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
       if (!wait_all(c, ph(l, kPhD) - 1)) return false;
       MARK(P, 3 + 12 * l + 6);
       WMARK(P, l, 10);
-      panel_from_q<cF, G>(P.aq, P.aqs, T, pcodes, pscales);
-      WMARK(P, l, 29);
-      float acc[1][G][4] = {};
-      wt_mma<G, 12>(ba, bs, 12 * wave, cBF, pcodes, pscales, acc[0]);
-      WMARK(P, l, 30);
-      gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T, xs, xs_valid);
+      if constexpr (WF == 1) {
+        stage_h<cF>(P.ah, T, s_x);
+        WMARK(P, l, 29);
+        float res[1];
+        h_dots<48, 1, 1, kTTD>(hd, s_x, T, s_p, res);
+        WMARK(P, l, 30);
+        resid_h(res[0], RX, T, xs, xs_valid);
+      } else {
+        panel_from_q<cF, G>(P.aq, P.aqs, T, pcodes, pscales);
+        WMARK(P, l, 29);
+        float acc[1][G][4] = {};
+        wt_mma<G, 12>(ba, bs, 12 * wave, cBF, pcodes, pscales, acc[0]);
+        WMARK(P, l, 30);
+        gemm_finish<G, 1, EPI_RESID>(acc, red, RX, cH, w, T, xs, xs_valid);
+      }
       xs_valid = true;
       publish(c, next_done(l, kPhD));
       MARK(P, 3 + 12 * l + 7);
@@ -1675,7 +2073,7 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     if (w == 0) {
       if (!wait_all(c, lm - 1)) return false;
       if constexpr (G == 1) gain16_load(P.out_norm, gq);
-      panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, P.hid, stg, G == 1 ? nullptr : P.out_norm);
+      panel_norm<G == 1, WF == 1>(RX, T, gq, P.eps, pcodes, pscales, P.hid, stg, G == 1 ? nullptr : P.out_norm);
       MARK(P, 2);
     }
     return false;
@@ -1683,8 +2081,10 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
   if (!wait_all(c, lm - 1)) return false;
   MARK(P, 3 + 12 * L);
   if constexpr (G == 1) gain16_load(P.out_norm, gq);
-  panel_norm<G == 1>(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr, stg, G == 1 ? nullptr : P.out_norm);
-  lm_head<G>(P, desc.penalty, desc.write_logits != 0, T, pcodes, pscales, s_best);
+  panel_norm<G == 1, WF == 1>(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr, stg,
+                              G == 1 ? nullptr : P.out_norm);
+  if constexpr (WF == 1) lm_head_h(P, desc.penalty, desc.write_logits != 0, T, s_x, s_p, s_pen, s_best);
+  else lm_head<G>(P, desc.penalty, desc.write_logits != 0, T, pcodes, pscales, s_best);
   publish(c, lm);
   MARK(P, 4 + 12 * L);
   if (w == 0) {
@@ -1712,7 +2112,7 @@ static_assert(step_lds_stage_offset(1) >= (size_t)kGenLdsIds * 4, "the controlle
 // workgroup left at a wait that ran out) a failed step, in which case the
 // descriptor stays as it is (other workgroups may still read it) and the next
 // launches return on g->done.
-template <int G, int KVH, bool PROF, bool DEV = false>
+template <int G, int KVH, bool PROF, bool DEV = false, int WF = 0>
 __global__ void __launch_bounds__(kT, 1)
 k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoch,
         int mode, const StepDesc* __restrict__ desc_dev, GenCtl gc) {
@@ -1727,7 +2127,7 @@ k_step(const StepParams* __restrict__ Pp, const StepDesc desc_arg, uint32_t epoc
   if constexpr (DEV) {
     if (desc_dev->T == 0 || (gc.g && gc.g->done)) return;  // the controller has stopped
   }
-  const bool accepted = step_body<G, KVH, PROF, DEV>(Pp, desc_arg, epoch, mode, desc_dev, lds, s_ok, s_best, s_red,
+  const bool accepted = step_body<G, KVH, PROF, DEV, WF>(Pp, desc_arg, epoch, mode, desc_dev, lds, s_ok, s_best, s_red,
                                                      s_choice, s_tok, &s_nmatch);
   if constexpr (DEV) {
     if (gc.g && blockIdx.x == 0) {
@@ -1753,51 +2153,57 @@ uint32_t step_progress_per_step(int n_layers) { return 2u + (uint32_t)(n_layers 
 size_t step_lds_bytes(int G) { return step_lds_stage_offset(G) + (G == 1 ? (size_t)8 * kStageFloats * 4 : 0); }
 
 namespace {
-// [G - 1][f16 KV][profiled]
-const void* step_fn(int G, int kv_f16, bool prof) {
+// [G - 1][f16 KV][profiled]; the f16-weight variants: 8-row steps only
+const void* step_fn(int G, int kv_f16, bool prof, bool wf16) {
   static const void* fns[2][2][2] = {
       {{(const void*)k_step<1, 0, false>, (const void*)k_step<1, 0, true>},
        {(const void*)k_step<1, 1, false>, (const void*)k_step<1, 1, true>}},
       {{(const void*)k_step<2, 0, false>, (const void*)k_step<2, 0, true>},
        {(const void*)k_step<2, 1, false>, (const void*)k_step<2, 1, true>}}};
+  static const void* fns_h[2][2] = {
+      {(const void*)k_step<1, 0, false, false, 1>, (const void*)k_step<1, 0, true, false, 1>},
+      {(const void*)k_step<1, 1, false, false, 1>, (const void*)k_step<1, 1, true, false, 1>}};
+  if (wf16) return G == 1 ? fns_h[kv_f16 ? 1 : 0][prof ? 1 : 0] : nullptr;
   return fns[G - 1][kv_f16 ? 1 : 0][prof ? 1 : 0];
 }
 // the 8- and 16-row variants that read the descriptor from device memory
-const void* step_fn_dev(int G, int kv_f16) {
+const void* step_fn_dev(int G, int kv_f16, bool wf16) {
   static const void* fns[2][2] = {
       {(const void*)k_step<1, 0, false, true>, (const void*)k_step<1, 1, false, true>},
       {(const void*)k_step<2, 0, false, true>, (const void*)k_step<2, 1, false, true>}};
+  static const void* fns_h[2] = {(const void*)k_step<1, 0, false, true, 1>, (const void*)k_step<1, 1, false, true, 1>};
+  if (wf16) return G == 1 ? fns_h[kv_f16 ? 1 : 0] : nullptr;
   return fns[G - 1][kv_f16 ? 1 : 0];
 }
 }  // namespace
 
 hipError_t prepare_step_kernels() {
-  for (int G = 1; G <= 2; ++G)
-    for (int kv = 0; kv < 2; ++kv)
-      for (int prof = 0; prof < 2; ++prof) {
-        const hipError_t e = hipFuncSetAttribute(step_fn(G, kv, prof != 0), hipFuncAttributeMaxDynamicSharedMemorySize,
+  for (int wf = 0; wf < 2; ++wf)
+    for (int G = 1; G <= (wf ? 1 : 2); ++G)
+      for (int kv = 0; kv < 2; ++kv) {
+        for (int prof = 0; prof < 2; ++prof) {
+          const hipError_t e = hipFuncSetAttribute(step_fn(G, kv, prof != 0, wf != 0),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)step_lds_bytes(G));
+          if (e != hipSuccess) return e;
+        }
+        const hipError_t e = hipFuncSetAttribute(step_fn_dev(G, kv, wf != 0), hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)step_lds_bytes(G));
         if (e != hipSuccess) return e;
       }
-  for (int G = 1; G <= 2; ++G)
-    for (int kv = 0; kv < 2; ++kv) {
-      const hipError_t e = hipFuncSetAttribute(step_fn_dev(G, kv), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)step_lds_bytes(G));
-      if (e != hipSuccess) return e;
-    }
   return hipSuccess;
 }
 
-hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
+hipError_t launch_step(hipStream_t s, int G, int kv_f16, bool wf16, const StepParams* P, const StepDesc* desc,
                         uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev, const GenCtl* gc) {
   // desc: host memory; the launch copies it into the kernel arguments. desc_dev
   // (verify steps of up to 8 G rows): the kernel reads the descriptor there instead.
+  if (G < 1 || G > (wf16 ? 1 : 2)) return hipErrorInvalidValue;
   GenCtl ctl{};
   if (gc) ctl = *gc;
   void* args[] = {(void*)&P, (void*)desc, (void*)&epoch, (void*)&mode, (void*)&desc_dev, (void*)&ctl};
   if (desc_dev) {
-    if (G < 1 || G > 2 || profiled) return hipErrorInvalidValue;
-    return hipLaunchKernel(step_fn_dev(G, kv_f16), dim3(kNwg), dim3(kT), args, step_lds_bytes(G), s);
+    if (profiled) return hipErrorInvalidValue;
+    return hipLaunchKernel(step_fn_dev(G, kv_f16, wf16), dim3(kNwg), dim3(kT), args, step_lds_bytes(G), s);
   }
   const size_t lds = step_lds_bytes(G);
   // A plain launch: one workgroup per CU (the kernel's registers and LDS allow
@@ -1806,7 +2212,7 @@ hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, co
   // in the kernel is bounded: if another kernel holds CUs, the late workgroups
   // join when it ends, and a wait that outlasts its bound ends the step with an
   // error instead of a hang.
-  return hipLaunchKernel(step_fn(G, kv_f16, profiled), dim3(kNwg), dim3(kT), args, lds, s);
+  return hipLaunchKernel(step_fn(G, kv_f16, profiled, wf16), dim3(kNwg), dim3(kT), args, lds, s);
 }
 
 }  // namespace mtg

@@ -14,13 +14,22 @@ enum { kStepVerify = 0, kStepAppend = 1 };
 
 // One decoder layer's device tensors.
 struct LayerDev {
-  const uint8_t *wqkv, *wo, *wg, *wu, *wd;  // MFMA panel tiles
+  const uint8_t *wqkv, *wo, *wg, *wu, *wd;  // q8_0 MFMA panel tiles, or f16 rows [N][K]
   const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
   uint8_t *kc, *vc;                          // KV cache of the layer
 };
 
 // Layers the step kernel's parameter block holds.
 constexpr int kStepMaxLayers = 48;
+// Vocabulary of the f16-weight variant at most (its lm_head stages the penalty
+// words of 80 row groups per wave).
+constexpr int kStepF16MaxVocab = 163840;
+// KV length beyond which f16-weight steps take the per-op kernels by default:
+// there the persistent kernel's attention (one workgroup per CU, each walking 2+
+// chunks in turn) falls behind the per-op one (three workgroups per CU). Measured
+// on MI355X at 8 rows: 1,024 keys 1,079 vs 1,238 us, 3,072 1,263 vs 1,325, 4,096
+// 1,412 vs 1,383, 8,000 1,582 vs 1,521.
+constexpr int kStepF16MaxKeys = 3584;
 // Default wait bounds: 2^23 polls, 50 ms.
 constexpr uint32_t kWaitPolls = 1u << 23;
 constexpr uint32_t kWaitTicks = 5000000u;
@@ -42,6 +51,8 @@ struct StepParams {
   // SwiGLU output (gate/up -> down): codes [16][K] and f16-valued scales [16][K/32]
   int8_t *oq, *aq;
   float *oqs, *aqs;
+  // the same two activations as f16 rows [16][K] (f16 weights)
+  uint16_t *oh, *ah;
   uint32_t* bitmap;
   uint64_t* part_keys;      // [nwg][16]
   StepResult* result;
@@ -68,12 +79,13 @@ constexpr int kFlagStride = 32;
 uint32_t step_progress_per_step(int n_layers);
 size_t step_lds_bytes(int G);
 hipError_t prepare_step_kernels();
-// desc: the host copy of the step descriptor (passed by value as a kernel
-// argument). profiled: the variant that writes clock marks into StepParams::timing.
+// wf16: the variant for f16 weights (G == 1 only). desc: the host copy of the
+// step descriptor (passed by value as a kernel argument). profiled: the variant
+// that writes clock marks into StepParams::timing.
 // desc_dev: the variant that reads the descriptor from device memory (a device
 // loop); with gc, its workgroup 0 then runs the controller pass on the step's
 // outcome (gen_ctrl.hpp), and the launch returns at once once gc->g->done is set.
-hipError_t launch_step(hipStream_t s, int G, int kv_f16, const StepParams* P, const StepDesc* desc,
+hipError_t launch_step(hipStream_t s, int G, int kv_f16, bool wf16, const StepParams* P, const StepDesc* desc,
                         uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev = nullptr,
                         const GenCtl* gc = nullptr);
 

@@ -108,6 +108,8 @@ SIGNATURES = {
     "mtg_debug_abort_next_step": (c_int32, [c_void_p]),
     "mtg_debug_wait_limit": (c_int32, [c_void_p, c_int32]),
     "mtg_step_fallbacks": (c_int64, [c_void_p]),
+    "mtg_set_step_max_keys": (c_int32, [c_void_p, c_int32]),
+    "mtg_step_kernel_runs": (c_int64, [c_void_p]),
     "mtg_step_profile": (c_int32, [c_void_p, c_int32]),
     "mtg_launch_timing": (c_int32, [c_void_p, c_int32]),
     "mtg_launch_timing_read": (c_int32, [c_void_p, POINTER(c_double), POINTER(c_int64),
@@ -376,6 +378,14 @@ class Decoder:
     @property
     def step_fallbacks(self):
         return lib().mtg_step_fallbacks(self.ctx)
+
+    def set_step_max_keys(self, max_keys):
+        """KV length beyond which steps take the per-op graph (<= 0: the default)."""
+        self._chk(lib().mtg_set_step_max_keys(self.ctx, max_keys))
+
+    @property
+    def step_kernel_runs(self):
+        return lib().mtg_step_kernel_runs(self.ctx)
 
     def debug_buffer(self, which, width):
         out = np.empty((MAX_BATCH, width), np.float32)

@@ -23,6 +23,7 @@ CASES = [
     ("q8_0-f32kv-T4-ctx512-step", mtg.TYPE_Q8_0, mtg.TYPE_F32, 4, 512, mtg.EXEC_STEP_KERNEL),
     ("q8_0-f16kv-T16-ctx4000-step", mtg.TYPE_Q8_0, mtg.TYPE_F16, 16, 4000, mtg.EXEC_STEP_KERNEL),
     ("q8_0-f32kv-T8-ctx1600-graph", mtg.TYPE_Q8_0, mtg.TYPE_F32, 8, 1600, mtg.EXEC_GRAPH),
+    ("f16-f16kv-T8-ctx8000-step", mtg.TYPE_F16, mtg.TYPE_F16, 8, 8000, mtg.EXEC_STEP_KERNEL),
     ("f16-f16kv-T8-ctx8000-graph", mtg.TYPE_F16, mtg.TYPE_F16, 8, 8000, mtg.EXEC_GRAPH),
     ("q4_K-f16kv-T16-ctx16384-graph", mtg.TYPE_Q4_K, mtg.TYPE_F16, 16, 16384, mtg.EXEC_GRAPH),
     # the converter's default dtype: every matrix f32 (2.4 GB of weights)
@@ -51,6 +52,7 @@ def test_full_size_verify_matches_oracle(case):
     orc = oracle_py.Oracle(model, max_seq, kv)
     dec = mtg.Decoder(model, max_seq, kv)
     dec.set_exec(exec_mode)
+    dec.set_step_max_keys(1 << 30)  # the step cases run the persistent kernel at every context
     rng = np.random.default_rng(prefix + T)
     dt = np.float32 if kv == mtg.TYPE_F32 else np.float16
     # distinct seeded rows in every layer, so that a layer reading another layer's

@@ -184,6 +184,31 @@ def test_device_loop_finishes_on_the_host_after_an_abandoned_step():
     assert a.past_len == b.past_len
 
 
+@pytest.mark.parametrize("kv_type", [mtg.TYPE_F32, mtg.TYPE_F16], ids=["f32kv", "f16kv"])
+def test_device_loop_f16_weights_equals_host_loop_and_oracle(kv_type):
+    """f16 weights on the step kernel's f16 variant (8-row steps): the device loop,
+    the host loop and the oracle's controller agree with the penalty on; a device
+    loop with more than 7 drafts (16-row steps) is refused."""
+    print("device loop, f16 weights: kv %d" % kv_type, flush=True)
+    model, orc, a, b, rng = _setup(40, 600, kv_type, wtype=mtg.TYPE_F16)
+    assert a.exec_mode == mtg.EXEC_STEP_KERNEL
+    prior = _prior(rng, model.hp.vocab)
+    first = int(prior[-1])
+    kw = dict(max_steps=0, eos=-1, penalty=1.25, max_draft=7, prior=prior)
+    dev = a.generate_device(first, 200, **kw)
+    host = b.generate_from(first, 200, **kw)
+    ref = orc.generate_from(first, 200, **kw)
+    _same_run(dev, host, "device vs host")
+    _same_run(dev, ref, "device vs oracle")
+    assert dev[1].drafted_calls > 0
+    assert a.past_len == b.past_len == orc.past_len
+    assert a.step_fallbacks == 0 and b.step_fallbacks == 0
+    assert a.step_kernel_runs == dev[1].target_calls and b.step_kernel_runs == host[1].target_calls
+    with pytest.raises(mtg.MtgError) as e:
+        a.generate_device(int(dev[1].next_seed), 10, max_draft=8)
+    assert e.value.code == mtg.ERR_UNSUPPORTED
+
+
 def test_device_loop_unsupported_cases():
     model, orc, a, b, rng = _setup(10, 100)
     a.set_exec(mtg.EXEC_GRAPH)

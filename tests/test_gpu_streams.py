@@ -134,8 +134,9 @@ STREAMS = [(3, "k16-q8_0-f16kv-ctx4000-step"), (4, "k8-f16-f16kv-ctx8000-graph")
 def test_full_size_stream_all_steps(cfg_id):
     """Every greedy step of a workload (128, 128 and 64) at full size from the
     device's prefilled KV state, on the device and on the oracle: identical ids,
-    counters and appended KV rows. The q8_0 workload runs the persistent step kernel,
-    the f16 and q4_K workloads the per-op kernels from a graph."""
+    counters and appended KV rows. The q8_0 workload runs the persistent step kernel;
+    the f16 workload (8,000 keys, past the persistent kernel's default limit for f16
+    weights) and the q4_K workload the per-op kernels from a graph."""
     cfg = WORKLOADS[cfg_id]
     oracle_py.lib().orc_set_threads(THREADS)
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)

@@ -172,11 +172,14 @@ def test_generated_token_stream_matches_oracle(penalty):
 
 WTYPES = [mtg.TYPE_F16, mtg.TYPE_F32, mtg.TYPE_Q4_K]
 WT_NAMES = {mtg.TYPE_F16: "f16", mtg.TYPE_F32: "f32", mtg.TYPE_Q4_K: "q4_K"}
-WT_EXECS = [mtg.EXEC_GRAPH, mtg.EXEC_EAGER]  # the persistent kernel streams q8_0 only
+# (weight type, exec mode): the persistent kernel streams q8_0 tiles and f16 rows
+# (its 8-row steps; 16-row steps of f16 weights take the per-op kernels)
+WT_CASES = [(w, e) for w in WTYPES
+            for e in ([mtg.EXEC_STEP_KERNEL] if w == mtg.TYPE_F16 else []) + [mtg.EXEC_GRAPH, mtg.EXEC_EAGER]]
+WT_IDS = ["%s-%s" % (WT_NAMES[w], EXEC_NAMES[e]) for w, e in WT_CASES]
 
 
-@pytest.mark.parametrize("exec_mode", WT_EXECS, ids=lambda e: EXEC_NAMES[e])
-@pytest.mark.parametrize("wtype", WTYPES, ids=lambda w: WT_NAMES[w])
+@pytest.mark.parametrize("wtype,exec_mode", WT_CASES, ids=WT_IDS)
 def test_f16_f32_and_q4k_weights_verify_matches_oracle(wtype, exec_mode):
     """f16, f32 and q4_K weights (the converter's dtypes and the k-quant path): hidden
     rows, logits, choices, acceptance and the appended KV equal the oracle's, for
@@ -190,14 +193,16 @@ def test_f16_f32_and_q4k_weights_verify_matches_oracle(wtype, exec_mode):
         _close(h1, h0, "hidden T=%d" % T)
         _close(l1, l0, "logits T=%d" % T)
         assert np.array_equal(c1, c0) and m1 == m0
+    assert dec.step_fallbacks == 0  # every step-kernel step ran to its end there
+    # the persistent kernel took the 1- and 8-row steps (f16 weights, step mode)
+    assert dec.step_kernel_runs == (2 if exec_mode == mtg.EXEC_STEP_KERNEL else 0)
     k0, v0 = orc.kv_read(orc.past_len)
     k1, v1 = dec.kv_read(dec.past_len)
     _close(k1, k0, "K cache")
     _close(v1, v0, "V cache")
 
 
-@pytest.mark.parametrize("exec_mode", WT_EXECS, ids=lambda e: EXEC_NAMES[e])
-@pytest.mark.parametrize("wtype", WTYPES, ids=lambda w: WT_NAMES[w])
+@pytest.mark.parametrize("wtype,exec_mode", WT_CASES, ids=WT_IDS)
 def test_long_f16_context_matches_oracle(wtype, exec_mode):
     """A context of 8300 cached positions (130 chunks of 64 keys, more than the
     chunk attention's workgroups per kv head, so each walks several chunks with
@@ -210,6 +215,7 @@ def test_long_f16_context_matches_oracle(wtype, exec_mode):
     orc = oracle_py.Oracle(model, max_seq, mtg.TYPE_F16)
     dec = mtg.Decoder(model, max_seq, mtg.TYPE_F16)
     dec.set_exec(exec_mode)
+    dec.set_step_max_keys(1 << 30)  # the persistent kernel at this context too
     rng = np.random.default_rng(12)
     shape = (1, hp.n_kv_heads, prefix, hp.head_dim)
     k = rng.normal(0.0, 1.0, shape).astype(np.float16)
@@ -223,6 +229,51 @@ def test_long_f16_context_matches_oracle(wtype, exec_mode):
         _close(h1, h0, "hidden T=%d" % T)
         _close(l1, l0, "logits T=%d" % T)
         assert np.array_equal(c1, c0) and m1 == m0
+    assert dec.step_fallbacks == 0
+    assert dec.step_kernel_runs == (1 if exec_mode == mtg.EXEC_STEP_KERNEL else 0)  # the 5-row step
+
+
+@pytest.mark.parametrize("wtype", [mtg.TYPE_F16, mtg.TYPE_Q8_0], ids=["f16", "q8_0"])
+def test_step_kernel_key_limit(wtype):
+    """Path selection by KV length: with f16 weights an 8-row step up to 3,584 keys
+    (past + rows) runs on the persistent kernel and a longer one on the per-op
+    graph; q8_0 weights have no limit by default; mtg_set_step_max_keys moves it.
+    Every step equals the oracle."""
+    print("step kernel key limit: weights %d" % wtype, flush=True)
+    model = mtg.SynthModel(wtype, seed=21, std=0.02, gain_jitter=0.05, n_layers=1, vocab=4096)
+    hp = model.hp
+    prefix, max_seq = 3600, 3700
+    orc = oracle_py.Oracle(model, max_seq, mtg.TYPE_F16)
+    dec = mtg.Decoder(model, max_seq, mtg.TYPE_F16)
+    assert dec.exec_mode == mtg.EXEC_STEP_KERNEL
+    rng = np.random.default_rng(22)
+    shape = (1, hp.n_kv_heads, prefix, hp.head_dim)
+    k = rng.normal(0.0, 1.0, shape).astype(np.float16)
+    v = rng.normal(0.0, 0.5, shape).astype(np.float16)
+    orc.kv_write(k, v)
+    dec.kv_write(k, v)
+
+    def step(past, limit=None):
+        if limit is not None:
+            dec.set_step_max_keys(limit)
+        orc.rewind(past)
+        dec.rewind(past)
+        before = dec.step_kernel_runs
+        tokens = rng.integers(0, hp.vocab, 8)
+        c0, m0, h0, l0 = orc.verify(tokens, want_hidden=True, want_logits=True)
+        c1, m1, h1, l1 = dec.verify(tokens, want_hidden=True, want_logits=True)
+        _close(h1, h0, "hidden, past %d" % past)
+        _close(l1, l0, "logits, past %d" % past)
+        assert np.array_equal(c1, c0) and m1 == m0
+        return dec.step_kernel_runs - before
+
+    f16 = wtype == mtg.TYPE_F16  # (each step rewinds to an earlier position)
+    assert step(3577) == (0 if f16 else 1)     # 3,585 keys
+    assert step(3577, 1 << 20) == 1            # a higher limit
+    assert step(3577, 0) == (0 if f16 else 1)  # the default again
+    assert step(3576) == 1                     # 3,584 keys
+    assert step(3000, 2000) == 0               # a lower limit
+    assert dec.step_fallbacks == 0
 
 
 # (cached prefix, T, KV type): more than 32 chunks of 64 keys per kv head, so each
@@ -278,9 +329,12 @@ def test_f16_and_q4k_weights_penalty_prefill_and_stream(wtype):
     model = mtg.SynthModel(wtype, seed=9, std=0.02, gain_jitter=0.05, n_layers=2, vocab=4096)
     orc = oracle_py.Oracle(model, 512)
     dec = mtg.Decoder(model, 512)
-    assert dec.exec_mode == mtg.EXEC_GRAPH
-    with pytest.raises(Exception):
-        dec.set_exec(mtg.EXEC_STEP_KERNEL)
+    if wtype == mtg.TYPE_F16:
+        assert dec.exec_mode == mtg.EXEC_STEP_KERNEL
+    else:
+        assert dec.exec_mode == mtg.EXEC_GRAPH
+        with pytest.raises(Exception):
+            dec.set_exec(mtg.EXEC_STEP_KERNEL)
     rng = np.random.default_rng(10)
     rows = orc.embed(rng.integers(0, 4096, 37))
     ids = rng.integers(0, 4096, 5)
@@ -298,6 +352,7 @@ def test_f16_and_q4k_weights_penalty_prefill_and_stream(wtype):
     first = int(rng.integers(0, 4096))
     ids0, st0 = orc.generate_from(first, 200, max_steps=12, penalty=1.1, max_draft=7, draft=fn, user=user)
     ids1, st1 = dec.generate_from(first, 200, max_steps=12, penalty=1.1, max_draft=7, draft=fn, user=user)
+    assert dec.step_fallbacks == 0
     assert ids1.tolist() == ids0.tolist()
     assert st1.accepted == st0.accepted and st1.proposed == st0.proposed
 
