@@ -61,8 +61,8 @@ def log(msg):
 
 
 # the sources the step kernel is built from (its launch included)
-STEP_SOURCES = ("step_kernel.hip", "step_kernel.hpp", "device_common.hpp", "kernels.hpp", "mtg_internal.hpp",
-                "runtime.cpp", "runtime.hpp")
+STEP_SOURCES = ("step_kernel.hip", "step_kernel.hpp", "device_common.hpp", "lm_f16.hpp", "kernels.hpp",
+                "mtg_internal.hpp", "runtime.cpp", "runtime.hpp")
 
 
 def source_hash():

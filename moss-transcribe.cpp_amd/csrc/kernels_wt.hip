@@ -8,7 +8,7 @@
 //   k_gemm_f16 / k_gemm_q4m mul_mat(W, x) (+ add / silu*mul); k_gemm_q4k and
 //                           k_gemm_wt for other q4_K shapes
 //                                                         src/qwen3.cpp:92-97,192-193,204-216
-//   k_lm_head_f16 / k_lm_head_q4m
+//   k_lm_head_f16m / k_lm_head_q4m
 //                           tied lm_head + cpu_greedy_choice keys
 //                                                         src/qwen3_decoder.cpp:174-205,
 //                                                         src/cpu_speculative.cpp:39-50
@@ -39,6 +39,7 @@
 
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "lm_f16.hpp"
 
 namespace mtg {
 
@@ -393,7 +394,7 @@ __device__ __forceinline__ void q4k_row_dots(const uint8_t* __restrict__ wrow, c
 template <int WT, int SEG>
 __device__ __forceinline__ void row_dots(const uint8_t* w, int row, int K, const float* xa, const ActQ8K& a,
                                          int T, float* res) {
-  static_assert(WT == MTG_TYPE_Q4_K, "f16 rows go through k_gemm_f16 / k_lm_head_f16");
+  static_assert(WT == MTG_TYPE_Q4_K, "f16 rows go through k_gemm_f16 / k_lm_head_f16m");
   q4k_row_dots(w + (size_t)row * (K / 256) * 144, a, K, T, res);
 }
 
@@ -1330,65 +1331,67 @@ k_gemm_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, con
   }
 }
 
-// f16 lm_head over the rows of the tied embedding, grouped as in k_gemm_f16; per
-// verify row the best 64-bit key (value bits, lowest index on ties) of each
-// workgroup goes to part_keys (kLmWorkgroups slots per verify row: a grid of
-// kLmWorkgroups / PK workgroups writes its key in the first of its PK slots and
-// the smallest key, 0, in the others). NWV waves of NR rows per group.
-constexpr int kF16LmNWV = 8, kF16LmNR = 2, kF16LmBlocks = kLmWorkgroups / 4;  // 98.5 -> 78.5 us at T = 8 (vs 4 waves x 4 rows, 1,024 workgroups)
-template <int NWV, int NR>
-__global__ void __launch_bounds__(64 * NWV)
-k_lm_head_f16(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int vocab,
-              const uint16_t* __restrict__ xh, const uint32_t* __restrict__ bitmap, float* __restrict__ logits,
-              uint64_t* __restrict__ part_keys) {
-  constexpr int SEG = 16, K = SEG * 64, NT = 64 * NWV;
-  extern __shared__ v4i f16_lds_v4[];
-  uint16_t* s_x = (uint16_t*)f16_lds_v4;
-  const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float* s_p = (float*)(s_x + kMaxRows * K) + wave * (NR * kMaxRows * kF16PStride);
-  const bool pen = desc->penalty > 1.0f;
-  const float penalty = desc->penalty;
-  const bool write_logits = desc->write_logits != 0;
-  const int words = (vocab + 31) / 32;
-  const int ngroups = (vocab + NR - 1) / NR, nwaves = gridDim.x * NWV;
-  const uint16_t* base[1] = {(const uint16_t*)w};
-  int g = blockIdx.x * NWV + wave;
-  // two groups in flight ahead of the one being computed
-  F16Group<SEG, 1, NR> bt, bt2;
-  f16_load<SEG, 1, NR>(base, vocab, g * NR, bt);
-  if (g + nwaves < ngroups) f16_load<SEG, 1, NR>(base, vocab, (g + nwaves) * NR, bt2);
-  stage_pieces<kMaxRows * K / 8 / NT>((const v4i*)xh, T * K / 8, threadIdx.x, NT,
-                                      [&](int i) { return (v4i*)s_x + i; });
-  __syncthreads();
-  const int r = lane >> 4, t = lane & 15;
-  uint64_t best = 0;  // lane (r, t): verify row t
-  for (; g < ngroups; g += nwaves) {
-    const F16Group<SEG, 1, NR> cur = bt;
-    bt = bt2;
-    if (g + 2 * nwaves < ngroups) f16_load<SEG, 1, NR>(base, vocab, (g + 2 * nwaves) * NR, bt2);
-    float res[1];
-    f16_group<SEG, 1, NR>(cur, s_x, T, s_p, res);
-    const int row = g * NR + r;
-    if (r < NR && t < T && row < vocab) {
-      float v = res[0];
-      if (write_logits) logits[(size_t)t * vocab + row] = v;
-      if (pen && ((bitmap[(size_t)t * words + (row >> 5)] >> (row & 31)) & 1u))
-        v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
-      const uint64_t key = argmax_key(v, row);
-      best = key > best ? key : best;
-    }
+// ------------------------------------------------- f16 lm_head, f32 MFMA ----
+// The canonical f16 dots of the tied lm_head as chained v_mfma_f32_16x16x4f32
+// segment chains folded by the butterfly's tree (lm_f16.hpp), over a copy of the
+// embedding re-tiled at load time.
+//
+// k_lm16_retile: thread = (tile, piece, lane) of the copy, 16 bytes: the halves
+// 16 l + 4 s + kk (s < 4) of row 16 tile + m for the piece's two segments.
+__global__ void __launch_bounds__(256)
+k_lm16_retile(const uint16_t* __restrict__ w, int n_tiles, uint16_t* __restrict__ out) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)n_tiles * kLm16Pieces * 64) return;
+  const int lane = (int)(i & 63), q = (int)((i >> 6) & (kLm16Pieces - 1)), m = lane & 15, kk = lane >> 4;
+  const uint16_t* row = w + ((i >> 11) * 16 + m) * 1024;
+  uint32_t h[4];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const uint16_t* e = row + 16 * lm16_bitrev6(2 * q + s2) + kk;
+    h[2 * s2] = (uint32_t)e[0] | ((uint32_t)e[4] << 16);
+    h[2 * s2 + 1] = (uint32_t)e[8] | ((uint32_t)e[12] << 16);
   }
-  __shared__ uint64_t s_best[NWV][64];
-  s_best[wave][lane] = best;
+  *(uint4*)(out + i * 8) = make_uint4(h[0], h[1], h[2], h[3]);
+}
+
+// The per-op f16 lm_head: 256 workgroups of 8 waves (two per SIMD), wave gw taking
+// tiles gw, gw + 2,048, ..; the activation rows [T][1024] f16 staged in LDS, then
+// their B operands (96 KB). Per verify row the best key of each workgroup goes to
+// part_keys (kLmWorkgroups slots per row: the first of the workgroup's four, the
+// smallest key, 0, in the others).
+constexpr int kLm16NWV = 8, kLm16Blocks = kLmWorkgroups / 4;
+constexpr size_t kLm16LdsBytes = (size_t)kLm16BFloats * 4 + (size_t)kMaxRows * 1024 * 2;
+
+__global__ void __launch_bounds__(64 * kLm16NWV)
+k_lm_head_f16m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int vocab,
+               const uint16_t* __restrict__ xh, const uint32_t* __restrict__ bitmap, float* __restrict__ logits,
+               uint64_t* __restrict__ part_keys) {
+  constexpr int NT = 64 * kLm16NWV;
+  extern __shared__ v4i lm16_lds_v4[];
+  float* s_b = (float*)lm16_lds_v4;
+  uint16_t* s_x = (uint16_t*)(s_b + kLm16BFloats);
+  const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  stage_pieces<kMaxRows * 1024 / 8 / NT>((const v4i*)xh, T * 1024 / 8, threadIdx.x, NT,
+                                         [&](int i) { return (v4i*)s_x + i; });
+  __syncthreads();
+  lm16_stage_b<NT>(s_x, T, s_b);
+  __syncthreads();
+  uint64_t b = lm16_run<16>(w, blockIdx.x * kLm16NWV + wave, gridDim.x * kLm16NWV, vocab / 16, s_b, T, vocab,
+                        desc->penalty, bitmap, desc->write_logits ? logits : nullptr);
+  // the four lanes of a verify row: m, m + 16, m + 32, m + 48
+  uint64_t o = shfl_xor_u64(b, 16);
+  b = o > b ? o : b;
+  o = shfl_xor_u64(b, 32);
+  b = o > b ? o : b;
+  __shared__ uint64_t s_best[kLm16NWV][16];
+  if (lane < 16) s_best[wave][lane] = b;
   __syncthreads();
   if ((int)threadIdx.x < T) {
-    uint64_t b = 0;
-    for (int i = 0; i < 4 * NWV; ++i) {
-      const uint64_t c = s_best[i >> 2][(i & 3) * 16 + threadIdx.x];
-      b = c > b ? c : b;
-    }
+    uint64_t best = 0;
+    for (int i = 0; i < kLm16NWV; ++i) best = s_best[i][threadIdx.x] > best ? s_best[i][threadIdx.x] : best;
     const int pk = kLmWorkgroups / gridDim.x;
-    for (int k = 0; k < pk; ++k) part_keys[((size_t)blockIdx.x * pk + k) * kMaxRows + threadIdx.x] = k == 0 ? b : 0;
+    for (int k = 0; k < pk; ++k)
+      part_keys[((size_t)blockIdx.x * pk + k) * kMaxRows + threadIdx.x] = k == 0 ? best : 0;
   }
 }
 
@@ -1649,9 +1652,8 @@ hipError_t prepare_kernels_wt() {
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)f16_lds_bytes(1024, nm_nr, epi == 2 ? f16n_nwv(2) : f16n_nwv(0)));
     if (e != hipSuccess) return e;
   }
-  return hipFuncSetAttribute((const void*)k_lm_head_f16<kF16LmNWV, kF16LmNR>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)f16_lds_bytes(1024, kF16LmNR, kF16LmNWV));
+  return hipFuncSetAttribute((const void*)k_lm_head_f16m, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)kLm16LdsBytes);
 }
 
 bool wt_shape_supported(int wtype, int k) {
@@ -1712,10 +1714,9 @@ void launch_gemm_wt(hipStream_t s, int wtype, int epi, const StepDesc* desc, con
 void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int vocab, int k,
                        const WtAct& act, const uint32_t* bitmap, float* logits, uint64_t* part_keys) {
   const dim3 grid(kLmWorkgroups), block(256);
-  if (wtype == MTG_TYPE_F16)
-    hipLaunchKernelGGL((k_lm_head_f16<kF16LmNWV, kF16LmNR>), dim3(kF16LmBlocks), dim3(64 * kF16LmNWV),
-                       f16_lds_bytes(1024, kF16LmNR, kF16LmNWV), s, desc, w, vocab, act.f16h,
-                       bitmap, logits, part_keys);
+  if (wtype == MTG_TYPE_F16)  // w: the lm_head copy of the embedding (launch_lm16_retile)
+    hipLaunchKernelGGL(k_lm_head_f16m, dim3(kLm16Blocks), dim3(64 * kLm16NWV), kLm16LdsBytes, s, desc, w, vocab,
+                       act.f16h, bitmap, logits, part_keys);
   else if (wtype == MTG_TYPE_F32) {
     const float* wf = (const float*)w;
     if (k == 1024)
@@ -1736,6 +1737,12 @@ void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uin
   else
     hipLaunchKernelGGL((k_lm_head_wt<MTG_TYPE_Q4_K, 0>), grid, block, 0, s, desc, w, vocab, k, nullptr,
                        act.q8k, bitmap, logits, part_keys);
+}
+
+void launch_lm16_retile(hipStream_t s, const uint8_t* embd, int vocab, uint8_t* out) {
+  const size_t threads = (size_t)(vocab / 16) * kLm16Pieces * 64;
+  hipLaunchKernelGGL(k_lm16_retile, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                     (const uint16_t*)embd, vocab / 16, (uint16_t*)out);
 }
 
 void launch_embed_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int hidden,

@@ -108,6 +108,8 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
                 "3072; q4_K: K a multiple of 256)", wtype);
   if ((wtype == MTG_TYPE_F16 || wtype == MTG_TYPE_F32) && H != 1024)
     return fail(MTG_ERR_UNSUPPORTED, "f16 and f32 weights need hidden 1024 (their lm_head kernels)");
+  if (wtype == MTG_TYPE_F16 && (size_t)V * 2048 >= ((size_t)1 << 31))
+    return fail(MTG_ERR_UNSUPPORTED, "f16 weights: vocabulary of at most 1,048,560 rows (the lm_head's copy)");
   if (kv_type != MTG_TYPE_F32 && kv_type != MTG_TYPE_F16)
     return fail(MTG_ERR_UNSUPPORTED, "kv type %d", kv_type);
   if (D != kHeadDim || NH != 2 * NKV || H % kPairK || QN % kPairK || F % kPairK || V % 16 ||
@@ -171,6 +173,13 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
   out_norm = (float*)dalloc(H * 4, false);
   if (!embd || !out_norm) return fail(MTG_ERR_NOMEM, "token_embd");
   if ((rc = upload_weights(d->token_embd, V, H, embd, staging))) return rc;
+  if (wtype == MTG_TYPE_F16) {  // the f16 lm_head reads a copy in its MFMA operand order
+    lm16 = (uint8_t*)dalloc(weight_bytes(V, H), false);
+    if (!lm16) return fail(MTG_ERR_NOMEM, "lm_head copy of token_embd");
+    launch_lm16_retile(stream, embd, V, lm16);
+    if ((rc = check(hipGetLastError(), "lm_head copy launch")) || (rc = check(hipStreamSynchronize(stream), "lm_head copy")))
+      return rc;
+  }
   if ((rc = check(hipMemcpy(out_norm, d->output_norm, H * 4, hipMemcpyHostToDevice), "norms")))
     return rc;
   if (staging) {
@@ -258,7 +267,7 @@ int Ctx::init_step_kernel() {
     return rc;
   const int H = hp.hidden, F = hp.intermediate, V = hp.vocab;
   // the persistent kernel streams q8_0 panel tiles, or f16 rows (8-row steps)
-  if ((wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16) || (wtype == MTG_TYPE_F16 && V > kStepF16MaxVocab) ||
+  if ((wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16) ||
       !step_kernel_supported(H, hp.n_heads, hp.n_kv_heads, hp.head_dim, F, hp.n_layers, cus) ||
       prepare_step_kernels() != hipSuccess) {
     (void)hipGetLastError();
@@ -294,6 +303,7 @@ int Ctx::init_step_kernel() {
   P.kv_f16 = kv_type == MTG_TYPE_F16;
   P.eps = hp.rms_eps;
   P.embd = embd;
+  P.lm16 = lm16;
   P.out_norm = out_norm;
   P.rope = rope;
   P.embeds = embeds_dev;
@@ -426,7 +436,7 @@ void Ctx::enqueue_wt(int mode) {
   }
   if (mode == kModeAppend) return;
   if (mode == kModeVerifyPenalty) launch_penalty_bitmap(s, desc_dev, V, bitmap);
-  launch_lm_head_wt(s, wtype, desc_dev, embd, V, H, wact, bitmap, logits, part_keys);
+  launch_lm_head_wt(s, wtype, desc_dev, wtype == MTG_TYPE_F16 ? lm16 : embd, V, H, wact, bitmap, logits, part_keys);
   launch_accept(s, desc_dev, part_keys, result_dev);
 }
 

@@ -56,6 +56,7 @@ struct Ctx {
   std::vector<void*> allocations;
   std::vector<Layer> layers;
   uint8_t* embd = nullptr;
+  uint8_t* lm16 = nullptr;  // f16 weights: the lm_head's re-tiled copy of embd
   float* out_norm = nullptr;
   float* rope = nullptr;
   uint8_t *kcache = nullptr, *vcache = nullptr;

@@ -30,6 +30,7 @@
 // computes exactly (its 4-term dot is a sequential fma chain); chunk softmax,
 // butterfly sums and the chunk merge as in device_common.hpp.
 #include "device_common.hpp"
+#include "lm_f16.hpp"
 #include "step_kernel.hpp"
 
 namespace mtg {
@@ -1574,89 +1575,29 @@ __device__ __forceinline__ void resid_h(float v, Rsrc x, int T, float* xs, bool 
   bar();
 }
 
-// The tied f16 lm_head: wave gw takes row pairs (groups) gw, gw + 1024, .. of the
-// embedding, three groups in flight; per group the canonical dots (h_dots), the
-// penalty and 64-bit first-max keys. The penalty words of the workgroup's groups
-// (its 8 rows of a group index share one bitmap word) are staged in LDS first.
-constexpr int kHLmMax = 80;  // groups per wave at most (151,936-row vocabulary: 75)
-static_assert(kStepF16MaxVocab <= 2 * 4 * kNwg * kHLmMax, "the f16 lm_head's penalty words cover the vocabulary");
-
+// The tied f16 lm_head (lm_f16.hpp): the B operands of the final normed f16 rows
+// s_x built in LDS (s_b), then wave gw takes 16-row tiles gw, gw + 1,024, .. of the
+// embedding's lm_head copy on f32 MFMA; per verify row the workgroup's best key.
 __device__ __forceinline__ void lm_head_h(const StepParams& P, float penalty, bool write_logits, int T,
-                                          const uint16_t* s_x, float* s_p, uint32_t* s_pen, uint64_t* s_best) {
+                                          const uint16_t* s_x, float* s_b, uint64_t* s_best) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   T = __builtin_amdgcn_readfirstlane(T);
-  const int V = __builtin_amdgcn_readfirstlane(P.V), ngroups = V / 2, nwaves = kNwg * 4;
-  const int gw = blockIdx.x * 4 + wave;
-  const bool pen = penalty > 1.0f;
-  const int words = (V + 31) / 32;
-  float* const logits = uniform_ptr(P.logits);
-  const int my = gw < ngroups ? (ngroups - 1 - gw) / nwaves + 1 : 0;
-  if (pen) {
-    // group i of the workgroup's waves covers rows 8 blockIdx.x + 2048 i + 0..7:
-    // bitmap word 2 blockIdx.x / 8 + 64 i
-    const int g0 = blockIdx.x * 4, n_i = g0 < ngroups ? (ngroups - 1 - g0) / nwaves + 1 : 0;
-    const Rsrc rb = mk_rsrc(uniform_ptr(P.bitmap), (uint32_t)(kMaxRows * words * 4));
-    constexpr int NJ = (kHT * kHLmMax + kT - 1) / kT;
-    uint32_t pw[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int k = j * kT + (int)threadIdx.x, t = k / kHLmMax, i = k % kHLmMax;
-      const bool in = t < T && i < n_i;
-      pw[j] = __builtin_amdgcn_raw_buffer_load_b32(
-          rb, in ? (uint32_t)((t * words + ((2 * g0) >> 5) + i * (2 * nwaves / 32)) * 4) : 0x80000000u, 0, 16);
-    }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int k = j * kT + (int)threadIdx.x;
-      if (k < kHT * kHLmMax) s_pen[k] = pw[j];
-    }
-    bar();
-  }
-  const Rsrc re = mk_rsrc(uniform_ptr((const uint16_t*)P.embd), (uint32_t)((size_t)V * cH * 2));
-  auto issue = [&](int i, HRows<16, 1, 2>& h) {
-    const bool in = i < my;
-    const uint32_t base = in ? (uint32_t)((gw + i * nwaves) * 2 * cH * 2) : 0u;
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-        h.w[0][r][c] = __builtin_bit_cast(
-            v4i, __builtin_amdgcn_raw_buffer_load_b128(
-                     re, in ? base + (uint32_t)(r * cH * 2 + lane * 32 + 16 * c) : 0x80000000u, 0, 2));
-  };
-  uint64_t best = 0;  // lane j < 16: verify row j % 8
-  auto group = [&](HRows<16, 1, 2>& h, int i) {
-    float res[1];
-    h_dots<16, 1, 2, kTTLm>(h, s_x, T, s_p, res);
-    issue(i + 3, h);
-    const int t = lane & 7, row = 2 * (gw + i * nwaves) + (lane >> 3);
-    if (lane < 16 && t < T) {
-      float v = res[0];
-      if (write_logits) gst<float>(logits + (size_t)t * V + row, v);
-      if (pen && ((s_pen[t * kHLmMax + i] >> (row & 31)) & 1u)) v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
-      const uint64_t key = argmax_key(v, row);
-      best = key > best ? key : best;
-    }
-  };
-  HRows<16, 1, 2> r0, r1, r2;
-  issue(0, r0);
-  issue(1, r1);
-  issue(2, r2);
-  for (int i = 0; i < my; i += 3) {
-    group(r0, i);
-    if (i + 1 < my) group(r1, i + 1);
-    if (i + 2 < my) group(r2, i + 2);
-  }
-  {
-    const uint64_t o = shfl_xor_u64(best, 8);
-    best = o > best ? o : best;
-  }
-  if (lane < kHT) s_best[wave * kMaxRows + lane] = best;
+  const int V = __builtin_amdgcn_readfirstlane(P.V);
+  lm16_stage_b<kT>(s_x, T, s_b);
+  bar();
+  uint64_t b = lm16_run<32>(uniform_ptr(P.lm16), blockIdx.x * 4 + wave, kNwg * 4, V / 16, s_b, T, V, penalty,
+                        uniform_ptr(P.bitmap), write_logits ? uniform_ptr(P.logits) : nullptr);
+  // the four lanes of a verify row: m, m + 16, m + 32, m + 48
+  uint64_t o = shfl_xor_u64(b, 16);
+  b = o > b ? o : b;
+  o = shfl_xor_u64(b, 32);
+  b = o > b ? o : b;
+  if (lane < kHT) s_best[wave * kMaxRows + lane] = b;
   bar();
   if ((int)threadIdx.x < kHT) {
-    uint64_t b = s_best[threadIdx.x];
-    for (int wv = 1; wv < 4; ++wv) b = s_best[wv * kMaxRows + threadIdx.x] > b ? s_best[wv * kMaxRows + threadIdx.x] : b;
-    st_coh_u64(P.part_keys + (size_t)blockIdx.x * kMaxRows + threadIdx.x, b);
+    uint64_t best = s_best[threadIdx.x];
+    for (int wv = 1; wv < 4; ++wv) best = s_best[wv * kMaxRows + threadIdx.x] > best ? s_best[wv * kMaxRows + threadIdx.x] : best;
+    st_coh_u64(P.part_keys + (size_t)blockIdx.x * kMaxRows + threadIdx.x, best);
   }
 }
 
@@ -1691,13 +1632,14 @@ __device__ __forceinline__ const StepDesc& step_desc<true>(const StepDesc&, cons
 
 // LDS of the f16 variant's GEMM phases (inside the attention's region, before the
 // residual columns): the activation rows [kHT][K <= 3072] f16, each wave's partial
-// rows (at most 6 x kHT), the gate/up outputs gathered for their stores, the
-// lm_head's penalty words.
+// rows (at most 6 x kHT), the gate/up outputs gathered for their stores; the
+// lm_head's B operands after the final rows [kHT][1024].
 constexpr size_t kHxBytes = (size_t)kHT * cF * 2;
 constexpr size_t kHpWave = (size_t)6 * kHT * kHP * 4;
 constexpr size_t kHgOff = kHxBytes + 4 * kHpWave;
-constexpr size_t kHpenOff = kHgOff + 256;
-static_assert(kHpenOff + (size_t)kHT * kHLmMax * 4 <= kAttnLdsBytes, "f16 GEMM LDS inside the attention's region");
+constexpr size_t kHbOff = (size_t)kHT * cH * 2;
+static_assert(kHgOff + 256 <= kAttnLdsBytes, "f16 GEMM LDS inside the attention's region");
+static_assert(kHbOff + (size_t)kLm16BFloats * 4 <= kAttnLdsBytes, "f16 lm_head LDS inside the attention's region");
 
 // The step itself; the kernel below adds the device loop's controller pass. The
 // return value matters in workgroup 0 only: true once its acceptance is done.
@@ -1727,7 +1669,6 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
   uint16_t* s_x = (uint16_t*)lds;
   float* s_p = (float*)(lds + kHxBytes + wave * kHpWave);
   uint16_t* s_h = (uint16_t*)(lds + kHgOff);
-  uint32_t* s_pen = (uint32_t*)(lds + kHpenOff);
   bool xs_valid = false;
   Ctl c{&P, epoch, 0, &s_ok};
 #define RX mk_rsrc(P.x, kMaxRows * cH * 4)
@@ -2083,7 +2024,7 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
   if constexpr (G == 1) gain16_load(P.out_norm, gq);
   panel_norm<G == 1, WF == 1>(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr, stg,
                               G == 1 ? nullptr : P.out_norm);
-  if constexpr (WF == 1) lm_head_h(P, desc.penalty, desc.write_logits != 0, T, s_x, s_p, s_pen, s_best);
+  if constexpr (WF == 1) lm_head_h(P, desc.penalty, desc.write_logits != 0, T, s_x, (float*)(lds + kHbOff), s_best);
   else lm_head<G>(P, desc.penalty, desc.write_logits != 0, T, pcodes, pscales, s_best);
   publish(c, lm);
   MARK(P, 4 + 12 * L);

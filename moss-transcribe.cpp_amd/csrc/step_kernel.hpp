@@ -21,9 +21,6 @@ struct LayerDev {
 
 // Layers the step kernel's parameter block holds.
 constexpr int kStepMaxLayers = 48;
-// Vocabulary of the f16-weight variant at most (its lm_head stages the penalty
-// words of 80 row groups per wave).
-constexpr int kStepF16MaxVocab = 163840;
 // KV length beyond which f16-weight steps take the per-op kernels by default:
 // there the persistent kernel's attention (one workgroup per CU, each walking 2+
 // chunks in turn) falls behind the per-op one (three workgroups per CU). Measured
@@ -42,6 +39,7 @@ struct StepParams {
   // const restrict argument, so these pointers come in with scalar loads.
   LayerDev layer[kStepMaxLayers];
   const uint8_t* embd;
+  const uint8_t* lm16;  // f16 weights: the lm_head's copy of embd (lm_f16.hpp)
   const float* out_norm;
   const float* rope;
   const float* embeds;  // host rows uploaded for append
