@@ -15,6 +15,8 @@ softmax stress rows through the device attention.
   (16,384-row prompt, K=16, 64 steps), both with an f16 cache, on the per-op kernels:
   the prompt prefilled on the device, every greedy step of the workload on both sides
   from that KV state, identical ids, counters and appended KV rows.
+* The 1,600-row workload with f16 weights on the persistent kernel's f16 variant: 128
+  greedy steps through the host loop and the device loop, identical to the oracle.
 * Attention on scores of +-10000 and -inf (tests/test_cpu_softmax.cpp:40-46), made
   by planting keys of magnitude 10^4 in the cache: bit-identical to the oracle.
 """
@@ -209,3 +211,57 @@ def test_attention_on_extreme_scores(kv_type, exec_mode):
     dec.close()
     orc.close()
     model.close()
+
+
+@pytest.mark.timeout(600)
+def test_full_size_stream_f16_weights_step_kernel():
+    """f16 weights on the persistent kernel's f16 variant at full size: the 1,600-row
+    prompt of the K=8 workload prefilled on the device, then 128 greedy steps with the
+    stream drafter through the host loop and through the device loop (a second
+    decoder from the same KV state), against the oracle: identical ids, counters and
+    appended KV rows, every step on the persistent kernel (within its 3,584-key
+    limit for f16 weights)."""
+    cfg = dict(WORKLOADS[2])
+    cfg["wtype"] = mtg.TYPE_F16
+    steps, K = 128, cfg["K"]
+    oracle_py.lib().orc_set_threads(THREADS)
+    model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
+    n_prompt = prompt_rows(cfg)
+    max_seq = n_prompt + (steps + 4) * K
+    assert max_seq <= 3584
+    dec = mtg.Decoder(model, max_seq, cfg["kv"])
+    assert dec.exec_mode == mtg.EXEC_STEP_KERNEL
+    rows, text, stream = build_prompt(model, dec.embed, cfg)
+    _log("f16 stream: device prefill of %d rows" % n_prompt)
+    hid = dec.prefill(rows)
+    first = int(np.argmax(dec.logits(hid[-1:])[0]))
+    k, v = dec.kv_read(n_prompt)
+    orc = oracle_py.Oracle(model, max_seq, cfg["kv"])
+    orc.kv_write(k, v)
+    dev = mtg.Decoder(model, max_seq, cfg["kv"])
+    dev.kv_write(k, v)
+    del k, v
+    fn, user, _keep = mtg.stream_drafter(text, stream)
+    drafter = mtg.stream_drafter(text, stream)
+    _log("f16 stream: %d greedy steps, host loop, device loop and oracle" % steps)
+    runs0 = dec.step_kernel_runs
+    ids1, st1 = dec.generate_from(first, 1 << 20, max_steps=steps, max_draft=K - 1, draft=fn, user=user)
+    ids2, st2 = dev.generate_device(first, 1 << 20, max_steps=steps, max_draft=K - 1, stream=drafter)
+    ids0, st0 = orc.generate_from(first, 1 << 20, max_steps=steps, max_draft=K - 1, draft=fn, user=user)
+    assert ids1.tolist() == ids0.tolist()
+    assert ids2.tolist() == ids0.tolist()
+    for f in ("target_calls", "drafted_calls", "proposed", "accepted", "target_input_tokens", "rewinds"):
+        assert getattr(st1, f) == getattr(st0, f), f
+        assert getattr(st2, f) == getattr(st0, f), f
+    assert st1.target_calls == steps
+    assert dec.step_kernel_runs - runs0 == steps and dev.step_kernel_runs == steps
+    assert dec.step_fallbacks == 0 and dev.step_fallbacks == 0
+    assert dec.past_len == dev.past_len == orc.past_len
+    k0, v0 = orc.kv_read(orc.past_len)
+    for d, what in ((dec, "host loop"), (dev, "device loop")):
+        k1, v1 = d.kv_read(d.past_len)
+        _same(k1[:, :, n_prompt:], k0[:, :, n_prompt:], "K rows appended by the steps (%s)" % what)
+        _same(v1[:, :, n_prompt:], v0[:, :, n_prompt:], "V rows appended by the steps (%s)" % what)
+    _log("f16 stream: %d ids, %d accepted drafts" % (len(ids1), st1.accepted))
+    for x in (dec, dev, orc, model):
+        x.close()
