@@ -237,10 +237,12 @@ int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids
  * at the state every 8 steps). Same ids, counters, stop reason and KV position
  * as mtg_generate_from with draft == NULL. No draft or commit hooks; stats carry
  * no draft time (verify_seconds is the whole run). MTG_ERR_UNSUPPORTED unless
- * the step kernel runs this model (q8_0 weights, MTG_EXEC_STEP_KERNEL);
+ * the step kernel runs this model (q8_0 or f16 weights, MTG_EXEC_STEP_KERNEL);
  * max_draft is clamped to MTG_MAX_BATCH - 1 as in mtg_generate_from (above 7 the
- * 16-row step kernel runs every step). A step abandoned on a bounded wait is
- * finished by the host controller from the same state. */
+ * 16-row step kernel runs every step; with f16 weights, whose step kernel runs 8
+ * rows, a max_draft above 7 returns MTG_ERR_UNSUPPORTED). Every step runs on the
+ * step kernel, also past mtg_set_step_max_keys. A step abandoned on a bounded wait
+ * is finished by the host controller from the same state. */
 int mtg_generate_device(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
                         int32_t max_new, int32_t max_steps, int32_t eos, float penalty, int32_t max_draft,
                         int32_t* ids_out, int32_t* n_ids_out, mtg_gen_stats* stats);
