@@ -237,10 +237,10 @@ int mtg_generate_from(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids
  * at the state every 8 steps). Same ids, counters, stop reason and KV position
  * as mtg_generate_from with draft == NULL. No draft or commit hooks; stats carry
  * no draft time (verify_seconds is the whole run). MTG_ERR_UNSUPPORTED unless
- * the step kernel runs this model (q8_0 or f16 weights, MTG_EXEC_STEP_KERNEL);
+ * the step kernel runs this model (q8_0, f16 or f32 weights, MTG_EXEC_STEP_KERNEL);
  * max_draft is clamped to MTG_MAX_BATCH - 1 as in mtg_generate_from (above 7 the
- * 16-row step kernel runs every step; with f16 weights, whose step kernel runs 8
- * rows, a max_draft above 7 returns MTG_ERR_UNSUPPORTED). Every step runs on the
+ * 16-row step kernel runs every step; with f16 or f32 weights, whose step kernel
+ * runs 8 rows, a max_draft above 7 returns MTG_ERR_UNSUPPORTED). Every step runs on the
  * step kernel, also past mtg_set_step_max_keys. A step abandoned on a bounded wait
  * is finished by the host controller from the same state. */
 int mtg_generate_device(mtg_ctx* ctx, int32_t first_seed, const int32_t* prior_ids, int32_t n_prior,
@@ -273,9 +273,9 @@ int mtg_generate_device_stream(mtg_ctx* ctx, int32_t first_seed, const int32_t* 
                                mtg_gen_stats* stats);
 
 /* How a step runs on the device. MTG_EXEC_STEP_KERNEL (the default for the
- * Qwen3-0.6B shape with q8_0 or f16 weights on a device with at least 256 CUs):
- * one persistent dataflow kernel per step (f16 weights: steps of up to 8 rows;
- * longer ones take the per-op graph). MTG_EXEC_GRAPH (the default otherwise): the
+ * Qwen3-0.6B shape with q8_0, f16 or f32 weights on a device with at least 256
+ * CUs): one persistent dataflow kernel per step (f16 and f32 weights: steps of up
+ * to 8 rows; longer ones take the per-op graph). MTG_EXEC_GRAPH (the default otherwise): the
  * per-op kernels, replayed from a captured HIP graph. MTG_EXEC_EAGER: the per-op
  * kernels launched one by one (profiling). All modes produce the same results. */
 enum { MTG_EXEC_STEP_KERNEL = 0, MTG_EXEC_GRAPH = 1, MTG_EXEC_EAGER = 2 };
@@ -286,10 +286,11 @@ int32_t mtg_exec_mode(const mtg_ctx* ctx);
  * one CPU path): in MTG_EXEC_STEP_KERNEL mode a verify / append step whose KV
  * length (past_len + rows) exceeds max_keys runs on the per-op graph instead of
  * the persistent kernel. max_keys <= 0 restores the default: no limit for q8_0
- * weights; 3,584 for f16 weights, whose per-op attention (three workgroups per CU)
- * overtakes the persistent kernel's at longer contexts on MI355X. The device loop
- * (mtg_generate_device) always runs the persistent kernel. mtg_step_kernel_runs
- * counts the steps that ran to their end on the persistent kernel. */
+ * weights; 3,584 for f16 and 5,120 for f32 weights, whose per-op attention (three
+ * workgroups per CU) overtakes the persistent kernel's at longer contexts on
+ * MI355X. The device loop (mtg_generate_device) always runs the persistent
+ * kernel. mtg_step_kernel_runs counts the steps that ran to their end on the
+ * persistent kernel. */
 int mtg_set_step_max_keys(mtg_ctx* ctx, int32_t max_keys);
 int64_t mtg_step_kernel_runs(const mtg_ctx* ctx);
 

@@ -140,12 +140,13 @@ void launch_gemm_f16_norm(hipStream_t s, int epi, const StepDesc* desc, const ui
                           const float* x, const float* gain, float eps, float* out);
 void launch_gemm_wt(hipStream_t s, int wtype, int epi, const StepDesc* desc, const uint8_t* w,
                     const uint8_t* w2, int n, int k, const WtAct& act, float* out);
-// w: the embedding as uploaded; for f16 weights its lm_head copy (launch_lm16_retile)
+// w: the embedding as uploaded; for f16 weights, and f32 with k == 1024, its lm_head
+// copy (launch_lm16_retile)
 void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int vocab, int k,
                        const WtAct& act, const uint32_t* bitmap, float* logits, uint64_t* part_keys);
-// The f16 lm_head's copy of an f16 embedding [vocab][1024] (vocab % 16 == 0,
-// vocab * 2,048 < 2^31): 16-row tiles in the MFMA operand order (lm_f16.hpp).
-void launch_lm16_retile(hipStream_t s, const uint8_t* embd, int vocab, uint8_t* out);
+// The lm_head's copy of an f16 or f32 embedding [vocab][1024] (vocab % 16 == 0, the
+// copy under 2 GiB): 16-row tiles in the MFMA operand order (lm_f16.hpp).
+void launch_lm16_retile(hipStream_t s, int wtype, const uint8_t* embd, int vocab, uint8_t* out);
 void launch_embed_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int hidden,
                      const float* host_rows, float* x);
 

@@ -1,4 +1,4 @@
-// kernels_wt.hip - the f16 and q4_K weight paths of the verify step (gfx950).
+// kernels_wt.hip - the f16, f32 and q4_K weight paths of the verify step (gfx950).
 //
 // Reference ops replaced (moss-transcribe.cpp through ggml's CPU backend; ggml
 // itself is absent, its published semantics are restated):
@@ -8,7 +8,7 @@
 //   k_gemm_f16 / k_gemm_q4m mul_mat(W, x) (+ add / silu*mul); k_gemm_q4k and
 //                           k_gemm_wt for other q4_K shapes
 //                                                         src/qwen3.cpp:92-97,192-193,204-216
-//   k_lm_head_f16m / k_lm_head_q4m
+//   k_lm_head_f16m (f16 and f32) / k_lm_head_q4m
 //                           tied lm_head + cpu_greedy_choice keys
 //                                                         src/qwen3_decoder.cpp:174-205,
 //                                                         src/cpu_speculative.cpp:39-50
@@ -1354,30 +1354,45 @@ k_lm16_retile(const uint16_t* __restrict__ w, int n_tiles, uint16_t* __restrict_
   *(uint4*)(out + i * 8) = make_uint4(h[0], h[1], h[2], h[3]);
 }
 
-// The per-op f16 lm_head: 256 workgroups of 8 waves (two per SIMD), wave gw taking
-// tiles gw, gw + 2,048, ..; the activation rows [T][1024] f16 staged in LDS, then
-// their B operands (96 KB). Per verify row the best key of each workgroup goes to
-// part_keys (kLmWorkgroups slots per row: the first of the workgroup's four, the
-// smallest key, 0, in the others).
-constexpr int kLm16NWV = 8, kLm16Blocks = kLmWorkgroups / 4;
-constexpr size_t kLm16LdsBytes = (size_t)kLm16BFloats * 4 + (size_t)kMaxRows * 1024 * 2;
+// The f32 copy: thread = (tile, piece, lane), 16 bytes: the floats 16 l + 4 s + kk
+// (s < 4) of row 16 tile + m, segment l = bitrev6(piece).
+__global__ void __launch_bounds__(256)
+k_lm32_retile(const float* __restrict__ w, int n_tiles, float* __restrict__ out) {
+  constexpr int NPC = LmTile<true>::kPieces;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)n_tiles * NPC * 64) return;
+  const int lane = (int)(i & 63), q = (int)((i >> 6) & (NPC - 1)), m = lane & 15, kk = lane >> 4;
+  const float* e = w + ((i >> 12) * 16 + m) * 1024 + 16 * lm16_bitrev6(q) + kk;
+  *(v4f*)(out + i * 4) = v4f{e[0], e[4], e[8], e[12]};
+}
 
+// The per-op lm_head of f16 (and F32: f32) weights: 256 workgroups of 8 waves (two
+// per SIMD), wave gw taking tiles gw, gw + 2,048, ..; the activation rows [T][1024]
+// staged in LDS, then their B operands (96 / 128 KB). Per verify row the best key of
+// each workgroup goes to part_keys (kLmWorkgroups slots per row: the first of the
+// workgroup's four, the smallest key, 0, in the others).
+constexpr int kLm16NWV = 8, kLm16Blocks = kLmWorkgroups / 4;
+__host__ __device__ constexpr size_t lm_lds_bytes(bool f32) {
+  return (size_t)kLm16BFloats * 4 + (size_t)kMaxRows * 1024 * (f32 ? 4 : 2);
+}
+
+template <bool F32>
 __global__ void __launch_bounds__(64 * kLm16NWV)
 k_lm_head_f16m(const StepDesc* __restrict__ desc, const uint8_t* __restrict__ w, int vocab,
-               const uint16_t* __restrict__ xh, const uint32_t* __restrict__ bitmap, float* __restrict__ logits,
+               const void* __restrict__ xa, const uint32_t* __restrict__ bitmap, float* __restrict__ logits,
                uint64_t* __restrict__ part_keys) {
-  constexpr int NT = 64 * kLm16NWV;
+  constexpr int NT = 64 * kLm16NWV, EB = F32 ? 4 : 2;
   extern __shared__ v4i lm16_lds_v4[];
   float* s_b = (float*)lm16_lds_v4;
-  uint16_t* s_x = (uint16_t*)(s_b + kLm16BFloats);
+  v4i* s_x = (v4i*)(s_b + kLm16BFloats);
   const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  stage_pieces<kMaxRows * 1024 / 8 / NT>((const v4i*)xh, T * 1024 / 8, threadIdx.x, NT,
-                                         [&](int i) { return (v4i*)s_x + i; });
+  stage_pieces<kMaxRows * 1024 * EB / 16 / NT>((const v4i*)xa, T * 1024 * EB / 16, threadIdx.x, NT,
+                                               [&](int i) { return s_x + i; });
   __syncthreads();
-  lm16_stage_b<NT>(s_x, T, s_b);
+  lm16_stage_b<NT, F32>(s_x, T, s_b);
   __syncthreads();
-  uint64_t b = lm16_run<16>(w, blockIdx.x * kLm16NWV + wave, gridDim.x * kLm16NWV, vocab / 16, s_b, T, vocab,
-                        desc->penalty, bitmap, desc->write_logits ? logits : nullptr);
+  uint64_t b = lm16_run<16, F32>(w, blockIdx.x * kLm16NWV + wave, gridDim.x * kLm16NWV, vocab / 16, s_b, T, vocab,
+                                 desc->penalty, bitmap, desc->write_logits ? logits : nullptr);
   // the four lanes of a verify row: m, m + 16, m + 32, m + 48
   uint64_t o = shfl_xor_u64(b, 16);
   b = o > b ? o : b;
@@ -1652,8 +1667,12 @@ hipError_t prepare_kernels_wt() {
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)f16_lds_bytes(1024, nm_nr, epi == 2 ? f16n_nwv(2) : f16n_nwv(0)));
     if (e != hipSuccess) return e;
   }
-  return hipFuncSetAttribute((const void*)k_lm_head_f16m, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)kLm16LdsBytes);
+  for (int f32 = 0; f32 < 2; ++f32) {
+    const hipError_t e = hipFuncSetAttribute(f32 ? (const void*)k_lm_head_f16m<true> : (const void*)k_lm_head_f16m<false>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lm_lds_bytes(f32 != 0));
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 bool wt_shape_supported(int wtype, int k) {
@@ -1715,13 +1734,13 @@ void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uin
                        const WtAct& act, const uint32_t* bitmap, float* logits, uint64_t* part_keys) {
   const dim3 grid(kLmWorkgroups), block(256);
   if (wtype == MTG_TYPE_F16)  // w: the lm_head copy of the embedding (launch_lm16_retile)
-    hipLaunchKernelGGL(k_lm_head_f16m, dim3(kLm16Blocks), dim3(64 * kLm16NWV), kLm16LdsBytes, s, desc, w, vocab,
-                       act.f16h, bitmap, logits, part_keys);
+    hipLaunchKernelGGL(k_lm_head_f16m<false>, dim3(kLm16Blocks), dim3(64 * kLm16NWV), lm_lds_bytes(false), s, desc, w,
+                       vocab, (const void*)act.f16h, bitmap, logits, part_keys);
   else if (wtype == MTG_TYPE_F32) {
     const float* wf = (const float*)w;
-    if (k == 1024)
-      hipLaunchKernelGGL((k_lm_head_f32<16, 4>), grid, block, 0, s, desc, wf, vocab, act.f32, bitmap, logits,
-                         part_keys);
+    if (k == 1024)  // w: the lm_head copy of the embedding (launch_lm16_retile)
+      hipLaunchKernelGGL(k_lm_head_f16m<true>, dim3(kLm16Blocks), dim3(64 * kLm16NWV), lm_lds_bytes(true), s, desc,
+                         w, vocab, (const void*)act.f32, bitmap, logits, part_keys);
     else if (k == 2048)
       hipLaunchKernelGGL((k_lm_head_f32<32, 2>), grid, block, 0, s, desc, wf, vocab, act.f32, bitmap, logits,
                          part_keys);
@@ -1739,10 +1758,14 @@ void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uin
                        act.q8k, bitmap, logits, part_keys);
 }
 
-void launch_lm16_retile(hipStream_t s, const uint8_t* embd, int vocab, uint8_t* out) {
-  const size_t threads = (size_t)(vocab / 16) * kLm16Pieces * 64;
-  hipLaunchKernelGGL(k_lm16_retile, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                     (const uint16_t*)embd, vocab / 16, (uint16_t*)out);
+void launch_lm16_retile(hipStream_t s, int wtype, const uint8_t* embd, int vocab, uint8_t* out) {
+  const bool f32 = wtype == MTG_TYPE_F32;
+  const size_t threads = (size_t)(vocab / 16) * (f32 ? LmTile<true>::kPieces : LmTile<false>::kPieces) * 64;
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  if (f32)
+    hipLaunchKernelGGL(k_lm32_retile, grid, dim3(256), 0, s, (const float*)embd, vocab / 16, (float*)out);
+  else
+    hipLaunchKernelGGL(k_lm16_retile, grid, dim3(256), 0, s, (const uint16_t*)embd, vocab / 16, (uint16_t*)out);
 }
 
 void launch_embed_wt(hipStream_t s, int wtype, const StepDesc* desc, const uint8_t* w, int hidden,

@@ -108,8 +108,8 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
                 "3072; q4_K: K a multiple of 256)", wtype);
   if ((wtype == MTG_TYPE_F16 || wtype == MTG_TYPE_F32) && H != 1024)
     return fail(MTG_ERR_UNSUPPORTED, "f16 and f32 weights need hidden 1024 (their lm_head kernels)");
-  if (wtype == MTG_TYPE_F16 && (size_t)V * 2048 >= ((size_t)1 << 31))
-    return fail(MTG_ERR_UNSUPPORTED, "f16 weights: vocabulary of at most 1,048,560 rows (the lm_head's copy)");
+  if ((wtype == MTG_TYPE_F16 || wtype == MTG_TYPE_F32) && weight_bytes(V, H) >= ((size_t)1 << 31))
+    return fail(MTG_ERR_UNSUPPORTED, "f16 / f32 weights: the lm_head's copy of token_embd must stay under 2 GiB");
   if (kv_type != MTG_TYPE_F32 && kv_type != MTG_TYPE_F16)
     return fail(MTG_ERR_UNSUPPORTED, "kv type %d", kv_type);
   if (D != kHeadDim || NH != 2 * NKV || H % kPairK || QN % kPairK || F % kPairK || V % 16 ||
@@ -173,10 +173,10 @@ int Ctx::init(const mtg_model_desc* d, int max_seq_in, int kv_type_in) {
   out_norm = (float*)dalloc(H * 4, false);
   if (!embd || !out_norm) return fail(MTG_ERR_NOMEM, "token_embd");
   if ((rc = upload_weights(d->token_embd, V, H, embd, staging))) return rc;
-  if (wtype == MTG_TYPE_F16) {  // the f16 lm_head reads a copy in its MFMA operand order
-    lm16 = (uint8_t*)dalloc(weight_bytes(V, H), false);
-    if (!lm16) return fail(MTG_ERR_NOMEM, "lm_head copy of token_embd");
-    launch_lm16_retile(stream, embd, V, lm16);
+  if (wtype == MTG_TYPE_F16 || wtype == MTG_TYPE_F32) {  // the lm_head reads a copy in its MFMA operand order
+    lm_copy = (uint8_t*)dalloc(weight_bytes(V, H), false);
+    if (!lm_copy) return fail(MTG_ERR_NOMEM, "lm_head copy of token_embd");
+    launch_lm16_retile(stream, wtype, embd, V, lm_copy);
     if ((rc = check(hipGetLastError(), "lm_head copy launch")) || (rc = check(hipStreamSynchronize(stream), "lm_head copy")))
       return rc;
   }
@@ -266,8 +266,8 @@ int Ctx::init_step_kernel() {
   if ((rc = check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count")))
     return rc;
   const int H = hp.hidden, F = hp.intermediate, V = hp.vocab;
-  // the persistent kernel streams q8_0 panel tiles, or f16 rows (8-row steps)
-  if ((wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16) ||
+  // the persistent kernel streams q8_0 panel tiles, or f16 / f32 rows (8-row steps)
+  if ((wtype != MTG_TYPE_Q8_0 && wtype != MTG_TYPE_F16 && wtype != MTG_TYPE_F32) ||
       !step_kernel_supported(H, hp.n_heads, hp.n_kv_heads, hp.head_dim, F, hp.n_layers, cus) ||
       prepare_step_kernels() != hipSuccess) {
     (void)hipGetLastError();
@@ -303,7 +303,7 @@ int Ctx::init_step_kernel() {
   P.kv_f16 = kv_type == MTG_TYPE_F16;
   P.eps = hp.rms_eps;
   P.embd = embd;
-  P.lm16 = lm16;
+  P.lm_copy = lm_copy;
   P.out_norm = out_norm;
   P.rope = rope;
   P.embeds = embeds_dev;
@@ -326,6 +326,11 @@ int Ctx::init_step_kernel() {
     P.oh = (uint16_t*)dalloc((size_t)kMaxRows * hp.n_heads * hp.head_dim * 2, true);
     P.ah = (uint16_t*)dalloc((size_t)kMaxRows * F * 2, true);
     if (!P.oh || !P.ah) return fail(MTG_ERR_NOMEM, "step kernel buffers");
+  }
+  if (wtype == MTG_TYPE_F32) {
+    P.o32 = (float*)dalloc((size_t)kMaxRows * hp.n_heads * hp.head_dim * 4, true);
+    P.a32 = (float*)dalloc((size_t)kMaxRows * F * 4, true);
+    if (!P.o32 || !P.a32) return fail(MTG_ERR_NOMEM, "step kernel buffers");
   }
   P.result = result_map;  // choices and n_match go straight to pinned host memory
   P.flags = (uint32_t*)dalloc((size_t)nwg * kFlagStride * 4, true);
@@ -436,7 +441,7 @@ void Ctx::enqueue_wt(int mode) {
   }
   if (mode == kModeAppend) return;
   if (mode == kModeVerifyPenalty) launch_penalty_bitmap(s, desc_dev, V, bitmap);
-  launch_lm_head_wt(s, wtype, desc_dev, wtype == MTG_TYPE_F16 ? lm16 : embd, V, H, wact, bitmap, logits, part_keys);
+  launch_lm_head_wt(s, wtype, desc_dev, lm_copy ? lm_copy : embd, V, H, wact, bitmap, logits, part_keys);
   launch_accept(s, desc_dev, part_keys, result_dev);
 }
 
@@ -445,10 +450,12 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
   const int G = (T + 7) / 8;
   int rc = MTG_OK;
   const bool step_mode = mode == kModeVerify || mode == kModeVerifyPenalty || mode == kModeAppend;
-  // the f16-weight variant of the step kernel runs steps of up to 8 rows; longer
-  // ones, and steps beyond the KV length limit, take the per-op kernels
+  // the f16- and f32-weight variants of the step kernel run steps of up to 8 rows;
+  // longer ones, and steps beyond the KV length limit, take the per-op kernels
   const int max_keys = step_max_keys > 0 ? step_max_keys
-                                         : (wtype == MTG_TYPE_F16 ? kStepF16MaxKeys : std::numeric_limits<int>::max());
+                       : wtype == MTG_TYPE_F16 ? kStepF16MaxKeys
+                       : wtype == MTG_TYPE_F32 ? kStepF32MaxKeys
+                                               : std::numeric_limits<int>::max();
   const bool on_step = exec == kExecStep && step_ok && step_mode && (wtype == MTG_TYPE_Q8_0 || G == 1) &&
                        (int64_t)past + T <= max_keys;
   const bool timed = timing && mode != kModeLogits;
@@ -471,7 +478,7 @@ int Ctx::run(int mode, int T, bool want_hidden, bool want_logits, float* hidden_
       if ((rc = check(hipMemsetAsync(&result_dev->err, 1, sizeof(int32_t), stream), "abort")))
         return rc;
     }
-    if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, wtype == MTG_TYPE_F16, params_dev, desc_host, epoch, smode,
+    if ((rc = check(launch_step(stream, G, kv_type == MTG_TYPE_F16, step_wf(), params_dev, desc_host, epoch, smode,
                                     params_host.timing != nullptr), "step kernel launch")))
       return rc;
     epoch += step_progress_per_step(hp.n_layers);
@@ -844,8 +851,8 @@ int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prom
   int rc = MTG_OK;
   if (!step_ok || exec != kExecStep || g.max_draft + 1 > kMaxRows)
     return fail(MTG_ERR_UNSUPPORTED, "device generation needs the step kernel and max_draft <= %d", kMaxRows - 1);
-  if (wtype == MTG_TYPE_F16 && g.max_draft + 1 > 8)
-    return fail(MTG_ERR_UNSUPPORTED, "device generation with f16 weights needs max_draft <= 7 (8-row steps)");
+  if ((wtype == MTG_TYPE_F16 || wtype == MTG_TYPE_F32) && g.max_draft + 1 > 8)
+    return fail(MTG_ERR_UNSUPPORTED, "device generation with f16 or f32 weights needs max_draft <= 7 (8-row steps)");
   // the 16-row step variant when a step can hold more than 8 rows
   const int G = g.max_draft + 1 > 8 ? 2 : 1;
   // the stream drafter's prompt ids and stream period, in one device buffer
@@ -924,7 +931,7 @@ int Ctx::generate_device(GenState& g, int32_t* ids, int cap, const int32_t* prom
     if (g.max_steps > 0) steps = (int)std::min<int64_t>(kChunkSteps, std::max<int64_t>(0, g.max_steps - launched));
     for (int i = 0; i < steps; ++i) {
       if (timing && (rc = check(hipEventRecord(gen_events[slot][2 * i], stream), "timing event"))) return rc;
-      if ((rc = check(launch_step(stream, G, kv_f16, wtype == MTG_TYPE_F16, params_dev, &unused, epoch, kStepVerify,
+      if ((rc = check(launch_step(stream, G, kv_f16, step_wf(), params_dev, &unused, epoch, kStepVerify,
                                   false, desc_dev, &ctl),
                       "step kernel launch")))
         return rc;

@@ -43,6 +43,8 @@ struct Ctx {
   int64_t step_fallbacks = 0;  // steps rerun on the per-op kernels after a wait ran out
   int64_t step_runs = 0;       // steps that ran to their end on the persistent kernel
   int step_max_keys = 0;       // KV length limit of the persistent kernel (0: the weight type's default)
+  // the step kernel's weight variant: 0 q8_0 tiles, 1 f16 rows, 2 f32 rows
+  int step_wf() const { return wtype == MTG_TYPE_F16 ? 1 : wtype == MTG_TYPE_F32 ? 2 : 0; }
   StepParams* params_dev = nullptr;
   StepParams params_host{};
   uint64_t* timing_dev = nullptr;  // step-kernel phase clock marks (profiling)
@@ -56,7 +58,7 @@ struct Ctx {
   std::vector<void*> allocations;
   std::vector<Layer> layers;
   uint8_t* embd = nullptr;
-  uint8_t* lm16 = nullptr;  // f16 weights: the lm_head's re-tiled copy of embd
+  uint8_t* lm_copy = nullptr;  // f16 / f32 weights: the lm_head's re-tiled copy of embd
   float* out_norm = nullptr;
   float* rope = nullptr;
   uint8_t *kcache = nullptr, *vcache = nullptr;

@@ -480,9 +480,10 @@ __device__ __forceinline__ void gain16_load(const float* __restrict__ gain, floa
 // gain_late (nullable): the gains are loaded here, after the rows, instead of
 // coming prefetched in gv (the 16-row variant: 16 fewer registers held across
 // the phases, for 0.3 us more per panel).
-// HOUT: the normed rows leave as f16 rows [t][1024] at pcodes (the f16 GEMMs'
-// vec_dot_type; lane l writes its elements 16 l .. 16 l + 15) instead of q8_0 codes.
-template <bool COAL, bool HOUT = false>
+// HOUT 1 / 2: the normed rows leave as f16 / f32 rows [t][1024] at pcodes (the f16
+// and f32 GEMMs' vec_dot_type; lane l writes its elements 16 l .. 16 l + 15) instead
+// of q8_0 codes.
+template <bool COAL, int HOUT = 0>
 __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv_in)[16], float eps, uint8_t* pcodes,
                                            float* pscales, float* normed_out, float* stage,
                                            const float* gain_late = nullptr, const StepParams* prof = nullptr) {
@@ -569,7 +570,11 @@ __device__ __forceinline__ void panel_norm(Rsrc x, int T, const float (&gv_in)[1
           const v4f o = {y[j][4 * i], y[j][4 * i + 1], y[j][4 * i + 2], y[j][4 * i + 3]};
           gst<v4f>(normed_out + (size_t)t * cH + 16 * lane + 4 * i, o);
         }
-      if constexpr (HOUT) {
+      if constexpr (HOUT == 2) {
+        v4f* dst = (v4f*)((float*)pcodes + t * cH + 16 * lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = v4f{y[j][4 * i], y[j][4 * i + 1], y[j][4 * i + 2], y[j][4 * i + 3]};
+      } else if constexpr (HOUT == 1) {
         uint32_t h[8];
 #pragma unroll
         for (int e = 0; e < 16; e += 2) {
@@ -1108,10 +1113,10 @@ __device__ __forceinline__ void attn_item(const StepParams& P, const LayerDev& L
 
 // Merge the chunk partials of (q head hq, row t) in chunk order; 128 threads,
 // thread = head_dim element d (two waves). The merged row leaves as four q8_0
-// blocks (32 lanes each), or (HOUT) as f16 values (the f16 o-projection's
-// vec_dot_type), two per 4-byte store. valid == false: the lanes only take part
-// in the lane exchanges.
-template <bool HOUT = false>
+// blocks (32 lanes each), or (HOUT 1) as f16 values (the f16 o-projection's
+// vec_dot_type), two per 4-byte store, or (HOUT 2) as f32 values. valid == false:
+// the lanes only take part in the lane exchanges.
+template <int HOUT = 0>
 __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, int hq, int t, int d,
                                            bool valid, bool prof, float* fl) {
   // the item is uniform over each wave (two waves per item): made visibly so, or
@@ -1184,7 +1189,11 @@ __device__ __forceinline__ void merge_item(const StepParams& P, int T, int nch, 
   }
   if (prof) wmark(P, 1, 31);
   if (valid) out = __fdiv_rn(O, L);
-  if constexpr (HOUT) {
+  if constexpr (HOUT == 2) {
+    if (valid) stc1(mk_rsrc(P.o32, kMaxRows * cQN * 4), (uint32_t)((t * cQN + hq * cHD + d) * 4), out);
+    return;
+  }
+  if constexpr (HOUT == 1) {
     // lane d (even) stores elements d and d + 1
     const uint32_t h = (uint32_t)__half_as_ushort(__float2half_rn(out));
     const uint32_t pair = h | (dpp_u<kDppQuadXor1>(h) << 16);
@@ -1396,41 +1405,43 @@ __device__ void accept(const uint64_t* part_keys, int32_t tok, StepResult* resul
   }
 }
 
-// ----------------------------------------------------------- f16 weights ---
-// f16 weights (vec_dot_type F16) stay in the GGUF row layout, [N][K] halves, and
-// the GEMM phases of the f16 variant spread over all 256 workgroups: q|k|v rows
-// 16 w + 4 wave + r (r < 4), o-proj and down row 4 w + wave, gate and up rows
-// 12 w + 3 wave + r (r < 3). Canonical order (mul_mat_f16 of the oracle): the
-// activation rounded to f16; lane l runs the fma chain from 0 over elements
-// [l K/64, (l + 1) K/64) (the product of two f16 values is exact in f32, and the
-// compiler folds the conversions into v_fma_mix_f32); the 64 lane partials of an
-// output meet in LDS and one lane adds them in the pairing of the xor butterfly
-// 32, 16, 8, 4, 2, 1. The variant runs 8-row steps (T <= 8).
+// ------------------------------------------------------ f16 and f32 weights ---
+// f16 weights (vec_dot_type F16) and f32 weights (vec_dot_type F32) stay in the
+// GGUF row layout, [N][K] halves or floats, and the GEMM phases of these row
+// variants spread over all 256 workgroups: q|k|v rows 16 w + 4 wave + r (r < 4),
+// o-proj and down row 4 w + wave, gate and up rows 12 w + 3 wave + r (r < 3).
+// Canonical order (mul_mat_f16 / mul_mat_f32 of the oracle): the activation
+// rounded to f16 (f16 weights) or as it is (f32); lane l runs the fma chain from 0
+// over elements [l K/64, (l + 1) K/64) (the product of two f16 values is exact in
+// f32, and the compiler folds the conversions into v_fma_mix_f32); the 64 lane
+// partials of an output meet in LDS and one lane adds them in the pairing of the
+// xor butterfly 32, 16, 8, 4, 2, 1. The variants run 8-row steps (T <= 8).
 constexpr int kHT = 8;                 // verify-row slots
 constexpr int kHP = 68;                // words per partial row in LDS (16-byte reads)
 constexpr int cGuRows = cF / kNwg;     // 12 gate and 12 up rows per workgroup
-static_assert(cNQKV == 16 * kNwg && cH == 4 * kNwg && cGuRows == 12, "row split of the f16 variant");
+static_assert(cNQKV == 16 * kNwg && cH == 4 * kNwg && cGuRows == 12, "row split of the row variants");
 
-template <int SEG, int NM, int NR>
+template <int SEG, int NM, int NR, bool F32 = false>
 struct HRows {
-  v4i w[NM][NR][SEG / 8];  // the lane's SEG halves of each row, 8 per piece
+  v4i w[NM][NR][F32 ? SEG / 4 : SEG / 8];  // the lane's SEG elements of each row, 16 bytes per piece
 };
 
-// NR consecutive rows starting at rows[m] (wave-uniform) of each matrix, K = 64 SEG:
-// lane l's SEG halves, non-temporal 16-byte loads.
-template <int SEG, int NM, int NR>
-__device__ __forceinline__ void h_load(const uint16_t* const (&rows)[NM], HRows<SEG, NM, NR>& g) {
-  constexpr int K = SEG * 64;
+// NR consecutive rows starting at rows[m] (wave-uniform) of each matrix, K = 64 SEG
+// elements of 2 (f16) or 4 (F32) bytes: lane l's SEG elements, non-temporal 16-byte
+// loads.
+template <int SEG, int NM, int NR, bool F32 = false>
+__device__ __forceinline__ void h_load(const uint8_t* const (&rows)[NM], HRows<SEG, NM, NR, F32>& g) {
+  constexpr int K = SEG * 64, EB = F32 ? 4 : 2;
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int m = 0; m < NM; ++m) {
-    const Rsrc r = mk_rsrc(rows[m], (uint32_t)(NR * K * 2));
+    const Rsrc r = mk_rsrc(rows[m], (uint32_t)(NR * K * EB));
 #pragma unroll
     for (int rr = 0; rr < NR; ++rr)
 #pragma unroll
-      for (int c = 0; c < SEG / 8; ++c)
+      for (int c = 0; c < SEG * EB / 16; ++c)
         g.w[m][rr][c] = __builtin_bit_cast(
-            v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(rr * K * 2 + lane * SEG * 2 + 16 * c), 0, 2));
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(rr * K * EB + lane * SEG * EB + 16 * c), 0, 2));
   }
 }
 
@@ -1442,10 +1453,12 @@ __device__ __forceinline__ void h_load(const uint16_t* const (&rows)[NM], HRows<
 // and their partials written to slots no sum reads. s_p: this wave's NM NR kHT
 // partial rows. Lane j < kHT NR ends with res[m] = output (row j / kHT, verify row
 // j % kHT).
-template <int SEG, int NM, int NR, int TT>
-__device__ __forceinline__ void h_dots(const HRows<SEG, NM, NR>& g, const uint16_t* s_x, int T, float* s_p,
+// F32: f32 weights and activation rows (each step of a chain one fma of two f32
+// values, the oracle's mul_mat_f32); otherwise f16 (exact products).
+template <int SEG, int NM, int NR, int TT, bool F32 = false>
+__device__ __forceinline__ void h_dots(const HRows<SEG, NM, NR, F32>& g, const void* s_xv, int T, float* s_p,
                                        float (&res)[NM]) {
-  constexpr int K = SEG * 64, NC = SEG / 8;
+  constexpr int K = SEG * 64, EB = F32 ? 4 : 2, EP = 16 / EB, NC = SEG / EP;
   static_assert(kHT % TT == 0, "passes of TT rows cover the slots");
   const int lane = threadIdx.x & 63;
   float wf[NM][NR][SEG];
@@ -1458,11 +1471,16 @@ __device__ __forceinline__ void h_dots(const HRows<SEG, NM, NR>& g, const uint16
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t u = (uint32_t)g.w[m][r][c][q];
-          wf[m][r][8 * c + 2 * q] = half_bits_to_float((uint16_t)u);
-          wf[m][r][8 * c + 2 * q + 1] = half_bits_to_float((uint16_t)(u >> 16));
+          if constexpr (F32) {
+            wf[m][r][4 * c + q] = __uint_as_float(u);
+          } else {
+            wf[m][r][8 * c + 2 * q] = half_bits_to_float((uint16_t)u);
+            wf[m][r][8 * c + 2 * q + 1] = half_bits_to_float((uint16_t)(u >> 16));
+          }
         }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous call's partial reads are done
-  const uint16_t* xr = s_x + lane * SEG;
+  // lane l's elements of row t: bytes (t K + l SEG) EB
+  const uint8_t* xr = (const uint8_t*)s_xv + lane * SEG * EB;
 #pragma unroll
   for (int t0 = 0; t0 < kHT; t0 += TT) {
     if (t0 >= T) break;
@@ -1475,30 +1493,34 @@ __device__ __forceinline__ void h_dots(const HRows<SEG, NM, NR>& g, const uint16
         for (int r = 0; r < NR; ++r) acc[tt][m][r] = 0.0f;
     v4i xa[TT], xb[TT];
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) xa[tt] = *(const v4i*)(xr + (t0 + tt) * K);
+    for (int tt = 0; tt < TT; ++tt) xa[tt] = *(const v4i*)(xr + (t0 + tt) * K * EB);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       if (c + 1 < NC) {
 #pragma unroll
-        for (int tt = 0; tt < TT; ++tt) xb[tt] = *(const v4i*)(xr + (t0 + tt) * K + 8 * (c + 1));
+        for (int tt = 0; tt < TT; ++tt) xb[tt] = *(const v4i*)(xr + (t0 + tt) * K * EB + 16 * (c + 1));
       }
-      float xf[TT][8];
+      float xf[TT][EP];
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t u = (uint32_t)xa[tt][q];
-          xf[tt][2 * q] = half_bits_to_float((uint16_t)u);
-          xf[tt][2 * q + 1] = half_bits_to_float((uint16_t)(u >> 16));
+          if constexpr (F32) {
+            xf[tt][q] = __uint_as_float(u);
+          } else {
+            xf[tt][2 * q] = half_bits_to_float((uint16_t)u);
+            xf[tt][2 * q + 1] = half_bits_to_float((uint16_t)(u >> 16));
+          }
         }
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
+      for (int e = 0; e < EP; ++e)
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
           for (int m = 0; m < NM; ++m)
 #pragma unroll
-            for (int r = 0; r < NR; ++r) acc[tt][m][r] = fmaf(wf[m][r][8 * c + e], xf[tt][e], acc[tt][m][r]);
+            for (int r = 0; r < NR; ++r) acc[tt][m][r] = fmaf(wf[m][r][EP * c + e], xf[tt][e], acc[tt][m][r]);
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) xa[tt] = xb[tt];
     }
@@ -1538,20 +1560,20 @@ __device__ __forceinline__ void h_dots(const HRows<SEG, NM, NR>& g, const uint16
 // verify rows per pass of each f16 phase
 constexpr int kTTQkv = 4, kTTO = 8, kTTGu = 4, kTTD = 8, kTTLm = 4;
 
-// f16 rows [T][K] of an exchange buffer (written by other workgroups in this
-// launch) into s_x: every device-coherent 16-byte load of the thread issued before
+// f16 (F32: f32) rows [T][K] of an exchange buffer (written by other workgroups in
+// this launch) into s_x: every device-coherent 16-byte load of the thread issued before
 // the first LDS write (one round trip); pieces past the T rows read past the
 // range (zeros, no memory traffic) and are not written.
-template <int K>
-__device__ __forceinline__ void stage_h(const uint16_t* src, int T, uint16_t* s_x) {
-  constexpr int NP = kHT * K / 8 / kT;
-  const Rsrc r = mk_rsrc(src, (uint32_t)(T * K * 2));
+template <int K, bool F32 = false>
+__device__ __forceinline__ void stage_h(const void* src, int T, void* s_x) {
+  constexpr int EB = F32 ? 4 : 2, NP = kHT * K * EB / 16 / kT;
+  const Rsrc r = mk_rsrc(src, (uint32_t)(T * K * EB));
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));  // addresses computed here, not hoisted out of the layer loop
   v4u q[NP];
 #pragma unroll
   for (int j = 0; j < NP; ++j) q[j] = __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)((j * kT + tid) * 16), 0, 16);
-  const int n = T * K / 8;
+  const int n = T * K * EB / 16;
 #pragma unroll
   for (int j = 0; j < NP; ++j)
     if (j * kT + tid < n) ((v4u*)s_x)[j * kT + tid] = q[j];
@@ -1575,18 +1597,19 @@ __device__ __forceinline__ void resid_h(float v, Rsrc x, int T, float* xs, bool 
   bar();
 }
 
-// The tied f16 lm_head (lm_f16.hpp): the B operands of the final normed f16 rows
+// The tied f16 / f32 lm_head (lm_f16.hpp): the B operands of the final normed rows
 // s_x built in LDS (s_b), then wave gw takes 16-row tiles gw, gw + 1,024, .. of the
 // embedding's lm_head copy on f32 MFMA; per verify row the workgroup's best key.
+template <bool F32>
 __device__ __forceinline__ void lm_head_h(const StepParams& P, float penalty, bool write_logits, int T,
-                                          const uint16_t* s_x, float* s_b, uint64_t* s_best) {
+                                          const void* s_x, float* s_b, uint64_t* s_best) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   T = __builtin_amdgcn_readfirstlane(T);
   const int V = __builtin_amdgcn_readfirstlane(P.V);
-  lm16_stage_b<kT>(s_x, T, s_b);
+  lm16_stage_b<kT, F32>(s_x, T, s_b);
   bar();
-  uint64_t b = lm16_run<32>(uniform_ptr(P.lm16), blockIdx.x * 4 + wave, kNwg * 4, V / 16, s_b, T, V, penalty,
-                        uniform_ptr(P.bitmap), write_logits ? uniform_ptr(P.logits) : nullptr);
+  uint64_t b = lm16_run<32, F32>(uniform_ptr(P.lm_copy), blockIdx.x * 4 + wave, kNwg * 4, V / 16, s_b, T, V,
+                                 penalty, uniform_ptr(P.bitmap), write_logits ? uniform_ptr(P.logits) : nullptr);
   // the four lanes of a verify row: m, m + 16, m + 32, m + 48
   uint64_t o = shfl_xor_u64(b, 16);
   b = o > b ? o : b;
@@ -1630,20 +1653,25 @@ __device__ __forceinline__ const StepDesc& step_desc<false>(const StepDesc& arg,
 template <>
 __device__ __forceinline__ const StepDesc& step_desc<true>(const StepDesc&, const StepDesc* dev) { return *dev; }
 
-// LDS of the f16 variant's GEMM phases (inside the attention's region, before the
-// residual columns): the activation rows [kHT][K <= 3072] f16, each wave's partial
-// rows (at most 6 x kHT), the gate/up outputs gathered for their stores; the
-// lm_head's B operands after the final rows [kHT][1024].
-constexpr size_t kHxBytes = (size_t)kHT * cF * 2;
-constexpr size_t kHpWave = (size_t)6 * kHT * kHP * 4;
-constexpr size_t kHgOff = kHxBytes + 4 * kHpWave;
-constexpr size_t kHbOff = (size_t)kHT * cH * 2;
-static_assert(kHgOff + 256 <= kAttnLdsBytes, "f16 GEMM LDS inside the attention's region");
-static_assert(kHbOff + (size_t)kLm16BFloats * 4 <= kAttnLdsBytes, "f16 lm_head LDS inside the attention's region");
+// LDS of the f16 / f32 variants' GEMM phases (inside the attention's region, before
+// the residual columns): a phase's activation rows [kHT][K] (eb bytes per element)
+// at 0, then each wave's partial rows (NM NR kHT rows of kHP words); the gate/up
+// outputs gathered for their stores at kHgOff; the lm_head's B operands after the
+// final rows [kHT][1024].
+__host__ __device__ constexpr size_t h_act_bytes(int K, int eb) { return (size_t)kHT * K * eb; }
+__host__ __device__ constexpr size_t h_part_bytes(int rows) { return (size_t)rows * kHT * kHP * 4; }
+constexpr size_t kHgOff = kAttnLdsBytes - 512;
+static_assert(h_act_bytes(cF, 4) + 4 * h_part_bytes(1) <= kHgOff, "f32 down phase inside the attention's region");
+static_assert(h_act_bytes(cQN, 4) + 4 * h_part_bytes(1) <= kHgOff, "f32 o-proj phase");
+static_assert(h_act_bytes(cH, 4) + 4 * h_part_bytes(6) <= kHgOff, "f32 gate/up phase");
+static_assert(h_act_bytes(cH, 4) + 4 * h_part_bytes(4) <= kHgOff, "f32 q|k|v phase");
+static_assert(h_act_bytes(cH, 4) + (size_t)kLm16BFloats * 4 <= kAttnLdsBytes, "f32 lm_head");
+static_assert(kHT * cGuRows * 4 <= 512, "the gate/up gather");
 
 // The step itself; the kernel below adds the device loop's controller pass. The
 // return value matters in workgroup 0 only: true once its acceptance is done.
-// WF: 0 q8_0 weights (MFMA panel tiles), 1 f16 weights (GGUF rows; 8-row steps).
+// WF: 0 q8_0 weights (MFMA panel tiles), 1 f16 and 2 f32 weights (GGUF rows; 8-row
+// steps).
 template <int G, int KVH, bool PROF, bool DEV, int WF>
 __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, const StepDesc& desc_arg,
                                           uint32_t epoch, int mode, const StepDesc* __restrict__ desc_dev,
@@ -1651,7 +1679,9 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
                                           int32_t* s_choice, int32_t* s_tok, int32_t* s_nmatch) {
 #define MARK(...) do { if constexpr (PROF) mark(__VA_ARGS__); } while (0)
 #define WMARK(...) do { if constexpr (PROF) wmark(__VA_ARGS__); } while (0)
-  static_assert(WF == 0 || G == 1, "the f16 variant runs 8-row steps");
+  static_assert(WF == 0 || G == 1, "the f16 and f32 variants run 8-row steps");
+  constexpr bool F32 = WF == 2;
+  constexpr int EB = F32 ? 4 : 2;  // bytes per weight / activation element of the row variants
   const StepParams& P = *Pp;
   const int w = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // The step descriptor arrives by value in the kernel arguments (no copy to
@@ -1665,10 +1695,11 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
   float* red = (float*)(lds + (size_t)G * cBF * (kPanelUnit + 4 * kScaleStride));
   float* xs = (float*)(lds + step_lds_x_offset(G));  // this workgroup's residual columns
   float* stg = (float*)(lds + step_lds_stage_offset(G));
-  // the f16 variant's GEMM space
-  uint16_t* s_x = (uint16_t*)lds;
-  float* s_p = (float*)(lds + kHxBytes + wave * kHpWave);
-  uint16_t* s_h = (uint16_t*)(lds + kHgOff);
+  // the f16 / f32 variants' GEMM space: the activation rows, then a phase's partial
+  // rows (K, rows of the wave)
+  void* s_x = lds;
+  auto s_p_for = [&](int K, int rows) { return (float*)(lds + h_act_bytes(K, EB) + wave * h_part_bytes(rows)); };
+  uint8_t* s_h = lds + kHgOff;
   bool xs_valid = false;
   Ctl c{&P, epoch, 0, &s_ok};
 #define RX mk_rsrc(P.x, kMaxRows * cH * 4)
@@ -1717,7 +1748,7 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
   // chunks run from the last down: the first one staged holds the new rows if any does
   const int att_first = att_c1 - 1;
   const bool att_new = att_c1 * kChunk > past;
-  // o-proj and down tiles, gate/up rows 32j..32j+31 (the f16 variant: every
+  // o-proj and down tiles, gate/up rows 32j..32j+31 (the row variants: every
   // workgroup has rows of all three)
   const bool gu_blk = w >= cOTiles && w < cOTiles + cGuBlocks;
   const bool od = WF ? true : w < cOTiles;
@@ -1743,14 +1774,14 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
   uint2 bs[16];
   KvRegs kv;              // K / V of the first attention item
   float gq[16], gf[16];   // attn_norm / ffn_norm gains of the lane's 16 elements
-  // the f16 variant's rows: q|k|v, o-proj, gate|up, down
-  HRows<16, 1, 4> hqkv;
-  HRows<32, 1, 1> ho;
-  HRows<16, 2, 3> hgu;
-  HRows<48, 1, 1> hd;
+  // the f16 / f32 variants' rows: q|k|v, o-proj, gate|up, down
+  HRows<16, 1, 4, F32> hqkv;
+  HRows<32, 1, 1, F32> ho;
+  HRows<16, 2, 3, F32> hgu;
+  HRows<48, 1, 1, F32> hd;
   auto h_qkv_load = [&](const LayerDev& Ly) {
-    const uint16_t* r[1] = {(const uint16_t*)Ly.wqkv + (size_t)(16 * w + 4 * wave) * cH};
-    h_load<16, 1, 4>(r, hqkv);
+    const uint8_t* r[1] = {Ly.wqkv + (size_t)(16 * w + 4 * wave) * cH * EB};
+    h_load<16, 1, 4, F32>(r, hqkv);
   };
 
   // ---- embeddings (and the penalty bitmap) ----
@@ -1760,6 +1791,8 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     v4f e;
     if (desc.use_embeds) {
       e = gld<v4f>(P.embeds + (size_t)t * cH + k);
+    } else if constexpr (WF == 2) {
+      e = gld<v4f>((const float*)P.embd + (size_t)desc.tokens[t] * cH + k);
     } else if constexpr (WF == 1) {
       const v2u h = gld<v2u>((const uint16_t*)P.embd + (size_t)desc.tokens[t] * cH + k);
       e = v4f{half_bits_to_float((uint16_t)h.x), half_bits_to_float((uint16_t)(h.x >> 16)),
@@ -1794,7 +1827,7 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     }
   }
   // prefetch layer 0: q|k|v tile and the first attention item's K / V
-  if constexpr (WF == 1) h_qkv_load(layer_at(P, 0));
+  if constexpr (WF != 0) h_qkv_load(layer_at(P, 0));
   else wt_load<4>(layer_at(P, 0).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
   if constexpr (G == 1) gain16_load(layer_at(P, 0).attn_norm, gq);
   if (has_attn) kv_prefetch<KVH>(layer_at(P, 0), P, att_g, att_first * kChunk, past, kv);
@@ -1805,12 +1838,12 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     if (!wait_all(c, ph(l, kPhQkv) - 1)) return false;
     MARK(P, 3 + 12 * l + 0);
     WMARK(P, l, 0);
-    if constexpr (WF == 1) {
-      panel_norm<true, true>(RX, T, gq, P.eps, (uint8_t*)s_x, nullptr, nullptr, stg, nullptr,
-                             (PROF && P.timing && l == 1) ? &P : nullptr);
+    if constexpr (WF != 0) {
+      panel_norm<true, WF>(RX, T, gq, P.eps, (uint8_t*)s_x, nullptr, nullptr, stg, nullptr,
+                           (PROF && P.timing && l == 1) ? &P : nullptr);
       WMARK(P, l, 25);
       float res[1];
-      h_dots<16, 1, 4, kTTQkv>(hqkv, s_x, T, s_p, res);
+      h_dots<16, 1, 4, kTTQkv, F32>(hqkv, s_x, T, s_p_for(cH, 4), res);
       WMARK(P, l, 26);
       // (value, tag) pairs of rows 16 w + 4 wave + lane / 8, verify row lane % 8
       const int lane = threadIdx.x & 63, t = lane & 7;
@@ -1848,12 +1881,12 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     }
     // the o-proj tile's weights: issued after the attention, so that no register
     // holds them through it (the o-proj starts after the merge, well after they land)
-    if constexpr (WF == 1) {
-      const uint16_t* ro[1] = {(const uint16_t*)Ly.wo + (size_t)(4 * w + wave) * cQN};
-      h_load<32, 1, 1>(ro, ho);
-      const uint16_t* rg[2] = {(const uint16_t*)Ly.wg + (size_t)(cGuRows * w + 3 * wave) * cH,
-                               (const uint16_t*)Ly.wu + (size_t)(cGuRows * w + 3 * wave) * cH};
-      h_load<16, 2, 3>(rg, hgu);
+    if constexpr (WF != 0) {
+      const uint8_t* ro[1] = {Ly.wo + (size_t)(4 * w + wave) * cQN * EB};
+      h_load<32, 1, 1, F32>(ro, ho);
+      const uint8_t* rg[2] = {Ly.wg + (size_t)(cGuRows * w + 3 * wave) * cH * EB,
+                              Ly.wu + (size_t)(cGuRows * w + 3 * wave) * cH * EB};
+      h_load<16, 2, 3, F32>(rg, hgu);
       gain16_load(Ly.ffn_norm, gf);
     }
     if (WF == 0 && od) wt_load<8>(Ly.wo + (size_t)w * cBQ * kUnitBytes, 8 * wave, ba, bs);
@@ -1873,7 +1906,7 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
       for (int i0 = 2 * merge_slot; i0 < n_merge; i0 += 2 * kMergeSlots) {
         const int item = i0 + half;
         const bool valid = item < n_merge;
-        merge_item<WF == 1>(P, T, nch, valid ? item / T : 0, valid ? item % T : 0, threadIdx.x & 127, valid,
+        merge_item<WF>(P, T, nch, valid ? item / T : 0, valid ? item % T : 0, threadIdx.x & 127, valid,
                             PROF && l == 1 && i0 == 2 * merge_slot, (float*)lds + wave * 128);
       }
       WMARK(P, l, 22);
@@ -1891,11 +1924,11 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
       if (!wait_all(c, ph(l, kPhO) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return false;
       MARK(P, 3 + 12 * l + 4);
       WMARK(P, l, 6);
-      if constexpr (WF == 1) {
-        stage_h<cQN>(P.oh, T, s_x);
+      if constexpr (WF != 0) {
+        stage_h<cQN, F32>(F32 ? (const void*)P.o32 : (const void*)P.oh, T, s_x);
         WMARK(P, l, 27);
         float res[1];
-        h_dots<32, 1, 1, kTTO>(ho, s_x, T, s_p, res);
+        h_dots<32, 1, 1, kTTO, F32>(ho, s_x, T, s_p_for(cQN, 1), res);
         WMARK(P, l, 28);
         resid_h(res[0], RX, T, xs, xs_valid);
       } else {
@@ -1911,16 +1944,16 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
       publish(c, next_done(l, kPhO));
       MARK(P, 3 + 12 * l + 5);
       WMARK(P, l, 7);
-      if constexpr (WF == 1) {
-        const uint16_t* rd[1] = {(const uint16_t*)Ly.wd + (size_t)(4 * w + wave) * cF};
-        h_load<48, 1, 1>(rd, hd);
+      if constexpr (WF != 0) {
+        const uint8_t* rd[1] = {Ly.wd + (size_t)(4 * w + wave) * cF * EB};
+        h_load<48, 1, 1, F32>(rd, hd);
       } else {
         wt_load<12>(Ly.wd + (size_t)w * cBF * kUnitBytes, 12 * wave, ba, bs);
       }
       // the next layer's q|k|v tile and attention K / V, so that they are in flight
       // before the down wait (issued after the down phase, the tile's loads would
       // hold up the residual rows of the next q|k|v panel: loads complete in order);
-      // the f16 variant issues them after its gate/up phase
+      // the row variants issue them after their gate/up phase
       if (WF == 0 && l + 1 < L) {
         wt_load<4>(layer_at(P, l + 1).wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
         if constexpr (G == 1) gain16_load(layer_at(P, l + 1).attn_norm, gq);
@@ -1932,27 +1965,39 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     if (gu) {
       if (!wait_all(c, ph(l, kPhGu) - 1, PROF && l == 1 ? wslot(w, 12) : -1)) return false;
       WMARK(P, l, 8);
-      if constexpr (WF == 1) {
-        panel_norm<true, true>(RX, T, gf, P.eps, (uint8_t*)s_x, nullptr, nullptr, stg);
+      if constexpr (WF != 0) {
+        panel_norm<true, WF>(RX, T, gf, P.eps, (uint8_t*)s_x, nullptr, nullptr, stg);
         WMARK(P, l, 27);
         float res[2];
-        h_dots<16, 2, 3, kTTGu>(hgu, s_x, T, s_p, res);
+        h_dots<16, 2, 3, kTTGu, F32>(hgu, s_x, T, s_p_for(cH, 6), res);
         WMARK(P, l, 28);
-        // SwiGLU rows as f16 (the down projection's vec_dot_type); the workgroup's
-        // 12 values of each verify row meet in LDS and leave as three 8-byte stores
+        // SwiGLU rows as f16 / f32 (the down projection's vec_dot_type); the
+        // workgroup's 12 values of each verify row meet in LDS and leave as three
+        // 8-byte (f16) or 16-byte (f32) stores
         const int lane = threadIdx.x & 63, t = lane & 7;
         if (lane < 3 * kHT && t < T) {
           float v = dev_swiglu(res[0], res[1]);
-          // the float product first (no fma_mix: one rounding instead of two)
-          asm volatile("" : "+v"(v));
-          s_h[t * cGuRows + 3 * wave + (lane >> 3)] = __half_as_ushort(__float2half_rn(v));
+          const int i = t * cGuRows + 3 * wave + (lane >> 3);
+          if constexpr (F32) {
+            ((float*)s_h)[i] = v;
+          } else {
+            // the float product first (no fma_mix: one rounding instead of two)
+            asm volatile("" : "+v"(v));
+            ((uint16_t*)s_h)[i] = __half_as_ushort(__float2half_rn(v));
+          }
         }
         bar();
         if ((int)threadIdx.x < 3 * T) {
           const int tt = threadIdx.x / 3, pc = threadIdx.x % 3;
-          const v2u v = *(const v2u*)(s_h + tt * cGuRows + 4 * pc);
-          __builtin_amdgcn_raw_buffer_store_b64(v, mk_rsrc(P.ah, kMaxRows * cF * 2),
-                                                (tt * cF + cGuRows * w + 4 * pc) * 2, 0, 16);
+          if constexpr (F32) {
+            const v4u v = *(const v4u*)((const float*)s_h + tt * cGuRows + 4 * pc);
+            __builtin_amdgcn_raw_buffer_store_b128(v, mk_rsrc(P.a32, kMaxRows * cF * 4),
+                                                   (tt * cF + cGuRows * w + 4 * pc) * 4, 0, 16);
+          } else {
+            const v2u v = *(const v2u*)((const uint16_t*)s_h + tt * cGuRows + 4 * pc);
+            __builtin_amdgcn_raw_buffer_store_b64(v, mk_rsrc(P.ah, kMaxRows * cF * 2),
+                                                  (tt * cF + cGuRows * w + 4 * pc) * 2, 0, 16);
+          }
         }
       } else {
         panel_norm<G == 1>(RX, T, gf, P.eps, pcodes, pscales, nullptr, stg, G == 1 ? nullptr : Ly.ffn_norm);
@@ -1968,7 +2013,7 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
       WMARK(P, l, 9);
       if (l + 1 < L) {
         const LayerDev& Ln = layer_at(P, l + 1);
-        if constexpr (WF == 1) h_qkv_load(Ln);
+        if constexpr (WF != 0) h_qkv_load(Ln);
         else wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);
         if constexpr (G == 1) gain16_load(Ln.attn_norm, gq);
         if (has_attn) kv_prefetch<KVH>(Ln, P, att_g, att_first * kChunk, past, kv);
@@ -1979,11 +2024,11 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
       if (!wait_all(c, ph(l, kPhD) - 1)) return false;
       MARK(P, 3 + 12 * l + 6);
       WMARK(P, l, 10);
-      if constexpr (WF == 1) {
-        stage_h<cF>(P.ah, T, s_x);
+      if constexpr (WF != 0) {
+        stage_h<cF, F32>(F32 ? (const void*)P.a32 : (const void*)P.ah, T, s_x);
         WMARK(P, l, 29);
         float res[1];
-        h_dots<48, 1, 1, kTTD>(hd, s_x, T, s_p, res);
+        h_dots<48, 1, 1, kTTD, F32>(hd, s_x, T, s_p_for(cF, 1), res);
         WMARK(P, l, 30);
         resid_h(res[0], RX, T, xs, xs_valid);
       } else {
@@ -2014,7 +2059,7 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
     if (w == 0) {
       if (!wait_all(c, lm - 1)) return false;
       if constexpr (G == 1) gain16_load(P.out_norm, gq);
-      panel_norm<G == 1, WF == 1>(RX, T, gq, P.eps, pcodes, pscales, P.hid, stg, G == 1 ? nullptr : P.out_norm);
+      panel_norm<G == 1, WF>(RX, T, gq, P.eps, pcodes, pscales, P.hid, stg, G == 1 ? nullptr : P.out_norm);
       MARK(P, 2);
     }
     return false;
@@ -2022,9 +2067,10 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
   if (!wait_all(c, lm - 1)) return false;
   MARK(P, 3 + 12 * L);
   if constexpr (G == 1) gain16_load(P.out_norm, gq);
-  panel_norm<G == 1, WF == 1>(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr, stg,
-                              G == 1 ? nullptr : P.out_norm);
-  if constexpr (WF == 1) lm_head_h(P, desc.penalty, desc.write_logits != 0, T, s_x, (float*)(lds + kHbOff), s_best);
+  panel_norm<G == 1, WF>(RX, T, gq, P.eps, pcodes, pscales, w == 0 ? P.hid : nullptr, stg,
+                         G == 1 ? nullptr : P.out_norm);
+  if constexpr (WF != 0)
+    lm_head_h<F32>(P, desc.penalty, desc.write_logits != 0, T, s_x, (float*)(lds + h_act_bytes(cH, EB)), s_best);
   else lm_head<G>(P, desc.penalty, desc.write_logits != 0, T, pcodes, pscales, s_best);
   publish(c, lm);
   MARK(P, 4 + 12 * L);
@@ -2094,57 +2140,61 @@ uint32_t step_progress_per_step(int n_layers) { return 2u + (uint32_t)(n_layers 
 size_t step_lds_bytes(int G) { return step_lds_stage_offset(G) + (G == 1 ? (size_t)8 * kStageFloats * 4 : 0); }
 
 namespace {
-// [G - 1][f16 KV][profiled]; the f16-weight variants: 8-row steps only
-const void* step_fn(int G, int kv_f16, bool prof, bool wf16) {
+// [G - 1][f16 KV][profiled]; the f16- and f32-weight variants (wf 1, 2): 8-row steps only
+const void* step_fn(int G, int kv_f16, bool prof, int wf) {
   static const void* fns[2][2][2] = {
       {{(const void*)k_step<1, 0, false>, (const void*)k_step<1, 0, true>},
        {(const void*)k_step<1, 1, false>, (const void*)k_step<1, 1, true>}},
       {{(const void*)k_step<2, 0, false>, (const void*)k_step<2, 0, true>},
        {(const void*)k_step<2, 1, false>, (const void*)k_step<2, 1, true>}}};
-  static const void* fns_h[2][2] = {
-      {(const void*)k_step<1, 0, false, false, 1>, (const void*)k_step<1, 0, true, false, 1>},
-      {(const void*)k_step<1, 1, false, false, 1>, (const void*)k_step<1, 1, true, false, 1>}};
-  if (wf16) return G == 1 ? fns_h[kv_f16 ? 1 : 0][prof ? 1 : 0] : nullptr;
+  static const void* fns_h[2][2][2] = {
+      {{(const void*)k_step<1, 0, false, false, 1>, (const void*)k_step<1, 0, true, false, 1>},
+       {(const void*)k_step<1, 1, false, false, 1>, (const void*)k_step<1, 1, true, false, 1>}},
+      {{(const void*)k_step<1, 0, false, false, 2>, (const void*)k_step<1, 0, true, false, 2>},
+       {(const void*)k_step<1, 1, false, false, 2>, (const void*)k_step<1, 1, true, false, 2>}}};
+  if (wf) return G == 1 ? fns_h[wf - 1][kv_f16 ? 1 : 0][prof ? 1 : 0] : nullptr;
   return fns[G - 1][kv_f16 ? 1 : 0][prof ? 1 : 0];
 }
 // the 8- and 16-row variants that read the descriptor from device memory
-const void* step_fn_dev(int G, int kv_f16, bool wf16) {
+const void* step_fn_dev(int G, int kv_f16, int wf) {
   static const void* fns[2][2] = {
       {(const void*)k_step<1, 0, false, true>, (const void*)k_step<1, 1, false, true>},
       {(const void*)k_step<2, 0, false, true>, (const void*)k_step<2, 1, false, true>}};
-  static const void* fns_h[2] = {(const void*)k_step<1, 0, false, true, 1>, (const void*)k_step<1, 1, false, true, 1>};
-  if (wf16) return G == 1 ? fns_h[kv_f16 ? 1 : 0] : nullptr;
+  static const void* fns_h[2][2] = {
+      {(const void*)k_step<1, 0, false, true, 1>, (const void*)k_step<1, 1, false, true, 1>},
+      {(const void*)k_step<1, 0, false, true, 2>, (const void*)k_step<1, 1, false, true, 2>}};
+  if (wf) return G == 1 ? fns_h[wf - 1][kv_f16 ? 1 : 0] : nullptr;
   return fns[G - 1][kv_f16 ? 1 : 0];
 }
 }  // namespace
 
 hipError_t prepare_step_kernels() {
-  for (int wf = 0; wf < 2; ++wf)
+  for (int wf = 0; wf < 3; ++wf)
     for (int G = 1; G <= (wf ? 1 : 2); ++G)
       for (int kv = 0; kv < 2; ++kv) {
         for (int prof = 0; prof < 2; ++prof) {
-          const hipError_t e = hipFuncSetAttribute(step_fn(G, kv, prof != 0, wf != 0),
+          const hipError_t e = hipFuncSetAttribute(step_fn(G, kv, prof != 0, wf),
                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)step_lds_bytes(G));
           if (e != hipSuccess) return e;
         }
-        const hipError_t e = hipFuncSetAttribute(step_fn_dev(G, kv, wf != 0), hipFuncAttributeMaxDynamicSharedMemorySize,
+        const hipError_t e = hipFuncSetAttribute(step_fn_dev(G, kv, wf), hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)step_lds_bytes(G));
         if (e != hipSuccess) return e;
       }
   return hipSuccess;
 }
 
-hipError_t launch_step(hipStream_t s, int G, int kv_f16, bool wf16, const StepParams* P, const StepDesc* desc,
+hipError_t launch_step(hipStream_t s, int G, int kv_f16, int wf, const StepParams* P, const StepDesc* desc,
                         uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev, const GenCtl* gc) {
   // desc: host memory; the launch copies it into the kernel arguments. desc_dev
   // (verify steps of up to 8 G rows): the kernel reads the descriptor there instead.
-  if (G < 1 || G > (wf16 ? 1 : 2)) return hipErrorInvalidValue;
+  if (G < 1 || G > (wf ? 1 : 2) || wf < 0 || wf > 2) return hipErrorInvalidValue;
   GenCtl ctl{};
   if (gc) ctl = *gc;
   void* args[] = {(void*)&P, (void*)desc, (void*)&epoch, (void*)&mode, (void*)&desc_dev, (void*)&ctl};
   if (desc_dev) {
     if (profiled) return hipErrorInvalidValue;
-    return hipLaunchKernel(step_fn_dev(G, kv_f16, wf16), dim3(kNwg), dim3(kT), args, step_lds_bytes(G), s);
+    return hipLaunchKernel(step_fn_dev(G, kv_f16, wf), dim3(kNwg), dim3(kT), args, step_lds_bytes(G), s);
   }
   const size_t lds = step_lds_bytes(G);
   // A plain launch: one workgroup per CU (the kernel's registers and LDS allow
@@ -2153,7 +2203,7 @@ hipError_t launch_step(hipStream_t s, int G, int kv_f16, bool wf16, const StepPa
   // in the kernel is bounded: if another kernel holds CUs, the late workgroups
   // join when it ends, and a wait that outlasts its bound ends the step with an
   // error instead of a hang.
-  return hipLaunchKernel(step_fn(G, kv_f16, profiled, wf16), dim3(kNwg), dim3(kT), args, lds, s);
+  return hipLaunchKernel(step_fn(G, kv_f16, profiled, wf), dim3(kNwg), dim3(kT), args, lds, s);
 }
 
 }  // namespace mtg

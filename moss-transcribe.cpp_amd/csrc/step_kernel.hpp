@@ -27,6 +27,10 @@ constexpr int kStepMaxLayers = 48;
 // on MI355X at 8 rows: 1,024 keys 1,079 vs 1,238 us, 3,072 1,263 vs 1,325, 4,096
 // 1,412 vs 1,383, 8,000 1,582 vs 1,521.
 constexpr int kStepF16MaxKeys = 3584;
+// The same for f32 weights, where the row streams weigh more against attention.
+// Measured at 8 rows: 1,024 keys 1,636 vs 1,877 us, 3,584 1,839 vs 1,973, 5,120
+// 1,985 vs 2,051, 6,144 2,110 vs 2,091, 8,000 2,137 vs 2,151.
+constexpr int kStepF32MaxKeys = 5120;
 // Default wait bounds: 2^23 polls, 50 ms.
 constexpr uint32_t kWaitPolls = 1u << 23;
 constexpr uint32_t kWaitTicks = 5000000u;
@@ -39,7 +43,7 @@ struct StepParams {
   // const restrict argument, so these pointers come in with scalar loads.
   LayerDev layer[kStepMaxLayers];
   const uint8_t* embd;
-  const uint8_t* lm16;  // f16 weights: the lm_head's copy of embd (lm_f16.hpp)
+  const uint8_t* lm_copy;  // f16 / f32 weights: the lm_head's copy of embd (lm_f16.hpp)
   const float* out_norm;
   const float* rope;
   const float* embeds;  // host rows uploaded for append
@@ -49,8 +53,9 @@ struct StepParams {
   // SwiGLU output (gate/up -> down): codes [16][K] and f16-valued scales [16][K/32]
   int8_t *oq, *aq;
   float *oqs, *aqs;
-  // the same two activations as f16 rows [16][K] (f16 weights)
+  // the same two activations as f16 rows [16][K] (f16 weights) or f32 rows (f32)
   uint16_t *oh, *ah;
+  float *o32, *a32;
   uint32_t* bitmap;
   uint64_t* part_keys;      // [nwg][16]
   StepResult* result;
@@ -77,13 +82,13 @@ constexpr int kFlagStride = 32;
 uint32_t step_progress_per_step(int n_layers);
 size_t step_lds_bytes(int G);
 hipError_t prepare_step_kernels();
-// wf16: the variant for f16 weights (G == 1 only). desc: the host copy of the
+// wf: the weight variant, 0 q8_0, 1 f16, 2 f32 (1 and 2: G == 1 only). desc: the host copy of the
 // step descriptor (passed by value as a kernel argument). profiled: the variant
 // that writes clock marks into StepParams::timing.
 // desc_dev: the variant that reads the descriptor from device memory (a device
 // loop); with gc, its workgroup 0 then runs the controller pass on the step's
 // outcome (gen_ctrl.hpp), and the launch returns at once once gc->g->done is set.
-hipError_t launch_step(hipStream_t s, int G, int kv_f16, bool wf16, const StepParams* P, const StepDesc* desc,
+hipError_t launch_step(hipStream_t s, int G, int kv_f16, int wf, const StepParams* P, const StepDesc* desc,
                         uint32_t epoch, int mode, bool profiled, const StepDesc* desc_dev = nullptr,
                         const GenCtl* gc = nullptr);
 

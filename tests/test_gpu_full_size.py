@@ -28,6 +28,7 @@ CASES = [
     ("q4_K-f16kv-T16-ctx16384-graph", mtg.TYPE_Q4_K, mtg.TYPE_F16, 16, 16384, mtg.EXEC_GRAPH),
     # the converter's default dtype: every matrix f32 (2.4 GB of weights)
     ("f32-f32kv-T8-ctx1600-graph", mtg.TYPE_F32, mtg.TYPE_F32, 8, 1600, mtg.EXEC_GRAPH),
+    ("f32-f32kv-T8-ctx1600-step", mtg.TYPE_F32, mtg.TYPE_F32, 8, 1600, mtg.EXEC_STEP_KERNEL),
 ]
 
 

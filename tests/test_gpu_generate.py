@@ -184,13 +184,15 @@ def test_device_loop_finishes_on_the_host_after_an_abandoned_step():
     assert a.past_len == b.past_len
 
 
-@pytest.mark.parametrize("kv_type", [mtg.TYPE_F32, mtg.TYPE_F16], ids=["f32kv", "f16kv"])
-def test_device_loop_f16_weights_equals_host_loop_and_oracle(kv_type):
-    """f16 weights on the step kernel's f16 variant (8-row steps): the device loop,
-    the host loop and the oracle's controller agree with the penalty on; a device
-    loop with more than 7 drafts (16-row steps) is refused."""
-    print("device loop, f16 weights: kv %d" % kv_type, flush=True)
-    model, orc, a, b, rng = _setup(40, 600, kv_type, wtype=mtg.TYPE_F16)
+@pytest.mark.parametrize("wtype,kv_type", [(mtg.TYPE_F16, mtg.TYPE_F32), (mtg.TYPE_F16, mtg.TYPE_F16),
+                                           (mtg.TYPE_F32, mtg.TYPE_F32), (mtg.TYPE_F32, mtg.TYPE_F16)],
+                         ids=["f16-f32kv", "f16-f16kv", "f32-f32kv", "f32-f16kv"])
+def test_device_loop_f16_weights_equals_host_loop_and_oracle(wtype, kv_type):
+    """f16 and f32 weights on the step kernel's row variants (8-row steps): the device
+    loop, the host loop and the oracle's controller agree with the penalty on; a
+    device loop with more than 7 drafts (16-row steps) is refused."""
+    print("device loop, weights %d: kv %d" % (wtype, kv_type), flush=True)
+    model, orc, a, b, rng = _setup(40, 600, kv_type, wtype=wtype)
     assert a.exec_mode == mtg.EXEC_STEP_KERNEL
     prior = _prior(rng, model.hp.vocab)
     first = int(prior[-1])

@@ -15,8 +15,9 @@ softmax stress rows through the device attention.
   (16,384-row prompt, K=16, 64 steps), both with an f16 cache, on the per-op kernels:
   the prompt prefilled on the device, every greedy step of the workload on both sides
   from that KV state, identical ids, counters and appended KV rows.
-* The 1,600-row workload with f16 weights on the persistent kernel's f16 variant: 128
-  greedy steps through the host loop and the device loop, identical to the oracle.
+* The 1,600-row workload with f16 and with f32 weights on the persistent kernel's row
+  variants: 128 greedy steps through the host loop and the device loop, identical to
+  the oracle.
 * Attention on scores of +-10000 and -inf (tests/test_cpu_softmax.cpp:40-46), made
   by planting keys of magnitude 10^4 in the cache: bit-identical to the oracle.
 """
@@ -214,15 +215,16 @@ def test_attention_on_extreme_scores(kv_type, exec_mode):
 
 
 @pytest.mark.timeout(600)
-def test_full_size_stream_f16_weights_step_kernel():
-    """f16 weights on the persistent kernel's f16 variant at full size: the 1,600-row
-    prompt of the K=8 workload prefilled on the device, then 128 greedy steps with the
-    stream drafter through the host loop and through the device loop (a second
-    decoder from the same KV state), against the oracle: identical ids, counters and
-    appended KV rows, every step on the persistent kernel (within its 3,584-key
-    limit for f16 weights)."""
+@pytest.mark.parametrize("wtype", [mtg.TYPE_F16, mtg.TYPE_F32], ids=["f16", "f32"])
+def test_full_size_stream_f16_weights_step_kernel(wtype):
+    """f16 and f32 weights on the persistent kernel's row variants at full size: the
+    1,600-row prompt of the K=8 workload prefilled on the device, then 128 greedy steps
+    with the stream drafter through the host loop and through the device loop (a
+    second decoder from the same KV state), against the oracle: identical ids,
+    counters and appended KV rows, every step on the persistent kernel (within its
+    3,584-key limit)."""
     cfg = dict(WORKLOADS[2])
-    cfg["wtype"] = mtg.TYPE_F16
+    cfg["wtype"] = wtype
     steps, K = 128, cfg["K"]
     oracle_py.lib().orc_set_threads(THREADS)
     model = mtg.SynthModel(cfg["wtype"], seed=0, std=0.02, gain_jitter=0.0)
@@ -232,7 +234,7 @@ def test_full_size_stream_f16_weights_step_kernel():
     dec = mtg.Decoder(model, max_seq, cfg["kv"])
     assert dec.exec_mode == mtg.EXEC_STEP_KERNEL
     rows, text, stream = build_prompt(model, dec.embed, cfg)
-    _log("f16 stream: device prefill of %d rows" % n_prompt)
+    _log("row-weight stream: device prefill of %d rows" % n_prompt)
     hid = dec.prefill(rows)
     first = int(np.argmax(dec.logits(hid[-1:])[0]))
     k, v = dec.kv_read(n_prompt)
@@ -243,7 +245,7 @@ def test_full_size_stream_f16_weights_step_kernel():
     del k, v
     fn, user, _keep = mtg.stream_drafter(text, stream)
     drafter = mtg.stream_drafter(text, stream)
-    _log("f16 stream: %d greedy steps, host loop, device loop and oracle" % steps)
+    _log("row-weight stream: %d greedy steps, host loop, device loop and oracle" % steps)
     runs0 = dec.step_kernel_runs
     ids1, st1 = dec.generate_from(first, 1 << 20, max_steps=steps, max_draft=K - 1, draft=fn, user=user)
     ids2, st2 = dev.generate_device(first, 1 << 20, max_steps=steps, max_draft=K - 1, stream=drafter)
@@ -262,6 +264,6 @@ def test_full_size_stream_f16_weights_step_kernel():
         k1, v1 = d.kv_read(d.past_len)
         _same(k1[:, :, n_prompt:], k0[:, :, n_prompt:], "K rows appended by the steps (%s)" % what)
         _same(v1[:, :, n_prompt:], v0[:, :, n_prompt:], "V rows appended by the steps (%s)" % what)
-    _log("f16 stream: %d ids, %d accepted drafts" % (len(ids1), st1.accepted))
+    _log("row-weight stream: %d ids, %d accepted drafts" % (len(ids1), st1.accepted))
     for x in (dec, dev, orc, model):
         x.close()

@@ -172,10 +172,11 @@ def test_generated_token_stream_matches_oracle(penalty):
 
 WTYPES = [mtg.TYPE_F16, mtg.TYPE_F32, mtg.TYPE_Q4_K]
 WT_NAMES = {mtg.TYPE_F16: "f16", mtg.TYPE_F32: "f32", mtg.TYPE_Q4_K: "q4_K"}
-# (weight type, exec mode): the persistent kernel streams q8_0 tiles and f16 rows
-# (its 8-row steps; 16-row steps of f16 weights take the per-op kernels)
+# (weight type, exec mode): the persistent kernel streams q8_0 tiles and f16 / f32
+# rows (its 8-row steps; 16-row steps of f16 / f32 weights take the per-op kernels)
+ROW_STEP = (mtg.TYPE_F16, mtg.TYPE_F32)
 WT_CASES = [(w, e) for w in WTYPES
-            for e in ([mtg.EXEC_STEP_KERNEL] if w == mtg.TYPE_F16 else []) + [mtg.EXEC_GRAPH, mtg.EXEC_EAGER]]
+            for e in ([mtg.EXEC_STEP_KERNEL] if w in ROW_STEP else []) + [mtg.EXEC_GRAPH, mtg.EXEC_EAGER]]
 WT_IDS = ["%s-%s" % (WT_NAMES[w], EXEC_NAMES[e]) for w, e in WT_CASES]
 
 
@@ -233,16 +234,21 @@ def test_long_f16_context_matches_oracle(wtype, exec_mode):
     assert dec.step_kernel_runs == (1 if exec_mode == mtg.EXEC_STEP_KERNEL else 0)  # the 5-row step
 
 
-@pytest.mark.parametrize("wtype", [mtg.TYPE_F16, mtg.TYPE_Q8_0], ids=["f16", "q8_0"])
-def test_step_kernel_key_limit(wtype):
+# default key limits of the persistent kernel (None: no limit)
+KEY_LIMITS = [(mtg.TYPE_F16, 3584), (mtg.TYPE_F32, 5120), (mtg.TYPE_Q8_0, None)]
+
+
+@pytest.mark.parametrize("wtype,limit", KEY_LIMITS, ids=["f16", "f32", "q8_0"])
+def test_step_kernel_key_limit(wtype, limit):
     """Path selection by KV length: with f16 weights an 8-row step up to 3,584 keys
-    (past + rows) runs on the persistent kernel and a longer one on the per-op
-    graph; q8_0 weights have no limit by default; mtg_set_step_max_keys moves it.
-    Every step equals the oracle."""
+    (past + rows), with f32 weights up to 5,120, runs on the persistent kernel and a
+    longer one on the per-op graph; q8_0 weights have no limit by default;
+    mtg_set_step_max_keys moves it. Every step equals the oracle."""
     print("step kernel key limit: weights %d" % wtype, flush=True)
     model = mtg.SynthModel(wtype, seed=21, std=0.02, gain_jitter=0.05, n_layers=1, vocab=4096)
     hp = model.hp
-    prefix, max_seq = 3600, 3700
+    edge = limit or 3584  # q8_0: the same steps, all on the persistent kernel
+    prefix, max_seq = edge + 16, edge + 116
     orc = oracle_py.Oracle(model, max_seq, mtg.TYPE_F16)
     dec = mtg.Decoder(model, max_seq, mtg.TYPE_F16)
     assert dec.exec_mode == mtg.EXEC_STEP_KERNEL
@@ -267,11 +273,11 @@ def test_step_kernel_key_limit(wtype):
         assert np.array_equal(c1, c0) and m1 == m0
         return dec.step_kernel_runs - before
 
-    f16 = wtype == mtg.TYPE_F16  # (each step rewinds to an earlier position)
-    assert step(3577) == (0 if f16 else 1)     # 3,585 keys
-    assert step(3577, 1 << 20) == 1            # a higher limit
-    assert step(3577, 0) == (0 if f16 else 1)  # the default again
-    assert step(3576) == 1                     # 3,584 keys
+    over = 0 if limit else 1  # (each step rewinds to an earlier position)
+    assert step(edge - 7) == over              # edge + 1 keys
+    assert step(edge - 7, 1 << 20) == 1        # a higher limit
+    assert step(edge - 7, 0) == over           # the default again
+    assert step(edge - 8) == 1                 # edge keys
     assert step(3000, 2000) == 0               # a lower limit
     assert dec.step_fallbacks == 0
 
@@ -329,7 +335,7 @@ def test_f16_and_q4k_weights_penalty_prefill_and_stream(wtype):
     model = mtg.SynthModel(wtype, seed=9, std=0.02, gain_jitter=0.05, n_layers=2, vocab=4096)
     orc = oracle_py.Oracle(model, 512)
     dec = mtg.Decoder(model, 512)
-    if wtype == mtg.TYPE_F16:
+    if wtype in ROW_STEP:
         assert dec.exec_mode == mtg.EXEC_STEP_KERNEL
     else:
         assert dec.exec_mode == mtg.EXEC_GRAPH
