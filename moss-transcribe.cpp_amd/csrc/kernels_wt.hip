@@ -1498,54 +1498,6 @@ k_gemm_f32(const StepDesc* __restrict__ desc, const float* __restrict__ w, const
   }
 }
 
-// f32 lm_head over the rows of the tied embedding, grouped as in k_gemm_f32; per
-// verify row the best 64-bit key of the workgroup goes to part_keys
-// (kLmWorkgroups workgroups, one slot each).
-template <int SEG, int NR>
-__global__ void __launch_bounds__(256)
-k_lm_head_f32(const StepDesc* __restrict__ desc, const float* __restrict__ w, int vocab, const float* __restrict__ x,
-              const uint32_t* __restrict__ bitmap, float* __restrict__ logits, uint64_t* __restrict__ part_keys) {
-  const int T = desc->T, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const bool pen = desc->penalty > 1.0f;
-  const float penalty = desc->penalty;
-  const bool write_logits = desc->write_logits != 0;
-  const int words = (vocab + 31) / 32;
-  const int ngroups = (vocab + NR - 1) / NR, nwaves = gridDim.x * 4;
-  const float* base[1] = {w};
-  int g = blockIdx.x * 4 + wave;
-  F32Group<SEG, 1, NR> nxt;
-  if (g < ngroups) f32_load<SEG, 1, NR>(base, vocab, g * NR, nxt);
-  uint64_t best = 0;  // lane t: verify row t
-  for (; g < ngroups; g += nwaves) {
-    const F32Group<SEG, 1, NR> cur = nxt;
-    if (g + nwaves < ngroups) f32_load<SEG, 1, NR>(base, vocab, (g + nwaves) * NR, nxt);
-    for (int t = 0; t < T; ++t) {
-      float acc[NR];
-      f32_dots<SEG, 1, NR>(cur, x, t, acc);
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const int row = g * NR + r;
-        if (row < vocab) {
-          float v = acc[r];
-          if (write_logits && lane == 0) logits[(size_t)t * vocab + row] = v;
-          if (pen && ((bitmap[(size_t)t * words + (row >> 5)] >> (row & 31)) & 1u))
-            v = v > 0.0f ? __fdiv_rn(v, penalty) : __fmul_rn(v, penalty);
-          const uint64_t key = argmax_key(v, row);
-          if (lane == t) best = key > best ? key : best;
-        }
-      }
-    }
-  }
-  __shared__ uint64_t s_best[4][64];
-  s_best[wave][lane] = best;
-  __syncthreads();
-  if ((int)threadIdx.x < T) {
-    uint64_t b = 0;
-    for (int i = 0; i < 4; ++i) b = s_best[i][threadIdx.x] > b ? s_best[i][threadIdx.x] : b;
-    part_keys[(size_t)blockIdx.x * kMaxRows + threadIdx.x] = b;
-  }
-}
-
 // weight rows per wave and group of the f32 GEMM: NM * NR * K / 64 <= 64 weight
 // floats per lane (twice that with the next group in flight)
 constexpr int f32_nr(int nm, int seg) { return seg == 16 ? 4 / nm : seg == 32 ? (nm == 1 ? 2 : 1) : 1; }
@@ -1736,18 +1688,10 @@ void launch_lm_head_wt(hipStream_t s, int wtype, const StepDesc* desc, const uin
   if (wtype == MTG_TYPE_F16)  // w: the lm_head copy of the embedding (launch_lm16_retile)
     hipLaunchKernelGGL(k_lm_head_f16m<false>, dim3(kLm16Blocks), dim3(64 * kLm16NWV), lm_lds_bytes(false), s, desc, w,
                        vocab, (const void*)act.f16h, bitmap, logits, part_keys);
-  else if (wtype == MTG_TYPE_F32) {
-    const float* wf = (const float*)w;
-    if (k == 1024)  // w: the lm_head copy of the embedding (launch_lm16_retile)
-      hipLaunchKernelGGL(k_lm_head_f16m<true>, dim3(kLm16Blocks), dim3(64 * kLm16NWV), lm_lds_bytes(true), s, desc,
-                         w, vocab, (const void*)act.f32, bitmap, logits, part_keys);
-    else if (k == 2048)
-      hipLaunchKernelGGL((k_lm_head_f32<32, 2>), grid, block, 0, s, desc, wf, vocab, act.f32, bitmap, logits,
-                         part_keys);
-    else
-      hipLaunchKernelGGL((k_lm_head_f32<48, 1>), grid, block, 0, s, desc, wf, vocab, act.f32, bitmap, logits,
-                         part_keys);
-  } else if (k == 1024 && vocab % 16 == 0)
+  else if (wtype == MTG_TYPE_F32)  // w: the lm_head copy of the embedding (launch_lm16_retile)
+    hipLaunchKernelGGL(k_lm_head_f16m<true>, dim3(kLm16Blocks), dim3(64 * kLm16NWV), lm_lds_bytes(true), s, desc, w,
+                       vocab, (const void*)act.f32, bitmap, logits, part_keys);
+  else if (k == 1024 && vocab % 16 == 0)
     hipLaunchKernelGGL(k_lm_head_q4m<4>, grid, block, q4m_lds_bytes(k), s, desc, w, vocab, act.q8k, bitmap, logits,
                        part_keys);
   else if (k <= kQ4MaxK)
