@@ -286,9 +286,9 @@ int32_t mtg_exec_mode(const mtg_ctx* ctx);
  * one CPU path): in MTG_EXEC_STEP_KERNEL mode a verify / append step whose KV
  * length (past_len + rows) exceeds max_keys runs on the per-op graph instead of
  * the persistent kernel. max_keys <= 0 restores the default: no limit for q8_0
- * weights; 3,584 for f16 and 5,120 for f32 weights, whose per-op attention (three
- * workgroups per CU) overtakes the persistent kernel's at longer contexts on
- * MI355X. The device loop (mtg_generate_device) always runs the persistent
+ * weights; 5,120 for f16 weights, whose per-op attention (three workgroups per
+ * CU) overtakes the persistent kernel's at longer contexts on MI355X, and 8,192
+ * (the longest measured length) for f32 weights. The device loop (mtg_generate_device) always runs the persistent
  * kernel. mtg_step_kernel_runs counts the steps that ran to their end on the
  * persistent kernel. */
 int mtg_set_step_max_keys(mtg_ctx* ctx, int32_t max_keys);

@@ -1880,15 +1880,21 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
       WMARK(P, l, 3);
     }
     // the o-proj tile's weights: issued after the attention, so that no register
-    // holds them through it (the o-proj starts after the merge, well after they land)
-    if constexpr (WF != 0) {
-      const uint8_t* ro[1] = {Ly.wo + (size_t)(4 * w + wave) * cQN * EB};
-      h_load<32, 1, 1, F32>(ro, ho);
-      const uint8_t* rg[2] = {Ly.wg + (size_t)(cGuRows * w + 3 * wave) * cH * EB,
-                              Ly.wu + (size_t)(cGuRows * w + 3 * wave) * cH * EB};
-      h_load<16, 2, 3, F32>(rg, hgu);
-      gain16_load(Ly.ffn_norm, gf);
-    }
+    // holds them through it (the o-proj starts after the merge, well after they land).
+    // Row variants: a merge workgroup issues its o-proj and gate/up rows after its
+    // merge (loads complete in order: issued first, 64 or 128 KB of rows would hold
+    // up the merge's progress polls and partials)
+    auto row_loads = [&]() {
+      if constexpr (WF != 0) {
+        const uint8_t* ro[1] = {Ly.wo + (size_t)(4 * w + wave) * cQN * EB};
+        h_load<32, 1, 1, F32>(ro, ho);
+        const uint8_t* rg[2] = {Ly.wg + (size_t)(cGuRows * w + 3 * wave) * cH * EB,
+                                Ly.wu + (size_t)(cGuRows * w + 3 * wave) * cH * EB};
+        h_load<16, 2, 3, F32>(rg, hgu);
+        gain16_load(Ly.ffn_norm, gf);
+      }
+    };
+    if (WF != 0 && !has_merge) row_loads();
     if (WF == 0 && od) wt_load<8>(Ly.wo + (size_t)w * cBQ * kUnitBytes, 8 * wave, ba, bs);
     if (WF == 0 && gu) {  // gate / up tiles 2j, 2j + 1 of this layer
       const int j = w - cOTiles;
@@ -1912,6 +1918,7 @@ __device__ __forceinline__ bool step_body(const StepParams* __restrict__ Pp, con
       WMARK(P, l, 22);
       publish(c, next_done(l, kPhMerge));
       WMARK(P, l, 5);
+      if (WF != 0) row_loads();
       if (!gu && l + 1 < L) {  // nothing more in this layer: prefetch the next one
         const LayerDev& Ln = layer_at(P, l + 1);
         wt_load<4>(Ln.wqkv + (size_t)w * cBH * kUnitBytes, 4 * wave, qa, qs);

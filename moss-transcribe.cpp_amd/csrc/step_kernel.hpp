@@ -24,13 +24,14 @@ constexpr int kStepMaxLayers = 48;
 // KV length beyond which f16-weight steps take the per-op kernels by default:
 // there the persistent kernel's attention (one workgroup per CU, each walking 2+
 // chunks in turn) falls behind the per-op one (three workgroups per CU). Measured
-// on MI355X at 8 rows: 1,024 keys 1,079 vs 1,238 us, 3,072 1,263 vs 1,325, 4,096
-// 1,412 vs 1,383, 8,000 1,582 vs 1,521.
-constexpr int kStepF16MaxKeys = 3584;
-// The same for f32 weights, where the row streams weigh more against attention.
-// Measured at 8 rows: 1,024 keys 1,636 vs 1,877 us, 3,584 1,839 vs 1,973, 5,120
-// 1,985 vs 2,051, 6,144 2,110 vs 2,091, 8,000 2,137 vs 2,151.
-constexpr int kStepF32MaxKeys = 5120;
+// on MI355X at 8 rows, f16 KV: 1,024 keys 1,044 vs 1,228 us, 3,072 1,216 vs 1,316,
+// 5,120 1,393 vs 1,406, 6,144 1,505 vs 1,453, 8,000 1,533 vs 1,516.
+constexpr int kStepF16MaxKeys = 5120;
+// The same for f32 weights, where the row streams weigh more against attention:
+// the persistent kernel won at every measured length (1,024 keys 1,533 vs 1,875
+// us, 5,120 1,875 vs 2,047, 6,144 1,985 vs 2,094, 8,000 2,014 vs 2,149); the
+// limit is the longest measured length.
+constexpr int kStepF32MaxKeys = 8192;
 // Default wait bounds: 2^23 polls, 50 ms.
 constexpr uint32_t kWaitPolls = 1u << 23;
 constexpr uint32_t kWaitTicks = 5000000u;

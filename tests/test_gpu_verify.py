@@ -235,13 +235,13 @@ def test_long_f16_context_matches_oracle(wtype, exec_mode):
 
 
 # default key limits of the persistent kernel (None: no limit)
-KEY_LIMITS = [(mtg.TYPE_F16, 3584), (mtg.TYPE_F32, 5120), (mtg.TYPE_Q8_0, None)]
+KEY_LIMITS = [(mtg.TYPE_F16, 5120), (mtg.TYPE_F32, 8192), (mtg.TYPE_Q8_0, None)]
 
 
 @pytest.mark.parametrize("wtype,limit", KEY_LIMITS, ids=["f16", "f32", "q8_0"])
 def test_step_kernel_key_limit(wtype, limit):
-    """Path selection by KV length: with f16 weights an 8-row step up to 3,584 keys
-    (past + rows), with f32 weights up to 5,120, runs on the persistent kernel and a
+    """Path selection by KV length: with f16 weights an 8-row step up to 5,120 keys
+    (past + rows), with f32 weights up to 8,192, runs on the persistent kernel and a
     longer one on the per-op graph; q8_0 weights have no limit by default;
     mtg_set_step_max_keys moves it. Every step equals the oracle."""
     print("step kernel key limit: weights %d" % wtype, flush=True)
